@@ -1,0 +1,116 @@
+// Device-side helpers shared by the gfx950 kernels of this library.
+//
+// * storage conversions for bf16 / fp16 / fp32 inputs,
+// * the two MFMA shapes used for 16x16 output tiles:
+//     v_mfma_f32_16x16x32_bf16  (gfx950; A/B: 8 bf16 per lane)
+//     v_mfma_f32_16x16x16_bf16  (A/B: 4 bf16 per lane)
+//     v_mfma_f32_16x16x4_f32    (A/B: 1 fp32 per lane)
+//   Lane l of a wave64 holds A row (l % 16) and B column (l % 16); the K
+//   elements it holds are k = KPL*(l / 16) + [0, KPL). The accumulator holds
+//   rows 4*(l / 16) + [0, 4) of column (l % 16).
+// * tile_mma: one 16x16 output tile from operands resident in LDS, with A
+//   stored row-major [row][k] and B stored transposed [col][k].
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace kch {
+
+typedef __bf16 bf16_t;
+typedef bf16_t bf16x8 __attribute__((ext_vector_type(8)));
+typedef bf16_t bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Input storage types accepted by the C-ABI (dtype enum: 0 fp32, 1 bf16, 2 fp16).
+enum DType : int { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(bf16_t x) { return (float)x; }
+__device__ __forceinline__ float to_f32(_Float16 x) { return (float)x; }
+
+template <typename T> __device__ __forceinline__ T from_f32(float x);
+template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <> __device__ __forceinline__ bf16_t from_f32<bf16_t>(float x) { return (bf16_t)x; }
+template <> __device__ __forceinline__ _Float16 from_f32<_Float16>(float x) { return (_Float16)x; }
+
+// Two consecutive elements of a storage type, converted to fp32.
+template <typename T> struct Pair;
+template <> struct Pair<float> {
+  typedef float2 raw;
+  static __device__ __forceinline__ float2 cvt(raw r) { return r; }
+};
+template <> struct Pair<bf16_t> {
+  typedef uint32_t raw;
+  static __device__ __forceinline__ float2 cvt(raw r) {
+    return make_float2(__uint_as_float(r << 16), __uint_as_float(r & 0xffff0000u));
+  }
+};
+template <> struct Pair<_Float16> {
+  typedef uint32_t raw;
+  static __device__ __forceinline__ float2 cvt(raw r) {
+    _Float16 lo = __builtin_bit_cast(_Float16, (uint16_t)(r & 0xffffu));
+    _Float16 hi = __builtin_bit_cast(_Float16, (uint16_t)(r >> 16));
+    return make_float2((float)lo, (float)hi);
+  }
+};
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Orders LDS traffic of one wave: every lane's earlier LDS writes are visible to
+// every lane's later LDS reads. Waves are not synchronised with each other.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+
+// ---------------------------------------------------------------------------
+// 16x16 output tile: acc += A[16 x kd] * B[kd x 16]
+//   A: LDS, row-major, row stride lda (elements); A[r][k] at A[r*lda + k]
+//   B: LDS, transposed, row stride ldb;            B[k][n] at B[n*ldb + k]
+// kd must be a multiple of 16 (bf16) or 4 (fp32).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ f32x4 tile_mma(f32x4 acc, const bf16_t* A, int lda,
+                                          const bf16_t* B, int ldb, int kd) {
+  const int l = lane_id();
+  const int r = l & 15;
+  const bf16_t* a = A + r * lda;
+  const bf16_t* b = B + r * ldb;
+  int k = 0;
+  const int k8 = (l >> 4) * 8;
+  for (; k + 32 <= kd; k += 32) {
+    bf16x8 av = *reinterpret_cast<const bf16x8*>(a + k + k8);
+    bf16x8 bv = *reinterpret_cast<const bf16x8*>(b + k + k8);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc, 0, 0, 0);
+  }
+  if (k < kd) {  // one 16-wide step
+    const int k4 = (l >> 4) * 4;
+    bf16x4 av = *reinterpret_cast<const bf16x4*>(a + k + k4);
+    bf16x4 bv = *reinterpret_cast<const bf16x4*>(b + k + k4);
+    acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, bv, acc, 0, 0, 0);
+  }
+  return acc;
+}
+
+__device__ __forceinline__ f32x4 tile_mma(f32x4 acc, const float* A, int lda,
+                                          const float* B, int ldb, int kd) {
+  const int l = lane_id();
+  const int r = l & 15;
+  const int kq = l >> 4;
+  const float* a = A + r * lda + kq;
+  const float* b = B + r * ldb + kq;
+  for (int k = 0; k < kd; k += 4)
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[k], b[k], acc, 0, 0, 0);
+  return acc;
+}
+
+// Row index (within a 16x16 tile) of accumulator element e held by this lane.
+__device__ __forceinline__ int acc_row(int e) { return ((lane_id() >> 4) << 2) + e; }
+__device__ __forceinline__ int acc_col() { return lane_id() & 15; }
+
+}  // namespace kch

@@ -1,0 +1,17 @@
+"""kch: MI355X (gfx950) HIP backend for the KDA / CSA / HCA hybrid-attention forward path.
+
+Drop-in twins of the reference operators (``/root/reference/ops_*.py``),
+running hand-written HIP kernels from ``libkch.so`` through the C ABI declared
+in ``include/kch.h``. Tensors must be on a ROCm GPU; there is no CPU path.
+"""
+
+from .ops_kda import naive_chunk_kda, naive_recurrent_kda
+from .ops_kda_backend import hip_available, kda_forward, validate_kda_backend
+
+__all__ = [
+    "hip_available",
+    "kda_forward",
+    "naive_chunk_kda",
+    "naive_recurrent_kda",
+    "validate_kda_backend",
+]

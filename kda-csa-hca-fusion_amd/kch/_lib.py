@@ -1,0 +1,94 @@
+"""ctypes binding of ``libkch.so`` (the gfx950 kernels behind ``include/kch.h``).
+
+The library is loaded lazily on first use. A missing library raises
+``ImportError`` naming the path and the build command; there is no fallback
+path of any kind: every operator in this package runs the HIP kernels.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libkch.so")
+
+_lock = threading.Lock()
+_lib = None
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_F = ctypes.c_float
+
+# name -> argument types (all return int status)
+_SIGNATURES = {
+    "kch_kda_chunk_fwd": [_P] * 8 + [_I] * 6 + [_F, _F, _I, _P],
+    "kch_kda_recurrent_fwd": [_P] * 8 + [_I] * 6 + [_F, _F, _I, _P],
+}
+
+EXPORTED = ["kch_abi_version", "kch_last_error"] + sorted(_SIGNATURES)
+
+DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+
+
+def load():
+    """Load and type the shared library (thread-safe, once)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"kch: native library {LIB_PATH} is missing; build it with "
+                f"`python -c 'import __graft_entry__ as g; g.build()'` from the repo root")
+        lib = ctypes.CDLL(LIB_PATH)
+        lib.kch_abi_version.restype = _I
+        lib.kch_abi_version.argtypes = []
+        lib.kch_last_error.restype = ctypes.c_char_p
+        lib.kch_last_error.argtypes = []
+        for name, args in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = _I
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def call(name: str, *args) -> None:
+    """Invoke ``name`` and raise ``RuntimeError`` on a non-zero status."""
+    lib = load()
+    rc = getattr(lib, name)(*args)
+    if rc != 0:
+        msg = lib.kch_last_error().decode(errors="replace")
+        raise RuntimeError(f"{name} failed (status {rc}): {msg}")
+
+
+def ptr(t):
+    """Device pointer of a tensor (or None for an absent optional tensor)."""
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_of(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def require_gpu(fn: str, *tensors) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(
+                f"{fn}: the HIP backend requires tensors on a ROCm GPU device "
+                f"(got {t.device}); this package has no CPU path.")
+
+
+def dtype_code(fn: str, dtype) -> int:
+    try:
+        return DTYPE_CODE[dtype]
+    except KeyError:
+        raise NotImplementedError(
+            f"{fn}: dtype {dtype} is not supported by the HIP kernels "
+            f"(float32, bfloat16, float16)") from None

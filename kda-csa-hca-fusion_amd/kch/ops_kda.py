@@ -1,0 +1,143 @@
+"""KDA operators on the HIP backend (drop-in twins of the reference's ``ops_kda``).
+
+``naive_chunk_kda``      <- ``/root/reference/ops_kda.py:464-494``
+``naive_recurrent_kda``  <- ``/root/reference/ops_kda.py:175-267``
+
+Same signatures, argument meaning, validation messages (``ValueError`` naming
+the operator, ``ops_kda.py:29-122``) and dtype contract (output in ``v.dtype``,
+state in ``state_dtype`` or fp32). Inputs must live on a ROCm GPU; the work runs
+in ``kch_kda_chunk_fwd`` / ``kch_kda_recurrent_fwd`` of ``libkch.so`` on the
+current stream. ``chunk_size`` is validated as in the reference; the result
+does not depend on it (chunking is a reassociation of the same recurrence), and
+the kernel uses its own chunk length.
+
+Not covered: float64 inputs (the reference computes them in fp64) raise
+``NotImplementedError``.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+
+
+def _validate_kda_inputs(q, k, v, g, beta, fn_name):
+    """Rank / batch / device / dtype contract of ``ops_kda.py:29-83``."""
+    for name, t, rank in [('q', q, 4), ('k', k, 4), ('v', v, 4), ('g', g, 4), ('beta', beta, 3)]:
+        if t.dim() != rank:
+            expect = ("[B, T, H, K]" if name in ('q', 'k') else "[B, T, HV, V]" if name == 'v'
+                      else "[B, T, HV, K]" if name == 'g' else "[B, T, HV]")
+            raise ValueError(
+                f"{fn_name}: {name} must have rank {rank} but got rank {t.dim()} "
+                f"(shape={tuple(t.shape)}). Expected shape: {expect}")
+    Bq, Tq = q.shape[0], q.shape[1]
+    for name, t in [('k', k), ('v', v), ('g', g), ('beta', beta)]:
+        if t.shape[0] != Bq or t.shape[1] != Tq:
+            raise ValueError(
+                f"{fn_name}: {name}.shape[0:2]={tuple(t.shape[0:2])} does not match "
+                f"q.shape[0:2]=({Bq}, {Tq}). All inputs must share the same batch (B) "
+                f"and sequence (T) dimensions.")
+    for name, t in [('k', k), ('v', v), ('g', g), ('beta', beta)]:
+        if t.device != q.device:
+            raise ValueError(
+                f"{fn_name}: {name}.device={t.device} does not match q.device={q.device}. "
+                f"All inputs must be on the same device.")
+    for name, t in [('k', k), ('v', v), ('g', g), ('beta', beta)]:
+        if t.dtype != q.dtype:
+            raise ValueError(
+                f"{fn_name}: {name}.dtype={t.dtype} does not match q.dtype={q.dtype}. "
+                f"All inputs must share the same dtype (cast before calling if needed).")
+
+
+def _validate_kda_shapes(q, k, v, g, beta, fn_name, chunk_size=None):
+    """Dimension contract of ``ops_kda.py:86-122``."""
+    B, T, H, K = q.shape
+    HV, V = v.shape[2], v.shape[-1]
+    if H < 1:
+        raise ValueError(f"{fn_name}: H={H} must be >= 1 (would cause ZeroDivisionError in HV // H)")
+    if K < 1:
+        raise ValueError(f"{fn_name}: K={K} must be >= 1")
+    if V < 1:
+        raise ValueError(f"{fn_name}: V={V} must be >= 1")
+    if chunk_size is not None and chunk_size < 1:
+        raise ValueError(
+            f"{fn_name}: chunk_size={chunk_size} must be >= 1 (would cause ZeroDivisionError "
+            f"in T // chunk_size and (-T) % chunk_size)")
+    if HV % H != 0:
+        raise ValueError(f"{fn_name}: HV={HV} must be divisible by H={H} (GVA factor)")
+    if g.shape[2] != HV:
+        raise ValueError(
+            f"{fn_name}: g.shape[2]={g.shape[2]} must equal HV={HV} "
+            f"(g must be [B, T, HV, K], got {tuple(g.shape)})")
+    if g.shape[-1] != K:
+        raise ValueError(
+            f"{fn_name}: g.shape[-1]={g.shape[-1]} must equal K={K} "
+            f"(g must be [B, T, HV, K], got {tuple(g.shape)})")
+    if beta.shape[2] != HV:
+        raise ValueError(
+            f"{fn_name}: beta.shape[2]={beta.shape[2]} must equal HV={HV} "
+            f"(beta must be [B, T, HV], got {tuple(beta.shape)})")
+
+
+def _scale_value(scale, K):
+    if scale is None:
+        return K ** -0.5
+    if isinstance(scale, torch.Tensor):
+        return float(scale.detach().float().item())
+    return float(scale)
+
+
+def _clamp_value(g_clamp_min) -> float:
+    v = float(g_clamp_min)
+    return v if v > -math.inf else -math.inf
+
+
+def _run(entry, fn_name, q, k, v, g, beta, scale, initial_state, output_final_state,
+         g_clamp_min, state_dtype, chunk_size=None):
+    _validate_kda_inputs(q, k, v, g, beta, fn_name)
+    _validate_kda_shapes(q, k, v, g, beta, fn_name, chunk_size=chunk_size)
+    _lib.require_gpu(fn_name, q, initial_state)
+    code = _lib.dtype_code(fn_name, v.dtype)
+    B, T, H, K = q.shape
+    HV, V = v.shape[2], v.shape[-1]
+    sc = _scale_value(scale, K)
+    target_state = state_dtype if state_dtype is not None else torch.float32
+    q, k, v, g, beta = (t.contiguous() for t in (q, k, v, g, beta))
+    s0 = None
+    if initial_state is not None:
+        s0 = initial_state.to(device=q.device, dtype=torch.float32).contiguous()
+    o = torch.empty_like(v)
+    s_out = torch.empty(B, HV, K, V, device=q.device, dtype=torch.float32) \
+        if output_final_state else None
+    if T == 0 or B == 0:
+        if s_out is not None:
+            s_out.copy_(s0) if s0 is not None else s_out.zero_()
+        return o, (s_out.to(target_state) if s_out is not None else None)
+    _lib.call(entry, _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(beta),
+              _lib.ptr(s0), _lib.ptr(o), _lib.ptr(s_out), B, T, H, HV, K, V, sc,
+              _clamp_value(g_clamp_min), code, _lib.stream_of(q))
+    if s_out is not None and target_state != torch.float32:
+        s_out = s_out.to(target_state)
+    return o, s_out
+
+
+def naive_chunk_kda(q, k, v, g, beta, scale=None, initial_state=None, output_final_state=False,
+                    chunk_size: int = 64, *, g_clamp_min: float = -10.0, state_dtype=None):
+    """Chunkwise-parallel KDA on the HIP backend (``ops_kda.py:464-494``)."""
+    return _run("kch_kda_chunk_fwd", "naive_chunk_kda", q, k, v, g, beta, scale,
+                initial_state, output_final_state, g_clamp_min, state_dtype, chunk_size)
+
+
+def naive_recurrent_kda(q, k, v, g, beta, scale=None, initial_state=None,
+                        output_final_state=False, *, g_clamp_min: float = -10.0,
+                        state_dtype=None):
+    """Per-token KDA recurrence on the HIP backend (``ops_kda.py:175-267``)."""
+    return _run("kch_kda_recurrent_fwd", "naive_recurrent_kda", q, k, v, g, beta, scale,
+                initial_state, output_final_state, g_clamp_min, state_dtype)
+
+
+chunk_kda = naive_chunk_kda
+recurrent_kda = naive_recurrent_kda

@@ -1,0 +1,344 @@
+"""CSA / HCA oracle: numpy restatement of the reference (test infrastructure only).
+
+Functions and the reference lines each restates:
+
+``compress_kv``              ``csa_compress_kv``            ``ops_csa.py:198-234``
+``compress_kv_overlapped``   ``csa_compress_kv_overlapped`` ``ops_csa.py:237-305``
+``causal_block_mask``        ``_causal_block_mask``         ``ops_csa.py:179-195``
+``lightning_indexer``        ``csa_lightning_indexer``      ``ops_csa.py:330-573``
+                             (forward only; the STE soft weights are training-only)
+``window_scores``            ``_sliding_window_scores``     ``ops_csa.py:151-176``
+``joint_softmax_csa``        joint softmax + sink           ``ops_csa.py:1126-1149``
+``joint_softmax_hca``        joint softmax + sink           ``ops_hca.py:166-186``
+``csa_core``                 ``naive_csa`` after the projections, ``ops_csa.py:869-1165``
+``naive_csa``                ``naive_csa`` incl. bf16 projections, ``ops_csa.py:576-1184``
+``hca_core``                 ``naive_hca`` after the projections, ``ops_hca.py:132-194``
+``naive_hca``                ``naive_hca`` incl. bf16 projections, ``ops_hca.py:30-201``
+
+Tie rule: ``torch.topk`` (``ops_csa.py:550``) does not document its order on
+exactly-equal logits (the reference notes it depends on the tensor size,
+``ops_decoding_cache.py:62-87``). The oracle fixes it as "descending logit,
+then ascending block index" (a stable descending sort), the same rule the HIP
+kernels implement; the order on exact ties is therefore "parity unpinned"
+against torch itself, and the tests compare such indices tie-aware.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from .common import bf16_round, l2_normalize, round_to
+
+NEG_INF = -np.inf
+
+
+def compress_kv(C, Z, B_pos, m, compute=np.float32):
+    """Single-branch softmax-gated compression ``[B,T,c] -> [B,T//m,c]``."""
+    C = np.asarray(C, compute)
+    Z = np.asarray(Z, compute)
+    Bn, T, c = C.shape
+    if m < 1:
+        raise ValueError("m must be >= 1")
+    if T % m:
+        raise ValueError("T must be divisible by m")
+    nb = T // m
+    C = C.reshape(Bn, nb, m, c)
+    logits = Z.reshape(Bn, nb, m, c) + np.asarray(B_pos, compute)[None, None]
+    mx = logits.max(axis=2, keepdims=True)
+    e = np.exp(logits - mx)
+    S = e / e.sum(axis=2, keepdims=True)
+    return (S * C).sum(axis=2)
+
+
+def compress_kv_overlapped(Ca, Cb, Za, Zb, Ba, Bb, m, compute=np.float32):
+    """Two-branch overlapped compression: block i mixes Ca_i with Cb_{i-1}."""
+    Ca, Cb, Za, Zb = (np.asarray(x, compute) for x in (Ca, Cb, Za, Zb))
+    Bn, T, c = Ca.shape
+    if m < 1:
+        raise ValueError("m must be >= 1")
+    if T % m:
+        raise ValueError("T must be divisible by m")
+    if T == 0:
+        return np.zeros((Bn, 0, c), compute)
+    nb = T // m
+    Ca, Cb, Za, Zb = (x.reshape(Bn, nb, m, c) for x in (Ca, Cb, Za, Zb))
+    a_log = Za + np.asarray(Ba, compute)[None, None]
+    zb_prev = np.concatenate([np.full((Bn, 1, m, c), -np.inf, compute), Zb[:, :-1]], axis=1)
+    b_log = zb_prev + np.asarray(Bb, compute)[None, None]
+    allg = np.concatenate([a_log, b_log], axis=2)
+    mx = allg.max(axis=2, keepdims=True)
+    e = np.exp(allg - mx)
+    S = e / e.sum(axis=2, keepdims=True)
+    cb_prev = np.concatenate([np.zeros((Bn, 1, m, c), compute), Cb[:, :-1]], axis=1)
+    return (S[:, :, :m] * Ca).sum(2) + (S[:, :, m:] * cb_prev).sum(2)
+
+
+def causal_block_mask(T, n_blocks, m):
+    """``mask[t, b] = (t + 1) // m > b``."""
+    t = np.arange(T)[:, None]
+    b = np.arange(n_blocks)[None, :]
+    return (t + 1) // m > b
+
+
+def topk_desc_lowest_index(logits, topk):
+    """Top-k along the last axis: descending value, ties by ascending index.
+
+    Entries whose value is +-inf become -1, and the result is padded with -1
+    up to ``topk`` (``ops_csa.py:550-554``).
+    """
+    nb = logits.shape[-1]
+    S = min(topk, nb)
+    order = np.argsort(-logits, axis=-1, kind='stable')[..., :S]
+    vals = np.take_along_axis(logits, order, axis=-1)
+    idx = np.where(np.isinf(vals), -1, order).astype(np.int64)
+    if topk > S:
+        pad = np.full(idx.shape[:-1] + (topk - S,), -1, np.int64)
+        idx = np.concatenate([idx, pad], axis=-1)
+    return idx
+
+
+def indexer_logits(q_idx, k_idx, w_idx, scale=None, causal_block_mask=None,
+                   normalize_qk=False, compute=np.float32):
+    """Head-weighted ReLU scores ``[B, T, n_blocks]`` (``ops_csa.py:503-536``)."""
+    q = np.asarray(q_idx, compute)
+    k = np.asarray(k_idx, compute)
+    DI = q.shape[-1]
+    if scale is None:
+        scale = 1.0 if normalize_qk else DI ** -0.5
+    if normalize_qk:
+        q = l2_normalize(q)
+        k = l2_normalize(k)
+    score = np.maximum(np.einsum('bthd,bnd->bhtn', q, k) * compute(scale), compute(0))
+    if w_idx is None:
+        logits = score.sum(1)
+    else:
+        logits = np.einsum('bhtn,bth->btn', score, np.asarray(w_idx, compute))
+    if causal_block_mask is not None:
+        logits = np.where(causal_block_mask, logits, compute(-np.inf))
+    return logits.astype(compute)
+
+
+def lightning_indexer(q_idx, k_idx, w_idx, topk, scale=None, causal_block_mask=None,
+                      normalize_qk=False, compute=np.float32, return_logits=False):
+    if topk < 0:
+        raise ValueError("topk must be >= 0")
+    logits = indexer_logits(q_idx, k_idx, w_idx, scale, causal_block_mask,
+                            normalize_qk, compute)
+    Bn, T = logits.shape[:2]
+    if topk == 0:
+        idx = np.zeros((Bn, T, 0), np.int64)
+    else:
+        idx = topk_desc_lowest_index(logits, topk)
+    return (idx, logits) if return_logits else idx
+
+
+def window_scores(q, C_local, win, scale):
+    """Per-query causal window scores ``[B,T,nh,win]`` and keys ``[B,T,win,c]``.
+
+    Window slot ``j`` of query ``t`` holds position ``t - win + 1 + j``; slots
+    before position 0 are ``-inf`` (``ops_csa.py:151-176``).
+    """
+    Bn, T, nh, c = q.shape
+    Cp = np.concatenate([np.zeros((Bn, win - 1, c), C_local.dtype), C_local], axis=1)
+    idx = np.arange(T)[:, None] + np.arange(win)[None, :]
+    Cw = Cp[:, idx]                                    # [B, T, win, c]
+    valid = np.arange(win)[None, :] >= (win - 1 - np.arange(T)[:, None])
+    s = np.einsum('bthd,btwd->bthw', q, Cw) * q.dtype.type(scale)
+    s = np.where(valid[None, :, None, :], s, -np.inf)
+    return s, Cw, valid
+
+
+def _logaddexp(a, b):
+    return np.logaddexp(a, b)
+
+
+def _logsumexp(x, axis=-1):
+    mx = np.max(x, axis=axis, keepdims=True)
+    mx_safe = np.where(np.isfinite(mx), mx, 0)
+    with np.errstate(divide='ignore'):
+        return np.log(np.exp(x - mx_safe).sum(axis=axis, keepdims=True)) + mx_safe
+
+
+def joint_softmax_csa(cat, cat_valid, sink):
+    """CSA / decode-cache joint softmax: ``row_max = max(0, max s)``."""
+    all_invalid = ~cat_valid.any(-1, keepdims=True)
+    if sink is not None:
+        row_max = np.maximum(cat.max(-1, keepdims=True), 0)
+        shifted = cat - row_max
+        s_sink = sink - row_max
+        lse = _logsumexp(shifted)
+        log_denom = _logaddexp(lse, s_sink)
+        with np.errstate(invalid='ignore'):
+            p = np.exp(shifted - log_denom) * cat_valid
+    else:
+        safe = np.where(all_invalid, 0, cat)
+        mx = safe.max(-1, keepdims=True)
+        e = np.exp(safe - mx)
+        p = e / e.sum(-1, keepdims=True)
+    return np.where(all_invalid, 0, p).astype(cat.dtype)
+
+
+def joint_softmax_hca(cat, sink):
+    """naive_hca joint softmax: ``row_max = max s`` (0 if all masked)."""
+    all_masked = np.isneginf(cat).all(-1, keepdims=True)
+    if sink is not None:
+        row_max = cat.max(-1, keepdims=True)
+        row_max = np.where(np.isneginf(row_max), 0, row_max)
+        shifted = cat - row_max
+        lse = _logsumexp(shifted)
+        log_denom = _logaddexp(lse, sink - row_max)
+        p = np.exp(shifted - log_denom)
+    else:
+        safe = np.where(all_masked, 0, cat)
+        mx = safe.max(-1, keepdims=True)
+        e = np.exp(safe - mx)
+        p = e / e.sum(-1, keepdims=True)
+    return np.where(all_masked, 0, p).astype(cat.dtype)
+
+
+def _pad_time(x, pad):
+    if not pad:
+        return x
+    w = [(0, 0)] * x.ndim
+    w[1] = (0, pad)
+    return np.pad(x, w)
+
+
+def csa_core(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, *,
+             m, topk, sliding_window=0, sink_logits=None, normalize_qk=True,
+             scale=None, compute=np.float32, return_indices=False):
+    """CSA forward from the projections: ``[B,T,nh,c]`` in ``compute``.
+
+    Inputs are the bf16 projection values (as float arrays): ``Ca..Zb``
+    ``[B,T,c]``, ``K_idx, Z_idx`` ``[B,T,cI]``, ``q`` ``[B,T,nh,c]``,
+    ``q_idx`` ``[B,T,nIh,cI]``, ``w_idx`` ``[B,T,nIh]``.
+    """
+    Bn, T, c = np.shape(Ca)
+    nh = np.shape(q)[2]
+    pad = (-T) % m
+    Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx = (
+        _pad_time(np.asarray(x, compute), pad)
+        for x in (Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx))
+    Tp = T + pad
+    nb = Tp // m
+    C_comp = compress_kv_overlapped(Ca, Cb, Za, Zb, Ba, Bb, m, compute)
+    K_IComp = compress_kv(K_idx, Z_idx, B_idx, m, compute)
+    cbm = causal_block_mask(Tp, nb, m)
+    idx = lightning_indexer(q_idx, K_IComp, w_idx, topk, None, cbm, normalize_qk, compute)
+    if normalize_qk:
+        qn = l2_normalize(q)
+        Cn = l2_normalize(C_comp)
+    else:
+        qn, Cn = q, C_comp
+    if scale is None:
+        scale = 1.0 if normalize_qk else c ** -0.5
+    if idx.shape[-1] == 0:
+        scores = np.zeros((Bn, Tp, nh, 0), compute)
+        valid = np.zeros((Bn, Tp, 0), bool)
+        kv = np.zeros((Bn, Tp, 0, c), compute)
+    else:
+        valid = idx >= 0
+        kv = Cn[np.arange(Bn)[:, None, None], np.maximum(idx, 0)]
+        scores = np.einsum('bthd,btkd->bthk', qn, kv) * compute(scale)
+        scores = np.where(valid[:, :, None, :], scores, -np.inf)
+    if sliding_window > 0:
+        C_local = l2_normalize(Ca) if normalize_qk else Ca
+        sw, Cw, wvalid = window_scores(qn, C_local, sliding_window, scale)
+    else:
+        sw = np.zeros((Bn, Tp, nh, 0), compute)
+        Cw = np.zeros((Bn, Tp, 0, c), compute)
+        wvalid = np.zeros((Tp, 0), bool)
+    cat = np.concatenate([scores, sw], axis=-1).astype(compute)
+    cat_valid = np.concatenate(
+        [valid[:, :, None, :],
+         np.broadcast_to(wvalid[None, :, None, :], (Bn, Tp, 1, wvalid.shape[-1]))], axis=-1)
+    if cat.shape[-1] == 0:
+        out = np.zeros((Bn, Tp, nh, c), compute)
+    else:
+        sink = None if sink_logits is None else np.asarray(sink_logits, compute).reshape(1, 1, nh, 1)
+        p = joint_softmax_csa(cat, cat_valid, sink)
+        k_ = scores.shape[-1]
+        out = (np.einsum('bthk,btkd->bthd', p[..., :k_], kv)
+               + np.einsum('bthw,btwd->bthd', p[..., k_:], Cw))
+    out = out[:, :T].astype(compute)
+    if return_indices:
+        return out, idx[:, :T]
+    return out
+
+
+def hca_core(C, Z, q, B_pos, *, m2, sliding_window=0, sink_logits=None,
+             scale=1.0, C_local_raw=None, compute=np.float32):
+    """HCA forward from the projections: ``[B,T,nh,c]`` in ``compute``."""
+    Bn, T, c = np.shape(C)
+    nh = np.shape(q)[2]
+    pad = (-T) % m2
+    C, Z, q = (_pad_time(np.asarray(x, compute), pad) for x in (C, Z, q))
+    if C_local_raw is not None:
+        C_local_raw = _pad_time(np.asarray(C_local_raw, compute), pad)
+    Tp = T + pad
+    nb = Tp // m2
+    Cn = l2_normalize(compress_kv(C, Z, B_pos, m2, compute))
+    qn = l2_normalize(q)
+    cbm = causal_block_mask(Tp, nb, m2)
+    scores = np.einsum('bthd,bnd->bhtn', qn, Cn) * compute(scale)
+    scores = np.where(cbm[None, None], scores, -np.inf)
+    if sliding_window > 0:
+        C_local = l2_normalize(C if C_local_raw is None else C_local_raw)
+        sw, Cw, _ = window_scores(qn, C_local, sliding_window, scale)
+        sw = sw.transpose(0, 2, 1, 3)
+    else:
+        sw = np.zeros((Bn, nh, Tp, 0), compute)
+        Cw = np.zeros((Bn, Tp, 0, c), compute)
+    cat = np.concatenate([scores, sw], axis=-1).astype(compute)
+    if cat.shape[-1] == 0:
+        out = np.zeros((Bn, Tp, nh, c), compute)
+    else:
+        sink = None if sink_logits is None else np.asarray(sink_logits, compute).reshape(1, nh, 1, 1)
+        p = joint_softmax_hca(cat, sink)
+        out = (np.einsum('bhtn,bnd->bthd', p[..., :nb], Cn)
+               + np.einsum('bhtw,btwd->bthd', p[..., nb:], Cw))
+    return out[:, :T].astype(compute)
+
+
+def linear_lowp(x, W, dtype='bf16'):
+    """``F.linear`` on low-precision tensors: fp32 accumulate, rounded output."""
+    y = np.asarray(x, np.float32) @ np.asarray(W, np.float32).T
+    return round_to(y, dtype)
+
+
+def csa_projections(H, W, dtype='bf16', *, c, cI, nh, nIh):
+    """The fused 6-way projection plus cQ/q/q_idx/w_idx (``ops_csa.py:841-878,923``)."""
+    Bn, T, _ = H.shape
+    Ca = linear_lowp(H, W['W_aKV'], dtype)
+    Cb = linear_lowp(H, W['W_bKV'], dtype)
+    Za = linear_lowp(H, W['W_aZ'], dtype)
+    Zb = linear_lowp(H, W['W_bZ'], dtype)
+    K_idx = linear_lowp(H, W['W_KV_idx'], dtype)
+    Z_idx = linear_lowp(H, W['W_Z_idx'], dtype)
+    cQ = linear_lowp(H, W['W_DQ'], dtype)
+    q_idx = linear_lowp(cQ, W['W_IUQ'], dtype).reshape(Bn, T, nIh, cI)
+    w_idx = linear_lowp(H, W['W_w'], dtype)
+    q = linear_lowp(cQ, W['W_UQ'], dtype).reshape(Bn, T, nh, c)
+    return Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx
+
+
+def naive_csa(H, W, *, m, topk, nh, nIh, c, c_I, sliding_window=0, sink=None,
+              dtype='bf16', normalize_qk=True):
+    """Full CSA forward incl. projections; returns ``[B,T,nh*c]`` rounded to dtype."""
+    Bn, T, _ = H.shape
+    proj = csa_projections(H, W, dtype, c=c, cI=c_I, nh=nh, nIh=nIh)
+    out = csa_core(*proj, W['Ba'], W['Bb'], W['B_idx'], m=m, topk=topk,
+                   sliding_window=sliding_window, sink_logits=sink,
+                   normalize_qk=normalize_qk)
+    return round_to(out.reshape(Bn, T, nh * c), dtype), proj
+
+
+def naive_hca(H, W, *, m2, nh, c, sliding_window=0, sink=None, dtype='bf16'):
+    Bn, T, _ = H.shape
+    C = linear_lowp(H, W['W_KV'], dtype)
+    Z = linear_lowp(H, W['W_Z'], dtype)
+    cQ = linear_lowp(H, W['W_DQ'], dtype)
+    q = linear_lowp(cQ, W['W_UQ'], dtype).reshape(Bn, T, nh, c)
+    out = hca_core(C, Z, q, W['B_pos'], m2=m2, sliding_window=sliding_window,
+                   sink_logits=sink)
+    return round_to(out.reshape(Bn, T, nh * c), dtype), (C, Z, q)

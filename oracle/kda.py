@@ -1,0 +1,155 @@
+"""KDA oracle: numpy restatement of the reference delta rule (test only).
+
+Functions
+---------
+``recurrent_kda``  restates ``naive_recurrent_kda`` (``ops_kda.py:175-267``):
+    per token ``S <- S * exp(g_t)``; ``S += (b_t k_t) (x) (v_t - k_t^T S)``;
+    ``o_t = (scale q_t)^T S`` with the post-update state (``:253-258``).
+``chunk_kda``      restates ``naive_chunk_kda`` (``ops_kda.py:340-536``):
+    right-pad to a multiple of the chunk (``:375-382``), in-chunk cumsum of the
+    clamped gate (``:388-394``), the per-column build of A with
+    ``clamp(max=50)`` on the decay exponent (``:409-417``), the triangular
+    solve and ``(A + I) diag(beta)`` (``:418-421``), ``w``/``u`` (``:423-424``),
+    and the sequential chunk loop (``:509-535``).
+``delta_rule_matrix_form``  an independent fp64 statement of the recurrence
+    as explicit matrices, ``S_t = (I - b k k^T) Diag(exp g) S_{t-1} + b k v^T``
+    (module docstring, ``ops_kda.py:6-9``), used only to pin ``recurrent_kda``.
+
+All functions take float arrays (bf16 inputs are passed as their exact float32
+values) and compute in ``compute`` precision (float32 mirrors the reference's
+fp32 compute dtype, ``ops_kda.py:125-127``). GVA: q/k heads are repeated
+``HV // H`` times (``ops_kda.py:226-227,386-387``).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+
+def _prep_common(q, k, v, g, beta, scale, compute):
+    B, T, H, K = q.shape
+    HV, V = v.shape[2], v.shape[3]
+    if HV % H:
+        raise ValueError("HV must be divisible by H")
+    G = HV // H
+    if scale is None:
+        scale = K ** -0.5
+    q = np.repeat(np.asarray(q, compute), G, axis=2) * compute(scale)
+    k = np.repeat(np.asarray(k, compute), G, axis=2)
+    return (q, k, np.asarray(v, compute), np.asarray(g, compute),
+            np.asarray(beta, compute), B, T, HV, K, V)
+
+
+def recurrent_kda(q, k, v, g, beta, scale=None, initial_state=None,
+                  g_clamp_min=-10.0, compute=np.float32):
+    """Per-token recurrence; returns ``(o [B,T,HV,V], S [B,HV,K,V])``."""
+    q, k, v, g, beta, B, T, HV, K, V = _prep_common(q, k, v, g, beta, scale, compute)
+    if g_clamp_min > -np.inf:
+        g = np.maximum(g, compute(g_clamp_min))
+    S = np.zeros((B, HV, K, V), compute)
+    if initial_state is not None:
+        S = S + np.asarray(initial_state, compute)
+    o = np.zeros((B, T, HV, V), compute)
+    for t in range(T):
+        S = S * np.exp(g[:, t])[..., None]
+        kS = np.einsum('bhk,bhkv->bhv', k[:, t], S)
+        S = S + np.einsum('bhk,bhv->bhkv', beta[:, t][..., None] * k[:, t], v[:, t] - kS)
+        o[:, t] = np.einsum('bhk,bhkv->bhv', q[:, t], S)
+    return o, S
+
+
+def delta_rule_matrix_form(q, k, v, g, beta, scale=None, initial_state=None,
+                           g_clamp_min=-10.0):
+    """fp64 explicit-matrix recurrence (independent pin for the oracle)."""
+    q, k, v, g, beta, B, T, HV, K, V = _prep_common(q, k, v, g, beta, scale, np.float64)
+    if g_clamp_min > -np.inf:
+        g = np.maximum(g, g_clamp_min)
+    S = np.zeros((B, HV, K, V))
+    if initial_state is not None:
+        S = S + np.asarray(initial_state, np.float64)
+    o = np.zeros((B, T, HV, V))
+    eye = np.eye(K)
+    for b in range(B):
+        for h in range(HV):
+            St = S[b, h].copy()
+            for t in range(T):
+                kt = k[b, t, h][:, None]
+                P = eye - beta[b, t, h] * (kt @ kt.T)
+                St = P @ np.diag(np.exp(g[b, t, h])) @ St + beta[b, t, h] * kt @ v[b, t, h][None, :]
+                o[b, t, h] = St.T @ q[b, t, h]
+            S[b, h] = St
+    return o, S
+
+
+def _forward_substitution_unit_lower(N):
+    """Solve ``(I - N) X = N`` for strictly-lower ``N`` (batched, last 2 dims).
+
+    Restates ``torch.linalg.solve_triangular(I - A, A, upper=False)``
+    (``ops_kda.py:418-420``) by row-wise forward substitution.
+    """
+    C = N.shape[-1]
+    X = np.zeros_like(N)
+    for r in range(C):
+        acc = N[..., r, :].copy()
+        if r:
+            acc += np.einsum('...c,...cj->...j', N[..., r, :r], X[..., :r, :])
+        X[..., r, :] = acc
+    return X
+
+
+def chunk_kda(q, k, v, g, beta, scale=None, initial_state=None, chunk_size=64,
+              g_clamp_min=-10.0, compute=np.float32):
+    """Chunkwise WY form; returns ``(o [B,T,HV,V], S [B,HV,K,V])``."""
+    q, k, v, g, beta, B, T, HV, K, V = _prep_common(q, k, v, g, beta, scale, compute)
+    S = np.zeros((B, HV, K, V), compute)
+    if initial_state is not None:
+        S = S + np.asarray(initial_state, compute)
+    if T == 0:
+        return np.zeros((B, 0, HV, V), compute), S
+    C = chunk_size
+    pad = (-T) % C
+    if pad:
+        def _p(x):
+            w = [(0, 0)] * x.ndim
+            w[1] = (0, pad)
+            return np.pad(x, w)
+        q, k, v, g, beta = map(_p, (q, k, v, g, beta))
+    Tp = T + pad
+    NT = Tp // C
+
+    def to_chunks(x):  # [B, Tp, HV, ...] -> [B, HV, NT, C, ...]
+        x = x.reshape(B, NT, C, HV, *x.shape[3:])
+        return np.moveaxis(x, 3, 1)
+
+    q, k, v, g = (to_chunks(x) for x in (q, k, v, g))
+    beta = to_chunks(beta)
+    if g_clamp_min > -np.inf:
+        g = np.maximum(g, compute(g_clamp_min))
+    g = np.cumsum(g, axis=-2, dtype=compute)
+
+    # A[..., j, i] = sum_k k_j exp(min(g_j - g_i, 50)) k_i   (ops_kda.py:409-415)
+    A = np.zeros(g.shape[:-1] + (C,), compute)
+    for i in range(C):
+        gd = np.minimum(g - g[..., i:i + 1, :], compute(50.0))
+        A[..., i] = (k * np.exp(gd) * k[..., i:i + 1, :]).sum(-1)
+    A = A * beta[..., None]
+    upper_incl = np.triu(np.ones((C, C), bool), 0)
+    A = -np.where(upper_incl, compute(0), A)
+    X = _forward_substitution_unit_lower(A)
+    A = (X + np.eye(C, dtype=compute)) * beta[..., None, :]
+    w = A @ (np.exp(g) * k)
+    u = A @ v
+
+    strict_upper = np.triu(np.ones((C, C), bool), 1)
+    o = np.zeros((B, HV, NT, C, V), compute)
+    for n in range(NT):
+        q_i, k_i, u_i, g_i, w_i = q[:, :, n], k[:, :, n], u[:, :, n], g[:, :, n], w[:, :, n]
+        diff = np.minimum(g_i[..., :, None, :] - g_i[..., None, :, :], compute(50.0))
+        Aqk = (q_i[..., :, None, :] * np.exp(diff) * k_i[..., None, :, :]).sum(-1)
+        Aqk = np.where(strict_upper, compute(0), Aqk)
+        v_i = u_i - w_i @ S
+        o[:, :, n] = (q_i * np.exp(g_i)) @ S + Aqk @ v_i
+        S = S * np.exp(g_i[:, :, -1])[..., None]
+        S = S + np.einsum('bhck,bhcv->bhkv', np.exp(g_i[:, :, -1:] - g_i) * k_i, v_i)
+    o = o.reshape(B, HV, Tp, V).transpose(0, 2, 1, 3)[:, :T]
+    return np.ascontiguousarray(o), S
