@@ -306,30 +306,38 @@ __global__ __launch_bounds__(256) void kda_chunk_kernel(KdaParams p) {
 
     // ---------------- stage 3: L and Aqk ----------------
     if (!slow) {
+      // sL / sLop alias the sA / sQ / sB operands: every wave finishes its
+      // products (held in registers) before any wave stores a result.
       constexpr int NTILE = NB * NB;
-      for (int job = wave; job < 2 * NTILE; job += 4) {
+      constexpr int JPW = (2 * NTILE) / 4;  // jobs per wave
+      f32x4 tacc[JPW];
+#pragma unroll
+      for (int jj = 0; jj < JPW; ++jj) {
+        const int job = wave + 4 * jj;
         const int mat = job / NTILE;
         const int ti = (job % NTILE) / NB;
         const int tj = (job % NTILE) % NB;
-        if (tj > ti) {
-          if (mat == 1) {
+        tacc[jj] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (tj <= ti)
+          tacc[jj] = tile_mma(tacc[jj], (mat == 0 ? sA : sQ) + 16 * ti * LDK, LDK,
+                              sB + 16 * tj * LDK, LDK, K);
+      }
+      __syncthreads();  // all reads of sA / sQ / sB done
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              sAqk[(16 * ti + acc_row(e)) * LDC + 16 * tj + acc_col()] = from_f32<OpT>(0.f);
-          }
-          continue;
-        }
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        acc = tile_mma(acc, (mat == 0 ? sA : sQ) + 16 * ti * LDK, LDK, sB + 16 * tj * LDK, LDK, K);
+      for (int jj = 0; jj < JPW; ++jj) {
+        const int job = wave + 4 * jj;
+        const int mat = job / NTILE;
+        const int ti = (job % NTILE) / NB;
+        const int tj = (job % NTILE) % NB;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int r = 16 * ti + acc_row(e), c = 16 * tj + acc_col();
           if (mat == 0) {
-            const float val = (r > c) ? acc[e] * sBeta[r] : 0.f;
+            const float val = (r > c) ? tacc[jj][e] * sBeta[r] : 0.f;
             sL[r * LDF + c] = val;
             sLop[r * LDC + c] = from_f32<OpT>(val);
           } else {
-            sAqk[r * LDC + c] = from_f32<OpT>((c <= r) ? acc[e] : 0.f);
+            sAqk[r * LDC + c] = from_f32<OpT>((c <= r) ? tacc[jj][e] : 0.f);
           }
         }
       }
