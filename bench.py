@@ -135,7 +135,7 @@ def main():
                    "chunk": 64, "state": "fp32", "baseline_config": "configs[1]"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "algorithmic_bytes": bytes_, "kernel": "kda_chunk_kernel<128,64,bf16,bf16>",
+                     "algorithmic_bytes": bytes_, "kernel": "kda_chunk_lp_kernel<128,bf16>",
                      "mfma_tflops": flops / t / 1e12,
                      "mfma_frac": flops / t / 1e12 / BF16_PEAK_TFLOPS},
         "ms_per_step_median": ms_med,

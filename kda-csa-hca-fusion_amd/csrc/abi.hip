@@ -2,6 +2,7 @@
 // Declarations and the reference operator each one replaces: include/kch.h.
 
 #include <cmath>
+#include <cstdint>
 #include <cstdarg>
 #include <cstdio>
 #include <string>
@@ -89,6 +90,13 @@ int kch_kda_chunk_fwd(const void* q, const void* k, const void* v, const void* g
       return hip_status(fn, e);
     }
     return KCH_OK;
+  }
+  if ((long long)T * HV * (K > V ? K : V) >= (1LL << 31) || (long long)T * H * K >= (1LL << 31))
+    return fail(KCH_ERR_UNSUPPORTED, "%s: T * heads * head_dim must stay below 2^31", fn);
+  if (dtype != KCH_DT_F32) {
+    const uintptr_t any = (uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)g | (uintptr_t)o;
+    if (any & 15)
+      return fail(KCH_ERR_INVALID, "%s: q, k, v, g and o must be 16-byte aligned", fn);
   }
   kch::KdaParams p = make_kda(q, k, v, g, beta, s0, o, s_out, B, T, H, HV, K, V, scale, g_clamp_min);
   return hip_status(fn, kch::kda_chunk_dispatch(p, dtype, (hipStream_t)stream));

@@ -1,14 +1,17 @@
 // Device-side helpers shared by the gfx950 kernels of this library.
 //
 // * storage conversions for bf16 / fp16 / fp32 inputs,
-// * the two MFMA shapes used for 16x16 output tiles:
+// * the MFMA shapes used for 16x16 output tiles:
 //     v_mfma_f32_16x16x32_bf16  (gfx950; A/B: 8 bf16 per lane)
 //     v_mfma_f32_16x16x16_bf16  (A/B: 4 bf16 per lane)
 //     v_mfma_f32_16x16x4_f32    (A/B: 1 fp32 per lane)
 //   Lane l of a wave64 holds A row (l % 16) and B column (l % 16); the K
 //   elements it holds are k = KPL*(l / 16) + [0, KPL). The accumulator holds
 //   rows 4*(l / 16) + [0, 4) of column (l % 16).
-// * tile_mma: one 16x16 output tile from operands resident in LDS, with A
+//   One accumulation chain uses a single MFMA shape: feeding the accumulator
+//   of a 16x16x32 bf16 MFMA into a 16x16x16 one gave wrong, timing-dependent
+//   results on gfx950 in this library's kernels.
+// * tile_mma: one 16x16 fp32 output tile from operands resident in LDS, with A
 //   stored row-major [row][k] and B stored transposed [col][k].
 #pragma once
 
@@ -75,28 +78,6 @@ __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 //   B: LDS, transposed, row stride ldb;            B[k][n] at B[n*ldb + k]
 // kd must be a multiple of 16 (bf16) or 4 (fp32).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ f32x4 tile_mma(f32x4 acc, const bf16_t* A, int lda,
-                                          const bf16_t* B, int ldb, int kd) {
-  const int l = lane_id();
-  const int r = l & 15;
-  const bf16_t* a = A + r * lda;
-  const bf16_t* b = B + r * ldb;
-  int k = 0;
-  const int k8 = (l >> 4) * 8;
-  for (; k + 32 <= kd; k += 32) {
-    bf16x8 av = *reinterpret_cast<const bf16x8*>(a + k + k8);
-    bf16x8 bv = *reinterpret_cast<const bf16x8*>(b + k + k8);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc, 0, 0, 0);
-  }
-  if (k < kd) {  // one 16-wide step
-    const int k4 = (l >> 4) * 4;
-    bf16x4 av = *reinterpret_cast<const bf16x4*>(a + k + k4);
-    bf16x4 bv = *reinterpret_cast<const bf16x4*>(b + k + k4);
-    acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, bv, acc, 0, 0, 0);
-  }
-  return acc;
-}
-
 __device__ __forceinline__ f32x4 tile_mma(f32x4 acc, const float* A, int lda,
                                           const float* B, int ldb, int kd) {
   const int l = lane_id();

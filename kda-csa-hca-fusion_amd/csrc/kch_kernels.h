@@ -24,7 +24,8 @@ struct KdaParams {
 };
 
 hipError_t kda_chunk_dispatch(const KdaParams& p, int dtype, hipStream_t stream);
-int kda_chunk_bytes(int K, int dtype);
+// bf16 / fp16 inputs, K in {64, 128}, V a multiple of 64 (kda_chunk_lp.hip)
+hipError_t kda_chunk_lp_dispatch(const KdaParams& p, int dtype, hipStream_t stream);
 hipError_t kda_recurrent_dispatch(const KdaParams& p, int dtype, hipStream_t stream);
 
 }  // namespace kch

@@ -1,4 +1,4 @@
-// KDA chunked prefill for gfx950.
+// KDA chunked prefill for fp32 inputs on gfx950 (bf16 / fp16: kda_chunk_lp.hip).
 //
 // Restates the chunkwise WY/UT form of the reference
 // (/root/reference/ops_kda.py:340-536, naive_chunk_kda) as one fused kernel:
@@ -508,24 +508,14 @@ static hipError_t launch_chunk(const KdaParams& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-int kda_chunk_bytes(int K, int dtype) {
-  if (dtype == DT_F32)
-    return K == 128 ? KdaChunkLayout<128, 32, float>::BYTES : KdaChunkLayout<64, 32, float>::BYTES;
-  return K == 128 ? KdaChunkLayout<128, 64, bf16_t>::BYTES : KdaChunkLayout<64, 64, bf16_t>::BYTES;
-}
-
 hipError_t kda_chunk_dispatch(const KdaParams& p, int dtype, hipStream_t stream) {
   const int K = p.K;
   if (dtype == DT_F32) {
     if (K == 128) return launch_chunk<128, 32, float, float>(p, stream);
     return launch_chunk<64, 32, float, float>(p, stream);
   }
-  if (dtype == DT_BF16) {
-    if (K == 128) return launch_chunk<128, 64, bf16_t, bf16_t>(p, stream);
-    return launch_chunk<64, 64, bf16_t, bf16_t>(p, stream);
-  }
-  if (K == 128) return launch_chunk<128, 64, _Float16, bf16_t>(p, stream);
-  return launch_chunk<64, 64, _Float16, bf16_t>(p, stream);
+  // bf16 / fp16: the 8-wave kernel of kda_chunk_lp.hip
+  return kda_chunk_lp_dispatch(p, dtype, stream);
 }
 
 }  // namespace kch

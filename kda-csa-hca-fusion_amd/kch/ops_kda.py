@@ -95,6 +95,10 @@ def _clamp_value(g_clamp_min) -> float:
     return v if v > -math.inf else -math.inf
 
 
+def _aligned(t):
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
 def _run(entry, fn_name, q, k, v, g, beta, scale, initial_state, output_final_state,
          g_clamp_min, state_dtype, chunk_size=None):
     _validate_kda_inputs(q, k, v, g, beta, fn_name)
@@ -105,7 +109,8 @@ def _run(entry, fn_name, q, k, v, g, beta, scale, initial_state, output_final_st
     HV, V = v.shape[2], v.shape[-1]
     sc = _scale_value(scale, K)
     target_state = state_dtype if state_dtype is not None else torch.float32
-    q, k, v, g, beta = (t.contiguous() for t in (q, k, v, g, beta))
+    # the kernels read 16-byte vectors: contiguous, 16-byte aligned storage
+    q, k, v, g, beta = (_aligned(t.contiguous()) for t in (q, k, v, g, beta))
     s0 = None
     if initial_state is not None:
         s0 = initial_state.to(device=q.device, dtype=torch.float32).contiguous()
