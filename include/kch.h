@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define KCH_ABI_VERSION 1
+#define KCH_ABI_VERSION 2
 
 #define KCH_OK 0
 #define KCH_ERR_INVALID 1     /* bad pointer / shape / argument */
@@ -65,6 +65,84 @@ int kch_kda_recurrent_fwd(const void* q, const void* k, const void* v, const voi
                           const void* beta, const float* s0, void* o, float* s_out,
                           int B, int T, int H, int HV, int K, int V, float scale,
                           float g_clamp_min, int dtype, void* stream);
+
+
+/*
+ * Single-branch softmax-gated KV compression, [B,T,c] -> [B,T/m,c].
+ * Replaces csa_compress_kv (ops_csa.py:198-234); used for the CSA indexer keys
+ * (ops_csa.py:874) and for HCA (ops_hca.py:134).
+ *   C, Z   rows of c values, ld* elements apart (dtype); B_pos [m,c] fp32
+ *   out_raw  [B,T/m,c] fp32 block values, or NULL
+ *   out_key  [B,T/m,c] attention key rows: L2-normalised when `normalize`,
+ *            fp32 when key_f32 else bf16; or NULL
+ *   local    [B,T,c] bf16 per-token window keys L2norm(C) (raw C when not
+ *            `normalize`), or NULL
+ * T must be a multiple of m (callers right-pad as ops_csa.py:772-777 does).
+ */
+int kch_compress(const void* C, long long ldC, const void* Z, long long ldZ, const float* B_pos,
+                 float* out_raw, void* out_key, int key_f32, int normalize, void* local, int B,
+                 int T, int m, int c, int dtype, void* stream);
+
+/*
+ * Two-branch overlapped compression: block i mixes Ca_i with Cb_{i-1}
+ * (block 0: the b-branch has -inf logits and zero values).
+ * Replaces csa_compress_kv_overlapped (ops_csa.py:237-305). Outputs as in
+ * kch_compress; `local` is built from Ca (the CSA window keys,
+ * ops_csa.py:1108-1116).
+ */
+int kch_compress_overlapped(const void* Ca, long long ldCa, const void* Cb, long long ldCb,
+                            const void* Za, long long ldZa, const void* Zb, long long ldZb,
+                            const float* Ba, const float* Bb, float* out_raw, void* out_key,
+                            int key_f32, int normalize, void* local, int B, int T, int m, int c,
+                            int dtype, void* stream);
+
+/*
+ * Lightning indexer + top-k. Replaces csa_lightning_indexer
+ * (ops_csa.py:330-573) in its forward (hard top-k) form.
+ *   q_idx [B,T,nIh,cI] (dtype), k_idx [B,nb,cI] fp32 (already L2-normalised
+ *   when normalize_q), w_idx [B,T,nIh] (dtype) or NULL (= all ones)
+ *   idx_out [B,T,topk] int64 (idx64) or int32: blocks by descending logit,
+ *   ties by ascending index, -1 for masked blocks and padding
+ *   logits_out [B,T,nb] fp32 (masked = -inf) or NULL
+ * Block n is visible to query t when n < (pos0 + t + 1) / m, or always when
+ * dense_visible (decode). nIh in {1,2,4,8,16}; cI in {32,64,128}.
+ */
+int kch_csa_indexer_topk(const void* q_idx, const float* k_idx, const void* w_idx, void* idx_out,
+                         int idx64, float* logits_out, int B, int T, int nb, int nIh, int cI,
+                         int topk, int m, int pos0, int dense_visible, int normalize_q, float scale,
+                         int dtype, void* stream);
+
+/*
+ * CSA core attention over the selected compressed blocks plus the sliding
+ * window, one joint softmax with an optional sink. Replaces the attention part
+ * of naive_csa (ops_csa.py:959-1155).
+ *   q [B,T,nh,hd] (qdtype; L2-normalised in-kernel when normalize_q)
+ *   kv_comp [B,nb,hd] bf16 key/value rows, idx [B,T,topk] int32 (-1 = unused)
+ *   kv_local [B,T,hd] bf16 window rows or NULL; sink [nh] fp32 or NULL
+ *   out [B,T,nh,hd] (odtype)
+ * nh <= 16; hd in {64,128}.
+ */
+int kch_csa_sparse_attn(const void* q, const void* kv_comp, const int* idx, const void* kv_local,
+                        const float* sink, void* out, int B, int T, int nb, int nh, int hd,
+                        int topk, int win, float scale, int normalize_q, int qdtype, int odtype,
+                        void* stream);
+
+/*
+ * HCA core attention: dense MQA over the compressed blocks b < (t+1)/m plus
+ * the window, one joint softmax with an optional sink. Replaces the attention
+ * part of naive_hca (ops_hca.py:136-194). Arguments as kch_csa_sparse_attn.
+ */
+int kch_hca_attn(const void* q, const void* kv_comp, const void* kv_local, const float* sink,
+                 void* out, int B, int T, int nb, int nh, int hd, int m, int win, float scale,
+                 int normalize_q, int qdtype, int odtype, void* stream);
+
+/*
+ * Row-wise L2 normalisation x / max(||x||, 1e-12) (F.normalize, as used at
+ * ops_csa.py:523-525,1110-1112 and ops_hca.py:135,154), or a plain copy when
+ * !normalize. x rows are ldx elements apart; out is [rows,c] fp32 or bf16.
+ */
+int kch_l2norm_rows(const void* x, long long ldx, void* out, int out_f32, int rows, int c,
+                    int normalize, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

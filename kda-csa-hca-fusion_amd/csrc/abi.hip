@@ -8,6 +8,7 @@
 #include <string>
 
 #include "../../include/kch.h"
+#include "kch_csa.h"
 #include "kch_kernels.h"
 
 namespace {
@@ -126,6 +127,126 @@ int kch_kda_recurrent_fwd(const void* q, const void* k, const void* v, const voi
   }
   kch::KdaParams p = make_kda(q, k, v, g, beta, s0, o, s_out, B, T, H, HV, K, V, scale, g_clamp_min);
   return hip_status(fn, kch::kda_recurrent_dispatch(p, dtype, (hipStream_t)stream));
+}
+
+int kch_compress(const void* C, long long ldC, const void* Z, long long ldZ, const float* B_pos,
+                 float* out_raw, void* out_key, int key_f32, int normalize, void* local, int B,
+                 int T, int m, int c, int dtype, void* stream) {
+  const char* fn = "kch_compress";
+  if (!dtype_ok(dtype)) return fail(KCH_ERR_INVALID, "%s: unknown dtype %d", fn, dtype);
+  if (m < 1) return fail(KCH_ERR_INVALID, "%s: compression factor m=%d must be >= 1", fn, m);
+  if (B < 0 || T < 0 || c < 1) return fail(KCH_ERR_INVALID, "%s: bad sizes B=%d T=%d c=%d", fn, B, T, c);
+  if (T % m) return fail(KCH_ERR_INVALID, "%s: T=%d must be divisible by m=%d", fn, T, m);
+  if (c > 128) return fail(KCH_ERR_UNSUPPORTED, "%s: c=%d > 128 not supported", fn, c);
+  if (B * T == 0) return KCH_OK;
+  if (!C || !Z || !B_pos) return fail(KCH_ERR_INVALID, "%s: null input pointer", fn);
+  if (ldC < c || ldZ < c) return fail(KCH_ERR_INVALID, "%s: row strides must be >= c", fn);
+  kch::CompressParams p{C, Z, nullptr, nullptr, ldC, ldZ, 0, 0, B_pos, nullptr, out_raw, out_key,
+                        (kch::bf16_t*)local, B, T, m, c, 0, normalize, key_f32};
+  return hip_status(fn, kch::compress_dispatch(p, dtype, (hipStream_t)stream));
+}
+
+int kch_compress_overlapped(const void* Ca, long long ldCa, const void* Cb, long long ldCb,
+                            const void* Za, long long ldZa, const void* Zb, long long ldZb,
+                            const float* Ba, const float* Bb, float* out_raw, void* out_key,
+                            int key_f32, int normalize, void* local, int B, int T, int m, int c,
+                            int dtype, void* stream) {
+  const char* fn = "kch_compress_overlapped";
+  if (!dtype_ok(dtype)) return fail(KCH_ERR_INVALID, "%s: unknown dtype %d", fn, dtype);
+  if (m < 1) return fail(KCH_ERR_INVALID, "%s: compression factor m=%d must be >= 1", fn, m);
+  if (B < 0 || T < 0 || c < 1) return fail(KCH_ERR_INVALID, "%s: bad sizes B=%d T=%d c=%d", fn, B, T, c);
+  if (T % m) return fail(KCH_ERR_INVALID, "%s: T=%d must be divisible by m=%d", fn, T, m);
+  if (c > 128) return fail(KCH_ERR_UNSUPPORTED, "%s: c=%d > 128 not supported", fn, c);
+  if (B * T == 0) return KCH_OK;
+  if (!Ca || !Cb || !Za || !Zb || !Ba || !Bb) return fail(KCH_ERR_INVALID, "%s: null input pointer", fn);
+  if (ldCa < c || ldCb < c || ldZa < c || ldZb < c)
+    return fail(KCH_ERR_INVALID, "%s: row strides must be >= c", fn);
+  kch::CompressParams p{Ca, Za, Cb, Zb, ldCa, ldZa, ldCb, ldZb, Ba, Bb, out_raw, out_key,
+                        (kch::bf16_t*)local, B, T, m, c, 1, normalize, key_f32};
+  return hip_status(fn, kch::compress_dispatch(p, dtype, (hipStream_t)stream));
+}
+
+int kch_csa_indexer_topk(const void* q_idx, const float* k_idx, const void* w_idx, void* idx_out,
+                         int idx64, float* logits_out, int B, int T, int nb, int nIh, int cI,
+                         int topk, int m, int pos0, int dense_visible, int normalize_q, float scale,
+                         int dtype, void* stream) {
+  const char* fn = "kch_csa_indexer_topk";
+  if (!dtype_ok(dtype)) return fail(KCH_ERR_INVALID, "%s: unknown dtype %d", fn, dtype);
+  if (topk < 0) return fail(KCH_ERR_INVALID, "%s: topk=%d must be >= 0", fn, topk);
+  if (B < 0 || T < 0 || nb < 0 || m < 1 || pos0 < 0)
+    return fail(KCH_ERR_INVALID, "%s: bad sizes B=%d T=%d nb=%d m=%d", fn, B, T, nb, m);
+  if (nIh != 1 && nIh != 2 && nIh != 4 && nIh != 8 && nIh != 16)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: nIh=%d not in {1,2,4,8,16}", fn, nIh);
+  if (cI != 32 && cI != 64 && cI != 128)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: cI=%d not in {32,64,128}", fn, cI);
+  if (B * T == 0 || topk == 0) return KCH_OK;
+  if (!q_idx || !idx_out || (nb > 0 && !k_idx)) return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
+  int ptop = 1;
+  while (ptop < topk) ptop <<= 1;
+  const long long lds = (long long)(16 / nIh) * nb * 4 + (256 + 16) * 4 + (long long)ptop * 8;
+  if (lds > 160 * 1024)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: nb=%d with nIh=%d and topk=%d exceeds the LDS budget", fn,
+                nb, nIh, topk);
+  if (nb == 0) {
+    // no block at all: every slot is -1
+    hipError_t e = hipMemsetAsync(idx_out, 0xff, (size_t)B * T * topk * (idx64 ? 8 : 4), (hipStream_t)stream);
+    return hip_status(fn, e);
+  }
+  kch::IndexerParams p{q_idx, k_idx, w_idx, idx_out, logits_out, B, T, nb, nIh, cI, topk, m,
+                       pos0, normalize_q, idx64, dense_visible, scale};
+  return hip_status(fn, kch::indexer_dispatch(p, dtype, (hipStream_t)stream));
+}
+
+static int check_attn(const char* fn, int B, int T, int nb, int nh, int hd, int qdtype, int odtype) {
+  if (!dtype_ok(qdtype) || !dtype_ok(odtype)) return fail(KCH_ERR_INVALID, "%s: unknown dtype", fn);
+  if (B < 0 || T < 0 || nb < 0) return fail(KCH_ERR_INVALID, "%s: bad sizes", fn);
+  if (nh < 1 || nh > 16) return fail(KCH_ERR_UNSUPPORTED, "%s: nh=%d not in [1, 16]", fn, nh);
+  if (hd != 64 && hd != 128) return fail(KCH_ERR_UNSUPPORTED, "%s: head dim %d not in {64,128}", fn, hd);
+  if (odtype != KCH_DT_F32 && odtype != qdtype)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: output dtype must be fp32 or the query dtype", fn);
+  return KCH_OK;
+}
+
+int kch_csa_sparse_attn(const void* q, const void* kv_comp, const int* idx, const void* kv_local,
+                        const float* sink, void* out, int B, int T, int nb, int nh, int hd,
+                        int topk, int win, float scale, int normalize_q, int qdtype, int odtype,
+                        void* stream) {
+  const char* fn = "kch_csa_sparse_attn";
+  int rc = check_attn(fn, B, T, nb, nh, hd, qdtype, odtype);
+  if (rc) return rc;
+  if (topk < 0 || win < 0) return fail(KCH_ERR_INVALID, "%s: topk / window must be >= 0", fn);
+  if (B * T == 0) return KCH_OK;
+  if (!q || !out || (topk > 0 && (!idx || !kv_comp)) || (win > 0 && !kv_local))
+    return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
+  kch::AttnParams p{q, (const kch::bf16_t*)kv_comp, idx, (const kch::bf16_t*)kv_local, sink, out,
+                    B, T, nb, nh, hd, topk, 1, win, normalize_q, scale};
+  return hip_status(fn, kch::attn_dispatch(p, true, qdtype, odtype, (hipStream_t)stream));
+}
+
+int kch_hca_attn(const void* q, const void* kv_comp, const void* kv_local, const float* sink,
+                 void* out, int B, int T, int nb, int nh, int hd, int m, int win, float scale,
+                 int normalize_q, int qdtype, int odtype, void* stream) {
+  const char* fn = "kch_hca_attn";
+  int rc = check_attn(fn, B, T, nb, nh, hd, qdtype, odtype);
+  if (rc) return rc;
+  if (m < 1 || win < 0) return fail(KCH_ERR_INVALID, "%s: m must be >= 1 and window >= 0", fn);
+  if (B * T == 0) return KCH_OK;
+  if (!q || !out || (nb > 0 && !kv_comp) || (win > 0 && !kv_local))
+    return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
+  kch::AttnParams p{q, (const kch::bf16_t*)kv_comp, nullptr, (const kch::bf16_t*)kv_local, sink,
+                    out, B, T, nb, nh, hd, 0, m, win, normalize_q, scale};
+  return hip_status(fn, kch::attn_dispatch(p, false, qdtype, odtype, (hipStream_t)stream));
+}
+
+int kch_l2norm_rows(const void* x, long long ldx, void* out, int out_f32, int rows, int c,
+                    int normalize, int dtype, void* stream) {
+  const char* fn = "kch_l2norm_rows";
+  if (!dtype_ok(dtype)) return fail(KCH_ERR_INVALID, "%s: unknown dtype %d", fn, dtype);
+  if (rows < 0 || c < 1 || c > 256 || ldx < c) return fail(KCH_ERR_INVALID, "%s: bad sizes", fn);
+  if (rows == 0) return KCH_OK;
+  if (!x || !out) return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
+  return hip_status(fn, kch::l2norm_rows_dispatch(x, ldx, out, out_f32, rows, c, normalize, dtype,
+                                                  (hipStream_t)stream));
 }
 
 }  // extern "C"

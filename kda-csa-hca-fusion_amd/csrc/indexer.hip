@@ -1,0 +1,316 @@
+// Lightning indexer with top-k block selection for gfx950.
+//
+// Restates csa_lightning_indexer (/root/reference/ops_csa.py:330-573), forward:
+//   logits[t, n] = sum_h w_idx[t, h] * relu(scale * <q_idx[t, h], k_idx[n]>)
+//   masked to -inf unless n < (t + 1) // m (ops_csa.py:179-195), then the top
+//   min(topk, n_blocks) blocks by descending logit, -1 for -inf and for padding
+//   (ops_csa.py:550-554). normalize_qk L2-normalises q_idx (here) and k_idx
+//   (by the caller) first (ops_csa.py:503-525).
+// Tie rule on exactly-equal logits: ascending block index (the reference's
+// torch.topk order is unspecified there).
+//
+// Mapping: one wave per group of QPW = 16 / nIh consecutive queries; MFMA
+// column n = (query n / nIh, head n % nIh). Scores use a split-bf16 product
+// (x = hi + lo, hi*hi + hi*lo + lo*hi with fp32 accumulation) so the logits
+// carry ~2^-16 relative error instead of bf16's 2^-8. Per query, the logits sit
+// in LDS; the k-th largest is found by a 4 x 8-bit radix select on
+// order-preserving 32-bit keys, the winners are gathered (ties at the threshold
+// in ascending index order) and bitonic-sorted by (logit desc, index asc).
+
+#include "attn_common.h"
+#include "kch_csa.h"
+
+namespace kch {
+
+namespace {
+
+// Order-preserving map float -> uint32 (larger float, larger key); -0 maps to +0
+// so that the two zeros tie as they do in a float comparison.
+__device__ __forceinline__ uint32_t order_key(float f) {
+  uint32_t u = __float_as_uint(f);
+  if (u == 0x80000000u) u = 0u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ int wave_excl_scan(int v) {
+  const int lane = lane_id();
+  int x = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(x, d);
+    if (lane >= d) x += y;
+  }
+  return x - v;
+}
+
+__device__ __forceinline__ void split_bf16(const float* f, bf16x8& hi, bf16x8& lo) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const bf16_t h = (bf16_t)f[i];
+    hi[i] = h;
+    lo[i] = (bf16_t)(f[i] - (float)h);
+  }
+}
+
+}  // namespace
+
+template <typename QT, int CI>
+__global__ __launch_bounds__(64) void indexer_kernel(IndexerParams p) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  constexpr int NS = CI / 32;
+  const int nIh = p.nIh;
+  const int QPW = 16 / nIh;
+  const int lane = threadIdx.x;
+  const int q4 = lane >> 4, n = lane & 15;
+  const int groups_per_row = (p.T + QPW - 1) / QPW;
+  const int b = blockIdx.x / groups_per_row;
+  const int t0 = (blockIdx.x - b * groups_per_row) * QPW;
+  const int nb = p.nb;
+  const int topk = p.topk;
+
+  const size_t lg_bytes = ((size_t)QPW * nb * 4 + 15) & ~(size_t)15;
+  float* logits = reinterpret_cast<float*>(smem);                       // [QPW][nb]
+  uint32_t* hist = reinterpret_cast<uint32_t*>(smem + lg_bytes);        // [256]
+  unsigned long long* sel = reinterpret_cast<unsigned long long*>(hist + 256 + 16);  // [ptop]
+  int* counters = reinterpret_cast<int*>(hist + 256);
+
+  auto nvis_of = [&](int t) {
+    if (p.dense_visible) return nb;
+    const int v = (p.q_pos0 + t + 1) / p.m;
+    return v < nb ? v : nb;
+  };
+
+  // ---- this lane's query column: query tq = t0 + n / nIh, head h = n % nIh ----
+  const int jq = n / nIh, hh = n - jq * nIh;
+  const int tq = t0 + jq;
+  const bool qok = tq < p.T;
+  bf16x8 qhi[NS], qlo[NS];
+  float wq = 0.f;
+  {
+    float f[NS][8];
+    float ss = 0.f;
+    const QT* qrow = static_cast<const QT*>(p.q_idx) +
+                     (((size_t)b * p.T + (qok ? tq : 0)) * nIh + hh) * CI;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      Load8<QT>::run(qrow + 32 * s + 8 * q4, f[s]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss += f[s][i] * f[s][i];
+    }
+    const float inv = p.normalize_q ? l2_inv(colq_sum(ss)) : 1.f;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) f[s][i] = qok ? f[s][i] * inv : 0.f;
+      split_bf16(f[s], qhi[s], qlo[s]);
+    }
+    if (qok) {
+      const size_t wi = ((size_t)b * p.T + tq) * nIh + hh;
+      wq = p.w_idx ? ld_f32(static_cast<const QT*>(p.w_idx) + wi) : 1.f;
+    }
+  }
+
+  // ---- logits of all blocks visible to any query of the group ----
+  int nv_max = 0;
+  for (int j = 0; j < QPW; ++j)
+    if (t0 + j < p.T) nv_max = max(nv_max, nvis_of(t0 + j));
+  const int nv_me = qok ? nvis_of(tq) : 0;
+  const float* kbase = p.k_idx + (size_t)b * nb * CI;
+  for (int c0 = 0; c0 < nv_max; c0 += 16) {
+    const int r = c0 + n;
+    const float* krow = kbase + (size_t)(r < nb ? r : nb - 1) * CI;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      float f[8];
+      Load8<float>::run(krow + 32 * s + 8 * q4, f);
+      bf16x8 khi, klo;
+      split_bf16(f, khi, klo);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi, qhi[s], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi, qlo[s], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(klo, qhi[s], acc, 0, 0, 0);
+    }
+    // acc[e]: block c0 + 4*q4 + e, column n
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float v = fmaxf(acc[e] * p.scale, 0.f) * wq;
+      // head sum over the nIh adjacent lanes of this query
+      for (int d = 1; d < nIh; d <<= 1) v += __shfl_xor(v, d);
+      const int blk = c0 + 4 * q4 + e;
+      if (hh == 0 && qok && blk < nv_me) logits[jq * nb + blk] = v;
+    }
+  }
+  wave_lds_sync();
+
+  // ---- per query: top-k ----
+  for (int j = 0; j < QPW; ++j) {
+    const int t = t0 + j;
+    if (t >= p.T) break;
+    const int nv = nvis_of(t);
+    const float* lg = logits + (size_t)j * nb;
+    const size_t orow = ((size_t)b * p.T + t) * topk;
+    if (p.logits_out) {
+      for (int i = lane; i < nb; i += 64)
+        p.logits_out[((size_t)b * p.T + t) * nb + i] = i < nv ? lg[i] : -INFINITY;
+    }
+    const int cnt = nv < topk ? nv : topk;
+    if (cnt > 0) {
+      if (nv <= topk) {
+        for (int i = lane; i < nv; i += 64)
+          sel[i] = ((unsigned long long)order_key(lg[i]) << 32) | (uint32_t)(~i);
+      } else {
+        // radix select of the topk-th largest key
+        uint32_t prefix = 0, pmask = 0;
+        int need = topk, above_total = 0;
+        for (int pass = 0; pass < 4; ++pass) {
+          const int shift = 24 - 8 * pass;
+          for (int i = lane; i < 256; i += 64) hist[i] = 0;
+          wave_lds_sync();
+          for (int i = lane; i < nv; i += 64) {
+            const uint32_t u = order_key(lg[i]);
+            if ((u & pmask) == prefix) atomicAdd(&hist[(u >> shift) & 255u], 1u);
+          }
+          wave_lds_sync();
+          // bins in descending order: lane l holds 255-4l .. 252-4l
+          int c[4], tot = 0;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) { c[k] = (int)hist[255 - 4 * lane - k]; tot += c[k]; }
+          int cum = wave_excl_scan(tot);
+          int found_bin = -1, found_above = 0;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            if (found_bin < 0 && cum < need && cum + c[k] >= need) {
+              found_bin = 255 - 4 * lane - k;
+              found_above = cum;
+            }
+            cum += c[k];
+          }
+          const unsigned long long who = __ballot(found_bin >= 0);
+          const int src = __ffsll((long long)who) - 1;
+          const int bin = __shfl(found_bin, src);
+          const int above = __shfl(found_above, src);
+          prefix |= (uint32_t)bin << shift;
+          pmask |= 255u << shift;
+          need -= above;
+          above_total += above;
+        }
+        // gather: keys > threshold anywhere in [0, above_total), ties in index order
+        const uint32_t thr = prefix;
+        if (lane == 0) counters[0] = 0;
+        wave_lds_sync();
+        int ties = 0;
+        for (int base = 0; base < nv; base += 64) {
+          const int i = base + lane;
+          const uint32_t u = i < nv ? order_key(lg[i]) : 0u;
+          const bool gt = i < nv && u > thr;
+          const bool eq = i < nv && u == thr;
+          if (gt) {
+            const int slot = atomicAdd(&counters[0], 1);
+            sel[slot] = ((unsigned long long)u << 32) | (uint32_t)(~i);
+          }
+          const unsigned long long eqm = __ballot(eq);
+          if (eq) {
+            const int rank = ties + __popcll(eqm & ((1ull << lane) - 1ull));
+            if (rank < need) sel[above_total + rank] = ((unsigned long long)u << 32) | (uint32_t)(~i);
+          }
+          ties += __popcll(eqm);
+        }
+      }
+      // pad to a power of two with keys that sort last
+      int pw = 1;
+      while (pw < cnt) pw <<= 1;
+      for (int i = cnt + lane; i < pw; i += 64) sel[i] = 0ull;
+      wave_lds_sync();
+      // bitonic sort, descending
+      for (int k = 2; k <= pw; k <<= 1) {
+        for (int jj = k >> 1; jj > 0; jj >>= 1) {
+          for (int i = lane; i < pw / 2; i += 64) {
+            const int lo = ((i & ~(jj - 1)) << 1) | (i & (jj - 1));
+            const int hi = lo + jj;
+            const unsigned long long a = sel[lo], c2 = sel[hi];
+            const bool desc = (lo & k) == 0;
+            if (desc ? (a < c2) : (a > c2)) { sel[lo] = c2; sel[hi] = a; }
+          }
+          wave_lds_sync();
+        }
+      }
+    }
+    // write indices (-1 beyond the visible count)
+    for (int i = lane; i < topk; i += 64) {
+      int id = -1;
+      if (i < cnt) id = (int)(~(uint32_t)(sel[i] & 0xffffffffull));
+      if (p.idx64) static_cast<long long*>(p.idx_out)[orow + i] = id;
+      else static_cast<int*>(p.idx_out)[orow + i] = id;
+    }
+    wave_lds_sync();
+  }
+}
+
+hipError_t indexer_dispatch(const IndexerParams& p, int dtype, hipStream_t s) {
+  const int QPW = 16 / p.nIh;
+  int ptop = 1;
+  while (ptop < p.topk) ptop <<= 1;
+  const size_t lds = (((size_t)QPW * p.nb * 4 + 15) & ~(size_t)15) + (256 + 16) * 4 + (size_t)ptop * 8;
+  const unsigned groups = (unsigned)(p.B * ((p.T + QPW - 1) / QPW));
+#define KCH_IDX_LAUNCH(QT, CI) \
+  hipLaunchKernelGGL((indexer_kernel<QT, CI>), dim3(groups), dim3(64), lds, s, p)
+  if (dtype == DT_BF16) {
+    if (p.cI == 64) KCH_IDX_LAUNCH(bf16_t, 64);
+    else if (p.cI == 128) KCH_IDX_LAUNCH(bf16_t, 128);
+    else KCH_IDX_LAUNCH(bf16_t, 32);
+  } else if (dtype == DT_F32) {
+    if (p.cI == 64) KCH_IDX_LAUNCH(float, 64);
+    else if (p.cI == 128) KCH_IDX_LAUNCH(float, 128);
+    else KCH_IDX_LAUNCH(float, 32);
+  } else {
+    if (p.cI == 64) KCH_IDX_LAUNCH(_Float16, 64);
+    else if (p.cI == 128) KCH_IDX_LAUNCH(_Float16, 128);
+    else KCH_IDX_LAUNCH(_Float16, 32);
+  }
+#undef KCH_IDX_LAUNCH
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Row-wise L2 normalisation (one wave per row, rows of up to 256 channels).
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void l2norm_rows_kernel(const T* x, long long ldx, void* out,
+                                                          int out_f32, int rows, int c, int normalize) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  float v[4];
+  float ss = 0.f;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int ch = lane + 64 * u;
+    v[u] = ch < c ? to_f32(x[(size_t)row * ldx + ch]) : 0.f;
+    ss += v[u] * v[u];
+  }
+  const float inv = normalize ? l2_inv(wave_sum(ss)) : 1.f;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int ch = lane + 64 * u;
+    if (ch >= c) continue;
+    if (out_f32) static_cast<float*>(out)[(size_t)row * c + ch] = v[u] * inv;
+    else static_cast<bf16_t*>(out)[(size_t)row * c + ch] = (bf16_t)(v[u] * inv);
+  }
+}
+
+hipError_t l2norm_rows_dispatch(const void* x, long long ldx, void* out, int out_f32, int rows,
+                                int c, int normalize, int dtype, hipStream_t s) {
+  const dim3 grid((rows + 3) / 4), block(256);
+  if (dtype == DT_F32)
+    hipLaunchKernelGGL((l2norm_rows_kernel<float>), grid, block, 0, s, static_cast<const float*>(x), ldx,
+                       out, out_f32, rows, c, normalize);
+  else if (dtype == DT_BF16)
+    hipLaunchKernelGGL((l2norm_rows_kernel<bf16_t>), grid, block, 0, s, static_cast<const bf16_t*>(x),
+                       ldx, out, out_f32, rows, c, normalize);
+  else
+    hipLaunchKernelGGL((l2norm_rows_kernel<_Float16>), grid, block, 0, s,
+                       static_cast<const _Float16*>(x), ldx, out, out_f32, rows, c, normalize);
+  return hipGetLastError();
+}
+
+}  // namespace kch

@@ -1,0 +1,55 @@
+// Internal launch interface of the CSA / HCA kernels (csa_hca.hip, indexer.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "kch_device.h"
+
+namespace kch {
+
+// KV compression. Rows of C*/Z* are `ld*` elements apart ([B, T] rows of c
+// channels each); B_pos / Ba / Bb are fp32 [m, c].
+struct CompressParams {
+  const void* Ca; const void* Za; const void* Cb; const void* Zb;
+  long long ldCa, ldZa, ldCb, ldZb;
+  const float* Ba; const float* Bb;
+  float* out_raw;   // [B, nb, c] fp32 or null
+  void* out_key;    // [B, nb, c] bf16 / fp32 (key_f32) or null
+  bf16_t* local;    // [B, T, c] bf16 window keys (from Ca) or null
+  int B, T, m, c;
+  int overlap, normalize, key_f32;
+};
+hipError_t compress_dispatch(const CompressParams& p, int dtype, hipStream_t stream);
+
+// Joint-softmax MQA (prefill: one query per token of [B, T]).
+struct AttnParams {
+  const void* q;            // [B, T, nh, hd] (raw; normalised in-kernel if normalize_q)
+  const bf16_t* kv_comp;    // [B, nb, hd] key/value rows
+  const int* idx;           // [B, T, topk] selected rows (sparse) or null
+  const bf16_t* kv_local;   // [B, T, hd] window rows or null
+  const float* sink;        // [nh] or null
+  void* out;                // [B, T, nh, hd]
+  int B, T, nb, nh, hd, topk, m, win, normalize_q;
+  float scale;
+};
+hipError_t attn_dispatch(const AttnParams& p, bool sparse, int qdtype, int odtype, hipStream_t s);
+
+// Lightning indexer + top-k.
+struct IndexerParams {
+  const void* q_idx;     // [B, T, nIh, cI]
+  const float* k_idx;    // [B, nb, cI] fp32 (already L2-normalised when normalize)
+  const void* w_idx;     // [B, T, nIh] or null (= ones)
+  void* idx_out;         // [B, T, topk] int32 or int64
+  float* logits_out;     // optional [B, T, nb] fp32 (diagnostics / tests) or null
+  int B, T, nb, nIh, cI, topk, m;
+  int q_pos0;            // position of query 0 (decode: the cache's token index)
+  int normalize_q, idx64, dense_visible;  // dense_visible: every block visible
+  float scale;
+};
+hipError_t indexer_dispatch(const IndexerParams& p, int dtype, hipStream_t s);
+
+// Row-wise L2 normalisation: out[r] = x[r] / max(||x[r]||, 1e-12) (or a copy).
+hipError_t l2norm_rows_dispatch(const void* x, long long ldx, void* out, int out_f32, int rows,
+                                int c, int normalize, int dtype, hipStream_t s);
+
+}  // namespace kch

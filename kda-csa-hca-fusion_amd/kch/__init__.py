@@ -5,11 +5,22 @@ running hand-written HIP kernels from ``libkch.so`` through the C ABI declared
 in ``include/kch.h``. Tensors must be on a ROCm GPU; there is no CPU path.
 """
 
+from .ops_csa import (csa_compress_kv, csa_compress_kv_overlapped, csa_core,
+                      csa_lightning_indexer, l2_normalize_rows, naive_csa)
+from .ops_hca import hca_core, naive_hca
 from .ops_kda import naive_chunk_kda, naive_recurrent_kda
 from .ops_kda_backend import hip_available, kda_forward, validate_kda_backend
 
 __all__ = [
+    "csa_compress_kv",
+    "csa_compress_kv_overlapped",
+    "csa_core",
+    "hca_core",
+    "csa_lightning_indexer",
     "hip_available",
+    "l2_normalize_rows",
+    "naive_csa",
+    "naive_hca",
     "kda_forward",
     "naive_chunk_kda",
     "naive_recurrent_kda",

@@ -22,11 +22,19 @@ _lib = None
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _F = ctypes.c_float
+_L = ctypes.c_longlong
 
 # name -> argument types (all return int status)
 _SIGNATURES = {
     "kch_kda_chunk_fwd": [_P] * 8 + [_I] * 6 + [_F, _F, _I, _P],
     "kch_kda_recurrent_fwd": [_P] * 8 + [_I] * 6 + [_F, _F, _I, _P],
+    "kch_compress": [_P, _L, _P, _L, _P, _P, _P, _I, _I, _P, _I, _I, _I, _I, _I, _P],
+    "kch_compress_overlapped": [_P, _L, _P, _L, _P, _L, _P, _L, _P, _P, _P, _P, _I, _I, _P,
+                                _I, _I, _I, _I, _I, _P],
+    "kch_csa_indexer_topk": [_P] * 4 + [_I, _P] + [_I] * 10 + [_F, _I, _P],
+    "kch_csa_sparse_attn": [_P] * 6 + [_I] * 7 + [_F, _I, _I, _I, _P],
+    "kch_hca_attn": [_P] * 5 + [_I] * 7 + [_F, _I, _I, _I, _P],
+    "kch_l2norm_rows": [_P, _L, _P, _I, _I, _I, _I, _I, _P],
 }
 
 EXPORTED = ["kch_abi_version", "kch_last_error"] + sorted(_SIGNATURES)

@@ -1,0 +1,346 @@
+"""CSA operators on the HIP backend (drop-in twins of the reference's ``ops_csa``).
+
+``csa_compress_kv``             <- ``/root/reference/ops_csa.py:198-234``
+``csa_compress_kv_overlapped``  <- ``/root/reference/ops_csa.py:237-305``
+``csa_lightning_indexer``       <- ``/root/reference/ops_csa.py:330-573`` (forward)
+``naive_csa``                   <- ``/root/reference/ops_csa.py:576-1184`` (forward)
+
+Same signatures, argument meaning and validation messages as the reference.
+The projections are plain ``F.linear`` GEMMs on the GPU (the reference's own
+fused 6-way weight concatenation, ``ops_csa.py:837-850``); compression, the
+indexer with top-k selection and the joint sparse + window + sink attention
+run in ``libkch.so``.
+
+Differences, all documented:
+
+* Forward only: autograd through the HIP kernels is not provided. With
+  ``use_ste=True`` the reference's forward value is the hard top-k path
+  (the straight-through surrogate adds zero in the forward pass), which is
+  what these twins return.
+* Exactly-equal indexer logits are ordered by ascending block index (the
+  reference's ``torch.topk`` leaves that order unspecified).
+* Attention keys/values are the L2-normalised compressed rows rounded to
+  bfloat16 (the reference keeps them in fp32); scores and the softmax are fp32.
+* float64 inputs raise ``NotImplementedError``.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+
+
+def _check_gpu_dtype(fn, *ts):
+    _lib.require_gpu(fn, *ts)
+    for t in ts:
+        if t is not None and t.dtype == torch.float64:
+            raise NotImplementedError(f"{fn}: float64 inputs are not supported by the HIP kernels")
+
+
+def _rows(x):
+    """(tensor, row stride) for a [B, T, c] tensor whose rows may be strided."""
+    if (x.dim() == 3 and x.stride(-1) == 1 and x.stride(0) == x.shape[1] * x.stride(1)
+            and x.data_ptr() % 16 == 0):
+        return x, x.stride(1)
+    x = x.contiguous()
+    return x, x.shape[-1]
+
+
+def _aligned(t):
+    """Contiguous, 16-byte aligned storage (the kernels read 16-byte vectors)."""
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+def _f32(t, device):
+    return t.detach().to(device=device, dtype=torch.float32).contiguous()
+
+
+def _compress(fn, C, Z, B_pos, m, *, out_raw=True, key=None, normalize=False, local=None):
+    B_, T, c = C.shape
+    if m < 1:
+        raise ValueError(f"compression factor m={m} must be >= 1")
+    if T % m != 0:
+        raise ValueError(f"T={T} must be divisible by m={m}")
+    _check_gpu_dtype(fn, C, Z)
+    nb = T // m
+    C, ldc = _rows(C)
+    Z, ldz = _rows(Z)
+    bpos = _f32(B_pos, C.device)
+    raw = torch.empty(B_, nb, c, device=C.device, dtype=torch.float32) if out_raw else None
+    key_f32 = 1 if (key is not None and key.dtype == torch.float32) else 0
+    _lib.call("kch_compress", _lib.ptr(C), ldc, _lib.ptr(Z), ldz, _lib.ptr(bpos), _lib.ptr(raw),
+              _lib.ptr(key), key_f32, int(normalize), _lib.ptr(local), B_, T, m, c,
+              _lib.dtype_code(fn, C.dtype), _lib.stream_of(C))
+    return raw
+
+
+def _compress_overlapped(fn, Ca, Cb, Za, Zb, Ba, Bb, m, *, out_raw=True, key=None,
+                         normalize=False, local=None):
+    B_, T, c = Ca.shape
+    if m < 1:
+        raise ValueError(f"compression factor m={m} must be >= 1")
+    if T % m != 0:
+        raise ValueError(f"T={T} must be divisible by m={m}")
+    if T == 0:
+        return Ca.new_zeros(B_, 0, c)
+    _check_gpu_dtype(fn, Ca, Cb, Za, Zb)
+    nb = T // m
+    (Ca, lca), (Cb, lcb), (Za, lza), (Zb, lzb) = (_rows(x) for x in (Ca, Cb, Za, Zb))
+    ba, bb = _f32(Ba, Ca.device), _f32(Bb, Ca.device)
+    raw = torch.empty(B_, nb, c, device=Ca.device, dtype=torch.float32) if out_raw else None
+    key_f32 = 1 if (key is not None and key.dtype == torch.float32) else 0
+    _lib.call("kch_compress_overlapped", _lib.ptr(Ca), lca, _lib.ptr(Cb), lcb, _lib.ptr(Za), lza,
+              _lib.ptr(Zb), lzb, _lib.ptr(ba), _lib.ptr(bb), _lib.ptr(raw), _lib.ptr(key),
+              key_f32, int(normalize), _lib.ptr(local), B_, T, m, c,
+              _lib.dtype_code(fn, Ca.dtype), _lib.stream_of(Ca))
+    return raw
+
+
+def csa_compress_kv(C, Z, B_pos, m):
+    """Single-branch compression ``[B, T, c] -> [B, T//m, c]`` in fp32 (``ops_csa.py:198-234``)."""
+    return _compress("csa_compress_kv", C, Z, B_pos, m)
+
+
+def csa_compress_kv_overlapped(Ca, Cb, Za, Zb, Ba, Bb, m):
+    """Two-branch overlapped compression in fp32 (``ops_csa.py:237-305``)."""
+    return _compress_overlapped("csa_compress_kv_overlapped", Ca, Cb, Za, Zb, Ba, Bb, m)
+
+
+def l2_normalize_rows(x, *, out_dtype=torch.float32, normalize=True):
+    """``F.normalize(x, dim=-1)`` over the last axis on the GPU (or a dtype copy)."""
+    shape = x.shape
+    c = shape[-1]
+    x2 = x.reshape(-1, c)
+    if x2.stride(-1) != 1 or x2.data_ptr() % 16 != 0:
+        x2 = x2.contiguous()
+    out = torch.empty(x2.shape[0], c, device=x.device, dtype=out_dtype)
+    _lib.call("kch_l2norm_rows", _lib.ptr(x2), x2.stride(0), _lib.ptr(out),
+              1 if out_dtype == torch.float32 else 0, x2.shape[0], c, int(normalize),
+              _lib.dtype_code("l2_normalize_rows", x.dtype), _lib.stream_of(x))
+    return out.view(*shape)
+
+
+def _standard_block_mask_m(mask, T, n_blocks):
+    """Return m when ``mask`` equals ``(t + 1) // m > b`` (``ops_csa.py:179-195``), else None."""
+    if mask.shape != (T, n_blocks):
+        return None
+    counts = mask.sum(-1)
+    nz = torch.nonzero(counts)
+    if nz.numel() == 0:
+        return 0  # nothing visible anywhere
+    m = int(nz[0, 0].item()) + 1
+    t = torch.arange(T, device=mask.device)
+    b = torch.arange(n_blocks, device=mask.device)
+    expect = (t[:, None] + 1) // m > b[None, :]
+    return m if bool(torch.equal(expect, mask.to(torch.bool))) else None
+
+
+def _indexer(fn, q_idx, k_norm, w_idx, topk, scale, m, *, dense, pos0=0, normalize_q,
+             idx64=True, want_logits=False):
+    B_, T, HI, DI = q_idx.shape
+    nb = k_norm.shape[1]
+    q_idx = _aligned(q_idx)
+    if w_idx is not None:
+        w_idx = w_idx.to(q_idx.dtype).contiguous()
+    idx = torch.empty(B_, T, topk, device=q_idx.device,
+                      dtype=torch.int64 if idx64 else torch.int32)
+    logits = (torch.empty(B_, T, nb, device=q_idx.device, dtype=torch.float32)
+              if want_logits else None)
+    _lib.call("kch_csa_indexer_topk", _lib.ptr(q_idx), _lib.ptr(k_norm), _lib.ptr(w_idx),
+              _lib.ptr(idx), 1 if idx64 else 0, _lib.ptr(logits), B_, T, nb, HI, DI, topk,
+              max(int(m), 1), pos0, int(dense), int(normalize_q), float(scale),
+              _lib.dtype_code(fn, q_idx.dtype), _lib.stream_of(q_idx))
+    return idx, logits
+
+
+def _nan_safe_softmax(logits, dim=-1):
+    all_masked = logits.isinf().all(dim=dim, keepdim=True)
+    soft = torch.softmax(logits.masked_fill(all_masked, 0.0), dim=dim)
+    return soft.masked_fill(all_masked, 0.0)
+
+
+def csa_lightning_indexer(q_idx, k_idx, w_idx, topk, scale=None, causal_block_mask=None,
+                          return_soft_weights=False, *, ste_mode='topk_columns',
+                          normalize_qk=False):
+    """Top-k selection over compressed indexer keys (``ops_csa.py:330-573``).
+
+    Returns int64 indices ``[B, T, topk]`` (descending logit, ties by ascending
+    block index, -1 for masked blocks and padding); with
+    ``return_soft_weights`` also the NaN-safe softmax of the logits.
+    ``causal_block_mask`` must be ``None`` or the standard block-causal mask.
+    """
+    fn = "csa_lightning_indexer"
+    if topk < 0:
+        raise ValueError(f"topk={topk} must be >= 0 (0 selects zero blocks)")
+    if q_idx.shape[-1] < 1:
+        raise ValueError(
+            f"q_idx.shape[-1]={q_idx.shape[-1]} must be >= 1 "
+            f"(indexer key dimension c_I must be positive)")
+    if ste_mode not in ('topk_columns', 'full_softmax', 'aux_contrastive'):
+        raise ValueError(
+            f"ste_mode={ste_mode!r} must be one of 'topk_columns', "
+            f"'full_softmax', or 'aux_contrastive'.")
+    if ste_mode == 'aux_contrastive':
+        raise NotImplementedError(
+            "ste_mode='aux_contrastive' is reserved for a future implementation of "
+            "DeepSeek-V4's contrastive auxiliary loss on the indexer selection logits.")
+    _check_gpu_dtype(fn, q_idx, k_idx, w_idx)
+    if scale is None:
+        scale = 1.0 if normalize_qk else q_idx.shape[-1] ** -0.5
+    B_, T, HI, DI = q_idx.shape
+    n_blocks = k_idx.shape[1]
+    dense, m = True, 1
+    if causal_block_mask is not None:
+        m = _standard_block_mask_m(causal_block_mask.to(q_idx.device), T, n_blocks)
+        if m is None:
+            raise NotImplementedError(
+                f"{fn}: the HIP backend supports causal_block_mask=None or the standard "
+                f"block-causal mask (t + 1) // m > b only")
+        dense = False
+    k_norm = l2_normalize_rows(k_idx, normalize=normalize_qk)
+    q_idx = _aligned(q_idx)
+    if m == 0:  # mask with no visible block
+        idx = torch.full((B_, T, topk), -1, dtype=torch.int64, device=q_idx.device)
+        logits = torch.full((B_, T, n_blocks), float('-inf'), device=q_idx.device)
+    elif topk == 0:
+        idx = torch.zeros(B_, T, 0, dtype=torch.long, device=q_idx.device)
+        logits = None
+        if return_soft_weights:
+            _, logits = _indexer(fn, q_idx, k_norm, w_idx, 1, scale, m, dense=dense,
+                                 normalize_q=normalize_qk, want_logits=True)
+    else:
+        idx, logits = _indexer(fn, q_idx, k_norm, w_idx, topk, scale, m, dense=dense,
+                               normalize_q=normalize_qk, want_logits=return_soft_weights)
+    if return_soft_weights:
+        return idx, _nan_safe_softmax(logits, dim=-1)
+    return idx
+
+
+def csa_core(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, *, m, topk,
+             sliding_window=0, sink_logits=None, normalize_qk=True, scale=None,
+             return_indices=False):
+    """CSA after the projections (``ops_csa.py:869-1155``) on the HIP backend.
+
+    ``Ca..Zb`` ``[B,T,c]``, ``K_idx, Z_idx`` ``[B,T,c_I]``, ``q`` ``[B,T,nh,c]``,
+    ``q_idx`` ``[B,T,nIh,c_I]``, ``w_idx`` ``[B,T,nIh]`` (rows may be strided
+    views of one fused projection), T a multiple of m. Returns ``[B,T,nh,c]``
+    in ``q.dtype`` (and the int32 selection ``[B,T,topk]`` when asked).
+    """
+    fn = "csa_core"
+    B_, T, c = Ca.shape
+    nh, c_I, nIh = q.shape[2], K_idx.shape[-1], q_idx.shape[2]
+    device = Ca.device
+    n_blocks = T // m
+    kv = torch.empty(B_, n_blocks, c, device=device, dtype=torch.bfloat16)
+    local = (torch.empty(B_, T, c, device=device, dtype=torch.bfloat16)
+             if sliding_window > 0 else None)
+    _compress_overlapped(fn, Ca, Cb, Za, Zb, Ba, Bb, m, out_raw=False, key=kv,
+                         normalize=normalize_qk, local=local)
+    k_norm = torch.empty(B_, n_blocks, c_I, device=device, dtype=torch.float32)
+    _compress(fn, K_idx, Z_idx, B_idx, m, out_raw=False, key=k_norm, normalize=normalize_qk)
+    if scale is None:
+        scale = 1.0 if normalize_qk else c ** -0.5
+    idx = None
+    if topk > 0:
+        idx, _ = _indexer(fn, q_idx, k_norm, w_idx, topk, 1.0 if normalize_qk else c_I ** -0.5,
+                          m, dense=False, normalize_q=normalize_qk, idx64=False)
+    sink = None if sink_logits is None else _f32(sink_logits, device)
+    qc = _aligned(q)
+    out = torch.empty(B_, T, nh, c, device=device, dtype=q.dtype)
+    code = _lib.dtype_code(fn, q.dtype)
+    _lib.call("kch_csa_sparse_attn", _lib.ptr(qc), _lib.ptr(kv), _lib.ptr(idx), _lib.ptr(local),
+              _lib.ptr(sink), _lib.ptr(out), B_, T, n_blocks, nh, c, topk, sliding_window,
+              float(scale), int(normalize_qk), code, code, _lib.stream_of(qc))
+    if return_indices:
+        return out, idx
+    return out
+
+
+def naive_csa(H, W_aKV, W_bKV, W_aZ, W_bZ, Ba, Bb, W_DQ, W_UQ, W_IUQ, W_w, W_KV_idx, W_Z_idx,
+              B_idx, *, m, topk, nh, nIh, c, c_I, dc, scale=None, sliding_window=0,
+              sink_logits=None, use_ste=True, ste_mode='topk_columns', normalize_qk=False,
+              fuse_projections=True, return_projections=False):
+    """CSA forward on the HIP backend (``ops_csa.py:576-1184``); returns ``[B, T, nh*c]``."""
+    fn = "naive_csa"
+    B_, T, d = H.shape
+    if m < 1:
+        raise ValueError(f"compression factor m={m} must be >= 1")
+    if topk < 0:
+        raise ValueError(f"topk={topk} must be >= 0 (0 disables sparse selection)")
+    if nh < 1:
+        raise ValueError(f"nh={nh} must be >= 1")
+    if c < 1:
+        raise ValueError(f"c={c} must be >= 1")
+    if dc < 1:
+        raise ValueError(f"dc={dc} must be >= 1")
+    if c_I < 1:
+        raise ValueError(f"c_I={c_I} must be >= 1 (indexer key dim)")
+    if nIh < 1:
+        raise ValueError(f"nIh={nIh} must be >= 1 (indexer head count)")
+    if sliding_window < 0:
+        raise ValueError(
+            f"sliding_window={sliding_window} must be >= 0 (0 disables the branch)")
+    if ste_mode not in ('topk_columns', 'full_softmax', 'aux_contrastive'):
+        raise ValueError(
+            f"ste_mode={ste_mode!r} must be one of 'topk_columns', "
+            f"'full_softmax', or 'aux_contrastive'.")
+    device = H.device
+    if T == 0:
+        out_empty = torch.zeros(B_, 0, nh * c, dtype=H.dtype, device=device)
+        if return_projections:
+            z = lambda w: torch.zeros(B_, 0, w, dtype=H.dtype, device=device)  # noqa: E731
+            return out_empty, (z(c), z(c), z(c), z(c), z(c_I), z(c_I))
+        return out_empty
+    for _w_name, _w in [('W_aKV', W_aKV), ('W_bKV', W_bKV), ('W_aZ', W_aZ), ('W_bZ', W_bZ),
+                        ('W_KV_idx', W_KV_idx), ('W_Z_idx', W_Z_idx)]:
+        if _w.device != H.device:
+            raise ValueError(
+                f"naive_csa: {_w_name}.device={_w.device} does not match "
+                f"H.device={H.device}. All weights must be on the same "
+                f"device as the input.")
+        if _w.dtype != H.dtype:
+            raise ValueError(
+                f"naive_csa: {_w_name}.dtype={_w.dtype} does not match "
+                f"H.dtype={H.dtype}. All weights must share the input's "
+                f"dtype (cast before calling if needed).")
+        if _w.shape[1] != d:
+            raise ValueError(
+                f"naive_csa: {_w_name}.shape={tuple(_w.shape)} — second dim "
+                f"(in_features) must equal d={d} (H.shape[-1]).")
+    _check_gpu_dtype(fn, H)
+    if nh > 16 or c not in (64, 128) or c_I not in (32, 64, 128) or nIh not in (1, 2, 4, 8, 16):
+        raise NotImplementedError(
+            f"{fn}: HIP kernels cover nh <= 16, c in (64, 128), c_I in (32, 64, 128), "
+            f"nIh in (1, 2, 4, 8, 16); got nh={nh}, c={c}, c_I={c_I}, nIh={nIh}")
+    original_T = T
+    pad = (-T) % m
+    if pad:
+        H = F.pad(H, (0, 0, 0, pad))
+        T = T + pad
+    n_blocks = T // m
+    with torch.no_grad():
+        if fuse_projections:
+            comb = F.linear(H, torch.cat([W_aKV, W_bKV, W_aZ, W_bZ, W_KV_idx, W_Z_idx], dim=0))
+            Ca, Cb, Za, Zb, K_idx_raw, Z_idx = comb.split([c, c, c, c, c_I, c_I], dim=-1)
+        else:
+            Ca, Cb, Za, Zb = (F.linear(H, w) for w in (W_aKV, W_bKV, W_aZ, W_bZ))
+            K_idx_raw, Z_idx = F.linear(H, W_KV_idx), F.linear(H, W_Z_idx)
+        cQ = F.linear(H, W_DQ)
+        q_idx = F.linear(cQ, W_IUQ).view(B_, T, nIh, c_I)
+        w_idx = F.linear(H, W_w)
+        q = F.linear(cQ, W_UQ).view(B_, T, nh, c)
+        out = csa_core(Ca, Cb, Za, Zb, K_idx_raw, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, m=m,
+                       topk=topk, sliding_window=sliding_window, sink_logits=sink_logits,
+                       normalize_qk=normalize_qk, scale=scale)
+    out_final = out.reshape(B_, T, nh * c)[:, :original_T]
+    if return_projections:
+        projections = tuple(x[:, :original_T] for x in (Ca, Cb, Za, Zb, K_idx_raw, Z_idx))
+        return out_final, projections
+    return out_final
+
+
+__all__ = ["csa_compress_kv", "csa_compress_kv_overlapped", "csa_core", "csa_lightning_indexer",
+           "naive_csa", "l2_normalize_rows"]

@@ -1,0 +1,122 @@
+"""HCA operator on the HIP backend (drop-in twin of ``/root/reference/ops_hca.py:30-201``).
+
+Same signature, validation (``ValueError`` / ``TypeError`` messages of
+``ops_hca.py:73-115``) and padding contract. The projections are ``F.linear``
+GEMMs on the GPU; the heavy compression (with L2-normalised bf16 key rows and
+the per-token window keys) and the dense MQA over compressed blocks + window +
+sink run in ``libkch.so``. Forward only; keys/values are bf16-rounded
+L2-normalised rows (fp32 in the reference); float64 is not supported.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+from .ops_csa import _aligned, _check_gpu_dtype, _compress, _f32, l2_normalize_rows
+
+
+def hca_core(C, Z, q, B_pos, *, m2, sliding_window=0, sink_logits=None, scale=1.0,
+             C_local_raw=None):
+    """HCA after the projections (``ops_hca.py:132-194``) on the HIP backend.
+
+    ``C, Z`` ``[B,T,c]`` (rows may be strided views), ``q`` ``[B,T,nh,c]``, T a
+    multiple of m2; the window keys are L2norm(C) or L2norm(``C_local_raw``).
+    Returns ``[B,T,nh,c]`` in ``q.dtype``.
+    """
+    fn = "hca_core"
+    B_, T, c = C.shape
+    nh = q.shape[2]
+    device = C.device
+    n_blocks = T // m2
+    kv = torch.empty(B_, n_blocks, c, device=device, dtype=torch.bfloat16)
+    local = None
+    if sliding_window > 0:
+        if C_local_raw is None:
+            local = torch.empty(B_, T, c, device=device, dtype=torch.bfloat16)
+        else:
+            local = l2_normalize_rows(C_local_raw, out_dtype=torch.bfloat16)
+    _compress(fn, C, Z, B_pos, m2, out_raw=False, key=kv, normalize=True,
+              local=local if C_local_raw is None else None)
+    sink = None if sink_logits is None else _f32(sink_logits, device)
+    qc = _aligned(q)
+    out = torch.empty(B_, T, nh, c, device=device, dtype=q.dtype)
+    code = _lib.dtype_code(fn, q.dtype)
+    _lib.call("kch_hca_attn", _lib.ptr(qc), _lib.ptr(kv), _lib.ptr(local), _lib.ptr(sink),
+              _lib.ptr(out), B_, T, n_blocks, nh, c, m2, sliding_window, float(scale), 1,
+              code, code, _lib.stream_of(qc))
+    return out
+
+
+def naive_hca(H, W_KV, W_Z, B_pos, W_DQ, W_UQ, *, m2, nh, c, dc, scale=1.0, sliding_window=0,
+              sink_logits=None, return_projections=False, W_KV_local=None):
+    """HCA forward on the HIP backend; returns ``[B, T, nh*c]`` in ``H.dtype``."""
+    fn = "naive_hca"
+    B_, T, d = H.shape
+    if m2 < 1:
+        raise ValueError(f"heavy compression factor m2={m2} must be >= 1")
+    if nh < 1:
+        raise ValueError(f"nh={nh} must be >= 1")
+    if c < 1:
+        raise ValueError(f"c={c} must be >= 1")
+    if dc < 1:
+        raise ValueError(f"dc={dc} must be >= 1")
+    if sliding_window < 0:
+        raise ValueError(
+            f"sliding_window={sliding_window} must be >= 0 (0 disables the branch)")
+    if not torch.is_floating_point(H):
+        raise TypeError(f"naive_hca: H must be a floating-point tensor, got dtype={H.dtype}")
+    if W_KV.shape != (c, d):
+        raise ValueError(
+            f"naive_hca: W_KV.shape={tuple(W_KV.shape)} must equal (c, d)=({c}, {d})")
+    if W_Z.shape != (c, d):
+        raise ValueError(
+            f"naive_hca: W_Z.shape={tuple(W_Z.shape)} must equal (c, d)=({c}, {d})")
+    if W_DQ.shape != (dc, d):
+        raise ValueError(
+            f"naive_hca: W_DQ.shape={tuple(W_DQ.shape)} must equal (dc, d)=({dc}, {d})")
+    if W_UQ.shape != (c * nh, dc):
+        raise ValueError(
+            f"naive_hca: W_UQ.shape={tuple(W_UQ.shape)} must equal (c*nh, dc)=({c*nh}, {dc})")
+    if B_pos.shape != (m2, c):
+        raise ValueError(
+            f"naive_hca: B_pos.shape={tuple(B_pos.shape)} must equal (m2, c)=({m2}, {c})")
+    if sink_logits is not None and sink_logits.shape != (nh,):
+        raise ValueError(
+            f"naive_hca: sink_logits.shape={tuple(sink_logits.shape)} must equal (nh,)=({nh},)")
+    if W_KV_local is not None and W_KV_local.shape != (c, d):
+        raise ValueError(
+            f"naive_hca: W_KV_local.shape={tuple(W_KV_local.shape)} must equal (c, d)=({c}, {d})")
+    device = H.device
+    if T == 0:
+        out_empty = torch.zeros(B_, 0, nh * c, dtype=H.dtype, device=device)
+        if return_projections:
+            z = torch.zeros(B_, 0, c, dtype=H.dtype, device=device)
+            return out_empty, (z, z.clone())
+        return out_empty
+    _check_gpu_dtype(fn, H)
+    if nh > 16 or c not in (64, 128):
+        raise NotImplementedError(
+            f"{fn}: HIP kernels cover nh <= 16 and c in (64, 128); got nh={nh}, c={c}")
+    original_T = T
+    pad = (-T) % m2
+    if pad:
+        H = F.pad(H, (0, 0, 0, pad))
+        T = T + pad
+    n_blocks = T // m2
+    with torch.no_grad():
+        CZ = F.linear(H, torch.cat([W_KV, W_Z], dim=0))
+        C, Z = CZ.split([c, c], dim=-1)
+        q = F.linear(F.linear(H, W_DQ), W_UQ).view(B_, T, nh, c)
+        C_local_raw = F.linear(H, W_KV_local) if (W_KV_local is not None and sliding_window > 0) \
+            else None
+        out = hca_core(C, Z, q, B_pos, m2=m2, sliding_window=sliding_window,
+                       sink_logits=sink_logits, scale=scale, C_local_raw=C_local_raw)
+    out_final = out.reshape(B_, T, nh * c)[:, :original_T]
+    if return_projections:
+        return out_final, (C[:, :original_T], Z[:, :original_T])
+    return out_final
+
+
+__all__ = ["hca_core", "naive_hca"]

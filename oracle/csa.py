@@ -206,12 +206,14 @@ def _pad_time(x, pad):
 
 def csa_core(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, *,
              m, topk, sliding_window=0, sink_logits=None, normalize_qk=True,
-             scale=None, compute=np.float32, return_indices=False):
+             scale=None, compute=np.float32, return_indices=False, indices=None):
     """CSA forward from the projections: ``[B,T,nh,c]`` in ``compute``.
 
     Inputs are the bf16 projection values (as float arrays): ``Ca..Zb``
     ``[B,T,c]``, ``K_idx, Z_idx`` ``[B,T,cI]``, ``q`` ``[B,T,nh,c]``,
-    ``q_idx`` ``[B,T,nIh,cI]``, ``w_idx`` ``[B,T,nIh]``.
+    ``q_idx`` ``[B,T,nIh,cI]``, ``w_idx`` ``[B,T,nIh]``. ``indices``
+    (``[B,T,topk]``, -1 = unused) replaces the indexer's selection, so the
+    attention can be checked on a given selection.
     """
     Bn, T, c = np.shape(Ca)
     nh = np.shape(q)[2]
@@ -224,7 +226,13 @@ def csa_core(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, *,
     C_comp = compress_kv_overlapped(Ca, Cb, Za, Zb, Ba, Bb, m, compute)
     K_IComp = compress_kv(K_idx, Z_idx, B_idx, m, compute)
     cbm = causal_block_mask(Tp, nb, m)
-    idx = lightning_indexer(q_idx, K_IComp, w_idx, topk, None, cbm, normalize_qk, compute)
+    if indices is None:
+        idx = lightning_indexer(q_idx, K_IComp, w_idx, topk, None, cbm, normalize_qk, compute)
+    else:
+        idx = np.asarray(indices, np.int64)
+        if idx.shape[1] < Tp:
+            idx = np.concatenate([idx, np.full((Bn, Tp - idx.shape[1], idx.shape[2]), -1,
+                                               np.int64)], axis=1)
     if normalize_qk:
         qn = l2_normalize(q)
         Cn = l2_normalize(C_comp)

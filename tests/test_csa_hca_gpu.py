@@ -1,0 +1,289 @@
+"""HIP CSA / HCA kernels vs the CPU oracle (needs a ROCm GPU).
+
+Both sides get the identical bf16 inputs. Tolerances:
+* compression (fp32 math on exact bf16 inputs): 1e-5 relative to the row scale;
+* indexer: logits within 2e-5 absolute (split-bf16 products); indices equal
+  wherever the oracle's neighbouring logits are separated by more than 1e-4
+  (the tie rule "descending logit, ascending index" is shared, exactly-equal
+  logits are therefore compared exactly);
+* attention outputs: |hip - ref| <= 2e-3 + 2e-2 |ref| on bf16 outputs, with the
+  oracle attention fed the HIP selection (so a near-tie cannot change the set).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import csa as O
+from oracle.common import bf16_round
+
+pytestmark = pytest.mark.gpu
+
+
+def bf16_dev(x, dev):
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(dev, torch.bfloat16)
+
+
+def host(t):
+    return t.float().cpu().numpy()
+
+
+def close(name, got, ref, rtol=2e-2, atol=2e-3):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert got.shape == ref.shape, (name, got.shape, ref.shape)
+    assert np.isfinite(got).all(), f"{name}: non-finite values"
+    bad = np.abs(got - ref) > atol + rtol * np.abs(ref)
+    assert not bad.any(), (f"{name}: {bad.sum()} of {bad.size} outside atol {atol} + rtol {rtol}; "
+                           f"max abs err {np.abs(got - ref).max():.3e}")
+
+
+def check_topk(name, idx_gpu, idx_ref, logits_ref, gap=1e-4):
+    """Tie-aware index comparison (both sorted by descending logit).
+
+    The logits at the selected positions must agree within ``gap``; the index
+    rows must be identical wherever the oracle's sorted logits, down to one
+    past the last selected slot, have no two neighbours within ``gap``.
+    Returns the fraction of identical rows.
+    """
+    idx_gpu = np.asarray(idx_gpu, np.int64)
+    idx_ref = np.asarray(idx_ref, np.int64)
+    assert idx_gpu.shape == idx_ref.shape
+    assert np.array_equal(idx_gpu < 0, idx_ref < 0), f"{name}: different numbers of valid slots"
+    lg = np.asarray(logits_ref, np.float64)
+    vg = np.where(idx_gpu >= 0, np.take_along_axis(lg, np.maximum(idx_gpu, 0), -1), 0.0)
+    vr = np.where(idx_ref >= 0, np.take_along_axis(lg, np.maximum(idx_ref, 0), -1), 0.0)
+    assert np.all(np.abs(vg - vr) <= gap), f"{name}: selected logits differ"
+    same = np.all(idx_gpu == idx_ref, -1)
+    B, T, _ = idx_ref.shape
+    for b in range(B):
+        for t in range(T):
+            if same[b, t]:
+                continue
+            row = -np.sort(-lg[b, t][np.isfinite(lg[b, t])])
+            k = int(np.count_nonzero(idx_ref[b, t] >= 0))
+            near = np.abs(np.diff(row[: k + 1])) <= gap
+            assert near.any(), f"{name}: row ({b},{t}) differs without a near-tie"
+    return float(np.mean(same))
+
+
+def test_indexer_exact_tie_rule(dev):
+    """Duplicated key rows give bit-identical logits: ties go to the lower index."""
+    import kch
+    rng = np.random.default_rng(9)
+    B, T, cI, nIh, m, topk = 1, 64, 64, 4, 1, 6
+    base = rng.standard_normal((4, cI)).astype(np.float32)
+    K = base[rng.integers(0, 4, size=(B, T))]  # 64 blocks, 4 distinct rows
+    qi = bf16_dev(rng.standard_normal((B, T, nIh, cI)), dev)
+    wi = bf16_dev(rng.standard_normal((B, T, nIh)), dev)
+    idx = kch.csa_lightning_indexer(qi, torch.from_numpy(K).to(dev), wi, topk,
+                                    normalize_qk=True)
+    torch.cuda.synchronize()
+    idx_ref, lg = O.lightning_indexer(host(qi), K, host(wi), topk, None, None, True,
+                                      return_logits=True)
+    # within each group of equal logits the order is ascending block index
+    got = idx.cpu().numpy()
+    for t in range(T):
+        vals = lg[0, t, got[0, t]]
+        for j in range(topk - 1):
+            if vals[j] == vals[j + 1]:
+                assert got[0, t, j] < got[0, t, j + 1]
+    assert np.array_equal(got, idx_ref)
+
+
+def proj_inputs(seed, B, T, c, cI, nh, nIh, m, dev):
+    rng = np.random.default_rng(seed)
+    r = lambda *s: rng.standard_normal(s)  # noqa: E731
+    xs = dict(Ca=r(B, T, c), Cb=r(B, T, c), Za=r(B, T, c), Zb=r(B, T, c), K_idx=r(B, T, cI),
+              Z_idx=r(B, T, cI), q=r(B, T, nh, c), q_idx=r(B, T, nIh, cI), w_idx=r(B, T, nIh))
+    dv = {k: bf16_dev(v, dev) for k, v in xs.items()}
+    hs = {k: host(v) for k, v in dv.items()}
+    par = dict(Ba=0.02 * r(m, c), Bb=0.02 * r(m, c), B_idx=0.02 * r(m, cI))
+    parf = {k: v.astype(np.float32) for k, v in par.items()}
+    pard = {k: torch.from_numpy(v).to(dev) for k, v in parf.items()}
+    return dv, hs, pard, parf
+
+
+@pytest.mark.parametrize("m,c", [(4, 128), (128, 128), (4, 64), (7, 64)])
+def test_compress_single(dev, m, c):
+    import kch
+    B, T = 2, 4 * m * 3
+    dv, hs, pard, parf = proj_inputs(m + c, B, T, c, 32, 1, 1, m, dev)
+    out = kch.csa_compress_kv(dv["Ca"], dv["Za"], pard["Ba"], m)
+    torch.cuda.synchronize()
+    ref = O.compress_kv(hs["Ca"], hs["Za"], parf["Ba"], m)
+    assert np.abs(host(out) - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max())
+
+
+@pytest.mark.parametrize("m,c", [(4, 128), (16, 64)])
+def test_compress_overlapped(dev, m, c):
+    import kch
+    B, T = 2, 8 * m
+    dv, hs, pard, parf = proj_inputs(3 * m + c, B, T, c, 32, 1, 1, m, dev)
+    out = kch.csa_compress_kv_overlapped(dv["Ca"], dv["Cb"], dv["Za"], dv["Zb"], pard["Ba"],
+                                         pard["Bb"], m)
+    torch.cuda.synchronize()
+    ref = O.compress_kv_overlapped(hs["Ca"], hs["Cb"], hs["Za"], hs["Zb"], parf["Ba"], parf["Bb"], m)
+    assert np.abs(host(out) - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max())
+
+
+@pytest.mark.parametrize("normalize", [True, False])
+@pytest.mark.parametrize("T,m,topk", [(128, 4, 8), (64, 4, 32), (200, 4, 16), (96, 8, 0)])
+def test_indexer_matches_oracle(dev, normalize, T, m, topk):
+    import kch
+    B, cI, nIh = 2, 64, 4
+    nb = T // m
+    dv, hs, pard, parf = proj_inputs(T + topk, B, T, 64, cI, 1, nIh, m, dev)
+    K_ref = O.compress_kv(hs["K_idx"], hs["Z_idx"], parf["B_idx"], m)
+    K_dev = torch.from_numpy(K_ref).to(dev)
+    cbm = O.causal_block_mask(T, nb, m)
+    idx = kch.csa_lightning_indexer(dv["q_idx"], K_dev, dv["w_idx"], topk,
+                                    causal_block_mask=torch.from_numpy(cbm).to(dev),
+                                    normalize_qk=normalize)
+    torch.cuda.synchronize()
+    idx_ref, lg = O.lightning_indexer(hs["q_idx"], K_ref, hs["w_idx"], topk, None, cbm,
+                                      normalize, return_logits=True)
+    assert idx.dtype == torch.int64 and tuple(idx.shape) == (B, T, topk)
+    if topk:
+        frac = check_topk("indexer", idx.cpu().numpy(), idx_ref, lg)
+        assert frac > 0.9
+
+
+def test_indexer_soft_weights_and_no_mask(dev):
+    import kch
+    B, T, cI, nIh, m, topk = 1, 32, 32, 2, 4, 4
+    dv, hs, pard, parf = proj_inputs(5, B, T, 64, cI, 1, nIh, m, dev)
+    K_ref = O.compress_kv(hs["K_idx"], hs["Z_idx"], parf["B_idx"], m)
+    idx, soft = kch.csa_lightning_indexer(dv["q_idx"], torch.from_numpy(K_ref).to(dev), None,
+                                          topk, return_soft_weights=True, normalize_qk=True)
+    torch.cuda.synchronize()
+    idx_ref, lg = O.lightning_indexer(hs["q_idx"], K_ref, None, topk, None, None, True,
+                                      return_logits=True)
+    check_topk("indexer-dense", idx.cpu().numpy(), idx_ref, lg)
+    e = np.exp(lg - lg.max(-1, keepdims=True))
+    close("soft", soft.cpu().numpy(), e / e.sum(-1, keepdims=True), rtol=1e-4, atol=1e-6)
+
+
+@pytest.mark.parametrize("win,sink,topk,T", [(16, True, 8, 128), (0, True, 8, 96),
+                                             (16, False, 8, 100), (8, True, 0, 64),
+                                             (128, True, 512, 256)])
+def test_csa_core_matches_oracle(dev, win, sink, topk, T):
+    import kch
+    B, c, cI, nh, nIh, m = 2, 128, 64, 16, 4, 4
+    T = T - T % m
+    dv, hs, pard, parf = proj_inputs(win + T + topk, B, T, c, cI, nh, nIh, m, dev)
+    sink_v = np.random.default_rng(1).standard_normal(nh).astype(np.float32) if sink else None
+    out, idx = kch.csa_core(dv["Ca"], dv["Cb"], dv["Za"], dv["Zb"], dv["K_idx"], dv["Z_idx"],
+                            dv["q"], dv["q_idx"], dv["w_idx"], pard["Ba"], pard["Bb"],
+                            pard["B_idx"], m=m, topk=topk, sliding_window=win,
+                            sink_logits=None if sink_v is None else torch.from_numpy(sink_v).to(dev),
+                            normalize_qk=True, return_indices=True)
+    torch.cuda.synchronize()
+    args = [hs[k] for k in ("Ca", "Cb", "Za", "Zb", "K_idx", "Z_idx", "q", "q_idx", "w_idx")]
+    kw = dict(m=m, topk=topk, sliding_window=win, sink_logits=sink_v, normalize_qk=True)
+    if topk:
+        _, idx_ref = O.csa_core(*args, parf["Ba"], parf["Bb"], parf["B_idx"], return_indices=True, **kw)
+        K_ref = O.compress_kv(hs["K_idx"], hs["Z_idx"], parf["B_idx"], m)
+        lg = O.indexer_logits(hs["q_idx"], K_ref, hs["w_idx"], None,
+                              O.causal_block_mask(T, T // m, m), True)
+        check_topk("csa idx", idx.cpu().numpy().astype(np.int64), idx_ref, lg)
+        ref = O.csa_core(*args, parf["Ba"], parf["Bb"], parf["B_idx"],
+                         indices=idx.cpu().numpy(), **kw)
+    else:
+        ref = O.csa_core(*args, parf["Ba"], parf["Bb"], parf["B_idx"], **kw)
+    close("csa out", host(out), bf16_round(ref))
+
+
+@pytest.mark.parametrize("win,sink,m2,T", [(16, True, 16, 160), (0, True, 8, 64),
+                                           (32, False, 16, 96), (128, True, 128, 512)])
+def test_hca_core_matches_oracle(dev, win, sink, m2, T):
+    import kch
+    B, c, nh = 2, 128, 16
+    rng = np.random.default_rng(T + m2)
+    Cd, Zd = bf16_dev(rng.standard_normal((B, T, c)), dev), bf16_dev(rng.standard_normal((B, T, c)), dev)
+    qd = bf16_dev(rng.standard_normal((B, T, nh, c)), dev)
+    bpos = (0.02 * rng.standard_normal((m2, c))).astype(np.float32)
+    sink_v = rng.standard_normal(nh).astype(np.float32) if sink else None
+    out = kch.hca_core(Cd, Zd, qd, torch.from_numpy(bpos).to(dev), m2=m2, sliding_window=win,
+                       sink_logits=None if sink_v is None else torch.from_numpy(sink_v).to(dev))
+    torch.cuda.synchronize()
+    ref = O.hca_core(host(Cd), host(Zd), host(qd), bpos, m2=m2, sliding_window=win,
+                     sink_logits=sink_v)
+    close("hca out", host(out), bf16_round(ref))
+
+
+def _weights(rng, shapes, dev):
+    return {k: (rng.standard_normal(s) * s[1] ** -0.5) for k, s in shapes.items()}
+
+
+def test_naive_csa_end_to_end_plumbing(dev):
+    """naive_csa == csa_core on the same GPU projections (padding, split, trim)."""
+    import torch.nn.functional as F
+
+    import kch
+    B, T, d, c, cI, nh, nIh, dc, m = 2, 70, 64, 128, 64, 16, 4, 32, 4
+    rng = np.random.default_rng(3)
+    shapes = dict(W_aKV=(c, d), W_bKV=(c, d), W_aZ=(c, d), W_bZ=(c, d), W_DQ=(dc, d),
+                  W_UQ=(c * nh, dc), W_IUQ=(cI * nIh, dc), W_w=(nIh, d), W_KV_idx=(cI, d),
+                  W_Z_idx=(cI, d))
+    W = {k: bf16_dev(v, dev) for k, v in _weights(rng, shapes, dev).items()}
+    Ba, Bb = (bf16_dev(0.02 * rng.standard_normal((m, c)), dev) for _ in range(2))
+    B_idx = bf16_dev(0.02 * rng.standard_normal((m, cI)), dev)
+    H = bf16_dev(rng.standard_normal((B, T, d)), dev)
+    sink = torch.from_numpy(rng.standard_normal(nh).astype(np.float32)).to(dev).bfloat16()
+    kw = dict(m=m, topk=8, nh=nh, nIh=nIh, c=c, c_I=cI, dc=dc, sliding_window=16,
+              sink_logits=sink, normalize_qk=True)
+    out, proj = kch.naive_csa(H, W["W_aKV"], W["W_bKV"], W["W_aZ"], W["W_bZ"], Ba, Bb, W["W_DQ"],
+                              W["W_UQ"], W["W_IUQ"], W["W_w"], W["W_KV_idx"], W["W_Z_idx"], B_idx,
+                              return_projections=True, **kw)
+    assert out.shape == (B, T, nh * c) and out.dtype == torch.bfloat16
+    assert all(p.shape[1] == T for p in proj)
+    Hp = F.pad(H, (0, 0, 0, (-T) % m))
+    cat = F.linear(Hp, torch.cat([W[k] for k in ("W_aKV", "W_bKV", "W_aZ", "W_bZ", "W_KV_idx",
+                                                 "W_Z_idx")], 0))
+    Ca, Cb, Za, Zb, Ki, Zi = cat.split([c, c, c, c, cI, cI], -1)
+    cQ = F.linear(Hp, W["W_DQ"])
+    core = kch.csa_core(Ca, Cb, Za, Zb, Ki, Zi, F.linear(cQ, W["W_UQ"]).view(B, -1, nh, c),
+                        F.linear(cQ, W["W_IUQ"]).view(B, -1, nIh, cI), F.linear(Hp, W["W_w"]),
+                        Ba, Bb, B_idx, m=m, topk=8, sliding_window=16, sink_logits=sink,
+                        normalize_qk=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out, core.reshape(B, -1, nh * c)[:, :T])
+    assert torch.equal(proj[0], Ca[:, :T])
+    # T = 0 and validation
+    e = kch.naive_csa(H[:, :0], W["W_aKV"], W["W_bKV"], W["W_aZ"], W["W_bZ"], Ba, Bb, W["W_DQ"],
+                      W["W_UQ"], W["W_IUQ"], W["W_w"], W["W_KV_idx"], W["W_Z_idx"], B_idx, **kw)
+    assert e.shape == (B, 0, nh * c)
+    with pytest.raises(ValueError, match="topk"):
+        kch.naive_csa(H, W["W_aKV"], W["W_bKV"], W["W_aZ"], W["W_bZ"], Ba, Bb, W["W_DQ"],
+                      W["W_UQ"], W["W_IUQ"], W["W_w"], W["W_KV_idx"], W["W_Z_idx"], B_idx,
+                      **{**kw, "topk": -1})
+
+
+def test_naive_hca_end_to_end_plumbing(dev):
+    import torch.nn.functional as F
+
+    import kch
+    B, T, d, c, nh, dc, m2 = 2, 100, 64, 128, 16, 32, 16
+    rng = np.random.default_rng(4)
+    shapes = dict(W_KV=(c, d), W_Z=(c, d), W_DQ=(dc, d), W_UQ=(c * nh, dc))
+    W = {k: bf16_dev(v, dev) for k, v in _weights(rng, shapes, dev).items()}
+    bpos = bf16_dev(0.02 * rng.standard_normal((m2, c)), dev)
+    H = bf16_dev(rng.standard_normal((B, T, d)), dev)
+    out, (C, Z) = kch.naive_hca(H, W["W_KV"], W["W_Z"], bpos, W["W_DQ"], W["W_UQ"], m2=m2, nh=nh,
+                                c=c, dc=dc, sliding_window=32, return_projections=True)
+    Hp = F.pad(H, (0, 0, 0, (-T) % m2))
+    CZ = F.linear(Hp, torch.cat([W["W_KV"], W["W_Z"]], 0))
+    q = F.linear(F.linear(Hp, W["W_DQ"]), W["W_UQ"]).view(B, -1, nh, c)
+    core = kch.hca_core(CZ[..., :c], CZ[..., c:], q, bpos, m2=m2, sliding_window=32)
+    torch.cuda.synchronize()
+    assert torch.equal(out, core.reshape(B, -1, nh * c)[:, :T])
+    assert C.shape == (B, T, c)
+    with pytest.raises(TypeError):
+        kch.naive_hca(H.long(), W["W_KV"], W["W_Z"], bpos, W["W_DQ"], W["W_UQ"], m2=m2, nh=nh,
+                      c=c, dc=dc)
+    with pytest.raises(ValueError, match="B_pos"):
+        kch.naive_hca(H, W["W_KV"], W["W_Z"], bpos[:1], W["W_DQ"], W["W_UQ"], m2=m2, nh=nh, c=c,
+                      dc=dc)
