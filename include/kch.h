@@ -144,6 +144,36 @@ int kch_hca_attn(const void* q, const void* kv_comp, const void* kv_local, const
 int kch_l2norm_rows(const void* x, long long ldx, void* out, int out_f32, int rows, int c,
                     int normalize, int dtype, void* stream);
 
+/*
+ * One CSA decode step for the last appended token of each sequence:
+ * lightning indexer over every cached block (all are complete, hence visible),
+ * top-k, then one joint softmax over the selected blocks, the ring-buffer
+ * window and the sink. Replaces CSADecodingCache.forward_step
+ * (ops_decoding_cache.py:783-1070).
+ *   q [B,nh,hd] (normalised in-kernel when normalize_q), q_idx [B,nIh,cI]
+ *   (normalised in-kernel when normalize_qidx), w_idx [B,nIh] or NULL (qdtype)
+ *   kv_comp [B,*,hd] bf16 key/value rows (batch stride kv_bstride elements)
+ *   k_idx [B,*,cI] fp32 indexer keys (already L2-normalised when normalize_qidx)
+ *   ring [B,*,hd] bf16: the first ring_len rows are the window (any order)
+ *   idx_ws [B,topk] int32 workspace; out [B,nh,hd] (odtype)
+ */
+int kch_csa_decode_step(const void* q, const void* q_idx, const void* w_idx, const void* kv_comp,
+                        long long kv_bstride, const float* k_idx, long long k_bstride,
+                        const void* ring, long long ring_bstride, int ring_len, const float* sink,
+                        void* out, int* idx_ws, int B, int nb, int nh, int hd, int nIh, int cI,
+                        int topk, float scale, float idx_scale, int normalize_q,
+                        int normalize_qidx, int qdtype, int odtype, void* stream);
+
+/*
+ * One HCA decode step: dense MQA over every cached compressed block plus the
+ * ring-buffer window and the sink. Replaces HCADecodingCache.forward_step
+ * (ops_decoding_cache.py:1268-1395). Arguments as kch_csa_decode_step.
+ */
+int kch_hca_decode_step(const void* q, const void* kv_comp, long long kv_bstride, const void* ring,
+                        long long ring_bstride, int ring_len, const float* sink, void* out, int B,
+                        int nb, int nh, int hd, float scale, int normalize_q, int qdtype, int odtype,
+                        void* stream);
+
 #ifdef __cplusplus
 }
 #endif

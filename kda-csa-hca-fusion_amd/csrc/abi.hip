@@ -193,7 +193,7 @@ int kch_csa_indexer_topk(const void* q_idx, const float* k_idx, const void* w_id
     return hip_status(fn, e);
   }
   kch::IndexerParams p{q_idx, k_idx, w_idx, idx_out, logits_out, B, T, nb, nIh, cI, topk, m,
-                       pos0, normalize_q, idx64, dense_visible, scale};
+                       pos0, normalize_q, idx64, dense_visible, scale, 0};
   return hip_status(fn, kch::indexer_dispatch(p, dtype, (hipStream_t)stream));
 }
 
@@ -219,7 +219,7 @@ int kch_csa_sparse_attn(const void* q, const void* kv_comp, const int* idx, cons
   if (!q || !out || (topk > 0 && (!idx || !kv_comp)) || (win > 0 && !kv_local))
     return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
   kch::AttnParams p{q, (const kch::bf16_t*)kv_comp, idx, (const kch::bf16_t*)kv_local, sink, out,
-                    B, T, nb, nh, hd, topk, 1, win, normalize_q, scale};
+                    B, T, nb, nh, hd, topk, 1, win, normalize_q, scale, 0, 0, -1, 0};
   return hip_status(fn, kch::attn_dispatch(p, true, qdtype, odtype, (hipStream_t)stream));
 }
 
@@ -234,7 +234,7 @@ int kch_hca_attn(const void* q, const void* kv_comp, const void* kv_local, const
   if (!q || !out || (nb > 0 && !kv_comp) || (win > 0 && !kv_local))
     return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
   kch::AttnParams p{q, (const kch::bf16_t*)kv_comp, nullptr, (const kch::bf16_t*)kv_local, sink,
-                    out, B, T, nb, nh, hd, 0, m, win, normalize_q, scale};
+                    out, B, T, nb, nh, hd, 0, m, win, normalize_q, scale, 0, 0, -1, 0};
   return hip_status(fn, kch::attn_dispatch(p, false, qdtype, odtype, (hipStream_t)stream));
 }
 
@@ -247,6 +247,59 @@ int kch_l2norm_rows(const void* x, long long ldx, void* out, int out_f32, int ro
   if (!x || !out) return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
   return hip_status(fn, kch::l2norm_rows_dispatch(x, ldx, out, out_f32, rows, c, normalize, dtype,
                                                   (hipStream_t)stream));
+}
+
+int kch_csa_decode_step(const void* q, const void* q_idx, const void* w_idx, const void* kv_comp,
+                        long long kv_bstride, const float* k_idx, long long k_bstride,
+                        const void* ring, long long ring_bstride, int ring_len, const float* sink,
+                        void* out, int* idx_ws, int B, int nb, int nh, int hd, int nIh, int cI,
+                        int topk, float scale, float idx_scale, int normalize_q,
+                        int normalize_qidx, int qdtype, int odtype, void* stream) {
+  const char* fn = "kch_csa_decode_step";
+  int rc = check_attn(fn, B, 1, nb, nh, hd, qdtype, odtype);
+  if (rc) return rc;
+  if (topk < 0 || ring_len < 0) return fail(KCH_ERR_INVALID, "%s: topk / ring_len must be >= 0", fn);
+  if (nIh != 1 && nIh != 2 && nIh != 4 && nIh != 8 && nIh != 16)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: nIh=%d not in {1,2,4,8,16}", fn, nIh);
+  if (cI != 32 && cI != 64 && cI != 128)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: cI=%d not in {32,64,128}", fn, cI);
+  if (B == 0) return KCH_OK;
+  if (!q || !out || (ring_len > 0 && !ring)) return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
+  hipStream_t s = (hipStream_t)stream;
+  const int use_sel = (topk > 0 && nb > 0);
+  if (use_sel) {
+    if (!q_idx || !k_idx || !kv_comp || !idx_ws) return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
+    int ptop = 1;
+    while (ptop < topk) ptop <<= 1;
+    const long long lds = (long long)(16 / nIh) * nb * 4 + (256 + 16) * 4 + (long long)ptop * 8;
+    if (lds > 160 * 1024)
+      return fail(KCH_ERR_UNSUPPORTED, "%s: %d cached blocks exceed the indexer LDS budget", fn, nb);
+    kch::IndexerParams ip{q_idx, k_idx, w_idx, idx_ws, nullptr, B, 1, nb, nIh, cI, topk, 1,
+                          0, normalize_qidx, 0, 1, idx_scale, k_bstride};
+    rc = hip_status(fn, kch::indexer_dispatch(ip, qdtype, s));
+    if (rc) return rc;
+  }
+  kch::AttnParams p{q, (const kch::bf16_t*)kv_comp, idx_ws, (const kch::bf16_t*)ring, sink, out,
+                    B, 1, nb, nh, hd, use_sel ? topk : 0, 1, 0, 0, scale, kv_bstride,
+                    ring_bstride, ring_len, 0};
+  return hip_status(fn, kch::attn_dispatch(p, true, qdtype, odtype, s));
+}
+
+int kch_hca_decode_step(const void* q, const void* kv_comp, long long kv_bstride, const void* ring,
+                        long long ring_bstride, int ring_len, const float* sink, void* out, int B,
+                        int nb, int nh, int hd, float scale, int normalize_q, int qdtype, int odtype,
+                        void* stream) {
+  const char* fn = "kch_hca_decode_step";
+  int rc = check_attn(fn, B, 1, nb, nh, hd, qdtype, odtype);
+  if (rc) return rc;
+  if (ring_len < 0) return fail(KCH_ERR_INVALID, "%s: ring_len must be >= 0", fn);
+  if (B == 0) return KCH_OK;
+  if (!q || !out || (nb > 0 && !kv_comp) || (ring_len > 0 && !ring))
+    return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
+  // every cached block is complete, hence visible: nvis = min(nb, (pos0 + 1) / 1)
+  kch::AttnParams p{q, (const kch::bf16_t*)kv_comp, nullptr, (const kch::bf16_t*)ring, sink, out,
+                    B, 1, nb, nh, hd, 0, 1, 0, 0, scale, kv_bstride, ring_bstride, ring_len, nb};
+  return hip_status(fn, kch::attn_dispatch(p, false, qdtype, odtype, (hipStream_t)stream));
 }
 
 }  // extern "C"

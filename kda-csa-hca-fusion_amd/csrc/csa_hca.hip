@@ -136,7 +136,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnParams p) {
   W w;
   w.template init<QT>(n < p.nh ? qrow : nullptr, p.normalize_q != 0, p.scale);
 
-  const bf16_t* kv = p.kv_comp + (size_t)b * p.nb * HD;
+  const bf16_t* kv = p.kv_comp + (size_t)b * (p.kv_bstride ? p.kv_bstride : (long long)p.nb * HD);
   if (SPARSE) {
     // selected compressed blocks; -1 marks an unused slot
     const int* idx = p.idx + (size_t)qi * p.topk;
@@ -150,7 +150,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnParams p) {
     }
   } else {
     // dense: compressed blocks b < (t + 1) // m
-    const int nvis = min(p.nb, (t + 1) / p.m);
+    const int nvis = min(p.nb, (p.pos0 + t + 1) / p.m);
     for (int j0 = 0; j0 < nvis; j0 += 16) {
       const int j = j0 + n;
       const bool ok = j < nvis;
@@ -158,9 +158,20 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnParams p) {
       w.chunk(kv + (size_t)(ok ? j : 0) * HD, valid, stage);
     }
   }
-  if (p.win > 0 && p.kv_local) {
+  if (p.kv_local && p.local_count >= 0) {
+    // window = the first local_count rows (a ring buffer, order irrelevant)
+    const bf16_t* loc =
+        p.kv_local + (size_t)b * (p.local_bstride ? p.local_bstride : (long long)T * HD);
+    for (int j0 = 0; j0 < p.local_count; j0 += 16) {
+      const int j = j0 + n;
+      const bool ok = j < p.local_count;
+      const unsigned valid = (unsigned)__ballot(ok && lane < 16) & 0xffffu;
+      w.chunk(loc + (size_t)(ok ? j : 0) * HD, valid, stage);
+    }
+  } else if (p.win > 0 && p.kv_local) {
     // window positions t - win + 1 .. t (those >= 0)
-    const bf16_t* loc = p.kv_local + (size_t)b * T * HD;
+    const bf16_t* loc =
+        p.kv_local + (size_t)b * (p.local_bstride ? p.local_bstride : (long long)T * HD);
     const int lo = t - p.win + 1;
     for (int j0 = lo; j0 <= t; j0 += 16) {
       const int j = j0 + n;

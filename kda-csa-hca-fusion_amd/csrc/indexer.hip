@@ -115,7 +115,7 @@ __global__ __launch_bounds__(64) void indexer_kernel(IndexerParams p) {
   for (int j = 0; j < QPW; ++j)
     if (t0 + j < p.T) nv_max = max(nv_max, nvis_of(t0 + j));
   const int nv_me = qok ? nvis_of(tq) : 0;
-  const float* kbase = p.k_idx + (size_t)b * nb * CI;
+  const float* kbase = p.k_idx + (size_t)b * (p.k_bstride ? p.k_bstride : (long long)nb * CI);
   for (int c0 = 0; c0 < nv_max; c0 += 16) {
     const int r = c0 + n;
     const float* krow = kbase + (size_t)(r < nb ? r : nb - 1) * CI;

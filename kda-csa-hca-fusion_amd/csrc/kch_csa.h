@@ -31,6 +31,11 @@ struct AttnParams {
   void* out;                // [B, T, nh, hd]
   int B, T, nb, nh, hd, topk, m, win, normalize_q;
   float scale;
+  long long kv_bstride;     // elements between batches of kv_comp (0: nb * hd)
+  long long local_bstride;  // elements between batches of kv_local (0: T * hd)
+  int local_count;          // < 0: window of positions [t-win+1, t]; >= 0: the first
+                            // local_count rows of kv_local are the window (ring buffer)
+  int pos0;                 // position of query 0 (causal block rule of the dense mode)
 };
 hipError_t attn_dispatch(const AttnParams& p, bool sparse, int qdtype, int odtype, hipStream_t s);
 
@@ -45,6 +50,7 @@ struct IndexerParams {
   int q_pos0;            // position of query 0 (decode: the cache's token index)
   int normalize_q, idx64, dense_visible;  // dense_visible: every block visible
   float scale;
+  long long k_bstride;   // elements between batches of k_idx (0: nb * cI)
 };
 hipError_t indexer_dispatch(const IndexerParams& p, int dtype, hipStream_t s);
 

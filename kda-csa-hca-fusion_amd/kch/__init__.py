@@ -5,6 +5,7 @@ running hand-written HIP kernels from ``libkch.so`` through the C ABI declared
 in ``include/kch.h``. Tensors must be on a ROCm GPU; there is no CPU path.
 """
 
+from .decoding_cache import CSADecodingCache, HCADecodingCache, SlidingWindowRingBuffer
 from .ops_csa import (csa_compress_kv, csa_compress_kv_overlapped, csa_core,
                       csa_lightning_indexer, l2_normalize_rows, naive_csa)
 from .ops_hca import hca_core, naive_hca
@@ -12,6 +13,9 @@ from .ops_kda import naive_chunk_kda, naive_recurrent_kda
 from .ops_kda_backend import hip_available, kda_forward, validate_kda_backend
 
 __all__ = [
+    "CSADecodingCache",
+    "HCADecodingCache",
+    "SlidingWindowRingBuffer",
     "csa_compress_kv",
     "csa_compress_kv_overlapped",
     "csa_core",

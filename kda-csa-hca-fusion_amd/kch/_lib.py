@@ -35,6 +35,9 @@ _SIGNATURES = {
     "kch_csa_sparse_attn": [_P] * 6 + [_I] * 7 + [_F, _I, _I, _I, _P],
     "kch_hca_attn": [_P] * 5 + [_I] * 7 + [_F, _I, _I, _I, _P],
     "kch_l2norm_rows": [_P, _L, _P, _I, _I, _I, _I, _I, _P],
+    "kch_csa_decode_step": [_P, _P, _P, _P, _L, _P, _L, _P, _L, _I, _P, _P, _P] + [_I] * 7
+                           + [_F, _F, _I, _I, _I, _I, _P],
+    "kch_hca_decode_step": [_P, _P, _L, _P, _L, _I, _P, _P] + [_I] * 4 + [_F, _I, _I, _I, _P],
 }
 
 EXPORTED = ["kch_abi_version", "kch_last_error"] + sorted(_SIGNATURES)

@@ -1,0 +1,520 @@
+"""Incremental CSA / HCA decode state on the HIP backend.
+
+Drop-in twins of ``/root/reference/ops_decoding_cache.py``:
+
+``SlidingWindowRingBuffer``  <- ``_SlidingWindowRingBuffer`` (``:251-400``)
+``CSADecodingCache``         <- ``CSADecodingCache`` (``:407-1070``)
+``HCADecodingCache``         <- ``HCADecodingCache`` (``:1077-1395``)
+
+Same constructors, ``append_step`` / ``forward_step`` / ``reset`` / ``to``,
+properties (``n_tokens_seen``, ``n_blocks``, ``accumulator_len``,
+``C_comp``, ``K_IComp``, ``sw_buffer``) and the ``_normalize_qk`` attribute.
+
+State lives in GPU tensors instead of Python lists:
+
+* the partial-block accumulator is a ``[B, m, width]`` buffer per projection;
+* completed blocks are compressed by ``kch_compress(_overlapped)`` in one
+  launch per ``append_step`` (however many blocks it completes, so a prefill
+  populates the cache in bulk), rounded to the cache dtype as the reference
+  stores them (``:750-763``), with the previous block's ``Cb / Zb`` kept for
+  the overlap;
+* L2-normalised copies of the cached rows (bf16 attention keys, fp32 indexer
+  keys) are produced once per new block, where the reference re-normalises
+  every cached block on every step (``:919-924``);
+* ``forward_step`` is one ``kch_csa_decode_step`` / ``kch_hca_decode_step``
+  call (indexer + top-k + joint sparse/window/sink softmax).
+
+Forward only (``use_ste`` does not change the forward value); float64 caches
+are not supported.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .ops_csa import _aligned, _compress, _compress_overlapped, _f32, l2_normalize_rows
+
+
+def _validate_cache_dtype(dtype) -> None:
+    try:
+        is_float = torch.empty((), dtype=dtype).is_floating_point()
+    except (TypeError, RuntimeError) as exc:
+        raise TypeError(f'cache dtype must be a floating torch.dtype, got {dtype!r}') from exc
+    if not is_float:
+        raise TypeError(f'cache dtype must be floating-point, got {dtype!r}')
+    if dtype == torch.float64:
+        raise NotImplementedError("float64 caches are not supported by the HIP kernels")
+
+
+class SlidingWindowRingBuffer:
+    """FIFO of the last ``win`` entries ``[B, c]``; the i-th entry ever written
+    sits at row ``i % win`` (``ops_decoding_cache.py:321-357``)."""
+
+    def __init__(self, B: int, win: int, c: int, device, dtype):
+        if win < 1:
+            raise ValueError(
+                f"_SlidingWindowRingBuffer: win={win} must be >= 1 "
+                f"(win=0 disables the SW branch and should bypass this class entirely).")
+        self.B, self.win, self.c = B, win, c
+        self.device, self.dtype = torch.device(device), dtype
+        self._buf = torch.zeros(B, win, c, device=self.device, dtype=dtype)
+        self._written = 0
+
+    def reset(self) -> None:
+        self._buf.zero_()
+        self._written = 0
+
+    def append(self, x: torch.Tensor) -> None:
+        """Append ``x`` ``[B, T_new, c]`` (oldest first)."""
+        if x.dim() != 3 or x.shape[0] != self.B or x.shape[-1] != self.c:
+            raise ValueError(
+                f"_SlidingWindowRingBuffer.append: expected [{self.B}, T_new, {self.c}], "
+                f"got {tuple(x.shape)}.")
+        x = x.to(device=self._buf.device, dtype=self._buf.dtype)
+        T_new = x.shape[1]
+        if T_new == 0:
+            return
+        keep = min(T_new, self.win)
+        first = self._written + T_new - keep
+        pos = torch.arange(first, first + keep, device=self._buf.device) % self.win
+        self._buf.index_copy_(1, pos, x[:, T_new - keep:])
+        self._written += T_new
+
+    @property
+    def n_valid(self) -> int:
+        return min(self._written, self.win)
+
+    @property
+    def _sw_len(self) -> int:
+        return self.n_valid
+
+    @property
+    def _sw_head(self) -> int:
+        return 0 if self._written < self.win else self._written % self.win
+
+    def get(self) -> torch.Tensor:
+        """Contents in causal order (oldest first), ``[B, n_valid, c]``."""
+        n = self.n_valid
+        if n < self.win:
+            return self._buf[:, :n]
+        h = self._sw_head
+        return self._buf if h == 0 else torch.cat([self._buf[:, h:], self._buf[:, :h]], dim=1)
+
+    def raw(self) -> torch.Tensor:
+        """The storage ``[B, win, c]``; its first ``n_valid`` rows are the window."""
+        return self._buf
+
+    def to(self, device=None, dtype=None) -> 'SlidingWindowRingBuffer':
+        if device is not None:
+            self._buf = self._buf.to(device=torch.device(device))
+            self.device = self._buf.device
+        if dtype is not None and dtype != self._buf.dtype:
+            self._buf = self._buf.to(dtype=dtype)
+            self.dtype = dtype
+        return self
+
+
+class _BlockStore:
+    """Geometric-capacity rows ``[B, cap, width]`` in the cache dtype plus the
+    attention copy (bf16 or fp32) of the same rows, optionally L2-normalised."""
+
+    def __init__(self, B, width, device, dtype, key_dtype):
+        self.B, self.width, self.device, self.dtype, self.key_dtype = B, width, device, dtype, key_dtype
+        self.rows = None
+        self.keys = None
+        self.key_norm = None
+
+    def ensure(self, n_valid, required):
+        if self.rows is not None and required <= self.rows.shape[1]:
+            return
+        old = 0 if self.rows is None else self.rows.shape[1]
+        cap = max(required, max(1, old * 2))
+        rows = torch.empty(self.B, cap, self.width, device=self.device, dtype=self.dtype)
+        keys = torch.empty(self.B, cap, self.width, device=self.device, dtype=self.key_dtype)
+        if n_valid:
+            rows[:, :n_valid] = self.rows[:, :n_valid]
+            keys[:, :n_valid] = self.keys[:, :n_valid]
+        self.rows, self.keys = rows, keys
+
+    def push(self, n_valid, new_rows, normalize):
+        k = new_rows.shape[1]
+        self.ensure(n_valid, n_valid + k)
+        self.rows[:, n_valid:n_valid + k] = new_rows.to(self.dtype)
+        if self.key_norm is None:
+            self.key_norm = normalize
+        self.keys[:, n_valid:n_valid + k] = l2_normalize_rows(
+            self.rows[:, n_valid:n_valid + k], out_dtype=self.key_dtype,
+            normalize=self.key_norm)
+
+    def keys_for(self, n_valid, normalize):
+        """Attention rows normalised as asked (rebuilt if the flag changed)."""
+        if self.rows is not None and n_valid and self.key_norm != normalize:
+            self.keys[:, :n_valid] = l2_normalize_rows(self.rows[:, :n_valid],
+                                                       out_dtype=self.key_dtype,
+                                                       normalize=normalize)
+            self.key_norm = normalize
+        return self.keys
+
+    def to(self, device, dtype, n_valid):
+        self.device, self.dtype = device, dtype
+        if self.rows is not None:
+            self.rows = self.rows.to(device=device, dtype=dtype)
+            self.keys = self.keys.to(device=device)
+            if n_valid:
+                self.keys[:, :n_valid] = l2_normalize_rows(
+                    self.rows[:, :n_valid], out_dtype=self.key_dtype,
+                    normalize=bool(self.key_norm))
+
+
+def _device(device):
+    d = torch.device(device)
+    if d.type == 'cuda' and d.index is None and torch.cuda.is_available():
+        d = torch.device('cuda', torch.cuda.current_device())
+    return d
+
+
+def _ring_bf16(sw):
+    buf = sw.raw()
+    return buf if buf.dtype == torch.bfloat16 else buf.to(torch.bfloat16)
+
+
+class CSADecodingCache:
+    """CSA incremental decode state (``ops_decoding_cache.py:407-1070``) on the HIP backend."""
+
+    def __init__(self, B: int, c: int, c_I: int, m: int, win: int, device, dtype):
+        if B < 1:
+            raise ValueError(f"B={B} must be >= 1")
+        if c < 1:
+            raise ValueError(f"c={c} must be >= 1")
+        if c_I < 1:
+            raise ValueError(f"c_I={c_I} must be >= 1")
+        if m < 1:
+            raise ValueError(f"m={m} must be >= 1")
+        if win < 0:
+            raise ValueError(f"win={win} must be >= 0 (0 disables SW)")
+        self.B, self.c, self.c_I, self.m, self.win = B, c, c_I, m, win
+        _validate_cache_dtype(dtype)
+        self.device, self.dtype = _device(device), dtype
+        self._normalize_qk: bool = True
+        self.reset()
+
+    def reset(self) -> None:
+        self._acc = None          # 6 buffers [B, m, width] (projection dtype)
+        self._acc_len = 0
+        self._prev = None         # (Cb, Zb) of the last completed block, [B, m, c]
+        self._C = _BlockStore(self.B, self.c, self.device, self.dtype, torch.bfloat16)
+        self._K = _BlockStore(self.B, self.c_I, self.device, self.dtype, torch.float32)
+        self._sw = (SlidingWindowRingBuffer(self.B, self.win, self.c, self.device, self.dtype)
+                    if self.win > 0 else None)
+        self._n_tokens_seen = 0
+        self._n_blocks = 0
+
+    @property
+    def n_tokens_seen(self) -> int:
+        return self._n_tokens_seen
+
+    @property
+    def n_blocks(self) -> int:
+        return self._n_blocks
+
+    @property
+    def accumulator_len(self) -> int:
+        return self._acc_len
+
+    @property
+    def C_comp(self):
+        return None if self._C.rows is None else self._C.rows[:, :self._n_blocks]
+
+    @property
+    def K_IComp(self):
+        return None if self._K.rows is None else self._K.rows[:, :self._n_blocks]
+
+    @property
+    def sw_buffer(self):
+        return self._sw
+
+    def to(self, device=None, dtype=None) -> 'CSADecodingCache':
+        if device is not None:
+            self.device = torch.device(device)
+        if dtype is not None:
+            _validate_cache_dtype(dtype)
+            self.dtype = dtype
+        if self._acc is not None:
+            self._acc = [a.to(device=self.device) for a in self._acc]
+        if self._prev is not None:
+            self._prev = tuple(p.to(device=self.device) for p in self._prev)
+        self._C.to(self.device, self.dtype, self._n_blocks)
+        self._K.to(self.device, self.dtype, self._n_blocks)
+        if self._sw is not None:
+            self._sw.to(device=self.device, dtype=self.dtype)
+        return self
+
+    def append_step(self, Ca_new, Cb_new, Za_new, Zb_new, K_idx_new, Z_idx_new, Ba, Bb, B_idx):
+        """Append ``T_new`` tokens' projections; returns the new block indices."""
+        B, T_new, c = Ca_new.shape
+        if B != self.B:
+            raise ValueError(
+                f"CSADecodingCache.append_step: batch size {B} does not match cache's "
+                f"B={self.B}. Call reset() between sequences with different batch sizes.")
+        if c != self.c:
+            raise ValueError(
+                f"CSADecodingCache.append_step: c={c} does not match cache's c={self.c}.")
+        if K_idx_new.shape[-1] != self.c_I:
+            raise ValueError(
+                f"CSADecodingCache.append_step: c_I={K_idx_new.shape[-1]} does not match "
+                f"cache's c_I={self.c_I}.")
+        for _name, _t in [('Cb_new', Cb_new), ('Za_new', Za_new), ('Zb_new', Zb_new),
+                          ('K_idx_new', K_idx_new), ('Z_idx_new', Z_idx_new)]:
+            if _t.shape[1] != T_new:
+                raise ValueError(
+                    f"CSADecodingCache.append_step: {_name}.shape[1]={_t.shape[1]} does not "
+                    f"match Ca_new.shape[1]={T_new}. All inputs must share the same T_new.")
+        if T_new == 0:
+            return []
+        _lib.require_gpu("CSADecodingCache.append_step", Ca_new)
+        new = [Ca_new, Cb_new, Za_new, Zb_new, K_idx_new, Z_idx_new]
+        with torch.no_grad():
+            if self._sw is not None:
+                self._sw.append(l2_normalize_rows(Ca_new, out_dtype=torch.float32,
+                                                  normalize=self._normalize_qk).to(self.dtype))
+            if self._acc is None:
+                self._acc = [torch.empty(B, self.m, x.shape[-1], device=x.device, dtype=x.dtype)
+                             for x in new]
+            total = self._acc_len + T_new
+            nfull = total // self.m
+            rem = total - nfull * self.m
+            out_idx = []
+            if nfull:
+                take = nfull * self.m - self._acc_len
+                toks = [torch.cat([a[:, :self._acc_len], x[:, :take].to(a.dtype)], dim=1)
+                        for a, x in zip(self._acc, new)]
+                Ca, Cb, Za, Zb, Ki, Zi = toks
+                if self._prev is not None:
+                    z = torch.zeros_like(Ca[:, :self.m])
+                    Ca_s, Za_s = torch.cat([z, Ca], 1), torch.cat([z, Za], 1)
+                    Cb_s, Zb_s = torch.cat([self._prev[0], Cb], 1), torch.cat([self._prev[1], Zb], 1)
+                    rows = _compress_overlapped("CSADecodingCache", Ca_s, Cb_s, Za_s, Zb_s, Ba, Bb,
+                                                self.m)[:, 1:]
+                else:
+                    rows = _compress_overlapped("CSADecodingCache", Ca, Cb, Za, Zb, Ba, Bb, self.m)
+                krows = _compress("CSADecodingCache", Ki, Zi, B_idx, self.m)
+                self._C.push(self._n_blocks, rows, self._normalize_qk)
+                self._K.push(self._n_blocks, krows, self._normalize_qk)
+                out_idx = list(range(self._n_blocks, self._n_blocks + nfull))
+                self._n_blocks += nfull
+                self._prev = (Cb[:, -self.m:].clone(), Zb[:, -self.m:].clone())
+                for a, x in zip(self._acc, new):
+                    if rem:
+                        a[:, :rem] = x[:, T_new - rem:].to(a.dtype)
+            else:
+                for a, x in zip(self._acc, new):
+                    a[:, self._acc_len:total] = x.to(a.dtype)
+            self._acc_len = rem
+            self._n_tokens_seen += T_new
+        return out_idx
+
+    def forward_step(self, q, q_idx, w_idx, *, topk, nh, nIh, scale=None, sink_logits=None,
+                     use_ste=True, ste_mode='topk_columns', normalize_qk=True):
+        """CSA output ``[B, 1, nh, c]`` (fp32) for the last appended token."""
+        B, T_new = q.shape[0], q.shape[1]
+        if T_new != 1:
+            raise ValueError(
+                f"CSADecodingCache.forward_step: T_new={T_new} must be 1. For multi-token "
+                f"chunks, call append_step + forward_step in a loop (or use naive_csa on the "
+                f"full chunk and populate the cache via the prefill path).")
+        if B != self.B:
+            raise ValueError(
+                f"CSADecodingCache.forward_step: batch size {B} does not match cache's B={self.B}.")
+        if q.shape[2] != nh:
+            raise ValueError(f"q.shape[2]={q.shape[2]} does not match nh={nh}.")
+        if q_idx.shape[2] != nIh:
+            raise ValueError(f"q_idx.shape[2]={q_idx.shape[2]} does not match nIh={nIh}.")
+        if q.device != self.device:
+            raise ValueError(
+                f"CSADecodingCache.forward_step: q.device={q.device} does not match cache's "
+                f"device={self.device}. Call cache.to(device=q.device) or move q to the cache's "
+                f"device.")
+        if ste_mode not in ('topk_columns', 'full_softmax', 'aux_contrastive'):
+            raise ValueError(
+                f"ste_mode={ste_mode!r} must be one of 'topk_columns', "
+                f"'full_softmax', or 'aux_contrastive'.")
+        _lib.require_gpu("CSADecodingCache.forward_step", q)
+        core_scale = (1.0 if normalize_qk else self.c ** -0.5) if scale is None else scale
+        nb = self._n_blocks
+        n_win = self._sw.n_valid if self._sw is not None else 0
+        out = torch.zeros(B, 1, nh, self.c, device=q.device, dtype=torch.float32)
+        if nb == 0 and n_win == 0:
+            return out
+        if q.dtype == torch.float64:
+            raise NotImplementedError("float64 queries are not supported by the HIP kernels")
+        with torch.no_grad():
+            kv = self._C.keys_for(nb, normalize_qk) if nb else None
+            kn = self._K.keys_for(nb, normalize_qk) if nb else None
+            ring = _ring_bf16(self._sw) if n_win else None
+            qc = _aligned(q)
+            qi = _aligned(q_idx.to(q.dtype))
+            wi = None if w_idx is None else w_idx.to(q.dtype).contiguous()
+            ws = torch.empty(B, max(topk, 1), device=q.device, dtype=torch.int32)
+            self._last_indices = ws
+            sink = None if sink_logits is None else _f32(sink_logits, q.device)
+            cap_c = kv.shape[1] if kv is not None else 0
+            cap_k = kn.shape[1] if kn is not None else 0
+            _lib.call("kch_csa_decode_step", _lib.ptr(qc), _lib.ptr(qi), _lib.ptr(wi),
+                      _lib.ptr(kv), cap_c * self.c, _lib.ptr(kn), cap_k * self.c_I,
+                      _lib.ptr(ring), self.win * self.c, n_win, _lib.ptr(sink), _lib.ptr(out),
+                      _lib.ptr(ws), B, nb, nh, self.c, nIh, self.c_I, topk, float(core_scale),
+                      1.0 if normalize_qk else self.c_I ** -0.5, 0, int(normalize_qk),
+                      _lib.dtype_code("CSADecodingCache.forward_step", q.dtype), 0,
+                      _lib.stream_of(q))
+        return out
+
+
+class HCADecodingCache:
+    """HCA incremental decode state (``ops_decoding_cache.py:1077-1395``) on the HIP backend."""
+
+    def __init__(self, B: int, c: int, m2: int, win: int, device, dtype):
+        if B < 1:
+            raise ValueError(f"B={B} must be >= 1")
+        if c < 1:
+            raise ValueError(f"c={c} must be >= 1")
+        if m2 < 1:
+            raise ValueError(f"m2={m2} must be >= 1")
+        if win < 0:
+            raise ValueError(f"win={win} must be >= 0 (0 disables SW)")
+        self.B, self.c, self.m2, self.win = B, c, m2, win
+        _validate_cache_dtype(dtype)
+        self.device, self.dtype = _device(device), dtype
+        self._normalize_qk: bool = True
+        self.reset()
+
+    def reset(self) -> None:
+        self._acc = None
+        self._acc_len = 0
+        self._C = _BlockStore(self.B, self.c, self.device, self.dtype, torch.bfloat16)
+        self._sw = (SlidingWindowRingBuffer(self.B, self.win, self.c, self.device, self.dtype)
+                    if self.win > 0 else None)
+        self._n_tokens_seen = 0
+        self._n_blocks = 0
+
+    @property
+    def n_tokens_seen(self) -> int:
+        return self._n_tokens_seen
+
+    @property
+    def n_blocks(self) -> int:
+        return self._n_blocks
+
+    @property
+    def accumulator_len(self) -> int:
+        return self._acc_len
+
+    @property
+    def C_comp(self):
+        return None if self._C.rows is None else self._C.rows[:, :self._n_blocks]
+
+    @property
+    def sw_buffer(self):
+        return self._sw
+
+    def to(self, device=None, dtype=None) -> 'HCADecodingCache':
+        if device is not None:
+            self.device = torch.device(device)
+        if dtype is not None:
+            _validate_cache_dtype(dtype)
+            self.dtype = dtype
+        if self._acc is not None:
+            self._acc = [a.to(device=self.device) for a in self._acc]
+        self._C.to(self.device, self.dtype, self._n_blocks)
+        if self._sw is not None:
+            self._sw.to(device=self.device, dtype=self.dtype)
+        return self
+
+    def append_step(self, C_new, Z_new, B_pos):
+        """Append ``T_new`` tokens' projections; returns the new block indices."""
+        B, T_new, c = C_new.shape
+        if B != self.B:
+            raise ValueError(
+                f"HCADecodingCache.append_step: batch size {B} does not match cache's "
+                f"B={self.B}. Call reset() between sequences with different batch sizes.")
+        if c != self.c:
+            raise ValueError(
+                f"HCADecodingCache.append_step: c={c} does not match cache's c={self.c}.")
+        if Z_new.shape[1] != T_new:
+            raise ValueError(
+                f"HCADecodingCache.append_step: Z_new.shape[1]={Z_new.shape[1]} does not "
+                f"match C_new.shape[1]={T_new}.")
+        if T_new == 0:
+            return []
+        _lib.require_gpu("HCADecodingCache.append_step", C_new)
+        new = [C_new, Z_new]
+        with torch.no_grad():
+            if self._sw is not None:
+                self._sw.append(l2_normalize_rows(C_new, out_dtype=torch.float32,
+                                                  normalize=self._normalize_qk).to(self.dtype))
+            if self._acc is None:
+                self._acc = [torch.empty(B, self.m2, x.shape[-1], device=x.device, dtype=x.dtype)
+                             for x in new]
+            total = self._acc_len + T_new
+            nfull = total // self.m2
+            rem = total - nfull * self.m2
+            out_idx = []
+            if nfull:
+                take = nfull * self.m2 - self._acc_len
+                Cc, Zc = (torch.cat([a[:, :self._acc_len], x[:, :take].to(a.dtype)], dim=1)
+                          for a, x in zip(self._acc, new))
+                rows = _compress("HCADecodingCache", Cc, Zc, B_pos, self.m2)
+                self._C.push(self._n_blocks, rows, self._normalize_qk)
+                out_idx = list(range(self._n_blocks, self._n_blocks + nfull))
+                self._n_blocks += nfull
+                for a, x in zip(self._acc, new):
+                    if rem:
+                        a[:, :rem] = x[:, T_new - rem:].to(a.dtype)
+            else:
+                for a, x in zip(self._acc, new):
+                    a[:, self._acc_len:total] = x.to(a.dtype)
+            self._acc_len = rem
+            self._n_tokens_seen += T_new
+        return out_idx
+
+    def forward_step(self, q, *, nh, scale=None, sink_logits=None, normalize_qk=True):
+        """HCA output ``[B, 1, nh, c]`` (fp32) for the last appended token."""
+        B, T_new = q.shape[0], q.shape[1]
+        if T_new != 1:
+            raise ValueError(f"HCADecodingCache.forward_step: T_new={T_new} must be 1.")
+        if B != self.B:
+            raise ValueError(
+                f"HCADecodingCache.forward_step: batch size {B} does not match cache's B={self.B}.")
+        if q.shape[2] != nh:
+            raise ValueError(f"q.shape[2]={q.shape[2]} does not match nh={nh}.")
+        if q.device != self.device:
+            raise ValueError(
+                f"HCADecodingCache.forward_step: q.device={q.device} does not match cache's "
+                f"device={self.device}. Call cache.to(device=q.device) or move q to the cache's "
+                f"device.")
+        _lib.require_gpu("HCADecodingCache.forward_step", q)
+        core_scale = (1.0 if normalize_qk else self.c ** -0.5) if scale is None else scale
+        nb = self._n_blocks
+        n_win = self._sw.n_valid if self._sw is not None else 0
+        out = torch.zeros(B, 1, nh, self.c, device=q.device, dtype=torch.float32)
+        if nb == 0 and n_win == 0:
+            return out
+        if q.dtype == torch.float64:
+            raise NotImplementedError("float64 queries are not supported by the HIP kernels")
+        with torch.no_grad():
+            kv = self._C.keys_for(nb, normalize_qk) if nb else None
+            ring = _ring_bf16(self._sw) if n_win else None
+            qc = _aligned(q)
+            sink = None if sink_logits is None else _f32(sink_logits, q.device)
+            cap = kv.shape[1] if kv is not None else 0
+            _lib.call("kch_hca_decode_step", _lib.ptr(qc), _lib.ptr(kv), cap * self.c,
+                      _lib.ptr(ring), self.win * self.c, n_win, _lib.ptr(sink), _lib.ptr(out), B,
+                      nb, nh, self.c, float(core_scale), 0,
+                      _lib.dtype_code("HCADecodingCache.forward_step", q.dtype), 0,
+                      _lib.stream_of(q))
+        return out
+
+
+_SlidingWindowRingBuffer = SlidingWindowRingBuffer
+
+__all__ = ["CSADecodingCache", "HCADecodingCache", "SlidingWindowRingBuffer"]

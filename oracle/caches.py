@@ -80,8 +80,11 @@ class CSACacheOracle:
         return new
 
     def forward_step(self, q, q_idx, w_idx, *, topk, scale=None, sink_logits=None,
-                     normalize_qk=True):
-        """``q`` ``[B,1,nh,c]`` (already normalised), returns ``[B,1,nh,c]`` fp32."""
+                     normalize_qk=True, indices=None):
+        """``q`` ``[B,1,nh,c]`` (already normalised), returns ``[B,1,nh,c]`` fp32.
+
+        ``indices`` (``[B,1,topk]``, -1 = unused) replaces the indexer's selection.
+        """
         q = np.asarray(q, np.float32)
         Bn, _, nh, c = q.shape
         t = self.n_tokens_seen - 1
@@ -94,9 +97,12 @@ class CSACacheOracle:
         else:
             cbm = (np.arange(nb) < (t + 1) // self.m)[None, :]
             Cn = l2_normalize(self.C_comp) if normalize_qk else self.C_comp
-            idx = lightning_indexer(np.asarray(q_idx, np.float32), self.K_IComp,
-                                    np.asarray(w_idx, np.float32), topk, None, cbm,
-                                    normalize_qk)
+            if indices is None:
+                idx = lightning_indexer(np.asarray(q_idx, np.float32), self.K_IComp,
+                                        np.asarray(w_idx, np.float32), topk, None, cbm,
+                                        normalize_qk)
+            else:
+                idx = np.asarray(indices, np.int64).reshape(Bn, 1, -1)
             if idx.shape[-1] == 0:
                 scores = np.zeros((Bn, 1, nh, 0), np.float32)
                 valid = np.zeros((Bn, 1, 0), bool)
