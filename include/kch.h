@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define KCH_ABI_VERSION 2
+#define KCH_ABI_VERSION 3
 
 #define KCH_OK 0
 #define KCH_ERR_INVALID 1     /* bad pointer / shape / argument */
@@ -173,6 +173,30 @@ int kch_hca_decode_step(const void* q, const void* kv_comp, long long kv_bstride
                         long long ring_bstride, int ring_len, const float* sink, void* out, int B,
                         int nb, int nh, int hd, float scale, int normalize_q, int qdtype, int odtype,
                         void* stream);
+
+/*
+ * Causal depthwise convolution with kernel 3 of the KDA layer
+ * (KDAHybridLayer.forward_functional, ops_fused.py:480-527: nn.Conv1d with
+ * groups=d over [lookback ; x], or over [0 ; 0 ; x] without a lookback):
+ *   out[b,t,c] = bias[c] + w[c,0] x[b,t-2,c] + w[c,1] x[b,t-1,c] + w[c,2] x[b,t,c]
+ *   x, out [B,T,d]; lookback [B,2,d] or NULL (zeros) supplies x[b,-2], x[b,-1];
+ *   weight [d,3] (the Conv1d weight [d,1,3]); bias [d] or NULL. All of dtype.
+ * For d % 8 == 0, x / out / lookback must be 16-byte aligned.
+ */
+int kch_short_conv(const void* x, const void* lookback, const void* weight, const void* bias,
+                   void* out, int B, int T, int d, int dtype, void* stream);
+
+/*
+ * KDA layer activations (ops_fused.py:559-581): from the projection rows
+ *   proj[r] = [q (H*K) | k (H*K) | v (HV*V) | beta logits (HV) | ...] (ld_proj apart)
+ *   gl[r]   = g_up(g_down(x_conv)) (HV*K, ld_gl apart),  r = b*T + t,
+ * writes q, k = L2norm(silu(.)) per head [B,T,H,K]; v = silu(.) [B,T,HV,V];
+ * g = -softplus(gl) * decay_scale [B,T,HV,K]; beta = sigmoid(.) [B,T,HV].
+ * K <= 256.
+ */
+int kch_kda_gates(const void* proj, long long ld_proj, const void* gl, long long ld_gl, void* q,
+                  void* k, void* v, void* g, void* beta, int B, int T, int H, int HV, int K, int V,
+                  float decay_scale, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -302,4 +302,39 @@ int kch_hca_decode_step(const void* q, const void* kv_comp, long long kv_bstride
   return hip_status(fn, kch::attn_dispatch(p, false, qdtype, odtype, (hipStream_t)stream));
 }
 
+int kch_short_conv(const void* x, const void* lookback, const void* weight, const void* bias,
+                   void* out, int B, int T, int d, int dtype, void* stream) {
+  const char* fn = "kch_short_conv";
+  if (!dtype_ok(dtype)) return fail(KCH_ERR_INVALID, "%s: unknown dtype %d", fn, dtype);
+  if (B < 0 || T < 0 || d < 1) return fail(KCH_ERR_INVALID, "%s: bad sizes B=%d T=%d d=%d", fn, B, T, d);
+  if ((long long)B * T * d >= (1LL << 40)) return fail(KCH_ERR_INVALID, "%s: tensor too large", fn);
+  if ((long long)B * T == 0) return KCH_OK;
+  if (!x || !weight || !out) return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
+  if (d % 8 == 0) {
+    const uintptr_t a = (uintptr_t)x | (uintptr_t)out | (uintptr_t)lookback;
+    if (a % 16) return fail(KCH_ERR_INVALID, "%s: x / out / lookback must be 16-byte aligned", fn);
+  }
+  kch::ShortConvParams p{x, lookback, weight, bias, out, B, T, d};
+  return hip_status(fn, kch::short_conv_dispatch(p, dtype, (hipStream_t)stream));
+}
+
+int kch_kda_gates(const void* proj, long long ld_proj, const void* gl, long long ld_gl, void* q,
+                  void* k, void* v, void* g, void* beta, int B, int T, int H, int HV, int K, int V,
+                  float decay_scale, int dtype, void* stream) {
+  const char* fn = "kch_kda_gates";
+  if (!dtype_ok(dtype)) return fail(KCH_ERR_INVALID, "%s: unknown dtype %d", fn, dtype);
+  if (B < 0 || T < 0 || H < 1 || HV < 1 || K < 1 || V < 1)
+    return fail(KCH_ERR_INVALID, "%s: bad sizes", fn);
+  if (K > 256) return fail(KCH_ERR_UNSUPPORTED, "%s: K=%d > 256 not supported", fn, K);
+  if (ld_proj < 2LL * H * K + (long long)HV * V + HV || ld_gl < (long long)HV * K)
+    return fail(KCH_ERR_INVALID, "%s: row strides too small", fn);
+  if ((long long)B * T >= (1LL << 31)) return fail(KCH_ERR_INVALID, "%s: too many rows", fn);
+  if ((long long)B * T == 0) return KCH_OK;
+  if (!proj || !gl || !q || !k || !v || !g || !beta)
+    return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
+  kch::KdaGatesParams p{proj, ld_proj, gl, ld_gl, q, k, v, g, beta, B, T, H, HV, K, V,
+                        decay_scale};
+  return hip_status(fn, kch::kda_gates_dispatch(p, dtype, (hipStream_t)stream));
+}
+
 }  // extern "C"

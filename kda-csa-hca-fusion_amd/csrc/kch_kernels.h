@@ -28,4 +28,36 @@ hipError_t kda_chunk_dispatch(const KdaParams& p, int dtype, hipStream_t stream)
 hipError_t kda_chunk_lp_dispatch(const KdaParams& p, int dtype, hipStream_t stream);
 hipError_t kda_recurrent_dispatch(const KdaParams& p, int dtype, hipStream_t stream);
 
+// Causal depthwise convolution, kernel 3 (kda_frontend.hip).
+//   x, out : [B, T, d]   lookback : [B, 2, d] or null (zeros)
+//   weight : [d, 3]      bias : [d] or null            (all of the dtype)
+struct ShortConvParams {
+  const void* x;
+  const void* lookback;
+  const void* weight;
+  const void* bias;
+  void* out;
+  int B, T, d;
+};
+hipError_t short_conv_dispatch(const ShortConvParams& p, int dtype, hipStream_t stream);
+
+// KDA activations (kda_frontend.hip). Row r = b*T + t of `proj` holds
+// [q (H*K) | k (H*K) | v (HV*V) | beta logits (HV) | ...], ld_proj elements
+// apart; row r of `gl` holds the HV*K gate pre-activations, ld_gl apart.
+// Outputs are contiguous: q, k [B,T,H,K]; v [B,T,HV,V]; g [B,T,HV,K]; beta [B,T,HV].
+struct KdaGatesParams {
+  const void* proj;
+  long long ld_proj;
+  const void* gl;
+  long long ld_gl;
+  void* q;
+  void* k;
+  void* v;
+  void* g;
+  void* beta;
+  int B, T, H, HV, K, V;
+  float decay_scale;
+};
+hipError_t kda_gates_dispatch(const KdaGatesParams& p, int dtype, hipStream_t stream);
+
 }  // namespace kch

@@ -1,0 +1,174 @@
+// KDA layer front-end: the causal depthwise short convolution and the fused
+// q/k/v/g/beta activations that sit between the layer's projection GEMMs and
+// the KDA kernels (KDAHybridLayer.forward_functional, ops_fused.py:480-581).
+//
+// Both kernels are HBM-bound elementwise passes: fp32 arithmetic, one rounding
+// to the storage dtype per output element.
+
+#include <hip/hip_runtime.h>
+
+#include "attn_common.h"
+#include "kch_kernels.h"
+
+namespace kch {
+
+namespace {
+
+// Eight consecutive channels as fp32 (VEC=8) or one channel (VEC=1).
+template <typename T, int VEC>
+__device__ __forceinline__ void load_vec(const T* p, float* f) {
+  if constexpr (VEC == 8) {
+    Load8<T>::run(p, f);
+  } else {
+    f[0] = to_f32(*p);
+  }
+}
+
+template <typename T, int VEC>
+__device__ __forceinline__ void store_vec(T* p, const float* f) {
+  if constexpr (VEC == 8 && sizeof(T) == 2) {
+    union { T h[8]; uint4 u; } r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r.h[i] = from_f32<T>(f[i]);
+    *reinterpret_cast<uint4*>(p) = r.u;
+  } else if constexpr (VEC == 8) {
+    reinterpret_cast<float4*>(p)[0] = make_float4(f[0], f[1], f[2], f[3]);
+    reinterpret_cast<float4*>(p)[1] = make_float4(f[4], f[5], f[6], f[7]);
+  } else {
+    *p = from_f32<T>(f[0]);
+  }
+}
+
+// out[b,t,c] = bias[c] + w[c,0] x[t-2] + w[c,1] x[t-1] + w[c,2] x[t], where
+// x[-2], x[-1] are lookback[b,0], lookback[b,1] (zeros without a lookback).
+// A thread owns VEC channels of a run of RUN tokens and slides the window,
+// so every input row is read once; a wave covers 64 channel vectors of the
+// same tokens (contiguous 1 KB rows for VEC=8, bf16).
+template <typename T, int VEC, int RUN>
+__global__ __launch_bounds__(256) void short_conv_kernel(ShortConvParams p) {
+  const int nvec = p.d / VEC;
+  const int runs = (p.T + RUN - 1) / RUN;
+  const long long id = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (id >= (long long)nvec * runs * p.B) return;
+  const int cv = (int)(id % nvec);
+  const long long rest = id / nvec;
+  const int run = (int)(rest % runs);
+  const int b = (int)(rest / runs);
+  const int c0 = cv * VEC;
+  const T* x = static_cast<const T*>(p.x) + (size_t)b * p.T * p.d + c0;
+  const T* w = static_cast<const T*>(p.weight);
+  float w0[VEC], w1[VEC], w2[VEC], bias[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) {
+    w0[i] = to_f32(w[(c0 + i) * 3 + 0]);
+    w1[i] = to_f32(w[(c0 + i) * 3 + 1]);
+    w2[i] = to_f32(w[(c0 + i) * 3 + 2]);
+    bias[i] = p.bias ? to_f32(static_cast<const T*>(p.bias)[c0 + i]) : 0.f;
+  }
+  const int t0 = run * RUN;
+  const int t1 = min(t0 + RUN, p.T);
+  float xm2[VEC], xm1[VEC], cur[VEC], o[VEC];
+  auto fetch = [&](int t, float* f) {
+    if (t >= 0) {
+      load_vec<T, VEC>(x + (size_t)t * p.d, f);
+    } else if (p.lookback) {
+      load_vec<T, VEC>(static_cast<const T*>(p.lookback) + ((size_t)b * 2 + (t + 2)) * p.d + c0, f);
+    } else {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) f[i] = 0.f;
+    }
+  };
+  fetch(t0 - 2, xm2);
+  fetch(t0 - 1, xm1);
+  T* out = static_cast<T*>(p.out) + (size_t)b * p.T * p.d + c0;
+  for (int t = t0; t < t1; ++t) {
+    load_vec<T, VEC>(x + (size_t)t * p.d, cur);
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      o[i] = fmaf(w2[i], cur[i], fmaf(w1[i], xm1[i], fmaf(w0[i], xm2[i], bias[i])));
+      xm2[i] = xm1[i];
+      xm1[i] = cur[i];
+    }
+    store_vec<T, VEC>(out + (size_t)t * p.d, o);
+  }
+}
+
+__device__ __forceinline__ float silu_f(float x) { return x / (1.f + __expf(-x)); }
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.f / (1.f + __expf(-x)); }
+// torch's softplus (beta 1, threshold 20): x above the threshold, else log1p(e^x)
+__device__ __forceinline__ float softplus_f(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
+
+// One workgroup per token row: waves take the 2H q/k head vectors (silu, then
+// per-head L2 normalisation), then all threads take v (silu), g
+// (-softplus * decay) and beta (sigmoid).
+template <typename T>
+__global__ __launch_bounds__(256) void kda_gates_kernel(KdaGatesParams p) {
+  const long long row = blockIdx.x;
+  const T* pr = static_cast<const T*>(p.proj) + row * p.ld_proj;
+  const T* gr = static_cast<const T*>(p.gl) + row * p.ld_gl;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int HK = p.H * p.K;
+  for (int h = wave; h < 2 * p.H; h += 4) {
+    const T* src = pr + (size_t)h * p.K;
+    float vals[4];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = lane + 64 * j;
+      vals[j] = e < p.K ? silu_f(to_f32(src[e])) : 0.f;
+      ss += vals[j] * vals[j];
+    }
+    const float inv = l2_inv(wave_sum(ss));
+    T* dst = h < p.H ? static_cast<T*>(p.q) + (row * p.H + h) * p.K
+                     : static_cast<T*>(p.k) + (row * p.H + (h - p.H)) * p.K;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = lane + 64 * j;
+      if (e < p.K) dst[e] = from_f32<T>(vals[j] * inv);
+    }
+  }
+  const int nv = p.HV * p.V, ng = p.HV * p.K;
+  T* v = static_cast<T*>(p.v) + row * nv;
+  for (int i = threadIdx.x; i < nv; i += 256) v[i] = from_f32<T>(silu_f(to_f32(pr[2 * HK + i])));
+  T* g = static_cast<T*>(p.g) + row * ng;
+  for (int i = threadIdx.x; i < ng; i += 256)
+    g[i] = from_f32<T>(-softplus_f(to_f32(gr[i])) * p.decay_scale);
+  T* beta = static_cast<T*>(p.beta) + row * p.HV;
+  for (int i = threadIdx.x; i < p.HV; i += 256)
+    beta[i] = from_f32<T>(sigmoid_f(to_f32(pr[2 * HK + nv + i])));
+}
+
+template <typename T>
+hipError_t short_conv_launch(const ShortConvParams& p, hipStream_t s) {
+  constexpr int RUN = 16;
+  const bool vec = (p.d % 8 == 0);
+  const long long runs = (p.T + RUN - 1) / RUN;
+  const long long threads = (long long)(vec ? p.d / 8 : p.d) * runs * p.B;
+  const dim3 grid((unsigned)((threads + 255) / 256)), block(256);
+  if (vec)
+    hipLaunchKernelGGL((short_conv_kernel<T, 8, RUN>), grid, block, 0, s, p);
+  else
+    hipLaunchKernelGGL((short_conv_kernel<T, 1, RUN>), grid, block, 0, s, p);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t short_conv_dispatch(const ShortConvParams& p, int dtype, hipStream_t s) {
+  if (dtype == DT_F32) return short_conv_launch<float>(p, s);
+  if (dtype == DT_BF16) return short_conv_launch<bf16_t>(p, s);
+  return short_conv_launch<_Float16>(p, s);
+}
+
+hipError_t kda_gates_dispatch(const KdaGatesParams& p, int dtype, hipStream_t s) {
+  const dim3 grid((unsigned)((long long)p.B * p.T)), block(256);
+  if (dtype == DT_F32)
+    hipLaunchKernelGGL((kda_gates_kernel<float>), grid, block, 0, s, p);
+  else if (dtype == DT_BF16)
+    hipLaunchKernelGGL((kda_gates_kernel<bf16_t>), grid, block, 0, s, p);
+  else
+    hipLaunchKernelGGL((kda_gates_kernel<_Float16>), grid, block, 0, s, p);
+  return hipGetLastError();
+}
+
+}  // namespace kch

@@ -6,6 +6,8 @@ in ``include/kch.h``. Tensors must be on a ROCm GPU; there is no CPU path.
 """
 
 from .decoding_cache import CSADecodingCache, HCADecodingCache, SlidingWindowRingBuffer
+from .hybrid import (CSAHybridLayer, HCAHybridLayer, HybridConfig, HybridDecoding,
+                     HybridKCHAttention, KDAHybridLayer)
 from .ops_csa import (csa_compress_kv, csa_compress_kv_overlapped, csa_core,
                       csa_lightning_indexer, l2_normalize_rows, naive_csa)
 from .ops_hca import hca_core, naive_hca
@@ -13,6 +15,12 @@ from .ops_kda import naive_chunk_kda, naive_recurrent_kda
 from .ops_kda_backend import hip_available, kda_forward, validate_kda_backend
 
 __all__ = [
+    "CSAHybridLayer",
+    "HCAHybridLayer",
+    "HybridConfig",
+    "HybridDecoding",
+    "HybridKCHAttention",
+    "KDAHybridLayer",
     "CSADecodingCache",
     "HCADecodingCache",
     "SlidingWindowRingBuffer",

@@ -38,6 +38,8 @@ _SIGNATURES = {
     "kch_csa_decode_step": [_P, _P, _P, _P, _L, _P, _L, _P, _L, _I, _P, _P, _P] + [_I] * 7
                            + [_F, _F, _I, _I, _I, _I, _P],
     "kch_hca_decode_step": [_P, _P, _L, _P, _L, _I, _P, _P] + [_I] * 4 + [_F, _I, _I, _I, _P],
+    "kch_short_conv": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
+    "kch_kda_gates": [_P, _L, _P, _L, _P, _P, _P, _P, _P] + [_I] * 6 + [_F, _I, _P],
 }
 
 EXPORTED = ["kch_abi_version", "kch_last_error"] + sorted(_SIGNATURES)

@@ -1,0 +1,657 @@
+"""Hybrid KDA / CSA / HCA stack on the HIP backend.
+
+Drop-in twins of the reference's composition layer:
+
+``HybridConfig``        <- ``/root/reference/ops_fused.py:65-313`` (``kda_backend="hip"``)
+``_Fp32LayerNorm``      <- ``ops_fused.py:42-60``
+``KDAHybridLayer``      <- ``ops_fused.py:316-609``
+``CSAHybridLayer``      <- ``ops_fused.py:612-713``
+``HCAHybridLayer``      <- ``ops_fused.py:716-739``
+``HybridKCHAttention``  <- ``ops_fused.py:742-1131``
+``HybridDecoding``      <- ``/root/reference/run_decoding.py:601-851``
+
+Parameter and buffer names, shapes and the layout rule are the reference's, so
+a reference ``state_dict`` loads unchanged. The forward passes run on a ROCm
+GPU: projections are torch GEMMs (hipBLASLt); the KDA short convolution and
+activations, KDA itself, CSA, HCA and the decode caches are ``libkch.so``
+kernels. Forward only: every forward runs under ``torch.no_grad()``.
+
+``HybridDecoding`` takes any ``HybridConfig`` (the reference hard-codes a tiny
+geometry with ``kda_chunk_size=0``); prefill goes through the chunked KDA
+kernel and the bulk cache population, decode through the T=1 recurrent step
+and the cache decode kernels.
+"""
+
+from __future__ import annotations
+
+import logging
+import math
+import os
+import warnings
+from dataclasses import dataclass
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _lib
+from .decoding_cache import CSADecodingCache, HCADecodingCache
+from .ops_csa import naive_csa
+from .ops_hca import naive_hca
+from .ops_kda_backend import kda_forward, validate_kda_backend
+
+logger = logging.getLogger(__name__)
+
+_CONV_K = 3  # short-conv kernel size (ops_fused.py:333)
+
+
+class _Fp32LayerNorm(nn.LayerNorm):
+    """LayerNorm computed in fp32, returned in the input dtype (``ops_fused.py:42-60``)."""
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if x.dtype in (torch.float16, torch.bfloat16):
+            out = F.layer_norm(x.float(), self.normalized_shape, self.weight.float(),
+                               self.bias.float(), self.eps)
+            return out.to(x.dtype)
+        return super().forward(x)
+
+
+def _is_int(v) -> bool:
+    return isinstance(v, int) and not isinstance(v, bool)
+
+
+@dataclass
+class HybridConfig:
+    """Fields, defaults and validation of ``ops_fused.py:65-313``.
+
+    ``kda_backend`` defaults to ``"hip"``, the backend this package provides.
+    """
+
+    d_model: int = 256
+    n_heads_qk: int = 4
+    n_heads_v: int = 4
+    head_dim_k: int = 64
+    head_dim_v: int = 64
+    kda_chunk_size: int = 64
+    kda_backend: str = "hip"
+    csa_m: int = 16
+    csa_topk: int = 8
+    csa_nh: int = 4
+    csa_c: int = 64
+    csa_dc: int = 128
+    csa_nIh: int = 2
+    csa_cI: int = 32
+    csa_sliding_window: int = 16
+    hca_m2: int = 64
+    hca_nh: int = 4
+    hca_c: int = 64
+    hca_dc: int = 128
+    hca_sliding_window: int = 16
+    n_kda: int = 3
+    n_csa: int = 1
+    n_hca: int = 1
+    kda_decay_scale: float = 0.1
+    init_std: float = 0.02
+    dropout: float = 0.0
+
+    def __post_init__(self):
+        # dropout: type, finiteness and range first, then "not implemented"
+        # for a valid non-zero rate (ops_fused.py:121-150)
+        if not isinstance(self.dropout, (int, float)):
+            raise TypeError(f"HybridConfig.dropout={self.dropout!r} must be a float, "
+                            f"got {type(self.dropout).__name__}.")
+        if isinstance(self.dropout, bool):
+            raise TypeError(f"HybridConfig.dropout={self.dropout!r} must be a float, got bool.")
+        if math.isnan(self.dropout) or math.isinf(self.dropout):
+            raise ValueError(f"HybridConfig.dropout={self.dropout} must be finite (not NaN or Inf).")
+        if self.dropout < 0.0 or self.dropout > 1.0:
+            raise ValueError(f"HybridConfig.dropout={self.dropout} must be in [0.0, 1.0].")
+        if self.dropout != 0.0:
+            raise NotImplementedError(
+                f"HybridConfig.dropout={self.dropout} is not yet implemented: the KDA/CSA/HCA "
+                f"sub-layers apply no dropout. Set dropout=0.0.")
+        validate_kda_backend(self.kda_backend)
+        # head counts and the GVA factor (ops_fused.py:157-175)
+        if not _is_int(self.n_heads_qk) or self.n_heads_qk < 1:
+            raise ValueError(f"n_heads_qk={self.n_heads_qk!r} must be a positive int")
+        if not _is_int(self.n_heads_v) or self.n_heads_v < 1:
+            raise ValueError(f"n_heads_v={self.n_heads_v!r} must be a positive int")
+        if self.n_heads_v % self.n_heads_qk != 0:
+            raise ValueError(
+                f"n_heads_v={self.n_heads_v} must be divisible by n_heads_qk={self.n_heads_qk} "
+                f"(KDA GVA factor G = HV // H must be an integer).")
+        # strictly positive dimensions (ops_fused.py:176-203)
+        for name in ("d_model", "head_dim_k", "head_dim_v", "csa_m", "csa_c", "csa_dc", "csa_cI",
+                     "csa_nIh", "hca_m2", "hca_c", "hca_dc"):
+            val = getattr(self, name)
+            if not _is_int(val):
+                raise ValueError(f"HybridConfig.{name}={val!r} must be a positive int.")
+            if val < 1:
+                raise ValueError(f"HybridConfig.{name}={val} must be >= 1.")
+        if not isinstance(self.kda_chunk_size, int):
+            raise ValueError(
+                f"kda_chunk_size={self.kda_chunk_size!r} must be an int (>= 1 enables the chunk "
+                f"path; <= 0 forces the recurrent path; default 64).")
+        # layer counts (ops_fused.py:237-262)
+        for name in ("n_kda", "n_csa", "n_hca"):
+            val = getattr(self, name)
+            if not _is_int(val):
+                raise ValueError(f"HybridConfig.{name}={val!r} must be an int.")
+            if val < 0:
+                raise ValueError(f"HybridConfig.{name}={val} must be >= 0.")
+        if self.n_kda + self.n_csa + self.n_hca == 0:
+            raise ValueError("HybridConfig has n_kda=n_csa=n_hca=0; the model would have no "
+                             "attention layers at all.")
+        # CSA / HCA branch parameters (ops_fused.py:263-296)
+        if not _is_int(self.csa_topk) or self.csa_topk < 0:
+            raise ValueError(f"csa_topk={self.csa_topk!r} must be a non-negative int "
+                             f"(0 disables sparse selection).")
+        if not _is_int(self.csa_nh) or self.csa_nh < 1:
+            raise ValueError(f"csa_nh={self.csa_nh!r} must be a positive int (head count).")
+        if not _is_int(self.csa_sliding_window) or self.csa_sliding_window < 0:
+            raise ValueError(f"csa_sliding_window={self.csa_sliding_window!r} must be a "
+                             f"non-negative int (0 disables the branch).")
+        if not _is_int(self.hca_nh) or self.hca_nh < 1:
+            raise ValueError(f"hca_nh={self.hca_nh!r} must be a positive int (head count).")
+        if not _is_int(self.hca_sliding_window) or self.hca_sliding_window < 0:
+            raise ValueError(f"hca_sliding_window={self.hca_sliding_window!r} must be a "
+                             f"non-negative int (0 disables the branch).")
+        # KDA decay scale (ops_fused.py:297-313)
+        if not isinstance(self.kda_decay_scale, (int, float)):
+            raise ValueError(f"kda_decay_scale={self.kda_decay_scale!r} must be a number.")
+        if not math.isfinite(self.kda_decay_scale):
+            raise ValueError(f"kda_decay_scale={self.kda_decay_scale} must be finite.")
+        if self.kda_decay_scale < 0:
+            raise ValueError(f"kda_decay_scale={self.kda_decay_scale} must be >= 0.")
+
+
+class _FusedWeight:
+    """Row-concatenation of several weight matrices, rebuilt only when one of
+    them changes (storage, in-place version, dtype or device)."""
+
+    def __init__(self):
+        self._key = None
+        self._w = None
+
+    def get(self, params, dtype, device) -> torch.Tensor:
+        key = tuple((p.data_ptr(), p._version) for p in params) + (dtype, device)
+        if key != self._key:
+            self._w = torch.cat([p.detach() for p in params], 0).to(device=device, dtype=dtype)
+            self._key = key
+        return self._w
+
+
+class KDAHybridLayer(nn.Module):
+    """KDA sub-layer (``ops_fused.py:316-609``).
+
+    The short convolution and the q/k/v/g/beta activations run in
+    ``kch_short_conv`` / ``kch_kda_gates``; q, k, v, beta and the gate's
+    down-projection are one GEMM against the concatenated weights.
+    """
+
+    def __init__(self, cfg: HybridConfig):
+        super().__init__()
+        self.cfg = cfg
+        d, H, K, V = cfg.d_model, cfg.n_heads_qk, cfg.head_dim_k, cfg.head_dim_v
+        self.q_proj = nn.Linear(d, H * K, bias=False)
+        self.k_proj = nn.Linear(d, H * K, bias=False)
+        self.v_proj = nn.Linear(d, cfg.n_heads_v * V, bias=False)
+        self.g_down = nn.Linear(d, K, bias=False)
+        self.g_up = nn.Linear(K, cfg.n_heads_v * K, bias=False)
+        self.beta = nn.Linear(d, cfg.n_heads_v, bias=False)
+        self.o_proj = nn.Linear(cfg.n_heads_v * V, d, bias=False)
+        self.short_conv = nn.Conv1d(d, d, kernel_size=_CONV_K, padding=0, groups=d, bias=True)
+        # a buffer so that .bfloat16() rounds it like the reference's (ops_fused.py:342-344)
+        self.register_buffer('scale', torch.tensor(K ** -0.5), persistent=False)
+        self.register_buffer('_conv_lookback', None, persistent=False)
+        self._fused = _FusedWeight()
+
+    def reset_conv_state(self) -> None:
+        self._conv_lookback = None
+
+    def _scale_value(self) -> float:
+        # K^-0.5 rounded to the buffer's dtype, computed on the host (no device sync)
+        return float(torch.tensor(self.cfg.head_dim_k ** -0.5).to(self.scale.dtype))
+
+    def forward(self, x: torch.Tensor, state: torch.Tensor | None = None):
+        """Stateful forward: reads and writes ``self._conv_lookback`` (``ops_fused.py:365-389``)."""
+        o, new_state, new_lookback = self.forward_functional(x, state, self._conv_lookback)
+        self._conv_lookback = new_lookback
+        return o, new_state
+
+    def forward_functional(self, x: torch.Tensor, state: torch.Tensor | None,
+                           conv_lookback: torch.Tensor | None, *, detach_lookback: bool = True):
+        """Side-effect-free forward (``ops_fused.py:391-609``).
+
+        Returns ``(output [B,T,d], new_state [B,HV,K,V] fp32, new_lookback [B,2,d] | None)``.
+        """
+        B, T, d = x.shape
+        cfg = self.cfg
+        H, K, V, HV = cfg.n_heads_qk, cfg.head_dim_k, cfg.head_dim_v, cfg.n_heads_v
+        if T == 0:  # ops_fused.py:468-479
+            if state is not None and state.shape[0] == B:
+                new_state = state.to(device=x.device, dtype=torch.float32)
+            else:
+                new_state = torch.zeros(B, HV, K, V, device=x.device, dtype=torch.float32)
+            lb = conv_lookback
+            if lb is not None:
+                lb = None if lb.shape[0] != B else lb.to(device=x.device, dtype=x.dtype).clone()
+            return x.new_zeros(B, 0, d), new_state, lb
+        _lib.require_gpu("KDAHybridLayer", x)
+        lookback = conv_lookback
+        if lookback is not None:  # batch / device / dtype guards (ops_fused.py:500-518)
+            if lookback.shape[0] != B:
+                lookback = None
+            else:
+                lookback = lookback.to(device=x.device, dtype=x.dtype)
+        with torch.no_grad():
+            xc = x.contiguous()
+            if xc.data_ptr() % 16:
+                xc = xc.clone()
+            lb = None
+            if lookback is not None:
+                lb = lookback.contiguous()
+                if lb.data_ptr() % 16:
+                    lb = lb.clone()
+            # new lookback: the last two rows of [lookback ; x] (zeros if shorter)
+            if T >= _CONV_K - 1:
+                new_lookback = x[:, -(_CONV_K - 1):].clone()
+            elif lookback is not None:
+                new_lookback = torch.cat([lookback, x], dim=1)[:, -(_CONV_K - 1):].clone()
+            else:
+                new_lookback = torch.cat([x.new_zeros(B, _CONV_K - 1 - T, d), x], dim=1)
+            code = _lib.dtype_code("KDAHybridLayer", x.dtype)
+            stream = _lib.stream_of(xc)
+            w = self.short_conv.weight.detach().to(x.dtype).reshape(d, _CONV_K).contiguous()
+            bias = self.short_conv.bias
+            bias = None if bias is None else bias.detach().to(x.dtype).contiguous()
+            x_conv = torch.empty_like(xc)
+            _lib.call("kch_short_conv", _lib.ptr(xc), _lib.ptr(lb), _lib.ptr(w), _lib.ptr(bias),
+                      _lib.ptr(x_conv), B, T, d, code, stream)
+            W = self._fused.get([self.q_proj.weight, self.k_proj.weight, self.v_proj.weight,
+                                 self.beta.weight, self.g_down.weight], x.dtype, x.device)
+            proj = F.linear(x_conv, W)  # [B, T, 2HK + HV*V + HV + K]
+            off_gd = 2 * H * K + HV * V + HV
+            gl = F.linear(proj[..., off_gd:off_gd + K], self.g_up.weight.to(x.dtype))
+            q = torch.empty(B, T, H, K, device=x.device, dtype=x.dtype)
+            k = torch.empty_like(q)
+            v = torch.empty(B, T, HV, V, device=x.device, dtype=x.dtype)
+            g = torch.empty(B, T, HV, K, device=x.device, dtype=x.dtype)
+            beta = torch.empty(B, T, HV, device=x.device, dtype=x.dtype)
+            _lib.call("kch_kda_gates", _lib.ptr(proj), proj.stride(1), _lib.ptr(gl), gl.stride(1),
+                      _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(beta),
+                      B, T, H, HV, K, V, float(cfg.kda_decay_scale), code, stream)
+            use_chunk = cfg.kda_chunk_size >= 1 and T >= cfg.kda_chunk_size
+            o, new_state = kda_forward(
+                q, k, v, g, beta, scale=self._scale_value(), initial_state=state,
+                output_final_state=True, chunk_size=max(cfg.kda_chunk_size, 1),
+                use_chunk=use_chunk, backend=cfg.kda_backend)
+            out = self.o_proj(o.reshape(B, T, HV * V))
+        return out, new_state, new_lookback
+
+
+class CSAHybridLayer(nn.Module):
+    """CSA sub-layer (``ops_fused.py:612-713``): ``naive_csa`` then ``o_proj``."""
+
+    _indexer_warned = False
+
+    def __init__(self, cfg: HybridConfig):
+        super().__init__()
+        self.cfg = cfg
+        d, c = cfg.d_model, cfg.csa_c
+        self.W_aKV = nn.Linear(d, c, bias=False)
+        self.W_bKV = nn.Linear(d, c, bias=False)
+        self.W_aZ = nn.Linear(d, c, bias=False)
+        self.W_bZ = nn.Linear(d, c, bias=False)
+        self.Ba = nn.Parameter(torch.randn(cfg.csa_m, c) * cfg.init_std)
+        self.Bb = nn.Parameter(torch.randn(cfg.csa_m, c) * cfg.init_std)
+        self.W_DQ = nn.Linear(d, cfg.csa_dc, bias=False)
+        self.W_UQ = nn.Linear(cfg.csa_dc, c * cfg.csa_nh, bias=False)
+        self.W_IUQ = nn.Linear(cfg.csa_dc, cfg.csa_cI * cfg.csa_nIh, bias=False)
+        self.W_w = nn.Linear(d, cfg.csa_nIh, bias=False)
+        self.W_KV_idx = nn.Linear(d, cfg.csa_cI, bias=False)
+        self.W_Z_idx = nn.Linear(d, cfg.csa_cI, bias=False)
+        self.B_idx = nn.Parameter(torch.randn(cfg.csa_m, cfg.csa_cI) * cfg.init_std)
+        self.sink = nn.Parameter(torch.zeros(cfg.csa_nh))
+        self.o_proj = nn.Linear(c * cfg.csa_nh, d, bias=False)
+        self.indexer_is_trained = True
+        self.use_ste = True
+        self._fused = _FusedWeight()
+
+    @classmethod
+    def reset_warned(cls):
+        cls._indexer_warned = False
+
+    def _maybe_warn_indexer(self):
+        # only with STE explicitly disabled (ops_fused.py:678-692)
+        if not self.indexer_is_trained and not CSAHybridLayer._indexer_warned:
+            warnings.warn(
+                "CSAHybridLayer: STE is disabled (use_ste=False), so the lightning indexer "
+                "parameters (W_IUQ, W_w, W_KV_idx, W_Z_idx, B_idx) will NOT be trained.",
+                stacklevel=3)
+            CSAHybridLayer._indexer_warned = True
+
+    def forward(self, x: torch.Tensor, state: torch.Tensor | None = None):
+        cfg = self.cfg
+        if self.training and not self.use_ste:
+            self._maybe_warn_indexer()
+        with torch.no_grad():
+            o = naive_csa(
+                x, self.W_aKV.weight, self.W_bKV.weight, self.W_aZ.weight, self.W_bZ.weight,
+                self.Ba, self.Bb, self.W_DQ.weight, self.W_UQ.weight, self.W_IUQ.weight,
+                self.W_w.weight, self.W_KV_idx.weight, self.W_Z_idx.weight, self.B_idx,
+                m=cfg.csa_m, topk=cfg.csa_topk, nh=cfg.csa_nh, nIh=cfg.csa_nIh, c=cfg.csa_c,
+                c_I=cfg.csa_cI, dc=cfg.csa_dc, sliding_window=cfg.csa_sliding_window,
+                sink_logits=self.sink, use_ste=self.use_ste, normalize_qk=True)
+            return self.o_proj(o), None
+
+
+class HCAHybridLayer(nn.Module):
+    """HCA sub-layer (``ops_fused.py:716-739``): ``naive_hca`` then ``o_proj``."""
+
+    def __init__(self, cfg: HybridConfig):
+        super().__init__()
+        self.cfg = cfg
+        d, c = cfg.d_model, cfg.hca_c
+        self.W_KV = nn.Linear(d, c, bias=False)
+        self.W_Z = nn.Linear(d, c, bias=False)
+        self.B_pos = nn.Parameter(torch.randn(cfg.hca_m2, c) * cfg.init_std)
+        self.W_DQ = nn.Linear(d, cfg.hca_dc, bias=False)
+        self.W_UQ = nn.Linear(cfg.hca_dc, c * cfg.hca_nh, bias=False)
+        self.sink = nn.Parameter(torch.zeros(cfg.hca_nh))
+        self.o_proj = nn.Linear(c * cfg.hca_nh, d, bias=False)
+        self._fused = _FusedWeight()
+
+    def forward(self, x: torch.Tensor, state: torch.Tensor | None = None):
+        cfg = self.cfg
+        with torch.no_grad():
+            o = naive_hca(x, self.W_KV.weight, self.W_Z.weight, self.B_pos, self.W_DQ.weight,
+                          self.W_UQ.weight, m2=cfg.hca_m2, nh=cfg.hca_nh, c=cfg.hca_c,
+                          dc=cfg.hca_dc, sliding_window=cfg.hca_sliding_window,
+                          sink_logits=self.sink)
+            return self.o_proj(o), None
+
+
+class HybridKCHAttention(nn.Module):
+    """Stack of KDA / CSA / HCA sub-layers (``ops_fused.py:742-1131``).
+
+    Layout ``[KDA * n_kda, CSA * n_csa, HCA * n_hca]`` repeated and cut to
+    ``total_layers``; every sub-layer is ``x + layer(LayerNorm_fp32(x))``;
+    one recurrent state and one conv lookback per KDA layer.
+    """
+
+    LAYER_TYPES = ('kda', 'csa', 'hca')
+    _stateful_warned = False
+
+    def __init__(self, cfg: HybridConfig, total_layers: int = 5):
+        super().__init__()
+        self.cfg = cfg
+        if not isinstance(total_layers, int) or total_layers < 0:
+            raise ValueError(f"total_layers={total_layers!r} must be a non-negative int "
+                             f"(0 produces an empty no-op model).")
+        self.total_layers = total_layers
+        if total_layers > 0 and cfg.n_kda == 0 and cfg.n_csa == 0 and cfg.n_hca == 0:
+            raise ValueError(
+                "HybridKCHAttention requires at least one non-zero layer count (n_kda, n_csa, "
+                f"n_hca); got ({cfg.n_kda}, {cfg.n_csa}, {cfg.n_hca}) with "
+                f"total_layers={total_layers}.")
+        self.layout = self._build_layout()
+        kinds = {'kda': KDAHybridLayer, 'csa': CSAHybridLayer, 'hca': HCAHybridLayer}
+        self.layers = nn.ModuleList([kinds[k](cfg) for k in self.layout])
+        self.norms = nn.ModuleList([_Fp32LayerNorm(cfg.d_model) for _ in self.layout])
+        self.n_kda_layers = sum(1 for k in self.layout if k == 'kda')
+        self.register_buffer('_kda_state', None, persistent=False)
+
+    def _build_layout(self) -> list[str]:
+        unit = (['kda'] * self.cfg.n_kda + ['csa'] * self.cfg.n_csa + ['hca'] * self.cfg.n_hca)
+        if not unit and self.total_layers > 0:
+            raise ValueError("_build_layout: cannot build a non-empty layout from an empty "
+                             "repeating unit (n_kda=n_csa=n_hca=0).")
+        layout: list[str] = []
+        while len(layout) < self.total_layers:
+            layout.extend(unit)
+        return layout[:self.total_layers]
+
+    def layout_str(self) -> str:
+        return '-'.join(s.upper() for s in self.layout)
+
+    def reset_state(self) -> None:
+        """Clear the KDA states and every KDA layer's conv lookback (``ops_fused.py:856-885``)."""
+        self._kda_state = None
+        for layer in self.layers:
+            if isinstance(layer, KDAHybridLayer):
+                layer.reset_conv_state()
+        HybridKCHAttention._stateful_warned = False
+
+    def _kda_layers(self):
+        return [layer for layer in self.layers if isinstance(layer, KDAHybridLayer)]
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        """Stateful forward: reads and writes the KDA states and conv lookbacks."""
+        if self.training and not HybridKCHAttention._stateful_warned:
+            warnings.warn(
+                "HybridKCHAttention.forward() mutates self._kda_state and per-layer "
+                "_conv_lookback buffers; use forward_functional() for code that must not "
+                "share module state.", stacklevel=2)
+            HybridKCHAttention._stateful_warned = True
+        kda = self._kda_layers()
+        o, new_state, new_lbs = self.forward_functional(
+            x, self._kda_state, [layer._conv_lookback for layer in kda])
+        self._kda_state = new_state
+        for layer, lb in zip(kda, new_lbs):
+            layer._conv_lookback = lb
+        return o
+
+    def _unstack_states(self, kda_state, B, device, detach_state=True):
+        stacked = kda_state
+        if stacked is not None:
+            if stacked.shape[1] != B:
+                logger.debug("HybridKCHAttention: dropping KDA state (batch %d -> %d)",
+                             stacked.shape[1], B)
+                stacked = None
+            else:
+                stacked = stacked.to(device=device)
+                if detach_state:
+                    stacked = stacked.detach()
+        if stacked is None:
+            return [None] * self.n_kda_layers
+        if stacked.shape[0] != self.n_kda_layers:
+            raise ValueError(
+                f"HybridKCHAttention.forward_functional: stacked KDA state has "
+                f"{stacked.shape[0]} layers but the model has {self.n_kda_layers} KDA layers.")
+        return list(stacked.unbind(0))
+
+    def _stack_states(self, states):
+        if self.n_kda_layers == 0:
+            return None
+        if any(s is None for s in states):
+            raise RuntimeError("HybridKCHAttention: a KDA layer returned new_state=None.")
+        ref = tuple(states[0].shape)
+        for i, s in enumerate(states):
+            if tuple(s.shape) != ref:
+                raise RuntimeError(f"HybridKCHAttention: KDA layer {i} returned new_state with "
+                                   f"shape {tuple(s.shape)}, layer 0 returned {ref}.")
+        return torch.stack(states, dim=0)
+
+    def forward_functional(self, x: torch.Tensor, kda_state: torch.Tensor | None,
+                           conv_lookbacks: list, *, detach_state: bool = True,
+                           detach_lookback: bool = True):
+        """Pure forward (``ops_fused.py:956-1128``).
+
+        Returns ``(output [B,T,d], new_kda_state [n_kda,B,HV,K,V] | None, new_conv_lookbacks)``.
+        """
+        states = self._unstack_states(kda_state, x.shape[0], x.device, detach_state)
+        lookbacks = list(conv_lookbacks)
+        if len(lookbacks) != self.n_kda_layers:
+            raise ValueError(
+                f"HybridKCHAttention.forward_functional: conv_lookbacks has length "
+                f"{len(lookbacks)} but the model has {self.n_kda_layers} KDA layers.")
+        kda_idx = 0
+        new_lookbacks = []
+        with torch.no_grad():
+            for layer, norm, kind in zip(self.layers, self.norms, self.layout):
+                residual = x
+                h = norm(x)
+                if kind == 'kda':
+                    o, st, lb = layer.forward_functional(h, states[kda_idx], lookbacks[kda_idx],
+                                                         detach_lookback=detach_lookback)
+                    states[kda_idx] = st
+                    new_lookbacks.append(lb)
+                    kda_idx += 1
+                else:
+                    o, _ = layer(h, None)
+                x = residual + o
+            return x, self._stack_states(states), new_lookbacks
+
+
+class HybridDecoding(nn.Module):
+    """Hybrid stack with one decode cache per CSA / HCA sub-layer
+    (``run_decoding.py:601-851``), for any ``HybridConfig``.
+
+    ``forward(x)`` with T > 1 is a prefill: the full operators produce the
+    output and their projections populate the caches in bulk; T == 1 is a
+    decode step through the caches and the KDA recurrent state.
+
+    Without ``cfg``: ``HybridConfig(d_model=d_model, csa_topk=csa_topk)`` with
+    the backend from ``KDA_BACKEND`` (default ``"hip"``). The reference's own
+    decode geometry (head dims 8-16) is below what the kernels cover.
+    """
+
+    def __init__(self, d_model: int = 64, total_layers: int = 5, csa_topk: int = 2, *,
+                 cfg: HybridConfig | None = None):
+        super().__init__()
+        if cfg is None:
+            cfg = HybridConfig(d_model=d_model, csa_topk=csa_topk,
+                               kda_backend=validate_kda_backend(
+                                   os.environ.get('KDA_BACKEND', 'hip')))
+        self.cfg = cfg
+        self.model = HybridKCHAttention(cfg, total_layers=total_layers)
+        self._csa_caches: list = [None for k in self.model.layout if k == 'csa']
+        self._hca_caches: list = [None for k in self.model.layout if k == 'hca']
+
+    def reset(self):
+        self.model.reset_state()
+        self._csa_caches = [None for _ in self._csa_caches]
+        self._hca_caches = [None for _ in self._hca_caches]
+
+    def _ensure_csa_cache(self, idx: int, layer: CSAHybridLayer, h: torch.Tensor):
+        cfg = layer.cfg
+        cache = self._csa_caches[idx]
+        if cache is None or cache.B != h.shape[0] or cache.device != h.device \
+                or cache.dtype != h.dtype:
+            cache = CSADecodingCache(h.shape[0], cfg.csa_c, cfg.csa_cI, cfg.csa_m,
+                                     cfg.csa_sliding_window, h.device, h.dtype)
+            self._csa_caches[idx] = cache
+        return cache
+
+    def _ensure_hca_cache(self, idx: int, layer: HCAHybridLayer, h: torch.Tensor):
+        cfg = layer.cfg
+        cache = self._hca_caches[idx]
+        if cache is None or cache.B != h.shape[0] or cache.device != h.device \
+                or cache.dtype != h.dtype:
+            cache = HCADecodingCache(h.shape[0], cfg.hca_c, cfg.hca_m2, cfg.hca_sliding_window,
+                                     h.device, h.dtype)
+            self._hca_caches[idx] = cache
+        return cache
+
+    @staticmethod
+    def _project_csa(layer: CSAHybridLayer, h: torch.Tensor):
+        """The decode-step projections (``run_decoding.py:710-730``) as two GEMMs."""
+        cfg = layer.cfg
+        B, T, _ = h.shape
+        c, cI, nh, nIh, dc = cfg.csa_c, cfg.csa_cI, cfg.csa_nh, cfg.csa_nIh, cfg.csa_dc
+        W = layer._fused.get([layer.W_aKV.weight, layer.W_bKV.weight, layer.W_aZ.weight,
+                              layer.W_bZ.weight, layer.W_KV_idx.weight, layer.W_Z_idx.weight,
+                              layer.W_DQ.weight, layer.W_w.weight], h.dtype, h.device)
+        out = F.linear(h, W)
+        Ca, Cb, Za, Zb, K_idx, Z_idx, cQ, w_idx = out.split([c, c, c, c, cI, cI, dc, nIh], -1)
+        q = F.linear(cQ, layer.W_UQ.weight).view(B, T, nh, c)
+        q_idx = F.linear(cQ, layer.W_IUQ.weight).view(B, T, nIh, cI)
+        return Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx
+
+    @staticmethod
+    def _project_hca(layer: HCAHybridLayer, h: torch.Tensor):
+        cfg = layer.cfg
+        B, T, _ = h.shape
+        W = layer._fused.get([layer.W_KV.weight, layer.W_Z.weight, layer.W_DQ.weight],
+                             h.dtype, h.device)
+        C, Z, cQ = F.linear(h, W).split([cfg.hca_c, cfg.hca_c, cfg.hca_dc], -1)
+        q = F.linear(cQ, layer.W_UQ.weight).view(B, T, cfg.hca_nh, cfg.hca_c)
+        return C, Z, q
+
+    def _forward_csa_layer(self, layer: CSAHybridLayer, h: torch.Tensor, idx: int):
+        cfg = layer.cfg
+        B, T_new, _ = h.shape
+        if T_new == 0:
+            return h.new_zeros(B, 0, cfg.d_model)
+        cache = self._ensure_csa_cache(idx, layer, h)
+        if T_new > 1:
+            o_core, (Ca, Cb, Za, Zb, K_idx, Z_idx) = naive_csa(
+                h, layer.W_aKV.weight, layer.W_bKV.weight, layer.W_aZ.weight, layer.W_bZ.weight,
+                layer.Ba, layer.Bb, layer.W_DQ.weight, layer.W_UQ.weight, layer.W_IUQ.weight,
+                layer.W_w.weight, layer.W_KV_idx.weight, layer.W_Z_idx.weight, layer.B_idx,
+                m=cfg.csa_m, topk=cfg.csa_topk, nh=cfg.csa_nh, nIh=cfg.csa_nIh, c=cfg.csa_c,
+                c_I=cfg.csa_cI, dc=cfg.csa_dc, sliding_window=cfg.csa_sliding_window,
+                sink_logits=layer.sink, use_ste=False, normalize_qk=True,
+                return_projections=True)
+            cache.append_step(Ca, Cb, Za, Zb, K_idx, Z_idx, layer.Ba, layer.Bb, layer.B_idx)
+        else:
+            Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx = self._project_csa(layer, h)
+            cache.append_step(Ca, Cb, Za, Zb, K_idx, Z_idx, layer.Ba, layer.Bb, layer.B_idx)
+            q_n = F.normalize(q.float(), dim=-1)
+            o = cache.forward_step(q_n, q_idx, w_idx, topk=cfg.csa_topk, nh=cfg.csa_nh,
+                                   nIh=cfg.csa_nIh, scale=1.0, sink_logits=layer.sink,
+                                   use_ste=False, normalize_qk=True)
+            o_core = o.reshape(B, T_new, cfg.csa_nh * cfg.csa_c).to(h.dtype)
+        return layer.o_proj(o_core)
+
+    def _forward_hca_layer(self, layer: HCAHybridLayer, h: torch.Tensor, idx: int):
+        cfg = layer.cfg
+        B, T_new, _ = h.shape
+        if T_new == 0:
+            return h.new_zeros(B, 0, cfg.d_model)
+        cache = self._ensure_hca_cache(idx, layer, h)
+        if T_new > 1:
+            o_core, (C, Z) = naive_hca(
+                h, layer.W_KV.weight, layer.W_Z.weight, layer.B_pos, layer.W_DQ.weight,
+                layer.W_UQ.weight, m2=cfg.hca_m2, nh=cfg.hca_nh, c=cfg.hca_c, dc=cfg.hca_dc,
+                sliding_window=cfg.hca_sliding_window, sink_logits=layer.sink,
+                return_projections=True)
+            cache.append_step(C, Z, layer.B_pos)
+        else:
+            C, Z, q = self._project_hca(layer, h)
+            cache.append_step(C, Z, layer.B_pos)
+            q_n = F.normalize(q.float(), dim=-1)
+            o = cache.forward_step(q_n, nh=cfg.hca_nh, scale=1.0, sink_logits=layer.sink)
+            o_core = o.reshape(B, T_new, cfg.hca_nh * cfg.hca_c).to(h.dtype)
+        return layer.o_proj(o_core)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        B = x.shape[0]
+        model = self.model
+        stacked = model._kda_state
+        if stacked is not None and stacked.shape[1] == B:
+            states = list(stacked.unbind(0))
+        else:
+            states = [None] * model.n_kda_layers
+        kda_idx = csa_idx = hca_idx = 0
+        with torch.no_grad():
+            for layer, norm, kind in zip(model.layers, model.norms, model.layout):
+                residual = x
+                h = norm(x)
+                if kind == 'kda':
+                    o, states[kda_idx] = layer(h, states[kda_idx])
+                    kda_idx += 1
+                elif kind == 'csa':
+                    o = self._forward_csa_layer(layer, h, csa_idx)
+                    csa_idx += 1
+                else:
+                    o = self._forward_hca_layer(layer, h, hca_idx)
+                    hca_idx += 1
+                x = residual + o
+            model._kda_state = torch.stack(states, 0) if model.n_kda_layers > 0 else None
+        return x
+
+
+__all__ = ["HybridConfig", "KDAHybridLayer", "CSAHybridLayer", "HCAHybridLayer",
+           "HybridKCHAttention", "HybridDecoding"]
