@@ -5,14 +5,28 @@ with fp32 state, B=8 T=4096 H=16 K=V=128, q/k L2-normalised N(0,1), v N(0,1),
 g = logsigmoid(N(0,1)) per channel, beta = sigmoid(N(0,1)), S0 ~ 0.02 N(0,1).
 A step is one ``kch.naive_chunk_kda`` call over that batch (inputs resident in
 HBM). ``value`` is B*T tokens per second of step time, measured with HIP events
-on the stream the kernel runs on.
+on the stream the kernel runs on (the torch current stream).
 
 ``roofline``: algorithmic HBM bytes of the step (q,k,v,g,o bf16 + beta bf16 +
-S0 read and S write fp32) over the measured kernel time, against 8 TB/s.
+S0 read and S write fp32) over the measured kernel time, against 8 TB/s;
+``traffic`` is the measured HBM bytes per launch (rocprofv3 FETCH_SIZE +
+WRITE_SIZE, scaled by the same counters on a copy of known size).
 ``cpu_baseline``: the numpy oracle (a from-scratch CPU restatement of the
 reference algorithm) on a bounded sample of the same workload, one thread.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+``extra`` (skipped with ``--headline-only``): the other prefill workloads of
+the metric, each at its configuration, with the same timing protocol:
+  * ``kda_T8K``: KDA chunk at B=4 T=8192 (same generators);
+  * ``csa_C2``: ``naive_csa`` at configs[2] (B4 T8192 d2048, 16 heads of 128,
+    m=4 overlapped, indexer 4x64 top-512, window 128 + sink) and its core
+    (compression + indexer + sparse attention, projections excluded);
+  * ``hca_C3`` / ``hca_T8K``: ``naive_hca`` at configs[3] (B4 T32768 d2048,
+    16 heads of 128, m'=128, window 128 + sink) and at T=8192, plus its core;
+  * ``hybrid_C4``: ``HybridDecoding`` (5 layers, 3:1:1, d2048, the configs
+    1-3 head shapes) prefill of B=2 T=16384, then 256 single-token steps.
+Weights are N(0, 1/fan_in) random (no checkpoints), inputs N(0,1).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--headline-only]
 """
 
 from __future__ import annotations
@@ -35,6 +49,15 @@ import torch  # noqa: E402
 METRIC = "prefill tokens/s (KDA chunk, CSA, HCA) at T=8K; % of MFMA/HBM roofline"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+
+# Measured HBM bytes per launch of the headline kernel: rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE (KiB per dispatch) on `bench.py --headline-only`, each scaled by the
+# counter's reading on a device copy of known size (profiles/kda_chunk_lp_C1_pmc.md).
+HEADLINE_TRAFFIC_BYTES = int((267542 * 2.0 + 142848 * 1.0) * 1024)
+
+
+def _log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
 def kda_inputs(B, T, H, K, V, seed=1, dev="cuda"):
@@ -93,12 +116,173 @@ def cpu_baseline_kda(host, s0, B, T, H):
                       f"host {platform.processor() or platform.machine()}"}
 
 
+# ----------------------------------------------------------------------------- extras
+
+def _w(gen, o, i, dev):
+    return (torch.randn(o, i, generator=gen) * i ** -0.5).to(dev, torch.bfloat16)
+
+
+def csa_weights(d, c, nh, dc, nIh, cI, m, dev, seed=2):
+    g = torch.Generator().manual_seed(seed)
+    W = {n: _w(g, c, d, dev) for n in ('W_aKV', 'W_bKV', 'W_aZ', 'W_bZ')}
+    W['Ba'] = (0.02 * torch.randn(m, c, generator=g)).to(dev, torch.bfloat16)
+    W['Bb'] = (0.02 * torch.randn(m, c, generator=g)).to(dev, torch.bfloat16)
+    W['W_DQ'] = _w(g, dc, d, dev)
+    W['W_UQ'] = _w(g, c * nh, dc, dev)
+    W['W_IUQ'] = _w(g, cI * nIh, dc, dev)
+    W['W_w'] = _w(g, nIh, d, dev)
+    W['W_KV_idx'] = _w(g, cI, d, dev)
+    W['W_Z_idx'] = _w(g, cI, d, dev)
+    W['B_idx'] = (0.02 * torch.randn(m, cI, generator=g)).to(dev, torch.bfloat16)
+    W['sink'] = torch.randn(nh, generator=g).to(dev)
+    return W
+
+
+def csa_core_algorithmic(B, T, m, topk, win, nh, c, nIh, cI):
+    t = np.arange(T, dtype=np.int64)
+    vis = (t + 1) // m
+    idx_entries = int(vis.sum())
+    sel = int(np.minimum(vis, topk).sum())
+    wslots = int(np.minimum(win, t + 1).sum())
+    flops = B * (idx_entries * 2 * nIh * cI + (sel + wslots) * 4 * nh * c)
+    nb = T // m
+    # bf16 inputs of the core, bf16 out, int32 indices, fp32 indexer keys
+    bytes_ = B * T * 2 * (4 * c + 2 * cI + nh * c + nIh * cI + nIh + nh * c) \
+        + B * T * topk * 4 + B * nb * (c * 2 + cI * 4)
+    return flops, bytes_
+
+
+def hca_core_algorithmic(B, T, m2, win, nh, c):
+    t = np.arange(T, dtype=np.int64)
+    comp = int(((t + 1) // m2).sum())
+    wslots = int(np.minimum(win, t + 1).sum())
+    flops = B * (comp + wslots) * 4 * nh * c
+    bytes_ = B * T * 2 * (2 * c + 2 * nh * c)
+    return flops, bytes_
+
+
+def _roof(flops, bytes_, ms):
+    t = ms * 1e-3
+    return {"tflops": flops / t / 1e12, "mfma_frac": flops / t / 1e12 / BF16_PEAK_TFLOPS,
+            "gbs": bytes_ / t / 1e9, "hbm_frac": bytes_ / t / 1e9 / HBM_PEAK_GBS,
+            "algorithmic_flops": flops, "algorithmic_bytes": bytes_}
+
+
+def bench_kda(B, T, steps, warmup, dev):
+    import kch
+    H, K, V = 16, 128, 128
+    xs, s0, _, _ = kda_inputs(B, T, H, K, V, dev=dev)
+    ms, med, _ = time_steps(
+        lambda: kch.naive_chunk_kda(*xs, initial_state=s0, output_final_state=True), steps, warmup)
+    flops, bytes_ = kda_algorithmic(B, T, H, K, V)
+    out = {"B": B, "T": T, "tokens_per_s": B * T / (ms * 1e-3), "ms": ms, "ms_median": med}
+    out.update(_roof(flops, bytes_, ms))
+    return out
+
+
+def bench_csa(B, T, steps, warmup, dev):
+    import kch
+    d, c, nh, dc, nIh, cI, m, topk, win = 2048, 128, 16, 128, 4, 64, 4, 512, 128
+    W = csa_weights(d, c, nh, dc, nIh, cI, m, dev)
+    Hs = torch.randn(B, T, d, generator=torch.Generator().manual_seed(2)).to(dev, torch.bfloat16)
+    args = [W[n] for n in ('W_aKV', 'W_bKV', 'W_aZ', 'W_bZ', 'Ba', 'Bb', 'W_DQ', 'W_UQ',
+                           'W_IUQ', 'W_w', 'W_KV_idx', 'W_Z_idx', 'B_idx')]
+    kw = dict(m=m, topk=topk, nh=nh, nIh=nIh, c=c, c_I=cI, dc=dc, sliding_window=win,
+              sink_logits=W['sink'], normalize_qk=True)
+    ms_full, _, _ = time_steps(lambda: kch.naive_csa(Hs, *args, **kw), steps, warmup)
+    with torch.no_grad():
+        comb = torch.nn.functional.linear(Hs, torch.cat(
+            [W['W_aKV'], W['W_bKV'], W['W_aZ'], W['W_bZ'], W['W_KV_idx'], W['W_Z_idx']], 0))
+        Ca, Cb, Za, Zb, Ki, Zi = comb.split([c, c, c, c, cI, cI], -1)
+        cQ = torch.nn.functional.linear(Hs, W['W_DQ'])
+        q_idx = torch.nn.functional.linear(cQ, W['W_IUQ']).view(B, T, nIh, cI)
+        w_idx = torch.nn.functional.linear(Hs, W['W_w'])
+        q = torch.nn.functional.linear(cQ, W['W_UQ']).view(B, T, nh, c)
+    ms_core, _, _ = time_steps(
+        lambda: kch.csa_core(Ca, Cb, Za, Zb, Ki, Zi, q, q_idx, w_idx, W['Ba'], W['Bb'],
+                             W['B_idx'], m=m, topk=topk, sliding_window=win,
+                             sink_logits=W['sink'], normalize_qk=True), steps, warmup)
+    flops, bytes_ = csa_core_algorithmic(B, T, m, topk, win, nh, c, nIh, cI)
+    core = {"ms": ms_core, "tokens_per_s": B * T / (ms_core * 1e-3)}
+    core.update(_roof(flops, bytes_, ms_core))
+    return {"B": B, "T": T, "tokens_per_s": B * T / (ms_full * 1e-3), "ms": ms_full,
+            "includes": "projections (hipBLASLt) + core", "core": core}
+
+
+def bench_hca(B, T, steps, warmup, dev):
+    import kch
+    d, c, nh, dc, m2, win = 2048, 128, 16, 128, 128, 128
+    g = torch.Generator().manual_seed(3)
+    W_KV, W_Z, W_DQ = _w(g, c, d, dev), _w(g, c, d, dev), _w(g, dc, d, dev)
+    W_UQ = _w(g, c * nh, dc, dev)
+    B_pos = (0.02 * torch.randn(m2, c, generator=g)).to(dev, torch.bfloat16)
+    sink = torch.randn(nh, generator=g).to(dev)
+    Hs = torch.randn(B, T, d, generator=g).to(dev, torch.bfloat16)
+    kw = dict(m2=m2, nh=nh, c=c, dc=dc, sliding_window=win, sink_logits=sink)
+    ms_full, _, _ = time_steps(lambda: kch.naive_hca(Hs, W_KV, W_Z, B_pos, W_DQ, W_UQ, **kw),
+                               steps, warmup)
+    with torch.no_grad():
+        CZ = torch.nn.functional.linear(Hs, torch.cat([W_KV, W_Z], 0))
+        C, Z = CZ.split([c, c], -1)
+        q = torch.nn.functional.linear(torch.nn.functional.linear(Hs, W_DQ), W_UQ).view(B, T, nh, c)
+    ms_core, _, _ = time_steps(
+        lambda: kch.hca_core(C, Z, q, B_pos, m2=m2, sliding_window=win, sink_logits=sink),
+        steps, warmup)
+    flops, bytes_ = hca_core_algorithmic(B, T, m2, win, nh, c)
+    core = {"ms": ms_core, "tokens_per_s": B * T / (ms_core * 1e-3)}
+    core.update(_roof(flops, bytes_, ms_core))
+    return {"B": B, "T": T, "tokens_per_s": B * T / (ms_full * 1e-3), "ms": ms_full,
+            "includes": "projections (hipBLASLt) + core", "core": core}
+
+
+def bench_hybrid(dev, T=16384, B=2, n_decode=256):
+    import kch
+    cfg = kch.HybridConfig(d_model=2048, n_heads_qk=16, n_heads_v=16, head_dim_k=128,
+                           head_dim_v=128, kda_chunk_size=64, csa_m=4, csa_topk=512, csa_nh=16,
+                           csa_c=128, csa_dc=128, csa_nIh=4, csa_cI=64, csa_sliding_window=128,
+                           hca_m2=128, hca_nh=16, hca_c=128, hca_dc=128, hca_sliding_window=128)
+    torch.manual_seed(4)
+    dec = kch.HybridDecoding(cfg=cfg, total_layers=5)
+    with torch.no_grad():
+        for layer in dec.model.layers:
+            if hasattr(layer, 'sink'):
+                layer.sink.normal_()
+    dec = dec.to(dev, torch.bfloat16).eval()
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(B, T, cfg.d_model, generator=g).to(dev, torch.bfloat16)
+    xs = torch.randn(n_decode, B, 1, cfg.d_model, generator=g).to(dev, torch.bfloat16)
+    # warm-up pass (kernel loading, GEMM heuristics), then the measured run
+    dec.reset()
+    dec(x[:, :1024])
+    dec(xs[0])
+    torch.cuda.synchronize()
+    dec.reset()
+    stream = torch.cuda.current_stream()
+    e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+    e0.record(stream)
+    y = dec(x)
+    e1.record(stream)
+    for i in range(n_decode):
+        y = dec(xs[i])
+    e2.record(stream)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(y).all())
+    pre_ms, dec_ms = e0.elapsed_time(e1), e1.elapsed_time(e2)
+    return {"B": B, "T": T, "layout": dec.model.layout_str(), "prefill_ms": pre_ms,
+            "prefill_tokens_per_s": B * T / (pre_ms * 1e-3), "decode_steps": n_decode,
+            "decode_ms_per_step": dec_ms / n_decode,
+            "decode_tokens_per_s": B * n_decode / (dec_ms * 1e-3)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--headline-only", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run three 1 GiB device-to-device copies (HBM counter scale)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (every box has one MI355X); "
@@ -115,6 +299,7 @@ def main():
         return kch.naive_chunk_kda(*xs, initial_state=s0, output_final_state=True)
 
     ms_mean, ms_med, _ = time_steps(step, args.steps, args.warmup)
+    _log(f"kda C1: {ms_mean:.3f} ms/step")
     flops, bytes_ = kda_algorithmic(B, T, H, K, V)
     t = ms_mean * 1e-3
     achieved = bytes_ / t / 1e9
@@ -134,14 +319,39 @@ def main():
         "config": {"workload": "kda_chunk_prefill", "B": B, "T": T, "H": H, "K": K, "V": V,
                    "chunk": 64, "state": "fp32", "baseline_config": "configs[1]"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": HEADLINE_TRAFFIC_BYTES,
                      "algorithmic_bytes": bytes_, "kernel": "kda_chunk_lp_kernel<128,bf16>",
                      "mfma_tflops": flops / t / 1e12,
                      "mfma_frac": flops / t / 1e12 / BF16_PEAK_TFLOPS},
         "ms_per_step_median": ms_med,
     }
+    del xs, s0
+    if args.copy_calibration:
+        src = torch.empty(1 << 29, device=dev, dtype=torch.bfloat16).normal_()
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        rec["copy_calibration_bytes"] = {"read": src.numel() * 2, "write": dst.numel() * 2}
+        del src, dst
+    if not args.headline_only:
+        extra = {}
+        extra["kda_T8K"] = bench_kda(4, 8192, args.steps, args.warmup, dev)
+        _log(f"kda T8K: {extra['kda_T8K']['ms']:.3f} ms")
+        extra["csa_C2"] = bench_csa(4, 8192, max(3, args.steps // 4), 1, dev)
+        _log(f"csa C2: {extra['csa_C2']['ms']:.3f} ms")
+        extra["hca_C3"] = bench_hca(4, 32768, max(3, args.steps // 4), 1, dev)
+        _log(f"hca C3: {extra['hca_C3']['ms']:.3f} ms")
+        extra["hca_T8K"] = bench_hca(4, 8192, max(3, args.steps // 4), 1, dev)
+        _log(f"hca T8K: {extra['hca_T8K']['ms']:.3f} ms")
+        torch.cuda.empty_cache()
+        extra["hybrid_C4"] = bench_hybrid(dev)
+        _log(f"hybrid C4: prefill {extra['hybrid_C4']['prefill_ms']:.2f} ms, decode "
+             f"{extra['hybrid_C4']['decode_ms_per_step']:.3f} ms/step")
+        rec["extra"] = extra
     if not args.no_cpu:
         rec["cpu_baseline"] = cpu_baseline_kda(host, s0h, B, T, H)
+        _log("cpu baseline done")
     print(json.dumps(rec))
 
 

@@ -1,0 +1,274 @@
+"""Pins for the CSA / HCA / decode-cache oracle (CPU only).
+
+Each check is an independent statement of what the mathematics fixes, chosen
+so that a plausible restatement mistake fails one of them:
+
+* compression: per-(block, channel) loops of the softmax-gated sums of the
+  paper's Eqs. 11-12 / 22-23 (``2606.19348v1.txt:474-488,639-644``), the
+  block-0 rule of the overlapped branch and its causality
+  (``run_correctness.py:701-762``) -> wrong branch pairing, wrong softmax axis;
+* block mask: window-close counts (``run_correctness.py:1145-1163``);
+* indexer: loop logits (ReLU per head, weighted head sum), selection by an
+  explicit sort on (-logit, index), -1 padding, ``w_idx=None`` == ones,
+  ``topk=0`` (``run_correctness.py:1095-1264``);
+* joint softmax + sink: a per-(token, head) fp64 loop of
+  p_i = e^{s_i} / (sum_j e^{s_j} + e^{sink}) over the selected / compressed and
+  window rows (the independent formula of ``run_correctness.py:2530-2707``);
+* causality under future perturbations (``:1937-2155``), T < m' (``:3360-3403``),
+  topk = 0 (``:3297-3357``);
+* decode caches == the full-sequence operator row by row
+  (``run_correctness.py:4731-4830``), ring contents (``:4872-4894``).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+from oracle import csa as O
+from oracle.caches import CSACacheOracle, HCACacheOracle
+from oracle.common import l2_normalize
+
+
+def _rn(rng, *s, scale=1.0):
+    return scale * rng.standard_normal(s)
+
+
+def _softmax_list(xs):
+    mx = max(xs)
+    e = [math.exp(x - mx) for x in xs]
+    s = sum(e)
+    return [v / s for v in e]
+
+
+def test_compress_kv_bruteforce():
+    rng = np.random.default_rng(0)
+    B, T, c, m = 2, 12, 3, 4
+    C, Z, Bp = _rn(rng, B, T, c), _rn(rng, B, T, c), _rn(rng, m, c, scale=0.3)
+    out = O.compress_kv(C, Z, Bp, m, compute=np.float64)
+    for b in range(B):
+        for i in range(T // m):
+            for ch in range(c):
+                w = _softmax_list([Z[b, i * m + j, ch] + Bp[j, ch] for j in range(m)])
+                ref = sum(w[j] * C[b, i * m + j, ch] for j in range(m))
+                assert abs(out[b, i, ch] - ref) < 1e-12
+
+
+def test_compress_overlapped_bruteforce_and_causality():
+    rng = np.random.default_rng(1)
+    B, T, c, m = 2, 16, 3, 4
+    Ca, Cb, Za, Zb = (_rn(rng, B, T, c) for _ in range(4))
+    Ba, Bb = _rn(rng, m, c, scale=0.3), _rn(rng, m, c, scale=0.3)
+    out = O.compress_kv_overlapped(Ca, Cb, Za, Zb, Ba, Bb, m, compute=np.float64)
+    for b in range(B):
+        for i in range(T // m):
+            for ch in range(c):
+                logits = [Za[b, i * m + j, ch] + Ba[j, ch] for j in range(m)]
+                vals = [Ca[b, i * m + j, ch] for j in range(m)]
+                if i > 0:  # block i mixes Ca_i with Cb_{i-1}; block 0 has no b-branch
+                    logits += [Zb[b, (i - 1) * m + j, ch] + Bb[j, ch] for j in range(m)]
+                    vals += [Cb[b, (i - 1) * m + j, ch] for j in range(m)]
+                w = _softmax_list(logits)
+                assert abs(out[b, i, ch] - sum(a * v for a, v in zip(w, vals))) < 1e-12
+    # causality: changing block 2's tokens leaves blocks 0..1 alone; changing
+    # Cb of block 1 moves block 2 but not block 1
+    Ca2 = Ca.copy()
+    Ca2[:, 2 * m:3 * m] += 1.0
+    out2 = O.compress_kv_overlapped(Ca2, Cb, Za, Zb, Ba, Bb, m, compute=np.float64)
+    assert np.array_equal(out2[:, :2], out[:, :2]) and not np.allclose(out2[:, 2], out[:, 2])
+    Cb2 = Cb.copy()
+    Cb2[:, m:2 * m] += 1.0
+    out3 = O.compress_kv_overlapped(Ca, Cb2, Za, Zb, Ba, Bb, m, compute=np.float64)
+    assert np.array_equal(out3[:, :2], out[:, :2]) and not np.allclose(out3[:, 2], out[:, 2])
+
+
+def test_causal_block_mask_counts():
+    for m in (1, 3, 4):
+        T = 13
+        nb = T // m
+        mask = O.causal_block_mask(T, nb, m)
+        for t in range(T):
+            vis = [b for b in range(nb) if mask[t, b]]
+            # a block becomes visible at the token that closes it
+            assert vis == list(range(min(nb, (t + 1) // m)))
+
+
+def _brute_logits(q, k, w, scale, normalize):
+    B, T, Hh, D = q.shape
+    nb = k.shape[1]
+    if normalize:
+        q, k = l2_normalize(q), l2_normalize(k)
+    out = np.zeros((B, T, nb))
+    for b in range(B):
+        for t in range(T):
+            for n in range(nb):
+                s = 0.0
+                for h in range(Hh):
+                    dot = sum(q[b, t, h, d] * k[b, n, d] for d in range(D))
+                    s += (1.0 if w is None else w[b, t, h]) * max(scale * dot, 0.0)
+                out[b, t, n] = s
+    return out
+
+
+@pytest.mark.parametrize("normalize", [True, False])
+def test_indexer_bruteforce(normalize):
+    rng = np.random.default_rng(2)
+    B, T, Hh, D, nb, m, topk = 2, 9, 2, 4, 4, 2, 3
+    q, k, w = _rn(rng, B, T, Hh, D), _rn(rng, B, nb, D), _rn(rng, B, T, Hh)
+    mask = O.causal_block_mask(T, nb, m)
+    scale = 1.0 if normalize else D ** -0.5
+    lg = O.indexer_logits(q, k, w, None, mask, normalize, compute=np.float64)
+    ref = _brute_logits(q, k, w, scale, normalize)
+    ref = np.where(mask[None], ref, -np.inf)
+    np.testing.assert_allclose(lg, ref, rtol=1e-12, atol=1e-12)
+    idx = O.lightning_indexer(q, k, w, topk, None, mask, normalize, compute=np.float64)
+    for b in range(B):
+        for t in range(T):
+            order = sorted(range(nb), key=lambda n: (-ref[b, t, n], n))[:topk]
+            exp = [n if np.isfinite(ref[b, t, n]) else -1 for n in order]
+            exp += [-1] * (topk - len(exp))
+            assert list(idx[b, t]) == exp
+    # w_idx=None is all-ones weights; topk=0 gives an empty selection; ties by index
+    np.testing.assert_allclose(
+        O.indexer_logits(q, k, None, None, mask, normalize, compute=np.float64),
+        O.indexer_logits(q, k, np.ones_like(w), None, mask, normalize, compute=np.float64))
+    assert O.lightning_indexer(q, k, w, 0, None, mask, normalize).shape == (B, T, 0)
+    tie = O.topk_desc_lowest_index(np.array([[1.0, 3.0, 3.0, 0.0, 3.0]]), 4)
+    assert list(tie[0]) == [1, 2, 4, 0]
+
+
+def _joint_loop(rows_s, rows_v, sink):
+    """sum_i p_i v_i with p_i = e^{s_i}/(sum e^{s_j} + e^{sink}); 0 with no rows."""
+    if not rows_s:
+        return np.zeros(rows_v.shape[-1] if hasattr(rows_v, 'shape') else 0)
+    terms = list(rows_s) + ([sink] if sink is not None else [])
+    mx = max(terms)
+    den = sum(math.exp(x - mx) for x in terms)
+    return sum(math.exp(s - mx) / den * v for s, v in zip(rows_s, rows_v))
+
+
+def _csa_inputs(rng, B, T, c, cI, nh, nIh):
+    Ca, Cb, Za, Zb = (_rn(rng, B, T, c) for _ in range(4))
+    Ki, Zi = _rn(rng, B, T, cI), _rn(rng, B, T, cI)
+    q, qi, wi = _rn(rng, B, T, nh, c), _rn(rng, B, T, nIh, cI), _rn(rng, B, T, nIh)
+    return Ca, Cb, Za, Zb, Ki, Zi, q, qi, wi
+
+
+@pytest.mark.parametrize("sink", [True, False])
+def test_csa_core_joint_softmax_loop(sink):
+    rng = np.random.default_rng(3)
+    B, T, c, cI, nh, nIh, m, topk, win = 1, 11, 4, 3, 2, 2, 2, 3, 3
+    Ca, Cb, Za, Zb, Ki, Zi, q, qi, wi = _csa_inputs(rng, B, T, c, cI, nh, nIh)
+    Ba, Bb, Bi = _rn(rng, m, c), _rn(rng, m, c), _rn(rng, m, cI)
+    sk = _rn(rng, nh) if sink else None
+    out, idx = O.csa_core(Ca, Cb, Za, Zb, Ki, Zi, q, qi, wi, Ba, Bb, Bi, m=m, topk=topk,
+                          sliding_window=win, sink_logits=sk, compute=np.float64,
+                          return_indices=True)
+    Tp = T + (-T) % m
+    pad = lambda x: np.concatenate([x, np.zeros((B, Tp - T) + x.shape[2:])], 1)  # noqa: E731
+    Cn = l2_normalize(O.compress_kv_overlapped(pad(Ca), pad(Cb), pad(Za), pad(Zb), Ba, Bb, m,
+                                               compute=np.float64))
+    Cl = l2_normalize(Ca)
+    qn = l2_normalize(q)
+    for t in range(T):
+        sel = [int(n) for n in idx[0, t] if n >= 0]
+        assert all(n < (t + 1) // m for n in sel)  # only visible blocks
+        wpos = list(range(max(0, t - win + 1), t + 1))
+        for h in range(nh):
+            s = [float(qn[0, t, h] @ Cn[0, n]) for n in sel] + \
+                [float(qn[0, t, h] @ Cl[0, p]) for p in wpos]
+            v = [Cn[0, n] for n in sel] + [Cl[0, p] for p in wpos]
+            ref = _joint_loop(s, v, None if sk is None else float(sk[h]))
+            np.testing.assert_allclose(out[0, t, h], ref, rtol=1e-10, atol=1e-12)
+
+
+def test_hca_core_joint_softmax_loop_and_short_T():
+    rng = np.random.default_rng(4)
+    B, T, c, nh, m2, win = 1, 13, 4, 2, 4, 3
+    C, Z, q = _rn(rng, B, T, c), _rn(rng, B, T, c), _rn(rng, B, T, nh, c)
+    Bp, sk = _rn(rng, m2, c), _rn(rng, nh)
+    out = O.hca_core(C, Z, q, Bp, m2=m2, sliding_window=win, sink_logits=sk, compute=np.float64)
+    Tp = T + (-T) % m2
+    pad = lambda x: np.concatenate([x, np.zeros((B, Tp - T) + x.shape[2:])], 1)  # noqa: E731
+    Cn = l2_normalize(O.compress_kv(pad(C), pad(Z), Bp, m2, compute=np.float64))
+    Cl, qn = l2_normalize(C), l2_normalize(q)
+    for t in range(T):
+        blocks = list(range((t + 1) // m2))
+        wpos = list(range(max(0, t - win + 1), t + 1))
+        for h in range(nh):
+            s = [float(qn[0, t, h] @ Cn[0, n]) for n in blocks] + \
+                [float(qn[0, t, h] @ Cl[0, p]) for p in wpos]
+            v = [Cn[0, n] for n in blocks] + [Cl[0, p] for p in wpos]
+            np.testing.assert_allclose(out[0, t, h], _joint_loop(s, v, float(sk[h])),
+                                       rtol=1e-10, atol=1e-12)
+    # T < m2: no compressed block is visible, only the window contributes
+    short = O.hca_core(C[:, :3], Z[:, :3], q[:, :3], Bp, m2=m2, sliding_window=0,
+                       sink_logits=sk, compute=np.float64)
+    assert np.all(short == 0)
+
+
+def test_causality_csa_hca():
+    rng = np.random.default_rng(5)
+    B, T, c, cI, nh, nIh, m, t0 = 1, 16, 4, 3, 2, 2, 4, 9
+    args = list(_csa_inputs(rng, B, T, c, cI, nh, nIh))
+    W = [_rn(rng, m, c), _rn(rng, m, c), _rn(rng, m, cI)]
+    kw = dict(m=m, topk=2, sliding_window=3, sink_logits=_rn(rng, nh), compute=np.float64)
+    base = O.csa_core(*args, *W, **kw)
+    pert = [a.copy() for a in args]
+    for a in pert:
+        a[:, t0 + 1:] += _rn(rng, *a[:, t0 + 1:].shape)
+    moved = O.csa_core(*pert, *W, **kw)
+    np.testing.assert_array_equal(moved[:, :t0 + 1], base[:, :t0 + 1])
+    assert not np.allclose(moved[:, t0 + 1:], base[:, t0 + 1:])
+    C, Z, q = args[0], args[2], args[6]
+    hk = dict(m2=m, sliding_window=3, sink_logits=kw['sink_logits'], compute=np.float64)
+    hb = O.hca_core(C, Z, q, W[0], **hk)
+    hm = O.hca_core(pert[0], pert[2], pert[6], W[0], **hk)
+    np.testing.assert_array_equal(hm[:, :t0 + 1], hb[:, :t0 + 1])
+
+
+def test_topk_zero_is_window_only():
+    rng = np.random.default_rng(6)
+    B, T, c, cI, nh, nIh, m = 1, 8, 4, 3, 2, 2, 2
+    args = _csa_inputs(rng, B, T, c, cI, nh, nIh)
+    W = [_rn(rng, m, c), _rn(rng, m, c), _rn(rng, m, cI)]
+    sk = _rn(rng, nh)
+    a = O.csa_core(*args, *W, m=m, topk=0, sliding_window=3, sink_logits=sk, compute=np.float64)
+    # the same as an all-empty selection
+    b = O.csa_core(*args, *W, m=m, topk=2, sliding_window=3, sink_logits=sk, compute=np.float64,
+                   indices=np.full((B, T, 2), -1))
+    np.testing.assert_allclose(a, b, rtol=1e-12, atol=1e-14)
+    # no window and no selection: zero output
+    z = O.csa_core(*args, *W, m=m, topk=0, sliding_window=0, sink_logits=sk, compute=np.float64)
+    assert np.all(z == 0)
+
+
+def test_cache_oracles_match_full_sequence():
+    rng = np.random.default_rng(7)
+    B, T, c, cI, nh, nIh, m, win = 2, 19, 4, 3, 2, 2, 3, 4
+    Ca, Cb, Za, Zb, Ki, Zi, q, qi, wi = _csa_inputs(rng, B, T, c, cI, nh, nIh)
+    Ba, Bb, Bi, sk = _rn(rng, m, c), _rn(rng, m, c), _rn(rng, m, cI), _rn(rng, nh)
+    full = O.csa_core(Ca, Cb, Za, Zb, Ki, Zi, q, qi, wi, Ba, Bb, Bi, m=m, topk=64,
+                      sliding_window=win, sink_logits=sk)
+    cache = CSACacheOracle(B, c, cI, m, win, 'fp32')
+    for t in range(T):
+        sl = slice(t, t + 1)
+        cache.append_step(Ca[:, sl], Cb[:, sl], Za[:, sl], Zb[:, sl], Ki[:, sl], Zi[:, sl],
+                          Ba, Bb, Bi)
+        o = cache.forward_step(l2_normalize(q[:, sl]), qi[:, sl], wi[:, sl], topk=64,
+                               sink_logits=sk)
+        np.testing.assert_allclose(o[:, 0], full[:, t], rtol=1e-5, atol=1e-6)
+        assert cache.n_blocks == (t + 1) // m
+    ring = np.stack(cache.ring, axis=1)
+    np.testing.assert_allclose(ring, l2_normalize(Ca[:, T - win:]).astype(np.float32),
+                               rtol=1e-6)
+    C, Z = Ca, Za
+    hfull = O.hca_core(C, Z, q, Ba, m2=m, sliding_window=win, sink_logits=sk)
+    hc = HCACacheOracle(B, c, m, win, 'fp32')
+    hc.append_step(C[:, :7], Z[:, :7], Ba)  # bulk prefill, then single tokens
+    for t in range(7, T):
+        hc.append_step(C[:, t:t + 1], Z[:, t:t + 1], Ba)
+        o = hc.forward_step(l2_normalize(q[:, t:t + 1]), sink_logits=sk)
+        np.testing.assert_allclose(o[:, 0], hfull[:, t], rtol=1e-5, atol=1e-6)
