@@ -8,9 +8,11 @@ HBM). ``value`` is B*T tokens per second of step time, measured with HIP events
 on the stream the kernel runs on (the torch current stream).
 
 ``roofline``: algorithmic HBM bytes of the step (q,k,v,g,o bf16 + beta bf16 +
-S0 read and S write fp32) over the measured kernel time, against 8 TB/s;
-``traffic`` is the measured HBM bytes per launch (rocprofv3 FETCH_SIZE +
-WRITE_SIZE, scaled by the same counters on a copy of known size).
+S0 read and S write fp32) over the measured step time, against 8 TB/s. The step
+is two kernels (a parallel per-chunk kernel and the state-carrying kernel);
+``traffic`` is their measured HBM bytes per step (rocprofv3 FETCH_SIZE +
+WRITE_SIZE, scaled by the same counters on a copy of known size), including the
+per-chunk workspace that passes between them.
 ``cpu_baseline``: the numpy oracle (a from-scratch CPU restatement of the
 reference algorithm) on a bounded sample of the same workload, one thread.
 
@@ -50,10 +52,10 @@ METRIC = "prefill tokens/s (KDA chunk, CSA, HCA) at T=8K; % of MFMA/HBM roofline
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 
-# Measured HBM bytes per launch of the headline kernel: rocprofv3 --pmc FETCH_SIZE and
+# Measured HBM bytes per headline step (both kernels): rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE (KiB per dispatch) on `bench.py --headline-only`, each scaled by the
-# counter's reading on a device copy of known size (profiles/kda_chunk_lp_C1_pmc.md).
-HEADLINE_TRAFFIC_BYTES = int((267542 * 2.0 + 142848 * 1.0) * 1024)
+# counter's reading on a device copy of known size (profiles/kda_split_C1.md).
+HEADLINE_TRAFFIC_BYTES = int(((263994 + 301219) * 2.0 + (594634 + 139264) * 1.0) * 1024)
 
 
 def _log(msg):
@@ -320,7 +322,8 @@ def main():
                    "chunk": 64, "state": "fp32", "baseline_config": "configs[1]"},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": HEADLINE_TRAFFIC_BYTES,
-                     "algorithmic_bytes": bytes_, "kernel": "kda_chunk_lp_kernel<128,bf16>",
+                     "algorithmic_bytes": bytes_,
+                     "kernel": "kda_prep_kernel<128,128,bf16> + kda_state_kernel<128,64,bf16>",
                      "mfma_tflops": flops / t / 1e12,
                      "mfma_frac": flops / t / 1e12 / BF16_PEAK_TFLOPS},
         "ms_per_step_median": ms_med,

@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define KCH_ABI_VERSION 3
+#define KCH_ABI_VERSION 4
 
 #define KCH_OK 0
 #define KCH_ERR_INVALID 1     /* bad pointer / shape / argument */
@@ -54,6 +54,26 @@ int kch_kda_chunk_fwd(const void* q, const void* k, const void* v, const void* g
                       const void* beta, const float* s0, void* o, float* s_out,
                       int B, int T, int H, int HV, int K, int V, float scale,
                       float g_clamp_min, int dtype, void* stream);
+
+/*
+ * Workspace bytes kch_kda_chunk_fwd_ws needs for these sizes, or 0 when the
+ * sizes run without one (fp32 inputs, V = 192, 256, ...).
+ */
+size_t kch_kda_chunk_ws_bytes(int B, int T, int H, int HV, int K, int V, int dtype);
+
+/*
+ * kch_kda_chunk_fwd with a caller-provided device workspace (256-byte aligned,
+ * at least kch_kda_chunk_ws_bytes bytes; ignored when that is 0). Replaces the
+ * same reference function. For bf16 / fp16 inputs with K, V in {64, 128} the
+ * state-independent part of every chunk runs fully parallel and writes its
+ * operands to the workspace; a second kernel carries the state through the
+ * chunks. Same arguments, coverage and results as kch_kda_chunk_fwd.
+ */
+int kch_kda_chunk_fwd_ws(const void* q, const void* k, const void* v, const void* g,
+                         const void* beta, const float* s0, void* o, float* s_out,
+                         int B, int T, int H, int HV, int K, int V, float scale,
+                         float g_clamp_min, int dtype, void* ws, size_t ws_bytes,
+                         void* stream);
 
 /*
  * Per-token KDA recurrence (decode steps and short sequences).

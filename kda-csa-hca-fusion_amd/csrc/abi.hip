@@ -69,11 +69,13 @@ int kch_abi_version(void) { return KCH_ABI_VERSION; }
 
 const char* kch_last_error(void) { return g_last_error.c_str(); }
 
-int kch_kda_chunk_fwd(const void* q, const void* k, const void* v, const void* g,
-                      const void* beta, const float* s0, void* o, float* s_out, int B, int T,
-                      int H, int HV, int K, int V, float scale, float g_clamp_min, int dtype,
-                      void* stream) {
-  const char* fn = "kch_kda_chunk_fwd";
+// Shared checks and the empty-input case of the chunk entry points; returns
+// KCH_OK with *done set when nothing remains to launch.
+static int chunk_prologue(const char* fn, const void* q, const void* k, const void* v,
+                          const void* g, const void* beta, const float* s0, void* o,
+                          float* s_out, int B, int T, int H, int HV, int K, int V,
+                          float g_clamp_min, int dtype, void* stream, bool* done) {
+  *done = false;
   int rc = check_kda_common(fn, q, k, v, g, beta, o, B, T, H, HV, K, V, dtype);
   if (rc) return rc;
   if (K != 64 && K != 128)
@@ -84,6 +86,7 @@ int kch_kda_chunk_fwd(const void* q, const void* k, const void* v, const void* g
   if (rc) return rc;
   if (B == 0 || T == 0) {
     // nothing to compute; the state passes through unchanged
+    *done = true;
     if (s_out && B > 0) {
       const size_t n = (size_t)B * HV * K * V * sizeof(float);
       hipError_t e = s0 ? hipMemcpyAsync(s_out, s0, n, hipMemcpyDeviceToDevice, (hipStream_t)stream)
@@ -99,8 +102,45 @@ int kch_kda_chunk_fwd(const void* q, const void* k, const void* v, const void* g
     if (any & 15)
       return fail(KCH_ERR_INVALID, "%s: q, k, v, g and o must be 16-byte aligned", fn);
   }
+  return KCH_OK;
+}
+
+int kch_kda_chunk_fwd(const void* q, const void* k, const void* v, const void* g,
+                      const void* beta, const float* s0, void* o, float* s_out, int B, int T,
+                      int H, int HV, int K, int V, float scale, float g_clamp_min, int dtype,
+                      void* stream) {
+  const char* fn = "kch_kda_chunk_fwd";
+  bool done;
+  int rc = chunk_prologue(fn, q, k, v, g, beta, s0, o, s_out, B, T, H, HV, K, V, g_clamp_min,
+                          dtype, stream, &done);
+  if (rc || done) return rc;
   kch::KdaParams p = make_kda(q, k, v, g, beta, s0, o, s_out, B, T, H, HV, K, V, scale, g_clamp_min);
   return hip_status(fn, kch::kda_chunk_dispatch(p, dtype, (hipStream_t)stream));
+}
+
+size_t kch_kda_chunk_ws_bytes(int B, int T, int H, int HV, int K, int V, int dtype) {
+  if (B <= 0 || T <= 0 || H < 1 || HV < 1 || HV % H || !kch::kda_split_supported(K, V, dtype))
+    return 0;
+  return kch::kda_split_ws_bytes(B, T, HV, K, V);
+}
+
+int kch_kda_chunk_fwd_ws(const void* q, const void* k, const void* v, const void* g,
+                         const void* beta, const float* s0, void* o, float* s_out, int B, int T,
+                         int H, int HV, int K, int V, float scale, float g_clamp_min, int dtype,
+                         void* ws, size_t ws_bytes, void* stream) {
+  const char* fn = "kch_kda_chunk_fwd_ws";
+  bool done;
+  int rc = chunk_prologue(fn, q, k, v, g, beta, s0, o, s_out, B, T, H, HV, K, V, g_clamp_min,
+                          dtype, stream, &done);
+  if (rc || done) return rc;
+  kch::KdaParams p = make_kda(q, k, v, g, beta, s0, o, s_out, B, T, H, HV, K, V, scale, g_clamp_min);
+  const size_t need = kch_kda_chunk_ws_bytes(B, T, H, HV, K, V, dtype);
+  if (need == 0) return hip_status(fn, kch::kda_chunk_dispatch(p, dtype, (hipStream_t)stream));
+  if (!ws || ws_bytes < need)
+    return fail(KCH_ERR_INVALID, "%s: workspace of %zu bytes required, got %zu", fn, need,
+                ws ? ws_bytes : (size_t)0);
+  if ((uintptr_t)ws & 255) return fail(KCH_ERR_INVALID, "%s: workspace must be 256-byte aligned", fn);
+  return hip_status(fn, kch::kda_split_dispatch(p, ws, dtype, (hipStream_t)stream));
 }
 
 int kch_kda_recurrent_fwd(const void* q, const void* k, const void* v, const void* g,

@@ -27,6 +27,11 @@ hipError_t kda_chunk_dispatch(const KdaParams& p, int dtype, hipStream_t stream)
 // bf16 / fp16 inputs, K in {64, 128}, V a multiple of 64 (kda_chunk_lp.hip)
 hipError_t kda_chunk_lp_dispatch(const KdaParams& p, int dtype, hipStream_t stream);
 hipError_t kda_recurrent_dispatch(const KdaParams& p, int dtype, hipStream_t stream);
+// Two-kernel chunk path (kda_split.hip): bf16 / fp16, K in {64,128}, V in {64,128};
+// ws is 256-byte aligned and holds kda_split_ws_bytes bytes.
+bool kda_split_supported(int K, int V, int dtype);
+size_t kda_split_ws_bytes(int B, int T, int HV, int K, int V);
+hipError_t kda_split_dispatch(const KdaParams& p, void* ws, int dtype, hipStream_t stream);
 
 // Causal depthwise convolution, kernel 3 (kda_frontend.hip).
 //   x, out : [B, T, d]   lookback : [B, 2, d] or null (zeros)

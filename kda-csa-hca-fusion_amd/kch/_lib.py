@@ -23,10 +23,12 @@ _P = ctypes.c_void_p
 _I = ctypes.c_int
 _F = ctypes.c_float
 _L = ctypes.c_longlong
+_SZ = ctypes.c_size_t
 
 # name -> argument types (all return int status)
 _SIGNATURES = {
     "kch_kda_chunk_fwd": [_P] * 8 + [_I] * 6 + [_F, _F, _I, _P],
+    "kch_kda_chunk_fwd_ws": [_P] * 8 + [_I] * 6 + [_F, _F, _I, _P, _SZ, _P],
     "kch_kda_recurrent_fwd": [_P] * 8 + [_I] * 6 + [_F, _F, _I, _P],
     "kch_compress": [_P, _L, _P, _L, _P, _P, _P, _I, _I, _P, _I, _I, _I, _I, _I, _P],
     "kch_compress_overlapped": [_P, _L, _P, _L, _P, _L, _P, _L, _P, _P, _P, _P, _I, _I, _P,
@@ -42,7 +44,12 @@ _SIGNATURES = {
     "kch_kda_gates": [_P, _L, _P, _L, _P, _P, _P, _P, _P] + [_I] * 6 + [_F, _I, _P],
 }
 
-EXPORTED = ["kch_abi_version", "kch_last_error"] + sorted(_SIGNATURES)
+# name -> (return type, argument types) of the entry points that return a value
+_QUERIES = {
+    "kch_kda_chunk_ws_bytes": (_SZ, [_I] * 7),
+}
+
+EXPORTED = ["kch_abi_version", "kch_last_error"] + sorted(_SIGNATURES) + sorted(_QUERIES)
 
 DTYPE_CODE = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 
@@ -67,6 +74,10 @@ def load():
         for name, args in _SIGNATURES.items():
             fn = getattr(lib, name)
             fn.restype = _I
+            fn.argtypes = args
+        for name, (ret, args) in _QUERIES.items():
+            fn = getattr(lib, name)
+            fn.restype = ret
             fn.argtypes = args
         _lib = lib
     return _lib

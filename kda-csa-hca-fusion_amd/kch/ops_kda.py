@@ -121,9 +121,16 @@ def _run(entry, fn_name, q, k, v, g, beta, scale, initial_state, output_final_st
         if s_out is not None:
             s_out.copy_(s0) if s0 is not None else s_out.zero_()
         return o, (s_out.to(target_state) if s_out is not None else None)
-    _lib.call(entry, _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(beta),
-              _lib.ptr(s0), _lib.ptr(o), _lib.ptr(s_out), B, T, H, HV, K, V, sc,
-              _clamp_value(g_clamp_min), code, _lib.stream_of(q))
+    args = (_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(beta),
+            _lib.ptr(s0), _lib.ptr(o), _lib.ptr(s_out), B, T, H, HV, K, V, sc,
+            _clamp_value(g_clamp_min), code)
+    if entry == "kch_kda_chunk_fwd":
+        # the two-kernel path: per-chunk operands go through a device workspace
+        nbytes = _lib.load().kch_kda_chunk_ws_bytes(B, T, H, HV, K, V, code)
+        ws = torch.empty(max(nbytes, 1), device=q.device, dtype=torch.uint8)
+        _lib.call("kch_kda_chunk_fwd_ws", *args, _lib.ptr(ws), nbytes, _lib.stream_of(q))
+    else:
+        _lib.call(entry, *args, _lib.stream_of(q))
     if s_out is not None and target_state != torch.float32:
         s_out = s_out.to(target_state)
     return o, s_out

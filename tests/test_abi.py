@@ -51,3 +51,19 @@ def test_invalid_arguments_report_errors_without_gpu():
                                1, 8, 2, 2, 96, 128, ctypes.c_float(1.0),
                                ctypes.c_float(-10.0), 1, None)
     assert rc == 2
+
+
+def test_chunk_workspace_size_query():
+    """kch_kda_chunk_ws_bytes: 0 where no workspace is used, else the sum of
+    the six per-chunk records, each region padded to 256 bytes."""
+    from kch import _lib
+    lib = _lib.load()
+    assert lib.kch_kda_chunk_ws_bytes(2, 100, 2, 2, 128, 128, 0) == 0    # fp32
+    assert lib.kch_kda_chunk_ws_bytes(2, 100, 2, 2, 128, 192, 1) == 0    # V outside {64,128}
+    assert lib.kch_kda_chunk_ws_bytes(2, 0, 2, 2, 128, 128, 1) == 0
+    B, T, HV, K, V = 2, 100, 4, 128, 64
+    R = B * HV * ((T + 63) // 64)
+    pad = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    expect = (3 * pad(R * 64 * K * 2) + pad(R * 64 * 64 * 2) + pad(R * 64 * V * 2)
+              + pad(R * K * 4))
+    assert lib.kch_kda_chunk_ws_bytes(B, T, 2, HV, K, V, 1) == expect

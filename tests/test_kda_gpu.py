@@ -185,3 +185,50 @@ def test_kda_forward_dispatch_and_errors(dev):
     o3, s3 = kch.naive_chunk_kda(*[t[:, :0] for t in ts], initial_state=s0.to(dev),
                                  output_final_state=True)
     assert o3.shape == (1, 0, 1, 64) and torch.equal(s3.cpu(), s0)
+
+
+def test_fused_entry_point_without_workspace(dev):
+    """kch_kda_chunk_fwd (one fused kernel, no workspace) stays correct beside
+    the two-kernel path of kch_kda_chunk_fwd_ws."""
+    from kch import _lib
+    B, T, H, HV, K, V = 2, 150, 2, 2, 128, 128
+    ts, host, s0 = make(21, B, T, H, HV, K, V, "bf16")
+    q, k, v, g, beta = [t.to(dev) for t in ts]
+    s0d = s0.to(dev)
+    o = torch.empty_like(v)
+    s = torch.empty(B, HV, K, V, device=dev)
+    _lib.call("kch_kda_chunk_fwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g),
+              _lib.ptr(beta), _lib.ptr(s0d), _lib.ptr(o), _lib.ptr(s), B, T, H, HV, K, V,
+              K ** -0.5, -10.0, 1, _lib.stream_of(q))
+    torch.cuda.synchronize()
+    o_ref, s_ref = o_chunk(*host, initial_state=s0.numpy(), chunk_size=64)
+    check("o", o.float().cpu().numpy(), bf16_round(o_ref), "bf16")
+    check("state", s.cpu().numpy(), s_ref, "bf16")
+
+
+def test_workspace_too_small_is_an_error(dev):
+    from kch import _lib
+    B, T, H, HV, K, V = 1, 64, 1, 1, 64, 64
+    ts, _, _ = make(22, B, T, H, HV, K, V, "bf16")
+    q, k, v, g, beta = [t.to(dev) for t in ts]
+    o = torch.empty_like(v)
+    need = _lib.load().kch_kda_chunk_ws_bytes(B, T, H, HV, K, V, 1)
+    ws = torch.empty(need, device=dev, dtype=torch.uint8)
+    with pytest.raises(RuntimeError, match="workspace"):
+        _lib.call("kch_kda_chunk_fwd_ws", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g),
+                  _lib.ptr(beta), None, _lib.ptr(o), None, B, T, H, HV, K, V, 0.125, -10.0, 1,
+                  _lib.ptr(ws), need - 1, _lib.stream_of(q))
+
+
+def test_chunk_exact_path_some_chunks_k128(dev):
+    # strong decay only in the second and fourth chunk: exact and anchored chunks alternate
+    def gfn(rng, sh):
+        g = logsigmoid(rng.standard_normal(sh))
+        g[:, 64:128] = -5.0 + 0.1 * rng.standard_normal(g[:, 64:128].shape)
+        g[:, 192:240] = -4.0
+        return g
+    ts, host, s0 = make(23, 2, 250, 2, 4, 128, 64, "bf16", g_fn=gfn)
+    o, s = run_chunk(dev, ts, s0)
+    o_ref, s_ref = o_chunk(*host, initial_state=s0.numpy(), chunk_size=64)
+    check("o", o, bf16_round(o_ref), "bf16")
+    check("state", s, s_ref, "bf16")
