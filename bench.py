@@ -24,6 +24,8 @@ the metric, each at its configuration, with the same timing protocol:
     (compression + indexer + sparse attention, projections excluded);
   * ``hca_C3`` / ``hca_T8K``: ``naive_hca`` at configs[3] (B4 T32768 d2048,
     16 heads of 128, m'=128, window 128 + sink) and at T=8192, plus its core;
+  * ``decode_bw``: one CSA and one HCA decode step on long caches (B=64 /
+    B=128 at a 1M-token context), HBM bandwidth against 8 TB/s;
   * ``hybrid_C4``: ``HybridDecoding`` (5 layers, 3:1:1, d2048, the configs
     1-3 head shapes) prefill of B=2 T=16384, then 256 single-token steps.
 Weights are N(0, 1/fan_in) random (no checkpoints), inputs N(0,1).
@@ -276,6 +278,78 @@ def bench_hybrid(dev, T=16384, B=2, n_decode=256):
             "decode_tokens_per_s": B * n_decode / (dec_ms * 1e-3)}
 
 
+def bench_decode_bw(dev, reps=5):
+    """Decode steps on long caches, timed one by one with the 256 MB MALL flushed
+    before each (a 512 MB write), so the reads come from HBM:
+      CSA: B=64, 1M-token context (262144 blocks of m=4), indexer 4 x 64 top-512
+           over bf16 key rows, 16 heads of 128, window 128 + sink;
+      HCA: B=128, 1M-token context (8192 blocks of m'=128), 16 heads of 128,
+           window 128 + sink.
+    Algorithmic bytes: every key row, its inverse norm, the selected rows and the
+    window for CSA; every compressed row and the window for HCA."""
+    from kch import _lib
+    lib = _lib.load()
+    g = torch.Generator(device=dev).manual_seed(5)
+    flush = torch.empty(512 << 20, device=dev, dtype=torch.uint8)
+
+    def timed(fn):
+        ts = []
+        for i in range(reps + 1):
+            flush.fill_(i & 0xff)
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            torch.cuda.synchronize()
+            if i:
+                ts.append(a.elapsed_time(b))
+        return float(np.median(ts))
+
+    res = {}
+    B, nb, c, cI, nh, nIh, topk, win = 64, 262144, 128, 64, 16, 4, 512, 128
+    kr = torch.randn(B, nb, cI, device=dev, generator=g).to(torch.bfloat16)
+    kinv = kr.float().norm(dim=-1).clamp_min(1e-12).reciprocal()
+    kv = torch.nn.functional.normalize(torch.randn(B, nb, c, device=dev, generator=g), dim=-1).to(torch.bfloat16)
+    ring = torch.nn.functional.normalize(torch.randn(B, win, c, device=dev, generator=g), dim=-1).to(torch.bfloat16)
+    q = torch.randn(B, nh, c, device=dev, generator=g)
+    qi = torch.randn(B, nIh, cI, device=dev, generator=g)
+    wi = torch.randn(B, nIh, device=dev, generator=g)
+    sink = torch.randn(nh, device=dev, generator=g)
+    out = torch.empty(B, nh, c, device=dev)
+    nbytes = lib.kch_decode_ws_bytes(B, nb, nh, c, topk, win, 1)
+    ws = torch.empty(nbytes, device=dev, dtype=torch.uint8)
+    st = _lib.stream_of(q)
+
+    def csa():
+        _lib.call("kch_csa_decode", _lib.ptr(q), _lib.ptr(qi), _lib.ptr(wi), _lib.ptr(kv), nb * c,
+                  _lib.ptr(kr), nb * cI, _lib.ptr(kinv), nb, _lib.ptr(ring), win * c, win,
+                  _lib.ptr(sink), _lib.ptr(out), None, B, nb, nh, c, nIh, cI, topk, 1.0, 1.0, 1, 1,
+                  0, 1, 0, _lib.ptr(ws), nbytes, st)
+    ms = timed(csa)
+    byts = B * (nb * (cI * 2 + 4) + (topk + win) * c * 2 + (nh * c + nIh * cI + nIh) * 4 + nh * c * 4)
+    res["csa"] = {"B": B, "context": nb * 4, "blocks": nb, "topk": topk, "ms": ms,
+                  "algorithmic_bytes": byts, "gbs": byts / (ms * 1e-3) / 1e9,
+                  "hbm_frac": byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    del kr, kinv, kv, ring, ws
+    torch.cuda.empty_cache()
+    B, nb = 128, 8192
+    kv = torch.nn.functional.normalize(torch.randn(B, nb, c, device=dev, generator=g), dim=-1).to(torch.bfloat16)
+    ring = torch.nn.functional.normalize(torch.randn(B, win, c, device=dev, generator=g), dim=-1).to(torch.bfloat16)
+    q = torch.randn(B, nh, c, device=dev, generator=g)
+    out = torch.empty(B, nh, c, device=dev)
+    nbytes = lib.kch_decode_ws_bytes(B, nb, nh, c, 0, win, 0)
+    ws = torch.empty(nbytes, device=dev, dtype=torch.uint8)
+
+    def hca():
+        _lib.call("kch_hca_decode", _lib.ptr(q), _lib.ptr(kv), nb * c, _lib.ptr(ring), win * c, win,
+                  _lib.ptr(sink), _lib.ptr(out), B, nb, nh, c, 1.0, 1, 0, 0, _lib.ptr(ws), nbytes, st)
+    ms = timed(hca)
+    byts = B * ((nb + win) * c * 2 + nh * c * 4 * 2)
+    res["hca"] = {"B": B, "context": nb * 128, "blocks": nb, "ms": ms, "algorithmic_bytes": byts,
+                  "gbs": byts / (ms * 1e-3) / 1e9, "hbm_frac": byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -347,6 +421,11 @@ def main():
         _log(f"hca C3: {extra['hca_C3']['ms']:.3f} ms")
         extra["hca_T8K"] = bench_hca(4, 8192, max(3, args.steps // 4), 1, dev)
         _log(f"hca T8K: {extra['hca_T8K']['ms']:.3f} ms")
+        torch.cuda.empty_cache()
+        extra["decode_bw"] = bench_decode_bw(dev)
+        _log(f"decode bw: csa {extra['decode_bw']['csa']['ms']:.3f} ms "
+             f"({extra['decode_bw']['csa']['hbm_frac']:.1%} of HBM), hca "
+             f"{extra['decode_bw']['hca']['ms']:.3f} ms ({extra['decode_bw']['hca']['hbm_frac']:.1%})")
         torch.cuda.empty_cache()
         extra["hybrid_C4"] = bench_hybrid(dev)
         _log(f"hybrid C4: prefill {extra['hybrid_C4']['prefill_ms']:.2f} ms, decode "

@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define KCH_ABI_VERSION 4
+#define KCH_ABI_VERSION 5
 
 #define KCH_OK 0
 #define KCH_ERR_INVALID 1     /* bad pointer / shape / argument */
@@ -193,6 +193,47 @@ int kch_hca_decode_step(const void* q, const void* kv_comp, long long kv_bstride
                         long long ring_bstride, int ring_len, const float* sink, void* out, int B,
                         int nb, int nh, int hd, float scale, int normalize_q, int qdtype, int odtype,
                         void* stream);
+
+/*
+ * Workspace bytes of one kch_csa_decode (sparse = 1) or kch_hca_decode
+ * (sparse = 0) step for these sizes.
+ */
+size_t kch_decode_ws_bytes(int B, int nb, int nh, int hd, int topk, int ring_len, int sparse);
+
+/*
+ * One CSA decode step, split across the cache (CSADecodingCache.forward_step,
+ * ops_decoding_cache.py:783-1070): lightning indexer + top-k over every cached
+ * block (all are complete, hence visible), then one joint softmax over the
+ * selected blocks, the ring window and the sink.
+ *   q [B,nh,hd], q_idx [B,nIh,cI], w_idx [B,nIh] or NULL (qdtype); q_idx is
+ *     L2-normalised in-kernel when normalize_qidx, q when normalize_q
+ *   kv_comp [B,*,hd] bf16 attention rows (batch stride kv_bstride elements)
+ *   k_rows [B,*,cI] indexer key rows as cached (kdtype), k_inv [B,*] fp32
+ *     1/max(||row||, 1e-12) or NULL for 1 (batch strides k_bstride, kinv_bstride)
+ *   ring [B,*,hd] bf16: the first ring_len rows are the window (any order)
+ *   out [B,nh,hd] (odtype); idx_out [B,topk] int32 selected blocks or NULL
+ *   ws: kch_decode_ws_bytes(B, nb, nh, hd, topk, ring_len, 1) bytes, 256-aligned
+ * Ties at the top-k threshold are taken in ascending block index. Coverage as
+ * kch_csa_decode_step; nb <= 16384 * 8192 / topk cached blocks.
+ */
+int kch_csa_decode(const void* q, const void* q_idx, const void* w_idx, const void* kv_comp,
+                   long long kv_bstride, const void* k_rows, long long k_bstride,
+                   const float* k_inv, long long kinv_bstride, const void* ring,
+                   long long ring_bstride, int ring_len, const float* sink, void* out,
+                   int* idx_out, int B, int nb, int nh, int hd, int nIh, int cI, int topk,
+                   float scale, float idx_scale, int normalize_q, int normalize_qidx,
+                   int qdtype, int kdtype, int odtype, void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * One HCA decode step, split across the cache (HCADecodingCache.forward_step,
+ * ops_decoding_cache.py:1268-1395): dense MQA over every cached compressed
+ * block, the ring window and the sink. Arguments as kch_csa_decode; ws holds
+ * kch_decode_ws_bytes(B, nb, nh, hd, 0, ring_len, 0) bytes.
+ */
+int kch_hca_decode(const void* q, const void* kv_comp, long long kv_bstride, const void* ring,
+                   long long ring_bstride, int ring_len, const float* sink, void* out, int B,
+                   int nb, int nh, int hd, float scale, int normalize_q, int qdtype, int odtype,
+                   void* ws, size_t ws_bytes, void* stream);
 
 /*
  * Causal depthwise convolution with kernel 3 of the KDA layer

@@ -378,3 +378,146 @@ int kch_kda_gates(const void* proj, long long ld_proj, const void* gl, long long
 }
 
 }  // extern "C"
+
+namespace {
+
+// Workspace plan of a decode step (kch_csa_decode / kch_hca_decode).
+struct DecodePlan {
+  int rb = 0, nr = 0;             // indexer ranges (sparse with blocks and topk > 0)
+  int na = 0, nsplit = 0, rps = 0;  // attended rows before the ring, splits, rows per split
+  size_t off_cand = 0, off_idx = 0, off_po = 0, off_pml = 0, bytes = 0;
+};
+
+size_t a256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+DecodePlan decode_plan(int B, int nb, int nh, int hd, int topk, int ring_len, bool sparse) {
+  DecodePlan pl;
+  const bool sel = sparse && nb > 0 && topk > 0;
+  if (sel) kch::decode_idx_plan(nb, topk, &pl.rb, &pl.nr);
+  pl.na = sparse ? (sel ? topk : 0) : nb;
+  const long long rows = (long long)pl.na + ring_len;
+  // about 2048 waves over the batch, 64 .. 4096 rows each, a multiple of 16
+  long long rps = ((long long)B * rows + 2047) / 2048;
+  rps = rps < 64 ? 64 : (rps > 4096 ? 4096 : rps);
+  rps = (rps + 15) & ~15LL;
+  pl.rps = (int)rps;
+  pl.nsplit = rows > 0 ? (int)((rows + rps - 1) / rps) : 0;
+  size_t off = 0;
+  pl.off_cand = off;
+  if (sel && pl.nr > 1) off += a256((size_t)B * pl.nr * topk * 8);
+  pl.off_idx = off;
+  if (sel) off += a256((size_t)B * topk * 4);
+  pl.off_po = off;
+  off += a256((size_t)B * pl.nsplit * nh * hd * 4);
+  pl.off_pml = off;
+  off += a256((size_t)B * pl.nsplit * nh * 2 * 4);
+  pl.bytes = off;
+  return pl;
+}
+
+int run_decode_attn(const char* fn, const DecodePlan& pl, const void* q, const void* kv_comp,
+                    long long kv_bstride, const int* idx, const void* ring, long long ring_bstride,
+                    int ring_len, const float* sink, void* out, int B, int nb, int nh, int hd,
+                    float scale, int normalize_q, int qdtype, int odtype, char* ws,
+                    hipStream_t s) {
+  kch::DecodeAttnParams a;
+  a.q = q;
+  a.kv = (const kch::bf16_t*)kv_comp;
+  a.idx = idx;
+  a.ring = (const kch::bf16_t*)ring;
+  a.sink = sink;
+  a.out = out;
+  a.part_o = (float*)(ws + pl.off_po);
+  a.part_ml = (float*)(ws + pl.off_pml);
+  a.kv_bstride = kv_bstride;
+  a.ring_bstride = ring_bstride;
+  a.B = B; a.nb = nb; a.nh = nh; a.hd = hd; a.na = pl.na; a.ring_len = ring_len;
+  a.nsplit = pl.nsplit; a.rows_per_split = pl.rps; a.normalize_q = normalize_q;
+  a.scale = scale;
+  if (pl.nsplit == 0) {
+    // nothing to attend to: the output is zero (hd is even, so 16-bit outputs fill whole words)
+    const long long elems = (long long)B * nh * hd;
+    const long long words = odtype == KCH_DT_F32 ? elems : elems / 2;
+    return hip_status(fn, kch::fill_u32(out, words, 0u, s));
+  }
+  return hip_status(fn, kch::decode_attn_dispatch(a, qdtype, odtype, s));
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t kch_decode_ws_bytes(int B, int nb, int nh, int hd, int topk, int ring_len, int sparse) {
+  if (B <= 0 || nb < 0 || nh < 1 || hd < 1 || topk < 0 || ring_len < 0) return 0;
+  return decode_plan(B, nb, nh, hd, topk, ring_len, sparse != 0).bytes;
+}
+
+int kch_csa_decode(const void* q, const void* q_idx, const void* w_idx, const void* kv_comp,
+                   long long kv_bstride, const void* k_rows, long long k_bstride,
+                   const float* k_inv, long long kinv_bstride, const void* ring,
+                   long long ring_bstride, int ring_len, const float* sink, void* out,
+                   int* idx_out, int B, int nb, int nh, int hd, int nIh, int cI, int topk,
+                   float scale, float idx_scale, int normalize_q, int normalize_qidx,
+                   int qdtype, int kdtype, int odtype, void* ws, size_t ws_bytes, void* stream) {
+  const char* fn = "kch_csa_decode";
+  int rc = check_attn(fn, B, 1, nb, nh, hd, qdtype, odtype);
+  if (rc) return rc;
+  if (!dtype_ok(kdtype)) return fail(KCH_ERR_INVALID, "%s: unknown key dtype %d", fn, kdtype);
+  if (topk < 0 || ring_len < 0) return fail(KCH_ERR_INVALID, "%s: topk / ring_len must be >= 0", fn);
+  if (nIh != 1 && nIh != 2 && nIh != 4 && nIh != 8 && nIh != 16)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: nIh=%d not in {1,2,4,8,16}", fn, nIh);
+  if (cI != 32 && cI != 64 && cI != 128)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: cI=%d not in {32,64,128}", fn, cI);
+  if (B == 0) return KCH_OK;
+  const DecodePlan pl = decode_plan(B, nb, nh, hd, topk, ring_len, true);
+  if (!ws || ws_bytes < pl.bytes)
+    return fail(KCH_ERR_INVALID, "%s: workspace of %zu bytes required", fn, pl.bytes);
+  if ((uintptr_t)ws & 255) return fail(KCH_ERR_INVALID, "%s: workspace must be 256-byte aligned", fn);
+  if (!q || !out || (ring_len > 0 && !ring)) return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
+  hipStream_t s = (hipStream_t)stream;
+  char* w = (char*)ws;
+  int* idx = nullptr;
+  if (pl.nr > 0) {
+    if (!q_idx || !k_rows || !kv_comp) return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
+    if ((long long)pl.nr * topk > kch::decode_merge_max())
+      return fail(KCH_ERR_UNSUPPORTED, "%s: %d cached blocks with topk=%d exceed the merge capacity",
+                  fn, nb, topk);
+    idx = idx_out ? idx_out : (int*)(w + pl.off_idx);
+    kch::DecodeIdxParams ip;
+    ip.q_idx = q_idx; ip.w_idx = w_idx; ip.keys = k_rows; ip.inv_norm = k_inv;
+    ip.k_bstride = k_bstride; ip.n_bstride = kinv_bstride;
+    ip.cand = (unsigned long long*)(w + pl.off_cand);
+    ip.idx_out = idx;
+    ip.B = B; ip.nb = nb; ip.nIh = nIh; ip.cI = cI; ip.topk = topk; ip.rb = pl.rb; ip.nr = pl.nr;
+    ip.normalize_q = normalize_qidx; ip.scale = idx_scale;
+    rc = hip_status(fn, kch::decode_idx_dispatch(ip, qdtype, kdtype, s));
+    if (rc) return rc;
+  } else if (idx_out && topk > 0) {
+    rc = hip_status(fn, kch::fill_u32(idx_out, (long long)B * topk, 0xffffffffu, s));  // all -1
+    if (rc) return rc;
+  }
+  return run_decode_attn(fn, pl, q, kv_comp, kv_bstride, idx, ring, ring_bstride, ring_len, sink,
+                         out, B, nb, nh, hd, scale, normalize_q, qdtype, odtype, w, s);
+}
+
+int kch_hca_decode(const void* q, const void* kv_comp, long long kv_bstride, const void* ring,
+                   long long ring_bstride, int ring_len, const float* sink, void* out, int B,
+                   int nb, int nh, int hd, float scale, int normalize_q, int qdtype, int odtype,
+                   void* ws, size_t ws_bytes, void* stream) {
+  const char* fn = "kch_hca_decode";
+  int rc = check_attn(fn, B, 1, nb, nh, hd, qdtype, odtype);
+  if (rc) return rc;
+  if (ring_len < 0) return fail(KCH_ERR_INVALID, "%s: ring_len must be >= 0", fn);
+  if (B == 0) return KCH_OK;
+  const DecodePlan pl = decode_plan(B, nb, nh, hd, 0, ring_len, false);
+  if (!ws || ws_bytes < pl.bytes)
+    return fail(KCH_ERR_INVALID, "%s: workspace of %zu bytes required", fn, pl.bytes);
+  if ((uintptr_t)ws & 255) return fail(KCH_ERR_INVALID, "%s: workspace must be 256-byte aligned", fn);
+  if (!q || !out || (nb > 0 && !kv_comp) || (ring_len > 0 && !ring))
+    return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
+  return run_decode_attn(fn, pl, q, kv_comp, kv_bstride, nullptr, ring, ring_bstride, ring_len,
+                         sink, out, B, nb, nh, hd, scale, normalize_q, qdtype, odtype, (char*)ws,
+                         (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -137,22 +137,37 @@ struct MqaWave {
     qscale2 = scale * kLog2eF;
   }
 
+  // Fragments of 16 key rows: this lane's key row (key n = lane & 15) at dims
+  // 32s + 8q .. 32s + 8q + 7.
+  struct Frag {
+    bf16x8 k[NS];
+  };
+  __device__ __forceinline__ static void load(Frag& f, const bf16_t* row) {
+    const int q = lane_id() >> 4;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) f.k[s] = *reinterpret_cast<const bf16x8*>(row + 32 * s + 8 * q);
+  }
+
   // Consume 16 keys. `row` is this lane's key row (key n = lane & 15), valid
   // for every lane (point invalid keys at any readable row); `valid16` has bit
   // k set when key k of the chunk is valid. `stage` is this wave's LDS buffer.
   __device__ __forceinline__ void chunk(const bf16_t* row, unsigned valid16, bf16_t* stage) {
+    Frag f;
+    load(f, row);
+    chunk(f, valid16, stage);
+  }
+
+  // Consume 16 keys already loaded into registers.
+  __device__ __forceinline__ void chunk(const Frag& f, unsigned valid16, bf16_t* stage) {
     const int l = lane_id();
     const int q = l >> 4, n = l & 15;
-    bf16x8 kf[NS];
-#pragma unroll
-    for (int s = 0; s < NS; ++s) kf[s] = *reinterpret_cast<const bf16x8*>(row + 32 * s + 8 * q);
     // previous chunk's V^T reads by this wave are complete before the overwrite
     wave_lds_sync();
 #pragma unroll
-    for (int s = 0; s < NS; ++s) *reinterpret_cast<bf16x8*>(stage + n * LDS_LD + 32 * s + 8 * q) = kf[s];
+    for (int s = 0; s < NS; ++s) *reinterpret_cast<bf16x8*>(stage + n * LDS_LD + 32 * s + 8 * q) = f.k[s];
     f32x4 st = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < NS; ++s) st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[s], qf[s], st, 0, 0, 0);
+    for (int s = 0; s < NS; ++s) st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.k[s], qf[s], st, 0, 0, 0);
     float sv[4];
     float cm = -INFINITY;
 #pragma unroll

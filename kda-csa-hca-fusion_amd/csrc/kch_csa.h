@@ -54,6 +54,46 @@ struct IndexerParams {
 };
 hipError_t indexer_dispatch(const IndexerParams& p, int dtype, hipStream_t s);
 
+// Decode-step indexer (decode.hip): one query per sequence over every cached block.
+struct DecodeIdxParams {
+  const void* q_idx;       // [B, nIh, cI] (normalised in-kernel when normalize_q)
+  const void* w_idx;       // [B, nIh] or null (= ones), q_idx's dtype
+  const void* keys;        // [B, *, cI] cached key rows (bf16 or fp32), batch stride k_bstride
+  const float* inv_norm;   // [B, *] 1 / ||key row||, batch stride n_bstride; null = 1
+  long long k_bstride, n_bstride;
+  unsigned long long* cand;  // [B, nr, topk] per-range candidates (nr > 1)
+  int* idx_out;            // [B, topk] selected blocks, sorted, -1 padded
+  int B, nb, nIh, cI, topk;
+  int rb, nr;              // range size and count (decode_idx_plan)
+  int normalize_q;
+  float scale;
+};
+void decode_idx_plan(int nb, int topk, int* rb, int* nr);
+int decode_merge_max();  // largest nr * topk the merge holds in LDS
+hipError_t fill_u32(void* p, long long n, uint32_t v, hipStream_t s);
+size_t decode_idx_lds(int rb, int topk);
+size_t decode_merge_lds(int nr, int topk);
+hipError_t decode_idx_dispatch(const DecodeIdxParams& p, int qdtype, int kdtype, hipStream_t s);
+
+// Decode-step joint-softmax MQA, split over the attended rows (decode.hip).
+// Rows of sequence b: j < na -> compressed block idx[b][j] (or j without idx;
+// -1 = unused), then the ring_len rows of the ring. Split sp covers rows
+// [sp * rows_per_split, ...) and leaves M, L and the unnormalised o per head.
+struct DecodeAttnParams {
+  const void* q;           // [B, nh, hd]
+  const bf16_t* kv;        // [B, *, hd] key/value rows, batch stride kv_bstride
+  const int* idx;          // [B, na] or null (dense)
+  const bf16_t* ring;      // [B, *, hd] window rows, batch stride ring_bstride
+  const float* sink;       // [nh] or null
+  void* out;               // [B, nh, hd]
+  float* part_o;           // [B, nsplit, nh, hd]
+  float* part_ml;          // [B, nsplit, nh, 2]
+  long long kv_bstride, ring_bstride;
+  int B, nb, nh, hd, na, ring_len, nsplit, rows_per_split, normalize_q;
+  float scale;
+};
+hipError_t decode_attn_dispatch(const DecodeAttnParams& p, int qdtype, int odtype, hipStream_t s);
+
 // Row-wise L2 normalisation: out[r] = x[r] / max(||x[r]||, 1e-12) (or a copy).
 hipError_t l2norm_rows_dispatch(const void* x, long long ldx, void* out, int out_f32, int rows,
                                 int c, int normalize, int dtype, hipStream_t s);

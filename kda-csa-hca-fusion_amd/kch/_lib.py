@@ -41,12 +41,16 @@ _SIGNATURES = {
                            + [_F, _F, _I, _I, _I, _I, _P],
     "kch_hca_decode_step": [_P, _P, _L, _P, _L, _I, _P, _P] + [_I] * 4 + [_F, _I, _I, _I, _P],
     "kch_short_conv": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
+    "kch_csa_decode": [_P, _P, _P, _P, _L, _P, _L, _P, _L, _P, _L, _I, _P, _P, _P] + [_I] * 7
+                      + [_F, _F] + [_I] * 5 + [_P, _SZ, _P],
+    "kch_hca_decode": [_P, _P, _L, _P, _L, _I, _P, _P] + [_I] * 4 + [_F, _I, _I, _I, _P, _SZ, _P],
     "kch_kda_gates": [_P, _L, _P, _L, _P, _P, _P, _P, _P] + [_I] * 6 + [_F, _I, _P],
 }
 
 # name -> (return type, argument types) of the entry points that return a value
 _QUERIES = {
     "kch_kda_chunk_ws_bytes": (_SZ, [_I] * 7),
+    "kch_decode_ws_bytes": (_SZ, [_I] * 7),
 }
 
 EXPORTED = ["kch_abi_version", "kch_last_error"] + sorted(_SIGNATURES) + sorted(_QUERIES)

@@ -18,11 +18,13 @@ State lives in GPU tensors instead of Python lists:
   populates the cache in bulk), rounded to the cache dtype as the reference
   stores them (``:750-763``), with the previous block's ``Cb / Zb`` kept for
   the overlap;
-* L2-normalised copies of the cached rows (bf16 attention keys, fp32 indexer
-  keys) are produced once per new block, where the reference re-normalises
-  every cached block on every step (``:919-924``);
-* ``forward_step`` is one ``kch_csa_decode_step`` / ``kch_hca_decode_step``
-  call (indexer + top-k + joint sparse/window/sink softmax).
+* the L2-normalised bf16 attention rows and the indexer keys' inverse norms
+  are produced once per new block, where the reference re-normalises every
+  cached block on every step (``:919-924``); the indexer reads the stored
+  rows (cache dtype) times their inverse norm;
+* ``forward_step`` is one ``kch_csa_decode`` / ``kch_hca_decode`` call: the
+  indexer, top-k and the joint sparse/window/sink softmax, each split across
+  the cache so that a step streams it at memory bandwidth.
 
 Forward only (``use_ste`` does not change the forward value); float64 caches
 are not supported.
@@ -116,13 +118,16 @@ class SlidingWindowRingBuffer:
 
 
 class _BlockStore:
-    """Geometric-capacity rows ``[B, cap, width]`` in the cache dtype plus the
-    attention copy (bf16 or fp32) of the same rows, optionally L2-normalised."""
+    """Geometric-capacity rows ``[B, cap, width]`` in the cache dtype plus, per
+    row, either the attention copy (``key_dtype``: bf16 or fp32, optionally
+    L2-normalised) or, with ``key_dtype=None``, the fp32 ``1 / max(||row||,
+    1e-12)`` of the stored row (``inv``)."""
 
     def __init__(self, B, width, device, dtype, key_dtype):
         self.B, self.width, self.device, self.dtype, self.key_dtype = B, width, device, dtype, key_dtype
         self.rows = None
         self.keys = None
+        self.inv = None
         self.key_norm = None
 
     def ensure(self, n_valid, required):
@@ -131,16 +136,31 @@ class _BlockStore:
         old = 0 if self.rows is None else self.rows.shape[1]
         cap = max(required, max(1, old * 2))
         rows = torch.empty(self.B, cap, self.width, device=self.device, dtype=self.dtype)
-        keys = torch.empty(self.B, cap, self.width, device=self.device, dtype=self.key_dtype)
+        if self.key_dtype is not None:
+            keys = torch.empty(self.B, cap, self.width, device=self.device, dtype=self.key_dtype)
+        else:
+            keys = None
+            inv = torch.empty(self.B, cap, device=self.device, dtype=torch.float32)
         if n_valid:
             rows[:, :n_valid] = self.rows[:, :n_valid]
-            keys[:, :n_valid] = self.keys[:, :n_valid]
+            if keys is not None:
+                keys[:, :n_valid] = self.keys[:, :n_valid]
+            else:
+                inv[:, :n_valid] = self.inv[:, :n_valid]
         self.rows, self.keys = rows, keys
+        if keys is None:
+            self.inv = inv
+
+    def _inv_of(self, rows):
+        return rows.float().norm(dim=-1).clamp_min(1e-12).reciprocal()
 
     def push(self, n_valid, new_rows, normalize):
         k = new_rows.shape[1]
         self.ensure(n_valid, n_valid + k)
         self.rows[:, n_valid:n_valid + k] = new_rows.to(self.dtype)
+        if self.key_dtype is None:
+            self.inv[:, n_valid:n_valid + k] = self._inv_of(self.rows[:, n_valid:n_valid + k])
+            return
         if self.key_norm is None:
             self.key_norm = normalize
         self.keys[:, n_valid:n_valid + k] = l2_normalize_rows(
@@ -160,6 +180,11 @@ class _BlockStore:
         self.device, self.dtype = device, dtype
         if self.rows is not None:
             self.rows = self.rows.to(device=device, dtype=dtype)
+            if self.key_dtype is None:
+                self.inv = self.inv.to(device=device)
+                if n_valid:
+                    self.inv[:, :n_valid] = self._inv_of(self.rows[:, :n_valid])
+                return
             self.keys = self.keys.to(device=device)
             if n_valid:
                 self.keys[:, :n_valid] = l2_normalize_rows(
@@ -204,7 +229,8 @@ class CSADecodingCache:
         self._acc_len = 0
         self._prev = None         # (Cb, Zb) of the last completed block, [B, m, c]
         self._C = _BlockStore(self.B, self.c, self.device, self.dtype, torch.bfloat16)
-        self._K = _BlockStore(self.B, self.c_I, self.device, self.dtype, torch.float32)
+        # indexer keys: the stored rows and their inverse norms (no normalised copy)
+        self._K = _BlockStore(self.B, self.c_I, self.device, self.dtype, None)
         self._sw = (SlidingWindowRingBuffer(self.B, self.win, self.c, self.device, self.dtype)
                     if self.win > 0 else None)
         self._n_tokens_seen = 0
@@ -350,23 +376,29 @@ class CSADecodingCache:
             raise NotImplementedError("float64 queries are not supported by the HIP kernels")
         with torch.no_grad():
             kv = self._C.keys_for(nb, normalize_qk) if nb else None
-            kn = self._K.keys_for(nb, normalize_qk) if nb else None
+            krows = self._K.rows if nb else None
+            kinv = self._K.inv if (nb and normalize_qk) else None
             ring = _ring_bf16(self._sw) if n_win else None
             qc = _aligned(q)
             qi = _aligned(q_idx.to(q.dtype))
             wi = None if w_idx is None else w_idx.to(q.dtype).contiguous()
-            ws = torch.empty(B, max(topk, 1), device=q.device, dtype=torch.int32)
-            self._last_indices = ws
+            idx = torch.empty(B, max(topk, 1), device=q.device, dtype=torch.int32)
+            self._last_indices = idx
             sink = None if sink_logits is None else _f32(sink_logits, q.device)
             cap_c = kv.shape[1] if kv is not None else 0
-            cap_k = kn.shape[1] if kn is not None else 0
-            _lib.call("kch_csa_decode_step", _lib.ptr(qc), _lib.ptr(qi), _lib.ptr(wi),
-                      _lib.ptr(kv), cap_c * self.c, _lib.ptr(kn), cap_k * self.c_I,
-                      _lib.ptr(ring), self.win * self.c, n_win, _lib.ptr(sink), _lib.ptr(out),
-                      _lib.ptr(ws), B, nb, nh, self.c, nIh, self.c_I, topk, float(core_scale),
+            cap_k = krows.shape[1] if krows is not None else 0
+            lib = _lib.load()
+            nbytes = lib.kch_decode_ws_bytes(B, nb, nh, self.c, topk, n_win, 1)
+            ws = torch.empty(max(nbytes, 1), device=q.device, dtype=torch.uint8)
+            fn = "CSADecodingCache.forward_step"
+            _lib.call("kch_csa_decode", _lib.ptr(qc), _lib.ptr(qi), _lib.ptr(wi),
+                      _lib.ptr(kv), cap_c * self.c, _lib.ptr(krows), cap_k * self.c_I,
+                      _lib.ptr(kinv), cap_k, _lib.ptr(ring), self.win * self.c, n_win,
+                      _lib.ptr(sink), _lib.ptr(out), _lib.ptr(idx) if topk else None, B, nb, nh,
+                      self.c, nIh, self.c_I, topk, float(core_scale),
                       1.0 if normalize_qk else self.c_I ** -0.5, 0, int(normalize_qk),
-                      _lib.dtype_code("CSADecodingCache.forward_step", q.dtype), 0,
-                      _lib.stream_of(q))
+                      _lib.dtype_code(fn, q.dtype), _lib.dtype_code(fn, self.dtype), 0,
+                      _lib.ptr(ws), nbytes, _lib.stream_of(q))
         return out
 
 
@@ -507,11 +539,13 @@ class HCADecodingCache:
             qc = _aligned(q)
             sink = None if sink_logits is None else _f32(sink_logits, q.device)
             cap = kv.shape[1] if kv is not None else 0
-            _lib.call("kch_hca_decode_step", _lib.ptr(qc), _lib.ptr(kv), cap * self.c,
+            nbytes = _lib.load().kch_decode_ws_bytes(B, nb, nh, self.c, 0, n_win, 0)
+            ws = torch.empty(max(nbytes, 1), device=q.device, dtype=torch.uint8)
+            _lib.call("kch_hca_decode", _lib.ptr(qc), _lib.ptr(kv), cap * self.c,
                       _lib.ptr(ring), self.win * self.c, n_win, _lib.ptr(sink), _lib.ptr(out), B,
                       nb, nh, self.c, float(core_scale), 0,
                       _lib.dtype_code("HCADecodingCache.forward_step", q.dtype), 0,
-                      _lib.stream_of(q))
+                      _lib.ptr(ws), nbytes, _lib.stream_of(q))
         return out
 
 
