@@ -393,7 +393,7 @@ size_t a256(size_t x) { return (x + 255) & ~(size_t)255; }
 DecodePlan decode_plan(int B, int nb, int nh, int hd, int topk, int ring_len, bool sparse) {
   DecodePlan pl;
   const bool sel = sparse && nb > 0 && topk > 0;
-  if (sel) kch::decode_idx_plan(nb, topk, &pl.rb, &pl.nr);
+  if (sel) kch::decode_idx_plan(B, nb, topk, &pl.rb, &pl.nr);
   pl.na = sparse ? (sel ? topk : 0) : nb;
   const long long rows = (long long)pl.na + ring_len;
   // about 2048 waves over the batch, 64 .. 4096 rows each, a multiple of 16
@@ -479,7 +479,7 @@ int kch_csa_decode(const void* q, const void* q_idx, const void* w_idx, const vo
   int* idx = nullptr;
   if (pl.nr > 0) {
     if (!q_idx || !k_rows || !kv_comp) return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
-    if ((long long)pl.nr * topk > kch::decode_merge_max())
+    if (pl.nr > 1 && !kch::decode_merge_fits(topk))
       return fail(KCH_ERR_UNSUPPORTED, "%s: %d cached blocks with topk=%d exceed the merge capacity",
                   fn, nb, topk);
     idx = idx_out ? idx_out : (int*)(w + pl.off_idx);

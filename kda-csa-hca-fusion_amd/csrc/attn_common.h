@@ -19,6 +19,10 @@
 //   16x16x16 MFMA in O^T = V^T P^T (k = keys), so P never leaves the lane.
 //   V^T fragments (4 keys of one dim) are read from a wave-private LDS copy of
 //   the 16 rows. O^T tile t holds dims 16t + 4q..4q+3 of head n.
+// Softmax reference: M (per head) trails the running max by at most 8 in
+// log2 units; o and L are rescaled only when a chunk exceeds that, and the
+// final o / L (with the sink term taken relative to the same M) is the same
+// quotient.
 #pragma once
 
 #include "kch_device.h"
@@ -26,6 +30,7 @@
 namespace kch {
 
 constexpr float kLog2eF = 1.4426950408889634f;
+constexpr float kRescaleLog2 = 8.f;  // MqaWave: slack of the softmax reference point
 
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m); }
 
@@ -102,7 +107,7 @@ struct MqaWave {
 
   bf16x8 qf[NS];  // Q fragments: head n, dims 8q + 32s
   f32x4 o[NT];
-  float M, L;     // running max (log2 units) and sum of head n
+  float M, L;     // softmax reference point (log2 units) and sum of head n
   float qscale2;  // score scale * log2(e)
 
   // q_row: this lane's head row (nullptr for a padding head -> zeros);
@@ -177,23 +182,23 @@ struct MqaWave {
       cm = fmaxf(cm, sv[e]);
     }
     cm = colq_max(cm);
-    const float mnew = fmaxf(M, cm);
-    float p[4];
-    float ps = 0.f;
-    if (mnew == -INFINITY) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) p[e] = 0.f;
-    } else {
-      const float alpha = fast_exp2(M - mnew);  // M = -inf -> 0
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        p[e] = fast_exp2(sv[e] - mnew);
-        ps += p[e];
-      }
+    // M is a reference point, not necessarily the running max: o and L are
+    // rescaled only when some head's chunk max exceeds its M by more than 8
+    // (log2 units), so p <= 2^8 and most chunks skip the rescale.
+    if (__ballot(cm > M + kRescaleLog2)) {
+      const float mnew = fmaxf(M, cm);
+      const float alpha = mnew == -INFINITY ? 1.f : fast_exp2(M - mnew);  // M = -inf -> 0
       L = L * alpha;
 #pragma unroll
       for (int t = 0; t < NT; ++t) o[t] *= alpha;
       M = mnew;
+    }
+    float p[4];
+    float ps = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      p[e] = sv[e] == -INFINITY ? 0.f : fast_exp2(sv[e] - M);  // M is finite when sv is
+      ps += p[e];
     }
     L += colq_sum(ps);
     bf16x4 pb = {(bf16_t)p[0], (bf16_t)p[1], (bf16_t)p[2], (bf16_t)p[3]};

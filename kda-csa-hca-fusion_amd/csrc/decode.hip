@@ -5,21 +5,24 @@
 // is bound by reading the cache, so every kernel splits the cache across many
 // workgroups instead of giving one workgroup to each sequence.
 //
-// idx_range_kernel   lightning-indexer logits of one range of <= RB cached
+// idx_range_kernel   lightning-indexer logits of one range of <= RB_MAX cached
 //   blocks of one sequence (ops_csa.py:503-536: relu(scale q_h . k_n / ||k_n||),
-//   weighted head sum), then the range's top-k: a block-level 4 x 8-bit radix
-//   select on order-preserving keys and an order-preserving compaction (ties
-//   at the threshold taken in ascending block index). Keys are the cached rows
-//   as stored (cache dtype) times a per-row fp32 1/||k|| (1 without
+//   weighted head sum), then the range's top-k. Keys are the cached rows as
+//   stored (cache dtype) times a per-row fp32 1/||k|| (1 without
 //   normalisation); q is split into bf16 hi + lo, so a bf16 key row gives the
-//   logit to ~2^-16 relative error with two MFMAs.
-//   With one range per sequence the result is sorted and final; otherwise the
-//   selected (key, index) pairs are written in index order as candidates.
-// idx_merge_kernel   the top-k of the candidates of all ranges of a sequence.
-//   A global top-k lies in the union of the per-range top-ks under the same
-//   tie rule, and the candidates are laid out range-major in index order, so
-//   an order-preserving selection keeps the lowest-index rule. Output sorted by
-//   (logit desc, index asc).
+//   logit to ~2^-16 relative error with two MFMAs. Each logit becomes a unique
+//   64-bit value (order-preserving key, then the complement of the block
+//   index), so "larger value" is exactly the reference's order with ties taken
+//   in ascending block index, and a selection needs no tie bookkeeping.
+//   Selection: each thread holds 32 values in registers; a threshold
+//   estimated from 256 evenly spaced samples narrows an exact radix select
+//   (reg_select) to the values at or above it (about 2 topk of them), all
+//   values when the estimate misses. One range per sequence: sorted and final; otherwise the range's
+//   top-k are candidates.
+// idx_merge_kernel   the top-k of the candidates of all ranges of a sequence
+//   (a global top-k lies in the union of the per-range top-ks), by the same
+//   estimate-gather-select over the candidates streamed from global memory;
+//   output sorted by value (logit desc, index asc).
 // attn_part_kernel   joint-softmax MQA over a slice of the attended rows of a
 //   sequence (selected or all compressed blocks, then the ring window): per
 //   head the running max M, sum L and the unnormalised o (MqaWave).
@@ -36,7 +39,10 @@ namespace kch {
 
 namespace {
 
-constexpr int RB_MAX = 8192;  // blocks per indexer range
+constexpr int RB_MAX = 8192;     // blocks per indexer range (keys held in LDS)
+constexpr int WG_TARGET = 1024;  // indexer workgroups worth splitting a small batch for
+constexpr int SV_CAP = 2048;     // key positions a range gathers at or above its estimate
+constexpr int MV_CAP = 4096;     // candidates the merge gathers at or above its estimate
 
 __device__ __forceinline__ uint32_t okey(float f) {
   uint32_t u = __float_as_uint(f);
@@ -53,9 +59,23 @@ __device__ __forceinline__ void split8(const float* f, bf16x8& hi, bf16x8& lo) {
   }
 }
 
-// Exclusive prefix sum over the 256 threads of the block (scratch: 8 ints).
+// Wave index within the block, as a wave-uniform (scalar) value.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
+// Lanes below this one with their bit set in m.
+__device__ __forceinline__ int mbcnt64(unsigned long long m) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+  for (int d = 32; d; d >>= 1) v += __shfl_xor(v, d);
+  return v;
+}
+
+// Exclusive prefix sum over the 256 threads of the block (scratch: 4 ints).
 __device__ __forceinline__ int block_excl_scan(int v, int* scratch) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   int x = v;
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
@@ -70,79 +90,310 @@ __device__ __forceinline__ int block_excl_scan(int v, int* scratch) {
   return x - v + off;
 }
 
-// Top-`topk` of `n` keys (order-preserving uint32, key(i)) held in LDS by a
-// 256-thread block: returns the threshold key and sets *n_above (keys >
-// threshold) and *n_tie_take (keys == threshold to take, lowest position first).
-// Requires topk < n.
-template <typename KeyF>
-__device__ uint32_t block_radix_select(KeyF key, int n, int topk, uint32_t* hist, int* scratch,
-                                       int* n_above, int* n_tie_take) {
-  const int tid = threadIdx.x;
-  uint32_t prefix = 0, pmask = 0;
-  int need = topk, above_total = 0;
-  for (int pass = 0; pass < 4; ++pass) {
-    const int shift = 24 - 8 * pass;
-    hist[tid] = 0;
-    __syncthreads();
-    for (int i = tid; i < n; i += 256) {
-      const uint32_t u = key(i);
-      if ((u & pmask) == prefix) atomicAdd(&hist[(u >> shift) & 255u], 1u);
-    }
-    __syncthreads();
-    // thread t: bin 255 - t (descending); cumulative count of larger bins
-    const int c = (int)hist[255 - tid];
-    const int cum = block_excl_scan(c, scratch);
-    if (cum < need && cum + c >= need) {
-      scratch[8] = 255 - tid;
-      scratch[9] = cum;
-    }
-    __syncthreads();
-    const int bin = scratch[8], above = scratch[9];
-    __syncthreads();
-    prefix |= (uint32_t)bin << shift;
-    pmask |= 255u << shift;
-    need -= above;
-    above_total += above;
-  }
-  *n_above = above_total;
-  *n_tie_take = need;
-  return prefix;
+typedef unsigned long long u64;
+
+// Ordered value of a logit key and its block index: unique within a sequence,
+// and larger for a larger logit, then for a lower index (the tie rule).
+__device__ __forceinline__ u64 kv64(uint32_t key, int index) {
+  return ((u64)key << 32) | (uint32_t)(~(uint32_t)index);
+}
+__device__ __forceinline__ int kv64_index(u64 v) { return (int)(~(uint32_t)(v & 0xffffffffull)); }
+
+__device__ __forceinline__ u64 shfl_xor64(u64 v, int d) {
+  const int lo = __shfl_xor((int)(uint32_t)v, d), hi = __shfl_xor((int)(uint32_t)(v >> 32), d);
+  return ((u64)(uint32_t)hi << 32) | (uint32_t)lo;
 }
 
-// Order-preserving compaction of the selected positions (key > thr, or key ==
-// thr among the first `tie_take` such positions; every position when
-// take_all) into out[0 .. count): out[j] = val(i). Each thread scans one
-// contiguous segment of the n positions. Returns the count.
-template <typename KeyF, typename ValF>
-__device__ int block_compact(KeyF key, ValF val, int n, uint32_t thr, int tie_take, bool take_all,
-                             unsigned long long* out, int* scratch) {
+// The topk largest of a set of unique values: exactly those with
+// (v & mask) >= thr (mask: a run of leading ones).
+struct Sel64 {
+  u64 thr, mask;
+};
+
+// Radix select of the topk largest of n unique 64-bit values val(i), i < n,
+// topk < n, by a 256-thread block. The leading bits common to all values are
+// skipped (an AND / OR reduction); 8-bit digits are then resolved high to low
+// and the search stops as soon as the boundary digit holds exactly the values
+// still needed (at the latest when one value is left). hist: 256 words,
+// scratch: 12 ints.
+template <typename ValF>
+__device__ Sel64 block_select64(ValF val, int n, int topk, uint32_t* hist, int* scratch) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  u64 a = ~0ull, o = 0ull;
+  for (int i = tid; i < n; i += 256) {
+    const u64 v = val(i);
+    a &= v;
+    o |= v;
+  }
+#pragma unroll
+  for (int d = 32; d; d >>= 1) {
+    a &= shfl_xor64(a, d);
+    o |= shfl_xor64(o, d);
+  }
+  u64* s64 = reinterpret_cast<u64*>(scratch);  // 8 words = scratch[0 .. 15]
+  if (lane == 0) {
+    s64[wave] = a;
+    s64[4 + wave] = o;
+  }
+  __syncthreads();
+  a = s64[0] & s64[1] & s64[2] & s64[3];
+  o = s64[4] | s64[5] | s64[6] | s64[7];
+  __syncthreads();
+  int lo_bit = 64 - __clzll((long long)(a ^ o));  // values differ (n >= 2): lo_bit >= 1
+  u64 mask = lo_bit >= 64 ? 0ull : (~0ull << lo_bit);
+  u64 thr = a & mask;
+  int need = topk;
+  while (lo_bit > 0) {
+    const int w = lo_bit < 8 ? lo_bit : 8;
+    const int shift = lo_bit - w;
+    const uint32_t dm = (1u << w) - 1u;
+    hist[tid] = 0u;
+    __syncthreads();
+    for (int i = tid; i < n; i += 256) {
+      const u64 v = val(i);
+      if ((v & mask) == thr) atomicAdd(&hist[(uint32_t)(v >> shift) & dm], 1u);
+    }
+    __syncthreads();
+    // thread t: digit dm - t (descending); count of values in larger digits
+    const int bin = (int)dm - tid;
+    const int c = bin >= 0 ? (int)hist[bin] : 0;
+    const int cum = block_excl_scan(c, scratch + 16);
+    if (bin >= 0 && cum < need && cum + c >= need) {
+      scratch[20] = bin;
+      scratch[21] = cum;
+      scratch[22] = c;
+    }
+    __syncthreads();
+    const int sb = scratch[20], above = scratch[21], cnt = scratch[22];
+    __syncthreads();
+    thr |= (u64)sb << shift;
+    mask |= (u64)dm << shift;
+    need -= above;
+    lo_bit = shift;
+    if (cnt == need) break;  // the boundary digit's values are all taken
+  }
+  return Sel64{thr, mask};
+}
+
+// Calls put(slot, i, v) for every i < n with pred(v), v = val(i), slots 0,
+// 1, ... in no particular order; slots past cap are skipped. *counter (LDS,
+// zero on entry) ends as the number of such i. One LDS atomic per wave and 64
+// values.
+template <typename ValF, typename PredF, typename PutF>
+__device__ void block_gather(ValF val, int n, PredF pred, PutF put, int cap, int* counter) {
+  const int lane = threadIdx.x & 63;
+  for (int base = wave_id() * 64; base < n; base += 256) {
+    const int i = base + lane;
+    u64 v = 0ull;
+    bool t = false;
+    if (i < n) {
+      v = val(i);
+      t = pred(v);
+    }
+    const u64 m = __ballot(t);
+    if (m) {
+      int at = 0;
+      if (lane == 0) at = atomicAdd(counter, __popcll(m));
+      at = __builtin_amdgcn_readlane(at, 0) + mbcnt64(m);
+      if (t && at < cap) put(at, i, v);
+    }
+  }
+}
+
+// An estimate, from evenly spaced samples, of a value that at least topk of
+// the n values reach: the sample ranked r among S = min(n, 256) samples, with
+// r chosen three standard deviations past topk S / n. Returns false (no
+// estimate) when the samples cannot bound the set below `cap` values or half
+// of n. smp: 256 words of LDS, 16-byte aligned; scratch: 48 ints.
+template <typename ValF>
+__device__ bool sample_estimate(ValF val, int n, int topk, int cap, u64* smp, int* scratch, u64* est) {
   const int tid = threadIdx.x;
-  const int seg = (n + 255) / 256;
-  const int lo = min(n, tid * seg), hi = min(n, lo + seg);
-  int eq = 0;
-  if (!take_all)
-    for (int i = lo; i < hi; ++i) eq += key(i) == thr;
-  const int eq_before = block_excl_scan(eq, scratch);
-  auto taken = [&](uint32_t u, int& e) {
-    if (take_all) return true;
-    if (u == thr) return (e++) < tie_take;
-    return u > thr;
-  };
-  int cnt = 0, e = eq_before;
-  for (int i = lo; i < hi; ++i) cnt += taken(key(i), e);
-  int pos = block_excl_scan(cnt, scratch);
-  e = eq_before;
-  for (int i = lo; i < hi; ++i)
-    if (taken(key(i), e)) out[pos++] = val(i);
-  if (tid == 255) scratch[10] = pos;
+  const int S = n < 256 ? n : 256;
+  const float ex = (float)topk * (float)S / (float)n;
+  const int r = (int)ceilf(ex + 3.f * sqrtf(ex) + 2.f) - 1;
+  const float keep = (float)(r + 1) * (float)n / (float)S * 1.25f;
+  if (2 * (r + 1) > S || keep > (float)cap) return false;
+  u64 v = 0ull;
+  if (tid < S) v = val((int)(((long long)tid * n) / S));
+  smp[tid] = v;  // zeros past S rank below every value
   __syncthreads();
-  const int total = scratch[10];
+  if (tid < S) {
+    int rank = 0;
+#pragma unroll 8
+    for (int u = 0; u < S; u += 2) {
+      const ulonglong2 pr = *reinterpret_cast<const ulonglong2*>(smp + u);
+      rank += (pr.x > v) + (pr.y > v);
+    }
+    if (rank == r) *reinterpret_cast<u64*>(scratch + 40) = v;
+  }
   __syncthreads();
-  return total;
+  *est = *reinterpret_cast<const u64*>(scratch + 40);
+  return true;
+}
+
+// Block-wide count, AND and OR (scratch: ints 0 .. 23, 8-byte aligned).
+__device__ __forceinline__ void block_cnt_and_or(int& c, u64& a, u64& o, int* scratch) {
+  const int lane = threadIdx.x & 63, wave = wave_id();
+#pragma unroll
+  for (int d = 32; d; d >>= 1) {
+    c += __shfl_xor(c, d);
+    a &= shfl_xor64(a, d);
+    o |= shfl_xor64(o, d);
+  }
+  u64* s64 = reinterpret_cast<u64*>(scratch);
+  if (lane == 0) {
+    s64[wave] = a;
+    s64[4 + wave] = o;
+    scratch[16 + wave] = c;
+  }
+  __syncthreads();
+  a = s64[0] & s64[1] & s64[2] & s64[3];
+  o = s64[4] | s64[5] | s64[6] | s64[7];
+  c = scratch[16] + scratch[17] + scratch[18] + scratch[19];
+  __syncthreads();
+}
+
+// Radix select over values a thread holds: src.load(g) fetches them into
+// registers g (once per pass, all reads issued together), src.get(g, k, ok)
+// returns the k-th (k < R) and whether it takes part. The cnt > topk
+// participating values have AND a and OR o. Returns thr / mask such that
+// exactly topk of them have (v & mask) >= thr. 8-bit digits below the common
+// prefix, high to low, histograms double-buffered so that a pass takes three
+// barriers; stops once the boundary digit holds exactly the values still
+// needed. hist: 512 words; scratch: ints 24 .. 31.
+template <int R, typename Src>
+__device__ Sel64 reg_select(const Src& src, int topk, u64 a, u64 o, uint32_t* hist, int* scratch) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  int lo_bit = 64 - __clzll((long long)(a ^ o));
+  u64 mask = lo_bit >= 64 ? 0ull : (~0ull << lo_bit);
+  u64 thr = a & mask;
+  int need = topk, buf = 0;
+  hist[tid] = 0u;
+  hist[256 + tid] = 0u;
+  __syncthreads();
+  while (lo_bit > 0) {
+    const int w = lo_bit < 8 ? lo_bit : 8;
+    const int shift = lo_bit - w;
+    const uint32_t dm = (1u << w) - 1u;
+    uint32_t* h = hist + 256 * buf;
+    typename Src::Regs g;
+    src.load(g);
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      bool ok;
+      const u64 v = src.get(g, k, ok);
+      if (ok && (v & mask) == thr) atomicAdd(&h[(uint32_t)(v >> shift) & dm], 1u);
+    }
+    __syncthreads();
+    hist[256 * (buf ^ 1) + tid] = 0u;  // the next pass's histogram
+    // thread t: digit dm - t (descending); values in larger digits
+    const int bin = (int)dm - tid;
+    const int c = bin >= 0 ? (int)h[bin] : 0;
+    int x = c;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int y = __shfl_up(x, d);
+      if (lane >= d) x += y;
+    }
+    if (lane == 63) scratch[24 + wave] = x;
+    __syncthreads();
+    int cum = x - c;
+    for (int w2 = 0; w2 < wave; ++w2) cum += scratch[24 + w2];
+    if (bin >= 0 && cum < need && cum + c >= need) {
+      scratch[28] = bin;
+      scratch[29] = cum;
+      scratch[30] = c;
+    }
+    __syncthreads();
+    const int sb = scratch[28], above = scratch[29], cnt = scratch[30];
+    thr |= (u64)sb << shift;
+    mask |= (u64)dm << shift;
+    need -= above;
+    lo_bit = shift;
+    buf ^= 1;
+    if (cnt == need) break;  // the boundary digit's values are all taken
+  }
+  return Sel64{thr, mask};
+}
+
+// Block-wide count, AND and OR of the participating values of src.
+template <int R, typename Src>
+__device__ void reg_census(const Src& src, int& c, u64& a, u64& o, int* scratch) {
+  typename Src::Regs g;
+  src.load(g);
+  c = 0;
+  a = ~0ull;
+  o = 0ull;
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    bool ok;
+    const u64 v = src.get(g, k, ok);
+    c += ok;
+    a &= ok ? v : ~0ull;
+    o |= ok ? v : 0ull;
+  }
+  block_cnt_and_or(c, a, o, scratch);
+}
+
+// put(slot, v) for this thread's participating values with (v & mask) >= thr
+// (all of them when take_all), slots 0, 1, ... in no particular order: one
+// LDS atomic per wave. *counter (LDS) is zero on entry.
+template <int R, typename Src, typename PutF>
+__device__ void reg_gather(const Src& src, Sel64 sl, bool take_all, PutF put, int* counter) {
+  const int lane = threadIdx.x & 63;
+  typename Src::Regs g;
+  src.load(g);
+  int c = 0;
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    bool ok;
+    const u64 v = src.get(g, k, ok);
+    c += ok && (take_all || (v & sl.mask) >= sl.thr);
+  }
+  int x = c;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(x, d);
+    if (lane >= d) x += y;
+  }
+  int base = 0;
+  if (lane == 63 && x) base = atomicAdd(counter, x);
+  int at = __builtin_amdgcn_readlane(base, 63) + x - c;
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    bool ok;
+    const u64 v = src.get(g, k, ok);
+    if (ok && (take_all || (v & sl.mask) >= sl.thr)) put(at++, v);
+  }
+}
+
+// Writes out(rank, v) for the cnt unique values s[0 .. cnt) (rank 0 = the
+// largest), s 16-byte aligned with a zero at s[cnt] when cnt is odd; each
+// thread ranks EPT values against all of them, two per LDS read.
+template <int EPT, typename OutF>
+__device__ void block_rank_sort(const u64* s, int cnt, OutF out) {
+  const int tid = threadIdx.x;
+  u64 v[EPT];
+  int rk[EPT];
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const int i = tid + 256 * e;
+    v[e] = i < cnt ? s[i] : ~0ull;
+    rk[e] = 0;
+  }
+#pragma unroll 4
+  for (int f = 0; f < cnt; f += 2) {
+    const ulonglong2 pr = *reinterpret_cast<const ulonglong2*>(s + f);
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) rk[e] += (pr.x > v[e]) + (pr.y > v[e]);
+  }
+#pragma unroll
+  for (int e = 0; e < EPT; ++e)
+    if (tid + 256 * e < cnt) out(rk[e], v[e]);
 }
 
 // Bitonic sort of s[0 .. cnt) descending, padded to a power of two with zeros.
-__device__ void block_sort_desc(unsigned long long* s, int cnt) {
+__device__ void block_sort_desc(u64* s, int cnt) {
   const int tid = threadIdx.x;
   int pw = 1;
   while (pw < cnt) pw <<= 1;
@@ -153,7 +404,7 @@ __device__ void block_sort_desc(unsigned long long* s, int cnt) {
       for (int i = tid; i < pw / 2; i += 256) {
         const int a = ((i & ~(j - 1)) << 1) | (i & (j - 1));
         const int c = a + j;
-        const unsigned long long x = s[a], y = s[c];
+        const u64 x = s[a], y = s[c];
         const bool desc = (a & k) == 0;
         if (desc ? (x < y) : (x > y)) {
           s[a] = y;
@@ -165,30 +416,169 @@ __device__ void block_sort_desc(unsigned long long* s, int cnt) {
   }
 }
 
+// Sorts the cnt selected values s[0 .. cnt) descending and writes their block
+// indices to out[0 .. topk), -1 past cnt. s holds pow2_at_least(cnt + 1)
+// words, 16-byte aligned.
+__device__ void write_sorted(u64* s, int cnt, int topk, int* out) {
+  const int tid = threadIdx.x;
+  for (int i = cnt + tid; i < topk; i += 256) out[i] = -1;
+  if (cnt <= 2048) {
+    if (tid == 0 && (cnt & 1)) s[cnt] = 0ull;
+    __syncthreads();
+    auto put = [&](int rank, u64 v) { out[rank] = kv64_index(v); };
+    if (cnt <= 256) block_rank_sort<1>(s, cnt, put);
+    else if (cnt <= 512) block_rank_sort<2>(s, cnt, put);
+    else if (cnt <= 1024) block_rank_sort<4>(s, cnt, put);
+    else block_rank_sort<8>(s, cnt, put);
+  } else {
+    block_sort_desc(s, cnt);
+    for (int i = tid; i < cnt; i += 256) out[i] = kv64_index(s[i]);
+  }
+}
+
+__host__ __device__ inline int pow2_at_least(int x) {
+  int p = 1;
+  while (p < x) p <<= 1;
+  return p;
+}
+
+// Eight key elements of one row as stored: bf16 rows feed the MFMA as they
+// are; fp16 / fp32 rows are split into bf16 hi + lo when consumed.
+template <typename KT>
+struct KeyFrag {
+  bf16x8 v;
+  __device__ __forceinline__ void load(const KT* p) { v = *reinterpret_cast<const bf16x8*>(p); }
+};
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+template <>
+struct KeyFrag<_Float16> {
+  f16x8 v;
+  __device__ __forceinline__ void load(const _Float16* p) { v = *reinterpret_cast<const f16x8*>(p); }
+};
+template <>
+struct KeyFrag<float> {
+  float4 a, b;
+  __device__ __forceinline__ void load(const float* p) {
+    a = *reinterpret_cast<const float4*>(p);
+    b = *reinterpret_cast<const float4*>(p + 4);
+  }
+};
+
+template <typename KT>
+__device__ __forceinline__ f32x4 key_mfma(const KeyFrag<KT>& k, const bf16x8& qhi, const bf16x8& qlo, f32x4 acc) {
+  if constexpr (std::is_same<KT, bf16_t>::value) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qhi, k.v, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qlo, k.v, acc, 0, 0, 0);
+  } else {
+    float f[8];
+    if constexpr (std::is_same<KT, float>::value) {
+      f[0] = k.a.x; f[1] = k.a.y; f[2] = k.a.z; f[3] = k.a.w;
+      f[4] = k.b.x; f[5] = k.b.y; f[6] = k.b.z; f[7] = k.b.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) f[i] = (float)k.v[i];
+    }
+    bf16x8 khi, klo;
+    split8(f, khi, klo);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qhi, khi, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qlo, khi, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qhi, klo, acc, 0, 0, 0);
+  }
+  return acc;
+}
+
+// The logit keys of a range in LDS, as the values of thread t: positions
+// 4 t + 1024 s + e (s < RB_MAX / 1024, e < 4); a value takes part when its
+// position is in the range and it is at or above est.
+struct RangeKeys {
+  const uint32_t* keys;
+  int n, r0;
+  u64 est;
+  struct Regs {
+    uint4 q[RB_MAX / 1024];
+  };
+  __device__ __forceinline__ void load(Regs& g) const {
+#pragma unroll
+    for (int s = 0; s < RB_MAX / 1024; ++s)
+      g.q[s] = *reinterpret_cast<const uint4*>(keys + 4 * threadIdx.x + 1024 * s);
+  }
+  __device__ __forceinline__ u64 get(const Regs& g, int k, bool& ok) const {
+    const int pos = 4 * threadIdx.x + 1024 * (k >> 2) + (k & 3);
+    const uint4 q = g.q[k >> 2];
+    const uint32_t key = (k & 3) == 0 ? q.x : ((k & 3) == 1 ? q.y : ((k & 3) == 2 ? q.z : q.w));
+    const u64 v = kv64(key, r0 + pos);
+    ok = pos < n && v >= est;
+    return v;
+  }
+};
+
+// Gathered positions of a range's keys (sv[j], j < cnt), as the values of
+// thread t: j = t + 256 k (k < SV_CAP / 256).
+struct SvKeys {
+  const uint32_t* keys;
+  const unsigned short* sv;
+  int cnt, r0;
+  struct Regs {
+    u64 v[SV_CAP / 256];
+  };
+  __device__ __forceinline__ void load(Regs& g) const {
+#pragma unroll
+    for (int k = 0; k < SV_CAP / 256; ++k) {
+      const int j = threadIdx.x + 256 * k;
+      const int pos = j < cnt ? sv[j] : 0;
+      g.v[k] = kv64(keys[pos], r0 + pos);
+    }
+  }
+  __device__ __forceinline__ u64 get(const Regs& g, int k, bool& ok) const {
+    ok = (int)threadIdx.x + 256 * k < cnt;
+    return g.v[k];
+  }
+};
+
+// Survivor values held in registers, RM per thread (value k of thread t is
+// survivor t + 256 k; those past cnt do not take part).
+template <int RM>
+struct RegVals {
+  const u64* v;
+  int cnt;
+  struct Regs {};
+  __device__ __forceinline__ void load(Regs&) const {}
+  __device__ __forceinline__ u64 get(const Regs&, int k, bool& ok) const {
+    ok = (int)threadIdx.x + 256 * k < cnt;
+    return v[k];
+  }
+};
+
+// LDS of the range kernel: keys [RB_MAX] | hist [512] | scratch [48] | counter [4] |
+// sv [SV_CAP ushort], aliased by smp [256 u64] | sel [pow2(min(topk, rb) + 1) u64, one range only]
 template <typename QT, typename KT, int CI>
-__global__ __launch_bounds__(256) void idx_range_kernel(DecodeIdxParams p) {
+__global__ __launch_bounds__(256, 4) void idx_range_kernel(DecodeIdxParams p) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   constexpr int NS = CI / 32;
-  uint32_t* keys = reinterpret_cast<uint32_t*>(smem);                          // [RB]
-  uint32_t* hist = keys + p.rb;                                                 // [256]
-  int* scratch = reinterpret_cast<int*>(hist + 256);                            // [16]
-  unsigned long long* sel = reinterpret_cast<unsigned long long*>(scratch + 16);  // [ptop]
+  // fragments in flight per wave: about 16 KB of key rows
+  constexpr int VG = NS * 8 * (int)sizeof(KT) / 4;
+  constexpr int D = 64 / VG < 2 ? 2 : (64 / VG > 8 ? 8 : 64 / VG);
+  uint32_t* keys = reinterpret_cast<uint32_t*>(smem);       // [RB_MAX] (reads of whole 16-byte groups)
+  uint32_t* hist = keys + RB_MAX;                            // [512]
+  int* scratch = reinterpret_cast<int*>(hist + 512);         // [48]
+  int* counter = scratch + 48;                               // [4]
+  unsigned short* sv = reinterpret_cast<unsigned short*>(counter + 4);  // [SV_CAP]
+  u64* smp = reinterpret_cast<u64*>(sv);                     // [256], before sv is gathered
+  u64* sel = reinterpret_cast<u64*>(sv + SV_CAP);            // [ptop]
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int q4 = lane >> 4, n = lane & 15;
   const int b = blockIdx.x / p.nr, r = blockIdx.x - b * p.nr;
   const int r0 = r * p.rb;
   const int nr_blocks = min(p.rb, p.nb - r0);
   const int nIh = p.nIh;
-  if (nr_blocks <= 0) {  // an empty trailing range: no candidates
-    unsigned long long* out = p.cand + ((size_t)b * p.nr + r) * p.topk;
-    for (int i = tid; i < p.topk; i += 256) out[i] = 0ull;
-    return;
-  }
+  // a sequence's candidates: nr lists of topk (range r holds min(its blocks, topk))
+  u64* cout = p.cand + ((size_t)b * p.nr + r) * p.topk;
+  if (nr_blocks <= 0) return;  // no range is empty (decode_idx_plan)
 
-  // ---- q fragments: column n = head (zero beyond nIh), split bf16 ----
+  // ---- q fragments (MFMA A operand: row = index head n, zero beyond nIh), split bf16 ----
   bf16x8 qhi[NS], qlo[NS];
-  float wq = 0.f;
+  float w4[4];  // weights of the heads 4 q4 + e this lane's accumulator rows hold
   {
     float f[NS][8];
     float ss = 0.f;
@@ -206,130 +596,241 @@ __global__ __launch_bounds__(256) void idx_range_kernel(DecodeIdxParams p) {
       for (int i = 0; i < 8; ++i) f[s][i] = n < nIh ? f[s][i] * inv : 0.f;
       split8(f[s], qhi[s], qlo[s]);
     }
-    if (n < nIh) wq = p.w_idx ? ld_f32(static_cast<const QT*>(p.w_idx) + (size_t)b * nIh + n) : 1.f;
-  }
-
-  // ---- logits of this range: wave w takes 16-block chunks w, w + 4, ... ----
-  const KT* kbase = static_cast<const KT*>(p.keys) + (size_t)b * p.k_bstride;
-  const float* ibase = p.inv_norm ? p.inv_norm + (size_t)b * p.n_bstride : nullptr;
-  const int nchunk = (nr_blocks + 15) / 16;
-  auto load_k = [&](int c, float (&kf)[NS][8]) {
-    const int blk = r0 + min(16 * c + n, nr_blocks - 1);
-    const KT* krow = kbase + (size_t)blk * CI;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) Load8<KT>::run(krow + 32 * s + 8 * q4, kf[s]);
-  };
-  float kf[NS][8];
-  if (wave < nchunk) load_k(wave, kf);
-  for (int c = wave; c < nchunk; c += 4) {
-    float cur[NS][8];
-#pragma unroll
-    for (int s = 0; s < NS; ++s)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) cur[s][i] = kf[s][i];
-    if (c + 4 < nchunk) load_k(c + 4, kf);
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      bf16x8 khi, klo;
-      split8(cur[s], khi, klo);
-      // D[block][head]: A = key rows, B = q columns
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi, qhi[s], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi, qlo[s], acc, 0, 0, 0);
-      if constexpr (!std::is_same<KT, bf16_t>::value)
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(klo, qhi[s], acc, 0, 0, 0);
-    }
-    const int j0 = 16 * c + 4 * q4;  // range-local blocks j0 .. j0 + 3 of this lane
-    float4 iv = make_float4(1.f, 1.f, 1.f, 1.f);
-    if (ibase) {
-      iv.x = ibase[r0 + min(j0, nr_blocks - 1)];
-      iv.y = ibase[r0 + min(j0 + 1, nr_blocks - 1)];
-      iv.z = ibase[r0 + min(j0 + 2, nr_blocks - 1)];
-      iv.w = ibase[r0 + min(j0 + 3, nr_blocks - 1)];
-    }
-    const float ivs[4] = {iv.x, iv.y, iv.z, iv.w};
+    const QT* wrow = static_cast<const QT*>(p.w_idx) + (size_t)b * nIh;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      float v = fmaxf(acc[e] * p.scale * ivs[e], 0.f) * wq;
-      for (int d = 1; d < nIh; d <<= 1) v += __shfl_xor(v, d);
-      if (n == 0 && j0 + e < nr_blocks) keys[j0 + e] = okey(v);
+      const int hh = 4 * q4 + e;
+      w4[e] = hh < nIh ? (p.w_idx ? ld_f32(wrow + hh) : 1.f) : 0.f;
     }
   }
+
+  // ---- logits: wave w takes 16-block chunks w, w + 4, ..., D of them in flight ----
+  // D[head][block] = q_head . key_block: the head sum is then lane-local
+  // (plus one or two cross-row adds when nIh > 4).
+  const KT* kbase = static_cast<const KT*>(p.keys) + (size_t)b * p.k_bstride + (size_t)r0 * CI;
+  // without inverse norms, a readable word (the first key) is loaded and replaced by 1
+  const bool has_inv = p.inv_norm != nullptr;
+  const float* ibase = has_inv ? p.inv_norm + (size_t)b * p.n_bstride + r0 : static_cast<const float*>(p.keys);
+  const int istride = has_inv ? 1 : 0;
+  const int nchunk = (nr_blocks + 15) / 16;
+  const int mine = nchunk > wave ? (nchunk - wave + 3) / 4 : 0;
+  KeyFrag<KT> kf[D][NS];
+  float iv[D];
+  auto load = [&](int m, KeyFrag<KT> (&f)[NS], float& ivv) {
+    const int j = min(16 * (wave + 4 * m) + n, nr_blocks - 1);
+    const KT* krow = kbase + (size_t)j * CI + 8 * q4;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) f[s].load(krow + 32 * s);
+    ivv = ibase[j * istride];
+  };
+  // consume slot d as chunk m, then (RELOAD) refill it with chunk m + D
+  auto step = [&](int m, KeyFrag<KT> (&f)[NS], float& ivv, auto reload) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < NS; ++s) acc = key_mfma<KT>(f[s], qhi[s], qlo[s], acc);
+    const float sc = p.scale * (has_inv ? ivv : 1.f);
+    float v = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v += fmaxf(acc[e] * sc, 0.f) * w4[e];
+    if constexpr (decltype(reload)::value) load(m + D, f, ivv);
+    if (nIh > 4) v += __shfl_xor(v, 16);
+    if (nIh > 8) v += __shfl_xor(v, 32);
+    const int j = 16 * (wave + 4 * m) + n;
+    if (q4 == 0 && j < nr_blocks) keys[j] = okey(v);
+  };
+#pragma unroll
+  for (int d = 0; d < D; ++d) load(d, kf[d], iv[d]);
+  // whole groups of D chunks without conditions (so that every wait for a slot
+  // counts only the loads issued before it), then the remainder
+  int m0 = 0;
+  for (; m0 + D <= mine; m0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) step(m0 + d, kf[d], iv[d], std::true_type{});
+  }
+#pragma unroll
+  for (int d = 0; d < D; ++d)
+    if (m0 + d < mine) step(m0 + d, kf[d], iv[d], std::false_type{});
   __syncthreads();
 
   // ---- top-k of the range ----
+  // Thread t owns the keys at positions 4 t + 1024 s + e (s < 8, e < 4),
+  // re-read from LDS in every pass as eight unconditional 16-byte reads
+  // (holding them would cost 64 VGPRs; words past the range are masked off); a
+  // sampled estimate narrows the radix select to the values at or above it
+  // (about 2 topk), all values when it misses.
   const int topk = p.topk;
-  const bool take_all = nr_blocks <= topk;
-  int above = 0, tie_take = 0;
-  uint32_t thr = 0;
-  auto key_at = [&](int i) { return keys[i]; };
-  auto val_at = [&](int i) {
-    return ((unsigned long long)keys[i] << 32) | (uint32_t)(~(uint32_t)(r0 + i));
-  };
-  if (!take_all) thr = block_radix_select(key_at, nr_blocks, topk, hist, scratch, &above, &tie_take);
-  const int cnt = block_compact(key_at, val_at, nr_blocks, thr, tie_take, take_all, sel, scratch);
+  constexpr int RK = 4 * (RB_MAX / 1024);
+  RangeKeys src{keys, nr_blocks, r0, 0ull};
+  Sel64 sl{0ull, 0ull};
+  bool all = nr_blocks <= topk, gathered = false;
+  int c = 0;
+  if (!all) {
+    if (sample_estimate([&](int i) { return kv64(keys[i], r0 + i); }, nr_blocks, topk, SV_CAP, smp,
+                        scratch, &src.est)) {
+      // census of the values at or above the estimate, gathering their positions
+      if (tid == 0) counter[2] = 0;
+      __syncthreads();
+      RangeKeys::Regs g;
+      src.load(g);
+      u64 a = ~0ull, o = 0ull;
+      uint32_t okm = 0u;  // bit k: value k takes part
+#pragma unroll
+      for (int k = 0; k < RK; ++k) {
+        bool ok;
+        const u64 v = src.get(g, k, ok);
+        okm |= (uint32_t)ok << k;
+        a &= ok ? v : ~0ull;
+        o |= ok ? v : 0ull;
+      }
+      c = __popc(okm);
+      int x = c;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(x, d);
+        if (lane >= d) x += y;
+      }
+      int base = 0;
+      if (lane == 63 && x) base = atomicAdd(counter + 2, x);
+      int at = __builtin_amdgcn_readlane(base, 63) + x - c;
+#pragma unroll
+      for (int k = 0; k < RK; ++k) {
+        if ((okm >> k) & 1u) {
+          if (at < SV_CAP) sv[at] = (unsigned short)(4 * tid + 1024 * (k >> 2) + (k & 3));
+          ++at;
+        }
+      }
+      block_cnt_and_or(c, a, o, scratch);
+      if (c >= topk && c <= SV_CAP) {
+        gathered = true;
+        all = c == topk;
+        if (!all) sl = reg_select<SV_CAP / 256>(SvKeys{keys, sv, c, r0}, topk, a, o, hist, scratch);
+      }
+    }
+    if (!gathered) {  // no estimate, or it missed: select among all
+      src.est = 0ull;
+      u64 a, o;
+      reg_census<RK>(src, c, a, o, scratch);
+      sl = reg_select<RK>(src, topk, a, o, hist, scratch);
+    }
+  }
+  if (tid == 0) counter[0] = 0;
+  __syncthreads();
+  if (gathered) {
+    const SvKeys gsrc{keys, sv, c, r0};
+    if (p.nr == 1) {
+      reg_gather<SV_CAP / 256>(gsrc, sl, all, [&](int at, u64 v) { sel[at] = v; }, counter);
+      __syncthreads();
+      write_sorted(sel, topk, topk, p.idx_out + (size_t)b * topk);
+    } else {
+      reg_gather<SV_CAP / 256>(gsrc, sl, all, [&](int at, u64 v) { cout[at] = v; }, counter);
+    }
+    return;
+  }
+  if (tid == 0) counter[0] = 0;
+  __syncthreads();
   if (p.nr == 1) {
-    block_sort_desc(sel, cnt);
-    int* out = p.idx_out + (size_t)b * topk;
-    for (int i = tid; i < topk; i += 256) out[i] = i < cnt ? (int)(~(uint32_t)(sel[i] & 0xffffffffull)) : -1;
+    reg_gather<RK>(src, sl, all, [&](int at, u64 v) { sel[at] = v; }, counter);
+    __syncthreads();
+    write_sorted(sel, min(nr_blocks, topk), topk, p.idx_out + (size_t)b * topk);
   } else {
-    unsigned long long* out = p.cand + ((size_t)b * p.nr + r) * topk;
-    for (int i = tid; i < topk; i += 256) out[i] = i < cnt ? sel[i] : 0ull;
+    // candidates (any order) straight to global: min(nr_blocks, topk) of them
+    reg_gather<RK>(src, sl, all, [&](int at, u64 v) { cout[at] = v; }, counter);
   }
 }
 
+// Gather capacity of the merge: MV_CAP when an estimate can pay off, else
+// just room for the samples.
+__host__ __device__ inline int merge_cap(int topk) { return topk <= MV_CAP / 2 ? MV_CAP : 256; }
+
+// LDS of the merge kernel: sv [merge_cap u64] | sel [pow2(topk + 1) u64] |
+// hist [512] | scratch [48] | counter [4]
 __global__ __launch_bounds__(256) void idx_merge_kernel(DecodeIdxParams p) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  const int topk = p.topk, nr = p.nr, nc = nr * topk;
-  unsigned long long* cand = reinterpret_cast<unsigned long long*>(smem);  // [nc]
-  uint32_t* hist = reinterpret_cast<uint32_t*>(cand + nc);                 // [256]
-  int* scratch = reinterpret_cast<int*>(hist + 256);                       // [16]
-  int* roff = scratch + 16;                                                // [nr + 1]
-  unsigned long long* sel = reinterpret_cast<unsigned long long*>(roff + ((nr + 2) & ~1));  // [ptop]
+  const int topk = p.topk, nr = p.nr;
+  const int mcap = merge_cap(topk);
+  u64* sv = reinterpret_cast<u64*>(smem);                   // [mcap]
+  u64* sel = sv + mcap;                                      // [ptop]
+  uint32_t* hist = reinterpret_cast<uint32_t*>(sel + pow2_at_least(topk + 1));  // [512]
+  int* scratch = reinterpret_cast<int*>(hist + 512);         // [48]
+  int* counter = scratch + 48;                               // [4]
   const int tid = threadIdx.x, b = blockIdx.x;
-  const unsigned long long* src = p.cand + (size_t)b * nc;
-  // each range's list holds its selected pairs first, then zeros (no real key is
-  // 0: every logit is >= 0, whose key is 2^31): count by binary search
-  for (int r = tid; r < nr; r += 256) {
-    const unsigned long long* lst = src + (size_t)r * topk;
-    int lo = 0, hi = topk;
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      if ((lst[mid] >> 32) != 0ull) lo = mid + 1;
-      else hi = mid;
+  const u64* src = p.cand + (size_t)b * nr * topk;
+  // candidate f of the sequence: ranges before the last hold c0 each
+  const int c0 = min(p.rb, topk);
+  const int cl = min(p.nb - (nr - 1) * p.rb, topk);
+  const int N = (nr - 1) * c0 + cl;
+  auto gval = [&](int f) {
+    const int r = min(f / c0, nr - 1);
+    return src[(size_t)r * topk + (f - r * c0)];
+  };
+  int cnt = N;
+  if (N <= topk) {
+    for (int f = tid; f < N; f += 256) sel[f] = gval(f);
+    __syncthreads();
+  } else {
+    u64 est = 0ull;
+    bool done = false;
+    if (sample_estimate(gval, N, topk, mcap, sv, scratch, &est)) {
+      // stream the candidates once: those at or above the estimate into sv
+      if (tid == 0) counter[0] = 0;
+      __syncthreads();
+      constexpr int U = 8;
+      const int lane = tid & 63;
+      for (int base = wave_id() * 64 * U; base < N; base += 256 * U) {
+        u64 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = gval(min(base + 64 * u + lane, N - 1));
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const bool t = base + 64 * u + lane < N && v[u] >= est;
+          const u64 m = __ballot(t);
+          if (m) {
+            int at = 0;
+            if (lane == 0) at = atomicAdd(counter, __popcll(m));
+            at = __builtin_amdgcn_readlane(at, 0) + mbcnt64(m);
+            if (t && at < mcap) sv[at] = v[u];
+          }
+        }
+      }
+      __syncthreads();
+      const int total = counter[0];
+      if (total >= topk && total <= mcap) {
+        constexpr int RM = MV_CAP / 256;
+        u64 rv[RM];
+#pragma unroll
+        for (int k = 0; k < RM; ++k) rv[k] = tid + 256 * k < total ? sv[tid + 256 * k] : 0ull;
+        const RegVals<RM> src{rv, total};
+        Sel64 sl{0ull, 0ull};
+        if (total > topk) {
+          int c;
+          u64 a, o;
+          reg_census<RM>(src, c, a, o, scratch);
+          sl = reg_select<RM>(src, topk, a, o, hist, scratch);
+        }
+        if (tid == 0) counter[1] = 0;
+        __syncthreads();
+        reg_gather<RM>(src, sl, total == topk, [&](int at, u64 v) { sel[at] = v; }, counter + 1);
+        done = true;
+      }
     }
-    roff[r + 1] = lo;
+    if (!done) {
+      const Sel64 sl = block_select64(gval, N, topk, hist, scratch);
+      if (tid == 0) counter[1] = 0;
+      __syncthreads();
+      block_gather(gval, N, [&](u64 v) { return (v & sl.mask) >= sl.thr; },
+                   [&](int at, int, u64 v) { sel[at] = v; }, topk, counter + 1);
+    }
+    __syncthreads();
+    cnt = topk;
   }
-  __syncthreads();
-  if (tid == 0) {
-    roff[0] = 0;
-    for (int r = 0; r < nr; ++r) roff[r + 1] += roff[r];
-  }
-  __syncthreads();
-  const int total = roff[nr];
-  // compacted candidates: ranges ascending, index order within a range = index order
-  for (int i = tid; i < nc; i += 256) {
-    const int r = i / topk, j = i - r * topk;
-    if (j < roff[r + 1] - roff[r]) cand[roff[r] + j] = src[i];
-  }
-  __syncthreads();
-  auto key_at = [&](int i) { return (uint32_t)(cand[i] >> 32); };
-  auto val_at = [&](int i) { return cand[i]; };
-  int above = 0, tie_take = 0;
-  uint32_t thr = 0;
-  const bool take_all = total <= topk;
-  if (!take_all) thr = block_radix_select(key_at, total, topk, hist, scratch, &above, &tie_take);
-  const int cnt = block_compact(key_at, val_at, total, thr, tie_take, take_all, sel, scratch);
-  block_sort_desc(sel, cnt);
-  int* out = p.idx_out + (size_t)b * topk;
-  for (int i = tid; i < topk; i += 256) out[i] = i < cnt ? (int)(~(uint32_t)(sel[i] & 0xffffffffull)) : -1;
+  write_sorted(sel, cnt, topk, p.idx_out + (size_t)b * topk);
 }
 
 template <int HD, typename QT>
 __global__ __launch_bounds__(256) void attn_part_kernel(DecodeAttnParams p) {
   using W = MqaWave<HD>;
   __shared__ __attribute__((aligned(16))) bf16_t stage_all[4][16 * W::LDS_LD];
-  const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63, n = lane & 15;
+  const int wv = wave_id(), lane = threadIdx.x & 63, n = lane & 15;
   bf16_t* stage = stage_all[wv];
   const long long gs = (long long)blockIdx.x * 4 + wv;  // global split id
   if (gs >= (long long)p.B * p.nsplit) return;
@@ -346,46 +847,55 @@ __global__ __launch_bounds__(256) void attn_part_kernel(DecodeAttnParams p) {
   // rows of padding lanes must still be readable: a cached block when there is
   // one, else the ring (a split only exists when one of the two holds rows)
   const bf16_t* dflt = p.na > 0 ? kv : ring;
-  // chunk c covers rows j0 + 16c .. ; its row pointer and validity
-  auto row_of = [&](int c, bool& ok) {
+  // Block indices come 64 rows (4 chunks) at a time, one per lane, from a load
+  // issued a group ahead of its use, so that waiting for it never waits for
+  // the row loads issued after it.
+  // (row_of reads an entry only for rows below min(j1, na), so the clamped
+  // loads past that need no masking; without indices a readable word is loaded)
+  const int* ip = idx ? idx : reinterpret_cast<const int*>(dflt);
+  const int ilim = idx ? max(min(j1, p.na), 1) : 1;
+  auto idx_group = [&](int g) { return ip[min(j0 + 64 * g + lane, ilim - 1)]; };
+  // chunk c covers rows j0 + 16c .. ; this lane's row (n) and its validity
+  auto row_of = [&](int c, int ig, bool& ok) {
     const int j = j0 + 16 * c + n;
+    const int blk = idx ? __shfl(ig, (16 * c + n) & 63) : j;
     ok = j < j1;
     const bf16_t* row = dflt;
-    if (ok) {
-      if (j < p.na) {
-        const int blk = idx ? idx[j] : j;
-        ok = blk >= 0 && blk < p.nb;
-        if (ok) row = kv + (size_t)blk * HD;
-      } else {
-        row = ring + (size_t)(j - p.na) * HD;
-      }
+    if (j < p.na) {
+      ok = ok && blk >= 0 && blk < p.nb;
+      if (ok) row = kv + (size_t)blk * HD;
+    } else if (ok) {
+      row = ring + (size_t)(j - p.na) * HD;
     }
     return row;
   };
-  // software pipeline: the rows of chunk c + D are requested while chunk c is consumed
-  constexpr int D = 4;
-  typename W::Frag fr[D];
-  unsigned vm[D];
+  // software pipeline over groups of 4 chunks: chunk c + 4 is requested once
+  // chunk c is consumed; refills are unconditional (past the end they read the
+  // default row, masked off) so that no loaded register is ever copied
+  typename W::Frag fr[4];
+  unsigned vm[4];
   const int nch = (j1 - j0 + 15) / 16;
+  const int ng = (nch + 3) / 4;
+  const int ig0 = idx_group(0);
+  int ig1 = idx_group(1);
 #pragma unroll
-  for (int d = 0; d < D; ++d) {
+  for (int t = 0; t < 4; ++t) {
     bool ok;
-    const bf16_t* row = row_of(d, ok);
-    vm[d] = (unsigned)__ballot(ok && lane < 16) & 0xffffu;
-    if (d < nch) W::load(fr[d], row);
+    const bf16_t* row = row_of(t, ig0, ok);
+    vm[t] = (unsigned)__ballot(ok && lane < 16) & 0xffffu;
+    W::load(fr[t], row);
   }
-  for (int c0 = 0; c0 < nch; c0 += D) {
+  for (int g = 0; g < ng; ++g) {
+    const int ig2 = idx_group(g + 2);
 #pragma unroll
-    for (int d = 0; d < D; ++d) {
-      const int c = c0 + d;
-      if (c < nch) {
-        if (vm[d]) w.chunk(fr[d], vm[d], stage);
-        bool ok;
-        const bf16_t* row = row_of(c + D, ok);
-        vm[d] = (unsigned)__ballot(ok && lane < 16) & 0xffffu;
-        if (c + D < nch) W::load(fr[d], row);
-      }
+    for (int t = 0; t < 4; ++t) {
+      if (vm[t]) w.chunk(fr[t], vm[t], stage);
+      bool ok;
+      const bf16_t* row = row_of(4 * (g + 1) + t, ig1, ok);
+      vm[t] = (unsigned)__ballot(ok && lane < 16) & 0xffffu;
+      W::load(fr[t], row);
     }
+    ig1 = ig2;
   }
   // partial state of head n: unnormalised o, M (log2 units), L
   if (n < p.nh) {
@@ -452,32 +962,34 @@ hipError_t fill_u32(void* p, long long n, uint32_t v, hipStream_t s) {
   return hipGetLastError();
 }
 
-int decode_merge_max() { return 16384; }
-
-void decode_idx_plan(int nb, int topk, int* rb, int* nr) {
-  // ranges of at most RB_MAX blocks; a single range when it fits
-  const int r = (nb + RB_MAX - 1) / RB_MAX;
-  *nr = r < 1 ? 1 : r;
-  *rb = (nb + *nr - 1) / *nr;
-  *rb = (*rb + 15) & ~15;
-  (void)topk;
+void decode_idx_plan(int B, int nb, int topk, int* rb, int* nr) {
+  // ranges of at most RB_MAX blocks; a small batch is split further, down to
+  // ranges of max(1024, 2 topk) blocks, for about WG_TARGET workgroups
+  const int r_need = nb > 0 ? (nb + RB_MAX - 1) / RB_MAX : 1;
+  const int rb_min = max(1024, 2 * topk);
+  const int r_fine = (nb + rb_min - 1) / rb_min;
+  const int r_par = (WG_TARGET + B - 1) / max(B, 1);
+  const int r = max(1, max(r_need, min(r_par, r_fine)));
+  int b = (nb + r - 1) / r;
+  b = (b + 15) & ~15;
+  *rb = b;
+  *nr = b > 0 ? (nb + b - 1) / b : 1;  // every range holds at least one block
+  if (*nr < 1) *nr = 1;
 }
 
-size_t decode_idx_lds(int rb, int topk) {
-  int ptop = 1;
-  while (ptop < topk) ptop <<= 1;
-  return (size_t)rb * 4 + 256 * 4 + 16 * 4 + (size_t)ptop * 8;
+size_t decode_idx_lds(int rb, int topk, int nr) {
+  const size_t base = (size_t)RB_MAX * 4 + 512 * 4 + 52 * 4 + (size_t)SV_CAP * 2;
+  return base + (nr == 1 ? (size_t)pow2_at_least(min(topk, rb) + 1) * 8 : 0);
 }
 
-size_t decode_merge_lds(int nr, int topk) {
-  int ptop = 1;
-  while (ptop < topk) ptop <<= 1;
-  const size_t nc = (size_t)nr * topk;
-  return nc * 8 + 256 * 4 + 16 * 4 + (size_t)((nr + 2) & ~1) * 4 + (size_t)ptop * 8;
+size_t decode_merge_lds(int topk) {
+  return (size_t)merge_cap(topk) * 8 + (size_t)pow2_at_least(topk + 1) * 8 + 512 * 4 + 52 * 4;
 }
+
+bool decode_merge_fits(int topk) { return decode_merge_lds(topk) <= 160 * 1024; }
 
 hipError_t decode_idx_dispatch(const DecodeIdxParams& p, int qdtype, int kdtype, hipStream_t s) {
-  const size_t lds = decode_idx_lds(p.rb, p.topk);
+  const size_t lds = decode_idx_lds(p.rb, p.topk, p.nr);
   const dim3 grid((unsigned)(p.B * p.nr)), block(256);
 #define KCH_DIDX(QT, KT, CI) hipLaunchKernelGGL((idx_range_kernel<QT, KT, CI>), grid, block, lds, s, p)
 #define KCH_DIDX_CI(QT, KT)             \
@@ -501,7 +1013,7 @@ hipError_t decode_idx_dispatch(const DecodeIdxParams& p, int qdtype, int kdtype,
 #undef KCH_DIDX
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.nr == 1) return e;
-  hipLaunchKernelGGL(idx_merge_kernel, dim3((unsigned)p.B), dim3(256), decode_merge_lds(p.nr, p.topk), s, p);
+  hipLaunchKernelGGL(idx_merge_kernel, dim3((unsigned)p.B), dim3(256), decode_merge_lds(p.topk), s, p);
   return hipGetLastError();
 }
 

@@ -68,11 +68,11 @@ struct DecodeIdxParams {
   int normalize_q;
   float scale;
 };
-void decode_idx_plan(int nb, int topk, int* rb, int* nr);
-int decode_merge_max();  // largest nr * topk the merge holds in LDS
+void decode_idx_plan(int B, int nb, int topk, int* rb, int* nr);
+bool decode_merge_fits(int topk);  // the merge kernel's LDS holds its buffers for topk
 hipError_t fill_u32(void* p, long long n, uint32_t v, hipStream_t s);
-size_t decode_idx_lds(int rb, int topk);
-size_t decode_merge_lds(int nr, int topk);
+size_t decode_idx_lds(int rb, int topk, int nr);
+size_t decode_merge_lds(int topk);
 hipError_t decode_idx_dispatch(const DecodeIdxParams& p, int qdtype, int kdtype, hipStream_t s);
 
 // Decode-step joint-softmax MQA, split over the attended rows (decode.hip).

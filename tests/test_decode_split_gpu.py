@@ -101,7 +101,7 @@ def check_csa(name, out, idx, kr_used, crow, ring, q, qi, wi, sink, topk, normal
         close(f"{name} out b{b}", out[b], joint_ref(q[b], rows, sink))
 
 
-@pytest.mark.parametrize("nb,topk", [(20000, 512), (9000, 64), (3000, 512), (700, 1024)])
+@pytest.mark.parametrize("nb,topk", [(20000, 512), (9000, 64), (3000, 512), (700, 1024), (5000, 37)])
 def test_csa_decode_multi_range(dev, nb, topk):
     rng = np.random.default_rng(nb + topk)
     B, c, cI, nh, nIh, win = 2, 128, 64, 16, 4, 128
