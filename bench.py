@@ -280,7 +280,8 @@ def bench_hybrid(dev, T=16384, B=2, n_decode=256):
 
 def bench_decode_bw(dev, reps=5):
     """Decode steps on long caches, timed one by one with the 256 MB MALL flushed
-    before each (a 512 MB write), so the reads come from HBM:
+    before each by READING 512 MB (a write would leave dirty lines whose
+    write-back then competes with the timed reads), so the reads come from HBM:
       CSA: B=64, 1M-token context (262144 blocks of m=4), indexer 4 x 64 top-512
            over bf16 key rows, 16 heads of 128, window 128 + sink;
       HCA: B=128, 1M-token context (8192 blocks of m'=128), 16 heads of 128,
@@ -290,12 +291,13 @@ def bench_decode_bw(dev, reps=5):
     from kch import _lib
     lib = _lib.load()
     g = torch.Generator(device=dev).manual_seed(5)
-    flush = torch.empty(512 << 20, device=dev, dtype=torch.uint8)
+    flush = torch.ones(128 << 20, device=dev, dtype=torch.float32)  # 512 MB
+    torch.cuda.synchronize()
 
     def timed(fn):
         ts = []
         for i in range(reps + 1):
-            flush.fill_(i & 0xff)
+            flush.amax()
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record()
             fn()

@@ -384,7 +384,7 @@ namespace {
 // Workspace plan of a decode step (kch_csa_decode / kch_hca_decode).
 struct DecodePlan {
   int rb = 0, nr = 0;             // indexer ranges (sparse with blocks and topk > 0)
-  int na = 0, nsplit = 0, rps = 0;  // attended rows before the ring, splits, rows per split
+  int na = 0, ngrp = 0, grows = 0;  // attended rows before the ring, row groups, rows per group
   size_t off_cand = 0, off_idx = 0, off_po = 0, off_pml = 0, bytes = 0;
 };
 
@@ -396,21 +396,24 @@ DecodePlan decode_plan(int B, int nb, int nh, int hd, int topk, int ring_len, bo
   if (sel) kch::decode_idx_plan(B, nb, topk, &pl.rb, &pl.nr);
   pl.na = sparse ? (sel ? topk : 0) : nb;
   const long long rows = (long long)pl.na + ring_len;
-  // about 2048 waves over the batch, 64 .. 4096 rows each, a multiple of 16
-  long long rps = ((long long)B * rows + 2047) / 2048;
-  rps = rps < 64 ? 64 : (rps > 4096 ? 4096 : rps);
-  rps = (rps + 15) & ~15LL;
-  pl.rps = (int)rps;
-  pl.nsplit = rows > 0 ? (int)((rows + rps - 1) / rps) : 0;
+  // row groups (one workgroup each): about 768 over the batch (three resident
+  // per CU: one round), at least 128 rows, at most 64 per sequence, a
+  // multiple of 64 rows
+  long long grows = ((long long)B * rows + 767) / 768;
+  grows = grows < 128 ? 128 : grows;
+  grows = grows < (rows + 63) / 64 ? (rows + 63) / 64 : grows;
+  grows = (grows + 63) & ~63LL;
+  pl.grows = (int)grows;
+  pl.ngrp = rows > 0 ? (int)((rows + grows - 1) / grows) : 0;
   size_t off = 0;
   pl.off_cand = off;
   if (sel && pl.nr > 1) off += a256((size_t)B * pl.nr * topk * 8);
   pl.off_idx = off;
   if (sel) off += a256((size_t)B * topk * 4);
   pl.off_po = off;
-  off += a256((size_t)B * pl.nsplit * nh * hd * 4);
+  if (pl.ngrp > 1) off += a256((size_t)B * pl.ngrp * nh * hd * 4);
   pl.off_pml = off;
-  off += a256((size_t)B * pl.nsplit * nh * 2 * 4);
+  if (pl.ngrp > 1) off += a256((size_t)B * pl.ngrp * nh * 2 * 4);
   pl.bytes = off;
   return pl;
 }
@@ -432,9 +435,9 @@ int run_decode_attn(const char* fn, const DecodePlan& pl, const void* q, const v
   a.kv_bstride = kv_bstride;
   a.ring_bstride = ring_bstride;
   a.B = B; a.nb = nb; a.nh = nh; a.hd = hd; a.na = pl.na; a.ring_len = ring_len;
-  a.nsplit = pl.nsplit; a.rows_per_split = pl.rps; a.normalize_q = normalize_q;
+  a.ngrp = pl.ngrp; a.rows_per_group = pl.grows; a.normalize_q = normalize_q;
   a.scale = scale;
-  if (pl.nsplit == 0) {
+  if (pl.ngrp == 0) {
     // nothing to attend to: the output is zero (hd is even, so 16-bit outputs fill whole words)
     const long long elems = (long long)B * nh * hd;
     const long long words = odtype == KCH_DT_F32 ? elems : elems / 2;

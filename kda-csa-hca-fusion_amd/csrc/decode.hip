@@ -23,10 +23,11 @@
 //   (a global top-k lies in the union of the per-range top-ks), by the same
 //   estimate-gather-select over the candidates streamed from global memory;
 //   output sorted by value (logit desc, index asc).
-// attn_part_kernel   joint-softmax MQA over a slice of the attended rows of a
+// attn_kernel   joint-softmax MQA over a group of the attended rows of a
 //   sequence (selected or all compressed blocks, then the ring window): per
-//   head the running max M, sum L and the unnormalised o (MqaWave).
-// attn_combine_kernel  merges the slices of a sequence and adds the sink:
+//   wave and head M, L and the unnormalised o (MqaWave), merged across the
+//   workgroup; attn_combine_kernel merges the groups' partials and adds the
+//   sink:
 //   o = sum_s o_s 2^(M_s-M) / (sum_s L_s 2^(M_s-M) + e^sink 2^-M), 0 when no
 //   row is valid (the all-invalid rule of ops_decoding_cache.py:1044-1059).
 
@@ -826,17 +827,24 @@ __global__ __launch_bounds__(256) void idx_merge_kernel(DecodeIdxParams p) {
   write_sorted(sel, cnt, topk, p.idx_out + (size_t)b * topk);
 }
 
-template <int HD, typename QT>
-__global__ __launch_bounds__(256) void attn_part_kernel(DecodeAttnParams p) {
+// Decode attention over one group of rows of one sequence (a workgroup): the
+// 4 waves take the group's 16-row chunks in turn (wave w: chunks w, w + 4,
+// ...), four chunks in flight per wave, merge their (M, L, o) in LDS, and
+// either finish the sequence (one group) or leave a partial for
+// attn_combine_kernel.
+template <int HD, typename QT, typename OT>
+__global__ __launch_bounds__(256, 3) void attn_kernel(DecodeAttnParams p) {
   using W = MqaWave<HD>;
-  __shared__ __attribute__((aligned(16))) bf16_t stage_all[4][16 * W::LDS_LD];
-  const int wv = wave_id(), lane = threadIdx.x & 63, n = lane & 15;
-  bf16_t* stage = stage_all[wv];
-  const long long gs = (long long)blockIdx.x * 4 + wv;  // global split id
-  if (gs >= (long long)p.B * p.nsplit) return;
-  const int b = (int)(gs / p.nsplit), sp = (int)(gs - (long long)b * p.nsplit);
+  constexpr int D = 4;
+  constexpr int STAGE = 16 * W::LDS_LD;                 // bf16 per wave
+  constexpr int MERGE = 4 * 16 * HD + 4 * 16 * 2;       // floats: o and (M, L) per wave and head
+  constexpr int LDS_BYTES = (4 * STAGE * 2 > MERGE * 4) ? 4 * STAGE * 2 : MERGE * 4;
+  __shared__ __attribute__((aligned(16))) char lds[LDS_BYTES];
+  const int tid = threadIdx.x, wv = wave_id(), lane = tid & 63, n = lane & 15;
+  bf16_t* stage = reinterpret_cast<bf16_t*>(lds) + wv * STAGE;
+  const int b = blockIdx.x / p.ngrp, g = blockIdx.x - b * p.ngrp;
   const int nrows = p.na + p.ring_len;
-  const int j0 = sp * p.rows_per_split, j1 = min(nrows, j0 + p.rows_per_split);
+  const int jg0 = g * p.rows_per_group, jg1 = min(nrows, jg0 + p.rows_per_group);
 
   const QT* qrow = static_cast<const QT*>(p.q) + ((size_t)b * p.nh + n) * HD;
   W w;
@@ -845,21 +853,19 @@ __global__ __launch_bounds__(256) void attn_part_kernel(DecodeAttnParams p) {
   const bf16_t* ring = p.ring ? p.ring + (size_t)b * p.ring_bstride : nullptr;
   const int* idx = p.idx ? p.idx + (size_t)b * p.na : nullptr;
   // rows of padding lanes must still be readable: a cached block when there is
-  // one, else the ring (a split only exists when one of the two holds rows)
+  // one, else the ring (a group only exists when one of the two holds rows)
   const bf16_t* dflt = p.na > 0 ? kv : ring;
-  // Block indices come 64 rows (4 chunks) at a time, one per lane, from a load
-  // issued a group ahead of its use, so that waiting for it never waits for
-  // the row loads issued after it.
-  // (row_of reads an entry only for rows below min(j1, na), so the clamped
-  // loads past that need no masking; without indices a readable word is loaded)
+  // Block indices are loaded 2D chunks ahead of their use; the loads are
+  // clamped, unmasked: row_of reads an entry only for rows below min(jg1, na).
+  // Without indices a readable word is loaded.
   const int* ip = idx ? idx : reinterpret_cast<const int*>(dflt);
-  const int ilim = idx ? max(min(j1, p.na), 1) : 1;
-  auto idx_group = [&](int g) { return ip[min(j0 + 64 * g + lane, ilim - 1)]; };
-  // chunk c covers rows j0 + 16c .. ; this lane's row (n) and its validity
-  auto row_of = [&](int c, int ig, bool& ok) {
-    const int j = j0 + 16 * c + n;
-    const int blk = idx ? __shfl(ig, (16 * c + n) & 63) : j;
-    ok = j < j1;
+  const int ilim = idx ? max(min(jg1, p.na), 1) : 1;
+  auto row_j = [&](int m) { return jg0 + 16 * (wv + 4 * m) + n; };
+  auto idx_of = [&](int m) { return ip[min(row_j(m), ilim - 1)]; };
+  auto row_of = [&](int m, int ix, bool& ok) {
+    const int j = row_j(m);
+    const int blk = idx ? ix : j;
+    ok = j < jg1;
     const bf16_t* row = dflt;
     if (j < p.na) {
       ok = ok && blk >= 0 && blk < p.nb;
@@ -869,71 +875,145 @@ __global__ __launch_bounds__(256) void attn_part_kernel(DecodeAttnParams p) {
     }
     return row;
   };
-  // software pipeline over groups of 4 chunks: chunk c + 4 is requested once
-  // chunk c is consumed; refills are unconditional (past the end they read the
-  // default row, masked off) so that no loaded register is ever copied
-  typename W::Frag fr[4];
-  unsigned vm[4];
-  const int nch = (j1 - j0 + 15) / 16;
-  const int ng = (nch + 3) / 4;
-  const int ig0 = idx_group(0);
-  int ig1 = idx_group(1);
+  const int ncg = (jg1 - jg0 + 15) / 16;                  // chunks in the group
+  const int mine = ncg > wv ? (ncg - wv + 3) / 4 : 0;      // this wave's
+  typename W::Frag fr[D];
+  unsigned vm[D];
+  int ix[D];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
+  for (int d = 0; d < D; ++d) ix[d] = idx_of(d);
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
     bool ok;
-    const bf16_t* row = row_of(t, ig0, ok);
-    vm[t] = (unsigned)__ballot(ok && lane < 16) & 0xffffu;
-    W::load(fr[t], row);
+    const bf16_t* row = row_of(d, ix[d], ok);
+    vm[d] = (unsigned)__ballot(ok && lane < 16) & 0xffffu;
+    W::load(fr[d], row);
+    ix[d] = idx_of(d + D);
   }
-  for (int g = 0; g < ng; ++g) {
-    const int ig2 = idx_group(g + 2);
+  // groups of D chunks with unconditional refills (past the end they read the
+  // default row, masked off), so that no loaded register is copied; chunks
+  // past this wave's last are masked (vm = 0) rather than peeled off, which
+  // would cost a second copy of the loop body's registers
+  for (int m0 = 0; m0 < mine; m0 += D) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      if (vm[t]) w.chunk(fr[t], vm[t], stage);
+    for (int d = 0; d < D; ++d) {
+      if (vm[d]) w.chunk(fr[d], vm[d], stage);
       bool ok;
-      const bf16_t* row = row_of(4 * (g + 1) + t, ig1, ok);
-      vm[t] = (unsigned)__ballot(ok && lane < 16) & 0xffffu;
-      W::load(fr[t], row);
+      const bf16_t* row = row_of(m0 + d + D, ix[d], ok);
+      vm[d] = (unsigned)__ballot(ok && lane < 16) & 0xffffu;
+      W::load(fr[d], row);
+      ix[d] = idx_of(m0 + d + 2 * D);
     }
-    ig1 = ig2;
   }
-  // partial state of head n: unnormalised o, M (log2 units), L
-  if (n < p.nh) {
-    float* po = p.part_o + ((size_t)gs * p.nh + n) * HD;
+
+  // ---- merge the 4 waves: thread t -> head t / (HD / 8), dims 8 (t % (HD / 8)) ----
+  __syncthreads();  // staging buffers are free
+  float* mo = reinterpret_cast<float*>(lds);                // [4][16][HD]
+  float* mml = mo + 4 * 16 * HD;                             // [4][16][2]
+  {
     const int q4 = 4 * (lane >> 4);
 #pragma unroll
-    for (int tt = 0; tt < W::NT; ++tt)
-      *reinterpret_cast<float4*>(po + 16 * tt + q4) = make_float4(w.o[tt][0], w.o[tt][1], w.o[tt][2], w.o[tt][3]);
-    if (lane < 16) *reinterpret_cast<float2*>(p.part_ml + ((size_t)gs * p.nh + n) * 2) = make_float2(w.M, w.L);
+    for (int t = 0; t < W::NT; ++t)
+      *reinterpret_cast<float4*>(mo + (wv * 16 + n) * HD + 16 * t + q4) =
+          make_float4(w.o[t][0], w.o[t][1], w.o[t][2], w.o[t][3]);
+    if (lane < 16) *reinterpret_cast<float2*>(mml + (wv * 16 + n) * 2) = make_float2(w.M, w.L);
+  }
+  __syncthreads();
+  constexpr int PH = HD / 8;  // threads per head
+  const int h = tid / PH, d8 = tid - h * PH;
+  const bool mine_out = h < p.nh;
+  float M = -INFINITY, L = 0.f, acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+  auto fold = [&](float Ms, float Ls, const float* os) {
+    if (!(Ls > 0.f)) return;
+    const float Mn = fmaxf(M, Ms);
+    const float a = fast_exp2(M - Mn), c = fast_exp2(Ms - Mn);  // M = -inf -> a = 0
+    L = L * a + Ls * c;
+    const float4 x0 = *reinterpret_cast<const float4*>(os), x1 = *reinterpret_cast<const float4*>(os + 4);
+    const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = acc[i] * a + xs[i] * c;
+    M = Mn;
+  };
+  if (mine_out) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const float2 ml = *reinterpret_cast<const float2*>(mml + (s * 16 + h) * 2);
+      fold(ml.x, ml.y, mo + (s * 16 + h) * HD + 8 * d8);
+    }
+  }
+  auto finish = [&]() {
+    float f = 0.f;
+    if (L > 0.f) {
+      float denom = L;
+      if (p.sink) denom += fast_exp2(p.sink[h] * kLog2eF - M);
+      f = 1.f / denom;
+    }
+    OT* out = static_cast<OT*>(p.out) + ((size_t)b * p.nh + h) * HD + 8 * d8;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[i] = from_f32<OT>(acc[i] * f);
+  };
+  if (p.ngrp == 1) {
+    if (mine_out) finish();
+    return;
+  }
+  // ---- partial of this group, merged by attn_combine_kernel ----
+  if (mine_out) {
+    const size_t slot = ((size_t)b * p.ngrp + g) * p.nh + h;
+    float* po = p.part_o + slot * HD + 8 * d8;
+    *reinterpret_cast<float4*>(po) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    *reinterpret_cast<float4*>(po + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+    if (d8 == 0) *reinterpret_cast<float2*>(p.part_ml + slot * 2) = make_float2(M, L);
   }
 }
 
-template <typename OT>
+// Merges the ngrp partials of each (sequence, head) and adds the sink; thread
+// -> (sequence, head, 8 dims), one pass with a running reference point, the
+// partial loads of four groups in flight.
+template <int HD, typename OT>
 __global__ __launch_bounds__(256) void attn_combine_kernel(DecodeAttnParams p) {
-  // thread -> (head, 8 dims); a block covers 256 * 8 outputs of one sequence
-  const int hd = p.hd, per_head = hd / 8;
-  const long long g = (long long)blockIdx.x * 256 + threadIdx.x;
-  const long long total = (long long)p.B * p.nh * per_head;
-  if (g >= total) return;
-  const int d8 = (int)(g % per_head);
-  const long long bh = g / per_head;
+  constexpr int PH = HD / 8;
+  const long long gid = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (gid >= (long long)p.B * p.nh * PH) return;
+  const int d8 = (int)(gid % PH);
+  const long long bh = gid / PH;
   const int h = (int)(bh % p.nh), b = (int)(bh / p.nh);
-  const float2* ml = reinterpret_cast<const float2*>(p.part_ml) + (size_t)b * p.nsplit * p.nh + h;
-  float M = -INFINITY;
-  for (int s = 0; s < p.nsplit; ++s) M = fmaxf(M, ml[(size_t)s * p.nh].x);
-  float L = 0.f, acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  if (M > -INFINITY) {
-    for (int s = 0; s < p.nsplit; ++s) {
-      const float2 v = ml[(size_t)s * p.nh];
-      if (v.y <= 0.f) continue;
-      const float a = fast_exp2(v.x - M);
-      L += v.y * a;
-      const float* po = p.part_o + (((size_t)b * p.nsplit + s) * p.nh + h) * hd + 8 * d8;
-      const float4 x0 = *reinterpret_cast<const float4*>(po);
-      const float4 x1 = *reinterpret_cast<const float4*>(po + 4);
-      acc[0] += a * x0.x; acc[1] += a * x0.y; acc[2] += a * x0.z; acc[3] += a * x0.w;
-      acc[4] += a * x1.x; acc[5] += a * x1.y; acc[6] += a * x1.z; acc[7] += a * x1.w;
-    }
+  float M = -INFINITY, L = 0.f, acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+  auto fold = [&](float2 ml, float4 x0, float4 x1) {
+    if (!(ml.y > 0.f)) return;
+    const float Mn = fmaxf(M, ml.x);
+    const float a = fast_exp2(M - Mn), c = fast_exp2(ml.x - Mn);
+    L = L * a + ml.y * c;
+    const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = acc[i] * a + xs[i] * c;
+    M = Mn;
+  };
+  const size_t s0 = (size_t)b * p.ngrp;
+  auto ld = [&](int s, float2& ml, float4& x0, float4& x1) {
+    const size_t sl = (s0 + s) * p.nh + h;
+    ml = *reinterpret_cast<const float2*>(p.part_ml + sl * 2);
+    const float* po = p.part_o + sl * HD + 8 * d8;
+    x0 = *reinterpret_cast<const float4*>(po);
+    x1 = *reinterpret_cast<const float4*>(po + 4);
+  };
+  int s = 0;
+  for (; s + 4 <= p.ngrp; s += 4) {
+    float2 ml[4];
+    float4 x0[4], x1[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) ld(s + u, ml[u], x0[u], x1[u]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) fold(ml[u], x0[u], x1[u]);
+  }
+  for (; s < p.ngrp; ++s) {
+    float2 ml;
+    float4 x0, x1;
+    ld(s, ml, x0, x1);
+    fold(ml, x0, x1);
   }
   float f = 0.f;
   if (L > 0.f) {
@@ -941,7 +1021,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(DecodeAttnParams p) {
     if (p.sink) denom += fast_exp2(p.sink[h] * kLog2eF - M);
     f = 1.f / denom;
   }
-  OT* out = static_cast<OT*>(p.out) + ((size_t)b * p.nh + h) * hd + 8 * d8;
+  OT* out = static_cast<OT*>(p.out) + ((size_t)b * p.nh + h) * HD + 8 * d8;
 #pragma unroll
   for (int i = 0; i < 8; ++i) out[i] = from_f32<OT>(acc[i] * f);
 }
@@ -1018,24 +1098,31 @@ hipError_t decode_idx_dispatch(const DecodeIdxParams& p, int qdtype, int kdtype,
 }
 
 hipError_t decode_attn_dispatch(const DecodeAttnParams& p, int qdtype, int odtype, hipStream_t s) {
-  const long long nw = (long long)p.B * p.nsplit;
-  const dim3 grid((unsigned)((nw + 3) / 4)), block(256);
+  const dim3 grid((unsigned)((long long)p.B * p.ngrp)), block(256);
+#define KCH_DATT(HD, QT)                                                                          \
+  if (odtype == DT_F32) hipLaunchKernelGGL((attn_kernel<HD, QT, float>), grid, block, 0, s, p);    \
+  else if (odtype == DT_BF16) hipLaunchKernelGGL((attn_kernel<HD, QT, bf16_t>), grid, block, 0, s, p); \
+  else hipLaunchKernelGGL((attn_kernel<HD, QT, _Float16>), grid, block, 0, s, p);
   if (p.hd == 128) {
-    if (qdtype == DT_F32) hipLaunchKernelGGL((attn_part_kernel<128, float>), grid, block, 0, s, p);
-    else if (qdtype == DT_BF16) hipLaunchKernelGGL((attn_part_kernel<128, bf16_t>), grid, block, 0, s, p);
-    else hipLaunchKernelGGL((attn_part_kernel<128, _Float16>), grid, block, 0, s, p);
+    if (qdtype == DT_F32) { KCH_DATT(128, float) }
+    else if (qdtype == DT_BF16) { KCH_DATT(128, bf16_t) }
+    else { KCH_DATT(128, _Float16) }
   } else {
-    if (qdtype == DT_F32) hipLaunchKernelGGL((attn_part_kernel<64, float>), grid, block, 0, s, p);
-    else if (qdtype == DT_BF16) hipLaunchKernelGGL((attn_part_kernel<64, bf16_t>), grid, block, 0, s, p);
-    else hipLaunchKernelGGL((attn_part_kernel<64, _Float16>), grid, block, 0, s, p);
+    if (qdtype == DT_F32) { KCH_DATT(64, float) }
+    else if (qdtype == DT_BF16) { KCH_DATT(64, bf16_t) }
+    else { KCH_DATT(64, _Float16) }
   }
+#undef KCH_DATT
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  if (e != hipSuccess || p.ngrp == 1) return e;
   const long long outs = (long long)p.B * p.nh * (p.hd / 8);
   const dim3 g2((unsigned)((outs + 255) / 256));
-  if (odtype == DT_F32) hipLaunchKernelGGL((attn_combine_kernel<float>), g2, block, 0, s, p);
-  else if (odtype == DT_BF16) hipLaunchKernelGGL((attn_combine_kernel<bf16_t>), g2, block, 0, s, p);
-  else hipLaunchKernelGGL((attn_combine_kernel<_Float16>), g2, block, 0, s, p);
+#define KCH_DCMB(HD)                                                                           \
+  if (odtype == DT_F32) hipLaunchKernelGGL((attn_combine_kernel<HD, float>), g2, block, 0, s, p); \
+  else if (odtype == DT_BF16) hipLaunchKernelGGL((attn_combine_kernel<HD, bf16_t>), g2, block, 0, s, p); \
+  else hipLaunchKernelGGL((attn_combine_kernel<HD, _Float16>), g2, block, 0, s, p);
+  if (p.hd == 128) { KCH_DCMB(128) } else { KCH_DCMB(64) }
+#undef KCH_DCMB
   return hipGetLastError();
 }
 

@@ -77,8 +77,9 @@ hipError_t decode_idx_dispatch(const DecodeIdxParams& p, int qdtype, int kdtype,
 
 // Decode-step joint-softmax MQA, split over the attended rows (decode.hip).
 // Rows of sequence b: j < na -> compressed block idx[b][j] (or j without idx;
-// -1 = unused), then the ring_len rows of the ring. Split sp covers rows
-// [sp * rows_per_split, ...) and leaves M, L and the unnormalised o per head.
+// -1 = unused), then the ring_len rows of the ring. Group g (a workgroup)
+// covers rows [g * rows_per_group, ...); with several groups per sequence
+// each leaves M, L and the unnormalised o per head for the combine kernel.
 struct DecodeAttnParams {
   const void* q;           // [B, nh, hd]
   const bf16_t* kv;        // [B, *, hd] key/value rows, batch stride kv_bstride
@@ -86,10 +87,10 @@ struct DecodeAttnParams {
   const bf16_t* ring;      // [B, *, hd] window rows, batch stride ring_bstride
   const float* sink;       // [nh] or null
   void* out;               // [B, nh, hd]
-  float* part_o;           // [B, nsplit, nh, hd]
-  float* part_ml;          // [B, nsplit, nh, 2]
+  float* part_o;           // [B, ngrp, nh, hd]  partials of the row groups (ngrp > 1)
+  float* part_ml;          // [B, ngrp, nh, 2]
   long long kv_bstride, ring_bstride;
-  int B, nb, nh, hd, na, ring_len, nsplit, rows_per_split, normalize_q;
+  int B, nb, nh, hd, na, ring_len, ngrp, rows_per_group, normalize_q;
   float scale;
 };
 hipError_t decode_attn_dispatch(const DecodeAttnParams& p, int qdtype, int odtype, hipStream_t s);
