@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define KCH_ABI_VERSION 5
+#define KCH_ABI_VERSION 6
 
 #define KCH_OK 0
 #define KCH_ERR_INVALID 1     /* bad pointer / shape / argument */
@@ -258,6 +258,15 @@ int kch_short_conv(const void* x, const void* lookback, const void* weight, cons
 int kch_kda_gates(const void* proj, long long ld_proj, const void* gl, long long ld_gl, void* q,
                   void* k, void* v, void* g, void* beta, int B, int T, int H, int HV, int K, int V,
                   float decay_scale, int dtype, void* stream);
+
+/*
+ * LayerNorm computed in fp32 and returned in the input dtype (_Fp32LayerNorm,
+ * ops_fused.py:42-60: F.layer_norm(x.float(), w.float(), b.float()).to(dtype)):
+ *   out[r] = (x[r] - mean) / sqrt(var + eps) * w + b   (mean, biased var over d)
+ * x, out [rows, d] contiguous, of dtype; w, b [d] of wdtype (b may be NULL).
+ */
+int kch_layer_norm(const void* x, const void* w, const void* b, void* out, int rows, int d,
+                   float eps, int dtype, int wdtype, void* stream);
 
 #ifdef __cplusplus
 }

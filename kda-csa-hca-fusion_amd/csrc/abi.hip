@@ -377,6 +377,18 @@ int kch_kda_gates(const void* proj, long long ld_proj, const void* gl, long long
   return hip_status(fn, kch::kda_gates_dispatch(p, dtype, (hipStream_t)stream));
 }
 
+int kch_layer_norm(const void* x, const void* w, const void* b, void* out, int rows, int d,
+                   float eps, int dtype, int wdtype, void* stream) {
+  const char* fn = "kch_layer_norm";
+  if (!dtype_ok(dtype) || !dtype_ok(wdtype))
+    return fail(KCH_ERR_INVALID, "%s: unknown dtype %d / %d", fn, dtype, wdtype);
+  if (rows < 0 || d < 1) return fail(KCH_ERR_INVALID, "%s: bad sizes", fn);
+  if (rows == 0) return KCH_OK;
+  if (!x || !w || !out) return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
+  kch::LayerNormParams p{x, w, b, out, rows, d, eps};
+  return hip_status(fn, kch::layer_norm_dispatch(p, dtype, wdtype, (hipStream_t)stream));
+}
+
 }  // extern "C"
 
 namespace {

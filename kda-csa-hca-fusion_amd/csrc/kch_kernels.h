@@ -65,4 +65,15 @@ struct KdaGatesParams {
 };
 hipError_t kda_gates_dispatch(const KdaGatesParams& p, int dtype, hipStream_t stream);
 
+// fp32 LayerNorm of rows of d elements (kda_frontend.hip).
+struct LayerNormParams {
+  const void* x;
+  const void* w;
+  const void* b;  // may be null
+  void* out;
+  int rows, d;
+  float eps;
+};
+hipError_t layer_norm_dispatch(const LayerNormParams& p, int dtype, int wdtype, hipStream_t stream);
+
 }  // namespace kch

@@ -98,9 +98,13 @@ __device__ __forceinline__ float sigmoid_f(float x) { return 1.f / (1.f + __expf
 // torch's softplus (beta 1, threshold 20): x above the threshold, else log1p(e^x)
 __device__ __forceinline__ float softplus_f(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
 
-// One workgroup per token row: waves take the 2H q/k head vectors (silu, then
-// per-head L2 normalisation), then all threads take v (silu), g
-// (-softplus * decay) and beta (sigmoid).
+// Workgroup (row, y) for token row `row`: y < QK_UNITS(H) -> waves take q/k
+// head vectors 4y .. 4y + 3 of the 2H (silu, then per-head L2
+// normalisation); higher y -> a 1024-element slice of v (silu), g (-softplus *
+// decay) and beta (sigmoid). Spreading a row over several workgroups keeps a
+// decode step (one row per sequence) from running on a couple of CUs.
+__host__ __device__ inline int gates_qk_units(int H) { return (2 * H + 3) / 4; }
+
 template <typename T>
 __global__ __launch_bounds__(256) void kda_gates_kernel(KdaGatesParams p) {
   const long long row = blockIdx.x;
@@ -108,7 +112,10 @@ __global__ __launch_bounds__(256) void kda_gates_kernel(KdaGatesParams p) {
   const T* gr = static_cast<const T*>(p.gl) + row * p.ld_gl;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int HK = p.H * p.K;
-  for (int h = wave; h < 2 * p.H; h += 4) {
+  const int qku = gates_qk_units(p.H);
+  if ((int)blockIdx.y < qku) {
+    const int h = 4 * blockIdx.y + wave;
+    if (h >= 2 * p.H) return;
     const T* src = pr + (size_t)h * p.K;
     float vals[4];
     float ss = 0.f;
@@ -126,16 +133,86 @@ __global__ __launch_bounds__(256) void kda_gates_kernel(KdaGatesParams p) {
       const int e = lane + 64 * j;
       if (e < p.K) dst[e] = from_f32<T>(vals[j] * inv);
     }
+    return;
   }
   const int nv = p.HV * p.V, ng = p.HV * p.K;
+  const int i0 = ((int)blockIdx.y - qku) * 1024;
   T* v = static_cast<T*>(p.v) + row * nv;
-  for (int i = threadIdx.x; i < nv; i += 256) v[i] = from_f32<T>(silu_f(to_f32(pr[2 * HK + i])));
   T* g = static_cast<T*>(p.g) + row * ng;
-  for (int i = threadIdx.x; i < ng; i += 256)
+  for (int i = i0 + threadIdx.x; i < min(nv, i0 + 1024); i += 256)
+    v[i] = from_f32<T>(silu_f(to_f32(pr[2 * HK + i])));
+  for (int i = i0 + threadIdx.x; i < min(ng, i0 + 1024); i += 256)
     g[i] = from_f32<T>(-softplus_f(to_f32(gr[i])) * p.decay_scale);
-  T* beta = static_cast<T*>(p.beta) + row * p.HV;
-  for (int i = threadIdx.x; i < p.HV; i += 256)
-    beta[i] = from_f32<T>(sigmoid_f(to_f32(pr[2 * HK + nv + i])));
+  if (i0 == 0) {
+    T* beta = static_cast<T*>(p.beta) + row * p.HV;
+    for (int i = threadIdx.x; i < p.HV; i += 256)
+      beta[i] = from_f32<T>(sigmoid_f(to_f32(pr[2 * HK + nv + i])));
+  }
+}
+
+// One workgroup per row: the row's values stay in registers (d <= 4096), the
+// mean and the biased variance come from two block reductions in fp32, then
+// (x - mean) * rstd * w + b is rounded once to the output dtype.
+template <typename T, typename WT>
+__global__ __launch_bounds__(256) void layer_norm_kernel(LayerNormParams p) {
+  constexpr int MAXV = 16;
+  __shared__ float red[8];
+  const long long row = blockIdx.x;
+  const T* x = static_cast<const T*>(p.x) + row * p.d;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float v[MAXV];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) {
+    const int e = tid + 256 * i;
+    v[i] = e < p.d ? to_f32(x[e]) : 0.f;
+    s += v[i];
+  }
+  for (int e = tid + 256 * MAXV; e < p.d; e += 256) s += to_f32(x[e]);
+  s = wave_sum(s);
+  if (lane == 0) red[wave] = s;
+  __syncthreads();
+  const float mean = (red[0] + red[1] + red[2] + red[3]) / (float)p.d;
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) {
+    const int e = tid + 256 * i;
+    const float dv = v[i] - mean;
+    ss += e < p.d ? dv * dv : 0.f;
+  }
+  for (int e = tid + 256 * MAXV; e < p.d; e += 256) {
+    const float dv = to_f32(x[e]) - mean;
+    ss += dv * dv;
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) red[4 + wave] = ss;
+  __syncthreads();
+  const float var = (red[4] + red[5] + red[6] + red[7]) / (float)p.d;
+  const float rstd = 1.f / sqrtf(var + p.eps);
+  const WT* w = static_cast<const WT*>(p.w);
+  const WT* bb = static_cast<const WT*>(p.b);
+  T* out = static_cast<T*>(p.out) + row * p.d;
+#pragma unroll
+  for (int i = 0; i < MAXV; ++i) {
+    const int e = tid + 256 * i;
+    if (e < p.d) {
+      const float y = (v[i] - mean) * rstd * to_f32(w[e]) + (bb ? to_f32(bb[e]) : 0.f);
+      out[e] = from_f32<T>(y);
+    }
+  }
+  for (int e = tid + 256 * MAXV; e < p.d; e += 256) {
+    const float y = (to_f32(x[e]) - mean) * rstd * to_f32(w[e]) + (bb ? to_f32(bb[e]) : 0.f);
+    out[e] = from_f32<T>(y);
+  }
+}
+
+template <typename T>
+hipError_t layer_norm_launch(const LayerNormParams& p, int wdtype, hipStream_t s) {
+  const dim3 grid((unsigned)p.rows), block(256);
+  if (wdtype == DT_F32) hipLaunchKernelGGL((layer_norm_kernel<T, float>), grid, block, 0, s, p);
+  else if (wdtype == DT_BF16) hipLaunchKernelGGL((layer_norm_kernel<T, bf16_t>), grid, block, 0, s, p);
+  else hipLaunchKernelGGL((layer_norm_kernel<T, _Float16>), grid, block, 0, s, p);
+  return hipGetLastError();
 }
 
 template <typename T>
@@ -161,7 +238,8 @@ hipError_t short_conv_dispatch(const ShortConvParams& p, int dtype, hipStream_t 
 }
 
 hipError_t kda_gates_dispatch(const KdaGatesParams& p, int dtype, hipStream_t s) {
-  const dim3 grid((unsigned)((long long)p.B * p.T)), block(256);
+  const int slices = (max(p.HV * p.V, p.HV * p.K) + 1023) / 1024;
+  const dim3 grid((unsigned)((long long)p.B * p.T), (unsigned)(gates_qk_units(p.H) + max(slices, 1))), block(256);
   if (dtype == DT_F32)
     hipLaunchKernelGGL((kda_gates_kernel<float>), grid, block, 0, s, p);
   else if (dtype == DT_BF16)
@@ -169,6 +247,12 @@ hipError_t kda_gates_dispatch(const KdaGatesParams& p, int dtype, hipStream_t s)
   else
     hipLaunchKernelGGL((kda_gates_kernel<_Float16>), grid, block, 0, s, p);
   return hipGetLastError();
+}
+
+hipError_t layer_norm_dispatch(const LayerNormParams& p, int dtype, int wdtype, hipStream_t s) {
+  if (dtype == DT_F32) return layer_norm_launch<float>(p, wdtype, s);
+  if (dtype == DT_BF16) return layer_norm_launch<bf16_t>(p, wdtype, s);
+  return layer_norm_launch<_Float16>(p, wdtype, s);
 }
 
 }  // namespace kch

@@ -78,9 +78,13 @@ class SlidingWindowRingBuffer:
         if T_new == 0:
             return
         keep = min(T_new, self.win)
-        first = self._written + T_new - keep
-        pos = torch.arange(first, first + keep, device=self._buf.device) % self.win
-        self._buf.index_copy_(1, pos, x[:, T_new - keep:])
+        first = (self._written + T_new - keep) % self.win
+        src = x[:, T_new - keep:]
+        # ring positions first, first + 1, ... (mod win): at most two runs
+        n1 = min(keep, self.win - first)
+        self._buf[:, first:first + n1] = src[:, :n1]
+        if keep > n1:
+            self._buf[:, :keep - n1] = src[:, n1:]
         self._written += T_new
 
     @property
@@ -341,8 +345,12 @@ class CSADecodingCache:
         return out_idx
 
     def forward_step(self, q, q_idx, w_idx, *, topk, nh, nIh, scale=None, sink_logits=None,
-                     use_ste=True, ste_mode='topk_columns', normalize_qk=True):
-        """CSA output ``[B, 1, nh, c]`` (fp32) for the last appended token."""
+                     use_ste=True, ste_mode='topk_columns', normalize_qk=True,
+                     _normalize_q=False, _out_dtype=None):
+        """CSA output ``[B, 1, nh, c]`` (fp32) for the last appended token.
+
+        ``_normalize_q`` (internal): L2-normalise ``q`` in the kernel (the
+        caller passes the raw projection); ``_out_dtype``: output dtype."""
         B, T_new = q.shape[0], q.shape[1]
         if T_new != 1:
             raise ValueError(
@@ -369,11 +377,12 @@ class CSADecodingCache:
         core_scale = (1.0 if normalize_qk else self.c ** -0.5) if scale is None else scale
         nb = self._n_blocks
         n_win = self._sw.n_valid if self._sw is not None else 0
-        out = torch.zeros(B, 1, nh, self.c, device=q.device, dtype=torch.float32)
+        odt = torch.float32 if _out_dtype is None else _out_dtype
         if nb == 0 and n_win == 0:
-            return out
+            return torch.zeros(B, 1, nh, self.c, device=q.device, dtype=odt)
         if q.dtype == torch.float64:
             raise NotImplementedError("float64 queries are not supported by the HIP kernels")
+        out = torch.empty(B, 1, nh, self.c, device=q.device, dtype=odt)
         with torch.no_grad():
             kv = self._C.keys_for(nb, normalize_qk) if nb else None
             krows = self._K.rows if nb else None
@@ -396,8 +405,9 @@ class CSADecodingCache:
                       _lib.ptr(kinv), cap_k, _lib.ptr(ring), self.win * self.c, n_win,
                       _lib.ptr(sink), _lib.ptr(out), _lib.ptr(idx) if topk else None, B, nb, nh,
                       self.c, nIh, self.c_I, topk, float(core_scale),
-                      1.0 if normalize_qk else self.c_I ** -0.5, 0, int(normalize_qk),
-                      _lib.dtype_code(fn, q.dtype), _lib.dtype_code(fn, self.dtype), 0,
+                      1.0 if normalize_qk else self.c_I ** -0.5, int(_normalize_q),
+                      int(normalize_qk), _lib.dtype_code(fn, q.dtype),
+                      _lib.dtype_code(fn, self.dtype), _lib.dtype_code(fn, odt),
                       _lib.ptr(ws), nbytes, _lib.stream_of(q))
         return out
 
@@ -509,8 +519,12 @@ class HCADecodingCache:
             self._n_tokens_seen += T_new
         return out_idx
 
-    def forward_step(self, q, *, nh, scale=None, sink_logits=None, normalize_qk=True):
-        """HCA output ``[B, 1, nh, c]`` (fp32) for the last appended token."""
+    def forward_step(self, q, *, nh, scale=None, sink_logits=None, normalize_qk=True,
+                     _normalize_q=False, _out_dtype=None):
+        """HCA output ``[B, 1, nh, c]`` (fp32) for the last appended token.
+
+        ``_normalize_q`` (internal): L2-normalise ``q`` in the kernel (the
+        caller passes the raw projection); ``_out_dtype``: output dtype."""
         B, T_new = q.shape[0], q.shape[1]
         if T_new != 1:
             raise ValueError(f"HCADecodingCache.forward_step: T_new={T_new} must be 1.")
@@ -528,11 +542,12 @@ class HCADecodingCache:
         core_scale = (1.0 if normalize_qk else self.c ** -0.5) if scale is None else scale
         nb = self._n_blocks
         n_win = self._sw.n_valid if self._sw is not None else 0
-        out = torch.zeros(B, 1, nh, self.c, device=q.device, dtype=torch.float32)
+        odt = torch.float32 if _out_dtype is None else _out_dtype
         if nb == 0 and n_win == 0:
-            return out
+            return torch.zeros(B, 1, nh, self.c, device=q.device, dtype=odt)
         if q.dtype == torch.float64:
             raise NotImplementedError("float64 queries are not supported by the HIP kernels")
+        out = torch.empty(B, 1, nh, self.c, device=q.device, dtype=odt)
         with torch.no_grad():
             kv = self._C.keys_for(nb, normalize_qk) if nb else None
             ring = _ring_bf16(self._sw) if n_win else None
@@ -543,8 +558,9 @@ class HCADecodingCache:
             ws = torch.empty(max(nbytes, 1), device=q.device, dtype=torch.uint8)
             _lib.call("kch_hca_decode", _lib.ptr(qc), _lib.ptr(kv), cap * self.c,
                       _lib.ptr(ring), self.win * self.c, n_win, _lib.ptr(sink), _lib.ptr(out), B,
-                      nb, nh, self.c, float(core_scale), 0,
-                      _lib.dtype_code("HCADecodingCache.forward_step", q.dtype), 0,
+                      nb, nh, self.c, float(core_scale), int(_normalize_q),
+                      _lib.dtype_code("HCADecodingCache.forward_step", q.dtype),
+                      _lib.dtype_code("HCADecodingCache.forward_step", odt),
                       _lib.ptr(ws), nbytes, _lib.stream_of(q))
         return out
 

@@ -38,6 +38,7 @@ from . import _lib
 from .decoding_cache import CSADecodingCache, HCADecodingCache
 from .ops_csa import naive_csa
 from .ops_hca import naive_hca
+from .ops_kda import kda_recurrent_into
 from .ops_kda_backend import kda_forward, validate_kda_backend
 
 logger = logging.getLogger(__name__)
@@ -46,14 +47,26 @@ _CONV_K = 3  # short-conv kernel size (ops_fused.py:333)
 
 
 class _Fp32LayerNorm(nn.LayerNorm):
-    """LayerNorm computed in fp32, returned in the input dtype (``ops_fused.py:42-60``)."""
+    """LayerNorm computed in fp32, returned in the input dtype (``ops_fused.py:42-60``),
+    as one kernel (``kch_layer_norm``)."""
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if x.dtype in (torch.float16, torch.bfloat16):
-            out = F.layer_norm(x.float(), self.normalized_shape, self.weight.float(),
-                               self.bias.float(), self.eps)
-            return out.to(x.dtype)
-        return super().forward(x)
+        if x.numel() == 0:
+            return torch.empty_like(x)
+        _lib.require_gpu("_Fp32LayerNorm", x)
+        d = self.normalized_shape[-1]
+        if len(self.normalized_shape) != 1 or x.shape[-1] != d or self.weight is None:
+            raise ValueError("_Fp32LayerNorm: expects an affine LayerNorm over the last dim")
+        xc = x.contiguous()
+        out = torch.empty_like(xc)
+        fn = "_Fp32LayerNorm"
+        w = self.weight.detach()
+        b = None if self.bias is None else self.bias.detach().to(w.dtype).contiguous()
+        _lib.call("kch_layer_norm", _lib.ptr(xc), _lib.ptr(w.contiguous()), _lib.ptr(b),
+                  _lib.ptr(out), xc.numel() // d, d, float(self.eps),
+                  _lib.dtype_code(fn, xc.dtype), _lib.dtype_code(fn, w.dtype),
+                  _lib.stream_of(xc))
+        return out
 
 
 def _is_int(v) -> bool:
@@ -213,14 +226,20 @@ class KDAHybridLayer(nn.Module):
         # K^-0.5 rounded to the buffer's dtype, computed on the host (no device sync)
         return float(torch.tensor(self.cfg.head_dim_k ** -0.5).to(self.scale.dtype))
 
-    def forward(self, x: torch.Tensor, state: torch.Tensor | None = None):
-        """Stateful forward: reads and writes ``self._conv_lookback`` (``ops_fused.py:365-389``)."""
-        o, new_state, new_lookback = self.forward_functional(x, state, self._conv_lookback)
+    def forward(self, x: torch.Tensor, state: torch.Tensor | None = None, *,
+                state_out: torch.Tensor | None = None):
+        """Stateful forward: reads and writes ``self._conv_lookback`` (``ops_fused.py:365-389``).
+
+        ``state_out`` (fp32 ``[B,HV,K,V]``, contiguous; may be ``state`` itself)
+        receives the final state in place of a new tensor."""
+        o, new_state, new_lookback = self.forward_functional(x, state, self._conv_lookback,
+                                                             state_out=state_out)
         self._conv_lookback = new_lookback
         return o, new_state
 
     def forward_functional(self, x: torch.Tensor, state: torch.Tensor | None,
-                           conv_lookback: torch.Tensor | None, *, detach_lookback: bool = True):
+                           conv_lookback: torch.Tensor | None, *, detach_lookback: bool = True,
+                           state_out: torch.Tensor | None = None):
         """Side-effect-free forward (``ops_fused.py:391-609``).
 
         Returns ``(output [B,T,d], new_state [B,HV,K,V] fp32, new_lookback [B,2,d] | None)``.
@@ -257,7 +276,7 @@ class KDAHybridLayer(nn.Module):
             if T >= _CONV_K - 1:
                 new_lookback = x[:, -(_CONV_K - 1):].clone()
             elif lookback is not None:
-                new_lookback = torch.cat([lookback, x], dim=1)[:, -(_CONV_K - 1):].clone()
+                new_lookback = torch.cat([lookback[:, T:], x], dim=1)  # the last K - 1 rows
             else:
                 new_lookback = torch.cat([x.new_zeros(B, _CONV_K - 1 - T, d), x], dim=1)
             code = _lib.dtype_code("KDAHybridLayer", x.dtype)
@@ -282,10 +301,19 @@ class KDAHybridLayer(nn.Module):
                       _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(beta),
                       B, T, H, HV, K, V, float(cfg.kda_decay_scale), code, stream)
             use_chunk = cfg.kda_chunk_size >= 1 and T >= cfg.kda_chunk_size
-            o, new_state = kda_forward(
-                q, k, v, g, beta, scale=self._scale_value(), initial_state=state,
-                output_final_state=True, chunk_size=max(cfg.kda_chunk_size, 1),
-                use_chunk=use_chunk, backend=cfg.kda_backend)
+            if state_out is not None and not use_chunk:
+                # the recurrent kernel reads and writes each state element in the
+                # same thread, so the state may be updated in place
+                o = kda_recurrent_into(q, k, v, g, beta, self._scale_value(), state, state_out)
+                new_state = state_out
+            else:
+                o, new_state = kda_forward(
+                    q, k, v, g, beta, scale=self._scale_value(), initial_state=state,
+                    output_final_state=True, chunk_size=max(cfg.kda_chunk_size, 1),
+                    use_chunk=use_chunk, backend=cfg.kda_backend)
+                if state_out is not None:
+                    state_out.copy_(new_state)
+                    new_state = state_out
             out = self.o_proj(o.reshape(B, T, HV * V))
         return out, new_state, new_lookback
 
@@ -598,11 +626,12 @@ class HybridDecoding(nn.Module):
         else:
             Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx = self._project_csa(layer, h)
             cache.append_step(Ca, Cb, Za, Zb, K_idx, Z_idx, layer.Ba, layer.Bb, layer.B_idx)
-            q_n = F.normalize(q.float(), dim=-1)
-            o = cache.forward_step(q_n, q_idx, w_idx, topk=cfg.csa_topk, nh=cfg.csa_nh,
+            # q is L2-normalised in the kernel (F.normalize(q.float()) of the reference)
+            o = cache.forward_step(q, q_idx, w_idx, topk=cfg.csa_topk, nh=cfg.csa_nh,
                                    nIh=cfg.csa_nIh, scale=1.0, sink_logits=layer.sink,
-                                   use_ste=False, normalize_qk=True)
-            o_core = o.reshape(B, T_new, cfg.csa_nh * cfg.csa_c).to(h.dtype)
+                                   use_ste=False, normalize_qk=True, _normalize_q=True,
+                                   _out_dtype=h.dtype)
+            o_core = o.reshape(B, T_new, cfg.csa_nh * cfg.csa_c)
         return layer.o_proj(o_core)
 
     def _forward_hca_layer(self, layer: HCAHybridLayer, h: torch.Tensor, idx: int):
@@ -621,26 +650,33 @@ class HybridDecoding(nn.Module):
         else:
             C, Z, q = self._project_hca(layer, h)
             cache.append_step(C, Z, layer.B_pos)
-            q_n = F.normalize(q.float(), dim=-1)
-            o = cache.forward_step(q_n, nh=cfg.hca_nh, scale=1.0, sink_logits=layer.sink)
-            o_core = o.reshape(B, T_new, cfg.hca_nh * cfg.hca_c).to(h.dtype)
+            # q is L2-normalised in the kernel (F.normalize(q.float()) of the reference)
+            o = cache.forward_step(q, nh=cfg.hca_nh, scale=1.0, sink_logits=layer.sink,
+                                   _normalize_q=True, _out_dtype=h.dtype)
+            o_core = o.reshape(B, T_new, cfg.hca_nh * cfg.hca_c)
         return layer.o_proj(o_core)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         B = x.shape[0]
         model = self.model
         stacked = model._kda_state
-        if stacked is not None and stacked.shape[1] == B:
-            states = list(stacked.unbind(0))
-        else:
-            states = [None] * model.n_kda_layers
+        fresh = stacked is None or stacked.shape[1] != B
+        if not fresh and (stacked.dtype != torch.float32 or stacked.device != x.device
+                          or not stacked.is_contiguous()):
+            stacked = stacked.to(device=x.device, dtype=torch.float32).contiguous()
+        if model.n_kda_layers > 0 and fresh:
+            cfg = model.cfg
+            # one persistent [L, B, HV, K, V] fp32 state, updated in place by the layers
+            stacked = torch.zeros(model.n_kda_layers, B, cfg.n_heads_v, cfg.head_dim_k,
+                                  cfg.head_dim_v, device=x.device, dtype=torch.float32)
         kda_idx = csa_idx = hca_idx = 0
         with torch.no_grad():
             for layer, norm, kind in zip(model.layers, model.norms, model.layout):
                 residual = x
                 h = norm(x)
                 if kind == 'kda':
-                    o, states[kda_idx] = layer(h, states[kda_idx])
+                    st = stacked[kda_idx]
+                    o, _ = layer(h, None if fresh else st, state_out=st)
                     kda_idx += 1
                 elif kind == 'csa':
                     o = self._forward_csa_layer(layer, h, csa_idx)
@@ -649,7 +685,7 @@ class HybridDecoding(nn.Module):
                     o = self._forward_hca_layer(layer, h, hca_idx)
                     hca_idx += 1
                 x = residual + o
-            model._kda_state = torch.stack(states, 0) if model.n_kda_layers > 0 else None
+            model._kda_state = stacked if model.n_kda_layers > 0 else None
         return x
 
 

@@ -151,5 +151,37 @@ def naive_recurrent_kda(q, k, v, g, beta, scale=None, initial_state=None,
                 initial_state, output_final_state, g_clamp_min, state_dtype)
 
 
+def kda_recurrent_into(q, k, v, g, beta, scale, state, state_out):
+    """One recurrent pass with the final state written to ``state_out`` (fp32
+    ``[B,HV,K,V]``, contiguous, 16-byte aligned), which may be ``state``
+    itself (or ``state`` None: zero initial state); returns ``o``."""
+    fn = "kda_recurrent_into"
+    _validate_kda_inputs(q, k, v, g, beta, fn)
+    _validate_kda_shapes(q, k, v, g, beta, fn)
+    _lib.require_gpu(fn, q, state, state_out)
+    B, T, H, K = q.shape
+    HV, V = v.shape[2], v.shape[-1]
+    if (state_out.dtype != torch.float32 or tuple(state_out.shape) != (B, HV, K, V)
+            or not state_out.is_contiguous()):
+        raise ValueError(f"{fn}: state_out must be a contiguous fp32 [{B}, {HV}, {K}, {V}] tensor")
+    code = _lib.dtype_code(fn, v.dtype)
+    q, k, v, g, beta = (_aligned(t.contiguous()) for t in (q, k, v, g, beta))
+    s0 = None
+    if state is not None:
+        s0 = state if state.data_ptr() == state_out.data_ptr() else \
+            state.to(device=q.device, dtype=torch.float32).contiguous()
+    o = torch.empty_like(v)
+    if T == 0 or B == 0:
+        if s0 is None:
+            state_out.zero_()
+        elif s0.data_ptr() != state_out.data_ptr():
+            state_out.copy_(s0)
+        return o
+    _lib.call("kch_kda_recurrent_fwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g),
+              _lib.ptr(beta), _lib.ptr(s0), _lib.ptr(o), _lib.ptr(state_out), B, T, H, HV, K, V,
+              _scale_value(scale, K), _clamp_value(-10.0), code, _lib.stream_of(q))
+    return o
+
+
 chunk_kda = naive_chunk_kda
 recurrent_kda = naive_recurrent_kda
