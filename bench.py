@@ -361,6 +361,8 @@ def main():
     ap.add_argument("--headline-only", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run three 1 GiB device-to-device copies (HBM counter scale)")
+    ap.add_argument("--only-extra", choices=["decode_bw", "hybrid_C4"],
+                    help="run just this extra workload and print its JSON (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (every box has one MI355X); "
@@ -369,8 +371,12 @@ def main():
 
     import kch
 
-    B, T, H, K, V = 8, 4096, 16, 128, 128
     dev = torch.device("cuda:0")
+    if args.only_extra:
+        fn = {"decode_bw": bench_decode_bw, "hybrid_C4": bench_hybrid}[args.only_extra]
+        print(json.dumps({args.only_extra: fn(dev)}))
+        return
+    B, T, H, K, V = 8, 4096, 16, 128, 128
     xs, s0, host, s0h = kda_inputs(B, T, H, K, V, dev=dev)
 
     def step():
