@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define KCH_ABI_VERSION 6
+#define KCH_ABI_VERSION 7
 
 #define KCH_OK 0
 #define KCH_ERR_INVALID 1     /* bad pointer / shape / argument */
@@ -121,8 +121,9 @@ int kch_compress_overlapped(const void* Ca, long long ldCa, const void* Cb, long
  * (ops_csa.py:330-573) in its forward (hard top-k) form.
  *   q_idx [B,T,nIh,cI] (dtype), k_idx [B,nb,cI] fp32 (already L2-normalised
  *   when normalize_q), w_idx [B,T,nIh] (dtype) or NULL (= all ones)
- *   idx_out [B,T,topk] int64 (idx64) or int32: blocks by descending logit,
- *   ties by ascending index, -1 for masked blocks and padding
+ *   idx_out [B,T,topk] int64 (idx64) or int32: the top-k blocks by descending
+ *   logit, ties by ascending index (sorted), or the same set in ascending
+ *   block index (sorted = 0); -1 for masked blocks and padding
  *   logits_out [B,T,nb] fp32 (masked = -inf) or NULL
  * Block n is visible to query t when n < (pos0 + t + 1) / m, or always when
  * dense_visible (decode). nIh in {1,2,4,8,16}; cI in {32,64,128}.
@@ -130,7 +131,7 @@ int kch_compress_overlapped(const void* Ca, long long ldCa, const void* Cb, long
 int kch_csa_indexer_topk(const void* q_idx, const float* k_idx, const void* w_idx, void* idx_out,
                          int idx64, float* logits_out, int B, int T, int nb, int nIh, int cI,
                          int topk, int m, int pos0, int dense_visible, int normalize_q, float scale,
-                         int dtype, void* stream);
+                         int sorted, int dtype, void* stream);
 
 /*
  * CSA core attention over the selected compressed blocks plus the sliding

@@ -209,7 +209,7 @@ int kch_compress_overlapped(const void* Ca, long long ldCa, const void* Cb, long
 int kch_csa_indexer_topk(const void* q_idx, const float* k_idx, const void* w_idx, void* idx_out,
                          int idx64, float* logits_out, int B, int T, int nb, int nIh, int cI,
                          int topk, int m, int pos0, int dense_visible, int normalize_q, float scale,
-                         int dtype, void* stream) {
+                         int sorted, int dtype, void* stream) {
   const char* fn = "kch_csa_indexer_topk";
   if (!dtype_ok(dtype)) return fail(KCH_ERR_INVALID, "%s: unknown dtype %d", fn, dtype);
   if (topk < 0) return fail(KCH_ERR_INVALID, "%s: topk=%d must be >= 0", fn, topk);
@@ -221,19 +221,17 @@ int kch_csa_indexer_topk(const void* q_idx, const float* k_idx, const void* w_id
     return fail(KCH_ERR_UNSUPPORTED, "%s: cI=%d not in {32,64,128}", fn, cI);
   if (B * T == 0 || topk == 0) return KCH_OK;
   if (!q_idx || !idx_out || (nb > 0 && !k_idx)) return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
-  int ptop = 1;
-  while (ptop < topk) ptop <<= 1;
-  const long long lds = (long long)(16 / nIh) * nb * 4 + (256 + 16) * 4 + (long long)ptop * 8;
+  const long long lds = (long long)kch::indexer_lds_bytes(nb, nIh, topk);
   if (lds > 160 * 1024)
     return fail(KCH_ERR_UNSUPPORTED, "%s: nb=%d with nIh=%d and topk=%d exceeds the LDS budget", fn,
                 nb, nIh, topk);
   if (nb == 0) {
-    // no block at all: every slot is -1
-    hipError_t e = hipMemsetAsync(idx_out, 0xff, (size_t)B * T * topk * (idx64 ? 8 : 4), (hipStream_t)stream);
-    return hip_status(fn, e);
+    // no block at all: every slot is -1 (a fill kernel: graph-capture safe)
+    const long long words = (long long)B * T * topk * (idx64 ? 2 : 1);
+    return hip_status(fn, kch::fill_u32(idx_out, words, 0xffffffffu, (hipStream_t)stream));
   }
   kch::IndexerParams p{q_idx, k_idx, w_idx, idx_out, logits_out, B, T, nb, nIh, cI, topk, m,
-                       pos0, normalize_q, idx64, dense_visible, scale, 0};
+                       pos0, normalize_q, idx64, dense_visible, sorted ? 1 : 0, scale, 0};
   return hip_status(fn, kch::indexer_dispatch(p, dtype, (hipStream_t)stream));
 }
 
@@ -309,13 +307,11 @@ int kch_csa_decode_step(const void* q, const void* q_idx, const void* w_idx, con
   const int use_sel = (topk > 0 && nb > 0);
   if (use_sel) {
     if (!q_idx || !k_idx || !kv_comp || !idx_ws) return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
-    int ptop = 1;
-    while (ptop < topk) ptop <<= 1;
-    const long long lds = (long long)(16 / nIh) * nb * 4 + (256 + 16) * 4 + (long long)ptop * 8;
+    const long long lds = (long long)kch::indexer_lds_bytes(nb, nIh, topk);
     if (lds > 160 * 1024)
       return fail(KCH_ERR_UNSUPPORTED, "%s: %d cached blocks exceed the indexer LDS budget", fn, nb);
     kch::IndexerParams ip{q_idx, k_idx, w_idx, idx_ws, nullptr, B, 1, nb, nIh, cI, topk, 1,
-                          0, normalize_qidx, 0, 1, idx_scale, k_bstride};
+                          0, normalize_qidx, 0, 1, 1, idx_scale, k_bstride};
     rc = hip_status(fn, kch::indexer_dispatch(ip, qdtype, s));
     if (rc) return rc;
   }

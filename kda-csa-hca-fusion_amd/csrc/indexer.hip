@@ -13,9 +13,9 @@
 // column n = (query n / nIh, head n % nIh). Scores use a split-bf16 product
 // (x = hi + lo, hi*hi + hi*lo + lo*hi with fp32 accumulation) so the logits
 // carry ~2^-16 relative error instead of bf16's 2^-8. Per query, the logits sit
-// in LDS; the k-th largest is found by a 4 x 8-bit radix select on
-// order-preserving 32-bit keys, the winners are gathered (ties at the threshold
-// in ascending index order) and bitonic-sorted by (logit desc, index asc).
+// in LDS; the top-k of the unique 64-bit (key, index) values is found by an
+// 8-bit radix select, gathered in index order and, when asked, bitonic-sorted
+// by (logit desc, index asc).
 
 #include "attn_common.h"
 #include "kch_csa.h"
@@ -41,6 +41,24 @@ __device__ __forceinline__ int wave_excl_scan(int v) {
     if (lane >= d) x += y;
   }
   return x - v;
+}
+
+typedef unsigned long long u64;
+
+// Unique ordered value of a logit key and its block index (larger key first,
+// then lower index).
+__device__ __forceinline__ u64 kv64(uint32_t key, int index) {
+  return ((u64)key << 32) | (uint32_t)(~(uint32_t)index);
+}
+
+__device__ __forceinline__ u64 shfl_xor64(u64 v, int d) {
+  const int lo = __shfl_xor((int)(uint32_t)v, d), hi = __shfl_xor((int)(uint32_t)(v >> 32), d);
+  return ((u64)(uint32_t)hi << 32) | (uint32_t)lo;
+}
+
+// Lanes below this one with their bit set in m.
+__device__ __forceinline__ int mbcnt64(unsigned long long m) {
+  return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
 __device__ __forceinline__ void split_bf16(const float* f, bf16x8& hi, bf16x8& lo) {
@@ -71,8 +89,7 @@ __global__ __launch_bounds__(64) void indexer_kernel(IndexerParams p) {
   const size_t lg_bytes = ((size_t)QPW * nb * 4 + 15) & ~(size_t)15;
   float* logits = reinterpret_cast<float*>(smem);                       // [QPW][nb]
   uint32_t* hist = reinterpret_cast<uint32_t*>(smem + lg_bytes);        // [256]
-  unsigned long long* sel = reinterpret_cast<unsigned long long*>(hist + 256 + 16);  // [ptop]
-  int* counters = reinterpret_cast<int*>(hist + 256);
+  u64* sel = reinterpret_cast<u64*>(hist + 256);                         // [ptop]
 
   auto nvis_of = [&](int t) {
     if (p.dense_visible) return nb;
@@ -143,6 +160,13 @@ __global__ __launch_bounds__(64) void indexer_kernel(IndexerParams p) {
   wave_lds_sync();
 
   // ---- per query: top-k ----
+  // Each logit becomes a unique 64-bit value (order-preserving key, then the
+  // complement of the block index), so "larger" is the reference's order with
+  // ties in ascending index and the selection needs no tie bookkeeping: an
+  // 8-bit radix select below the leading bits common to all values, stopped
+  // as soon as the boundary digit holds exactly the values still needed, then
+  // one gather in index order. Sorting (descending) only when asked.
+  constexpr int U = 8;  // LDS reads in flight per pass
   for (int j = 0; j < QPW; ++j) {
     const int t = t0 + j;
     if (t >= p.T) break;
@@ -153,92 +177,108 @@ __global__ __launch_bounds__(64) void indexer_kernel(IndexerParams p) {
       for (int i = lane; i < nb; i += 64)
         p.logits_out[((size_t)b * p.T + t) * nb + i] = i < nv ? lg[i] : -INFINITY;
     }
+    auto val = [&](int i) { return kv64(order_key(lg[i]), i); };
     const int cnt = nv < topk ? nv : topk;
-    if (cnt > 0) {
-      if (nv <= topk) {
-        for (int i = lane; i < nv; i += 64)
-          sel[i] = ((unsigned long long)order_key(lg[i]) << 32) | (uint32_t)(~i);
-      } else {
-        // radix select of the topk-th largest key
-        uint32_t prefix = 0, pmask = 0;
-        int need = topk, above_total = 0;
-        for (int pass = 0; pass < 4; ++pass) {
-          const int shift = 24 - 8 * pass;
-          for (int i = lane; i < 256; i += 64) hist[i] = 0;
-          wave_lds_sync();
-          for (int i = lane; i < nv; i += 64) {
-            const uint32_t u = order_key(lg[i]);
-            if ((u & pmask) == prefix) atomicAdd(&hist[(u >> shift) & 255u], 1u);
-          }
-          wave_lds_sync();
-          // bins in descending order: lane l holds 255-4l .. 252-4l
-          int c[4], tot = 0;
-#pragma unroll
-          for (int k = 0; k < 4; ++k) { c[k] = (int)hist[255 - 4 * lane - k]; tot += c[k]; }
-          int cum = wave_excl_scan(tot);
-          int found_bin = -1, found_above = 0;
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            if (found_bin < 0 && cum < need && cum + c[k] >= need) {
-              found_bin = 255 - 4 * lane - k;
-              found_above = cum;
-            }
-            cum += c[k];
-          }
-          const unsigned long long who = __ballot(found_bin >= 0);
-          const int src = __ffsll((long long)who) - 1;
-          const int bin = __shfl(found_bin, src);
-          const int above = __shfl(found_above, src);
-          prefix |= (uint32_t)bin << shift;
-          pmask |= 255u << shift;
-          need -= above;
-          above_total += above;
-        }
-        // gather: keys > threshold anywhere in [0, above_total), ties in index order
-        const uint32_t thr = prefix;
-        if (lane == 0) counters[0] = 0;
-        wave_lds_sync();
-        int ties = 0;
-        for (int base = 0; base < nv; base += 64) {
-          const int i = base + lane;
-          const uint32_t u = i < nv ? order_key(lg[i]) : 0u;
-          const bool gt = i < nv && u > thr;
-          const bool eq = i < nv && u == thr;
-          if (gt) {
-            const int slot = atomicAdd(&counters[0], 1);
-            sel[slot] = ((unsigned long long)u << 32) | (uint32_t)(~i);
-          }
-          const unsigned long long eqm = __ballot(eq);
-          if (eq) {
-            const int rank = ties + __popcll(eqm & ((1ull << lane) - 1ull));
-            if (rank < need) sel[above_total + rank] = ((unsigned long long)u << 32) | (uint32_t)(~i);
-          }
-          ties += __popcll(eqm);
-        }
+    u64 thr = 0ull, mask = 0ull;  // with mask = 0 every value is taken
+    if (nv > topk) {
+      u64 a = ~0ull, o = 0ull;
+      for (int i = lane; i < nv; i += 64) {
+        const u64 v = val(i);
+        a &= v;
+        o |= v;
       }
-      // pad to a power of two with keys that sort last
+#pragma unroll
+      for (int d = 32; d; d >>= 1) {
+        a &= shfl_xor64(a, d);
+        o |= shfl_xor64(o, d);
+      }
+      int lo_bit = 64 - __clzll((long long)(a ^ o));  // values differ: lo_bit >= 1
+      mask = lo_bit >= 64 ? 0ull : (~0ull << lo_bit);
+      thr = a & mask;
+      int need = topk;
+      while (lo_bit > 0) {
+        const int w = lo_bit < 8 ? lo_bit : 8;
+        const int shift = lo_bit - w;
+        const uint32_t dm = (1u << w) - 1u;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) hist[lane + 64 * k] = 0u;
+        // a wave's LDS operations complete in order: the clear precedes the adds
+        for (int i0 = 0; i0 < nv; i0 += 64 * U) {
+          u64 v[U];
+#pragma unroll
+          for (int u = 0; u < U; ++u) v[u] = val(min(i0 + 64 * u + lane, nv - 1));
+#pragma unroll
+          for (int u = 0; u < U; ++u)
+            if (i0 + 64 * u + lane < nv && (v[u] & mask) == thr)
+              atomicAdd(&hist[(uint32_t)(v[u] >> shift) & dm], 1u);
+        }
+        wave_lds_sync();
+        // digits in descending order: lane l holds dm - 4l .. dm - 4l - 3
+        int c[4], tot = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int bin = (int)dm - 4 * lane - k;
+          c[k] = bin >= 0 ? (int)hist[bin] : 0;
+          tot += c[k];
+        }
+        int cum = wave_excl_scan(tot);
+        int found_bin = -1, found_above = 0, found_cnt = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          if (found_bin < 0 && cum < need && cum + c[k] >= need) {
+            found_bin = (int)dm - 4 * lane - k;
+            found_above = cum;
+            found_cnt = c[k];
+          }
+          cum += c[k];
+        }
+        const unsigned long long who = __ballot(found_bin >= 0);
+        const int src = __ffsll((long long)who) - 1;
+        const int bin = __shfl(found_bin, src);
+        const int above = __shfl(found_above, src);
+        const int bcnt = __shfl(found_cnt, src);
+        wave_lds_sync();  // histogram reads done before the next pass clears it
+        thr |= (u64)bin << shift;
+        mask |= (u64)dm << shift;
+        need -= above;
+        lo_bit = shift;
+        if (bcnt == need) break;  // the boundary digit's values are all taken
+      }
+    }
+    // gather the cnt selected values in index order
+    int at = 0;
+    for (int i0 = 0; i0 < nv; i0 += 64) {
+      const int i = i0 + lane;
+      const u64 v = i < nv ? val(i) : 0ull;
+      const bool tk = i < nv && (v & mask) >= thr;
+      const unsigned long long tm = __ballot(tk);
+      if (tk) sel[at + mbcnt64(tm)] = v;
+      at += __popcll(tm);
+    }
+    if (p.sorted && cnt > 1) {
+      // pad to a power of two with values that sort last, bitonic sort descending
       int pw = 1;
       while (pw < cnt) pw <<= 1;
       for (int i = cnt + lane; i < pw; i += 64) sel[i] = 0ull;
       wave_lds_sync();
-      // bitonic sort, descending
       for (int k = 2; k <= pw; k <<= 1) {
         for (int jj = k >> 1; jj > 0; jj >>= 1) {
           for (int i = lane; i < pw / 2; i += 64) {
             const int lo = ((i & ~(jj - 1)) << 1) | (i & (jj - 1));
             const int hi = lo + jj;
-            const unsigned long long a = sel[lo], c2 = sel[hi];
+            const u64 x = sel[lo], y = sel[hi];
             const bool desc = (lo & k) == 0;
-            if (desc ? (a < c2) : (a > c2)) { sel[lo] = c2; sel[hi] = a; }
+            if (desc ? (x < y) : (x > y)) { sel[lo] = y; sel[hi] = x; }
           }
           wave_lds_sync();
         }
       }
+    } else {
+      wave_lds_sync();
     }
-    // write indices (-1 beyond the visible count)
+    // write indices (-1 beyond the selected count)
     for (int i = lane; i < topk; i += 64) {
-      int id = -1;
-      if (i < cnt) id = (int)(~(uint32_t)(sel[i] & 0xffffffffull));
+      const int id = i < cnt ? (int)(~(uint32_t)(sel[i] & 0xffffffffull)) : -1;
       if (p.idx64) static_cast<long long*>(p.idx_out)[orow + i] = id;
       else static_cast<int*>(p.idx_out)[orow + i] = id;
     }
@@ -246,11 +286,15 @@ __global__ __launch_bounds__(64) void indexer_kernel(IndexerParams p) {
   }
 }
 
+size_t indexer_lds_bytes(int nb, int nIh, int topk) {
+  int ptop = 1;
+  while (ptop < topk) ptop <<= 1;
+  return (((size_t)(16 / nIh) * nb * 4 + 15) & ~(size_t)15) + 256 * 4 + (size_t)ptop * 8;
+}
+
 hipError_t indexer_dispatch(const IndexerParams& p, int dtype, hipStream_t s) {
   const int QPW = 16 / p.nIh;
-  int ptop = 1;
-  while (ptop < p.topk) ptop <<= 1;
-  const size_t lds = (((size_t)QPW * p.nb * 4 + 15) & ~(size_t)15) + (256 + 16) * 4 + (size_t)ptop * 8;
+  const size_t lds = indexer_lds_bytes(p.nb, p.nIh, p.topk);
   const unsigned groups = (unsigned)(p.B * ((p.T + QPW - 1) / QPW));
 #define KCH_IDX_LAUNCH(QT, CI) \
   hipLaunchKernelGGL((indexer_kernel<QT, CI>), dim3(groups), dim3(64), lds, s, p)

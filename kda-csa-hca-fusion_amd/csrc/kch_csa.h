@@ -49,10 +49,12 @@ struct IndexerParams {
   int B, T, nb, nIh, cI, topk, m;
   int q_pos0;            // position of query 0 (decode: the cache's token index)
   int normalize_q, idx64, dense_visible;  // dense_visible: every block visible
+  int sorted;            // 1: indices by descending logit; 0: the same set in ascending index
   float scale;
   long long k_bstride;   // elements between batches of k_idx (0: nb * cI)
 };
 hipError_t indexer_dispatch(const IndexerParams& p, int dtype, hipStream_t s);
+size_t indexer_lds_bytes(int nb, int nIh, int topk);  // dynamic LDS of the indexer kernel
 
 // Decode-step indexer (decode.hip): one query per sequence over every cached block.
 struct DecodeIdxParams {

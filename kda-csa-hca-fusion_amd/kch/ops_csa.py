@@ -139,7 +139,7 @@ def _standard_block_mask_m(mask, T, n_blocks):
 
 
 def _indexer(fn, q_idx, k_norm, w_idx, topk, scale, m, *, dense, pos0=0, normalize_q,
-             idx64=True, want_logits=False):
+             idx64=True, want_logits=False, sorted_=True):
     B_, T, HI, DI = q_idx.shape
     nb = k_norm.shape[1]
     q_idx = _aligned(q_idx)
@@ -152,7 +152,7 @@ def _indexer(fn, q_idx, k_norm, w_idx, topk, scale, m, *, dense, pos0=0, normali
     _lib.call("kch_csa_indexer_topk", _lib.ptr(q_idx), _lib.ptr(k_norm), _lib.ptr(w_idx),
               _lib.ptr(idx), 1 if idx64 else 0, _lib.ptr(logits), B_, T, nb, HI, DI, topk,
               max(int(m), 1), pos0, int(dense), int(normalize_q), float(scale),
-              _lib.dtype_code(fn, q_idx.dtype), _lib.stream_of(q_idx))
+              int(sorted_), _lib.dtype_code(fn, q_idx.dtype), _lib.stream_of(q_idx))
     return idx, logits
 
 
@@ -245,8 +245,10 @@ def csa_core(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, *, m,
         scale = 1.0 if normalize_qk else c ** -0.5
     idx = None
     if topk > 0:
+        # the attention takes the selected set in any order: sort only for a caller
         idx, _ = _indexer(fn, q_idx, k_norm, w_idx, topk, 1.0 if normalize_qk else c_I ** -0.5,
-                          m, dense=False, normalize_q=normalize_qk, idx64=False)
+                          m, dense=False, normalize_q=normalize_qk, idx64=False,
+                          sorted_=bool(return_indices))
     sink = None if sink_logits is None else _f32(sink_logits, device)
     qc = _aligned(q)
     out = torch.empty(B_, T, nh, c, device=device, dtype=q.dtype)
