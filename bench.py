@@ -361,7 +361,7 @@ def main():
     ap.add_argument("--headline-only", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run three 1 GiB device-to-device copies (HBM counter scale)")
-    ap.add_argument("--only-extra", choices=["decode_bw", "hybrid_C4"],
+    ap.add_argument("--only-extra", choices=["decode_bw", "hybrid_C4", "csa_C2", "hca_C3"],
                     help="run just this extra workload and print its JSON (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -373,7 +373,9 @@ def main():
 
     dev = torch.device("cuda:0")
     if args.only_extra:
-        fn = {"decode_bw": bench_decode_bw, "hybrid_C4": bench_hybrid}[args.only_extra]
+        fn = {"decode_bw": bench_decode_bw, "hybrid_C4": bench_hybrid,
+              "csa_C2": lambda d: bench_csa(4, 8192, max(3, args.steps // 4), 1, d),
+              "hca_C3": lambda d: bench_hca(4, 32768, max(3, args.steps // 4), 1, d)}[args.only_extra]
         print(json.dumps({args.only_extra: fn(dev)}))
         return
     B, T, H, K, V = 8, 4096, 16, 128, 128

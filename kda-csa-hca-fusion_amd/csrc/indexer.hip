@@ -9,8 +9,9 @@
 // Tie rule on exactly-equal logits: ascending block index (the reference's
 // torch.topk order is unspecified there).
 //
-// Mapping: one wave per group of QPW = 16 / nIh consecutive queries; MFMA
-// column n = (query n / nIh, head n % nIh). Scores use a split-bf16 product
+// Mapping: one 4-wave workgroup per group of QPW = 16 / nIh consecutive
+// queries; MFMA column n = (query n / nIh, head n % nIh). The waves split the
+// logits by 16-block chunk, then take one query's selection each. Scores use a split-bf16 product
 // (x = hi + lo, hi*hi + hi*lo + lo*hi with fp32 accumulation) so the logits
 // carry ~2^-16 relative error instead of bf16's 2^-8. Per query, the logits sit
 // in LDS; the top-k of the unique 64-bit (key, index) values is found by an
@@ -73,12 +74,13 @@ __device__ __forceinline__ void split_bf16(const float* f, bf16x8& hi, bf16x8& l
 }  // namespace
 
 template <typename QT, int CI>
-__global__ __launch_bounds__(64) void indexer_kernel(IndexerParams p) {
+__global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   constexpr int NS = CI / 32;
   const int nIh = p.nIh;
   const int QPW = 16 / nIh;
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int q4 = lane >> 4, n = lane & 15;
   const int groups_per_row = (p.T + QPW - 1) / QPW;
   const int b = blockIdx.x / groups_per_row;
@@ -87,9 +89,12 @@ __global__ __launch_bounds__(64) void indexer_kernel(IndexerParams p) {
   const int topk = p.topk;
 
   const size_t lg_bytes = ((size_t)QPW * nb * 4 + 15) & ~(size_t)15;
-  float* logits = reinterpret_cast<float*>(smem);                       // [QPW][nb]
-  uint32_t* hist = reinterpret_cast<uint32_t*>(smem + lg_bytes);        // [256]
-  u64* sel = reinterpret_cast<u64*>(hist + 256);                         // [ptop]
+  int ptop = 1;
+  while (ptop < topk) ptop <<= 1;
+  float* logits = reinterpret_cast<float*>(smem);                                   // [QPW][nb]
+  uint32_t* hist = reinterpret_cast<uint32_t*>(smem + lg_bytes) + 256 * wave;        // [4][256]
+  u64* sel = reinterpret_cast<u64*>(reinterpret_cast<uint32_t*>(smem + lg_bytes) + 1024) +
+             (size_t)ptop * wave;                                                     // [4][ptop]
 
   auto nvis_of = [&](int t) {
     if (p.dense_visible) return nb;
@@ -133,33 +138,56 @@ __global__ __launch_bounds__(64) void indexer_kernel(IndexerParams p) {
     if (t0 + j < p.T) nv_max = max(nv_max, nvis_of(t0 + j));
   const int nv_me = qok ? nvis_of(tq) : 0;
   const float* kbase = p.k_idx + (size_t)b * (p.k_bstride ? p.k_bstride : (long long)nb * CI);
-  for (int c0 = 0; c0 < nv_max; c0 += 16) {
-    const int r = c0 + n;
-    const float* krow = kbase + (size_t)(r < nb ? r : nb - 1) * CI;
+  // key rows of chunk c (row 16c + n, clamped: past the end the last row is
+  // re-read and masked); wave w takes chunks w, w + 4, ..., D in flight;
+  // refills are unconditional so that no loaded register is copied
+  constexpr int D = 4;
+  const int nch = (nv_max + 15) / 16;
+  const int mine = nch > wave ? (nch - wave + 3) / 4 : 0;
+  auto load = [&](int c, float (&kf)[NS][8]) {
+    const int r = min(16 * c + n, nb - 1);
+    const float* krow = kbase + (size_t)r * CI + 8 * q4;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) Load8<float>::run(krow + 32 * s, kf[s]);
+  };
+  auto consume = [&](int c, const float (&kf)[NS][8]) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      float f[8];
-      Load8<float>::run(krow + 32 * s + 8 * q4, f);
       bf16x8 khi, klo;
-      split_bf16(f, khi, klo);
+      split_bf16(kf[s], khi, klo);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi, qhi[s], acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi, qlo[s], acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(klo, qhi[s], acc, 0, 0, 0);
     }
-    // acc[e]: block c0 + 4*q4 + e, column n
+    // acc[e]: block 16c + 4*q4 + e, column n
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       float v = fmaxf(acc[e] * p.scale, 0.f) * wq;
       // head sum over the nIh adjacent lanes of this query
-      for (int d = 1; d < nIh; d <<= 1) v += __shfl_xor(v, d);
-      const int blk = c0 + 4 * q4 + e;
+#pragma unroll
+      for (int d = 1; d < 16; d <<= 1)
+        if (d < nIh) v += __shfl_xor(v, d);
+      const int blk = 16 * c + 4 * q4 + e;
       if (hh == 0 && qok && blk < nv_me) logits[jq * nb + blk] = v;
     }
+  };
+  float kf[D][NS][8];
+#pragma unroll
+  for (int d = 0; d < D; ++d) load(wave + 4 * d, kf[d]);
+  // chunks past this wave's last are consumed too: their blocks lie beyond
+  // every query's visible count, so nothing is stored (a condition here would
+  // cost the loads' overlap)
+  for (int m0 = 0; m0 < mine; m0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      consume(wave + 4 * (m0 + d), kf[d]);
+      load(wave + 4 * (m0 + d + D), kf[d]);
+    }
   }
-  wave_lds_sync();
+  __syncthreads();
 
-  // ---- per query: top-k ----
+  // ---- per query: top-k (wave w takes queries w, w + 4, ...) ----
   // Each logit becomes a unique 64-bit value (order-preserving key, then the
   // complement of the block index), so "larger" is the reference's order with
   // ties in ascending index and the selection needs no tie bookkeeping: an
@@ -167,7 +195,7 @@ __global__ __launch_bounds__(64) void indexer_kernel(IndexerParams p) {
   // as soon as the boundary digit holds exactly the values still needed, then
   // one gather in index order. Sorting (descending) only when asked.
   constexpr int U = 8;  // LDS reads in flight per pass
-  for (int j = 0; j < QPW; ++j) {
+  for (int j = wave; j < QPW; j += 4) {
     const int t = t0 + j;
     if (t >= p.T) break;
     const int nv = nvis_of(t);
@@ -289,7 +317,7 @@ __global__ __launch_bounds__(64) void indexer_kernel(IndexerParams p) {
 size_t indexer_lds_bytes(int nb, int nIh, int topk) {
   int ptop = 1;
   while (ptop < topk) ptop <<= 1;
-  return (((size_t)(16 / nIh) * nb * 4 + 15) & ~(size_t)15) + 256 * 4 + (size_t)ptop * 8;
+  return (((size_t)(16 / nIh) * nb * 4 + 15) & ~(size_t)15) + 4 * 256 * 4 + 4 * (size_t)ptop * 8;
 }
 
 hipError_t indexer_dispatch(const IndexerParams& p, int dtype, hipStream_t s) {
@@ -297,7 +325,7 @@ hipError_t indexer_dispatch(const IndexerParams& p, int dtype, hipStream_t s) {
   const size_t lds = indexer_lds_bytes(p.nb, p.nIh, p.topk);
   const unsigned groups = (unsigned)(p.B * ((p.T + QPW - 1) / QPW));
 #define KCH_IDX_LAUNCH(QT, CI) \
-  hipLaunchKernelGGL((indexer_kernel<QT, CI>), dim3(groups), dim3(64), lds, s, p)
+  hipLaunchKernelGGL((indexer_kernel<QT, CI>), dim3(groups), dim3(256), lds, s, p)
   if (dtype == DT_BF16) {
     if (p.cI == 64) KCH_IDX_LAUNCH(bf16_t, 64);
     else if (p.cI == 128) KCH_IDX_LAUNCH(bf16_t, 128);
