@@ -122,7 +122,7 @@ template <int HD, typename QT, typename OT, bool SPARSE>
 __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnParams p) {
   using W = MqaWave<HD>;
   __shared__ __attribute__((aligned(16))) bf16_t stage_all[4][16 * W::LDS_LD];
-  const int wv = threadIdx.x >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
   const int n = lane & 15;
   bf16_t* stage = stage_all[wv];
@@ -136,49 +136,75 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(AttnParams p) {
   W w;
   w.template init<QT>(n < p.nh ? qrow : nullptr, p.normalize_q != 0, p.scale);
 
+  // The rows of this query: n_main compressed rows (the selected blocks, -1 =
+  // unused slot; or the causally visible blocks), then n_win window rows (the
+  // first local_count rows of a ring, or positions max(t - win + 1, 0) .. t).
   const bf16_t* kv = p.kv_comp + (size_t)b * (p.kv_bstride ? p.kv_bstride : (long long)p.nb * HD);
-  if (SPARSE) {
-    // selected compressed blocks; -1 marks an unused slot
-    const int* idx = p.idx + (size_t)qi * p.topk;
-    for (int j0 = 0; j0 < p.topk; j0 += 16) {
-      const int j = j0 + n;
-      const int id = (j < p.topk) ? idx[j] : -1;
-      const bool ok = id >= 0 && id < p.nb;
-      const unsigned valid = (unsigned)__ballot(ok && lane < 16) & 0xffffu;
-      if (valid == 0) continue;
-      w.chunk(kv + (size_t)(ok ? id : 0) * HD, valid, stage);
-    }
-  } else {
-    // dense: compressed blocks b < (t + 1) // m
-    const int nvis = min(p.nb, (p.pos0 + t + 1) / p.m);
-    for (int j0 = 0; j0 < nvis; j0 += 16) {
-      const int j = j0 + n;
-      const bool ok = j < nvis;
-      const unsigned valid = (unsigned)__ballot(ok && lane < 16) & 0xffffu;
-      w.chunk(kv + (size_t)(ok ? j : 0) * HD, valid, stage);
-    }
-  }
+  const int n_main = SPARSE ? p.topk : max(0, min(p.nb, (p.pos0 + t + 1) / p.m));
+  const bf16_t* loc = nullptr;
+  int n_win = 0, wbase = 0;
   if (p.kv_local && p.local_count >= 0) {
-    // window = the first local_count rows (a ring buffer, order irrelevant)
-    const bf16_t* loc =
-        p.kv_local + (size_t)b * (p.local_bstride ? p.local_bstride : (long long)T * HD);
-    for (int j0 = 0; j0 < p.local_count; j0 += 16) {
-      const int j = j0 + n;
-      const bool ok = j < p.local_count;
-      const unsigned valid = (unsigned)__ballot(ok && lane < 16) & 0xffffu;
-      w.chunk(loc + (size_t)(ok ? j : 0) * HD, valid, stage);
-    }
+    loc = p.kv_local + (size_t)b * (p.local_bstride ? p.local_bstride : (long long)T * HD);
+    n_win = p.local_count;
   } else if (p.win > 0 && p.kv_local) {
-    // window positions t - win + 1 .. t (those >= 0)
-    const bf16_t* loc =
-        p.kv_local + (size_t)b * (p.local_bstride ? p.local_bstride : (long long)T * HD);
-    const int lo = t - p.win + 1;
-    for (int j0 = lo; j0 <= t; j0 += 16) {
-      const int j = j0 + n;
-      const bool ok = j >= 0 && j <= t;
-      const unsigned valid = (unsigned)__ballot(ok && lane < 16) & 0xffffu;
-      if (valid == 0) continue;
-      w.chunk(loc + (size_t)(ok ? j : 0) * HD, valid, stage);
+    loc = p.kv_local + (size_t)b * (p.local_bstride ? p.local_bstride : (long long)T * HD);
+    wbase = max(t - p.win + 1, 0);
+    n_win = t - wbase + 1;
+  }
+  const int n_tot = (p.nb > 0 ? n_main : 0) + n_win;
+  if (n_tot > 0) {
+    const int nm = p.nb > 0 ? n_main : 0;
+    // rows of padding lanes must be readable: a compressed row when any exists
+    const bf16_t* dflt = p.nb > 0 ? kv : loc;
+    // Selected block indices come 64 at a time, one per lane, from a load issued
+    // a group ahead of its use (so that waiting for it never waits for the row
+    // loads issued after it); loads are clamped, read entries are only those of
+    // rows below n_main. Without indices a readable word is loaded.
+    const bool has_idx = SPARSE && nm > 0;
+    const int* ip = has_idx ? p.idx + (size_t)qi * p.topk : reinterpret_cast<const int*>(dflt);
+    const int ilim = has_idx ? nm : 1;
+    auto idx_group = [&](int g) { return ip[min(64 * g + lane, ilim - 1)]; };
+    auto row_of = [&](int c, int ig, bool& ok) {
+      const int j = 16 * c + n;
+      const int sel = SPARSE ? __shfl(ig, (16 * c + n) & 63) : j;
+      const bf16_t* row = dflt;
+      ok = false;
+      if (j < nm) {
+        ok = sel >= 0 && sel < p.nb;
+        if (ok) row = kv + (size_t)sel * HD;
+      } else if (j < n_tot) {
+        ok = true;
+        row = loc + (size_t)(wbase + j - nm) * HD;
+      }
+      return row;
+    };
+    // groups of 4 chunks, four chunks in flight; refills are unconditional (past
+    // the end they read the default row, masked off) so that no loaded register
+    // is copied
+    typename W::Frag fr[4];
+    unsigned vm[4];
+    const int nch = (n_tot + 15) / 16;
+    const int ng = (nch + 3) / 4;
+    const int ig0 = idx_group(0);
+    int ig1 = idx_group(1);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      bool ok;
+      const bf16_t* row = row_of(c, ig0, ok);
+      vm[c] = (unsigned)__ballot(ok && lane < 16) & 0xffffu;
+      W::load(fr[c], row);
+    }
+    for (int g = 0; g < ng; ++g) {
+      const int ig2 = idx_group(g + 2);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if (vm[c]) w.chunk(fr[c], vm[c], stage);
+        bool ok;
+        const bf16_t* row = row_of(4 * (g + 1) + c, ig1, ok);
+        vm[c] = (unsigned)__ballot(ok && lane < 16) & 0xffffu;
+        W::load(fr[c], row);
+      }
+      ig1 = ig2;
     }
   }
   const float f = w.finish(p.sink != nullptr, (p.sink && n < p.nh) ? p.sink[n] : 0.f);
