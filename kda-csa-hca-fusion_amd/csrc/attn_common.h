@@ -18,7 +18,8 @@
 //   keys 4q..4q+3 of head n, which is exactly the B operand layout of the
 //   16x16x16 MFMA in O^T = V^T P^T (k = keys), so P never leaves the lane.
 //   V^T fragments (4 keys of one dim) are read from a wave-private LDS copy of
-//   the 16 rows. O^T tile t holds dims 16t + 4q..4q+3 of head n.
+//   the 16 rows with the transposing LDS read (one instruction per tile).
+//   O^T tile t holds dims 16t + 4q..4q+3 of head n.
 // Softmax reference: M (per head) trails the running max by at most 8 in
 // log2 units; o and L are rescaled only when a chunk exceeds that, and the
 // final o / L (with the sink term taken relative to the same M) is the same
@@ -210,9 +211,15 @@ struct MqaWave {
     wave_lds_sync();  // staged rows visible to the whole wave
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      bf16x4 va;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) va[j] = stage[(4 * q + j) * LDS_LD + 16 * t + n];
+      // V^T fragment: rows 4q .. 4q + 3, column 16t + n. The gfx950 transposing
+      // read does it in one instruction: the 16 lanes of a row group each read
+      // 8 bytes (row 4q + n / 4, columns 16t + 4 (n % 4) .. + 3) and lane n
+      // receives column 16t + n of the 4 rows.
+      typedef short s16x4 __attribute__((ext_vector_type(4)));
+      const bf16_t* src = stage + (4 * q + (n >> 2)) * LDS_LD + 16 * t + 4 * (n & 3);
+      const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4*)(src));
+      const bf16x4 va = __builtin_bit_cast(bf16x4, r);
       o[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, o[t], 0, 0, 0);
     }
   }
