@@ -119,7 +119,7 @@ hipError_t compress_dispatch(const CompressParams& p, int dtype, hipStream_t str
 // ---------------------------------------------------------------------------
 
 template <int HD, typename QT, typename OT, bool SPARSE>
-__global__ __launch_bounds__(256) void attn_prefill_kernel(AttnParams p) {
+__global__ __launch_bounds__(256, 3) void attn_prefill_kernel(AttnParams p) {
   using W = MqaWave<HD>;
   __shared__ __attribute__((aligned(16))) bf16_t stage_all[4][16 * W::LDS_LD];
   const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
