@@ -32,6 +32,13 @@ namespace kch {
 
 constexpr float kLog2eF = 1.4426950408889634f;
 constexpr float kRescaleLog2 = 8.f;  // MqaWave: slack of the softmax reference point
+// Initial reference point of the query-tile kernel: finite, so exp2(s - M) of a
+// masked score (-inf) is 0 without a guard; any finite score exceeds it by far
+// more than kRescaleLog2, so the first valid key always resets M.
+constexpr float kMFloor = -1e30f;
+
+// max without NaN canonicalisation (operands are never NaN here)
+__device__ __forceinline__ float fmax_nc(float a, float b) { return __builtin_amdgcn_fmed3f(a, b, INFINITY); }
 
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m); }
 
@@ -146,6 +153,40 @@ struct MqaWave {
     M = -INFINITY;
     L = 0.f;
     qscale2 = scale * kLog2eF;
+  }
+
+  // As init, for the query-tile kernel: the row is always readable (`keep`
+  // false, for a padding head or query, zeroes it after the load, so the load
+  // is not conditional); the sign of `scale` is folded into the fragments so
+  // that qscale2 >= 0; M starts at a finite floor (kMFloor) instead of -inf.
+  template <typename QT>
+  __device__ __forceinline__ void init_always(const QT* q_row, bool keep, bool normalise, float scale) {
+    const int q = lane_id() >> 4;
+    float f[NS][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      Load8<QT>::run(q_row + 32 * s + 8 * q, f[s]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        f[s][i] = keep ? f[s][i] : 0.f;
+        ss += f[s][i] * f[s][i];
+      }
+    }
+    float inv = 1.f;
+    if (normalise) inv = l2_inv(colq_sum(ss));
+    if (scale < 0.f) inv = -inv;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) f[s][i] *= inv;
+      qf[s] = to_bf16x8(f[s]);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    M = kMFloor;
+    L = 0.f;
+    qscale2 = fabsf(scale) * kLog2eF;
   }
 
   // Fragments of 16 key rows: this lane's key row (key n = lane & 15) at dims

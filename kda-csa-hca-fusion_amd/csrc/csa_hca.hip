@@ -218,6 +218,272 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(AttnParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Dense joint-softmax MQA over query tiles (the naive_hca core with window
+// positions [t-win+1, t]). A workgroup takes QG = 4 * QW consecutive queries
+// of one sequence. Their key rows -- the union of the causally visible
+// compressed blocks, then the union of the window positions -- are streamed
+// through LDS 64 rows at a time and shared by the four waves; each wave owns
+// QW queries and masks, per query, the rows outside that query's own set, so
+// every query attends to exactly the rows of the per-query kernel above.
+//
+// LDS tile: rows of HD bf16; 16-byte chunk c of row r is stored at chunk
+// c ^ tile_swz(r % 16). The swizzle keeps the three access patterns free of
+// bank conflicts: the tile loads (a row's chunks by consecutive lanes), the
+// key fragments (16 lanes read chunk c of 16 consecutive rows) and the
+// transposing V^T reads (32 lanes read two adjacent chunks of 8 rows).
+// ---------------------------------------------------------------------------
+template <int HD>
+__device__ __forceinline__ int tile_swz(int r) {
+  if constexpr (HD == 128) return ((r & 7) << 1) | ((r >> 3) & 1);
+  else return (((r >> 1) & 3) << 1) | ((r >> 3) & 1);  // 128-byte rows: two rows per bank sweep
+}
+
+template <typename T> struct Store4;
+template <> struct Store4<float> {
+  static __device__ __forceinline__ void run(float* p, f32x4 v, float f) {
+    *reinterpret_cast<float4*>(p) = make_float4(v[0] * f, v[1] * f, v[2] * f, v[3] * f);
+  }
+};
+template <> struct Store4<bf16_t> {
+  static __device__ __forceinline__ void run(bf16_t* p, f32x4 v, float f) {
+    const bf16x4 r = {(bf16_t)(v[0] * f), (bf16_t)(v[1] * f), (bf16_t)(v[2] * f), (bf16_t)(v[3] * f)};
+    *reinterpret_cast<bf16x4*>(p) = r;
+  }
+};
+template <> struct Store4<_Float16> {
+  static __device__ __forceinline__ void run(_Float16* p, f32x4 v, float f) {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    const h4 r = {(_Float16)(v[0] * f), (_Float16)(v[1] * f), (_Float16)(v[2] * f), (_Float16)(v[3] * f)};
+    *reinterpret_cast<h4*>(p) = r;
+  }
+};
+
+template <int HD, int QW, typename QT, typename OT>
+__global__ __launch_bounds__(256, 2) void attn_dense_tile_kernel(AttnParams p, int ntile, int per_xcd) {
+  using W = MqaWave<HD>;
+  constexpr int QG = 4 * QW;            // queries per workgroup
+  constexpr int KC = 64;                // key rows per LDS tile
+  constexpr int TPR = HD / 8;           // 16-byte chunks per row
+  constexpr int RSTEP = 256 / TPR;      // rows covered by one load of the workgroup
+  constexpr int NLD = KC / RSTEP;       // loads per thread per tile
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  __shared__ __attribute__((aligned(16))) bf16_t tile[2][KC * HD];
+
+  // The 8 XCDs take contiguous ranges of tiles (workgroup i runs on XCD i % 8),
+  // so that neighbouring tiles, which share window rows, share an L2.
+  const int tix = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
+  if (tix >= ntile) return;
+  const int T = p.T;
+  const int tps = (T + QG - 1) / QG;
+  const int b = tix / tps;
+  const int t0 = (tix - b * tps) * QG;
+  const int tl = min(t0 + QG, T) - 1;
+  const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, q4 = lane >> 4, n = lane & 15;
+
+  auto nvis = [&](int t) { return max(0, min(p.nb, (p.pos0 + t + 1) / p.m)); };
+  const bf16_t* kv = p.kv_comp + (size_t)b * (p.kv_bstride ? p.kv_bstride : (long long)p.nb * HD);
+  const int nc = p.nb > 0 ? nvis(tl) : 0;
+  const bf16_t* loc = nullptr;
+  int wlo = 0, nw = 0;
+  if (p.win > 0 && p.kv_local) {
+    loc = p.kv_local + (size_t)b * (p.local_bstride ? p.local_bstride : (long long)T * HD);
+    wlo = max(t0 - p.win + 1, 0);
+    nw = tl - wlo + 1;
+  }
+  const int R = nc + nw;
+
+  // This wave's queries and, per query, its rows: [0, a) and [lo, hi].
+  W w[QW];
+  int a_[QW], lo_[QW], hi_[QW];
+#pragma unroll
+  for (int u = 0; u < QW; ++u) {
+    const int t = t0 + QW * wv + u;
+    const bool live = t < T;
+    const QT* qrow = static_cast<const QT*>(p.q) +
+                     (((size_t)b * T + (live ? t : tl)) * p.nh + min(n, p.nh - 1)) * HD;
+    w[u].template init_always<QT>(qrow, live && n < p.nh, p.normalize_q != 0, p.scale);
+    a_[u] = live && p.nb > 0 ? nvis(t) : 0;
+    lo_[u] = 1;
+    hi_[u] = 0;
+    if (live && nw > 0) {
+      lo_[u] = nc + max(t - p.win + 1, 0) - wlo;
+      hi_[u] = nc + t - wlo;
+    }
+  }
+
+  if (R > 0) {
+    const int lrow = tid / TPR, lch = tid % TPR;
+    const int lsw = lch ^ tile_swz<HD>(lrow & 15);  // RSTEP is a multiple of 16
+    // row j of the union -> this thread's 16 bytes of it: row j of kvb below
+    // nc, else row j of lcb (window position wlo + j - nc); past R, row R - 1
+    const bf16_t* kvb = kv + 8 * lch;
+    const bf16_t* lcb = loc ? loc + (long long)(wlo - nc) * HD + 8 * lch : kvb;
+    auto src_of = [&](int j) -> const bf16_t* {
+      const int jj = min(j, R - 1);
+      return (jj < nc ? kvb : lcb) + (size_t)(unsigned)jj * HD;
+    };
+    // Per-lane LDS offsets (elements) within a 16-row slice: key fragments
+    // (row n, chunk 4s + q), V^T reads (row 4q + n / 4, half-chunk 2t + n % 4 / 2)
+    // and this thread's tile stores.
+    int koff[W::NS], voff[W::NT], soff[NLD];
+    {
+      const int ksw = tile_swz<HD>(n);
+      const int vr = 4 * q4 + (n >> 2);
+      const int vsw = tile_swz<HD>(vr);
+#pragma unroll
+      for (int s2 = 0; s2 < W::NS; ++s2) koff[s2] = n * HD + 8 * ((4 * s2 + q4) ^ ksw);
+#pragma unroll
+      for (int t = 0; t < W::NT; ++t) voff[t] = vr * HD + 8 * ((2 * t + ((n >> 1) & 1)) ^ vsw) + 4 * (n & 1);
+#pragma unroll
+      for (int i = 0; i < NLD; ++i) soff[i] = (lrow + RSTEP * i) * HD + 8 * lsw;
+    }
+    // Rescale threshold per query and head: a score st (before the scale)
+    // above thr = (M + kRescaleLog2) / qscale2 moves M (qscale2 >= 0).
+    float thr[QW];
+#pragma unroll
+    for (int u = 0; u < QW; ++u) thr[u] = (w[u].M + kRescaleLog2) / w[u].qscale2;
+
+    // 16 rows of the tile (LDS row base `rows`, key index j0 of row 0) for all
+    // queries of the wave.
+    auto rows16 = [&](const bf16_t* rows, int j0) {
+      bf16x8 kf[W::NS];
+#pragma unroll
+      for (int s2 = 0; s2 < W::NS; ++s2) kf[s2] = *reinterpret_cast<const bf16x8*>(rows + koff[s2]);
+      f32x4 st[QW];
+#pragma unroll
+      for (int u = 0; u < QW; ++u) {
+        st[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s2 = 0; s2 < W::NS; ++s2)
+          st[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[s2], w[u].qf[s2], st[u], 0, 0, 0);
+      }
+      // Softmax of the 16 keys per query. w.L is this lane's partial sum (its 4
+      // keys), reduced over the 4 lanes of a head at the end. M (per head) only
+      // moves when some score exceeds it by more than kRescaleLog2 (the head's
+      // column max is taken only then), so p = exp2(st * qscale2 - M) <= 2^8.
+      bf16x4 pb[QW];
+#pragma unroll
+      for (int u = 0; u < QW; ++u) {
+        f32x4 sc = st[u];
+        const bool full = (j0 + 16 <= a_[u]) || (j0 >= lo_[u] && j0 + 15 <= hi_[u]);
+        if (!full) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int j = j0 + 4 * q4 + e;
+            const bool ok = (j < a_[u]) | ((j >= lo_[u]) & (j <= hi_[u]));
+            sc[e] = ok ? sc[e] : -INFINITY;
+          }
+        }
+        const bool up = (sc[0] > thr[u]) | (sc[1] > thr[u]) | (sc[2] > thr[u]) | (sc[3] > thr[u]);
+        if (__ballot(up)) {
+          const float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+          const float mnew = fmaxf(w[u].M, colq_max(mx) * w[u].qscale2);
+          const float alpha = fast_exp2(w[u].M - mnew);
+          w[u].L *= alpha;
+#pragma unroll
+          for (int t = 0; t < W::NT; ++t) w[u].o[t] *= alpha;
+          w[u].M = mnew;
+          thr[u] = (mnew + kRescaleLog2) / w[u].qscale2;
+        }
+        const float nm = -w[u].M;
+        f32x4 pe;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pe[e] = fast_exp2(fmaf(sc[e], w[u].qscale2, nm));
+        w[u].L += (pe[0] + pe[1]) + (pe[2] + pe[3]);
+        pb[u] = __builtin_convertvector(pe, bf16x4);
+      }
+#pragma unroll
+      for (int t = 0; t < W::NT; ++t) {
+        // V^T fragment: rows 4q .. 4q + 3, column 16t + n (transposing read of
+        // row 4q + n / 4, columns 16t + 4 (n % 4) .. + 3)
+        const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(rows + voff[t]));
+        const bf16x4 va = __builtin_bit_cast(bf16x4, r);
+#pragma unroll
+        for (int u = 0; u < QW; ++u)
+          w[u].o[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb[u], w[u].o[t], 0, 0, 0);
+      }
+    };
+
+    const int nct = (R + KC - 1) / KC;
+    static_assert(NLD == 2 || NLD == 4, "tile loads per thread");
+    // named registers (an indexed array of them ends up in scratch memory)
+    uint4 pf0, pf1, pf2, pf3;
+    auto issue = [&](int c) {
+      pf0 = *reinterpret_cast<const uint4*>(src_of(c * KC + lrow));
+      pf1 = *reinterpret_cast<const uint4*>(src_of(c * KC + lrow + RSTEP));
+      if constexpr (NLD == 4) {
+        pf2 = *reinterpret_cast<const uint4*>(src_of(c * KC + lrow + 2 * RSTEP));
+        pf3 = *reinterpret_cast<const uint4*>(src_of(c * KC + lrow + 3 * RSTEP));
+      }
+    };
+    auto store = [&](bf16_t* dst) {
+      *reinterpret_cast<uint4*>(dst + soff[0]) = pf0;
+      *reinterpret_cast<uint4*>(dst + soff[1]) = pf1;
+      if constexpr (NLD == 4) {
+        *reinterpret_cast<uint4*>(dst + soff[2]) = pf2;
+        *reinterpret_cast<uint4*>(dst + soff[3]) = pf3;
+      }
+    };
+    // one tile: the next tile's rows are in flight while this one is consumed
+    // (past R: row R - 1 again, stored but never read)
+    auto step = [&](int c, const bf16_t* cur, bf16_t* nxt) {
+      issue(c + 1);
+      const int nsc = min(KC / 16, (R - c * KC + 15) / 16);
+#pragma unroll
+      for (int sc = 0; sc < KC / 16; ++sc)
+        if (sc < nsc) rows16(cur + 16 * sc * HD, c * KC + 16 * sc);
+      store(nxt);
+      __syncthreads();
+    };
+    issue(0);
+    store(tile[0]);
+    __syncthreads();
+    // two tiles per iteration, so that each LDS buffer address is static
+    for (int c = 0; c < nct; c += 2) {
+      step(c, tile[0], tile[1]);
+      if (c + 1 < nct) step(c + 1, tile[1], tile[0]);
+    }
+  }
+
+#pragma unroll
+  for (int u = 0; u < QW; ++u) {
+    const int t = t0 + QW * wv + u;
+    w[u].L = colq_sum(w[u].L);
+    const float f = w[u].finish(p.sink != nullptr, (p.sink && n < p.nh) ? p.sink[n] : 0.f);
+    if (t < T && n < p.nh) {
+      OT* out = static_cast<OT*>(p.out) + (((size_t)b * T + t) * p.nh + n) * HD;
+#pragma unroll
+      for (int tt = 0; tt < W::NT; ++tt) Store4<OT>::run(out + 16 * tt + 4 * q4, w[u].o[tt], f);
+    }
+  }
+}
+
+template <int HD>
+static hipError_t launch_dense_tile(const AttnParams& p, int qdtype, int odtype, hipStream_t s) {
+  constexpr int QW = 2, QG = 4 * QW;
+  const long long ntile = (long long)p.B * ((p.T + QG - 1) / QG);
+  const int per_xcd = (int)((ntile + 7) / 8);
+  const dim3 grid((unsigned)(8 * per_xcd)), block(256);
+#define KCH_TILE_LAUNCH(QT, OT) \
+  hipLaunchKernelGGL((attn_dense_tile_kernel<HD, QW, QT, OT>), grid, block, 0, s, p, (int)ntile, per_xcd)
+  if (qdtype == DT_BF16) {
+    if (odtype == DT_F32) KCH_TILE_LAUNCH(bf16_t, float);
+    else KCH_TILE_LAUNCH(bf16_t, bf16_t);
+  } else if (qdtype == DT_F32) {
+    if (odtype == DT_F32) KCH_TILE_LAUNCH(float, float);
+    else KCH_TILE_LAUNCH(float, bf16_t);
+  } else {
+    if (odtype == DT_F32) KCH_TILE_LAUNCH(_Float16, float);
+    else KCH_TILE_LAUNCH(_Float16, _Float16);
+  }
+#undef KCH_TILE_LAUNCH
+  return hipGetLastError();
+}
+
 template <int HD, bool SPARSE>
 static hipError_t launch_attn(const AttnParams& p, int qdtype, int odtype, hipStream_t s) {
   const long long nq = (long long)p.B * p.T;
@@ -239,6 +505,10 @@ static hipError_t launch_attn(const AttnParams& p, int qdtype, int odtype, hipSt
 }
 
 hipError_t attn_dispatch(const AttnParams& p, bool sparse, int qdtype, int odtype, hipStream_t s) {
+  // dense with a window of positions: query tiles sharing the key rows
+  if (!sparse && p.local_count < 0)
+    return p.hd == 128 ? launch_dense_tile<128>(p, qdtype, odtype, s)
+                       : launch_dense_tile<64>(p, qdtype, odtype, s);
   if (p.hd == 128) return sparse ? launch_attn<128, true>(p, qdtype, odtype, s)
                                  : launch_attn<128, false>(p, qdtype, odtype, s);
   return sparse ? launch_attn<64, true>(p, qdtype, odtype, s)

@@ -214,6 +214,58 @@ def test_hca_core_matches_oracle(dev, win, sink, m2, T):
     close("hca out", host(out), bf16_round(ref))
 
 
+def _hca_attn_ref(q, kv, loc, sink, m, win, scale):
+    """Dense MQA of ``ops_hca.py:136-194`` over given key rows (oracle pieces)."""
+    from oracle.common import l2_normalize
+    Bn, T, nh, hd = q.shape
+    nb = kv.shape[1]
+    qn = l2_normalize(q.astype(np.float32))
+    scores = np.einsum('bthd,bnd->bhtn', qn, kv) * np.float32(scale)
+    scores = np.where(O.causal_block_mask(T, nb, m)[None, None], scores, -np.inf)
+    if win > 0:
+        sw, Cw, _ = O.window_scores(qn, loc, win, scale)
+        sw = sw.transpose(0, 2, 1, 3)
+    else:
+        sw, Cw = np.zeros((Bn, nh, T, 0), np.float32), np.zeros((Bn, T, 0, hd), np.float32)
+    cat = np.concatenate([scores, sw], -1).astype(np.float32)
+    if cat.shape[-1] == 0:
+        return np.zeros((Bn, T, nh, hd), np.float32)
+    s = None if sink is None else sink.reshape(1, nh, 1, 1)
+    p = O.joint_softmax_hca(cat, s)
+    return (np.einsum('bhtn,bnd->bthd', p[..., :nb], kv)
+            + np.einsum('bhtw,btwd->bthd', p[..., nb:], Cw))
+
+
+@pytest.mark.parametrize("hd,nh,T,nb,m,win,qdt,odt", [
+    (128, 16, 77, 9, 8, 20, "bf16", "bf16"),   # T not a multiple of the query tile
+    (64, 5, 45, 6, 7, 100, "fp32", "fp32"),    # window longer than the sequence
+    (128, 3, 33, 0, 4, 16, "bf16", "fp32"),    # no compressed block
+    (64, 16, 50, 12, 4, 0, "bf16", "bf16"),    # no window
+    (128, 16, 130, 40, 3, 64, "fp16", "fp16"),  # several key tiles, fp16 queries
+])
+def test_hca_attn_abi_shapes(dev, hd, nh, T, nb, m, win, qdt, odt):
+    """kch_hca_attn over ragged shapes: query tiles cut by T, head counts below 16,
+    head dim 64, empty compressed or window parts, every query / output dtype."""
+    from kch import _lib
+    from oracle.common import l2_normalize
+    dts = {"bf16": torch.bfloat16, "fp32": torch.float32, "fp16": torch.float16}
+    B = 2
+    rng = np.random.default_rng(T * 7 + nb)
+    q = torch.from_numpy(rng.standard_normal((B, T, nh, hd)).astype(np.float32)).to(dev, dts[qdt])
+    kv = bf16_dev(l2_normalize(rng.standard_normal((B, max(nb, 1), hd)).astype(np.float32)), dev)
+    loc = bf16_dev(l2_normalize(rng.standard_normal((B, T, hd)).astype(np.float32)), dev)
+    sink = torch.from_numpy(rng.standard_normal(nh).astype(np.float32)).to(dev)
+    out = torch.full((B, T, nh, hd), float("nan"), device=dev, dtype=dts[odt])
+    code = {"bf16": 1, "fp32": 0, "fp16": 2}
+    scale = hd ** -0.5
+    _lib.call("kch_hca_attn", _lib.ptr(q), _lib.ptr(kv), _lib.ptr(loc if win > 0 else None),
+              _lib.ptr(sink), _lib.ptr(out), B, T, nb, nh, hd, m, win, scale, 1, code[qdt],
+              code[odt], _lib.stream_of(q))
+    torch.cuda.synchronize()
+    ref = _hca_attn_ref(host(q), host(kv)[:, :nb], host(loc), host(sink), m, win, scale)
+    close("hca attn", host(out), ref if odt == "fp32" else host(torch.from_numpy(ref).to(dts[odt])))
+
+
 def _weights(rng, shapes, dev):
     return {k: (rng.standard_normal(s) * s[1] ** -0.5) for k, s in shapes.items()}
 
