@@ -99,7 +99,183 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressParams p) {
   }
 }
 
+// Row-parallel compression for long blocks (m or 2m >= 16 rows, c in {64,128},
+// 16-byte aligned rows). A workgroup (4 waves) takes one compressed block:
+// lane l of wave w owns channels 8 (l % LPR) .. + 7 of the row slot
+// w * RPW + l / LPR; the slots take the block's rows round-robin, four rows
+// in flight per slot. Each slot keeps, per channel, an online softmax of its
+// rows (running max, sum of exp, exp-weighted sum of C); the slots are then
+// merged (lane shuffles, then LDS across the waves) into the same weighted
+// mean as the two-pass form of compress_kernel. The per-token window keys are
+// written from the slot that reads the token's a-branch row.
+template <typename InT, bool OVERLAP, int C>
+__global__ __launch_bounds__(256) void compress_rows_kernel(CompressParams p) {
+  constexpr int LPR = C / 8;           // lanes per row
+  constexpr int RPW = 64 / LPR;        // row slots per wave
+  constexpr int NSLOT = 4 * RPW;
+  constexpr int U = 4;                 // rows in flight per slot
+  __shared__ float part[4][3][C];
+  __shared__ float red[4];
+  const int nb = p.T / p.m;
+  const int b = blockIdx.x / nb, blk = blockIdx.x - b * nb;
+  const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int slot = wv * RPW + lane / LPR, ch0 = 8 * (lane % LPR);
+  const int m = p.m;
+  const int nrows = (OVERLAP && blk > 0) ? 2 * m : m;
+  const InT* Ca = static_cast<const InT*>(p.Ca);
+  const InT* Za = static_cast<const InT*>(p.Za);
+  const InT* Cb = static_cast<const InT*>(p.Cb);
+  const InT* Zb = static_cast<const InT*>(p.Zb);
+  const long long ta = (long long)b * p.T + (long long)blk * m;  // token of a-branch row 0
+
+  float mx[8], den[8], num[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    mx[i] = -INFINITY;
+    den[i] = 0.f;
+    num[i] = 0.f;
+  }
+  for (int r0 = slot; r0 < nrows; r0 += U * NSLOT) {
+    float z[U][8], v[U][8];
+    bool bsel[U];
+    long long tok[U];
+    // loads of U rows (past the end: row r0 again, not used)
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      const int rr = r0 + k * NSLOT;
+      const int r = rr < nrows ? rr : r0;
+      const bool bb = OVERLAP && r >= m;
+      const int j = bb ? r - m : r;
+      bsel[k] = bb;
+      tok[k] = bb ? ta - m + j : ta + j;
+      const InT* zp = bb ? Zb + tok[k] * p.ldZb : Za + tok[k] * p.ldZa;
+      const InT* cp = bb ? Cb + tok[k] * p.ldCb : Ca + tok[k] * p.ldCa;
+      const float* bp = (bb ? p.Bb : p.Ba) + (size_t)j * C + ch0;
+      Load8<InT>::run(zp + ch0, z[k]);
+      Load8<InT>::run(cp + ch0, v[k]);
+      const float4 b0 = *reinterpret_cast<const float4*>(bp);
+      const float4 b1 = *reinterpret_cast<const float4*>(bp + 4);
+      z[k][0] += b0.x; z[k][1] += b0.y; z[k][2] += b0.z; z[k][3] += b0.w;
+      z[k][4] += b1.x; z[k][5] += b1.y; z[k][6] += b1.z; z[k][7] += b1.w;
+    }
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+      if (r0 + k * NSLOT >= nrows) continue;  // same for the whole slot
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        // online softmax step: one exp per element
+        const float d = z[k][i] - mx[i];
+        const bool up = d > 0.f;
+        const float e = expf(up ? -d : d);  // mx = -inf: d = +inf, e = 0
+        den[i] = up ? fmaf(den[i], e, 1.f) : den[i] + e;
+        num[i] = up ? fmaf(num[i], e, v[k][i]) : fmaf(e, v[k][i], num[i]);
+        mx[i] = up ? z[k][i] : mx[i];
+      }
+      if (p.local && !bsel[k]) {
+        // window key of this token: L2norm over the row's LPR lanes
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss += v[k][i] * v[k][i];
+#pragma unroll
+        for (int o = 1; o < LPR; o <<= 1) ss += __shfl_xor(ss, o);
+        const float inv = p.normalize ? l2_inv(ss) : 1.f;
+        float f[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) f[i] = v[k][i] * inv;
+        *reinterpret_cast<bf16x8*>(p.local + tok[k] * C + ch0) = to_bf16x8(f);
+      }
+    }
+  }
+  // merge the slots of the wave (lanes LPR, 2 LPR, .. apart), then the waves
+#pragma unroll
+  for (int o = LPR; o < 64; o <<= 1) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float m2 = __shfl_xor(mx[i], o), d2 = __shfl_xor(den[i], o), n2 = __shfl_xor(num[i], o);
+      const float mm = fmaxf(mx[i], m2);
+      if (mm != -INFINITY) {
+        const float e1 = expf(mx[i] - mm), e2 = expf(m2 - mm);
+        den[i] = den[i] * e1 + d2 * e2;
+        num[i] = num[i] * e1 + n2 * e2;
+        mx[i] = mm;
+      }
+    }
+  }
+  if (lane < LPR) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      part[wv][0][ch0 + i] = mx[i];
+      part[wv][1][ch0 + i] = den[i];
+      part[wv][2][ch0 + i] = num[i];
+    }
+  }
+  __syncthreads();
+  const int ch = threadIdx.x;
+  float acc = 0.f;
+  if (ch < C) {
+    float M = part[0][0][ch];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) M = fmaxf(M, part[w][0][ch]);
+    float dd = 0.f, nn = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float mw = part[w][0][ch];
+      if (mw != -INFINITY) {
+        const float e = expf(mw - M);
+        dd += part[w][1][ch] * e;
+        nn += part[w][2][ch] * e;
+      }
+    }
+    acc = nn / dd;
+  }
+  const size_t orow = (size_t)b * nb + blk;
+  if (ch < C && p.out_raw) p.out_raw[orow * C + ch] = acc;
+  if (p.out_key) {
+    float inv = 1.f;
+    if (p.normalize) {
+      const float s = wave_sum(acc * acc);  // channels >= C contribute 0
+      if (lane == 0) red[wv] = s;
+      __syncthreads();
+      inv = l2_inv(red[0] + red[1] + red[2] + red[3]);
+    }
+    if (ch < C) {
+      if (p.key_f32) static_cast<float*>(p.out_key)[orow * C + ch] = acc * inv;
+      else static_cast<bf16_t*>(p.out_key)[orow * C + ch] = (bf16_t)(acc * inv);
+    }
+  }
+}
+
+// The row-parallel kernel applies: 16-byte aligned 8-channel groups everywhere.
+static bool compress_rows_ok(const CompressParams& p, int dtype) {
+  const int rows = p.m * (p.overlap ? 2 : 1);
+  if (rows < 16 || (p.c != 64 && p.c != 128)) return false;
+  const long long es = dtype == DT_F32 ? 4 : 2;
+  auto al = [](const void* q) { return q == nullptr || ((uintptr_t)q & 15) == 0; };
+  auto ld_ok = [&](long long ld) { return (ld * es) % 16 == 0; };
+  bool ok = al(p.Ca) && al(p.Za) && al(p.Ba) && al(p.local) && ld_ok(p.ldCa) && ld_ok(p.ldZa);
+  if (p.overlap) ok = ok && al(p.Cb) && al(p.Zb) && al(p.Bb) && ld_ok(p.ldCb) && ld_ok(p.ldZb);
+  return ok;
+}
+
+template <bool OVERLAP, int C>
+static void launch_compress_rows(const CompressParams& p, int dtype, hipStream_t stream) {
+  const dim3 grid(p.B * (p.T / p.m)), block(256);
+  if (dtype == DT_F32) hipLaunchKernelGGL((compress_rows_kernel<float, OVERLAP, C>), grid, block, 0, stream, p);
+  else if (dtype == DT_BF16) hipLaunchKernelGGL((compress_rows_kernel<bf16_t, OVERLAP, C>), grid, block, 0, stream, p);
+  else hipLaunchKernelGGL((compress_rows_kernel<_Float16, OVERLAP, C>), grid, block, 0, stream, p);
+}
+
 hipError_t compress_dispatch(const CompressParams& p, int dtype, hipStream_t stream) {
+  if (p.B * (p.T / p.m) > 0 && compress_rows_ok(p, dtype)) {
+    if (p.overlap) {
+      if (p.c == 128) launch_compress_rows<true, 128>(p, dtype, stream);
+      else launch_compress_rows<true, 64>(p, dtype, stream);
+    } else {
+      if (p.c == 128) launch_compress_rows<false, 128>(p, dtype, stream);
+      else launch_compress_rows<false, 64>(p, dtype, stream);
+    }
+    return hipGetLastError();
+  }
   const int nwaves = p.B * (p.T / p.m);
   const dim3 grid((nwaves + 3) / 4), block(256);
   if (p.overlap) {
@@ -259,8 +435,10 @@ template <> struct Store4<_Float16> {
   }
 };
 
+constexpr int kTileGroup = 16;  // consecutive query tiles kept on one XCD
+
 template <int HD, int QW, typename QT, typename OT>
-__global__ __launch_bounds__(256, 2) void attn_dense_tile_kernel(AttnParams p, int ntile, int per_xcd) {
+__global__ __launch_bounds__(256, 2) void attn_dense_tile_kernel(AttnParams p, int ntile) {
   using W = MqaWave<HD>;
   constexpr int QG = 4 * QW;            // queries per workgroup
   constexpr int KC = 64;                // key rows per LDS tile
@@ -270,9 +448,12 @@ __global__ __launch_bounds__(256, 2) void attn_dense_tile_kernel(AttnParams p, i
   typedef short s16x4 __attribute__((ext_vector_type(4)));
   __shared__ __attribute__((aligned(16))) bf16_t tile[2][KC * HD];
 
-  // The 8 XCDs take contiguous ranges of tiles (workgroup i runs on XCD i % 8),
-  // so that neighbouring tiles, which share window rows, share an L2.
-  const int tix = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
+  // Workgroup i runs on XCD i % 8. Groups of kTileGroup consecutive tiles
+  // (which share window rows) stay on one XCD, hence one L2, and the groups
+  // are dealt to the XCDs round-robin, so that every XCD gets the same mix of
+  // short (early) and long (late) queries.
+  const int xcd = (int)(blockIdx.x & 7), slot = (int)(blockIdx.x >> 3);
+  const int tix = ((slot / kTileGroup) * 8 + xcd) * kTileGroup + slot % kTileGroup;
   if (tix >= ntile) return;
   const int T = p.T;
   const int tps = (T + QG - 1) / QG;
@@ -466,10 +647,10 @@ template <int HD>
 static hipError_t launch_dense_tile(const AttnParams& p, int qdtype, int odtype, hipStream_t s) {
   constexpr int QW = 2, QG = 4 * QW;
   const long long ntile = (long long)p.B * ((p.T + QG - 1) / QG);
-  const int per_xcd = (int)((ntile + 7) / 8);
-  const dim3 grid((unsigned)(8 * per_xcd)), block(256);
+  const long long ngroup = (ntile + kTileGroup - 1) / kTileGroup;
+  const dim3 grid((unsigned)(((ngroup + 7) / 8) * 8 * kTileGroup)), block(256);
 #define KCH_TILE_LAUNCH(QT, OT) \
-  hipLaunchKernelGGL((attn_dense_tile_kernel<HD, QW, QT, OT>), grid, block, 0, s, p, (int)ntile, per_xcd)
+  hipLaunchKernelGGL((attn_dense_tile_kernel<HD, QW, QT, OT>), grid, block, 0, s, p, (int)ntile)
   if (qdtype == DT_BF16) {
     if (odtype == DT_F32) KCH_TILE_LAUNCH(bf16_t, float);
     else KCH_TILE_LAUNCH(bf16_t, bf16_t);

@@ -129,6 +129,46 @@ def test_compress_overlapped(dev, m, c):
     assert np.abs(host(out) - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max())
 
 
+@pytest.mark.parametrize("m,c,overlap,dt,key_dt", [
+    (32, 128, False, "bf16", "bf16"),   # row-parallel kernel, strided rows
+    (16, 64, True, "fp32", "fp32"),     # row-parallel, overlapped, fp32 inputs
+    (128, 64, False, "fp16", "bf16"),   # row-parallel, long blocks
+    (4, 128, True, "bf16", "bf16"),     # per-block kernel (8 rows)
+    (5, 64, False, "fp32", "fp32"),     # per-block kernel, odd m
+])
+def test_compress_key_and_window_outputs(dev, m, c, overlap, dt, key_dt):
+    """All compression outputs: raw fp32 blocks, L2-normalised key rows (bf16 or
+    fp32) and the per-token window keys L2norm(C_a) (bf16), for both kernels."""
+    from kch.ops_csa import _compress, _compress_overlapped
+    from oracle.common import l2_normalize
+    dts = {"bf16": torch.bfloat16, "fp32": torch.float32, "fp16": torch.float16}
+    B, T = 2, 6 * m
+    rng = np.random.default_rng(m * 31 + c)
+    # strided rows: the four inputs are column slices of one [B, T, 4c + 8] tensor
+    big = torch.from_numpy(rng.standard_normal((B, T, 4 * c + 8)).astype(np.float32)).to(dev, dts[dt])
+    Ca, Cb, Za, Zb = big[..., :c], big[..., c:2 * c], big[..., 2 * c:3 * c], big[..., 3 * c:4 * c]
+    Ba = (0.5 * rng.standard_normal((m, c))).astype(np.float32)
+    Bb = (0.5 * rng.standard_normal((m, c))).astype(np.float32)
+    key = torch.empty(B, T // m, c, device=dev, dtype=dts[key_dt])
+    local = torch.empty(B, T, c, device=dev, dtype=torch.bfloat16)
+    if overlap:
+        raw = _compress_overlapped("t", Ca, Cb, Za, Zb, torch.from_numpy(Ba).to(dev),
+                                   torch.from_numpy(Bb).to(dev), m, key=key, normalize=True,
+                                   local=local)
+        ref = O.compress_kv_overlapped(host(Ca), host(Cb), host(Za), host(Zb), Ba, Bb, m)
+    else:
+        raw = _compress("t", Ca, Za, torch.from_numpy(Ba).to(dev), m, key=key, normalize=True,
+                        local=local)
+        ref = O.compress_kv(host(Ca), host(Za), Ba, m)
+    torch.cuda.synchronize()
+    assert np.abs(host(raw) - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max())
+    kref = l2_normalize(ref)
+    ktol = 1e-6 if key_dt == "fp32" else 8e-3
+    assert np.abs(host(key) - kref).max() <= ktol
+    lref = l2_normalize(host(Ca).astype(np.float32))
+    assert np.abs(host(local) - lref).max() <= 8e-3
+
+
 @pytest.mark.parametrize("normalize", [True, False])
 @pytest.mark.parametrize("T,m,topk", [(128, 4, 8), (64, 4, 32), (200, 4, 16), (96, 8, 0)])
 def test_indexer_matches_oracle(dev, normalize, T, m, topk):
