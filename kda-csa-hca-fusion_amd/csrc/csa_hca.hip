@@ -437,15 +437,20 @@ template <> struct Store4<_Float16> {
 
 constexpr int kTileGroup = 16;  // consecutive query tiles kept on one XCD
 
-template <int HD, int QW, typename QT, typename OT>
-__global__ __launch_bounds__(256, 2) void attn_dense_tile_kernel(AttnParams p, int ntile) {
+template <int HD, int QW, int NWV, int MINB, typename QT, typename OT>
+__global__ __launch_bounds__(64 * NWV, MINB) void attn_dense_tile_kernel(AttnParams p, int ntile) {
   using W = MqaWave<HD>;
-  constexpr int QG = 4 * QW;            // queries per workgroup
+  constexpr int NTH = 64 * NWV;         // threads per workgroup
+  constexpr int QG = NWV * QW;          // queries per workgroup
   constexpr int KC = 64;                // key rows per LDS tile
   constexpr int TPR = HD / 8;           // 16-byte chunks per row
-  constexpr int RSTEP = 256 / TPR;      // rows covered by one load of the workgroup
+  constexpr int RSTEP = NTH / TPR;      // rows per load pass of the workgroup
   constexpr int NLD = KC / RSTEP;       // loads per thread per tile
+  static_assert(NLD == 1 || NLD == 2 || NLD == 4, "tile loads per thread");
+  static_assert(RSTEP % 16 == 0, "load rows keep their swizzle");
   typedef short s16x4 __attribute__((ext_vector_type(4)));
+  typedef short s16x8 __attribute__((ext_vector_type(8)));
+  typedef float f32x8 __attribute__((ext_vector_type(8)));
   __shared__ __attribute__((aligned(16))) bf16_t tile[2][KC * HD];
 
   // Workgroup i runs on XCD i % 8. Groups of kTileGroup consecutive tiles
@@ -496,30 +501,31 @@ __global__ __launch_bounds__(256, 2) void attn_dense_tile_kernel(AttnParams p, i
   }
 
   if (R > 0) {
+    // Tile loads: thread tid takes 16-byte chunk tid % TPR of rows
+    // tid / TPR + RSTEP i. Row j of the union is row j of kvb below nc, else
+    // row j of lcb (window position wlo + j - nc); past R, row R - 1 again
+    // (loaded, never read).
     const int lrow = tid / TPR, lch = tid % TPR;
-    const int lsw = lch ^ tile_swz<HD>(lrow & 15);  // RSTEP is a multiple of 16
-    // row j of the union -> this thread's 16 bytes of it: row j of kvb below
-    // nc, else row j of lcb (window position wlo + j - nc); past R, row R - 1
+    const int soff = lrow * HD + 8 * (lch ^ tile_swz<HD>(lrow & 15));
     const bf16_t* kvb = kv + 8 * lch;
     const bf16_t* lcb = loc ? loc + (long long)(wlo - nc) * HD + 8 * lch : kvb;
     auto src_of = [&](int j) -> const bf16_t* {
       const int jj = min(j, R - 1);
       return (jj < nc ? kvb : lcb) + (size_t)(unsigned)jj * HD;
     };
-    // Per-lane LDS offsets (elements) within a 16-row slice: key fragments
-    // (row n, chunk 4s + q), V^T reads (row 4q + n / 4, half-chunk 2t + n % 4 / 2)
-    // and this thread's tile stores.
-    int koff[W::NS], voff[W::NT], soff[NLD];
+    // Per-lane LDS offsets (elements) within a 16-row slice. Key fragment s:
+    // row n, chunk (4s + q) ^ swz(n) = 4 (s ^ (swz >> 2)) + (q ^ (swz & 3));
+    // V^T read t: row 4q + n / 4, half-chunk 2t + n % 4 / 2 of chunk
+    // (2t + h) ^ swz = 2 (t ^ (swz >> 1)) + (h ^ (swz & 1)). The s and t terms
+    // only flip bits of their own: the offsets are kbase ^ (s << 5) and
+    // vbase ^ (t << 4).
+    int kbase, vbase;
     {
       const int ksw = tile_swz<HD>(n);
       const int vr = 4 * q4 + (n >> 2);
       const int vsw = tile_swz<HD>(vr);
-#pragma unroll
-      for (int s2 = 0; s2 < W::NS; ++s2) koff[s2] = n * HD + 8 * ((4 * s2 + q4) ^ ksw);
-#pragma unroll
-      for (int t = 0; t < W::NT; ++t) voff[t] = vr * HD + 8 * ((2 * t + ((n >> 1) & 1)) ^ vsw) + 4 * (n & 1);
-#pragma unroll
-      for (int i = 0; i < NLD; ++i) soff[i] = (lrow + RSTEP * i) * HD + 8 * lsw;
+      kbase = n * HD + 8 * (q4 ^ (ksw & 3)) + 32 * (ksw >> 2);
+      vbase = vr * HD + 8 * (((n >> 1) & 1) ^ (vsw & 1)) + 16 * (vsw >> 1) + 4 * (n & 1);
     }
     // Rescale threshold per query and head: a score st (before the scale)
     // above thr = (M + kRescaleLog2) / qscale2 moves M (qscale2 >= 0).
@@ -527,40 +533,54 @@ __global__ __launch_bounds__(256, 2) void attn_dense_tile_kernel(AttnParams p, i
 #pragma unroll
     for (int u = 0; u < QW; ++u) thr[u] = (w[u].M + kRescaleLog2) / w[u].qscale2;
 
-    // 16 rows of the tile (LDS row base `rows`, key index j0 of row 0) for all
-    // queries of the wave.
-    auto rows16 = [&](const bf16_t* rows, int j0) {
-      bf16x8 kf[W::NS];
+    // 32 rows of the tile (LDS row base `rows`, key index j0 of row 0) for the
+    // wave's queries. Both products use v_mfma_f32_16x16x32_bf16 (the 16x16x16
+    // form runs at half its rate on gfx950). The 32 keys sit in the k slots
+    // as: slot 8q + i <-> key 4q + i (i < 4, first 16 rows) and key
+    // 16 + 4q + i - 4 (i >= 4, second 16 rows), which is where the S^T
+    // accumulators of the two 16-row slices leave them, so P never moves.
+    auto rows32 = [&](const bf16_t* rows, int j0) {
+      f32x4 sa[QW], sb[QW];
 #pragma unroll
-      for (int s2 = 0; s2 < W::NS; ++s2) kf[s2] = *reinterpret_cast<const bf16x8*>(rows + koff[s2]);
-      f32x4 st[QW];
-#pragma unroll
-      for (int u = 0; u < QW; ++u) {
-        st[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int h = 0; h < 2; ++h) {
+        bf16x8 kf[W::NS];
 #pragma unroll
         for (int s2 = 0; s2 < W::NS; ++s2)
-          st[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[s2], w[u].qf[s2], st[u], 0, 0, 0);
+          kf[s2] = *reinterpret_cast<const bf16x8*>(rows + 16 * HD * h + (kbase ^ (s2 << 5)));
+#pragma unroll
+        for (int u = 0; u < QW; ++u) {
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int s2 = 0; s2 < W::NS; ++s2)
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[s2], w[u].qf[s2], acc, 0, 0, 0);
+          if (h == 0) sa[u] = acc;
+          else sb[u] = acc;
+        }
       }
-      // Softmax of the 16 keys per query. w.L is this lane's partial sum (its 4
+      // Softmax of the 32 keys per query. w.L is this lane's partial sum (its 8
       // keys), reduced over the 4 lanes of a head at the end. M (per head) only
       // moves when some score exceeds it by more than kRescaleLog2 (the head's
       // column max is taken only then), so p = exp2(st * qscale2 - M) <= 2^8.
-      bf16x4 pb[QW];
+      bf16x8 pb[QW];
 #pragma unroll
       for (int u = 0; u < QW; ++u) {
-        f32x4 sc = st[u];
-        const bool full = (j0 + 16 <= a_[u]) || (j0 >= lo_[u] && j0 + 15 <= hi_[u]);
+        float sc[8] = {sa[u][0], sa[u][1], sa[u][2], sa[u][3], sb[u][0], sb[u][1], sb[u][2], sb[u][3]};
+        const bool full = (j0 + 32 <= a_[u]) || (j0 >= lo_[u] && j0 + 31 <= hi_[u]);
         if (!full) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int j = j0 + 4 * q4 + e;
+          for (int e = 0; e < 8; ++e) {
+            const int j = j0 + 4 * q4 + (e < 4 ? e : 12 + e);
             const bool ok = (j < a_[u]) | ((j >= lo_[u]) & (j <= hi_[u]));
             sc[e] = ok ? sc[e] : -INFINITY;
           }
         }
-        const bool up = (sc[0] > thr[u]) | (sc[1] > thr[u]) | (sc[2] > thr[u]) | (sc[3] > thr[u]);
+        bool up = false;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) up |= sc[e] > thr[u];
         if (__ballot(up)) {
-          const float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+          float mx = sc[0];
+#pragma unroll
+          for (int e = 1; e < 8; ++e) mx = fmaxf(mx, sc[e]);
           const float mnew = fmaxf(w[u].M, colq_max(mx) * w[u].qscale2);
           const float alpha = fast_exp2(w[u].M - mnew);
           w[u].L *= alpha;
@@ -570,53 +590,54 @@ __global__ __launch_bounds__(256, 2) void attn_dense_tile_kernel(AttnParams p, i
           thr[u] = (mnew + kRescaleLog2) / w[u].qscale2;
         }
         const float nm = -w[u].M;
-        f32x4 pe;
+        f32x8 pe;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) pe[e] = fast_exp2(fmaf(sc[e], w[u].qscale2, nm));
-        w[u].L += (pe[0] + pe[1]) + (pe[2] + pe[3]);
-        pb[u] = __builtin_convertvector(pe, bf16x4);
+        for (int e = 0; e < 8; ++e) pe[e] = fast_exp2(fmaf(sc[e], w[u].qscale2, nm));
+        w[u].L += ((pe[0] + pe[1]) + (pe[2] + pe[3])) + ((pe[4] + pe[5]) + (pe[6] + pe[7]));
+        pb[u] = __builtin_convertvector(pe, bf16x8);
       }
 #pragma unroll
       for (int t = 0; t < W::NT; ++t) {
-        // V^T fragment: rows 4q .. 4q + 3, column 16t + n (transposing read of
-        // row 4q + n / 4, columns 16t + 4 (n % 4) .. + 3)
-        const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4*)(rows + voff[t]));
-        const bf16x4 va = __builtin_bit_cast(bf16x4, r);
+        // V^T fragment (16 dims x 32 keys): column 16t + n of rows 4q .. 4q + 3
+        // of each slice, one transposing read per slice
+        const int vo = vbase ^ (t << 4);
+        const s16x4 r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(rows + vo));
+        const s16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(rows + 16 * HD + vo));
+        const bf16x8 va = __builtin_bit_cast(bf16x8, __builtin_shufflevector(r0, r1, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
         for (int u = 0; u < QW; ++u)
-          w[u].o[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb[u], w[u].o[t], 0, 0, 0);
+          w[u].o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[u], w[u].o[t], 0, 0, 0);
       }
     };
 
     const int nct = (R + KC - 1) / KC;
-    static_assert(NLD == 2 || NLD == 4, "tile loads per thread");
     // named registers (an indexed array of them ends up in scratch memory)
     uint4 pf0, pf1, pf2, pf3;
     auto issue = [&](int c) {
       pf0 = *reinterpret_cast<const uint4*>(src_of(c * KC + lrow));
-      pf1 = *reinterpret_cast<const uint4*>(src_of(c * KC + lrow + RSTEP));
+      if constexpr (NLD >= 2) pf1 = *reinterpret_cast<const uint4*>(src_of(c * KC + lrow + RSTEP));
       if constexpr (NLD == 4) {
         pf2 = *reinterpret_cast<const uint4*>(src_of(c * KC + lrow + 2 * RSTEP));
         pf3 = *reinterpret_cast<const uint4*>(src_of(c * KC + lrow + 3 * RSTEP));
       }
     };
     auto store = [&](bf16_t* dst) {
-      *reinterpret_cast<uint4*>(dst + soff[0]) = pf0;
-      *reinterpret_cast<uint4*>(dst + soff[1]) = pf1;
+      *reinterpret_cast<uint4*>(dst + soff) = pf0;
+      if constexpr (NLD >= 2) *reinterpret_cast<uint4*>(dst + soff + RSTEP * HD) = pf1;
       if constexpr (NLD == 4) {
-        *reinterpret_cast<uint4*>(dst + soff[2]) = pf2;
-        *reinterpret_cast<uint4*>(dst + soff[3]) = pf3;
+        *reinterpret_cast<uint4*>(dst + soff + 2 * RSTEP * HD) = pf2;
+        *reinterpret_cast<uint4*>(dst + soff + 3 * RSTEP * HD) = pf3;
       }
     };
     // one tile: the next tile's rows are in flight while this one is consumed
-    // (past R: row R - 1 again, stored but never read)
     auto step = [&](int c, const bf16_t* cur, bf16_t* nxt) {
       issue(c + 1);
-      const int nsc = min(KC / 16, (R - c * KC + 15) / 16);
+      const int nsc = min(KC / 32, (R - c * KC + 31) / 32);
 #pragma unroll
-      for (int sc = 0; sc < KC / 16; ++sc)
-        if (sc < nsc) rows16(cur + 16 * sc * HD, c * KC + 16 * sc);
+      for (int sc = 0; sc < KC / 32; ++sc)
+        if (sc < nsc) rows32(cur + 32 * sc * HD, c * KC + 32 * sc);
       store(nxt);
       __syncthreads();
     };
@@ -630,27 +651,59 @@ __global__ __launch_bounds__(256, 2) void attn_dense_tile_kernel(AttnParams p, i
     }
   }
 
+  if constexpr (QW == 1 && sizeof(OT) == 2) {
+    // 16-bit output through LDS, so that the stores are whole rows: the wave
+    // writes its [16 heads][HD] block to its own LDS slice (every wave is past
+    // its last tile read: the tile loop ends with a barrier), 16-byte chunk c of
+    // head row r at chunk c ^ (r % TPR), then stores 16 bytes per lane.
+    static_assert(NWV * 16 * HD <= 2 * KC * HD, "staging fits in the tile buffers");
+    const int t = t0 + wv;
+    w[0].L = colq_sum(w[0].L);
+    const float f = w[0].finish(p.sink != nullptr, (p.sink && n < p.nh) ? p.sink[n] : 0.f);
+    OT* stg = reinterpret_cast<OT*>(&tile[0][0]) + wv * 16 * HD;
 #pragma unroll
-  for (int u = 0; u < QW; ++u) {
-    const int t = t0 + QW * wv + u;
-    w[u].L = colq_sum(w[u].L);
-    const float f = w[u].finish(p.sink != nullptr, (p.sink && n < p.nh) ? p.sink[n] : 0.f);
-    if (t < T && n < p.nh) {
-      OT* out = static_cast<OT*>(p.out) + (((size_t)b * T + t) * p.nh + n) * HD;
+    for (int tt = 0; tt < W::NT; ++tt) {
+      const int c = 2 * tt + (q4 >> 1);
+      Store4<OT>::run(stg + n * HD + 8 * (c ^ (n & (TPR - 1))) + 4 * (q4 & 1), w[0].o[tt], f);
+    }
+    wave_lds_sync();
+    if (t < T) {
+      OT* out = static_cast<OT*>(p.out) + ((size_t)b * T + t) * p.nh * HD;
 #pragma unroll
-      for (int tt = 0; tt < W::NT; ++tt) Store4<OT>::run(out + 16 * tt + 4 * q4, w[u].o[tt], f);
+      for (int i = 0; i < 16 * TPR / 64; ++i) {
+        const int r = i * (64 / TPR) + lane / TPR, c = lane % TPR;
+        if (r < p.nh)
+          *reinterpret_cast<uint4*>(out + r * HD + 8 * c) =
+              *reinterpret_cast<const uint4*>(stg + r * HD + 8 * (c ^ (r & (TPR - 1))));
+      }
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < QW; ++u) {
+      const int t = t0 + QW * wv + u;
+      w[u].L = colq_sum(w[u].L);
+      const float f = w[u].finish(p.sink != nullptr, (p.sink && n < p.nh) ? p.sink[n] : 0.f);
+      if (t < T && n < p.nh) {
+        OT* out = static_cast<OT*>(p.out) + (((size_t)b * T + t) * p.nh + n) * HD;
+#pragma unroll
+        for (int tt = 0; tt < W::NT; ++tt) Store4<OT>::run(out + 16 * tt + 4 * q4, w[u].o[tt], f);
+      }
     }
   }
 }
 
+// Query-tile shape: QW queries per wave, NWV waves per workgroup, at least
+// MINB workgroups per CU.
+constexpr int kTileQW = 1, kTileWaves = 8, kTileMinBlocks = 2;
+
 template <int HD>
 static hipError_t launch_dense_tile(const AttnParams& p, int qdtype, int odtype, hipStream_t s) {
-  constexpr int QW = 2, QG = 4 * QW;
+  constexpr int QW = kTileQW, NWV = kTileWaves, MINB = kTileMinBlocks, QG = NWV * QW;
   const long long ntile = (long long)p.B * ((p.T + QG - 1) / QG);
   const long long ngroup = (ntile + kTileGroup - 1) / kTileGroup;
-  const dim3 grid((unsigned)(((ngroup + 7) / 8) * 8 * kTileGroup)), block(256);
+  const dim3 grid((unsigned)(((ngroup + 7) / 8) * 8 * kTileGroup)), block(64 * NWV);
 #define KCH_TILE_LAUNCH(QT, OT) \
-  hipLaunchKernelGGL((attn_dense_tile_kernel<HD, QW, QT, OT>), grid, block, 0, s, p, (int)ntile)
+  hipLaunchKernelGGL((attn_dense_tile_kernel<HD, QW, NWV, MINB, QT, OT>), grid, block, 0, s, p, (int)ntile)
   if (qdtype == DT_BF16) {
     if (odtype == DT_F32) KCH_TILE_LAUNCH(bf16_t, float);
     else KCH_TILE_LAUNCH(bf16_t, bf16_t);

@@ -282,6 +282,7 @@ def _hca_attn_ref(q, kv, loc, sink, m, win, scale):
     (128, 3, 33, 0, 4, 16, "bf16", "fp32"),    # no compressed block
     (64, 16, 50, 12, 4, 0, "bf16", "bf16"),    # no window
     (128, 16, 130, 40, 3, 64, "fp16", "fp16"),  # several key tiles, fp16 queries
+    (64, 5, 21, 3, 5, 8, "bf16", "bf16"),      # head count below 16, 16-bit output rows
 ])
 def test_hca_attn_abi_shapes(dev, hd, nh, T, nb, m, win, qdt, odt):
     """kch_hca_attn over ragged shapes: query tiles cut by T, head counts below 16,
