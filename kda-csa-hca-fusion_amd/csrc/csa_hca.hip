@@ -442,7 +442,7 @@ __global__ __launch_bounds__(64 * NWV, MINB) void attn_dense_tile_kernel(AttnPar
   using W = MqaWave<HD>;
   constexpr int NTH = 64 * NWV;         // threads per workgroup
   constexpr int QG = NWV * QW;          // queries per workgroup
-  constexpr int KC = 64;                // key rows per LDS tile
+  constexpr int KC = 128;               // key rows per LDS tile
   constexpr int TPR = HD / 8;           // 16-byte chunks per row
   constexpr int RSTEP = NTH / TPR;      // rows per load pass of the workgroup
   constexpr int NLD = KC / RSTEP;       // loads per thread per tile
@@ -481,6 +481,31 @@ __global__ __launch_bounds__(64 * NWV, MINB) void attn_dense_tile_kernel(AttnPar
   }
   const int R = nc + nw;
 
+  // Tile loads: thread tid takes 16-byte chunk tid % TPR of rows
+  // tid / TPR + RSTEP i. Row j of the union is row j of kvb below nc, else
+  // row j of lcb (window position wlo + j - nc); past R, row R - 1 again
+  // (loaded, never read).
+  const int lrow = tid / TPR, lch = tid % TPR;
+  const int soff = lrow * HD + 8 * (lch ^ tile_swz<HD>(lrow & 15));
+  const bf16_t* kvb = kv + 8 * lch;
+  const bf16_t* lcb = loc ? loc + (long long)(wlo - nc) * HD + 8 * lch : kvb;
+  auto src_of = [&](int j) -> const bf16_t* {
+    const int jj = min(j, R - 1);
+    return (jj < nc ? kvb : lcb) + (size_t)(unsigned)jj * HD;
+  };
+  // named registers (an indexed array of them ends up in scratch memory)
+  uint4 pf0, pf1, pf2, pf3;
+  auto issue = [&](int c) {
+    pf0 = *reinterpret_cast<const uint4*>(src_of(c * KC + lrow));
+    if constexpr (NLD >= 2) pf1 = *reinterpret_cast<const uint4*>(src_of(c * KC + lrow + RSTEP));
+    if constexpr (NLD == 4) {
+      pf2 = *reinterpret_cast<const uint4*>(src_of(c * KC + lrow + 2 * RSTEP));
+      pf3 = *reinterpret_cast<const uint4*>(src_of(c * KC + lrow + 3 * RSTEP));
+    }
+  };
+  // the first tile's rows are in flight while the queries load
+  if (R > 0) issue(0);
+
   // This wave's queries and, per query, its rows: [0, a) and [lo, hi].
   W w[QW];
   int a_[QW], lo_[QW], hi_[QW];
@@ -501,18 +526,6 @@ __global__ __launch_bounds__(64 * NWV, MINB) void attn_dense_tile_kernel(AttnPar
   }
 
   if (R > 0) {
-    // Tile loads: thread tid takes 16-byte chunk tid % TPR of rows
-    // tid / TPR + RSTEP i. Row j of the union is row j of kvb below nc, else
-    // row j of lcb (window position wlo + j - nc); past R, row R - 1 again
-    // (loaded, never read).
-    const int lrow = tid / TPR, lch = tid % TPR;
-    const int soff = lrow * HD + 8 * (lch ^ tile_swz<HD>(lrow & 15));
-    const bf16_t* kvb = kv + 8 * lch;
-    const bf16_t* lcb = loc ? loc + (long long)(wlo - nc) * HD + 8 * lch : kvb;
-    auto src_of = [&](int j) -> const bf16_t* {
-      const int jj = min(j, R - 1);
-      return (jj < nc ? kvb : lcb) + (size_t)(unsigned)jj * HD;
-    };
     // Per-lane LDS offsets (elements) within a 16-row slice. Key fragment s:
     // row n, chunk (4s + q) ^ swz(n) = 4 (s ^ (swz >> 2)) + (q ^ (swz & 3));
     // V^T read t: row 4q + n / 4, half-chunk 2t + n % 4 / 2 of chunk
@@ -613,16 +626,6 @@ __global__ __launch_bounds__(64 * NWV, MINB) void attn_dense_tile_kernel(AttnPar
     };
 
     const int nct = (R + KC - 1) / KC;
-    // named registers (an indexed array of them ends up in scratch memory)
-    uint4 pf0, pf1, pf2, pf3;
-    auto issue = [&](int c) {
-      pf0 = *reinterpret_cast<const uint4*>(src_of(c * KC + lrow));
-      if constexpr (NLD >= 2) pf1 = *reinterpret_cast<const uint4*>(src_of(c * KC + lrow + RSTEP));
-      if constexpr (NLD == 4) {
-        pf2 = *reinterpret_cast<const uint4*>(src_of(c * KC + lrow + 2 * RSTEP));
-        pf3 = *reinterpret_cast<const uint4*>(src_of(c * KC + lrow + 3 * RSTEP));
-      }
-    };
     auto store = [&](bf16_t* dst) {
       *reinterpret_cast<uint4*>(dst + soff) = pf0;
       if constexpr (NLD >= 2) *reinterpret_cast<uint4*>(dst + soff + RSTEP * HD) = pf1;
@@ -641,7 +644,6 @@ __global__ __launch_bounds__(64 * NWV, MINB) void attn_dense_tile_kernel(AttnPar
       store(nxt);
       __syncthreads();
     };
-    issue(0);
     store(tile[0]);
     __syncthreads();
     // two tiles per iteration, so that each LDS buffer address is static
