@@ -6,24 +6,30 @@
 //   ops_hca.py:135,141,154).
 // * MqaWave: one wave computes the joint-softmax MQA output of ONE query
 //   (up to 16 heads of head dim HD) over a list of shared key/value rows,
-//   fed 16 keys at a time. Scores, masking, the running max / sum and the
+//   fed 32 keys at a time. Scores, masking, the running max / sum and the
 //   sink follow ops_csa.py:1126-1149 / ops_hca.py:166-186:
 //       p_i = exp(s_i) / (sum_valid exp(s_j) + exp(sink))   (sink present)
 //       p_i = softmax over the valid keys                   (no sink)
 //   and an output of 0 when no key is valid.
 //
 // MQA layout (lane l, q = l >> 4, n = l & 15):
-//   S^T = K Q^T with v_mfma_f32_16x16x32_bf16: A = 16 key rows (row-major, the
-//   lane reads 8 dims of key n), B = Q stored [head][dim]. The accumulator holds
-//   keys 4q..4q+3 of head n, which is exactly the B operand layout of the
-//   16x16x16 MFMA in O^T = V^T P^T (k = keys), so P never leaves the lane.
-//   V^T fragments (4 keys of one dim) are read from a wave-private LDS copy of
-//   the 16 rows with the transposing LDS read (one instruction per tile).
-//   O^T tile t holds dims 16t + 4q..4q+3 of head n.
-// Softmax reference: M (per head) trails the running max by at most 8 in
-// log2 units; o and L are rescaled only when a chunk exceeds that, and the
-// final o / L (with the sink term taken relative to the same M) is the same
-// quotient.
+//   S^T = K Q^T with v_mfma_f32_16x16x32_bf16 per 16 keys: A = 16 key rows
+//   (the lane reads 8 dims of key n), B = Q stored [head][dim]. The
+//   accumulator holds keys 4q..4q+3 of head n. O^T = V^T P^T takes 32 keys per
+//   v_mfma_f32_16x16x32_bf16 (the 16x16x16 form runs at half its rate on
+//   gfx950): k slot 8q + i holds key 4q + i (i < 4) of the first 16 keys and
+//   key 16 + 4q + i - 4 (i >= 4) of the second, which is where the two S^T
+//   accumulators leave them, so P never leaves the lane. V^T fragments are
+//   read with the gfx950 transposing LDS read from a swizzled LDS copy of the
+//   rows (tile_swz), two reads per O^T tile. O^T tile t holds dims
+//   16t + 4q..4q+3 of head n.
+// Softmax reference: M (per head) starts at a finite floor and trails the
+// running max by at most 8 in log2 units: o and L are rescaled only when a
+// score exceeds M + 8 (a compare against a threshold on the raw score), so
+// p = exp2(s - M) <= 2^8 and a masked score (-inf) gives p = 0 without a
+// guard. Each lane sums its own keys' p; finalize() totals the four lanes of a
+// head. The final o / L (with the sink term taken relative to the same M) is
+// the same quotient as with the exact running max.
 #pragma once
 
 #include "kch_device.h"
@@ -32,13 +38,10 @@ namespace kch {
 
 constexpr float kLog2eF = 1.4426950408889634f;
 constexpr float kRescaleLog2 = 8.f;  // MqaWave: slack of the softmax reference point
-// Initial reference point of the query-tile kernel: finite, so exp2(s - M) of a
-// masked score (-inf) is 0 without a guard; any finite score exceeds it by far
-// more than kRescaleLog2, so the first valid key always resets M.
+// Initial reference point of MqaWave: finite, so exp2(s - M) of a masked score
+// (-inf) is 0 without a guard; any finite score exceeds it by far more than
+// kRescaleLog2, so the first valid key always resets M.
 constexpr float kMFloor = -1e30f;
-
-// max without NaN canonicalisation (operands are never NaN here)
-__device__ __forceinline__ float fmax_nc(float a, float b) { return __builtin_amdgcn_fmed3f(a, b, INFINITY); }
 
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m); }
 
@@ -110,18 +113,99 @@ __device__ __forceinline__ bf16x8 to_bf16x8(const float* f) {
   return r;
 }
 
+// LDS tiles of rows of HD bf16 (row stride HD, no padding): the 16-byte chunk
+// c of row r sits at chunk c ^ tile_swz(r % 16). The swizzle keeps free of
+// bank conflicts the row writes (16 lanes, one chunk of 16 consecutive rows,
+// or one row's chunks by consecutive lanes), the key-fragment reads (the
+// same pattern) and the transposing V^T reads (32 lanes: two adjacent chunks
+// of 8 consecutive rows).
+template <int HD>
+__device__ __forceinline__ int tile_swz(int r) {
+  if constexpr (HD == 128) return ((r & 7) << 1) | ((r >> 3) & 1);
+  else return (((r >> 1) & 3) << 1) | ((r >> 3) & 1);  // 128-byte rows: two rows per bank sweep
+}
+
+// This lane's element offsets into a 16-row slice of a swizzled tile. Key
+// fragment s (row n, chunk 4s + q) sits at chunk
+// (4s + q) ^ swz(n) = 4 (s ^ (swz >> 2)) + (q ^ (swz & 3)); V^T read t (row
+// 4q + n / 4, half-chunk 2t + (n % 4) / 2) at chunk
+// (2t + h) ^ swz = 2 (t ^ (swz >> 1)) + (h ^ (swz & 1)). The s and t terms only
+// flip bits of their own, so the offsets are kbase ^ (s << 5), vbase ^ (t << 4).
+template <int HD>
+struct TileOffsets {
+  int kbase, vbase;
+  __device__ __forceinline__ TileOffsets() {
+    const int l = lane_id(), q = l >> 4, n = l & 15;
+    const int ksw = tile_swz<HD>(n);
+    const int vr = 4 * q + (n >> 2);
+    const int vsw = tile_swz<HD>(vr);
+    kbase = n * HD + 8 * (q ^ (ksw & 3)) + 32 * (ksw >> 2);
+    vbase = vr * HD + 8 * (((n >> 1) & 1) ^ (vsw & 1)) + 16 * (vsw >> 1) + 4 * (n & 1);
+  }
+  __device__ __forceinline__ int key(int s) const { return kbase ^ (s << 5); }
+  __device__ __forceinline__ int vt(int t) const { return vbase ^ (t << 4); }
+};
+
+template <typename T> struct Store4;
+template <> struct Store4<float> {
+  static __device__ __forceinline__ void run(float* p, f32x4 v, float f) {
+    *reinterpret_cast<float4*>(p) = make_float4(v[0] * f, v[1] * f, v[2] * f, v[3] * f);
+  }
+};
+template <> struct Store4<bf16_t> {
+  static __device__ __forceinline__ void run(bf16_t* p, f32x4 v, float f) {
+    const bf16x4 r = {(bf16_t)(v[0] * f), (bf16_t)(v[1] * f), (bf16_t)(v[2] * f), (bf16_t)(v[3] * f)};
+    *reinterpret_cast<bf16x4*>(p) = r;
+  }
+};
+template <> struct Store4<_Float16> {
+  static __device__ __forceinline__ void run(_Float16* p, f32x4 v, float f) {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    const h4 r = {(_Float16)(v[0] * f), (_Float16)(v[1] * f), (_Float16)(v[2] * f), (_Float16)(v[3] * f)};
+    *reinterpret_cast<h4*>(p) = r;
+  }
+};
+
+// Stores o * f of one query (heads [0, nh), row-major [nh][HD] of OT at out)
+// as whole rows: the wave writes its 16 x HD block to `buf` (its own LDS, at
+// least 16 * HD * sizeof(OT) bytes, 16-byte aligned), 16-byte chunk c of head
+// row r at chunk c ^ (r % CPR), then each lane stores 16-byte chunks.
+template <int HD, typename OT>
+__device__ __forceinline__ void store_rows(const f32x4 (&o)[HD / 16], float f, OT* out, int nh,
+                                           void* buf) {
+  constexpr int CPR = HD * (int)sizeof(OT) / 16;  // 16-byte chunks per row
+  constexpr int EPC = 16 / (int)sizeof(OT);       // elements per chunk
+  const int l = lane_id(), q = l >> 4, n = l & 15;
+  OT* sb = static_cast<OT*>(buf);
+#pragma unroll
+  for (int t = 0; t < HD / 16; ++t) {
+    const int e0 = 16 * t + 4 * q;                 // first of the lane's 4 dims
+    const int c = e0 / EPC;
+    Store4<OT>::run(sb + n * HD + EPC * (c ^ (n & (CPR - 1))) + e0 % EPC, o[t], f);
+  }
+  wave_lds_sync();
+#pragma unroll
+  for (int i = 0; i < 16 * CPR / 64; ++i) {
+    const int r = i * (64 / CPR) + l / CPR, c = l % CPR;
+    if (r < nh)
+      *reinterpret_cast<uint4*>(out + r * HD + EPC * c) =
+          *reinterpret_cast<const uint4*>(sb + r * HD + EPC * (c ^ (r & (CPR - 1))));
+  }
+}
+
 // One wave, one query, up to 16 heads of head dim HD (64 or 128).
 template <int HD>
 struct MqaWave {
-  static constexpr int NS = HD / 32;   // 32-wide k steps of S^T
-  static constexpr int NT = HD / 16;   // O^T tiles
-  static constexpr int LDS_LD = HD + 8;  // staging row stride (bf16)
-  static constexpr int STAGE_BYTES = 16 * LDS_LD * 2;
+  static constexpr int NS = HD / 32;          // 32-wide k steps of S^T
+  static constexpr int NT = HD / 16;          // O^T tiles
+  static constexpr int STAGE_ELEMS = 32 * HD;  // bf16 of a 32-row stage (chunk2)
 
-  bf16x8 qf[NS];  // Q fragments: head n, dims 8q + 32s
+  bf16x8 qf[NS];  // Q fragments: head n, dims 8q + 32s (sign of the scale folded in)
   f32x4 o[NT];
-  float M, L;     // softmax reference point (log2 units) and sum of head n
-  float qscale2;  // score scale * log2(e)
+  float M;        // softmax reference point of head n (log2 units), finite
+  float L;        // sum of p over this lane's keys (finalize(): over the head)
+  float qscale2;  // |score scale| * log2(e), > 0
+  float thr;      // (M + kRescaleLog2) / qscale2: a raw score above it moves M
 
   // q_row: this lane's head row (nullptr for a padding head -> zeros);
   // normalise: L2-normalise each head row (4 lanes share a head).
@@ -129,7 +213,6 @@ struct MqaWave {
   __device__ __forceinline__ void init(const QT* q_row, bool normalise, float scale) {
     const int q = lane_id() >> 4;
     float f[NS][8];
-    float ss = 0.f;
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       if (q_row) Load8<QT>::run(q_row + 32 * s + 8 * q, f[s]);
@@ -137,45 +220,32 @@ struct MqaWave {
 #pragma unroll
         for (int i = 0; i < 8; ++i) f[s][i] = 0.f;
       }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) ss += f[s][i] * f[s][i];
     }
-    float inv = 1.f;
-    if (normalise) inv = l2_inv(colq_sum(ss));
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) f[s][i] *= inv;
-      qf[s] = to_bf16x8(f[s]);
-    }
-#pragma unroll
-    for (int t = 0; t < NT; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    M = -INFINITY;
-    L = 0.f;
-    qscale2 = scale * kLog2eF;
+    setup(f, normalise, scale);
   }
-
-  // As init, for the query-tile kernel: the row is always readable (`keep`
-  // false, for a padding head or query, zeroes it after the load, so the load
-  // is not conditional); the sign of `scale` is folded into the fragments so
-  // that qscale2 >= 0; M starts at a finite floor (kMFloor) instead of -inf.
+  // As init, for a row that is always readable: `keep` false (a padding head
+  // or query) zeroes it after the load, so that the load is not conditional.
   template <typename QT>
   __device__ __forceinline__ void init_always(const QT* q_row, bool keep, bool normalise, float scale) {
     const int q = lane_id() >> 4;
     float f[NS][8];
-    float ss = 0.f;
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       Load8<QT>::run(q_row + 32 * s + 8 * q, f[s]);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        f[s][i] = keep ? f[s][i] : 0.f;
-        ss += f[s][i] * f[s][i];
-      }
+      for (int i = 0; i < 8; ++i) f[s][i] = keep ? f[s][i] : 0.f;
     }
+    setup(f, normalise, scale);
+  }
+  __device__ __forceinline__ void setup(float (&f)[NS][8], bool normalise, float scale) {
+    float ss = 0.f;
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss += f[s][i] * f[s][i];
     float inv = 1.f;
     if (normalise) inv = l2_inv(colq_sum(ss));
-    if (scale < 0.f) inv = -inv;
+    if (scale < 0.f) inv = -inv;  // scores times |scale| from here on
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
 #pragma unroll
@@ -186,7 +256,58 @@ struct MqaWave {
     for (int t = 0; t < NT; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
     M = kMFloor;
     L = 0.f;
-    qscale2 = fabsf(scale) * kLog2eF;
+    qscale2 = fmaxf(fabsf(scale) * kLog2eF, 1e-30f);  // -inf * qscale2 stays -inf
+    thr = (M + kRescaleLog2) / qscale2;
+  }
+
+  // S^T accumulator of 16 key rows whose fragments are k (row n of the lane).
+  __device__ __forceinline__ f32x4 scores(const bf16x8 (&k)[NS]) const {
+    f32x4 st = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < NS; ++s) st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k[s], qf[s], st, 0, 0, 0);
+    return st;
+  }
+
+  // Softmax step and O^T update over 32 keys: sc = this lane's raw scores of
+  // keys 4q..4q+3 and 16+4q..16+4q+3 (-inf = masked), `rows` the 32 key rows in
+  // a swizzled LDS tile (the V^T source), visible to this wave.
+  __device__ __forceinline__ void accumulate32(const float (&sc)[8], const bf16_t* rows,
+                                               const TileOffsets<HD>& to) {
+    bool up = false;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) up |= sc[e] > thr;
+    if (__ballot(up)) {
+      float mx = sc[0];
+#pragma unroll
+      for (int e = 1; e < 8; ++e) mx = fmaxf(mx, sc[e]);
+      const float mnew = fmaxf(M, colq_max(mx) * qscale2);
+      const float alpha = fast_exp2(M - mnew);
+      L *= alpha;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) o[t] *= alpha;
+      M = mnew;
+      thr = (mnew + kRescaleLog2) / qscale2;
+    }
+    typedef float f32x8 __attribute__((ext_vector_type(8)));
+    f32x8 pe;
+    const float nm = -M;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pe[e] = fast_exp2(fmaf(sc[e], qscale2, nm));
+    L += ((pe[0] + pe[1]) + (pe[2] + pe[3])) + ((pe[4] + pe[5]) + (pe[6] + pe[7]));
+    const bf16x8 pb = __builtin_convertvector(pe, bf16x8);
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      // V^T fragment (16 dims x 32 keys): column 16t + n of rows 4q .. 4q + 3
+      // of each 16-row slice, one transposing read per slice
+      const int vo = to.vt(t);
+      const s16x4 r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4*)(rows + vo));
+      const s16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s16x4*)(rows + 16 * HD + vo));
+      const bf16x8 va = __builtin_bit_cast(bf16x8, __builtin_shufflevector(r0, r1, 0, 1, 2, 3, 4, 5, 6, 7));
+      o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, o[t], 0, 0, 0);
+    }
   }
 
   // Fragments of 16 key rows: this lane's key row (key n = lane & 15) at dims
@@ -200,75 +321,39 @@ struct MqaWave {
     for (int s = 0; s < NS; ++s) f.k[s] = *reinterpret_cast<const bf16x8*>(row + 32 * s + 8 * q);
   }
 
-  // Consume 16 keys. `row` is this lane's key row (key n = lane & 15), valid
-  // for every lane (point invalid keys at any readable row); `valid16` has bit
-  // k set when key k of the chunk is valid. `stage` is this wave's LDS buffer.
-  __device__ __forceinline__ void chunk(const bf16_t* row, unsigned valid16, bf16_t* stage) {
-    Frag f;
-    load(f, row);
-    chunk(f, valid16, stage);
-  }
-
-  // Consume 16 keys already loaded into registers.
-  __device__ __forceinline__ void chunk(const Frag& f, unsigned valid16, bf16_t* stage) {
-    const int l = lane_id();
-    const int q = l >> 4, n = l & 15;
-    // previous chunk's V^T reads by this wave are complete before the overwrite
-    wave_lds_sync();
+  // Consume 32 keys already in registers: fa keys 0..15, fb keys 16..31; bit
+  // k of valid32 set when key k is valid. `stage` is this wave's LDS buffer of
+  // STAGE_ELEMS (the V^T source).
+  __device__ __forceinline__ void chunk2(const Frag& fa, const Frag& fb, unsigned valid32,
+                                         bf16_t* stage, const TileOffsets<HD>& to) {
+    const int q = lane_id() >> 4;
+    wave_lds_sync();  // the previous step's V^T reads are done before the overwrite
 #pragma unroll
-    for (int s = 0; s < NS; ++s) *reinterpret_cast<bf16x8*>(stage + n * LDS_LD + 32 * s + 8 * q) = f.k[s];
-    f32x4 st = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < NS; ++s) st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.k[s], qf[s], st, 0, 0, 0);
-    float sv[4];
-    float cm = -INFINITY;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const bool ok = (valid16 >> (4 * q + e)) & 1u;
-      sv[e] = ok ? st[e] * qscale2 : -INFINITY;
-      cm = fmaxf(cm, sv[e]);
+    for (int s = 0; s < NS; ++s) {
+      *reinterpret_cast<bf16x8*>(stage + to.key(s)) = fa.k[s];
+      *reinterpret_cast<bf16x8*>(stage + 16 * HD + to.key(s)) = fb.k[s];
     }
-    cm = colq_max(cm);
-    // M is a reference point, not necessarily the running max: o and L are
-    // rescaled only when some head's chunk max exceeds its M by more than 8
-    // (log2 units), so p <= 2^8 and most chunks skip the rescale.
-    if (__ballot(cm > M + kRescaleLog2)) {
-      const float mnew = fmaxf(M, cm);
-      const float alpha = mnew == -INFINITY ? 1.f : fast_exp2(M - mnew);  // M = -inf -> 0
-      L = L * alpha;
+    const f32x4 sa = scores(fa.k), sb = scores(fb.k);
+    float sc[8] = {sa[0], sa[1], sa[2], sa[3], sb[0], sb[1], sb[2], sb[3]};
+    if (valid32 != 0xffffffffu) {
 #pragma unroll
-      for (int t = 0; t < NT; ++t) o[t] *= alpha;
-      M = mnew;
+      for (int e = 0; e < 4; ++e) {
+        if (!((valid32 >> (4 * q + e)) & 1u)) sc[e] = -INFINITY;
+        if (!((valid32 >> (16 + 4 * q + e)) & 1u)) sc[4 + e] = -INFINITY;
+      }
     }
-    float p[4];
-    float ps = 0.f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      p[e] = sv[e] == -INFINITY ? 0.f : fast_exp2(sv[e] - M);  // M is finite when sv is
-      ps += p[e];
-    }
-    L += colq_sum(ps);
-    bf16x4 pb = {(bf16_t)p[0], (bf16_t)p[1], (bf16_t)p[2], (bf16_t)p[3]};
     wave_lds_sync();  // staged rows visible to the whole wave
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      // V^T fragment: rows 4q .. 4q + 3, column 16t + n. The gfx950 transposing
-      // read does it in one instruction: the 16 lanes of a row group each read
-      // 8 bytes (row 4q + n / 4, columns 16t + 4 (n % 4) .. + 3) and lane n
-      // receives column 16t + n of the 4 rows.
-      typedef short s16x4 __attribute__((ext_vector_type(4)));
-      const bf16_t* src = stage + (4 * q + (n >> 2)) * LDS_LD + 16 * t + 4 * (n & 3);
-      const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) s16x4*)(src));
-      const bf16x4 va = __builtin_bit_cast(bf16x4, r);
-      o[t] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, o[t], 0, 0, 0);
-    }
+    accumulate32(sc, stage, to);
   }
 
-  // Final normalisation. Returns the multiplier for o (0 when nothing valid).
+  // Totals L over the 4 lanes of each head; call once, after the last step.
+  __device__ __forceinline__ void finalize() { L = colq_sum(L); }
+
+  // Final normalisation (after finalize). Returns the multiplier for o (0 when
+  // nothing is valid).
   __device__ __forceinline__ float finish(bool has_sink, float sink) const {
     float denom = L;
-    if (has_sink) denom += fast_exp2(sink * kLog2eF - M);  // M = -inf -> +inf
+    if (has_sink) denom += fast_exp2(sink * kLog2eF - M);
     return (L > 0.f) ? 1.f / denom : 0.f;
   }
 };

@@ -25,7 +25,6 @@ namespace kch {
 
 namespace {
 
-template <typename T> __device__ __forceinline__ void st_val(T* p, float v) { *p = from_f32<T>(v); }
 
 }  // namespace
 
@@ -297,7 +296,8 @@ hipError_t compress_dispatch(const CompressParams& p, int dtype, hipStream_t str
 template <int HD, typename QT, typename OT, bool SPARSE>
 __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(AttnParams p) {
   using W = MqaWave<HD>;
-  __shared__ __attribute__((aligned(16))) bf16_t stage_all[4][16 * W::LDS_LD];
+  __shared__ __attribute__((aligned(16))) bf16_t stage_all[4][W::STAGE_ELEMS];
+  static_assert(16 * HD * sizeof(OT) <= sizeof(stage_all[0]), "output rows fit in the stage");
   const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
   const int n = lane & 15;
@@ -354,9 +354,10 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(AttnParams p) {
       }
       return row;
     };
-    // groups of 4 chunks, four chunks in flight; refills are unconditional (past
-    // the end they read the default row, masked off) so that no loaded register
-    // is copied
+    // groups of 4 chunks (two 32-key steps), four chunks in flight; refills are
+    // unconditional (past the end they read the default row, masked off) so
+    // that no loaded register is copied
+    const TileOffsets<HD> to;
     typename W::Frag fr[4];
     unsigned vm[4];
     const int nch = (n_tot + 15) / 16;
@@ -373,25 +374,23 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(AttnParams p) {
     for (int g = 0; g < ng; ++g) {
       const int ig2 = idx_group(g + 2);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        if (vm[c]) w.chunk(fr[c], vm[c], stage);
-        bool ok;
-        const bf16_t* row = row_of(4 * (g + 1) + c, ig1, ok);
-        vm[c] = (unsigned)__ballot(ok && lane < 16) & 0xffffu;
-        W::load(fr[c], row);
+      for (int c = 0; c < 4; c += 2) {
+        if (vm[c] | vm[c + 1]) w.chunk2(fr[c], fr[c + 1], vm[c] | (vm[c + 1] << 16), stage, to);
+#pragma unroll
+        for (int d = c; d < c + 2; ++d) {
+          bool ok;
+          const bf16_t* row = row_of(4 * (g + 1) + d, ig1, ok);
+          vm[d] = (unsigned)__ballot(ok && lane < 16) & 0xffffu;
+          W::load(fr[d], row);
+        }
       }
       ig1 = ig2;
     }
   }
+  w.finalize();
   const float f = w.finish(p.sink != nullptr, (p.sink && n < p.nh) ? p.sink[n] : 0.f);
-  if (n < p.nh) {
-    OT* out = static_cast<OT*>(p.out) + ((size_t)qi * p.nh + n) * HD;
-    const int q4 = 4 * (lane >> 4);
-#pragma unroll
-    for (int tt = 0; tt < W::NT; ++tt)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) st_val<OT>(out + 16 * tt + q4 + e, w.o[tt][e] * f);
-  }
+  wave_lds_sync();  // the last step's V^T reads are done before the stage is reused
+  store_rows<HD, OT>(w.o, f, static_cast<OT*>(p.out) + (size_t)qi * p.nh * HD, p.nh, stage);
 }
 
 // ---------------------------------------------------------------------------
@@ -409,32 +408,6 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(AttnParams p) {
 // key fragments (16 lanes read chunk c of 16 consecutive rows) and the
 // transposing V^T reads (32 lanes read two adjacent chunks of 8 rows).
 // ---------------------------------------------------------------------------
-template <int HD>
-__device__ __forceinline__ int tile_swz(int r) {
-  if constexpr (HD == 128) return ((r & 7) << 1) | ((r >> 3) & 1);
-  else return (((r >> 1) & 3) << 1) | ((r >> 3) & 1);  // 128-byte rows: two rows per bank sweep
-}
-
-template <typename T> struct Store4;
-template <> struct Store4<float> {
-  static __device__ __forceinline__ void run(float* p, f32x4 v, float f) {
-    *reinterpret_cast<float4*>(p) = make_float4(v[0] * f, v[1] * f, v[2] * f, v[3] * f);
-  }
-};
-template <> struct Store4<bf16_t> {
-  static __device__ __forceinline__ void run(bf16_t* p, f32x4 v, float f) {
-    const bf16x4 r = {(bf16_t)(v[0] * f), (bf16_t)(v[1] * f), (bf16_t)(v[2] * f), (bf16_t)(v[3] * f)};
-    *reinterpret_cast<bf16x4*>(p) = r;
-  }
-};
-template <> struct Store4<_Float16> {
-  static __device__ __forceinline__ void run(_Float16* p, f32x4 v, float f) {
-    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-    const h4 r = {(_Float16)(v[0] * f), (_Float16)(v[1] * f), (_Float16)(v[2] * f), (_Float16)(v[3] * f)};
-    *reinterpret_cast<h4*>(p) = r;
-  }
-};
-
 constexpr int kTileGroup = 16;  // consecutive query tiles kept on one XCD
 
 template <int HD, int QW, int NWV, int MINB, typename QT, typename OT>
@@ -449,8 +422,6 @@ __global__ __launch_bounds__(64 * NWV, MINB) void attn_dense_tile_kernel(AttnPar
   static_assert(NLD == 1 || NLD == 2 || NLD == 4, "tile loads per thread");
   static_assert(RSTEP % 16 == 0, "load rows keep their swizzle");
   typedef short s16x4 __attribute__((ext_vector_type(4)));
-  typedef short s16x8 __attribute__((ext_vector_type(8)));
-  typedef float f32x8 __attribute__((ext_vector_type(8)));
   __shared__ __attribute__((aligned(16))) bf16_t tile[2][KC * HD];
 
   // Workgroup i runs on XCD i % 8. Groups of kTileGroup consecutive tiles
@@ -526,32 +497,8 @@ __global__ __launch_bounds__(64 * NWV, MINB) void attn_dense_tile_kernel(AttnPar
   }
 
   if (R > 0) {
-    // Per-lane LDS offsets (elements) within a 16-row slice. Key fragment s:
-    // row n, chunk (4s + q) ^ swz(n) = 4 (s ^ (swz >> 2)) + (q ^ (swz & 3));
-    // V^T read t: row 4q + n / 4, half-chunk 2t + n % 4 / 2 of chunk
-    // (2t + h) ^ swz = 2 (t ^ (swz >> 1)) + (h ^ (swz & 1)). The s and t terms
-    // only flip bits of their own: the offsets are kbase ^ (s << 5) and
-    // vbase ^ (t << 4).
-    int kbase, vbase;
-    {
-      const int ksw = tile_swz<HD>(n);
-      const int vr = 4 * q4 + (n >> 2);
-      const int vsw = tile_swz<HD>(vr);
-      kbase = n * HD + 8 * (q4 ^ (ksw & 3)) + 32 * (ksw >> 2);
-      vbase = vr * HD + 8 * (((n >> 1) & 1) ^ (vsw & 1)) + 16 * (vsw >> 1) + 4 * (n & 1);
-    }
-    // Rescale threshold per query and head: a score st (before the scale)
-    // above thr = (M + kRescaleLog2) / qscale2 moves M (qscale2 >= 0).
-    float thr[QW];
-#pragma unroll
-    for (int u = 0; u < QW; ++u) thr[u] = (w[u].M + kRescaleLog2) / w[u].qscale2;
-
-    // 32 rows of the tile (LDS row base `rows`, key index j0 of row 0) for the
-    // wave's queries. Both products use v_mfma_f32_16x16x32_bf16 (the 16x16x16
-    // form runs at half its rate on gfx950). The 32 keys sit in the k slots
-    // as: slot 8q + i <-> key 4q + i (i < 4, first 16 rows) and key
-    // 16 + 4q + i - 4 (i >= 4, second 16 rows), which is where the S^T
-    // accumulators of the two 16-row slices leave them, so P never moves.
+    const TileOffsets<HD> to;
+    // 32 rows of the tile (LDS row base `rows`, key index j0 of row 0)
     auto rows32 = [&](const bf16_t* rows, int j0) {
       f32x4 sa[QW], sb[QW];
 #pragma unroll
@@ -559,22 +506,13 @@ __global__ __launch_bounds__(64 * NWV, MINB) void attn_dense_tile_kernel(AttnPar
         bf16x8 kf[W::NS];
 #pragma unroll
         for (int s2 = 0; s2 < W::NS; ++s2)
-          kf[s2] = *reinterpret_cast<const bf16x8*>(rows + 16 * HD * h + (kbase ^ (s2 << 5)));
+          kf[s2] = *reinterpret_cast<const bf16x8*>(rows + 16 * HD * h + to.key(s2));
 #pragma unroll
         for (int u = 0; u < QW; ++u) {
-          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int s2 = 0; s2 < W::NS; ++s2)
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[s2], w[u].qf[s2], acc, 0, 0, 0);
-          if (h == 0) sa[u] = acc;
-          else sb[u] = acc;
+          if (h == 0) sa[u] = w[u].scores(kf);
+          else sb[u] = w[u].scores(kf);
         }
       }
-      // Softmax of the 32 keys per query. w.L is this lane's partial sum (its 8
-      // keys), reduced over the 4 lanes of a head at the end. M (per head) only
-      // moves when some score exceeds it by more than kRescaleLog2 (the head's
-      // column max is taken only then), so p = exp2(st * qscale2 - M) <= 2^8.
-      bf16x8 pb[QW];
 #pragma unroll
       for (int u = 0; u < QW; ++u) {
         float sc[8] = {sa[u][0], sa[u][1], sa[u][2], sa[u][3], sb[u][0], sb[u][1], sb[u][2], sb[u][3]};
@@ -587,41 +525,7 @@ __global__ __launch_bounds__(64 * NWV, MINB) void attn_dense_tile_kernel(AttnPar
             sc[e] = ok ? sc[e] : -INFINITY;
           }
         }
-        bool up = false;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) up |= sc[e] > thr[u];
-        if (__ballot(up)) {
-          float mx = sc[0];
-#pragma unroll
-          for (int e = 1; e < 8; ++e) mx = fmaxf(mx, sc[e]);
-          const float mnew = fmaxf(w[u].M, colq_max(mx) * w[u].qscale2);
-          const float alpha = fast_exp2(w[u].M - mnew);
-          w[u].L *= alpha;
-#pragma unroll
-          for (int t = 0; t < W::NT; ++t) w[u].o[t] *= alpha;
-          w[u].M = mnew;
-          thr[u] = (mnew + kRescaleLog2) / w[u].qscale2;
-        }
-        const float nm = -w[u].M;
-        f32x8 pe;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) pe[e] = fast_exp2(fmaf(sc[e], w[u].qscale2, nm));
-        w[u].L += ((pe[0] + pe[1]) + (pe[2] + pe[3])) + ((pe[4] + pe[5]) + (pe[6] + pe[7]));
-        pb[u] = __builtin_convertvector(pe, bf16x8);
-      }
-#pragma unroll
-      for (int t = 0; t < W::NT; ++t) {
-        // V^T fragment (16 dims x 32 keys): column 16t + n of rows 4q .. 4q + 3
-        // of each slice, one transposing read per slice
-        const int vo = vbase ^ (t << 4);
-        const s16x4 r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4*)(rows + vo));
-        const s16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s16x4*)(rows + 16 * HD + vo));
-        const bf16x8 va = __builtin_bit_cast(bf16x8, __builtin_shufflevector(r0, r1, 0, 1, 2, 3, 4, 5, 6, 7));
-#pragma unroll
-        for (int u = 0; u < QW; ++u)
-          w[u].o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[u], w[u].o[t], 0, 0, 0);
+        w[u].accumulate32(sc, rows, to);
       }
     };
 
@@ -653,45 +557,17 @@ __global__ __launch_bounds__(64 * NWV, MINB) void attn_dense_tile_kernel(AttnPar
     }
   }
 
-  if constexpr (QW == 1 && sizeof(OT) == 2) {
-    // 16-bit output through LDS, so that the stores are whole rows: the wave
-    // writes its [16 heads][HD] block to its own LDS slice (every wave is past
-    // its last tile read: the tile loop ends with a barrier), 16-byte chunk c of
-    // head row r at chunk c ^ (r % TPR), then stores 16 bytes per lane.
-    static_assert(NWV * 16 * HD <= 2 * KC * HD, "staging fits in the tile buffers");
-    const int t = t0 + wv;
-    w[0].L = colq_sum(w[0].L);
-    const float f = w[0].finish(p.sink != nullptr, (p.sink && n < p.nh) ? p.sink[n] : 0.f);
-    OT* stg = reinterpret_cast<OT*>(&tile[0][0]) + wv * 16 * HD;
-#pragma unroll
-    for (int tt = 0; tt < W::NT; ++tt) {
-      const int c = 2 * tt + (q4 >> 1);
-      Store4<OT>::run(stg + n * HD + 8 * (c ^ (n & (TPR - 1))) + 4 * (q4 & 1), w[0].o[tt], f);
-    }
-    wave_lds_sync();
-    if (t < T) {
-      OT* out = static_cast<OT*>(p.out) + ((size_t)b * T + t) * p.nh * HD;
-#pragma unroll
-      for (int i = 0; i < 16 * TPR / 64; ++i) {
-        const int r = i * (64 / TPR) + lane / TPR, c = lane % TPR;
-        if (r < p.nh)
-          *reinterpret_cast<uint4*>(out + r * HD + 8 * c) =
-              *reinterpret_cast<const uint4*>(stg + r * HD + 8 * (c ^ (r & (TPR - 1))));
-      }
-    }
-  } else {
-#pragma unroll
-    for (int u = 0; u < QW; ++u) {
-      const int t = t0 + QW * wv + u;
-      w[u].L = colq_sum(w[u].L);
-      const float f = w[u].finish(p.sink != nullptr, (p.sink && n < p.nh) ? p.sink[n] : 0.f);
-      if (t < T && n < p.nh) {
-        OT* out = static_cast<OT*>(p.out) + (((size_t)b * T + t) * p.nh + n) * HD;
-#pragma unroll
-        for (int tt = 0; tt < W::NT; ++tt) Store4<OT>::run(out + 16 * tt + 4 * q4, w[u].o[tt], f);
-      }
-    }
-  }
+  // Output rows through LDS (whole-row stores): each wave stages its block in
+  // its own slice of the tile buffers, which every wave is done reading (the
+  // tile loop ends with a barrier; without rows it never ran).
+  static_assert(QW == 1, "one query per wave");
+  static_assert(NWV * 16 * HD * sizeof(OT) <= sizeof(tile), "staging fits in the tile buffers");
+  const int t = t0 + wv;
+  w[0].finalize();
+  const float f = w[0].finish(p.sink != nullptr, (p.sink && n < p.nh) ? p.sink[n] : 0.f);
+  if (t < T)
+    store_rows<HD, OT>(w[0].o, f, static_cast<OT*>(p.out) + ((size_t)b * T + t) * p.nh * HD, p.nh,
+                       reinterpret_cast<char*>(&tile[0][0]) + wv * 16 * HD * sizeof(OT));
 }
 
 // Query-tile shape: QW queries per wave, NWV waves per workgroup, at least

@@ -835,8 +835,8 @@ __global__ __launch_bounds__(256) void idx_merge_kernel(DecodeIdxParams p) {
 template <int HD, typename QT, typename OT>
 __global__ __launch_bounds__(256, 3) void attn_kernel(DecodeAttnParams p) {
   using W = MqaWave<HD>;
-  constexpr int D = 4;
-  constexpr int STAGE = 16 * W::LDS_LD;                 // bf16 per wave
+  constexpr int D = 4;                                  // chunks in flight (two 32-key steps)
+  constexpr int STAGE = W::STAGE_ELEMS;                 // bf16 per wave
   constexpr int MERGE = 4 * 16 * HD + 4 * 16 * 2;       // floats: o and (M, L) per wave and head
   constexpr int LDS_BYTES = (4 * STAGE * 2 > MERGE * 4) ? 4 * STAGE * 2 : MERGE * 4;
   __shared__ __attribute__((aligned(16))) char lds[LDS_BYTES];
@@ -875,6 +875,7 @@ __global__ __launch_bounds__(256, 3) void attn_kernel(DecodeAttnParams p) {
     }
     return row;
   };
+  const TileOffsets<HD> to;
   const int ncg = (jg1 - jg0 + 15) / 16;                  // chunks in the group
   const int mine = ncg > wv ? (ncg - wv + 3) / 4 : 0;      // this wave's
   typename W::Frag fr[D];
@@ -896,15 +897,19 @@ __global__ __launch_bounds__(256, 3) void attn_kernel(DecodeAttnParams p) {
   // would cost a second copy of the loop body's registers
   for (int m0 = 0; m0 < mine; m0 += D) {
 #pragma unroll
-    for (int d = 0; d < D; ++d) {
-      if (vm[d]) w.chunk(fr[d], vm[d], stage);
-      bool ok;
-      const bf16_t* row = row_of(m0 + d + D, ix[d], ok);
-      vm[d] = (unsigned)__ballot(ok && lane < 16) & 0xffffu;
-      W::load(fr[d], row);
-      ix[d] = idx_of(m0 + d + 2 * D);
+    for (int d0 = 0; d0 < D; d0 += 2) {
+      if (vm[d0] | vm[d0 + 1]) w.chunk2(fr[d0], fr[d0 + 1], vm[d0] | (vm[d0 + 1] << 16), stage, to);
+#pragma unroll
+      for (int d = d0; d < d0 + 2; ++d) {
+        bool ok;
+        const bf16_t* row = row_of(m0 + d + D, ix[d], ok);
+        vm[d] = (unsigned)__ballot(ok && lane < 16) & 0xffffu;
+        W::load(fr[d], row);
+        ix[d] = idx_of(m0 + d + 2 * D);
+      }
     }
   }
+  w.finalize();
 
   // ---- merge the 4 waves: thread t -> head t / (HD / 8), dims 8 (t % (HD / 8)) ----
   __syncthreads();  // staging buffers are free
