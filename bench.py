@@ -83,22 +83,35 @@ def kda_algorithmic(B, T, H, K, V, C=64):
     return flops, bytes_
 
 
-def time_steps(fn, steps, warmup):
+def time_steps(fn, steps, warmup, per_step=False):
+    """Mean ms per step over ``steps`` back-to-back steps, bracketed by one pair of
+    HIP events on the current stream with a synchronize on both sides (no event
+    packets between the steps). With ``per_step`` a second, separate pass records
+    an event pair around every step for the median."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(steps)]
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    for a, b in ev:
-        a.record(stream)
+    e0.record(stream)
+    for _ in range(steps):
         fn()
-        b.record(stream)
+    e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    per = [a.elapsed_time(b) for a, b in ev]
-    return float(np.mean(per)), float(np.median(per)), wall
+    mean = e0.elapsed_time(e1) / steps
+    med = mean
+    if per_step:
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(steps)]
+        for a, b in ev:
+            a.record(stream)
+            fn()
+            b.record(stream)
+        torch.cuda.synchronize()
+        med = float(np.median([a.elapsed_time(b) for a, b in ev]))
+    return float(mean), med, wall
 
 
 def cpu_baseline_kda(host, s0, B, T, H):
@@ -355,8 +368,9 @@ def bench_decode_bw(dev, reps=5):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=50)
+    # the first tens of steps after idle run at lower clocks (~10% slower at C1)
+    ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--headline-only", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -384,7 +398,7 @@ def main():
     def step():
         return kch.naive_chunk_kda(*xs, initial_state=s0, output_final_state=True)
 
-    ms_mean, ms_med, _ = time_steps(step, args.steps, args.warmup)
+    ms_mean, ms_med, _ = time_steps(step, args.steps, args.warmup, per_step=True)
     _log(f"kda C1: {ms_mean:.3f} ms/step")
     flops, bytes_ = kda_algorithmic(B, T, H, K, V)
     t = ms_mean * 1e-3
