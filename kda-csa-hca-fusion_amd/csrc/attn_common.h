@@ -346,6 +346,51 @@ struct MqaWave {
     accumulate32(sc, stage, to);
   }
 
+  // Row-major gathers of 32 key rows: a wave load instruction covers RPI whole
+  // rows (TPR lanes of 16 bytes per row), so it touches 2 RPI cache lines
+  // instead of the 16 half-lines of a fragment-layout load. Load i of a step
+  // holds rows i * RPI + lane / TPR, 16-byte chunk lane % TPR.
+  static constexpr int TPR = HD / 8;        // lanes (16-byte chunks) per row
+  static constexpr int RPI = 64 / TPR;      // rows per load instruction
+  static constexpr int NLI = 32 / RPI;      // load instructions per 32 rows
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  struct Rows {
+    u32x4 v[NLI];
+  };
+  // Consume 32 keys gathered row-major (row r of the step = key r); bit r of
+  // valid32 set when key r is valid. The rows go to this wave's swizzled stage
+  // (STAGE_ELEMS), from which both the key fragments and V^T are read.
+  __device__ __forceinline__ void chunk_rows(const Rows& rr, unsigned valid32, bf16_t* stage,
+                                             const TileOffsets<HD>& to) {
+    const int l = lane_id(), q = l >> 4;
+    wave_lds_sync();  // the previous step's reads of the stage are done before the overwrite
+#pragma unroll
+    for (int i = 0; i < NLI; ++i) {
+      const int r = i * RPI + l / TPR, c = l % TPR;
+      *reinterpret_cast<u32x4*>(stage + r * HD + 8 * (c ^ tile_swz<HD>(r & 15))) = rr.v[i];
+    }
+    wave_lds_sync();  // staged rows visible to the whole wave
+    f32x4 sa, sb;
+    {
+      bf16x8 kf[NS];
+#pragma unroll
+      for (int s = 0; s < NS; ++s) kf[s] = *reinterpret_cast<const bf16x8*>(stage + to.key(s));
+      sa = scores(kf);
+#pragma unroll
+      for (int s = 0; s < NS; ++s) kf[s] = *reinterpret_cast<const bf16x8*>(stage + 16 * HD + to.key(s));
+      sb = scores(kf);
+    }
+    float sc[8] = {sa[0], sa[1], sa[2], sa[3], sb[0], sb[1], sb[2], sb[3]};
+    if (valid32 != 0xffffffffu) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (!((valid32 >> (4 * q + e)) & 1u)) sc[e] = -INFINITY;
+        if (!((valid32 >> (16 + 4 * q + e)) & 1u)) sc[4 + e] = -INFINITY;
+      }
+    }
+    accumulate32(sc, stage, to);
+  }
+
   // Totals L over the 4 lanes of each head; call once, after the last step.
   __device__ __forceinline__ void finalize() { L = colq_sum(L); }
 

@@ -340,9 +340,10 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(AttnParams p) {
     const int* ip = has_idx ? p.idx + (size_t)qi * p.topk : reinterpret_cast<const int*>(dflt);
     const int ilim = has_idx ? nm : 1;
     auto idx_group = [&](int g) { return ip[min(64 * g + lane, ilim - 1)]; };
-    auto row_of = [&](int c, int ig, bool& ok) {
-      const int j = 16 * c + n;
-      const int sel = SPARSE ? __shfl(ig, (16 * c + n) & 63) : j;
+    // row j of the query (any row of the index group ig) -> its address; ok
+    // when the row is valid (padding rows read the default row)
+    auto row_ptr = [&](int j, int ig, bool& ok) {
+      const int sel = SPARSE ? __shfl(ig, j & 63) : j;
       const bf16_t* row = dflt;
       ok = false;
       if (j < nm) {
@@ -354,36 +355,41 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(AttnParams p) {
       }
       return row;
     };
-    // groups of 4 chunks (two 32-key steps), four chunks in flight; refills are
+    // 32-row step st (of the 64-row index group ig), gathered row-major;
+    // returns the step's validity bits (bit r: row 32 st + r)
+    auto load_step = [&](int st, int ig, unsigned& valid) {
+      typename W::Rows rr;
+      valid = 0u;
+#pragma unroll
+      for (int i = 0; i < W::NLI; ++i) {
+        bool ok;
+        const bf16_t* row = row_ptr(32 * st + i * W::RPI + lane / W::TPR, ig, ok);
+        rr.v[i] = *reinterpret_cast<const typename W::u32x4*>(row + 8 * (lane % W::TPR));
+        const unsigned long long m = __ballot(ok);
+#pragma unroll
+        for (int k = 0; k < W::RPI; ++k)
+          valid |= (unsigned)((m >> (W::TPR * k)) & 1ull) << (i * W::RPI + k);
+      }
+      return rr;
+    };
+    // groups of two 32-row steps, two steps in flight (named registers: an
+    // indexed array of them ends up in scratch memory); refills are
     // unconditional (past the end they read the default row, masked off) so
     // that no loaded register is copied
     const TileOffsets<HD> to;
-    typename W::Frag fr[4];
-    unsigned vm[4];
-    const int nch = (n_tot + 15) / 16;
-    const int ng = (nch + 3) / 4;
+    const int nst = (n_tot + 31) / 32;
+    const int ng = (nst + 1) / 2;
     const int ig0 = idx_group(0);
     int ig1 = idx_group(1);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      bool ok;
-      const bf16_t* row = row_of(c, ig0, ok);
-      vm[c] = (unsigned)__ballot(ok && lane < 16) & 0xffffu;
-      W::load(fr[c], row);
-    }
+    unsigned vm0, vm1;
+    typename W::Rows fr0 = load_step(0, ig0, vm0);
+    typename W::Rows fr1 = load_step(1, ig0, vm1);
     for (int g = 0; g < ng; ++g) {
       const int ig2 = idx_group(g + 2);
-#pragma unroll
-      for (int c = 0; c < 4; c += 2) {
-        if (vm[c] | vm[c + 1]) w.chunk2(fr[c], fr[c + 1], vm[c] | (vm[c + 1] << 16), stage, to);
-#pragma unroll
-        for (int d = c; d < c + 2; ++d) {
-          bool ok;
-          const bf16_t* row = row_of(4 * (g + 1) + d, ig1, ok);
-          vm[d] = (unsigned)__ballot(ok && lane < 16) & 0xffffu;
-          W::load(fr[d], row);
-        }
-      }
+      if (vm0) w.chunk_rows(fr0, vm0, stage, to);
+      fr0 = load_step(2 * (g + 1), ig1, vm0);
+      if (vm1) w.chunk_rows(fr1, vm1, stage, to);
+      fr1 = load_step(2 * (g + 1) + 1, ig1, vm1);
       ig1 = ig2;
     }
   }
