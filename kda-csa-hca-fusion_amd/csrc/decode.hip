@@ -835,7 +835,6 @@ __global__ __launch_bounds__(256) void idx_merge_kernel(DecodeIdxParams p) {
 template <int HD, typename QT, typename OT>
 __global__ __launch_bounds__(256, 3) void attn_kernel(DecodeAttnParams p) {
   using W = MqaWave<HD>;
-  constexpr int D = 4;                                  // chunks in flight (two 32-key steps)
   constexpr int STAGE = W::STAGE_ELEMS;                 // bf16 per wave
   constexpr int MERGE = 4 * 16 * HD + 4 * 16 * 2;       // floats: o and (M, L) per wave and head
   constexpr int LDS_BYTES = (4 * STAGE * 2 > MERGE * 4) ? 4 * STAGE * 2 : MERGE * 4;
@@ -855,59 +854,62 @@ __global__ __launch_bounds__(256, 3) void attn_kernel(DecodeAttnParams p) {
   // rows of padding lanes must still be readable: a cached block when there is
   // one, else the ring (a group only exists when one of the two holds rows)
   const bf16_t* dflt = p.na > 0 ? kv : ring;
-  // Block indices are loaded 2D chunks ahead of their use; the loads are
-  // clamped, unmasked: row_of reads an entry only for rows below min(jg1, na).
-  // Without indices a readable word is loaded.
+  // The group's rows come in 32-row steps, wave w taking steps w, w + 4, ...,
+  // gathered row-major (whole rows per TPR lanes: a load instruction covers
+  // RPI full rows, contiguous for consecutive cached blocks) with nontemporal
+  // loads (every row is read once). Block indices of a step (one per lane of
+  // the first 32) are loaded two steps ahead; the loads are clamped, entries
+  // are read only for rows below min(jg1, na). Without indices a readable word
+  // is loaded.
   const int* ip = idx ? idx : reinterpret_cast<const int*>(dflt);
   const int ilim = idx ? max(min(jg1, p.na), 1) : 1;
-  auto row_j = [&](int m) { return jg0 + 16 * (wv + 4 * m) + n; };
-  auto idx_of = [&](int m) { return ip[min(row_j(m), ilim - 1)]; };
-  auto row_of = [&](int m, int ix, bool& ok) {
-    const int j = row_j(m);
-    const int blk = idx ? ix : j;
-    ok = j < jg1;
-    const bf16_t* row = dflt;
-    if (j < p.na) {
-      ok = ok && blk >= 0 && blk < p.nb;
-      if (ok) row = kv + (size_t)blk * HD;
-    } else if (ok) {
-      row = ring + (size_t)(j - p.na) * HD;
+  auto row_j = [&](int m, int r) { return jg0 + 32 * (wv + 4 * m) + r; };
+  auto idx_of = [&](int m) { return ip[min(row_j(m, lane & 31), ilim - 1)]; };
+  typedef typename W::u32x4 u32x4;
+  auto load_step = [&](int m, int ix, unsigned& valid) {
+    typename W::Rows rr;
+    valid = 0u;
+#pragma unroll
+    for (int i = 0; i < W::NLI; ++i) {
+      const int r = i * W::RPI + lane / W::TPR;
+      const int j = row_j(m, r);
+      const int blk = idx ? __shfl(ix, r) : j;
+      bool ok = j < jg1;
+      const bf16_t* row = dflt;
+      if (j < p.na) {
+        ok = ok && blk >= 0 && blk < p.nb;
+        if (ok) row = kv + (size_t)blk * HD;
+      } else if (ok) {
+        row = ring + (size_t)(j - p.na) * HD;
+      }
+      rr.v[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(row + 8 * (lane % W::TPR)));
+      const unsigned long long mb = __ballot(ok);
+#pragma unroll
+      for (int k = 0; k < W::RPI; ++k)
+        valid |= (unsigned)((mb >> (W::TPR * k)) & 1ull) << (i * W::RPI + k);
     }
-    return row;
+    return rr;
   };
   const TileOffsets<HD> to;
-  const int ncg = (jg1 - jg0 + 15) / 16;                  // chunks in the group
-  const int mine = ncg > wv ? (ncg - wv + 3) / 4 : 0;      // this wave's
-  typename W::Frag fr[D];
-  unsigned vm[D];
-  int ix[D];
-#pragma unroll
-  for (int d = 0; d < D; ++d) ix[d] = idx_of(d);
-#pragma unroll
-  for (int d = 0; d < D; ++d) {
-    bool ok;
-    const bf16_t* row = row_of(d, ix[d], ok);
-    vm[d] = (unsigned)__ballot(ok && lane < 16) & 0xffffu;
-    W::load(fr[d], row);
-    ix[d] = idx_of(d + D);
-  }
-  // groups of D chunks with unconditional refills (past the end they read the
-  // default row, masked off), so that no loaded register is copied; chunks
-  // past this wave's last are masked (vm = 0) rather than peeled off, which
-  // would cost a second copy of the loop body's registers
-  for (int m0 = 0; m0 < mine; m0 += D) {
-#pragma unroll
-    for (int d0 = 0; d0 < D; d0 += 2) {
-      if (vm[d0] | vm[d0 + 1]) w.chunk2(fr[d0], fr[d0 + 1], vm[d0] | (vm[d0 + 1] << 16), stage, to);
-#pragma unroll
-      for (int d = d0; d < d0 + 2; ++d) {
-        bool ok;
-        const bf16_t* row = row_of(m0 + d + D, ix[d], ok);
-        vm[d] = (unsigned)__ballot(ok && lane < 16) & 0xffffu;
-        W::load(fr[d], row);
-        ix[d] = idx_of(m0 + d + 2 * D);
-      }
-    }
+  const int nsg = (jg1 - jg0 + 31) / 32;                   // steps in the group
+  const int mine = nsg > wv ? (nsg - wv + 3) / 4 : 0;      // this wave's
+  // two steps in flight (named registers: an indexed array of them ends up in
+  // scratch memory); refills are unconditional (past the end they read the
+  // default row, masked off), and a wave's odd last step is masked (vm = 0)
+  // rather than peeled off
+  int ix0 = idx_of(0), ix1 = idx_of(1);
+  unsigned vm0, vm1;
+  typename W::Rows fr0 = load_step(0, ix0, vm0);
+  ix0 = idx_of(2);
+  typename W::Rows fr1 = load_step(1, ix1, vm1);
+  ix1 = idx_of(3);
+  for (int m0 = 0; m0 < mine; m0 += 2) {
+    if (vm0) w.chunk_rows(fr0, vm0, stage, to);
+    fr0 = load_step(m0 + 2, ix0, vm0);
+    ix0 = idx_of(m0 + 4);
+    if (vm1) w.chunk_rows(fr1, vm1, stage, to);
+    fr1 = load_step(m0 + 3, ix1, vm1);
+    ix1 = idx_of(m0 + 5);
   }
   w.finalize();
 
