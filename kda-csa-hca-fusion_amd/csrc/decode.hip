@@ -617,18 +617,53 @@ __global__ __launch_bounds__(256, 4) void idx_range_kernel(DecodeIdxParams p) {
   const int mine = nchunk > wave ? (nchunk - wave + 3) / 4 : 0;
   KeyFrag<KT> kf[D][NS];
   float iv[D];
+  // bf16 rows of 64 channels (128 bytes) load row-major: load A covers rows
+  // 0..7 of the chunk, load B rows 8..15, lane (q, n) taking row n % 8, 16-byte
+  // chunk q + 4 (n / 8) -- whole rows, contiguous 1 KB for consecutive blocks,
+  // with nontemporal loads (read once). The fragments (lane (q, n): row n,
+  // chunk q for k step 0, chunk 4 + q for step 1) are A / B and their
+  // within-row rotation by 8 lanes: s0 = n < 8 ? A : rot8(B),
+  // s1 = n < 8 ? rot8(A) : B.
+  constexpr bool ROWMAJOR = std::is_same<KT, bf16_t>::value && CI == 64;
   auto load = [&](int m, KeyFrag<KT> (&f)[NS], float& ivv) {
-    const int j = min(16 * (wave + 4 * m) + n, nr_blocks - 1);
-    const KT* krow = kbase + (size_t)j * CI + 8 * q4;
+    const int base = 16 * (wave + 4 * m);
+    if constexpr (ROWMAJOR) {
+      typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+      const int c = q4 + 4 * (n >> 3);
+      const int ja = min(base + (n & 7), nr_blocks - 1), jb = min(base + 8 + (n & 7), nr_blocks - 1);
+      f[0].v = __builtin_bit_cast(bf16x8, __builtin_nontemporal_load(
+                                              reinterpret_cast<const u32x4*>(kbase + (size_t)ja * CI + 8 * c)));
+      f[1].v = __builtin_bit_cast(bf16x8, __builtin_nontemporal_load(
+                                              reinterpret_cast<const u32x4*>(kbase + (size_t)jb * CI + 8 * c)));
+    } else {
+      const int jr = min(base + n, nr_blocks - 1);
+      const KT* krow = kbase + (size_t)jr * CI + 8 * q4;
 #pragma unroll
-    for (int s = 0; s < NS; ++s) f[s].load(krow + 32 * s);
-    ivv = ibase[j * istride];
+      for (int s = 0; s < NS; ++s) f[s].load(krow + 32 * s);
+    }
+    ivv = ibase[min(base + n, nr_blocks - 1) * istride];
+  };
+  auto rot8 = [](bf16x8 x) {
+    typedef int i32x4 __attribute__((ext_vector_type(4)));
+    i32x4 w = __builtin_bit_cast(i32x4, x);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = __builtin_amdgcn_update_dpp(0, w[i], 0x128, 0xf, 0xf, false);  // row_ror:8
+    return __builtin_bit_cast(bf16x8, w);
   };
   // consume slot d as chunk m, then (RELOAD) refill it with chunk m + D
   auto step = [&](int m, KeyFrag<KT> (&f)[NS], float& ivv, auto reload) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (ROWMAJOR) {
+      KeyFrag<KT> g0, g1;
+      const bf16x8 ra = rot8(f[0].v), rb = rot8(f[1].v);
+      g0.v = n < 8 ? f[0].v : rb;
+      g1.v = n < 8 ? ra : f[1].v;
+      acc = key_mfma<KT>(g0, qhi[0], qlo[0], acc);
+      acc = key_mfma<KT>(g1, qhi[1], qlo[1], acc);
+    } else {
 #pragma unroll
-    for (int s = 0; s < NS; ++s) acc = key_mfma<KT>(f[s], qhi[s], qlo[s], acc);
+      for (int s = 0; s < NS; ++s) acc = key_mfma<KT>(f[s], qhi[s], qlo[s], acc);
+    }
     const float sc = p.scale * (has_inv ? ivv : 1.f);
     float v = 0.f;
 #pragma unroll
