@@ -276,17 +276,21 @@ def _hca_attn_ref(q, kv, loc, sink, m, win, scale):
             + np.einsum('bhtw,btwd->bthd', p[..., nb:], Cw))
 
 
-@pytest.mark.parametrize("hd,nh,T,nb,m,win,qdt,odt", [
-    (128, 16, 77, 9, 8, 20, "bf16", "bf16"),   # T not a multiple of the query tile
-    (64, 5, 45, 6, 7, 100, "fp32", "fp32"),    # window longer than the sequence
-    (128, 3, 33, 0, 4, 16, "bf16", "fp32"),    # no compressed block
-    (64, 16, 50, 12, 4, 0, "bf16", "bf16"),    # no window
-    (128, 16, 130, 40, 3, 64, "fp16", "fp16"),  # several key tiles, fp16 queries
-    (64, 5, 21, 3, 5, 8, "bf16", "bf16"),      # head count below 16, 16-bit output rows
+@pytest.mark.parametrize("hd,nh,T,nb,m,win,qdt,odt,scale", [
+    (128, 16, 77, 9, 8, 20, "bf16", "bf16", None),  # T not a multiple of the query tile
+    (64, 5, 45, 6, 7, 100, "fp32", "fp32", None),  # window longer than the sequence
+    (128, 3, 33, 0, 4, 16, "bf16", "fp32", None),  # no compressed block
+    (64, 16, 50, 12, 4, 0, "bf16", "bf16", None),  # no window
+    (128, 16, 130, 40, 3, 64, "fp16", "fp16", None),  # fp16 queries and output
+    (64, 5, 21, 3, 5, 8, "bf16", "bf16", None),  # head count below 16, 16-bit output rows
+    (64, 16, 400, 200, 2, 64, "bf16", "bf16", None),  # up to 3 key tiles of 128 rows per query tile
+    (128, 8, 300, 150, 2, 100, "bf16", "fp32", None),  # 2 key tiles, rows cut inside a 32-row step
+    (128, 16, 96, 12, 8, 40, "bf16", "bf16", -0.7),  # negative score scale
 ])
-def test_hca_attn_abi_shapes(dev, hd, nh, T, nb, m, win, qdt, odt):
+def test_hca_attn_abi_shapes(dev, hd, nh, T, nb, m, win, qdt, odt, scale):
     """kch_hca_attn over ragged shapes: query tiles cut by T, head counts below 16,
-    head dim 64, empty compressed or window parts, every query / output dtype."""
+    head dim 64, empty compressed or window parts, several key tiles, every query /
+    output dtype, a negative scale."""
     from kch import _lib
     from oracle.common import l2_normalize
     dts = {"bf16": torch.bfloat16, "fp32": torch.float32, "fp16": torch.float16}
@@ -298,7 +302,7 @@ def test_hca_attn_abi_shapes(dev, hd, nh, T, nb, m, win, qdt, odt):
     sink = torch.from_numpy(rng.standard_normal(nh).astype(np.float32)).to(dev)
     out = torch.full((B, T, nh, hd), float("nan"), device=dev, dtype=dts[odt])
     code = {"bf16": 1, "fp32": 0, "fp16": 2}
-    scale = hd ** -0.5
+    scale = hd ** -0.5 if scale is None else scale
     _lib.call("kch_hca_attn", _lib.ptr(q), _lib.ptr(kv), _lib.ptr(loc if win > 0 else None),
               _lib.ptr(sink), _lib.ptr(out), B, T, nb, nh, hd, m, win, scale, 1, code[qdt],
               code[odt], _lib.stream_of(q))
