@@ -205,25 +205,35 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
       for (int i = lane; i < nb; i += 64)
         p.logits_out[((size_t)b * p.T + t) * nb + i] = i < nv ? lg[i] : -INFINITY;
     }
-    auto val = [&](int i) { return kv64(order_key(lg[i]), i); };
+    // The radix select runs on the 32-bit order keys (written over the logits
+    // in place by the first pass). It finds the boundary key K: every key
+    // above K is taken, and of the keys equal to K the lowest indices, as
+    // many as still needed -- the reference's order (descending logit, ties
+    // by ascending index). A select stopped early (its boundary digit taken
+    // whole) takes every key in or above the boundary bin.
+    uint32_t* lk = reinterpret_cast<uint32_t*>(const_cast<float*>(lg));
     const int cnt = nv < topk ? nv : topk;
-    u64 thr = 0ull, mask = 0ull;  // with mask = 0 every value is taken
+    uint32_t thr = 0u, mask = 0u;  // with mask = 0 every key is in the boundary bin
+    int tie_take = 0x7fffffff;      // boundary-bin keys taken (in index order)
     if (nv > topk) {
-      u64 a = ~0ull, o = 0ull;
+      uint32_t a = ~0u, o = 0u;
       for (int i = lane; i < nv; i += 64) {
-        const u64 v = val(i);
-        a &= v;
-        o |= v;
+        const uint32_t k = order_key(lg[i]);
+        lk[i] = k;
+        a &= k;
+        o |= k;
       }
 #pragma unroll
       for (int d = 32; d; d >>= 1) {
-        a &= shfl_xor64(a, d);
-        o |= shfl_xor64(o, d);
+        a &= (uint32_t)__shfl_xor((int)a, d);
+        o |= (uint32_t)__shfl_xor((int)o, d);
       }
-      int lo_bit = 64 - __clzll((long long)(a ^ o));  // values differ: lo_bit >= 1
-      mask = lo_bit >= 64 ? 0ull : (~0ull << lo_bit);
+      wave_lds_sync();  // keys in place before the passes read them
+      int lo_bit = (a ^ o) ? 32 - __clz((int)(a ^ o)) : 0;
+      mask = lo_bit >= 32 ? 0u : (~0u << lo_bit);
       thr = a & mask;
       int need = topk;
+      bool whole = false;  // the last pass took its boundary digit whole
       while (lo_bit > 0) {
         const int w = lo_bit < 8 ? lo_bit : 8;
         const int shift = lo_bit - w;
@@ -232,13 +242,12 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
         for (int k = 0; k < 4; ++k) hist[lane + 64 * k] = 0u;
         // a wave's LDS operations complete in order: the clear precedes the adds
         for (int i0 = 0; i0 < nv; i0 += 64 * U) {
-          u64 v[U];
+          uint32_t v[U];
 #pragma unroll
-          for (int u = 0; u < U; ++u) v[u] = val(min(i0 + 64 * u + lane, nv - 1));
+          for (int u = 0; u < U; ++u) v[u] = lk[min(i0 + 64 * u + lane, nv - 1)];
 #pragma unroll
           for (int u = 0; u < U; ++u)
-            if (i0 + 64 * u + lane < nv && (v[u] & mask) == thr)
-              atomicAdd(&hist[(uint32_t)(v[u] >> shift) & dm], 1u);
+            if (i0 + 64 * u + lane < nv && (v[u] & mask) == thr) atomicAdd(&hist[(v[u] >> shift) & dm], 1u);
         }
         wave_lds_sync();
         // digits in descending order: lane l holds dm - 4l .. dm - 4l - 3
@@ -266,22 +275,33 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
         const int above = __shfl(found_above, src);
         const int bcnt = __shfl(found_cnt, src);
         wave_lds_sync();  // histogram reads done before the next pass clears it
-        thr |= (u64)bin << shift;
-        mask |= (u64)dm << shift;
+        thr |= (uint32_t)bin << shift;
+        mask |= dm << shift;
         need -= above;
         lo_bit = shift;
-        if (bcnt == need) break;  // the boundary digit's values are all taken
+        if (bcnt == need) {  // the boundary digit's keys are all taken
+          whole = true;
+          break;
+        }
       }
+      if (!whole) tie_take = need;  // all 32 bits fixed: `need` of the keys equal to thr
+    } else {
+      for (int i = lane; i < nv; i += 64) lk[i] = order_key(lg[i]);
+      wave_lds_sync();
     }
-    // gather the cnt selected values in index order
-    int at = 0;
+    // gather the cnt selected values (key, ~index) in index order
+    int at = 0, eqs = 0;
     for (int i0 = 0; i0 < nv; i0 += 64) {
       const int i = i0 + lane;
-      const u64 v = i < nv ? val(i) : 0ull;
-      const bool tk = i < nv && (v & mask) >= thr;
+      const uint32_t k = i < nv ? lk[i] : 0u;
+      const bool gt = i < nv && (k & mask) > thr;
+      const bool eq = i < nv && (k & mask) == thr;
+      const unsigned long long em = __ballot(eq);
+      const bool tk = gt || (eq && eqs + mbcnt64(em) < tie_take);
       const unsigned long long tm = __ballot(tk);
-      if (tk) sel[at + mbcnt64(tm)] = v;
+      if (tk) sel[at + mbcnt64(tm)] = kv64(k, i);
       at += __popcll(tm);
+      eqs += __popcll(em);
     }
     if (p.sorted && cnt > 1) {
       // pad to a power of two with values that sort last, bitonic sort descending
