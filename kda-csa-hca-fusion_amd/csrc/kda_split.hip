@@ -265,13 +265,34 @@ __global__ __launch_bounds__(256, 2) void kda_prep_kernel(KdaParams p, SplitPtrs
   };
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
-    float ts[4][8];
+    // G - G_a = (in-tile prefix) + off, with the carry of the earlier tiles and
+    // the anchor G_a = T_0 + T_1 (tile sums T_w) folded into one offset per
+    // channel: -(T_0 + T_1), -T_1, 0, T_2 for waves 0..3
+    float off[8];
+    {
+      auto tile8 = [&](int w, float (&f)[8]) {
+        const float4 a = *reinterpret_cast<const float4*>(sTs + w * K + 32 * s + 8 * q4);
+        const float4 c = *reinterpret_cast<const float4*>(sTs + w * K + 32 * s + 8 * q4 + 4);
+        f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+        f[4] = c.x; f[5] = c.y; f[6] = c.z; f[7] = c.w;
+      };
+      float t1[8];
+      if (wave == 0) {
+        float t0[8];
+        tile8(0, t0);
+        tile8(1, t1);
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float4 a = *reinterpret_cast<const float4*>(sTs + w * K + 32 * s + 8 * q4);
-      const float4 c = *reinterpret_cast<const float4*>(sTs + w * K + 32 * s + 8 * q4 + 4);
-      ts[w][0] = a.x; ts[w][1] = a.y; ts[w][2] = a.z; ts[w][3] = a.w;
-      ts[w][4] = c.x; ts[w][5] = c.y; ts[w][6] = c.z; ts[w][7] = c.w;
+        for (int i = 0; i < 8; ++i) off[i] = -(t0[i] + t1[i]);
+      } else if (wave == 1) {
+        tile8(1, t1);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) off[i] = -t1[i];
+      } else if (wave == 2) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) off[i] = 0.f;
+      } else {
+        tile8(2, off);
+      }
     }
     // Per-channel constants e(G_a) and e(G_l - G_a): lane r of the row evaluates
     // them for channel 32s + 8q4 + (r & 7) and row_share broadcasts them. With
@@ -291,8 +312,7 @@ __global__ __launch_bounds__(256, 2) void kda_prep_kernel(KdaParams p, SplitPtrs
     float a8[8], q8[8], b8[8], qg8[8], kg8[8], kd8[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      G[s][i] += fmaf(m1, ts[0][i], fmaf(m2, ts[1][i], m3 * ts[2][i]));
-      const float d = G[s][i] - (ts[0][i] + ts[1][i]);
+      const float d = G[s][i] + off[i];
       dmax = fmaxf(dmax, fabsf(d));
       const float R = fast_exp2(d), Ci = fast_exp2(-d);
       a8[i] = kf[i] * R;              // k e(G - G_a)
