@@ -593,12 +593,23 @@ __global__ __launch_bounds__(256, 2) void kda_prep_kernel(KdaParams p, SplitPtrs
 template <int K, int BV, typename OutT>
 __global__ __launch_bounds__(256, BV == 32 ? 2 : 1) void kda_state_kernel(KdaParams p, SplitPtrs ws) {
   constexpr int KS = K / 32, CT = BV / 16, RT = K / 64;
-  constexpr int LDS_ = K + 8;  // sS row stride: row = value column, K channels
-  constexpr int LDV = C + 8;   // sVn row stride: row = value column, C tokens
   constexpr int LDO = BV + 8;  // sO row stride: row = token
-  __shared__ __attribute__((aligned(16))) bf16_t sS[BV * LDS_];
-  __shared__ __attribute__((aligned(16))) bf16_t sVn[BV * LDV];
+  // sS (row = value column, K channels) and sVn (row = value column, C tokens)
+  // hold each 32-element block in packed order, element 4a + i (a, i < 4) at
+  // 8a + i and element 16 + 4a + i at 8a + 4 + i, so an MFMA fragment of the
+  // block (packed k = 4q .. 4q+3, 16+4q .. 16+4q+3) is one 16-byte read. The
+  // 16-byte chunks of a row are XOR-swizzled by the row (swz_s, swz_v): every
+  // fragment read and every 16-byte state write is free of bank conflicts (a
+  // 16-byte LDS read is served 16 lanes at a time, lanes 4a .. 4a+3 of a
+  // 32-lane half grouped by the parity of a; 16-byte writes 8 lanes at a
+  // time). Pairs of 8-byte reads would be merged into ds_read2_b64, which
+  // moves a quarter of the bytes per cycle of ds_read_b128.
+  __shared__ __attribute__((aligned(16))) bf16_t sS[BV * K];
+  __shared__ __attribute__((aligned(16))) bf16_t sVn[BV * C];
   __shared__ __attribute__((aligned(16))) OutT sO[C * LDO];
+  // 256-byte rows (K = 128): chunk ^ (row % 16); 128-byte rows: chunk ^ (row / 2 % 8)
+  auto swz_s = [](int row) { return K == 128 ? (row & 15) : ((row >> 1) & 7); };
+  auto swz_v = [](int row) { return (row >> 1) & 7; };
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -665,11 +676,19 @@ __global__ __launch_bounds__(256, BV == 32 ? 2 : 1) void kda_state_kernel(KdaPar
       }
   auto write_state = [&]() {
 #pragma unroll
-    for (int j = 0; j < RT; ++j)
-#pragma unroll
-      for (int ct = 0; ct < CT; ++ct)
-        *reinterpret_cast<bf16x4*>(sS + (16 * ct + r) * LDS_ + 16 * (RT * wave + j) + 4 * q4) =
-            to_bf16x4(S[j][ct]);
+    for (int ct = 0; ct < CT; ++ct) {
+      const int row = 16 * ct + r;
+      if constexpr (RT == 2) {
+        // channels 32 wave + 4 q4 + e (j = 0) and 32 wave + 16 + 4 q4 + e (j = 1):
+        // packed positions 8 q4 .. 8 q4 + 7 of block `wave`, one chunk
+        *reinterpret_cast<bf16x8*>(sS + row * K + 8 * ((4 * wave + q4) ^ swz_s(row))) =
+            cat4(to_bf16x4(S[0][ct]), to_bf16x4(S[1][ct]));
+      } else {
+        // channels 16 wave + 4 q4 + e: half (wave & 1) of chunk q4 of block wave / 2
+        *reinterpret_cast<bf16x4*>(sS + row * K + 8 * ((4 * (wave >> 1) + q4) ^ swz_s(row)) +
+                                   4 * (wave & 1)) = to_bf16x4(S[0][ct]);
+      }
+    }
   };
   OutT* go = static_cast<OutT*>(p.o) + ((size_t)b * T * p.HV + hv) * V + vs * BV;
   const size_t ostride = (size_t)p.HV * V;
@@ -708,9 +727,9 @@ __global__ __launch_bounds__(256, BV == 32 ? 2 : 1) void kda_state_kernel(KdaPar
     for (int s = 0; s < KS; ++s) {
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) {
-        const bf16_t* srow = sS + (16 * ct + r) * LDS_ + 32 * s;
-        const bf16x8 sf = cat4(*reinterpret_cast<const bf16x4*>(srow + 4 * q4),
-                               *reinterpret_cast<const bf16x4*>(srow + 16 + 4 * q4));
+        const int row = 16 * ct + r;
+        const bf16x8 sf =
+            *reinterpret_cast<const bf16x8*>(sS + row * K + 8 * ((4 * s + q4) ^ swz_s(row)));
         va[ct] = mfma32(cur.wp[s], sf, va[ct]);
         oa[ct] = mfma32(sf, cur.qg[s], oa[ct]);
       }
@@ -729,7 +748,10 @@ __global__ __launch_bounds__(256, BV == 32 ? 2 : 1) void kda_state_kernel(KdaPar
       f32x4 vn;
 #pragma unroll
       for (int e = 0; e < 4; ++e) vn[e] = (float)cur.u[ct][e] - va[ct][e];
-      *reinterpret_cast<bf16x4*>(sVn + (16 * ct + r) * LDV + 16 * wave + 4 * q4) = to_bf16x4(vn);
+      // tokens 16 wave + 4 q4 + e: half (wave & 1) of chunk q4 of block wave / 2
+      const int row = 16 * ct + r;
+      *reinterpret_cast<bf16x4*>(sVn + row * C + 8 * ((4 * (wave >> 1) + q4) ^ swz_v(row)) +
+                                 4 * (wave & 1)) = to_bf16x4(vn);
     }
     __syncthreads();  // v_new visible; every read of sS is done
     bf16x8 vf[2][CT];
@@ -737,9 +759,8 @@ __global__ __launch_bounds__(256, BV == 32 ? 2 : 1) void kda_state_kernel(KdaPar
     for (int s = 0; s < 2; ++s)
 #pragma unroll
       for (int ct = 0; ct < CT; ++ct) {
-        const bf16_t* vrow = sVn + (16 * ct + r) * LDV + 32 * s;
-        vf[s][ct] = cat4(*reinterpret_cast<const bf16x4*>(vrow + 4 * q4),
-                         *reinterpret_cast<const bf16x4*>(vrow + 16 + 4 * q4));
+        const int row = 16 * ct + r;
+        vf[s][ct] = *reinterpret_cast<const bf16x8*>(sVn + row * C + 8 * ((4 * s + q4) ^ swz_v(row)));
       }
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
