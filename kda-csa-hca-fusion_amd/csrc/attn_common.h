@@ -114,15 +114,20 @@ __device__ __forceinline__ bf16x8 to_bf16x8(const float* f) {
 }
 
 // LDS tiles of rows of HD bf16 (row stride HD, no padding): the 16-byte chunk
-// c of row r sits at chunk c ^ tile_swz(r % 16). The swizzle keeps free of
-// bank conflicts the row writes (16 lanes, one chunk of 16 consecutive rows,
-// or one row's chunks by consecutive lanes), the key-fragment reads (the
-// same pattern) and the transposing V^T reads (32 lanes: two adjacent chunks
-// of 8 consecutive rows).
+// c of row r sits at chunk c ^ tile_swz(r % 16). gfx950 serves a 16-byte LDS
+// read 16 lanes at a time over 64 banks (the lanes 4a .. 4a+3 of a 32-lane half
+// with the same parity of popcount(a)), a 16-byte write 8 consecutive lanes at
+// a time over 32 banks, and the 8-byte transposing read 32 lanes at a time over
+// 64 banks. The swizzle keeps all four patterns on a tile free of bank
+// conflicts: key-fragment reads (lane: row n = lane % 16, chunk 4s + lane / 16),
+// V^T reads (row 4 (lane / 16) + n / 4, half-chunk 2 (2t + n / 2 % 2) + n % 2:
+// rows 0..7 and 8..15 each need distinct tile_swz / 2 within a 256-byte bank
+// sweep), fragment-layout writes (rows 0..7 need distinct tile_swz % 8 in a
+// 128-byte sweep) and row writes (consecutive lanes on one row's chunks).
 template <int HD>
 __device__ __forceinline__ int tile_swz(int r) {
-  if constexpr (HD == 128) return ((r & 7) << 1) | ((r >> 3) & 1);
-  else return (((r >> 1) & 3) << 1) | ((r >> 3) & 1);  // 128-byte rows: two rows per bank sweep
+  if constexpr (HD == 128) return ((r & 7) << 1) | ((r >> 2) & 1);
+  else return r & 7;  // 128-byte rows: two rows per 256-byte bank sweep
 }
 
 // This lane's element offsets into a 16-row slice of a swizzled tile. Key

@@ -411,7 +411,7 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(AttnParams p) {
 // LDS tile: rows of HD bf16; 16-byte chunk c of row r is stored at chunk
 // c ^ tile_swz(r % 16). The swizzle keeps the three access patterns free of
 // bank conflicts: the tile loads (a row's chunks by consecutive lanes), the
-// key fragments (16 lanes read chunk c of 16 consecutive rows) and the
+// key-fragment reads (chunk 4s + lane / 16 of row lane % 16) and the
 // transposing V^T reads (32 lanes read two adjacent chunks of 8 rows).
 // ---------------------------------------------------------------------------
 constexpr int kTileGroup = 16;  // consecutive query tiles kept on one XCD
