@@ -799,11 +799,18 @@ __global__ __launch_bounds__(256, BV == 32 ? 2 : 1) void kda_state_kernel(KdaPar
     load(f1, 1, 0);
     load(f1, 1, 1);
   }
-  for (int n = 0; n < NT; n += 3) {
+  // The loop body is three unconditional chunks and the tail is peeled: with a
+  // branch between the chunks the compiler's wait counts lose track at the
+  // join and it waits for nearly every outstanding load (memory counts are
+  // in issue order, so that includes the operands fetched for later chunks).
+  int n = 0;
+  for (; n + 3 <= NT; n += 3) {
     chunk(n, f0, f2);
-    if (n + 1 < NT) chunk(n + 1, f1, f0);
-    if (n + 2 < NT) chunk(n + 2, f2, f1);
+    chunk(n + 1, f1, f0);
+    chunk(n + 2, f2, f1);
   }
+  if (n < NT) chunk(n, f0, f2);
+  if (n + 1 < NT) chunk(n + 1, f1, f0);
   __syncthreads();
   store_o(NT - 1);
   if (p.s_out) {
