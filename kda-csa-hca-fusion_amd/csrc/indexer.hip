@@ -14,9 +14,11 @@
 // logits by 16-block chunk, then take one query's selection each. Scores use a split-bf16 product
 // (x = hi + lo, hi*hi + hi*lo + lo*hi with fp32 accumulation) so the logits
 // carry ~2^-16 relative error instead of bf16's 2^-8. Per query, the logits sit
-// in LDS; the top-k of the unique 64-bit (key, index) values is found by an
-// 8-bit radix select, gathered in index order and, when asked, bitonic-sorted
-// by (logit desc, index asc).
+// in LDS; the top-k is found by an 8-bit radix select on 32-bit order keys
+// (ties at the boundary key taken in ascending index), gathered in index
+// order and, when asked, bitonic-sorted by (logit desc, index asc). The head
+// count is a template parameter: with it known, the lane's (query, head)
+// split and the head sum compile to shifts and two or four lane exchanges.
 
 #include "attn_common.h"
 #include "kch_csa.h"
@@ -73,12 +75,12 @@ __device__ __forceinline__ void split_bf16(const float* f, bf16x8& hi, bf16x8& l
 
 }  // namespace
 
-template <typename QT, int CI>
+template <typename QT, int CI, int NIH>
 __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   constexpr int NS = CI / 32;
-  const int nIh = p.nIh;
-  const int QPW = 16 / nIh;
+  constexpr int nIh = NIH;
+  constexpr int QPW = 16 / NIH;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int q4 = lane >> 4, n = lane & 15;
@@ -166,8 +168,7 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
       float v = fmaxf(acc[e] * p.scale, 0.f) * wq;
       // head sum over the nIh adjacent lanes of this query
 #pragma unroll
-      for (int d = 1; d < 16; d <<= 1)
-        if (d < nIh) v += __shfl_xor(v, d);
+      for (int d = 1; d < nIh; d <<= 1) v += __shfl_xor(v, d);
       const int blk = 16 * c + 4 * q4 + e;
       if (hh == 0 && qok && blk < nv_me) logits[jq * nb + blk] = v;
     }
@@ -344,8 +345,18 @@ hipError_t indexer_dispatch(const IndexerParams& p, int dtype, hipStream_t s) {
   const int QPW = 16 / p.nIh;
   const size_t lds = indexer_lds_bytes(p.nb, p.nIh, p.topk);
   const unsigned groups = (unsigned)(p.B * ((p.T + QPW - 1) / QPW));
-#define KCH_IDX_LAUNCH(QT, CI) \
-  hipLaunchKernelGGL((indexer_kernel<QT, CI>), dim3(groups), dim3(256), lds, s, p)
+#define KCH_IDX_NIH(QT, CI, NIH) \
+  hipLaunchKernelGGL((indexer_kernel<QT, CI, NIH>), dim3(groups), dim3(256), lds, s, p)
+#define KCH_IDX_LAUNCH(QT, CI)                \
+  do {                                        \
+    switch (p.nIh) {                          \
+      case 1: KCH_IDX_NIH(QT, CI, 1); break;  \
+      case 2: KCH_IDX_NIH(QT, CI, 2); break;  \
+      case 4: KCH_IDX_NIH(QT, CI, 4); break;  \
+      case 8: KCH_IDX_NIH(QT, CI, 8); break;  \
+      default: KCH_IDX_NIH(QT, CI, 16); break; \
+    }                                         \
+  } while (0)
   if (dtype == DT_BF16) {
     if (p.cI == 64) KCH_IDX_LAUNCH(bf16_t, 64);
     else if (p.cI == 128) KCH_IDX_LAUNCH(bf16_t, 128);
@@ -360,6 +371,7 @@ hipError_t indexer_dispatch(const IndexerParams& p, int dtype, hipStream_t s) {
     else KCH_IDX_LAUNCH(_Float16, 32);
   }
 #undef KCH_IDX_LAUNCH
+#undef KCH_IDX_NIH
   return hipGetLastError();
 }
 

@@ -191,6 +191,24 @@ def test_indexer_matches_oracle(dev, normalize, T, m, topk):
         assert frac > 0.9
 
 
+@pytest.mark.parametrize("nIh", [1, 2, 8, 16])
+def test_indexer_head_counts(dev, nIh):
+    # the kernel is compiled per head count (the MFMA column is (query, head))
+    import kch
+    B, T, cI, m, topk = 2, 128, 64, 4, 8
+    nb = T // m
+    dv, hs, pard, parf = proj_inputs(T + topk + nIh, B, T, 64, cI, 1, nIh, m, dev)
+    K_ref = O.compress_kv(hs["K_idx"], hs["Z_idx"], parf["B_idx"], m)
+    cbm = O.causal_block_mask(T, nb, m)
+    idx = kch.csa_lightning_indexer(dv["q_idx"], torch.from_numpy(K_ref).to(dev), dv["w_idx"],
+                                    topk, causal_block_mask=torch.from_numpy(cbm).to(dev),
+                                    normalize_qk=True)
+    torch.cuda.synchronize()
+    idx_ref, lg = O.lightning_indexer(hs["q_idx"], K_ref, hs["w_idx"], topk, None, cbm, True,
+                                      return_logits=True)
+    assert check_topk("indexer-nIh", idx.cpu().numpy(), idx_ref, lg) > 0.9
+
+
 def test_indexer_soft_weights_and_no_mask(dev):
     import kch
     B, T, cI, nIh, m, topk = 1, 32, 32, 2, 4, 4
