@@ -64,6 +64,27 @@ __device__ __forceinline__ int mbcnt64(unsigned long long m) {
   return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over the NIH adjacent lanes (a query's heads) of a 16-lane row, with DPP
+// exchanges instead of LDS permutes: quad_perm [1,0,3,2] and [2,3,0,1] pair
+// lanes within a quad; once every lane of a quad holds the quad's sum,
+// row_half_mirror (lane i <-> 7 - i of each 8) and row_mirror (i <-> 15 - i)
+// bring in the neighbouring quad's and half row's. Each step adds two
+// partials that every lane of the pair holds bit for bit, so all NIH lanes end
+// with the same sum.
+template <int NIH>
+__device__ __forceinline__ float head_sum(float v) {
+  if constexpr (NIH >= 2) v += dpp_mov<0xb1>(v);
+  if constexpr (NIH >= 4) v += dpp_mov<0x4e>(v);
+  if constexpr (NIH >= 8) v += dpp_mov<0x141>(v);
+  if constexpr (NIH >= 16) v += dpp_mov<0x140>(v);
+  return v;
+}
+
 __device__ __forceinline__ void split_bf16(const float* f, bf16x8& hi, bf16x8& lo) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
@@ -162,20 +183,28 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi, qlo[s], acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(klo, qhi[s], acc, 0, 0, 0);
     }
-    // acc[e]: block 16c + 4*q4 + e, column n
+    // acc[e]: block 16c + 4*q4 + e, column n. No branch in here: the lanes
+    // whose value is not kept write their own word of this wave's histogram
+    // (cleared by the selection before use), since a branch costs the
+    // overlap of the chunks loaded ahead.
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      float v = fmaxf(acc[e] * p.scale, 0.f) * wq;
-      // head sum over the nIh adjacent lanes of this query
-#pragma unroll
-      for (int d = 1; d < nIh; d <<= 1) v += __shfl_xor(v, d);
+      const float v = head_sum<NIH>(fmaxf(acc[e] * p.scale, 0.f) * wq);
       const int blk = 16 * c + 4 * q4 + e;
-      if (hh == 0 && qok && blk < nv_me) logits[jq * nb + blk] = v;
+      float* dst = (hh == 0 && qok && blk < nv_me) ? logits + jq * nb + blk
+                                                   : reinterpret_cast<float*>(hist) + lane;
+      *dst = v;
     }
   };
   float kf[D][NS][8];
+  // (issued in order, each refill right after its consumer: the scheduler
+  // would otherwise reorder them, and the wait before a chunk's use would then
+  // also cover the chunks loaded after it)
 #pragma unroll
-  for (int d = 0; d < D; ++d) load(wave + 4 * d, kf[d]);
+  for (int d = 0; d < D; ++d) {
+    load(wave + 4 * d, kf[d]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
   // chunks past this wave's last are consumed too: their blocks lie beyond
   // every query's visible count, so nothing is stored (a condition here would
   // cost the loads' overlap)
@@ -184,6 +213,7 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
     for (int d = 0; d < D; ++d) {
       consume(wave + 4 * (m0 + d), kf[d]);
       load(wave + 4 * (m0 + d + D), kf[d]);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
   __syncthreads();
