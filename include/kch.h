@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define KCH_ABI_VERSION 7
+#define KCH_ABI_VERSION 8
 
 #define KCH_OK 0
 #define KCH_ERR_INVALID 1     /* bad pointer / shape / argument */
@@ -268,6 +268,18 @@ int kch_kda_gates(const void* proj, long long ld_proj, const void* gl, long long
  */
 int kch_layer_norm(const void* x, const void* w, const void* b, void* out, int rows, int d,
                    float eps, int dtype, int wdtype, void* stream);
+
+/*
+ * Linear map of up to 16 rows, torch.nn.functional.linear without bias as the
+ * layer projections of a decode step call it (ops_fused.py:571-581,609,713,739;
+ * run_decoding.py:334-336,522,598,783,815):
+ *   y[m, n] = sum_k x[m, k] * w[n, k]   (fp32 accumulation, result in dtype)
+ * x [M, K] (row stride ldx), w [N, K] (row stride ldw), y [M, N] (row stride
+ * ldy), all of dtype (1 bf16, 2 fp16). 1 <= M <= 16; K a multiple of 32; x and
+ * w 16-byte aligned with ldx, ldw multiples of 8.
+ */
+int kch_linear_rows(const void* x, long long ldx, const void* w, long long ldw, void* y,
+                    long long ldy, int M, int N, int K, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

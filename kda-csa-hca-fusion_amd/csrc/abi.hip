@@ -385,6 +385,25 @@ int kch_layer_norm(const void* x, const void* w, const void* b, void* out, int r
   return hip_status(fn, kch::layer_norm_dispatch(p, dtype, wdtype, (hipStream_t)stream));
 }
 
+int kch_linear_rows(const void* x, long long ldx, const void* w, long long ldw, void* y,
+                    long long ldy, int M, int N, int K, int dtype, void* stream) {
+  const char* fn = "kch_linear_rows";
+  if (dtype != KCH_DT_BF16 && dtype != KCH_DT_F16)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: dtype %d (bf16 or fp16 only)", fn, dtype);
+  if (M < 0 || N < 0 || K < 0) return fail(KCH_ERR_INVALID, "%s: bad sizes", fn);
+  if (M == 0 || N == 0) return KCH_OK;
+  if (M > 16) return fail(KCH_ERR_UNSUPPORTED, "%s: M=%d > 16 rows", fn, M);
+  if (K < 32 || K % 32) return fail(KCH_ERR_UNSUPPORTED, "%s: K=%d not a multiple of 32", fn, K);
+  if (!x || !w || !y) return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
+  if (ldx < K || ldw < K || ldy < N)
+    return fail(KCH_ERR_INVALID, "%s: row strides (%lld, %lld, %lld) below the row lengths", fn,
+                ldx, ldw, ldy);
+  if ((ldx | ldw) % 8 || (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) % 16)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: x and w rows must be 16-byte aligned", fn);
+  kch::LinearRowsParams p{x, w, y, ldx, ldw, ldy, M, N, K};
+  return hip_status(fn, kch::linear_rows_dispatch(p, dtype, (hipStream_t)stream));
+}
+
 }  // extern "C"
 
 namespace {

@@ -76,4 +76,14 @@ struct LayerNormParams {
 };
 hipError_t layer_norm_dispatch(const LayerNormParams& p, int dtype, int wdtype, hipStream_t stream);
 
+// y[M, N] = x[M, K] w[N, K]^T for M <= 16 rows (linear_rows.hip).
+struct LinearRowsParams {
+  const void* x;
+  const void* w;
+  void* y;
+  long long ldx, ldw, ldy;  // row strides in elements
+  int M, N, K;
+};
+hipError_t linear_rows_dispatch(const LinearRowsParams& p, int dtype, hipStream_t stream);
+
 }  // namespace kch

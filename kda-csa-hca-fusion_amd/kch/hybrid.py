@@ -46,6 +46,32 @@ logger = logging.getLogger(__name__)
 _CONV_K = 3  # short-conv kernel size (ops_fused.py:333)
 
 
+def _rows_ok(t: torch.Tensor) -> bool:
+    return t.stride(-1) == 1 and t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0
+
+
+def _linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """``F.linear(x, w)`` without bias. A decode step's few rows (at most 16)
+    go to ``kch_linear_rows``, one HIP launch: a BLAS call costs more host time
+    than its GEMM takes on the GPU at that size. Larger inputs use ``F.linear``."""
+    K = x.shape[-1]
+    rows = x.numel() // K if K else 0
+    if not (x.is_cuda and x.dtype in (torch.bfloat16, torch.float16) and w.dtype == x.dtype
+            and 0 < rows <= 16 and K % 32 == 0 and w.dim() == 2 and w.shape[1] == K):
+        return F.linear(x, w)
+    xr = x.reshape(rows, K)
+    if not _rows_ok(xr):
+        xr = xr.contiguous()
+    if not _rows_ok(w):
+        w = w.contiguous()
+    N = w.shape[0]
+    y = torch.empty(*x.shape[:-1], N, device=x.device, dtype=x.dtype)
+    _lib.call("kch_linear_rows", _lib.ptr(xr), xr.stride(0), _lib.ptr(w), w.stride(0),
+              _lib.ptr(y), N, rows, N, K, _lib.dtype_code("kch_linear_rows", x.dtype),
+              _lib.stream_of(x))
+    return y
+
+
 class _Fp32LayerNorm(nn.LayerNorm):
     """LayerNorm computed in fp32, returned in the input dtype (``ops_fused.py:42-60``),
     as one kernel (``kch_layer_norm``)."""
@@ -289,9 +315,9 @@ class KDAHybridLayer(nn.Module):
                       _lib.ptr(x_conv), B, T, d, code, stream)
             W = self._fused.get([self.q_proj.weight, self.k_proj.weight, self.v_proj.weight,
                                  self.beta.weight, self.g_down.weight], x.dtype, x.device)
-            proj = F.linear(x_conv, W)  # [B, T, 2HK + HV*V + HV + K]
+            proj = _linear(x_conv, W)  # [B, T, 2HK + HV*V + HV + K]
             off_gd = 2 * H * K + HV * V + HV
-            gl = F.linear(proj[..., off_gd:off_gd + K], self.g_up.weight.to(x.dtype))
+            gl = _linear(proj[..., off_gd:off_gd + K], self.g_up.weight.to(x.dtype))
             q = torch.empty(B, T, H, K, device=x.device, dtype=x.dtype)
             k = torch.empty_like(q)
             v = torch.empty(B, T, HV, V, device=x.device, dtype=x.dtype)
@@ -314,7 +340,7 @@ class KDAHybridLayer(nn.Module):
                 if state_out is not None:
                     state_out.copy_(new_state)
                     new_state = state_out
-            out = self.o_proj(o.reshape(B, T, HV * V))
+            out = _linear(o.reshape(B, T, HV * V), self.o_proj.weight)
         return out, new_state, new_lookback
 
 
@@ -591,10 +617,10 @@ class HybridDecoding(nn.Module):
         W = layer._fused.get([layer.W_aKV.weight, layer.W_bKV.weight, layer.W_aZ.weight,
                               layer.W_bZ.weight, layer.W_KV_idx.weight, layer.W_Z_idx.weight,
                               layer.W_DQ.weight, layer.W_w.weight], h.dtype, h.device)
-        out = F.linear(h, W)
+        out = _linear(h, W)
         Ca, Cb, Za, Zb, K_idx, Z_idx, cQ, w_idx = out.split([c, c, c, c, cI, cI, dc, nIh], -1)
-        q = F.linear(cQ, layer.W_UQ.weight).view(B, T, nh, c)
-        q_idx = F.linear(cQ, layer.W_IUQ.weight).view(B, T, nIh, cI)
+        q = _linear(cQ, layer.W_UQ.weight).view(B, T, nh, c)
+        q_idx = _linear(cQ, layer.W_IUQ.weight).view(B, T, nIh, cI)
         return Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx
 
     @staticmethod
@@ -603,8 +629,8 @@ class HybridDecoding(nn.Module):
         B, T, _ = h.shape
         W = layer._fused.get([layer.W_KV.weight, layer.W_Z.weight, layer.W_DQ.weight],
                              h.dtype, h.device)
-        C, Z, cQ = F.linear(h, W).split([cfg.hca_c, cfg.hca_c, cfg.hca_dc], -1)
-        q = F.linear(cQ, layer.W_UQ.weight).view(B, T, cfg.hca_nh, cfg.hca_c)
+        C, Z, cQ = _linear(h, W).split([cfg.hca_c, cfg.hca_c, cfg.hca_dc], -1)
+        q = _linear(cQ, layer.W_UQ.weight).view(B, T, cfg.hca_nh, cfg.hca_c)
         return C, Z, q
 
     def _forward_csa_layer(self, layer: CSAHybridLayer, h: torch.Tensor, idx: int):
@@ -632,7 +658,7 @@ class HybridDecoding(nn.Module):
                                    use_ste=False, normalize_qk=True, _normalize_q=True,
                                    _out_dtype=h.dtype)
             o_core = o.reshape(B, T_new, cfg.csa_nh * cfg.csa_c)
-        return layer.o_proj(o_core)
+        return _linear(o_core, layer.o_proj.weight)
 
     def _forward_hca_layer(self, layer: HCAHybridLayer, h: torch.Tensor, idx: int):
         cfg = layer.cfg
@@ -654,7 +680,7 @@ class HybridDecoding(nn.Module):
             o = cache.forward_step(q, nh=cfg.hca_nh, scale=1.0, sink_logits=layer.sink,
                                    _normalize_q=True, _out_dtype=h.dtype)
             o_core = o.reshape(B, T_new, cfg.hca_nh * cfg.hca_c)
-        return layer.o_proj(o_core)
+        return _linear(o_core, layer.o_proj.weight)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         B = x.shape[0]

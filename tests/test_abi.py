@@ -51,6 +51,11 @@ def test_invalid_arguments_report_errors_without_gpu():
                                1, 8, 2, 2, 96, 128, ctypes.c_float(1.0),
                                ctypes.c_float(-10.0), 1, None)
     assert rc == 2
+    # kch_linear_rows: row count and K checked before any pointer or HIP call
+    rc = lib.kch_linear_rows(None, 64, None, 64, None, 8, 17, 8, 64, 1, None)
+    assert rc == 2 and b"M=17" in lib.kch_last_error()
+    rc = lib.kch_linear_rows(None, 64, None, 64, None, 8, 2, 8, 48, 1, None)
+    assert rc == 2 and b"multiple of 32" in lib.kch_last_error()
 
 
 def test_chunk_workspace_size_query():
