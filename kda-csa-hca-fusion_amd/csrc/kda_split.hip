@@ -183,17 +183,22 @@ __global__ __launch_bounds__(256, 2) void kda_prep_kernel(KdaParams p, SplitPtrs
   const InT* krow = static_cast<const InT*>(p.k) + ((size_t)(b * T + tl) * p.H + h) * K;
   const InT* grow = static_cast<const InT*>(p.g) + ((size_t)(b * T + tl) * p.HV + hv) * K;
   const InT* vrow = static_cast<const InT*>(p.v) + ((size_t)(b * T + tl) * p.HV + hv) * V;
+  // Issued in the order they are consumed (the gate scan, beta, the factor
+  // stage's k and q, then v): memory waits count in issue order, so a value
+  // needed early must not sit behind loads needed later.
   uint4 rq[KS], rk[KS], rg[KS], rv[VS];
 #pragma unroll
+  for (int s = 0; s < KS; ++s) rg[s] = *reinterpret_cast<const uint4*>(grow + 32 * s + 8 * q4);
+  const float bt =
+      valid ? to_f32(static_cast<const InT*>(p.beta)[(size_t)(b * T + tl) * p.HV + hv]) : 0.f;
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
   for (int s = 0; s < KS; ++s) {
-    rg[s] = *reinterpret_cast<const uint4*>(grow + 32 * s + 8 * q4);
     rk[s] = *reinterpret_cast<const uint4*>(krow + 32 * s + 8 * q4);
     rq[s] = *reinterpret_cast<const uint4*>(qrow + 32 * s + 8 * q4);
   }
 #pragma unroll
   for (int s = 0; s < VS; ++s) rv[s] = *reinterpret_cast<const uint4*>(vrow + 32 * s + 8 * q4);
-  const float bt =
-      valid ? to_f32(static_cast<const InT*>(p.beta)[(size_t)(b * T + tl) * p.HV + hv]) : 0.f;
   if (tid == 0) sFlag[0] = 0;
 
   // ---- gate: clamp, log2 units, in-tile inclusive scan over the 16 tokens of the row ----
