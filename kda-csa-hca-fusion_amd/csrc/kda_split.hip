@@ -739,13 +739,8 @@ __global__ __launch_bounds__(256, BV == 32 ? 2 : 1) void kda_state_kernel(KdaPar
         oa[ct] = mfma32(sf, cur.qg[s], oa[ct]);
       }
     }
-    // one pair of products, two LDS reads and one global request at a time
-#pragma unroll
-    for (int i = 0; i < KS * CT; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
-    }
+    // (the compiler's own order of these reads, products and requests is as
+    // fast as a forced interleave of two reads, two products and one request)
     load(nxt, npf, 1);
     // v_new = U - W' S (lane: tokens 16 wave + 4 q4 + e of column 16 ct + r)
 #pragma unroll
