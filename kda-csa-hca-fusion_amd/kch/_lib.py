@@ -103,7 +103,16 @@ def ptr(t):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
+# torch's raw current-stream query (one C call) where this torch provides it;
+# torch.cuda.current_stream() costs about 2 us of host time per call, which a
+# decode step pays some thirty times
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t: torch.Tensor):
+    """The current HIP stream of ``t``'s device, as a ctypes pointer."""
+    if _raw_stream is not None and t.is_cuda:
+        return ctypes.c_void_p(_raw_stream(t.get_device()))
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
