@@ -35,21 +35,8 @@ __device__ __forceinline__ uint32_t order_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Exclusive prefix sum over the 64 lanes with DPP: row_shr 1, 2, 4, 8 scan each
-// 16-lane row (a lane whose source lies before its row start adds 0), then
-// row_bcast:15 adds row 0's total to row 1 and row 2's to row 3, and
-// row_bcast:31 adds the total of rows 0-1 to rows 2 and 3 (lanes outside the
-// row mask keep 0).
-__device__ __forceinline__ int wave_excl_scan(int v) {
-  int x = v;
-  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);
-  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);
-  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);
-  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);
-  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);
-  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);
-  return x - v;
-}
+// Exclusive prefix sum over the 64 lanes.
+__device__ __forceinline__ int wave_excl_scan(int v) { return wave_incl_scan(v) - v; }
 
 typedef unsigned long long u64;
 
