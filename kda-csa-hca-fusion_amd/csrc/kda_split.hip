@@ -381,8 +381,13 @@ __global__ __launch_bounds__(256, 2) void kda_prep_kernel(KdaParams p, SplitPtrs
     }
   }
   {
-    const int fl = (dmax > kRange2 ? 1 : 0) | (gmax > 0.f ? 2 : 0) | (dmax > kPos2 ? 4 : 0);
-    if (fl) atomicOr(sFlag, fl);
+    // the wave's flags, OR-ed by ballots: one LDS atomic per wave (the lanes'
+    // own atomics on one word serialise, and the outer token tiles, far from
+    // the anchor, set the range flag on most lanes)
+    const int fl = (__builtin_amdgcn_ballot_w64(dmax > kRange2) ? 1 : 0) |
+                   (__builtin_amdgcn_ballot_w64(gmax > 0.f) ? 2 : 0) |
+                   (__builtin_amdgcn_ballot_w64(dmax > kPos2) ? 4 : 0);
+    if (fl && lane == 0) atomicOr(sFlag, fl);
   }
   __syncthreads();  // ---- B2: sB exchange, kg^T, (beta v)^T, flags ----
 
