@@ -238,7 +238,15 @@ __global__ __launch_bounds__(256) void kda_chunk_kernel(KdaParams p) {
       if (dm > 120.f) flag |= 1;
       if (dm > 25.f * LOG2E) flag |= 4;
     }
-    if (flag) atomicOr(&sFlag[n & 1], flag);
+    // OR-ed over the active lanes by ballots: one LDS atomic per wave, from its
+    // first active lane (the lanes' own atomics on one word serialise)
+    {
+      const int wf = (__builtin_amdgcn_ballot_w64((flag & 1) != 0) ? 1 : 0) |
+                     (__builtin_amdgcn_ballot_w64((flag & 2) != 0) ? 2 : 0) |
+                     (__builtin_amdgcn_ballot_w64((flag & 4) != 0) ? 4 : 0);
+      const int first = __ffsll((long long)__builtin_amdgcn_ballot_w64(true)) - 1;
+      if (wf && (int)(threadIdx.x & 63) == first) atomicOr(&sFlag[n & 1], wf);
+    }
     if (cp == 0) {
 #pragma unroll
       for (int i = 0; i < NTOK; ++i) sBeta[r0 + i] = rb[i];

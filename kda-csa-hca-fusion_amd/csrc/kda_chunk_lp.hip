@@ -275,7 +275,15 @@ __global__ __launch_bounds__(512) void kda_chunk_lp_kernel(KdaParams p) {
       }
       const bool bad = !(dmax <= kRange2) || !(amin >= -kRange2);
       const int fl = (bad ? 1 : 0) | (gmax > 0.f ? 2 : 0) | (dmax > kPos2 ? 4 : 0);
-      if (fl) atomicOr(&sFlag[n & 1], fl);
+      // OR-ed over the active lanes by ballots: one LDS atomic per wave, from its
+      // first active lane (the lanes' own atomics on one word serialise)
+      {
+        const int wf = (__builtin_amdgcn_ballot_w64((fl & 1) != 0) ? 1 : 0) |
+                       (__builtin_amdgcn_ballot_w64((fl & 2) != 0) ? 2 : 0) |
+                       (__builtin_amdgcn_ballot_w64((fl & 4) != 0) ? 4 : 0);
+        const int first = __ffsll((long long)__builtin_amdgcn_ballot_w64(true)) - 1;
+        if (wf && (int)(threadIdx.x & 63) == first) atomicOr(&sFlag[n & 1], wf);
+      }
       // row-major operands [token][channel]: CPL channels per token
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
