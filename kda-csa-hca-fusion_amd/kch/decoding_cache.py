@@ -208,6 +208,42 @@ def _ring_bf16(sw):
     return buf if buf.dtype == torch.bfloat16 else buf.to(torch.bfloat16)
 
 
+def _alloc_acc(new, B, m):
+    """Accumulators for the projections of a block still being filled: one
+    ``[B, m, sum of widths]`` buffer split into per-input views when the inputs
+    share a dtype (so that one copy can fill them all), else separate buffers."""
+    widths = [x.shape[-1] for x in new]
+    dt, dev = new[0].dtype, new[0].device
+    if all(x.dtype == dt for x in new):
+        buf = torch.empty(B, m, sum(widths), device=dev, dtype=dt)
+        return buf, list(buf.split(widths, -1))
+    return None, [torch.empty(B, m, w, device=dev, dtype=x.dtype) for w, x in zip(widths, new)]
+
+
+def _column_group(ts):
+    """One ``[..., sum of widths]`` view over ``ts`` when they are adjacent column
+    ranges of one tensor (the slices of one projection output), else None."""
+    t0 = ts[0]
+    st = t0.stride()
+    if st[-1] != 1:
+        return None
+    lead, dt, es = t0.shape[:-1], t0.dtype, t0.element_size()
+    p, w = t0.data_ptr(), 0
+    for t in ts:
+        if t.dtype != dt or t.stride() != st or t.shape[:-1] != lead or t.data_ptr() != p + w * es:
+            return None
+        w += t.shape[-1]
+    return t0.as_strided((*lead, w), st)
+
+
+def _ring_rows(x, dtype, normalize):
+    """Sliding-window rows of ``x``: L2-normalised in fp32 and rounded to the
+    cache dtype (the kernel writes bf16 itself, rounding the same fp32 value)."""
+    if dtype == torch.bfloat16:
+        return l2_normalize_rows(x, out_dtype=torch.bfloat16, normalize=normalize)
+    return l2_normalize_rows(x, out_dtype=torch.float32, normalize=normalize).to(dtype)
+
+
 class CSADecodingCache:
     """CSA incremental decode state (``ops_decoding_cache.py:407-1070``) on the HIP backend."""
 
@@ -230,6 +266,7 @@ class CSADecodingCache:
 
     def reset(self) -> None:
         self._acc = None          # 6 buffers [B, m, width] (projection dtype)
+        self._acc_buf = None      # the buffer they are views of, if one
         self._acc_len = 0
         self._prev = None         # (Cb, Zb) of the last completed block, [B, m, c]
         self._C = _BlockStore(self.B, self.c, self.device, self.dtype, torch.bfloat16)
@@ -270,7 +307,10 @@ class CSADecodingCache:
         if dtype is not None:
             _validate_cache_dtype(dtype)
             self.dtype = dtype
-        if self._acc is not None:
+        if self._acc_buf is not None:
+            self._acc_buf = self._acc_buf.to(device=self.device)
+            self._acc = list(self._acc_buf.split([a.shape[-1] for a in self._acc], -1))
+        elif self._acc is not None:
             self._acc = [a.to(device=self.device) for a in self._acc]
         if self._prev is not None:
             self._prev = tuple(p.to(device=self.device) for p in self._prev)
@@ -306,11 +346,9 @@ class CSADecodingCache:
         new = [Ca_new, Cb_new, Za_new, Zb_new, K_idx_new, Z_idx_new]
         with torch.no_grad():
             if self._sw is not None:
-                self._sw.append(l2_normalize_rows(Ca_new, out_dtype=torch.float32,
-                                                  normalize=self._normalize_qk).to(self.dtype))
+                self._sw.append(_ring_rows(Ca_new, self.dtype, self._normalize_qk))
             if self._acc is None:
-                self._acc = [torch.empty(B, self.m, x.shape[-1], device=x.device, dtype=x.dtype)
-                             for x in new]
+                self._acc_buf, self._acc = _alloc_acc(new, B, self.m)
             total = self._acc_len + T_new
             nfull = total // self.m
             rem = total - nfull * self.m
@@ -338,8 +376,12 @@ class CSADecodingCache:
                     if rem:
                         a[:, :rem] = x[:, T_new - rem:].to(a.dtype)
             else:
-                for a, x in zip(self._acc, new):
-                    a[:, self._acc_len:total] = x.to(a.dtype)
+                grp = None if self._acc_buf is None else _column_group(new)
+                if grp is not None and grp.dtype == self._acc_buf.dtype:
+                    self._acc_buf[:, self._acc_len:total] = grp
+                else:
+                    for a, x in zip(self._acc, new):
+                        a[:, self._acc_len:total] = x.to(a.dtype)
             self._acc_len = rem
             self._n_tokens_seen += T_new
         return out_idx
@@ -432,6 +474,7 @@ class HCADecodingCache:
 
     def reset(self) -> None:
         self._acc = None
+        self._acc_buf = None
         self._acc_len = 0
         self._C = _BlockStore(self.B, self.c, self.device, self.dtype, torch.bfloat16)
         self._sw = (SlidingWindowRingBuffer(self.B, self.win, self.c, self.device, self.dtype)
@@ -465,7 +508,10 @@ class HCADecodingCache:
         if dtype is not None:
             _validate_cache_dtype(dtype)
             self.dtype = dtype
-        if self._acc is not None:
+        if self._acc_buf is not None:
+            self._acc_buf = self._acc_buf.to(device=self.device)
+            self._acc = list(self._acc_buf.split([a.shape[-1] for a in self._acc], -1))
+        elif self._acc is not None:
             self._acc = [a.to(device=self.device) for a in self._acc]
         self._C.to(self.device, self.dtype, self._n_blocks)
         if self._sw is not None:
@@ -492,11 +538,9 @@ class HCADecodingCache:
         new = [C_new, Z_new]
         with torch.no_grad():
             if self._sw is not None:
-                self._sw.append(l2_normalize_rows(C_new, out_dtype=torch.float32,
-                                                  normalize=self._normalize_qk).to(self.dtype))
+                self._sw.append(_ring_rows(C_new, self.dtype, self._normalize_qk))
             if self._acc is None:
-                self._acc = [torch.empty(B, self.m2, x.shape[-1], device=x.device, dtype=x.dtype)
-                             for x in new]
+                self._acc_buf, self._acc = _alloc_acc(new, B, self.m2)
             total = self._acc_len + T_new
             nfull = total // self.m2
             rem = total - nfull * self.m2
@@ -513,8 +557,12 @@ class HCADecodingCache:
                     if rem:
                         a[:, :rem] = x[:, T_new - rem:].to(a.dtype)
             else:
-                for a, x in zip(self._acc, new):
-                    a[:, self._acc_len:total] = x.to(a.dtype)
+                grp = None if self._acc_buf is None else _column_group(new)
+                if grp is not None and grp.dtype == self._acc_buf.dtype:
+                    self._acc_buf[:, self._acc_len:total] = grp
+                else:
+                    for a, x in zip(self._acc, new):
+                        a[:, self._acc_len:total] = x.to(a.dtype)
             self._acc_len = rem
             self._n_tokens_seen += T_new
         return out_idx

@@ -212,10 +212,14 @@ class _FusedWeight:
         self._key = None
         self._w = None
 
-    def get(self, params, dtype, device) -> torch.Tensor:
-        key = tuple((p.data_ptr(), p._version) for p in params) + (dtype, device)
+    def get(self, params, dtype, device, build=None):
+        """The row-concatenation of ``params`` in ``dtype`` on ``device``, or
+        ``build()``'s result (anything derived from ``params``) when given."""
+        key = tuple((0, 0) if p is None else (p.data_ptr(), p._version)
+                    for p in params) + (dtype, device)
         if key != self._key:
-            self._w = torch.cat([p.detach() for p in params], 0).to(device=device, dtype=dtype)
+            self._w = (torch.cat([p.detach() for p in params], 0).to(device=device, dtype=dtype)
+                       if build is None else build())
             self._key = key
         return self._w
 
@@ -244,13 +248,34 @@ class KDAHybridLayer(nn.Module):
         self.register_buffer('scale', torch.tensor(K ** -0.5), persistent=False)
         self.register_buffer('_conv_lookback', None, persistent=False)
         self._fused = _FusedWeight()
+        self._scale_cache = None
 
     def reset_conv_state(self) -> None:
         self._conv_lookback = None
 
     def _scale_value(self) -> float:
-        # K^-0.5 rounded to the buffer's dtype, computed on the host (no device sync)
-        return float(torch.tensor(self.cfg.head_dim_k ** -0.5).to(self.scale.dtype))
+        # K^-0.5 rounded to the buffer's dtype, computed on the host (no device
+        # sync) once per dtype
+        dt = self.scale.dtype
+        if self._scale_cache is None or self._scale_cache[0] != dt:
+            self._scale_cache = (dt, float(torch.tensor(self.cfg.head_dim_k ** -0.5).to(dt)))
+        return self._scale_cache[1]
+
+    def _weights(self, dtype, device):
+        """(fused q/k/v/beta/g_down weight, conv weight [d, 3], conv bias, g_up
+        weight) in ``dtype``, rebuilt only when a parameter changes."""
+        conv, bias = self.short_conv.weight, self.short_conv.bias
+        fused = [self.q_proj.weight, self.k_proj.weight, self.v_proj.weight,
+                 self.beta.weight, self.g_down.weight]
+        g_up = self.g_up.weight
+
+        def build():
+            W = torch.cat([p.detach() for p in fused], 0).to(device=device, dtype=dtype)
+            w = conv.detach().to(device=device, dtype=dtype).reshape(conv.shape[0], _CONV_K)
+            b = None if bias is None else bias.detach().to(device=device, dtype=dtype)
+            return W, w.contiguous(), None if b is None else b.contiguous(), \
+                g_up.detach().to(device=device, dtype=dtype)
+        return self._fused.get(fused + [conv, bias, g_up], dtype, device, build)
 
     def forward(self, x: torch.Tensor, state: torch.Tensor | None = None, *,
                 state_out: torch.Tensor | None = None):
@@ -307,17 +332,13 @@ class KDAHybridLayer(nn.Module):
                 new_lookback = torch.cat([x.new_zeros(B, _CONV_K - 1 - T, d), x], dim=1)
             code = _lib.dtype_code("KDAHybridLayer", x.dtype)
             stream = _lib.stream_of(xc)
-            w = self.short_conv.weight.detach().to(x.dtype).reshape(d, _CONV_K).contiguous()
-            bias = self.short_conv.bias
-            bias = None if bias is None else bias.detach().to(x.dtype).contiguous()
+            W, w, bias, g_up = self._weights(x.dtype, x.device)
             x_conv = torch.empty_like(xc)
             _lib.call("kch_short_conv", _lib.ptr(xc), _lib.ptr(lb), _lib.ptr(w), _lib.ptr(bias),
                       _lib.ptr(x_conv), B, T, d, code, stream)
-            W = self._fused.get([self.q_proj.weight, self.k_proj.weight, self.v_proj.weight,
-                                 self.beta.weight, self.g_down.weight], x.dtype, x.device)
             proj = _linear(x_conv, W)  # [B, T, 2HK + HV*V + HV + K]
             off_gd = 2 * H * K + HV * V + HV
-            gl = _linear(proj[..., off_gd:off_gd + K], self.g_up.weight.to(x.dtype))
+            gl = _linear(proj[..., off_gd:off_gd + K], g_up)
             q = torch.empty(B, T, H, K, device=x.device, dtype=x.dtype)
             k = torch.empty_like(q)
             v = torch.empty(B, T, HV, V, device=x.device, dtype=x.dtype)
