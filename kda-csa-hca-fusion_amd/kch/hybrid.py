@@ -38,7 +38,7 @@ from . import _lib
 from .decoding_cache import CSADecodingCache, HCADecodingCache
 from .ops_csa import naive_csa
 from .ops_hca import naive_hca
-from .ops_kda import kda_recurrent_into
+from .ops_kda import _recurrent_launch, kda_recurrent_into
 from .ops_kda_backend import kda_forward, validate_kda_backend
 
 logger = logging.getLogger(__name__)
@@ -351,7 +351,15 @@ class KDAHybridLayer(nn.Module):
             if state_out is not None and not use_chunk:
                 # the recurrent kernel reads and writes each state element in the
                 # same thread, so the state may be updated in place
-                o = kda_recurrent_into(q, k, v, g, beta, self._scale_value(), state, state_out)
+                if T > 0 and B > 0 and (state is None or state.data_ptr() == state_out.data_ptr()) \
+                        and state_out.dtype == torch.float32 and state_out.is_contiguous() \
+                        and state_out.shape == (B, HV, K, V) and state_out.device == x.device:
+                    # q, k, v, g, beta are this layer's own kch_kda_gates outputs
+                    o = _recurrent_launch(q, k, v, g, beta, self._scale_value(), state,
+                                          state_out, code, stream)
+                else:
+                    o = kda_recurrent_into(q, k, v, g, beta, self._scale_value(), state,
+                                           state_out)
                 new_state = state_out
             else:
                 o, new_state = kda_forward(

@@ -170,16 +170,27 @@ def kda_recurrent_into(q, k, v, g, beta, scale, state, state_out):
     if state is not None:
         s0 = state if state.data_ptr() == state_out.data_ptr() else \
             state.to(device=q.device, dtype=torch.float32).contiguous()
-    o = torch.empty_like(v)
     if T == 0 or B == 0:
         if s0 is None:
             state_out.zero_()
         elif s0.data_ptr() != state_out.data_ptr():
             state_out.copy_(s0)
-        return o
+        return torch.empty_like(v)
+    return _recurrent_launch(q, k, v, g, beta, _scale_value(scale, K), s0, state_out, code,
+                             _lib.stream_of(q))
+
+
+def _recurrent_launch(q, k, v, g, beta, scale: float, s0, state_out, code, stream):
+    """``kch_kda_recurrent_fwd`` on inputs already checked or built consistent by
+    the caller: q, k ``[B,T,H,K]``, v ``[B,T,HV,V]``, g ``[B,T,HV,K]``, beta
+    ``[B,T,HV]``, all contiguous, 16-byte aligned, one dtype; ``s0`` None, or an
+    fp32 ``[B,HV,K,V]`` state that may be ``state_out`` itself. Returns ``o``."""
+    B, T, H, K = q.shape
+    HV, V = v.shape[2], v.shape[-1]
+    o = torch.empty_like(v)
     _lib.call("kch_kda_recurrent_fwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g),
               _lib.ptr(beta), _lib.ptr(s0), _lib.ptr(o), _lib.ptr(state_out), B, T, H, HV, K, V,
-              _scale_value(scale, K), _clamp_value(-10.0), code, _lib.stream_of(q))
+              scale, -10.0, code, stream)
     return o
 
 
