@@ -59,14 +59,21 @@ def _linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     if not (x.is_cuda and x.dtype in (torch.bfloat16, torch.float16) and w.dtype == x.dtype
             and 0 < rows <= 16 and K % 32 == 0 and w.dim() == 2 and w.shape[1] == K):
         return F.linear(x, w)
-    xr = x.reshape(rows, K)
-    if not _rows_ok(xr):
-        xr = xr.contiguous()
-    if not _rows_ok(w):
-        w = w.contiguous()
+    if x.is_contiguous() and x.data_ptr() % 16 == 0:
+        xr = x  # rows of K elements, K % 32 == 0
+    else:
+        xr = x.reshape(rows, K)
+        if not _rows_ok(xr):
+            xr = xr.contiguous()
+    if w.is_contiguous() and w.data_ptr() % 16 == 0:
+        ldw = K  # a contiguous [N, K] weight (its stride(0) is arbitrary when N == 1)
+    else:
+        if not _rows_ok(w):
+            w = w.contiguous()
+        ldw = w.stride(0)
     N = w.shape[0]
     y = torch.empty(*x.shape[:-1], N, device=x.device, dtype=x.dtype)
-    _lib.call("kch_linear_rows", _lib.ptr(xr), xr.stride(0), _lib.ptr(w), w.stride(0),
+    _lib.call("kch_linear_rows", _lib.ptr(xr), K if xr is x else xr.stride(0), _lib.ptr(w), ldw,
               _lib.ptr(y), N, rows, N, K, _lib.dtype_code("kch_linear_rows", x.dtype),
               _lib.stream_of(x))
     return y

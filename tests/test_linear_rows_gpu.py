@@ -66,3 +66,19 @@ def test_linear_rows_in_hybrid_decode_matches_f_linear(dev):
         ref = torch.nn.functional.linear(x.float(), w.float())
         assert tuple(y.shape) == (rows, 1, 512)
         assert float((y.float() - ref).abs().max()) <= 1e-2 * float(ref.abs().max())
+
+
+def test_linear_rows_in_hybrid_decode_views(dev):
+    # column slices of a wider input and row slices of a wider weight take the
+    # strided path; a one-row weight view takes the contiguous one
+    from kch import hybrid
+    g = torch.Generator(device="cpu").manual_seed(10)
+    xw = torch.randn(3, 1, 2048 + 256, generator=g).to(dev, torch.bfloat16)
+    ww = (torch.randn(700, 2048, generator=g) / 45.0).to(dev, torch.bfloat16)
+    cases = [(xw[..., :2048], ww[:512]), (xw[..., 64:64 + 2048], ww[8:520]),
+             (xw[..., :2048].contiguous(), ww[5:6]), (xw[..., 256:], ww[:, :2048])]
+    for x, w in cases:
+        y = hybrid._linear(x, w)
+        ref = torch.nn.functional.linear(x.float(), w.float())
+        assert tuple(y.shape) == (3, 1, w.shape[0])
+        assert float((y.float() - ref).abs().max()) <= 1e-2 * float(ref.abs().max())
