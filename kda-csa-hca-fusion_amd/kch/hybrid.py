@@ -86,16 +86,20 @@ class _Fp32LayerNorm(nn.LayerNorm):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if x.numel() == 0:
             return torch.empty_like(x)
-        _lib.require_gpu("_Fp32LayerNorm", x)
-        d = self.normalized_shape[-1]
-        if len(self.normalized_shape) != 1 or x.shape[-1] != d or self.weight is None:
+        if not x.is_cuda:
+            _lib.require_gpu("_Fp32LayerNorm", x)
+        ns, w, b = self.normalized_shape, self.weight, self.bias
+        d = ns[-1]
+        if len(ns) != 1 or x.shape[-1] != d or w is None:
             raise ValueError("_Fp32LayerNorm: expects an affine LayerNorm over the last dim")
         xc = x.contiguous()
         out = torch.empty_like(xc)
         fn = "_Fp32LayerNorm"
-        w = self.weight.detach()
-        b = None if self.bias is None else self.bias.detach().to(w.dtype).contiguous()
-        _lib.call("kch_layer_norm", _lib.ptr(xc), _lib.ptr(w.contiguous()), _lib.ptr(b),
+        # the kernel reads the parameters through raw pointers: no autograd use
+        w = w.contiguous()
+        if b is not None and (b.dtype != w.dtype or not b.is_contiguous()):
+            b = b.detach().to(w.dtype).contiguous()
+        _lib.call("kch_layer_norm", _lib.ptr(xc), _lib.ptr(w), _lib.ptr(b),
                   _lib.ptr(out), xc.numel() // d, d, float(self.eps),
                   _lib.dtype_code(fn, xc.dtype), _lib.dtype_code(fn, w.dtype),
                   _lib.stream_of(xc))
