@@ -331,13 +331,15 @@ def csa_projections(H, W, dtype='bf16', *, c, cI, nh, nIh):
 
 
 def naive_csa(H, W, *, m, topk, nh, nIh, c, c_I, sliding_window=0, sink=None,
-              dtype='bf16', normalize_qk=True):
-    """Full CSA forward incl. projections; returns ``[B,T,nh*c]`` rounded to dtype."""
+              dtype='bf16', normalize_qk=True, indices=None):
+    """Full CSA forward incl. projections; returns ``[B,T,nh*c]`` rounded to dtype.
+
+    ``indices`` (``[B,T,topk]``) replaces the indexer's selection (see ``csa_core``)."""
     Bn, T, _ = H.shape
     proj = csa_projections(H, W, dtype, c=c, cI=c_I, nh=nh, nIh=nIh)
     out = csa_core(*proj, W['Ba'], W['Bb'], W['B_idx'], m=m, topk=topk,
                    sliding_window=sliding_window, sink_logits=sink,
-                   normalize_qk=normalize_qk)
+                   normalize_qk=normalize_qk, indices=indices)
     return round_to(out.reshape(Bn, T, nh * c), dtype), proj
 
 

@@ -121,10 +121,11 @@ def _hca_w(W):
     return out
 
 
-def csa_layer(x, W, cfg, dtype='fp32'):
+def csa_layer(x, W, cfg, dtype='fp32', indices=None):
     o, _ = naive_csa(x, _csa_w(W), m=cfg['csa_m'], topk=cfg['csa_topk'], nh=cfg['csa_nh'],
                      nIh=cfg['csa_nIh'], c=cfg['csa_c'], c_I=cfg['csa_cI'],
-                     sliding_window=cfg['csa_sliding_window'], sink=W['sink'], dtype=dtype)
+                     sliding_window=cfg['csa_sliding_window'], sink=W['sink'], dtype=dtype,
+                     indices=indices)
     return linear_lowp(o, W['o_proj.weight'], dtype)
 
 
@@ -148,8 +149,13 @@ def build_layout(cfg, total_layers):
     return layout[:total_layers]
 
 
-def hybrid_forward(x, sd, cfg, layout, states=None, lookbacks=None, dtype='fp32'):
-    """Returns ``(y, states, lookbacks)`` (one state / lookback per KDA layer)."""
+def hybrid_forward(x, sd, cfg, layout, states=None, lookbacks=None, dtype='fp32',
+                   csa_indices=None):
+    """Returns ``(y, states, lookbacks)`` (one state / lookback per KDA layer).
+
+    ``csa_indices`` maps a CSA layer's position in ``layout`` to a selection
+    ``[B,T,topk]`` that replaces its indexer's (to check the rest of the stack
+    on a given selection)."""
     x = round_to(x, dtype)
     n_kda = layout.count('kda')
     states = list(states) if states is not None else [None] * n_kda
@@ -162,7 +168,7 @@ def hybrid_forward(x, sd, cfg, layout, states=None, lookbacks=None, dtype='fp32'
             o, states[j], lookbacks[j] = kda_layer(h, W, cfg, states[j], lookbacks[j], dtype)
             j += 1
         elif kind == 'csa':
-            o = csa_layer(h, W, cfg, dtype)
+            o = csa_layer(h, W, cfg, dtype, None if csa_indices is None else csa_indices.get(i))
         else:
             o = hca_layer(h, W, cfg, dtype)
         x = round_to(x + o, dtype)
@@ -195,7 +201,9 @@ class HybridDecodingOracle:
                                                 cfg['hca_sliding_window'], cd)
         return self.caches[i]
 
-    def step(self, x):
+    def step(self, x, csa_indices=None):
+        """One call of ``HybridDecoding.forward``; ``csa_indices`` (layer position
+        -> selection ``[B,T,topk]``) replaces a CSA layer's indexer output."""
         cfg, dtype = self.cfg, self.dtype
         x = round_to(x, dtype)
         B, T, _ = x.shape
@@ -211,12 +219,13 @@ class HybridDecodingOracle:
             elif kind == 'csa':
                 cache = self._cache(i, 'csa', B)
                 w = _csa_w(W)
+                sel = None if csa_indices is None else csa_indices.get(i)
                 if T > 1:
                     oc, proj = naive_csa(h, w, m=cfg['csa_m'], topk=cfg['csa_topk'],
                                          nh=cfg['csa_nh'], nIh=cfg['csa_nIh'], c=cfg['csa_c'],
                                          c_I=cfg['csa_cI'],
                                          sliding_window=cfg['csa_sliding_window'],
-                                         sink=W['sink'], dtype=dtype)
+                                         sink=W['sink'], dtype=dtype, indices=sel)
                     cache.append_step(*proj[:6], w['Ba'], w['Bb'], w['B_idx'])
                 else:
                     Ca, Cb, Za, Zb, Ki, Zi, q, qi, wi = csa_projections(
@@ -224,7 +233,8 @@ class HybridDecodingOracle:
                         nIh=cfg['csa_nIh'])
                     cache.append_step(Ca, Cb, Za, Zb, Ki, Zi, w['Ba'], w['Bb'], w['B_idx'])
                     oc = cache.forward_step(l2_normalize(q), qi, wi, topk=cfg['csa_topk'],
-                                            scale=1.0, sink_logits=W['sink'], normalize_qk=True)
+                                            scale=1.0, sink_logits=W['sink'], normalize_qk=True,
+                                            indices=sel)
                     oc = round_to(oc.reshape(B, T, -1), dtype)
                 o = linear_lowp(oc, W['o_proj.weight'], dtype)
             else:
