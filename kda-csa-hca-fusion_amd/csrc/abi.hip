@@ -88,9 +88,10 @@ static int chunk_prologue(const char* fn, const void* q, const void* k, const vo
     // nothing to compute; the state passes through unchanged
     *done = true;
     if (s_out && B > 0) {
+      // zeros by the fill kernel, not a memset node (graph-capture safe)
       const size_t n = (size_t)B * HV * K * V * sizeof(float);
       hipError_t e = s0 ? hipMemcpyAsync(s_out, s0, n, hipMemcpyDeviceToDevice, (hipStream_t)stream)
-                        : hipMemsetAsync(s_out, 0, n, (hipStream_t)stream);
+                        : kch::fill_u32(s_out, (long long)(n / 4), 0u, (hipStream_t)stream);
       return hip_status(fn, e);
     }
     return KCH_OK;
@@ -158,9 +159,10 @@ int kch_kda_recurrent_fwd(const void* q, const void* k, const void* v, const voi
   if (B == 0) return KCH_OK;
   if (T == 0) {
     if (s_out) {
+      // zeros by the fill kernel, not a memset node (graph-capture safe)
       const size_t n = (size_t)B * HV * K * V * sizeof(float);
       hipError_t e = s0 ? hipMemcpyAsync(s_out, s0, n, hipMemcpyDeviceToDevice, (hipStream_t)stream)
-                        : hipMemsetAsync(s_out, 0, n, (hipStream_t)stream);
+                        : kch::fill_u32(s_out, (long long)(n / 4), 0u, (hipStream_t)stream);
       return hip_status(fn, e);
     }
     return KCH_OK;
@@ -512,6 +514,10 @@ int kch_csa_decode(const void* q, const void* q_idx, const void* w_idx, const vo
     if (pl.nr > 1 && !kch::decode_merge_fits(topk))
       return fail(KCH_ERR_UNSUPPORTED, "%s: %d cached blocks with topk=%d exceed the merge capacity",
                   fn, nb, topk);
+    if (!kch::decode_idx_fits(pl.rb, topk, pl.nr))
+      return fail(KCH_ERR_UNSUPPORTED,
+                  "%s: %d cached blocks with topk=%d exceed the indexer's LDS (%zu bytes > 160 KB)",
+                  fn, nb, topk, kch::decode_idx_lds(pl.rb, topk, pl.nr));
     idx = idx_out ? idx_out : (int*)(w + pl.off_idx);
     kch::DecodeIdxParams ip;
     ip.q_idx = q_idx; ip.w_idx = w_idx; ip.keys = k_rows; ip.inv_norm = k_inv;

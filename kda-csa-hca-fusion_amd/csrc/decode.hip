@@ -1110,6 +1110,8 @@ size_t decode_merge_lds(int topk) {
 
 bool decode_merge_fits(int topk) { return decode_merge_lds(topk) <= 160 * 1024; }
 
+bool decode_idx_fits(int rb, int topk, int nr) { return decode_idx_lds(rb, topk, nr) <= 160 * 1024; }
+
 hipError_t decode_idx_dispatch(const DecodeIdxParams& p, int qdtype, int kdtype, hipStream_t s) {
   const size_t lds = decode_idx_lds(p.rb, p.topk, p.nr);
   const dim3 grid((unsigned)(p.B * p.nr)), block(256);

@@ -74,6 +74,7 @@ void decode_idx_plan(int B, int nb, int topk, int* rb, int* nr);
 bool decode_merge_fits(int topk);  // the merge kernel's LDS holds its buffers for topk
 hipError_t fill_u32(void* p, long long n, uint32_t v, hipStream_t s);
 size_t decode_idx_lds(int rb, int topk, int nr);
+bool decode_idx_fits(int rb, int topk, int nr);  // the range kernel's LDS fits one CU's 160 KB
 size_t decode_merge_lds(int topk);
 hipError_t decode_idx_dispatch(const DecodeIdxParams& p, int qdtype, int kdtype, hipStream_t s);
 

@@ -2,8 +2,9 @@
 // q/k/v/g/beta activations that sit between the layer's projection GEMMs and
 // the KDA kernels (KDAHybridLayer.forward_functional, ops_fused.py:480-581).
 //
-// Both kernels are HBM-bound elementwise passes: fp32 arithmetic, one rounding
-// to the storage dtype per output element.
+// Both kernels are HBM-bound elementwise passes in fp32 arithmetic. Where the
+// reference chains several torch operations on a bf16 / fp16 tensor, every
+// intermediate it stores is rounded to that dtype here too.
 
 #include <hip/hip_runtime.h>
 
@@ -93,10 +94,19 @@ __global__ __launch_bounds__(256) void short_conv_kernel(ShortConvParams p) {
   }
 }
 
-__device__ __forceinline__ float silu_f(float x) { return x / (1.f + __expf(-x)); }
-__device__ __forceinline__ float sigmoid_f(float x) { return 1.f / (1.f + __expf(-x)); }
+__device__ __forceinline__ float silu_f(float x) { return x / (1.f + expf(-x)); }
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.f / (1.f + expf(-x)); }
 // torch's softplus (beta 1, threshold 20): x above the threshold, else log1p(e^x)
-__device__ __forceinline__ float softplus_f(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
+__device__ __forceinline__ float softplus_f(float x) { return x > 20.f ? x : log1pf(expf(x)); }
+
+// The value a tensor of type T stores for x (identity for fp32): each torch
+// operation of the reference writes its result in the layer's dtype, and the
+// next one reads it back from there.
+template <typename T>
+__device__ __forceinline__ float stored(float x) {
+  if constexpr (sizeof(T) == 2) return to_f32(from_f32<T>(x));
+  return x;
+}
 
 // Workgroup (row, y) for token row `row`: y < QK_UNITS(H) -> waves take q/k
 // head vectors 4y .. 4y + 3 of the 2H (silu, then per-head L2
@@ -117,21 +127,23 @@ __global__ __launch_bounds__(256) void kda_gates_kernel(KdaGatesParams p) {
     const int h = 4 * blockIdx.y + wave;
     if (h >= 2 * p.H) return;
     const T* src = pr + (size_t)h * p.K;
+    // F.normalize(F.silu(proj)) on a tensor of type T (ops_fused.py:571-572):
+    // silu's output, the norm and the quotient are each stored in T
     float vals[4];
     float ss = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int e = lane + 64 * j;
-      vals[j] = e < p.K ? silu_f(to_f32(src[e])) : 0.f;
+      vals[j] = e < p.K ? stored<T>(silu_f(to_f32(src[e]))) : 0.f;
       ss += vals[j] * vals[j];
     }
-    const float inv = l2_inv(wave_sum(ss));
+    const float nrm = fmaxf(stored<T>(sqrtf(wave_sum(ss))), 1e-12f);
     T* dst = h < p.H ? static_cast<T*>(p.q) + (row * p.H + h) * p.K
                      : static_cast<T*>(p.k) + (row * p.H + (h - p.H)) * p.K;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int e = lane + 64 * j;
-      if (e < p.K) dst[e] = from_f32<T>(vals[j] * inv);
+      if (e < p.K) dst[e] = from_f32<T>(vals[j] / nrm);
     }
     return;
   }
@@ -141,8 +153,9 @@ __global__ __launch_bounds__(256) void kda_gates_kernel(KdaGatesParams p) {
   T* g = static_cast<T*>(p.g) + row * ng;
   for (int i = i0 + threadIdx.x; i < min(nv, i0 + 1024); i += 256)
     v[i] = from_f32<T>(silu_f(to_f32(pr[2 * HK + i])));
+  // -softplus(.) is stored in T before the decay scale multiplies it (ops_fused.py:579)
   for (int i = i0 + threadIdx.x; i < min(ng, i0 + 1024); i += 256)
-    g[i] = from_f32<T>(-softplus_f(to_f32(gr[i])) * p.decay_scale);
+    g[i] = from_f32<T>(-stored<T>(softplus_f(to_f32(gr[i]))) * p.decay_scale);
   if (i0 == 0) {
     T* beta = static_cast<T*>(p.beta) + row * p.HV;
     for (int i = threadIdx.x; i < p.HV; i += 256)

@@ -8,7 +8,7 @@ in ``include/kch.h``. Tensors must be on a ROCm GPU; there is no CPU path.
 from .decoding_cache import CSADecodingCache, HCADecodingCache, SlidingWindowRingBuffer
 from .hybrid import (CSAHybridLayer, HCAHybridLayer, HybridConfig, HybridDecoding,
                      HybridKCHAttention, KDAHybridLayer)
-from .ops_csa import (csa_compress_kv, csa_compress_kv_overlapped, csa_core,
+from .ops_csa import (csa_compress_kv, csa_compress_kv_overlapped, csa_core, record_selections,
                       csa_lightning_indexer, l2_normalize_rows, naive_csa)
 from .ops_hca import hca_core, naive_hca
 from .ops_kda import naive_chunk_kda, naive_recurrent_kda
@@ -32,6 +32,7 @@ __all__ = [
     "hip_available",
     "l2_normalize_rows",
     "naive_csa",
+    "record_selections",
     "naive_hca",
     "kda_forward",
     "naive_chunk_kda",

@@ -34,7 +34,7 @@ from __future__ import annotations
 
 import torch
 
-from . import _lib
+from . import _lib, ops_csa
 from .ops_csa import _aligned, _compress, _compress_overlapped, _f32, l2_normalize_rows
 
 
@@ -451,6 +451,8 @@ class CSADecodingCache:
                       int(normalize_qk), _lib.dtype_code(fn, q.dtype),
                       _lib.dtype_code(fn, self.dtype), _lib.dtype_code(fn, odt),
                       _lib.ptr(ws), nbytes, _lib.stream_of(q))
+        if topk:
+            ops_csa._log_selection(idx.view(B, 1, topk))
         return out
 
 

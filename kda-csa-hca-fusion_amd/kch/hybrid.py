@@ -64,12 +64,15 @@ def _linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     else:
         xr = x.reshape(rows, K)
         if not _rows_ok(xr):
-            xr = xr.contiguous()
+            # fresh storage: a contiguous view that starts off a 16-byte
+            # boundary (a column slice of one row) stays misaligned under
+            # .contiguous(), which returns the view itself
+            xr = xr.clone(memory_format=torch.contiguous_format)
     if w.is_contiguous() and w.data_ptr() % 16 == 0:
         ldw = K  # a contiguous [N, K] weight (its stride(0) is arbitrary when N == 1)
     else:
         if not _rows_ok(w):
-            w = w.contiguous()
+            w = w.clone(memory_format=torch.contiguous_format)
         ldw = w.stride(0)
     N = w.shape[0]
     y = torch.empty(*x.shape[:-1], N, device=x.device, dtype=x.dtype)
@@ -217,9 +220,18 @@ class HybridConfig:
 
 class _FusedWeight:
     """Row-concatenation of several weight matrices, rebuilt only when one of
-    them changes (storage, in-place version, dtype or device)."""
+    them changes (storage, in-place version, dtype or device).
+
+    Writes through ``param.data`` (``p.data.copy_(...)``, EMA or weight-swap
+    code) change neither the storage nor the autograd version counter: after
+    such a write call the owning layer's ``invalidate_weight_cache()``.
+    ``load_state_dict`` and ``.to()`` / ``.half()`` invalidate by themselves."""
 
     def __init__(self):
+        self._key = None
+        self._w = None
+
+    def invalidate(self):
         self._key = None
         self._w = None
 
@@ -235,7 +247,30 @@ class _FusedWeight:
         return self._w
 
 
-class KDAHybridLayer(nn.Module):
+def _invalidate_after_load(module, incompatible_keys):
+    module.invalidate_weight_cache()
+
+
+class _FusedWeightLayer(nn.Module):
+    """Base of the sub-layers that keep fused copies of their weights: the
+    copies are dropped by ``load_state_dict``, by ``.to()`` / ``.half()`` /
+    ``.cuda()`` (``_apply``) and by ``invalidate_weight_cache()``."""
+
+    def __init__(self):
+        super().__init__()
+        self._fused = _FusedWeight()
+        self.register_load_state_dict_post_hook(_invalidate_after_load)
+
+    def invalidate_weight_cache(self) -> None:
+        """Drop the fused weight copies (call after writing parameters through ``.data``)."""
+        self._fused.invalidate()
+
+    def _apply(self, fn, *args, **kwargs):
+        self._fused.invalidate()
+        return super()._apply(fn, *args, **kwargs)
+
+
+class KDAHybridLayer(_FusedWeightLayer):
     """KDA sub-layer (``ops_fused.py:316-609``).
 
     The short convolution and the q/k/v/g/beta activations run in
@@ -258,7 +293,6 @@ class KDAHybridLayer(nn.Module):
         # a buffer so that .bfloat16() rounds it like the reference's (ops_fused.py:342-344)
         self.register_buffer('scale', torch.tensor(K ** -0.5), persistent=False)
         self.register_buffer('_conv_lookback', None, persistent=False)
-        self._fused = _FusedWeight()
         self._scale_cache = None
 
     def reset_conv_state(self) -> None:
@@ -384,7 +418,7 @@ class KDAHybridLayer(nn.Module):
         return out, new_state, new_lookback
 
 
-class CSAHybridLayer(nn.Module):
+class CSAHybridLayer(_FusedWeightLayer):
     """CSA sub-layer (``ops_fused.py:612-713``): ``naive_csa`` then ``o_proj``."""
 
     _indexer_warned = False
@@ -410,7 +444,6 @@ class CSAHybridLayer(nn.Module):
         self.o_proj = nn.Linear(c * cfg.csa_nh, d, bias=False)
         self.indexer_is_trained = True
         self.use_ste = True
-        self._fused = _FusedWeight()
 
     @classmethod
     def reset_warned(cls):
@@ -440,7 +473,7 @@ class CSAHybridLayer(nn.Module):
             return self.o_proj(o), None
 
 
-class HCAHybridLayer(nn.Module):
+class HCAHybridLayer(_FusedWeightLayer):
     """HCA sub-layer (``ops_fused.py:716-739``): ``naive_hca`` then ``o_proj``."""
 
     def __init__(self, cfg: HybridConfig):
@@ -454,7 +487,6 @@ class HCAHybridLayer(nn.Module):
         self.W_UQ = nn.Linear(cfg.hca_dc, c * cfg.hca_nh, bias=False)
         self.sink = nn.Parameter(torch.zeros(cfg.hca_nh))
         self.o_proj = nn.Linear(c * cfg.hca_nh, d, bias=False)
-        self._fused = _FusedWeight()
 
     def forward(self, x: torch.Tensor, state: torch.Tensor | None = None):
         cfg = self.cfg

@@ -26,10 +26,35 @@ Differences, all documented:
 
 from __future__ import annotations
 
+import contextlib
+
 import torch
 import torch.nn.functional as F
 
 from . import _lib
+
+# the top-k selections made while ``record_selections()`` is active, else None
+_selection_log = None
+
+
+@contextlib.contextmanager
+def record_selections():
+    """Collect the int32 top-k selection (``[B, T, topk]``, -1 = empty slot,
+    in no particular order) of every CSA attention computed inside the block:
+    ``naive_csa`` / ``csa_core`` and ``CSADecodingCache.forward_step`` (one
+    ``[B, 1, topk]`` entry per step), in call order. For tests that check the
+    rest of a composed model on the selection this backend made."""
+    global _selection_log
+    prev, _selection_log = _selection_log, []
+    try:
+        yield _selection_log
+    finally:
+        _selection_log = prev
+
+
+def _log_selection(idx):
+    if _selection_log is not None:
+        _selection_log.append(idx)
 
 
 def _check_gpu_dtype(fn, *ts):
@@ -249,6 +274,7 @@ def csa_core(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, *, m,
         idx, _ = _indexer(fn, q_idx, k_norm, w_idx, topk, 1.0 if normalize_qk else c_I ** -0.5,
                           m, dense=False, normalize_q=normalize_qk, idx64=False,
                           sorted_=bool(return_indices))
+        _log_selection(idx)
     sink = None if sink_logits is None else _f32(sink_logits, device)
     qc = _aligned(q)
     out = torch.empty(B_, T, nh, c, device=device, dtype=q.dtype)
@@ -345,4 +371,4 @@ def naive_csa(H, W_aKV, W_bKV, W_aZ, W_bZ, Ba, Bb, W_DQ, W_UQ, W_IUQ, W_w, W_KV_
 
 
 __all__ = ["csa_compress_kv", "csa_compress_kv_overlapped", "csa_core", "csa_lightning_indexer",
-           "naive_csa", "l2_normalize_rows"]
+           "naive_csa", "l2_normalize_rows", "record_selections"]

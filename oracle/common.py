@@ -16,12 +16,17 @@ import numpy as np
 def bf16_round(x) -> np.ndarray:
     """Round float32 values to the nearest bfloat16 (ties to even)."""
     a = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
-    u = a.view(np.uint32).astype(np.uint64)
+    u = a.view(np.uint32)
+    # u + 0x7FFF + lsb stays below 2^32 for every non-NaN pattern (the largest,
+    # -inf = 0xFF800000, gains at most 0x8000); NaNs are restored afterwards
+    r = (u >> 16) & np.uint32(1)
+    r += np.uint32(0x7FFF)
+    r += u
+    r &= np.uint32(0xFFFF0000)
+    out = r.view(np.float32)
     nan = np.isnan(a)
-    lsb = (u >> 16) & 1
-    u = (u + 0x7FFF + lsb) & 0xFFFF0000
-    out = u.astype(np.uint32).view(np.float32).copy()
-    out[nan] = np.nan
+    if nan.any():
+        out[nan] = np.nan
     return out
 
 

@@ -274,6 +274,72 @@ def csa_core(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, *,
     return out
 
 
+def csa_core_at(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, *, m, topk,
+                queries, sliding_window=0, sink_logits=None, normalize_qk=True, scale=None,
+                compute=np.float32, indices=None, logits_compute=None):
+    """``csa_core`` evaluated at the query positions ``queries`` only.
+
+    The same arithmetic per query row as ``csa_core`` (``ops_csa.py:959-1155``),
+    for sequences whose full ``[B,T,topk,c]`` gather would not fit: T must be
+    a multiple of m. ``indices`` (``[B,len(queries),topk]``) replaces the
+    indexer's selection. Returns ``(out [B,Q,nh,c], idx [B,Q,topk],
+    logits [B,Q,n_blocks])``; the logits are computed in ``logits_compute``
+    (default ``compute``).
+    """
+    Bn, T, c = np.shape(Ca)
+    if T % m:
+        raise ValueError("csa_core_at: T must be a multiple of m")
+    Q = np.asarray(queries, np.int64)
+    nh = np.shape(q)[2]
+    nb = T // m
+    Ca = np.asarray(Ca, compute)
+    C_comp = compress_kv_overlapped(Ca, Cb, Za, Zb, Ba, Bb, m, compute)
+    K_IComp = compress_kv(np.asarray(K_idx, compute), np.asarray(Z_idx, compute), B_idx, m,
+                          compute)
+    cbm = causal_block_mask(T, nb, m)[Q]
+    lc = compute if logits_compute is None else logits_compute
+    logits = indexer_logits(np.asarray(q_idx)[:, Q], K_IComp, np.asarray(w_idx)[:, Q], None, cbm,
+                            normalize_qk, lc)
+    if indices is None:
+        idx = topk_desc_lowest_index(logits, topk) if topk else np.zeros((Bn, len(Q), 0), np.int64)
+    else:
+        idx = np.asarray(indices, np.int64)
+    qq = np.asarray(q, compute)[:, Q]
+    if normalize_qk:
+        qn = l2_normalize(qq)
+        Cn = l2_normalize(C_comp)
+    else:
+        qn, Cn = qq, C_comp
+    if scale is None:
+        scale = 1.0 if normalize_qk else c ** -0.5
+    valid = idx >= 0
+    kv = Cn[np.arange(Bn)[:, None, None], np.maximum(idx, 0)]
+    scores = np.einsum('bthd,btkd->bthk', qn, kv) * compute(scale)
+    scores = np.where(valid[:, :, None, :], scores, -np.inf)
+    win = sliding_window
+    if win > 0:
+        C_local = l2_normalize(Ca) if normalize_qk else Ca
+        pos = Q[:, None] - win + 1 + np.arange(win)[None, :]          # [Q, win]
+        wvalid = pos >= 0
+        Cw = C_local[:, np.maximum(pos, 0)]                            # [B, Q, win, c]
+        sw = np.einsum('bthd,btwd->bthw', qn, Cw) * compute(scale)
+        sw = np.where(wvalid[None, :, None, :], sw, -np.inf)
+    else:
+        wvalid = np.zeros((len(Q), 0), bool)
+        Cw = np.zeros((Bn, len(Q), 0, c), compute)
+        sw = np.zeros((Bn, len(Q), nh, 0), compute)
+    cat = np.concatenate([scores, sw], axis=-1).astype(compute)
+    cat_valid = np.concatenate(
+        [valid[:, :, None, :],
+         np.broadcast_to(wvalid[None, :, None, :], (Bn, len(Q), 1, wvalid.shape[-1]))], axis=-1)
+    sink = None if sink_logits is None else np.asarray(sink_logits, compute).reshape(1, 1, nh, 1)
+    p = joint_softmax_csa(cat, cat_valid, sink)
+    k_ = scores.shape[-1]
+    out = (np.einsum('bthk,btkd->bthd', p[..., :k_], kv)
+           + np.einsum('bthw,btwd->bthd', p[..., k_:], Cw)).astype(compute)
+    return out, idx, logits
+
+
 def hca_core(C, Z, q, B_pos, *, m2, sliding_window=0, sink_logits=None,
              scale=1.0, C_local_raw=None, compute=np.float32):
     """HCA forward from the projections: ``[B,T,nh,c]`` in ``compute``."""

@@ -82,21 +82,32 @@ def _normalize_lowp(x, dtype):
     return round_to(x / np.maximum(n, 1e-12), dtype)
 
 
+def kda_activations(pq, pk, pv, gl, pb, H, HV, K, V, decay_scale, dtype='fp32'):
+    """The KDA layer's activations from its projections (``ops_fused.py:571-581``):
+    ``q, k = F.normalize(F.silu(.))`` per head, ``v = F.silu(.)``,
+    ``g = -F.softplus(.) * decay_scale``, ``beta = sigmoid(.)``, each torch
+    operation's result stored in ``dtype``. Inputs ``[B, T, width]``."""
+    B, T = pq.shape[:2]
+    q = _normalize_lowp(round_to(_silu(pq), dtype).reshape(B, T, H, K), dtype)
+    k = _normalize_lowp(round_to(_silu(pk), dtype).reshape(B, T, H, K), dtype)
+    v = round_to(_silu(pv), dtype).reshape(B, T, HV, V)
+    g = round_to(-round_to(_softplus(gl), dtype) * np.float32(decay_scale), dtype)
+    g = g.reshape(B, T, HV, K)
+    beta = round_to(1.0 / (1.0 + np.exp(-np.asarray(pb, np.float32))), dtype)
+    return q, k, v, g, beta
+
+
 def kda_layer(x, W, cfg, state=None, lookback=None, dtype='fp32'):
     """One KDA sub-layer; returns ``(out [B,T,d], new_state fp32, new_lookback)``."""
     B, T, d = x.shape
     H, K, V, HV = cfg['n_heads_qk'], cfg['head_dim_k'], cfg['head_dim_v'], cfg['n_heads_v']
     xc = short_conv(x, W['short_conv.weight'], W.get('short_conv.bias'), lookback, dtype)
     lb = new_lookback(x, lookback)
-    q = _normalize_lowp(round_to(_silu(linear_lowp(xc, W['q_proj.weight'], dtype)), dtype)
-                        .reshape(B, T, H, K), dtype)
-    k = _normalize_lowp(round_to(_silu(linear_lowp(xc, W['k_proj.weight'], dtype)), dtype)
-                        .reshape(B, T, H, K), dtype)
-    v = round_to(_silu(linear_lowp(xc, W['v_proj.weight'], dtype)), dtype).reshape(B, T, HV, V)
     gl = linear_lowp(linear_lowp(xc, W['g_down.weight'], dtype), W['g_up.weight'], dtype)
-    g = round_to(-round_to(_softplus(gl), dtype) * np.float32(cfg['kda_decay_scale']), dtype)
-    g = g.reshape(B, T, HV, K)
-    beta = round_to(1.0 / (1.0 + np.exp(-linear_lowp(xc, W['beta.weight'], dtype))), dtype)
+    q, k, v, g, beta = kda_activations(
+        linear_lowp(xc, W['q_proj.weight'], dtype), linear_lowp(xc, W['k_proj.weight'], dtype),
+        linear_lowp(xc, W['v_proj.weight'], dtype), gl, linear_lowp(xc, W['beta.weight'], dtype),
+        H, HV, K, V, cfg['kda_decay_scale'], dtype)
     scale = float(round_to(np.float32(K ** -0.5), dtype).reshape(-1)[0])
     cs = cfg['kda_chunk_size']
     if cs >= 1 and T >= cs:
@@ -150,18 +161,24 @@ def build_layout(cfg, total_layers):
 
 
 def hybrid_forward(x, sd, cfg, layout, states=None, lookbacks=None, dtype='fp32',
-                   csa_indices=None):
+                   csa_indices=None, layer_inputs=None):
     """Returns ``(y, states, lookbacks)`` (one state / lookback per KDA layer).
 
     ``csa_indices`` maps a CSA layer's position in ``layout`` to a selection
     ``[B,T,topk]`` that replaces its indexer's (to check the rest of the stack
-    on a given selection)."""
+    on a given selection). ``layer_inputs`` (one ``[B,T,d]`` residual stream per
+    layer) feeds layer i that stream instead of layer i-1's output, and the
+    result is then ``(per-layer outputs, states, lookbacks)``: each layer
+    checked on the input another implementation gave it."""
     x = round_to(x, dtype)
     n_kda = layout.count('kda')
     states = list(states) if states is not None else [None] * n_kda
     lookbacks = list(lookbacks) if lookbacks is not None else [None] * n_kda
+    outs = []
     j = 0
     for i, kind in enumerate(layout):
+        if layer_inputs is not None:
+            x = round_to(layer_inputs[i], dtype)
         W = layer_weights(sd, i)
         h = layer_norm(x, sd[f'norms.{i}.weight'], sd[f'norms.{i}.bias'], dtype=dtype)
         if kind == 'kda':
@@ -172,7 +189,8 @@ def hybrid_forward(x, sd, cfg, layout, states=None, lookbacks=None, dtype='fp32'
         else:
             o = hca_layer(h, W, cfg, dtype)
         x = round_to(x + o, dtype)
-    return x, states, lookbacks
+        outs.append(x)
+    return (outs if layer_inputs is not None else x), states, lookbacks
 
 
 class HybridDecodingOracle:
@@ -201,14 +219,19 @@ class HybridDecodingOracle:
                                                 cfg['hca_sliding_window'], cd)
         return self.caches[i]
 
-    def step(self, x, csa_indices=None):
+    def step(self, x, csa_indices=None, layer_inputs=None):
         """One call of ``HybridDecoding.forward``; ``csa_indices`` (layer position
-        -> selection ``[B,T,topk]``) replaces a CSA layer's indexer output."""
+        -> selection ``[B,T,topk]``) replaces a CSA layer's indexer output;
+        ``layer_inputs`` feeds each layer a given residual stream and makes the
+        result the list of per-layer outputs (as in ``hybrid_forward``)."""
         cfg, dtype = self.cfg, self.dtype
         x = round_to(x, dtype)
         B, T, _ = x.shape
+        outs = []
         j = 0
         for i, kind in enumerate(self.layout):
+            if layer_inputs is not None:
+                x = round_to(layer_inputs[i], dtype)
             W = layer_weights(self.sd, i)
             h = layer_norm(x, self.sd[f'norms.{i}.weight'], self.sd[f'norms.{i}.bias'],
                            dtype=dtype)
@@ -256,4 +279,5 @@ class HybridDecodingOracle:
                     oc = round_to(oc.reshape(B, T, -1), dtype)
                 o = linear_lowp(oc, W['o_proj.weight'], dtype)
             x = round_to(x + o, dtype)
-        return x
+            outs.append(x)
+        return outs if layer_inputs is not None else x

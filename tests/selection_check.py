@@ -1,0 +1,71 @@
+"""Index parity of the HIP top-k selections against the oracle's (test helper).
+
+The kernels form indexer logits from split-bf16 MFMA products
+(``x = hi + lo``, both bf16; ``hi*hi + hi*lo + lo*hi``) of L2-normalised fp32
+rows. For unit vectors each dot product is then off the exact one by at most
+three terms of 2^-18 (the dropped ``lo*lo``, and the bf16 rounding of each
+``lo``) plus fp32 accumulation and normalisation (< 2^-20), so a logit
+``sum_h w_h relu(q_h . k)`` is off by at most ``eps = sum_h |w_h| * 1.5e-5``
+(1.2e-5 rounded up), plus 1e-7 for the head sum.
+
+A HIP selection may differ from the oracle's (fp64 logits, ties by ascending
+block index) only where the k-th and (k+1)-th exact logits lie within
+``2 eps``, and then only by blocks whose logits lie within ``2 eps`` of the
+k-th. Exactly equal logits (duplicated rows, ReLU zeros) tie in both and
+follow the same lowest-index rule, so they never differ.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+
+def logit_eps(w_idx, nIh):
+    """Per-row logit error bound; ``w_idx`` ``[..., nIh]`` or None (all ones)."""
+    if w_idx is None:
+        return np.float64(1.5e-5 * nIh + 1e-7)
+    return 1.5e-5 * np.abs(np.asarray(w_idx, np.float64)).sum(-1) + 1e-7
+
+
+def check_selection(name, got, ref, logits, eps, sorted_=False):
+    """Compare ``got`` with ``ref`` (``[..., topk]``, -1 = empty) under the rule
+    above; ``logits`` ``[..., n_blocks]`` (exact, -inf = masked), ``eps``
+    broadcastable to the row shape. With ``sorted_`` the HIP rows must also
+    be in descending logit order (within ``2 eps``).
+
+    Returns ``(rows, rows_that_differ, rows_with_a_near_tie_at_the_boundary)``."""
+    got = np.asarray(got, np.int64)
+    ref = np.asarray(ref, np.int64)
+    lg = np.asarray(logits, np.float64)
+    topk = got.shape[-1]
+    rows_shape = got.shape[:-1]
+    eps = np.broadcast_to(np.asarray(eps, np.float64), rows_shape)
+    got2 = got.reshape(-1, topk)
+    ref2 = ref.reshape(-1, topk)
+    lg2 = lg.reshape(got2.shape[0], -1)
+    eps2 = eps.reshape(-1)
+    differ = near = 0
+    for r in range(got2.shape[0]):
+        a, b, e = got2[r], ref2[r], 2 * eps2[r]
+        ka, kb = np.count_nonzero(a >= 0), np.count_nonzero(b >= 0)
+        assert ka == kb, f"{name}: row {r} has {ka} selected blocks, the oracle {kb}"
+        assert np.all(a[:ka] >= 0) and np.all(a[ka:] == -1), f"{name}: row {r} -1 slots"
+        assert len(set(a[:ka].tolist())) == ka, f"{name}: row {r} repeats a block"
+        vis = np.sort(lg2[r][np.isfinite(lg2[r])])[::-1]
+        tie = False
+        if 0 < kb < vis.size:
+            kth = vis[kb - 1]
+            tie = (kth - vis[kb]) <= e
+        near += int(tie)
+        if sorted_ and ka > 1:
+            va = lg2[r, a[:ka]]
+            assert np.all(va[:-1] >= va[1:] - e), f"{name}: row {r} not in descending order"
+        sa, sb = set(a[:ka].tolist()), set(b[:kb].tolist())
+        if sa == sb:
+            continue
+        differ += 1
+        assert tie, f"{name}: row {r} differs without a near-tie at the boundary"
+        diff = np.array(sorted(sa ^ sb))
+        assert np.all(np.abs(lg2[r, diff] - kth) <= e), \
+            f"{name}: row {r} differs by a block beyond the error bound"
+    return got2.shape[0], differ, near

@@ -186,3 +186,36 @@ def test_hca_decode_split(dev, B, nb, win):
     for b in range(B):
         rows = np.concatenate([crow[b], ring[b]], axis=0)
         close(f"hca b{b}", o[b], joint_ref(qn[b], rows, sink))
+
+
+@pytest.mark.parametrize("nb,topk,win", [(300, 64, 128), (2000, 512, 16), (50, 64, 0)])
+def test_decode_step_entry_points(dev, nb, topk, win):
+    """``kch_csa_decode_step`` / ``kch_hca_decode_step`` (one workgroup per
+    sequence, the prefill kernels in ring mode) against the oracle's indexer
+    and the fp64 joint softmax."""
+    from kch import _lib
+    rng = np.random.default_rng(nb + 3 * topk + win)
+    B, c, cI, nh, nIh = 2, 128, 64, 16, 4
+    kraw, crow, ring, q, qi, wi, sink = make_csa(rng, B, nb, c, cI, nh, nIh, win)
+    kn = l2_normalize(kraw.astype(np.float64)).astype(np.float32)  # fp32 unit key rows
+    kd = torch.from_numpy(kn).to(dev)
+    kv = torch.from_numpy(crow).to(dev, torch.bfloat16)
+    rg = torch.from_numpy(ring).to(dev, torch.bfloat16) if win else None
+    qd, qid, wid, sk = (torch.from_numpy(a).to(dev) for a in (q, qi, wi, sink))
+    out = torch.empty(B, nh, c, device=dev)
+    idx = torch.empty(B, topk, device=dev, dtype=torch.int32)
+    _lib.call("kch_csa_decode_step", _lib.ptr(qd), _lib.ptr(qid), _lib.ptr(wid), _lib.ptr(kv),
+              nb * c, _lib.ptr(kd), nb * cI, _lib.ptr(rg), win * c, win, _lib.ptr(sk),
+              _lib.ptr(out), _lib.ptr(idx), B, nb, nh, c, nIh, cI, topk, 1.0, 1.0, 0, 1, 0, 0,
+              _lib.stream_of(qd))
+    torch.cuda.synchronize()
+    check_csa("csa decode_step", out.cpu().numpy(), idx.cpu().numpy(), kn, crow, ring, q, qi, wi,
+              sink, topk)
+    out_h = torch.empty(B, nh, c, device=dev)
+    _lib.call("kch_hca_decode_step", _lib.ptr(qd), _lib.ptr(kv), nb * c, _lib.ptr(rg), win * c, win,
+              _lib.ptr(sk), _lib.ptr(out_h), B, nb, nh, c, 1.0, 0, 0, 0, _lib.stream_of(qd))
+    torch.cuda.synchronize()
+    oh = out_h.cpu().numpy()
+    for b in range(B):
+        rows = np.concatenate([crow[b], ring[b]], axis=0)
+        close(f"hca decode_step b{b}", oh[b], joint_ref(q[b], rows, sink))

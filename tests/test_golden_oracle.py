@@ -217,16 +217,13 @@ def test_hybrid_golden():
     pos = layout.index("csa")
     x = u2f(z["x_bf16"])
     # each sub-layer on the reference's own residual stream: the strict bar
-    xs = [u2f(z[f"layer_in{i}_bf16"]) for i in range(len(layout))] + [u2f(z["y_bf16"])]
+    xs = [u2f(z[f"layer_in{i}_bf16"]) for i in range(len(layout))]
     np.testing.assert_array_equal(xs[0], x)
+    outs, _, _ = OH.hybrid_forward(x, sd, SMALL_CFG, layout, dtype="bf16",
+                                   csa_indices={pos: z["csa_idx"]}, layer_inputs=xs)
     for i, kind in enumerate(layout):
-        sub = {kk: v for kk, v in sd.items()
-               if kk.startswith((f"layers.{i}.", f"norms.{i}."))}
-        sub = {kk.replace(f"layers.{i}.", "layers.0.").replace(f"norms.{i}.", "norms.0."): v
-               for kk, v in sub.items()}
-        xi, _, _ = OH.hybrid_forward(xs[i], sub, SMALL_CFG, [kind], dtype="bf16",
-                                     csa_indices={0: z["csa_idx"]})
-        check_bf16(f"HybridKCHAttention layer {i} ({kind})", xi, xs[i + 1])
+        check_bf16(f"HybridKCHAttention layer {i} ({kind})", outs[i],
+                   (xs + [u2f(z["y_bf16"])])[i + 1])
     # the whole stack: the same composition, with one-ulp differences of the
     # first layers carried through later bf16 roundings (relative error ~1e-3)
     y, st, lb = OH.hybrid_forward(x, sd, SMALL_CFG, layout, dtype="bf16",

@@ -272,3 +272,23 @@ def test_cache_oracles_match_full_sequence():
         hc.append_step(C[:, t:t + 1], Z[:, t:t + 1], Ba)
         o = hc.forward_step(l2_normalize(q[:, t:t + 1]), sink_logits=sk)
         np.testing.assert_allclose(o[:, 0], hfull[:, t], rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("win,sink,topk", [(8, True, 5), (0, False, 3), (16, True, 0)])
+def test_csa_core_at_equals_csa_core_rows(win, sink, topk):
+    """The query-sliced restatement gives csa_core's rows, its selection and logits."""
+    rng = np.random.default_rng(win + topk)
+    B, T, c, cI, nh, nIh, m = 2, 64, 16, 8, 3, 2, 4
+    r = lambda *s: rng.standard_normal(s).astype(np.float32)  # noqa: E731
+    args = (r(B, T, c), r(B, T, c), r(B, T, c), r(B, T, c), r(B, T, cI), r(B, T, cI),
+            r(B, T, nh, c), r(B, T, nIh, cI), r(B, T, nIh))
+    par = (0.1 * r(m, c), 0.1 * r(m, c), 0.1 * r(m, cI))
+    kw = dict(m=m, topk=topk, sliding_window=win, sink_logits=r(nh) if sink else None,
+              normalize_qk=True)
+    full, idx_full = O.csa_core(*args, *par, return_indices=True, **kw)
+    Q = np.array([0, 3, 17, 40, 63])
+    out, idx, lg = O.csa_core_at(*args, *par, queries=Q, **kw)
+    np.testing.assert_allclose(out, full[:, Q], rtol=1e-5, atol=1e-6)
+    np.testing.assert_array_equal(idx, idx_full[:, Q])
+    out2, _, _ = O.csa_core_at(*args, *par, queries=Q, indices=idx, **kw)
+    np.testing.assert_array_equal(out2, out)

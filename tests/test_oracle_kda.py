@@ -140,3 +140,23 @@ def test_t_zero():
     o, s = chunk_kda(q, k, v, g, beta, initial_state=S0)
     assert o.shape == (2, 0, 1, 4)
     assert np.allclose(s, S0)
+
+
+def test_bf16_round_matches_torch_conversion():
+    """``bf16_round`` is torch's float32 -> bfloat16 conversion (round to
+    nearest even, NaN kept), on random values, random bit patterns and the
+    special values."""
+    import torch
+
+    from oracle.common import bf16_round
+    rng = np.random.default_rng(0)
+    x = np.concatenate([
+        (rng.standard_normal(200_000) * 1e3).astype(np.float32),
+        rng.integers(0, 2 ** 32, 200_000, dtype=np.uint64).astype(np.uint32).view(np.float32),
+        np.array([np.inf, -np.inf, np.nan, 0.0, -0.0, 3.3895314e38, -3.3895314e38, 1e-40,
+                  -1e-40, 1.00390625, 1.01171875], np.float32)])
+    got = bf16_round(x)
+    ref = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    nan = np.isnan(ref)
+    np.testing.assert_array_equal(np.isnan(got), nan)
+    np.testing.assert_array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))

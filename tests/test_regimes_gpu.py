@@ -1,0 +1,152 @@
+"""Parity at the benchmark configurations' own regimes (needs a ROCm GPU).
+
+* ``configs[1]`` at full length: KDA chunk prefill, bf16, T=4096 (64 chunks
+  of 64), K=V=128, S0 ~ 0.02 N(0,1): output and final state against the fp64
+  oracle, rtol 2e-2 + atol 2e-3 on every element.
+* ``configs[2]``'s selection regime: ``csa_core`` at B=1 T=8192 (m=4, 2048
+  blocks, indexer 4 x 64, top-512, window 128 + sink, 16 heads of 128) on
+  projections of random layer weights. Late queries see 1536-2048 blocks, so
+  the top-512 binds. Indices are compared with the oracle's (fp64 logits,
+  ties by ascending index): a row may differ only where its k-th and
+  (k+1)-th logits lie within twice the kernel's logit error bound
+  ``eps = 1.5e-5 * sum_h |w_h| + 1e-7`` (split-bf16 products of unit
+  vectors: three dropped or rounded cross terms of 2^-18 each, plus fp32
+  accumulation and normalisation), and then only by blocks within 2 eps of
+  the boundary. The mismatch fraction is printed. Outputs at those queries
+  are checked against the oracle on the selection the kernel made.
+* ``configs[4]``'s shapes: ``HybridDecoding`` (d=2048, 16 x 128 KDA heads,
+  CSA as above, HCA m'=128) in bf16, prefill of T=2176 (544 blocks: the
+  top-512 binds), then 6 decode steps, against ``oracle.hybrid`` layer by
+  layer (``composed_check.decode_vs_oracle``: each oracle sub-layer fed the
+  residual stream the HIP sub-layer saw, the CSA layer on the selection the
+  kernels made). Every element within rtol 2e-2 + atol 2e-3.
+"""
+
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from composed_check import decode_vs_oracle
+from oracle import csa as OC
+from oracle import hybrid as OH
+from oracle.kda import chunk_kda
+from selection_check import check_selection, logit_eps
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 2e-2, 2e-3
+
+
+def close(name, got, ref, rtol=RTOL, atol=ATOL):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert got.shape == ref.shape, (name, got.shape, ref.shape)
+    assert np.isfinite(got).all(), f"{name}: non-finite output"
+    err = np.abs(got - ref)
+    bad = err > atol + rtol * np.abs(ref)
+    rel = np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30)
+    print(f"{name}: max abs err {err.max():.3e}, rel fro {rel:.2e}", file=sys.stderr)
+    assert not bad.any(), (f"{name}: {bad.sum()} of {bad.size} beyond atol {atol} + rtol {rtol}; "
+                           f"max abs err {err.max():.3e}")
+
+
+def test_kda_config1_full_length(dev):
+    import kch
+    B, T, H, K, V = 1, 4096, 2, 128, 128
+    g = torch.Generator().manual_seed(11)
+    q = torch.nn.functional.normalize(torch.randn(B, T, H, K, generator=g), dim=-1)
+    k = torch.nn.functional.normalize(torch.randn(B, T, H, K, generator=g), dim=-1)
+    v = torch.randn(B, T, H, V, generator=g)
+    gt = torch.nn.functional.logsigmoid(torch.randn(B, T, H, K, generator=g))
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=g))
+    s0 = 0.02 * torch.randn(B, H, K, V, generator=g)
+    xs = [x.to(torch.bfloat16) for x in (q, k, v, gt, beta)]
+    o, s = kch.naive_chunk_kda(*[x.to(dev) for x in xs], initial_state=s0.to(dev),
+                               output_final_state=True)
+    torch.cuda.synchronize()
+    o_ref, s_ref = chunk_kda(*[x.double().numpy() for x in xs], initial_state=s0.double().numpy(),
+                             chunk_size=64, compute=np.float64)
+    close("kda C1 T4096 o", o.float().cpu().numpy(), o_ref)
+    close("kda C1 T4096 state", s.cpu().numpy(), s_ref)
+
+
+def _c2_projections(dev, B, T, seed):
+    """configs[2] projections of random weights (bf16, N(0, fan_in^-1/2))."""
+    d, c, nh, dc, nIh, cI, m = 2048, 128, 16, 128, 4, 64, 4
+    g = torch.Generator().manual_seed(seed)
+
+    def w(o, i):
+        return (torch.randn(o, i, generator=g) * i ** -0.5).to(dev, torch.bfloat16)
+    W6 = torch.cat([w(c, d), w(c, d), w(c, d), w(c, d), w(cI, d), w(cI, d)], 0)
+    W_DQ, W_UQ, W_IUQ, W_w = w(dc, d), w(c * nh, dc), w(cI * nIh, dc), w(nIh, d)
+    par = [(0.02 * torch.randn(m, n, generator=g)).to(dev, torch.bfloat16) for n in (c, c, cI)]
+    sink = torch.randn(nh, generator=g).to(dev)
+    H = torch.randn(B, T, d, generator=g).to(dev, torch.bfloat16)
+    with torch.no_grad():
+        comb = torch.nn.functional.linear(H, W6)
+        Ca, Cb, Za, Zb, Ki, Zi = comb.split([c, c, c, c, cI, cI], -1)
+        cQ = torch.nn.functional.linear(H, W_DQ)
+        q = torch.nn.functional.linear(cQ, W_UQ).view(B, T, nh, c)
+        qi = torch.nn.functional.linear(cQ, W_IUQ).view(B, T, nIh, cI)
+        wi = torch.nn.functional.linear(H, W_w)
+    return (Ca, Cb, Za, Zb, Ki, Zi, q, qi, wi), par, sink
+
+
+def test_csa_config2_late_queries(dev):
+    import kch
+    B, T, m, topk, win = 1, 8192, 4, 512, 128
+    proj, par, sink = _c2_projections(dev, B, T, seed=21)
+    out, idx = kch.csa_core(*proj, *par, m=m, topk=topk, sliding_window=win, sink_logits=sink,
+                            normalize_qk=True, return_indices=True)
+    torch.cuda.synchronize()
+    Q = np.concatenate([np.arange(6144, 6144 + 128), np.arange(T - 128, T)])
+    hp = [x.float().cpu().numpy() for x in proj]
+    hpar = [x.float().cpu().numpy() for x in par]
+    hs = sink.cpu().numpy()
+    hidx = idx.cpu().numpy()[:, Q].astype(np.int64)
+    # the oracle's own selection, on fp64 logits
+    _, ref_idx, lg = OC.csa_core_at(*hp, *hpar, m=m, topk=topk, queries=Q, sliding_window=win,
+                                    sink_logits=hs, compute=np.float64)
+    assert np.all(np.isfinite(lg).sum(-1) >= 1536)   # the top-512 binds at every such query
+    rows, differ, near = check_selection("C2 selection", hidx, ref_idx, lg,
+                                         logit_eps(hp[8][:, Q], 4), sorted_=True)
+    print(f"C2 selection: {differ} of {rows} rows differ from the oracle "
+          f"({differ / rows:.4f}); {near} rows have a k-th/(k+1)-th gap within 2 eps",
+          file=sys.stderr)
+    ref_out, _, _ = OC.csa_core_at(*hp, *hpar, m=m, topk=topk, queries=Q, sliding_window=win,
+                                   sink_logits=hs, indices=hidx)
+    close("C2 csa_core out (late queries)", out.float().cpu().numpy()[:, Q], ref_out)
+
+
+def c4_cfg():
+    import kch
+    return kch.HybridConfig(d_model=2048, n_heads_qk=16, n_heads_v=16, head_dim_k=128,
+                            head_dim_v=128, kda_chunk_size=64, csa_m=4, csa_topk=512, csa_nh=16,
+                            csa_c=128, csa_dc=128, csa_nIh=4, csa_cI=64, csa_sliding_window=128,
+                            hca_m2=128, hca_nh=16, hca_c=128, hca_dc=128, hca_sliding_window=128)
+
+
+def test_hybrid_decoding_config4_shapes(dev):
+    import kch
+    cfg = c4_cfg()
+    torch.manual_seed(31)
+    dec = kch.HybridDecoding(cfg=cfg, total_layers=5)
+    with torch.no_grad():
+        for layer in dec.model.layers:
+            if hasattr(layer, 'sink'):
+                layer.sink.normal_()
+        for n in dec.model.norms:
+            n.weight.normal_(1.0, 0.1)
+            n.bias.normal_(0.0, 0.1)
+    dec = dec.to(dev, torch.bfloat16).eval()
+    sd = {k: v.float().cpu().numpy() for k, v in dec.model.state_dict().items()}
+    cfgd = {k: getattr(cfg, k) for k in cfg.__dataclass_fields__}
+    T0, steps = 2176, 6
+    x = torch.randn(1, T0 + steps, cfg.d_model,
+                    generator=torch.Generator().manual_seed(32)).to(dev, torch.bfloat16)
+    oracle = OH.HybridDecodingOracle(sd, cfgd, dec.model.layout, "bf16")
+    decode_vs_oracle(dec, oracle, x, T0, "C4 HybridDecoding")
