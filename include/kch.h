@@ -237,6 +237,29 @@ int kch_hca_decode(const void* q, const void* kv_comp, long long kv_bstride, con
                    void* ws, size_t ws_bytes, void* stream);
 
 /*
+ * kch_csa_decode without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation). It has no counterpart in the reference.
+ * The workspace kch_csa_decode takes lives instead in a file-scope device
+ * array of KCH_NOALLOC_SCRATCH_BYTES (16 MiB), one copy per GPU, held from the
+ * library's load until the process ends; its device address is looked up on
+ * the first call on each device. Arguments, coverage and results are those of
+ * kch_csa_decode. A call whose workspace (kch_decode_ws_bytes) exceeds
+ * KCH_NOALLOC_SCRATCH_BYTES returns KCH_ERR_UNSUPPORTED. Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (other streams,
+ * other threads) race and must be serialised by the caller.
+ */
+#define KCH_NOALLOC_SCRATCH_BYTES (16 * 1024 * 1024)
+int kch_csa_decode_noalloc(const void* q, const void* q_idx, const void* w_idx,
+                           const void* kv_comp, long long kv_bstride, const void* k_rows,
+                           long long k_bstride, const float* k_inv, long long kinv_bstride,
+                           const void* ring, long long ring_bstride, int ring_len,
+                           const float* sink, void* out, int* idx_out, int B, int nb, int nh,
+                           int hd, int nIh, int cI, int topk, float scale, float idx_scale,
+                           int normalize_q, int normalize_qidx, int qdtype, int kdtype,
+                           int odtype, void* stream);
+
+/*
  * Causal depthwise convolution with kernel 3 of the KDA layer
  * (KDAHybridLayer.forward_functional, ops_fused.py:480-527: nn.Conv1d with
  * groups=d over [lookback ; x], or over [0 ; 0 ; x] without a lookback):

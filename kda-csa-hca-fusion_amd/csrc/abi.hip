@@ -5,6 +5,8 @@
 #include <cstdint>
 #include <cstdarg>
 #include <cstdio>
+#include <atomic>
+#include <mutex>
 #include <string>
 
 #include "../../include/kch.h"
@@ -554,6 +556,85 @@ int kch_hca_decode(const void* q, const void* kv_comp, long long kv_bstride, con
   return run_decode_attn(fn, pl, q, kv_comp, kv_bstride, nullptr, ring, ring_bstride, ring_len,
                          sink, out, B, nb, nh, hd, scale, normalize_q, qdtype, odtype, (char*)ws,
                          (hipStream_t)stream);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Allocation-free CSA decode step. The workspace of kch_csa_decode lives in a
+// file-scope device array, one copy per GPU, so the call needs no allocation
+// from its caller or from this library.
+
+namespace {
+
+static __device__ __align__(256) unsigned char scratch[KCH_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_addr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// The device address of the copy of `scratch` on the stream's GPU. In host code
+// the array's name is only a handle: its address comes from
+// hipGetSymbolAddress, called once per device with that device current.
+int scratch_address(const char* fn, hipStream_t s, void** out) {
+  int dev = -1;
+  hipError_t e = s ? hipStreamGetDevice(s, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(fn, e);
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: device %d beyond the %d this library tracks", fn, dev,
+                kMaxDevices);
+  void* p = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_addr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      int cur = -1;
+      e = hipGetDevice(&cur);
+      if (e != hipSuccess) return hip_status(fn, e);
+      if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return hip_status(fn, e);
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      const hipError_t back = cur != dev ? hipSetDevice(cur) : hipSuccess;
+      if (e != hipSuccess || !p)
+        return fail(KCH_ERR_HIP, "%s: hipGetSymbolAddress(scratch) on device %d: %s", fn, dev,
+                    hipGetErrorString(e));
+      if (back != hipSuccess) return hip_status(fn, back);
+      g_scratch_addr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return KCH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kch_csa_decode_noalloc(const void* q, const void* q_idx, const void* w_idx,
+                           const void* kv_comp, long long kv_bstride, const void* k_rows,
+                           long long k_bstride, const float* k_inv, long long kinv_bstride,
+                           const void* ring, long long ring_bstride, int ring_len,
+                           const float* sink, void* out, int* idx_out, int B, int nb, int nh,
+                           int hd, int nIh, int cI, int topk, float scale, float idx_scale,
+                           int normalize_q, int normalize_qidx, int qdtype, int kdtype,
+                           int odtype, void* stream) {
+  const char* fn = "kch_csa_decode_noalloc";
+  if (B < 0 || nb < 0 || nh < 1 || hd < 1 || topk < 0 || ring_len < 0)
+    return fail(KCH_ERR_INVALID, "%s: bad sizes B=%d nb=%d nh=%d hd=%d topk=%d ring_len=%d", fn,
+                B, nb, nh, hd, topk, ring_len);
+  if (B == 0) return KCH_OK;
+  const size_t need = decode_plan(B, nb, nh, hd, topk, ring_len, true).bytes;
+  if (need > (size_t)KCH_NOALLOC_SCRATCH_BYTES)
+    return fail(KCH_ERR_UNSUPPORTED,
+                "%s: B=%d nb=%d topk=%d ring_len=%d needs %zu bytes of scratch, more than the "
+                "%d this entry point holds; call kch_csa_decode with a workspace",
+                fn, B, nb, topk, ring_len, need, (int)KCH_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  const int rc = scratch_address(fn, (hipStream_t)stream, &ws);
+  if (rc) return rc;
+  return kch_csa_decode(q, q_idx, w_idx, kv_comp, kv_bstride, k_rows, k_bstride, k_inv,
+                        kinv_bstride, ring, ring_bstride, ring_len, sink, out, idx_out, B, nb, nh,
+                        hd, nIh, cI, topk, scale, idx_scale, normalize_q, normalize_qidx, qdtype,
+                        kdtype, odtype, ws, (size_t)KCH_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 }  // extern "C"

@@ -44,6 +44,8 @@ _SIGNATURES = {
     "kch_csa_decode": [_P, _P, _P, _P, _L, _P, _L, _P, _L, _P, _L, _I, _P, _P, _P] + [_I] * 7
                       + [_F, _F] + [_I] * 5 + [_P, _SZ, _P],
     "kch_hca_decode": [_P, _P, _L, _P, _L, _I, _P, _P] + [_I] * 4 + [_F, _I, _I, _I, _P, _SZ, _P],
+    "kch_csa_decode_noalloc": [_P, _P, _P, _P, _L, _P, _L, _P, _L, _P, _L, _I, _P, _P, _P]
+                              + [_I] * 7 + [_F, _F] + [_I] * 5 + [_P],
     "kch_kda_gates": [_P, _L, _P, _L, _P, _P, _P, _P, _P] + [_I] * 6 + [_F, _I, _P],
     "kch_layer_norm": [_P, _P, _P, _P, _I, _I, _F, _I, _I, _P],
     "kch_linear_rows": [_P, _L, _P, _L, _P, _L, _I, _I, _I, _I, _P],
