@@ -14,7 +14,9 @@ is two kernels (a parallel per-chunk kernel and the state-carrying kernel);
 WRITE_SIZE, scaled by the same counters on a copy of known size), including the
 per-chunk workspace that passes between them.
 ``cpu_baseline``: the numpy oracle (a from-scratch CPU restatement of the
-reference algorithm) on a bounded sample of the same workload, one thread.
+reference algorithm) on bounded samples of configs[1]-[3] (one sequence;
+query subsets for CSA / HCA), one warm-up and the median of three runs, with
+all of the process's cores and with one thread, and the CPU model.
 
 ``extra`` (skipped with ``--headline-only``): the other prefill workloads of
 the metric, each at its configuration, with the same timing protocol:
@@ -114,23 +116,107 @@ def time_steps(fn, steps, warmup, per_step=False):
     return float(mean), med, wall
 
 
-def cpu_baseline_kda(host, s0, B, T, H):
-    """Oracle on a bounded sample: the first ``nb`` batches, all heads, one thread."""
-    from threadpoolctl import threadpool_limits
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
+
+def _cpu_timed(fn, threads):
+    """One warm-up, then the median of three runs (the CPU protocol of the
+    reference's ``run_benchmark._measure``, run_benchmark.py:169-198), with the
+    BLAS thread pool limited to ``threads``."""
+    from threadpoolctl import threadpool_limits
+    with threadpool_limits(threads):
+        fn()
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+    return float(np.median(ts))
+
+
+def cpu_baselines(host, s0):
+    """The numpy oracle (a from-scratch CPU restatement of the reference
+    algorithm) on bounded samples of configs[1], [2] and [3], with all the
+    process's cores and with one thread; tokens/s of the whole workload."""
+    from oracle.csa import compress_kv, compress_kv_overlapped, csa_core_at, hca_core_at
     from oracle.kda import chunk_kda
-    nb = 2
-    q, k, v, g, beta = (x[:nb] for x in host)
-    with threadpool_limits(1):
-        t0 = time.perf_counter()
-        chunk_kda(q, k, v, g, beta, initial_state=s0[:nb], chunk_size=64)
-        dt = time.perf_counter() - t0
-    frac = nb / B
-    tok_s = (B * T) / (dt / frac)
-    return {"value": tok_s, "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"numpy oracle chunk_kda, {nb} of {B} sequences (all {H} heads, "
-                      f"T={T}) in {dt:.1f} s, scaled to the full batch; 1 thread; "
-                      f"host {platform.processor() or platform.machine()}"}
+    n_aff = len(os.sched_getaffinity(0))
+    omp = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    N = min(n_aff, omp) if omp > 0 else n_aff
+    rng = np.random.default_rng(0)
+    res = {}
+
+    # configs[1]: one of the 8 sequences, 4 of its 16 heads, T=4096 (all 64 chunks)
+    q, k, v, g = (x[:1, :, :4] for x in host[:4])
+    beta = host[4][:1, :, :4]
+    T = q.shape[1]
+    fn = lambda: chunk_kda(q, k, v, g, beta, initial_state=s0[:1, :4], chunk_size=64)  # noqa: E731
+    t = {th: _cpu_timed(fn, th) for th in (N, 1)}
+    res["C1_kda_chunk"] = {th: T / (4.0 * t[th]) for th in t}
+    samples = ["C1: chunk_kda on 1 of 8 sequences x 4 of 16 heads, T=4096"]
+
+    # configs[2]: the CSA core of one sequence (T=8192): its two compressions,
+    # then the sparse + window attention at 256 evenly spaced queries
+    T, c, cI, nh, nIh, m, topk, win = 8192, 128, 64, 16, 4, 4, 512, 128
+    r = lambda *sh: rng.standard_normal(sh).astype(np.float32)  # noqa: E731
+    Ca, Cb, Za, Zb, Ki, Zi = r(1, T, c), r(1, T, c), r(1, T, c), r(1, T, c), r(1, T, cI), r(1, T, cI)
+    Ba, Bb, Bi = 0.02 * r(m, c), 0.02 * r(m, c), 0.02 * r(m, cI)
+    Q = np.linspace(0, T - 1, 256).astype(np.int64)
+    qq, qi, wi = np.zeros((1, T, nh, c), np.float32), np.zeros((1, T, nIh, cI), np.float32), \
+        np.zeros((1, T, nIh), np.float32)
+    qq[:, Q], qi[:, Q], wi[:, Q] = r(1, len(Q), nh, c), r(1, len(Q), nIh, cI), r(1, len(Q), nIh)
+    sink = r(nh)
+    comp = {}
+
+    def csa_compress():
+        comp["C"] = compress_kv_overlapped(Ca, Cb, Za, Zb, Ba, Bb, m)
+        comp["K"] = compress_kv(Ki, Zi, Bi, m)
+
+    def csa_queries():
+        csa_core_at(Ca, Cb, Za, Zb, Ki, Zi, qq, qi, wi, Ba, Bb, Bi, m=m, topk=topk, queries=Q,
+                    sliding_window=win, sink_logits=sink, C_comp=comp["C"], K_IComp=comp["K"])
+    res["C2_csa_core"] = {}
+    for th in (N, 1):
+        tc, tq = _cpu_timed(csa_compress, th), _cpu_timed(csa_queries, th)
+        res["C2_csa_core"][th] = 1.0 / (tc / T + tq / len(Q))
+    samples.append("C2: csa core of 1 of 4 sequences (T=8192), compression of the whole "
+                   "sequence + attention at 256 evenly spaced queries")
+
+    # configs[3]: the HCA core of one sequence (T=32768), attention at 512 queries
+    T, m2 = 32768, 128
+    C, Z = r(1, T, c), r(1, T, c)
+    Bp = 0.02 * r(m2, c)
+    Q = np.linspace(0, T - 1, 512).astype(np.int64)
+    qq = np.zeros((1, T, nh, c), np.float32)
+    qq[:, Q] = r(1, len(Q), nh, c)
+
+    def hca_compress():
+        comp["H"] = compress_kv(C, Z, Bp, m2)
+
+    def hca_queries():
+        hca_core_at(C, Z, qq, Bp, m2=m2, queries=Q, sliding_window=win, sink_logits=sink,
+                    C_comp=comp["H"])
+    res["C3_hca_core"] = {}
+    for th in (N, 1):
+        tc, tq = _cpu_timed(hca_compress, th), _cpu_timed(hca_queries, th)
+        res["C3_hca_core"][th] = 1.0 / (tc / T + tq / len(Q))
+    samples.append("C3: hca core of 1 of 4 sequences (T=32768), compression of the whole "
+                   "sequence + attention at 512 evenly spaced queries")
+    cfgs = {name: {"tokens_per_s": v[N], "tokens_per_s_1thread": v[1]} for name, v in res.items()}
+    return {"value": res["C1_kda_chunk"][N], "unit": "tokens/s", "cores": N, "kind": "port",
+            "sample": "; ".join(samples) + f"; 1 warm-up then the median of 3 runs; "
+                      f"{N} BLAS threads ({n_aff} cores in the process's affinity) and 1 thread; "
+                      f"numpy oracle; host {_cpu_model()}",
+            "value_1thread": res["C1_kda_chunk"][1], "cpu_model": _cpu_model(),
+            "affinity_cores": n_aff, "configs": cfgs}
 
 
 # ----------------------------------------------------------------------------- extras
@@ -456,7 +542,7 @@ def main():
              f"{extra['hybrid_C4']['decode_ms_per_step']:.3f} ms/step")
         rec["extra"] = extra
     if not args.no_cpu:
-        rec["cpu_baseline"] = cpu_baseline_kda(host, s0h, B, T, H)
+        rec["cpu_baseline"] = cpu_baselines(host, s0h)
         _log("cpu baseline done")
     print(json.dumps(rec))
 

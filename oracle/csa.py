@@ -276,7 +276,8 @@ def csa_core(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, *,
 
 def csa_core_at(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, *, m, topk,
                 queries, sliding_window=0, sink_logits=None, normalize_qk=True, scale=None,
-                compute=np.float32, indices=None, logits_compute=None):
+                compute=np.float32, indices=None, logits_compute=None, C_comp=None,
+                K_IComp=None):
     """``csa_core`` evaluated at the query positions ``queries`` only.
 
     The same arithmetic per query row as ``csa_core`` (``ops_csa.py:959-1155``),
@@ -284,7 +285,8 @@ def csa_core_at(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, *,
     a multiple of m. ``indices`` (``[B,len(queries),topk]``) replaces the
     indexer's selection. Returns ``(out [B,Q,nh,c], idx [B,Q,topk],
     logits [B,Q,n_blocks])``; the logits are computed in ``logits_compute``
-    (default ``compute``).
+    (default ``compute``). ``C_comp`` / ``K_IComp`` (the two compressions of
+    the sequence) may be passed in when they are already known.
     """
     Bn, T, c = np.shape(Ca)
     if T % m:
@@ -293,9 +295,11 @@ def csa_core_at(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, *,
     nh = np.shape(q)[2]
     nb = T // m
     Ca = np.asarray(Ca, compute)
-    C_comp = compress_kv_overlapped(Ca, Cb, Za, Zb, Ba, Bb, m, compute)
-    K_IComp = compress_kv(np.asarray(K_idx, compute), np.asarray(Z_idx, compute), B_idx, m,
-                          compute)
+    if C_comp is None:
+        C_comp = compress_kv_overlapped(Ca, Cb, Za, Zb, Ba, Bb, m, compute)
+    if K_IComp is None:
+        K_IComp = compress_kv(np.asarray(K_idx, compute), np.asarray(Z_idx, compute), B_idx, m,
+                              compute)
     cbm = causal_block_mask(T, nb, m)[Q]
     lc = compute if logits_compute is None else logits_compute
     logits = indexer_logits(np.asarray(q_idx)[:, Q], K_IComp, np.asarray(w_idx)[:, Q], None, cbm,
@@ -372,6 +376,44 @@ def hca_core(C, Z, q, B_pos, *, m2, sliding_window=0, sink_logits=None,
         out = (np.einsum('bhtn,bnd->bthd', p[..., :nb], Cn)
                + np.einsum('bhtw,btwd->bthd', p[..., nb:], Cw))
     return out[:, :T].astype(compute)
+
+
+def hca_core_at(C, Z, q, B_pos, *, m2, queries, sliding_window=0, sink_logits=None,
+                scale=1.0, compute=np.float32, C_comp=None):
+    """``hca_core`` evaluated at the query positions ``queries`` only: the same
+    arithmetic per query row (``ops_hca.py:132-194``); T a multiple of m2.
+    ``C_comp`` (the compressed blocks, ``compress_kv(C, Z, B_pos, m2)``) may be
+    passed in when it is already known. Returns ``[B, len(queries), nh, c]``."""
+    Bn, T, c = np.shape(C)
+    if T % m2:
+        raise ValueError("hca_core_at: T must be a multiple of m2")
+    Q = np.asarray(queries, np.int64)
+    nh = np.shape(q)[2]
+    nb = T // m2
+    C = np.asarray(C, compute)
+    if C_comp is None:
+        C_comp = compress_kv(C, np.asarray(Z, compute), B_pos, m2, compute)
+    Cn = l2_normalize(np.asarray(C_comp, compute))
+    qn = l2_normalize(np.asarray(q, compute)[:, Q])
+    cbm = causal_block_mask(T, nb, m2)[Q]                                 # [Q, nb]
+    scores = np.einsum('bthd,bnd->bhtn', qn, Cn) * compute(scale)
+    scores = np.where(cbm[None, None], scores, -np.inf)
+    win = sliding_window
+    if win > 0:
+        C_local = l2_normalize(C)
+        pos = Q[:, None] - win + 1 + np.arange(win)[None, :]
+        Cw = C_local[:, np.maximum(pos, 0)]                                # [B, Q, win, c]
+        sw = np.einsum('bthd,btwd->bhtw', qn, Cw) * compute(scale)
+        sw = np.where((pos >= 0)[None, None], sw, -np.inf)
+    else:
+        Cw = np.zeros((Bn, len(Q), 0, c), compute)
+        sw = np.zeros((Bn, nh, len(Q), 0), compute)
+    cat = np.concatenate([scores, sw], axis=-1).astype(compute)
+    sink = None if sink_logits is None else np.asarray(sink_logits, compute).reshape(1, nh, 1, 1)
+    p = joint_softmax_hca(cat, sink)
+    out = (np.einsum('bhtn,bnd->bthd', p[..., :nb], Cn)
+           + np.einsum('bhtw,btwd->bthd', p[..., nb:], Cw))
+    return out.astype(compute)
 
 
 def linear_lowp(x, W, dtype='bf16'):

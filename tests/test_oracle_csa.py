@@ -292,3 +292,20 @@ def test_csa_core_at_equals_csa_core_rows(win, sink, topk):
     np.testing.assert_array_equal(idx, idx_full[:, Q])
     out2, _, _ = O.csa_core_at(*args, *par, queries=Q, indices=idx, **kw)
     np.testing.assert_array_equal(out2, out)
+
+
+@pytest.mark.parametrize("win,sink", [(8, True), (0, False)])
+def test_hca_core_at_equals_hca_core_rows(win, sink):
+    """The query-sliced HCA restatement gives hca_core's rows."""
+    rng = np.random.default_rng(win + 3)
+    B, T, c, nh, m2 = 2, 64, 16, 3, 8
+    r = lambda *s: rng.standard_normal(s).astype(np.float32)  # noqa: E731
+    C, Z, q, Bp = r(B, T, c), r(B, T, c), r(B, T, nh, c), 0.1 * r(m2, c)
+    sk = r(nh) if sink else None
+    full = O.hca_core(C, Z, q, Bp, m2=m2, sliding_window=win, sink_logits=sk)
+    Q = np.array([0, 5, 7, 8, 31, 63])
+    out = O.hca_core_at(C, Z, q, Bp, m2=m2, queries=Q, sliding_window=win, sink_logits=sk)
+    np.testing.assert_allclose(out, full[:, Q], rtol=1e-5, atol=1e-6)
+    out2 = O.hca_core_at(C, Z, q, Bp, m2=m2, queries=Q, sliding_window=win, sink_logits=sk,
+                         C_comp=O.compress_kv(C, Z, Bp, m2))
+    np.testing.assert_array_equal(out2, out)
