@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define KCH_ABI_VERSION 8
+#define KCH_ABI_VERSION 9
 
 #define KCH_OK 0
 #define KCH_ERR_INVALID 1     /* bad pointer / shape / argument */
@@ -93,8 +93,10 @@ int kch_kda_recurrent_fwd(const void* q, const void* k, const void* v, const voi
  * (ops_csa.py:874) and for HCA (ops_hca.py:134).
  *   C, Z   rows of c values, ld* elements apart (dtype); B_pos [m,c] fp32
  *   out_raw  [B,T/m,c] fp32 block values, or NULL
- *   out_key  [B,T/m,c] attention key rows: L2-normalised when `normalize`,
- *            fp32 when key_f32 else bf16; or NULL
+ *   out_key  [B,T/m,c] key rows, L2-normalised when `normalize`: bf16
+ *            (key_f32 = 0), fp32 (1), or split (2): [B,T/m,2,c] bf16, each
+ *            row's high parts then low parts of its fp32 value (x = hi + lo,
+ *            the operands of kch_csa_indexer_topk with key_split); or NULL
  *   local    [B,T,c] bf16 per-token window keys L2norm(C) (raw C when not
  *            `normalize`), or NULL
  * T must be a multiple of m (callers right-pad as ops_csa.py:772-777 does).
@@ -119,8 +121,10 @@ int kch_compress_overlapped(const void* Ca, long long ldCa, const void* Cb, long
 /*
  * Lightning indexer + top-k. Replaces csa_lightning_indexer
  * (ops_csa.py:330-573) in its forward (hard top-k) form.
- *   q_idx [B,T,nIh,cI] (dtype), k_idx [B,nb,cI] fp32 (already L2-normalised
- *   when normalize_q), w_idx [B,T,nIh] (dtype) or NULL (= all ones)
+ *   q_idx [B,T,nIh,cI] (dtype), k_idx [B,nb,cI] fp32, or with key_split
+ *   [B,nb,2,cI] bf16 high / low parts of each row (kch_compress key_f32 = 2);
+ *   already L2-normalised when normalize_q. w_idx [B,T,nIh] (dtype) or NULL
+ *   (= all ones)
  *   idx_out [B,T,topk] int64 (idx64) or int32: the top-k blocks by descending
  *   logit, ties by ascending index (sorted), or the same set in ascending
  *   block index (sorted = 0); -1 for masked blocks and padding
@@ -128,10 +132,10 @@ int kch_compress_overlapped(const void* Ca, long long ldCa, const void* Cb, long
  * Block n is visible to query t when n < (pos0 + t + 1) / m, or always when
  * dense_visible (decode). nIh in {1,2,4,8,16}; cI in {32,64,128}.
  */
-int kch_csa_indexer_topk(const void* q_idx, const float* k_idx, const void* w_idx, void* idx_out,
+int kch_csa_indexer_topk(const void* q_idx, const void* k_idx, const void* w_idx, void* idx_out,
                          int idx64, float* logits_out, int B, int T, int nb, int nIh, int cI,
                          int topk, int m, int pos0, int dense_visible, int normalize_q, float scale,
-                         int sorted, int dtype, void* stream);
+                         int sorted, int key_split, int dtype, void* stream);
 
 /*
  * CSA core attention over the selected compressed blocks plus the sliding

@@ -210,10 +210,10 @@ int kch_compress_overlapped(const void* Ca, long long ldCa, const void* Cb, long
   return hip_status(fn, kch::compress_dispatch(p, dtype, (hipStream_t)stream));
 }
 
-int kch_csa_indexer_topk(const void* q_idx, const float* k_idx, const void* w_idx, void* idx_out,
+int kch_csa_indexer_topk(const void* q_idx, const void* k_idx, const void* w_idx, void* idx_out,
                          int idx64, float* logits_out, int B, int T, int nb, int nIh, int cI,
                          int topk, int m, int pos0, int dense_visible, int normalize_q, float scale,
-                         int sorted, int dtype, void* stream) {
+                         int sorted, int key_split, int dtype, void* stream) {
   const char* fn = "kch_csa_indexer_topk";
   if (!dtype_ok(dtype)) return fail(KCH_ERR_INVALID, "%s: unknown dtype %d", fn, dtype);
   if (topk < 0) return fail(KCH_ERR_INVALID, "%s: topk=%d must be >= 0", fn, topk);
@@ -235,7 +235,8 @@ int kch_csa_indexer_topk(const void* q_idx, const float* k_idx, const void* w_id
     return hip_status(fn, kch::fill_u32(idx_out, words, 0xffffffffu, (hipStream_t)stream));
   }
   kch::IndexerParams p{q_idx, k_idx, w_idx, idx_out, logits_out, B, T, nb, nIh, cI, topk, m,
-                       pos0, normalize_q, idx64, dense_visible, sorted ? 1 : 0, scale, 0};
+                       pos0, normalize_q, idx64, dense_visible, sorted ? 1 : 0, scale, 0,
+                       key_split ? 1 : 0};
   return hip_status(fn, kch::indexer_dispatch(p, dtype, (hipStream_t)stream));
 }
 
@@ -315,7 +316,7 @@ int kch_csa_decode_step(const void* q, const void* q_idx, const void* w_idx, con
     if (lds > 160 * 1024)
       return fail(KCH_ERR_UNSUPPORTED, "%s: %d cached blocks exceed the indexer LDS budget", fn, nb);
     kch::IndexerParams ip{q_idx, k_idx, w_idx, idx_ws, nullptr, B, 1, nb, nIh, cI, topk, 1,
-                          0, normalize_qidx, 0, 1, 1, idx_scale, k_bstride};
+                          0, normalize_qidx, 0, 1, 1, idx_scale, k_bstride, 0};
     rc = hip_status(fn, kch::indexer_dispatch(ip, qdtype, s));
     if (rc) return rc;
   }

@@ -23,6 +23,23 @@
 
 namespace kch {
 
+// One channel of a compressed key row: bf16 (key_f32 0), fp32 (1), or the
+// bf16 high and low parts x = hi + lo of the fp32 value (2), stored as two
+// half rows [hi(c) | lo(c)] -- the split the indexer's MFMA products use.
+__device__ __forceinline__ void store_key(const CompressParams& p, size_t orow, int c, int ch,
+                                          float x) {
+  if (p.key_f32 == 1) {
+    static_cast<float*>(p.out_key)[orow * c + ch] = x;
+  } else if (p.key_f32 == 2) {
+    const bf16_t hi = (bf16_t)x;
+    bf16_t* row = static_cast<bf16_t*>(p.out_key) + orow * 2 * c;
+    row[ch] = hi;
+    row[c + ch] = (bf16_t)(x - (float)hi);
+  } else {
+    static_cast<bf16_t*>(p.out_key)[orow * c + ch] = (bf16_t)x;
+  }
+}
+
 namespace {
 
 
@@ -79,9 +96,7 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressParams p) {
     if (p.normalize) inv = l2_inv(wave_sum(acc[0] * acc[0] + acc[1] * acc[1]));
     for (int u = 0; u < 2; ++u) {
       if (lane + 64 * u >= c) continue;
-      const size_t o = orow * c + lane + 64 * u;
-      if (p.key_f32) static_cast<float*>(p.out_key)[o] = acc[u] * inv;
-      else static_cast<bf16_t*>(p.out_key)[o] = (bf16_t)(acc[u] * inv);
+      store_key(p, orow, c, lane + 64 * u, acc[u] * inv);
     }
   }
   if (p.local) {
@@ -237,10 +252,7 @@ __global__ __launch_bounds__(256) void compress_rows_kernel(CompressParams p) {
       __syncthreads();
       inv = l2_inv(red[0] + red[1] + red[2] + red[3]);
     }
-    if (ch < C) {
-      if (p.key_f32) static_cast<float*>(p.out_key)[orow * C + ch] = acc * inv;
-      else static_cast<bf16_t*>(p.out_key)[orow * C + ch] = (bf16_t)(acc * inv);
-    }
+    if (ch < C) store_key(p, orow, C, ch, acc * inv);
   }
 }
 

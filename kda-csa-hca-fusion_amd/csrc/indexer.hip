@@ -11,7 +11,10 @@
 //
 // Mapping: one 4-wave workgroup per group of QPW = 16 / nIh consecutive
 // queries; MFMA column n = (query n / nIh, head n % nIh). The waves split the
-// logits by 16-block chunk, then take one query's selection each. Scores use a split-bf16 product
+// logits by 16-block chunk, then take one query's selection each. The key
+// rows come as fp32, or already split (KSPLIT: the bf16 high and low parts of
+// each row side by side, as the compression kernel writes them for
+// csa_core), which spares every workgroup the conversion. Scores use a split-bf16 product
 // (x = hi + lo, hi*hi + hi*lo + lo*hi with fp32 accumulation) so the logits
 // carry ~2^-16 relative error instead of bf16's 2^-8. Per query, the logits sit
 // in LDS; the top-k is found by an 8-bit radix select on 32-bit order keys
@@ -86,14 +89,121 @@ __device__ __forceinline__ void split_bf16(const float* f, bf16x8& hi, bf16x8& l
   }
 }
 
+// Groups of 256 blocks whose order keys one wave holds in registers (4 per
+// lane and group): rows of up to 256 * RG visible blocks are selected there.
+constexpr int RG = 8;
+
+// Unsorted output with every row short enough for the register selection:
+// the launch needs no histogram or selection buffers in LDS.
+__host__ __device__ inline bool indexer_lean(const IndexerParams& p) {
+  return !p.sorted && p.nb <= 256 * RG;
+}
+
+__host__ __device__ inline size_t indexer_lds(int nb, int nIh, int topk, bool lean) {
+  int ptop = 1;
+  while (ptop < topk) ptop <<= 1;
+  const size_t base = (size_t)(16 / nIh) * ((nb + 3) & ~3) * 4 + 4 * 64 * 4;
+  return lean ? base : base + 4 * 256 * 4 + 4 * (size_t)ptop * 8;
+}
+
+// Top-k of one query's logits row lg[0 .. nv) (LDS, 16-byte aligned) by one
+// wave: the order keys go to registers (lane l holds blocks 256 g + 4 l + e),
+// the k-th largest key K is found bit by bit from the most significant bit
+// that differs among them, each step counting the keys >= a candidate with
+// ballots and scalar popcounts, and the keys above K plus the lowest-indexed
+// keys equal to K (as many as still needed: the reference's order with ties
+// by ascending index) are written in ascending block order: to sel as
+// (key, ~index) values, or without sel as block indices to out[0 .. topk),
+// -1 past the selected count. No LDS atomics, no LDS traffic but one read of
+// the row.
+template <typename IdxT>
+__device__ __forceinline__ void select_in_registers(const float* lg, int nv, int topk, int lane,
+                                                    u64* sel, IdxT* out) {
+  uint32_t key[4 * RG];  // 0 = no block (every order key of a float is above 0)
+#pragma unroll
+  for (int g = 0; g < RG; ++g) {
+    const int b0 = 256 * g + 4 * lane;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (b0 < nv) v = *reinterpret_cast<const float4*>(lg + b0);
+    key[4 * g + 0] = b0 + 0 < nv ? order_key(v.x) : 0u;
+    key[4 * g + 1] = b0 + 1 < nv ? order_key(v.y) : 0u;
+    key[4 * g + 2] = b0 + 2 < nv ? order_key(v.z) : 0u;
+    key[4 * g + 3] = b0 + 3 < nv ? order_key(v.w) : 0u;
+  }
+  uint32_t K = 0u;  // with nv <= topk every block is taken: keys > 0
+  int need = 0;
+  if (nv > topk) {
+    uint32_t a = ~0u, o = 0u;
+#pragma unroll
+    for (int r = 0; r < 4 * RG; ++r) {
+      if (key[r]) {
+        a &= key[r];
+        o |= key[r];
+      }
+    }
+#pragma unroll
+    for (int d = 32; d; d >>= 1) {
+      a &= (uint32_t)__shfl_xor((int)a, d);
+      o |= (uint32_t)__shfl_xor((int)o, d);
+    }
+    const uint32_t diff = a ^ o;
+    const int hb = diff ? 31 - __clz((int)diff) : -1;  // highest bit that differs
+    K = hb >= 31 ? 0u : (a & (~0u << (hb + 1)));      // the common leading bits
+    for (int bit = hb; bit >= 0; --bit) {
+      const uint32_t cand = K | (1u << bit);
+      int c = 0;
+#pragma unroll
+      for (int r = 0; r < 4 * RG; ++r) c += __popcll(__builtin_amdgcn_ballot_w64(key[r] >= cand));
+      if (c >= topk) K = cand;
+    }
+    int gt = 0;
+#pragma unroll
+    for (int r = 0; r < 4 * RG; ++r) gt += __popcll(__builtin_amdgcn_ballot_w64(key[r] > K));
+    need = topk - gt;  // keys equal to K still to take, lowest block index first
+  }
+  int base_out = 0, base_eq = 0;
+#pragma unroll
+  for (int g = 0; g < RG; ++g) {
+    int neq = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) neq += (key[4 * g + e] == K && key[4 * g + e]) ? 1 : 0;
+    const int eq_incl = wave_incl_scan(neq);
+    int eq_rank = base_eq + eq_incl - neq;
+    bool take[4];
+    int ntake = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t k = key[4 * g + e];
+      const bool eq = k == K && k;
+      take[e] = k > K || (eq && eq_rank < need);
+      eq_rank += eq ? 1 : 0;
+      ntake += take[e] ? 1 : 0;
+    }
+    const int out_incl = wave_incl_scan(ntake);
+    int at = base_out + out_incl - ntake;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (take[e]) {
+        if (sel) sel[at] = kv64(key[4 * g + e], 256 * g + 4 * lane + e);
+        else out[at] = (IdxT)(256 * g + 4 * lane + e);
+        ++at;
+      }
+    }
+    base_out += __builtin_amdgcn_readlane(out_incl, 63);
+    base_eq += __builtin_amdgcn_readlane(eq_incl, 63);
+  }
+  if (!sel)
+    for (int i = base_out + lane; i < topk; i += 64) out[i] = (IdxT)-1;
+}
+
 }  // namespace
 
-template <typename QT, int CI, int NIH>
+template <typename QT, int CI, int NIH, bool KSPLIT>
 __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   constexpr int NS = CI / 32;
   constexpr int nIh = NIH;
-  constexpr int QPW = 16 / NIH;
+  constexpr int QPW = 16 / NIH;  // queries per workgroup
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int q4 = lane >> 4, n = lane & 15;
@@ -103,13 +213,19 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
   const int nb = p.nb;
   const int topk = p.topk;
 
-  const size_t lg_bytes = ((size_t)QPW * nb * 4 + 15) & ~(size_t)15;
+  const int ldl = (nb + 3) & ~3;  // logits row stride: rows start 16-byte aligned
+  const size_t lg_bytes = (size_t)QPW * ldl * 4;
   int ptop = 1;
   while (ptop < topk) ptop <<= 1;
-  float* logits = reinterpret_cast<float*>(smem);                                   // [QPW][nb]
-  uint32_t* hist = reinterpret_cast<uint32_t*>(smem + lg_bytes) + 256 * wave;        // [4][256]
-  u64* sel = reinterpret_cast<u64*>(reinterpret_cast<uint32_t*>(smem + lg_bytes) + 1024) +
-             (size_t)ptop * wave;                                                     // [4][ptop]
+  // LDS: logits [QPW][ldl] | sink words [4][64] | (unless lean) histograms
+  // [4][256] and selections [4][ptop]. Lean: unsorted output of rows that the
+  // register selection handles, whose indices go straight to global memory.
+  const bool lean = indexer_lean(p);
+  float* logits = reinterpret_cast<float*>(smem);
+  float* sink = reinterpret_cast<float*>(smem + lg_bytes) + 64 * wave;
+  uint32_t* hist = reinterpret_cast<uint32_t*>(smem + lg_bytes + 4 * 64 * 4) + 256 * wave;
+  u64* sel = reinterpret_cast<u64*>(smem + lg_bytes + 4 * 64 * 4 + 4 * 256 * 4) +
+             (size_t)ptop * wave;
 
   auto nvis_of = [&](int t) {
     if (p.dense_visible) return nb;
@@ -152,43 +268,59 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
   for (int j = 0; j < QPW; ++j)
     if (t0 + j < p.T) nv_max = max(nv_max, nvis_of(t0 + j));
   const int nv_me = qok ? nvis_of(tq) : 0;
-  const float* kbase = p.k_idx + (size_t)b * (p.k_bstride ? p.k_bstride : (long long)nb * CI);
   // key rows of chunk c (row 16c + n, clamped: past the end the last row is
   // re-read and masked); wave w takes chunks w, w + 4, ..., D in flight;
-  // refills are unconditional so that no loaded register is copied
+  // refills are unconditional so that no loaded register is copied. A row is
+  // CI fp32, or (KSPLIT) CI bf16 high parts then CI bf16 low parts: the same
+  // 4 bytes per channel either way.
   constexpr int D = 4;
   const int nch = (nv_max + 15) / 16;
   const int mine = nch > wave ? (nch - wave + 3) / 4 : 0;
-  auto load = [&](int c, float (&kf)[NS][8]) {
-    const int r = min(16 * c + n, nb - 1);
-    const float* krow = kbase + (size_t)r * CI + 8 * q4;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) Load8<float>::run(krow + 32 * s, kf[s]);
+  const long long kbs = p.k_bstride ? p.k_bstride : (long long)nb * CI;  // 4-byte units
+  const char* kbase = reinterpret_cast<const char*>(p.k_idx) + (size_t)b * kbs * 4;
+  struct KFrag {
+    bf16x8 hi[NS], lo[NS];
   };
-  auto consume = [&](int c, const float (&kf)[NS][8]) {
+  auto load = [&](int c, KFrag& kf) {
+    const int r = min(16 * c + n, nb - 1);
+    const char* krow = kbase + (size_t)r * CI * 4;
+    if constexpr (KSPLIT) {
+      const bf16_t* kh = reinterpret_cast<const bf16_t*>(krow);
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        kf.hi[s] = *reinterpret_cast<const bf16x8*>(kh + 32 * s + 8 * q4);
+        kf.lo[s] = *reinterpret_cast<const bf16x8*>(kh + CI + 32 * s + 8 * q4);
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        float f[8];
+        Load8<float>::run(reinterpret_cast<const float*>(krow) + 32 * s + 8 * q4, f);
+        split_bf16(f, kf.hi[s], kf.lo[s]);
+      }
+    }
+  };
+  auto consume = [&](int c, const KFrag& kf) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      bf16x8 khi, klo;
-      split_bf16(kf[s], khi, klo);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi, qhi[s], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(khi, qlo[s], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(klo, qhi[s], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.hi[s], qhi[s], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.hi[s], qlo[s], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.lo[s], qhi[s], acc, 0, 0, 0);
     }
     // acc[e]: block 16c + 4*q4 + e, column n. No branch in here: the lanes
-    // whose value is not kept write their own word of this wave's histogram
-    // (cleared by the selection before use), since a branch costs the
-    // overlap of the chunks loaded ahead.
+    // whose value is not kept write their own word of this wave's sink
+    // words, since a branch costs the overlap of the chunks loaded ahead.
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const float v = head_sum<NIH>(fmaxf(acc[e] * p.scale, 0.f) * wq);
       const int blk = 16 * c + 4 * q4 + e;
-      float* dst = (hh == 0 && qok && blk < nv_me) ? logits + jq * nb + blk
-                                                   : reinterpret_cast<float*>(hist) + lane;
+      float* dst = (hh == 0 && qok && blk < nv_me) ? logits + jq * ldl + blk
+                                                   : sink + lane;
       *dst = v;
     }
   };
-  float kf[D][NS][8];
+  KFrag kf[D];
   // (issued in order, each refill right after its consumer: the scheduler
   // would otherwise reorder them, and the wait before a chunk's use would then
   // also cover the chunks loaded after it)
@@ -222,7 +354,7 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
     const int t = t0 + j;
     if (t >= p.T) break;
     const int nv = nvis_of(t);
-    const float* lg = logits + (size_t)j * nb;
+    const float* lg = logits + (size_t)j * ldl;
     const size_t orow = ((size_t)b * p.T + t) * topk;
     if (p.logits_out) {
       for (int i = lane; i < nb; i += 64)
@@ -236,6 +368,16 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
     // whole) takes every key in or above the boundary bin.
     uint32_t* lk = reinterpret_cast<uint32_t*>(const_cast<float*>(lg));
     const int cnt = nv < topk ? nv : topk;
+    if (nv <= 256 * RG) {
+      if (lean) {
+        if (p.idx64)
+          select_in_registers(lg, nv, topk, lane, nullptr, static_cast<long long*>(p.idx_out) + orow);
+        else
+          select_in_registers(lg, nv, topk, lane, nullptr, static_cast<int*>(p.idx_out) + orow);
+        continue;  // the indices are written
+      }
+      select_in_registers(lg, nv, topk, lane, sel, static_cast<int*>(nullptr));
+    } else {
     uint32_t thr = 0u, mask = 0u;  // with mask = 0 every key is in the boundary bin
     int tie_take = 0x7fffffff;      // boundary-bin keys taken (in index order)
     if (nv > topk) {
@@ -326,6 +468,8 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
       at += __popcll(tm);
       eqs += __popcll(em);
     }
+    }
+    wave_lds_sync();  // the selected values are in LDS
     if (p.sorted && cnt > 1) {
       // pad to a power of two with values that sort last, bitonic sort descending
       int pw = 1;
@@ -357,18 +501,19 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
   }
 }
 
-size_t indexer_lds_bytes(int nb, int nIh, int topk) {
-  int ptop = 1;
-  while (ptop < topk) ptop <<= 1;
-  return (((size_t)(16 / nIh) * nb * 4 + 15) & ~(size_t)15) + 4 * 256 * 4 + 4 * (size_t)ptop * 8;
-}
+size_t indexer_lds_bytes(int nb, int nIh, int topk) { return indexer_lds(nb, nIh, topk, false); }
 
 hipError_t indexer_dispatch(const IndexerParams& p, int dtype, hipStream_t s) {
   const int QPW = 16 / p.nIh;
-  const size_t lds = indexer_lds_bytes(p.nb, p.nIh, p.topk);
+  const size_t lds = indexer_lds(p.nb, p.nIh, p.topk, indexer_lean(p));
   const unsigned groups = (unsigned)(p.B * ((p.T + QPW - 1) / QPW));
-#define KCH_IDX_NIH(QT, CI, NIH) \
-  hipLaunchKernelGGL((indexer_kernel<QT, CI, NIH>), dim3(groups), dim3(256), lds, s, p)
+#define KCH_IDX_T(QT, CI, NIH, KS) \
+  hipLaunchKernelGGL((indexer_kernel<QT, CI, NIH, KS>), dim3(groups), dim3(256), lds, s, p)
+#define KCH_IDX_NIH(QT, CI, NIH)                   \
+  do {                                             \
+    if (p.k_split) KCH_IDX_T(QT, CI, NIH, true);   \
+    else KCH_IDX_T(QT, CI, NIH, false);            \
+  } while (0)
 #define KCH_IDX_LAUNCH(QT, CI)                \
   do {                                        \
     switch (p.nIh) {                          \

@@ -14,7 +14,7 @@ struct CompressParams {
   long long ldCa, ldZa, ldCb, ldZb;
   const float* Ba; const float* Bb;
   float* out_raw;   // [B, nb, c] fp32 or null
-  void* out_key;    // [B, nb, c] bf16 / fp32 (key_f32) or null
+  void* out_key;    // [B, nb, c] bf16 (key_f32 0) / fp32 (1), [B, nb, 2, c] split bf16 (2), or null
   bf16_t* local;    // [B, T, c] bf16 window keys (from Ca) or null
   int B, T, m, c;
   int overlap, normalize, key_f32;
@@ -42,7 +42,8 @@ hipError_t attn_dispatch(const AttnParams& p, bool sparse, int qdtype, int odtyp
 // Lightning indexer + top-k.
 struct IndexerParams {
   const void* q_idx;     // [B, T, nIh, cI]
-  const float* k_idx;    // [B, nb, cI] fp32 (already L2-normalised when normalize)
+  const void* k_idx;     // [B, nb, cI] fp32, or (k_split) [B, nb, 2, cI] bf16 high / low
+                         // parts of each row; already L2-normalised when normalize
   const void* w_idx;     // [B, T, nIh] or null (= ones)
   void* idx_out;         // [B, T, topk] int32 or int64
   float* logits_out;     // optional [B, T, nb] fp32 (diagnostics / tests) or null
@@ -51,7 +52,8 @@ struct IndexerParams {
   int normalize_q, idx64, dense_visible;  // dense_visible: every block visible
   int sorted;            // 1: indices by descending logit; 0: the same set in ascending index
   float scale;
-  long long k_bstride;   // elements between batches of k_idx (0: nb * cI)
+  long long k_bstride;   // 4-byte units between batches of k_idx (0: nb * cI)
+  int k_split;           // k_idx rows are split bf16 (high, low) instead of fp32
 };
 hipError_t indexer_dispatch(const IndexerParams& p, int dtype, hipStream_t s);
 size_t indexer_lds_bytes(int nb, int nIh, int topk);  // dynamic LDS of the indexer kernel

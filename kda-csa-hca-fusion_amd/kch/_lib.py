@@ -33,7 +33,7 @@ _SIGNATURES = {
     "kch_compress": [_P, _L, _P, _L, _P, _P, _P, _I, _I, _P, _I, _I, _I, _I, _I, _P],
     "kch_compress_overlapped": [_P, _L, _P, _L, _P, _L, _P, _L, _P, _P, _P, _P, _I, _I, _P,
                                 _I, _I, _I, _I, _I, _P],
-    "kch_csa_indexer_topk": [_P] * 4 + [_I, _P] + [_I] * 10 + [_F, _I, _I, _P],
+    "kch_csa_indexer_topk": [_P] * 4 + [_I, _P] + [_I] * 10 + [_F, _I, _I, _I, _P],
     "kch_csa_sparse_attn": [_P] * 6 + [_I] * 7 + [_F, _I, _I, _I, _P],
     "kch_hca_attn": [_P] * 5 + [_I] * 7 + [_F, _I, _I, _I, _P],
     "kch_l2norm_rows": [_P, _L, _P, _I, _I, _I, _I, _I, _P],

@@ -83,7 +83,8 @@ def _f32(t, device):
     return t.detach().to(device=device, dtype=torch.float32).contiguous()
 
 
-def _compress(fn, C, Z, B_pos, m, *, out_raw=True, key=None, normalize=False, local=None):
+def _compress(fn, C, Z, B_pos, m, *, out_raw=True, key=None, normalize=False, local=None,
+              key_split=False):
     B_, T, c = C.shape
     if m < 1:
         raise ValueError(f"compression factor m={m} must be >= 1")
@@ -95,7 +96,7 @@ def _compress(fn, C, Z, B_pos, m, *, out_raw=True, key=None, normalize=False, lo
     Z, ldz = _rows(Z)
     bpos = _f32(B_pos, C.device)
     raw = torch.empty(B_, nb, c, device=C.device, dtype=torch.float32) if out_raw else None
-    key_f32 = 1 if (key is not None and key.dtype == torch.float32) else 0
+    key_f32 = 2 if key_split else (1 if (key is not None and key.dtype == torch.float32) else 0)
     _lib.call("kch_compress", _lib.ptr(C), ldc, _lib.ptr(Z), ldz, _lib.ptr(bpos), _lib.ptr(raw),
               _lib.ptr(key), key_f32, int(normalize), _lib.ptr(local), B_, T, m, c,
               _lib.dtype_code(fn, C.dtype), _lib.stream_of(C))
@@ -164,7 +165,7 @@ def _standard_block_mask_m(mask, T, n_blocks):
 
 
 def _indexer(fn, q_idx, k_norm, w_idx, topk, scale, m, *, dense, pos0=0, normalize_q,
-             idx64=True, want_logits=False, sorted_=True):
+             idx64=True, want_logits=False, sorted_=True, key_split=False):
     B_, T, HI, DI = q_idx.shape
     nb = k_norm.shape[1]
     q_idx = _aligned(q_idx)
@@ -177,7 +178,8 @@ def _indexer(fn, q_idx, k_norm, w_idx, topk, scale, m, *, dense, pos0=0, normali
     _lib.call("kch_csa_indexer_topk", _lib.ptr(q_idx), _lib.ptr(k_norm), _lib.ptr(w_idx),
               _lib.ptr(idx), 1 if idx64 else 0, _lib.ptr(logits), B_, T, nb, HI, DI, topk,
               max(int(m), 1), pos0, int(dense), int(normalize_q), float(scale),
-              int(sorted_), _lib.dtype_code(fn, q_idx.dtype), _lib.stream_of(q_idx))
+              int(sorted_), int(key_split), _lib.dtype_code(fn, q_idx.dtype),
+              _lib.stream_of(q_idx))
     return idx, logits
 
 
@@ -264,8 +266,10 @@ def csa_core(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, *, m,
              if sliding_window > 0 else None)
     _compress_overlapped(fn, Ca, Cb, Za, Zb, Ba, Bb, m, out_raw=False, key=kv,
                          normalize=normalize_qk, local=local)
-    k_norm = torch.empty(B_, n_blocks, c_I, device=device, dtype=torch.float32)
-    _compress(fn, K_idx, Z_idx, B_idx, m, out_raw=False, key=k_norm, normalize=normalize_qk)
+    # indexer keys as split bf16 rows (high, low parts): the indexer's MFMA operands
+    k_norm = torch.empty(B_, n_blocks, 2 * c_I, device=device, dtype=torch.bfloat16)
+    _compress(fn, K_idx, Z_idx, B_idx, m, out_raw=False, key=k_norm, normalize=normalize_qk,
+              key_split=True)
     if scale is None:
         scale = 1.0 if normalize_qk else c ** -0.5
     idx = None
@@ -273,7 +277,7 @@ def csa_core(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, *, m,
         # the attention takes the selected set in any order: sort only for a caller
         idx, _ = _indexer(fn, q_idx, k_norm, w_idx, topk, 1.0 if normalize_qk else c_I ** -0.5,
                           m, dense=False, normalize_q=normalize_qk, idx64=False,
-                          sorted_=bool(return_indices))
+                          sorted_=bool(return_indices), key_split=True)
         _log_selection(idx)
     sink = None if sink_logits is None else _f32(sink_logits, device)
     qc = _aligned(q)
