@@ -85,14 +85,31 @@ def kda_algorithmic(B, T, H, K, V, C=64):
     return flops, bytes_
 
 
+SETTLE_S = 0.3   # minimum wall time of untimed work before timing (GPU clock ramp)
+SETTLE_STEPS = {}
+
+
 def time_steps(fn, steps, warmup, per_step=False):
     """Mean ms per step over ``steps`` back-to-back steps, bracketed by one pair of
     HIP events on the current stream with a synchronize on both sides (no event
     packets between the steps). With ``per_step`` a second, separate pass records
-    an event pair around every step for the median."""
+    an event pair around every step for the median.
+
+    After the ``warmup`` steps, further untimed steps run until ``SETTLE_S``
+    seconds of warm-up have passed: a few steps of well under a millisecond
+    finish before the GPU clocks have ramped, and the first timed steps would
+    then measure the ramp. Their count is kept in ``SETTLE_STEPS``."""
+    t0 = time.perf_counter()
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    extra = 0
+    while time.perf_counter() - t0 < SETTLE_S:
+        for _ in range(8):
+            fn()
+        extra += 8
+        torch.cuda.synchronize()
+    SETTLE_STEPS[getattr(fn, "__name__", "step")] = extra
     stream = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
@@ -461,7 +478,7 @@ def main():
     ap.add_argument("--headline-only", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run three 1 GiB device-to-device copies (HBM counter scale)")
-    ap.add_argument("--only-extra", choices=["decode_bw", "hybrid_C4", "csa_C2", "hca_C3"],
+    ap.add_argument("--only-extra", choices=["decode_bw", "hybrid_C4", "kda_T8K", "csa_C2", "hca_C3"],
                     help="run just this extra workload and print its JSON (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -474,6 +491,7 @@ def main():
     dev = torch.device("cuda:0")
     if args.only_extra:
         fn = {"decode_bw": bench_decode_bw, "hybrid_C4": bench_hybrid,
+              "kda_T8K": lambda d: bench_kda(4, 8192, args.steps, args.warmup, d),
               "csa_C2": lambda d: bench_csa(4, 8192, max(3, args.steps // 4), 1, d),
               "hca_C3": lambda d: bench_hca(4, 32768, max(3, args.steps // 4), 1, d)}[args.only_extra]
         print(json.dumps({args.only_extra: fn(dev)}))
@@ -496,6 +514,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_settle_steps": SETTLE_STEPS.get("step", 0),
         "ms_per_step": ms_mean,
         "higher_is_better": True,
         "scaling": "weak",
