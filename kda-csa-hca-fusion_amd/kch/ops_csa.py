@@ -7,7 +7,8 @@
 
 Same signatures, argument meaning and validation messages as the reference.
 The projections are plain ``F.linear`` GEMMs on the GPU (the reference's own
-fused 6-way weight concatenation, ``ops_csa.py:837-850``); compression, the
+fused 6-way weight concatenation, ``ops_csa.py:837-850``, extended by
+``W_DQ`` and ``W_w`` so that one GEMM reads H once); compression, the
 indexer with top-k selection and the joint sparse + window + sink attention
 run in ``libkch.so``.
 
@@ -355,14 +356,17 @@ def naive_csa(H, W_aKV, W_bKV, W_aZ, W_bZ, Ba, Bb, W_DQ, W_UQ, W_IUQ, W_w, W_KV_
     n_blocks = T // m
     with torch.no_grad():
         if fuse_projections:
-            comb = F.linear(H, torch.cat([W_aKV, W_bKV, W_aZ, W_bZ, W_KV_idx, W_Z_idx], dim=0))
-            Ca, Cb, Za, Zb, K_idx_raw, Z_idx = comb.split([c, c, c, c, c_I, c_I], dim=-1)
+            # every projection of H in one GEMM: H is read from HBM once
+            comb = F.linear(H, torch.cat([W_aKV, W_bKV, W_aZ, W_bZ, W_KV_idx, W_Z_idx, W_DQ, W_w],
+                                         dim=0))
+            Ca, Cb, Za, Zb, K_idx_raw, Z_idx, cQ, w_idx = comb.split(
+                [c, c, c, c, c_I, c_I, dc, nIh], dim=-1)
         else:
             Ca, Cb, Za, Zb = (F.linear(H, w) for w in (W_aKV, W_bKV, W_aZ, W_bZ))
             K_idx_raw, Z_idx = F.linear(H, W_KV_idx), F.linear(H, W_Z_idx)
-        cQ = F.linear(H, W_DQ)
+            cQ = F.linear(H, W_DQ)
+            w_idx = F.linear(H, W_w)
         q_idx = F.linear(cQ, W_IUQ).view(B_, T, nIh, c_I)
-        w_idx = F.linear(H, W_w)
         q = F.linear(cQ, W_UQ).view(B_, T, nh, c)
         out = csa_core(Ca, Cb, Za, Zb, K_idx_raw, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, m=m,
                        topk=topk, sliding_window=sliding_window, sink_logits=sink_logits,

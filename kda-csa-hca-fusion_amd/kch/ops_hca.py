@@ -2,7 +2,7 @@
 
 Same signature, validation (``ValueError`` / ``TypeError`` messages of
 ``ops_hca.py:73-115``) and padding contract. The projections are ``F.linear``
-GEMMs on the GPU; the heavy compression (with L2-normalised bf16 key rows and
+GEMMs on the GPU (W_KV, W_Z and W_DQ concatenated: one GEMM reads H once); the heavy compression (with L2-normalised bf16 key rows and
 the per-token window keys) and the dense MQA over compressed blocks + window +
 sink run in ``libkch.so``. Forward only; keys/values are bf16-rounded
 L2-normalised rows (fp32 in the reference); float64 is not supported.
@@ -106,9 +106,10 @@ def naive_hca(H, W_KV, W_Z, B_pos, W_DQ, W_UQ, *, m2, nh, c, dc, scale=1.0, slid
         T = T + pad
     n_blocks = T // m2
     with torch.no_grad():
-        CZ = F.linear(H, torch.cat([W_KV, W_Z], dim=0))
-        C, Z = CZ.split([c, c], dim=-1)
-        q = F.linear(F.linear(H, W_DQ), W_UQ).view(B_, T, nh, c)
+        # the three projections of H in one GEMM: H is read from HBM once
+        CZQ = F.linear(H, torch.cat([W_KV, W_Z, W_DQ], dim=0))
+        C, Z, cQ = CZQ.split([c, c, dc], dim=-1)
+        q = F.linear(cQ, W_UQ).view(B_, T, nh, c)
         C_local_raw = F.linear(H, W_KV_local) if (W_KV_local is not None and sliding_window > 0) \
             else None
         out = hca_core(C, Z, q, B_pos, m2=m2, sliding_window=sliding_window,
