@@ -35,7 +35,9 @@ from __future__ import annotations
 import torch
 
 from . import _lib, ops_csa
-from .ops_csa import _aligned, _compress, _compress_overlapped, _f32, l2_normalize_rows
+from .ops_csa import (_HEAD_DIMS, _IDX_DIMS, _IDX_HEADS, _aligned, _compress,
+                      _compress_overlapped, _f32, _head_groups, _kernel_size, _pad_last,
+                      l2_normalize_rows)
 
 
 def _validate_cache_dtype(dtype) -> None:
@@ -424,36 +426,62 @@ class CSADecodingCache:
             return torch.zeros(B, 1, nh, self.c, device=q.device, dtype=odt)
         if q.dtype == torch.float64:
             raise NotImplementedError("float64 queries are not supported by the HIP kernels")
-        out = torch.empty(B, 1, nh, self.c, device=q.device, dtype=odt)
+        fn = "CSADecodingCache.forward_step"
+        c, cI = self.c, self.c_I
+        cp = _kernel_size(fn, "c", c, _HEAD_DIMS)
+        cIp = _kernel_size(fn, "c_I", cI, _IDX_DIMS)
+        nIp = _kernel_size(fn, "nIh", nIh, _IDX_HEADS)
+        out = torch.empty(B, 1, nh, cp, device=q.device, dtype=odt)
         with torch.no_grad():
             kv = self._C.keys_for(nb, normalize_qk) if nb else None
             krows = self._K.rows if nb else None
             kinv = self._K.inv if (nb and normalize_qk) else None
             ring = _ring_bf16(self._sw) if n_win else None
-            qc = _aligned(q)
-            qi = _aligned(q_idx.to(q.dtype))
-            wi = None if w_idx is None else w_idx.to(q.dtype).contiguous()
+            qi = q_idx.to(q.dtype)
+            wi = None if w_idx is None else w_idx.to(q.dtype)
+            if (cp, cIp, nIp) != (c, cI, nIh):
+                # sizes between the kernels' own: zero-padded copies of this
+                # step's operands (zero channels and zero-weight indexer heads
+                # change no score, norm or logit)
+                kv = None if kv is None else _pad_last(kv[:, :nb], cp)
+                krows = None if krows is None else _pad_last(krows[:, :nb], cIp)
+                ring = None if ring is None else _pad_last(ring, cp)
+                q = _pad_last(q, cp)
+                qi = torch.nn.functional.pad(qi, (0, cIp - cI, 0, nIp - nIh))
+                if wi is None and nIp != nIh:
+                    wi = torch.cat([qi.new_ones(B, 1, nIh), qi.new_zeros(B, 1, nIp - nIh)], -1)
+                elif wi is not None:
+                    wi = _pad_last(wi, nIp)
+            qi = _aligned(qi)
+            wi = None if wi is None else wi.contiguous()
             idx = torch.empty(B, max(topk, 1), device=q.device, dtype=torch.int32)
             self._last_indices = idx
             sink = None if sink_logits is None else _f32(sink_logits, q.device)
             cap_c = kv.shape[1] if kv is not None else 0
             cap_k = krows.shape[1] if krows is not None else 0
+            win_stride = (ring.shape[1] if ring is not None else self.win) * cp
             lib = _lib.load()
-            nbytes = lib.kch_decode_ws_bytes(B, nb, nh, self.c, topk, n_win, 1)
-            ws = torch.empty(max(nbytes, 1), device=q.device, dtype=torch.uint8)
-            fn = "CSADecodingCache.forward_step"
-            _lib.call("kch_csa_decode", _lib.ptr(qc), _lib.ptr(qi), _lib.ptr(wi),
-                      _lib.ptr(kv), cap_c * self.c, _lib.ptr(krows), cap_k * self.c_I,
-                      _lib.ptr(kinv), cap_k, _lib.ptr(ring), self.win * self.c, n_win,
-                      _lib.ptr(sink), _lib.ptr(out), _lib.ptr(idx) if topk else None, B, nb, nh,
-                      self.c, nIh, self.c_I, topk, float(core_scale),
-                      1.0 if normalize_qk else self.c_I ** -0.5, int(_normalize_q),
-                      int(normalize_qk), _lib.dtype_code(fn, q.dtype),
-                      _lib.dtype_code(fn, self.dtype), _lib.dtype_code(fn, odt),
-                      _lib.ptr(ws), nbytes, _lib.stream_of(q))
+            for h0, h1 in _head_groups(nh):
+                # (the indexer runs once per head group, with the same selection)
+                qc = _aligned(q if h1 - h0 == nh else q[:, :, h0:h1])
+                og = out if h1 - h0 == nh else torch.empty(B, 1, h1 - h0, cp, device=q.device,
+                                                           dtype=odt)
+                nbytes = lib.kch_decode_ws_bytes(B, nb, h1 - h0, cp, topk, n_win, 1)
+                ws = torch.empty(max(nbytes, 1), device=q.device, dtype=torch.uint8)
+                _lib.call("kch_csa_decode", _lib.ptr(qc), _lib.ptr(qi), _lib.ptr(wi),
+                          _lib.ptr(kv), cap_c * cp, _lib.ptr(krows), cap_k * cIp,
+                          _lib.ptr(kinv), cap_k, _lib.ptr(ring), win_stride, n_win,
+                          _lib.ptr(None if sink is None else sink[h0:h1]), _lib.ptr(og),
+                          _lib.ptr(idx) if topk else None, B, nb, h1 - h0, cp, nIp, cIp, topk,
+                          float(core_scale), 1.0 if normalize_qk else cI ** -0.5,
+                          int(_normalize_q), int(normalize_qk), _lib.dtype_code(fn, q.dtype),
+                          _lib.dtype_code(fn, self.dtype), _lib.dtype_code(fn, odt),
+                          _lib.ptr(ws), nbytes, _lib.stream_of(q))
+                if og is not out:
+                    out[:, :, h0:h1] = og
         if topk:
             ops_csa._log_selection(idx.view(B, 1, topk))
-        return out
+        return out if cp == c else out[..., :c]
 
 
 class HCADecodingCache:
@@ -597,22 +625,37 @@ class HCADecodingCache:
             return torch.zeros(B, 1, nh, self.c, device=q.device, dtype=odt)
         if q.dtype == torch.float64:
             raise NotImplementedError("float64 queries are not supported by the HIP kernels")
-        out = torch.empty(B, 1, nh, self.c, device=q.device, dtype=odt)
+        fn = "HCADecodingCache.forward_step"
+        c = self.c
+        cp = _kernel_size(fn, "c", c, _HEAD_DIMS)
+        out = torch.empty(B, 1, nh, cp, device=q.device, dtype=odt)
         with torch.no_grad():
             kv = self._C.keys_for(nb, normalize_qk) if nb else None
             ring = _ring_bf16(self._sw) if n_win else None
-            qc = _aligned(q)
+            if cp != c:
+                # a head dim between the kernels' own: zero-padded copies of this
+                # step's operands (zero channels change no norm or score)
+                kv = None if kv is None else _pad_last(kv[:, :nb], cp)
+                ring = None if ring is None else _pad_last(ring, cp)
+                q = _pad_last(q, cp)
             sink = None if sink_logits is None else _f32(sink_logits, q.device)
             cap = kv.shape[1] if kv is not None else 0
-            nbytes = _lib.load().kch_decode_ws_bytes(B, nb, nh, self.c, 0, n_win, 0)
-            ws = torch.empty(max(nbytes, 1), device=q.device, dtype=torch.uint8)
-            _lib.call("kch_hca_decode", _lib.ptr(qc), _lib.ptr(kv), cap * self.c,
-                      _lib.ptr(ring), self.win * self.c, n_win, _lib.ptr(sink), _lib.ptr(out), B,
-                      nb, nh, self.c, float(core_scale), int(_normalize_q),
-                      _lib.dtype_code("HCADecodingCache.forward_step", q.dtype),
-                      _lib.dtype_code("HCADecodingCache.forward_step", odt),
-                      _lib.ptr(ws), nbytes, _lib.stream_of(q))
-        return out
+            win_stride = (ring.shape[1] if ring is not None else self.win) * cp
+            for h0, h1 in _head_groups(nh):
+                qc = _aligned(q if h1 - h0 == nh else q[:, :, h0:h1])
+                og = out if h1 - h0 == nh else torch.empty(B, 1, h1 - h0, cp, device=q.device,
+                                                           dtype=odt)
+                nbytes = _lib.load().kch_decode_ws_bytes(B, nb, h1 - h0, cp, 0, n_win, 0)
+                ws = torch.empty(max(nbytes, 1), device=q.device, dtype=torch.uint8)
+                _lib.call("kch_hca_decode", _lib.ptr(qc), _lib.ptr(kv), cap * cp,
+                          _lib.ptr(ring), win_stride, n_win,
+                          _lib.ptr(None if sink is None else sink[h0:h1]), _lib.ptr(og), B,
+                          nb, h1 - h0, cp, float(core_scale), int(_normalize_q),
+                          _lib.dtype_code(fn, q.dtype), _lib.dtype_code(fn, odt),
+                          _lib.ptr(ws), nbytes, _lib.stream_of(q))
+                if og is not out:
+                    out[:, :, h0:h1] = og
+        return out if cp == c else out[..., :c]
 
 
 _SlidingWindowRingBuffer = SlidingWindowRingBuffer

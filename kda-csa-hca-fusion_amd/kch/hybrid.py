@@ -638,18 +638,24 @@ class HybridDecoding(nn.Module):
     output and their projections populate the caches in bulk; T == 1 is a
     decode step through the caches and the KDA recurrent state.
 
-    Without ``cfg``: ``HybridConfig(d_model=d_model, csa_topk=csa_topk)`` with
-    the backend from ``KDA_BACKEND`` (default ``"hip"``). The reference's own
-    decode geometry (head dims 8-16) is below what the kernels cover.
+    Without ``cfg``: the reference's own decode geometry
+    (``run_decoding.py:642-656``: 2 x 16 KDA heads on the recurrent path, CSA
+    and HCA with 2 heads of 8, c_I = 4, one indexer head, m = m' = 4, windows
+    of 4) with the backend from ``KDA_BACKEND`` (default ``"hip"``). Its head
+    dims run zero-padded to the kernels' sizes.
     """
 
     def __init__(self, d_model: int = 64, total_layers: int = 5, csa_topk: int = 2, *,
                  cfg: HybridConfig | None = None):
         super().__init__()
         if cfg is None:
-            cfg = HybridConfig(d_model=d_model, csa_topk=csa_topk,
-                               kda_backend=validate_kda_backend(
-                                   os.environ.get('KDA_BACKEND', 'hip')))
+            cfg = HybridConfig(
+                d_model=d_model, n_heads_qk=2, n_heads_v=2, head_dim_k=16, head_dim_v=16,
+                kda_chunk_size=0,
+                kda_backend=validate_kda_backend(os.environ.get('KDA_BACKEND', 'hip')),
+                csa_m=4, csa_topk=csa_topk, csa_nh=2, csa_c=8, csa_dc=8, csa_nIh=1, csa_cI=4,
+                csa_sliding_window=4, hca_m2=4, hca_nh=2, hca_c=8, hca_dc=8,
+                hca_sliding_window=4, n_kda=3, n_csa=1, n_hca=1)
         self.cfg = cfg
         self.model = HybridKCHAttention(cfg, total_layers=total_layers)
         self._csa_caches: list = [None for k in self.model.layout if k == 'csa']

@@ -84,6 +84,35 @@ def _f32(t, device):
     return t.detach().to(device=device, dtype=torch.float32).contiguous()
 
 
+# Sizes the kernels take: attention head dim, indexer key dim, indexer heads,
+# heads per attention launch. Other sizes up to the largest are zero-padded up
+# to the next one: zero channels add nothing to a dot product or an L2 norm,
+# a zero-weight indexer head adds nothing to a logit, and attention heads are
+# independent, so more than 16 run as groups of 16.
+_HEAD_DIMS = (64, 128)
+_IDX_DIMS = (32, 64, 128)
+_IDX_HEADS = (1, 2, 4, 8, 16)
+_MAX_HEADS = 16
+
+
+def _kernel_size(fn, what, n, sizes):
+    for k in sizes:
+        if n <= k:
+            return k
+    raise NotImplementedError(f"{fn}: {what}={n} exceeds the largest size the HIP kernels "
+                              f"cover ({sizes[-1]})")
+
+
+def _pad_last(x, n):
+    """``x`` zero-padded along its last axis to ``n`` (``x`` itself when it has ``n``)."""
+    k = x.shape[-1]
+    return x if k == n else F.pad(x, (0, n - k))
+
+
+def _head_groups(nh):
+    return [(h0, min(nh, h0 + _MAX_HEADS)) for h0 in range(0, nh, _MAX_HEADS)]
+
+
 def _compress(fn, C, Z, B_pos, m, *, out_raw=True, key=None, normalize=False, local=None,
               key_split=False):
     B_, T, c = C.shape
@@ -219,6 +248,16 @@ def csa_lightning_indexer(q_idx, k_idx, w_idx, topk, scale=None, causal_block_ma
     if scale is None:
         scale = 1.0 if normalize_qk else q_idx.shape[-1] ** -0.5
     B_, T, HI, DI = q_idx.shape
+    DIp = _kernel_size(fn, "c_I", DI, _IDX_DIMS)
+    HIp = _kernel_size(fn, "nIh", HI, _IDX_HEADS)
+    if (DIp, HIp) != (DI, HI):
+        q_idx = F.pad(q_idx, (0, DIp - DI, 0, HIp - HI))
+        k_idx = _pad_last(k_idx, DIp)
+        w_idx = None if w_idx is None else _pad_last(w_idx, HIp)
+        if w_idx is None and HIp != HI:
+            # the reference's w_idx=None weighs every head 1: padded heads weigh 0
+            w_idx = torch.cat([q_idx.new_ones(B_, T, HI), q_idx.new_zeros(B_, T, HIp - HI)], -1)
+        B_, T, HI, DI = q_idx.shape
     n_blocks = k_idx.shape[1]
     dense, m = True, 1
     if causal_block_mask is not None:
@@ -257,9 +296,37 @@ def csa_core(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, *, m,
     views of one fused projection), T a multiple of m. Returns ``[B,T,nh,c]``
     in ``q.dtype`` (and the int32 selection ``[B,T,topk]`` when asked).
     """
+    return _csa_core(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, m=m, topk=topk,
+                     sliding_window=sliding_window, sink_logits=sink_logits,
+                     normalize_qk=normalize_qk, scale=scale, return_indices=return_indices)
+
+
+def _csa_core(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, *, m, topk,
+              sliding_window, sink_logits, normalize_qk, scale, return_indices, idx_scale=None):
     fn = "csa_core"
     B_, T, c = Ca.shape
     nh, c_I, nIh = q.shape[2], K_idx.shape[-1], q_idx.shape[2]
+    if scale is None:
+        scale = 1.0 if normalize_qk else c ** -0.5
+    if idx_scale is None:
+        idx_scale = 1.0 if normalize_qk else c_I ** -0.5
+    cp = _kernel_size(fn, "c", c, _HEAD_DIMS)
+    cIp = _kernel_size(fn, "c_I", c_I, _IDX_DIMS)
+    nIp = _kernel_size(fn, "nIh", nIh, _IDX_HEADS)
+    if (cp, cIp, nIp) != (c, c_I, nIh):
+        # padded channels compress to zero (zero values under any softmax weights)
+        Ca, Cb, Za, Zb, q = (_pad_last(x, cp) for x in (Ca, Cb, Za, Zb, q))
+        Ba, Bb = _pad_last(Ba, cp), _pad_last(Bb, cp)
+        K_idx, Z_idx, B_idx = (_pad_last(x, cIp) for x in (K_idx, Z_idx, B_idx))
+        q_idx = F.pad(q_idx, (0, cIp - c_I, 0, nIp - nIh))
+        w_idx = _pad_last(w_idx, nIp)
+        res = _csa_core(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, m=m,
+                        topk=topk, sliding_window=sliding_window, sink_logits=sink_logits,
+                        normalize_qk=normalize_qk, scale=scale, return_indices=return_indices,
+                        idx_scale=idx_scale)
+        if return_indices:
+            return res[0][..., :c], res[1]
+        return res[..., :c]
     device = Ca.device
     n_blocks = T // m
     kv = torch.empty(B_, n_blocks, c, device=device, dtype=torch.bfloat16)
@@ -271,22 +338,26 @@ def csa_core(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, *, m,
     k_norm = torch.empty(B_, n_blocks, 2 * c_I, device=device, dtype=torch.bfloat16)
     _compress(fn, K_idx, Z_idx, B_idx, m, out_raw=False, key=k_norm, normalize=normalize_qk,
               key_split=True)
-    if scale is None:
-        scale = 1.0 if normalize_qk else c ** -0.5
     idx = None
     if topk > 0:
         # the attention takes the selected set in any order: sort only for a caller
-        idx, _ = _indexer(fn, q_idx, k_norm, w_idx, topk, 1.0 if normalize_qk else c_I ** -0.5,
-                          m, dense=False, normalize_q=normalize_qk, idx64=False,
-                          sorted_=bool(return_indices), key_split=True)
+        idx, _ = _indexer(fn, q_idx, k_norm, w_idx, topk, idx_scale, m, dense=False,
+                          normalize_q=normalize_qk, idx64=False, sorted_=bool(return_indices),
+                          key_split=True)
         _log_selection(idx)
     sink = None if sink_logits is None else _f32(sink_logits, device)
-    qc = _aligned(q)
     out = torch.empty(B_, T, nh, c, device=device, dtype=q.dtype)
     code = _lib.dtype_code(fn, q.dtype)
-    _lib.call("kch_csa_sparse_attn", _lib.ptr(qc), _lib.ptr(kv), _lib.ptr(idx), _lib.ptr(local),
-              _lib.ptr(sink), _lib.ptr(out), B_, T, n_blocks, nh, c, topk, sliding_window,
-              float(scale), int(normalize_qk), code, code, _lib.stream_of(qc))
+    for h0, h1 in _head_groups(nh):
+        qc = _aligned(q if h1 - h0 == nh else q[:, :, h0:h1])
+        og = out if h1 - h0 == nh else torch.empty(B_, T, h1 - h0, c, device=device,
+                                                   dtype=q.dtype)
+        _lib.call("kch_csa_sparse_attn", _lib.ptr(qc), _lib.ptr(kv), _lib.ptr(idx),
+                  _lib.ptr(local), _lib.ptr(None if sink is None else sink[h0:h1]), _lib.ptr(og),
+                  B_, T, n_blocks, h1 - h0, c, topk, sliding_window, float(scale),
+                  int(normalize_qk), code, code, _lib.stream_of(qc))
+        if og is not out:
+            out[:, :, h0:h1] = og
     if return_indices:
         return out, idx
     return out
@@ -344,10 +415,10 @@ def naive_csa(H, W_aKV, W_bKV, W_aZ, W_bZ, Ba, Bb, W_DQ, W_UQ, W_IUQ, W_w, W_KV_
                 f"naive_csa: {_w_name}.shape={tuple(_w.shape)} — second dim "
                 f"(in_features) must equal d={d} (H.shape[-1]).")
     _check_gpu_dtype(fn, H)
-    if nh > 16 or c not in (64, 128) or c_I not in (32, 64, 128) or nIh not in (1, 2, 4, 8, 16):
+    if c > _HEAD_DIMS[-1] or c_I > _IDX_DIMS[-1] or nIh > _IDX_HEADS[-1]:
         raise NotImplementedError(
-            f"{fn}: HIP kernels cover nh <= 16, c in (64, 128), c_I in (32, 64, 128), "
-            f"nIh in (1, 2, 4, 8, 16); got nh={nh}, c={c}, c_I={c_I}, nIh={nIh}")
+            f"{fn}: the HIP kernels cover c <= 128, c_I <= 128 and nIh <= 16; got c={c}, "
+            f"c_I={c_I}, nIh={nIh}")
     original_T = T
     pad = (-T) % m
     if pad:

@@ -14,7 +14,8 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib
-from .ops_csa import _aligned, _check_gpu_dtype, _compress, _f32, l2_normalize_rows
+from .ops_csa import (_HEAD_DIMS, _aligned, _check_gpu_dtype, _compress, _f32, _head_groups,
+                      _kernel_size, _pad_last, l2_normalize_rows)
 
 
 def hca_core(C, Z, q, B_pos, *, m2, sliding_window=0, sink_logits=None, scale=1.0,
@@ -28,6 +29,14 @@ def hca_core(C, Z, q, B_pos, *, m2, sliding_window=0, sink_logits=None, scale=1.
     fn = "hca_core"
     B_, T, c = C.shape
     nh = q.shape[2]
+    cp = _kernel_size(fn, "c", c, _HEAD_DIMS)
+    if cp != c:
+        # zero channels compress to zero and add nothing to norms and scores
+        C, Z, q = (_pad_last(x, cp) for x in (C, Z, q))
+        out = hca_core(C, Z, q, _pad_last(B_pos, cp), m2=m2, sliding_window=sliding_window,
+                       sink_logits=sink_logits, scale=scale,
+                       C_local_raw=None if C_local_raw is None else _pad_last(C_local_raw, cp))
+        return out[..., :c]
     device = C.device
     n_blocks = T // m2
     kv = torch.empty(B_, n_blocks, c, device=device, dtype=torch.bfloat16)
@@ -40,12 +49,18 @@ def hca_core(C, Z, q, B_pos, *, m2, sliding_window=0, sink_logits=None, scale=1.
     _compress(fn, C, Z, B_pos, m2, out_raw=False, key=kv, normalize=True,
               local=local if C_local_raw is None else None)
     sink = None if sink_logits is None else _f32(sink_logits, device)
-    qc = _aligned(q)
     out = torch.empty(B_, T, nh, c, device=device, dtype=q.dtype)
     code = _lib.dtype_code(fn, q.dtype)
-    _lib.call("kch_hca_attn", _lib.ptr(qc), _lib.ptr(kv), _lib.ptr(local), _lib.ptr(sink),
-              _lib.ptr(out), B_, T, n_blocks, nh, c, m2, sliding_window, float(scale), 1,
-              code, code, _lib.stream_of(qc))
+    for h0, h1 in _head_groups(nh):
+        qc = _aligned(q if h1 - h0 == nh else q[:, :, h0:h1])
+        og = out if h1 - h0 == nh else torch.empty(B_, T, h1 - h0, c, device=device,
+                                                   dtype=q.dtype)
+        _lib.call("kch_hca_attn", _lib.ptr(qc), _lib.ptr(kv), _lib.ptr(local),
+                  _lib.ptr(None if sink is None else sink[h0:h1]), _lib.ptr(og), B_, T, n_blocks,
+                  h1 - h0, c, m2, sliding_window, float(scale), 1, code, code,
+                  _lib.stream_of(qc))
+        if og is not out:
+            out[:, :, h0:h1] = og
     return out
 
 
@@ -96,9 +111,8 @@ def naive_hca(H, W_KV, W_Z, B_pos, W_DQ, W_UQ, *, m2, nh, c, dc, scale=1.0, slid
             return out_empty, (z, z.clone())
         return out_empty
     _check_gpu_dtype(fn, H)
-    if nh > 16 or c not in (64, 128):
-        raise NotImplementedError(
-            f"{fn}: HIP kernels cover nh <= 16 and c in (64, 128); got nh={nh}, c={c}")
+    if c > _HEAD_DIMS[-1]:
+        raise NotImplementedError(f"{fn}: the HIP kernels cover c <= 128; got c={c}")
     original_T = T
     pad = (-T) % m2
     if pad:

@@ -20,6 +20,7 @@ from __future__ import annotations
 import math
 
 import torch
+import torch.nn.functional as F
 
 from . import _lib
 
@@ -99,6 +100,26 @@ def _aligned(t):
     return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
+def _kernel_kv(entry, K, V, dtype):
+    """(entry, K, V) the kernels run for head dims K, V: the chunk kernels take
+    K in {64, 128} and V a multiple of 64 (bf16 / fp16: V in {64, 128} for the
+    two-kernel path, larger V on the fused kernel), the recurrent kernel K in
+    {16, 32, 64, 128, 256}; other sizes are zero-padded up to the next one, and
+    a chunk call with K > 128 runs the recurrence (the same function)."""
+    if entry == "kch_kda_chunk_fwd" and K > 128:
+        entry = "kch_kda_recurrent_fwd"
+    if entry == "kch_kda_chunk_fwd":
+        Kp = 64 if K <= 64 else 128
+        Vp = -(-V // 64) * 64
+    else:
+        Kp = next((n for n in (16, 32, 64, 128, 256) if n >= K), None)
+        if Kp is None:
+            raise NotImplementedError(f"KDA: head dim K={K} > 256 is not supported by the HIP "
+                                      f"kernels")
+        Vp = V
+    return entry, Kp, Vp
+
+
 def _run(entry, fn_name, q, k, v, g, beta, scale, initial_state, output_final_state,
          g_clamp_min, state_dtype, chunk_size=None):
     _validate_kda_inputs(q, k, v, g, beta, fn_name)
@@ -108,6 +129,24 @@ def _run(entry, fn_name, q, k, v, g, beta, scale, initial_state, output_final_st
     B, T, H, K = q.shape
     HV, V = v.shape[2], v.shape[-1]
     sc = _scale_value(scale, K)
+    entry, Kp, Vp = _kernel_kv(entry, K, V, v.dtype)
+    if (Kp, Vp) != (K, V):
+        # Zero channels of q, k and g (no decay), zero columns of v and of the
+        # initial state: every padded row and column of the state stays zero and
+        # adds nothing to the outputs, which are the leading K x V block.
+        target_state = state_dtype if state_dtype is not None else torch.float32
+        q, k, g = (F.pad(t, (0, Kp - K)) for t in (q, k, g))
+        v = F.pad(v, (0, Vp - V))
+        s0 = None
+        if initial_state is not None:
+            s0 = F.pad(initial_state.to(device=q.device, dtype=torch.float32),
+                       (0, Vp - V, 0, Kp - K))
+        o, s = _run(entry, fn_name, q, k, v, g, beta, sc, s0, output_final_state, g_clamp_min,
+                    None)
+        o = o[..., :V].contiguous()
+        if s is not None:
+            s = s[:, :, :K, :V].to(target_state).contiguous()
+        return o, s
     target_state = state_dtype if state_dtype is not None else torch.float32
     # the kernels read 16-byte vectors: contiguous, 16-byte aligned storage
     q, k, v, g, beta = (_aligned(t.contiguous()) for t in (q, k, v, g, beta))

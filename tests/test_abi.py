@@ -72,3 +72,15 @@ def test_chunk_workspace_size_query():
     expect = (3 * pad(R * 64 * K * 2) + pad(R * 64 * 64 * 2) + pad(R * 64 * V * 2)
               + pad(R * K * 4))
     assert lib.kch_kda_chunk_ws_bytes(B, T, 2, HV, K, V, 1) == expect
+
+
+def test_hybrid_decoding_default_geometry_is_the_references():
+    """``HybridDecoding()`` builds the reference's decode model
+    (``run_decoding.py:642-656``)."""
+    import kch
+    cfg = kch.HybridDecoding().cfg
+    expect = dict(d_model=64, n_heads_qk=2, n_heads_v=2, head_dim_k=16, head_dim_v=16,
+                  kda_chunk_size=0, csa_m=4, csa_topk=2, csa_nh=2, csa_c=8, csa_dc=8,
+                  csa_nIh=1, csa_cI=4, csa_sliding_window=4, hca_m2=4, hca_nh=2, hca_c=8,
+                  hca_dc=8, hca_sliding_window=4, n_kda=3, n_csa=1, n_hca=1)
+    assert {k: getattr(cfg, k) for k in expect} == expect
