@@ -16,6 +16,11 @@
  *     asynchronously on it and nothing is allocated or freed.
  *   - Return value 0 = success; otherwise a KCH_ERR_* code, with a message
  *     available from kch_last_error() (per calling thread).
+ *   - With KCH_SYNC set to a value other than "0" in the environment (read
+ *     once, at the first call), every entry point waits for the device after
+ *     its launches and returns an error raised while its kernels ran as its
+ *     own KCH_ERR_HIP, naming itself. A debugging mode: the wait serialises
+ *     the streams and must not be used under graph capture.
  */
 #ifndef KCH_H
 #define KCH_H

@@ -3,6 +3,13 @@
 Usage: ``python kda-csa-hca-fusion_amd/build_lib.py`` (also called by
 ``__graft_entry__.build()``). Objects go to ``_build/`` next to this file; the
 shared library is written in-tree so it travels with the source tree.
+
+``python kda-csa-hca-fusion_amd/build_lib.py asan`` builds
+``_build_asan/libkch_asan.so``: the same library with the C-ABI layer
+(``csrc/abi.hip``: argument validation, workspace planning, error reporting)
+compiled with the host AddressSanitizer (device code is unchanged), for the CPU
+tests of that layer (``KCH_LIBRARY`` selects it; the process needs the clang
+ASan runtime preloaded, ``asan_runtime()``).
 """
 
 from __future__ import annotations
@@ -51,6 +58,50 @@ def build(verbose: bool = True) -> str:
     return OUT
 
 
+ASAN_DIR = os.path.join(HERE, "_build_asan")
+ASAN_OUT = os.path.join(ASAN_DIR, "libkch_asan.so")
+
+
+def asan_runtime():
+    """Path of the clang ASan runtime shared library of this ROCm, or None."""
+    root = os.path.join(os.path.dirname(HIPCC), "..", "llvm", "lib", "clang")
+    if not os.path.isdir(root):
+        return None
+    for ver in sorted(os.listdir(root), reverse=True):
+        rt = os.path.join(root, ver, "lib", "linux", "libclang_rt.asan-x86_64.so")
+        if os.path.exists(rt):
+            return os.path.abspath(rt)
+    return None
+
+
+def build_asan(verbose: bool = True) -> str:
+    """libkch_asan.so: abi.hip with host ASan, linked with the other objects
+    of the plain build (built first when missing)."""
+    srcs = sorted(f for f in os.listdir(CSRC) if f.endswith(".hip"))
+    objs = [os.path.join(BUILD, f.replace(".hip", ".o")) for f in srcs if f != "abi.hip"]
+    if not all(os.path.exists(o) for o in objs):
+        build(verbose)
+    os.makedirs(ASAN_DIR, exist_ok=True)
+    abi_obj = os.path.join(ASAN_DIR, "abi.o")
+    cmd = [HIPCC, *[f for f in FLAGS if f != "-O3"], "-O1", "-g",
+           "-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fno-omit-frame-pointer",
+           "-c", os.path.join(CSRC, "abi.hip"), "-o", abi_obj]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed for abi.hip (asan):\n{r.stderr}")
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-shared-libasan",
+           "-Xarch_host", "-fsanitize=address", "-o", ASAN_OUT, abi_obj, *objs]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"asan link failed:\n{r.stderr}")
+    if verbose:
+        print(f"built {ASAN_OUT}")
+    return ASAN_OUT
+
+
 if __name__ == "__main__":
-    build()
+    if sys.argv[1:] == ["asan"]:
+        build_asan()
+    else:
+        build()
     sys.exit(0)

@@ -6,6 +6,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <atomic>
+#include <cstdlib>
 #include <mutex>
 #include <string>
 
@@ -27,7 +28,19 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
+// KCH_SYNC (environment, read once): wait for the device after each entry
+// point's launches, so that an execution error is reported by the entry point
+// that caused it rather than by a later call.
+bool sync_mode() {
+  static const bool on = [] {
+    const char* e = getenv("KCH_SYNC");
+    return e && *e && !(e[0] == '0' && e[1] == 0);
+  }();
+  return on;
+}
+
 int hip_status(const char* fn, hipError_t e) {
+  if (e == hipSuccess && sync_mode()) e = hipDeviceSynchronize();
   if (e != hipSuccess) return fail(KCH_ERR_HIP, "%s: HIP error %s", fn, hipGetErrorString(e));
   return KCH_OK;
 }

@@ -14,7 +14,9 @@ import threading
 import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libkch.so")
+# KCH_LIBRARY names another build of the same library (the host-sanitizer
+# build of build_lib.py's ``asan`` target, for the CPU validation tests)
+LIB_PATH = os.environ.get("KCH_LIBRARY") or os.path.join(_HERE, "libkch.so")
 
 _lock = threading.Lock()
 _lib = None
