@@ -17,9 +17,12 @@
 // csa_core), which spares every workgroup the conversion. Scores use a split-bf16 product
 // (x = hi + lo, hi*hi + hi*lo + lo*hi with fp32 accumulation) so the logits
 // carry ~2^-16 relative error instead of bf16's 2^-8. Per query, the logits sit
-// in LDS; the top-k is found by an 8-bit radix select on 32-bit order keys
-// (ties at the boundary key taken in ascending index), gathered in index
-// order and, when asked, bitonic-sorted by (logit desc, index asc). The head
+// in LDS as 32-bit order keys. A row of up to 256 * RG visible blocks is
+// selected by one wave in registers (the k-th largest key found bit by bit
+// with ballot counts); a longer row by an 8-bit radix select in LDS. Either
+// way the keys above the boundary key and, of the keys equal to it, the
+// lowest block indices are taken (ascending index on ties), in index order;
+// when asked, they are bitonic-sorted by (logit desc, index asc). The head
 // count is a template parameter: with it known, the lane's (query, head)
 // split and the head sum compile to shifts and two or four lane exchanges.
 
@@ -343,12 +346,11 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
   __syncthreads();
 
   // ---- per query: top-k (wave w takes queries w, w + 4, ...) ----
-  // Each logit becomes a unique 64-bit value (order-preserving key, then the
-  // complement of the block index), so "larger" is the reference's order with
-  // ties in ascending index and the selection needs no tie bookkeeping: an
-  // 8-bit radix select below the leading bits common to all values, stopped
-  // as soon as the boundary digit holds exactly the values still needed, then
-  // one gather in index order. Sorting (descending) only when asked.
+  // Rows of up to 256 * RG visible blocks: select_in_registers. Longer rows:
+  // an 8-bit radix select on the order keys below the leading bits common to
+  // all of them, stopped as soon as the boundary digit holds exactly the keys
+  // still needed, then one gather in index order. The selected (key, ~index)
+  // values are sorted (descending) only when asked.
   constexpr int U = 8;  // LDS reads in flight per pass
   for (int j = wave; j < QPW; j += 4) {
     const int t = t0 + j;
