@@ -33,6 +33,7 @@ from dataclasses import dataclass
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
+from torch.nn.modules import module as _nn_module
 
 from . import _lib
 from .decoding_cache import CSADecodingCache, HCADecodingCache
@@ -418,6 +419,40 @@ class KDAHybridLayer(_FusedWeightLayer):
         return out, new_state, new_lookback
 
 
+    def _decode_step_inplace(self, x: torch.Tensor, state: torch.Tensor,
+                             lookback: torch.Tensor) -> torch.Tensor:
+        """One decode token (``x`` ``[B,1,d]``) with the conv lookback ``[B,2,d]`` and
+        the fp32 state ``[B,HV,K,V]`` updated in place: the same launches and
+        values as ``forward_functional`` on one token with that lookback and
+        state, without a new lookback tensor (so that the step can be captured
+        in a graph and replayed on the same buffers)."""
+        B, T, d = x.shape
+        cfg = self.cfg
+        H, K, V, HV = cfg.n_heads_qk, cfg.head_dim_k, cfg.head_dim_v, cfg.n_heads_v
+        code = _lib.dtype_code("KDAHybridLayer", x.dtype)
+        stream = _lib.stream_of(x)
+        W, w, bias, g_up = self._weights(x.dtype, x.device)
+        x_conv = torch.empty_like(x)
+        _lib.call("kch_short_conv", _lib.ptr(x), _lib.ptr(lookback), _lib.ptr(w), _lib.ptr(bias),
+                  _lib.ptr(x_conv), B, T, d, code, stream)
+        # the new lookback: the last two rows of [lookback ; x]
+        lookback[:, 0].copy_(lookback[:, 1])
+        lookback[:, 1].copy_(x[:, 0])
+        proj = _linear(x_conv, W)
+        off_gd = 2 * H * K + HV * V + HV
+        gl = _linear(proj[..., off_gd:off_gd + K], g_up)
+        q = torch.empty(B, T, H, K, device=x.device, dtype=x.dtype)
+        k = torch.empty_like(q)
+        v = torch.empty(B, T, HV, V, device=x.device, dtype=x.dtype)
+        g = torch.empty(B, T, HV, K, device=x.device, dtype=x.dtype)
+        beta = torch.empty(B, T, HV, device=x.device, dtype=x.dtype)
+        _lib.call("kch_kda_gates", _lib.ptr(proj), proj.stride(1), _lib.ptr(gl), gl.stride(1),
+                  _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(beta),
+                  B, T, H, HV, K, V, float(cfg.kda_decay_scale), code, stream)
+        o = _recurrent_launch(q, k, v, g, beta, self._scale_value(), state, state, code, stream)
+        return _linear(o.reshape(B, T, HV * V), self.o_proj.weight)
+
+
 class CSAHybridLayer(_FusedWeightLayer):
     """CSA sub-layer (``ops_fused.py:612-713``): ``naive_csa`` then ``o_proj``."""
 
@@ -630,6 +665,18 @@ class HybridKCHAttention(nn.Module):
             return x, self._stack_states(states), new_lookbacks
 
 
+class _DecodeGraphs:
+    """The captured segments of a decode step and what they hold on to."""
+
+    def __init__(self):
+        self.key = None
+        self.params = []
+        self.parts = []
+        self.keep = []
+        self.xin = None
+        self.xout = None
+
+
 class HybridDecoding(nn.Module):
     """Hybrid stack with one decode cache per CSA / HCA sub-layer
     (``run_decoding.py:601-851``), for any ``HybridConfig``.
@@ -643,11 +690,23 @@ class HybridDecoding(nn.Module):
     and HCA with 2 heads of 8, c_I = 4, one indexer head, m = m' = 4, windows
     of 4) with the backend from ``KDA_BACKEND`` (default ``"hip"``). Its head
     dims run zero-padded to the kernels' sizes.
+
+    ``use_graphs`` (default on): a decode step replays HIP graphs of its
+    static parts -- the norms, the KDA layers (conv lookback and state updated
+    in place), the CSA / HCA projections and output projections, the residual
+    adds -- and runs only the cache updates and attention eagerly between
+    them (their block counts and window lengths change every step). The
+    graphs are captured on the first eligible step and captured again when
+    the batch, dtype, a parameter (address or in-place version), the KDA state
+    or lookback buffers or a cache object change. Results are those of the
+    eager step, launch for launch.
     """
 
     def __init__(self, d_model: int = 64, total_layers: int = 5, csa_topk: int = 2, *,
-                 cfg: HybridConfig | None = None):
+                 cfg: HybridConfig | None = None, use_graphs: bool = True):
         super().__init__()
+        self.use_graphs = use_graphs
+        self._graphs = None
         if cfg is None:
             cfg = HybridConfig(
                 d_model=d_model, n_heads_qk=2, n_heads_v=2, head_dim_k=16, head_dim_v=16,
@@ -665,6 +724,188 @@ class HybridDecoding(nn.Module):
         self.model.reset_state()
         self._csa_caches = [None for _ in self._csa_caches]
         self._hca_caches = [None for _ in self._hca_caches]
+        self._graphs = None
+
+    def _apply(self, fn, *args, **kwargs):
+        self._graphs = None
+        return super()._apply(fn, *args, **kwargs)
+
+    # ---------------- graphed decode step ----------------
+    def _graph_eligible(self, x: torch.Tensor, stacked) -> bool:
+        """Every projection of the step on ``kch_linear_rows`` (no BLAS call in a
+        graph), every KDA layer on the recurrent step with a lookback buffer,
+        every cache present, and no forward hook anywhere in the model (a hook
+        must see each step's values; a replay would not call it)."""
+        if not (self.use_graphs and x.is_cuda and x.dtype in (torch.bfloat16, torch.float16)
+                and x.shape[1] == 1 and x.shape[0] <= 16):
+            return False
+        if _nn_module._global_forward_hooks or _nn_module._global_forward_pre_hooks \
+                or any(m._forward_hooks or m._forward_pre_hooks for m in self._called_modules()):
+            return False
+        cfg, model = self.cfg, self.model
+        widths = [cfg.d_model]
+        if model.n_kda_layers:
+            if stacked is None or stacked.shape[1] != x.shape[0]:
+                return False
+            widths += [cfg.head_dim_k, cfg.n_heads_v * cfg.head_dim_v]
+        if 'csa' in model.layout:
+            widths += [cfg.csa_dc, cfg.csa_nh * cfg.csa_c]
+        if 'hca' in model.layout:
+            widths += [cfg.hca_dc, cfg.hca_nh * cfg.hca_c]
+        if any(w % 32 for w in widths):
+            return False
+        for layer, kind in zip(model.layers, model.layout):
+            if kind == 'kda':
+                lb = layer._conv_lookback
+                if lb is None or lb.shape[0] != x.shape[0] or lb.dtype != x.dtype:
+                    return False
+        return all(c is not None for c in self._csa_caches + self._hca_caches)
+
+    def _called_modules(self):
+        """The modules an eager decode step calls as modules (the norms and the
+        KDA layers; the CSA / HCA layers' weights are used directly)."""
+        model = self.model
+        return [model] + list(model.norms) + [l for l, k in zip(model.layers, model.layout)
+                                              if k == 'kda']
+
+    def _graph_key(self, x: torch.Tensor, stacked):
+        g = self._graphs
+        params = g.params if g is not None else list(self.model.parameters())
+        lbs = tuple(id(l._conv_lookback) for l, k in zip(self.model.layers, self.model.layout)
+                    if k == 'kda')
+        return (x.shape, x.dtype, x.device, None if stacked is None else stacked.data_ptr(), lbs,
+                tuple(id(c) for c in self._csa_caches + self._hca_caches),
+                tuple((p.data_ptr(), p._version) for p in params))
+
+    def _capture(self, x: torch.Tensor, stacked):
+        """Capture the step's static segments (nothing is executed) and return
+        the runner: the graphs' replays and the eager cache calls in order."""
+        model = self.model
+        gs = _DecodeGraphs()
+        gs.params = list(model.parameters())
+        # persistent lookback buffers (updated in place by the replays)
+        for layer, kind in zip(model.layers, model.layout):
+            if kind == 'kda':
+                layer._conv_lookback = layer._conv_lookback.contiguous().clone()
+        # fused weights built outside the capture
+        for layer, kind in zip(model.layers, model.layout):
+            if kind == 'kda':
+                layer._weights(x.dtype, x.device)
+        with torch.no_grad():
+            for layer, kind in zip(model.layers, model.layout):
+                if kind == 'csa':
+                    self._project_csa(layer, x)
+                elif kind == 'hca':
+                    self._project_hca(layer, x)
+        torch.cuda.synchronize(x.device)
+        pool = torch.cuda.graph_pool_handle()
+        gs.xin = x.clone()
+        parts, keep, open_ctx = [], [], []
+
+        def open_graph():
+            g = torch.cuda.CUDAGraph()
+            ctx = torch.cuda.graph(g, pool=pool)
+            ctx.__enter__()
+            open_ctx.append(ctx)
+            return g, ctx
+
+        def close_graph(g, ctx):
+            open_ctx.pop()
+            ctx.__exit__(None, None, None)
+            parts.append(g.replay)
+            keep.append(g)
+
+        try:
+            self._capture_segments(gs, stacked, open_graph, close_graph, parts, keep)
+        except BaseException:
+            # end an open capture before the error propagates (a graph destroyed
+            # while its stream still captures aborts the process)
+            for ctx in open_ctx:
+                try:
+                    ctx.__exit__(None, None, None)
+                except Exception:
+                    pass
+            raise
+        gs.parts, gs.keep = parts, keep
+        return gs
+
+    def _capture_segments(self, gs, stacked, open_graph, close_graph, parts, keep):
+        """Norms, KDA layers and projections of the step into graphs, split at
+        each CSA / HCA cache call (an eager part between two graphs)."""
+        model, cfg = self.model, self.cfg
+        x = gs.xin
+        B = x.shape[0]
+        kda_idx = csa_idx = hca_idx = 0
+        with torch.no_grad():
+            g, ctx = open_graph()
+            x_cur = gs.xin
+            for layer, norm, kind in zip(model.layers, model.norms, model.layout):
+                residual = x_cur
+                h = norm(x_cur)
+                if kind == 'kda':
+                    o = layer._decode_step_inplace(h, stacked[kda_idx], layer._conv_lookback)
+                    kda_idx += 1
+                else:
+                    if kind == 'csa':
+                        proj = self._project_csa(layer, h)
+                        cache = self._csa_caches[csa_idx]
+                        width = cfg.csa_nh * cfg.csa_c
+                        csa_idx += 1
+                    else:
+                        proj = self._project_hca(layer, h)
+                        cache = self._hca_caches[hca_idx]
+                        width = cfg.hca_nh * cfg.hca_c
+                        hca_idx += 1
+                    close_graph(g, ctx)
+                    o_core = torch.empty(B, 1, width, device=x.device, dtype=x.dtype)
+                    keep.append((proj, o_core))
+                    parts.append(self._eager_cache_part(kind, layer, cache, proj, o_core))
+                    g, ctx = open_graph()
+                    o = _linear(o_core, layer.o_proj.weight)
+                x_cur = residual + o
+            gs.xout = x_cur
+            close_graph(g, ctx)
+
+    @staticmethod
+    def _eager_cache_part(kind, layer, cache, proj, o_core):
+        """The cache update and decode attention of a CSA / HCA layer, writing
+        its output into the static ``o_core``."""
+        cfg = layer.cfg
+        B = o_core.shape[0]
+
+        def run():
+            with torch.no_grad():
+                if kind == 'csa':
+                    Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx = proj
+                    cache.append_step(Ca, Cb, Za, Zb, K_idx, Z_idx, layer.Ba, layer.Bb,
+                                      layer.B_idx)
+                    o = cache.forward_step(q, q_idx, w_idx, topk=cfg.csa_topk, nh=cfg.csa_nh,
+                                           nIh=cfg.csa_nIh, scale=1.0, sink_logits=layer.sink,
+                                           use_ste=False, normalize_qk=True, _normalize_q=True,
+                                           _out_dtype=o_core.dtype)
+                else:
+                    C, Z, q = proj
+                    cache.append_step(C, Z, layer.B_pos)
+                    o = cache.forward_step(q, nh=cfg.hca_nh, scale=1.0, sink_logits=layer.sink,
+                                           _normalize_q=True, _out_dtype=o_core.dtype)
+                o_core.copy_(o.reshape(B, 1, -1))
+        return run
+
+    def _forward_graphed(self, x: torch.Tensor, stacked) -> torch.Tensor | None:
+        """The decode step through graphs, or None when it is not eligible."""
+        if not self._graph_eligible(x, stacked):
+            return None
+        key = self._graph_key(x, stacked)
+        gs = self._graphs
+        if gs is None or gs.key != key:
+            self._graphs = None
+            gs = self._capture(x, stacked)
+            gs.key = self._graph_key(x, stacked)  # after the lookback buffers were replaced
+            self._graphs = gs
+        gs.xin.copy_(x)
+        for part in gs.parts:
+            part()
+        return gs.xout.clone()
 
     def _ensure_csa_cache(self, idx: int, layer: CSAHybridLayer, h: torch.Tensor):
         cfg = layer.cfg
@@ -768,6 +1009,11 @@ class HybridDecoding(nn.Module):
         if not fresh and (stacked.dtype != torch.float32 or stacked.device != x.device
                           or not stacked.is_contiguous()):
             stacked = stacked.to(device=x.device, dtype=torch.float32).contiguous()
+        if not fresh and x.shape[1] == 1:
+            model._kda_state = stacked
+            y = self._forward_graphed(x, stacked)
+            if y is not None:
+                return y
         if model.n_kda_layers > 0 and fresh:
             cfg = model.cfg
             # one persistent [L, B, HV, K, V] fp32 state, updated in place by the layers
