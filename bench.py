@@ -395,7 +395,7 @@ def bench_hybrid(dev, T=16384, B=2, n_decode=256):
     pre_ms, dec_ms = e0.elapsed_time(e1), e2.elapsed_time(e3)
     return {"B": B, "T": T, "layout": dec.model.layout_str(), "prefill_ms": pre_ms,
             "prefill_tokens_per_s": B * T / (pre_ms * 1e-3), "decode_steps": n_decode,
-            "decode_untimed_steps": n_untimed, "decode_graphs": dec._graphs is not None,
+            "decode_untimed_steps": n_untimed, "decode_graph": dec._graph is not None, "decode_device_steps": dec._device_steps,
             "decode_ms_per_step": dec_ms / n_decode,
             "decode_tokens_per_s": B * n_decode / (dec_ms * 1e-3)}
 

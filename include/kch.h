@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define KCH_ABI_VERSION 9
+#define KCH_ABI_VERSION 10
 
 #define KCH_OK 0
 #define KCH_ERR_INVALID 1     /* bad pointer / shape / argument */
@@ -312,6 +312,124 @@ int kch_layer_norm(const void* x, const void* w, const void* b, void* out, int r
  */
 int kch_linear_rows(const void* x, long long ldx, const void* w, long long ldw, void* y,
                     long long ldy, int M, int N, int K, int dtype, void* stream);
+
+/* ---- Device-driven decode step ----------------------------------------
+ * The entry points below make up one single-token decode step of
+ * HybridDecoding (run_decoding.py:601-851) in which every count that changes
+ * from step to step is derived on the GPU from n_seen, a device int holding
+ * the number of tokens the caches held before the step: the step's launches
+ * are then identical on every step and one captured graph replays it. The
+ * caller keeps the caches' buffers at fixed addresses with room for `cap`
+ * compressed blocks, and increments n_seen once at the end of each step
+ * (kch_linear_rows_fused's counter, on the step's last launch).
+ */
+
+/*
+ * kch_linear_rows with the pieces of a decode sub-layer around it
+ * (HybridKCHAttention.forward, ops_fused.py:879-955: x + layer(norm(x))):
+ *   ln_w != NULL: x rows are first replaced by LayerNorm(x) (_Fp32LayerNorm,
+ *     ops_fused.py:42-60; fp32, rounded to dtype), ln_w / ln_b [K] of
+ *     ln_wdtype (ln_b may be NULL), K <= 4096, M * K <= 32768;
+ *   res != NULL: y = res + y, y rounded to dtype before the add (res [M, N],
+ *     row stride ldr, of dtype; may be y itself);
+ *   counter != NULL: *counter += 1 (one thread, after nothing else reads it).
+ */
+int kch_linear_rows_fused(const void* x, long long ldx, const void* w, long long ldw, void* y,
+                          long long ldy, int M, int N, int K, const void* ln_w, const void* ln_b,
+                          float ln_eps, int ln_wdtype, const void* res, long long ldr, int* counter,
+                          int dtype, void* stream);
+
+/*
+ * The front of a KDA sub-layer for one token (KDAHybridLayer.forward_functional,
+ * ops_fused.py:480-551, after the norm of HybridKCHAttention.forward): h =
+ * LayerNorm(x) (as kch_layer_norm), out = causal depthwise conv3 over
+ * [lookback ; h] (as kch_short_conv), then lookback <- [lookback[1] ; h] in
+ * place. x [B, d] (row stride ldx), lookback [B, 2, d], conv_w [d, 3], conv_b
+ * [d] or NULL, out [B, d] of dtype; ln_w, ln_b [d] of wdtype. d a multiple of
+ * 8, at most 4096; operands 16-byte aligned.
+ */
+int kch_kda_decode_front(const void* x, long long ldx, const void* ln_w, const void* ln_b,
+                         float eps, void* lookback, const void* conv_w, const void* conv_b,
+                         void* out, int B, int d, int dtype, int wdtype, void* stream);
+
+/*
+ * The rest of a KDA sub-layer for one token, in one launch: the activations of
+ * ops_fused.py:571-581 (as kch_kda_gates, with the g_up product inside) and the
+ * recurrent update of naive_recurrent_kda (ops_kda.py:175-267, as
+ * kch_kda_recurrent_fwd with T = 1). proj [B, ld_proj] rows hold q (H*K) |
+ * k (H*K) | v (HV*V) | beta logits (HV) | g_down (K); g_up [HV*K, K] of dtype
+ * (16-byte aligned); state [B, HV, K, V] fp32, updated in place; o [B, HV*V].
+ * K in {16, 32, 64, 128, 256}, V a multiple of 32.
+ */
+int kch_kda_decode_step(const void* proj, long long ld_proj, const void* g_up, float* state,
+                        void* o, int B, int H, int HV, int K, int V, float scale,
+                        float decay_scale, float g_clamp_min, int dtype, void* stream);
+
+/*
+ * CSADecodingCache.append_step for one token (ops_decoding_cache.py:631-782).
+ * proj [B, ld_proj] rows start with [Ca | Cb | Za | Zb | K_idx | Z_idx] (widths
+ * c, c, c, c, cI, cI, dtype); acc [B, m, 4c + 2cI] the rows of the block being
+ * filled; prev [B, m, 2c] the [Cb | Zb] rows of the last completed block; Ba,
+ * Bb [m, c], B_idx [m, cI] fp32. Writes ring row (n_seen % win) of ring [B, win,
+ * c] (the token's Ca, L2-normalised when normalize), accumulator slot n_seen %
+ * m, and when the token completes block n_seen / m (< cap): its overlapped
+ * compressed row into c_rows [B, cap, c] (dtype) and c_keys [B, cap, c] (bf16,
+ * L2-normalised when normalize), its indexer key row into k_rows [B, cap, cI]
+ * (dtype) with k_inv [B, cap] = 1 / max(||row||, 1e-12), and its [Cb | Zb] rows
+ * into prev. c + cI <= 256.
+ */
+int kch_csa_cache_append(const void* proj, long long ld_proj, void* acc, void* prev,
+                         const float* Ba, const float* Bb, const float* B_idx, void* ring,
+                         void* c_rows, void* c_keys, void* k_rows, float* k_inv,
+                         const int* n_seen, int B, int c, int cI, int m, int win, int cap,
+                         int normalize, int dtype, void* stream);
+
+/*
+ * HCADecodingCache.append_step for one token (ops_decoding_cache.py:1200-1267):
+ * proj rows start with [C | Z] (c each); acc [B, m2, 2c]; B_pos [m2, c] fp32;
+ * ring, c_rows, c_keys as kch_csa_cache_append. c <= 256.
+ */
+int kch_hca_cache_append(const void* proj, long long ld_proj, void* acc, const float* B_pos,
+                         void* ring, void* c_rows, void* c_keys, const int* n_seen, int B, int c,
+                         int m2, int win, int cap, int normalize, int dtype, void* stream);
+
+/*
+ * Workspace bytes of kch_csa_decode_dyn (sparse = 1) / kch_hca_decode_dyn for
+ * caches of up to cap blocks and a window of win rows.
+ */
+size_t kch_decode_dyn_ws_bytes(int B, int cap, int nh, int hd, int topk, int win, int sparse);
+
+/*
+ * kch_csa_decode with the block count and window length taken from the device
+ * counter: nb = min((*n_seen + 1) / m, cap), ring_len = min(*n_seen + 1, win)
+ * (CSADecodingCache.forward_step, ops_decoding_cache.py:783-1070, after
+ * kch_csa_cache_append of the same step). q, q_idx, w_idx rows are ld_q,
+ * ld_qidx, ld_w elements apart per sequence; ring [B, win, hd] with batch
+ * stride ring_bstride; idx_out [B, topk] receives the selection; ws holds
+ * kch_decode_dyn_ws_bytes(B, cap, nh, hd, topk, win, 1) bytes, 256-byte
+ * aligned. topk >= 1.
+ */
+int kch_csa_decode_dyn(const void* q, long long ld_q, const void* q_idx, long long ld_qidx,
+                       const void* w_idx, long long ld_w, const void* kv_comp,
+                       long long kv_bstride, const void* k_rows, long long k_bstride,
+                       const float* k_inv, long long kinv_bstride, const void* ring,
+                       long long ring_bstride, const int* n_seen, int m, int win, int cap,
+                       const float* sink, void* out, int* idx_out, int B, int nh, int hd, int nIh,
+                       int cI, int topk, float scale, float idx_scale, int normalize_q,
+                       int normalize_qidx, int qdtype, int kdtype, int odtype, void* ws,
+                       size_t ws_bytes, void* stream);
+
+/*
+ * kch_hca_decode with nb = min((*n_seen + 1) / m2, cap) and ring_len =
+ * min(*n_seen + 1, win) from the device counter (HCADecodingCache.forward_step,
+ * ops_decoding_cache.py:1268-1395); ws holds kch_decode_dyn_ws_bytes(B, cap,
+ * nh, hd, 0, win, 0) bytes.
+ */
+int kch_hca_decode_dyn(const void* q, long long ld_q, const void* kv_comp, long long kv_bstride,
+                       const void* ring, long long ring_bstride, const int* n_seen, int m2,
+                       int win, int cap, const float* sink, void* out, int B, int nh, int hd,
+                       float scale, int normalize_q, int qdtype, int odtype, void* ws,
+                       size_t ws_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -422,6 +422,138 @@ int kch_linear_rows(const void* x, long long ldx, const void* w, long long ldw, 
   return hip_status(fn, kch::linear_rows_dispatch(p, dtype, (hipStream_t)stream));
 }
 
+int kch_linear_rows_fused(const void* x, long long ldx, const void* w, long long ldw, void* y,
+                          long long ldy, int M, int N, int K, const void* ln_w, const void* ln_b,
+                          float ln_eps, int ln_wdtype, const void* res, long long ldr, int* counter,
+                          int dtype, void* stream) {
+  const char* fn = "kch_linear_rows_fused";
+  if (dtype != KCH_DT_BF16 && dtype != KCH_DT_F16)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: dtype %d (bf16 or fp16 only)", fn, dtype);
+  if (M < 0 || N < 0 || K < 0) return fail(KCH_ERR_INVALID, "%s: bad sizes", fn);
+  if (M == 0 || N == 0) {
+    if (counter) return fail(KCH_ERR_INVALID, "%s: a counter needs a launch (M, N >= 1)", fn);
+    return KCH_OK;
+  }
+  if (M > 16) return fail(KCH_ERR_UNSUPPORTED, "%s: M=%d > 16 rows", fn, M);
+  if (K < 32 || K % 32) return fail(KCH_ERR_UNSUPPORTED, "%s: K=%d not a multiple of 32", fn, K);
+  if (!x || !w || !y) return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
+  if (ldx < K || ldw < K || ldy < N || (res && ldr < N))
+    return fail(KCH_ERR_INVALID, "%s: row strides below the row lengths", fn);
+  if ((ldx | ldw) % 8 || (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) % 16)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: x and w rows must be 16-byte aligned", fn);
+  kch::LinearRowsParams p{x, w, y, ldx, ldw, ldy, M, N, K};
+  if (ln_w) {
+    if (!dtype_ok(ln_wdtype)) return fail(KCH_ERR_INVALID, "%s: unknown norm dtype %d", fn, ln_wdtype);
+    if (K > 4096 || (long long)M * K > kch::kLinearLnMax)
+      return fail(KCH_ERR_UNSUPPORTED, "%s: a normalised input holds at most 4096 columns and %d "
+                  "elements (M=%d, K=%d)", fn, kch::kLinearLnMax, M, K);
+    if ((reinterpret_cast<uintptr_t>(ln_w) | reinterpret_cast<uintptr_t>(ln_b)) % 16)
+      return fail(KCH_ERR_UNSUPPORTED, "%s: norm parameters must be 16-byte aligned", fn);
+    if (std::isnan(ln_eps) || ln_eps < 0.f) return fail(KCH_ERR_INVALID, "%s: bad eps", fn);
+    p.ln_w = ln_w;
+    p.ln_b = ln_b;
+    p.ln_eps = ln_eps;
+    p.ln_wdtype = ln_wdtype;
+  } else if (ln_b) {
+    return fail(KCH_ERR_INVALID, "%s: a norm bias without a norm weight", fn);
+  }
+  p.res = res;
+  p.ldr = ldr;
+  p.counter = counter;
+  return hip_status(fn, kch::linear_rows_dispatch(p, dtype, (hipStream_t)stream));
+}
+
+int kch_kda_decode_front(const void* x, long long ldx, const void* ln_w, const void* ln_b,
+                         float eps, void* lookback, const void* conv_w, const void* conv_b,
+                         void* out, int B, int d, int dtype, int wdtype, void* stream) {
+  const char* fn = "kch_kda_decode_front";
+  if (!dtype_ok(dtype) || !dtype_ok(wdtype))
+    return fail(KCH_ERR_INVALID, "%s: unknown dtype %d / %d", fn, dtype, wdtype);
+  if (B < 0 || d < 1) return fail(KCH_ERR_INVALID, "%s: bad sizes B=%d d=%d", fn, B, d);
+  if (d % 8 || d > 4096) return fail(KCH_ERR_UNSUPPORTED, "%s: d=%d (a multiple of 8, at most 4096)", fn, d);
+  if (ldx < d) return fail(KCH_ERR_INVALID, "%s: row stride %lld below d=%d", fn, ldx, d);
+  if (B == 0) return KCH_OK;
+  if (!x || !ln_w || !lookback || !conv_w || !out) return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
+  const uintptr_t a = (uintptr_t)x | (uintptr_t)ln_w | (uintptr_t)ln_b | (uintptr_t)lookback |
+                      (uintptr_t)conv_w | (uintptr_t)conv_b | (uintptr_t)out;
+  if (a % 16 || ldx % 8) return fail(KCH_ERR_INVALID, "%s: operands must be 16-byte aligned", fn);
+  if (std::isnan(eps) || eps < 0.f) return fail(KCH_ERR_INVALID, "%s: bad eps", fn);
+  kch::KdaFrontParams p{x, ldx, ln_w, ln_b, eps, lookback, conv_w, conv_b, out, B, d};
+  return hip_status(fn, kch::kda_front_dispatch(p, dtype, wdtype, (hipStream_t)stream));
+}
+
+int kch_kda_decode_step(const void* proj, long long ld_proj, const void* g_up, float* state,
+                        void* o, int B, int H, int HV, int K, int V, float scale,
+                        float decay_scale, float g_clamp_min, int dtype, void* stream) {
+  const char* fn = "kch_kda_decode_step";
+  if (!dtype_ok(dtype)) return fail(KCH_ERR_INVALID, "%s: unknown dtype %d", fn, dtype);
+  if (B < 0 || H < 1 || HV < 1 || V < 1) return fail(KCH_ERR_INVALID, "%s: bad sizes", fn);
+  if (HV % H) return fail(KCH_ERR_INVALID, "%s: HV=%d must be divisible by H=%d", fn, HV, H);
+  if (K != 16 && K != 32 && K != 64 && K != 128 && K != 256)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: K=%d not in {16, 32, 64, 128, 256}", fn, K);
+  if (V % 32) return fail(KCH_ERR_UNSUPPORTED, "%s: V=%d must be a multiple of 32", fn, V);
+  if (ld_proj < 2LL * H * K + (long long)HV * V + HV + K)
+    return fail(KCH_ERR_INVALID, "%s: row stride %lld too small", fn, ld_proj);
+  if ((long long)B * HV * (V / 32) >= (1LL << 31)) return fail(KCH_ERR_INVALID, "%s: too large", fn);
+  if (std::isnan(g_clamp_min)) return fail(KCH_ERR_INVALID, "%s: g_clamp_min is NaN", fn);
+  if (B == 0) return KCH_OK;
+  if (!proj || !g_up || !state || !o) return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
+  if ((uintptr_t)g_up % 16) return fail(KCH_ERR_INVALID, "%s: g_up must be 16-byte aligned", fn);
+  kch::KdaStepParams p{proj, ld_proj, g_up, state, o, B, H, HV, K, V, scale, decay_scale,
+                       g_clamp_min};
+  return hip_status(fn, kch::kda_step_dispatch(p, dtype, (hipStream_t)stream));
+}
+
+// Shared checks of the cache append entry points.
+static int check_cache_append(const char* fn, const void* proj, long long ld_proj, long long width,
+                              const void* acc, const void* c_rows, const void* c_keys,
+                              const int* n_seen, int B, int c, int m, int win, const void* ring,
+                              int cap, int dtype) {
+  if (!dtype_ok(dtype)) return fail(KCH_ERR_INVALID, "%s: unknown dtype %d", fn, dtype);
+  if (B < 0 || c < 1 || m < 1 || win < 0 || cap < 1)
+    return fail(KCH_ERR_INVALID, "%s: bad sizes B=%d c=%d m=%d win=%d cap=%d", fn, B, c, m, win, cap);
+  if (ld_proj < width) return fail(KCH_ERR_INVALID, "%s: row stride %lld below %lld", fn, ld_proj, width);
+  if (!proj || !acc || !c_rows || !c_keys || !n_seen || (win > 0 && !ring))
+    return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
+  return KCH_OK;
+}
+
+int kch_csa_cache_append(const void* proj, long long ld_proj, void* acc, void* prev,
+                         const float* Ba, const float* Bb, const float* B_idx, void* ring,
+                         void* c_rows, void* c_keys, void* k_rows, float* k_inv,
+                         const int* n_seen, int B, int c, int cI, int m, int win, int cap,
+                         int normalize, int dtype, void* stream) {
+  const char* fn = "kch_csa_cache_append";
+  if (c < 1 || cI < 1 || c > 256 || c + cI > 256)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: c=%d, cI=%d (c + cI at most 256)", fn, c, cI);
+  int rc = check_cache_append(fn, proj, ld_proj, 4LL * c + 2LL * cI, acc, c_rows, c_keys, n_seen,
+                              B, c, m, win, ring, cap, dtype);
+  if (rc) return rc;
+  if (B == 0) return KCH_OK;
+  if (!prev || !Ba || !Bb || !B_idx || !k_rows || !k_inv)
+    return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
+  kch::CacheStepParams p{proj, ld_proj, acc, prev, Ba, Bb, B_idx, win > 0 ? ring : nullptr,
+                         c_rows, c_keys, k_rows, k_inv, n_seen, B, c, cI, m, win, cap,
+                         normalize != 0, 1};
+  return hip_status(fn, kch::cache_step_dispatch(p, dtype, (hipStream_t)stream));
+}
+
+int kch_hca_cache_append(const void* proj, long long ld_proj, void* acc, const float* B_pos,
+                         void* ring, void* c_rows, void* c_keys, const int* n_seen, int B, int c,
+                         int m2, int win, int cap, int normalize, int dtype, void* stream) {
+  const char* fn = "kch_hca_cache_append";
+  if (c < 1 || c > 256) return fail(KCH_ERR_UNSUPPORTED, "%s: c=%d > 256", fn, c);
+  int rc = check_cache_append(fn, proj, ld_proj, 2LL * c, acc, c_rows, c_keys, n_seen, B, c, m2,
+                              win, ring, cap, dtype);
+  if (rc) return rc;
+  if (B == 0) return KCH_OK;
+  if (!B_pos) return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
+  kch::CacheStepParams p{proj, ld_proj, acc, nullptr, B_pos, nullptr, nullptr,
+                         win > 0 ? ring : nullptr, c_rows, c_keys, nullptr, nullptr, n_seen, B, c,
+                         0, m2, win, cap, normalize != 0, 0};
+  return hip_status(fn, kch::cache_step_dispatch(p, dtype, (hipStream_t)stream));
+}
+
 }  // extern "C"
 
 namespace {
@@ -463,12 +595,24 @@ DecodePlan decode_plan(int B, int nb, int nh, int hd, int topk, int ring_len, bo
   return pl;
 }
 
+// Per-step counts of a device-driven decode step (decode_step.hip).
+struct DynStep {
+  const int* n_seen = nullptr;
+  int m = 1, win = 0, cap = 0;
+  long long ld_qb = 0;
+};
+
 int run_decode_attn(const char* fn, const DecodePlan& pl, const void* q, const void* kv_comp,
                     long long kv_bstride, const int* idx, const void* ring, long long ring_bstride,
                     int ring_len, const float* sink, void* out, int B, int nb, int nh, int hd,
                     float scale, int normalize_q, int qdtype, int odtype, char* ws,
-                    hipStream_t s) {
+                    hipStream_t s, const DynStep& dyn = DynStep()) {
   kch::DecodeAttnParams a;
+  a.n_seen = dyn.n_seen;
+  a.m = dyn.m;
+  a.win = dyn.win;
+  a.cap = dyn.cap;
+  a.ld_qb = dyn.ld_qb;
   a.q = q;
   a.kv = (const kch::bf16_t*)kv_comp;
   a.idx = idx;
@@ -570,6 +714,89 @@ int kch_hca_decode(const void* q, const void* kv_comp, long long kv_bstride, con
   return run_decode_attn(fn, pl, q, kv_comp, kv_bstride, nullptr, ring, ring_bstride, ring_len,
                          sink, out, B, nb, nh, hd, scale, normalize_q, qdtype, odtype, (char*)ws,
                          (hipStream_t)stream);
+}
+
+size_t kch_decode_dyn_ws_bytes(int B, int cap, int nh, int hd, int topk, int win, int sparse) {
+  if (B <= 0 || cap < 1 || nh < 1 || hd < 1 || topk < 0 || win < 0) return 0;
+  return decode_plan(B, cap, nh, hd, topk, win, sparse != 0).bytes;
+}
+
+int kch_csa_decode_dyn(const void* q, long long ld_q, const void* q_idx, long long ld_qidx,
+                       const void* w_idx, long long ld_w, const void* kv_comp,
+                       long long kv_bstride, const void* k_rows, long long k_bstride,
+                       const float* k_inv, long long kinv_bstride, const void* ring,
+                       long long ring_bstride, const int* n_seen, int m, int win, int cap,
+                       const float* sink, void* out, int* idx_out, int B, int nh, int hd, int nIh,
+                       int cI, int topk, float scale, float idx_scale, int normalize_q,
+                       int normalize_qidx, int qdtype, int kdtype, int odtype, void* ws,
+                       size_t ws_bytes, void* stream) {
+  const char* fn = "kch_csa_decode_dyn";
+  int rc = check_attn(fn, B, 1, cap, nh, hd, qdtype, odtype);
+  if (rc) return rc;
+  if (!dtype_ok(kdtype)) return fail(KCH_ERR_INVALID, "%s: unknown key dtype %d", fn, kdtype);
+  if (m < 1 || win < 0 || cap < 1) return fail(KCH_ERR_INVALID, "%s: bad m / win / cap", fn);
+  if (topk < 1) return fail(KCH_ERR_UNSUPPORTED, "%s: topk=%d (at least 1)", fn, topk);
+  if (nIh != 1 && nIh != 2 && nIh != 4 && nIh != 8 && nIh != 16)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: nIh=%d not in {1,2,4,8,16}", fn, nIh);
+  if (cI != 32 && cI != 64 && cI != 128)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: cI=%d not in {32,64,128}", fn, cI);
+  if (ld_q < (long long)nh * hd || ld_qidx < (long long)nIh * cI || (w_idx && ld_w < nIh))
+    return fail(KCH_ERR_INVALID, "%s: query row strides too small", fn);
+  if (B == 0) return KCH_OK;
+  const DecodePlan pl = decode_plan(B, cap, nh, hd, topk, win, true);
+  if (!ws || ws_bytes < pl.bytes)
+    return fail(KCH_ERR_INVALID, "%s: workspace of %zu bytes required", fn, pl.bytes);
+  if ((uintptr_t)ws & 255) return fail(KCH_ERR_INVALID, "%s: workspace must be 256-byte aligned", fn);
+  if (!q || !q_idx || !kv_comp || !k_rows || !out || !idx_out || !n_seen || (win > 0 && !ring))
+    return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
+  if (pl.nr > 1 && !kch::decode_merge_fits(topk))
+    return fail(KCH_ERR_UNSUPPORTED, "%s: cap=%d blocks with topk=%d exceed the merge capacity", fn,
+                cap, topk);
+  if (!kch::decode_idx_fits(pl.rb, topk, pl.nr))
+    return fail(KCH_ERR_UNSUPPORTED, "%s: cap=%d blocks with topk=%d exceed the indexer's LDS", fn,
+                cap, topk);
+  hipStream_t s = (hipStream_t)stream;
+  char* w = (char*)ws;
+  kch::DecodeIdxParams ip;
+  ip.q_idx = q_idx; ip.w_idx = w_idx; ip.keys = k_rows; ip.inv_norm = k_inv;
+  ip.k_bstride = k_bstride; ip.n_bstride = kinv_bstride;
+  ip.cand = (unsigned long long*)(w + pl.off_cand);
+  ip.idx_out = idx_out;
+  ip.B = B; ip.nb = cap; ip.nIh = nIh; ip.cI = cI; ip.topk = topk; ip.rb = pl.rb; ip.nr = pl.nr;
+  ip.normalize_q = normalize_qidx; ip.scale = idx_scale;
+  ip.ld_qb = ld_qidx; ip.ld_wb = ld_w;
+  ip.n_seen = n_seen; ip.m = m; ip.cap = cap;
+  rc = hip_status(fn, kch::decode_idx_dispatch(ip, qdtype, kdtype, s));
+  if (rc) return rc;
+  DynStep dyn;
+  dyn.n_seen = n_seen; dyn.m = m; dyn.win = win; dyn.cap = cap; dyn.ld_qb = ld_q;
+  return run_decode_attn(fn, pl, q, kv_comp, kv_bstride, idx_out, win > 0 ? ring : nullptr,
+                         ring_bstride, win, sink, out, B, cap, nh, hd, scale, normalize_q, qdtype,
+                         odtype, w, s, dyn);
+}
+
+int kch_hca_decode_dyn(const void* q, long long ld_q, const void* kv_comp, long long kv_bstride,
+                       const void* ring, long long ring_bstride, const int* n_seen, int m2,
+                       int win, int cap, const float* sink, void* out, int B, int nh, int hd,
+                       float scale, int normalize_q, int qdtype, int odtype, void* ws,
+                       size_t ws_bytes, void* stream) {
+  const char* fn = "kch_hca_decode_dyn";
+  int rc = check_attn(fn, B, 1, cap, nh, hd, qdtype, odtype);
+  if (rc) return rc;
+  if (m2 < 1 || win < 0 || cap < 1) return fail(KCH_ERR_INVALID, "%s: bad m2 / win / cap", fn);
+  if (ld_q < (long long)nh * hd) return fail(KCH_ERR_INVALID, "%s: query row stride too small", fn);
+  if (B == 0) return KCH_OK;
+  const DecodePlan pl = decode_plan(B, cap, nh, hd, 0, win, false);
+  if (!ws || ws_bytes < pl.bytes)
+    return fail(KCH_ERR_INVALID, "%s: workspace of %zu bytes required", fn, pl.bytes);
+  if ((uintptr_t)ws & 255) return fail(KCH_ERR_INVALID, "%s: workspace must be 256-byte aligned", fn);
+  if (!q || !kv_comp || !out || !n_seen || (win > 0 && !ring))
+    return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
+  DynStep dyn;
+  dyn.n_seen = n_seen; dyn.m = m2; dyn.win = win; dyn.cap = cap; dyn.ld_qb = ld_q;
+  return run_decode_attn(fn, pl, q, kv_comp, kv_bstride, nullptr, win > 0 ? ring : nullptr,
+                         ring_bstride, win, sink, out, B, cap, nh, hd, scale, normalize_q, qdtype,
+                         odtype, (char*)ws, (hipStream_t)stream, dyn);
 }
 
 }  // extern "C"

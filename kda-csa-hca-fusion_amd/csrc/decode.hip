@@ -571,11 +571,18 @@ __global__ __launch_bounds__(256, 4) void idx_range_kernel(DecodeIdxParams p) {
   const int q4 = lane >> 4, n = lane & 15;
   const int b = blockIdx.x / p.nr, r = blockIdx.x - b * p.nr;
   const int r0 = r * p.rb;
-  const int nr_blocks = min(p.rb, p.nb - r0);
+  const int nb = p.n_seen ? min((p.n_seen[0] + 1) / p.m, p.cap) : p.nb;
+  const int nr_blocks = min(p.rb, nb - r0);
   const int nIh = p.nIh;
   // a sequence's candidates: nr lists of topk (range r holds min(its blocks, topk))
   u64* cout = p.cand + ((size_t)b * p.nr + r) * p.topk;
-  if (nr_blocks <= 0) return;  // no range is empty (decode_idx_plan)
+  if (nr_blocks <= 0) {
+    // only a device-driven step has empty ranges (those past its blocks); with
+    // one range the selection is empty
+    if (p.nr == 1)
+      for (int i = tid; i < p.topk; i += 256) p.idx_out[(size_t)b * p.topk + i] = -1;
+    return;
+  }
 
   // ---- q fragments (MFMA A operand: row = index head n, zero beyond nIh), split bf16 ----
   bf16x8 qhi[NS], qlo[NS];
@@ -583,7 +590,8 @@ __global__ __launch_bounds__(256, 4) void idx_range_kernel(DecodeIdxParams p) {
   {
     float f[NS][8];
     float ss = 0.f;
-    const QT* qrow = static_cast<const QT*>(p.q_idx) + ((size_t)b * nIh + (n < nIh ? n : 0)) * CI;
+    const QT* qrow = static_cast<const QT*>(p.q_idx) + (size_t)b * (p.ld_qb ? p.ld_qb : (long long)nIh * CI) +
+                     (size_t)(n < nIh ? n : 0) * CI;
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       Load8<QT>::run(qrow + 32 * s + 8 * q4, f[s]);
@@ -597,7 +605,7 @@ __global__ __launch_bounds__(256, 4) void idx_range_kernel(DecodeIdxParams p) {
       for (int i = 0; i < 8; ++i) f[s][i] = n < nIh ? f[s][i] * inv : 0.f;
       split8(f[s], qhi[s], qlo[s]);
     }
-    const QT* wrow = static_cast<const QT*>(p.w_idx) + (size_t)b * nIh;
+    const QT* wrow = static_cast<const QT*>(p.w_idx) + (size_t)b * (p.ld_wb ? p.ld_wb : (long long)nIh);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int hh = 4 * q4 + e;
@@ -791,12 +799,15 @@ __global__ __launch_bounds__(256) void idx_merge_kernel(DecodeIdxParams p) {
   int* counter = scratch + 48;                               // [4]
   const int tid = threadIdx.x, b = blockIdx.x;
   const u64* src = p.cand + (size_t)b * nr * topk;
+  // ranges holding blocks (all nr unless the step is device-driven)
+  const int nb = p.n_seen ? min((p.n_seen[0] + 1) / p.m, p.cap) : p.nb;
+  const int na = (nb + p.rb - 1) / p.rb;
   // candidate f of the sequence: ranges before the last hold c0 each
   const int c0 = min(p.rb, topk);
-  const int cl = min(p.nb - (nr - 1) * p.rb, topk);
-  const int N = (nr - 1) * c0 + cl;
+  const int cl = na > 0 ? min(nb - (na - 1) * p.rb, topk) : 0;
+  const int N = na > 0 ? (na - 1) * c0 + cl : 0;
   auto gval = [&](int f) {
-    const int r = min(f / c0, nr - 1);
+    const int r = min(f / c0, na - 1);
     return src[(size_t)r * topk + (f - r * c0)];
   };
   int cnt = N;
@@ -877,18 +888,27 @@ __global__ __launch_bounds__(256, 3) void attn_kernel(DecodeAttnParams p) {
   const int tid = threadIdx.x, wv = wave_id(), lane = tid & 63, n = lane & 15;
   bf16_t* stage = reinterpret_cast<bf16_t*>(lds) + wv * STAGE;
   const int b = blockIdx.x / p.ngrp, g = blockIdx.x - b * p.ngrp;
-  const int nrows = p.na + p.ring_len;
+  int nb = p.nb, na = p.na, ring_len = p.ring_len;
+  if (p.n_seen) {
+    const int t1 = p.n_seen[0] + 1;
+    nb = min(t1 / p.m, p.cap);
+    ring_len = min(t1, p.win);
+    if (!p.idx) na = nb;
+  }
+  const int nrows = na + ring_len;
   const int jg0 = g * p.rows_per_group, jg1 = min(nrows, jg0 + p.rows_per_group);
 
-  const QT* qrow = static_cast<const QT*>(p.q) + ((size_t)b * p.nh + n) * HD;
+  const QT* qrow = static_cast<const QT*>(p.q) + (size_t)b * (p.ld_qb ? p.ld_qb : (long long)p.nh * HD) +
+                   (size_t)n * HD;
   W w;
   w.template init<QT>(n < p.nh ? qrow : nullptr, p.normalize_q != 0, p.scale);
   const bf16_t* kv = p.kv + (size_t)b * p.kv_bstride;
   const bf16_t* ring = p.ring ? p.ring + (size_t)b * p.ring_bstride : nullptr;
   const int* idx = p.idx ? p.idx + (size_t)b * p.na : nullptr;
   // rows of padding lanes must still be readable: a cached block when there is
-  // one, else the ring (a group only exists when one of the two holds rows)
-  const bf16_t* dflt = p.na > 0 ? kv : ring;
+  // one, else the ring (a group only exists when one of the two holds rows; a
+  // device-driven step always has the key storage)
+  const bf16_t* dflt = (na > 0 || !ring) ? kv : ring;
   // The group's rows come in 32-row steps, wave w taking steps w, w + 4, ...,
   // gathered row-major (whole rows per TPR lanes: a load instruction covers
   // RPI full rows, contiguous for consecutive cached blocks) with nontemporal
@@ -897,7 +917,7 @@ __global__ __launch_bounds__(256, 3) void attn_kernel(DecodeAttnParams p) {
   // are read only for rows below min(jg1, na). Without indices a readable word
   // is loaded.
   const int* ip = idx ? idx : reinterpret_cast<const int*>(dflt);
-  const int ilim = idx ? max(min(jg1, p.na), 1) : 1;
+  const int ilim = idx ? max(min(jg1, na), 1) : 1;
   auto row_j = [&](int m, int r) { return jg0 + 32 * (wv + 4 * m) + r; };
   auto idx_of = [&](int m) { return ip[min(row_j(m, lane & 31), ilim - 1)]; };
   typedef typename W::u32x4 u32x4;
@@ -911,11 +931,11 @@ __global__ __launch_bounds__(256, 3) void attn_kernel(DecodeAttnParams p) {
       const int blk = idx ? __shfl(ix, r) : j;
       bool ok = j < jg1;
       const bf16_t* row = dflt;
-      if (j < p.na) {
-        ok = ok && blk >= 0 && blk < p.nb;
+      if (j < na) {
+        ok = ok && blk >= 0 && blk < nb;
         if (ok) row = kv + (size_t)blk * HD;
       } else if (ok) {
-        row = ring + (size_t)(j - p.na) * HD;
+        row = ring + (size_t)(j - na) * HD;
       }
       rr.v[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(row + 8 * (lane % W::TPR)));
       const unsigned long long mb = __ballot(ok);

@@ -71,6 +71,10 @@ struct DecodeIdxParams {
   int rb, nr;              // range size and count (decode_idx_plan)
   int normalize_q;
   float scale;
+  long long ld_qb = 0, ld_wb = 0;  // elements between batches of q_idx / w_idx (0: nIh cI, nIh)
+  // device-driven step: nb = (*n_seen + 1) / m, at most cap (nr ranges cover cap)
+  const int* n_seen = nullptr;
+  int m = 1, cap = 0;
 };
 void decode_idx_plan(int B, int nb, int topk, int* rb, int* nr);
 bool decode_merge_fits(int topk);  // the merge kernel's LDS holds its buffers for topk
@@ -97,6 +101,11 @@ struct DecodeAttnParams {
   long long kv_bstride, ring_bstride;
   int B, nb, nh, hd, na, ring_len, ngrp, rows_per_group, normalize_q;
   float scale;
+  long long ld_qb = 0;  // elements between batches of q (0: nh hd)
+  // device-driven step: t1 = *n_seen + 1 tokens cached, nb = min(t1 / m, cap),
+  // ring_len = min(t1, win), and without idx na = nb (dense)
+  const int* n_seen = nullptr;
+  int m = 1, win = 0, cap = 0;
 };
 hipError_t decode_attn_dispatch(const DecodeAttnParams& p, int qdtype, int odtype, hipStream_t s);
 

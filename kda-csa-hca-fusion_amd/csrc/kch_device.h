@@ -77,6 +77,21 @@ template <> struct Pair<_Float16> {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// The KDA layer's activations in fp32 (torch's silu, sigmoid, and softplus
+// with beta 1 and threshold 20: x above the threshold, else log1p(e^x)).
+__device__ __forceinline__ float silu_f(float x) { return x / (1.f + expf(-x)); }
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.f / (1.f + expf(-x)); }
+__device__ __forceinline__ float softplus_f(float x) { return x > 20.f ? x : log1pf(expf(x)); }
+
+// The value a tensor of type T stores for x (identity for fp32): each torch
+// operation of the reference writes its result in the layer's dtype, and the
+// next one reads it back from there.
+template <typename T>
+__device__ __forceinline__ float stored(float x) {
+  if constexpr (sizeof(T) == 2) return to_f32(from_f32<T>(x));
+  return x;
+}
+
 // Orders LDS traffic of one wave: every lane's earlier LDS writes are visible to
 // every lane's later LDS reads. Waves are not synchronised with each other.
 __device__ __forceinline__ void wave_lds_sync() {

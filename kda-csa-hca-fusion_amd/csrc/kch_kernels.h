@@ -76,14 +76,90 @@ struct LayerNormParams {
 };
 hipError_t layer_norm_dispatch(const LayerNormParams& p, int dtype, int wdtype, hipStream_t stream);
 
-// y[M, N] = x[M, K] w[N, K]^T for M <= 16 rows (linear_rows.hip).
+// y[M, N] = x[M, K] w[N, K]^T for M <= 16 rows (linear_rows.hip), optionally
+//   x <- LayerNorm(x) first (ln_w non-null: the rows are normalised into LDS,
+//        M * K <= kLinearLnMax),
+//   y <- res + y (res non-null; y rounded to the dtype before the add, as a
+//        separate residual add would see it),
+//   and (*counter)++ by one thread (counter non-null).
+constexpr int kLinearLnMax = 32768;
 struct LinearRowsParams {
-  const void* x;
-  const void* w;
-  void* y;
-  long long ldx, ldw, ldy;  // row strides in elements
-  int M, N, K;
+  const void* x = nullptr;
+  const void* w = nullptr;
+  void* y = nullptr;
+  long long ldx = 0, ldw = 0, ldy = 0;  // row strides in elements
+  int M = 0, N = 0, K = 0;
+  const void* ln_w = nullptr;  // [K] of ln_wdtype
+  const void* ln_b = nullptr;  // [K] of ln_wdtype or null
+  float ln_eps = 0.f;
+  int ln_wdtype = 0;
+  const void* res = nullptr;   // [M, N], row stride ldr, of the dtype (may be y itself)
+  long long ldr = 0;
+  int* counter = nullptr;
 };
 hipError_t linear_rows_dispatch(const LinearRowsParams& p, int dtype, hipStream_t stream);
+
+// ---- device-driven decode step (decode_step.hip) ----
+// n_seen: tokens the caches held before this step (device int); the step's
+// token is number n_seen of its sequence.
+
+// LayerNorm of x rows -> causal depthwise conv over [lookback ; h] ->
+// lookback <- [lookback[1] ; h]. x [B, d] (row stride ldx); lookback [B, 2, d];
+// conv_w [d, 3]; conv_b [d] or null; out [B, d]; all of dtype except ln_w /
+// ln_b (wdtype). d a multiple of 8, at most 4096.
+struct KdaFrontParams {
+  const void* x;
+  long long ldx;
+  const void* ln_w;
+  const void* ln_b;
+  float eps;
+  void* lookback;
+  const void* conv_w;
+  const void* conv_b;
+  void* out;
+  int B, d;
+};
+hipError_t kda_front_dispatch(const KdaFrontParams& p, int dtype, int wdtype, hipStream_t s);
+
+// One token's KDA activations and recurrent update. proj [B, ld_proj] rows:
+// q (H*K) | k (H*K) | v (HV*V) | beta logits (HV) | g_down (K); g_up [HV*K, K];
+// state [B, HV, K, V] fp32 updated in place; o [B, HV*V]. K in {16, 32, 64,
+// 128, 256}, V a multiple of 32.
+struct KdaStepParams {
+  const void* proj;
+  long long ld_proj;
+  const void* g_up;
+  float* state;
+  void* o;
+  int B, H, HV, K, V;
+  float scale, decay_scale, g_clamp_min;
+};
+hipError_t kda_step_dispatch(const KdaStepParams& p, int dtype, hipStream_t s);
+
+// One token appended to a CSA (csa = 1) or HCA cache. proj [B, ld_proj] rows
+// start with [Ca | Cb | Za | Zb | K_idx | Z_idx] (CSA: widths c x 4, cI x 2) or
+// [C | Z] (HCA); acc [B, m, W] holds the rows of the block being filled
+// (W = 4c + 2cI or 2c); prev [B, m, 2c] the [Cb | Zb] rows of the last
+// completed CSA block. Written: ring row n_seen % win (L2-normalised when
+// normalize), accumulator slot n_seen % m, and on a block's last token block
+// n_seen / m of c_rows (dtype), c_keys (bf16, normalised when normalize),
+// k_rows (dtype) and k_inv (fp32 1 / max(||row||, 1e-12)), then prev.
+struct CacheStepParams {
+  const void* proj;
+  long long ld_proj;
+  void* acc;
+  void* prev;
+  const float* Ba;   // [m, c] a-branch (HCA: B_pos)
+  const float* Bb;   // [m, c] b-branch (CSA)
+  const float* Bk;   // [m, cI] indexer keys (CSA)
+  void* ring;        // [B, win, c] or null
+  void* c_rows;      // [B, cap, c]
+  void* c_keys;      // [B, cap, c] bf16
+  void* k_rows;      // [B, cap, cI] (CSA)
+  float* k_inv;      // [B, cap] (CSA)
+  const int* n_seen;
+  int B, c, cI, m, win, cap, normalize, csa;
+};
+hipError_t cache_step_dispatch(const CacheStepParams& p, int dtype, hipStream_t s);
 
 }  // namespace kch

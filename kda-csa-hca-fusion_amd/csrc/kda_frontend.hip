@@ -94,20 +94,6 @@ __global__ __launch_bounds__(256) void short_conv_kernel(ShortConvParams p) {
   }
 }
 
-__device__ __forceinline__ float silu_f(float x) { return x / (1.f + expf(-x)); }
-__device__ __forceinline__ float sigmoid_f(float x) { return 1.f / (1.f + expf(-x)); }
-// torch's softplus (beta 1, threshold 20): x above the threshold, else log1p(e^x)
-__device__ __forceinline__ float softplus_f(float x) { return x > 20.f ? x : log1pf(expf(x)); }
-
-// The value a tensor of type T stores for x (identity for fp32): each torch
-// operation of the reference writes its result in the layer's dtype, and the
-// next one reads it back from there.
-template <typename T>
-__device__ __forceinline__ float stored(float x) {
-  if constexpr (sizeof(T) == 2) return to_f32(from_f32<T>(x));
-  return x;
-}
-
 // Workgroup (row, y) for token row `row`: y < QK_UNITS(H) -> waves take q/k
 // head vectors 4y .. 4y + 3 of the 2H (silu, then per-head L2
 // normalisation); higher y -> a 1024-element slice of v (silu), g (-softplus *

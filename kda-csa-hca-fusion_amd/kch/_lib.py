@@ -51,12 +51,23 @@ _SIGNATURES = {
     "kch_kda_gates": [_P, _L, _P, _L, _P, _P, _P, _P, _P] + [_I] * 6 + [_F, _I, _P],
     "kch_layer_norm": [_P, _P, _P, _P, _I, _I, _F, _I, _I, _P],
     "kch_linear_rows": [_P, _L, _P, _L, _P, _L, _I, _I, _I, _I, _P],
+    "kch_linear_rows_fused": [_P, _L, _P, _L, _P, _L, _I, _I, _I, _P, _P, _F, _I, _P, _L, _P,
+                              _I, _P],
+    "kch_kda_decode_front": [_P, _L, _P, _P, _F, _P, _P, _P, _P, _I, _I, _I, _I, _P],
+    "kch_kda_decode_step": [_P, _L, _P, _P, _P] + [_I] * 5 + [_F] * 3 + [_I, _P],
+    "kch_csa_cache_append": [_P, _L] + [_P] * 11 + [_I] * 8 + [_P],
+    "kch_hca_cache_append": [_P, _L] + [_P] * 6 + [_I] * 7 + [_P],
+    "kch_csa_decode_dyn": [_P, _L] * 7 + [_P, _I, _I, _I, _P, _P, _P] + [_I] * 6 + [_F, _F]
+                          + [_I] * 5 + [_P, _SZ, _P],
+    "kch_hca_decode_dyn": [_P, _L] * 3 + [_P, _I, _I, _I, _P, _P, _I, _I, _I, _F, _I, _I, _I,
+                                          _P, _SZ, _P],
 }
 
 # name -> (return type, argument types) of the entry points that return a value
 _QUERIES = {
     "kch_kda_chunk_ws_bytes": (_SZ, [_I] * 7),
     "kch_decode_ws_bytes": (_SZ, [_I] * 7),
+    "kch_decode_dyn_ws_bytes": (_SZ, [_I] * 7),
 }
 
 EXPORTED = ["kch_abi_version", "kch_last_error"] + sorted(_SIGNATURES) + sorted(_QUERIES)

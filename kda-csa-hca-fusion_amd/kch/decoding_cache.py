@@ -270,7 +270,8 @@ class CSADecodingCache:
         self._acc = None          # 6 buffers [B, m, width] (projection dtype)
         self._acc_buf = None      # the buffer they are views of, if one
         self._acc_len = 0
-        self._prev = None         # (Cb, Zb) of the last completed block, [B, m, c]
+        self._prev = None         # (Cb, Zb) of the last completed block, [B, m, c]:
+        self._prev_buf = None     # views of one [B, m, 2c] buffer at a fixed address
         self._C = _BlockStore(self.B, self.c, self.device, self.dtype, torch.bfloat16)
         # indexer keys: the stored rows and their inverse norms (no normalised copy)
         self._K = _BlockStore(self.B, self.c_I, self.device, self.dtype, None)
@@ -314,8 +315,8 @@ class CSADecodingCache:
             self._acc = list(self._acc_buf.split([a.shape[-1] for a in self._acc], -1))
         elif self._acc is not None:
             self._acc = [a.to(device=self.device) for a in self._acc]
-        if self._prev is not None:
-            self._prev = tuple(p.to(device=self.device) for p in self._prev)
+        if self._prev_buf is not None:
+            self._set_prev_buf(self._prev_buf.to(device=self.device))
         self._C.to(self.device, self.dtype, self._n_blocks)
         self._K.to(self.device, self.dtype, self._n_blocks)
         if self._sw is not None:
@@ -373,7 +374,11 @@ class CSADecodingCache:
                 self._K.push(self._n_blocks, krows, self._normalize_qk)
                 out_idx = list(range(self._n_blocks, self._n_blocks + nfull))
                 self._n_blocks += nfull
-                self._prev = (Cb[:, -self.m:].clone(), Zb[:, -self.m:].clone())
+                if self._prev_buf is None or self._prev_buf.dtype != Cb.dtype:
+                    self._set_prev_buf(torch.empty(B, self.m, 2 * c, device=Cb.device,
+                                                   dtype=Cb.dtype))
+                self._prev[0].copy_(Cb[:, -self.m:])
+                self._prev[1].copy_(Zb[:, -self.m:])
                 for a, x in zip(self._acc, new):
                     if rem:
                         a[:, :rem] = x[:, T_new - rem:].to(a.dtype)
@@ -387,6 +392,48 @@ class CSADecodingCache:
             self._acc_len = rem
             self._n_tokens_seen += T_new
         return out_idx
+
+    def _set_prev_buf(self, buf):
+        self._prev_buf = buf
+        self._prev = (buf[..., :self.c], buf[..., self.c:])
+
+    # ---- device-driven steps (kch_csa_cache_append, kch_csa_decode_dyn) ----
+    def _device_ready(self, dtype) -> bool:
+        """Whether one-token device steps can continue this cache in place: the
+        accumulator is one buffer of the step's dtype (or none yet), and so are
+        the block stores."""
+        if self.dtype != dtype:
+            return False
+        if self._acc is not None and (self._acc_buf is None or self._acc_buf.dtype != dtype):
+            return False
+        return self._prev_buf is None or self._prev_buf.dtype == dtype
+
+    def _device_buffers(self, headroom: int = 1):
+        """Allocate what a device step writes and return the block capacity:
+        room for the block the next token may complete (``headroom`` blocks past
+        the current ones, doubling the storage when it grows)."""
+        B, m, c, cI = self.B, self.m, self.c, self.c_I
+        if self._acc is None:
+            self._acc_buf = torch.empty(B, m, 4 * c + 2 * cI, device=self.device, dtype=self.dtype)
+            self._acc = list(self._acc_buf.split([c, c, c, c, cI, cI], -1))
+        if self._prev_buf is None:
+            self._set_prev_buf(torch.zeros(B, m, 2 * c, device=self.device, dtype=self.dtype))
+        need = max(1, self._n_blocks + headroom)
+        self._C.ensure(self._n_blocks, need)
+        self._K.ensure(self._n_blocks, need)
+        if self._C.key_norm is None:
+            self._C.key_norm = self._normalize_qk
+        return min(self._C.rows.shape[1], self._K.rows.shape[1])
+
+    def _device_advance(self) -> None:
+        """The host counters after one token appended on the device."""
+        n = self._n_tokens_seen
+        if self._sw is not None:
+            self._sw._written += 1
+        if n % self.m == self.m - 1:
+            self._n_blocks += 1
+        self._acc_len = (n + 1) % self.m
+        self._n_tokens_seen = n + 1
 
     def forward_step(self, q, q_idx, w_idx, *, topk, nh, nIh, scale=None, sink_logits=None,
                      use_ste=True, ste_mode='topk_columns', normalize_qk=True,
@@ -596,6 +643,31 @@ class HCADecodingCache:
             self._acc_len = rem
             self._n_tokens_seen += T_new
         return out_idx
+
+    # ---- device-driven steps (kch_hca_cache_append, kch_hca_decode_dyn) ----
+    def _device_ready(self, dtype) -> bool:
+        if self.dtype != dtype:
+            return False
+        return self._acc is None or (self._acc_buf is not None and self._acc_buf.dtype == dtype)
+
+    def _device_buffers(self, headroom: int = 1):
+        B, m2, c = self.B, self.m2, self.c
+        if self._acc is None:
+            self._acc_buf = torch.empty(B, m2, 2 * c, device=self.device, dtype=self.dtype)
+            self._acc = list(self._acc_buf.split([c, c], -1))
+        self._C.ensure(self._n_blocks, max(1, self._n_blocks + headroom))
+        if self._C.key_norm is None:
+            self._C.key_norm = self._normalize_qk
+        return self._C.rows.shape[1]
+
+    def _device_advance(self) -> None:
+        n = self._n_tokens_seen
+        if self._sw is not None:
+            self._sw._written += 1
+        if n % self.m2 == self.m2 - 1:
+            self._n_blocks += 1
+        self._acc_len = (n + 1) % self.m2
+        self._n_tokens_seen = n + 1
 
     def forward_step(self, q, *, nh, scale=None, sink_logits=None, normalize_qk=True,
                      _normalize_q=False, _out_dtype=None):

@@ -37,6 +37,7 @@ from torch.nn.modules import module as _nn_module
 
 from . import _lib
 from .decoding_cache import CSADecodingCache, HCADecodingCache
+from . import ops_csa
 from .ops_csa import naive_csa
 from .ops_hca import naive_hca
 from .ops_kda import _recurrent_launch, kda_recurrent_into
@@ -260,14 +261,17 @@ class _FusedWeightLayer(nn.Module):
     def __init__(self):
         super().__init__()
         self._fused = _FusedWeight()
+        self._fused_step = _FusedWeight()  # the decode step's operands
         self.register_load_state_dict_post_hook(_invalidate_after_load)
 
     def invalidate_weight_cache(self) -> None:
         """Drop the fused weight copies (call after writing parameters through ``.data``)."""
         self._fused.invalidate()
+        self._fused_step.invalidate()
 
     def _apply(self, fn, *args, **kwargs):
         self._fused.invalidate()
+        self._fused_step.invalidate()
         return super()._apply(fn, *args, **kwargs)
 
 
@@ -419,40 +423,6 @@ class KDAHybridLayer(_FusedWeightLayer):
         return out, new_state, new_lookback
 
 
-    def _decode_step_inplace(self, x: torch.Tensor, state: torch.Tensor,
-                             lookback: torch.Tensor) -> torch.Tensor:
-        """One decode token (``x`` ``[B,1,d]``) with the conv lookback ``[B,2,d]`` and
-        the fp32 state ``[B,HV,K,V]`` updated in place: the same launches and
-        values as ``forward_functional`` on one token with that lookback and
-        state, without a new lookback tensor (so that the step can be captured
-        in a graph and replayed on the same buffers)."""
-        B, T, d = x.shape
-        cfg = self.cfg
-        H, K, V, HV = cfg.n_heads_qk, cfg.head_dim_k, cfg.head_dim_v, cfg.n_heads_v
-        code = _lib.dtype_code("KDAHybridLayer", x.dtype)
-        stream = _lib.stream_of(x)
-        W, w, bias, g_up = self._weights(x.dtype, x.device)
-        x_conv = torch.empty_like(x)
-        _lib.call("kch_short_conv", _lib.ptr(x), _lib.ptr(lookback), _lib.ptr(w), _lib.ptr(bias),
-                  _lib.ptr(x_conv), B, T, d, code, stream)
-        # the new lookback: the last two rows of [lookback ; x]
-        lookback[:, 0].copy_(lookback[:, 1])
-        lookback[:, 1].copy_(x[:, 0])
-        proj = _linear(x_conv, W)
-        off_gd = 2 * H * K + HV * V + HV
-        gl = _linear(proj[..., off_gd:off_gd + K], g_up)
-        q = torch.empty(B, T, H, K, device=x.device, dtype=x.dtype)
-        k = torch.empty_like(q)
-        v = torch.empty(B, T, HV, V, device=x.device, dtype=x.dtype)
-        g = torch.empty(B, T, HV, K, device=x.device, dtype=x.dtype)
-        beta = torch.empty(B, T, HV, device=x.device, dtype=x.dtype)
-        _lib.call("kch_kda_gates", _lib.ptr(proj), proj.stride(1), _lib.ptr(gl), gl.stride(1),
-                  _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(beta),
-                  B, T, H, HV, K, V, float(cfg.kda_decay_scale), code, stream)
-        o = _recurrent_launch(q, k, v, g, beta, self._scale_value(), state, state, code, stream)
-        return _linear(o.reshape(B, T, HV * V), self.o_proj.weight)
-
-
 class CSAHybridLayer(_FusedWeightLayer):
     """CSA sub-layer (``ops_fused.py:612-713``): ``naive_csa`` then ``o_proj``."""
 
@@ -483,6 +453,21 @@ class CSAHybridLayer(_FusedWeightLayer):
     @classmethod
     def reset_warned(cls):
         cls._indexer_warned = False
+
+    def _step_weights(self, dtype, device):
+        """Operands of the device-driven decode step: the projection weight
+        [W_aKV; W_bKV; W_aZ; W_bZ; W_KV_idx; W_Z_idx; W_DQ; W_w], the query
+        up-projection [W_UQ; W_IUQ], and fp32 Ba, Bb, B_idx and sink."""
+        proj = [self.W_aKV.weight, self.W_bKV.weight, self.W_aZ.weight, self.W_bZ.weight,
+                self.W_KV_idx.weight, self.W_Z_idx.weight, self.W_DQ.weight, self.W_w.weight]
+        up = [self.W_UQ.weight, self.W_IUQ.weight]
+        small = [self.Ba, self.Bb, self.B_idx, self.sink]
+
+        def build():
+            cat = lambda ps: torch.cat([p.detach() for p in ps], 0).to(device=device, dtype=dtype)  # noqa: E731
+            return (cat(proj), cat(up)) + tuple(
+                p.detach().to(device=device, dtype=torch.float32).contiguous() for p in small)
+        return self._fused_step.get(proj + up + small, dtype, device, build)
 
     def _maybe_warn_indexer(self):
         # only with STE explicitly disabled (ops_fused.py:678-692)
@@ -522,6 +507,18 @@ class HCAHybridLayer(_FusedWeightLayer):
         self.W_UQ = nn.Linear(cfg.hca_dc, c * cfg.hca_nh, bias=False)
         self.sink = nn.Parameter(torch.zeros(cfg.hca_nh))
         self.o_proj = nn.Linear(c * cfg.hca_nh, d, bias=False)
+
+    def _step_weights(self, dtype, device):
+        """Operands of the device-driven decode step: [W_KV; W_Z; W_DQ], W_UQ,
+        and fp32 B_pos and sink."""
+        proj = [self.W_KV.weight, self.W_Z.weight, self.W_DQ.weight]
+        small = [self.B_pos, self.sink]
+
+        def build():
+            W = torch.cat([p.detach() for p in proj], 0).to(device=device, dtype=dtype)
+            return (W, self.W_UQ.weight.detach().to(device=device, dtype=dtype).contiguous()) + \
+                tuple(p.detach().to(device=device, dtype=torch.float32).contiguous() for p in small)
+        return self._fused_step.get(proj + [self.W_UQ.weight] + small, dtype, device, build)
 
     def forward(self, x: torch.Tensor, state: torch.Tensor | None = None):
         cfg = self.cfg
@@ -665,16 +662,15 @@ class HybridKCHAttention(nn.Module):
             return x, self._stack_states(states), new_lookbacks
 
 
-class _DecodeGraphs:
-    """The captured segments of a decode step and what they hold on to."""
+def _pad8(n: int) -> int:
+    return (n + 7) & ~7
 
-    def __init__(self):
-        self.key = None
-        self.params = []
-        self.parts = []
-        self.keep = []
-        self.xin = None
-        self.xout = None
+
+class _StepGraph:
+    """A captured device-driven decode step and the buffers it replays on."""
+
+    def __init__(self, key, graph, xin, xout, idx_bufs):
+        self.key, self.graph, self.xin, self.xout, self.idx_bufs = key, graph, xin, xout, idx_bufs
 
 
 class HybridDecoding(nn.Module):
@@ -691,22 +687,31 @@ class HybridDecoding(nn.Module):
     of 4) with the backend from ``KDA_BACKEND`` (default ``"hip"``). Its head
     dims run zero-padded to the kernels' sizes.
 
-    ``use_graphs`` (default on): a decode step replays HIP graphs of its
-    static parts -- the norms, the KDA layers (conv lookback and state updated
-    in place), the CSA / HCA projections and output projections, the residual
-    adds -- and runs only the cache updates and attention eagerly between
-    them (their block counts and window lengths change every step). The
-    graphs are captured on the first eligible step and captured again when
-    the batch, dtype, a parameter (address or in-place version), the KDA state
-    or lookback buffers or a cache object change. Results are those of the
-    eager step, launch for launch.
+    Decode steps on bf16 models whose sizes the step kernels take run the
+    device-driven step: per sub-layer a norm-fused projection, the KDA
+    front end and fused activation + recurrence kernels, the one-token cache
+    append and the cache attention, and an output projection fused with the
+    residual add, every per-step count (blocks, window, slots) read from one
+    device counter of cached tokens. ``use_graphs`` (default on) captures that
+    step once in a HIP graph and replays it on every later step; the graph is
+    captured again when the batch, a parameter (address or in-place version),
+    a fused weight copy, the KDA state or lookback buffers, or a cache buffer
+    (which grows by doubling) change. Results are the eager step's, launch for
+    launch. ``fused_decode = False`` keeps every step on the per-operator path
+    of ``_forward_csa_layer`` / ``_forward_hca_layer``, as do models with
+    forward hooks on the modules that path calls (the norms, the KDA layers).
     """
 
     def __init__(self, d_model: int = 64, total_layers: int = 5, csa_topk: int = 2, *,
                  cfg: HybridConfig | None = None, use_graphs: bool = True):
         super().__init__()
         self.use_graphs = use_graphs
-        self._graphs = None
+        self.fused_decode = True
+        self._graph = None
+        self._n_dev = None        # device int32 [1]: tokens the caches held before the step
+        self._n_dev_host = None   # the value it holds, None when unknown
+        self._trace = None        # list: per call, the stream entering each sub-layer
+        self._device_steps = 0    # decode steps run on the device-driven kernels
         if cfg is None:
             cfg = HybridConfig(
                 d_model=d_model, n_heads_qk=2, n_heads_v=2, head_dim_k=16, head_dim_v=16,
@@ -724,188 +729,280 @@ class HybridDecoding(nn.Module):
         self.model.reset_state()
         self._csa_caches = [None for _ in self._csa_caches]
         self._hca_caches = [None for _ in self._hca_caches]
-        self._graphs = None
+        self._graph = None
+        self._n_dev_host = None
 
     def _apply(self, fn, *args, **kwargs):
-        self._graphs = None
+        self._graph = None
+        self._n_dev = None
+        self._n_dev_host = None
         return super()._apply(fn, *args, **kwargs)
 
-    # ---------------- graphed decode step ----------------
-    def _graph_eligible(self, x: torch.Tensor, stacked) -> bool:
-        """Every projection of the step on ``kch_linear_rows`` (no BLAS call in a
-        graph), every KDA layer on the recurrent step with a lookback buffer,
-        every cache present, and no forward hook anywhere in the model (a hook
-        must see each step's values; a replay would not call it)."""
-        if not (self.use_graphs and x.is_cuda and x.dtype in (torch.bfloat16, torch.float16)
-                and x.shape[1] == 1 and x.shape[0] <= 16):
+    # ---------------- device-driven decode step ----------------
+    def _called_modules(self):
+        """The modules the per-operator decode step calls as modules (the norms
+        and the KDA layers; the CSA / HCA layers' weights are used directly)."""
+        model = self.model
+        return list(model.norms) + [l for l, k in zip(model.layers, model.layout) if k == 'kda']
+
+    def _caches(self):
+        return self._csa_caches + self._hca_caches
+
+    def _device_step_ok(self, x: torch.Tensor, stacked) -> bool:
+        """Whether this decode step can run on the device-driven kernels."""
+        if not (self.fused_decode and x.is_cuda and x.dtype == torch.bfloat16 and x.dim() == 3
+                and x.shape[1] == 1 and 1 <= x.shape[0] <= 16):
             return False
         if _nn_module._global_forward_hooks or _nn_module._global_forward_pre_hooks \
                 or any(m._forward_hooks or m._forward_pre_hooks for m in self._called_modules()):
             return False
         cfg, model = self.cfg, self.model
-        widths = [cfg.d_model]
-        if model.n_kda_layers:
-            if stacked is None or stacked.shape[1] != x.shape[0]:
-                return False
-            widths += [cfg.head_dim_k, cfg.n_heads_v * cfg.head_dim_v]
-        if 'csa' in model.layout:
-            widths += [cfg.csa_dc, cfg.csa_nh * cfg.csa_c]
-        if 'hca' in model.layout:
-            widths += [cfg.hca_dc, cfg.hca_nh * cfg.hca_c]
-        if any(w % 32 for w in widths):
+        B, d = x.shape[0], cfg.d_model
+        if d % 32 or d > 4096 or B * d > 32768:
             return False
-        for layer, kind in zip(model.layers, model.layout):
-            if kind == 'kda':
-                lb = layer._conv_lookback
-                if lb is None or lb.shape[0] != x.shape[0] or lb.dtype != x.dtype:
-                    return False
-        return all(c is not None for c in self._csa_caches + self._hca_caches)
-
-    def _called_modules(self):
-        """The modules an eager decode step calls as modules (the norms and the
-        KDA layers; the CSA / HCA layers' weights are used directly)."""
-        model = self.model
-        return [model] + list(model.norms) + [l for l, k in zip(model.layers, model.layout)
-                                              if k == 'kda']
-
-    def _graph_key(self, x: torch.Tensor, stacked):
-        g = self._graphs
-        params = g.params if g is not None else list(self.model.parameters())
-        lbs = tuple(id(l._conv_lookback) for l, k in zip(self.model.layers, self.model.layout)
-                    if k == 'kda')
-        return (x.shape, x.dtype, x.device, None if stacked is None else stacked.data_ptr(), lbs,
-                tuple(id(c) for c in self._csa_caches + self._hca_caches),
-                tuple((p.data_ptr(), p._version) for p in params))
-
-    def _capture(self, x: torch.Tensor, stacked):
-        """Capture the step's static segments (nothing is executed) and return
-        the runner: the graphs' replays and the eager cache calls in order."""
-        model = self.model
-        gs = _DecodeGraphs()
-        gs.params = list(model.parameters())
-        # persistent lookback buffers (updated in place by the replays)
-        for layer, kind in zip(model.layers, model.layout):
-            if kind == 'kda':
-                layer._conv_lookback = layer._conv_lookback.contiguous().clone()
-        # fused weights built outside the capture
-        for layer, kind in zip(model.layers, model.layout):
-            if kind == 'kda':
-                layer._weights(x.dtype, x.device)
-        with torch.no_grad():
+        for n in model.norms:
+            if n.weight is None or len(n.normalized_shape) != 1 or \
+                    (n.bias is not None and n.bias.dtype != n.weight.dtype):
+                return False
+        if model.n_kda_layers:
+            H, HV, K, V = cfg.n_heads_qk, cfg.n_heads_v, cfg.head_dim_k, cfg.head_dim_v
+            if stacked is None or tuple(stacked.shape) != (model.n_kda_layers, B, HV, K, V) \
+                    or stacked.dtype != torch.float32 or not stacked.is_contiguous() \
+                    or stacked.device != x.device:
+                return False
+            if K not in (16, 32, 64, 128, 256) or V % 32 or HV % H:
+                return False
             for layer, kind in zip(model.layers, model.layout):
-                if kind == 'csa':
-                    self._project_csa(layer, x)
-                elif kind == 'hca':
-                    self._project_hca(layer, x)
-        torch.cuda.synchronize(x.device)
-        pool = torch.cuda.graph_pool_handle()
-        gs.xin = x.clone()
-        parts, keep, open_ctx = [], [], []
+                if kind != 'kda':
+                    continue
+                lb = layer._conv_lookback
+                if lb is None or tuple(lb.shape) != (B, 2, d) or lb.dtype != x.dtype \
+                        or lb.device != x.device or not lb.is_contiguous() or lb.data_ptr() % 16:
+                    return False
+        if 'csa' in model.layout:
+            c, cI, nIh, nh = cfg.csa_c, cfg.csa_cI, cfg.csa_nIh, cfg.csa_nh
+            if c not in (64, 128) or cI not in (32, 64, 128) or nIh not in (1, 2, 4, 8, 16) \
+                    or nh > 16 or cfg.csa_topk < 1 or cfg.csa_dc % 32 or c + cI > 256:
+                return False
+        if 'hca' in model.layout:
+            if cfg.hca_c not in (64, 128) or cfg.hca_nh > 16 or cfg.hca_dc % 32:
+                return False
+        for cache in self._caches():
+            if cache is None or cache.B != B or cache.device != x.device \
+                    or not cache._device_ready(x.dtype):
+                return False
+        return True
 
-        def open_graph():
-            g = torch.cuda.CUDAGraph()
-            ctx = torch.cuda.graph(g, pool=pool)
-            ctx.__enter__()
-            open_ctx.append(ctx)
-            return g, ctx
+    def _sync_counter(self, device) -> bool:
+        """The device token counter holds the caches' common token count."""
+        caches = self._caches()
+        if not caches:
+            return True
+        n = caches[0].n_tokens_seen
+        if any(c.n_tokens_seen != n for c in caches):
+            return False
+        if self._n_dev is None or self._n_dev.device != device:
+            self._n_dev = torch.zeros(1, device=device, dtype=torch.int32)
+            self._n_dev_host = 0
+        if self._n_dev_host != n:
+            self._n_dev.fill_(n)
+            self._n_dev_host = n
+        return True
 
-        def close_graph(g, ctx):
-            open_ctx.pop()
-            ctx.__exit__(None, None, None)
-            parts.append(g.replay)
-            keep.append(g)
+    def _step_operands(self, dtype, device):
+        """Every operand of the step that is not a parameter itself, built (or
+        taken from the layers' caches) outside any capture."""
+        ops = []
+        for layer, kind in zip(self.model.layers, self.model.layout):
+            ops.append(layer._weights(dtype, device) if kind == 'kda'
+                       else layer._step_weights(dtype, device))
+        return ops
 
-        try:
-            self._capture_segments(gs, stacked, open_graph, close_graph, parts, keep)
-        except BaseException:
-            # end an open capture before the error propagates (a graph destroyed
-            # while its stream still captures aborts the process)
-            for ctx in open_ctx:
-                try:
-                    ctx.__exit__(None, None, None)
-                except Exception:
-                    pass
-            raise
-        gs.parts, gs.keep = parts, keep
-        return gs
+    def _step_key(self, x, stacked, caps, ops):
+        def ptrs(ts):
+            return tuple(0 if t is None else t.data_ptr() for t in ts)
+        model = self.model
+        key = [tuple(x.shape), x.dtype, x.device, ptrs([stacked, self._n_dev]), tuple(caps)]
+        key += [ptrs(op) for op in ops]
+        key += [(p.data_ptr(), p._version) for p in model.parameters()]
+        key += [ptrs([layer._conv_lookback]) for layer, k in zip(model.layers, model.layout)
+                if k == 'kda']
+        for cache in self._caches():
+            key.append(ptrs([None if cache._sw is None else cache._sw._buf, cache._acc_buf,
+                             getattr(cache, '_prev_buf', None), cache._C.rows, cache._C.keys,
+                             getattr(cache, '_K', None) and cache._K.rows,
+                             getattr(cache, '_K', None) and cache._K.inv]))
+        return tuple(key)
 
-    def _capture_segments(self, gs, stacked, open_graph, close_graph, parts, keep):
-        """Norms, KDA layers and projections of the step into graphs, split at
-        each CSA / HCA cache call (an eager part between two graphs)."""
+    def _prepare_caches(self):
+        """Room for the block this token may complete, in every cache; returns
+        the block capacities (the CSA stores share one)."""
+        caps = []
+        for cache in self._caches():
+            cap = cache._device_buffers()
+            if isinstance(cache, CSADecodingCache):
+                # the append kernel addresses both stores with one block stride
+                cap = max(cache._C.rows.shape[1], cache._K.rows.shape[1])
+                cache._C.ensure(cache.n_blocks, cap)
+                cache._K.ensure(cache.n_blocks, cap)
+            caps.append(cap)
+        return caps
+
+    def _device_step(self, x: torch.Tensor, stacked, caps, ops):
+        """One token (``x`` ``[B, 1, d]``) through every sub-layer on the
+        device-driven kernels. Returns the output ``[B, 1, d]`` and the CSA
+        selections ``[B, topk]``; records the sub-layers' inputs when tracing."""
         model, cfg = self.model, self.cfg
-        x = gs.xin
-        B = x.shape[0]
-        kda_idx = csa_idx = hca_idx = 0
-        with torch.no_grad():
-            g, ctx = open_graph()
-            x_cur = gs.xin
-            for layer, norm, kind in zip(model.layers, model.norms, model.layout):
-                residual = x_cur
-                h = norm(x_cur)
-                if kind == 'kda':
-                    o = layer._decode_step_inplace(h, stacked[kda_idx], layer._conv_lookback)
-                    kda_idx += 1
+        B, _, d = x.shape
+        dt, dev = x.dtype, x.device
+        code = _lib.dtype_code("HybridDecoding", dt)
+        stream = _lib.stream_of(x)
+        lib = _lib.load()
+        x_cur = x.reshape(B, d)
+        if x_cur.stride(1) != 1 or x_cur.stride(0) % 8 or x_cur.data_ptr() % 16:
+            x_cur = x_cur.contiguous()
+        n_dev = self._n_dev if self._caches() else None
+        trace = [] if self._trace is not None else None
+        idx_bufs = []
+        csa_i = hca_i = kda_i = 0
+        n_layers = len(model.layers)
+
+        def linear(xin, ldx, w, y, ldy, *, norm=None, res=None, counter=None):
+            ln_w = ln_b = None
+            eps, wcode = 0.0, 0
+            if norm is not None:
+                ln_w, ln_b, eps = norm.weight, norm.bias, float(norm.eps)
+                wcode = _lib.dtype_code("HybridDecoding", ln_w.dtype)
+            N, K = w.shape
+            _lib.call("kch_linear_rows_fused", _lib.ptr(xin), ldx, _lib.ptr(w), K, _lib.ptr(y),
+                      ldy, B, N, K, _lib.ptr(ln_w), _lib.ptr(ln_b), eps, wcode, _lib.ptr(res),
+                      0 if res is None else res.stride(0), _lib.ptr(counter), code, stream)
+            return y
+
+        for li, (layer, norm, kind) in enumerate(zip(model.layers, model.norms, model.layout)):
+            if trace is not None:
+                trace.append(x_cur.view(B, 1, d).clone())
+            counter = n_dev if li == n_layers - 1 else None
+            op = ops[li]
+            if kind == 'kda':
+                H, HV, K, V = cfg.n_heads_qk, cfg.n_heads_v, cfg.head_dim_k, cfg.head_dim_v
+                W, w_conv, b_conv, g_up = op
+                xc = torch.empty(B, d, device=dev, dtype=dt)
+                ln_w, ln_b = norm.weight, norm.bias
+                _lib.call("kch_kda_decode_front", _lib.ptr(x_cur), x_cur.stride(0), _lib.ptr(ln_w),
+                          _lib.ptr(ln_b), float(norm.eps), _lib.ptr(layer._conv_lookback),
+                          _lib.ptr(w_conv), _lib.ptr(b_conv), _lib.ptr(xc), B, d, code,
+                          _lib.dtype_code("HybridDecoding", ln_w.dtype), stream)
+                NP = _pad8(W.shape[0])
+                proj = linear(xc, d, W, torch.empty(B, NP, device=dev, dtype=dt), NP)
+                o = torch.empty(B, HV * V, device=dev, dtype=dt)
+                _lib.call("kch_kda_decode_step", _lib.ptr(proj), NP, _lib.ptr(g_up),
+                          _lib.ptr(stacked[kda_i]), _lib.ptr(o), B, H, HV, K, V,
+                          layer._scale_value(), float(cfg.kda_decay_scale), -10.0, code, stream)
+                kda_i += 1
+            else:
+                csa = kind == 'csa'
+                if csa:
+                    cache = self._csa_caches[csa_i]
+                    cap = caps[csa_i]
+                    c, nh, dc = cfg.csa_c, cfg.csa_nh, cfg.csa_dc
+                    Wp, Wq, Ba, Bb, Bk, sink = op
                 else:
-                    if kind == 'csa':
-                        proj = self._project_csa(layer, h)
-                        cache = self._csa_caches[csa_idx]
-                        width = cfg.csa_nh * cfg.csa_c
-                        csa_idx += 1
-                    else:
-                        proj = self._project_hca(layer, h)
-                        cache = self._hca_caches[hca_idx]
-                        width = cfg.hca_nh * cfg.hca_c
-                        hca_idx += 1
-                    close_graph(g, ctx)
-                    o_core = torch.empty(B, 1, width, device=x.device, dtype=x.dtype)
-                    keep.append((proj, o_core))
-                    parts.append(self._eager_cache_part(kind, layer, cache, proj, o_core))
-                    g, ctx = open_graph()
-                    o = _linear(o_core, layer.o_proj.weight)
-                x_cur = residual + o
-            gs.xout = x_cur
-            close_graph(g, ctx)
-
-    @staticmethod
-    def _eager_cache_part(kind, layer, cache, proj, o_core):
-        """The cache update and decode attention of a CSA / HCA layer, writing
-        its output into the static ``o_core``."""
-        cfg = layer.cfg
-        B = o_core.shape[0]
-
-        def run():
-            with torch.no_grad():
-                if kind == 'csa':
-                    Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx = proj
-                    cache.append_step(Ca, Cb, Za, Zb, K_idx, Z_idx, layer.Ba, layer.Bb,
-                                      layer.B_idx)
-                    o = cache.forward_step(q, q_idx, w_idx, topk=cfg.csa_topk, nh=cfg.csa_nh,
-                                           nIh=cfg.csa_nIh, scale=1.0, sink_logits=layer.sink,
-                                           use_ste=False, normalize_qk=True, _normalize_q=True,
-                                           _out_dtype=o_core.dtype)
+                    cache = self._hca_caches[hca_i]
+                    cap = caps[len(self._csa_caches) + hca_i]
+                    c, nh, dc = cfg.hca_c, cfg.hca_nh, cfg.hca_dc
+                    Wp, Wq, Bpos, sink = op
+                NP, NQ = _pad8(Wp.shape[0]), _pad8(Wq.shape[0])
+                P = linear(x_cur, x_cur.stride(0), Wp, torch.empty(B, NP, device=dev, dtype=dt),
+                           NP, norm=norm)
+                off_cq = 4 * c + 2 * cfg.csa_cI if csa else 2 * c
+                Q = linear(P[:, off_cq:off_cq + dc], NP, Wq,
+                           torch.empty(B, NQ, device=dev, dtype=dt), NQ)
+                sw = cache._sw
+                ring = None if sw is None else sw._buf
+                win = 0 if sw is None else sw.win
+                normalize = int(bool(cache._C.key_norm))
+                out = torch.empty(B, nh * c, device=dev, dtype=dt)
+                if csa:
+                    cI, nIh, topk, m = cfg.csa_cI, cfg.csa_nIh, cfg.csa_topk, cfg.csa_m
+                    _lib.call("kch_csa_cache_append", _lib.ptr(P), NP, _lib.ptr(cache._acc_buf),
+                              _lib.ptr(cache._prev_buf), _lib.ptr(Ba), _lib.ptr(Bb), _lib.ptr(Bk),
+                              _lib.ptr(ring), _lib.ptr(cache._C.rows), _lib.ptr(cache._C.keys),
+                              _lib.ptr(cache._K.rows), _lib.ptr(cache._K.inv), _lib.ptr(n_dev),
+                              B, c, cI, m, win, cap, normalize, code, stream)
+                    nbytes = lib.kch_decode_dyn_ws_bytes(B, cap, nh, c, topk, win, 1)
+                    ws = torch.empty(max(nbytes, 256), device=dev, dtype=torch.uint8)
+                    idx = torch.empty(B, topk, device=dev, dtype=torch.int32)
+                    _lib.call("kch_csa_decode_dyn", _lib.ptr(Q), NQ, _lib.ptr(Q[:, nh * c:]), NQ,
+                              _lib.ptr(P[:, off_cq + dc:]), NP, _lib.ptr(cache._C.keys), cap * c,
+                              _lib.ptr(cache._K.rows), cap * cI, _lib.ptr(cache._K.inv), cap,
+                              _lib.ptr(ring), win * c, _lib.ptr(n_dev), m, win, cap,
+                              _lib.ptr(sink), _lib.ptr(out), _lib.ptr(idx), B, nh, c, nIh, cI,
+                              topk, 1.0, 1.0, 1, 1, code, code, code, _lib.ptr(ws), ws.numel(),
+                              stream)
+                    idx_bufs.append(idx)
+                    csa_i += 1
                 else:
-                    C, Z, q = proj
-                    cache.append_step(C, Z, layer.B_pos)
-                    o = cache.forward_step(q, nh=cfg.hca_nh, scale=1.0, sink_logits=layer.sink,
-                                           _normalize_q=True, _out_dtype=o_core.dtype)
-                o_core.copy_(o.reshape(B, 1, -1))
-        return run
+                    m2 = cfg.hca_m2
+                    _lib.call("kch_hca_cache_append", _lib.ptr(P), NP, _lib.ptr(cache._acc_buf),
+                              _lib.ptr(Bpos), _lib.ptr(ring), _lib.ptr(cache._C.rows),
+                              _lib.ptr(cache._C.keys), _lib.ptr(n_dev), B, c, m2, win, cap,
+                              normalize, code, stream)
+                    nbytes = lib.kch_decode_dyn_ws_bytes(B, cap, nh, c, 0, win, 0)
+                    ws = torch.empty(max(nbytes, 256), device=dev, dtype=torch.uint8)
+                    _lib.call("kch_hca_decode_dyn", _lib.ptr(Q), NQ, _lib.ptr(cache._C.keys),
+                              cap * c, _lib.ptr(ring), win * c, _lib.ptr(n_dev), m2, win, cap,
+                              _lib.ptr(sink), _lib.ptr(out), B, nh, c, 1.0, 1, code, code,
+                              _lib.ptr(ws), ws.numel(), stream)
+                    hca_i += 1
+                o = out
+            x_cur = linear(o, o.stride(0), layer.o_proj.weight,
+                           torch.empty(B, d, device=dev, dtype=dt), d, res=x_cur,
+                           counter=counter)
+        return x_cur.view(B, 1, d), idx_bufs, trace
 
-    def _forward_graphed(self, x: torch.Tensor, stacked) -> torch.Tensor | None:
-        """The decode step through graphs, or None when it is not eligible."""
-        if not self._graph_eligible(x, stacked):
+    def _after_device_step(self, idx_bufs, B) -> None:
+        """Host bookkeeping of a device step: the caches' counters, the
+        selections for ``record_selections``."""
+        self._device_steps += 1
+        for cache in self._caches():
+            cache._device_advance()
+        if self._caches():
+            self._n_dev_host += 1
+        for cache, idx in zip(self._csa_caches, idx_bufs):
+            cache._last_indices = idx
+            if ops_csa._selection_log is not None:
+                ops_csa._log_selection(idx.clone().view(B, 1, -1))
+
+    def _forward_device(self, x: torch.Tensor, stacked) -> torch.Tensor | None:
+        """The decode step on the device-driven kernels (from the captured graph
+        when allowed), or None when the step does not qualify."""
+        if not self._device_step_ok(x, stacked) or not self._sync_counter(x.device):
             return None
-        key = self._graph_key(x, stacked)
-        gs = self._graphs
-        if gs is None or gs.key != key:
-            self._graphs = None
-            gs = self._capture(x, stacked)
-            gs.key = self._graph_key(x, stacked)  # after the lookback buffers were replaced
-            self._graphs = gs
-        gs.xin.copy_(x)
-        for part in gs.parts:
-            part()
-        return gs.xout.clone()
+        caps = self._prepare_caches()
+        ops = self._step_operands(x.dtype, x.device)
+        B = x.shape[0]
+        with torch.no_grad():
+            if self.use_graphs and self._trace is None and ops_csa._selection_log is None:
+                key = self._step_key(x, stacked, caps, ops)
+                g = self._graph
+                if g is None or g.key != key:
+                    self._graph = None
+                    xin = x.contiguous().clone()
+                    torch.cuda.synchronize(x.device)
+                    graph = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(graph):
+                        y, idx_bufs, _ = self._device_step(xin, stacked, caps, ops)
+                    g = self._graph = _StepGraph(key, graph, xin, y, idx_bufs)
+                g.xin.copy_(x)
+                g.graph.replay()
+                y, idx_bufs = g.xout.clone(), g.idx_bufs
+            else:
+                y, idx_bufs, trace = self._device_step(x, stacked, caps, ops)
+                if trace is not None:
+                    self._trace.append(trace)
+        self._after_device_step(idx_bufs, B)
+        return y
 
     def _ensure_csa_cache(self, idx: int, layer: CSAHybridLayer, h: torch.Tensor):
         cfg = layer.cfg
@@ -1011,7 +1108,7 @@ class HybridDecoding(nn.Module):
             stacked = stacked.to(device=x.device, dtype=torch.float32).contiguous()
         if not fresh and x.shape[1] == 1:
             model._kda_state = stacked
-            y = self._forward_graphed(x, stacked)
+            y = self._forward_device(x, stacked)
             if y is not None:
                 return y
         if model.n_kda_layers > 0 and fresh:
@@ -1020,8 +1117,11 @@ class HybridDecoding(nn.Module):
             stacked = torch.zeros(model.n_kda_layers, B, cfg.n_heads_v, cfg.head_dim_k,
                                   cfg.head_dim_v, device=x.device, dtype=torch.float32)
         kda_idx = csa_idx = hca_idx = 0
+        trace = [] if self._trace is not None else None
         with torch.no_grad():
             for layer, norm, kind in zip(model.layers, model.norms, model.layout):
+                if trace is not None:
+                    trace.append(x.clone())
                 residual = x
                 h = norm(x)
                 if kind == 'kda':
@@ -1036,6 +1136,8 @@ class HybridDecoding(nn.Module):
                     hca_idx += 1
                 x = residual + o
             model._kda_state = stacked if model.n_kda_layers > 0 else None
+        if trace is not None:
+            self._trace.append(trace)
         return x
 
 

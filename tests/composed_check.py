@@ -86,18 +86,26 @@ def decode_vs_oracle(dec, oracle, x, T0, dtype_name):
     """Prefill ``x[:, :T0]`` then one token at a time; at every call each HIP
     sub-layer is checked against the teacher-forced oracle (fed the same
     residual stream, keeping its own KDA states and caches from those inputs,
-    with the CSA layer on the HIP selection), every element at the bar."""
+    with the CSA layer on the HIP selection), every element at the bar. The
+    stream entering each sub-layer comes from the decoder's own trace
+    (``dec._trace``), so each step runs on the path it takes without the
+    check: the device-driven step kernels wherever they apply. Returns the
+    number of decode steps that ran on them."""
     import kch
     xn = x.float().cpu().numpy()
     pos = dec.model.layout.index("csa")
-    cap = LayerInputs(dec.model)
+    dec._trace = []
+    steps0 = dec._device_steps
     try:
         for a, b in [(0, T0)] + [(t, t + 1) for t in range(T0, x.shape[1])]:
             with kch.record_selections() as sel:
                 y = dec(x[:, a:b])
             assert len(sel) == 1
+            assert len(dec._trace) == 1
+            layer_in = [t.float().cpu().numpy() for t in dec._trace.pop()]
             outs = oracle.step(xn[:, a:b], csa_indices={pos: host_sel(sel[0])},
-                               layer_inputs=cap.get())
-            check_layers(f"{dtype_name} [{a}:{b}]", cap.get(), y, outs)
+                               layer_inputs=layer_in)
+            check_layers(f"{dtype_name} [{a}:{b}]", layer_in, y, outs)
     finally:
-        cap.remove()
+        dec._trace = None
+    return dec._device_steps - steps0

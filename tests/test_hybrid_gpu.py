@@ -217,17 +217,22 @@ def test_hybrid_decoding_incremental_equals_full(dev, topk):
     assert dec._hca_caches[0].n_blocks == 140 // cfg.hca_m2
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_hybrid_decoding_vs_oracle(dev, dtype):
+@pytest.mark.parametrize("dtype,fused", [(torch.float32, True), (torch.bfloat16, True),
+                                         (torch.bfloat16, False)])
+def test_hybrid_decoding_vs_oracle(dev, dtype, fused):
+    """Decode steps across CSA (m=4) and HCA (m'=16, at t=79) block completions;
+    bf16 steps run on the device-driven kernels unless ``fused_decode`` is off."""
     import kch
     cfg = small_cfg()
     model, sd = build(cfg, dev, dtype, seed=4)
     dec = kch.HybridDecoding(cfg=cfg, total_layers=5)
     dec.model = model
+    dec.fused_decode = fused
     oracle = OH.HybridDecodingOracle(sd, cfg_dict(cfg), model.layout, DT[dtype])
     rng = np.random.default_rng(11)
-    x = torch.from_numpy(rng.standard_normal((2, 75, cfg.d_model)).astype(np.float32)).to(dev, dtype)
-    decode_vs_oracle(dec, oracle, x, 67, DT[dtype])
+    x = torch.from_numpy(rng.standard_normal((2, 82, cfg.d_model)).astype(np.float32)).to(dev, dtype)
+    n_dev = decode_vs_oracle(dec, oracle, x, 67, DT[dtype])
+    assert n_dev == (15 if fused and dtype == torch.bfloat16 else 0)
 
 
 def test_hybrid_padding_no_crash(dev):
@@ -241,19 +246,21 @@ def test_hybrid_padding_no_crash(dev):
             assert y.shape == x.shape and bool(torch.isfinite(y).all())
 
 
-@pytest.mark.parametrize("hv", [2, 4])
-def test_hybrid_decoding_bf16_single_sequence(dev, hv):
+@pytest.mark.parametrize("hv,fused", [(2, False), (4, False), (2, True), (4, True)])
+def test_hybrid_decoding_bf16_single_sequence(dev, hv, fused):
     """B=1 bf16 decode: the KDA gate input is a column slice of the fused
     projection that starts 2HK+HV*V+HV elements into the row; with one row and
     HV % 8 != 0 it is contiguous but not 16-byte aligned, so the few-row
-    projection must copy it into fresh storage."""
+    projection of the per-operator path must copy it into fresh storage (the
+    device-driven step reads it in place)."""
     import kch
     cfg = small_cfg(n_heads_v=hv)
     model, sd = build(cfg, dev, torch.bfloat16, seed=6)
     dec = kch.HybridDecoding(cfg=cfg, total_layers=5)
     dec.model = model
+    dec.fused_decode = fused
     oracle = OH.HybridDecodingOracle(sd, cfg_dict(cfg), model.layout, 'bf16')
     rng = np.random.default_rng(12 + hv)
     x = torch.from_numpy(rng.standard_normal((1, 40, cfg.d_model)).astype(np.float32)).to(
         dev, torch.bfloat16)
-    decode_vs_oracle(dec, oracle, x, 34, "bf16 B1")
+    assert decode_vs_oracle(dec, oracle, x, 34, "bf16 B1") == (6 if fused else 0)

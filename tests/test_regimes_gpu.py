@@ -149,4 +149,5 @@ def test_hybrid_decoding_config4_shapes(dev):
     x = torch.randn(1, T0 + steps, cfg.d_model,
                     generator=torch.Generator().manual_seed(32)).to(dev, torch.bfloat16)
     oracle = OH.HybridDecodingOracle(sd, cfgd, dec.model.layout, "bf16")
-    decode_vs_oracle(dec, oracle, x, T0, "C4 HybridDecoding")
+    # every decode step on the device-driven kernels
+    assert decode_vs_oracle(dec, oracle, x, T0, "C4 HybridDecoding") == steps
