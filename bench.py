@@ -387,15 +387,21 @@ def bench_hybrid(dev, T=16384, B=2, n_decode=256):
     for i in range(n_untimed):
         y = dec(xs[i])
     e2.record(stream)
+    captures = dec._graph_captures
+    h0 = time.perf_counter()
     for i in range(n_untimed, n_untimed + n_decode):
         y = dec(xs[i])
     e3.record(stream)
+    h1 = time.perf_counter()
     torch.cuda.synchronize()
+    captures = dec._graph_captures - captures
     assert bool(torch.isfinite(y).all())
     pre_ms, dec_ms = e0.elapsed_time(e1), e2.elapsed_time(e3)
     return {"B": B, "T": T, "layout": dec.model.layout_str(), "prefill_ms": pre_ms,
             "prefill_tokens_per_s": B * T / (pre_ms * 1e-3), "decode_steps": n_decode,
-            "decode_untimed_steps": n_untimed, "decode_graph": dec._graph is not None, "decode_device_steps": dec._device_steps,
+            "decode_untimed_steps": n_untimed, "decode_device_steps": dec._device_steps,
+            "decode_graph_captures_timed": captures,
+            "decode_host_ms_per_step": 1e3 * (h1 - h0) / n_decode,
             "decode_ms_per_step": dec_ms / n_decode,
             "decode_tokens_per_s": B * n_decode / (dec_ms * 1e-3)}
 

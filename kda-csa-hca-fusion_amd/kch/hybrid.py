@@ -667,10 +667,21 @@ def _pad8(n: int) -> int:
 
 
 class _StepGraph:
-    """A captured device-driven decode step and the buffers it replays on."""
+    """A captured device-driven decode step, the buffers it replays on, and
+    what a later step checks before replaying it: the input's shape, the
+    tensors and caches it was captured on, every parameter's storage and
+    in-place version, the fused weight copies, the modules whose hooks would
+    send the step elsewhere, and the caches' block capacities."""
 
     def __init__(self, key, graph, xin, xout, idx_bufs):
         self.key, self.graph, self.xin, self.xout, self.idx_bufs = key, graph, xin, xout, idx_bufs
+        self.stacked = None
+        self.model = None
+        self.watch = ()       # (param, data_ptr, _version)
+        self.fused = ()       # (_FusedWeight, the copy it held at capture)
+        self.lookbacks = ()   # (layer, lookback tensor)
+        self.caches = ()      # (cache, its buffers, block capacity)
+        self.hook_modules = ()
 
 
 class HybridDecoding(nn.Module):
@@ -712,6 +723,7 @@ class HybridDecoding(nn.Module):
         self._n_dev_host = None   # the value it holds, None when unknown
         self._trace = None        # list: per call, the stream entering each sub-layer
         self._device_steps = 0    # decode steps run on the device-driven kernels
+        self._graph_captures = 0
         if cfg is None:
             cfg = HybridConfig(
                 d_model=d_model, n_heads_qk=2, n_heads_v=2, head_dim_k=16, head_dim_v=16,
@@ -828,10 +840,7 @@ class HybridDecoding(nn.Module):
         key += [ptrs([layer._conv_lookback]) for layer, k in zip(model.layers, model.layout)
                 if k == 'kda']
         for cache in self._caches():
-            key.append(ptrs([None if cache._sw is None else cache._sw._buf, cache._acc_buf,
-                             getattr(cache, '_prev_buf', None), cache._C.rows, cache._C.keys,
-                             getattr(cache, '_K', None) and cache._K.rows,
-                             getattr(cache, '_K', None) and cache._K.inv]))
+            key.append(ptrs(self._cache_bufs(cache)))
         return tuple(key)
 
     def _prepare_caches(self):
@@ -974,9 +983,63 @@ class HybridDecoding(nn.Module):
             if ops_csa._selection_log is not None:
                 ops_csa._log_selection(idx.clone().view(B, 1, -1))
 
+    @staticmethod
+    def _cache_bufs(cache):
+        K = getattr(cache, '_K', None)
+        return (None if cache._sw is None else cache._sw._buf, cache._acc_buf,
+                getattr(cache, '_prev_buf', None), cache._C.rows, cache._C.keys,
+                None if K is None else K.rows, None if K is None else K.inv)
+
+    def _graph_still_valid(self, g: _StepGraph, x: torch.Tensor, stacked) -> bool:
+        """Whether the captured step replays correctly for this step (cheap
+        checks of everything it was captured on); otherwise the full path
+        re-checks, re-synchronises and captures again."""
+        if not (self.use_graphs and self.fused_decode and self._trace is None
+                and ops_csa._selection_log is None):
+            return False
+        if x.shape != g.xin.shape or x.dtype != g.xin.dtype or x.device != g.xin.device \
+                or stacked is not g.stacked or self.model is not g.model:
+            return False
+        if _nn_module._global_forward_hooks or _nn_module._global_forward_pre_hooks:
+            return False
+        for m in g.hook_modules:
+            if m._forward_hooks or m._forward_pre_hooks:
+                return False
+        for p, ptr, ver in g.watch:
+            if p._version != ver or p.data_ptr() != ptr:
+                return False
+        for fw, w in g.fused:
+            if fw._w is not w:
+                return False
+        for layer, lb in g.lookbacks:
+            if layer._conv_lookback is not lb:
+                return False
+        caches = self._caches()
+        if len(caches) != len(g.caches):
+            return False
+        n = self._n_dev_host
+        for cache, (c0, bufs, cap) in zip(caches, g.caches):
+            if cache is not c0 or cache.n_tokens_seen != n:
+                return False
+            m = cache.m if isinstance(cache, CSADecodingCache) else cache.m2
+            if n // m >= cap:
+                return False  # the block this token completes needs more room
+            for a, b in zip(self._cache_bufs(cache), bufs):
+                if a is not b:
+                    return False
+        return True
+
     def _forward_device(self, x: torch.Tensor, stacked) -> torch.Tensor | None:
         """The decode step on the device-driven kernels (from the captured graph
         when allowed), or None when the step does not qualify."""
+        g = self._graph
+        if g is not None and self._graph_still_valid(g, x, stacked):
+            with torch.no_grad():
+                g.xin.copy_(x)
+                g.graph.replay()
+                y = g.xout.clone()
+            self._after_device_step(g.idx_bufs, x.shape[0])
+            return y
         if not self._device_step_ok(x, stacked) or not self._sync_counter(x.device):
             return None
         caps = self._prepare_caches()
@@ -994,6 +1057,19 @@ class HybridDecoding(nn.Module):
                     with torch.cuda.graph(graph):
                         y, idx_bufs, _ = self._device_step(xin, stacked, caps, ops)
                     g = self._graph = _StepGraph(key, graph, xin, y, idx_bufs)
+                    self._graph_captures += 1
+                    model = self.model
+                    g.stacked = stacked
+                    g.model = model
+                    g.watch = tuple((p, p.data_ptr(), p._version) for p in model.parameters())
+                    g.fused = tuple((layer._fused if k == 'kda' else layer._fused_step,
+                                     ops[i]) for i, (layer, k) in
+                                    enumerate(zip(model.layers, model.layout)))
+                    g.lookbacks = tuple((layer, layer._conv_lookback) for layer, k in
+                                        zip(model.layers, model.layout) if k == 'kda')
+                    g.caches = tuple((cache, self._cache_bufs(cache), cap)
+                                     for cache, cap in zip(self._caches(), caps))
+                    g.hook_modules = tuple(self._called_modules())
                 g.xin.copy_(x)
                 g.graph.replay()
                 y, idx_bufs = g.xout.clone(), g.idx_bufs
