@@ -561,16 +561,29 @@ namespace {
 // Workspace plan of a decode step (kch_csa_decode / kch_hca_decode).
 struct DecodePlan {
   int rb = 0, nr = 0;             // indexer ranges (sparse with blocks and topk > 0)
+  bool split = false;             // score / select split: off_keys holds [B, ko] keys
+  long long ko = 0;
+  size_t off_keys = 0;
   int na = 0, ngrp = 0, grows = 0;  // attended rows before the ring, row groups, rows per group
   size_t off_cand = 0, off_idx = 0, off_po = 0, off_pml = 0, bytes = 0;
 };
 
 size_t a256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-DecodePlan decode_plan(int B, int nb, int nh, int hd, int topk, int ring_len, bool sparse) {
+DecodePlan decode_plan(int B, int nb, int nh, int hd, int topk, int ring_len, bool sparse,
+                       bool one_range = false) {
   DecodePlan pl;
   const bool sel = sparse && nb > 0 && topk > 0;
   if (sel) kch::decode_idx_plan(B, nb, topk, &pl.rb, &pl.nr);
+  if (sel && one_range && nb <= kch::decode_range_max() &&
+      kch::decode_select_lds(topk) <= 160 * 1024) {
+    // a device-driven step's capacity: ranges of 256 blocks write their logit
+    // keys, one workgroup per sequence selects from all of them (no merge)
+    pl.split = true;
+    pl.rb = 256;
+    pl.nr = (nb + 255) / 256;
+    pl.ko = (nb + 3) & ~3;
+  }
   pl.na = sparse ? (sel ? topk : 0) : nb;
   const long long rows = (long long)pl.na + ring_len;
   // row groups (one workgroup each): about 768 over the batch (three resident
@@ -583,8 +596,10 @@ DecodePlan decode_plan(int B, int nb, int nh, int hd, int topk, int ring_len, bo
   pl.grows = (int)grows;
   pl.ngrp = rows > 0 ? (int)((rows + grows - 1) / grows) : 0;
   size_t off = 0;
+  pl.off_keys = off;
+  if (pl.split) off += a256((size_t)B * pl.ko * 4);
   pl.off_cand = off;
-  if (sel && pl.nr > 1) off += a256((size_t)B * pl.nr * topk * 8);
+  if (sel && pl.nr > 1 && !pl.split) off += a256((size_t)B * pl.nr * topk * 8);
   pl.off_idx = off;
   if (sel) off += a256((size_t)B * topk * 4);
   pl.off_po = off;
@@ -718,7 +733,7 @@ int kch_hca_decode(const void* q, const void* kv_comp, long long kv_bstride, con
 
 size_t kch_decode_dyn_ws_bytes(int B, int cap, int nh, int hd, int topk, int win, int sparse) {
   if (B <= 0 || cap < 1 || nh < 1 || hd < 1 || topk < 0 || win < 0) return 0;
-  return decode_plan(B, cap, nh, hd, topk, win, sparse != 0).bytes;
+  return decode_plan(B, cap, nh, hd, topk, win, sparse != 0, true).bytes;
 }
 
 int kch_csa_decode_dyn(const void* q, long long ld_q, const void* q_idx, long long ld_qidx,
@@ -743,13 +758,13 @@ int kch_csa_decode_dyn(const void* q, long long ld_q, const void* q_idx, long lo
   if (ld_q < (long long)nh * hd || ld_qidx < (long long)nIh * cI || (w_idx && ld_w < nIh))
     return fail(KCH_ERR_INVALID, "%s: query row strides too small", fn);
   if (B == 0) return KCH_OK;
-  const DecodePlan pl = decode_plan(B, cap, nh, hd, topk, win, true);
+  const DecodePlan pl = decode_plan(B, cap, nh, hd, topk, win, true, true);
   if (!ws || ws_bytes < pl.bytes)
     return fail(KCH_ERR_INVALID, "%s: workspace of %zu bytes required", fn, pl.bytes);
   if ((uintptr_t)ws & 255) return fail(KCH_ERR_INVALID, "%s: workspace must be 256-byte aligned", fn);
   if (!q || !q_idx || !kv_comp || !k_rows || !out || !idx_out || !n_seen || (win > 0 && !ring))
     return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
-  if (pl.nr > 1 && !kch::decode_merge_fits(topk))
+  if (pl.nr > 1 && !pl.split && !kch::decode_merge_fits(topk))
     return fail(KCH_ERR_UNSUPPORTED, "%s: cap=%d blocks with topk=%d exceed the merge capacity", fn,
                 cap, topk);
   if (!kch::decode_idx_fits(pl.rb, topk, pl.nr))
@@ -766,6 +781,10 @@ int kch_csa_decode_dyn(const void* q, long long ld_q, const void* q_idx, long lo
   ip.normalize_q = normalize_qidx; ip.scale = idx_scale;
   ip.ld_qb = ld_qidx; ip.ld_wb = ld_w;
   ip.n_seen = n_seen; ip.m = m; ip.cap = cap;
+  if (pl.split) {
+    ip.keys_out = (uint32_t*)(w + pl.off_keys);
+    ip.ko_bstride = pl.ko;
+  }
   rc = hip_status(fn, kch::decode_idx_dispatch(ip, qdtype, kdtype, s));
   if (rc) return rc;
   DynStep dyn;
@@ -786,7 +805,7 @@ int kch_hca_decode_dyn(const void* q, long long ld_q, const void* kv_comp, long 
   if (m2 < 1 || win < 0 || cap < 1) return fail(KCH_ERR_INVALID, "%s: bad m2 / win / cap", fn);
   if (ld_q < (long long)nh * hd) return fail(KCH_ERR_INVALID, "%s: query row stride too small", fn);
   if (B == 0) return KCH_OK;
-  const DecodePlan pl = decode_plan(B, cap, nh, hd, 0, win, false);
+  const DecodePlan pl = decode_plan(B, cap, nh, hd, 0, win, false, true);
   if (!ws || ws_bytes < pl.bytes)
     return fail(KCH_ERR_INVALID, "%s: workspace of %zu bytes required", fn, pl.bytes);
   if ((uintptr_t)ws & 255) return fail(KCH_ERR_INVALID, "%s: workspace must be 256-byte aligned", fn);

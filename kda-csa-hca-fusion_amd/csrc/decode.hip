@@ -19,6 +19,11 @@
 //   (reg_select) to the values at or above it (about 2 topk of them), all
 //   values when the estimate misses. One range per sequence: sorted and final; otherwise the range's
 //   top-k are candidates.
+//   With keys_out the range only writes its logit keys there (score pass of
+//   a score / select split).
+// idx_select_kernel  the top-k of all logit keys of a sequence (at most
+//   RB_MAX, held in LDS): radix select over the ordered 64-bit values, gather,
+//   rank sort; output sorted, -1 padded.
 // idx_merge_kernel   the top-k of the candidates of all ranges of a sequence
 //   (a global top-k lies in the union of the per-range top-ks), by the same
 //   estimate-gather-select over the candidates streamed from global memory;
@@ -117,7 +122,7 @@ struct Sel64 {
 // and the search stops as soon as the boundary digit holds exactly the values
 // still needed (at the latest when one value is left). hist: 256 words,
 // scratch: 12 ints.
-template <typename ValF>
+template <int SPLIT = 1, typename ValF>
 __device__ Sel64 block_select64(ValF val, int n, int topk, uint32_t* hist, int* scratch) {
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   u64 a = ~0ull, o = 0ull;
@@ -148,16 +153,23 @@ __device__ Sel64 block_select64(ValF val, int n, int topk, uint32_t* hist, int* 
     const int w = lo_bit < 8 ? lo_bit : 8;
     const int shift = lo_bit - w;
     const uint32_t dm = (1u << w) - 1u;
-    hist[tid] = 0u;
+#pragma unroll
+    for (int w2 = 0; w2 < SPLIT; ++w2) hist[256 * w2 + tid] = 0u;
     __syncthreads();
+    // SPLIT > 1: wave w counts into copy w % SPLIT (fewer colliding atomics)
+    uint32_t* hw = hist + 256 * (wave % SPLIT);
     for (int i = tid; i < n; i += 256) {
       const u64 v = val(i);
-      if ((v & mask) == thr) atomicAdd(&hist[(uint32_t)(v >> shift) & dm], 1u);
+      if ((v & mask) == thr) atomicAdd(&hw[(uint32_t)(v >> shift) & dm], 1u);
     }
     __syncthreads();
     // thread t: digit dm - t (descending); count of values in larger digits
     const int bin = (int)dm - tid;
-    const int c = bin >= 0 ? (int)hist[bin] : 0;
+    int c = 0;
+    if (bin >= 0) {
+#pragma unroll
+      for (int w2 = 0; w2 < SPLIT; ++w2) c += (int)hist[256 * w2 + bin];
+    }
     const int cum = block_excl_scan(c, scratch + 16);
     if (bin >= 0 && cum < need && cum + c >= need) {
       scratch[20] = bin;
@@ -417,20 +429,98 @@ __device__ void block_sort_desc(u64* s, int cnt) {
   }
 }
 
+// Bitonic sort, descending, of the cnt values s[0 .. cnt) padded with zeros to
+// P = 256 EPT (zeros rank below every value); out(rank, v) for each value.
+// Wave w holds positions 64 EPT w .. + 64 EPT - 1 in registers, lane l the EPT
+// consecutive ones from 64 EPT w + EPT l: stages whose partner distance is
+// below EPT compare within the lane, those below 64 EPT exchange by lane
+// shuffles, and only the last stages of the two largest merges go through s
+// (which holds P words).
+template <int EPT, typename OutF>
+__device__ void block_bitonic_desc(u64* s, int cnt, OutF out) {
+  constexpr int P = 256 * EPT, WCH = 64 * EPT;
+  constexpr int LOGP = EPT == 1 ? 8 : (EPT == 2 ? 9 : 10);
+  static_assert((1 << LOGP) == P, "EPT in {1, 2, 4}");
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int base = wave * WCH + EPT * lane;
+  u64 x[EPT];
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) x[e] = base + e < cnt ? s[base + e] : 0ull;
+  // constant trip counts: every stage unrolled, x indexed by constants
+#pragma unroll
+  for (int kk = 1; kk <= LOGP; ++kk) {
+    const int k = 1 << kk;
+#pragma unroll
+    for (int jj = kk - 1; jj >= 0; --jj) {
+      const int j = 1 << jj;
+      // position p keeps the larger of the pair when it is the lower one of a
+      // descending run or the upper one of an ascending run
+      if (j >= WCH) {
+        __syncthreads();  // every read of s by the previous stage is done
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) s[base + e] = x[e];
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) {
+          const int p = base + e;
+          const u64 y = s[p ^ j];
+          const bool keep_max = ((p & j) == 0) == ((p & k) == 0);
+          x[e] = keep_max ? (x[e] > y ? x[e] : y) : (x[e] < y ? x[e] : y);
+        }
+      } else if (j >= EPT) {
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) {
+          const int p = base + e;
+          const u64 y = shfl_xor64(x[e], j / EPT);
+          const bool keep_max = ((p & j) == 0) == ((p & k) == 0);
+          x[e] = keep_max ? (x[e] > y ? x[e] : y) : (x[e] < y ? x[e] : y);
+        }
+      } else {
+        u64 nx[EPT];
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) {
+          const int p = base + e;
+          const u64 y = x[e ^ j];
+          const bool keep_max = ((p & j) == 0) == ((p & k) == 0);
+          nx[e] = keep_max ? (x[e] > y ? x[e] : y) : (x[e] < y ? x[e] : y);
+        }
+#pragma unroll
+        for (int e = 0; e < EPT; ++e) x[e] = nx[e];
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < EPT; ++e)
+    if (base + e < cnt) out(base + e, x[e]);
+}
+
 // Sorts the cnt selected values s[0 .. cnt) descending and writes their block
 // indices to out[0 .. topk), -1 past cnt. s holds pow2_at_least(cnt + 1)
-// words, 16-byte aligned.
+// words, 16-byte aligned. BITONIC: a bitonic network for 256 < cnt <= 1024
+// (where s has room for its padding); kernels held to 128 VGPRs keep the rank
+// count, whose registers they can afford.
+template <bool BITONIC>
 __device__ void write_sorted(u64* s, int cnt, int topk, int* out) {
   const int tid = threadIdx.x;
   for (int i = cnt + tid; i < topk; i += 256) out[i] = -1;
+  auto put_idx = [&](int rank, u64 v) { out[rank] = kv64_index(v); };
+  if constexpr (BITONIC) {
+    if (cnt > 256 && cnt <= 512) {
+      block_bitonic_desc<2>(s, cnt, put_idx);
+      return;
+    }
+    if (cnt > 512 && cnt <= 1024) {
+      block_bitonic_desc<4>(s, cnt, put_idx);
+      return;
+    }
+  }
   if (cnt <= 2048) {
     if (tid == 0 && (cnt & 1)) s[cnt] = 0ull;
     __syncthreads();
-    auto put = [&](int rank, u64 v) { out[rank] = kv64_index(v); };
-    if (cnt <= 256) block_rank_sort<1>(s, cnt, put);
-    else if (cnt <= 512) block_rank_sort<2>(s, cnt, put);
-    else if (cnt <= 1024) block_rank_sort<4>(s, cnt, put);
-    else block_rank_sort<8>(s, cnt, put);
+    if (cnt <= 256) block_rank_sort<1>(s, cnt, put_idx);
+    else if (cnt <= 512) block_rank_sort<2>(s, cnt, put_idx);
+    else if (cnt <= 1024) block_rank_sort<4>(s, cnt, put_idx);
+    else block_rank_sort<8>(s, cnt, put_idx);
   } else {
     block_sort_desc(s, cnt);
     for (int i = tid; i < cnt; i += 256) out[i] = kv64_index(s[i]);
@@ -552,7 +642,7 @@ struct RegVals {
 
 // LDS of the range kernel: keys [RB_MAX] | hist [512] | scratch [48] | counter [4] |
 // sv [SV_CAP ushort], aliased by smp [256 u64] | sel [pow2(min(topk, rb) + 1) u64, one range only]
-template <typename QT, typename KT, int CI>
+template <typename QT, typename KT, int CI, bool SCORE>
 __global__ __launch_bounds__(256, 4) void idx_range_kernel(DecodeIdxParams p) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   constexpr int NS = CI / 32;
@@ -695,6 +785,17 @@ __global__ __launch_bounds__(256, 4) void idx_range_kernel(DecodeIdxParams p) {
   for (int d = 0; d < D; ++d)
     if (m0 + d < mine) step(m0 + d, kf[d], iv[d], std::false_type{});
   __syncthreads();
+  if constexpr (SCORE) {
+    // score pass only: the range's keys out, 16 bytes a thread
+    uint32_t* kout = p.keys_out + (size_t)b * p.ko_bstride + r0;
+    for (int i = 4 * tid; i < nr_blocks; i += 1024) {
+      if (i + 4 <= nr_blocks) {
+        *reinterpret_cast<uint4*>(kout + i) = *reinterpret_cast<const uint4*>(keys + i);
+      } else {
+        for (int e = i; e < nr_blocks; ++e) kout[e] = keys[e];
+      }
+    }
+  } else {
 
   // ---- top-k of the range ----
   // Thread t owns the keys at positions 4 t + 1024 s + e (s < 8, e < 4),
@@ -764,7 +865,7 @@ __global__ __launch_bounds__(256, 4) void idx_range_kernel(DecodeIdxParams p) {
     if (p.nr == 1) {
       reg_gather<SV_CAP / 256>(gsrc, sl, all, [&](int at, u64 v) { sel[at] = v; }, counter);
       __syncthreads();
-      write_sorted(sel, topk, topk, p.idx_out + (size_t)b * topk);
+      write_sorted<false>(sel, topk, topk, p.idx_out + (size_t)b * topk);
     } else {
       reg_gather<SV_CAP / 256>(gsrc, sl, all, [&](int at, u64 v) { cout[at] = v; }, counter);
     }
@@ -775,11 +876,47 @@ __global__ __launch_bounds__(256, 4) void idx_range_kernel(DecodeIdxParams p) {
   if (p.nr == 1) {
     reg_gather<RK>(src, sl, all, [&](int at, u64 v) { sel[at] = v; }, counter);
     __syncthreads();
-    write_sorted(sel, min(nr_blocks, topk), topk, p.idx_out + (size_t)b * topk);
+    write_sorted<false>(sel, min(nr_blocks, topk), topk, p.idx_out + (size_t)b * topk);
   } else {
     // candidates (any order) straight to global: min(nr_blocks, topk) of them
     reg_gather<RK>(src, sl, all, [&](int at, u64 v) { cout[at] = v; }, counter);
   }
+  }
+}
+
+// LDS of the select kernel: keys [RB_MAX] | hist [1024] | scratch [48] | counter [4] |
+// sel [pow2(topk + 1) u64]
+__global__ __launch_bounds__(256) void idx_select_kernel(DecodeIdxParams p) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  uint32_t* keys = reinterpret_cast<uint32_t*>(smem);     // [RB_MAX]
+  uint32_t* hist = keys + RB_MAX;                          // [1024]
+  int* scratch = reinterpret_cast<int*>(hist + 1024);      // [48]
+  int* counter = scratch + 48;                             // [4]
+  u64* sel = reinterpret_cast<u64*>(counter + 4);          // [pow2(topk + 1)]
+  const int tid = threadIdx.x, b = blockIdx.x, topk = p.topk;
+  const int nb = min(p.n_seen ? min((p.n_seen[0] + 1) / p.m, p.cap) : p.nb, RB_MAX);
+  // the keys of the score pass (rows ko_bstride words apart, a multiple of 4)
+  const uint32_t* src = p.keys_out + (size_t)b * p.ko_bstride;
+  for (int i = 4 * tid; i < nb; i += 1024) {
+    if (i + 4 <= nb) {
+      *reinterpret_cast<uint4*>(keys + i) = *reinterpret_cast<const uint4*>(src + i);
+    } else {
+      for (int e = i; e < nb; ++e) keys[e] = src[e];
+    }
+  }
+  if (tid == 0) counter[0] = 0;
+  __syncthreads();
+  int* out = p.idx_out + (size_t)b * topk;
+  constexpr int RK = 4 * (RB_MAX / 1024);
+  const RangeKeys rk{keys, nb, 0, 0ull};
+  Sel64 sl{0ull, 0ull};
+  const bool all = nb <= topk;
+  if (!all) {
+    sl = block_select64<4>([&](int i) { return kv64(keys[i], i); }, nb, topk, hist, scratch);
+  }
+  reg_gather<RK>(rk, sl, all, [&](int at, u64 v) { sel[at] = v; }, counter);
+  __syncthreads();
+  write_sorted<true>(sel, min(nb, topk), topk, out);
 }
 
 // Gather capacity of the merge: MV_CAP when an estimate can pay off, else
@@ -870,7 +1007,7 @@ __global__ __launch_bounds__(256) void idx_merge_kernel(DecodeIdxParams p) {
     __syncthreads();
     cnt = topk;
   }
-  write_sorted(sel, cnt, topk, p.idx_out + (size_t)b * topk);
+  write_sorted<true>(sel, cnt, topk, p.idx_out + (size_t)b * topk);
 }
 
 // Decode attention over one group of rows of one sequence (a workgroup): the
@@ -1104,6 +1241,8 @@ hipError_t fill_u32(void* p, long long n, uint32_t v, hipStream_t s) {
   return hipGetLastError();
 }
 
+int decode_range_max() { return RB_MAX; }
+
 void decode_idx_plan(int B, int nb, int topk, int* rb, int* nr) {
   // ranges of at most RB_MAX blocks; a small batch is split further, down to
   // ranges of max(1024, 2 topk) blocks, for about WG_TARGET workgroups
@@ -1124,6 +1263,10 @@ size_t decode_idx_lds(int rb, int topk, int nr) {
   return base + (nr == 1 ? (size_t)pow2_at_least(min(topk, rb) + 1) * 8 : 0);
 }
 
+size_t decode_select_lds(int topk) {
+  return (size_t)RB_MAX * 4 + 1024 * 4 + 52 * 4 + (size_t)pow2_at_least(topk + 1) * 8;
+}
+
 size_t decode_merge_lds(int topk) {
   return (size_t)merge_cap(topk) * 8 + (size_t)pow2_at_least(topk + 1) * 8 + 512 * 4 + 52 * 4;
 }
@@ -1135,7 +1278,9 @@ bool decode_idx_fits(int rb, int topk, int nr) { return decode_idx_lds(rb, topk,
 hipError_t decode_idx_dispatch(const DecodeIdxParams& p, int qdtype, int kdtype, hipStream_t s) {
   const size_t lds = decode_idx_lds(p.rb, p.topk, p.nr);
   const dim3 grid((unsigned)(p.B * p.nr)), block(256);
-#define KCH_DIDX(QT, KT, CI) hipLaunchKernelGGL((idx_range_kernel<QT, KT, CI>), grid, block, lds, s, p)
+#define KCH_DIDX(QT, KT, CI)                                                                   \
+  if (p.keys_out) hipLaunchKernelGGL((idx_range_kernel<QT, KT, CI, true>), grid, block, lds, s, p); \
+  else hipLaunchKernelGGL((idx_range_kernel<QT, KT, CI, false>), grid, block, lds, s, p)
 #define KCH_DIDX_CI(QT, KT)             \
   if (p.cI == 64) KCH_DIDX(QT, KT, 64); \
   else if (p.cI == 128) KCH_DIDX(QT, KT, 128); \
@@ -1156,7 +1301,12 @@ hipError_t decode_idx_dispatch(const DecodeIdxParams& p, int qdtype, int kdtype,
 #undef KCH_DIDX_CI
 #undef KCH_DIDX
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || p.nr == 1) return e;
+  if (e != hipSuccess) return e;
+  if (p.keys_out) {
+    hipLaunchKernelGGL(idx_select_kernel, dim3((unsigned)p.B), dim3(256), decode_select_lds(p.topk), s, p);
+    return hipGetLastError();
+  }
+  if (p.nr == 1) return e;
   hipLaunchKernelGGL(idx_merge_kernel, dim3((unsigned)p.B), dim3(256), decode_merge_lds(p.topk), s, p);
   return hipGetLastError();
 }

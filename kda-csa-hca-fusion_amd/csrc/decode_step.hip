@@ -149,10 +149,23 @@ __global__ __launch_bounds__(256) void kda_step_kernel(KdaStepParams p) {
   const T* pr = static_cast<const T*>(p.proj) + (size_t)b * p.ld_proj;
   float* st = p.state + (size_t)(b * p.HV + hv) * K * p.V + col;
 
-  // the state column first: its loads overlap the activations below
+  // the state column and this thread's gate weights first: their loads
+  // overlap the activations below
   float S[RPT];
 #pragma unroll
   for (int i = 0; i < RPT; ++i) S[i] = st[(size_t)(ph + 8 * i) * p.V];
+  constexpr int HALF = K / 2;
+  constexpr int GW = (K + 127) / 128;  // gate outputs per thread pair
+  typedef T vec8 __attribute__((ext_vector_type(8)));  // held as stored (16-bit types packed)
+  const int half = tid & 1;
+  vec8 wg[GW][HALF / 8];
+#pragma unroll
+  for (int r = 0; r < GW; ++r) {
+    const int i = (tid >> 1) + 128 * r;
+    const T* wr = static_cast<const T*>(p.g_up) + (size_t)(hv * K + min(i, K - 1)) * K + half * HALF;
+#pragma unroll
+    for (int j = 0; j < HALF / 8; ++j) wg[r][j] = *reinterpret_cast<const vec8*>(wr + 8 * j);
+  }
   const float vt = stored<T>(silu_f(to_f32(pr[2 * HK + hv * p.V + col])));
   const float bt = stored<T>(sigmoid_f(to_f32(pr[2 * HK + HVV + hv])));
   if (tid < K) sgd[tid] = to_f32(pr[2 * HK + HVV + p.HV + tid]);
@@ -183,24 +196,14 @@ __global__ __launch_bounds__(256) void kda_step_kernel(KdaStepParams p) {
   // gate pre-activations of head hv: gl[i] = g_up[hv K + i, :] . g_down, two
   // threads per output (halves of the dot product)
   {
-    constexpr int HALF = K / 2;
-    const int half = tid & 1;
-    for (int i = tid >> 1; i < K; i += 128) {
-      const T* wr = static_cast<const T*>(p.g_up) + (size_t)(hv * K + i) * K + half * HALF;
+#pragma unroll
+    for (int r = 0; r < GW; ++r) {
+      const int i = (tid >> 1) + 128 * r;
       float acc = 0.f;
-      if constexpr (HALF % 8 == 0) {
 #pragma unroll
-        for (int j0 = 0; j0 < HALF; j0 += 8) {
-          float w8[8];
-          Load8<T>::run(wr + j0, w8);
-#pragma unroll
-          for (int u = 0; u < 8; ++u) acc = fmaf(w8[u], sgd[half * HALF + j0 + u], acc);
-        }
-      } else {
-        for (int j = 0; j < HALF; ++j) acc = fmaf(to_f32(wr[j]), sgd[half * HALF + j], acc);
-      }
+      for (int j = 0; j < HALF; ++j) acc = fmaf(to_f32(wg[r][j / 8][j % 8]), sgd[half * HALF + j], acc);
       acc += __shfl_xor(acc, 1);
-      if (half == 0) {
+      if (half == 0 && i < K) {
         // the linear's output, -softplus and the decay product are each stored in T
         float g = stored<T>(-stored<T>(softplus_f(stored<T>(acc))) * p.decay_scale);
         g = fmaxf(g, p.g_clamp_min);

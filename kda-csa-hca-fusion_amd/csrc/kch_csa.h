@@ -75,8 +75,15 @@ struct DecodeIdxParams {
   // device-driven step: nb = (*n_seen + 1) / m, at most cap (nr ranges cover cap)
   const int* n_seen = nullptr;
   int m = 1, cap = 0;
+  // score / select split (nb <= decode_range_max()): the ranges only write
+  // their logit keys to keys_out [B, ko_bstride], then one workgroup per
+  // sequence selects from all of them
+  uint32_t* keys_out = nullptr;
+  long long ko_bstride = 0;
 };
 void decode_idx_plan(int B, int nb, int topk, int* rb, int* nr);
+int decode_range_max();  // most blocks one indexer range holds
+size_t decode_select_lds(int topk);
 bool decode_merge_fits(int topk);  // the merge kernel's LDS holds its buffers for topk
 hipError_t fill_u32(void* p, long long n, uint32_t v, hipStream_t s);
 size_t decode_idx_lds(int rb, int topk, int nr);

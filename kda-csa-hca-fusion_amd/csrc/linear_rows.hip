@@ -43,7 +43,7 @@ template <> struct Vec8<_Float16> {
   }
 };
 
-constexpr int kBatch = 8;  // K steps whose loads are in flight together
+constexpr int kBatch = 16;  // K steps whose loads are in flight together
 
 template <typename T, typename WT>
 __global__ __launch_bounds__(256) void linear_rows_kernel(LinearRowsParams p) {
