@@ -326,7 +326,7 @@ def bench_csa(B, T, steps, warmup, dev):
     core = {"ms": ms_core, "tokens_per_s": B * T / (ms_core * 1e-3)}
     core.update(_roof(flops, bytes_, ms_core))
     return {"B": B, "T": T, "tokens_per_s": B * T / (ms_full * 1e-3), "ms": ms_full,
-            "includes": "projections (hipBLASLt) + core", "core": core}
+            "includes": "projections (hipBLASLt; q up-projection kch_linear_up) + core", "core": core}
 
 
 def bench_hca(B, T, steps, warmup, dev):
@@ -352,7 +352,7 @@ def bench_hca(B, T, steps, warmup, dev):
     core = {"ms": ms_core, "tokens_per_s": B * T / (ms_core * 1e-3)}
     core.update(_roof(flops, bytes_, ms_core))
     return {"B": B, "T": T, "tokens_per_s": B * T / (ms_full * 1e-3), "ms": ms_full,
-            "includes": "projections (hipBLASLt) + core", "core": core}
+            "includes": "projections (hipBLASLt; q up-projection kch_linear_up) + core", "core": core}
 
 
 def bench_hybrid(dev, T=16384, B=2, n_decode=256):

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define KCH_ABI_VERSION 10
+#define KCH_ABI_VERSION 11
 
 #define KCH_OK 0
 #define KCH_ERR_INVALID 1     /* bad pointer / shape / argument */
@@ -312,6 +312,19 @@ int kch_layer_norm(const void* x, const void* w, const void* b, void* out, int r
  */
 int kch_linear_rows(const void* x, long long ldx, const void* w, long long ldw, void* y,
                     long long ldy, int M, int N, int K, int dtype, void* stream);
+
+/*
+ * The low-rank query up-projection of a prefill, torch.nn.functional.linear
+ * without bias for many rows and a short K: q = W_UQ cQ of naive_hca
+ * (ops_hca.py:140) and naive_csa's q / q_idx (ops_csa.py:923 and 877):
+ *   y[m, n] = sum_k x[m, k] * w[n, k]   (fp32 accumulation, result in dtype)
+ * x [M, K], w [N, K], y [M, N] with row strides ldx, ldw, ldy, all of dtype
+ * (bf16 or fp16). K in {32, 64, 128, 256}; x and w 16-byte aligned with row
+ * strides multiples of 8; when N % 8 == 0, y 16-byte aligned with ldy a
+ * multiple of 8.
+ */
+int kch_linear_up(const void* x, long long ldx, const void* w, long long ldw, void* y,
+                  long long ldy, long long M, int N, int K, int dtype, void* stream);
 
 /* ---- Device-driven decode step ----------------------------------------
  * The entry points below make up one single-token decode step of

@@ -463,6 +463,27 @@ int kch_linear_rows_fused(const void* x, long long ldx, const void* w, long long
   return hip_status(fn, kch::linear_rows_dispatch(p, dtype, (hipStream_t)stream));
 }
 
+int kch_linear_up(const void* x, long long ldx, const void* w, long long ldw, void* y,
+                  long long ldy, long long M, int N, int K, int dtype, void* stream) {
+  const char* fn = "kch_linear_up";
+  if (dtype != KCH_DT_BF16 && dtype != KCH_DT_F16)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: dtype %d (bf16 or fp16 only)", fn, dtype);
+  if (M < 0 || N < 1) return fail(KCH_ERR_INVALID, "%s: bad sizes M=%lld N=%d", fn, M, N);
+  if (K != 32 && K != 64 && K != 128 && K != 256)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: K=%d not in {32, 64, 128, 256}", fn, K);
+  if ((M + 63) / 64 >= (1LL << 31)) return fail(KCH_ERR_INVALID, "%s: too many rows", fn);
+  if (M == 0) return KCH_OK;
+  if (!x || !w || !y) return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
+  if (ldx < K || ldw < K || ldy < N)
+    return fail(KCH_ERR_INVALID, "%s: row strides below the row lengths", fn);
+  if ((ldx | ldw) % 8 || (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) % 16)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: x and w rows must be 16-byte aligned", fn);
+  if (N % 8 == 0 && (ldy % 8 || reinterpret_cast<uintptr_t>(y) % 16))
+    return fail(KCH_ERR_UNSUPPORTED, "%s: y rows must be 16-byte aligned", fn);
+  kch::RowsProjParams p{x, w, y, ldx, ldw, ldy, M, N, K};
+  return hip_status(fn, kch::rows_up_dispatch(p, dtype, (hipStream_t)stream));
+}
+
 int kch_kda_decode_front(const void* x, long long ldx, const void* ln_w, const void* ln_b,
                          float eps, void* lookback, const void* conv_w, const void* conv_b,
                          void* out, int B, int d, int dtype, int wdtype, void* stream) {

@@ -99,6 +99,19 @@ struct LinearRowsParams {
 };
 hipError_t linear_rows_dispatch(const LinearRowsParams& p, int dtype, hipStream_t stream);
 
+// Y[M, N] = X[M, K] W[N, K]^T for many rows and K in {32, 64, 128, 256}
+// (rows_up.hip): the low-rank query up-projection of a prefill. x, w, y of
+// one dtype, row strides ldx, ldw, ldy.
+struct RowsProjParams {
+  const void* x;
+  const void* w;
+  void* y;
+  long long ldx, ldw, ldy;
+  long long M;
+  int N, K;
+};
+hipError_t rows_up_dispatch(const RowsProjParams& p, int dtype, hipStream_t stream);
+
 // ---- device-driven decode step (decode_step.hip) ----
 // n_seen: tokens the caches held before this step (device int); the step's
 // token is number n_seen of its sequence.

@@ -51,6 +51,7 @@ _SIGNATURES = {
     "kch_kda_gates": [_P, _L, _P, _L, _P, _P, _P, _P, _P] + [_I] * 6 + [_F, _I, _P],
     "kch_layer_norm": [_P, _P, _P, _P, _I, _I, _F, _I, _I, _P],
     "kch_linear_rows": [_P, _L, _P, _L, _P, _L, _I, _I, _I, _I, _P],
+    "kch_linear_up": [_P, _L, _P, _L, _P, _L, _L, _I, _I, _I, _P],
     "kch_linear_rows_fused": [_P, _L, _P, _L, _P, _L, _I, _I, _I, _P, _P, _F, _I, _P, _L, _P,
                               _I, _P],
     "kch_kda_decode_front": [_P, _L, _P, _P, _F, _P, _P, _P, _P, _I, _I, _I, _I, _P],

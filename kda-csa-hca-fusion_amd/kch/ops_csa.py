@@ -84,6 +84,70 @@ def _f32(t, device):
     return t.detach().to(device=device, dtype=torch.float32).contiguous()
 
 
+class _DerivedCache:
+    """Tensors derived from parameters (a row concatenation, an fp32 copy),
+    kept across calls of the functional operators: an entry holds its source
+    tensors (so that their storage cannot be reused while it lives) and is
+    valid while each is the same object at the same in-place version."""
+
+    def __init__(self, size=16):
+        self.size = size
+        self.entries = {}  # key -> (sources, versions, value)
+
+    def get(self, key, sources, build):
+        versions = tuple(t._version for t in sources)
+        hit = self.entries.get(key)
+        if hit is not None and hit[1] == versions and all(a is b for a, b in zip(hit[0], sources)):
+            return hit[2]
+        if len(self.entries) >= self.size:
+            self.entries.pop(next(iter(self.entries)))
+        value = build()
+        self.entries[key] = (tuple(sources), versions, value)
+        return value
+
+
+_derived = _DerivedCache()
+
+
+def _cat_cached(ws, pad_rows_to=1):
+    """``torch.cat(ws, 0)`` (zero rows appended up to a multiple of
+    ``pad_rows_to``), built once per set of weights."""
+    key = ("cat", pad_rows_to) + tuple(id(w) for w in ws)
+
+    def build():
+        W = torch.cat([w.detach() for w in ws], 0)
+        extra = (-W.shape[0]) % pad_rows_to
+        return F.pad(W, (0, 0, 0, extra)) if extra else W
+    return _derived.get(key, ws, build)
+
+
+def _f32_cached(t, device):
+    if t.dtype == torch.float32 and t.is_contiguous() and t.device == device:
+        return t.detach()
+    return _derived.get(("f32", id(t), device), (t,), lambda: _f32(t, device))
+
+
+def _linear_up(x, w):
+    """``F.linear(x, w)`` of a prefill's query latent x ``[..., K]`` (rows may be
+    strided): ``kch_linear_up`` when it applies (bf16 / fp16, K in {32, 64,
+    128, 256}, 16-byte aligned rows, at least 512 output columns), else
+    ``F.linear``. At M = 131072, K = 128 on MI355X: N = 2048 126 us against
+    183 us for ``F.linear``; N = 256 28 us against 27 us."""
+    K = x.shape[-1]
+    N = w.shape[0]
+    x2 = x.reshape(-1, K) if x.dim() != 2 else x
+    if not (x.is_cuda and x.dtype in (torch.bfloat16, torch.float16) and w.dtype == x.dtype
+            and K in (32, 64, 128, 256) and w.dim() == 2 and w.shape[1] == K and N >= 512
+            and x2.stride(-1) == 1 and x2.stride(0) % 8 == 0 and x2.data_ptr() % 16 == 0):
+        return F.linear(x, w)
+    wc = w if (w.is_contiguous() and w.data_ptr() % 16 == 0) else w.clone(
+        memory_format=torch.contiguous_format)
+    y = torch.empty(*x.shape[:-1], N, device=x.device, dtype=x.dtype)
+    _lib.call("kch_linear_up", _lib.ptr(x2), x2.stride(0), _lib.ptr(wc), K, _lib.ptr(y), N,
+              x2.shape[0], N, K, _lib.dtype_code("linear_up", x.dtype), _lib.stream_of(x))
+    return y
+
+
 # Sizes the kernels take: attention head dim, indexer key dim, indexer heads,
 # heads per attention launch. Other sizes up to the largest are zero-padded up
 # to the next one: zero channels add nothing to a dot product or an L2 norm,
@@ -124,7 +188,7 @@ def _compress(fn, C, Z, B_pos, m, *, out_raw=True, key=None, normalize=False, lo
     nb = T // m
     C, ldc = _rows(C)
     Z, ldz = _rows(Z)
-    bpos = _f32(B_pos, C.device)
+    bpos = _f32_cached(B_pos, C.device)
     raw = torch.empty(B_, nb, c, device=C.device, dtype=torch.float32) if out_raw else None
     key_f32 = 2 if key_split else (1 if (key is not None and key.dtype == torch.float32) else 0)
     _lib.call("kch_compress", _lib.ptr(C), ldc, _lib.ptr(Z), ldz, _lib.ptr(bpos), _lib.ptr(raw),
@@ -145,7 +209,7 @@ def _compress_overlapped(fn, Ca, Cb, Za, Zb, Ba, Bb, m, *, out_raw=True, key=Non
     _check_gpu_dtype(fn, Ca, Cb, Za, Zb)
     nb = T // m
     (Ca, lca), (Cb, lcb), (Za, lza), (Zb, lzb) = (_rows(x) for x in (Ca, Cb, Za, Zb))
-    ba, bb = _f32(Ba, Ca.device), _f32(Bb, Ca.device)
+    ba, bb = _f32_cached(Ba, Ca.device), _f32_cached(Bb, Ca.device)
     raw = torch.empty(B_, nb, c, device=Ca.device, dtype=torch.float32) if out_raw else None
     key_f32 = 1 if (key is not None and key.dtype == torch.float32) else 0
     _lib.call("kch_compress_overlapped", _lib.ptr(Ca), lca, _lib.ptr(Cb), lcb, _lib.ptr(Za), lza,
@@ -345,7 +409,7 @@ def _csa_core(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, *, m
                           normalize_q=normalize_qk, idx64=False, sorted_=bool(return_indices),
                           key_split=True)
         _log_selection(idx)
-    sink = None if sink_logits is None else _f32(sink_logits, device)
+    sink = None if sink_logits is None else _f32_cached(sink_logits, device)
     out = torch.empty(B_, T, nh, c, device=device, dtype=q.dtype)
     code = _lib.dtype_code(fn, q.dtype)
     for h0, h1 in _head_groups(nh):
@@ -427,18 +491,20 @@ def naive_csa(H, W_aKV, W_bKV, W_aZ, W_bZ, Ba, Bb, W_DQ, W_UQ, W_IUQ, W_w, W_KV_
     n_blocks = T // m
     with torch.no_grad():
         if fuse_projections:
-            # every projection of H in one GEMM: H is read from HBM once
-            comb = F.linear(H, torch.cat([W_aKV, W_bKV, W_aZ, W_bZ, W_KV_idx, W_Z_idx, W_DQ, W_w],
-                                         dim=0))
-            Ca, Cb, Za, Zb, K_idx_raw, Z_idx, cQ, w_idx = comb.split(
+            # every projection of H in one GEMM: H is read from HBM once (rows
+            # padded to a multiple of 8 columns, so that the latent's rows stay
+            # 16-byte aligned for the up-projection)
+            comb = F.linear(H, _cat_cached([W_aKV, W_bKV, W_aZ, W_bZ, W_KV_idx, W_Z_idx, W_DQ,
+                                            W_w], pad_rows_to=8))
+            Ca, Cb, Za, Zb, K_idx_raw, Z_idx, cQ, w_idx = comb[..., :4 * c + 2 * c_I + dc + nIh].split(
                 [c, c, c, c, c_I, c_I, dc, nIh], dim=-1)
         else:
             Ca, Cb, Za, Zb = (F.linear(H, w) for w in (W_aKV, W_bKV, W_aZ, W_bZ))
             K_idx_raw, Z_idx = F.linear(H, W_KV_idx), F.linear(H, W_Z_idx)
             cQ = F.linear(H, W_DQ)
             w_idx = F.linear(H, W_w)
-        q_idx = F.linear(cQ, W_IUQ).view(B_, T, nIh, c_I)
-        q = F.linear(cQ, W_UQ).view(B_, T, nh, c)
+        q_idx = _linear_up(cQ, W_IUQ).view(B_, T, nIh, c_I)
+        q = _linear_up(cQ, W_UQ).view(B_, T, nh, c)
         out = csa_core(Ca, Cb, Za, Zb, K_idx_raw, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, m=m,
                        topk=topk, sliding_window=sliding_window, sink_logits=sink_logits,
                        normalize_qk=normalize_qk, scale=scale)

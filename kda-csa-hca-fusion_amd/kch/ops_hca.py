@@ -14,8 +14,8 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib
-from .ops_csa import (_HEAD_DIMS, _aligned, _check_gpu_dtype, _compress, _f32, _head_groups,
-                      _kernel_size, _pad_last, l2_normalize_rows)
+from .ops_csa import (_HEAD_DIMS, _aligned, _cat_cached, _check_gpu_dtype, _compress, _f32_cached,
+                      _head_groups, _kernel_size, _linear_up, _pad_last, l2_normalize_rows)
 
 
 def hca_core(C, Z, q, B_pos, *, m2, sliding_window=0, sink_logits=None, scale=1.0,
@@ -48,7 +48,7 @@ def hca_core(C, Z, q, B_pos, *, m2, sliding_window=0, sink_logits=None, scale=1.
             local = l2_normalize_rows(C_local_raw, out_dtype=torch.bfloat16)
     _compress(fn, C, Z, B_pos, m2, out_raw=False, key=kv, normalize=True,
               local=local if C_local_raw is None else None)
-    sink = None if sink_logits is None else _f32(sink_logits, device)
+    sink = None if sink_logits is None else _f32_cached(sink_logits, device)
     out = torch.empty(B_, T, nh, c, device=device, dtype=q.dtype)
     code = _lib.dtype_code(fn, q.dtype)
     for h0, h1 in _head_groups(nh):
@@ -121,9 +121,9 @@ def naive_hca(H, W_KV, W_Z, B_pos, W_DQ, W_UQ, *, m2, nh, c, dc, scale=1.0, slid
     n_blocks = T // m2
     with torch.no_grad():
         # the three projections of H in one GEMM: H is read from HBM once
-        CZQ = F.linear(H, torch.cat([W_KV, W_Z, W_DQ], dim=0))
-        C, Z, cQ = CZQ.split([c, c, dc], dim=-1)
-        q = F.linear(cQ, W_UQ).view(B_, T, nh, c)
+        CZQ = F.linear(H, _cat_cached([W_KV, W_Z, W_DQ], pad_rows_to=8))
+        C, Z, cQ = CZQ[..., :2 * c + dc].split([c, c, dc], dim=-1)
+        q = _linear_up(cQ, W_UQ).view(B_, T, nh, c)
         C_local_raw = F.linear(H, W_KV_local) if (W_KV_local is not None and sliding_window > 0) \
             else None
         out = hca_core(C, Z, q, B_pos, m2=m2, sliding_window=sliding_window,

@@ -56,6 +56,14 @@ def test_invalid_arguments_report_errors_without_gpu():
     assert rc == 2 and b"M=17" in lib.kch_last_error()
     rc = lib.kch_linear_rows(None, 64, None, 64, None, 8, 2, 8, 48, 1, None)
     assert rc == 2 and b"multiple of 32" in lib.kch_last_error()
+    # the prefill projections: sizes checked before any pointer or HIP call
+    rc = lib.kch_linear_up(None, 48, None, 48, None, 8, 4, 8, 48, 1, None)
+    assert rc == 2 and b"K=48" in lib.kch_last_error()
+    rc = lib.kch_linear_up(None, 64, None, 64, None, 8, 4, 8, 64, 0, None)
+    assert rc == 2 and b"bf16 or fp16" in lib.kch_last_error()
+    rc = lib.kch_linear_up(None, 64, None, 64, None, 8, 4, 8, 64, 1, None)
+    assert rc == 1 and b"null pointer" in lib.kch_last_error()
+    assert lib.kch_linear_up(None, 64, None, 64, None, 8, 0, 8, 64, 1, None) == 0
 
 
 def test_chunk_workspace_size_query():

@@ -82,3 +82,45 @@ def test_linear_rows_in_hybrid_decode_views(dev):
         ref = torch.nn.functional.linear(x.float(), w.float())
         assert tuple(y.shape) == (3, 1, w.shape[0])
         assert float((y.float() - ref).abs().max()) <= 1e-2 * float(ref.abs().max())
+
+
+def _run_up(x, w, y):
+    M, K = x.shape
+    N = w.shape[0]
+    _lib.call("kch_linear_up", _lib.ptr(x), x.stride(0), _lib.ptr(w), w.stride(0), _lib.ptr(y),
+              y.stride(0), M, N, K, _lib.dtype_code("test", x.dtype), _lib.stream_of(x))
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,N,K", [(1, 16, 32), (63, 2048, 128), (64, 2304, 128), (1000, 100, 64),
+                                   (4097, 2048, 256), (131072, 2048, 128), (77, 8, 32)])
+def test_linear_up_matches_fp32(dev, dt, M, N, K):
+    """kch_linear_up (the prefill query up-projection) against the fp32 product
+    of the same inputs, every element."""
+    g = torch.Generator(device="cpu").manual_seed(M + 3 * N + K)
+    x = torch.randn(M, K, generator=g).to(dev, dt)
+    w = (torch.randn(N, K, generator=g) / K ** 0.5).to(dev, dt)
+    y = torch.full((M, N), float("nan"), device=dev, dtype=dt)
+    _run_up(x, w, y)
+    ref = x.float() @ w.float().t()
+    err = (y.float() - ref).abs()
+    tol = 8e-3 * ref.abs() + 2e-3 * ref.abs().max()
+    assert bool(torch.isfinite(y.float()).all())
+    assert bool((err <= tol).all()), float(err.max())
+
+
+def test_linear_up_strided(dev):
+    # x: the latent columns of a fused projection output; y rows padded
+    M, N, K = 300, 2304, 128
+    g = torch.Generator(device="cpu").manual_seed(5)
+    big = torch.randn(M, 384 + K, generator=g).to(dev, torch.bfloat16)
+    x = big[:, 384:384 + K]
+    w = (torch.randn(N, K, generator=g) / K ** 0.5).to(dev, torch.bfloat16)
+    yb = torch.full((M, N + 16), 7.0, device=dev, dtype=torch.bfloat16)
+    y = yb[:, :N]
+    _run_up(x, w, y)
+    ref = x.float() @ w.float().t()
+    assert float((y.float() - ref).abs().max()) <= 1e-2 * float(ref.abs().max())
+    assert bool((yb[:, N:] == 7.0).all())
+
