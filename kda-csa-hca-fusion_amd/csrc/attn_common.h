@@ -273,11 +273,10 @@ struct MqaWave {
     return st;
   }
 
-  // Softmax step and O^T update over 32 keys: sc = this lane's raw scores of
-  // keys 4q..4q+3 and 16+4q..16+4q+3 (-inf = masked), `rows` the 32 key rows in
-  // a swizzled LDS tile (the V^T source), visible to this wave.
-  __device__ __forceinline__ void accumulate32(const float (&sc)[8], const bf16_t* rows,
-                                               const TileOffsets<HD>& to) {
+  // Softmax step over 32 keys: sc = this lane's raw scores of keys 4q..4q+3
+  // and 16+4q..16+4q+3 (-inf = masked). Rescales o and L when a score moves
+  // M, adds the keys' p to L and returns p as the B operand of the O^T update.
+  __device__ __forceinline__ bf16x8 softmax32(const float (&sc)[8]) {
     bool up = false;
 #pragma unroll
     for (int e = 0; e < 8; ++e) up |= sc[e] > thr;
@@ -299,20 +298,31 @@ struct MqaWave {
 #pragma unroll
     for (int e = 0; e < 8; ++e) pe[e] = fast_exp2(fmaf(sc[e], qscale2, nm));
     L += ((pe[0] + pe[1]) + (pe[2] + pe[3])) + ((pe[4] + pe[5]) + (pe[6] + pe[7]));
-    const bf16x8 pb = __builtin_convertvector(pe, bf16x8);
+    return __builtin_convertvector(pe, bf16x8);
+  }
+
+  // V^T fragment t (16 dims x 32 keys) of 32 key rows in a swizzled LDS tile:
+  // column 16t + n of rows 4q .. 4q + 3 of each 16-row slice, one transposing
+  // read per slice.
+  __device__ __forceinline__ static bf16x8 vt_frag(const bf16_t* rows, const TileOffsets<HD>& to,
+                                                   int t) {
     typedef short s16x4 __attribute__((ext_vector_type(4)));
+    const int vo = to.vt(t);
+    const s16x4 r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4*)(rows + vo));
+    const s16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4*)(rows + 16 * HD + vo));
+    return __builtin_bit_cast(bf16x8, __builtin_shufflevector(r0, r1, 0, 1, 2, 3, 4, 5, 6, 7));
+  }
+
+  // Softmax step and O^T update over 32 keys whose rows (the V^T source) are
+  // in a swizzled LDS tile visible to this wave.
+  __device__ __forceinline__ void accumulate32(const float (&sc)[8], const bf16_t* rows,
+                                               const TileOffsets<HD>& to) {
+    const bf16x8 pb = softmax32(sc);
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      // V^T fragment (16 dims x 32 keys): column 16t + n of rows 4q .. 4q + 3
-      // of each 16-row slice, one transposing read per slice
-      const int vo = to.vt(t);
-      const s16x4 r0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) s16x4*)(rows + vo));
-      const s16x4 r1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) s16x4*)(rows + 16 * HD + vo));
-      const bf16x8 va = __builtin_bit_cast(bf16x8, __builtin_shufflevector(r0, r1, 0, 1, 2, 3, 4, 5, 6, 7));
-      o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, o[t], 0, 0, 0);
-    }
+    for (int t = 0; t < NT; ++t)
+      o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt_frag(rows, to, t), pb, o[t], 0, 0, 0);
   }
 
   // Fragments of 16 key rows: this lane's key row (key n = lane & 15) at dims

@@ -531,6 +531,7 @@ __global__ __launch_bounds__(64 * NWV, MINB) void attn_dense_tile_kernel(AttnPar
           else sb[u] = w[u].scores(kf);
         }
       }
+      bf16x8 pb[QW];
 #pragma unroll
       for (int u = 0; u < QW; ++u) {
         float sc[8] = {sa[u][0], sa[u][1], sa[u][2], sa[u][3], sb[u][0], sb[u][1], sb[u][2], sb[u][3]};
@@ -543,7 +544,15 @@ __global__ __launch_bounds__(64 * NWV, MINB) void attn_dense_tile_kernel(AttnPar
             sc[e] = ok ? sc[e] : -INFINITY;
           }
         }
-        w[u].accumulate32(sc, rows, to);
+        pb[u] = w[u].softmax32(sc);
+      }
+      // each V^T fragment serves every query of the wave
+#pragma unroll
+      for (int t = 0; t < W::NT; ++t) {
+        const bf16x8 va = W::vt_frag(rows, to, t);
+#pragma unroll
+        for (int u = 0; u < QW; ++u)
+          w[u].o[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[u], w[u].o[t], 0, 0, 0);
       }
     };
 
@@ -578,14 +587,17 @@ __global__ __launch_bounds__(64 * NWV, MINB) void attn_dense_tile_kernel(AttnPar
   // Output rows through LDS (whole-row stores): each wave stages its block in
   // its own slice of the tile buffers, which every wave is done reading (the
   // tile loop ends with a barrier; without rows it never ran).
-  static_assert(QW == 1, "one query per wave");
   static_assert(NWV * 16 * HD * sizeof(OT) <= sizeof(tile), "staging fits in the tile buffers");
-  const int t = t0 + wv;
-  w[0].finalize();
-  const float f = w[0].finish(p.sink != nullptr, (p.sink && n < p.nh) ? p.sink[n] : 0.f);
-  if (t < T)
-    store_rows<HD, OT>(w[0].o, f, static_cast<OT*>(p.out) + ((size_t)b * T + t) * p.nh * HD, p.nh,
-                       reinterpret_cast<char*>(&tile[0][0]) + wv * 16 * HD * sizeof(OT));
+#pragma unroll
+  for (int u = 0; u < QW; ++u) {
+    const int t = t0 + QW * wv + u;
+    w[u].finalize();
+    const float f = w[u].finish(p.sink != nullptr, (p.sink && n < p.nh) ? p.sink[n] : 0.f);
+    if (u > 0) wave_lds_sync();  // the previous query's staged rows are read
+    if (t < T)
+      store_rows<HD, OT>(w[u].o, f, static_cast<OT*>(p.out) + ((size_t)b * T + t) * p.nh * HD, p.nh,
+                         reinterpret_cast<char*>(&tile[0][0]) + wv * 16 * HD * sizeof(OT));
+  }
 }
 
 // Query-tile shape: QW queries per wave, NWV waves per workgroup, at least
