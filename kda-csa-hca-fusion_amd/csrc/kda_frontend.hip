@@ -149,6 +149,78 @@ __global__ __launch_bounds__(256) void kda_gates_kernel(KdaGatesParams p) {
   }
 }
 
+// Wave per token row (4 rows per workgroup), 16-byte loads and stores: lane
+// (LPH lanes per head vector, LPH = K / 8) takes 8 consecutive channels. The
+// q/k head vectors go 64 / LPH per pass (the L2 norm is a reduction over the
+// head's LPH lanes), then v, g and beta, the loads of four passes in flight
+// together. Rounding as in kda_gates_kernel.
+template <typename T, int LPH>
+__global__ __launch_bounds__(256) void kda_gates_vec_kernel(KdaGatesParams p, long long rows) {
+  constexpr int U = 4;  // passes whose loads are in flight together
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const long long row = (long long)blockIdx.x * 4 + wave;
+  if (row >= rows) return;
+  const T* pr = static_cast<const T*>(p.proj) + row * p.ld_proj;
+  const T* gr = static_cast<const T*>(p.gl) + row * p.ld_gl;
+  const int HK = p.H * p.K;
+  constexpr int HPP = 64 / LPH;  // head vectors per pass
+  const int c = lane % LPH;
+  for (int h0 = 0; h0 < 2 * p.H; h0 += U * HPP) {
+    float f[U][8];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      Load8<T>::run(pr + (size_t)min(h0 + u * HPP + lane / LPH, 2 * p.H - 1) * p.K + 8 * c, f[u]);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int h = h0 + u * HPP + lane / LPH;
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        f[u][i] = stored<T>(silu_f(f[u][i]));
+        ss += f[u][i] * f[u][i];
+      }
+#pragma unroll
+      for (int o = 1; o < LPH; o <<= 1) ss += __shfl_xor(ss, o);
+      const float nrm = fmaxf(stored<T>(sqrtf(ss)), 1e-12f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) f[u][i] = f[u][i] / nrm;
+      if (h < 2 * p.H) {
+        T* dst = h < p.H ? static_cast<T*>(p.q) + (row * p.H + h) * p.K
+                         : static_cast<T*>(p.k) + (row * p.H + (h - p.H)) * p.K;
+        store_vec<T, 8>(dst + 8 * c, f[u]);
+      }
+    }
+  }
+  const int nv8 = p.HV * p.V / 8, ng8 = p.HV * p.K / 8;
+  T* v = static_cast<T*>(p.v) + row * (8LL * nv8);
+  T* g = static_cast<T*>(p.g) + row * (8LL * ng8);
+  for (int i0 = lane; i0 < nv8; i0 += U * 64) {
+    float f[U][8];
+#pragma unroll
+    for (int u = 0; u < U; ++u) Load8<T>::run(pr + 2 * HK + 8 * min(i0 + 64 * u, nv8 - 1), f[u]);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[u][e] = silu_f(f[u][e]);
+      if (i0 + 64 * u < nv8) store_vec<T, 8>(v + 8 * (i0 + 64 * u), f[u]);
+    }
+  }
+  // -softplus(.) is stored in T before the decay scale multiplies it (ops_fused.py:579)
+  for (int i0 = lane; i0 < ng8; i0 += U * 64) {
+    float f[U][8];
+#pragma unroll
+    for (int u = 0; u < U; ++u) Load8<T>::run(gr + 8 * min(i0 + 64 * u, ng8 - 1), f[u]);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[u][e] = -stored<T>(softplus_f(f[u][e])) * p.decay_scale;
+      if (i0 + 64 * u < ng8) store_vec<T, 8>(g + 8 * (i0 + 64 * u), f[u]);
+    }
+  }
+  T* beta = static_cast<T*>(p.beta) + row * p.HV;
+  for (int i = lane; i < p.HV; i += 64) beta[i] = from_f32<T>(sigmoid_f(to_f32(pr[2 * HK + 8 * nv8 + i])));
+}
+
 // One workgroup per row: the row's values stay in registers (d <= 4096), the
 // mean and the biased variance come from two block reductions in fp32, then
 // (x - mean) * rstd * w + b is rounded once to the output dtype.
@@ -205,8 +277,98 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(LayerNormParams p) {
   }
 }
 
+// Wave per row (4 rows per workgroup): lane l holds 16-byte chunks
+// l + 64 j (j < NC) of the row in registers, so d <= 512 NC; the mean and the
+// biased variance are wave reductions in fp32 (two passes over the registers).
+template <typename WT>
+__device__ __forceinline__ void load_w8(const WT* w, float* f) {
+  if constexpr (sizeof(WT) == 4) {
+    const float4 a = reinterpret_cast<const float4*>(w)[0], b = reinterpret_cast<const float4*>(w)[1];
+    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w; f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+  } else {
+    Load8<WT>::run(w, f);
+  }
+}
+
+template <typename T, typename WT, int NC>
+__global__ __launch_bounds__(256) void layer_norm_vec_kernel(LayerNormParams p) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const long long row = (long long)blockIdx.x * 4 + wave;
+  if (row >= p.rows) return;
+  const T* x = static_cast<const T*>(p.x) + row * p.d;
+  const int nch = p.d / 8;
+  float v[NC][8];
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int ch = lane + 64 * j;
+    if (ch < nch) {
+      Load8<T>::run(x + 8 * ch, v[j]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[j][i] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s += v[j][i];
+  }
+  const float mean = wave_sum(s) / (float)p.d;
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const bool ok = lane + 64 * j < nch;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float dv = v[j][i] - mean;
+      ss += ok ? dv * dv : 0.f;
+    }
+  }
+  const float var = wave_sum(ss) / (float)p.d;
+  const float rstd = 1.f / sqrtf(var + p.eps);
+  const WT* w = static_cast<const WT*>(p.w);
+  const WT* bb = static_cast<const WT*>(p.b);
+  T* out = static_cast<T*>(p.out) + row * p.d;
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int ch = lane + 64 * j;
+    if (ch < nch) {
+      float wf[8], bf[8];
+      load_w8<WT>(w + 8 * ch, wf);
+      if (bb) {
+        load_w8<WT>(bb + 8 * ch, bf);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) bf[i] = 0.f;
+      }
+      float y[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) y[i] = (v[j][i] - mean) * rstd * wf[i] + bf[i];
+      store_vec<T, 8>(out + 8 * ch, y);
+    }
+  }
+}
+
+template <typename T, typename WT>
+hipError_t layer_norm_vec_launch(const LayerNormParams& p, hipStream_t s) {
+  const dim3 grid((unsigned)((p.rows + 3) / 4)), block(256);
+  if (p.d <= 512) hipLaunchKernelGGL((layer_norm_vec_kernel<T, WT, 1>), grid, block, 0, s, p);
+  else if (p.d <= 1024) hipLaunchKernelGGL((layer_norm_vec_kernel<T, WT, 2>), grid, block, 0, s, p);
+  else if (p.d <= 2048) hipLaunchKernelGGL((layer_norm_vec_kernel<T, WT, 4>), grid, block, 0, s, p);
+  else hipLaunchKernelGGL((layer_norm_vec_kernel<T, WT, 8>), grid, block, 0, s, p);
+  return hipGetLastError();
+}
+
 template <typename T>
 hipError_t layer_norm_launch(const LayerNormParams& p, int wdtype, hipStream_t s) {
+  // 16-byte rows of 16-bit values: the wave-per-row kernel
+  const uintptr_t al = reinterpret_cast<uintptr_t>(p.x) | reinterpret_cast<uintptr_t>(p.out) |
+                       reinterpret_cast<uintptr_t>(p.w) | reinterpret_cast<uintptr_t>(p.b);
+  if constexpr (sizeof(T) == 2) {
+    if (p.d % 8 == 0 && p.d <= 4096 && al % 16 == 0) {
+      if (wdtype == DT_F32) return layer_norm_vec_launch<T, float>(p, s);
+      if (wdtype == DT_BF16) return layer_norm_vec_launch<T, bf16_t>(p, s);
+      return layer_norm_vec_launch<T, _Float16>(p, s);
+    }
+  }
   const dim3 grid((unsigned)p.rows), block(256);
   if (wdtype == DT_F32) hipLaunchKernelGGL((layer_norm_kernel<T, float>), grid, block, 0, s, p);
   else if (wdtype == DT_BF16) hipLaunchKernelGGL((layer_norm_kernel<T, bf16_t>), grid, block, 0, s, p);
@@ -236,7 +398,33 @@ hipError_t short_conv_dispatch(const ShortConvParams& p, int dtype, hipStream_t 
   return short_conv_launch<_Float16>(p, s);
 }
 
+template <typename T>
+bool gates_vec_launch(const KdaGatesParams& p, hipStream_t s) {
+  const int lph = p.K / 8;
+  const uintptr_t al = reinterpret_cast<uintptr_t>(p.proj) | reinterpret_cast<uintptr_t>(p.gl) |
+                       reinterpret_cast<uintptr_t>(p.q) | reinterpret_cast<uintptr_t>(p.k) |
+                       reinterpret_cast<uintptr_t>(p.v) | reinterpret_cast<uintptr_t>(p.g);
+  if (p.K % 8 || lph < 1 || lph > 64 || (lph & (lph - 1)) || (p.HV * p.V) % 8 || al % 16 ||
+      p.ld_proj % 8 || p.ld_gl % 8)
+    return false;
+  const long long rows = (long long)p.B * p.T;
+  const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+  switch (lph) {
+    case 1: hipLaunchKernelGGL((kda_gates_vec_kernel<T, 1>), grid, block, 0, s, p, rows); break;
+    case 2: hipLaunchKernelGGL((kda_gates_vec_kernel<T, 2>), grid, block, 0, s, p, rows); break;
+    case 4: hipLaunchKernelGGL((kda_gates_vec_kernel<T, 4>), grid, block, 0, s, p, rows); break;
+    case 8: hipLaunchKernelGGL((kda_gates_vec_kernel<T, 8>), grid, block, 0, s, p, rows); break;
+    case 16: hipLaunchKernelGGL((kda_gates_vec_kernel<T, 16>), grid, block, 0, s, p, rows); break;
+    case 32: hipLaunchKernelGGL((kda_gates_vec_kernel<T, 32>), grid, block, 0, s, p, rows); break;
+    default: hipLaunchKernelGGL((kda_gates_vec_kernel<T, 64>), grid, block, 0, s, p, rows); break;
+  }
+  return true;
+}
+
 hipError_t kda_gates_dispatch(const KdaGatesParams& p, int dtype, hipStream_t s) {
+  // 16-byte rows of 16-bit values: the wave-per-row kernel
+  if (dtype == DT_BF16 && gates_vec_launch<bf16_t>(p, s)) return hipGetLastError();
+  if (dtype == DT_F16 && gates_vec_launch<_Float16>(p, s)) return hipGetLastError();
   const int slices = (max(p.HV * p.V, p.HV * p.K) + 1023) / 1024;
   const dim3 grid((unsigned)((long long)p.B * p.T), (unsigned)(gates_qk_units(p.H) + max(slices, 1))), block(256);
   if (dtype == DT_F32)

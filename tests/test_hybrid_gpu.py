@@ -86,12 +86,16 @@ def test_short_conv(dev, dtype, d, T, with_lb):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("H,HV,K,V", [(2, 2, 64, 64), (2, 4, 128, 64), (16, 16, 128, 128),
-                                      (1, 1, 40, 24)])
-def test_kda_gates(dev, dtype, H, HV, K, V):
+                                      (1, 1, 40, 24), (2, 2, 16, 16), (3, 5, 8, 8)])
+@pytest.mark.parametrize("aligned", [False, True])
+def test_kda_gates(dev, dtype, H, HV, K, V, aligned):
+    """Odd row strides take the element-wise kernel; rows of whole 16-byte
+    pieces (bf16, K / 8 a power of two) the wave-per-row kernel."""
     from kch import _lib
     rng = np.random.default_rng(H * K + V)
     B, T = 2, 9
-    width = 2 * H * K + HV * V + HV + K + 3  # plus the gate down-projection and slack
+    width = 2 * H * K + HV * V + HV + K  # plus the gate down-projection
+    width += (8 + (-width) % 8) if aligned else 3  # and slack
     proj = torch.from_numpy((2 * rng.standard_normal((B, T, width))).astype(np.float32))
     proj = proj.to(dev, dtype)
     gl = torch.from_numpy((8 * rng.standard_normal((B, T, HV * K))).astype(np.float32)).to(dev, dtype)
@@ -117,6 +121,31 @@ def test_kda_gates(dev, dtype, H, HV, K, V):
         if dtype == torch.bfloat16:
             exact = np.mean(gn == ref)
             assert exact >= 0.99, f"{name}: only {exact:.4f} of the elements bit-identical"
+
+
+@pytest.mark.parametrize("dtype,wdtype", [(torch.bfloat16, torch.float32),
+                                          (torch.bfloat16, torch.bfloat16),
+                                          (torch.float16, torch.float32)])
+@pytest.mark.parametrize("rows,d", [(1, 64), (37, 2048), (5, 4096), (6, 1000), (3, 200)])
+@pytest.mark.parametrize("bias", [True, False])
+def test_layer_norm(dev, dtype, wdtype, rows, d, bias):
+    """kch_layer_norm against torch's fp32 LayerNorm of the same inputs, rounded
+    once to the output dtype: the two may differ by the fp32 summation order
+    of the mean and variance, at most one output ulp."""
+    from kch import _lib
+    g = torch.Generator().manual_seed(rows * d)
+    x = (3 * torch.randn(rows, d, generator=g) + 0.5).to(dev, dtype)
+    w = (1 + 0.1 * torch.randn(d, generator=g)).to(dev, wdtype)
+    b = (0.1 * torch.randn(d, generator=g)).to(dev, wdtype) if bias else None
+    out = torch.empty_like(x)
+    _lib.call("kch_layer_norm", _lib.ptr(x), _lib.ptr(w), _lib.ptr(b), _lib.ptr(out), rows, d, 1e-5,
+              _lib.dtype_code("t", dtype), _lib.dtype_code("t", wdtype), _lib.stream_of(x))
+    ref = torch.nn.functional.layer_norm(x.float(), (d,), w.float(), None if b is None else b.float(),
+                                         1e-5)
+    ulp = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10  # one ulp, relative
+    err = (out.float() - ref).abs()
+    assert bool((err <= ulp * ref.abs() + 1e-5).all()), float((err / (ref.abs() + 1e-6)).max())
+    assert float((out.float() == ref.to(dtype).float()).float().mean()) >= 0.99
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
