@@ -601,7 +601,7 @@ __global__ __launch_bounds__(256, 2) void kda_prep_kernel(KdaParams p, SplitPtrs
 }
 
 template <int K, int BV, typename OutT>
-__global__ __launch_bounds__(256, BV == 32 ? 2 : 1) void kda_state_kernel(KdaParams p, SplitPtrs ws) {
+__global__ __launch_bounds__(256, 1) void kda_state_kernel(KdaParams p, SplitPtrs ws) {
   constexpr int KS = K / 32, CT = BV / 16, RT = K / 64;
   constexpr int LDO = BV + 8;  // sO row stride: row = token
   // sS (row = value column, K channels) and sVn (row = value column, C tokens)
@@ -850,15 +850,32 @@ SplitSizes split_sizes(int B, int T, int HV, int K, int V) {
   return z;
 }
 
+int cu_count() {
+  // multiprocessor count of each device, queried once
+  static int counts[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (counts[dev] == 0) {
+    int c = 256;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+    counts[dev] = c;
+  }
+  return counts[dev];
+}
+
 template <int K, int V, typename InT>
 hipError_t launch_split(const KdaParams& p, SplitPtrs w, hipStream_t s) {
-  constexpr int BV = 64;
   const int NT = (p.T + C - 1) / C;
   hipLaunchKernelGGL((kda_prep_kernel<K, V, InT>), dim3(p.B * p.HV * NT), dim3(256), 0, s, p, w);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((kda_state_kernel<K, BV, InT>), dim3(p.B * p.HV * (V / BV)), dim3(256), 0, s,
-                     p, w);
+  // 32-column V slices when 64-column ones would leave more than half of the
+  // CUs without a state workgroup (one workgroup per CU either way: the
+  // operand sets need the whole register file)
+  if (V == 128 && 2LL * p.B * p.HV * (V / 64) <= cu_count())
+    hipLaunchKernelGGL((kda_state_kernel<K, 32, InT>), dim3(p.B * p.HV * (V / 32)), dim3(256), 0, s, p, w);
+  else
+    hipLaunchKernelGGL((kda_state_kernel<K, 64, InT>), dim3(p.B * p.HV * (V / 64)), dim3(256), 0, s, p, w);
   return hipGetLastError();
 }
 
