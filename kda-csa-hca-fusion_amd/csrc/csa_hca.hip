@@ -339,44 +339,54 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(AttnParams p) {
     wbase = max(t - p.win + 1, 0);
     n_win = t - wbase + 1;
   }
-  const int n_tot = (p.nb > 0 ? n_main : 0) + n_win;
-  if (n_tot > 0) {
-    const int nm = p.nb > 0 ? n_main : 0;
-    // rows of padding lanes must be readable: a compressed row when any exists
-    const bf16_t* dflt = p.nb > 0 ? kv : loc;
+  const int nm = p.nb > 0 ? n_main : 0;
+  // the compressed rows are padded to whole 32-row steps (padding rows are
+  // masked), so that every step is wholly compressed or wholly window rows
+  const int nm_pad = (nm + 31) & ~31;
+  const int n_tot = nm_pad + n_win;
+  if (nm + n_win > 0) {
+    // Rows are read through two buffer resources, the compressed rows of this
+    // batch row and its window rows, with 32-bit byte offsets: an offset past
+    // a resource's end (a -1 slot, a block index out of range, a padding row)
+    // reads zeros, so a row address is one multiply-add and no row needs a
+    // readable default.
+    constexpr int ROWB = HD * 2;  // bytes per row
+    const __amdgpu_buffer_rsrc_t rs_kv = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<bf16_t*>(kv), 0, p.nb > 0 ? p.nb * ROWB : 0, 0x00020000);
+    const int nloc = n_win > 0 ? (p.local_count >= 0 ? p.local_count : T) : 0;
+    const __amdgpu_buffer_rsrc_t rs_loc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<bf16_t*>(loc ? loc : kv), 0, nloc * ROWB, 0x00020000);
+    const int lane_off = 16 * (lane % W::TPR);
     // Selected block indices come 64 at a time, one per lane, from a load issued
     // a group ahead of its use (so that waiting for it never waits for the row
     // loads issued after it); loads are clamped, read entries are only those of
-    // rows below n_main. Without indices a readable word is loaded.
+    // rows below n_main.
     const bool has_idx = SPARSE && nm > 0;
-    const int* ip = has_idx ? p.idx + (size_t)qi * p.topk : reinterpret_cast<const int*>(dflt);
+    const int* ip = has_idx ? p.idx + (size_t)qi * p.topk : nullptr;
     const int ilim = has_idx ? nm : 1;
-    auto idx_group = [&](int g) { return ip[min(64 * g + lane, ilim - 1)]; };
-    // row j of the query (any row of the index group ig) -> its address; ok
-    // when the row is valid (padding rows read the default row)
-    auto row_ptr = [&](int j, int ig, bool& ok) {
-      const int sel = SPARSE ? __shfl(ig, j & 63) : j;
-      const bf16_t* row = dflt;
-      ok = false;
-      if (j < nm) {
-        ok = sel >= 0 && sel < p.nb;
-        if (ok) row = kv + (size_t)sel * HD;
-      } else if (j < n_tot) {
-        ok = true;
-        row = loc + (size_t)(wbase + j - nm) * HD;
-      }
-      return row;
-    };
+    auto idx_group = [&](int g) { return has_idx ? ip[min(64 * g + lane, ilim - 1)] : 0; };
     // 32-row step st (of the 64-row index group ig), gathered row-major;
     // returns the step's validity bits (bit r: row 32 st + r)
     auto load_step = [&](int st, int ig, unsigned& valid) {
       typename W::Rows rr;
       valid = 0u;
+      const int j0 = 32 * st;
+      const bool main_step = j0 < nm_pad;  // uniform
 #pragma unroll
       for (int i = 0; i < W::NLI; ++i) {
+        const int j = j0 + i * W::RPI + lane / W::TPR;
         bool ok;
-        const bf16_t* row = row_ptr(32 * st + i * W::RPI + lane / W::TPR, ig, ok);
-        rr.v[i] = *reinterpret_cast<const typename W::u32x4*>(row + 8 * (lane % W::TPR));
+        unsigned off;
+        if (main_step) {
+          const int sel = SPARSE ? __shfl(ig, j & 63) : j;
+          ok = j < nm && sel >= 0 && sel < p.nb;
+          off = ok ? (unsigned)(sel * ROWB + lane_off) : 0xffffffffu;
+        } else {
+          const int jw = j - nm_pad;
+          ok = jw < n_win;
+          off = ok ? (unsigned)((wbase + jw) * ROWB + lane_off) : 0xffffffffu;
+        }
+        rr.v[i] = __builtin_amdgcn_raw_buffer_load_b128(main_step ? rs_kv : rs_loc, (int)off, 0, 0);
         const unsigned long long m = __ballot(ok);
 #pragma unroll
         for (int k = 0; k < W::RPI; ++k)
