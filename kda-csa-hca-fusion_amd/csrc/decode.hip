@@ -943,7 +943,10 @@ __global__ __launch_bounds__(256) void idx_merge_kernel(DecodeIdxParams p) {
   const int c0 = min(p.rb, topk);
   const int cl = na > 0 ? min(nb - (na - 1) * p.rb, topk) : 0;
   const int N = na > 0 ? (na - 1) * c0 + cl : 0;
+  // (when every range holds topk candidates they are contiguous)
+  const bool contig = c0 == topk;
   auto gval = [&](int f) {
+    if (contig) return src[f];
     const int r = min(f / c0, na - 1);
     return src[(size_t)r * topk + (f - r * c0)];
   };
@@ -958,7 +961,7 @@ __global__ __launch_bounds__(256) void idx_merge_kernel(DecodeIdxParams p) {
       // stream the candidates once: those at or above the estimate into sv
       if (tid == 0) counter[0] = 0;
       __syncthreads();
-      constexpr int U = 8;
+      constexpr int U = 32;  // loads in flight per thread
       const int lane = tid & 63;
       for (int base = wave_id() * 64 * U; base < N; base += 256 * U) {
         u64 v[U];
