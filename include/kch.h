@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define KCH_ABI_VERSION 11
+#define KCH_ABI_VERSION 12
 
 #define KCH_OK 0
 #define KCH_ERR_INVALID 1     /* bad pointer / shape / argument */
@@ -90,6 +90,18 @@ int kch_kda_recurrent_fwd(const void* q, const void* k, const void* v, const voi
                           const void* beta, const float* s0, void* o, float* s_out,
                           int B, int T, int H, int HV, int K, int V, float scale,
                           float g_clamp_min, int dtype, void* stream);
+
+/*
+ * The same recurrence for float64 inputs: fp64 arithmetic and fp64 states
+ * (s0, s_out [B, HV, K, V]), scale and gate clamp in fp64, as the reference
+ * computes fp64 inputs (ops_kda.py:125-127, 175-267). naive_chunk_kda on
+ * fp64 inputs is the same function (ops_kda.py:464-494) and runs here too.
+ * Coverage: K in {16,32,64,128,256}; any V.
+ */
+int kch_kda_recurrent_fwd_f64(const double* q, const double* k, const double* v, const double* g,
+                              const double* beta, const double* s0, double* o, double* s_out,
+                              int B, int T, int H, int HV, int K, int V, double scale,
+                              double g_clamp_min, void* stream);
 
 
 /*

@@ -186,6 +186,40 @@ int kch_kda_recurrent_fwd(const void* q, const void* k, const void* v, const voi
   return hip_status(fn, kch::kda_recurrent_dispatch(p, dtype, (hipStream_t)stream));
 }
 
+int kch_kda_recurrent_fwd_f64(const double* q, const double* k, const double* v, const double* g,
+                              const double* beta, const double* s0, double* o, double* s_out, int B,
+                              int T, int H, int HV, int K, int V, double scale, double g_clamp_min,
+                              void* stream) {
+  const char* fn = "kch_kda_recurrent_fwd_f64";
+  int rc = check_kda_common(fn, q, k, v, g, beta, o, B, T, H, HV, K, V, KCH_DT_F32);
+  if (rc) return rc;
+  if (K != 16 && K != 32 && K != 64 && K != 128 && K != 256)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: K=%d not supported (16/32/64/128/256)", fn, K);
+  if (std::isnan(g_clamp_min) || std::isnan(scale))
+    return fail(KCH_ERR_INVALID, "%s: g_clamp_min or scale is NaN", fn);
+  rc = check_kda_pointers(fn, q, k, v, g, beta, o, B, T);
+  if (rc) return rc;
+  if ((long long)T * HV * (K > V ? K : V) >= (1LL << 31) || (long long)T * H * K >= (1LL << 31))
+    return fail(KCH_ERR_UNSUPPORTED, "%s: T * heads * head_dim must stay below 2^31", fn);
+  if (B == 0) return KCH_OK;
+  if (T == 0) {
+    if (s_out) {
+      // zeros by the fill kernel, not a memset node (graph-capture safe)
+      const size_t n = (size_t)B * HV * K * V * sizeof(double);
+      hipError_t e = s0 ? hipMemcpyAsync(s_out, s0, n, hipMemcpyDeviceToDevice, (hipStream_t)stream)
+                        : kch::fill_u32(s_out, (long long)(n / 4), 0u, (hipStream_t)stream);
+      return hip_status(fn, e);
+    }
+    return KCH_OK;
+  }
+  kch::KdaParams p = make_kda(q, k, v, g, beta, reinterpret_cast<const float*>(s0), o,
+                              reinterpret_cast<float*>(s_out), B, T, H, HV, K, V, (float)scale,
+                              (float)g_clamp_min);
+  p.scale64 = scale;
+  p.g_clamp_min64 = g_clamp_min;
+  return hip_status(fn, kch::kda_recurrent_f64_dispatch(p, (hipStream_t)stream));
+}
+
 int kch_compress(const void* C, long long ldC, const void* Z, long long ldZ, const float* B_pos,
                  float* out_raw, void* out_key, int key_f32, int normalize, void* local, int B,
                  int T, int m, int c, int dtype, void* stream) {

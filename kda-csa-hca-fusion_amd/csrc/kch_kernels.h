@@ -21,9 +21,15 @@ struct KdaParams {
   int B, T, H, HV, K, V;
   float scale;
   float g_clamp_min;  // -inf disables the clamp
+  // the fp64 recurrence (kda_recurrent_f64_dispatch): scale and clamp in fp64;
+  // s0 and s_out then point to fp64 states
+  double scale64 = 0.0;
+  double g_clamp_min64 = 0.0;
 };
 
 hipError_t kda_chunk_dispatch(const KdaParams& p, int dtype, hipStream_t stream);
+// fp64 inputs, state and arithmetic (kda_recurrent.hip)
+hipError_t kda_recurrent_f64_dispatch(const KdaParams& p, hipStream_t stream);
 // bf16 / fp16 inputs, K in {64, 128}, V a multiple of 64 (kda_chunk_lp.hip)
 hipError_t kda_chunk_lp_dispatch(const KdaParams& p, int dtype, hipStream_t stream);
 hipError_t kda_recurrent_dispatch(const KdaParams& p, int dtype, hipStream_t stream);

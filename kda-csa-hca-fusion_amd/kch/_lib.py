@@ -25,6 +25,7 @@ _P = ctypes.c_void_p
 _I = ctypes.c_int
 _F = ctypes.c_float
 _L = ctypes.c_longlong
+_D = ctypes.c_double
 _SZ = ctypes.c_size_t
 
 # name -> argument types (all return int status)
@@ -32,6 +33,7 @@ _SIGNATURES = {
     "kch_kda_chunk_fwd": [_P] * 8 + [_I] * 6 + [_F, _F, _I, _P],
     "kch_kda_chunk_fwd_ws": [_P] * 8 + [_I] * 6 + [_F, _F, _I, _P, _SZ, _P],
     "kch_kda_recurrent_fwd": [_P] * 8 + [_I] * 6 + [_F, _F, _I, _P],
+    "kch_kda_recurrent_fwd_f64": [_P] * 8 + [_I] * 6 + [_D, _D, _P],
     "kch_compress": [_P, _L, _P, _L, _P, _P, _P, _I, _I, _P, _I, _I, _I, _I, _I, _P],
     "kch_compress_overlapped": [_P, _L, _P, _L, _P, _L, _P, _L, _P, _P, _P, _P, _I, _I, _P,
                                 _I, _I, _I, _I, _I, _P],

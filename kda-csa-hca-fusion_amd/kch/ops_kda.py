@@ -11,8 +11,9 @@ current stream. ``chunk_size`` is validated as in the reference; the result
 does not depend on it (chunking is a reassociation of the same recurrence), and
 the kernel uses its own chunk length.
 
-Not covered: float64 inputs (the reference computes them in fp64) raise
-``NotImplementedError``.
+float64 inputs compute in fp64 with an fp64 state, as in the reference
+(``ops_kda.py:125-127``), on ``kch_kda_recurrent_fwd_f64`` for both operators
+(the chunked form is the same function).
 """
 
 from __future__ import annotations
@@ -120,11 +121,52 @@ def _kernel_kv(entry, K, V, dtype):
     return entry, Kp, Vp
 
 
+def _run_f64(fn_name, q, k, v, g, beta, scale, initial_state, output_final_state, g_clamp_min,
+             state_dtype):
+    """float64 inputs: the fp64 recurrence (fp64 arithmetic and state; the
+    reference's compute dtype for them, ``ops_kda.py:125-127``). K is
+    zero-padded to the kernel's next size as on the other paths."""
+    B, T, H, K = q.shape
+    HV, V = v.shape[2], v.shape[-1]
+    if scale is None:
+        sc = K ** -0.5
+    elif isinstance(scale, torch.Tensor):
+        sc = float(scale.detach().double().item())
+    else:
+        sc = float(scale)
+    Kp = next((n for n in (16, 32, 64, 128, 256) if n >= K), None)
+    if Kp is None:
+        raise NotImplementedError(f"{fn_name}: head dim K={K} > 256 is not supported by the HIP "
+                                  f"kernels")
+    target_state = state_dtype if state_dtype is not None else torch.float64
+    if Kp != K:
+        q, k, g = (F.pad(t, (0, Kp - K)) for t in (q, k, g))
+    q, k, v, g, beta = (t.contiguous() for t in (q, k, v, g, beta))
+    s0 = None
+    if initial_state is not None:
+        s0 = initial_state.to(device=q.device, dtype=torch.float64)
+        if Kp != K:
+            s0 = F.pad(s0, (0, 0, 0, Kp - K))
+        s0 = s0.contiguous()
+    o = torch.empty_like(v)
+    s_out = torch.empty(B, HV, Kp, V, device=q.device, dtype=torch.float64) \
+        if output_final_state else None
+    _lib.call("kch_kda_recurrent_fwd_f64", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g),
+              _lib.ptr(beta), _lib.ptr(s0), _lib.ptr(o), _lib.ptr(s_out), B, T, H, HV, Kp, V, sc,
+              _clamp_value(g_clamp_min), _lib.stream_of(q))
+    if s_out is not None:
+        s_out = s_out[:, :, :K].to(target_state).contiguous()
+    return o, s_out
+
+
 def _run(entry, fn_name, q, k, v, g, beta, scale, initial_state, output_final_state,
          g_clamp_min, state_dtype, chunk_size=None):
     _validate_kda_inputs(q, k, v, g, beta, fn_name)
     _validate_kda_shapes(q, k, v, g, beta, fn_name, chunk_size=chunk_size)
     _lib.require_gpu(fn_name, q, initial_state)
+    if v.dtype == torch.float64:
+        return _run_f64(fn_name, q, k, v, g, beta, scale, initial_state, output_final_state,
+                        g_clamp_min, state_dtype)
     code = _lib.dtype_code(fn_name, v.dtype)
     B, T, H, K = q.shape
     HV, V = v.shape[2], v.shape[-1]

@@ -232,3 +232,58 @@ def test_chunk_exact_path_some_chunks_k128(dev):
     o_ref, s_ref = o_chunk(*host, initial_state=s0.numpy(), chunk_size=64)
     check("o", o, bf16_round(o_ref), "bf16")
     check("state", s, s_ref, "bf16")
+
+
+def make64(seed, B, T, H, HV, K, V, s0_std=0.02):
+    rng = np.random.default_rng(seed)
+    q = l2_normalize(rng.standard_normal((B, T, H, K)))
+    k = l2_normalize(rng.standard_normal((B, T, H, K)))
+    v = rng.standard_normal((B, T, HV, V))
+    g = logsigmoid(rng.standard_normal((B, T, HV, K)))
+    beta = sigmoid(rng.standard_normal((B, T, HV)))
+    s0 = s0_std * rng.standard_normal((B, HV, K, V)) if s0_std else None
+    host = [np.ascontiguousarray(x, np.float64) for x in (q, k, v, g, beta)]
+    return host, s0
+
+
+@pytest.mark.parametrize("B,T,H,HV,K,V", [(2, 70, 2, 2, 64, 64), (1, 200, 2, 4, 128, 128),
+                                          (2, 33, 1, 2, 40, 24), (1, 9, 1, 1, 16, 200)])
+def test_fp64_matches_oracle(dev, B, T, H, HV, K, V):
+    """float64 inputs: fp64 arithmetic and state, as the reference computes
+    them; both operators against the fp64 oracle (recurrence and chunked WY
+    form), to the accumulation-order level of fp64."""
+    import kch
+    host, s0 = make64(B * T + K, B, T, H, HV, K, V)
+    ts = [torch.from_numpy(x).to(dev) for x in host]
+    s0t = torch.from_numpy(s0).to(dev)
+    o_r, s_r = kch.naive_recurrent_kda(*ts, initial_state=s0t, output_final_state=True)
+    o_c, s_c = kch.naive_chunk_kda(*ts, initial_state=s0t, output_final_state=True)
+    torch.cuda.synchronize()
+    assert o_r.dtype == torch.float64 and s_r.dtype == torch.float64
+    ref_o, ref_s = o_rec(*host, initial_state=s0, compute=np.float64)
+    ch_o, ch_s = o_chunk(*host, initial_state=s0, chunk_size=64, compute=np.float64)
+    for name, got, ref in (("o rec", o_r, ref_o), ("S rec", s_r, ref_s), ("o chunk", o_c, ch_o),
+                           ("S chunk", s_c, ch_s)):
+        err = float(np.abs(got.cpu().numpy() - ref).max())
+        assert err < 1e-10, f"{name}: max abs err {err:.3e}"
+
+
+def test_fp64_options(dev):
+    """fp64: no initial state, the gate clamp off, a requested fp32 state, and
+    T = 0 (the initial state passes through)."""
+    import kch
+    host, s0 = make64(5, 1, 21, 2, 2, 64, 32, s0_std=0)
+    host[3] = host[3] * 30.0  # gates below the default clamp
+    ts = [torch.from_numpy(x).to(dev) for x in host]
+    o, s = kch.naive_recurrent_kda(*ts, output_final_state=True, g_clamp_min=float("-inf"),
+                                   state_dtype=torch.float32)
+    torch.cuda.synchronize()
+    ref_o, ref_s = o_rec(*host, g_clamp_min=-np.inf, compute=np.float64)
+    assert s.dtype == torch.float32
+    assert float(np.abs(o.cpu().numpy() - ref_o).max()) < 1e-10
+    assert float(np.abs(s.double().cpu().numpy() - ref_s).max()) < 1e-6
+    z = [t[:, :0] for t in ts]
+    s_init = torch.randn(1, 2, 64, 32, device=dev, dtype=torch.float64)
+    o0, s0_out = kch.naive_chunk_kda(*z, initial_state=s_init, output_final_state=True)
+    torch.cuda.synchronize()
+    assert o0.shape == (1, 0, 2, 32) and torch.equal(s0_out, s_init)
