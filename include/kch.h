@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define KCH_ABI_VERSION 12
+#define KCH_ABI_VERSION 13
 
 #define KCH_OK 0
 #define KCH_ERR_INVALID 1     /* bad pointer / shape / argument */
@@ -102,6 +102,31 @@ int kch_kda_recurrent_fwd_f64(const double* q, const double* k, const double* v,
                               const double* beta, const double* s0, double* o, double* s_out,
                               int B, int T, int H, int HV, int K, int V, double scale,
                               double g_clamp_min, void* stream);
+
+/*
+ * Gradients of the KDA recurrence: the backward of naive_recurrent_kda
+ * (ops_kda.py:175-267), which the reference obtains from autograd and tests in
+ * run_correctness.py:765-833 (finite differences) and :1032-1092 (chunk
+ * gradients == recurrent gradients; naive_chunk_kda, ops_kda.py:464-494, is
+ * the same function and has these gradients too).
+ * Inputs: the forward's q, k [B,T,H,K], v [B,T,HV,V], g [B,T,HV,K],
+ * beta [B,T,HV] (dtype KCH_DT_F32 / BF16 / F16, or KCH_DT_F64 = 3), s0
+ * [B,HV,K,V] or NULL, d_o = dL/do [B,T,HV,V] (input dtype), ds_final =
+ * dL/dS_T [B,HV,K,V] or NULL. States are fp32, fp64 for fp64 inputs.
+ * Outputs: dq, dk, dv, dg, dbeta in the input dtype, laid out as their
+ * inputs; ds0 = dL/dS0 or NULL. dg is zero where g < g_clamp_min (the clamp's
+ * gradient). Arithmetic in fp32 (fp64 for fp64). ws: 256-byte aligned, at
+ * least kch_kda_recurrent_bwd_ws_bytes bytes. Coverage: K in
+ * {16,32,64,128,256}, any V, T >= 1.
+ */
+#define KCH_DT_F64 3
+size_t kch_kda_recurrent_bwd_ws_bytes(int B, int T, int HV, int K, int V, int dtype);
+int kch_kda_recurrent_bwd(const void* q, const void* k, const void* v, const void* g,
+                          const void* beta, const void* s0, const void* d_o,
+                          const void* ds_final, void* dq, void* dk, void* dv, void* dg,
+                          void* dbeta, void* ds0, int B, int T, int H, int HV, int K, int V,
+                          double scale, double g_clamp_min, int dtype, void* ws,
+                          size_t ws_bytes, void* stream);
 
 
 /*

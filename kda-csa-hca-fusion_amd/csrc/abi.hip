@@ -220,6 +220,51 @@ int kch_kda_recurrent_fwd_f64(const double* q, const double* k, const double* v,
   return hip_status(fn, kch::kda_recurrent_f64_dispatch(p, (hipStream_t)stream));
 }
 
+size_t kch_kda_recurrent_bwd_ws_bytes(int B, int T, int HV, int K, int V, int dtype) {
+  if (B <= 0 || T <= 0 || HV < 1 || V < 1 || (K != 16 && K != 32 && K != 64 && K != 128 && K != 256))
+    return 0;
+  if (!dtype_ok(dtype) && dtype != KCH_DT_F64) return 0;
+  return kch::kda_bwd_ws_bytes(B, T, HV, K, V, dtype == KCH_DT_F64);
+}
+
+int kch_kda_recurrent_bwd(const void* q, const void* k, const void* v, const void* g,
+                          const void* beta, const void* s0, const void* d_o,
+                          const void* ds_final, void* dq, void* dk, void* dv, void* dg,
+                          void* dbeta, void* ds0, int B, int T, int H, int HV, int K, int V,
+                          double scale, double g_clamp_min, int dtype, void* ws,
+                          size_t ws_bytes, void* stream) {
+  const char* fn = "kch_kda_recurrent_bwd";
+  if (!dtype_ok(dtype) && dtype != KCH_DT_F64)
+    return fail(KCH_ERR_INVALID, "%s: unknown dtype %d", fn, dtype);
+  if (B < 0 || T < 1 || H < 1 || HV < 1 || K < 1 || V < 1)
+    return fail(KCH_ERR_INVALID, "%s: bad sizes B=%d T=%d H=%d HV=%d K=%d V=%d (T >= 1)", fn, B, T,
+                H, HV, K, V);
+  if (HV % H) return fail(KCH_ERR_INVALID, "%s: HV=%d must be divisible by H=%d", fn, HV, H);
+  if (K != 16 && K != 32 && K != 64 && K != 128 && K != 256)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: K=%d not supported (16/32/64/128/256)", fn, K);
+  if (std::isnan(g_clamp_min) || std::isnan(scale))
+    return fail(KCH_ERR_INVALID, "%s: g_clamp_min or scale is NaN", fn);
+  if ((long long)T * HV * (K > V ? K : V) >= (1LL << 31) || (long long)T * H * K >= (1LL << 31) ||
+      (long long)B * T * HV * ((V + 31) / 32) * (3 * K + 1) >= (1LL << 40))
+    return fail(KCH_ERR_UNSUPPORTED, "%s: T * heads * head_dim must stay below 2^31", fn);
+  if (B == 0) return KCH_OK;
+  if (!q || !k || !v || !g || !beta || !d_o || !dq || !dk || !dv || !dg || !dbeta)
+    return fail(KCH_ERR_INVALID, "%s: null tensor pointer", fn);
+  const size_t need = kch_kda_recurrent_bwd_ws_bytes(B, T, HV, K, V, dtype);
+  if (!ws || ws_bytes < need)
+    return fail(KCH_ERR_INVALID, "%s: workspace of %zu bytes required, got %zu", fn, need,
+                ws ? ws_bytes : (size_t)0);
+  if ((uintptr_t)ws & 255) return fail(KCH_ERR_INVALID, "%s: workspace must be 256-byte aligned", fn);
+  kch::KdaBwdParams p;
+  p.q = q; p.k = k; p.v = v; p.g = g; p.beta = beta; p.s0 = s0;
+  p.d_o = d_o; p.ds_final = ds_final;
+  p.dq = dq; p.dk = dk; p.dv = dv; p.dg = dg; p.dbeta = dbeta; p.ds0 = ds0;
+  p.B = B; p.T = T; p.H = H; p.HV = HV; p.K = K; p.V = V;
+  p.scale = scale;
+  p.g_clamp_min = g_clamp_min;
+  return hip_status(fn, kch::kda_bwd_dispatch(p, dtype, ws, (hipStream_t)stream));
+}
+
 int kch_compress(const void* C, long long ldC, const void* Z, long long ldZ, const float* B_pos,
                  float* out_raw, void* out_key, int key_f32, int normalize, void* local, int B,
                  int T, int m, int c, int dtype, void* stream) {

@@ -35,8 +35,9 @@ __device__ __forceinline__ void store_stream16(void* dst, u32x4_t v) {
   __builtin_nontemporal_store(v, reinterpret_cast<u32x4_t*>(dst));
 }
 
-// Input storage types accepted by the C-ABI (dtype enum: 0 fp32, 1 bf16, 2 fp16).
-enum DType : int { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
+// Input storage types accepted by the C-ABI (dtype enum: 0 fp32, 1 bf16, 2 fp16;
+// 3 fp64 where an entry point says so).
+enum DType : int { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2, DT_F64 = 3 };
 
 __device__ __forceinline__ float to_f32(float x) { return x; }
 __device__ __forceinline__ float to_f32(bf16_t x) { return (float)x; }

@@ -27,6 +27,33 @@ struct KdaParams {
   double g_clamp_min64 = 0.0;
 };
 
+// Gradients of the KDA recurrence (kda_backward.hip). States (s0, ds_final,
+// ds0) are fp32, or fp64 for fp64 inputs; gradients are in the input dtype.
+struct KdaBwdParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* g;
+  const void* beta;
+  const void* s0;        // initial state or null
+  const void* d_o;       // dL/do [B,T,HV,V]
+  const void* ds_final;  // dL/dS_T [B,HV,K,V] or null
+  void* dq;
+  void* dk;
+  void* dv;
+  void* dg;
+  void* dbeta;
+  void* ds0;             // dL/dS0 or null
+  void* ck = nullptr;    // workspace regions, set by kda_bwd_dispatch
+  void* part = nullptr;
+  int B, T, H, HV, K, V;
+  double scale, g_clamp_min;  // -inf disables the clamp
+};
+size_t kda_bwd_ws_bytes(int B, int T, int HV, int K, int V, bool f64);
+// K in {16, 32, 64, 128, 256}; dtype DT_F32 / DT_BF16 / DT_F16 / DT_F64; ws
+// 256-byte aligned, kda_bwd_ws_bytes bytes
+hipError_t kda_bwd_dispatch(KdaBwdParams p, int dtype, void* ws, hipStream_t stream);
+
 hipError_t kda_chunk_dispatch(const KdaParams& p, int dtype, hipStream_t stream);
 // fp64 inputs, state and arithmetic (kda_recurrent.hip)
 hipError_t kda_recurrent_f64_dispatch(const KdaParams& p, hipStream_t stream);

@@ -1,0 +1,360 @@
+// KDA recurrence backward for gfx950: the gradients of naive_recurrent_kda
+// (/root/reference/ops_kda.py:175-267), the function the reference's own
+// gradient tests differentiate (run_correctness.py:765-833, 1032-1092). The
+// chunked form computes the same function, so its gradients are these too.
+//
+// Forward, per (b, hv) and token t (q^ = scale q, a = exp(max(g, clamp))):
+//   Sd = diag(a) S;   u = v - Sd^T k;   d = beta u;   S' = Sd + k d^T;   o = S'^T q^
+// Backward, tokens in reverse, carrying dS = dL/dS' from the later tokens:
+//   dSt = dS + q^ do^T
+//   dq^ = S' do;   dd = dSt^T k;   du = beta dd;   dv = du;   dbeta = dd . u
+//   dk  = dSt d - Sd du
+//   dSd = dSt - k du^T;   dg = rowsum(dSd * Sd)  (zero where g < clamp)
+//   dS  = diag(a) dSd
+// The columns of the state are independent in both directions; only dq^,
+// dk, dg and dbeta sum over columns.
+//
+// kda_recurrent_bwd_kernel  one workgroup per (b, hv, 32-column slice of V),
+//   thread (column tid/8, phase tid%8) owns rows phase + 8 i of its column,
+//   as in the forward kernel. Pass 1 runs the recurrence forward and stores
+//   the state at the start of every segment of SEG tokens (a checkpoint in the
+//   workspace). Pass 2 walks the segments in reverse: it reloads the
+//   checkpoint, recomputes the segment's decayed states Sd into registers,
+//   then runs the token backward in reverse. Per token the column sums of
+//   dq^, dk, dg (and dbeta) are formed within the wave by lane shuffles, the
+//   four waves' sums meet in LDS, and each slice writes one partial record
+//   per (b, t, hv) to the workspace.
+// kda_bwd_reduce_kernel     one workgroup per (b, t, h): sums the slices'
+//   partials and the value heads of a key head (q and k are shared by the
+//   HV / H value heads), applies scale and the clamp mask, writes dq, dk, dg,
+//   dbeta in the input dtype.
+// Arithmetic is fp32 for fp32 / bf16 / fp16 inputs and fp64 for fp64 inputs,
+// as in the forward (ops_kda.py:125-127).
+
+#include "kch_device.h"
+#include "kch_kernels.h"
+
+namespace kch {
+
+namespace {
+
+template <typename AccT, typename T>
+__device__ __forceinline__ AccT acc_of(T x) {
+  if constexpr (sizeof(T) == 8) return (AccT)x;
+  else return (AccT)to_f32(x);
+}
+
+template <typename OutT, typename AccT>
+__device__ __forceinline__ OutT out_of(AccT x) {
+  if constexpr (sizeof(OutT) == 8) return (OutT)x;
+  else return from_f32<OutT>((float)x);
+}
+
+// tokens per checkpoint segment: the segment's decayed states stay in
+// registers (SEG * K / 8 values per thread, at most 128 VGPRs)
+template <int K, typename AccT>
+constexpr int seg_len() {
+  constexpr int per_tok = K / 8 * (int)(sizeof(AccT) / 4);
+  return 128 / per_tok > 16 ? 16 : 128 / per_tok;
+}
+
+template <int K, typename InT, typename AccT>
+__global__ __launch_bounds__(256) void kda_recurrent_bwd_kernel(KdaBwdParams p) {
+  constexpr int RPT = K / 8;
+  constexpr int SEG = seg_len<K, AccT>();
+  constexpr int PS = 3 * K + 1;  // partial record: dq^ [K] | dk [K] | dg [K] | dbeta
+  constexpr bool F64 = sizeof(AccT) == 8;
+  __shared__ AccT sq[SEG][K], sk[SEG][K], sa[SEG][K], sb[SEG];
+  __shared__ AccT sw[SEG][4][3][K];
+  __shared__ AccT sbw[SEG][4];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nvs = (p.V + 31) / 32;
+  const int vs = blockIdx.x % nvs;
+  const int bh = blockIdx.x / nvs;
+  const int hv = bh % p.HV, b = bh / p.HV, h = hv / (p.HV / p.H);
+  const int cl = tid >> 3, ph = tid & 7;
+  const int col = vs * 32 + cl;
+  const bool okc = col < p.V;
+  const int T = p.T;
+  const int nseg = (T + SEG - 1) / SEG;
+  const InT* gq = static_cast<const InT*>(p.q);
+  const InT* gk = static_cast<const InT*>(p.k);
+  const InT* gv = static_cast<const InT*>(p.v);
+  const InT* gg = static_cast<const InT*>(p.g);
+  const InT* gb = static_cast<const InT*>(p.beta);
+  const InT* gdo = static_cast<const InT*>(p.d_o);
+  const AccT* s0 = static_cast<const AccT*>(p.s0);
+  const AccT* dsT = static_cast<const AccT*>(p.ds_final);
+  AccT* ds0 = static_cast<AccT*>(p.ds0);
+  AccT* ck = static_cast<AccT*>(p.ck) + (size_t)blockIdx.x * nseg * K * 32;
+  AccT* part = static_cast<AccT*>(p.part);
+  const AccT scale = (AccT)p.scale;
+  const AccT clampv = (AccT)p.g_clamp_min;
+  const bool do_clamp = p.g_clamp_min > -INFINITY;
+  const size_t sbase = (size_t)(b * p.HV + hv) * K * p.V;
+
+  auto red8 = [](AccT x) {  // over the 8 phases of a column
+    x += __shfl_xor(x, 1);
+    x += __shfl_xor(x, 2);
+    x += __shfl_xor(x, 4);
+    return x;
+  };
+  auto colsum = [](AccT x) {  // over the 8 columns of a wave
+    x += __shfl_xor(x, 8);
+    x += __shfl_xor(x, 16);
+    x += __shfl_xor(x, 32);
+    return x;
+  };
+  // the segment's key, decay and beta rows (and scaled q) into LDS
+  auto load_seg = [&](int t0, int len, bool with_q) {
+    for (int idx = tid; idx < len * K; idx += 256) {
+      const int j = idx / K, c = idx % K;
+      const int t = t0 + j;
+      const size_t qk = ((size_t)(b * T + t) * p.H + h) * K + c;
+      const size_t gi = ((size_t)(b * T + t) * p.HV + hv) * K + c;
+      sk[j][c] = acc_of<AccT>(gk[qk]);
+      if (with_q) sq[j][c] = acc_of<AccT>(gq[qk]) * scale;
+      AccT gt = acc_of<AccT>(gg[gi]);
+      if (do_clamp) gt = gt > clampv ? gt : clampv;
+      if constexpr (F64) sa[j][c] = exp(gt);
+      else sa[j][c] = expf(gt);
+    }
+    if (tid < len) sb[tid] = acc_of<AccT>(gb[(size_t)(b * T + t0 + tid) * p.HV + hv]);
+  };
+  auto col_val = [&](const InT* base, int t) -> AccT {
+    return okc ? acc_of<AccT>(base[((size_t)(b * T + t) * p.HV + hv) * p.V + col]) : (AccT)0;
+  };
+
+  // ---- pass 1: forward, a checkpoint at the start of every segment ----
+  AccT S[RPT];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i)
+    S[i] = (s0 && okc) ? s0[sbase + (size_t)(ph + 8 * i) * p.V + col] : (AccT)0;
+  for (int s = 0; s < nseg; ++s) {
+    const int t0 = s * SEG, len = min(SEG, T - t0);
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) ck[((size_t)s * K + ph + 8 * i) * 32 + cl] = S[i];
+    __syncthreads();  // the previous segment's LDS rows are consumed
+    load_seg(t0, len, false);
+    AccT vv[SEG];
+#pragma unroll
+    for (int j = 0; j < SEG; ++j) vv[j] = j < len ? col_val(gv, t0 + j) : (AccT)0;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < SEG; ++j) {
+      if (j < len) {
+        AccT kS = 0;
+#pragma unroll
+        for (int i = 0; i < RPT; ++i) {
+          S[i] *= sa[j][ph + 8 * i];
+          kS += sk[j][ph + 8 * i] * S[i];
+        }
+        kS = red8(kS);
+        const AccT d = sb[j] * (vv[j] - kS);
+#pragma unroll
+        for (int i = 0; i < RPT; ++i) S[i] += sk[j][ph + 8 * i] * d;
+      }
+    }
+  }
+  // the checkpoints are re-read by the thread that wrote them
+  __threadfence_block();
+
+  // ---- pass 2: segments in reverse ----
+  AccT dS[RPT];
+#pragma unroll
+  for (int i = 0; i < RPT; ++i)
+    dS[i] = (dsT && okc) ? dsT[sbase + (size_t)(ph + 8 * i) * p.V + col] : (AccT)0;
+  InT* gdv = static_cast<InT*>(p.dv);
+  for (int s = nseg - 1; s >= 0; --s) {
+    const int t0 = s * SEG, len = min(SEG, T - t0);
+    __syncthreads();  // LDS of the previous segment is free
+    load_seg(t0, len, true);
+    AccT vv[SEG], dov[SEG], uu[SEG];
+#pragma unroll
+    for (int j = 0; j < SEG; ++j) {
+      vv[j] = j < len ? col_val(gv, t0 + j) : (AccT)0;
+      dov[j] = j < len ? col_val(gdo, t0 + j) : (AccT)0;
+    }
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) S[i] = ck[((size_t)s * K + ph + 8 * i) * 32 + cl];
+    __syncthreads();
+    // recompute: Sd of every token of the segment, and u
+    AccT Sd[SEG][RPT];
+#pragma unroll
+    for (int j = 0; j < SEG; ++j) {
+      uu[j] = 0;
+      if (j < len) {
+        AccT kS = 0;
+#pragma unroll
+        for (int i = 0; i < RPT; ++i) {
+          S[i] *= sa[j][ph + 8 * i];
+          Sd[j][i] = S[i];
+          kS += sk[j][ph + 8 * i] * S[i];
+        }
+        kS = red8(kS);
+        uu[j] = vv[j] - kS;
+        const AccT d = sb[j] * uu[j];
+#pragma unroll
+        for (int i = 0; i < RPT; ++i) S[i] += sk[j][ph + 8 * i] * d;
+      }
+    }
+    // the token backward, last token first
+#pragma unroll
+    for (int jj = 0; jj < SEG; ++jj) {
+      const int j = SEG - 1 - jj;
+      if (j < len) {
+        const AccT d = sb[j] * uu[j];
+        AccT dd = 0;
+#pragma unroll
+        for (int i = 0; i < RPT; ++i) {
+          dS[i] += sq[j][ph + 8 * i] * dov[j];  // now dSt
+          dd += dS[i] * sk[j][ph + 8 * i];
+        }
+        dd = red8(dd);
+        const AccT du = sb[j] * dd;
+        if (ph == 0 && okc)
+          gdv[((size_t)(b * T + t0 + j) * p.HV + hv) * p.V + col] = out_of<InT>(du);
+        // each row's column sums go to LDS as soon as they are formed
+#pragma unroll
+        for (int i = 0; i < RPT; ++i) {
+          const AccT kr = sk[j][ph + 8 * i];
+          const AccT P = colsum((Sd[j][i] + kr * d) * dov[j]);
+          const AccT Dk = colsum(dS[i] * d - Sd[j][i] * du);
+          const AccT dSd = dS[i] - kr * du;
+          const AccT Gv = colsum(dSd * Sd[j][i]);
+          dS[i] = sa[j][ph + 8 * i] * dSd;
+          if (lane < 8) {
+            sw[j][wave][0][ph + 8 * i] = P;
+            sw[j][wave][1][ph + 8 * i] = Dk;
+            sw[j][wave][2][ph + 8 * i] = Gv;
+          }
+        }
+        const AccT cb = colsum(ph == 0 ? dd * uu[j] : (AccT)0);
+        if (lane == 0) sbw[j][wave] = cb;
+      }
+    }
+    __syncthreads();
+    // the four waves' sums: one partial record per token of the segment
+    for (int idx = tid; idx < len * PS; idx += 256) {
+      const int j = idx / PS, e = idx % PS;
+      AccT sum;
+      if (e < 3 * K) {
+        const int qn = e / K, c = e % K;
+        sum = sw[j][0][qn][c] + sw[j][1][qn][c] + sw[j][2][qn][c] + sw[j][3][qn][c];
+      } else {
+        sum = sbw[j][0] + sbw[j][1] + sbw[j][2] + sbw[j][3];
+      }
+      part[(((size_t)(b * T + t0 + j) * p.HV + hv) * nvs + vs) * PS + e] = sum;
+    }
+  }
+  if (ds0 && okc) {
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) ds0[sbase + (size_t)(ph + 8 * i) * p.V + col] = dS[i];
+  }
+}
+
+template <typename InT, typename AccT>
+__global__ __launch_bounds__(256) void kda_bwd_reduce_kernel(KdaBwdParams p) {
+  const int K = p.K, PS = 3 * K + 1;
+  const int nvs = (p.V + 31) / 32;
+  const int G = p.HV / p.H;
+  const int h = blockIdx.x % p.H;
+  const size_t bt = blockIdx.x / p.H;  // b * T + t
+  const AccT* part = static_cast<const AccT*>(p.part);
+  const InT* gg = static_cast<const InT*>(p.g);
+  const AccT clampv = (AccT)p.g_clamp_min;
+  const bool do_clamp = p.g_clamp_min > -INFINITY;
+  for (int c = threadIdx.x; c < K; c += blockDim.x) {
+    AccT dq = 0, dk = 0;
+    for (int gi = 0; gi < G; ++gi) {
+      const int hv = h * G + gi;
+      const AccT* pp = part + (bt * p.HV + hv) * nvs * PS;
+      AccT a = 0, kd = 0, gs = 0;
+      for (int vs = 0; vs < nvs; ++vs) {
+        a += pp[vs * PS + c];
+        kd += pp[vs * PS + K + c];
+        gs += pp[vs * PS + 2 * K + c];
+      }
+      dq += a;
+      dk += kd;
+      const size_t gi_idx = (bt * p.HV + hv) * K + c;
+      const bool pass = !do_clamp || acc_of<AccT>(gg[gi_idx]) >= clampv;
+      static_cast<InT*>(p.dg)[gi_idx] = out_of<InT>(pass ? gs : (AccT)0);
+      if (c == 0) {
+        AccT bs = 0;
+        for (int vs = 0; vs < nvs; ++vs) bs += pp[vs * PS + 3 * K];
+        static_cast<InT*>(p.dbeta)[bt * p.HV + hv] = out_of<InT>(bs);
+      }
+    }
+    const size_t qi = (bt * p.H + h) * K + c;
+    static_cast<InT*>(p.dq)[qi] = out_of<InT>(dq * (AccT)p.scale);
+    static_cast<InT*>(p.dk)[qi] = out_of<InT>(dk);
+  }
+}
+
+template <int K, typename InT, typename AccT>
+hipError_t launch_bwd(const KdaBwdParams& p, hipStream_t s) {
+  const int nvs = (p.V + 31) / 32;
+  hipLaunchKernelGGL((kda_recurrent_bwd_kernel<K, InT, AccT>), dim3(p.B * p.HV * nvs), dim3(256), 0, s,
+                     p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int threads = K <= 64 ? 64 : (K <= 128 ? 128 : 256);
+  hipLaunchKernelGGL((kda_bwd_reduce_kernel<InT, AccT>), dim3((unsigned)((size_t)p.B * p.T * p.H)),
+                     dim3(threads), 0, s, p);
+  return hipGetLastError();
+}
+
+template <typename InT, typename AccT>
+hipError_t bwd_by_k(const KdaBwdParams& p, hipStream_t s) {
+  switch (p.K) {
+    case 16: return launch_bwd<16, InT, AccT>(p, s);
+    case 32: return launch_bwd<32, InT, AccT>(p, s);
+    case 64: return launch_bwd<64, InT, AccT>(p, s);
+    case 128: return launch_bwd<128, InT, AccT>(p, s);
+    default: return launch_bwd<256, InT, AccT>(p, s);
+  }
+}
+
+template <int K, typename AccT>
+size_t ck_bytes(int B, int T, int HV, int V) {
+  constexpr int SEG = seg_len<K, AccT>();
+  return (size_t)B * HV * ((V + 31) / 32) * ((T + SEG - 1) / SEG) * K * 32 * sizeof(AccT);
+}
+
+template <typename AccT>
+size_t ck_bytes_by_k(int B, int T, int HV, int K, int V) {
+  switch (K) {
+    case 16: return ck_bytes<16, AccT>(B, T, HV, V);
+    case 32: return ck_bytes<32, AccT>(B, T, HV, V);
+    case 64: return ck_bytes<64, AccT>(B, T, HV, V);
+    case 128: return ck_bytes<128, AccT>(B, T, HV, V);
+    default: return ck_bytes<256, AccT>(B, T, HV, V);
+  }
+}
+
+size_t al256(size_t x) { return (x + 255) & ~size_t(255); }
+
+}  // namespace
+
+size_t kda_bwd_ws_bytes(int B, int T, int HV, int K, int V, bool f64) {
+  const size_t acc = f64 ? 8 : 4;
+  const size_t ck = f64 ? ck_bytes_by_k<double>(B, T, HV, K, V) : ck_bytes_by_k<float>(B, T, HV, K, V);
+  const size_t part = (size_t)B * T * HV * ((V + 31) / 32) * (3 * K + 1) * acc;
+  return al256(ck) + al256(part);
+}
+
+hipError_t kda_bwd_dispatch(KdaBwdParams p, int dtype, void* ws, hipStream_t stream) {
+  const bool f64 = dtype == DT_F64;
+  const size_t ck = f64 ? ck_bytes_by_k<double>(p.B, p.T, p.HV, p.K, p.V)
+                        : ck_bytes_by_k<float>(p.B, p.T, p.HV, p.K, p.V);
+  p.ck = ws;
+  p.part = static_cast<char*>(ws) + al256(ck);
+  if (f64) return bwd_by_k<double, double>(p, stream);
+  if (dtype == DT_F32) return bwd_by_k<float, float>(p, stream);
+  if (dtype == DT_BF16) return bwd_by_k<bf16_t, float>(p, stream);
+  return bwd_by_k<_Float16, float>(p, stream);
+}
+
+}  // namespace kch

@@ -11,7 +11,7 @@ from .hybrid import (CSAHybridLayer, HCAHybridLayer, HybridConfig, HybridDecodin
 from .ops_csa import (csa_compress_kv, csa_compress_kv_overlapped, csa_core, record_selections,
                       csa_lightning_indexer, l2_normalize_rows, naive_csa)
 from .ops_hca import hca_core, naive_hca
-from .ops_kda import naive_chunk_kda, naive_recurrent_kda
+from .ops_kda import kda_recurrent_grad, naive_chunk_kda, naive_recurrent_kda
 from .ops_kda_backend import hip_available, kda_forward, validate_kda_backend
 
 __all__ = [
@@ -27,6 +27,7 @@ __all__ = [
     "csa_compress_kv",
     "csa_compress_kv_overlapped",
     "csa_core",
+    "kda_recurrent_grad",
     "hca_core",
     "csa_lightning_indexer",
     "hip_available",

@@ -217,19 +217,123 @@ def _run(entry, fn_name, q, k, v, g, beta, scale, initial_state, output_final_st
     return o, s_out
 
 
+def _bwd_scale(scale, K, f64):
+    if scale is None:
+        return K ** -0.5
+    if isinstance(scale, torch.Tensor):
+        return float(scale.detach().double().item()) if f64 else float(scale.detach().float().item())
+    return float(scale)
+
+
+def kda_recurrent_grad(q, k, v, g, beta, d_o, scale=None, initial_state=None, ds_final=None,
+                       *, g_clamp_min: float = -10.0):
+    """Gradients of ``naive_recurrent_kda`` / ``naive_chunk_kda`` (the same
+    function, ``ops_kda.py:175-267`` / ``:464-494``) for the cotangents
+    ``d_o = dL/do`` and ``ds_final = dL/dS_T`` (or ``None``), on
+    ``kch_kda_recurrent_bwd``. Returns ``(dq, dk, dv, dg, dbeta, ds0)``: the
+    first five in the input dtype, ``ds0`` in the state dtype (fp32, fp64 for
+    fp64 inputs) or ``None`` without an initial state. K is zero-padded to the
+    kernel's next size; padded channels carry no gradient."""
+    fn = "kda_recurrent_grad"
+    B, T, H, K = q.shape
+    HV, V = v.shape[2], v.shape[-1]
+    f64 = v.dtype == torch.float64
+    code = 3 if f64 else _lib.dtype_code(fn, v.dtype)
+    st = torch.float64 if f64 else torch.float32
+    dtype = v.dtype
+    sc = _bwd_scale(scale, K, f64)
+    if T == 0 or B == 0:
+        ds0 = None
+        if initial_state is not None:
+            ds0 = (ds_final.to(st).clone() if ds_final is not None
+                   else torch.zeros(B, HV, K, V, device=q.device, dtype=st))
+        z = [torch.zeros_like(t) for t in (q, k, v, g, beta)]
+        return (*z, ds0)
+    Kp = next((n for n in (16, 32, 64, 128, 256) if n >= K), None)
+    if Kp is None:
+        raise NotImplementedError(f"{fn}: head dim K={K} > 256 is not supported by the HIP kernels")
+    q, k, g = (F.pad(t.to(dtype), (0, Kp - K)) if Kp != K else t.to(dtype) for t in (q, k, g))
+    q, k, v, g, beta, d_o = (t.to(dtype).contiguous() for t in (q, k, v, g, beta, d_o))
+    s0 = None if initial_state is None else initial_state.to(device=q.device, dtype=st)
+    dsf = None if ds_final is None else ds_final.to(device=q.device, dtype=st)
+    if Kp != K:
+        s0 = None if s0 is None else F.pad(s0, (0, 0, 0, Kp - K))
+        dsf = None if dsf is None else F.pad(dsf, (0, 0, 0, Kp - K))
+    s0 = None if s0 is None else s0.contiguous()
+    dsf = None if dsf is None else dsf.contiguous()
+    dq, dk, dg = (torch.empty_like(t) for t in (q, k, g))
+    dv, dbeta = torch.empty_like(v), torch.empty_like(beta)
+    ds0 = torch.empty(B, HV, Kp, V, device=q.device, dtype=st) if initial_state is not None \
+        else None
+    nbytes = _lib.load().kch_kda_recurrent_bwd_ws_bytes(B, T, HV, Kp, V, code)
+    ws = torch.empty(max(nbytes, 1), device=q.device, dtype=torch.uint8)
+    _lib.call("kch_kda_recurrent_bwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g),
+              _lib.ptr(beta), _lib.ptr(s0), _lib.ptr(d_o), _lib.ptr(dsf), _lib.ptr(dq),
+              _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dg), _lib.ptr(dbeta), _lib.ptr(ds0),
+              B, T, H, HV, Kp, V, sc, _clamp_value(g_clamp_min), code, _lib.ptr(ws), nbytes,
+              _lib.stream_of(q))
+    if Kp != K:
+        dq, dk, dg = (t[..., :K].contiguous() for t in (dq, dk, dg))
+        ds0 = None if ds0 is None else ds0[:, :, :K].contiguous()
+    return dq, dk, dv, dg, dbeta, ds0
+
+
+class _KdaFunction(torch.autograd.Function):
+    """The operators with gradients: forward on the operator's own kernels,
+    backward on ``kch_kda_recurrent_bwd`` (the reference differentiates its
+    torch code with autograd, ``run_correctness.py:765-833, 1032-1092``)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, beta, s0, entry, fn_name, scale, g_clamp_min, state_dtype,
+                chunk_size):
+        ctx.set_materialize_grads(False)
+        o, s = _run(entry, fn_name, q, k, v, g, beta, scale, s0, True, g_clamp_min,
+                    state_dtype, chunk_size)
+        ctx.save_for_backward(q, k, v, g, beta, s0)
+        ctx.scale, ctx.g_clamp_min = scale, g_clamp_min
+        return o, s
+
+    @staticmethod
+    def backward(ctx, d_o, d_s):
+        q, k, v, g, beta, s0 = ctx.saved_tensors
+        if d_o is None:
+            d_o = torch.zeros_like(v)
+        dq, dk, dv, dg, dbeta, ds0 = kda_recurrent_grad(
+            q, k, v, g, beta, d_o, ctx.scale, s0, d_s, g_clamp_min=ctx.g_clamp_min)
+        if ds0 is not None:
+            ds0 = ds0.to(s0.dtype)
+        return dq, dk, dv, dg, dbeta, ds0, None, None, None, None, None, None
+
+
+def _needs_grad(*ts):
+    return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts)
+
+
+def _run_op(entry, fn_name, q, k, v, g, beta, scale, initial_state, output_final_state,
+            g_clamp_min, state_dtype, chunk_size=None):
+    if not _needs_grad(q, k, v, g, beta, initial_state):
+        return _run(entry, fn_name, q, k, v, g, beta, scale, initial_state, output_final_state,
+                    g_clamp_min, state_dtype, chunk_size)
+    o, s = _KdaFunction.apply(q, k, v, g, beta, initial_state, entry, fn_name, scale,
+                              g_clamp_min, state_dtype, chunk_size)
+    return o, (s if output_final_state else None)
+
+
 def naive_chunk_kda(q, k, v, g, beta, scale=None, initial_state=None, output_final_state=False,
                     chunk_size: int = 64, *, g_clamp_min: float = -10.0, state_dtype=None):
-    """Chunkwise-parallel KDA on the HIP backend (``ops_kda.py:464-494``)."""
-    return _run("kch_kda_chunk_fwd", "naive_chunk_kda", q, k, v, g, beta, scale,
-                initial_state, output_final_state, g_clamp_min, state_dtype, chunk_size)
+    """Chunkwise-parallel KDA on the HIP backend (``ops_kda.py:464-494``).
+    Differentiable in q, k, v, g, beta and the initial state."""
+    return _run_op("kch_kda_chunk_fwd", "naive_chunk_kda", q, k, v, g, beta, scale,
+                   initial_state, output_final_state, g_clamp_min, state_dtype, chunk_size)
 
 
 def naive_recurrent_kda(q, k, v, g, beta, scale=None, initial_state=None,
                         output_final_state=False, *, g_clamp_min: float = -10.0,
                         state_dtype=None):
-    """Per-token KDA recurrence on the HIP backend (``ops_kda.py:175-267``)."""
-    return _run("kch_kda_recurrent_fwd", "naive_recurrent_kda", q, k, v, g, beta, scale,
-                initial_state, output_final_state, g_clamp_min, state_dtype)
+    """Per-token KDA recurrence on the HIP backend (``ops_kda.py:175-267``).
+    Differentiable in q, k, v, g, beta and the initial state."""
+    return _run_op("kch_kda_recurrent_fwd", "naive_recurrent_kda", q, k, v, g, beta, scale,
+                   initial_state, output_final_state, g_clamp_min, state_dtype)
 
 
 def kda_recurrent_into(q, k, v, g, beta, scale, state, state_out):

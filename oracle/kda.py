@@ -11,6 +11,8 @@ Functions
     ``clamp(max=50)`` on the decay exponent (``:409-417``), the triangular
     solve and ``(A + I) diag(beta)`` (``:418-421``), ``w``/``u`` (``:423-424``),
     and the sequential chunk loop (``:509-535``).
+``recurrent_kda_grad``  the reverse-mode gradients of ``recurrent_kda``, pinned by
+    central finite differences of ``recurrent_kda`` in fp64.
 ``delta_rule_matrix_form``  an independent fp64 statement of the recurrence
     as explicit matrices, ``S_t = (I - b k k^T) Diag(exp g) S_{t-1} + b k v^T``
     (module docstring, ``ops_kda.py:6-9``), used only to pin ``recurrent_kda``.
@@ -153,3 +155,66 @@ def chunk_kda(q, k, v, g, beta, scale=None, initial_state=None, chunk_size=64,
         S = S + np.einsum('bhck,bhcv->bhkv', np.exp(g_i[:, :, -1:] - g_i) * k_i, v_i)
     o = o.reshape(B, HV, Tp, V).transpose(0, 2, 1, 3)[:, :T]
     return np.ascontiguousarray(o), S
+
+
+def recurrent_kda_grad(q, k, v, g, beta, d_o, scale=None, initial_state=None, ds_final=None,
+                       g_clamp_min=-10.0, compute=np.float64):
+    """Gradients of ``recurrent_kda`` (the backward of ``naive_recurrent_kda``,
+    ``ops_kda.py:175-267``, which the reference takes from autograd and checks
+    in ``run_correctness.py:765-833``) for the cotangents ``d_o = dL/do``
+    ``[B,T,HV,V]`` and ``ds_final = dL/dS_T`` ``[B,HV,K,V]`` (or ``None``).
+
+    Reverse-mode pass written out by hand: the forward states are kept, then
+    per token, last first, with ``a = exp(max(g, clamp))``, ``Sd = a S``,
+    ``u = v - Sd^T k``, ``d = beta u``, ``S' = Sd + k d^T``, ``o = S'^T (scale q)``::
+
+        dSt = dS + q^ do^T;   dq^ = S' do;   dd = dSt^T k;   du = beta dd
+        dv = du;   dbeta = dd . u;   dk = dSt d - Sd du
+        dSd = dSt - k du^T;   dg = rowsum(dSd * Sd) (0 where g < clamp);   dS = a dSd
+
+    q and k are shared by the ``HV // H`` value heads of a key head, so their
+    gradients sum over them. Returns ``(dq, dk, dv, dg, dbeta, ds0)``.
+    """
+    B, T, H, K = np.shape(q)
+    G = np.shape(v)[2] // H
+    sc = K ** -0.5 if scale is None else scale
+    qh, kh, v, g_raw, beta, B, T, HV, K, V = _prep_common(q, k, v, g, beta, sc, compute)
+    g = np.maximum(g_raw, compute(g_clamp_min)) if g_clamp_min > -np.inf else g_raw
+    d_o = np.asarray(d_o, compute)
+    S = np.zeros((B, HV, K, V), compute)
+    if initial_state is not None:
+        S = S + np.asarray(initial_state, compute)
+    a = np.exp(g)
+    Sds, us = [], []
+    for t in range(T):
+        Sd = S * a[:, t][..., None]
+        u = v[:, t] - np.einsum('bhk,bhkv->bhv', kh[:, t], Sd)
+        S = Sd + np.einsum('bhk,bhv->bhkv', kh[:, t], beta[:, t][..., None] * u)
+        Sds.append(Sd)
+        us.append(u)
+    dS = np.zeros((B, HV, K, V), compute) if ds_final is None else np.array(ds_final, compute)
+    dqh = np.zeros_like(qh)
+    dkh = np.zeros_like(kh)
+    dv = np.zeros_like(v)
+    dg = np.zeros_like(g)
+    dbeta = np.zeros_like(beta)
+    for t in range(T - 1, -1, -1):
+        Sd, u = Sds[t], us[t]
+        d = beta[:, t][..., None] * u
+        Sp = Sd + np.einsum('bhk,bhv->bhkv', kh[:, t], d)
+        dSt = dS + np.einsum('bhk,bhv->bhkv', qh[:, t], d_o[:, t])
+        dqh[:, t] = np.einsum('bhkv,bhv->bhk', Sp, d_o[:, t])
+        dd = np.einsum('bhkv,bhk->bhv', dSt, kh[:, t])
+        du = beta[:, t][..., None] * dd
+        dv[:, t] = du
+        dbeta[:, t] = (dd * u).sum(-1)
+        dkh[:, t] = (np.einsum('bhkv,bhv->bhk', dSt, d)
+                     - np.einsum('bhkv,bhv->bhk', Sd, du))
+        dSd = dSt - np.einsum('bhk,bhv->bhkv', kh[:, t], du)
+        dg[:, t] = (dSd * Sd).sum(-1)
+        dS = dSd * a[:, t][..., None]
+    if g_clamp_min > -np.inf:
+        dg = np.where(g_raw >= compute(g_clamp_min), dg, compute(0))
+    dq = dqh.reshape(B, T, H, G, K).sum(3) * compute(sc)
+    dk = dkh.reshape(B, T, H, G, K).sum(3)
+    return dq, dk, dv, dg, dbeta, dS

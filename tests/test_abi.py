@@ -66,6 +66,32 @@ def test_invalid_arguments_report_errors_without_gpu():
     assert lib.kch_linear_up(None, 64, None, 64, None, 8, 0, 8, 64, 1, None) == 0
 
 
+def test_kda_backward_validation_and_workspace():
+    """kch_kda_recurrent_bwd: sizes checked before any pointer or HIP call; the
+    workspace is the checkpoints (one state slice per segment) plus one
+    partial record (3K + 1 values) per (b, t, hv, 32-column slice)."""
+    from kch import _lib
+    lib = _lib.load()
+    P = [None] * 14
+    rc = lib.kch_kda_recurrent_bwd(*P, 1, 8, 2, 2, 48, 16, 0.25, -10.0, 0, None, 0, None)
+    assert rc == 2 and b"K=48" in lib.kch_last_error()
+    rc = lib.kch_kda_recurrent_bwd(*P, 1, 0, 2, 2, 64, 16, 0.25, -10.0, 0, None, 0, None)
+    assert rc == 1 and b"T >= 1" in lib.kch_last_error()
+    rc = lib.kch_kda_recurrent_bwd(*P, 1, 8, 2, 2, 64, 16, 0.25, -10.0, 7, None, 0, None)
+    assert rc == 1 and b"dtype" in lib.kch_last_error()
+    rc = lib.kch_kda_recurrent_bwd(*P, 1, 8, 2, 2, 64, 16, 0.25, -10.0, 3, None, 0, None)
+    assert rc == 1 and b"null" in lib.kch_last_error()
+    assert lib.kch_kda_recurrent_bwd_ws_bytes(1, 8, 2, 48, 16, 0) == 0
+    pad = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    # fp32, K = 128: 8-token segments; fp64, K = 128: 4-token segments
+    B, T, HV, K, V = 2, 100, 3, 128, 40
+    nvs = (V + 31) // 32
+    for code, acc, seg in ((0, 4, 8), (1, 4, 8), (3, 8, 4)):
+        ck = B * HV * nvs * (-(-T // seg)) * K * 32 * acc
+        part = B * T * HV * nvs * (3 * K + 1) * acc
+        assert lib.kch_kda_recurrent_bwd_ws_bytes(B, T, HV, K, V, code) == pad(ck) + pad(part)
+
+
 def test_chunk_workspace_size_query():
     """kch_kda_chunk_ws_bytes: 0 where no workspace is used, else the sum of
     the six per-chunk records, each region padded to 256 bytes."""

@@ -8,7 +8,10 @@ Each check would fail under a plausible restatement mistake:
   run_correctness.py:103-133, at its 1e-6 fp32 tolerance) -> WY/UT mistakes,
   wrong decay direction (ops_kda.py:521-534), mask diagonal (ops_kda.py:396-408);
 * special cases with closed forms (beta=0 pure decay; beta=1, g=0 exact write);
-* GVA head sharing, padding/causality, the g clamp.
+* GVA head sharing, padding/causality, the g clamp;
+* the hand-written gradients against central finite differences of the
+  forward in fp64, every coordinate (the reference's gradient test,
+  run_correctness.py:765-833, samples 8 per tensor at the same 1e-6 bar).
 """
 
 from __future__ import annotations
@@ -17,7 +20,7 @@ import numpy as np
 import pytest
 
 from oracle.common import l2_normalize, logsigmoid, sigmoid
-from oracle.kda import chunk_kda, delta_rule_matrix_form, recurrent_kda
+from oracle.kda import chunk_kda, delta_rule_matrix_form, recurrent_kda, recurrent_kda_grad
 
 
 def _inputs(rng, B, T, H, HV, K, V, gscale=1.0):
@@ -160,3 +163,65 @@ def test_bf16_round_matches_torch_conversion():
     nan = np.isnan(ref)
     np.testing.assert_array_equal(np.isnan(got), nan)
     np.testing.assert_array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def _fd_check(q, k, v, g, beta, s0, W_o, W_s, scale, clamp):
+    """Largest error of recurrent_kda_grad against central differences of
+    L = sum(o * W_o) + sum(S_T * W_s) over every input coordinate, relative to
+    |num| + |ana| + 1e-2: the differences carry ~1e-10 of rounding noise, so a
+    gradient of 1e-5 cannot be resolved to 1e-6 relative, while a dropped or
+    wrong term moves a gradient by its own size."""
+    def loss(q, k, v, g, beta, s0):
+        o, S = recurrent_kda(q, k, v, g, beta, scale=scale, initial_state=s0, g_clamp_min=clamp,
+                             compute=np.float64)
+        return float((o * W_o).sum() + (S * W_s).sum())
+
+    grads = recurrent_kda_grad(q, k, v, g, beta, W_o, scale=scale, initial_state=s0,
+                               ds_final=W_s, g_clamp_min=clamp)
+    args = [q, k, v, g, beta, s0]
+    eps, worst = 1e-6, 0.0
+    for i, (x, gx) in enumerate(zip(args, grads)):
+        assert gx.shape == x.shape
+        for idx in np.ndindex(*x.shape):
+            orig = x[idx]
+            x[idx] = orig + eps
+            lp = loss(*args)
+            x[idx] = orig - eps
+            lm = loss(*args)
+            x[idx] = orig
+            num = (lp - lm) / (2 * eps)
+            rel = abs(num - gx[idx]) / (abs(num) + abs(gx[idx]) + 1e-2)
+            worst = max(worst, rel)
+    return worst
+
+
+def test_recurrent_grad_matches_finite_differences():
+    """The reference's gradient test shape (B=1, T=16, H=2, K=V=4, fp64, small
+    gates and betas), here with an initial state and a final-state cotangent."""
+    rng = np.random.default_rng(6)
+    B, T, H, K, V = 1, 16, 2, 4, 4
+    q = rng.standard_normal((B, T, H, K))
+    k = rng.standard_normal((B, T, H, K))
+    v = rng.standard_normal((B, T, H, V))
+    g = -rng.random((B, T, H, K)) * 0.1
+    beta = rng.random((B, T, H)) * 0.2
+    s0 = rng.standard_normal((B, H, K, V)) * 0.1
+    W_o = rng.standard_normal((B, T, H, V))
+    W_s = rng.standard_normal((B, H, K, V))
+    assert _fd_check(q, k, v, g, beta, s0, W_o, W_s, None, -10.0) < 1e-6
+
+
+def test_recurrent_grad_gva_and_clamp():
+    """GVA (2 value heads per key head): dq, dk sum over the value heads; gate
+    entries below the clamp get zero gradient (kept 0.5 away from the kink so
+    the differences do not straddle it); explicit scale."""
+    rng = np.random.default_rng(11)
+    B, T, H, HV, K, V = 2, 9, 1, 2, 4, 3
+    q, k, v, g, beta = _inputs(rng, B, T, H, HV, K, V)
+    g = np.where(rng.random(g.shape) < 0.3, -10.5 - rng.random(g.shape), g)
+    s0 = rng.standard_normal((B, HV, K, V)) * 0.1
+    W_o = rng.standard_normal((B, T, HV, V))
+    W_s = rng.standard_normal((B, HV, K, V))
+    assert _fd_check(q, k, v, g, beta, s0, W_o, W_s, 0.7, -10.0) < 1e-6
+    dg = recurrent_kda_grad(q, k, v, g, beta, W_o, scale=0.7, initial_state=s0, ds_final=W_s)[3]
+    assert np.all(dg[g < -10.0] == 0) and np.any(dg[g >= -10.0] != 0)
