@@ -14,9 +14,10 @@
 // The columns of the state are independent in both directions; only dq^,
 // dk, dg and dbeta sum over columns.
 //
-// kda_recurrent_bwd_kernel  one workgroup per (b, hv, 32-column slice of V),
-//   thread (column tid/8, phase tid%8) owns rows phase + 8 i of its column,
-//   as in the forward kernel. Pass 1 runs the recurrence forward and stores
+// kda_recurrent_bwd_kernel  one workgroup per (b, hv, 32-column slice of V);
+//   lane l of wave w owns rows (l / 8) + 8 i of column 8 w + l % 8: the sums
+//   over columns, three K-vectors per token, are then DPP steps within 8-lane
+//   groups, and only the two per-column sums over rows cross rows of lanes. Pass 1 runs the recurrence forward and stores
 //   the state at the start of every segment of SEG tokens (a checkpoint in the
 //   workspace). Pass 2 walks the segments in reverse: it reloads the
 //   checkpoint, recomputes the segment's decayed states Sd into registers,
@@ -50,6 +51,44 @@ __device__ __forceinline__ OutT out_of(AccT x) {
   else return from_f32<OutT>((float)x);
 }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_acc(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_acc(double v) {
+  const long long x = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xf, 0xf, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(x >> 32), CTRL, 0xf, 0xf, false);
+  return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
+// x of lane l ^ D (D = 16 or 32) by v_permlane16_swap / v_permlane32_swap of
+// x with itself: the swap leaves x[l ^ D] in the second result where l & D is
+// 0 and in the first where it is set.
+template <int D>
+__device__ __forceinline__ unsigned swap_u32(unsigned u) {
+  const bool hi = (__lane_id() & D) != 0;
+  if constexpr (D == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return hi ? r[0] : r[1];
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return hi ? r[0] : r[1];
+  }
+}
+template <int D>
+__device__ __forceinline__ float swap_acc(float v) {
+  return __uint_as_float(swap_u32<D>(__float_as_uint(v)));
+}
+template <int D>
+__device__ __forceinline__ double swap_acc(double v) {
+  const unsigned long long x = (unsigned long long)__double_as_longlong(v);
+  const unsigned lo = swap_u32<D>((unsigned)x);
+  const unsigned hi = swap_u32<D>((unsigned)(x >> 32));
+  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+
 // tokens per checkpoint segment: the segment's decayed states stay in
 // registers (SEG * K / 8 values per thread, at most 128 VGPRs)
 template <int K, typename AccT>
@@ -73,7 +112,7 @@ __global__ __launch_bounds__(256) void kda_recurrent_bwd_kernel(KdaBwdParams p) 
   const int vs = blockIdx.x % nvs;
   const int bh = blockIdx.x / nvs;
   const int hv = bh % p.HV, b = bh / p.HV, h = hv / (p.HV / p.H);
-  const int cl = tid >> 3, ph = tid & 7;
+  const int cl = wave * 8 + (lane & 7), ph = lane >> 3;
   const int col = vs * 32 + cl;
   const bool okc = col < p.V;
   const int T = p.T;
@@ -94,16 +133,16 @@ __global__ __launch_bounds__(256) void kda_recurrent_bwd_kernel(KdaBwdParams p) 
   const bool do_clamp = p.g_clamp_min > -INFINITY;
   const size_t sbase = (size_t)(b * p.HV + hv) * K * p.V;
 
-  auto red8 = [](AccT x) {  // over the 8 phases of a column
-    x += __shfl_xor(x, 1);
-    x += __shfl_xor(x, 2);
-    x += __shfl_xor(x, 4);
+  auto red8 = [](AccT x) {  // over the 8 phases of a column (lanes 8 apart)
+    x += dpp_acc<0x128>(x);  // row_ror:8, the other half of the 16-lane row
+    x += swap_acc<16>(x);
+    x += swap_acc<32>(x);
     return x;
   };
-  auto colsum = [](AccT x) {  // over the 8 columns of a wave
-    x += __shfl_xor(x, 8);
-    x += __shfl_xor(x, 16);
-    x += __shfl_xor(x, 32);
+  auto colsum = [](AccT x) {  // over the 8 columns of a wave (8-lane groups)
+    x += dpp_acc<0xB1>(x);   // quad_perm [1,0,3,2]
+    x += dpp_acc<0x4E>(x);   // quad_perm [2,3,0,1]
+    x += dpp_acc<0x141>(x);  // row_half_mirror: the other quad of the group
     return x;
   };
   // the segment's key, decay and beta rows (and scaled q) into LDS
@@ -224,7 +263,7 @@ __global__ __launch_bounds__(256) void kda_recurrent_bwd_kernel(KdaBwdParams p) 
           const AccT dSd = dS[i] - kr * du;
           const AccT Gv = colsum(dSd * Sd[j][i]);
           dS[i] = sa[j][ph + 8 * i] * dSd;
-          if (lane < 8) {
+          if ((lane & 7) == 0) {
             sw[j][wave][0][ph + 8 * i] = P;
             sw[j][wave][1][ph + 8 * i] = Dk;
             sw[j][wave][2][ph + 8 * i] = Gv;
