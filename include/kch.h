@@ -130,6 +130,28 @@ int kch_kda_recurrent_bwd(const void* q, const void* k, const void* v, const voi
 
 
 /*
+ * Gradients of the HCA attention: the backward of hca_core (ops_hca.py:132-194,
+ * which the reference differentiates with autograd; the gradient check of the
+ * hybrid stack, run_correctness.py:2710-2830, runs through it). fp32 tensors:
+ * q, d_out [B,T,nh,c] (queries as given; the kernel normalises them), kc / raw
+ * [B,T/m2,c] (the L2-normalised and the raw compressed rows of C, Z, B_pos,
+ * from kch_compress), kl / lsrc [B,T,c] (the normalised window rows and the
+ * rows they normalise; NULL when win = 0), C, Z [B,T,c], B_pos [m2,c], sink
+ * [nh] or NULL. Outputs: dq [B,T,nh,c]; dC, dZ [B,T,c]; dBp [B,T/m2,m2,c]
+ * (summed over the first two axes it is dB_pos); dlocal [B,T,c] (the window
+ * rows' source gradient) or NULL to add it into dC; sink_part [B,T,nh]
+ * (p_sink * D; dsink = -its sum over B and T) or NULL. Coverage: c in {64,
+ * 128}, nh <= 16 (c = 128) or 32 (c = 64), T a multiple of m2, T >= 1. ws:
+ * 256-byte aligned, kch_hca_attn_bwd_ws_bytes bytes.
+ */
+size_t kch_hca_attn_bwd_ws_bytes(int B, int T, int nh, int c, int m2, int win);
+int kch_hca_attn_bwd(const float* q, const float* d_out, const float* kc, const float* raw,
+                     const float* kl, const float* lsrc, const float* C, const float* Z,
+                     const float* B_pos, const float* sink, float* dq, float* dC, float* dZ,
+                     float* dBp, float* dlocal, float* sink_part, int B, int T, int nh, int c,
+                     int m2, int win, float scale, void* ws, size_t ws_bytes, void* stream);
+
+/*
  * Single-branch softmax-gated KV compression, [B,T,c] -> [B,T/m,c].
  * Replaces csa_compress_kv (ops_csa.py:198-234); used for the CSA indexer keys
  * (ops_csa.py:874) and for HCA (ops_hca.py:134).

@@ -265,6 +265,48 @@ int kch_kda_recurrent_bwd(const void* q, const void* k, const void* v, const voi
   return hip_status(fn, kch::kda_bwd_dispatch(p, dtype, ws, (hipStream_t)stream));
 }
 
+size_t kch_hca_attn_bwd_ws_bytes(int B, int T, int nh, int c, int m2, int win) {
+  if (B <= 0 || T <= 0 || nh < 1 || (c != 64 && c != 128) || m2 < 1 || T % m2 || win < 0) return 0;
+  return kch::hca_bwd_ws_bytes(B, T, nh, c, m2, win);
+}
+
+int kch_hca_attn_bwd(const float* q, const float* d_out, const float* kc, const float* raw,
+                     const float* kl, const float* lsrc, const float* C, const float* Z,
+                     const float* B_pos, const float* sink, float* dq, float* dC, float* dZ,
+                     float* dBp, float* dlocal, float* sink_part, int B, int T, int nh, int c,
+                     int m2, int win, float scale, void* ws, size_t ws_bytes, void* stream) {
+  const char* fn = "kch_hca_attn_bwd";
+  if (B < 0 || T < 1 || nh < 1 || m2 < 1 || win < 0)
+    return fail(KCH_ERR_INVALID, "%s: bad sizes B=%d T=%d nh=%d m2=%d win=%d (T >= 1)", fn, B, T, nh,
+                m2, win);
+  if (T % m2) return fail(KCH_ERR_INVALID, "%s: T=%d must be a multiple of m2=%d", fn, T, m2);
+  if (c != 64 && c != 128) return fail(KCH_ERR_UNSUPPORTED, "%s: c=%d not supported (64 or 128)", fn, c);
+  if (nh * (c / 8) > 256)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: nh=%d heads of %d exceed one workgroup", fn, nh, c);
+  if (std::isnan(scale)) return fail(KCH_ERR_INVALID, "%s: scale is NaN", fn);
+  if ((long long)B * T * nh * c >= (1LL << 40))
+    return fail(KCH_ERR_UNSUPPORTED, "%s: tensors too large", fn);
+  if (B == 0) return KCH_OK;
+  if (!q || !d_out || !kc || !raw || !C || !Z || !B_pos || !dq || !dC || !dZ || !dBp)
+    return fail(KCH_ERR_INVALID, "%s: null tensor pointer", fn);
+  if (win > 0 && (!kl || !lsrc)) return fail(KCH_ERR_INVALID, "%s: window rows required (win > 0)", fn);
+  const size_t need = kch_hca_attn_bwd_ws_bytes(B, T, nh, c, m2, win);
+  if (!ws || ws_bytes < need)
+    return fail(KCH_ERR_INVALID, "%s: workspace of %zu bytes required, got %zu", fn, need,
+                ws ? ws_bytes : (size_t)0);
+  if ((uintptr_t)ws & 255) return fail(KCH_ERR_INVALID, "%s: workspace must be 256-byte aligned", fn);
+  for (const void* ptr : {(const void*)q, (const void*)d_out, (const void*)kc, (const void*)kl,
+                          (const void*)dq})
+    if ((uintptr_t)ptr & 15) return fail(KCH_ERR_INVALID, "%s: q, d_out, kc, kl, dq must be 16-byte aligned", fn);
+  kch::HcaBwdParams p;
+  p.q = q; p.dout = d_out; p.kc = kc; p.raw = raw; p.kl = kl; p.lsrc = lsrc;
+  p.C = C; p.Z = Z; p.Bpos = B_pos; p.sink = sink;
+  p.dq = dq; p.dC = dC; p.dZ = dZ; p.dBp = dBp; p.dlocal = dlocal; p.sink_part = sink_part;
+  p.B = B; p.T = T; p.nh = nh; p.c = c; p.m2 = m2; p.nb = T / m2; p.win = win;
+  p.scale = scale;
+  return hip_status(fn, kch::hca_bwd_dispatch(p, ws, (hipStream_t)stream));
+}
+
 int kch_compress(const void* C, long long ldC, const void* Z, long long ldZ, const float* B_pos,
                  float* out_raw, void* out_key, int key_f32, int normalize, void* local, int B,
                  int T, int m, int c, int dtype, void* stream) {

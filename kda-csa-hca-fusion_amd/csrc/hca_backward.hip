@@ -1,0 +1,373 @@
+// HCA attention backward for gfx950: the gradients of hca_core
+// (/root/reference/ops_hca.py:132-194, differentiated by autograd in the
+// reference) with respect to the queries, the compression inputs C, Z,
+// B_pos, the window rows and the sink logits. fp32 throughout.
+//
+// Forward per query (b, t) and head h: qn = q / |q|; keys (= values) are the
+// L2-normalised compressed rows kc_n of the blocks the query sees
+// (n < (t+1) / m2) and the L2-normalised window rows kl_u (t-w < u <= t);
+// p = softmax over scale qn.k and the sink logit; out = sum p_j k_j.
+// Backward: dp_j = dout . k_j, D = sum p_j dp_j, ds_j = p_j (dp_j - D),
+//   dqn = scale sum ds_j k_j,   dk_j += scale ds_j qn + p_j dout,
+//   dsink = -sum p_sink D;
+// then the L2-norm backward (dx = (dy - y (y.dy)) / |x|) and the compression
+// backward (w = softmax over the block's tokens of Z + B_pos, per channel;
+// dC = w dr, dZ = w (C - r) dr).
+//
+// hca_bwd_query_kernel  one workgroup per (b, t); thread (head, 8-channel
+//   group). Pass A over the query's keys: running max, sum and sum p dp
+//   (lse and D); pass B: dqn, then dq. Writes lse, D, 1/|q| per (t, h).
+// hca_bwd_key_kernel    one workgroup per (tile of NBT key rows, chunk of up
+//   to QC queries, b): each query row (q, dout, lse, D) is read once for the
+//   NBT keys; the heads' sums meet in LDS; one partial gradient per key row
+//   and chunk. Mode 0: compressed rows (queries from (n+1) m2 - 1 on);
+//   mode 1: window rows (queries u .. u + w - 1).
+// hca_bwd_block_kernel  one workgroup per (b, block): sums the chunks, the
+//   L2-norm backward of the compressed row, the compression backward.
+// hca_bwd_window_kernel one workgroup per (b, token): the window row's
+//   L2-norm backward, added to dC (or written to dlocal).
+
+#include "kch_device.h"
+#include "kch_kernels.h"
+
+namespace kch {
+
+namespace {
+
+constexpr int NBT = 8;    // key rows per key-kernel tile
+constexpr int QC = 512;   // queries per key-kernel chunk
+constexpr float kEps = 1e-12f;
+
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// sum over the L lanes of a head group (L = 8 or 16, aligned); every lane of
+// the group gets the total
+template <int L>
+__device__ __forceinline__ float hsum(float v) {
+  v += dppf<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dppf<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dppf<0x141>(v);  // row_half_mirror: the other quad of the 8
+  if constexpr (L == 16) v += dppf<0x140>(v);  // row_mirror: the other 8 of the row
+  return v;
+}
+
+__device__ __forceinline__ void load8(const float* p, float* v) {
+  const float4 a = *reinterpret_cast<const float4*>(p);
+  const float4 b = *reinterpret_cast<const float4*>(p + 4);
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void hca_bwd_query_kernel(HcaBwdParams p) {
+  constexpr int LPH = HD / 8;
+  const int tid = threadIdx.x, h = tid / LPH, lc = tid % LPH;
+  const bool act = h < p.nh;
+  const int hh = act ? h : 0;
+  const size_t bt = blockIdx.x;
+  const int b = (int)(bt / p.T), t = (int)(bt % p.T);
+  const size_t qoff = (bt * p.nh + hh) * HD + 8 * lc;
+  float qn[8], dv[8];
+  load8(p.q + qoff, qn);
+  load8(p.dout + qoff, dv);
+  if (!act) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qn[e] = dv[e] = 0.f;
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += qn[e] * qn[e];
+  const float nrm = sqrtf(hsum<LPH>(ss));
+  const float rq = 1.f / fmaxf(nrm, kEps);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) qn[e] *= rq;
+
+  const int nvis = min((t + 1) / p.m2, p.nb);
+  const int i0 = p.win > 0 ? max(0, p.win - 1 - t) : 0;
+  const int nwin = p.win > 0 ? p.win - i0 : 0;
+  const int nk = nvis + nwin;
+  const int wpos0 = t - p.win + 1 + i0;  // first window position
+  auto krow = [&](int j) -> const float* {
+    return j < nvis ? p.kc + ((size_t)b * p.nb + j) * HD + 8 * lc
+                    : p.kl + ((size_t)b * p.T + wpos0 + (j - nvis)) * HD + 8 * lc;
+  };
+  auto score = [&](const float* k, float& s, float& dp) {
+    float a = 0.f, c = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      a += qn[e] * k[e];
+      c += dv[e] * k[e];
+    }
+    s = hsum<LPH>(a) * p.scale;
+    dp = hsum<LPH>(c);
+  };
+
+  // pass A: lse and D = sum p dp (the sink's value is zero)
+  float m = -INFINITY, l = 0.f, ad = 0.f;
+  float kc[8], kn[8];
+  if (nk > 0) load8(krow(0), kc);
+  for (int j = 0; j < nk; ++j) {
+    if (j + 1 < nk) load8(krow(j + 1), kn);
+    float s, dp;
+    score(kc, s, dp);
+    const float mn = fmaxf(m, s);
+    const float a = expf(m - mn), e1 = expf(s - mn);
+    l = l * a + e1;
+    ad = ad * a + e1 * dp;
+    m = mn;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) kc[e] = kn[e];
+  }
+  float sk = 0.f;
+  if (p.sink) {
+    sk = p.sink[hh];
+    const float mn = fmaxf(m, sk);
+    const float a = expf(m - mn);
+    l = l * a + expf(sk - mn);
+    ad *= a;
+    m = mn;
+  }
+  const float lse = l > 0.f ? m + logf(l) : INFINITY;
+  const float D = l > 0.f ? ad / l : 0.f;
+
+  // pass B: dqn = scale sum ds_j k_j
+  float dq[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) dq[e] = 0.f;
+  if (nk > 0) load8(krow(0), kc);
+  for (int j = 0; j < nk; ++j) {
+    if (j + 1 < nk) load8(krow(j + 1), kn);
+    float s, dp;
+    score(kc, s, dp);
+    const float ds = expf(s - lse) * (dp - D) * p.scale;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dq[e] += ds * kc[e];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) kc[e] = kn[e];
+  }
+  // L2-norm backward of the query row
+  float yd = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) yd += qn[e] * dq[e];
+  yd = hsum<LPH>(yd);
+  if (act) {
+    float o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = (nrm > kEps ? dq[e] - qn[e] * yd : dq[e]) * rq;
+    float* dst = p.dq + qoff;
+    *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
+    *reinterpret_cast<float4*>(dst + 4) = make_float4(o[4], o[5], o[6], o[7]);
+    if (lc == 0) {
+      const size_t i = bt * p.nh + h;
+      p.lse[i] = lse;
+      p.dval[i] = D;
+      p.rq[i] = rq;
+      if (p.sink_part) p.sink_part[i] = p.sink ? expf(sk - lse) * D : 0.f;
+    }
+  }
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void hca_bwd_key_kernel(HcaBwdParams p, int mode, int nchunk, int ntile) {
+  constexpr int LPH = HD / 8;
+  constexpr int HS = 256 / LPH;  // head slots
+  __shared__ float red[NBT][HS][HD];
+  const int tid = threadIdx.x, h = tid / LPH, lc = tid % LPH;
+  const bool act = h < p.nh;
+  const int hh = act ? h : 0;
+  const int b = blockIdx.y;
+  const int tile = blockIdx.x / nchunk, ci = blockIdx.x % nchunk;
+  const int r0 = tile * NBT;
+  const int nrows = mode == 0 ? p.nb : p.T;
+  const int rl = min(r0 + NBT, nrows) - 1;
+  auto lo = [&](int r) { return mode == 0 ? (r + 1) * p.m2 - 1 : r; };
+  auto hi = [&](int r) { return mode == 0 ? p.T : min(p.T, r + p.win); };
+  const int tlo = lo(r0) + ci * QC;
+  const int thi = min(hi(rl), tlo + QC);
+  float* out = (mode == 0 ? p.part_b : p.part_w) + (((size_t)b * ntile + tile) * nchunk + ci) * NBT * HD;
+  if (tlo >= thi) {
+    for (int i = tid; i < NBT * HD; i += 256) out[i] = 0.f;
+    return;
+  }
+  float k[NBT][8], acc[NBT][8];
+#pragma unroll
+  for (int i = 0; i < NBT; ++i) {
+    const int r = r0 + i;
+    if (r < nrows) {
+      load8((mode == 0 ? p.kc + ((size_t)b * p.nb + r) * HD : p.kl + ((size_t)b * p.T + r) * HD) + 8 * lc,
+            k[i]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) k[i][e] = 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[i][e] = 0.f;
+  }
+  for (int t = tlo; t < thi; ++t) {
+    const size_t i0 = ((size_t)b * p.T + t) * p.nh + hh;
+    float qn[8], dv[8];
+    load8(p.q + i0 * HD + 8 * lc, qn);
+    load8(p.dout + i0 * HD + 8 * lc, dv);
+    const float rq = p.rq[i0], lse = p.lse[i0], D = p.dval[i0];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qn[e] *= rq;
+    if (!act) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qn[e] = dv[e] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < NBT; ++i) {
+      const int r = r0 + i;
+      const bool valid = act && r < nrows && t >= lo(r) && t < hi(r);
+      float a = 0.f, c = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        a += qn[e] * k[i][e];
+        c += dv[e] * k[i][e];
+      }
+      const float s = hsum<LPH>(a) * p.scale, dp = hsum<LPH>(c);
+      const float pj = valid ? expf(s - lse) : 0.f;
+      const float ds = pj * (dp - D) * p.scale;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[i][e] += ds * qn[e] + pj * dv[e];
+    }
+  }
+  // the heads' sums
+#pragma unroll
+  for (int i = 0; i < NBT; ++i)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) red[i][h][8 * lc + e] = acc[i][e];
+  __syncthreads();
+  for (int o = tid; o < NBT * HD; o += 256) {
+    const int i = o / HD, c = o % HD;
+    float s = 0.f;
+    for (int hs = 0; hs < p.nh; ++hs) s += red[i][hs][c];
+    out[o] = s;
+  }
+}
+
+// block reduction over the first HD threads (HD <= 256, a multiple of 64)
+template <int HD>
+__device__ __forceinline__ float block_sum(float v, float* sh) {
+  const int tid = threadIdx.x;
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+  if ((tid & 63) == 0) sh[tid >> 6] = v;
+  __syncthreads();
+  float s = 0.f;
+#pragma unroll
+  for (int w = 0; w < HD / 64; ++w) s += sh[w];
+  __syncthreads();
+  return s;
+}
+
+template <int HD>
+__global__ __launch_bounds__(HD) void hca_bwd_block_kernel(HcaBwdParams p, int nchunk, int ntile) {
+  __shared__ float sh[4];
+  const int n = blockIdx.x, b = blockIdx.y, c = threadIdx.x;
+  const int tile = n / NBT, i = n % NBT;
+  float dk = 0.f;
+  for (int ci = 0; ci < nchunk; ++ci)
+    dk += p.part_b[((((size_t)b * ntile + tile) * nchunk + ci) * NBT + i) * HD + c];
+  const size_t ri = ((size_t)b * p.nb + n) * HD + c;
+  const float y = p.kc[ri], r = p.raw[ri];
+  const float yd = block_sum<HD>(y * dk, sh);
+  const float nrm = sqrtf(block_sum<HD>(r * r, sh));
+  const float dr = nrm > kEps ? (dk - y * yd) / nrm : dk / kEps;
+  // softmax over the block's m2 tokens of Z + B_pos (this channel)
+  const int m2 = p.m2;
+  float mx = -INFINITY;
+  for (int j = 0; j < m2; ++j) {
+    const size_t ti = ((size_t)b * p.T + (size_t)n * m2 + j) * HD + c;
+    mx = fmaxf(mx, p.Z[ti] + p.Bpos[j * HD + c]);
+  }
+  float den = 0.f;
+  for (int j = 0; j < m2; ++j) {
+    const size_t ti = ((size_t)b * p.T + (size_t)n * m2 + j) * HD + c;
+    den += expf(p.Z[ti] + p.Bpos[j * HD + c] - mx);
+  }
+  for (int j = 0; j < m2; ++j) {
+    const size_t ti = ((size_t)b * p.T + (size_t)n * m2 + j) * HD + c;
+    const float w = expf(p.Z[ti] + p.Bpos[j * HD + c] - mx) / den;
+    const float dz = w * (p.C[ti] - r) * dr;
+    p.dC[ti] = w * dr;
+    p.dZ[ti] = dz;
+    p.dBp[(((size_t)b * p.nb + n) * m2 + j) * HD + c] = dz;
+  }
+}
+
+template <int HD>
+__global__ __launch_bounds__(HD) void hca_bwd_window_kernel(HcaBwdParams p, int nchunk, int ntile) {
+  __shared__ float sh[4];
+  const int u = blockIdx.x, b = blockIdx.y, c = threadIdx.x;
+  const int tile = u / NBT, i = u % NBT;
+  float dk = 0.f;
+  for (int ci = 0; ci < nchunk; ++ci)
+    dk += p.part_w[((((size_t)b * ntile + tile) * nchunk + ci) * NBT + i) * HD + c];
+  const size_t ri = ((size_t)b * p.T + u) * HD + c;
+  const float y = p.kl[ri], x = p.lsrc[ri];
+  const float yd = block_sum<HD>(y * dk, sh);
+  const float nrm = sqrtf(block_sum<HD>(x * x, sh));
+  const float dx = nrm > kEps ? (dk - y * yd) / nrm : dk / kEps;
+  if (p.dlocal) p.dlocal[ri] = dx;
+  else p.dC[ri] += dx;
+}
+
+struct Plan {
+  int ntile_b, nchunk_b, ntile_w, nchunk_w;
+  size_t part_b, part_w;  // floats
+};
+
+Plan plan(int B, int T, int nb, int win, int HD) {
+  Plan z;
+  z.ntile_b = (nb + NBT - 1) / NBT;
+  z.nchunk_b = (T + QC - 1) / QC;
+  z.ntile_w = win > 0 ? (T + NBT - 1) / NBT : 0;
+  z.nchunk_w = win > 0 ? (NBT - 1 + win + QC - 1) / QC : 0;
+  z.part_b = (size_t)B * z.ntile_b * z.nchunk_b * NBT * HD;
+  z.part_w = (size_t)B * z.ntile_w * z.nchunk_w * NBT * HD;
+  return z;
+}
+
+size_t al256(size_t x) { return (x + 255) & ~size_t(255); }
+
+template <int HD>
+hipError_t launch_hca_bwd(const HcaBwdParams& p, const Plan& z, hipStream_t s) {
+  hipLaunchKernelGGL((hca_bwd_query_kernel<HD>), dim3((unsigned)((size_t)p.B * p.T)), dim3(256), 0, s, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (p.nb > 0) {
+    hipLaunchKernelGGL((hca_bwd_key_kernel<HD>), dim3(z.ntile_b * z.nchunk_b, p.B), dim3(256), 0, s, p, 0,
+                       z.nchunk_b, z.ntile_b);
+    hipLaunchKernelGGL((hca_bwd_block_kernel<HD>), dim3(p.nb, p.B), dim3(HD), 0, s, p, z.nchunk_b, z.ntile_b);
+  }
+  if (p.win > 0) {
+    hipLaunchKernelGGL((hca_bwd_key_kernel<HD>), dim3(z.ntile_w * z.nchunk_w, p.B), dim3(256), 0, s, p, 1,
+                       z.nchunk_w, z.ntile_w);
+    hipLaunchKernelGGL((hca_bwd_window_kernel<HD>), dim3(p.T, p.B), dim3(HD), 0, s, p, z.nchunk_w, z.ntile_w);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+size_t hca_bwd_ws_bytes(int B, int T, int nh, int c, int m2, int win) {
+  const Plan z = plan(B, T, T / m2, win, c);
+  return 3 * al256((size_t)B * T * nh * 4) + al256(z.part_b * 4) + al256(z.part_w * 4);
+}
+
+hipError_t hca_bwd_dispatch(HcaBwdParams p, void* ws, hipStream_t stream) {
+  const Plan z = plan(p.B, p.T, p.nb, p.win, p.c);
+  char* w = static_cast<char*>(ws);
+  const size_t per = al256((size_t)p.B * p.T * p.nh * 4);
+  p.lse = reinterpret_cast<float*>(w);
+  p.dval = reinterpret_cast<float*>(w + per);
+  p.rq = reinterpret_cast<float*>(w + 2 * per);
+  p.part_b = reinterpret_cast<float*>(w + 3 * per);
+  p.part_w = reinterpret_cast<float*>(w + 3 * per + al256(z.part_b * 4));
+  return p.c == 64 ? launch_hca_bwd<64>(p, z, stream) : launch_hca_bwd<128>(p, z, stream);
+}
+
+}  // namespace kch

@@ -54,6 +54,36 @@ size_t kda_bwd_ws_bytes(int B, int T, int HV, int K, int V, bool f64);
 // 256-byte aligned, kda_bwd_ws_bytes bytes
 hipError_t kda_bwd_dispatch(KdaBwdParams p, int dtype, void* ws, hipStream_t stream);
 
+// Gradients of the HCA attention (hca_backward.hip), fp32 tensors, c in
+// {64, 128}, nh <= 256 / (c / 8), T a multiple of m2.
+struct HcaBwdParams {
+  const float* q;       // [B,T,nh,c] queries as given (not normalised)
+  const float* dout;    // [B,T,nh,c]
+  const float* kc;      // [B,nb,c] L2-normalised compressed rows
+  const float* raw;     // [B,nb,c] compressed rows
+  const float* kl;      // [B,T,c] L2-normalised window rows (win > 0)
+  const float* lsrc;    // [B,T,c] rows the window keys normalise (win > 0)
+  const float* C;       // [B,T,c] compression inputs
+  const float* Z;
+  const float* Bpos;    // [m2,c]
+  const float* sink;    // [nh] or null
+  float* dq;            // [B,T,nh,c]
+  float* dC;            // [B,T,c]
+  float* dZ;            // [B,T,c]
+  float* dBp;           // [B,nb,m2,c] per-block terms of dB_pos
+  float* dlocal;        // [B,T,c] gradient of the window rows' source, or null: added to dC
+  float* sink_part;     // [B,T,nh] p_sink * D per query and head, or null
+  float* lse = nullptr;  // workspace regions, set by hca_bwd_dispatch
+  float* dval = nullptr;
+  float* rq = nullptr;
+  float* part_b = nullptr;
+  float* part_w = nullptr;
+  int B, T, nh, c, m2, nb, win;
+  float scale;
+};
+size_t hca_bwd_ws_bytes(int B, int T, int nh, int c, int m2, int win);
+hipError_t hca_bwd_dispatch(HcaBwdParams p, void* ws, hipStream_t stream);
+
 hipError_t kda_chunk_dispatch(const KdaParams& p, int dtype, hipStream_t stream);
 // fp64 inputs, state and arithmetic (kda_recurrent.hip)
 hipError_t kda_recurrent_f64_dispatch(const KdaParams& p, hipStream_t stream);

@@ -35,6 +35,7 @@ _SIGNATURES = {
     "kch_kda_recurrent_fwd": [_P] * 8 + [_I] * 6 + [_F, _F, _I, _P],
     "kch_kda_recurrent_fwd_f64": [_P] * 8 + [_I] * 6 + [_D, _D, _P],
     "kch_kda_recurrent_bwd": [_P] * 14 + [_I] * 6 + [_D, _D, _I, _P, _SZ, _P],
+    "kch_hca_attn_bwd": [_P] * 16 + [_I] * 6 + [_F, _P, _SZ, _P],
     "kch_compress": [_P, _L, _P, _L, _P, _P, _P, _I, _I, _P, _I, _I, _I, _I, _I, _P],
     "kch_compress_overlapped": [_P, _L, _P, _L, _P, _L, _P, _L, _P, _P, _P, _P, _I, _I, _P,
                                 _I, _I, _I, _I, _I, _P],
@@ -71,6 +72,7 @@ _SIGNATURES = {
 _QUERIES = {
     "kch_kda_chunk_ws_bytes": (_SZ, [_I] * 7),
     "kch_kda_recurrent_bwd_ws_bytes": (_SZ, [_I] * 6),
+    "kch_hca_attn_bwd_ws_bytes": (_SZ, [_I] * 6),
     "kch_decode_ws_bytes": (_SZ, [_I] * 7),
     "kch_decode_dyn_ws_bytes": (_SZ, [_I] * 7),
 }

@@ -460,3 +460,118 @@ def naive_hca(H, W, *, m2, nh, c, sliding_window=0, sink=None, dtype='bf16'):
     out = hca_core(C, Z, q, W['B_pos'], m2=m2, sliding_window=sliding_window,
                    sink_logits=sink)
     return round_to(out.reshape(Bn, T, nh * c), dtype), (C, Z, q)
+
+
+def _l2n_grad(x, dy, eps=1e-12):
+    """Backward of ``l2_normalize`` (``F.normalize``): for ``||x|| > eps``,
+    ``dx = (dy - y (y . dy)) / ||x||`` with ``y = x / ||x||``."""
+    n = np.sqrt((x * x).sum(-1, keepdims=True))
+    big = n > eps
+    nn = np.where(big, n, eps)
+    y = x / nn
+    return np.where(big, (dy - y * (y * dy).sum(-1, keepdims=True)) / nn, dy / nn)
+
+
+def compress_kv_grad(C, Z, B_pos, m, d_out):
+    """Backward of ``compress_kv`` (``ops_csa.py:198-234``) for ``d_out``
+    ``[B, T//m, c]``. With ``w = softmax_j(Z + B)`` per channel over the m
+    tokens of a block and ``r = sum_j w_j C_j``: ``dC_j = w_j dr``,
+    ``dZ_j = w_j (C_j - r) dr``, ``dB_j = sum over blocks of dZ_j``.
+    Returns ``(dC, dZ, dB)``."""
+    C = np.asarray(C, np.float64)
+    Z = np.asarray(Z, np.float64)
+    Bn, T, c = C.shape
+    nb = T // m
+    Cb = C.reshape(Bn, nb, m, c)
+    lg = Z.reshape(Bn, nb, m, c) + np.asarray(B_pos, np.float64)[None, None]
+    e = np.exp(lg - lg.max(axis=2, keepdims=True))
+    w = e / e.sum(axis=2, keepdims=True)
+    r = (w * Cb).sum(axis=2, keepdims=True)
+    dr = np.asarray(d_out, np.float64)[:, :, None]
+    dC = (w * dr).reshape(Bn, T, c)
+    dlg = w * (Cb - r) * dr
+    return dC, dlg.reshape(Bn, T, c), dlg.sum(axis=(0, 1))
+
+
+def hca_core_grad(C, Z, q, B_pos, d_out, *, m2, sliding_window=0, sink_logits=None,
+                  scale=1.0, C_local_raw=None):
+    """Gradients of ``hca_core`` (``ops_hca.py:132-194``, differentiated by
+    autograd in the reference) for ``d_out = dL/dout`` ``[B,T,nh,c]``, in fp64.
+
+    With ``p`` the joint softmax over the causal blocks, the window and the
+    sink, keys ``k_j`` (= values) the L2-normalised compressed rows and window
+    rows, ``qn`` the L2-normalised queries: ``dp_j = dout . k_j``,
+    ``D = sum_j p_j dp_j``, ``ds_j = p_j (dp_j - D)``, ``dqn = scale sum_j ds_j
+    k_j``, ``dk_j += scale ds_j qn + p_j dout``, ``dsink = -sum p_sink D``;
+    then the L2-norm and compression backwards. Returns a dict with ``C, Z,
+    q, B_pos`` and ``sink_logits`` / ``C_local_raw`` where given."""
+    f = np.float64
+    C, Z, q, d_out = (np.asarray(x, f) for x in (C, Z, q, d_out))
+    Bn, T, c = C.shape
+    nh = q.shape[2]
+    pad = (-T) % m2
+    Cp, Zp, qp, dop = (_pad_time(x, pad) for x in (C, Z, q, d_out))
+    Clr = None if C_local_raw is None else _pad_time(np.asarray(C_local_raw, f), pad)
+    Tp = T + pad
+    nb = Tp // m2
+    raw = compress_kv(Cp, Zp, B_pos, m2, f)
+    Cn = l2_normalize(raw)
+    qn = l2_normalize(qp)
+    cbm = causal_block_mask(Tp, nb, m2)
+    sc = np.einsum('bthd,bnd->bhtn', qn, Cn) * scale
+    sc = np.where(cbm[None, None], sc, -np.inf)
+    w = sliding_window
+    src_local = Cp if Clr is None else Clr
+    if w > 0:
+        Cl = l2_normalize(src_local)
+        sw, Cw, valid = window_scores(qn, Cl, w, scale)
+        sw = sw.transpose(0, 2, 1, 3)
+    else:
+        Cl = None
+        sw = np.zeros((Bn, nh, Tp, 0))
+        Cw = np.zeros((Bn, Tp, 0, c))
+    cat = np.concatenate([sc, sw], axis=-1)
+    sink = None if sink_logits is None else np.asarray(sink_logits, f).reshape(1, nh, 1, 1)
+    grads = {}
+    if cat.shape[-1] == 0:
+        p = np.zeros((Bn, nh, Tp, 0))
+    else:
+        p = joint_softmax_hca(cat, sink)
+    pb, pw = p[..., :nb], p[..., nb:]
+    out = np.einsum('bhtn,bnd->bthd', pb, Cn) + np.einsum('bhtw,btwd->bthd', pw, Cw)
+    dp_b = np.einsum('bthd,bnd->bhtn', dop, Cn)
+    dp_w = np.einsum('bthd,btwd->bhtw', dop, Cw)
+    D = np.einsum('bthd,bthd->bht', dop, out)[..., None]
+    ds_b = pb * (dp_b - D)
+    ds_w = pw * (dp_w - D)
+    dqn = scale * (np.einsum('bhtn,bnd->bthd', ds_b, Cn) + np.einsum('bhtw,btwd->bthd', ds_w, Cw))
+    dCn = (scale * np.einsum('bhtn,bthd->bnd', ds_b, qn)
+           + np.einsum('bhtn,bthd->bnd', pb, dop))
+    dC = np.zeros_like(Cp)
+    dq = _l2n_grad(qp, dqn)
+    draw = _l2n_grad(raw, dCn)
+    dCc, dZ, dB = compress_kv_grad(Cp, Zp, B_pos, m2, draw)
+    dC += dCc
+    if w > 0:
+        dCw = (scale * np.einsum('bhtw,bthd->btwd', ds_w, qn)
+               + np.einsum('bhtw,bthd->btwd', pw, dop))      # [B, T, w, c]
+        dCl = np.zeros_like(Cl)
+        for i in range(w):
+            # slot i of query t is position t - w + 1 + i
+            src = np.arange(Tp) - w + 1 + i
+            ok = src >= 0
+            np.add.at(dCl, (slice(None), src[ok]), dCw[:, ok, i])
+        dloc = _l2n_grad(src_local, dCl)
+        if Clr is None:
+            dC += dloc
+        else:
+            grads['C_local_raw'] = dloc[:, :T]
+    if sink is not None:
+        row_max = cat.max(-1, keepdims=True) if cat.shape[-1] else np.zeros((Bn, nh, Tp, 1))
+        row_max = np.where(np.isneginf(row_max), 0, row_max)
+        with np.errstate(divide='ignore'):
+            lse = np.log(np.exp(cat - row_max).sum(-1, keepdims=True)) + row_max
+        p_sink = np.exp(sink - np.logaddexp(lse, sink))
+        grads['sink_logits'] = -(p_sink * D).sum(axis=(0, 2, 3))
+    grads.update(C=dC[:, :T], Z=dZ[:, :T], q=dq[:, :T], B_pos=dB)
+    return grads

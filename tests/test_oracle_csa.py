@@ -309,3 +309,64 @@ def test_hca_core_at_equals_hca_core_rows(win, sink):
     out2 = O.hca_core_at(C, Z, q, Bp, m2=m2, queries=Q, sliding_window=win, sink_logits=sk,
                          C_comp=O.compress_kv(C, Z, Bp, m2))
     np.testing.assert_array_equal(out2, out)
+
+
+def _fd_worst(loss, args, grads):
+    """Largest |central difference - gradient| / (|num| + |ana| + 1e-2) over
+    every coordinate of every argument (the floor absorbs the ~1e-10 rounding
+    noise of the differences; a dropped or wrong term moves a gradient by its
+    own size)."""
+    worst = 0.0
+    for name, x in args.items():
+        for idx in np.ndindex(*x.shape):
+            orig = x[idx]
+            x[idx] = orig + 1e-6
+            lp = loss()
+            x[idx] = orig - 1e-6
+            lm = loss()
+            x[idx] = orig
+            num = (lp - lm) / 2e-6
+            a = grads[name][idx]
+            worst = max(worst, abs(num - a) / (abs(num) + abs(a) + 1e-2))
+    return worst
+
+
+@pytest.mark.parametrize("T,win,sink,local", [(10, 3, True, False), (12, 0, False, False),
+                                              (8, 5, True, True)])
+def test_hca_core_grad_matches_finite_differences(T, win, sink, local):
+    """``hca_core_grad`` (queries, compression inputs, window rows, sink) against
+    central differences of ``hca_core`` in fp64, every coordinate; T=10 pads to
+    a multiple of m2=4."""
+    from oracle.csa import hca_core_grad
+    rng = np.random.default_rng(T + win)
+    B, m2, nh, c = 1, 4, 2, 4
+    a = dict(C=rng.standard_normal((B, T, c)), Z=rng.standard_normal((B, T, c)),
+             q=rng.standard_normal((B, T, nh, c)), B_pos=rng.standard_normal((m2, c)) * 0.3)
+    if sink:
+        a["sink_logits"] = rng.standard_normal(nh)
+    if local:
+        a["C_local_raw"] = rng.standard_normal((B, T, c))
+    W = rng.standard_normal((B, T, nh, c))
+    kw = dict(m2=m2, sliding_window=win, scale=1.3)
+
+    def loss():
+        return float((O.hca_core(compute=np.float64, **kw, **a) * W).sum())
+
+    g = hca_core_grad(d_out=W, **kw, **a)
+    assert set(g) == set(a)
+    assert _fd_worst(loss, a, g) < 1e-6
+
+
+def test_compress_kv_grad_matches_finite_differences():
+    from oracle.csa import compress_kv_grad
+    rng = np.random.default_rng(2)
+    B, T, c, m = 2, 12, 3, 4
+    a = dict(C=rng.standard_normal((B, T, c)), Z=rng.standard_normal((B, T, c)),
+             B_pos=rng.standard_normal((m, c)))
+    W = rng.standard_normal((B, T // m, c))
+
+    def loss():
+        return float((O.compress_kv(a["C"], a["Z"], a["B_pos"], m, np.float64) * W).sum())
+
+    dC, dZ, dB = compress_kv_grad(a["C"], a["Z"], a["B_pos"], m, W)
+    assert _fd_worst(loss, a, dict(C=dC, Z=dZ, B_pos=dB)) < 1e-6
