@@ -152,6 +152,30 @@ int kch_hca_attn_bwd(const float* q, const float* d_out, const float* kc, const 
                      int m2, int win, float scale, void* ws, size_t ws_bytes, void* stream);
 
 /*
+ * Gradients of the CSA attention: the backward of the sparse attention of
+ * csa_core / naive_csa (ops_csa.py:869-1155, differentiated by autograd in the
+ * reference; run_correctness.py:1312-1473, 2710-2830) with the selection held
+ * fixed. Tensors as for kch_hca_attn_bwd, plus: idx [B,T,topk] int32 (the
+ * selection, -1 = unused slot), the overlapped compression's inputs Ca, Cb,
+ * Za, Zb [B,T,c], Ba, Bb [m,c] (kc / raw from kch_compress_overlapped; kl,
+ * lsrc the window rows of Ca), normalize = 0 for normalize_qk=False (queries
+ * and keys used as given). Outputs: dq; dCa, dCb, dZa, dZb [B,T,c] (dCb, dZb
+ * must be zeroed by the caller: the last block's second-branch rows receive
+ * nothing); dBap, dBbp [B,T/m,m,c]; sink_part as for HCA; slot_grad
+ * [B,T,topk] (zeroed by the caller): the gradient of each selected row dotted
+ * with that row, which the STE surrogate (ops_csa.py:1033-1099) turns into
+ * the indexer's gradient. The window rows' gradient is added into dCa.
+ */
+size_t kch_csa_attn_bwd_ws_bytes(int B, int T, int nh, int c, int m, int win, int topk);
+int kch_csa_attn_bwd(const float* q, const float* d_out, const float* kc, const float* raw,
+                     const float* kl, const float* lsrc, const int* idx, const float* Ca,
+                     const float* Cb, const float* Za, const float* Zb, const float* Ba,
+                     const float* Bb, const float* sink, float* dq, float* dCa, float* dCb,
+                     float* dZa, float* dZb, float* dBap, float* dBbp, float* sink_part,
+                     float* slot_grad, int B, int T, int nh, int c, int m, int topk, int win,
+                     float scale, int normalize, void* ws, size_t ws_bytes, void* stream);
+
+/*
  * Single-branch softmax-gated KV compression, [B,T,c] -> [B,T/m,c].
  * Replaces csa_compress_kv (ops_csa.py:198-234); used for the CSA indexer keys
  * (ops_csa.py:874) and for HCA (ops_hca.py:134).

@@ -267,7 +267,7 @@ int kch_kda_recurrent_bwd(const void* q, const void* k, const void* v, const voi
 
 size_t kch_hca_attn_bwd_ws_bytes(int B, int T, int nh, int c, int m2, int win) {
   if (B <= 0 || T <= 0 || nh < 1 || (c != 64 && c != 128) || m2 < 1 || T % m2 || win < 0) return 0;
-  return kch::hca_bwd_ws_bytes(B, T, nh, c, m2, win);
+  return kch::hca_bwd_ws_bytes(B, T, nh, c, m2, win, 0);
 }
 
 int kch_hca_attn_bwd(const float* q, const float* d_out, const float* kc, const float* raw,
@@ -303,6 +303,58 @@ int kch_hca_attn_bwd(const float* q, const float* d_out, const float* kc, const 
   p.C = C; p.Z = Z; p.Bpos = B_pos; p.sink = sink;
   p.dq = dq; p.dC = dC; p.dZ = dZ; p.dBp = dBp; p.dlocal = dlocal; p.sink_part = sink_part;
   p.B = B; p.T = T; p.nh = nh; p.c = c; p.m2 = m2; p.nb = T / m2; p.win = win;
+  p.scale = scale;
+  return hip_status(fn, kch::hca_bwd_dispatch(p, ws, (hipStream_t)stream));
+}
+
+size_t kch_csa_attn_bwd_ws_bytes(int B, int T, int nh, int c, int m, int win, int topk) {
+  if (B <= 0 || T <= 0 || nh < 1 || (c != 64 && c != 128) || m < 1 || T % m || win < 0 || topk < 0)
+    return 0;
+  return kch::hca_bwd_ws_bytes(B, T, nh, c, m, win, topk);
+}
+
+int kch_csa_attn_bwd(const float* q, const float* d_out, const float* kc, const float* raw,
+                     const float* kl, const float* lsrc, const int* idx, const float* Ca,
+                     const float* Cb, const float* Za, const float* Zb, const float* Ba,
+                     const float* Bb, const float* sink, float* dq, float* dCa, float* dCb,
+                     float* dZa, float* dZb, float* dBap, float* dBbp, float* sink_part,
+                     float* slot_grad, int B, int T, int nh, int c, int m, int topk, int win,
+                     float scale, int normalize, void* ws, size_t ws_bytes, void* stream) {
+  const char* fn = "kch_csa_attn_bwd";
+  if (B < 0 || T < 1 || nh < 1 || m < 1 || win < 0 || topk < 0)
+    return fail(KCH_ERR_INVALID, "%s: bad sizes B=%d T=%d nh=%d m=%d win=%d topk=%d (T >= 1)", fn, B,
+                T, nh, m, win, topk);
+  if (T % m) return fail(KCH_ERR_INVALID, "%s: T=%d must be a multiple of m=%d", fn, T, m);
+  if (c != 64 && c != 128) return fail(KCH_ERR_UNSUPPORTED, "%s: c=%d not supported (64 or 128)", fn, c);
+  if (nh * (c / 8) > 256)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: nh=%d heads of %d exceed one workgroup", fn, nh, c);
+  if (std::isnan(scale)) return fail(KCH_ERR_INVALID, "%s: scale is NaN", fn);
+  if ((long long)B * T * nh * c >= (1LL << 40) || (long long)B * T * topk >= (1LL << 40))
+    return fail(KCH_ERR_UNSUPPORTED, "%s: tensors too large", fn);
+  if (B == 0) return KCH_OK;
+  if (!q || !d_out || !kc || !raw || !Ca || !Cb || !Za || !Zb || !Ba || !Bb || !dq || !dCa || !dCb ||
+      !dZa || !dZb || !dBap || !dBbp || (topk > 0 && !idx))
+    return fail(KCH_ERR_INVALID, "%s: null tensor pointer", fn);
+  if (win > 0 && (!kl || !lsrc)) return fail(KCH_ERR_INVALID, "%s: window rows required (win > 0)", fn);
+  const size_t need = kch_csa_attn_bwd_ws_bytes(B, T, nh, c, m, win, topk);
+  if (!ws || ws_bytes < need)
+    return fail(KCH_ERR_INVALID, "%s: workspace of %zu bytes required, got %zu", fn, need,
+                ws ? ws_bytes : (size_t)0);
+  if ((uintptr_t)ws & 255) return fail(KCH_ERR_INVALID, "%s: workspace must be 256-byte aligned", fn);
+  for (const void* ptr : {(const void*)q, (const void*)d_out, (const void*)kc, (const void*)kl,
+                          (const void*)dq})
+    if ((uintptr_t)ptr & 15) return fail(KCH_ERR_INVALID, "%s: q, d_out, kc, kl, dq must be 16-byte aligned", fn);
+  kch::HcaBwdParams p;
+  p.q = q; p.dout = d_out; p.kc = kc; p.raw = raw; p.kl = kl; p.lsrc = lsrc;
+  p.C = Ca; p.Z = Za; p.Bpos = Ba; p.sink = sink;
+  p.Cb = Cb; p.Zb = Zb; p.Bb = Bb;
+  p.dq = dq; p.dC = dCa; p.dZ = dZa; p.dBp = dBap; p.dlocal = nullptr; p.sink_part = sink_part;
+  p.dCb = dCb; p.dZb = dZb; p.dBbp = dBbp;
+  p.idx = topk > 0 ? idx : nullptr;
+  p.topk = topk;
+  p.slot_grad = topk > 0 ? slot_grad : nullptr;
+  p.normalize = normalize ? 1 : 0;
+  p.B = B; p.T = T; p.nh = nh; p.c = c; p.m2 = m; p.nb = T / m; p.win = win;
   p.scale = scale;
   return hip_status(fn, kch::hca_bwd_dispatch(p, ws, (hipStream_t)stream));
 }

@@ -27,6 +27,7 @@
 // hca_bwd_window_kernel one workgroup per (b, token): the window row's
 //   L2-norm backward, added to dC (or written to dlocal).
 
+#include "kch_csa.h"
 #include "kch_device.h"
 #include "kch_kernels.h"
 
@@ -81,17 +82,23 @@ __global__ __launch_bounds__(256) void hca_bwd_query_kernel(HcaBwdParams p) {
 #pragma unroll
   for (int e = 0; e < 8; ++e) ss += qn[e] * qn[e];
   const float nrm = sqrtf(hsum<LPH>(ss));
-  const float rq = 1.f / fmaxf(nrm, kEps);
+  const float rq = p.normalize ? 1.f / fmaxf(nrm, kEps) : 1.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) qn[e] *= rq;
 
-  const int nvis = min((t + 1) / p.m2, p.nb);
+  // keys: the selected blocks (CSA; the selection's -1 slots are skipped) or
+  // every block the query sees (HCA), then the window rows
+  const int* sel_row = p.idx ? p.idx + bt * p.topk : nullptr;
+  const int nvis = p.idx ? p.topk : min((t + 1) / p.m2, p.nb);
   const int i0 = p.win > 0 ? max(0, p.win - 1 - t) : 0;
   const int nwin = p.win > 0 ? p.win - i0 : 0;
   const int nk = nvis + nwin;
   const int wpos0 = t - p.win + 1 + i0;  // first window position
+  // (an unused selection slot points at row 0 and is masked by kvalid)
+  auto kblock = [&](int j) { return sel_row ? max(sel_row[j], 0) : j; };
+  auto kvalid = [&](int j) { return j >= nvis || !sel_row || sel_row[j] >= 0; };
   auto krow = [&](int j) -> const float* {
-    return j < nvis ? p.kc + ((size_t)b * p.nb + j) * HD + 8 * lc
+    return j < nvis ? p.kc + ((size_t)b * p.nb + kblock(j)) * HD + 8 * lc
                     : p.kl + ((size_t)b * p.T + wpos0 + (j - nvis)) * HD + 8 * lc;
   };
   auto score = [&](const float* k, float& s, float& dp) {
@@ -113,11 +120,13 @@ __global__ __launch_bounds__(256) void hca_bwd_query_kernel(HcaBwdParams p) {
     if (j + 1 < nk) load8(krow(j + 1), kn);
     float s, dp;
     score(kc, s, dp);
-    const float mn = fmaxf(m, s);
-    const float a = expf(m - mn), e1 = expf(s - mn);
-    l = l * a + e1;
-    ad = ad * a + e1 * dp;
-    m = mn;
+    if (kvalid(j)) {
+      const float mn = fmaxf(m, s);
+      const float a = expf(m - mn), e1 = expf(s - mn);
+      l = l * a + e1;
+      ad = ad * a + e1 * dp;
+      m = mn;
+    }
 #pragma unroll
     for (int e = 0; e < 8; ++e) kc[e] = kn[e];
   }
@@ -142,9 +151,15 @@ __global__ __launch_bounds__(256) void hca_bwd_query_kernel(HcaBwdParams p) {
     if (j + 1 < nk) load8(krow(j + 1), kn);
     float s, dp;
     score(kc, s, dp);
-    const float ds = expf(s - lse) * (dp - D) * p.scale;
+    const float pj = kvalid(j) ? expf(s - lse) : 0.f;
+    const float ds = pj * (dp - D) * p.scale;
 #pragma unroll
     for (int e = 0; e < 8; ++e) dq[e] += ds * kc[e];
+    // the selected row's gradient dotted with the row, this head's share:
+    // (scale p (dp - D) qn + p dout) . k = p ((dp - D) s + dp); the heads add
+    // into slot_grad (zeroed by the caller)
+    if (p.slot_grad && act && lc == 0 && j < nvis && kvalid(j))
+      atomicAdd(p.slot_grad + bt * p.topk + j, pj * ((dp - D) * s + dp));
 #pragma unroll
     for (int e = 0; e < 8; ++e) kc[e] = kn[e];
   }
@@ -156,7 +171,8 @@ __global__ __launch_bounds__(256) void hca_bwd_query_kernel(HcaBwdParams p) {
   if (act) {
     float o[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = (nrm > kEps ? dq[e] - qn[e] * yd : dq[e]) * rq;
+    for (int e = 0; e < 8; ++e)
+      o[e] = p.normalize ? (nrm > kEps ? dq[e] - qn[e] * yd : dq[e]) * rq : dq[e];
     float* dst = p.dq + qoff;
     *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
     *reinterpret_cast<float4*>(dst + 4) = make_float4(o[4], o[5], o[6], o[7]);
@@ -206,8 +222,18 @@ __global__ __launch_bounds__(256) void hca_bwd_key_kernel(HcaBwdParams p, int mo
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[i][e] = 0.f;
   }
+  const int nw = (p.nb + 31) / 32;  // selection bitmap words per query
   for (int t = tlo; t < thi; ++t) {
     const size_t i0 = ((size_t)b * p.T + t) * p.nh + hh;
+    // CSA: the tile's rows this query selected (NBT consecutive bits)
+    uint32_t selbits = 0xffffffffu;
+    if (mode == 0 && p.sel) {
+      const uint32_t* w = p.sel + ((size_t)b * p.T + t) * nw;
+      const int w0 = r0 >> 5, sh = r0 & 31;
+      uint64_t two = w[w0];
+      if (w0 + 1 < nw) two |= (uint64_t)w[w0 + 1] << 32;
+      selbits = (uint32_t)(two >> sh);
+    }
     float qn[8], dv[8];
     load8(p.q + i0 * HD + 8 * lc, qn);
     load8(p.dout + i0 * HD + 8 * lc, dv);
@@ -221,7 +247,7 @@ __global__ __launch_bounds__(256) void hca_bwd_key_kernel(HcaBwdParams p, int mo
 #pragma unroll
     for (int i = 0; i < NBT; ++i) {
       const int r = r0 + i;
-      const bool valid = act && r < nrows && t >= lo(r) && t < hi(r);
+      const bool valid = act && r < nrows && t >= lo(r) && t < hi(r) && ((selbits >> i) & 1u);
       float a = 0.f, c = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -275,9 +301,45 @@ __global__ __launch_bounds__(HD) void hca_bwd_block_kernel(HcaBwdParams p, int n
   const float y = p.kc[ri], r = p.raw[ri];
   const float yd = block_sum<HD>(y * dk, sh);
   const float nrm = sqrtf(block_sum<HD>(r * r, sh));
-  const float dr = nrm > kEps ? (dk - y * yd) / nrm : dk / kEps;
-  // softmax over the block's m2 tokens of Z + B_pos (this channel)
+  const float dr = !p.normalize ? dk : (nrm > kEps ? (dk - y * yd) / nrm : dk / kEps);
   const int m2 = p.m2;
+  if (p.Cb) {
+    // overlapped: block n mixes Ca of its own tokens with Cb of block n-1's,
+    // one softmax over the 2 m logits (block 0 has no second branch)
+    auto la = [&](int j) { return p.Z[((size_t)b * p.T + (size_t)n * m2 + j) * HD + c] + p.Bpos[j * HD + c]; };
+    auto lb = [&](int j) {
+      return p.Zb[((size_t)b * p.T + (size_t)(n - 1) * m2 + j) * HD + c] + p.Bb[j * HD + c];
+    };
+    float mx = -INFINITY;
+    for (int j = 0; j < m2; ++j) mx = fmaxf(mx, la(j));
+    if (n > 0)
+      for (int j = 0; j < m2; ++j) mx = fmaxf(mx, lb(j));
+    float den = 0.f;
+    for (int j = 0; j < m2; ++j) den += expf(la(j) - mx);
+    if (n > 0)
+      for (int j = 0; j < m2; ++j) den += expf(lb(j) - mx);
+    for (int j = 0; j < m2; ++j) {
+      const size_t ti = ((size_t)b * p.T + (size_t)n * m2 + j) * HD + c;
+      const float w = expf(la(j) - mx) / den;
+      const float dz = w * (p.C[ti] - r) * dr;
+      p.dC[ti] = w * dr;
+      p.dZ[ti] = dz;
+      p.dBp[(((size_t)b * p.nb + n) * m2 + j) * HD + c] = dz;
+    }
+    for (int j = 0; j < m2; ++j) {
+      float dz = 0.f;
+      if (n > 0) {
+        const size_t ti = ((size_t)b * p.T + (size_t)(n - 1) * m2 + j) * HD + c;
+        const float w = expf(lb(j) - mx) / den;
+        dz = w * (p.Cb[ti] - r) * dr;
+        p.dCb[ti] = w * dr;
+        p.dZb[ti] = dz;
+      }
+      p.dBbp[(((size_t)b * p.nb + n) * m2 + j) * HD + c] = dz;
+    }
+    return;
+  }
+  // softmax over the block's m2 tokens of Z + B_pos (this channel)
   float mx = -INFINITY;
   for (int j = 0; j < m2; ++j) {
     const size_t ti = ((size_t)b * p.T + (size_t)n * m2 + j) * HD + c;
@@ -310,9 +372,19 @@ __global__ __launch_bounds__(HD) void hca_bwd_window_kernel(HcaBwdParams p, int 
   const float y = p.kl[ri], x = p.lsrc[ri];
   const float yd = block_sum<HD>(y * dk, sh);
   const float nrm = sqrtf(block_sum<HD>(x * x, sh));
-  const float dx = nrm > kEps ? (dk - y * yd) / nrm : dk / kEps;
+  const float dx = !p.normalize ? dk : (nrm > kEps ? (dk - y * yd) / nrm : dk / kEps);
   if (p.dlocal) p.dlocal[ri] = dx;
   else p.dC[ri] += dx;
+}
+
+// bit n of word (b, t, n / 32) set when query (b, t) selected block n
+__global__ __launch_bounds__(256) void sel_bitmap_kernel(const int* idx, uint32_t* sel, long long nq,
+                                                         int topk, int nw) {
+  const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= nq * topk) return;
+  const long long q = i / topk;
+  const int n = idx[i];
+  if (n >= 0) atomicOr(sel + q * nw + (n >> 5), 1u << (n & 31));
 }
 
 struct Plan {
@@ -335,6 +407,11 @@ size_t al256(size_t x) { return (x + 255) & ~size_t(255); }
 
 template <int HD>
 hipError_t launch_hca_bwd(const HcaBwdParams& p, const Plan& z, hipStream_t s) {
+  if (p.idx && p.topk > 0) {
+    const long long n = (long long)p.B * p.T * p.topk;
+    hipLaunchKernelGGL(sel_bitmap_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p.idx,
+                       const_cast<uint32_t*>(p.sel), (long long)p.B * p.T, p.topk, (p.nb + 31) / 32);
+  }
   hipLaunchKernelGGL((hca_bwd_query_kernel<HD>), dim3((unsigned)((size_t)p.B * p.T)), dim3(256), 0, s, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -353,9 +430,10 @@ hipError_t launch_hca_bwd(const HcaBwdParams& p, const Plan& z, hipStream_t s) {
 
 }  // namespace
 
-size_t hca_bwd_ws_bytes(int B, int T, int nh, int c, int m2, int win) {
+size_t hca_bwd_ws_bytes(int B, int T, int nh, int c, int m2, int win, int topk) {
   const Plan z = plan(B, T, T / m2, win, c);
-  return 3 * al256((size_t)B * T * nh * 4) + al256(z.part_b * 4) + al256(z.part_w * 4);
+  const size_t sel = topk > 0 ? al256((size_t)B * T * ((T / m2 + 31) / 32) * 4) : 0;
+  return 3 * al256((size_t)B * T * nh * 4) + al256(z.part_b * 4) + al256(z.part_w * 4) + sel;
 }
 
 hipError_t hca_bwd_dispatch(HcaBwdParams p, void* ws, hipStream_t stream) {
@@ -367,6 +445,14 @@ hipError_t hca_bwd_dispatch(HcaBwdParams p, void* ws, hipStream_t stream) {
   p.rq = reinterpret_cast<float*>(w + 2 * per);
   p.part_b = reinterpret_cast<float*>(w + 3 * per);
   p.part_w = reinterpret_cast<float*>(w + 3 * per + al256(z.part_b * 4));
+  p.sel = nullptr;
+  if (p.idx && p.topk > 0) {
+    uint32_t* sel = reinterpret_cast<uint32_t*>(w + 3 * per + al256(z.part_b * 4) + al256(z.part_w * 4));
+    // cleared by the fill kernel (no memset node under graph capture)
+    hipError_t e = fill_u32(sel, (long long)p.B * p.T * ((p.nb + 31) / 32), 0u, stream);
+    if (e != hipSuccess) return e;
+    p.sel = sel;
+  }
   return p.c == 64 ? launch_hca_bwd<64>(p, z, stream) : launch_hca_bwd<128>(p, z, stream);
 }
 

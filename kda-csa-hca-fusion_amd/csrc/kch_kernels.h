@@ -73,6 +73,21 @@ struct HcaBwdParams {
   float* dBp;           // [B,nb,m2,c] per-block terms of dB_pos
   float* dlocal;        // [B,T,c] gradient of the window rows' source, or null: added to dC
   float* sink_part;     // [B,T,nh] p_sink * D per query and head, or null
+  int normalize = 1;    // 0: queries and keys are used as given (no L2 norms)
+  // CSA: the selected blocks (idx [B,T,topk], -1 = unused) instead of every
+  // causal block, its bitmap sel [B,T,ceil(nb/32)], the overlapped
+  // compression's second branch, and the per-slot gradient of the selected
+  // rows against themselves (slot_grad [B,T,topk], for the STE surrogate)
+  const int* idx = nullptr;
+  const uint32_t* sel = nullptr;
+  int topk = 0;
+  const float* Cb = nullptr;
+  const float* Zb = nullptr;
+  const float* Bb = nullptr;
+  float* dCb = nullptr;
+  float* dZb = nullptr;
+  float* dBbp = nullptr;
+  float* slot_grad = nullptr;
   float* lse = nullptr;  // workspace regions, set by hca_bwd_dispatch
   float* dval = nullptr;
   float* rq = nullptr;
@@ -81,7 +96,7 @@ struct HcaBwdParams {
   int B, T, nh, c, m2, nb, win;
   float scale;
 };
-size_t hca_bwd_ws_bytes(int B, int T, int nh, int c, int m2, int win);
+size_t hca_bwd_ws_bytes(int B, int T, int nh, int c, int m2, int win, int topk);
 hipError_t hca_bwd_dispatch(HcaBwdParams p, void* ws, hipStream_t stream);
 
 hipError_t kda_chunk_dispatch(const KdaParams& p, int dtype, hipStream_t stream);

@@ -36,6 +36,7 @@ _SIGNATURES = {
     "kch_kda_recurrent_fwd_f64": [_P] * 8 + [_I] * 6 + [_D, _D, _P],
     "kch_kda_recurrent_bwd": [_P] * 14 + [_I] * 6 + [_D, _D, _I, _P, _SZ, _P],
     "kch_hca_attn_bwd": [_P] * 16 + [_I] * 6 + [_F, _P, _SZ, _P],
+    "kch_csa_attn_bwd": [_P] * 23 + [_I] * 7 + [_F, _I, _P, _SZ, _P],
     "kch_compress": [_P, _L, _P, _L, _P, _P, _P, _I, _I, _P, _I, _I, _I, _I, _I, _P],
     "kch_compress_overlapped": [_P, _L, _P, _L, _P, _L, _P, _L, _P, _P, _P, _P, _I, _I, _P,
                                 _I, _I, _I, _I, _I, _P],
@@ -73,6 +74,7 @@ _QUERIES = {
     "kch_kda_chunk_ws_bytes": (_SZ, [_I] * 7),
     "kch_kda_recurrent_bwd_ws_bytes": (_SZ, [_I] * 6),
     "kch_hca_attn_bwd_ws_bytes": (_SZ, [_I] * 6),
+    "kch_csa_attn_bwd_ws_bytes": (_SZ, [_I] * 7),
     "kch_decode_ws_bytes": (_SZ, [_I] * 7),
     "kch_decode_dyn_ws_bytes": (_SZ, [_I] * 7),
 }

@@ -352,14 +352,27 @@ def csa_lightning_indexer(q_idx, k_idx, w_idx, topk, scale=None, causal_block_ma
 
 def csa_core(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, *, m, topk,
              sliding_window=0, sink_logits=None, normalize_qk=True, scale=None,
-             return_indices=False):
+             return_indices=False, use_ste=False):
     """CSA after the projections (``ops_csa.py:869-1155``) on the HIP backend.
 
     ``Ca..Zb`` ``[B,T,c]``, ``K_idx, Z_idx`` ``[B,T,c_I]``, ``q`` ``[B,T,nh,c]``,
     ``q_idx`` ``[B,T,nIh,c_I]``, ``w_idx`` ``[B,T,nIh]`` (rows may be strided
     views of one fused projection), T a multiple of m. Returns ``[B,T,nh,c]``
     in ``q.dtype`` (and the int32 selection ``[B,T,topk]`` when asked).
+
+    Differentiable (with gradients enabled) in Ca, Cb, Za, Zb, q, Ba, Bb and the
+    sink logits through ``kch_csa_attn_bwd``, the selection held fixed; with
+    ``use_ste`` also in the indexer inputs through the straight-through
+    surrogate of ``ops_csa.py:1033-1099`` (``topk_columns``).
     """
+    if torch.is_grad_enabled() and any(
+            t is not None and t.requires_grad
+            for t in (Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, sink_logits)):
+        out, idx = _CsaCoreFunction.apply(
+            Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, sink_logits,
+            dict(m=m, topk=topk, sliding_window=sliding_window, normalize_qk=normalize_qk,
+                 scale=scale, use_ste=use_ste))
+        return (out, idx) if return_indices else out
     return _csa_core(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, m=m, topk=topk,
                      sliding_window=sliding_window, sink_logits=sink_logits,
                      normalize_qk=normalize_qk, scale=scale, return_indices=return_indices)
@@ -427,6 +440,163 @@ def _csa_core(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, *, m
     return out
 
 
+def csa_attn_grad(Ca, Cb, Za, Zb, q, Ba, Bb, idx, d_out, *, m, sliding_window=0,
+                  sink_logits=None, normalize_qk=True, scale=None):
+    """Gradients of the CSA attention (``ops_csa.py:869-1155``) with the selection
+    ``idx`` ``[B,T,topk]`` (int32, -1 = unused) held fixed, on
+    ``kch_csa_attn_bwd`` (fp32). Returns a dict with ``Ca, Cb, Za, Zb, q, Ba,
+    Bb`` (input dtypes), ``sink_logits`` where given, and ``slot`` ``[B,T,topk]``
+    (fp32): each selected row's gradient dotted with the row. Channels are
+    zero-padded to the kernel's size; more than 16 heads run as groups."""
+    fn = "csa_attn_grad"
+    B_, T, c = Ca.shape
+    nh = q.shape[2]
+    if T % m:
+        raise ValueError(f"{fn}: T={T} must be a multiple of m={m}")
+    topk = 0 if idx is None else idx.shape[-1]
+    if scale is None:
+        scale = 1.0 if normalize_qk else c ** -0.5
+    cp = _kernel_size(fn, "c", c, _HEAD_DIMS)
+    dev = Ca.device
+    f32 = torch.float32
+
+    def prep(x):
+        x = x.to(device=dev, dtype=f32)
+        return (_pad_last(x, cp) if cp != c else x).contiguous()
+
+    Caf, Cbf, Zaf, Zbf, qf, dof, Baf, Bbf = (prep(x) for x in (Ca, Cb, Za, Zb, q, d_out, Ba, Bb))
+    nb = T // m
+    kc = torch.empty(B_, nb, cp, device=dev, dtype=f32)
+    raw = _compress_overlapped(fn, Caf, Cbf, Zaf, Zbf, Baf, Bbf, m, out_raw=True, key=kc,
+                               normalize=bool(normalize_qk))
+    if not normalize_qk:
+        kc = raw
+    win = int(sliding_window)
+    kl = lsrc = None
+    if win > 0:
+        lsrc = Caf
+        kl = l2_normalize_rows(Caf, out_dtype=f32) if normalize_qk else Caf
+    idx32 = None if topk == 0 else idx.to(device=dev, dtype=torch.int32).contiguous()
+    sink = None if sink_logits is None else sink_logits.detach().to(device=dev, dtype=f32).contiguous()
+    dq = torch.empty_like(qf)
+    dCa = torch.zeros(B_, T, cp, device=dev, dtype=f32)
+    dCb, dZa, dZb = torch.zeros_like(dCa), torch.zeros_like(dCa), torch.zeros_like(dCa)
+    dBa = torch.zeros(m, cp, device=dev, dtype=f32)
+    dBb = torch.zeros_like(dBa)
+    slot = torch.zeros(B_, T, topk, device=dev, dtype=f32)
+    dsink = None if sink is None else torch.zeros(nh, device=dev, dtype=f32)
+    hmax = 256 // (cp // 8)
+    for h0 in range(0, nh, hmax):
+        h1 = min(nh, h0 + hmax)
+        g = h1 - h0
+        qg = qf if g == nh else qf[:, :, h0:h1].contiguous()
+        dog = dof if g == nh else dof[:, :, h0:h1].contiguous()
+        dqg = dq if g == nh else torch.empty_like(qg)
+        oa, ob = torch.empty_like(dCa), torch.zeros_like(dCa)
+        za, zb = torch.empty_like(dCa), torch.zeros_like(dCa)
+        bap = torch.empty(B_, nb, m, cp, device=dev, dtype=f32)
+        bbp = torch.empty_like(bap)
+        sp = None if sink is None else torch.empty(B_, T, g, device=dev, dtype=f32)
+        nbytes = _lib.load().kch_csa_attn_bwd_ws_bytes(B_, T, g, cp, m, win, topk)
+        ws = torch.empty(max(nbytes, 1), device=dev, dtype=torch.uint8)
+        _lib.call("kch_csa_attn_bwd", _lib.ptr(qg), _lib.ptr(dog), _lib.ptr(kc), _lib.ptr(raw),
+                  _lib.ptr(kl), _lib.ptr(lsrc), _lib.ptr(idx32), _lib.ptr(Caf), _lib.ptr(Cbf),
+                  _lib.ptr(Zaf), _lib.ptr(Zbf), _lib.ptr(Baf), _lib.ptr(Bbf),
+                  _lib.ptr(None if sink is None else sink[h0:h1].contiguous()), _lib.ptr(dqg),
+                  _lib.ptr(oa), _lib.ptr(ob), _lib.ptr(za), _lib.ptr(zb), _lib.ptr(bap),
+                  _lib.ptr(bbp), _lib.ptr(sp), _lib.ptr(slot if topk else None), B_, T, g, cp, m,
+                  topk, win, float(scale), int(bool(normalize_qk)), _lib.ptr(ws), nbytes,
+                  _lib.stream_of(qg))
+        if dqg is not dq:
+            dq[:, :, h0:h1] = dqg
+        dCa += oa
+        dCb += ob
+        dZa += za
+        dZb += zb
+        dBa += bap.sum(dim=(0, 1))
+        dBb += bbp.sum(dim=(0, 1))
+        if sp is not None:
+            dsink[h0:h1] = -sp.sum(dim=(0, 1))
+    out = {"Ca": dCa[..., :c].to(Ca.dtype), "Cb": dCb[..., :c].to(Cb.dtype),
+           "Za": dZa[..., :c].to(Za.dtype), "Zb": dZb[..., :c].to(Zb.dtype),
+           "q": dq[..., :c].to(q.dtype), "Ba": dBa[:, :c].to(Ba.dtype),
+           "Bb": dBb[:, :c].to(Bb.dtype), "slot": slot}
+    if sink_logits is not None:
+        out["sink_logits"] = dsink.to(sink_logits.dtype)
+    return out
+
+
+def _ste_indexer_grads(K_idx, Z_idx, q_idx, w_idx, B_idx, idx, slot, *, m, normalize_qk):
+    """The straight-through surrogate's gradients for the indexer inputs
+    (``ops_csa.py:1033-1099``, ``topk_columns``): the selected columns of the
+    soft weights (``softmax`` over every causal block of the indexer logits,
+    ``ops_csa.py:545-572``) receive ``slot``; autograd carries that through
+    the logits (``ops_csa.py:503-536``) and the key compression
+    (``ops_csa.py:198-234``). Dense over the blocks, written with torch
+    operations."""
+    leaves = [x.detach().requires_grad_(True) if x is not None else None
+              for x in (K_idx, Z_idx, q_idx, w_idx, B_idx)]
+    Kl, Zl, ql, wl, Bl = leaves
+    B_, T, cI = Kl.shape
+    nb = T // m
+    with torch.enable_grad():
+        f32 = torch.float32
+        lg = Zl.to(f32).reshape(B_, nb, m, cI) + Bl.to(f32)
+        kcmp = (torch.softmax(lg, dim=2) * Kl.to(f32).reshape(B_, nb, m, cI)).sum(2)
+        qi = ql.to(f32)
+        if normalize_qk:
+            qi = F.normalize(qi, dim=-1)
+            kcmp = F.normalize(kcmp, dim=-1)
+        sc = 1.0 if normalize_qk else cI ** -0.5
+        score = torch.relu(torch.einsum('bthd,bnd->bhtn', qi, kcmp) * sc)
+        logits = torch.einsum('bhtn,bth->btn', score, wl.to(f32))
+        t = torch.arange(T, device=Kl.device)
+        n = torch.arange(nb, device=Kl.device)
+        logits = logits.masked_fill(~((t[:, None] + 1) // m > n[None, :]), float('-inf'))
+        soft = _nan_safe_softmax(logits, dim=-1)
+        idx64 = idx.long()
+        sel = torch.gather(soft, -1, idx64.clamp(min=0)) * (idx64 >= 0).to(f32)
+        grads = torch.autograd.grad(sel, [x for x in leaves], grad_outputs=slot,
+                                    allow_unused=True)
+    return [None if g is None else g.to(x.dtype) for g, x in zip(grads, (K_idx, Z_idx, q_idx, w_idx,
+                                                                        B_idx))]
+
+
+class _CsaCoreFunction(torch.autograd.Function):
+    """``csa_core`` with gradients: the forward kernels (selection included),
+    ``kch_csa_attn_bwd`` for the attention's backward, and the STE surrogate
+    for the indexer inputs when asked."""
+
+    @staticmethod
+    def forward(ctx, Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, sink_logits, cfg):
+        out, idx = _csa_core(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx,
+                             m=cfg["m"], topk=cfg["topk"], sliding_window=cfg["sliding_window"],
+                             sink_logits=sink_logits, normalize_qk=cfg["normalize_qk"],
+                             scale=cfg["scale"], return_indices=True)
+        if idx is None:
+            idx = torch.zeros(Ca.shape[0], Ca.shape[1], 0, device=Ca.device, dtype=torch.int32)
+        ctx.save_for_backward(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx,
+                              sink_logits, idx)
+        ctx.cfg = cfg
+        ctx.mark_non_differentiable(idx)
+        return out, idx
+
+    @staticmethod
+    def backward(ctx, d_out, _d_idx):
+        Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, sink, idx = ctx.saved_tensors
+        cfg = ctx.cfg
+        g = csa_attn_grad(Ca, Cb, Za, Zb, q, Ba, Bb, idx if idx.shape[-1] else None, d_out,
+                          m=cfg["m"], sliding_window=cfg["sliding_window"], sink_logits=sink,
+                          normalize_qk=cfg["normalize_qk"], scale=cfg["scale"])
+        ig = [None] * 5
+        if cfg["use_ste"] and idx.shape[-1] and any(
+                x.requires_grad for x in (K_idx, Z_idx, q_idx, w_idx, B_idx)):
+            ig = _ste_indexer_grads(K_idx, Z_idx, q_idx, w_idx, B_idx, idx, g["slot"],
+                                    m=cfg["m"], normalize_qk=cfg["normalize_qk"])
+        return (g["Ca"], g["Cb"], g["Za"], g["Zb"], ig[0], ig[1], g["q"], ig[2], ig[3], g["Ba"],
+                g["Bb"], ig[4], g.get("sink_logits"), None)
+
+
 def naive_csa(H, W_aKV, W_bKV, W_aZ, W_bZ, Ba, Bb, W_DQ, W_UQ, W_IUQ, W_w, W_KV_idx, W_Z_idx,
               B_idx, *, m, topk, nh, nIh, c, c_I, dc, scale=None, sliding_window=0,
               sink_logits=None, use_ste=True, ste_mode='topk_columns', normalize_qk=False,
@@ -489,6 +659,28 @@ def naive_csa(H, W_aKV, W_bKV, W_aZ, W_bZ, Ba, Bb, W_DQ, W_UQ, W_IUQ, W_w, W_KV_
         H = F.pad(H, (0, 0, 0, pad))
         T = T + pad
     n_blocks = T // m
+    if torch.is_grad_enabled() and any(
+            t.requires_grad for t in (H, W_aKV, W_bKV, W_aZ, W_bZ, Ba, Bb, W_DQ, W_UQ, W_IUQ, W_w,
+                                      W_KV_idx, W_Z_idx, B_idx)
+            if t is not None) or (sink_logits is not None and sink_logits.requires_grad
+                                  and torch.is_grad_enabled()):
+        # training: the projections through autograd (library GEMMs), the core
+        # through its HIP backward and, with use_ste, the STE surrogate
+        if use_ste and ste_mode != 'topk_columns':
+            raise NotImplementedError(
+                f"{fn}: gradients for ste_mode={ste_mode!r} are not provided (topk_columns is)")
+        Ca, Cb, Za, Zb, K_idx_raw, Z_idx, cQ, w_idx = F.linear(
+            H, torch.cat([W_aKV, W_bKV, W_aZ, W_bZ, W_KV_idx, W_Z_idx, W_DQ, W_w])).split(
+            [c, c, c, c, c_I, c_I, dc, nIh], dim=-1)
+        q_idx = F.linear(cQ, W_IUQ).view(B_, T, nIh, c_I)
+        q = F.linear(cQ, W_UQ).view(B_, T, nh, c)
+        out = csa_core(Ca, Cb, Za, Zb, K_idx_raw, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, m=m,
+                       topk=topk, sliding_window=sliding_window, sink_logits=sink_logits,
+                       normalize_qk=normalize_qk, scale=scale, use_ste=use_ste)
+        out_final = out.reshape(B_, T, nh * c)[:, :original_T]
+        if return_projections:
+            return out_final, tuple(x[:, :original_T] for x in (Ca, Cb, Za, Zb, K_idx_raw, Z_idx))
+        return out_final
     with torch.no_grad():
         if fuse_projections:
             # every projection of H in one GEMM: H is read from HBM once (rows
@@ -515,5 +707,5 @@ def naive_csa(H, W_aKV, W_bKV, W_aZ, W_bZ, Ba, Bb, W_DQ, W_UQ, W_IUQ, W_w, W_KV_
     return out_final
 
 
-__all__ = ["csa_compress_kv", "csa_compress_kv_overlapped", "csa_core", "csa_lightning_indexer",
-           "naive_csa", "l2_normalize_rows", "record_selections"]
+__all__ = ["csa_attn_grad", "csa_compress_kv", "csa_compress_kv_overlapped", "csa_core",
+           "csa_lightning_indexer", "naive_csa", "l2_normalize_rows", "record_selections"]

@@ -575,3 +575,115 @@ def hca_core_grad(C, Z, q, B_pos, d_out, *, m2, sliding_window=0, sink_logits=No
         grads['sink_logits'] = -(p_sink * D).sum(axis=(0, 2, 3))
     grads.update(C=dC[:, :T], Z=dZ[:, :T], q=dq[:, :T], B_pos=dB)
     return grads
+
+
+def compress_kv_overlapped_grad(Ca, Cb, Za, Zb, Ba, Bb, m, d_out):
+    """Backward of ``compress_kv_overlapped`` (``ops_csa.py:237-305``): block
+    i's softmax runs over the 2m logits ``Za_i + Ba`` and ``Zb_{i-1} + Bb``
+    (block 0: the second half is -inf, ``Cb_{-1} = 0``); with ``r`` the block's
+    row and ``dr`` its cotangent, each weight ``w`` of value ``x`` gets
+    ``dx = w dr`` and ``dlogit = w (x - r) dr``. Returns ``(dCa, dCb, dZa,
+    dZb, dBa, dBb)``."""
+    f = np.float64
+    Ca, Cb, Za, Zb = (np.asarray(x, f) for x in (Ca, Cb, Za, Zb))
+    Bn, T, c = Ca.shape
+    nb = T // m
+    Ca4, Cb4, Za4, Zb4 = (x.reshape(Bn, nb, m, c) for x in (Ca, Cb, Za, Zb))
+    a_log = Za4 + np.asarray(Ba, f)[None, None]
+    zb_prev = np.concatenate([np.full((Bn, 1, m, c), -np.inf), Zb4[:, :-1]], axis=1)
+    b_log = zb_prev + np.asarray(Bb, f)[None, None]
+    allg = np.concatenate([a_log, b_log], axis=2)
+    e = np.exp(allg - allg.max(axis=2, keepdims=True))
+    S = e / e.sum(axis=2, keepdims=True)
+    cb_prev = np.concatenate([np.zeros((Bn, 1, m, c)), Cb4[:, :-1]], axis=1)
+    vals = np.concatenate([Ca4, cb_prev], axis=2)
+    r = (S * vals).sum(axis=2, keepdims=True)
+    dr = np.asarray(d_out, f)[:, :, None]
+    dv = S * dr
+    dl = S * (vals - r) * dr
+    dCa = dv[:, :, :m].reshape(Bn, T, c)
+    dZa = dl[:, :, :m].reshape(Bn, T, c)
+    dCb = np.zeros((Bn, nb, m, c))
+    dZb = np.zeros((Bn, nb, m, c))
+    dCb[:, :-1] = dv[:, 1:, m:]
+    dZb[:, :-1] = dl[:, 1:, m:]
+    return (dCa, dCb.reshape(Bn, T, c), dZa, dZb.reshape(Bn, T, c), dl[:, :, :m].sum((0, 1)),
+            dl[:, 1:, m:].sum((0, 1)))
+
+
+def csa_attn_grad(Ca, Cb, Za, Zb, q, Ba, Bb, idx, d_out, *, m, sliding_window=0,
+                  sink_logits=None, normalize_qk=True, scale=None):
+    """Gradients of ``csa_core``'s attention (``ops_csa.py:869-1155``) with the
+    selection ``idx`` ``[B,T,topk]`` (-1 = unused) held fixed, in fp64; T a
+    multiple of m. Same algebra as ``hca_core_grad`` over the selected rows,
+    the window rows of ``Ca`` and the sink, then the overlapped compression
+    backward. Also returns ``slot``: per selected slot, the gradient of the
+    gathered row dotted with that row (``sum_h p ((dp - D) s + dp)``), the
+    quantity the STE surrogate (``ops_csa.py:1033-1099``) turns into the
+    indexer's gradient."""
+    f = np.float64
+    Ca, Cb, Za, Zb, q, d_out = (np.asarray(x, f) for x in (Ca, Cb, Za, Zb, q, d_out))
+    Bn, T, c = Ca.shape
+    nh = q.shape[2]
+    nb = T // m
+    idx = np.asarray(idx, np.int64)
+    if scale is None:
+        scale = 1.0 if normalize_qk else c ** -0.5
+    raw = compress_kv_overlapped(Ca, Cb, Za, Zb, Ba, Bb, m, f)
+    Cn = l2_normalize(raw) if normalize_qk else raw
+    qn = l2_normalize(q) if normalize_qk else q
+    topk = idx.shape[-1]
+    valid = idx >= 0
+    kv = Cn[np.arange(Bn)[:, None, None], np.maximum(idx, 0)]            # [B,T,k,c]
+    s_k = np.einsum('bthd,btkd->bthk', qn, kv) * scale
+    s_k = np.where(valid[:, :, None, :], s_k, -np.inf)
+    w = sliding_window
+    if w > 0:
+        Cl = l2_normalize(Ca) if normalize_qk else Ca
+        s_w, Cw, wvalid = window_scores(qn, Cl, w, scale)
+    else:
+        s_w = np.zeros((Bn, T, nh, 0))
+        Cw = np.zeros((Bn, T, 0, c))
+        wvalid = np.zeros((T, 0), bool)
+    cat = np.concatenate([s_k, s_w], axis=-1)
+    cat_valid = np.concatenate(
+        [np.broadcast_to(valid[:, :, None, :], (Bn, T, nh, topk)),
+         np.broadcast_to(wvalid[None, :, None, :], (Bn, T, nh, wvalid.shape[-1]))], axis=-1)
+    sink = None if sink_logits is None else np.asarray(sink_logits, f).reshape(1, 1, nh, 1)
+    if cat.shape[-1]:
+        p = joint_softmax_csa(cat, cat_valid, sink)
+    else:
+        p = np.zeros((Bn, T, nh, 0))
+    pk, pw = p[..., :topk], p[..., topk:]
+    out = np.einsum('bthk,btkd->bthd', pk, kv) + np.einsum('bthw,btwd->bthd', pw, Cw)
+    dp_k = np.einsum('bthd,btkd->bthk', d_out, kv)
+    dp_w = np.einsum('bthd,btwd->bthw', d_out, Cw)
+    D = np.einsum('bthd,bthd->bth', d_out, out)[..., None]
+    ds_k = pk * (dp_k - D)
+    ds_w = pw * (dp_w - D)
+    dqn = scale * (np.einsum('bthk,btkd->bthd', ds_k, kv) + np.einsum('bthw,btwd->bthd', ds_w, Cw))
+    dkv = scale * np.einsum('bthk,bthd->btkd', ds_k, qn) + np.einsum('bthk,bthd->btkd', pk, d_out)
+    slot = np.where(valid, (dkv * kv).sum(-1), 0.0)
+    dCn = np.zeros((Bn, nb, c))
+    bi = np.broadcast_to(np.arange(Bn)[:, None, None], idx.shape)
+    np.add.at(dCn, (bi[valid], idx[valid]), dkv[valid])
+    dq = _l2n_grad(q, dqn) if normalize_qk else dqn
+    draw = _l2n_grad(raw, dCn) if normalize_qk else dCn
+    dCa, dCb, dZa, dZb, dBa, dBb = compress_kv_overlapped_grad(Ca, Cb, Za, Zb, Ba, Bb, m, draw)
+    if w > 0:
+        dCw = scale * np.einsum('bthw,bthd->btwd', ds_w, qn) + np.einsum('bthw,bthd->btwd', pw, d_out)
+        dCl = np.zeros((Bn, T, c))
+        for i in range(w):
+            src = np.arange(T) - w + 1 + i
+            ok = src >= 0
+            np.add.at(dCl, (slice(None), src[ok]), dCw[:, ok, i])
+        dCa = dCa + (_l2n_grad(Ca, dCl) if normalize_qk else dCl)
+    g = dict(Ca=dCa, Cb=dCb, Za=dZa, Zb=dZb, q=dq, Ba=dBa, Bb=dBb, slot=slot)
+    if sink is not None:
+        row_max = np.maximum(np.where(cat_valid, cat, -np.inf).max(-1, keepdims=True), 0) \
+            if cat.shape[-1] else np.zeros((Bn, T, nh, 1))
+        with np.errstate(divide='ignore', invalid='ignore'):
+            lse = np.log(np.where(cat_valid, np.exp(cat - row_max), 0).sum(-1, keepdims=True)) + row_max
+        p_sink = np.exp(sink - np.logaddexp(lse, sink))
+        g['sink_logits'] = -(p_sink * D).sum(axis=(0, 1, 3))
+    return g

@@ -1,0 +1,210 @@
+"""Gradients of the HIP CSA operators (needs a ROCm GPU).
+
+The reference differentiates ``naive_csa`` with autograd, its top-k selection
+held fixed, and adds a straight-through surrogate for the indexer
+(``ops_csa.py:1033-1099``; tests ``run_correctness.py:1312-1473``,
+``2710-2830``). Checked here:
+
+* ``kch_csa_attn_bwd`` (attention, overlapped compression, window, sink,
+  with and without ``normalize_qk``) against ``oracle.csa.csa_attn_grad``
+  (pinned by central finite differences on the CPU), including the per-slot
+  quantity the surrogate consumes: fp32 within 1e-4 of each tensor's largest
+  gradient;
+* the whole ``csa_core`` with ``use_ste=True`` against a float64 torch
+  statement of the reference's forward with the surrogate identity
+  ``kv + (soft_kv - soft_kv.detach())``, differentiated by autograd on the
+  CPU on the selection the kernel made: every gradient, indexer inputs
+  included, within 1e-4 of its largest entry;
+* the reference's contract: ``use_ste`` does not change the forward value, and
+  every indexer weight of ``naive_csa`` gets a finite, non-zero gradient.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle.csa import csa_attn_grad as o_grad
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(name, got, ref, tol_max=1e-4):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert got.shape == ref.shape, (name, got.shape, ref.shape)
+    assert np.isfinite(got).all(), f"{name}: non-finite"
+    scale = np.abs(ref).max() + 1e-30
+    err = np.abs(got - ref).max()
+    assert err <= tol_max * scale, f"{name}: max err {err:.3e} of max {scale:.3e}"
+
+
+def _selection(rng, B, T, m, topk, hole=None):
+    idx = np.full((B, T, topk), -1, np.int32)
+    for b in range(B):
+        for t in range(T):
+            vis = (t + 1) // m
+            if vis and t != hole:
+                pick = rng.choice(vis, size=min(vis, topk), replace=False)
+                idx[b, t, :len(pick)] = pick
+    return idx
+
+
+CASES = [
+    # B, T, nh, c, m, topk, win, sink, norm
+    (2, 64, 4, 64, 4, 8, 8, True, True),
+    (1, 128, 16, 128, 8, 4, 0, False, False),
+    (1, 48, 2, 16, 4, 3, 5, True, False),      # c padded to 64
+    (1, 64, 18, 128, 4, 6, 4, True, True),     # two head groups
+    (2, 1040, 3, 64, 8, 16, 24, True, False),  # several query chunks per key tile
+]
+
+
+@pytest.mark.parametrize("B,T,nh,c,m,topk,win,sink,norm", CASES)
+def test_attn_grad_matches_oracle(dev, B, T, nh, c, m, topk, win, sink, norm):
+    import kch
+    rng = np.random.default_rng(T + nh + c + topk)
+    X = {k: rng.standard_normal((B, T, c)) for k in ("Ca", "Cb", "Za", "Zb")}
+    q = rng.standard_normal((B, T, nh, c))
+    Ba, Bb = rng.standard_normal((m, c)) * 0.3, rng.standard_normal((m, c)) * 0.3
+    sk = rng.standard_normal(nh) if sink else None
+    W = rng.standard_normal((B, T, nh, c))
+    idx = _selection(rng, B, T, m, topk, hole=T // 2)
+    ref = o_grad(X["Ca"], X["Cb"], X["Za"], X["Zb"], q, Ba, Bb, idx, W, m=m, sliding_window=win,
+                 sink_logits=sk, normalize_qk=norm)
+    t = lambda x: torch.tensor(x, dtype=torch.float32, device=dev)  # noqa: E731
+    g = kch.ops_csa.csa_attn_grad(t(X["Ca"]), t(X["Cb"]), t(X["Za"]), t(X["Zb"]), t(q), t(Ba),
+                                  t(Bb), torch.tensor(idx, device=dev), t(W), m=m,
+                                  sliding_window=win, sink_logits=None if sk is None else t(sk),
+                                  normalize_qk=norm)
+    torch.cuda.synchronize()
+    for name in ("Ca", "Cb", "Za", "Zb", "q", "Ba", "Bb", "slot") + (("sink_logits",) if sink else ()):
+        _check(name, g[name].cpu().numpy(), ref[name])
+
+
+def _torch_reference(X, idx, *, m, topk, win, sink, norm):
+    """The reference's CSA forward (compression ``ops_csa.py:237-305``,
+    indexer ``:330-573``, the STE gather ``:1033-1099``, attention with window
+    and sink ``:1100-1155``) in float64 torch on the CPU, the selection given."""
+    Ca, Cb, Za, Zb, Kx, Zx, q, qi, wi, Ba, Bb, Bi = (X[k] for k in (
+        "Ca", "Cb", "Za", "Zb", "K_idx", "Z_idx", "q", "q_idx", "w_idx", "Ba", "Bb", "B_idx"))
+    B_, T, c = Ca.shape
+    nb = T // m
+    nh = q.shape[2]
+
+    def blocks(x):
+        return x.reshape(B_, nb, m, x.shape[-1])
+
+    zb_prev = torch.cat([torch.full_like(blocks(Zb)[:, :1], float('-inf')), blocks(Zb)[:, :-1]], 1)
+    cb_prev = torch.cat([torch.zeros_like(blocks(Cb)[:, :1]), blocks(Cb)[:, :-1]], 1)
+    wts = torch.softmax(torch.cat([blocks(Za) + Ba, zb_prev + Bb], dim=2), dim=2)
+    Ccomp = (wts * torch.cat([blocks(Ca), cb_prev], dim=2)).sum(2)
+    Kcomp = (torch.softmax(blocks(Zx) + Bi, dim=2) * blocks(Kx)).sum(2)
+    cI = Kx.shape[-1]
+    qn, Cn = (F.normalize(q, dim=-1), F.normalize(Ccomp, dim=-1)) if norm else (q, Ccomp)
+    qin, Kn = (F.normalize(qi, dim=-1), F.normalize(Kcomp, dim=-1)) if norm else (qi, Kcomp)
+    scale = 1.0 if norm else c ** -0.5
+    iscale = 1.0 if norm else cI ** -0.5
+    logits = torch.einsum('bhtn,bth->btn', torch.relu(torch.einsum('bthd,bnd->bhtn', qin, Kn) * iscale), wi)
+    tt, nn = torch.arange(T), torch.arange(nb)
+    logits = logits.masked_fill(~((tt[:, None] + 1) // m > nn[None, :]), float('-inf'))
+    allm = logits.isinf().all(-1, keepdim=True)
+    soft = torch.softmax(logits.masked_fill(allm, 0.0), -1).masked_fill(allm, 0.0)
+    idx = torch.as_tensor(idx, dtype=torch.long)
+    valid = idx >= 0
+    isafe = idx.clamp(min=0)
+    kv = Cn[torch.arange(B_)[:, None, None], isafe]                             # [B,T,k,c]
+    ssel = torch.gather(soft, -1, isafe) * valid.to(soft.dtype)
+    soft_kv = ssel.unsqueeze(-1) * kv.detach()
+    kv = kv + (soft_kv - soft_kv.detach())
+    s = torch.einsum('bthd,btkd->bthk', qn, kv) * scale
+    s = s.masked_fill(~valid[:, :, None, :], float('-inf'))
+    vals = [kv]
+    scores = [s]
+    if win:
+        Cl = F.normalize(Ca, dim=-1) if norm else Ca
+        pad = torch.cat([torch.zeros(B_, win - 1, c, dtype=Ca.dtype), Cl], 1)
+        wi_ = torch.arange(T)[:, None] + torch.arange(win)[None, :]
+        Cw = pad[:, wi_]                                                          # [B,T,w,c]
+        wv = torch.arange(win)[None, :] >= (win - 1 - torch.arange(T)[:, None])
+        sw = (torch.einsum('bthd,btwd->bthw', qn, Cw) * scale).masked_fill(~wv[None, :, None, :],
+                                                                            float('-inf'))
+        vals.append(Cw)
+        scores.append(sw)
+    cat = torch.cat(scores, -1)
+    catv = ~torch.isinf(cat)
+    rm = torch.clamp(cat.masked_fill(~catv, float('-inf')).amax(-1, keepdim=True), min=0.0)
+    e = torch.exp(cat - rm).masked_fill(~catv, 0.0)
+    den = e.sum(-1, keepdim=True)
+    if sink is not None:
+        den = den + torch.exp(sink.view(1, 1, nh, 1) - rm)
+    p = torch.where(den > 0, e / den.clamp_min(1e-300), torch.zeros_like(e))
+    out = torch.einsum('bthk,btkd->bthd', p[..., :topk], vals[0])
+    if win:
+        out = out + torch.einsum('bthw,btwd->bthd', p[..., topk:], vals[1])
+    return out
+
+
+@pytest.mark.parametrize("norm", [False, True])
+def test_csa_core_ste_grads_match_torch_reference(dev, norm):
+    import kch
+    rng = np.random.default_rng(21 + norm)
+    B, T, nh, c, m, topk, win, cI, nIh = 1, 64, 2, 64, 4, 4, 6, 32, 2
+    shapes = dict(Ca=(B, T, c), Cb=(B, T, c), Za=(B, T, c), Zb=(B, T, c), K_idx=(B, T, cI),
+                  Z_idx=(B, T, cI), q=(B, T, nh, c), q_idx=(B, T, nIh, cI), w_idx=(B, T, nIh),
+                  Ba=(m, c), Bb=(m, c), B_idx=(m, cI))
+    X = {k: rng.standard_normal(s) * (0.3 if k.startswith("B") else 1.0) for k, s in shapes.items()}
+    sk = rng.standard_normal(nh)
+    W = rng.standard_normal((B, T, nh, c))
+    xt = {k: torch.tensor(v, dtype=torch.float32, device=dev, requires_grad=True) for k, v in X.items()}
+    st = torch.tensor(sk, dtype=torch.float32, device=dev, requires_grad=True)
+    args = [xt[k] for k in ("Ca", "Cb", "Za", "Zb", "K_idx", "Z_idx", "q", "q_idx", "w_idx", "Ba",
+                            "Bb", "B_idx")]
+    out, idx = kch.csa_core(*args, m=m, topk=topk, sliding_window=win, sink_logits=st,
+                            normalize_qk=norm, return_indices=True, use_ste=True)
+    (out.double() * torch.tensor(W, device=dev)).sum().backward()
+    torch.cuda.synchronize()
+    # the same loss through the float64 torch statement, on the kernel's selection
+    xr = {k: torch.tensor(v, dtype=torch.float64, requires_grad=True) for k, v in X.items()}
+    sr = torch.tensor(sk, dtype=torch.float64, requires_grad=True)
+    ref_out = _torch_reference(xr, idx.cpu().numpy(), m=m, topk=topk, win=win, sink=sr, norm=norm)
+    # the forward holds its compressed rows in bf16 (2^-9 relative); without
+    # normalisation the scores reach |q||k| / sqrt(c) ~ 8, so the outputs move
+    # by a few 1e-3 of their largest value
+    _check("out", out.detach().cpu().numpy(), ref_out.detach().numpy(), 1e-2)
+    (ref_out * torch.tensor(W)).sum().backward()
+    for k in X:
+        _check(k, xt[k].grad.cpu().numpy(), xr[k].grad.numpy())
+    _check("sink", st.grad.cpu().numpy(), sr.grad.numpy())
+
+
+def test_naive_csa_ste_contract(dev):
+    """``run_correctness.py:1312-1473``: ``use_ste`` leaves the forward value
+    unchanged, and every indexer weight gets a finite, non-zero gradient."""
+    import kch
+    torch.manual_seed(42)
+    B, T, d = 1, 32, 16
+    m, topk, nh, nIh, c, cI, dc = 4, 2, 2, 2, 8, 4, 8
+    H = torch.randn(B, T, d, device=dev)
+    P = dict(W_aKV=(c, d), W_bKV=(c, d), W_aZ=(c, d), W_bZ=(c, d), Ba=(m, c), Bb=(m, c),
+             W_DQ=(dc, d), W_UQ=(c * nh, dc), W_IUQ=(cI * nIh, dc), W_w=(nIh, d),
+             W_KV_idx=(cI, d), W_Z_idx=(cI, d), B_idx=(m, cI))
+    base = {k: torch.randn(*s) * (0.02 if k.startswith("B") else 0.1) for k, s in P.items()}
+    outs = []
+    for ste in (False, True):
+        ps = {k: v.clone().to(dev).requires_grad_(True) for k, v in base.items()}
+        o = kch.naive_csa(H, *[ps[k] for k in P], m=m, topk=topk, nh=nh, nIh=nIh, c=c, c_I=cI,
+                          dc=dc, use_ste=ste)
+        o.square().sum().backward()
+        outs.append((o.detach(), ps))
+    assert torch.allclose(outs[0][0], outs[1][0], rtol=0, atol=1e-6)
+    for k in ("W_IUQ", "W_w", "W_KV_idx", "W_Z_idx", "B_idx"):
+        g = outs[1][1][k].grad
+        assert g is not None and torch.isfinite(g).all() and g.abs().sum() > 0, k
+        g0 = outs[0][1][k].grad
+        assert g0 is None or g0.abs().sum() == 0, k
+    for k in ("W_aKV", "W_bKV", "W_aZ", "W_bZ", "W_DQ", "W_UQ", "Ba", "Bb"):
+        g = outs[1][1][k].grad
+        assert g is not None and torch.isfinite(g).all() and g.abs().sum() > 0, k

@@ -370,3 +370,87 @@ def test_compress_kv_grad_matches_finite_differences():
 
     dC, dZ, dB = compress_kv_grad(a["C"], a["Z"], a["B_pos"], m, W)
     assert _fd_worst(loss, a, dict(C=dC, Z=dZ, B_pos=dB)) < 1e-6
+
+
+def test_compress_overlapped_grad_matches_finite_differences():
+    from oracle.csa import compress_kv_overlapped_grad
+    rng = np.random.default_rng(5)
+    B, T, c, m = 1, 12, 3, 4
+    a = {k: rng.standard_normal((B, T, c)) for k in ("Ca", "Cb", "Za", "Zb")}
+    a.update(Ba=rng.standard_normal((m, c)), Bb=rng.standard_normal((m, c)))
+    W = rng.standard_normal((B, T // m, c))
+
+    def loss():
+        return float((O.compress_kv_overlapped(a["Ca"], a["Cb"], a["Za"], a["Zb"], a["Ba"], a["Bb"],
+                                               m, np.float64) * W).sum())
+
+    g = compress_kv_overlapped_grad(a["Ca"], a["Cb"], a["Za"], a["Zb"], a["Ba"], a["Bb"], m, W)
+    assert _fd_worst(loss, a, dict(zip(("Ca", "Cb", "Za", "Zb", "Ba", "Bb"), g))) < 1e-6
+
+
+@pytest.mark.parametrize("norm,win,sink", [(True, 3, True), (False, 0, False), (False, 5, True)])
+def test_csa_attn_grad_matches_finite_differences(norm, win, sink):
+    """``csa_attn_grad`` with a fixed selection (including -1 slots and a
+    query whose every slot is unused) against central differences of
+    ``csa_core(indices=...)`` in fp64; ``slot`` against the derivative of the
+    loss along a rescaling of each selected row in the gather (one query's
+    attention restated from the oracle's joint softmax)."""
+    from oracle.csa import csa_attn_grad
+    rng = np.random.default_rng(7 + win)
+    B, T, c, m, nh, topk, cI, nIh = 1, 12, 4, 4, 2, 2, 4, 1
+    a = {k: rng.standard_normal((B, T, c)) for k in ("Ca", "Cb", "Za", "Zb")}
+    a.update(q=rng.standard_normal((B, T, nh, c)), Ba=rng.standard_normal((m, c)) * 0.3,
+             Bb=rng.standard_normal((m, c)) * 0.3)
+    if sink:
+        a["sink_logits"] = rng.standard_normal(nh)
+    nb = T // m
+    idx = np.full((B, T, topk), -1)
+    for t in range(T):
+        vis = (t + 1) // m
+        if vis and t != 9:
+            pick = rng.choice(vis, size=min(vis, topk), replace=False)
+            idx[0, t, :len(pick)] = pick
+    W = rng.standard_normal((B, T, nh, c))
+    dummy = dict(K_idx=np.zeros((B, T, cI)), Z_idx=np.zeros((B, T, cI)),
+                 q_idx=np.zeros((B, T, nIh, cI)), w_idx=np.zeros((B, T, nIh)),
+                 B_idx=np.zeros((m, cI)))
+    kw = dict(m=m, topk=topk, sliding_window=win, normalize_qk=norm, indices=idx)
+
+    def loss():
+        return float((O.csa_core(a["Ca"], a["Cb"], a["Za"], a["Zb"], dummy["K_idx"], dummy["Z_idx"],
+                                 a["q"], dummy["q_idx"], dummy["w_idx"], a["Ba"], a["Bb"],
+                                 dummy["B_idx"], sink_logits=a.get("sink_logits"),
+                                 compute=np.float64, **kw) * W).sum())
+
+    g = csa_attn_grad(a["Ca"], a["Cb"], a["Za"], a["Zb"], a["q"], a["Ba"], a["Bb"], idx, W, m=m,
+                      sliding_window=win, sink_logits=a.get("sink_logits"), normalize_qk=norm)
+    assert _fd_worst(loss, a, g) < 1e-6
+    assert nb == 3 and np.all(g["slot"][idx < 0] == 0)
+    # slot: d L / d alpha where selected row k of query t enters (as key and
+    # value) scaled by 1 + alpha; the attention of that one query, restated
+    # from the oracle's pieces
+    from oracle.common import l2_normalize as l2n
+    raw = O.compress_kv_overlapped(a["Ca"], a["Cb"], a["Za"], a["Zb"], a["Ba"], a["Bb"], m, np.float64)
+    Cn = l2n(raw) if norm else raw
+    qn = l2n(a["q"]) if norm else a["q"]
+    sc = 1.0 if norm else c ** -0.5
+    Cl = l2n(a["Ca"]) if norm else a["Ca"]
+    sk = a.get("sink_logits")
+
+    def q_loss(t, k, alpha):
+        rows = [Cn[0, j] * (1 + alpha if kk == k else 1) for kk, j in enumerate(idx[0, t]) if j >= 0]
+        rows += [Cl[0, u] for u in range(max(0, t - win + 1), t + 1)] if win else []
+        if not rows:
+            return 0.0
+        V = np.stack(rows)
+        s = np.einsum('hd,jd->hj', qn[0, t], V) * sc
+        pr = O.joint_softmax_csa(s[None], np.ones_like(s[None], bool),
+                                 None if sk is None else sk.reshape(1, nh, 1))[0]
+        return float((np.einsum('hj,jd->hd', pr, V) * W[0, t]).sum())
+
+    for t in range(T):
+        for k in range(topk):
+            if idx[0, t, k] >= 0:
+                num = (q_loss(t, k, 1e-6) - q_loss(t, k, -1e-6)) / 2e-6
+                ana = g["slot"][0, t, k]
+                assert abs(num - ana) <= 1e-6 * (abs(num) + abs(ana) + 1e-2), (t, k, num, ana)
