@@ -112,23 +112,31 @@ __global__ __launch_bounds__(256) void hca_bwd_query_kernel(HcaBwdParams p) {
     dp = hsum<LPH>(c);
   };
 
-  // pass A: lse and D = sum p dp (the sink's value is zero)
+  // pass A: lse and D = sum p dp (the sink's value is zero). Key rows are
+  // requested PD steps ahead (a ring of PD registers sets).
+  constexpr int PD = 4;
   float m = -INFINITY, l = 0.f, ad = 0.f;
-  float kc[8], kn[8];
-  if (nk > 0) load8(krow(0), kc);
-  for (int j = 0; j < nk; ++j) {
-    if (j + 1 < nk) load8(krow(j + 1), kn);
-    float s, dp;
-    score(kc, s, dp);
-    if (kvalid(j)) {
-      const float mn = fmaxf(m, s);
-      const float a = expf(m - mn), e1 = expf(s - mn);
-      l = l * a + e1;
-      ad = ad * a + e1 * dp;
-      m = mn;
-    }
+  float kb[PD][8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) kc[e] = kn[e];
+  for (int u = 0; u < PD; ++u)
+    if (u < nk) load8(krow(u), kb[u]);
+  for (int j0 = 0; j0 < nk; j0 += PD) {
+#pragma unroll
+    for (int u = 0; u < PD; ++u) {
+      const int j = j0 + u;
+      if (j < nk) {
+        float s, dp;
+        score(kb[u], s, dp);
+        if (j + PD < nk) load8(krow(j + PD), kb[u]);
+        if (kvalid(j)) {
+          const float mn = fmaxf(m, s);
+          const float a = expf(m - mn), e1 = expf(s - mn);
+          l = l * a + e1;
+          ad = ad * a + e1 * dp;
+          m = mn;
+        }
+      }
+    }
   }
   float sk = 0.f;
   if (p.sink) {
@@ -146,22 +154,28 @@ __global__ __launch_bounds__(256) void hca_bwd_query_kernel(HcaBwdParams p) {
   float dq[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) dq[e] = 0.f;
-  if (nk > 0) load8(krow(0), kc);
-  for (int j = 0; j < nk; ++j) {
-    if (j + 1 < nk) load8(krow(j + 1), kn);
-    float s, dp;
-    score(kc, s, dp);
-    const float pj = kvalid(j) ? expf(s - lse) : 0.f;
-    const float ds = pj * (dp - D) * p.scale;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) dq[e] += ds * kc[e];
-    // the selected row's gradient dotted with the row, this head's share:
-    // (scale p (dp - D) qn + p dout) . k = p ((dp - D) s + dp); the heads add
-    // into slot_grad (zeroed by the caller)
-    if (p.slot_grad && act && lc == 0 && j < nvis && kvalid(j))
-      atomicAdd(p.slot_grad + bt * p.topk + j, pj * ((dp - D) * s + dp));
+  for (int u = 0; u < PD; ++u)
+    if (u < nk) load8(krow(u), kb[u]);
+  for (int j0 = 0; j0 < nk; j0 += PD) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) kc[e] = kn[e];
+    for (int u = 0; u < PD; ++u) {
+      const int j = j0 + u;
+      if (j < nk) {
+        float s, dp;
+        score(kb[u], s, dp);
+        const float pj = kvalid(j) ? expf(s - lse) : 0.f;
+        const float ds = pj * (dp - D) * p.scale;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dq[e] += ds * kb[u][e];
+        if (j + PD < nk) load8(krow(j + PD), kb[u]);
+        // the selected row's gradient dotted with the row, this head's share:
+        // (scale p (dp - D) qn + p dout) . k = p ((dp - D) s + dp); the heads
+        // add into slot_grad (zeroed by the caller)
+        if (p.slot_grad && act && lc == 0 && j < nvis && kvalid(j))
+          atomicAdd(p.slot_grad + bt * p.topk + j, pj * ((dp - D) * s + dp));
+      }
+    }
   }
   // L2-norm backward of the query row
   float yd = 0.f;
@@ -223,26 +237,38 @@ __global__ __launch_bounds__(256) void hca_bwd_key_kernel(HcaBwdParams p, int mo
     for (int e = 0; e < 8; ++e) acc[i][e] = 0.f;
   }
   const int nw = (p.nb + 31) / 32;  // selection bitmap words per query
-  for (int t = tlo; t < thi; ++t) {
+  // the next query's row, scalars and selection word are requested while the
+  // current one is processed
+  struct QRow {
+    float q[8], d[8];
+    float rq, lse, D;
+    uint32_t sel;
+  };
+  auto fetch = [&](int t, QRow& r) {
     const size_t i0 = ((size_t)b * p.T + t) * p.nh + hh;
-    // CSA: the tile's rows this query selected (NBT consecutive bits)
-    uint32_t selbits = 0xffffffffu;
+    load8(p.q + i0 * HD + 8 * lc, r.q);
+    load8(p.dout + i0 * HD + 8 * lc, r.d);
+    r.rq = p.rq[i0];
+    r.lse = p.lse[i0];
+    r.D = p.dval[i0];
+    r.sel = 0xffffffffu;
     if (mode == 0 && p.sel) {
-      const uint32_t* w = p.sel + ((size_t)b * p.T + t) * nw;
-      const int w0 = r0 >> 5, sh = r0 & 31;
-      uint64_t two = w[w0];
-      if (w0 + 1 < nw) two |= (uint64_t)w[w0 + 1] << 32;
-      selbits = (uint32_t)(two >> sh);
+      // CSA: the tile's rows this query selected (NBT consecutive bits of one word)
+      r.sel = p.sel[((size_t)b * p.T + t) * nw + (r0 >> 5)] >> (r0 & 31);
     }
+  };
+  QRow nx;
+  fetch(tlo, nx);
+  for (int t = tlo; t < thi; ++t) {
+    const QRow cur = nx;
+    if (t + 1 < thi) fetch(t + 1, nx);
+    const uint32_t selbits = cur.sel;
     float qn[8], dv[8];
-    load8(p.q + i0 * HD + 8 * lc, qn);
-    load8(p.dout + i0 * HD + 8 * lc, dv);
-    const float rq = p.rq[i0], lse = p.lse[i0], D = p.dval[i0];
+    const float lse = cur.lse, D = cur.D;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) qn[e] *= rq;
-    if (!act) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qn[e] = dv[e] = 0.f;
+    for (int e = 0; e < 8; ++e) {
+      qn[e] = act ? cur.q[e] * cur.rq : 0.f;
+      dv[e] = act ? cur.d[e] : 0.f;
     }
 #pragma unroll
     for (int i = 0; i < NBT; ++i) {
