@@ -176,6 +176,30 @@ int kch_csa_attn_bwd(const float* q, const float* d_out, const float* kc, const 
                      float scale, int normalize, void* ws, size_t ws_bytes, void* stream);
 
 /*
+ * Backward of the KDA layer's front end and of the stack's LayerNorm (the
+ * autograd backward of ops_fused.py:480-581 and :42-60, exercised by the
+ * hybrid gradient test run_correctness.py:2710-2830).
+ * kch_kda_gates_bwd: given the forward's proj / gl rows (as kch_kda_gates)
+ *   and dq, dk [B,T,H,K], dv [B,T,HV,V], dg [B,T,HV,K], dbeta [B,T,HV],
+ *   writes the q | k | v | beta columns of dproj (ld_proj apart; the caller
+ *   zeroes the others) and dgl (ld_gl apart). K <= 256.
+ * kch_short_conv_bwd: dx [B,T,d] of the causal 3-tap depthwise conv, and adds
+ *   the taps' and the bias's gradients into fp32 dw [d,3] and db [d] (db may
+ *   be NULL); the lookback is an input only (the reference detaches it).
+ * kch_layer_norm_bwd: dx of the fp32 LayerNorm over the last dim, and adds
+ *   dw, db (fp32 [d]) . dtype / wdtype: the input's and the weight's.
+ */
+int kch_kda_gates_bwd(const void* proj, long long ld_proj, const void* gl, long long ld_gl,
+                      const void* dq, const void* dk, const void* dv, const void* dg,
+                      const void* dbeta, void* dproj, void* dgl, int B, int T, int H, int HV, int K,
+                      int V, float decay_scale, int dtype, void* stream);
+int kch_short_conv_bwd(const void* x, const void* lookback, const void* weight, const void* dy,
+                       void* dx, float* dw, float* db, int B, int T, int d, int dtype,
+                       void* stream);
+int kch_layer_norm_bwd(const void* x, const void* w, const void* dy, void* dx, float* dw, float* db,
+                       long long rows, int d, float eps, int dtype, int wdtype, void* stream);
+
+/*
  * Single-branch softmax-gated KV compression, [B,T,c] -> [B,T/m,c].
  * Replaces csa_compress_kv (ops_csa.py:198-234); used for the CSA indexer keys
  * (ops_csa.py:874) and for HCA (ops_hca.py:134).

@@ -359,6 +359,56 @@ int kch_csa_attn_bwd(const float* q, const float* d_out, const float* kc, const 
   return hip_status(fn, kch::hca_bwd_dispatch(p, ws, (hipStream_t)stream));
 }
 
+int kch_kda_gates_bwd(const void* proj, long long ld_proj, const void* gl, long long ld_gl,
+                      const void* dq, const void* dk, const void* dv, const void* dg,
+                      const void* dbeta, void* dproj, void* dgl, int B, int T, int H, int HV, int K,
+                      int V, float decay_scale, int dtype, void* stream) {
+  const char* fn = "kch_kda_gates_bwd";
+  if (!dtype_ok(dtype)) return fail(KCH_ERR_INVALID, "%s: unknown dtype %d", fn, dtype);
+  if (B < 0 || T < 0 || H < 1 || HV < 1 || K < 1 || V < 1)
+    return fail(KCH_ERR_INVALID, "%s: bad sizes", fn);
+  if (K > 256) return fail(KCH_ERR_UNSUPPORTED, "%s: K=%d > 256 not supported", fn, K);
+  if (ld_proj < 2LL * H * K + (long long)HV * V + HV || ld_gl < (long long)HV * K)
+    return fail(KCH_ERR_INVALID, "%s: row strides too small", fn);
+  if ((long long)B * T == 0) return KCH_OK;
+  if (!proj || !gl || !dq || !dk || !dv || !dg || !dbeta || !dproj || !dgl)
+    return fail(KCH_ERR_INVALID, "%s: null tensor pointer", fn);
+  kch::KdaGatesBwdParams p;
+  p.proj = proj; p.ld_proj = ld_proj; p.gl = gl; p.ld_gl = ld_gl;
+  p.dq = dq; p.dk = dk; p.dv = dv; p.dg = dg; p.dbeta = dbeta; p.dproj = dproj; p.dgl = dgl;
+  p.B = B; p.T = T; p.H = H; p.HV = HV; p.K = K; p.V = V;
+  p.decay_scale = decay_scale;
+  return hip_status(fn, kch::kda_gates_bwd_dispatch(p, dtype, (hipStream_t)stream));
+}
+
+int kch_short_conv_bwd(const void* x, const void* lookback, const void* weight, const void* dy,
+                       void* dx, float* dw, float* db, int B, int T, int d, int dtype,
+                       void* stream) {
+  const char* fn = "kch_short_conv_bwd";
+  if (!dtype_ok(dtype)) return fail(KCH_ERR_INVALID, "%s: unknown dtype %d", fn, dtype);
+  if (B < 0 || T < 0 || d < 1) return fail(KCH_ERR_INVALID, "%s: bad sizes B=%d T=%d d=%d", fn, B, T, d);
+  if ((long long)B * T == 0) return KCH_OK;
+  if (!x || !weight || !dy || !dx || !dw) return fail(KCH_ERR_INVALID, "%s: null tensor pointer", fn);
+  kch::ShortConvBwdParams p;
+  p.x = x; p.lookback = lookback; p.weight = weight; p.dy = dy; p.dx = dx; p.dw = dw; p.db = db;
+  p.B = B; p.T = T; p.d = d;
+  return hip_status(fn, kch::short_conv_bwd_dispatch(p, dtype, (hipStream_t)stream));
+}
+
+int kch_layer_norm_bwd(const void* x, const void* w, const void* dy, void* dx, float* dw, float* db,
+                       long long rows, int d, float eps, int dtype, int wdtype, void* stream) {
+  const char* fn = "kch_layer_norm_bwd";
+  if (!dtype_ok(dtype) || !dtype_ok(wdtype))
+    return fail(KCH_ERR_INVALID, "%s: unknown dtype %d / %d", fn, dtype, wdtype);
+  if (rows < 0 || d < 1) return fail(KCH_ERR_INVALID, "%s: bad sizes rows=%lld d=%d", fn, rows, d);
+  if (d > 16384) return fail(KCH_ERR_UNSUPPORTED, "%s: d=%d > 16384 not supported", fn, d);
+  if (rows == 0) return KCH_OK;
+  if (!x || !w || !dy || !dx || !dw) return fail(KCH_ERR_INVALID, "%s: null tensor pointer", fn);
+  kch::LayerNormBwdParams p;
+  p.x = x; p.w = w; p.dy = dy; p.dx = dx; p.dw = dw; p.db = db; p.rows = rows; p.d = d; p.eps = eps;
+  return hip_status(fn, kch::layer_norm_bwd_dispatch(p, dtype, wdtype, (hipStream_t)stream));
+}
+
 int kch_compress(const void* C, long long ldC, const void* Z, long long ldZ, const float* B_pos,
                  float* out_raw, void* out_key, int key_f32, int normalize, void* local, int B,
                  int T, int m, int c, int dtype, void* stream) {

@@ -143,6 +143,53 @@ struct KdaGatesParams {
 };
 hipError_t kda_gates_dispatch(const KdaGatesParams& p, int dtype, hipStream_t stream);
 
+// Backward of the activations (frontend_backward.hip): dproj receives the
+// q | k | v | beta columns (the caller zeroes the rest), dgl the gate's.
+struct KdaGatesBwdParams {
+  const void* proj;
+  long long ld_proj;
+  const void* gl;
+  long long ld_gl;
+  const void* dq;
+  const void* dk;
+  const void* dv;
+  const void* dg;
+  const void* dbeta;
+  void* dproj;   // ld_proj apart, as proj
+  void* dgl;     // ld_gl apart, as gl
+  int B, T, H, HV, K, V;
+  float decay_scale;
+};
+hipError_t kda_gates_bwd_dispatch(const KdaGatesBwdParams& p, int dtype, hipStream_t stream);
+
+// Backward of the short convolution: dx [B,T,d]; dw [d,3] and db [d] fp32,
+// accumulated (zeroed by the caller).
+struct ShortConvBwdParams {
+  const void* x;
+  const void* lookback;
+  const void* weight;
+  const void* dy;
+  void* dx;
+  float* dw;
+  float* db;
+  int B, T, d;
+};
+hipError_t short_conv_bwd_dispatch(const ShortConvBwdParams& p, int dtype, hipStream_t stream);
+
+// Backward of the fp32 LayerNorm: dx [rows,d]; dw, db [d] fp32, accumulated.
+struct LayerNormBwdParams {
+  const void* x;
+  const void* w;
+  const void* dy;
+  void* dx;
+  float* dw;
+  float* db;
+  long long rows;
+  int d;
+  float eps;
+};
+hipError_t layer_norm_bwd_dispatch(const LayerNormBwdParams& p, int dtype, int wdtype, hipStream_t stream);
+
 // fp32 LayerNorm of rows of d elements (kda_frontend.hip).
 struct LayerNormParams {
   const void* x;

@@ -14,7 +14,7 @@ Parameter and buffer names, shapes and the layout rule are the reference's, so
 a reference ``state_dict`` loads unchanged. The forward passes run on a ROCm
 GPU: projections are torch GEMMs (hipBLASLt); the KDA short convolution and
 activations, KDA itself, CSA, HCA and the decode caches are ``libkch.so``
-kernels. Forward only: every forward runs under ``torch.no_grad()``.
+kernels. With gradients enabled the layers run their HIP backward kernels.
 
 ``HybridDecoding`` takes any ``HybridConfig`` (the reference hard-codes a tiny
 geometry with ``kda_chunk_size=0``); prefill goes through the chunked KDA
@@ -40,7 +40,7 @@ from .decoding_cache import CSADecodingCache, HCADecodingCache
 from . import ops_csa
 from .ops_csa import naive_csa
 from .ops_hca import naive_hca
-from .ops_kda import _recurrent_launch, kda_recurrent_into
+from .ops_kda import _recurrent_launch, kda_recurrent_into, naive_chunk_kda, naive_recurrent_kda
 from .ops_kda_backend import kda_forward, validate_kda_backend
 
 logger = logging.getLogger(__name__)
@@ -84,11 +84,50 @@ def _linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     return y
 
 
+def _grad_wanted(*ts) -> bool:
+    return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts)
+
+
+class _LayerNormFn(torch.autograd.Function):
+    """``_Fp32LayerNorm`` with gradients: ``kch_layer_norm`` forward,
+    ``kch_layer_norm_bwd`` backward (dx in x's dtype; dw, db accumulated in
+    fp32, returned in the parameters' dtype)."""
+
+    @staticmethod
+    def forward(ctx, x, w, b, module):
+        ctx.save_for_backward(x, w, b)
+        ctx.eps = float(module.eps)
+        with torch.no_grad():
+            return module._forward_kernel(x)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w, b = ctx.saved_tensors
+        d = w.shape[-1]
+        xc = x.contiguous()
+        dyc = dy.to(x.dtype).contiguous()
+        wc = w.detach().contiguous()
+        dx = torch.empty_like(xc)
+        dw = torch.zeros(d, device=x.device, dtype=torch.float32)
+        db = torch.zeros_like(dw) if b is not None else None
+        fn = "_Fp32LayerNorm"
+        _lib.call("kch_layer_norm_bwd", _lib.ptr(xc), _lib.ptr(wc), _lib.ptr(dyc), _lib.ptr(dx),
+                  _lib.ptr(dw), _lib.ptr(db), xc.numel() // d, d, ctx.eps,
+                  _lib.dtype_code(fn, xc.dtype), _lib.dtype_code(fn, wc.dtype),
+                  _lib.stream_of(xc))
+        return dx, dw.to(w.dtype), None if db is None else db.to(b.dtype), None
+
+
 class _Fp32LayerNorm(nn.LayerNorm):
     """LayerNorm computed in fp32, returned in the input dtype (``ops_fused.py:42-60``),
-    as one kernel (``kch_layer_norm``)."""
+    as one kernel (``kch_layer_norm``; backward ``kch_layer_norm_bwd``)."""
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if _grad_wanted(x, self.weight, self.bias) and x.numel():
+            return _LayerNormFn.apply(x, self.weight, self.bias, self)
+        return self._forward_kernel(x)
+
+    def _forward_kernel(self, x: torch.Tensor) -> torch.Tensor:
         if x.numel() == 0:
             return torch.empty_like(x)
         if not x.is_cuda:
@@ -275,6 +314,91 @@ class _FusedWeightLayer(nn.Module):
         return super()._apply(fn, *args, **kwargs)
 
 
+class _ShortConvFn(torch.autograd.Function):
+    """The KDA layer's causal depthwise conv with gradients: ``kch_short_conv``
+    forward, ``kch_short_conv_bwd`` backward (the lookback is an input only,
+    detached as in the reference, ``ops_fused.py:480-527``)."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, lookback):
+        B, T, d = x.shape
+        w = weight.detach().reshape(d, _CONV_K).to(x.dtype).contiguous()
+        b = None if bias is None else bias.detach().to(x.dtype).contiguous()
+        xc = x.contiguous()
+        if xc.data_ptr() % 16:
+            xc = xc.clone()
+        lb = None if lookback is None else lookback.detach().to(x.dtype).contiguous()
+        out = torch.empty_like(xc)
+        code = _lib.dtype_code("KDAHybridLayer", x.dtype)
+        _lib.call("kch_short_conv", _lib.ptr(xc), _lib.ptr(lb), _lib.ptr(w), _lib.ptr(b),
+                  _lib.ptr(out), B, T, d, code, _lib.stream_of(xc))
+        ctx.save_for_backward(xc, w, lb)
+        ctx.meta = (weight.shape, weight.dtype, None if bias is None else bias.dtype)
+        return out
+
+    @staticmethod
+    def backward(ctx, dy):
+        xc, w, lb = ctx.saved_tensors
+        wshape, wdt, bdt = ctx.meta
+        B, T, d = xc.shape
+        dyc = dy.to(xc.dtype).contiguous()
+        dx = torch.empty_like(xc)
+        dw = torch.zeros(d * _CONV_K, device=xc.device, dtype=torch.float32)
+        db = None if bdt is None else torch.zeros(d, device=xc.device, dtype=torch.float32)
+        _lib.call("kch_short_conv_bwd", _lib.ptr(xc), _lib.ptr(lb), _lib.ptr(w), _lib.ptr(dyc),
+                  _lib.ptr(dx), _lib.ptr(dw), _lib.ptr(db), B, T, d,
+                  _lib.dtype_code("KDAHybridLayer", xc.dtype), _lib.stream_of(xc))
+        return dx, dw.view(wshape).to(wdt), None if db is None else db.to(bdt), None
+
+
+class _KdaGatesFn(torch.autograd.Function):
+    """The KDA layer's q/k/v/g/beta activations with gradients:
+    ``kch_kda_gates`` forward, ``kch_kda_gates_bwd`` backward
+    (``ops_fused.py:559-581``)."""
+
+    @staticmethod
+    def forward(ctx, proj, gl, dims):
+        H, HV, K, V, decay = dims
+        B, T = proj.shape[:2]
+        dev, dt = proj.device, proj.dtype
+        q = torch.empty(B, T, H, K, device=dev, dtype=dt)
+        k = torch.empty_like(q)
+        v = torch.empty(B, T, HV, V, device=dev, dtype=dt)
+        g = torch.empty(B, T, HV, K, device=dev, dtype=dt)
+        beta = torch.empty(B, T, HV, device=dev, dtype=dt)
+        code = _lib.dtype_code("KDAHybridLayer", dt)
+        _lib.call("kch_kda_gates", _lib.ptr(proj), proj.stride(1), _lib.ptr(gl), gl.stride(1),
+                  _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(beta),
+                  B, T, H, HV, K, V, float(decay), code, _lib.stream_of(proj))
+        ctx.save_for_backward(proj, gl)
+        ctx.dims = dims
+        return q, k, v, g, beta
+
+    @staticmethod
+    def backward(ctx, dq, dk, dv, dg, dbeta):
+        proj, gl = ctx.saved_tensors
+        H, HV, K, V, decay = ctx.dims
+        B, T = proj.shape[:2]
+        dt = proj.dtype
+
+        def grad_or_zero(t, shape):
+            return torch.zeros(shape, device=proj.device, dtype=dt) if t is None \
+                else t.to(dt).contiguous()
+
+        dq = grad_or_zero(dq, (B, T, H, K))
+        dk = grad_or_zero(dk, (B, T, H, K))
+        dv = grad_or_zero(dv, (B, T, HV, V))
+        dg = grad_or_zero(dg, (B, T, HV, K))
+        dbeta = grad_or_zero(dbeta, (B, T, HV))
+        dproj = torch.zeros_like(proj)
+        dgl = torch.zeros_like(gl)
+        _lib.call("kch_kda_gates_bwd", _lib.ptr(proj), proj.stride(1), _lib.ptr(gl), gl.stride(1),
+                  _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dg), _lib.ptr(dbeta),
+                  _lib.ptr(dproj), _lib.ptr(dgl), B, T, H, HV, K, V, float(decay),
+                  _lib.dtype_code("KDAHybridLayer", dt), _lib.stream_of(proj))
+        return dproj, dgl, None
+
+
 class KDAHybridLayer(_FusedWeightLayer):
     """KDA sub-layer (``ops_fused.py:316-609``).
 
@@ -364,6 +488,8 @@ class KDAHybridLayer(_FusedWeightLayer):
                 lookback = None
             else:
                 lookback = lookback.to(device=x.device, dtype=x.dtype)
+        if _grad_wanted(x, state, *self.parameters()):
+            return self._forward_grad(x, state, lookback, detach_lookback)
         with torch.no_grad():
             xc = x.contiguous()
             if xc.data_ptr() % 16:
@@ -420,6 +546,41 @@ class KDAHybridLayer(_FusedWeightLayer):
                     state_out.copy_(new_state)
                     new_state = state_out
             out = _linear(o.reshape(B, T, HV * V), self.o_proj.weight)
+        return out, new_state, new_lookback
+
+    def _forward_grad(self, x, state, lookback, detach_lookback):
+        """The same layer with gradients: the conv and the activations through
+        their HIP backward kernels, the projections through autograd (library
+        GEMMs), the KDA operator through ``kch_kda_recurrent_bwd``."""
+        B, T, d = x.shape
+        cfg = self.cfg
+        H, K, V, HV = cfg.n_heads_qk, cfg.head_dim_k, cfg.head_dim_v, cfg.n_heads_v
+        if T >= _CONV_K - 1:
+            new_lookback = x[:, -(_CONV_K - 1):]
+        elif lookback is not None:
+            new_lookback = torch.cat([lookback[:, T:], x], dim=1)
+        else:
+            new_lookback = torch.cat([x.new_zeros(B, _CONV_K - 1 - T, d), x], dim=1)
+        if detach_lookback:
+            new_lookback = new_lookback.detach()
+        new_lookback = new_lookback.clone()
+        x_conv = _ShortConvFn.apply(x, self.short_conv.weight, self.short_conv.bias, lookback)
+        W = torch.cat([self.q_proj.weight, self.k_proj.weight, self.v_proj.weight,
+                       self.beta.weight, self.g_down.weight], 0).to(x.dtype)
+        proj = F.linear(x_conv, W)
+        off_gd = 2 * H * K + HV * V + HV
+        gl = F.linear(proj[..., off_gd:off_gd + K], self.g_up.weight.to(x.dtype))
+        q, k, v, g, beta = _KdaGatesFn.apply(proj, gl, (H, HV, K, V, float(cfg.kda_decay_scale)))
+        use_chunk = cfg.kda_chunk_size >= 1 and T >= cfg.kda_chunk_size
+        st = None if state is None else state.to(device=x.device, dtype=torch.float32)
+        if use_chunk:
+            o, new_state = naive_chunk_kda(q, k, v, g, beta, scale=self._scale_value(),
+                                           initial_state=st, output_final_state=True,
+                                           chunk_size=cfg.kda_chunk_size)
+        else:
+            o, new_state = naive_recurrent_kda(q, k, v, g, beta, scale=self._scale_value(),
+                                               initial_state=st, output_final_state=True)
+        out = F.linear(o.reshape(B, T, HV * V), self.o_proj.weight.to(x.dtype))
         return out, new_state, new_lookback
 
 
@@ -482,7 +643,8 @@ class CSAHybridLayer(_FusedWeightLayer):
         cfg = self.cfg
         if self.training and not self.use_ste:
             self._maybe_warn_indexer()
-        with torch.no_grad():
+        # the operator takes its gradient path when autograd asks for one
+        with torch.set_grad_enabled(torch.is_grad_enabled()):
             o = naive_csa(
                 x, self.W_aKV.weight, self.W_bKV.weight, self.W_aZ.weight, self.W_bZ.weight,
                 self.Ba, self.Bb, self.W_DQ.weight, self.W_UQ.weight, self.W_IUQ.weight,
@@ -522,7 +684,7 @@ class HCAHybridLayer(_FusedWeightLayer):
 
     def forward(self, x: torch.Tensor, state: torch.Tensor | None = None):
         cfg = self.cfg
-        with torch.no_grad():
+        with torch.set_grad_enabled(torch.is_grad_enabled()):
             o = naive_hca(x, self.W_KV.weight, self.W_Z.weight, self.B_pos, self.W_DQ.weight,
                           self.W_UQ.weight, m2=cfg.hca_m2, nh=cfg.hca_nh, c=cfg.hca_c,
                           dc=cfg.hca_dc, sliding_window=cfg.hca_sliding_window,
@@ -646,7 +808,8 @@ class HybridKCHAttention(nn.Module):
                 f"{len(lookbacks)} but the model has {self.n_kda_layers} KDA layers.")
         kda_idx = 0
         new_lookbacks = []
-        with torch.no_grad():
+        grad = _grad_wanted(x, *self.parameters())
+        with torch.set_grad_enabled(grad):
             for layer, norm, kind in zip(self.layers, self.norms, self.layout):
                 residual = x
                 h = norm(x)

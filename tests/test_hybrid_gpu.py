@@ -28,6 +28,15 @@ from oracle import hybrid as OH
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(autouse=True)
+def _forward_only():
+    """These are forward-parity tests: the layers' parameters require grad, so
+    with autograd on they would take their gradient path (and return tensors
+    that require grad); that path is tested in test_hybrid_grad_gpu.py."""
+    with torch.no_grad():
+        yield
+
+
 def small_cfg(**kw):
     import kch
     base = dict(d_model=128, n_heads_qk=2, n_heads_v=2, head_dim_k=64, head_dim_v=64,
