@@ -355,6 +355,76 @@ def bench_hca(B, T, steps, warmup, dev):
             "includes": "projections (hipBLASLt; q up-projection kch_linear_up) + core", "core": core}
 
 
+def bench_training(dev, reps=3):
+    """The training path's backward passes at the configs' shapes (one call
+    each after a warm-up, mean of ``reps``): the KDA gradients at configs[1],
+    the HCA core's at configs[3], the CSA attention's at configs[2] (on the
+    kernel's own top-512 selection), and one forward + backward step of the
+    configs[4] stack geometry at B=2, T=2048 (bf16)."""
+    import kch
+    from kch.ops_csa import csa_attn_grad
+    from kch.ops_hca import hca_core_grad
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    g = torch.Generator().manual_seed(5)
+    out = {}
+    B, T, H, K, V = 8, 4096, 16, 128, 128
+    xs, s0, _, _ = kda_inputs(B, T, H, K, V, dev=dev)
+    do = torch.randn(B, T, H, V, generator=g).to(dev, torch.bfloat16)
+    out["kda_C1_backward_ms"] = timed(lambda: kch.kda_recurrent_grad(*xs, do, initial_state=s0))
+    del xs, s0, do
+    B, T, nh, c, m2, win = 4, 32768, 16, 128, 128, 128
+    C, Z = (torch.randn(B, T, c, generator=g).to(dev, torch.bfloat16) for _ in range(2))
+    q = torch.randn(B, T, nh, c, generator=g).to(dev, torch.bfloat16)
+    dq = torch.randn(B, T, nh, c, generator=g).to(dev, torch.bfloat16)
+    Bp = (0.02 * torch.randn(m2, c, generator=g)).to(dev)
+    sink = torch.randn(nh, generator=g).to(dev)
+    out["hca_C3_core_backward_ms"] = timed(
+        lambda: hca_core_grad(C, Z, q, Bp, dq, m2=m2, sliding_window=win, sink_logits=sink))
+    del C, Z, q, dq
+    B, T, nh, c, m, topk, win, cI, nIh = 4, 8192, 16, 128, 4, 512, 128, 64, 4
+    X = [torch.randn(B, T, c, generator=g).to(dev, torch.bfloat16) for _ in range(4)]
+    Ki, Zi = (torch.randn(B, T, cI, generator=g).to(dev, torch.bfloat16) for _ in range(2))
+    q = torch.randn(B, T, nh, c, generator=g).to(dev, torch.bfloat16)
+    qi = torch.randn(B, T, nIh, cI, generator=g).to(dev, torch.bfloat16)
+    wi = torch.randn(B, T, nIh, generator=g).to(dev, torch.bfloat16)
+    Ba, Bb = ((0.02 * torch.randn(m, c, generator=g)).to(dev) for _ in range(2))
+    Bi = (0.02 * torch.randn(m, cI, generator=g)).to(dev)
+    with torch.no_grad():
+        _, idx = kch.csa_core(*X, Ki, Zi, q, qi, wi, Ba, Bb, Bi, m=m, topk=topk,
+                              sliding_window=win, sink_logits=sink, normalize_qk=True,
+                              return_indices=True)
+    dq = torch.randn(B, T, nh, c, generator=g).to(dev, torch.bfloat16)
+    out["csa_C2_attention_backward_ms"] = timed(
+        lambda: csa_attn_grad(*X, q, Ba, Bb, idx, dq, m=m, sliding_window=win, sink_logits=sink,
+                              normalize_qk=True))
+    del X, q, dq, idx
+    cfg = kch.HybridConfig(d_model=2048, n_heads_qk=16, n_heads_v=16, head_dim_k=128,
+                           head_dim_v=128, kda_chunk_size=64, csa_m=4, csa_topk=512, csa_nh=16,
+                           csa_c=128, csa_dc=128, csa_nIh=4, csa_cI=64, csa_sliding_window=128,
+                           hca_m2=128, hca_nh=16, hca_c=128, hca_dc=128, hca_sliding_window=128)
+    model = kch.HybridKCHAttention(cfg, total_layers=5).to(dev, torch.bfloat16).train()
+    x = torch.randn(2, 2048, 2048, generator=g).to(dev, torch.bfloat16)
+
+    def train_step():
+        model.zero_grad(set_to_none=True)
+        y, _, _ = model.forward_functional(x, None, [None] * model.n_kda_layers)
+        y.float().square().mean().backward()
+
+    out["hybrid_C4_B2_T2048_train_step_ms"] = timed(train_step)
+    return out
+
+
 def bench_hybrid(dev, T=16384, B=2, n_decode=256):
     import kch
     cfg = kch.HybridConfig(d_model=2048, n_heads_qk=16, n_heads_v=16, head_dim_k=128,
@@ -490,7 +560,8 @@ def main():
     ap.add_argument("--headline-only", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run three 1 GiB device-to-device copies (HBM counter scale)")
-    ap.add_argument("--only-extra", choices=["decode_bw", "hybrid_C4", "kda_T8K", "csa_C2", "hca_C3"],
+    ap.add_argument("--only-extra", choices=["decode_bw", "hybrid_C4", "kda_T8K", "csa_C2", "hca_C3",
+                                             "training"],
                     help="run just this extra workload and print its JSON (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -502,7 +573,7 @@ def main():
 
     dev = torch.device("cuda:0")
     if args.only_extra:
-        fn = {"decode_bw": bench_decode_bw, "hybrid_C4": bench_hybrid,
+        fn = {"decode_bw": bench_decode_bw, "hybrid_C4": bench_hybrid, "training": bench_training,
               "kda_T8K": lambda d: bench_kda(4, 8192, args.steps, args.warmup, d),
               "csa_C2": lambda d: bench_csa(4, 8192, max(3, args.steps // 4), 1, d),
               "hca_C3": lambda d: bench_hca(4, 32768, max(3, args.steps // 4), 1, d)}[args.only_extra]

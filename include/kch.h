@@ -186,8 +186,8 @@ int kch_csa_attn_bwd(const float* q, const float* d_out, const float* kc, const 
  * kch_short_conv_bwd: dx [B,T,d] of the causal 3-tap depthwise conv, and adds
  *   the taps' and the bias's gradients into fp32 dw [d,3] and db [d] (db may
  *   be NULL); the lookback is an input only (the reference detaches it).
- * kch_layer_norm_bwd: dx of the fp32 LayerNorm over the last dim, and adds
- *   dw, db (fp32 [d]) . dtype / wdtype: the input's and the weight's.
+ * kch_layer_norm_bwd: dx of the fp32 LayerNorm over the last dim (d <= 4096),
+ *   and adds dw, db (fp32 [d]). dtype / wdtype: the input's and the weight's.
  */
 int kch_kda_gates_bwd(const void* proj, long long ld_proj, const void* gl, long long ld_gl,
                       const void* dq, const void* dk, const void* dv, const void* dg,

@@ -401,7 +401,7 @@ int kch_layer_norm_bwd(const void* x, const void* w, const void* dy, void* dx, f
   if (!dtype_ok(dtype) || !dtype_ok(wdtype))
     return fail(KCH_ERR_INVALID, "%s: unknown dtype %d / %d", fn, dtype, wdtype);
   if (rows < 0 || d < 1) return fail(KCH_ERR_INVALID, "%s: bad sizes rows=%lld d=%d", fn, rows, d);
-  if (d > 16384) return fail(KCH_ERR_UNSUPPORTED, "%s: d=%d > 16384 not supported", fn, d);
+  if (d > 4096) return fail(KCH_ERR_UNSUPPORTED, "%s: d=%d > 4096 not supported", fn, d);
   if (rows == 0) return KCH_OK;
   if (!x || !w || !dy || !dx || !dw) return fail(KCH_ERR_INVALID, "%s: null tensor pointer", fn);
   kch::LayerNormBwdParams p;

@@ -13,7 +13,8 @@
 //   run (the transposed 3-tap filter), and the run's sums for the filter taps
 //   and the bias, added to fp32 buffers.
 // layer_norm_bwd_kernel wave per row, 16 rows per wave: dx from the recomputed
-//   mean and rstd; the rows' dy x^ and dy add into LDS, then into fp32 buffers.
+//   mean and rstd; the rows' dy x^ and dy sums stay in registers, meet in LDS
+//   across the four waves, then add into fp32 buffers.
 
 #include <hip/hip_runtime.h>
 
@@ -130,14 +131,21 @@ __global__ __launch_bounds__(256) void short_conv_bwd_kernel(ShortConvBwdParams 
 
 constexpr int kLnRowsPerWave = 16;
 
-template <typename T, typename WT>
+// NJ = channels per lane (d <= 64 NJ): the rows' dy x^ and dy sums stay in
+// registers; the four waves meet in LDS at the end.
+template <typename T, typename WT, int NJ>
 __global__ __launch_bounds__(256) void layer_norm_bwd_kernel(LayerNormBwdParams p) {
-  extern __shared__ float lds[];  // dw [d] | db [d]
+  extern __shared__ float lds[];  // [2][d]
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int d = p.d;
-  for (int i = threadIdx.x; i < 2 * d; i += 256) lds[i] = 0.f;
-  __syncthreads();
   const WT* w = static_cast<const WT*>(p.w);
+  float aw[NJ], ab[NJ], wv[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int i = lane + 64 * j;
+    aw[j] = ab[j] = 0.f;
+    wv[j] = i < d ? to_f32(w[i]) : 0.f;
+  }
   const long long r0 = ((long long)blockIdx.x * 4 + wave) * kLnRowsPerWave;
   for (int rr = 0; rr < kLnRowsPerWave; ++rr) {
     const long long row = r0 + rr;
@@ -145,50 +153,81 @@ __global__ __launch_bounds__(256) void layer_norm_bwd_kernel(LayerNormBwdParams 
     const T* x = static_cast<const T*>(p.x) + row * d;
     const T* dy = static_cast<const T*>(p.dy) + row * d;
     T* dx = static_cast<T*>(p.dx) + row * d;
+    float xv[NJ], gv[NJ];
     float s = 0.f;
-    for (int i = lane; i < d; i += 64) s += to_f32(x[i]);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int i = lane + 64 * j;
+      xv[j] = i < d ? to_f32(x[i]) : 0.f;
+      gv[j] = i < d ? to_f32(dy[i]) : 0.f;
+      s += xv[j];
+    }
     const float mean = wave_sum(s) / d;
     float v = 0.f;
-    for (int i = lane; i < d; i += 64) {
-      const float e = to_f32(x[i]) - mean;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int i = lane + 64 * j;
+      const float e = i < d ? xv[j] - mean : 0.f;
       v += e * e;
     }
     const float rstd = rsqrtf(wave_sum(v) / d + p.eps);
     float sg = 0.f, sgx = 0.f;
-    for (int i = lane; i < d; i += 64) {
-      const float xh = (to_f32(x[i]) - mean) * rstd;
-      const float g = to_f32(dy[i]) * to_f32(w[i]);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      xv[j] = (xv[j] - mean) * rstd;  // now x^
+      const float g = gv[j] * wv[j];
       sg += g;
-      sgx += g * xh;
+      sgx += g * xv[j];
     }
     sg = wave_sum(sg) / d;
     sgx = wave_sum(sgx) / d;
-    for (int i = lane; i < d; i += 64) {
-      const float xh = (to_f32(x[i]) - mean) * rstd;
-      const float gy = to_f32(dy[i]);
-      dx[i] = from_f32<T>(rstd * (gy * to_f32(w[i]) - sg - xh * sgx));
-      atomicAdd(lds + i, gy * xh);
-      atomicAdd(lds + d + i, gy);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int i = lane + 64 * j;
+      if (i < d) {
+        dx[i] = from_f32<T>(rstd * (gv[j] * wv[j] - sg - xv[j] * sgx));
+        aw[j] += gv[j] * xv[j];
+        ab[j] += gv[j];
+      }
     }
   }
-  __syncthreads();
+  // the four waves' sums, one wave after another into [2][d] of LDS
+  for (int wv_ = 0; wv_ < 4; ++wv_) {
+    if (wave == wv_) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int i = lane + 64 * j;
+        if (i < d) {
+          lds[i] = (wv_ ? lds[i] : 0.f) + aw[j];
+          lds[d + i] = (wv_ ? lds[d + i] : 0.f) + ab[j];
+        }
+      }
+    }
+    __syncthreads();
+  }
   for (int i = threadIdx.x; i < d; i += 256) {
     atomicAdd(p.dw + i, lds[i]);
     if (p.db) atomicAdd(p.db + i, lds[d + i]);
   }
 }
 
-template <typename T>
-hipError_t ln_bwd_w(const LayerNormBwdParams& p, int wdtype, hipStream_t s) {
+template <typename T, typename WT>
+hipError_t ln_bwd_nj(const LayerNormBwdParams& p, hipStream_t s) {
   const unsigned blocks = (unsigned)((p.rows + 4 * kLnRowsPerWave - 1) / (4 * kLnRowsPerWave));
   const size_t lds = (size_t)2 * p.d * sizeof(float);
-  if (wdtype == DT_F32)
-    hipLaunchKernelGGL((layer_norm_bwd_kernel<T, float>), dim3(blocks), dim3(256), lds, s, p);
-  else if (wdtype == DT_BF16)
-    hipLaunchKernelGGL((layer_norm_bwd_kernel<T, bf16_t>), dim3(blocks), dim3(256), lds, s, p);
-  else
-    hipLaunchKernelGGL((layer_norm_bwd_kernel<T, _Float16>), dim3(blocks), dim3(256), lds, s, p);
+  const int nj = (p.d + 63) / 64;
+  if (nj <= 8) hipLaunchKernelGGL((layer_norm_bwd_kernel<T, WT, 8>), dim3(blocks), dim3(256), lds, s, p);
+  else if (nj <= 16) hipLaunchKernelGGL((layer_norm_bwd_kernel<T, WT, 16>), dim3(blocks), dim3(256), lds, s, p);
+  else if (nj <= 32) hipLaunchKernelGGL((layer_norm_bwd_kernel<T, WT, 32>), dim3(blocks), dim3(256), lds, s, p);
+  else hipLaunchKernelGGL((layer_norm_bwd_kernel<T, WT, 64>), dim3(blocks), dim3(256), lds, s, p);
   return hipGetLastError();
+}
+
+template <typename T>
+hipError_t ln_bwd_w(const LayerNormBwdParams& p, int wdtype, hipStream_t s) {
+  if (wdtype == DT_F32) return ln_bwd_nj<T, float>(p, s);
+  if (wdtype == DT_BF16) return ln_bwd_nj<T, bf16_t>(p, s);
+  return ln_bwd_nj<T, _Float16>(p, s);
 }
 
 }  // namespace
