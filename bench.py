@@ -55,6 +55,7 @@ import torch  # noqa: E402
 METRIC = "prefill tokens/s (KDA chunk, CSA, HCA) at T=8K; % of MFMA/HBM roofline"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+FP32_PEAK_TFLOPS = 157.3
 
 # Measured HBM bytes per headline step (both kernels): rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE (KiB per dispatch) on `bench.py --headline-only`, each scaled by the
@@ -422,6 +423,39 @@ def bench_training(dev, reps=3):
         y.float().square().mean().backward()
 
     out["hybrid_C4_B2_T2048_train_step_ms"] = timed(train_step)
+    # algorithmic FLOPs of the backwards: the attention ones recompute the
+    # scores and dp (2 x 2c per pair and head) and form dq and dk (2c + 4c):
+    # 2.5x the forward's 4c; the KDA one runs the recurrence forward twice and
+    # backward once, taken as 2x the chunk form's forward FLOPs. Against the
+    # fp32 peak: these kernels compute in fp32 on the vector units.
+    fl = {"kda_C1_backward_ms": 2.0 * kda_algorithmic(8, 4096, 16, 128, 128)[0],
+          "hca_C3_core_backward_ms": 2.5 * hca_core_algorithmic(4, 32768, 128, 128, 16, 128)[0],
+          "csa_C2_attention_backward_ms": 2.5 * csa_core_algorithmic(
+              4, 8192, 4, 512, 128, 16, 128, 4, 64)[0]}
+    out["fp32_peak_tflops"] = FP32_PEAK_TFLOPS
+    for k, f in fl.items():
+        tf = f / (out[k] * 1e-3) / 1e12
+        out[k.replace("_ms", "_tflops")] = tf
+        out[k.replace("_ms", "_fp32_frac")] = tf / FP32_PEAK_TFLOPS
+    # CPU beside it: the oracle's hand-written KDA backward (numpy, fp64) on a
+    # slice of configs[1], scaled to tokens/s of the whole workload
+    from oracle.kda import recurrent_kda_grad
+    rng = np.random.default_rng(0)
+    Tc, Hc = 2048, 4
+    qa = rng.standard_normal((1, Tc, Hc, 128))
+    qa /= np.linalg.norm(qa, axis=-1, keepdims=True)
+    ka = rng.standard_normal((1, Tc, Hc, 128))
+    ka /= np.linalg.norm(ka, axis=-1, keepdims=True)
+    va, doa = rng.standard_normal((1, Tc, Hc, 128)), rng.standard_normal((1, Tc, Hc, 128))
+    ga = -np.log1p(np.exp(-rng.standard_normal((1, Tc, Hc, 128))))
+    ba = 1.0 / (1.0 + np.exp(-rng.standard_normal((1, Tc, Hc))))
+    t0 = time.perf_counter()
+    recurrent_kda_grad(qa, ka, va, ga, ba, doa)
+    dt = time.perf_counter() - t0
+    out["cpu_kda_backward"] = {
+        "tokens_per_s": Tc * Hc / dt / 16, "sample": f"oracle.kda.recurrent_kda_grad, B=1 T={Tc} "
+        f"H={Hc} K=V=128 fp64 (numpy), scaled to configs[1]'s 16 heads", "seconds": dt,
+        "gpu_tokens_per_s": 8 * 4096 / (out["kda_C1_backward_ms"] * 1e-3)}
     return out
 
 
