@@ -352,6 +352,7 @@ int kch_csa_attn_bwd(const float* q, const float* d_out, const float* kc, const 
   p.dCb = dCb; p.dZb = dZb; p.dBbp = dBbp;
   p.idx = topk > 0 ? idx : nullptr;
   p.topk = topk;
+  p.sparse = 1;
   p.slot_grad = topk > 0 ? slot_grad : nullptr;
   p.normalize = normalize ? 1 : 0;
   p.B = B; p.T = T; p.nh = nh; p.c = c; p.m2 = m; p.nb = T / m; p.win = win;

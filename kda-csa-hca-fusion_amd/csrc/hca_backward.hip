@@ -89,7 +89,7 @@ __global__ __launch_bounds__(256) void hca_bwd_query_kernel(HcaBwdParams p) {
   // keys: the selected blocks (CSA; the selection's -1 slots are skipped) or
   // every block the query sees (HCA), then the window rows
   const int* sel_row = p.idx ? p.idx + bt * p.topk : nullptr;
-  const int nvis = p.idx ? p.topk : min((t + 1) / p.m2, p.nb);
+  const int nvis = p.sparse ? p.topk : min((t + 1) / p.m2, p.nb);
   const int i0 = p.win > 0 ? max(0, p.win - 1 - t) : 0;
   const int nwin = p.win > 0 ? p.win - i0 : 0;
   const int nk = nvis + nwin;
@@ -442,8 +442,14 @@ hipError_t launch_hca_bwd(const HcaBwdParams& p, const Plan& z, hipStream_t s) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (p.nb > 0) {
-    hipLaunchKernelGGL((hca_bwd_key_kernel<HD>), dim3(z.ntile_b * z.nchunk_b, p.B), dim3(256), 0, s, p, 0,
-                       z.nchunk_b, z.ntile_b);
+    if (p.sparse && p.topk == 0) {
+      // no selection: the compressed rows receive nothing
+      e = fill_u32(p.part_b, (long long)(z.part_b), 0u, s);
+      if (e != hipSuccess) return e;
+    } else {
+      hipLaunchKernelGGL((hca_bwd_key_kernel<HD>), dim3(z.ntile_b * z.nchunk_b, p.B), dim3(256), 0, s, p,
+                         0, z.nchunk_b, z.ntile_b);
+    }
     hipLaunchKernelGGL((hca_bwd_block_kernel<HD>), dim3(p.nb, p.B), dim3(HD), 0, s, p, z.nchunk_b, z.ntile_b);
   }
   if (p.win > 0) {

@@ -81,6 +81,7 @@ struct HcaBwdParams {
   const int* idx = nullptr;
   const uint32_t* sel = nullptr;
   int topk = 0;
+  int sparse = 0;  // CSA: only the selected blocks (none when topk = 0)
   const float* Cb = nullptr;
   const float* Zb = nullptr;
   const float* Bb = nullptr;

@@ -208,3 +208,27 @@ def test_naive_csa_ste_contract(dev):
     for k in ("W_aKV", "W_bKV", "W_aZ", "W_bZ", "W_DQ", "W_UQ", "Ba", "Bb"):
         g = outs[1][1][k].grad
         assert g is not None and torch.isfinite(g).all() and g.abs().sum() > 0, k
+
+
+@pytest.mark.parametrize("topk,win", [(6, 0), (0, 5)])
+def test_attn_grad_sparse_edges(dev, topk, win):
+    """A selection wider than the visible blocks (mostly -1 slots), and no
+    selection at all (window only)."""
+    import kch
+    rng = np.random.default_rng(31 + topk)
+    B, T, nh, c, m = 1, 16, 2, 64, 4
+    X = {k: rng.standard_normal((B, T, c)) for k in ("Ca", "Cb", "Za", "Zb")}
+    q = rng.standard_normal((B, T, nh, c))
+    Ba, Bb = rng.standard_normal((m, c)) * 0.3, rng.standard_normal((m, c)) * 0.3
+    sk = rng.standard_normal(nh)
+    W = rng.standard_normal((B, T, nh, c))
+    idx = _selection(rng, B, T, m, topk) if topk else np.zeros((B, T, 0), np.int32)
+    ref = o_grad(X["Ca"], X["Cb"], X["Za"], X["Zb"], q, Ba, Bb, idx, W, m=m, sliding_window=win,
+                 sink_logits=sk, normalize_qk=True)
+    t = lambda x: torch.tensor(x, dtype=torch.float32, device=dev)  # noqa: E731
+    g = kch.ops_csa.csa_attn_grad(t(X["Ca"]), t(X["Cb"]), t(X["Za"]), t(X["Zb"]), t(q), t(Ba),
+                                  t(Bb), torch.tensor(idx, device=dev) if topk else None, t(W),
+                                  m=m, sliding_window=win, sink_logits=t(sk), normalize_qk=True)
+    torch.cuda.synchronize()
+    for name in ("Ca", "Cb", "Za", "Zb", "q", "Ba", "Bb", "sink_logits"):
+        _check(name, g[name].cpu().numpy(), ref[name])

@@ -158,3 +158,21 @@ def test_no_grad_forward_unchanged(dev):
     assert o1.grad_fn is None
     o2 = kch.hca_core(*[a.clone().requires_grad_(True) for a in args], **kw)
     assert o2.grad_fn is not None and torch.equal(o1, o2.detach())
+
+
+@pytest.mark.parametrize("T,m2,win", [(16, 16, 40), (32, 8, 1)])
+def test_core_grad_edges(dev, T, m2, win):
+    """One block (most queries see none); a window wider than the sequence;
+    a one-token window."""
+    import kch
+    B, nh, c = 1, 2, 64
+    C, Z, q, Bp, sk, _, W = _make(T + m2 + win, B, T, nh, c, m2)
+    kw = dict(m2=m2, sliding_window=win, scale=1.1)
+    ref = o_grad(C, Z, q, Bp, W, sink_logits=sk, **kw)
+    t = lambda x: torch.tensor(x, dtype=torch.float32, device=dev, requires_grad=True)  # noqa: E731
+    Ct, Zt, qt, Bt, st = t(C), t(Z), t(q), t(Bp), t(sk)
+    out = kch.hca_core(Ct, Zt, qt, Bt, sink_logits=st, **kw)
+    (out.double() * torch.tensor(W, device=dev)).sum().backward()
+    torch.cuda.synchronize()
+    for name, x in (("C", Ct), ("Z", Zt), ("q", qt), ("B_pos", Bt), ("sink_logits", st)):
+        _check(name, x.grad.cpu().numpy(), ref[name], 1e-4)

@@ -214,3 +214,29 @@ def test_no_grad_path_unchanged(dev):
                                  output_final_state=True)
     assert o2.grad_fn is not None
     assert torch.equal(o1, o2.detach()) and torch.equal(s1, s2.detach())
+
+
+@pytest.mark.parametrize("B,T,H,HV,K,V", [(1, 1, 1, 4, 32, 16), (2, 17, 2, 2, 16, 33)])
+def test_fp64_edge_shapes(dev, B, T, H, HV, K, V):
+    """One token; GVA with four value heads per key head; V not a multiple of
+    the 32-column slice; T not a multiple of the checkpoint segment."""
+    import kch
+    host, s0, w_o, w_s = _make(B + T + HV, B, T, H, HV, K, V)
+    ts, s0t = _leaves(host, s0, dev, torch.float64, torch.float64)
+    got = _hip_grads(kch.naive_recurrent_kda, ts, s0t, w_o, w_s)
+    _check(got, _ref(host, s0, w_o, w_s), 1e-10, label="edge")
+
+
+def test_empty_sequence_grad(dev):
+    """T = 0: zero gradients, and dS0 = dL/dS_T (the state passes through)."""
+    import kch
+    q = torch.zeros(1, 0, 1, 16, dtype=torch.float64, device=dev, requires_grad=True)
+    k = torch.zeros_like(q, requires_grad=True)
+    v = torch.zeros(1, 0, 1, 16, dtype=torch.float64, device=dev, requires_grad=True)
+    g = torch.zeros_like(q, requires_grad=True)
+    beta = torch.zeros(1, 0, 1, dtype=torch.float64, device=dev, requires_grad=True)
+    s0 = torch.randn(1, 1, 16, 16, dtype=torch.float64, device=dev, requires_grad=True)
+    o, s = kch.naive_recurrent_kda(q, k, v, g, beta, initial_state=s0, output_final_state=True)
+    w = torch.randn_like(s)
+    (s * w).sum().backward()
+    assert torch.equal(s0.grad, w)
