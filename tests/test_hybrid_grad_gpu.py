@@ -183,3 +183,29 @@ def test_hybrid_backward_produces_grads(dev):
         elif p.grad.abs().sum() == 0:
             zero.append(n)
     assert not missing and not bad and not zero, (missing, bad, zero)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_hybrid_training_reduces_loss(dev, dtype):
+    """A few optimizer steps on one batch through the HIP stack (KDA, CSA with
+    the STE, HCA, LayerNorms): the loss goes down and stays finite."""
+    import kch
+    torch.manual_seed(11)
+    cfg = kch.HybridConfig(d_model=64, n_heads_qk=2, n_heads_v=2, head_dim_k=32, head_dim_v=32,
+                           csa_m=4, csa_topk=8, csa_nh=2, csa_c=64, csa_dc=32, csa_nIh=2,
+                           csa_cI=32, csa_sliding_window=8, hca_m2=8, hca_nh=2, hca_c=64,
+                           hca_dc=32, hca_sliding_window=8, kda_chunk_size=64)
+    model = kch.HybridKCHAttention(cfg, total_layers=5).to(dev, dtype).train()
+    opt = torch.optim.AdamW(model.parameters(), lr=3e-3)
+    x = torch.randn(2, 128, 64, device=dev).to(dtype)
+    target = torch.randn(2, 128, 64, device=dev).to(dtype)
+    losses = []
+    for _ in range(6):
+        opt.zero_grad(set_to_none=True)
+        y, _, _ = model.forward_functional(x, None, [None] * model.n_kda_layers)
+        loss = (y.float() - target.float()).square().mean()
+        loss.backward()
+        opt.step()
+        losses.append(loss.item())
+    assert all(np.isfinite(losses)), losses
+    assert losses[-1] < losses[0], losses
