@@ -176,6 +176,24 @@ int kch_csa_attn_bwd(const float* q, const float* d_out, const float* kc, const 
                      float scale, int normalize, void* ws, size_t ws_bytes, void* stream);
 
 /*
+ * The STE surrogate's backward for the CSA indexer (ops_csa.py:1033-1099,
+ * ste_mode='topk_columns'; the soft weights of ops_csa.py:545-572 over the
+ * logits of ops_csa.py:503-536): given dsel [B,T,nb] (each selected slot's
+ * value from kch_csa_attn_bwd's slot_grad, scattered to its block, 0
+ * elsewhere), the indexer queries q_idx [B,T,nIh,cI], head weights w_idx
+ * [B,T,nIh], the compressed indexer keys kc / raw [B,nb,cI] (kch_compress of
+ * K_idx, Z_idx, B_idx; kc normalised when normalize), writes dq_idx, dw_idx,
+ * dK_idx, dZ_idx and the per-block dB_idx terms dBp [B,nb,m,cI]. fp32; cI in
+ * {64, 128}, nIh in {1, 2, 4, 8}, nIh * cI <= 512.
+ */
+size_t kch_csa_ste_bwd_ws_bytes(int B, int T, int nIh, int cI, int m);
+int kch_csa_ste_bwd(const float* q_idx, const float* w_idx, const float* kc, const float* raw,
+                    const float* K_idx, const float* Z_idx, const float* B_idx, const float* dsel,
+                    float* dq_idx, float* dw_idx, float* dK_idx, float* dZ_idx, float* dBp, int B,
+                    int T, int m, int nIh, int cI, float scale, int normalize, void* ws,
+                    size_t ws_bytes, void* stream);
+
+/*
  * Backward of the KDA layer's front end and of the stack's LayerNorm (the
  * autograd backward of ops_fused.py:480-581 and :42-60, exercised by the
  * hybrid gradient test run_correctness.py:2710-2830).

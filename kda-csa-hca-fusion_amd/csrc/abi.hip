@@ -360,6 +360,49 @@ int kch_csa_attn_bwd(const float* q, const float* d_out, const float* kc, const 
   return hip_status(fn, kch::hca_bwd_dispatch(p, ws, (hipStream_t)stream));
 }
 
+size_t kch_csa_ste_bwd_ws_bytes(int B, int T, int nIh, int cI, int m) {
+  if (B <= 0 || T <= 0 || m < 1 || T % m || (cI != 64 && cI != 128) || nIh < 1 || nIh * cI > 512)
+    return 0;
+  return kch::ste_bwd_ws_bytes(B, T, nIh, cI, m);
+}
+
+int kch_csa_ste_bwd(const float* q_idx, const float* w_idx, const float* kc, const float* raw,
+                    const float* K_idx, const float* Z_idx, const float* B_idx, const float* dsel,
+                    float* dq_idx, float* dw_idx, float* dK_idx, float* dZ_idx, float* dBp, int B,
+                    int T, int m, int nIh, int cI, float scale, int normalize, void* ws,
+                    size_t ws_bytes, void* stream) {
+  const char* fn = "kch_csa_ste_bwd";
+  if (B < 0 || T < 1 || m < 1 || nIh < 1)
+    return fail(KCH_ERR_INVALID, "%s: bad sizes B=%d T=%d m=%d nIh=%d (T >= 1)", fn, B, T, m, nIh);
+  if (T % m) return fail(KCH_ERR_INVALID, "%s: T=%d must be a multiple of m=%d", fn, T, m);
+  if ((cI != 64 && cI != 128) || (nIh != 1 && nIh != 2 && nIh != 4 && nIh != 8) || nIh * cI > 512)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: nIh=%d, cI=%d not supported (cI 64 / 128, nIh * cI <= 512)",
+                fn, nIh, cI);
+  if (std::isnan(scale)) return fail(KCH_ERR_INVALID, "%s: scale is NaN", fn);
+  if ((long long)B * T * (T / m) >= (1LL << 40)) return fail(KCH_ERR_UNSUPPORTED, "%s: too large", fn);
+  if (B == 0) return KCH_OK;
+  if (!q_idx || !w_idx || !kc || !raw || !K_idx || !Z_idx || !B_idx || !dsel || !dq_idx || !dw_idx ||
+      !dK_idx || !dZ_idx || !dBp)
+    return fail(KCH_ERR_INVALID, "%s: null tensor pointer", fn);
+  const size_t need = kch_csa_ste_bwd_ws_bytes(B, T, nIh, cI, m);
+  if (!ws || ws_bytes < need)
+    return fail(KCH_ERR_INVALID, "%s: workspace of %zu bytes required, got %zu", fn, need,
+                ws ? ws_bytes : (size_t)0);
+  if ((uintptr_t)ws & 255) return fail(KCH_ERR_INVALID, "%s: workspace must be 256-byte aligned", fn);
+  kch::SteBwdParams p;
+  p.qi = q_idx; p.w = w_idx; p.kc = kc; p.dsel = dsel; p.dqi = dq_idx; p.dw = dw_idx;
+  p.B = B; p.T = T; p.nb = T / m; p.m = m; p.nIh = nIh; p.cI = cI; p.normalize = normalize ? 1 : 0;
+  p.scale = scale;
+  kch::HcaBwdParams bp;
+  bp.q = nullptr; bp.dout = nullptr; bp.kc = kc; bp.raw = raw; bp.kl = nullptr; bp.lsrc = nullptr;
+  bp.C = K_idx; bp.Z = Z_idx; bp.Bpos = B_idx; bp.sink = nullptr;
+  bp.dq = nullptr; bp.dC = dK_idx; bp.dZ = dZ_idx; bp.dBp = dBp; bp.dlocal = nullptr;
+  bp.sink_part = nullptr;
+  bp.normalize = p.normalize;
+  bp.B = B; bp.T = T; bp.nh = 1; bp.c = cI; bp.m2 = m; bp.nb = T / m; bp.win = 0; bp.scale = scale;
+  return hip_status(fn, kch::ste_bwd_dispatch(p, bp, ws, (hipStream_t)stream));
+}
+
 int kch_kda_gates_bwd(const void* proj, long long ld_proj, const void* gl, long long ld_gl,
                       const void* dq, const void* dk, const void* dv, const void* dg,
                       const void* dbeta, void* dproj, void* dgl, int B, int T, int H, int HV, int K,

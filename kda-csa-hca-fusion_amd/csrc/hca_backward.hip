@@ -460,6 +460,192 @@ hipError_t launch_hca_bwd(const HcaBwdParams& p, const Plan& z, hipStream_t s) {
   return hipGetLastError();
 }
 
+// ---- the STE surrogate's backward (ops_csa.py:1033-1099, topk_columns) ----
+// soft = softmax over the visible blocks n of the indexer logits
+//   lg_n = sum_h w_h relu(a_hn),  a_hn = scale qn_h . k_n
+// (ops_csa.py:503-572); the selected columns of soft receive dsel (the slot
+// gradients, scattered densely: 0 off the selection). Backward:
+//   D = sum_n soft_n dsel_n,  dl_n = soft_n (dsel_n - D),
+//   dw_h = sum_n dl_n relu(a_hn),  dqn_h = sum_n dl_n w_h [a_hn > 0] scale k_n,
+//   dk_n = sum_t sum_h dl_tn w_th [a > 0] scale qn_th,
+// then the L2-norm and compression backwards of the indexer keys (the block
+// kernel above, single-branch). A wave holds one query's NIH heads: lane
+// (h = lane / LPH, lane % LPH) takes CPL consecutive channels, LPH = 64 / NIH.
+
+template <int W>
+__device__ __forceinline__ float xsum_from(float v) {  // over lanes W, 2W, .. 32 apart
+#pragma unroll
+  for (int o = W; o < 64; o <<= 1) v += __shfl_xor(v, o);
+  return v;
+}
+template <int L>
+__device__ __forceinline__ float xsum_below(float v) {  // within aligned groups of L lanes
+#pragma unroll
+  for (int o = 1; o < L; o <<= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+template <int NIH, int CPL>
+__global__ __launch_bounds__(256) void ste_bwd_query_kernel(SteBwdParams p) {
+  constexpr int LPH = 64 / NIH, CI = LPH * CPL;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const long long bt = (long long)blockIdx.x * 4 + wave;
+  if (bt >= (long long)p.B * p.T) return;  // whole waves only: shuffles stay within a wave
+  const int b = (int)(bt / p.T), t = (int)(bt % p.T);
+  const int h = lane / LPH, lc = lane % LPH;
+  float qn[CPL], k[CPL], dq[CPL];
+  const float* qrow = p.qi + ((size_t)bt * NIH + h) * CI + lc * CPL;
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < CPL; ++e) {
+    qn[e] = qrow[e];
+    ss += qn[e] * qn[e];
+    dq[e] = 0.f;
+  }
+  const float nrm = sqrtf(xsum_below<LPH>(ss));
+  const float rq = p.normalize ? 1.f / fmaxf(nrm, kEps) : 1.f;
+#pragma unroll
+  for (int e = 0; e < CPL; ++e) qn[e] *= rq;
+  const float wh = p.w[bt * NIH + h];
+  const int nvis = min((t + 1) / p.m, p.nb);
+  const float* dsel = p.dsel + (size_t)bt * p.nb;
+  auto logit = [&](int n, float& a) {
+    const float* kr = p.kc + ((size_t)b * p.nb + n) * CI + lc * CPL;
+    float d = 0.f;
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) {
+      k[e] = kr[e];
+      d += qn[e] * k[e];
+    }
+    a = xsum_below<LPH>(d) * p.scale;
+    // a and w_h are the same on every lane of a head group: the sum over the
+    // lanes LPH apart (one per head) gives every lane the logit
+    return xsum_from<LPH>(wh * fmaxf(a, 0.f));
+  };
+  float m = -INFINITY, l = 0.f, ad = 0.f;
+  for (int n = 0; n < nvis; ++n) {
+    float a;
+    const float lg = logit(n, a);
+    const float mn = fmaxf(m, lg);
+    const float sc = expf(m - mn), e1 = expf(lg - mn);
+    l = l * sc + e1;
+    ad = ad * sc + e1 * dsel[n];
+    m = mn;
+  }
+  const float lse = l > 0.f ? m + logf(l) : INFINITY;
+  const float D = l > 0.f ? ad / l : 0.f;
+  float dwh = 0.f;
+  for (int n = 0; n < nvis; ++n) {
+    float a;
+    const float lg = logit(n, a);
+    const float dl = expf(lg - lse) * (dsel[n] - D);
+    dwh += dl * fmaxf(a, 0.f);
+    const float coef = a > 0.f ? dl * wh * p.scale : 0.f;
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) dq[e] += coef * k[e];
+  }
+  // L2-norm backward of the query row
+  float yd = 0.f;
+#pragma unroll
+  for (int e = 0; e < CPL; ++e) yd += qn[e] * dq[e];
+  yd = xsum_below<LPH>(yd);
+  float* dst = p.dqi + ((size_t)bt * NIH + h) * CI + lc * CPL;
+#pragma unroll
+  for (int e = 0; e < CPL; ++e)
+    dst[e] = p.normalize ? (nrm > kEps ? dq[e] - qn[e] * yd : dq[e]) * rq : dq[e];
+  if (lc == 0) {
+    p.dw[bt * NIH + h] = dwh;
+    p.rq[bt * NIH + h] = rq;
+  }
+  if (lane == 0) {
+    p.lse[bt] = lse;
+    p.dval[bt] = D;
+  }
+}
+
+template <int NIH, int CPL>
+__global__ __launch_bounds__(256) void ste_bwd_key_kernel(SteBwdParams p, int nchunk, int ntile) {
+  constexpr int LPH = 64 / NIH, CI = LPH * CPL;
+  __shared__ float red[4][NBT][CI];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int h = lane / LPH, lc = lane % LPH;
+  const int b = blockIdx.y;
+  const int tile = blockIdx.x / nchunk, ci = blockIdx.x % nchunk;
+  const int r0 = tile * NBT;
+  const int tlo = (r0 + 1) * p.m - 1 + ci * QC;
+  const int thi = min(p.T, tlo + QC);
+  float* out = p.part + (((size_t)b * ntile + tile) * nchunk + ci) * NBT * CI;
+  if (tlo >= thi) {
+    for (int i = threadIdx.x; i < NBT * CI; i += 256) out[i] = 0.f;
+    return;
+  }
+  float k[NBT][CPL], acc[NBT][CPL];
+#pragma unroll
+  for (int i = 0; i < NBT; ++i)
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) {
+      k[i][e] = r0 + i < p.nb ? p.kc[((size_t)b * p.nb + r0 + i) * CI + lc * CPL + e] : 0.f;
+      acc[i][e] = 0.f;
+    }
+  for (int t = tlo + wave; t < thi; t += 4) {
+    const size_t bt = (size_t)b * p.T + t;
+    const float rq = p.rq[bt * NIH + h], wh = p.w[bt * NIH + h];
+    const float lse = p.lse[bt], D = p.dval[bt];
+    float qn[CPL];
+    const float* qrow = p.qi + (bt * NIH + h) * CI + lc * CPL;
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) qn[e] = qrow[e] * rq;
+#pragma unroll
+    for (int i = 0; i < NBT; ++i) {
+      const int n = r0 + i;
+      const bool valid = n < p.nb && t >= (n + 1) * p.m - 1;
+      float d = 0.f;
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) d += qn[e] * k[i][e];
+      const float a = xsum_below<LPH>(d) * p.scale;
+      const float lg = xsum_from<LPH>(wh * fmaxf(a, 0.f));
+      const float ds = valid ? p.dsel[bt * p.nb + n] : 0.f;
+      const float dl = valid ? expf(lg - lse) * (ds - D) : 0.f;
+      const float coef = a > 0.f ? dl * wh * p.scale : 0.f;
+#pragma unroll
+      for (int e = 0; e < CPL; ++e) acc[i][e] += coef * qn[e];
+    }
+  }
+  // the heads' sums (lanes LPH apart), then the four waves'
+#pragma unroll
+  for (int i = 0; i < NBT; ++i)
+#pragma unroll
+    for (int e = 0; e < CPL; ++e) {
+      const float v = xsum_from<LPH>(acc[i][e]);
+      if (h == 0) red[wave][i][lc * CPL + e] = v;
+    }
+  __syncthreads();
+  for (int o = threadIdx.x; o < NBT * CI; o += 256) {
+    const int i = o / CI, c = o % CI;
+    out[o] = red[0][i][c] + red[1][i][c] + red[2][i][c] + red[3][i][c];
+  }
+}
+
+template <int NIH, int CPL>
+hipError_t launch_ste(SteBwdParams p, const Plan& z, HcaBwdParams bp, hipStream_t s) {
+  const unsigned rows = (unsigned)(((long long)p.B * p.T + 3) / 4);
+  hipLaunchKernelGGL((ste_bwd_query_kernel<NIH, CPL>), dim3(rows), dim3(256), 0, s, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (p.nb == 0) return hipSuccess;
+  hipLaunchKernelGGL((ste_bwd_key_kernel<NIH, CPL>), dim3(z.ntile_b * z.nchunk_b, p.B), dim3(256), 0, s,
+                     p, z.nchunk_b, z.ntile_b);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  // compression and L2-norm backward of the indexer keys
+  if (p.cI == 64)
+    hipLaunchKernelGGL((hca_bwd_block_kernel<64>), dim3(p.nb, p.B), dim3(64), 0, s, bp, z.nchunk_b, z.ntile_b);
+  else
+    hipLaunchKernelGGL((hca_bwd_block_kernel<128>), dim3(p.nb, p.B), dim3(128), 0, s, bp, z.nchunk_b,
+                       z.ntile_b);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 size_t hca_bwd_ws_bytes(int B, int T, int nh, int c, int m2, int win, int topk) {
@@ -486,6 +672,30 @@ hipError_t hca_bwd_dispatch(HcaBwdParams p, void* ws, hipStream_t stream) {
     p.sel = sel;
   }
   return p.c == 64 ? launch_hca_bwd<64>(p, z, stream) : launch_hca_bwd<128>(p, z, stream);
+}
+
+size_t ste_bwd_ws_bytes(int B, int T, int nIh, int cI, int m) {
+  const Plan z = plan(B, T, T / m, 0, cI);
+  return 2 * al256((size_t)B * T * 4) + al256((size_t)B * T * nIh * 4) + al256(z.part_b * 4);
+}
+
+hipError_t ste_bwd_dispatch(SteBwdParams p, HcaBwdParams bp, void* ws, hipStream_t stream) {
+  const Plan z = plan(p.B, p.T, p.nb, 0, p.cI);
+  char* w = static_cast<char*>(ws);
+  const size_t per = al256((size_t)p.B * p.T * 4);
+  p.lse = reinterpret_cast<float*>(w);
+  p.dval = reinterpret_cast<float*>(w + per);
+  p.rq = reinterpret_cast<float*>(w + 2 * per);
+  p.part = reinterpret_cast<float*>(w + 2 * per + al256((size_t)p.B * p.T * p.nIh * 4));
+  bp.part_b = p.part;
+  const int cpl = p.cI * p.nIh / 64;
+#define KCH_STE(NIH, CPL) \
+  if (p.nIh == NIH && cpl == CPL) return launch_ste<NIH, CPL>(p, z, bp, stream);
+  // nIh * cI <= 512 (one wave per query), cI in {64, 128}
+  KCH_STE(1, 1) KCH_STE(1, 2) KCH_STE(2, 2) KCH_STE(2, 4) KCH_STE(4, 4) KCH_STE(4, 8)
+  KCH_STE(8, 8)
+#undef KCH_STE
+  return hipErrorInvalidValue;
 }
 
 }  // namespace kch

@@ -98,6 +98,26 @@ struct HcaBwdParams {
   float scale;
 };
 size_t hca_bwd_ws_bytes(int B, int T, int nh, int c, int m2, int win, int topk);
+
+// The STE surrogate's backward for the indexer (hca_backward.hip): fp32,
+// cI in {64, 128}, nIh in {1, 2, 4, 8}, nIh * cI <= 512.
+struct SteBwdParams {
+  const float* qi;    // [B,T,nIh,cI] indexer queries as given
+  const float* w;     // [B,T,nIh] head weights
+  const float* kc;    // [B,nb,cI] compressed indexer keys (L2-normalised when normalize)
+  const float* dsel;  // [B,T,nb] the slot gradients at the selected blocks, 0 elsewhere
+  float* dqi;         // [B,T,nIh,cI]
+  float* dw;          // [B,T,nIh]
+  float* part = nullptr;  // workspace regions, set by ste_bwd_dispatch
+  float* lse = nullptr;
+  float* dval = nullptr;
+  float* rq = nullptr;
+  int B, T, nb, m, nIh, cI, normalize;
+  float scale;
+};
+size_t ste_bwd_ws_bytes(int B, int T, int nIh, int cI, int m);
+// bp: the key compression's inputs and outputs for the block kernel
+hipError_t ste_bwd_dispatch(SteBwdParams p, HcaBwdParams bp, void* ws, hipStream_t stream);
 hipError_t hca_bwd_dispatch(HcaBwdParams p, void* ws, hipStream_t stream);
 
 hipError_t kda_chunk_dispatch(const KdaParams& p, int dtype, hipStream_t stream);

@@ -38,6 +38,7 @@ _SIGNATURES = {
     "kch_hca_attn_bwd": [_P] * 16 + [_I] * 6 + [_F, _P, _SZ, _P],
     "kch_csa_attn_bwd": [_P] * 23 + [_I] * 7 + [_F, _I, _P, _SZ, _P],
     "kch_kda_gates_bwd": [_P, _L, _P, _L] + [_P] * 7 + [_I] * 6 + [_F, _I, _P],
+    "kch_csa_ste_bwd": [_P] * 13 + [_I] * 5 + [_F, _I, _P, _SZ, _P],
     "kch_short_conv_bwd": [_P] * 7 + [_I] * 4 + [_P],
     "kch_layer_norm_bwd": [_P] * 6 + [_L, _I, _F, _I, _I, _P],
     "kch_compress": [_P, _L, _P, _L, _P, _P, _P, _I, _I, _P, _I, _I, _I, _I, _I, _P],
@@ -78,6 +79,7 @@ _QUERIES = {
     "kch_kda_recurrent_bwd_ws_bytes": (_SZ, [_I] * 6),
     "kch_hca_attn_bwd_ws_bytes": (_SZ, [_I] * 6),
     "kch_csa_attn_bwd_ws_bytes": (_SZ, [_I] * 7),
+    "kch_csa_ste_bwd_ws_bytes": (_SZ, [_I] * 5),
     "kch_decode_ws_bytes": (_SZ, [_I] * 7),
     "kch_decode_dyn_ws_bytes": (_SZ, [_I] * 7),
 }

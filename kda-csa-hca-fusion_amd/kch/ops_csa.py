@@ -530,9 +530,57 @@ def _ste_indexer_grads(K_idx, Z_idx, q_idx, w_idx, B_idx, idx, slot, *, m, norma
     """The straight-through surrogate's gradients for the indexer inputs
     (``ops_csa.py:1033-1099``, ``topk_columns``): the selected columns of the
     soft weights (``softmax`` over every causal block of the indexer logits,
-    ``ops_csa.py:545-572``) receive ``slot``; autograd carries that through
-    the logits (``ops_csa.py:503-536``) and the key compression
-    (``ops_csa.py:198-234``). Dense over the blocks, written with torch
+    ``ops_csa.py:545-572``) receive ``slot``, carried through the logits
+    (``ops_csa.py:503-536``) and the key compression (``ops_csa.py:198-234``).
+    On ``kch_csa_ste_bwd`` when the padded ``nIh * c_I <= 512`` (a wave per
+    query); beyond that, ``_ste_indexer_grads_dense``."""
+    B_, T, cI = K_idx.shape
+    nIh = q_idx.shape[2]
+    cIp = 64 if cI <= 64 else 128
+    nIp = next((n for n in (1, 2, 4, 8) if n >= nIh), None)
+    if cI > 128 or nIp is None or nIp * cIp > 512:
+        return _ste_indexer_grads_dense(K_idx, Z_idx, q_idx, w_idx, B_idx, idx, slot, m=m,
+                                        normalize_qk=normalize_qk)
+    fn = "csa_ste_grad"
+    dev = K_idx.device
+    f32 = torch.float32
+    nb = T // m
+
+    def prep(x, n):
+        x = x.detach().to(device=dev, dtype=f32)
+        return (_pad_last(x, n) if x.shape[-1] != n else x).contiguous()
+
+    Kf, Zf = prep(K_idx, cIp), prep(Z_idx, cIp)
+    Bf = prep(B_idx, cIp)
+    qf = F.pad(q_idx.detach().to(f32), (0, cIp - cI, 0, nIp - nIh)).contiguous()
+    wf = prep(w_idx, nIp)
+    kc = torch.empty(B_, nb, cIp, device=dev, dtype=f32)
+    raw = _compress(fn, Kf, Zf, Bf, m, out_raw=True, key=kc, normalize=bool(normalize_qk))
+    if not normalize_qk:
+        kc = raw
+    idx64 = idx.long()
+    dsel = torch.zeros(B_, T, nb, device=dev, dtype=f32).scatter_add_(
+        -1, idx64.clamp(min=0), slot.to(f32) * (idx64 >= 0).to(f32))
+    scale = 1.0 if normalize_qk else cI ** -0.5
+    dq = torch.empty_like(qf)
+    dw = torch.empty_like(wf)
+    dK = torch.zeros(B_, T, cIp, device=dev, dtype=f32)
+    dZ = torch.zeros_like(dK)
+    dBp = torch.empty(B_, nb, m, cIp, device=dev, dtype=f32)
+    nbytes = _lib.load().kch_csa_ste_bwd_ws_bytes(B_, T, nIp, cIp, m)
+    ws = torch.empty(max(nbytes, 1), device=dev, dtype=torch.uint8)
+    _lib.call("kch_csa_ste_bwd", _lib.ptr(qf), _lib.ptr(wf), _lib.ptr(kc), _lib.ptr(raw),
+              _lib.ptr(Kf), _lib.ptr(Zf), _lib.ptr(Bf), _lib.ptr(dsel), _lib.ptr(dq), _lib.ptr(dw),
+              _lib.ptr(dK), _lib.ptr(dZ), _lib.ptr(dBp), B_, T, m, nIp, cIp, float(scale),
+              int(bool(normalize_qk)), _lib.ptr(ws), nbytes, _lib.stream_of(qf))
+    return [dK[..., :cI].to(K_idx.dtype), dZ[..., :cI].to(Z_idx.dtype),
+            dq[:, :, :nIh, :cI].to(q_idx.dtype), dw[..., :nIh].to(w_idx.dtype),
+            dBp.sum(dim=(0, 1))[:, :cI].to(B_idx.dtype)]
+
+
+def _ste_indexer_grads_dense(K_idx, Z_idx, q_idx, w_idx, B_idx, idx, slot, *, m, normalize_qk):
+    """The same gradients for indexers wider than one wave per query
+    (``nIh * c_I > 512`` after padding), dense over the blocks with torch
     operations."""
     leaves = [x.detach().requires_grad_(True) if x is not None else None
               for x in (K_idx, Z_idx, q_idx, w_idx, B_idx)]

@@ -232,3 +232,29 @@ def test_attn_grad_sparse_edges(dev, topk, win):
     torch.cuda.synchronize()
     for name in ("Ca", "Cb", "Za", "Zb", "q", "Ba", "Bb", "sink_logits"):
         _check(name, g[name].cpu().numpy(), ref[name])
+
+
+@pytest.mark.parametrize("nIh,cI,norm", [(4, 64, True), (4, 64, False), (2, 32, True),
+                                         (1, 128, False), (8, 64, True), (3, 48, False)])
+def test_ste_kernel_matches_dense_statement(dev, nIh, cI, norm):
+    """``kch_csa_ste_bwd`` against the dense torch statement of the same
+    surrogate (softmax over every causal block, autograd through the logits
+    and the key compression), on a selection with -1 slots; fp32, 1e-4 of each
+    tensor's largest gradient. Covers padded heads (3 -> 4) and channels
+    (32 -> 64, 48 -> 64)."""
+    from kch.ops_csa import _ste_indexer_grads, _ste_indexer_grads_dense
+    rng = np.random.default_rng(nIh * cI + norm)
+    B, T, m, topk = 2, 256, 4, 16
+    t = lambda x: torch.tensor(x, dtype=torch.float32, device=dev)  # noqa: E731
+    K = t(rng.standard_normal((B, T, cI)))
+    Z = t(rng.standard_normal((B, T, cI)))
+    q = t(rng.standard_normal((B, T, nIh, cI)))
+    w = t(rng.standard_normal((B, T, nIh)))
+    Bi = t(rng.standard_normal((m, cI)) * 0.3)
+    idx = torch.tensor(_selection(rng, B, T, m, topk, hole=100), device=dev)
+    slot = t(rng.standard_normal((B, T, topk))) * (idx >= 0)
+    got = _ste_indexer_grads(K, Z, q, w, Bi, idx, slot, m=m, normalize_qk=norm)
+    ref = _ste_indexer_grads_dense(K, Z, q, w, Bi, idx, slot, m=m, normalize_qk=norm)
+    torch.cuda.synchronize()
+    for name, a, r in zip(("K_idx", "Z_idx", "q_idx", "w_idx", "B_idx"), got, ref):
+        _check(name, a.cpu().numpy(), r.cpu().numpy())
