@@ -14,10 +14,14 @@
 // The columns of the state are independent in both directions; only dq^,
 // dk, dg and dbeta sum over columns.
 //
-// kda_recurrent_bwd_kernel  one workgroup per (b, hv, 32-column slice of V);
-//   lane l of wave w owns rows (l / 8) + 8 i of column 8 w + l % 8: the sums
-//   over columns, three K-vectors per token, are then DPP steps within 8-lane
-//   groups, and only the two per-column sums over rows cross rows of lanes. Pass 1 runs the recurrence forward and stores
+// kda_recurrent_bwd_kernel  one workgroup per (b, hv, slice of V): with PH
+//   row phases per column, lane l of wave w owns rows (l / CW) + PH i of
+//   column CW w + l % CW (CW = 64 / PH; slices of 4 CW columns). The sums over
+//   columns, three K-vectors per token, are DPP steps within CW-lane groups;
+//   the two per-column sums over rows are row rotations plus permlane swaps.
+//   PH = 8 (32-column slices) when the grid has a workgroup for every CU;
+//   PH = 16 (16-column slices: half the rows per thread, twice the
+//   workgroups) for smaller grids, whose per-token chain is the bound. Pass 1 runs the recurrence forward and stores
 //   the state at the start of every segment of SEG tokens (a checkpoint in the
 //   workspace). Pass 2 walks the segments in reverse: it reloads the
 //   checkpoint, recomputes the segment's decayed states Sd into registers,
@@ -90,17 +94,23 @@ __device__ __forceinline__ double swap_acc(double v) {
 }
 
 // tokens per checkpoint segment: the segment's decayed states stay in
-// registers (SEG * K / 8 values per thread, at most 128 VGPRs)
-template <int K, typename AccT>
+// registers (SEG * K / PH values per thread, at most 128 VGPRs), and the
+// segment's rows and per-token column sums (15 K values a token) in 64 KB of
+// LDS; at most 8
+template <int K, typename AccT, int PH>
 constexpr int seg_len() {
-  constexpr int per_tok = K / 8 * (int)(sizeof(AccT) / 4);
-  return 128 / per_tok > 16 ? 16 : 128 / per_tok;
+  constexpr int per_tok = K / PH * (int)(sizeof(AccT) / 4);
+  constexpr int by_regs = 128 / per_tok;
+  constexpr int by_lds = 65536 / (15 * K * (int)sizeof(AccT));
+  constexpr int s = by_regs < by_lds ? by_regs : by_lds;
+  return s > 8 ? 8 : s;
 }
 
-template <int K, typename InT, typename AccT>
+template <int K, typename InT, typename AccT, int kPh>
 __global__ __launch_bounds__(256) void kda_recurrent_bwd_kernel(KdaBwdParams p) {
-  constexpr int RPT = K / 8;
-  constexpr int SEG = seg_len<K, AccT>();
+  constexpr int kCw = 64 / kPh, kCols = 4 * kCw;
+  constexpr int RPT = K / kPh;
+  constexpr int SEG = seg_len<K, AccT, kPh>();
   constexpr int PS = 3 * K + 1;  // partial record: dq^ [K] | dk [K] | dg [K] | dbeta
   constexpr bool F64 = sizeof(AccT) == 8;
   __shared__ AccT sq[SEG][K], sk[SEG][K], sa[SEG][K], sb[SEG];
@@ -108,12 +118,12 @@ __global__ __launch_bounds__(256) void kda_recurrent_bwd_kernel(KdaBwdParams p) 
   __shared__ AccT sbw[SEG][4];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int nvs = (p.V + 31) / 32;
+  const int nvs = (p.V + kCols - 1) / kCols;
   const int vs = blockIdx.x % nvs;
   const int bh = blockIdx.x / nvs;
   const int hv = bh % p.HV, b = bh / p.HV, h = hv / (p.HV / p.H);
-  const int cl = wave * 8 + (lane & 7), ph = lane >> 3;
-  const int col = vs * 32 + cl;
+  const int cl = wave * kCw + (lane % kCw), ph = lane / kCw;
+  const int col = vs * kCols + cl;
   const bool okc = col < p.V;
   const int T = p.T;
   const int nseg = (T + SEG - 1) / SEG;
@@ -126,23 +136,25 @@ __global__ __launch_bounds__(256) void kda_recurrent_bwd_kernel(KdaBwdParams p) 
   const AccT* s0 = static_cast<const AccT*>(p.s0);
   const AccT* dsT = static_cast<const AccT*>(p.ds_final);
   AccT* ds0 = static_cast<AccT*>(p.ds0);
-  AccT* ck = static_cast<AccT*>(p.ck) + (size_t)blockIdx.x * nseg * K * 32;
+  AccT* ck = static_cast<AccT*>(p.ck) + (size_t)blockIdx.x * nseg * K * kCols;
   AccT* part = static_cast<AccT*>(p.part);
   const AccT scale = (AccT)p.scale;
   const AccT clampv = (AccT)p.g_clamp_min;
   const bool do_clamp = p.g_clamp_min > -INFINITY;
   const size_t sbase = (size_t)(b * p.HV + hv) * K * p.V;
 
-  auto red8 = [](AccT x) {  // over the 8 phases of a column (lanes 8 apart)
-    x += dpp_acc<0x128>(x);  // row_ror:8, the other half of the 16-lane row
+  auto red8 = [](AccT x) {  // over the phases of a column (lanes CW apart)
+    // row_ror by CW (and 8): the lanes of the 16-lane row sharing the column
+    if constexpr (kCw == 4) x += dpp_acc<0x124>(x);
+    x += dpp_acc<0x128>(x);
     x += swap_acc<16>(x);
     x += swap_acc<32>(x);
     return x;
   };
-  auto colsum = [](AccT x) {  // over the 8 columns of a wave (8-lane groups)
+  auto colsum = [](AccT x) {  // over the CW columns of a wave (CW-lane groups)
     x += dpp_acc<0xB1>(x);   // quad_perm [1,0,3,2]
     x += dpp_acc<0x4E>(x);   // quad_perm [2,3,0,1]
-    x += dpp_acc<0x141>(x);  // row_half_mirror: the other quad of the group
+    if constexpr (kCw == 8) x += dpp_acc<0x141>(x);  // row_half_mirror: the other quad
     return x;
   };
   // the segment's key, decay and beta rows (and scaled q) into LDS
@@ -169,11 +181,11 @@ __global__ __launch_bounds__(256) void kda_recurrent_bwd_kernel(KdaBwdParams p) 
   AccT S[RPT];
 #pragma unroll
   for (int i = 0; i < RPT; ++i)
-    S[i] = (s0 && okc) ? s0[sbase + (size_t)(ph + 8 * i) * p.V + col] : (AccT)0;
+    S[i] = (s0 && okc) ? s0[sbase + (size_t)(ph + kPh * i) * p.V + col] : (AccT)0;
   for (int s = 0; s < nseg; ++s) {
     const int t0 = s * SEG, len = min(SEG, T - t0);
 #pragma unroll
-    for (int i = 0; i < RPT; ++i) ck[((size_t)s * K + ph + 8 * i) * 32 + cl] = S[i];
+    for (int i = 0; i < RPT; ++i) ck[((size_t)s * K + ph + kPh * i) * kCols + cl] = S[i];
     __syncthreads();  // the previous segment's LDS rows are consumed
     load_seg(t0, len, false);
     AccT vv[SEG];
@@ -186,13 +198,13 @@ __global__ __launch_bounds__(256) void kda_recurrent_bwd_kernel(KdaBwdParams p) 
         AccT kS = 0;
 #pragma unroll
         for (int i = 0; i < RPT; ++i) {
-          S[i] *= sa[j][ph + 8 * i];
-          kS += sk[j][ph + 8 * i] * S[i];
+          S[i] *= sa[j][ph + kPh * i];
+          kS += sk[j][ph + kPh * i] * S[i];
         }
         kS = red8(kS);
         const AccT d = sb[j] * (vv[j] - kS);
 #pragma unroll
-        for (int i = 0; i < RPT; ++i) S[i] += sk[j][ph + 8 * i] * d;
+        for (int i = 0; i < RPT; ++i) S[i] += sk[j][ph + kPh * i] * d;
       }
     }
   }
@@ -203,7 +215,7 @@ __global__ __launch_bounds__(256) void kda_recurrent_bwd_kernel(KdaBwdParams p) 
   AccT dS[RPT];
 #pragma unroll
   for (int i = 0; i < RPT; ++i)
-    dS[i] = (dsT && okc) ? dsT[sbase + (size_t)(ph + 8 * i) * p.V + col] : (AccT)0;
+    dS[i] = (dsT && okc) ? dsT[sbase + (size_t)(ph + kPh * i) * p.V + col] : (AccT)0;
   InT* gdv = static_cast<InT*>(p.dv);
   for (int s = nseg - 1; s >= 0; --s) {
     const int t0 = s * SEG, len = min(SEG, T - t0);
@@ -216,7 +228,7 @@ __global__ __launch_bounds__(256) void kda_recurrent_bwd_kernel(KdaBwdParams p) 
       dov[j] = j < len ? col_val(gdo, t0 + j) : (AccT)0;
     }
 #pragma unroll
-    for (int i = 0; i < RPT; ++i) S[i] = ck[((size_t)s * K + ph + 8 * i) * 32 + cl];
+    for (int i = 0; i < RPT; ++i) S[i] = ck[((size_t)s * K + ph + kPh * i) * kCols + cl];
     __syncthreads();
     // recompute: Sd of every token of the segment, and u
     AccT Sd[SEG][RPT];
@@ -227,15 +239,15 @@ __global__ __launch_bounds__(256) void kda_recurrent_bwd_kernel(KdaBwdParams p) 
         AccT kS = 0;
 #pragma unroll
         for (int i = 0; i < RPT; ++i) {
-          S[i] *= sa[j][ph + 8 * i];
+          S[i] *= sa[j][ph + kPh * i];
           Sd[j][i] = S[i];
-          kS += sk[j][ph + 8 * i] * S[i];
+          kS += sk[j][ph + kPh * i] * S[i];
         }
         kS = red8(kS);
         uu[j] = vv[j] - kS;
         const AccT d = sb[j] * uu[j];
 #pragma unroll
-        for (int i = 0; i < RPT; ++i) S[i] += sk[j][ph + 8 * i] * d;
+        for (int i = 0; i < RPT; ++i) S[i] += sk[j][ph + kPh * i] * d;
       }
     }
     // the token backward, last token first
@@ -247,8 +259,8 @@ __global__ __launch_bounds__(256) void kda_recurrent_bwd_kernel(KdaBwdParams p) 
         AccT dd = 0;
 #pragma unroll
         for (int i = 0; i < RPT; ++i) {
-          dS[i] += sq[j][ph + 8 * i] * dov[j];  // now dSt
-          dd += dS[i] * sk[j][ph + 8 * i];
+          dS[i] += sq[j][ph + kPh * i] * dov[j];  // now dSt
+          dd += dS[i] * sk[j][ph + kPh * i];
         }
         dd = red8(dd);
         const AccT du = sb[j] * dd;
@@ -257,16 +269,16 @@ __global__ __launch_bounds__(256) void kda_recurrent_bwd_kernel(KdaBwdParams p) 
         // each row's column sums go to LDS as soon as they are formed
 #pragma unroll
         for (int i = 0; i < RPT; ++i) {
-          const AccT kr = sk[j][ph + 8 * i];
+          const AccT kr = sk[j][ph + kPh * i];
           const AccT P = colsum((Sd[j][i] + kr * d) * dov[j]);
           const AccT Dk = colsum(dS[i] * d - Sd[j][i] * du);
           const AccT dSd = dS[i] - kr * du;
           const AccT Gv = colsum(dSd * Sd[j][i]);
-          dS[i] = sa[j][ph + 8 * i] * dSd;
-          if ((lane & 7) == 0) {
-            sw[j][wave][0][ph + 8 * i] = P;
-            sw[j][wave][1][ph + 8 * i] = Dk;
-            sw[j][wave][2][ph + 8 * i] = Gv;
+          dS[i] = sa[j][ph + kPh * i] * dSd;
+          if (lane % kCw == 0) {
+            sw[j][wave][0][ph + kPh * i] = P;
+            sw[j][wave][1][ph + kPh * i] = Dk;
+            sw[j][wave][2][ph + kPh * i] = Gv;
           }
         }
         const AccT cb = colsum(ph == 0 ? dd * uu[j] : (AccT)0);
@@ -289,14 +301,14 @@ __global__ __launch_bounds__(256) void kda_recurrent_bwd_kernel(KdaBwdParams p) 
   }
   if (ds0 && okc) {
 #pragma unroll
-    for (int i = 0; i < RPT; ++i) ds0[sbase + (size_t)(ph + 8 * i) * p.V + col] = dS[i];
+    for (int i = 0; i < RPT; ++i) ds0[sbase + (size_t)(ph + kPh * i) * p.V + col] = dS[i];
   }
 }
 
 template <typename InT, typename AccT>
-__global__ __launch_bounds__(256) void kda_bwd_reduce_kernel(KdaBwdParams p) {
+__global__ __launch_bounds__(256) void kda_bwd_reduce_kernel(KdaBwdParams p, int cols) {
   const int K = p.K, PS = 3 * K + 1;
-  const int nvs = (p.V + 31) / 32;
+  const int nvs = (p.V + cols - 1) / cols;
   const int G = p.HV / p.H;
   const int h = blockIdx.x % p.H;
   const size_t bt = blockIdx.x / p.H;  // b * T + t
@@ -333,44 +345,59 @@ __global__ __launch_bounds__(256) void kda_bwd_reduce_kernel(KdaBwdParams p) {
 }
 
 template <int K, typename InT, typename AccT>
-hipError_t launch_bwd(const KdaBwdParams& p, hipStream_t s) {
-  const int nvs = (p.V + 31) / 32;
-  hipLaunchKernelGGL((kda_recurrent_bwd_kernel<K, InT, AccT>), dim3(p.B * p.HV * nvs), dim3(256), 0, s,
-                     p);
+hipError_t launch_bwd(const KdaBwdParams& p, int ph, hipStream_t s) {
+  const int cols = 4 * (64 / ph);
+  const int nvs = (p.V + cols - 1) / cols;
+  if (ph == 16)
+    hipLaunchKernelGGL((kda_recurrent_bwd_kernel<K, InT, AccT, 16>), dim3(p.B * p.HV * nvs), dim3(256), 0,
+                       s, p);
+  else
+    hipLaunchKernelGGL((kda_recurrent_bwd_kernel<K, InT, AccT, 8>), dim3(p.B * p.HV * nvs), dim3(256), 0,
+                       s, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int threads = K <= 64 ? 64 : (K <= 128 ? 128 : 256);
   hipLaunchKernelGGL((kda_bwd_reduce_kernel<InT, AccT>), dim3((unsigned)((size_t)p.B * p.T * p.H)),
-                     dim3(threads), 0, s, p);
+                     dim3(threads), 0, s, p, cols);
   return hipGetLastError();
 }
 
 template <typename InT, typename AccT>
-hipError_t bwd_by_k(const KdaBwdParams& p, hipStream_t s) {
+hipError_t bwd_by_k(const KdaBwdParams& p, int ph, hipStream_t s) {
   switch (p.K) {
-    case 16: return launch_bwd<16, InT, AccT>(p, s);
-    case 32: return launch_bwd<32, InT, AccT>(p, s);
-    case 64: return launch_bwd<64, InT, AccT>(p, s);
-    case 128: return launch_bwd<128, InT, AccT>(p, s);
-    default: return launch_bwd<256, InT, AccT>(p, s);
+    case 16: return launch_bwd<16, InT, AccT>(p, ph, s);
+    case 32: return launch_bwd<32, InT, AccT>(p, ph, s);
+    case 64: return launch_bwd<64, InT, AccT>(p, ph, s);
+    case 128: return launch_bwd<128, InT, AccT>(p, ph, s);
+    default: return launch_bwd<256, InT, AccT>(p, ph, s);
   }
 }
 
 template <int K, typename AccT>
-size_t ck_bytes(int B, int T, int HV, int V) {
-  constexpr int SEG = seg_len<K, AccT>();
-  return (size_t)B * HV * ((V + 31) / 32) * ((T + SEG - 1) / SEG) * K * 32 * sizeof(AccT);
+size_t ck_bytes(int B, int T, int HV, int V, int ph) {
+  const int seg = ph == 16 ? seg_len<K, AccT, 16>() : seg_len<K, AccT, 8>();
+  const int cols = 4 * (64 / ph);
+  return (size_t)B * HV * ((V + cols - 1) / cols) * ((T + seg - 1) / seg) * K * cols * sizeof(AccT);
 }
 
 template <typename AccT>
-size_t ck_bytes_by_k(int B, int T, int HV, int K, int V) {
+size_t ck_bytes_by_k(int B, int T, int HV, int K, int V, int ph) {
   switch (K) {
-    case 16: return ck_bytes<16, AccT>(B, T, HV, V);
-    case 32: return ck_bytes<32, AccT>(B, T, HV, V);
-    case 64: return ck_bytes<64, AccT>(B, T, HV, V);
-    case 128: return ck_bytes<128, AccT>(B, T, HV, V);
-    default: return ck_bytes<256, AccT>(B, T, HV, V);
+    case 16: return ck_bytes<16, AccT>(B, T, HV, V, ph);
+    case 32: return ck_bytes<32, AccT>(B, T, HV, V, ph);
+    case 64: return ck_bytes<64, AccT>(B, T, HV, V, ph);
+    case 128: return ck_bytes<128, AccT>(B, T, HV, V, ph);
+    default: return ck_bytes<256, AccT>(B, T, HV, V, ph);
   }
+}
+
+// 16 phases (16-column slices) when 32-column slices would leave CUs idle
+int phases(int B, int HV, int V) {
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  return (long long)B * HV * ((V + 31) / 32) < cus ? 16 : 8;
 }
 
 size_t al256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -378,22 +405,25 @@ size_t al256(size_t x) { return (x + 255) & ~size_t(255); }
 }  // namespace
 
 size_t kda_bwd_ws_bytes(int B, int T, int HV, int K, int V, bool f64) {
+  const int ph = phases(B, HV, V);
+  const int cols = 4 * (64 / ph);
   const size_t acc = f64 ? 8 : 4;
-  const size_t ck = f64 ? ck_bytes_by_k<double>(B, T, HV, K, V) : ck_bytes_by_k<float>(B, T, HV, K, V);
-  const size_t part = (size_t)B * T * HV * ((V + 31) / 32) * (3 * K + 1) * acc;
+  const size_t ck = f64 ? ck_bytes_by_k<double>(B, T, HV, K, V, ph) : ck_bytes_by_k<float>(B, T, HV, K, V, ph);
+  const size_t part = (size_t)B * T * HV * ((V + cols - 1) / cols) * (3 * K + 1) * acc;
   return al256(ck) + al256(part);
 }
 
 hipError_t kda_bwd_dispatch(KdaBwdParams p, int dtype, void* ws, hipStream_t stream) {
   const bool f64 = dtype == DT_F64;
-  const size_t ck = f64 ? ck_bytes_by_k<double>(p.B, p.T, p.HV, p.K, p.V)
-                        : ck_bytes_by_k<float>(p.B, p.T, p.HV, p.K, p.V);
+  const int ph = phases(p.B, p.HV, p.V);
+  const size_t ck = f64 ? ck_bytes_by_k<double>(p.B, p.T, p.HV, p.K, p.V, ph)
+                        : ck_bytes_by_k<float>(p.B, p.T, p.HV, p.K, p.V, ph);
   p.ck = ws;
   p.part = static_cast<char*>(ws) + al256(ck);
-  if (f64) return bwd_by_k<double, double>(p, stream);
-  if (dtype == DT_F32) return bwd_by_k<float, float>(p, stream);
-  if (dtype == DT_BF16) return bwd_by_k<bf16_t, float>(p, stream);
-  return bwd_by_k<_Float16, float>(p, stream);
+  if (f64) return bwd_by_k<double, double>(p, ph, stream);
+  if (dtype == DT_F32) return bwd_by_k<float, float>(p, ph, stream);
+  if (dtype == DT_BF16) return bwd_by_k<bf16_t, float>(p, ph, stream);
+  return bwd_by_k<_Float16, float>(p, ph, stream);
 }
 
 }  // namespace kch

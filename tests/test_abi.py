@@ -69,7 +69,7 @@ def test_invalid_arguments_report_errors_without_gpu():
 def test_kda_backward_validation_and_workspace():
     """kch_kda_recurrent_bwd: sizes checked before any pointer or HIP call; the
     workspace is the checkpoints (one state slice per segment) plus one
-    partial record (3K + 1 values) per (b, t, hv, 32-column slice)."""
+    partial record (3K + 1 values) per (b, t, hv, 16-column slice)."""
     from kch import _lib
     lib = _lib.load()
     P = [None] * 14
@@ -83,11 +83,11 @@ def test_kda_backward_validation_and_workspace():
     assert rc == 1 and b"null" in lib.kch_last_error()
     assert lib.kch_kda_recurrent_bwd_ws_bytes(1, 8, 2, 48, 16, 0) == 0
     pad = lambda x: (x + 255) // 256 * 256  # noqa: E731
-    # fp32, K = 128: 8-token segments; fp64, K = 128: 4-token segments
+    # 16-column slices; K = 128: 8-token segments (fp32), 4 (fp64: LDS)
     B, T, HV, K, V = 2, 100, 3, 128, 40
-    nvs = (V + 31) // 32
+    nvs = (V + 15) // 16
     for code, acc, seg in ((0, 4, 8), (1, 4, 8), (3, 8, 4)):
-        ck = B * HV * nvs * (-(-T // seg)) * K * 32 * acc
+        ck = B * HV * nvs * (-(-T // seg)) * K * 16 * acc
         part = B * T * HV * nvs * (3 * K + 1) * acc
         assert lib.kch_kda_recurrent_bwd_ws_bytes(B, T, HV, K, V, code) == pad(ck) + pad(part)
 

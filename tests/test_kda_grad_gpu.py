@@ -240,3 +240,17 @@ def test_empty_sequence_grad(dev):
     w = torch.randn_like(s)
     (s * w).sum().backward()
     assert torch.equal(s0.grad, w)
+
+
+def test_fp32_wide_grid_matches_oracle(dev):
+    """A grid with a workgroup for every CU (B * HV * V / 32 >= 256): the
+    backward then runs 32-column slices (8 row phases per column) instead of
+    16-column ones; same bar as the other fp32 cases."""
+    import kch
+    B, T, H, HV, K, V = 4, 40, 8, 16, 64, 128
+    host, s0, w_o, w_s = _make(99, B, T, H, HV, K, V)
+    host = [np.asarray(x, np.float32).astype(np.float64) for x in host]
+    s0 = s0.astype(np.float32).astype(np.float64)
+    ts, s0t = _leaves(host, s0, dev, torch.float32, torch.float32)
+    got = _hip_grads(kch.naive_recurrent_kda, ts, s0t, w_o, w_s)
+    _check(got, _ref(host, s0, w_o, w_s), 1e-4, label="fp32 wide")
