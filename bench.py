@@ -676,6 +676,11 @@ def main():
         extra["hybrid_C4"] = bench_hybrid(dev)
         _log(f"hybrid C4: prefill {extra['hybrid_C4']['prefill_ms']:.2f} ms, decode "
              f"{extra['hybrid_C4']['decode_ms_per_step']:.3f} ms/step")
+        torch.cuda.empty_cache()
+        # the training path (gradients): not part of the headline metric
+        extra["training"] = bench_training(dev)
+        _log(f"training: KDA C1 backward {extra['training']['kda_C1_backward_ms']:.2f} ms, "
+             f"stack step {extra['training']['hybrid_C4_B2_T2048_train_step_ms']:.2f} ms")
         rec["extra"] = extra
     if not args.no_cpu:
         rec["cpu_baseline"] = cpu_baselines(host, s0h)
