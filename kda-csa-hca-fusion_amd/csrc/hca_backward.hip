@@ -272,8 +272,10 @@ __global__ __launch_bounds__(256) void hca_bwd_key_kernel(HcaBwdParams p, int mo
     }
 #pragma unroll
     for (int i = 0; i < NBT; ++i) {
+      // (the same for every lane: a row this query did not select costs nothing)
+      if (!((selbits >> i) & 1u)) continue;
       const int r = r0 + i;
-      const bool valid = act && r < nrows && t >= lo(r) && t < hi(r) && ((selbits >> i) & 1u);
+      const bool valid = act && r < nrows && t >= lo(r) && t < hi(r);
       float a = 0.f, c = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
