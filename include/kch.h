@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define KCH_ABI_VERSION 13
+#define KCH_ABI_VERSION 14
 
 #define KCH_OK 0
 #define KCH_ERR_INVALID 1     /* bad pointer / shape / argument */
@@ -224,9 +224,10 @@ int kch_layer_norm_bwd(const void* x, const void* w, const void* dy, void* dx, f
  *   C, Z   rows of c values, ld* elements apart (dtype); B_pos [m,c] fp32
  *   out_raw  [B,T/m,c] fp32 block values, or NULL
  *   out_key  [B,T/m,c] key rows, L2-normalised when `normalize`: bf16
- *            (key_f32 = 0), fp32 (1), or split (2): [B,T/m,2,c] bf16, each
- *            row's high parts then low parts of its fp32 value (x = hi + lo,
- *            the operands of kch_csa_indexer_topk with key_split); or NULL
+ *            (key_f32 = 0), fp32 (1), or split (2): [B,T/m,3,c] bf16, each
+ *            row's high, middle then low parts of its fp32 value
+ *            (x = hi + mid + lo, the operands of kch_csa_indexer_topk with
+ *            key_split); or NULL
  *   local    [B,T,c] bf16 per-token window keys L2norm(C) (raw C when not
  *            `normalize`), or NULL
  * T must be a multiple of m (callers right-pad as ops_csa.py:772-777 does).
@@ -252,7 +253,8 @@ int kch_compress_overlapped(const void* Ca, long long ldCa, const void* Cb, long
  * Lightning indexer + top-k. Replaces csa_lightning_indexer
  * (ops_csa.py:330-573) in its forward (hard top-k) form.
  *   q_idx [B,T,nIh,cI] (dtype), k_idx [B,nb,cI] fp32, or with key_split
- *   [B,nb,2,cI] bf16 high / low parts of each row (kch_compress key_f32 = 2);
+ *   [B,nb,3,cI] bf16 high / middle / low parts of each row (kch_compress
+ *   key_f32 = 2); logits carry fp32-level error (three-part bf16 products);
  *   already L2-normalised when normalize_q. w_idx [B,T,nIh] (dtype) or NULL
  *   (= all ones)
  *   idx_out [B,T,topk] int64 (idx64) or int32: the top-k blocks by descending

@@ -24,17 +24,21 @@
 namespace kch {
 
 // One channel of a compressed key row: bf16 (key_f32 0), fp32 (1), or the
-// bf16 high and low parts x = hi + lo of the fp32 value (2), stored as two
-// half rows [hi(c) | lo(c)] -- the split the indexer's MFMA products use.
+// three bf16 parts x = hi + mid + lo of the fp32 value (2), stored as three
+// part rows [hi(c) | mid(c) | lo(c)] -- the split the indexer's MFMA products
+// use.
 __device__ __forceinline__ void store_key(const CompressParams& p, size_t orow, int c, int ch,
                                           float x) {
   if (p.key_f32 == 1) {
     static_cast<float*>(p.out_key)[orow * c + ch] = x;
   } else if (p.key_f32 == 2) {
     const bf16_t hi = (bf16_t)x;
-    bf16_t* row = static_cast<bf16_t*>(p.out_key) + orow * 2 * c;
+    const float r = x - (float)hi;
+    const bf16_t mid = (bf16_t)r;
+    bf16_t* row = static_cast<bf16_t*>(p.out_key) + orow * 3 * c;
     row[ch] = hi;
-    row[c + ch] = (bf16_t)(x - (float)hi);
+    row[c + ch] = mid;
+    row[2 * c + ch] = (bf16_t)(r - (float)mid);
   } else {
     static_cast<bf16_t*>(p.out_key)[orow * c + ch] = (bf16_t)x;
   }

@@ -9,8 +9,9 @@
 //   blocks of one sequence (ops_csa.py:503-536: relu(scale q_h . k_n / ||k_n||),
 //   weighted head sum), then the range's top-k. Keys are the cached rows as
 //   stored (cache dtype) times a per-row fp32 1/||k|| (1 without
-//   normalisation); q is split into bf16 hi + lo, so a bf16 key row gives the
-//   logit to ~2^-16 relative error with two MFMAs. Each logit becomes a unique
+//   normalisation); q is split into three bf16 parts hi + mid + lo, so a bf16
+//   key row gives the logit to fp32-level error with three MFMAs (fp16 / fp32
+//   rows are split the same way, six MFMAs). Each logit becomes a unique
 //   64-bit value (order-preserving key, then the complement of the block
 //   index), so "larger value" is exactly the reference's order with ties taken
 //   in ascending block index, and a selection needs no tie bookkeeping.
@@ -54,15 +55,6 @@ __device__ __forceinline__ uint32_t okey(float f) {
   uint32_t u = __float_as_uint(f);
   if (u == 0x80000000u) u = 0u;
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-__device__ __forceinline__ void split8(const float* f, bf16x8& hi, bf16x8& lo) {
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const bf16_t h = (bf16_t)f[i];
-    hi[i] = h;
-    lo[i] = (bf16_t)(f[i] - (float)h);
-  }
 }
 
 // Wave index within the block, as a wave-uniform (scalar) value.
@@ -534,7 +526,7 @@ __host__ __device__ inline int pow2_at_least(int x) {
 }
 
 // Eight key elements of one row as stored: bf16 rows feed the MFMA as they
-// are; fp16 / fp32 rows are split into bf16 hi + lo when consumed.
+// are; fp16 / fp32 rows are split into bf16 hi + mid + lo when consumed.
 template <typename KT>
 struct KeyFrag {
   bf16x8 v;
@@ -555,11 +547,18 @@ struct KeyFrag<float> {
   }
 };
 
+// q's three parts (MFMA A operand)
+struct QSplit {
+  bf16x8 hi, mid, lo;
+};
+
+// acc += q . key, the smallest cross products first
 template <typename KT>
-__device__ __forceinline__ f32x4 key_mfma(const KeyFrag<KT>& k, const bf16x8& qhi, const bf16x8& qlo, f32x4 acc) {
+__device__ __forceinline__ f32x4 key_mfma(const KeyFrag<KT>& k, const QSplit& q, f32x4 acc) {
   if constexpr (std::is_same<KT, bf16_t>::value) {
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qhi, k.v, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qlo, k.v, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(q.lo, k.v, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(q.mid, k.v, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(q.hi, k.v, acc, 0, 0, 0);
   } else {
     float f[8];
     if constexpr (std::is_same<KT, float>::value) {
@@ -569,11 +568,14 @@ __device__ __forceinline__ f32x4 key_mfma(const KeyFrag<KT>& k, const bf16x8& qh
 #pragma unroll
       for (int i = 0; i < 8; ++i) f[i] = (float)k.v[i];
     }
-    bf16x8 khi, klo;
-    split8(f, khi, klo);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qhi, khi, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qlo, khi, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qhi, klo, acc, 0, 0, 0);
+    bf16x8 khi, kmid, klo;
+    split3_bf16(f, khi, kmid, klo);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(q.mid, kmid, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(q.lo, khi, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(q.hi, klo, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(q.mid, khi, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(q.hi, kmid, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(q.hi, khi, acc, 0, 0, 0);
   }
   return acc;
 }
@@ -648,7 +650,10 @@ __global__ __launch_bounds__(256, 4) void idx_range_kernel(DecodeIdxParams p) {
   constexpr int NS = CI / 32;
   // fragments in flight per wave: about 16 KB of key rows
   constexpr int VG = NS * 8 * (int)sizeof(KT) / 4;
-  constexpr int D = 64 / VG < 2 ? 2 : (64 / VG > 8 ? 8 : 64 / VG);
+  // (128-channel rows: the q parts take 48 registers, so one chunk fewer fits
+  // in the 128 registers of four waves per SIMD)
+  constexpr int VGQ = CI >= 128 ? 48 : 64;
+  constexpr int D = VGQ / VG < 2 ? 2 : (VGQ / VG > 8 ? 8 : VGQ / VG);
   uint32_t* keys = reinterpret_cast<uint32_t*>(smem);       // [RB_MAX] (reads of whole 16-byte groups)
   uint32_t* hist = keys + RB_MAX;                            // [512]
   int* scratch = reinterpret_cast<int*>(hist + 512);         // [48]
@@ -675,7 +680,7 @@ __global__ __launch_bounds__(256, 4) void idx_range_kernel(DecodeIdxParams p) {
   }
 
   // ---- q fragments (MFMA A operand: row = index head n, zero beyond nIh), split bf16 ----
-  bf16x8 qhi[NS], qlo[NS];
+  QSplit qs[NS];
   float w4[4];  // weights of the heads 4 q4 + e this lane's accumulator rows hold
   {
     float f[NS][8];
@@ -693,7 +698,7 @@ __global__ __launch_bounds__(256, 4) void idx_range_kernel(DecodeIdxParams p) {
     for (int s = 0; s < NS; ++s) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) f[s][i] = n < nIh ? f[s][i] * inv : 0.f;
-      split8(f[s], qhi[s], qlo[s]);
+      split3_bf16(f[s], qs[s].hi, qs[s].mid, qs[s].lo);
     }
     const QT* wrow = static_cast<const QT*>(p.w_idx) + (size_t)b * (p.ld_wb ? p.ld_wb : (long long)nIh);
 #pragma unroll
@@ -756,11 +761,11 @@ __global__ __launch_bounds__(256, 4) void idx_range_kernel(DecodeIdxParams p) {
       const bf16x8 ra = rot8(f[0].v), rb = rot8(f[1].v);
       g0.v = n < 8 ? f[0].v : rb;
       g1.v = n < 8 ? ra : f[1].v;
-      acc = key_mfma<KT>(g0, qhi[0], qlo[0], acc);
-      acc = key_mfma<KT>(g1, qhi[1], qlo[1], acc);
+      acc = key_mfma<KT>(g0, qs[0], acc);
+      acc = key_mfma<KT>(g1, qs[1], acc);
     } else {
 #pragma unroll
-      for (int s = 0; s < NS; ++s) acc = key_mfma<KT>(f[s], qhi[s], qlo[s], acc);
+      for (int s = 0; s < NS; ++s) acc = key_mfma<KT>(f[s], qs[s], acc);
     }
     const float sc = p.scale * (has_inv ? ivv : 1.f);
     float v = 0.f;

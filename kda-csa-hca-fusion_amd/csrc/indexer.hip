@@ -12,11 +12,12 @@
 // Mapping: one 4-wave workgroup per group of QPW = 16 / nIh consecutive
 // queries; MFMA column n = (query n / nIh, head n % nIh). The waves split the
 // logits by 16-block chunk, then take one query's selection each. The key
-// rows come as fp32, or already split (KSPLIT: the bf16 high and low parts of
-// each row side by side, as the compression kernel writes them for
-// csa_core), which spares every workgroup the conversion. Scores use a split-bf16 product
-// (x = hi + lo, hi*hi + hi*lo + lo*hi with fp32 accumulation) so the logits
-// carry ~2^-16 relative error instead of bf16's 2^-8. Per query, the logits sit
+// rows come as fp32, or already split (KSPLIT: the three bf16 parts of each
+// row side by side, as the compression kernel writes them for csa_core),
+// which spares every workgroup the conversion. Scores use a three-part
+// split-bf16 product (x = hi + mid + lo on both sides; the six cross products
+// down to 2^-16 with fp32 accumulation) so the logits carry fp32-level error
+// (terms of 2^-24 dropped), as the reference's fp32 einsum does. Per query, the logits sit
 // in LDS as 32-bit order keys. A row of up to 256 * RG visible blocks is
 // selected by one wave in registers (the k-th largest key found bit by bit
 // with ballot counts); a longer row by an 8-bit radix select in LDS. Either
@@ -81,15 +82,6 @@ __device__ __forceinline__ float head_sum(float v) {
   if constexpr (NIH >= 8) v += dpp_mov<0x141>(v);
   if constexpr (NIH >= 16) v += dpp_mov<0x140>(v);
   return v;
-}
-
-__device__ __forceinline__ void split_bf16(const float* f, bf16x8& hi, bf16x8& lo) {
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const bf16_t h = (bf16_t)f[i];
-    hi[i] = h;
-    lo[i] = (bf16_t)(f[i] - (float)h);
-  }
 }
 
 // Groups of 256 blocks whose order keys one wave holds in registers (4 per
@@ -240,7 +232,7 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
   const int jq = n / nIh, hh = n - jq * nIh;
   const int tq = t0 + jq;
   const bool qok = tq < p.T;
-  bf16x8 qhi[NS], qlo[NS];
+  bf16x8 qhi[NS], qmid[NS], qlo[NS];
   float wq = 0.f;
   {
     float f[NS][8];
@@ -258,7 +250,7 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
     for (int s = 0; s < NS; ++s) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) f[s][i] = qok ? f[s][i] * inv : 0.f;
-      split_bf16(f[s], qhi[s], qlo[s]);
+      split3_bf16(f[s], qhi[s], qmid[s], qlo[s]);
     }
     if (qok) {
       const size_t wi = ((size_t)b * p.T + tq) * nIh + hh;
@@ -274,43 +266,56 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
   // key rows of chunk c (row 16c + n, clamped: past the end the last row is
   // re-read and masked); wave w takes chunks w, w + 4, ..., D in flight;
   // refills are unconditional so that no loaded register is copied. A row is
-  // CI fp32, or (KSPLIT) CI bf16 high parts then CI bf16 low parts: the same
-  // 4 bytes per channel either way.
+  // CI fp32 (4 bytes per channel, split here), or (KSPLIT) CI bf16 high parts,
+  // CI bf16 middle parts and CI bf16 low parts (6 bytes per channel).
   constexpr int D = 4;
+  constexpr int ROW_BYTES = KSPLIT ? 6 * CI : 4 * CI;
   const int nch = (nv_max + 15) / 16;
   const int mine = nch > wave ? (nch - wave + 3) / 4 : 0;
-  const long long kbs = p.k_bstride ? p.k_bstride : (long long)nb * CI;  // 4-byte units
-  const char* kbase = reinterpret_cast<const char*>(p.k_idx) + (size_t)b * kbs * 4;
+  // batch stride: k_bstride (4-byte units, fp32 rows only) or nb whole rows
+  const long long kbs = (!KSPLIT && p.k_bstride) ? p.k_bstride * 4 : (long long)nb * ROW_BYTES;
+  const char* kbase = reinterpret_cast<const char*>(p.k_idx) + (size_t)b * kbs;
   struct KFrag {
-    bf16x8 hi[NS], lo[NS];
+    bf16x8 hi[NS], mid[NS], lo[NS];
   };
   auto load = [&](int c, KFrag& kf) {
     const int r = min(16 * c + n, nb - 1);
-    const char* krow = kbase + (size_t)r * CI * 4;
+    const char* krow = kbase + (size_t)r * ROW_BYTES;
     if constexpr (KSPLIT) {
       const bf16_t* kh = reinterpret_cast<const bf16_t*>(krow);
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
         kf.hi[s] = *reinterpret_cast<const bf16x8*>(kh + 32 * s + 8 * q4);
-        kf.lo[s] = *reinterpret_cast<const bf16x8*>(kh + CI + 32 * s + 8 * q4);
+        kf.mid[s] = *reinterpret_cast<const bf16x8*>(kh + CI + 32 * s + 8 * q4);
+        kf.lo[s] = *reinterpret_cast<const bf16x8*>(kh + 2 * CI + 32 * s + 8 * q4);
       }
     } else {
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
         float f[8];
         Load8<float>::run(reinterpret_cast<const float*>(krow) + 32 * s + 8 * q4, f);
-        split_bf16(f, kf.hi[s], kf.lo[s]);
+        split3_bf16(f, kf.hi[s], kf.mid[s], kf.lo[s]);
       }
     }
   };
   auto consume = [&](int c, const KFrag& kf) {
+    // the smallest cross products first, so that each later (larger) term is
+    // added to an accumulator of the smaller ones
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.hi[s], qhi[s], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.mid[s], qmid[s], acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.hi[s], qlo[s], acc, 0, 0, 0);
       acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.lo[s], qhi[s], acc, 0, 0, 0);
     }
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.hi[s], qmid[s], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.mid[s], qhi[s], acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.hi[s], qhi[s], acc, 0, 0, 0);
     // acc[e]: block 16c + 4*q4 + e, column n. No branch in here: the lanes
     // whose value is not kept write their own word of this wave's sink
     // words, since a branch costs the overlap of the chunks loaded ahead.

@@ -84,6 +84,24 @@ template <> struct Pair<_Float16> {
   }
 };
 
+// Three-part bf16 split of fp32 values: x = hi + mid + lo up to the rounding
+// of the last part (each difference below is exact in fp32), so hi carries 8
+// significant bits, mid the next 8 and lo the next 8: together the 24 bits of
+// x. Dot products formed from the six leading cross products of such splits
+// (hi*hi, hi*mid, mid*hi, hi*lo, lo*hi, mid*mid: every bf16 product is exact
+// in fp32) carry fp32-level error (terms of 2^-24 and below dropped).
+__device__ __forceinline__ void split3_bf16(const float* f, bf16x8& hi, bf16x8& mid, bf16x8& lo) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const bf16_t h = (bf16_t)f[i];
+    const float r = f[i] - (float)h;
+    const bf16_t md = (bf16_t)r;
+    hi[i] = h;
+    mid[i] = md;
+    lo[i] = (bf16_t)(r - (float)md);
+  }
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // The KDA layer's activations in fp32 (torch's silu, sigmoid, and softplus

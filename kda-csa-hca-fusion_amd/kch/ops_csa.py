@@ -411,8 +411,8 @@ def _csa_core(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, *, m
              if sliding_window > 0 else None)
     _compress_overlapped(fn, Ca, Cb, Za, Zb, Ba, Bb, m, out_raw=False, key=kv,
                          normalize=normalize_qk, local=local)
-    # indexer keys as split bf16 rows (high, low parts): the indexer's MFMA operands
-    k_norm = torch.empty(B_, n_blocks, 2 * c_I, device=device, dtype=torch.bfloat16)
+    # indexer keys as split bf16 rows (high, middle, low parts): the indexer's MFMA operands
+    k_norm = torch.empty(B_, n_blocks, 3 * c_I, device=device, dtype=torch.bfloat16)
     _compress(fn, K_idx, Z_idx, B_idx, m, out_raw=False, key=k_norm, normalize=normalize_qk,
               key_split=True)
     idx = None

@@ -129,11 +129,13 @@ def chunk_kda(q, k, v, g, beta, scale=None, initial_state=None, chunk_size=64,
         g = np.maximum(g, compute(g_clamp_min))
     g = np.cumsum(g, axis=-2, dtype=compute)
 
-    # A[..., j, i] = sum_k k_j exp(min(g_j - g_i, 50)) k_i   (ops_kda.py:409-415)
+    # A[..., j, i] = sum_k k_j exp(min(g_j - g_i, 50)) k_i   (ops_kda.py:409-415);
+    # only the strictly lower part (j > i) survives the mask of :417, so only
+    # those rows are formed (the same arithmetic per element)
     A = np.zeros(g.shape[:-1] + (C,), compute)
-    for i in range(C):
-        gd = np.minimum(g - g[..., i:i + 1, :], compute(50.0))
-        A[..., i] = (k * np.exp(gd) * k[..., i:i + 1, :]).sum(-1)
+    for i in range(C - 1):
+        gd = np.minimum(g[..., i + 1:, :] - g[..., i:i + 1, :], compute(50.0))
+        A[..., i + 1:, i] = (k[..., i + 1:, :] * np.exp(gd) * k[..., i:i + 1, :]).sum(-1)
     A = A * beta[..., None]
     upper_incl = np.triu(np.ones((C, C), bool), 0)
     A = -np.where(upper_incl, compute(0), A)
@@ -142,13 +144,17 @@ def chunk_kda(q, k, v, g, beta, scale=None, initial_state=None, chunk_size=64,
     w = A @ (np.exp(g) * k)
     u = A @ v
 
-    strict_upper = np.triu(np.ones((C, C), bool), 1)
+    # Aqk[..., r, c] = sum_k q_r exp(min(g_r - g_c, 50)) k_c for r >= c, zero
+    # above the diagonal (ops_kda.py:515-517), for all chunks at once, column
+    # by column (the same arithmetic per element)
+    Aqk_all = np.zeros(g.shape[:-1] + (C,), compute)
+    for c in range(C):
+        diff = np.minimum(g[..., c:, :] - g[..., c:c + 1, :], compute(50.0))
+        Aqk_all[..., c:, c] = (q[..., c:, :] * np.exp(diff) * k[..., c:c + 1, :]).sum(-1)
     o = np.zeros((B, HV, NT, C, V), compute)
     for n in range(NT):
         q_i, k_i, u_i, g_i, w_i = q[:, :, n], k[:, :, n], u[:, :, n], g[:, :, n], w[:, :, n]
-        diff = np.minimum(g_i[..., :, None, :] - g_i[..., None, :, :], compute(50.0))
-        Aqk = (q_i[..., :, None, :] * np.exp(diff) * k_i[..., None, :, :]).sum(-1)
-        Aqk = np.where(strict_upper, compute(0), Aqk)
+        Aqk = Aqk_all[:, :, n]
         v_i = u_i - w_i @ S
         o[:, :, n] = (q_i * np.exp(g_i)) @ S + Aqk @ v_i
         S = S * np.exp(g_i[:, :, -1])[..., None]

@@ -10,7 +10,8 @@ rows past nb hold garbage that must not matter. Against ``kch_csa_decode`` /
 * the selection is bit-identical (both are exact top-k with ties to the lower
   block index; the counter-driven step scores in 256-block ranges and selects
   from all keys in one workgroup up to 8192 blocks, and takes the ranges +
-  merge path beyond), and also checked against the oracle's indexer;
+  merge path beyond), and also checked against the oracle's indexer (fp64
+  logits) under the near-tie rule of ``selection_check``;
 * outputs agree to fp32 summation order (the two plan their row groups from
   different row counts).
 
@@ -30,6 +31,7 @@ import pytest
 import torch
 
 from oracle.csa import indexer_logits, topk_desc_lowest_index
+from selection_check import check_selection, logit_eps
 from test_decode_split_gpu import joint_ref, make_csa, run_csa
 
 pytestmark = pytest.mark.gpu
@@ -95,11 +97,11 @@ def test_csa_decode_dyn_matches_planned(dev, nb, topk, cap, m):
             f"nb={nb}: selections differ"
         assert (idx_d[:, nb:] == -1).all()
         np.testing.assert_allclose(out_d, out_p, rtol=1e-5, atol=1e-6)
-    lg = indexer_logits(qi[:, None], kr_used, wi[:, None], None, None, True)[:, 0]
+    lg = indexer_logits(qi[:, None], kr_used, wi[:, None], None, None, True,
+                        compute=np.float64)[:, 0]
     ref = topk_desc_lowest_index(lg, topk)
+    check_selection(f"dyn nb={nb}", idx_d, ref, lg, logit_eps(wi, nIh), sorted_=True)
     for b in range(B):
-        clear = set(np.nonzero(lg[b] > np.sort(lg[b])[::-1][min(topk, nb) - 1] + 1e-4)[0])
-        assert clear <= set(idx_d[b].tolist())
         if nb >= 64 and 7 in ref[b] and 40 not in ref[b]:
             assert 7 in idx_d[b] and 40 not in idx_d[b]
 

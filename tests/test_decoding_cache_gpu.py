@@ -79,7 +79,10 @@ def test_csa_cache_prefill_then_decode(dev, topk):
         if topk < nb:
             idx = hip._last_indices.cpu().numpy()[:, None, :].astype(np.int64)
             cbm = (np.arange(nb) < (ora.n_tokens_seen) // m)[None, :]
-            ref_idx, lg = lightning_indexer(qi_h, ora.K_IComp, wi_h, topk, None, cbm, True,
+            # the exact logits of the key rows this cache holds (their parity with
+            # the oracle's rows is checked below, within one rounding of bf16)
+            k_rows = hip.K_IComp.float().cpu().numpy()
+            ref_idx, lg = lightning_indexer(qi_h, k_rows, wi_h, topk, None, cbm, True,
                                             compute=np.float64, return_logits=True)
             # only a near-tie of the k-th logit, within the kernels' error bound, may differ
             check_selection(f"csa step {step}", idx, ref_idx, lg, logit_eps(wi_h, nIh))
