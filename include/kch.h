@@ -164,7 +164,10 @@ int kch_hca_attn_bwd(const float* q, const float* d_out, const float* kc, const 
  * nothing); dBap, dBbp [B,T/m,m,c]; sink_part as for HCA; slot_grad
  * [B,T,topk] (zeroed by the caller): the gradient of each selected row dotted
  * with that row, which the STE surrogate (ops_csa.py:1033-1099) turns into
- * the indexer's gradient. The window rows' gradient is added into dCa.
+ * the indexer's gradient; gsum [B,T,c] or NULL: the sum over the selected
+ * slots of the selected rows' gradients (written), which the full-softmax
+ * surrogate's dense term (ops_csa.py:1050-1071) consumes. The window rows'
+ * gradient is added into dCa.
  */
 size_t kch_csa_attn_bwd_ws_bytes(int B, int T, int nh, int c, int m, int win, int topk);
 int kch_csa_attn_bwd(const float* q, const float* d_out, const float* kc, const float* raw,
@@ -172,8 +175,8 @@ int kch_csa_attn_bwd(const float* q, const float* d_out, const float* kc, const 
                      const float* Cb, const float* Za, const float* Zb, const float* Ba,
                      const float* Bb, const float* sink, float* dq, float* dCa, float* dCb,
                      float* dZa, float* dZb, float* dBap, float* dBbp, float* sink_part,
-                     float* slot_grad, int B, int T, int nh, int c, int m, int topk, int win,
-                     float scale, int normalize, void* ws, size_t ws_bytes, void* stream);
+                     float* slot_grad, float* gsum, int B, int T, int nh, int c, int m, int topk,
+                     int win, float scale, int normalize, void* ws, size_t ws_bytes, void* stream);
 
 /*
  * The STE surrogate's backward for the CSA indexer (ops_csa.py:1033-1099,
@@ -203,7 +206,9 @@ int kch_csa_ste_bwd(const float* q_idx, const float* w_idx, const float* kc, con
  *   zeroes the others) and dgl (ld_gl apart). K <= 256.
  * kch_short_conv_bwd: dx [B,T,d] of the causal 3-tap depthwise conv, and adds
  *   the taps' and the bias's gradients into fp32 dw [d,3] and db [d] (db may
- *   be NULL); the lookback is an input only (the reference detaches it).
+ *   be NULL). dlookback [B,2,d] (dtype, or NULL): the gradient of the two
+ *   lookback rows, for callers that keep the lookback attached to the
+ *   previous chunk's graph (ops_fused.py:480-527 with detach_lookback=False).
  * kch_layer_norm_bwd: dx of the fp32 LayerNorm over the last dim (d <= 4096),
  *   and adds dw, db (fp32 [d]). dtype / wdtype: the input's and the weight's.
  */
@@ -212,8 +217,8 @@ int kch_kda_gates_bwd(const void* proj, long long ld_proj, const void* gl, long 
                       const void* dbeta, void* dproj, void* dgl, int B, int T, int H, int HV, int K,
                       int V, float decay_scale, int dtype, void* stream);
 int kch_short_conv_bwd(const void* x, const void* lookback, const void* weight, const void* dy,
-                       void* dx, float* dw, float* db, int B, int T, int d, int dtype,
-                       void* stream);
+                       void* dx, float* dw, float* db, void* dlookback, int B, int T, int d,
+                       int dtype, void* stream);
 int kch_layer_norm_bwd(const void* x, const void* w, const void* dy, void* dx, float* dw, float* db,
                        long long rows, int d, float eps, int dtype, int wdtype, void* stream);
 

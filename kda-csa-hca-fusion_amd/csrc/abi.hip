@@ -318,8 +318,8 @@ int kch_csa_attn_bwd(const float* q, const float* d_out, const float* kc, const 
                      const float* Cb, const float* Za, const float* Zb, const float* Ba,
                      const float* Bb, const float* sink, float* dq, float* dCa, float* dCb,
                      float* dZa, float* dZb, float* dBap, float* dBbp, float* sink_part,
-                     float* slot_grad, int B, int T, int nh, int c, int m, int topk, int win,
-                     float scale, int normalize, void* ws, size_t ws_bytes, void* stream) {
+                     float* slot_grad, float* gsum, int B, int T, int nh, int c, int m, int topk,
+                     int win, float scale, int normalize, void* ws, size_t ws_bytes, void* stream) {
   const char* fn = "kch_csa_attn_bwd";
   if (B < 0 || T < 1 || nh < 1 || m < 1 || win < 0 || topk < 0)
     return fail(KCH_ERR_INVALID, "%s: bad sizes B=%d T=%d nh=%d m=%d win=%d topk=%d (T >= 1)", fn, B,
@@ -354,6 +354,7 @@ int kch_csa_attn_bwd(const float* q, const float* d_out, const float* kc, const 
   p.topk = topk;
   p.sparse = 1;
   p.slot_grad = topk > 0 ? slot_grad : nullptr;
+  p.gsum = gsum;
   p.normalize = normalize ? 1 : 0;
   p.B = B; p.T = T; p.nh = nh; p.c = c; p.m2 = m; p.nb = T / m; p.win = win;
   p.scale = scale;
@@ -426,8 +427,8 @@ int kch_kda_gates_bwd(const void* proj, long long ld_proj, const void* gl, long 
 }
 
 int kch_short_conv_bwd(const void* x, const void* lookback, const void* weight, const void* dy,
-                       void* dx, float* dw, float* db, int B, int T, int d, int dtype,
-                       void* stream) {
+                       void* dx, float* dw, float* db, void* dlookback, int B, int T, int d,
+                       int dtype, void* stream) {
   const char* fn = "kch_short_conv_bwd";
   if (!dtype_ok(dtype)) return fail(KCH_ERR_INVALID, "%s: unknown dtype %d", fn, dtype);
   if (B < 0 || T < 0 || d < 1) return fail(KCH_ERR_INVALID, "%s: bad sizes B=%d T=%d d=%d", fn, B, T, d);
@@ -435,6 +436,7 @@ int kch_short_conv_bwd(const void* x, const void* lookback, const void* weight, 
   if (!x || !weight || !dy || !dx || !dw) return fail(KCH_ERR_INVALID, "%s: null tensor pointer", fn);
   kch::ShortConvBwdParams p;
   p.x = x; p.lookback = lookback; p.weight = weight; p.dy = dy; p.dx = dx; p.dw = dw; p.db = db;
+  p.dlookback = dlookback;
   p.B = B; p.T = T; p.d = d;
   return hip_status(fn, kch::short_conv_bwd_dispatch(p, dtype, (hipStream_t)stream));
 }

@@ -11,7 +11,8 @@
 //   (sigmoid).
 // short_conv_bwd_kernel thread per (channel, run of tokens, b): dx of the
 //   run (the transposed 3-tap filter), and the run's sums for the filter taps
-//   and the bias, added to fp32 buffers.
+//   and the bias, added to fp32 buffers; the first run also writes the
+//   lookback rows' gradient when asked.
 // layer_norm_bwd_kernel wave per row, 16 rows per wave: dx from the recomputed
 //   mean and rstd; the rows' dy x^ and dy sums stay in registers, meet in LDS
 //   across the four waves, then add into fp32 buffers.
@@ -127,6 +128,14 @@ __global__ __launch_bounds__(256) void short_conv_bwd_kernel(ShortConvBwdParams 
   atomicAdd(p.dw + c * 3 + 1, s1);
   atomicAdd(p.dw + c * 3 + 2, s2);
   if (p.db) atomicAdd(p.db + c, sb);
+  if (p.dlookback && run == 0) {
+    // x[-2] feeds out[0] through w0; x[-1] feeds out[0] through w1 and out[1]
+    // through w0 (dy past T is zero)
+    T* dlb = static_cast<T*>(p.dlookback) + (size_t)b * 2 * p.d + c;
+    const float g0 = dyv(0), g1 = dyv(1);
+    dlb[0] = from_f32<T>(w0 * g0);
+    dlb[p.d] = from_f32<T>(w1 * g0 + w0 * g1);
+  }
 }
 
 constexpr int kLnRowsPerWave = 16;

@@ -16,7 +16,10 @@
 //
 // hca_bwd_query_kernel  one workgroup per (b, t); thread (head, 8-channel
 //   group). Pass A over the query's keys: running max, sum and sum p dp
-//   (lse and D); pass B: dqn, then dq. Writes lse, D, 1/|q| per (t, h).
+//   (lse and D); pass B: dqn, then dq. Writes lse, D, 1/|q| per (t, h), and
+//   for CSA the selected slots' row gradients: each one dotted with its row
+//   (slot_grad) and their sum over the slots (gsum: per head the selected
+//   p and ds sums times dout and qn, summed over the heads in LDS).
 // hca_bwd_key_kernel    one workgroup per (tile of NBT key rows, chunk of up
 //   to QC queries, b): each query row (q, dout, lse, D) is read once for the
 //   NBT keys; the heads' sums meet in LDS; one partial gradient per key row
@@ -154,6 +157,7 @@ __global__ __launch_bounds__(256) void hca_bwd_query_kernel(HcaBwdParams p) {
   float dq[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) dq[e] = 0.f;
+  float psel = 0.f, dssel = 0.f;  // sums over the selected slots of p and scale p (dp - D)
 #pragma unroll
   for (int u = 0; u < PD; ++u)
     if (u < nk) load8(krow(u), kb[u]);
@@ -174,8 +178,25 @@ __global__ __launch_bounds__(256) void hca_bwd_query_kernel(HcaBwdParams p) {
         // add into slot_grad (zeroed by the caller)
         if (p.slot_grad && act && lc == 0 && j < nvis && kvalid(j))
           atomicAdd(p.slot_grad + bt * p.topk + j, pj * ((dp - D) * s + dp));
+        if (j < nvis && kvalid(j)) {
+          psel += pj;
+          dssel += ds;
+        }
       }
     }
+  }
+  if (p.gsum) {
+    // sum over the selected slots of the rows' gradients, scale ds_j qn + p_j dout,
+    // over all heads: sum_h (dssel_h qn_h + psel_h dout_h)
+    __shared__ float gs[HD];
+    for (int i = tid; i < HD; i += 256) gs[i] = 0.f;
+    __syncthreads();
+    if (act) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) atomicAdd(&gs[8 * lc + e], dssel * qn[e] + psel * dv[e]);
+    }
+    __syncthreads();
+    for (int i = tid; i < HD; i += 256) p.gsum[bt * HD + i] = gs[i];
   }
   // L2-norm backward of the query row
   float yd = 0.f;

@@ -89,6 +89,9 @@ struct HcaBwdParams {
   float* dZb = nullptr;
   float* dBbp = nullptr;
   float* slot_grad = nullptr;
+  // CSA, full-softmax STE: the sum over the selected slots of each selected
+  // row's gradient, gsum [B,T,c] (written, the heads of this call summed)
+  float* gsum = nullptr;
   float* lse = nullptr;  // workspace regions, set by hca_bwd_dispatch
   float* dval = nullptr;
   float* rq = nullptr;
@@ -193,6 +196,7 @@ struct ShortConvBwdParams {
   void* dx;
   float* dw;
   float* db;
+  void* dlookback;  // [B, 2, d] or null: gradient of the lookback rows x[-2], x[-1]
   int B, T, d;
 };
 hipError_t short_conv_bwd_dispatch(const ShortConvBwdParams& p, int dtype, hipStream_t stream);

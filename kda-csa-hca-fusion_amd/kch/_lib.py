@@ -36,10 +36,10 @@ _SIGNATURES = {
     "kch_kda_recurrent_fwd_f64": [_P] * 8 + [_I] * 6 + [_D, _D, _P],
     "kch_kda_recurrent_bwd": [_P] * 14 + [_I] * 6 + [_D, _D, _I, _P, _SZ, _P],
     "kch_hca_attn_bwd": [_P] * 16 + [_I] * 6 + [_F, _P, _SZ, _P],
-    "kch_csa_attn_bwd": [_P] * 23 + [_I] * 7 + [_F, _I, _P, _SZ, _P],
+    "kch_csa_attn_bwd": [_P] * 24 + [_I] * 7 + [_F, _I, _P, _SZ, _P],
     "kch_kda_gates_bwd": [_P, _L, _P, _L] + [_P] * 7 + [_I] * 6 + [_F, _I, _P],
     "kch_csa_ste_bwd": [_P] * 13 + [_I] * 5 + [_F, _I, _P, _SZ, _P],
-    "kch_short_conv_bwd": [_P] * 7 + [_I] * 4 + [_P],
+    "kch_short_conv_bwd": [_P] * 8 + [_I] * 4 + [_P],
     "kch_layer_norm_bwd": [_P] * 6 + [_L, _I, _F, _I, _I, _P],
     "kch_compress": [_P, _L, _P, _L, _P, _P, _P, _I, _I, _P, _I, _I, _I, _I, _I, _P],
     "kch_compress_overlapped": [_P, _L, _P, _L, _P, _L, _P, _L, _P, _P, _P, _P, _I, _I, _P,

@@ -316,8 +316,10 @@ class _FusedWeightLayer(nn.Module):
 
 class _ShortConvFn(torch.autograd.Function):
     """The KDA layer's causal depthwise conv with gradients: ``kch_short_conv``
-    forward, ``kch_short_conv_bwd`` backward (the lookback is an input only,
-    detached as in the reference, ``ops_fused.py:480-527``)."""
+    forward, ``kch_short_conv_bwd`` backward. A lookback that requires grad
+    (the previous chunk's last two rows kept in its graph,
+    ``detach_lookback=False``, ``ops_fused.py:480-527``) gets its gradient
+    too: ``d lb[0] = w0 dy[0]``, ``d lb[1] = w1 dy[0] + w0 dy[1]``."""
 
     @staticmethod
     def forward(ctx, x, weight, bias, lookback):
@@ -328,27 +330,35 @@ class _ShortConvFn(torch.autograd.Function):
         if xc.data_ptr() % 16:
             xc = xc.clone()
         lb = None if lookback is None else lookback.detach().to(x.dtype).contiguous()
+        if lb is not None and lb.data_ptr() % 16:
+            lb = lb.clone()
         out = torch.empty_like(xc)
         code = _lib.dtype_code("KDAHybridLayer", x.dtype)
         _lib.call("kch_short_conv", _lib.ptr(xc), _lib.ptr(lb), _lib.ptr(w), _lib.ptr(b),
                   _lib.ptr(out), B, T, d, code, _lib.stream_of(xc))
         ctx.save_for_backward(xc, w, lb)
-        ctx.meta = (weight.shape, weight.dtype, None if bias is None else bias.dtype)
+        ctx.meta = (weight.shape, weight.dtype, None if bias is None else bias.dtype,
+                    None if lookback is None else lookback.dtype)
         return out
 
     @staticmethod
     def backward(ctx, dy):
         xc, w, lb = ctx.saved_tensors
-        wshape, wdt, bdt = ctx.meta
+        wshape, wdt, bdt, lbdt = ctx.meta
         B, T, d = xc.shape
         dyc = dy.to(xc.dtype).contiguous()
         dx = torch.empty_like(xc)
         dw = torch.zeros(d * _CONV_K, device=xc.device, dtype=torch.float32)
         db = None if bdt is None else torch.zeros(d, device=xc.device, dtype=torch.float32)
+        dlb = None
+        if ctx.needs_input_grad[3]:
+            dlb = (torch.empty(B, _CONV_K - 1, d, device=xc.device, dtype=xc.dtype) if T
+                   else torch.zeros(B, _CONV_K - 1, d, device=xc.device, dtype=xc.dtype))
         _lib.call("kch_short_conv_bwd", _lib.ptr(xc), _lib.ptr(lb), _lib.ptr(w), _lib.ptr(dyc),
-                  _lib.ptr(dx), _lib.ptr(dw), _lib.ptr(db), B, T, d,
+                  _lib.ptr(dx), _lib.ptr(dw), _lib.ptr(db), _lib.ptr(dlb), B, T, d,
                   _lib.dtype_code("KDAHybridLayer", xc.dtype), _lib.stream_of(xc))
-        return dx, dw.view(wshape).to(wdt), None if db is None else db.to(bdt), None
+        return (dx, dw.view(wshape).to(wdt), None if db is None else db.to(bdt),
+                None if dlb is None else dlb.to(lbdt))
 
 
 class _KdaGatesFn(torch.autograd.Function):
@@ -488,7 +498,7 @@ class KDAHybridLayer(_FusedWeightLayer):
                 lookback = None
             else:
                 lookback = lookback.to(device=x.device, dtype=x.dtype)
-        if _grad_wanted(x, state, *self.parameters()):
+        if _grad_wanted(x, state, lookback, *self.parameters()):
             return self._forward_grad(x, state, lookback, detach_lookback)
         with torch.no_grad():
             xc = x.contiguous()
@@ -808,7 +818,7 @@ class HybridKCHAttention(nn.Module):
                 f"{len(lookbacks)} but the model has {self.n_kda_layers} KDA layers.")
         kda_idx = 0
         new_lookbacks = []
-        grad = _grad_wanted(x, *self.parameters())
+        grad = _grad_wanted(x, *lookbacks, *self.parameters())
         with torch.set_grad_enabled(grad):
             for layer, norm, kind in zip(self.layers, self.norms, self.layout):
                 residual = x

@@ -2,8 +2,8 @@
 
 ``csa_compress_kv``             <- ``/root/reference/ops_csa.py:198-234``
 ``csa_compress_kv_overlapped``  <- ``/root/reference/ops_csa.py:237-305``
-``csa_lightning_indexer``       <- ``/root/reference/ops_csa.py:330-573`` (forward)
-``naive_csa``                   <- ``/root/reference/ops_csa.py:576-1184`` (forward)
+``csa_lightning_indexer``       <- ``/root/reference/ops_csa.py:330-573`` (forward, soft weights)
+``naive_csa``                   <- ``/root/reference/ops_csa.py:576-1184`` (forward and gradients)
 
 Same signatures, argument meaning and validation messages as the reference.
 The projections are plain ``F.linear`` GEMMs on the GPU (the reference's own
@@ -14,10 +14,17 @@ run in ``libkch.so``.
 
 Differences, all documented:
 
-* Forward only: autograd through the HIP kernels is not provided. With
-  ``use_ste=True`` the reference's forward value is the hard top-k path
-  (the straight-through surrogate adds zero in the forward pass), which is
-  what these twins return.
+* Gradients: with autograd on and an input that requires grad, ``naive_csa``
+  / ``csa_core`` run the projections through autograd (library GEMMs), the
+  attention's backward on ``kch_csa_attn_bwd`` with the selection held fixed,
+  and with ``use_ste`` the straight-through surrogate of
+  ``ops_csa.py:1033-1099`` for the indexer inputs on ``kch_csa_ste_bwd``:
+  ``ste_mode='topk_columns'`` and ``'full_softmax'`` (whose dense
+  zero-in-forward term adds ``gsum C_comp_n^T`` to the soft weights'
+  cotangent and ``soft^T gsum`` to the compressed rows'). ``'aux_contrastive'``
+  raises ``NotImplementedError``, as the reference's indexer does. The
+  forward value is the hard top-k path either way (the surrogate adds zero).
+* Indexer logits are fp32-level: three-part split-bf16 MFMA products.
 * Exactly-equal indexer logits are ordered by ascending block index (the
   reference's ``torch.topk`` leaves that order unspecified).
 * Attention keys/values are the L2-normalised compressed rows rounded to
@@ -352,7 +359,7 @@ def csa_lightning_indexer(q_idx, k_idx, w_idx, topk, scale=None, causal_block_ma
 
 def csa_core(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, *, m, topk,
              sliding_window=0, sink_logits=None, normalize_qk=True, scale=None,
-             return_indices=False, use_ste=False):
+             return_indices=False, use_ste=False, ste_mode='topk_columns'):
     """CSA after the projections (``ops_csa.py:869-1155``) on the HIP backend.
 
     ``Ca..Zb`` ``[B,T,c]``, ``K_idx, Z_idx`` ``[B,T,c_I]``, ``q`` ``[B,T,nh,c]``,
@@ -363,15 +370,21 @@ def csa_core(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, *, m,
     Differentiable (with gradients enabled) in Ca, Cb, Za, Zb, q, Ba, Bb and the
     sink logits through ``kch_csa_attn_bwd``, the selection held fixed; with
     ``use_ste`` also in the indexer inputs through the straight-through
-    surrogate of ``ops_csa.py:1033-1099`` (``topk_columns``).
+    surrogate of ``ops_csa.py:1033-1099``: ``ste_mode='topk_columns'`` (the
+    selected columns of the soft weights) or ``'full_softmax'`` (plus the
+    dense zero-in-forward term that reaches every causal block and, through
+    the expected row ``soft @ C_comp_n``, every compressed row).
     """
+    if ste_mode not in ('topk_columns', 'full_softmax'):
+        raise ValueError(f"csa_core: ste_mode={ste_mode!r} must be 'topk_columns' or "
+                         f"'full_softmax'")
     if torch.is_grad_enabled() and any(
             t is not None and t.requires_grad
             for t in (Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, sink_logits)):
         out, idx = _CsaCoreFunction.apply(
             Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, sink_logits,
             dict(m=m, topk=topk, sliding_window=sliding_window, normalize_qk=normalize_qk,
-                 scale=scale, use_ste=use_ste))
+                 scale=scale, use_ste=use_ste, ste_mode=ste_mode))
         return (out, idx) if return_indices else out
     return _csa_core(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, m=m, topk=topk,
                      sliding_window=sliding_window, sink_logits=sink_logits,
@@ -441,13 +454,15 @@ def _csa_core(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, *, m
 
 
 def csa_attn_grad(Ca, Cb, Za, Zb, q, Ba, Bb, idx, d_out, *, m, sliding_window=0,
-                  sink_logits=None, normalize_qk=True, scale=None):
+                  sink_logits=None, normalize_qk=True, scale=None, want_gsum=False):
     """Gradients of the CSA attention (``ops_csa.py:869-1155``) with the selection
     ``idx`` ``[B,T,topk]`` (int32, -1 = unused) held fixed, on
     ``kch_csa_attn_bwd`` (fp32). Returns a dict with ``Ca, Cb, Za, Zb, q, Ba,
     Bb`` (input dtypes), ``sink_logits`` where given, and ``slot`` ``[B,T,topk]``
-    (fp32): each selected row's gradient dotted with the row. Channels are
-    zero-padded to the kernel's size; more than 16 heads run as groups."""
+    (fp32): each selected row's gradient dotted with the row; with
+    ``want_gsum`` also ``gsum`` ``[B,T,c]`` (fp32): the sum of the selected
+    rows' gradients over the slots. Channels are zero-padded to the kernel's
+    size; more than 16 heads run as groups."""
     fn = "csa_attn_grad"
     B_, T, c = Ca.shape
     nh = q.shape[2]
@@ -484,6 +499,7 @@ def csa_attn_grad(Ca, Cb, Za, Zb, q, Ba, Bb, idx, d_out, *, m, sliding_window=0,
     dBa = torch.zeros(m, cp, device=dev, dtype=f32)
     dBb = torch.zeros_like(dBa)
     slot = torch.zeros(B_, T, topk, device=dev, dtype=f32)
+    gsum = torch.zeros(B_, T, cp, device=dev, dtype=f32) if want_gsum else None
     dsink = None if sink is None else torch.zeros(nh, device=dev, dtype=f32)
     hmax = 256 // (cp // 8)
     for h0 in range(0, nh, hmax):
@@ -497,6 +513,7 @@ def csa_attn_grad(Ca, Cb, Za, Zb, q, Ba, Bb, idx, d_out, *, m, sliding_window=0,
         bap = torch.empty(B_, nb, m, cp, device=dev, dtype=f32)
         bbp = torch.empty_like(bap)
         sp = None if sink is None else torch.empty(B_, T, g, device=dev, dtype=f32)
+        gs = None if gsum is None else (gsum if g == nh else torch.empty_like(gsum))
         nbytes = _lib.load().kch_csa_attn_bwd_ws_bytes(B_, T, g, cp, m, win, topk)
         ws = torch.empty(max(nbytes, 1), device=dev, dtype=torch.uint8)
         _lib.call("kch_csa_attn_bwd", _lib.ptr(qg), _lib.ptr(dog), _lib.ptr(kc), _lib.ptr(raw),
@@ -504,11 +521,13 @@ def csa_attn_grad(Ca, Cb, Za, Zb, q, Ba, Bb, idx, d_out, *, m, sliding_window=0,
                   _lib.ptr(Zaf), _lib.ptr(Zbf), _lib.ptr(Baf), _lib.ptr(Bbf),
                   _lib.ptr(None if sink is None else sink[h0:h1].contiguous()), _lib.ptr(dqg),
                   _lib.ptr(oa), _lib.ptr(ob), _lib.ptr(za), _lib.ptr(zb), _lib.ptr(bap),
-                  _lib.ptr(bbp), _lib.ptr(sp), _lib.ptr(slot if topk else None), B_, T, g, cp, m,
-                  topk, win, float(scale), int(bool(normalize_qk)), _lib.ptr(ws), nbytes,
-                  _lib.stream_of(qg))
+                  _lib.ptr(bbp), _lib.ptr(sp), _lib.ptr(slot if topk else None), _lib.ptr(gs),
+                  B_, T, g, cp, m, topk, win, float(scale), int(bool(normalize_qk)),
+                  _lib.ptr(ws), nbytes, _lib.stream_of(qg))
         if dqg is not dq:
             dq[:, :, h0:h1] = dqg
+        if gs is not None and gs is not gsum:
+            gsum += gs
         dCa += oa
         dCb += ob
         dZa += za
@@ -521,26 +540,31 @@ def csa_attn_grad(Ca, Cb, Za, Zb, q, Ba, Bb, idx, d_out, *, m, sliding_window=0,
            "Za": dZa[..., :c].to(Za.dtype), "Zb": dZb[..., :c].to(Zb.dtype),
            "q": dq[..., :c].to(q.dtype), "Ba": dBa[:, :c].to(Ba.dtype),
            "Bb": dBb[:, :c].to(Bb.dtype), "slot": slot}
+    if gsum is not None:
+        out["gsum"] = gsum[..., :c]
     if sink_logits is not None:
         out["sink_logits"] = dsink.to(sink_logits.dtype)
     return out
 
 
-def _ste_indexer_grads(K_idx, Z_idx, q_idx, w_idx, B_idx, idx, slot, *, m, normalize_qk):
+def _ste_indexer_grads(K_idx, Z_idx, q_idx, w_idx, B_idx, idx, slot, *, m, normalize_qk,
+                       dsel_extra=None):
     """The straight-through surrogate's gradients for the indexer inputs
-    (``ops_csa.py:1033-1099``, ``topk_columns``): the selected columns of the
-    soft weights (``softmax`` over every causal block of the indexer logits,
-    ``ops_csa.py:545-572``) receive ``slot``, carried through the logits
-    (``ops_csa.py:503-536``) and the key compression (``ops_csa.py:198-234``).
-    On ``kch_csa_ste_bwd`` when the padded ``nIh * c_I <= 512`` (a wave per
-    query); beyond that, ``_ste_indexer_grads_dense``."""
+    (``ops_csa.py:1033-1099``): the selected columns of the soft weights
+    (``softmax`` over every causal block of the indexer logits,
+    ``ops_csa.py:545-572``) receive ``slot`` (``topk_columns``), and with
+    ``dsel_extra`` ``[B,T,nb]`` every column receives that too (the dense term
+    of ``full_softmax``), carried through the logits (``ops_csa.py:503-536``)
+    and the key compression (``ops_csa.py:198-234``). On ``kch_csa_ste_bwd``
+    when the padded ``nIh * c_I <= 512`` (a wave per query); beyond that,
+    ``_ste_indexer_grads_dense``."""
     B_, T, cI = K_idx.shape
     nIh = q_idx.shape[2]
     cIp = 64 if cI <= 64 else 128
     nIp = next((n for n in (1, 2, 4, 8) if n >= nIh), None)
     if cI > 128 or nIp is None or nIp * cIp > 512:
         return _ste_indexer_grads_dense(K_idx, Z_idx, q_idx, w_idx, B_idx, idx, slot, m=m,
-                                        normalize_qk=normalize_qk)
+                                        normalize_qk=normalize_qk, dsel_extra=dsel_extra)
     fn = "csa_ste_grad"
     dev = K_idx.device
     f32 = torch.float32
@@ -559,7 +583,8 @@ def _ste_indexer_grads(K_idx, Z_idx, q_idx, w_idx, B_idx, idx, slot, *, m, norma
     if not normalize_qk:
         kc = raw
     idx64 = idx.long()
-    dsel = torch.zeros(B_, T, nb, device=dev, dtype=f32).scatter_add_(
+    dsel = (torch.zeros(B_, T, nb, device=dev, dtype=f32) if dsel_extra is None
+            else dsel_extra.to(f32).clone()).scatter_add_(
         -1, idx64.clamp(min=0), slot.to(f32) * (idx64 >= 0).to(f32))
     scale = 1.0 if normalize_qk else cI ** -0.5
     dq = torch.empty_like(qf)
@@ -578,7 +603,8 @@ def _ste_indexer_grads(K_idx, Z_idx, q_idx, w_idx, B_idx, idx, slot, *, m, norma
             dBp.sum(dim=(0, 1))[:, :cI].to(B_idx.dtype)]
 
 
-def _ste_indexer_grads_dense(K_idx, Z_idx, q_idx, w_idx, B_idx, idx, slot, *, m, normalize_qk):
+def _ste_indexer_grads_dense(K_idx, Z_idx, q_idx, w_idx, B_idx, idx, slot, *, m, normalize_qk,
+                             dsel_extra=None):
     """The same gradients for indexers wider than one wave per query
     (``nIh * c_I > 512`` after padding), dense over the blocks with torch
     operations."""
@@ -604,10 +630,77 @@ def _ste_indexer_grads_dense(K_idx, Z_idx, q_idx, w_idx, B_idx, idx, slot, *, m,
         soft = _nan_safe_softmax(logits, dim=-1)
         idx64 = idx.long()
         sel = torch.gather(soft, -1, idx64.clamp(min=0)) * (idx64 >= 0).to(f32)
-        grads = torch.autograd.grad(sel, [x for x in leaves], grad_outputs=slot,
+        outs, gouts = [sel], [slot]
+        if dsel_extra is not None:
+            outs.append(soft)
+            gouts.append(dsel_extra.to(f32))
+        grads = torch.autograd.grad(outs, [x for x in leaves], grad_outputs=gouts,
                                     allow_unused=True)
     return [None if g is None else g.to(x.dtype) for g, x in zip(grads, (K_idx, Z_idx, q_idx, w_idx,
                                                                         B_idx))]
+
+
+def _compress_overlapped_torch(Ca, Cb, Za, Zb, Ba, Bb, m):
+    """``csa_compress_kv_overlapped`` (``ops_csa.py:237-305``) as differentiable
+    fp32 torch operations: block i mixes Ca of its own m tokens with Cb of
+    block i-1's under one softmax over the 2m logits ``Za + Ba``, ``Zb + Bb``
+    (block 0: the second branch's logits -inf, its values zero)."""
+    f32 = torch.float32
+    B_, T, c = Ca.shape
+    nb = T // m
+
+    def blk(x):
+        return x.to(f32).reshape(B_, nb, m, c)
+    za, zb = blk(Za) + Ba.to(f32), blk(Zb) + Bb.to(f32)
+    zb_prev = torch.cat([torch.full_like(zb[:, :1], float('-inf')), zb[:, :-1]], 1)
+    cb = blk(Cb)
+    cb_prev = torch.cat([torch.zeros_like(cb[:, :1]), cb[:, :-1]], 1)
+    w = torch.softmax(torch.cat([za, zb_prev], 2), 2)
+    return (w * torch.cat([blk(Ca), cb_prev], 2)).sum(2)
+
+
+def _soft_weights(K_idx, Z_idx, q_idx, w_idx, B_idx, *, m, normalize_qk):
+    """The indexer's soft weights ``[B,T,nb]`` fp32 (``ops_csa.py:545-572``):
+    the NaN-safe softmax over the causal blocks of the HIP indexer's logits
+    (fp32-level, ``kch_csa_indexer_topk`` with the logits written out)."""
+    fn = "csa_soft_weights"
+    B_, T, cI = K_idx.shape
+    nIh = q_idx.shape[2]
+    nb = T // m
+    cIp = _kernel_size(fn, "c_I", cI, _IDX_DIMS)
+    nIp = _kernel_size(fn, "nIh", nIh, _IDX_HEADS)
+    f32 = torch.float32
+    Kf, Zf, Bf = (_pad_last(x.detach().to(f32), cIp).contiguous() for x in (K_idx, Z_idx, B_idx))
+    k_rows = torch.empty(B_, nb, cIp, device=K_idx.device, dtype=f32)
+    _compress(fn, Kf, Zf, Bf, m, out_raw=False, key=k_rows, normalize=bool(normalize_qk))
+    qf = F.pad(q_idx.detach().to(f32), (0, cIp - cI, 0, nIp - nIh)).contiguous()
+    wf = _pad_last(w_idx.detach().to(f32), nIp).contiguous()
+    scale = 1.0 if normalize_qk else cI ** -0.5
+    _, logits = _indexer(fn, qf, k_rows, wf, 1, scale, m, dense=False,
+                         normalize_q=bool(normalize_qk), idx64=False, want_logits=True,
+                         sorted_=False)
+    return _nan_safe_softmax(logits)
+
+
+def _full_softmax_grads(Ca, Cb, Za, Zb, Ba, Bb, K_idx, Z_idx, q_idx, w_idx, B_idx, gsum, *, m,
+                        normalize_qk):
+    """The dense term of ``ste_mode='full_softmax'`` (``ops_csa.py:1050-1071``):
+    ``soft_full = soft @ C_comp_n`` enters every selected slot as a zero in
+    the forward, so its cotangent is ``gsum`` (the selected rows' gradients
+    summed over the slots). Returns ``(dsel_extra [B,T,nb], grads of Ca, Cb,
+    Za, Zb, Ba, Bb)``: the soft weights' cotangent ``gsum C_comp_n^T`` (carried
+    on by the surrogate's indexer backward) and ``C_comp_n``'s,
+    ``soft^T gsum``, through the L2 norm and the overlapped compression."""
+    with torch.enable_grad():
+        leaves = [x.detach().to(torch.float32).requires_grad_(True)
+                  for x in (Ca, Cb, Za, Zb, Ba, Bb)]
+        cc = _compress_overlapped_torch(*leaves, m)
+        cn = F.normalize(cc, dim=-1) if normalize_qk else cc
+    soft = _soft_weights(K_idx, Z_idx, q_idx, w_idx, B_idx, m=m, normalize_qk=normalize_qk)
+    g = gsum.to(torch.float32)
+    dsel_extra = torch.bmm(g, cn.detach().transpose(1, 2))
+    dcn = torch.bmm(soft.transpose(1, 2), g)
+    return dsel_extra, torch.autograd.grad(cn, leaves, dcn)
 
 
 class _CsaCoreFunction(torch.autograd.Function):
@@ -633,14 +726,24 @@ class _CsaCoreFunction(torch.autograd.Function):
     def backward(ctx, d_out, _d_idx):
         Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, sink, idx = ctx.saved_tensors
         cfg = ctx.cfg
+        full = cfg["use_ste"] and cfg["ste_mode"] == "full_softmax" and idx.shape[-1] > 0
         g = csa_attn_grad(Ca, Cb, Za, Zb, q, Ba, Bb, idx if idx.shape[-1] else None, d_out,
                           m=cfg["m"], sliding_window=cfg["sliding_window"], sink_logits=sink,
-                          normalize_qk=cfg["normalize_qk"], scale=cfg["scale"])
+                          normalize_qk=cfg["normalize_qk"], scale=cfg["scale"], want_gsum=full)
+        dsel_extra = None
+        if full:
+            dsel_extra, extra = _full_softmax_grads(
+                Ca, Cb, Za, Zb, Ba, Bb, K_idx, Z_idx, q_idx, w_idx, B_idx, g["gsum"],
+                m=cfg["m"], normalize_qk=cfg["normalize_qk"])
+            for name, x, e in zip(("Ca", "Cb", "Za", "Zb", "Ba", "Bb"), (Ca, Cb, Za, Zb, Ba, Bb),
+                                  extra):
+                g[name] = (g[name].to(torch.float32) + e).to(x.dtype)
         ig = [None] * 5
         if cfg["use_ste"] and idx.shape[-1] and any(
                 x.requires_grad for x in (K_idx, Z_idx, q_idx, w_idx, B_idx)):
             ig = _ste_indexer_grads(K_idx, Z_idx, q_idx, w_idx, B_idx, idx, g["slot"],
-                                    m=cfg["m"], normalize_qk=cfg["normalize_qk"])
+                                    m=cfg["m"], normalize_qk=cfg["normalize_qk"],
+                                    dsel_extra=dsel_extra)
         return (g["Ca"], g["Cb"], g["Za"], g["Zb"], ig[0], ig[1], g["q"], ig[2], ig[3], g["Ba"],
                 g["Bb"], ig[4], g.get("sink_logits"), None)
 
@@ -696,6 +799,14 @@ def naive_csa(H, W_aKV, W_bKV, W_aZ, W_bZ, Ba, Bb, W_DQ, W_UQ, W_IUQ, W_w, W_KV_
             raise ValueError(
                 f"naive_csa: {_w_name}.shape={tuple(_w.shape)} — second dim "
                 f"(in_features) must equal d={d} (H.shape[-1]).")
+    if ste_mode == 'aux_contrastive':
+        # raised by the reference's indexer call (ops_csa.py:486-491), which
+        # every non-empty input reaches
+        raise NotImplementedError(
+            "ste_mode='aux_contrastive' is reserved for a future implementation of "
+            "DeepSeek-V4's contrastive auxiliary loss on the indexer selection logits. "
+            "Use 'topk_columns' (the default, simplified STE) or 'full_softmax' (dense STE) "
+            "for now.")
     _check_gpu_dtype(fn, H)
     if c > _HEAD_DIMS[-1] or c_I > _IDX_DIMS[-1] or nIh > _IDX_HEADS[-1]:
         raise NotImplementedError(
@@ -714,9 +825,6 @@ def naive_csa(H, W_aKV, W_bKV, W_aZ, W_bZ, Ba, Bb, W_DQ, W_UQ, W_IUQ, W_w, W_KV_
                                   and torch.is_grad_enabled()):
         # training: the projections through autograd (library GEMMs), the core
         # through its HIP backward and, with use_ste, the STE surrogate
-        if use_ste and ste_mode != 'topk_columns':
-            raise NotImplementedError(
-                f"{fn}: gradients for ste_mode={ste_mode!r} are not provided (topk_columns is)")
         Ca, Cb, Za, Zb, K_idx_raw, Z_idx, cQ, w_idx = F.linear(
             H, torch.cat([W_aKV, W_bKV, W_aZ, W_bZ, W_KV_idx, W_Z_idx, W_DQ, W_w])).split(
             [c, c, c, c, c_I, c_I, dc, nIh], dim=-1)
@@ -724,7 +832,8 @@ def naive_csa(H, W_aKV, W_bKV, W_aZ, W_bZ, Ba, Bb, W_DQ, W_UQ, W_IUQ, W_w, W_KV_
         q = F.linear(cQ, W_UQ).view(B_, T, nh, c)
         out = csa_core(Ca, Cb, Za, Zb, K_idx_raw, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, m=m,
                        topk=topk, sliding_window=sliding_window, sink_logits=sink_logits,
-                       normalize_qk=normalize_qk, scale=scale, use_ste=use_ste)
+                       normalize_qk=normalize_qk, scale=scale, use_ste=use_ste,
+                       ste_mode=ste_mode)
         out_final = out.reshape(B_, T, nh * c)[:, :original_T]
         if return_projections:
             return out_final, tuple(x[:, :original_T] for x in (Ca, Cb, Za, Zb, K_idx_raw, Z_idx))

@@ -14,6 +14,11 @@ Functions and the reference lines each restates:
 ``naive_csa``                ``naive_csa`` incl. bf16 projections, ``ops_csa.py:576-1184``
 ``hca_core``                 ``naive_hca`` after the projections, ``ops_hca.py:132-194``
 ``naive_hca``                ``naive_hca`` incl. bf16 projections, ``ops_hca.py:30-201``
+``hca_core_grad``            ``naive_hca``'s autograd backward, ``ops_hca.py:132-194``
+``csa_attn_grad``            ``naive_csa``'s attention backward, ``ops_csa.py:869-1155``
+``csa_ste_grad``             the STE surrogate's backward, ``ops_csa.py:1033-1099``
+                             (``topk_columns``, ``full_softmax``); pinned by the
+                             reference's gradients (``tests/golden/csa_ste_fp32.npz``)
 
 Tie rule: ``torch.topk`` (``ops_csa.py:550``) does not document its order on
 exactly-equal logits (the reference notes it depends on the tensor size,
@@ -620,7 +625,9 @@ def csa_attn_grad(Ca, Cb, Za, Zb, q, Ba, Bb, idx, d_out, *, m, sliding_window=0,
     backward. Also returns ``slot``: per selected slot, the gradient of the
     gathered row dotted with that row (``sum_h p ((dp - D) s + dp)``), the
     quantity the STE surrogate (``ops_csa.py:1033-1099``) turns into the
-    indexer's gradient."""
+    indexer's gradient, and ``gsum`` ``[B,T,c]``: the gathered rows'
+    gradients summed over the slots (the cotangent of ``full_softmax``'s
+    zero-in-forward term, ``ops_csa.py:1050-1071``)."""
     f = np.float64
     Ca, Cb, Za, Zb, q, d_out = (np.asarray(x, f) for x in (Ca, Cb, Za, Zb, q, d_out))
     Bn, T, c = Ca.shape
@@ -678,7 +685,8 @@ def csa_attn_grad(Ca, Cb, Za, Zb, q, Ba, Bb, idx, d_out, *, m, sliding_window=0,
             ok = src >= 0
             np.add.at(dCl, (slice(None), src[ok]), dCw[:, ok, i])
         dCa = dCa + (_l2n_grad(Ca, dCl) if normalize_qk else dCl)
-    g = dict(Ca=dCa, Cb=dCb, Za=dZa, Zb=dZb, q=dq, Ba=dBa, Bb=dBb, slot=slot)
+    g = dict(Ca=dCa, Cb=dCb, Za=dZa, Zb=dZb, q=dq, Ba=dBa, Bb=dBb, slot=slot,
+             gsum=dkv.sum(axis=2))
     if sink is not None:
         row_max = np.maximum(np.where(cat_valid, cat, -np.inf).max(-1, keepdims=True), 0) \
             if cat.shape[-1] else np.zeros((Bn, T, nh, 1))
@@ -686,4 +694,78 @@ def csa_attn_grad(Ca, Cb, Za, Zb, q, Ba, Bb, idx, d_out, *, m, sliding_window=0,
             lse = np.log(np.where(cat_valid, np.exp(cat - row_max), 0).sum(-1, keepdims=True)) + row_max
         p_sink = np.exp(sink - np.logaddexp(lse, sink))
         g['sink_logits'] = -(p_sink * D).sum(axis=(0, 1, 3))
+    return g
+
+
+def csa_ste_grad(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, idx, d_out, *,
+                 m, sliding_window=0, sink_logits=None, normalize_qk=True, scale=None,
+                 ste_mode='topk_columns'):
+    """Gradients of ``csa_core`` with the straight-through surrogate
+    (``ops_csa.py:1033-1099``), the selection ``idx`` held fixed, in fp64; T a
+    multiple of m.
+
+    The forward value is the hard top-k path; the backward adds, through
+    ``kv + (soft_kv - soft_kv.detach())`` with ``soft_kv = soft[idx] kv``:
+
+    * the soft weights' cotangent: ``slot`` (``csa_attn_grad``) at the selected
+      columns; with ``ste_mode='full_softmax'`` also ``gsum C_comp_n^T`` at
+      every column, and ``C_comp_n`` receives ``soft^T gsum`` (the expected
+      row ``soft @ C_comp_n``, broadcast over the slots, enters as
+      ``aux - aux.detach()``, ``ops_csa.py:1050-1071``);
+    * the softmax backward over the causal blocks (``ops_csa.py:545-572``),
+      ``dl = soft (dsoft - sum soft dsoft)``;
+    * the indexer logits ``lg = sum_h w_h relu(a_h)``,
+      ``a_h = scale qn_h . kn`` (``ops_csa.py:503-536``): ``dw_h = sum_n dl
+      relu(a_h)``, ``da_h = dl w_h [a_h > 0]``, then ``dqn``, ``dkn``;
+    * the L2-norm backwards and the key compression's (``ops_csa.py:198-234``).
+
+    Returns the dict of ``csa_attn_grad`` plus ``K_idx, Z_idx, q_idx, w_idx,
+    B_idx``."""
+    if ste_mode not in ('topk_columns', 'full_softmax'):
+        raise ValueError(f"ste_mode={ste_mode!r}")
+    f = np.float64
+    g = csa_attn_grad(Ca, Cb, Za, Zb, q, Ba, Bb, idx, d_out, m=m, sliding_window=sliding_window,
+                      sink_logits=sink_logits, normalize_qk=normalize_qk, scale=scale)
+    Bn, T, c = np.shape(Ca)
+    nb = T // m
+    cI = np.shape(K_idx)[-1]
+    kraw = compress_kv(np.asarray(K_idx, f), np.asarray(Z_idx, f), B_idx, m, f)
+    kn = l2_normalize(kraw) if normalize_qk else kraw
+    qi = np.asarray(q_idx, f)
+    qin = l2_normalize(qi) if normalize_qk else qi
+    iscale = 1.0 if normalize_qk else cI ** -0.5
+    w = np.asarray(w_idx, f)
+    a = np.einsum('bthd,bnd->bthn', qin, kn) * iscale
+    relu = np.maximum(a, 0.0)
+    lg = np.einsum('bthn,bth->btn', relu, w)
+    lg = np.where(causal_block_mask(T, nb, m)[None], lg, -np.inf)
+    finite = np.isfinite(lg)
+    any_vis = finite.any(-1, keepdims=True)
+    mx = np.where(any_vis, np.where(finite, lg, -np.inf).max(-1, keepdims=True), 0.0)
+    e = np.where(finite, np.exp(np.where(finite, lg, 0.0) - mx), 0.0)
+    soft = np.where(any_vis, e / np.where(any_vis, e.sum(-1, keepdims=True), 1.0), 0.0)
+    idx = np.asarray(idx, np.int64)
+    valid = idx >= 0
+    dsoft = np.zeros((Bn, T, nb))
+    bi, ti = np.broadcast_to(np.arange(Bn)[:, None, None], idx.shape), \
+        np.broadcast_to(np.arange(T)[None, :, None], idx.shape)
+    np.add.at(dsoft, (bi[valid], ti[valid], idx[valid]), g['slot'][valid])
+    if ste_mode == 'full_softmax':
+        raw = compress_kv_overlapped(np.asarray(Ca, f), Cb, Za, Zb, Ba, Bb, m, f)
+        cn = l2_normalize(raw) if normalize_qk else raw
+        dsoft = dsoft + np.einsum('btc,bnc->btn', g['gsum'], cn)
+        dcn = np.einsum('btn,btc->bnc', soft, g['gsum'])
+        draw = _l2n_grad(raw, dcn) if normalize_qk else dcn
+        for name, x in zip(('Ca', 'Cb', 'Za', 'Zb', 'Ba', 'Bb'),
+                           compress_kv_overlapped_grad(Ca, Cb, Za, Zb, Ba, Bb, m, draw)):
+            g[name] = g[name] + x
+    dl = soft * (dsoft - (soft * dsoft).sum(-1, keepdims=True))
+    dw = np.einsum('btn,bthn->bth', dl, relu)
+    da = dl[:, :, None, :] * w[..., None] * (a > 0)
+    dqin = iscale * np.einsum('bthn,bnd->bthd', da, kn)
+    dkn = iscale * np.einsum('bthn,bthd->bnd', da, qin)
+    dqi = _l2n_grad(qi, dqin) if normalize_qk else dqin
+    dkraw = _l2n_grad(kraw, dkn) if normalize_qk else dkn
+    dK, dZ, dB = compress_kv_grad(K_idx, Z_idx, B_idx, m, dkraw)
+    g.update(K_idx=dK, Z_idx=dZ, q_idx=dqi, w_idx=dw, B_idx=dB)
     return g

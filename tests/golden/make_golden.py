@@ -24,7 +24,14 @@ choice among exactly equal logits.
   (``ops_fused.py:956-1128``) and ``HybridDecoding`` (``run_decoding.py:601-851``,
   with the model swapped for one of this geometry): prefill, then decode steps;
 * ``indexer_ties.npz``    ``csa_lightning_indexer`` (``ops_csa.py:330-573``) on
-  keys with duplicated rows (exactly equal logits) and ReLU-zero logits.
+  keys with duplicated rows (exactly equal logits) and ReLU-zero logits;
+* ``csa_ste_fp32.npz``    the gradients of ``naive_csa`` in fp32 with the
+  straight-through surrogate (``ops_csa.py:1033-1099``), ``ste_mode``
+  ``topk_columns`` and ``full_softmax``, of the loss ``sum(out * G)``: every
+  weight's, the sink's and H's, with and without ``normalize_qk``.
+
+``python tests/golden/make_golden.py NAME ...`` writes only the named fixtures
+(``kda_ops kda_layer csa_hca caches hybrid indexer_ties csa_ste``).
 
 Inputs come from ``numpy.random.default_rng`` with fixed seeds; bf16 tensors
 are stored as their 16-bit patterns (``*_bf16`` keys), fp32 tensors as float32.
@@ -349,17 +356,105 @@ def make_indexer_ties(ref):
                         meta=np.array([B, T, nIh, cI, m, topk], np.int64))
 
 
+CSA_STE_NAMES = ("W_aKV", "W_bKV", "W_aZ", "W_bZ", "Ba", "Bb", "W_DQ", "W_UQ", "W_IUQ", "W_w",
+                 "W_KV_idx", "W_Z_idx", "B_idx")
+
+
+def _boundary_tie(H, P, m, topk, nIh, cI, norm):
+    """Whether any query's k-th and (k+1)-th indexer logits (fp64, from the
+    fp32 projections) are exactly equal: there ``torch.topk``'s choice among
+    the tied blocks is unspecified, so such inputs are not used."""
+    import torch
+    f = lambda a: torch.from_numpy(np.asarray(a, np.float64))  # noqa: E731
+    Hd = f(H)
+    K, Z = Hd @ f(P["W_KV_idx"]).T, Hd @ f(P["W_Z_idx"]).T
+    B, T, _ = K.shape
+    nb = T // m
+    wts = torch.softmax(Z.view(B, nb, m, cI) + f(P["B_idx"]), dim=2)
+    kc = (wts * K.view(B, nb, m, cI)).sum(2)
+    qi = ((Hd @ f(P["W_DQ"]).T) @ f(P["W_IUQ"]).T).view(B, T, nIh, cI)
+    wi = Hd @ f(P["W_w"]).T
+    if norm:
+        kc, qi = torch.nn.functional.normalize(kc, dim=-1), torch.nn.functional.normalize(qi, dim=-1)
+    sc = 1.0 if norm else cI ** -0.5
+    lg = torch.einsum('bhtn,bth->btn', torch.relu(torch.einsum('bthd,bnd->bhtn', qi, kc) * sc), wi)
+    for t in range(T):
+        vis = (t + 1) // m
+        if vis > topk:
+            v = torch.sort(lg[:, t, :vis], dim=-1, descending=True).values
+            if bool((v[:, topk - 1] == v[:, topk]).any()):
+                return True
+    return False
+
+
+def make_csa_ste(ref):
+    """fp32 ``naive_csa`` with ``use_ste=True`` under gradients: for each
+    (``normalize_qk``, ``ste_mode``) the output, the selection the indexer made
+    and the gradients of ``sum(out * G)``. Inputs whose selection would pass
+    through an exact tie at the top-k boundary are skipped (the next seed)."""
+    import torch
+    _, ops_csa, _, _, _, _ = ref
+    for seed in range(211, 400):
+        H, P, sink, G = _csa_ste_inputs(seed)
+        if not any(_boundary_tie(H, P, 4, 4, 4, 8, norm) for norm in (True, False)):
+            break
+    else:
+        raise SystemExit("no tie-free inputs found")
+    B, T, d, c, nh, dc, nIh, cI, m, win, topk = 1, 48, 32, 16, 2, 16, 4, 8, 4, 4, 4
+    out = {"H": H, "sink": sink, "G": G, "seed": np.array(seed)}
+    out.update({f"w.{k}": v for k, v in P.items()})
+    for norm in (True, False):
+        for mode in ("topk_columns", "full_softmax"):
+            tag = f"{'norm' if norm else 'raw'}.{mode}"
+            ts = {k: torch.from_numpy(v).requires_grad_(True) for k, v in P.items()}
+            Ht = torch.from_numpy(H).requires_grad_(True)
+            st = torch.from_numpy(sink).requires_grad_(True)
+            SELECTIONS.clear()
+            o = ops_csa.naive_csa(Ht, *[ts[n] for n in CSA_STE_NAMES], m=m, topk=topk, nh=nh,
+                                  nIh=nIh, c=c, c_I=cI, dc=dc, sliding_window=win,
+                                  sink_logits=st, use_ste=True, ste_mode=mode,
+                                  normalize_qk=norm)
+            (o * torch.from_numpy(G)).sum().backward()
+            assert len(SELECTIONS) == 1
+            out[f"{tag}.out"] = f32(o)
+            out[f"{tag}.idx"] = SELECTIONS[0]
+            out[f"{tag}.dH"] = f32(Ht.grad)
+            out[f"{tag}.dsink"] = f32(st.grad)
+            for n in CSA_STE_NAMES:
+                out[f"{tag}.d{n}"] = f32(ts[n].grad)
+    out["meta"] = np.array([B, T, d, c, nh, dc, nIh, cI, m, win, topk], np.int64)
+    np.savez_compressed(os.path.join(HERE, "csa_ste_fp32.npz"), **out)
+
+
+def _csa_ste_inputs(seed):
+    rng = np.random.default_rng(seed)
+    B, T, d, c, nh, dc, nIh, cI, m = 1, 48, 32, 16, 2, 16, 4, 8, 4
+    P = {n: rng.standard_normal((c, d)) / np.sqrt(d) for n in ("W_aKV", "W_bKV", "W_aZ", "W_bZ")}
+    P.update(Ba=0.3 * rng.standard_normal((m, c)), Bb=0.3 * rng.standard_normal((m, c)),
+             W_DQ=rng.standard_normal((dc, d)) / np.sqrt(d),
+             W_UQ=rng.standard_normal((c * nh, dc)) / np.sqrt(dc),
+             W_IUQ=rng.standard_normal((cI * nIh, dc)) / np.sqrt(dc),
+             W_w=rng.standard_normal((nIh, d)) / np.sqrt(d),
+             W_KV_idx=rng.standard_normal((cI, d)) / np.sqrt(d),
+             W_Z_idx=rng.standard_normal((cI, d)) / np.sqrt(d),
+             B_idx=0.3 * rng.standard_normal((m, cI)))
+    P = {k: v.astype(np.float32) for k, v in P.items()}
+    H = rng.standard_normal((B, T, d)).astype(np.float32)
+    sink = rng.standard_normal(nh).astype(np.float32)
+    G = rng.standard_normal((B, T, nh * c)).astype(np.float32)
+    return H, P, sink, G
+
+
 def main():
     import torch
     torch.manual_seed(0)
     torch.set_num_threads(1)
     ref = _import_reference()
-    make_kda_ops(ref)
-    make_kda_layer(ref)
-    make_csa_hca(ref)
-    make_caches(ref)
-    make_hybrid(ref)
-    make_indexer_ties(ref)
+    makers = dict(kda_ops=make_kda_ops, kda_layer=make_kda_layer, csa_hca=make_csa_hca,
+                  caches=make_caches, hybrid=make_hybrid, indexer_ties=make_indexer_ties,
+                  csa_ste=make_csa_ste)
+    for name in (sys.argv[1:] or list(makers)):
+        makers[name](ref)
     for f in sorted(os.listdir(HERE)):
         if f.endswith(".npz"):
             print(f"{f}: {os.path.getsize(os.path.join(HERE, f)) / 1024:.1f} KiB")

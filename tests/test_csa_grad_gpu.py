@@ -16,7 +16,15 @@ held fixed, and adds a straight-through surrogate for the indexer
   CPU on the selection the kernel made: every gradient, indexer inputs
   included, within 1e-4 of its largest entry;
 * the reference's contract: ``use_ste`` does not change the forward value, and
-  every indexer weight of ``naive_csa`` gets a finite, non-zero gradient.
+  every indexer weight of ``naive_csa`` gets a finite, non-zero gradient;
+* ``naive_csa`` in fp32 with ``use_ste=True`` against the reference's own
+  gradients (``tests/golden/csa_ste_fp32.npz``, both ``ste_mode`` values,
+  with and without ``normalize_qk``): the selection the reference made, and
+  every gradient (H, each weight, the sink) within 1e-4 of its largest entry;
+* ``full_softmax`` against ``oracle.csa.csa_ste_grad`` (itself pinned by that
+  fixture) at a shape with padded channels, and the reference's distinctness
+  contract (``run_correctness.py:1588-1731``): the same forward as
+  ``topk_columns``, a different and larger indexer gradient.
 """
 
 from __future__ import annotations
@@ -26,7 +34,9 @@ import pytest
 import torch
 import torch.nn.functional as F
 
+import ste_fixture as SF
 from oracle.csa import csa_attn_grad as o_grad
+from oracle.csa import csa_ste_grad as o_ste_grad
 
 pytestmark = pytest.mark.gpu
 
@@ -258,3 +268,85 @@ def test_ste_kernel_matches_dense_statement(dev, nIh, cI, norm):
     torch.cuda.synchronize()
     for name, a, r in zip(("K_idx", "Z_idx", "q_idx", "w_idx", "B_idx"), got, ref):
         _check(name, a.cpu().numpy(), r.cpu().numpy())
+
+
+@pytest.mark.parametrize("norm,mode", SF.CASES)
+def test_naive_csa_ste_grads_match_reference_fixture(dev, norm, mode):
+    import kch
+    z, meta, W = SF.load()
+    t = SF.tag(norm, mode)
+    Wt = {k: torch.tensor(v, device=dev, requires_grad=True) for k, v in W.items()}
+    H = torch.tensor(z["H"], device=dev, requires_grad=True)
+    sk = torch.tensor(z["sink"], device=dev, requires_grad=True)
+    with kch.record_selections() as sel:
+        out = kch.naive_csa(H, *[Wt[n] for n in SF.NAMES], m=meta["m"], topk=meta["topk"],
+                            nh=meta["nh"], nIh=meta["nIh"], c=meta["c"], c_I=meta["cI"],
+                            dc=meta["dc"], sliding_window=meta["win"], sink_logits=sk,
+                            use_ste=True, ste_mode=mode, normalize_qk=norm)
+    (out * torch.tensor(z["G"], device=dev)).sum().backward()
+    torch.cuda.synchronize()
+    got_idx = sel[0].cpu().numpy().astype(np.int64)
+    ref_idx = z[f"{t}.idx"]
+    assert got_idx.shape == ref_idx.shape
+    for r, (a, b) in enumerate(zip(got_idx.reshape(-1, got_idx.shape[-1]),
+                                   ref_idx.reshape(-1, ref_idx.shape[-1]))):
+        assert set(a.tolist()) == set(b.tolist()), f"row {r}: {a} vs the reference's {b}"
+    _check("out", out.detach().cpu().numpy(), z[f"{t}.out"], 1e-2)
+    got = {f"d{n}": Wt[n].grad.cpu().numpy() for n in SF.NAMES}
+    got["dH"] = H.grad.cpu().numpy()
+    got["dsink"] = sk.grad.cpu().numpy()
+    err = SF.worst_rel(got, z, t)
+    bad = {k: v for k, v in err.items() if v > 1e-4}
+    assert not bad, bad
+
+
+@pytest.mark.parametrize("norm", [True, False])
+def test_csa_core_full_softmax_matches_oracle(dev, norm):
+    import kch
+    rng = np.random.default_rng(61 + norm)
+    B, T, nh, c, m, topk, win, cI, nIh = 2, 64, 3, 40, 4, 5, 6, 24, 3
+    shapes = dict(Ca=(B, T, c), Cb=(B, T, c), Za=(B, T, c), Zb=(B, T, c), K_idx=(B, T, cI),
+                  Z_idx=(B, T, cI), q=(B, T, nh, c), q_idx=(B, T, nIh, cI), w_idx=(B, T, nIh),
+                  Ba=(m, c), Bb=(m, c), B_idx=(m, cI))
+    X = {k: rng.standard_normal(s) * (0.3 if k.startswith("B") else 1.0) for k, s in shapes.items()}
+    sk = rng.standard_normal(nh)
+    Gw = rng.standard_normal((B, T, nh, c))
+    names = ("Ca", "Cb", "Za", "Zb", "K_idx", "Z_idx", "q", "q_idx", "w_idx", "Ba", "Bb", "B_idx")
+    grads, outs = {}, {}
+    for mode in ("topk_columns", "full_softmax"):
+        xt = {k: torch.tensor(v, dtype=torch.float32, device=dev, requires_grad=True)
+              for k, v in X.items()}
+        st = torch.tensor(sk, dtype=torch.float32, device=dev, requires_grad=True)
+        out, idx = kch.csa_core(*[xt[k] for k in names], m=m, topk=topk, sliding_window=win,
+                                sink_logits=st, normalize_qk=norm, return_indices=True,
+                                use_ste=True, ste_mode=mode)
+        (out.double() * torch.tensor(Gw, device=dev)).sum().backward()
+        torch.cuda.synchronize()
+        grads[mode] = {k: xt[k].grad.cpu().numpy() for k in X}
+        grads[mode]["sink_logits"] = st.grad.cpu().numpy()
+        outs[mode] = out.detach().cpu().numpy()
+        if mode == "full_softmax":
+            ref = o_ste_grad(*[X[k] for k in names], idx.cpu().numpy(), Gw, m=m,
+                             sliding_window=win, sink_logits=sk, normalize_qk=norm,
+                             ste_mode=mode)
+            for k in list(X) + ["sink_logits"]:
+                _check(k, grads[mode][k], ref[k])
+    # run_correctness.py:1588-1731: same forward, distinct and larger indexer gradient
+    np.testing.assert_array_equal(outs["topk_columns"], outs["full_softmax"])
+    for k in ("K_idx", "q_idx", "w_idx"):
+        a, b = grads["topk_columns"][k], grads["full_softmax"][k]
+        assert np.abs(a - b).max() > 1e-6 * np.abs(b).max(), k
+    assert np.abs(grads["full_softmax"]["K_idx"]).sum() > np.abs(grads["topk_columns"]["K_idx"]).sum()
+
+
+def test_naive_csa_aux_contrastive_raises(dev):
+    import kch
+    B, T, d, c, nh, dc, nIh, cI, m = 1, 8, 16, 8, 2, 8, 2, 4, 4
+    H = torch.randn(B, T, d, device=dev)
+    P = dict(W_aKV=(c, d), W_bKV=(c, d), W_aZ=(c, d), W_bZ=(c, d), Ba=(m, c), Bb=(m, c),
+             W_DQ=(dc, d), W_UQ=(c * nh, dc), W_IUQ=(cI * nIh, dc), W_w=(nIh, d),
+             W_KV_idx=(cI, d), W_Z_idx=(cI, d), B_idx=(m, cI))
+    ps = [torch.randn(*s, device=dev) for s in P.values()]
+    with pytest.raises(NotImplementedError):
+        kch.naive_csa(H, *ps, m=m, topk=2, nh=nh, nIh=nIh, c=c, c_I=cI, dc=dc,
+                      ste_mode='aux_contrastive')

@@ -50,25 +50,65 @@ def test_layer_norm_grad(dev, dtype, tol):
     _check("db", ln.bias.grad, br.grad, tol)
 
 
-@pytest.mark.parametrize("lookback", [False, True])
-def test_short_conv_grad(dev, lookback):
+@pytest.mark.parametrize("lookback,T", [(False, 75), (True, 75), ("grad", 75), ("grad", 1),
+                                         ("grad", 2)])
+def test_short_conv_grad(dev, lookback, T):
+    """``lookback="grad"``: a lookback that requires grad (the previous
+    chunk's rows kept in its graph) gets its gradient, compared with autograd
+    of ``F.conv1d`` over ``[lookback ; x]`` (the reference's depthwise conv,
+    ``ops_fused.py:480-527``)."""
     from kch.hybrid import _ShortConvFn
     torch.manual_seed(1)
-    B, T, d = 2, 75, 40
+    B, d = 2, 40
     x = torch.randn(B, T, d, device=dev, requires_grad=True)
     w = torch.randn(d, 1, 3, device=dev, requires_grad=True)
     b = torch.randn(d, device=dev, requires_grad=True)
     lb = torch.randn(B, 2, d, device=dev) if lookback else None
+    if lookback == "grad":
+        lb.requires_grad_(True)
     G = torch.randn(B, T, d)
     (_ShortConvFn.apply(x, w, b, lb).double().cpu() * G).sum().backward()
     xr, wr, br = (t.detach().double().cpu().requires_grad_(True) for t in (x, w, b))
-    pre = lb.double().cpu() if lookback else torch.zeros(B, 2, d, dtype=torch.float64)
+    pre = (lb.detach().double().cpu() if lookback
+           else torch.zeros(B, 2, d, dtype=torch.float64)).requires_grad_(True)
     xp = torch.cat([pre, xr], 1)
-    out = br + wr[:, 0, 0] * xp[:, :-2] + wr[:, 0, 1] * xp[:, 1:-1] + wr[:, 0, 2] * xp[:, 2:]
+    out = F.conv1d(xp.transpose(1, 2), wr, br, groups=d).transpose(1, 2)
     (out * G).sum().backward()
     _check("dx", x.grad, xr.grad)
     _check("dw", w.grad, wr.grad)
     _check("db", b.grad, br.grad)
+    if lookback == "grad":
+        _check("dlookback", lb.grad, pre.grad)
+    elif lookback:
+        assert lb.grad is None
+
+
+def test_kda_cross_chunk_bptt(dev):
+    """``run_correctness.py:1731-1833`` on the HIP layer (fp32): with
+    ``detach_lookback=True`` chunk 2's output does not reach chunk 1's input;
+    with ``detach_lookback=False`` it does, through the lookback only (the
+    state is detached): the gradient is non-zero on chunk 1's last two rows
+    and zero on the others. The lookback gradient itself is checked against
+    ``F.conv1d`` in ``test_short_conv_grad``."""
+    import kch
+    torch.manual_seed(123)
+    cfg = kch.HybridConfig(d_model=16, n_heads_qk=2, n_heads_v=2, head_dim_k=8, head_dim_v=8,
+                           kda_chunk_size=0, n_kda=1, n_csa=0, n_hca=0)
+    layer = kch.KDAHybridLayer(cfg).to(dev)
+    x1 = torch.randn(1, 8, cfg.d_model, device=dev)
+    x2 = torch.randn(1, 8, cfg.d_model, device=dev)
+    grads = {}
+    for detach in (True, False):
+        xa = x1.clone().requires_grad_(True)
+        _, st, lb = layer.forward_functional(xa, None, None, detach_lookback=detach)
+        o2, _, _ = layer.forward_functional(x2.clone(), st.detach(), lb, detach_lookback=detach)
+        o2.sum().backward()
+        grads[detach] = xa.grad
+    assert grads[True] is None or grads[True].abs().sum().item() < 1e-12
+    g = grads[False]
+    assert g is not None and torch.isfinite(g).all()
+    assert g[:, -2:].abs().sum().item() > 0
+    assert g[:, :-2].abs().sum().item() == 0
 
 
 def _gates_ref(proj, gl, H, HV, K, V, decay):
