@@ -229,10 +229,11 @@ int kch_layer_norm_bwd(const void* x, const void* w, const void* dy, void* dx, f
  *   C, Z   rows of c values, ld* elements apart (dtype); B_pos [m,c] fp32
  *   out_raw  [B,T/m,c] fp32 block values, or NULL
  *   out_key  [B,T/m,c] key rows, L2-normalised when `normalize`: bf16
- *            (key_f32 = 0), fp32 (1), or split (2): [B,T/m,3,c] bf16, each
+ *            (key_f32 = 0), fp32 (1), split (2): [B,T/m,3,c] bf16, each
  *            row's high, middle then low parts of its fp32 value
  *            (x = hi + mid + lo, the operands of kch_csa_indexer_topk with
- *            key_split); or NULL
+ *            key_split = 1), or (3, normalize only) [B,T/m,2,c] fp16, the
+ *            high then low parts of 256 x (key_split = 2); or NULL
  *   local    [B,T,c] bf16 per-token window keys L2norm(C) (raw C when not
  *            `normalize`), or NULL
  * T must be a multiple of m (callers right-pad as ops_csa.py:772-777 does).
@@ -257,9 +258,11 @@ int kch_compress_overlapped(const void* Ca, long long ldCa, const void* Cb, long
 /*
  * Lightning indexer + top-k. Replaces csa_lightning_indexer
  * (ops_csa.py:330-573) in its forward (hard top-k) form.
- *   q_idx [B,T,nIh,cI] (dtype), k_idx [B,nb,cI] fp32, or with key_split
+ *   q_idx [B,T,nIh,cI] (dtype), k_idx [B,nb,cI] fp32, or with key_split = 1
  *   [B,nb,3,cI] bf16 high / middle / low parts of each row (kch_compress
- *   key_f32 = 2); logits carry fp32-level error (three-part bf16 products);
+ *   key_f32 = 2), or with key_split = 2 (normalize_q only) [B,nb,2,cI] fp16
+ *   high / low parts of 256 x (key_f32 = 3); the logits carry fp32-level
+ *   error (three-part bf16 or two-part fp16 products);
  *   already L2-normalised when normalize_q. w_idx [B,T,nIh] (dtype) or NULL
  *   (= all ones)
  *   idx_out [B,T,topk] int64 (idx64) or int32: the top-k blocks by descending

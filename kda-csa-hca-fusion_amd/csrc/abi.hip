@@ -464,6 +464,9 @@ int kch_compress(const void* C, long long ldC, const void* Z, long long ldZ, con
   if (B < 0 || T < 0 || c < 1) return fail(KCH_ERR_INVALID, "%s: bad sizes B=%d T=%d c=%d", fn, B, T, c);
   if (T % m) return fail(KCH_ERR_INVALID, "%s: T=%d must be divisible by m=%d", fn, T, m);
   if (c > 128) return fail(KCH_ERR_UNSUPPORTED, "%s: c=%d > 128 not supported", fn, c);
+  if (key_f32 < 0 || key_f32 > 3) return fail(KCH_ERR_INVALID, "%s: key format %d", fn, key_f32);
+  if (key_f32 == 3 && !normalize)
+    return fail(KCH_ERR_INVALID, "%s: fp16 split keys (key_f32=3) need normalize", fn);
   if (B * T == 0) return KCH_OK;
   if (!C || !Z || !B_pos) return fail(KCH_ERR_INVALID, "%s: null input pointer", fn);
   if (ldC < c || ldZ < c) return fail(KCH_ERR_INVALID, "%s: row strides must be >= c", fn);
@@ -505,6 +508,9 @@ int kch_csa_indexer_topk(const void* q_idx, const void* k_idx, const void* w_idx
     return fail(KCH_ERR_UNSUPPORTED, "%s: nIh=%d not in {1,2,4,8,16}", fn, nIh);
   if (cI != 32 && cI != 64 && cI != 128)
     return fail(KCH_ERR_UNSUPPORTED, "%s: cI=%d not in {32,64,128}", fn, cI);
+  if (key_split < 0 || key_split > 2) return fail(KCH_ERR_INVALID, "%s: key_split=%d", fn, key_split);
+  if (key_split == 2 && !normalize_q)
+    return fail(KCH_ERR_INVALID, "%s: fp16 split keys (key_split=2) need normalize_q", fn);
   if (B * T == 0 || topk == 0) return KCH_OK;
   if (!q_idx || !idx_out || (nb > 0 && !k_idx)) return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
   const long long lds = (long long)kch::indexer_lds_bytes(nb, nIh, topk);
@@ -518,7 +524,7 @@ int kch_csa_indexer_topk(const void* q_idx, const void* k_idx, const void* w_idx
   }
   kch::IndexerParams p{q_idx, k_idx, w_idx, idx_out, logits_out, B, T, nb, nIh, cI, topk, m,
                        pos0, normalize_q, idx64, dense_visible, sorted ? 1 : 0, scale, 0,
-                       key_split ? 1 : 0};
+                       key_split};
   return hip_status(fn, kch::indexer_dispatch(p, dtype, (hipStream_t)stream));
 }
 

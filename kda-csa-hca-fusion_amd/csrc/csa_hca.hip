@@ -23,10 +23,11 @@
 
 namespace kch {
 
-// One channel of a compressed key row: bf16 (key_f32 0), fp32 (1), or the
+// One channel of a compressed key row: bf16 (key_f32 0), fp32 (1), the
 // three bf16 parts x = hi + mid + lo of the fp32 value (2), stored as three
-// part rows [hi(c) | mid(c) | lo(c)] -- the split the indexer's MFMA products
-// use.
+// part rows [hi(c) | mid(c) | lo(c)], or (3, L2-normalised rows only) the two
+// fp16 parts of 256 x, [hi(c) | lo(c)] -- the splits the indexer's MFMA
+// products use.
 __device__ __forceinline__ void store_key(const CompressParams& p, size_t orow, int c, int ch,
                                           float x) {
   if (p.key_f32 == 1) {
@@ -39,6 +40,12 @@ __device__ __forceinline__ void store_key(const CompressParams& p, size_t orow, 
     row[ch] = hi;
     row[c + ch] = mid;
     row[2 * c + ch] = (bf16_t)(r - (float)mid);
+  } else if (p.key_f32 == 3) {
+    const float xs = x * kSplit16Scale;
+    const _Float16 hi = (_Float16)xs;
+    _Float16* row = static_cast<_Float16*>(p.out_key) + orow * 2 * c;
+    row[ch] = hi;
+    row[c + ch] = (_Float16)(xs - (float)hi);
   } else {
     static_cast<bf16_t*>(p.out_key)[orow * c + ch] = (bf16_t)x;
   }

@@ -532,7 +532,6 @@ struct KeyFrag {
   bf16x8 v;
   __device__ __forceinline__ void load(const KT* p) { v = *reinterpret_cast<const bf16x8*>(p); }
 };
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 template <>
 struct KeyFrag<_Float16> {
   f16x8 v;

@@ -12,12 +12,17 @@
 // Mapping: one 4-wave workgroup per group of QPW = 16 / nIh consecutive
 // queries; MFMA column n = (query n / nIh, head n % nIh). The waves split the
 // logits by 16-block chunk, then take one query's selection each. The key
-// rows come as fp32, or already split (KSPLIT: the three bf16 parts of each
-// row side by side, as the compression kernel writes them for csa_core),
-// which spares every workgroup the conversion. Scores use a three-part
-// split-bf16 product (x = hi + mid + lo on both sides; the six cross products
-// down to 2^-16 with fp32 accumulation) so the logits carry fp32-level error
-// (terms of 2^-24 dropped), as the reference's fp32 einsum does. Per query, the logits sit
+// rows come as fp32, or already split as the compression kernel writes them
+// for csa_core (which spares every workgroup the conversion). The logits carry
+// fp32-level error, as the reference's fp32 einsum does:
+//   KM 0: fp32 rows, split here into three bf16 parts (x = hi + mid + lo on
+//         both sides; the six cross products down to 2^-16, terms of 2^-24
+//         dropped);
+//   KM 1: rows of the three bf16 parts [hi | mid | lo], the same products;
+//   KM 2: L2-normalised rows as the two fp16 parts of 256 x [hi | lo] (q split
+//         the same way; hi*hi + hi*lo + lo*hi is 2^16 times the dot product to
+//         about 2^-22 relative): three MFMAs per step instead of six.
+// Per query, the logits sit
 // in LDS as 32-bit order keys. A row of up to 256 * RG visible blocks is
 // selected by one wave in registers (the k-th largest key found bit by bit
 // with ballot counts); a longer row by an 8-bit radix select in LDS. Either
@@ -26,6 +31,8 @@
 // when asked, they are bitonic-sorted by (logit desc, index asc). The head
 // count is a template parameter: with it known, the lane's (query, head)
 // split and the head sum compile to shifts and two or four lane exchanges.
+
+#include <type_traits>
 
 #include "attn_common.h"
 #include "kch_csa.h"
@@ -193,7 +200,7 @@ __device__ __forceinline__ void select_in_registers(const float* lg, int nv, int
 
 }  // namespace
 
-template <typename QT, int CI, int NIH, bool KSPLIT>
+template <typename QT, int CI, int NIH, int KM>
 __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   constexpr int NS = CI / 32;
@@ -232,7 +239,9 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
   const int jq = n / nIh, hh = n - jq * nIh;
   const int tq = t0 + jq;
   const bool qok = tq < p.T;
+  // q parts: bf16 hi / mid / lo (KM 0, 1) or fp16 hi / lo of 256 q (KM 2)
   bf16x8 qhi[NS], qmid[NS], qlo[NS];
+  f16x8 qh16[NS], ql16[NS];
   float wq = 0.f;
   {
     float f[NS][8];
@@ -250,7 +259,8 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
     for (int s = 0; s < NS; ++s) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) f[s][i] = qok ? f[s][i] * inv : 0.f;
-      split3_bf16(f[s], qhi[s], qmid[s], qlo[s]);
+      if constexpr (KM == 2) split2_f16(f[s], qh16[s], ql16[s]);
+      else split3_bf16(f[s], qhi[s], qmid[s], qlo[s]);
     }
     if (qok) {
       const size_t wi = ((size_t)b * p.T + tq) * nIh + hh;
@@ -266,22 +276,34 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
   // key rows of chunk c (row 16c + n, clamped: past the end the last row is
   // re-read and masked); wave w takes chunks w, w + 4, ..., D in flight;
   // refills are unconditional so that no loaded register is copied. A row is
-  // CI fp32 (4 bytes per channel, split here), or (KSPLIT) CI bf16 high parts,
-  // CI bf16 middle parts and CI bf16 low parts (6 bytes per channel).
+  // CI fp32 (KM 0: 4 bytes per channel, split here), CI bf16 high, middle and
+  // low parts (KM 1: 6 bytes per channel), or CI fp16 high and low parts
+  // (KM 2: 4 bytes per channel).
   constexpr int D = 4;
-  constexpr int ROW_BYTES = KSPLIT ? 6 * CI : 4 * CI;
+  constexpr int ROW_BYTES = KM == 1 ? 6 * CI : 4 * CI;
   const int nch = (nv_max + 15) / 16;
   const int mine = nch > wave ? (nch - wave + 3) / 4 : 0;
   // batch stride: k_bstride (4-byte units, fp32 rows only) or nb whole rows
-  const long long kbs = (!KSPLIT && p.k_bstride) ? p.k_bstride * 4 : (long long)nb * ROW_BYTES;
+  const long long kbs = (KM == 0 && p.k_bstride) ? p.k_bstride * 4 : (long long)nb * ROW_BYTES;
   const char* kbase = reinterpret_cast<const char*>(p.k_idx) + (size_t)b * kbs;
-  struct KFrag {
+  struct KFrag3 {
     bf16x8 hi[NS], mid[NS], lo[NS];
   };
+  struct KFrag2 {
+    f16x8 hi[NS], lo[NS];
+  };
+  using KFrag = std::conditional_t<KM == 2, KFrag2, KFrag3>;
   auto load = [&](int c, KFrag& kf) {
     const int r = min(16 * c + n, nb - 1);
     const char* krow = kbase + (size_t)r * ROW_BYTES;
-    if constexpr (KSPLIT) {
+    if constexpr (KM == 2) {
+      const _Float16* kh = reinterpret_cast<const _Float16*>(krow);
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        kf.hi[s] = *reinterpret_cast<const f16x8*>(kh + 32 * s + 8 * q4);
+        kf.lo[s] = *reinterpret_cast<const f16x8*>(kh + CI + 32 * s + 8 * q4);
+      }
+    } else if constexpr (KM == 1) {
       const bf16_t* kh = reinterpret_cast<const bf16_t*>(krow);
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
@@ -298,30 +320,43 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
       }
     }
   };
+  // the products' scale: 2^-16 undoes the fp16 parts' 256 on both sides
+  const float lscale = KM == 2 ? p.scale * kSplit16Unscale : p.scale;
   auto consume = [&](int c, const KFrag& kf) {
     // the smallest cross products first, so that each later (larger) term is
     // added to an accumulator of the smaller ones
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (KM == 2) {
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.mid[s], qmid[s], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.hi[s], qlo[s], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.lo[s], qhi[s], acc, 0, 0, 0);
+      for (int s = 0; s < NS; ++s) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf.hi[s], ql16[s], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf.lo[s], qh16[s], acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf.hi[s], qh16[s], acc, 0, 0, 0);
+    } else {
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.mid[s], qmid[s], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.hi[s], qlo[s], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.lo[s], qhi[s], acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.hi[s], qmid[s], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.mid[s], qhi[s], acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.hi[s], qhi[s], acc, 0, 0, 0);
     }
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.hi[s], qmid[s], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.mid[s], qhi[s], acc, 0, 0, 0);
-    }
-#pragma unroll
-    for (int s = 0; s < NS; ++s)
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.hi[s], qhi[s], acc, 0, 0, 0);
     // acc[e]: block 16c + 4*q4 + e, column n. No branch in here: the lanes
     // whose value is not kept write their own word of this wave's sink
     // words, since a branch costs the overlap of the chunks loaded ahead.
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float v = head_sum<NIH>(fmaxf(acc[e] * p.scale, 0.f) * wq);
+      const float v = head_sum<NIH>(fmaxf(acc[e] * lscale, 0.f) * wq);
       const int blk = 16 * c + 4 * q4 + e;
       float* dst = (hh == 0 && qok && blk < nv_me) ? logits + jq * ldl + blk
                                                    : sink + lane;
@@ -518,8 +553,9 @@ hipError_t indexer_dispatch(const IndexerParams& p, int dtype, hipStream_t s) {
   hipLaunchKernelGGL((indexer_kernel<QT, CI, NIH, KS>), dim3(groups), dim3(256), lds, s, p)
 #define KCH_IDX_NIH(QT, CI, NIH)                   \
   do {                                             \
-    if (p.k_split) KCH_IDX_T(QT, CI, NIH, true);   \
-    else KCH_IDX_T(QT, CI, NIH, false);            \
+    if (p.k_split == 2) KCH_IDX_T(QT, CI, NIH, 2); \
+    else if (p.k_split) KCH_IDX_T(QT, CI, NIH, 1); \
+    else KCH_IDX_T(QT, CI, NIH, 0);                \
   } while (0)
 #define KCH_IDX_LAUNCH(QT, CI)                \
   do {                                        \

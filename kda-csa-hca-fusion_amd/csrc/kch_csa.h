@@ -42,8 +42,10 @@ hipError_t attn_dispatch(const AttnParams& p, bool sparse, int qdtype, int odtyp
 // Lightning indexer + top-k.
 struct IndexerParams {
   const void* q_idx;     // [B, T, nIh, cI]
-  const void* k_idx;     // [B, nb, cI] fp32, or (k_split) [B, nb, 3, cI] bf16 high / middle /
-                         // low parts of each row; already L2-normalised when normalize
+  const void* k_idx;     // [B, nb, cI] fp32, or (k_split 1) [B, nb, 3, cI] bf16 high / middle /
+                         // low parts of each row, or (k_split 2, L2-normalised rows and
+                         // normalize_q) [B, nb, 2, cI] fp16 high / low parts of 256 x;
+                         // already L2-normalised when normalize
   const void* w_idx;     // [B, T, nIh] or null (= ones)
   void* idx_out;         // [B, T, topk] int32 or int64
   float* logits_out;     // optional [B, T, nb] fp32 (diagnostics / tests) or null
@@ -53,7 +55,7 @@ struct IndexerParams {
   int sorted;            // 1: indices by descending logit; 0: the same set in ascending index
   float scale;
   long long k_bstride;   // 4-byte units between batches of fp32 k_idx (0: nb * cI; split rows: nb rows)
-  int k_split;           // k_idx rows are split bf16 (high, middle, low) instead of fp32
+  int k_split;           // 0: fp32 rows; 1: bf16 three-part rows; 2: fp16 two-part rows
 };
 hipError_t indexer_dispatch(const IndexerParams& p, int dtype, hipStream_t s);
 size_t indexer_lds_bytes(int nb, int nIh, int topk);  // dynamic LDS of the indexer kernel

@@ -26,6 +26,7 @@ typedef __bf16 bf16_t;
 typedef bf16_t bf16x8 __attribute__((ext_vector_type(8)));
 typedef bf16_t bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 // 16-byte store of a large output stream (nontemporal: the lines are not kept
@@ -99,6 +100,24 @@ __device__ __forceinline__ void split3_bf16(const float* f, bf16x8& hi, bf16x8& 
     hi[i] = h;
     mid[i] = md;
     lo[i] = (bf16_t)(r - (float)md);
+  }
+}
+
+// Two-part fp16 split of components of unit vectors, prescaled by 2^8:
+// hi = fp16(256 x), lo = fp16(256 x - hi) (the difference is exact in fp32),
+// so hi + lo carries 22 significant bits of 256 x, and for |x| <= 1 no part
+// overflows or (down to |x| ~ 2^-20) leaves the normal range. A dot product
+// of two such splits from hi*hi + hi*lo + lo*hi (fp16 products are exact in
+// fp32) is 2^16 times the dot product, to about 2^-22 relative.
+constexpr float kSplit16Scale = 256.f;
+constexpr float kSplit16Unscale = 1.f / 65536.f;
+__device__ __forceinline__ void split2_f16(const float* f, f16x8& hi, f16x8& lo) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float x = f[i] * kSplit16Scale;
+    const _Float16 h = (_Float16)x;
+    hi[i] = h;
+    lo[i] = (_Float16)(x - (float)h);
   }
 }
 

@@ -1,18 +1,20 @@
 """Index parity of the HIP top-k selections against the oracle's (test helper).
 
-The kernels form indexer logits from three-part split-bf16 MFMA products
-(``x = hi + mid + lo``, each bf16, on both sides; the six cross products down
-to ``2^-16``, every one exact in fp32, accumulated in fp32) of L2-normalised
-fp32 rows: the dropped terms are below ``2^-24`` relative, so the logits carry
-the error of an fp32 computation, as the reference's fp32 einsum
-(``ops_csa.py:529-534``) does. Against the exact (fp64) logit of the same
-bf16 projections, the remaining error is the fp32 rounding of the compressed
-key, of the two L2 normalisations and of the 64- or 128-term dot product
-(a few units of ``2^-24`` each in a typical product of unit vectors). The
-bound used, ``eps = 1e-6 * sum_h |w_h| + 1e-7`` (about 17 units of ``2^-24``
-per unit of head weight), is asserted on the kernels' own logits wherever a
-test can read them (``check_logits``), so the selection rule below rests on a
-checked bound, not an assumed one.
+The kernels form indexer logits from split MFMA products of fp32 rows, every
+product exact in fp32 and accumulated in fp32: L2-normalised rows as the two
+fp16 parts of ``256 x`` (``hi*hi + hi*lo + lo*hi``: 22 significant bits per
+element, the dropped ``lo*lo`` at ``2^-22`` relative), other rows as three
+bf16 parts (``x = hi + mid + lo``, the six cross products down to ``2^-16``,
+terms of ``2^-24`` dropped). The logits thus carry the error of an fp32
+computation (a few units of ``2^-24`` per element), as the reference's fp32
+einsum (``ops_csa.py:529-534``) does, against ``2^-16`` for a two-part bf16
+split. Against the exact (fp64) logit of the same bf16 projections, the rest
+of the error is the fp32 rounding of the compressed key, of the two L2
+normalisations and of the 64- or 128-term dot product. The bound used,
+``eps = 1e-6 * sum_h |w_h| + 1e-7`` (4 units of ``2^-22`` per unit of head
+weight, the worst case of the fp16 split being 3), is asserted on the
+kernels' own logits wherever a test can read them (``check_logits``), so the
+selection rule below rests on a checked bound, not an assumed one.
 
 A HIP selection may differ from the oracle's (fp64 logits, ties by ascending
 block index) only where the k-th and (k+1)-th exact logits lie within

@@ -114,12 +114,12 @@ def test_csa_config2_late_queries(dev):
     # the kernel's own logits: the same compression and indexer launches, with
     # the logits written out
     nb = T // m
-    k_split = torch.empty(B, nb, 3 * cI, device=dev, dtype=torch.bfloat16)
+    k_split = torch.empty(B, nb, 2 * cI, device=dev, dtype=torch.float16)
     ops_csa._compress("t", proj[4], proj[5], par[2], m, out_raw=False, key=k_split,
-                      normalize=True, key_split=True)
+                      normalize=True, key_split=2)
     _, lg_dev = ops_csa._indexer("t", proj[7], k_split, proj[8], topk, 1.0, m, dense=False,
                                  normalize_q=True, idx64=False, want_logits=True,
-                                 sorted_=True, key_split=True)
+                                 sorted_=True, key_split=2)
     torch.cuda.synchronize()
     Q = np.concatenate([np.arange(4096, 4096 + 128), np.arange(6144, 6144 + 128),
                         np.arange(T - 128, T)])
