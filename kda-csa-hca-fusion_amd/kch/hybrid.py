@@ -84,6 +84,22 @@ def _linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     return y
 
 
+def _linear_residual(x: torch.Tensor, w: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
+    """``residual + F.linear(x, w)`` with the add in the GEMM's epilogue: one
+    ``addmm`` (C = the residual stream, beta = 1) reads the residual and writes
+    the new stream, so no separate add kernel reads both back. The sum is
+    rounded once to the stream's dtype (the reference rounds the projection,
+    then the sum: at most one unit in the last place apart). A decode step's
+    few rows keep ``_linear`` and the add."""
+    K = x.shape[-1]
+    rows = x.numel() // K if K else 0
+    if (rows <= 16 or not x.is_cuda or x.dtype != residual.dtype or w.dtype != x.dtype
+            or residual.shape[:-1] != x.shape[:-1]):
+        return residual + _linear(x, w)
+    out = torch.addmm(residual.reshape(rows, residual.shape[-1]), x.reshape(rows, K), w.t())
+    return out.view(residual.shape)
+
+
 def _grad_wanted(*ts) -> bool:
     return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts)
 
@@ -462,22 +478,26 @@ class KDAHybridLayer(_FusedWeightLayer):
         return self._fused.get(fused + [conv, bias, g_up], dtype, device, build)
 
     def forward(self, x: torch.Tensor, state: torch.Tensor | None = None, *,
-                state_out: torch.Tensor | None = None):
+                state_out: torch.Tensor | None = None, residual: torch.Tensor | None = None):
         """Stateful forward: reads and writes ``self._conv_lookback`` (``ops_fused.py:365-389``).
 
         ``state_out`` (fp32 ``[B,HV,K,V]``, contiguous; may be ``state`` itself)
-        receives the final state in place of a new tensor."""
+        receives the final state in place of a new tensor. With ``residual`` the
+        output is ``residual + o_proj(...)`` (the add fused into the GEMM)."""
         o, new_state, new_lookback = self.forward_functional(x, state, self._conv_lookback,
-                                                             state_out=state_out)
+                                                             state_out=state_out,
+                                                             residual=residual)
         self._conv_lookback = new_lookback
         return o, new_state
 
     def forward_functional(self, x: torch.Tensor, state: torch.Tensor | None,
                            conv_lookback: torch.Tensor | None, *, detach_lookback: bool = True,
-                           state_out: torch.Tensor | None = None):
+                           state_out: torch.Tensor | None = None,
+                           residual: torch.Tensor | None = None):
         """Side-effect-free forward (``ops_fused.py:391-609``).
 
-        Returns ``(output [B,T,d], new_state [B,HV,K,V] fp32, new_lookback [B,2,d] | None)``.
+        Returns ``(output [B,T,d], new_state [B,HV,K,V] fp32, new_lookback [B,2,d] | None)``;
+        with ``residual`` ``[B,T,d]`` the output is ``residual + o_proj(...)``.
         """
         B, T, d = x.shape
         cfg = self.cfg
@@ -490,7 +510,7 @@ class KDAHybridLayer(_FusedWeightLayer):
             lb = conv_lookback
             if lb is not None:
                 lb = None if lb.shape[0] != B else lb.to(device=x.device, dtype=x.dtype).clone()
-            return x.new_zeros(B, 0, d), new_state, lb
+            return (x.new_zeros(B, 0, d) if residual is None else residual.clone()), new_state, lb
         _lib.require_gpu("KDAHybridLayer", x)
         lookback = conv_lookback
         if lookback is not None:  # batch / device / dtype guards (ops_fused.py:500-518)
@@ -498,8 +518,9 @@ class KDAHybridLayer(_FusedWeightLayer):
                 lookback = None
             else:
                 lookback = lookback.to(device=x.device, dtype=x.dtype)
-        if _grad_wanted(x, state, lookback, *self.parameters()):
-            return self._forward_grad(x, state, lookback, detach_lookback)
+        if _grad_wanted(x, state, lookback, residual, *self.parameters()):
+            out, new_state, new_lookback = self._forward_grad(x, state, lookback, detach_lookback)
+            return (out if residual is None else residual + out), new_state, new_lookback
         with torch.no_grad():
             xc = x.contiguous()
             if xc.data_ptr() % 16:
@@ -555,7 +576,9 @@ class KDAHybridLayer(_FusedWeightLayer):
                 if state_out is not None:
                     state_out.copy_(new_state)
                     new_state = state_out
-            out = _linear(o.reshape(B, T, HV * V), self.o_proj.weight)
+            o2 = o.reshape(B, T, HV * V)
+            out = (_linear(o2, self.o_proj.weight) if residual is None
+                   else _linear_residual(o2, self.o_proj.weight, residual))
         return out, new_state, new_lookback
 
     def _forward_grad(self, x, state, lookback, detach_lookback):
@@ -592,6 +615,16 @@ class KDAHybridLayer(_FusedWeightLayer):
                                                initial_state=st, output_final_state=True)
         out = F.linear(o.reshape(B, T, HV * V), self.o_proj.weight.to(x.dtype))
         return out, new_state, new_lookback
+
+
+def _out_proj(o_proj: nn.Linear, o: torch.Tensor, residual: torch.Tensor | None):
+    """``o_proj(o)``, or ``residual + o_proj(o)``: fused into one GEMM when no
+    gradient is taken."""
+    if residual is None:
+        return o_proj(o)
+    if _grad_wanted(o, residual, o_proj.weight):
+        return residual + o_proj(o)
+    return _linear_residual(o, o_proj.weight, residual)
 
 
 class CSAHybridLayer(_FusedWeightLayer):
@@ -649,7 +682,10 @@ class CSAHybridLayer(_FusedWeightLayer):
                 stacklevel=3)
             CSAHybridLayer._indexer_warned = True
 
-    def forward(self, x: torch.Tensor, state: torch.Tensor | None = None):
+    def forward(self, x: torch.Tensor, state: torch.Tensor | None = None, *,
+                residual: torch.Tensor | None = None):
+        """``(o_proj(naive_csa(x)), None)``; with ``residual`` the first item is
+        ``residual + o_proj(...)`` (the add fused into the GEMM without gradients)."""
         cfg = self.cfg
         if self.training and not self.use_ste:
             self._maybe_warn_indexer()
@@ -662,7 +698,7 @@ class CSAHybridLayer(_FusedWeightLayer):
                 m=cfg.csa_m, topk=cfg.csa_topk, nh=cfg.csa_nh, nIh=cfg.csa_nIh, c=cfg.csa_c,
                 c_I=cfg.csa_cI, dc=cfg.csa_dc, sliding_window=cfg.csa_sliding_window,
                 sink_logits=self.sink, use_ste=self.use_ste, normalize_qk=True)
-            return self.o_proj(o), None
+            return _out_proj(self.o_proj, o, residual), None
 
 
 class HCAHybridLayer(_FusedWeightLayer):
@@ -692,14 +728,17 @@ class HCAHybridLayer(_FusedWeightLayer):
                 tuple(p.detach().to(device=device, dtype=torch.float32).contiguous() for p in small)
         return self._fused_step.get(proj + [self.W_UQ.weight] + small, dtype, device, build)
 
-    def forward(self, x: torch.Tensor, state: torch.Tensor | None = None):
+    def forward(self, x: torch.Tensor, state: torch.Tensor | None = None, *,
+                residual: torch.Tensor | None = None):
+        """``(o_proj(naive_hca(x)), None)``; with ``residual`` the first item is
+        ``residual + o_proj(...)`` (the add fused into the GEMM without gradients)."""
         cfg = self.cfg
         with torch.set_grad_enabled(torch.is_grad_enabled()):
             o = naive_hca(x, self.W_KV.weight, self.W_Z.weight, self.B_pos, self.W_DQ.weight,
                           self.W_UQ.weight, m2=cfg.hca_m2, nh=cfg.hca_nh, c=cfg.hca_c,
                           dc=cfg.hca_dc, sliding_window=cfg.hca_sliding_window,
                           sink_logits=self.sink)
-            return self.o_proj(o), None
+            return _out_proj(self.o_proj, o, residual), None
 
 
 class HybridKCHAttention(nn.Module):
@@ -821,17 +860,20 @@ class HybridKCHAttention(nn.Module):
         grad = _grad_wanted(x, *lookbacks, *self.parameters())
         with torch.set_grad_enabled(grad):
             for layer, norm, kind in zip(self.layers, self.norms, self.layout):
-                residual = x
+                # without gradients each sub-layer's output projection adds the
+                # residual stream in its GEMM
+                residual = None if grad else x
                 h = norm(x)
                 if kind == 'kda':
                     o, st, lb = layer.forward_functional(h, states[kda_idx], lookbacks[kda_idx],
-                                                         detach_lookback=detach_lookback)
+                                                         detach_lookback=detach_lookback,
+                                                         residual=residual)
                     states[kda_idx] = st
                     new_lookbacks.append(lb)
                     kda_idx += 1
                 else:
-                    o, _ = layer(h, None)
-                x = residual + o
+                    o, _ = layer(h, None, residual=residual)
+                x = o if residual is not None else x + o
             return x, self._stack_states(states), new_lookbacks
 
 
@@ -1298,11 +1340,13 @@ class HybridDecoding(nn.Module):
         q = _linear(cQ, layer.W_UQ.weight).view(B, T, cfg.hca_nh, cfg.hca_c)
         return C, Z, q
 
-    def _forward_csa_layer(self, layer: CSAHybridLayer, h: torch.Tensor, idx: int):
+    def _forward_csa_layer(self, layer: CSAHybridLayer, h: torch.Tensor, idx: int,
+                           residual: torch.Tensor):
+        """``residual + o_proj(CSA(h))`` with the cache updated."""
         cfg = layer.cfg
         B, T_new, _ = h.shape
         if T_new == 0:
-            return h.new_zeros(B, 0, cfg.d_model)
+            return residual.clone()
         cache = self._ensure_csa_cache(idx, layer, h)
         if T_new > 1:
             o_core, (Ca, Cb, Za, Zb, K_idx, Z_idx) = naive_csa(
@@ -1323,13 +1367,15 @@ class HybridDecoding(nn.Module):
                                    use_ste=False, normalize_qk=True, _normalize_q=True,
                                    _out_dtype=h.dtype)
             o_core = o.reshape(B, T_new, cfg.csa_nh * cfg.csa_c)
-        return _linear(o_core, layer.o_proj.weight)
+        return _linear_residual(o_core, layer.o_proj.weight, residual)
 
-    def _forward_hca_layer(self, layer: HCAHybridLayer, h: torch.Tensor, idx: int):
+    def _forward_hca_layer(self, layer: HCAHybridLayer, h: torch.Tensor, idx: int,
+                           residual: torch.Tensor):
+        """``residual + o_proj(HCA(h))`` with the cache updated."""
         cfg = layer.cfg
         B, T_new, _ = h.shape
         if T_new == 0:
-            return h.new_zeros(B, 0, cfg.d_model)
+            return residual.clone()
         cache = self._ensure_hca_cache(idx, layer, h)
         if T_new > 1:
             o_core, (C, Z) = naive_hca(
@@ -1345,7 +1391,7 @@ class HybridDecoding(nn.Module):
             o = cache.forward_step(q, nh=cfg.hca_nh, scale=1.0, sink_logits=layer.sink,
                                    _normalize_q=True, _out_dtype=h.dtype)
             o_core = o.reshape(B, T_new, cfg.hca_nh * cfg.hca_c)
-        return _linear(o_core, layer.o_proj.weight)
+        return _linear_residual(o_core, layer.o_proj.weight, residual)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         B = x.shape[0]
@@ -1371,19 +1417,18 @@ class HybridDecoding(nn.Module):
             for layer, norm, kind in zip(model.layers, model.norms, model.layout):
                 if trace is not None:
                     trace.append(x.clone())
-                residual = x
                 h = norm(x)
+                # each sub-layer's output projection adds the residual stream x
                 if kind == 'kda':
                     st = stacked[kda_idx]
-                    o, _ = layer(h, None if fresh else st, state_out=st)
+                    x, _ = layer(h, None if fresh else st, state_out=st, residual=x)
                     kda_idx += 1
                 elif kind == 'csa':
-                    o = self._forward_csa_layer(layer, h, csa_idx)
+                    x = self._forward_csa_layer(layer, h, csa_idx, x)
                     csa_idx += 1
                 else:
-                    o = self._forward_hca_layer(layer, h, hca_idx)
+                    x = self._forward_hca_layer(layer, h, hca_idx, x)
                     hca_idx += 1
-                x = residual + o
             model._kda_state = stacked if model.n_kda_layers > 0 else None
         if trace is not None:
             self._trace.append(trace)
