@@ -13,10 +13,15 @@ is two kernels (a parallel per-chunk kernel and the state-carrying kernel);
 ``traffic`` is their measured HBM bytes per step (rocprofv3 FETCH_SIZE +
 WRITE_SIZE, scaled by the same counters on a copy of known size), including the
 per-chunk workspace that passes between them.
-``cpu_baseline``: the numpy oracle (a from-scratch CPU restatement of the
-reference algorithm) on bounded samples of configs[1]-[3] (one sequence;
-query subsets for CSA / HCA), one warm-up and the median of three runs, with
-all of the process's cores and with one thread, and the CPU model.
+``cpu_baseline``: the oracle (from-scratch CPU restatements of the reference
+algorithm) on bounded samples of configs[1]-[3]: configs[1] on the torch-CPU
+restatement (``oracle.kda_torch``, one of the 8 sequences with all 16 heads)
+under ``torch.set_num_threads(N)``, N the process's cores, and under one
+thread, as the reference's own torch CPU path runs; configs[2] / [3] on the
+numpy restatement (one sequence, query subsets); one warm-up and the median
+of three runs, and the CPU model. The configs[2] sample also checks the GPU
+indexer's selection at its queries against the oracle's fp64 logits
+(``selection_vs_oracle``: rows that differ, rows with a near-tie).
 
 ``extra`` (skipped with ``--headline-only``): the other prefill workloads of
 the metric, each at its configuration, with the same timing protocol:
@@ -160,26 +165,78 @@ def _cpu_timed(fn, threads):
     return float(np.median(ts))
 
 
+def _cpu_timed_torch(fn, threads):
+    """The same protocol on torch's intra-op thread pool (``torch.set_num_threads``)."""
+    old = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        fn()
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+    finally:
+        torch.set_num_threads(old)
+    return float(np.median(ts))
+
+
+def _selection_vs_oracle(proj, par, Q, m, topk, win, sink):
+    """The GPU indexer's selection (``kch.csa_core``) at the queries ``Q``
+    against the oracle's (fp64 logits, ties by ascending index): rows whose
+    sets differ, and rows whose k-th and (k+1)-th exact logits lie within
+    2 eps (eps = 1e-6 sum_h |w_h| + 1e-7, the kernels' fp32-level bound)."""
+    import kch
+    from oracle.csa import compress_kv, indexer_logits, topk_desc_lowest_index, causal_block_mask
+    dev = torch.device("cuda:0")
+    Ca, Cb, Za, Zb, Ki, Zi, qq, qi, wi = proj
+    Ba, Bb, Bi = par
+    td = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)  # noqa: E731
+    with torch.no_grad():
+        _, idx = kch.csa_core(*(td(x) for x in proj), *(td(x) for x in par), m=m, topk=topk,
+                              sliding_window=win, sink_logits=td(sink), normalize_qk=True,
+                              return_indices=True)
+    got = idx.cpu().numpy()[0, Q].astype(np.int64)
+    T = Ca.shape[1]
+    kc = compress_kv(Ki.astype(np.float64), Zi.astype(np.float64), Bi, m, np.float64)
+    lg = indexer_logits(qi[:, Q], kc, wi[:, Q], None, causal_block_mask(T, T // m, m)[Q], True,
+                        np.float64)[0]
+    ref = topk_desc_lowest_index(lg[None], topk)[0]
+    eps = 1e-6 * np.abs(wi[0, Q].astype(np.float64)).sum(-1) + 1e-7
+    differ = near = 0
+    for r in range(len(Q)):
+        vis = np.sort(lg[r][np.isfinite(lg[r])])[::-1]
+        kb = int((ref[r] >= 0).sum())
+        if 0 < kb < vis.size and vis[kb - 1] - vis[kb] <= 2 * eps[r]:
+            near += 1
+        if set(got[r][got[r] >= 0].tolist()) != set(ref[r][ref[r] >= 0].tolist()):
+            differ += 1
+    return {"rows": int(len(Q)), "differ": differ, "near_ties": near,
+            "rule": "sets compared; a differing row is allowed only at a near-tie (tests)"}
+
+
 def cpu_baselines(host, s0):
-    """The numpy oracle (a from-scratch CPU restatement of the reference
-    algorithm) on bounded samples of configs[1], [2] and [3], with all the
-    process's cores and with one thread; tokens/s of the whole workload."""
+    """The oracle (from-scratch CPU restatements of the reference algorithm) on
+    bounded samples of configs[1], [2] and [3], with all the process's cores
+    and with one thread; tokens/s of the whole workload."""
     from oracle.csa import compress_kv, compress_kv_overlapped, csa_core_at, hca_core_at
-    from oracle.kda import chunk_kda
+    from oracle.kda_torch import chunk_kda as chunk_kda_torch
     n_aff = len(os.sched_getaffinity(0))
     omp = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
     N = min(n_aff, omp) if omp > 0 else n_aff
     rng = np.random.default_rng(0)
     res = {}
 
-    # configs[1]: one of the 8 sequences, 4 of its 16 heads, T=4096 (all 64 chunks)
-    q, k, v, g = (x[:1, :, :4] for x in host[:4])
-    beta = host[4][:1, :, :4]
+    # configs[1]: one of the 8 sequences with all 16 heads, T=4096 (all 64
+    # chunks), on the torch-CPU restatement
+    q, k, v, g, beta = (torch.from_numpy(np.ascontiguousarray(x[:1])) for x in host[:5])
+    S0 = torch.from_numpy(np.ascontiguousarray(s0[:1]))
     T = q.shape[1]
-    fn = lambda: chunk_kda(q, k, v, g, beta, initial_state=s0[:1, :4], chunk_size=64)  # noqa: E731
-    t = {th: _cpu_timed(fn, th) for th in (N, 1)}
-    res["C1_kda_chunk"] = {th: T / (4.0 * t[th]) for th in t}
-    samples = ["C1: chunk_kda on 1 of 8 sequences x 4 of 16 heads, T=4096"]
+    fn = lambda: chunk_kda_torch(q, k, v, g, beta, initial_state=S0, chunk_size=64)  # noqa: E731
+    t = {th: _cpu_timed_torch(fn, th) for th in (N, 1)}
+    res["C1_kda_chunk"] = {th: T / t[th] for th in t}
+    samples = ["C1: chunk_kda (torch-CPU restatement, torch.set_num_threads) on 1 of 8 "
+               "sequences with all 16 heads, T=4096"]
 
     # configs[2]: the CSA core of one sequence (T=8192): its two compressions,
     # then the sparse + window attention at 256 evenly spaced queries
@@ -206,7 +263,9 @@ def cpu_baselines(host, s0):
         tc, tq = _cpu_timed(csa_compress, th), _cpu_timed(csa_queries, th)
         res["C2_csa_core"][th] = 1.0 / (tc / T + tq / len(Q))
     samples.append("C2: csa core of 1 of 4 sequences (T=8192), compression of the whole "
-                   "sequence + attention at 256 evenly spaced queries")
+                   "sequence + attention at 256 evenly spaced queries (numpy)")
+    sel = _selection_vs_oracle((Ca, Cb, Za, Zb, Ki, Zi, qq, qi, wi), (Ba, Bb, Bi), Q, m, topk,
+                               win, sink)
 
     # the HCA core of one sequence (T=32768), attention at 512 queries
     T, m2 = 32768, 128
@@ -227,14 +286,14 @@ def cpu_baselines(host, s0):
         tc, tq = _cpu_timed(hca_compress, th), _cpu_timed(hca_queries, th)
         res["C3_hca_core"][th] = 1.0 / (tc / T + tq / len(Q))
     samples.append("C3: hca core of 1 of 4 sequences (T=32768), compression of the whole "
-                   "sequence + attention at 512 evenly spaced queries")
+                   "sequence + attention at 512 evenly spaced queries (numpy)")
     cfgs = {name: {"tokens_per_s": v[N], "tokens_per_s_1thread": v[1]} for name, v in res.items()}
     return {"value": res["C1_kda_chunk"][N], "unit": "tokens/s", "cores": N, "kind": "port",
             "sample": "; ".join(samples) + f"; 1 warm-up then the median of 3 runs; "
-                      f"{N} BLAS threads ({n_aff} cores in the process's affinity) and 1 thread; "
-                      f"numpy oracle; host {_cpu_model()}",
+                      f"{N} threads ({n_aff} cores in the process's affinity) and 1 thread; "
+                      f"host {_cpu_model()}",
             "value_1thread": res["C1_kda_chunk"][1], "cpu_model": _cpu_model(),
-            "affinity_cores": n_aff, "configs": cfgs}
+            "affinity_cores": n_aff, "configs": cfgs, "C2_selection_vs_oracle": sel}
 
 
 # ----------------------------------------------------------------------------- extras
@@ -661,6 +720,9 @@ def main():
         extra = {}
         extra["kda_T8K"] = bench_kda(4, 8192, args.steps, args.warmup, dev)
         _log(f"kda T8K: {extra['kda_T8K']['ms']:.3f} ms")
+        # the metric is quoted at T=8K: its KDA figure beside the headline
+        rec["value_T8K"] = extra["kda_T8K"]["tokens_per_s"]
+        rec["ms_per_step_T8K"] = extra["kda_T8K"]["ms"]
         extra["csa_C2"] = bench_csa(4, 8192, max(3, args.steps // 4), 1, dev)
         _log(f"csa C2: {extra['csa_C2']['ms']:.3f} ms")
         extra["hca_C3"] = bench_hca(4, 32768, max(3, args.steps // 4), 1, dev)

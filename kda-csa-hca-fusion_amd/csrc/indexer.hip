@@ -116,8 +116,11 @@ __host__ __device__ inline size_t indexer_lds(int nb, int nIh, int topk, bool le
 // keys equal to K (as many as still needed: the reference's order with ties
 // by ascending index) are written in ascending block order: to sel as
 // (key, ~index) values, or without sel as block indices to out[0 .. topk),
-// -1 past the selected count. No LDS atomics, no LDS traffic but one read of
-// the row.
+// -1 past the selected count. The search stops at the first candidate that
+// exactly topk keys reach: those keys are the selection (no key equal to the
+// k-th lies below the candidate, so no tie is split), typically after about
+// log2(rows) bits instead of all of them. No LDS atomics, no LDS traffic but
+// one read of the row.
 template <typename IdxT>
 __device__ __forceinline__ void select_in_registers(const float* lg, int nv, int topk, int lane,
                                                     u64* sel, IdxT* out) {
@@ -156,7 +159,13 @@ __device__ __forceinline__ void select_in_registers(const float* lg, int nv, int
       int c = 0;
 #pragma unroll
       for (int r = 0; r < 4 * RG; ++r) c += __popcll(__builtin_amdgcn_ballot_w64(key[r] >= cand));
-      if (c >= topk) K = cand;
+      if (c == topk) {
+        // exactly topk keys are >= cand: taking every key above cand - 1
+        // (none equal to it is needed) selects them
+        K = cand - 1u;
+        break;
+      }
+      if (c > topk) K = cand;
     }
     int gt = 0;
 #pragma unroll
@@ -320,8 +329,12 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
       }
     }
   };
-  // the products' scale: 2^-16 undoes the fp16 parts' 256 on both sides
+  // the products' scale (2^-16 undoes the fp16 parts' 256 on both sides)
+  // folded into the head weight: relu(a s) w = relu(a) (s w) for s > 0
   const float lscale = KM == 2 ? p.scale * kSplit16Unscale : p.scale;
+  const bool fold = lscale > 0.f;
+  const float wqs = fold ? wq * lscale : wq;
+  const float ascale = fold ? 1.f : lscale;
   auto consume = [&](int c, const KFrag& kf) {
     // the smallest cross products first, so that each later (larger) term is
     // added to an accumulator of the smaller ones
@@ -356,7 +369,7 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
     // words, since a branch costs the overlap of the chunks loaded ahead.
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float v = head_sum<NIH>(fmaxf(acc[e] * lscale, 0.f) * wq);
+      const float v = head_sum<NIH>(fmaxf(acc[e] * ascale, 0.f) * wqs);
       const int blk = 16 * c + 4 * q4 + e;
       float* dst = (hh == 0 && qok && blk < nv_me) ? logits + jq * ldl + blk
                                                    : sink + lane;

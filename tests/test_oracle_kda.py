@@ -11,7 +11,9 @@ Each check would fail under a plausible restatement mistake:
 * GVA head sharing, padding/causality, the g clamp;
 * the hand-written gradients against central finite differences of the
   forward in fp64, every coordinate (the reference's gradient test,
-  run_correctness.py:765-833, samples 8 per tensor at the same 1e-6 bar).
+  run_correctness.py:765-833, samples 8 per tensor at the same 1e-6 bar);
+* the torch-CPU restatement (``oracle.kda_torch``, the CPU baseline's) against
+  the numpy one and the recurrence in fp64, GVA and padding included.
 """
 
 from __future__ import annotations
@@ -21,6 +23,7 @@ import pytest
 
 from oracle.common import l2_normalize, logsigmoid, sigmoid
 from oracle.kda import chunk_kda, delta_rule_matrix_form, recurrent_kda, recurrent_kda_grad
+from oracle.kda_torch import chunk_kda as chunk_kda_torch
 
 
 def _inputs(rng, B, T, H, HV, K, V, gscale=1.0):
@@ -225,3 +228,19 @@ def test_recurrent_grad_gva_and_clamp():
     assert _fd_check(q, k, v, g, beta, s0, W_o, W_s, 0.7, -10.0) < 1e-6
     dg = recurrent_kda_grad(q, k, v, g, beta, W_o, scale=0.7, initial_state=s0, ds_final=W_s)[3]
     assert np.all(dg[g < -10.0] == 0) and np.any(dg[g >= -10.0] != 0)
+
+
+@pytest.mark.parametrize("B,T,H,HV,K,V,C", [(2, 200, 2, 4, 32, 16, 64), (1, 37, 1, 1, 16, 8, 16),
+                                            (1, 130, 2, 2, 64, 64, 64)])
+def test_torch_restatement_matches(B, T, H, HV, K, V, C):
+    import torch
+    rng = np.random.default_rng(T + K)
+    q, k, v, g, beta = _inputs(rng, B, T, H, HV, K, V, gscale=3.0)
+    S0 = 0.02 * rng.standard_normal((B, HV, K, V))
+    o1, s1 = chunk_kda(q, k, v, g, beta, initial_state=S0, chunk_size=C, compute=np.float64)
+    o2, s2 = chunk_kda_torch(q, k, v, g, beta, initial_state=S0, chunk_size=C,
+                             dtype=torch.float64)
+    assert np.abs(o1 - o2.numpy()).max() < 1e-12 * max(1.0, np.abs(o1).max())
+    assert np.abs(s1 - s2.numpy()).max() < 1e-12 * max(1.0, np.abs(s1).max())
+    o3, s3 = recurrent_kda(q, k, v, g, beta, initial_state=S0, compute=np.float64)
+    assert np.abs(o3 - o2.numpy()).max() < 1e-9
