@@ -344,8 +344,14 @@ __global__ __launch_bounds__(HD) void hca_bwd_block_kernel(HcaBwdParams p, int n
   const int n = blockIdx.x, b = blockIdx.y, c = threadIdx.x;
   const int tile = n / NBT, i = n % NBT;
   float dk = 0.f;
-  for (int ci = 0; ci < nchunk; ++ci)
-    dk += p.part_b[((((size_t)b * ntile + tile) * nchunk + ci) * NBT + i) * HD + c];
+  if (p.mfma_parts) {
+    // the chunks from the first one that holds a query seeing block n
+    for (int ci = ((n + 1) * p.m2 - 1) / p.part_qc; ci < nchunk; ++ci)
+      dk += p.part_b[(((size_t)b * nchunk + ci) * p.nb + n) * HD + c];
+  } else {
+    for (int ci = 0; ci < nchunk; ++ci)
+      dk += p.part_b[((((size_t)b * ntile + tile) * nchunk + ci) * NBT + i) * HD + c];
+  }
   const size_t ri = ((size_t)b * p.nb + n) * HD + c;
   const float y = p.kc[ri], r = p.raw[ri];
   const float yd = block_sum<HD>(y * dk, sh);
@@ -415,8 +421,12 @@ __global__ __launch_bounds__(HD) void hca_bwd_window_kernel(HcaBwdParams p, int 
   const int u = blockIdx.x, b = blockIdx.y, c = threadIdx.x;
   const int tile = u / NBT, i = u % NBT;
   float dk = 0.f;
-  for (int ci = 0; ci < nchunk; ++ci)
-    dk += p.part_w[((((size_t)b * ntile + tile) * nchunk + ci) * NBT + i) * HD + c];
+  if (p.mfma_parts) {
+    dk = p.part_w[((size_t)b * p.T + u) * HD + c];
+  } else {
+    for (int ci = 0; ci < nchunk; ++ci)
+      dk += p.part_w[((((size_t)b * ntile + tile) * nchunk + ci) * NBT + i) * HD + c];
+  }
   const size_t ri = ((size_t)b * p.T + u) * HD + c;
   const float y = p.kl[ri], x = p.lsrc[ri];
   const float yd = block_sum<HD>(y * dk, sh);
@@ -671,13 +681,42 @@ hipError_t launch_ste(SteBwdParams p, const Plan& z, HcaBwdParams bp, hipStream_
 
 }  // namespace
 
+hipError_t sel_bitmap_launch(const int* idx, uint32_t* sel, long long nq, int topk, int nw, hipStream_t s) {
+  const long long n = nq * topk;
+  hipLaunchKernelGGL(sel_bitmap_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, idx, sel, nq,
+                     topk, nw);
+  return hipGetLastError();
+}
+
+// The L2-norm and compression backward of the compressed rows and the window
+// rows' L2-norm backward, from MFMA-path partials (p.mfma_parts).
+hipError_t hca_bwd_finish_launch(const HcaBwdParams& p, int nchunk, hipStream_t s) {
+  if (p.nb > 0) {
+    if (p.c == 64)
+      hipLaunchKernelGGL((hca_bwd_block_kernel<64>), dim3(p.nb, p.B), dim3(64), 0, s, p, nchunk, 0);
+    else
+      hipLaunchKernelGGL((hca_bwd_block_kernel<128>), dim3(p.nb, p.B), dim3(128), 0, s, p, nchunk, 0);
+  }
+  if (p.win > 0) {
+    if (p.c == 64)
+      hipLaunchKernelGGL((hca_bwd_window_kernel<64>), dim3(p.T, p.B), dim3(64), 0, s, p, 0, 0);
+    else
+      hipLaunchKernelGGL((hca_bwd_window_kernel<128>), dim3(p.T, p.B), dim3(128), 0, s, p, 0, 0);
+  }
+  return hipGetLastError();
+}
+
 size_t hca_bwd_ws_bytes(int B, int T, int nh, int c, int m2, int win, int topk) {
   const Plan z = plan(B, T, T / m2, win, c);
   const size_t sel = topk > 0 ? al256((size_t)B * T * ((T / m2 + 31) / 32) * 4) : 0;
-  return 3 * al256((size_t)B * T * nh * 4) + al256(z.part_b * 4) + al256(z.part_w * 4) + sel;
+  const size_t simt = 3 * al256((size_t)B * T * nh * 4) + al256(z.part_b * 4) + al256(z.part_w * 4) + sel;
+  // the MFMA path (normalised rows) needs its own regions; the larger of the two
+  const size_t mfma = nh <= 16 ? attn_bwd_mfma_ws_bytes(B, T, c, m2, win, topk) : 0;
+  return simt > mfma ? simt : mfma;
 }
 
 hipError_t hca_bwd_dispatch(HcaBwdParams p, void* ws, hipStream_t stream) {
+  if (attn_bwd_mfma_supported(p)) return attn_bwd_mfma_dispatch(p, ws, stream);
   const Plan z = plan(p.B, p.T, p.nb, p.win, p.c);
   char* w = static_cast<char*>(ws);
   const size_t per = al256((size_t)p.B * p.T * p.nh * 4);

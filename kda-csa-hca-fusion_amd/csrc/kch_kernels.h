@@ -97,9 +97,28 @@ struct HcaBwdParams {
   float* rq = nullptr;
   float* part_b = nullptr;
   float* part_w = nullptr;
+  // MFMA path (attn_bwd_mfma.hip): the two-part bf16 splits of qn and dout
+  // ([B,T,16,c], heads padded to 16) and of the compressed and window rows;
+  // mfma_parts: part_b holds [B, nchunk, nb, c] per-chunk partials of the
+  // compressed rows (chunk ci = queries [ci part_qc, (ci+1) part_qc), written
+  // for the chunks a row's queries reach), part_w the window rows' [B, T, c]
+  bf16_t* qs_hi = nullptr;
+  bf16_t* qs_lo = nullptr;
+  bf16_t* ds_hi = nullptr;
+  bf16_t* ds_lo = nullptr;
+  bf16_t* kc_hi = nullptr;
+  bf16_t* kc_lo = nullptr;
+  bf16_t* kl_hi = nullptr;
+  bf16_t* kl_lo = nullptr;
+  int mfma_parts = 0;
+  int part_qc = 0;
   int B, T, nh, c, m2, nb, win;
   float scale;
 };
+// MFMA attention backward (normalised queries and keys, c in {64, 128}, nh <= 16)
+bool attn_bwd_mfma_supported(const HcaBwdParams& p);
+size_t attn_bwd_mfma_ws_bytes(int B, int T, int c, int m2, int win, int topk);
+hipError_t attn_bwd_mfma_dispatch(HcaBwdParams p, void* ws, hipStream_t s);
 size_t hca_bwd_ws_bytes(int B, int T, int nh, int c, int m2, int win, int topk);
 
 // The STE surrogate's backward for the indexer (hca_backward.hip): fp32,
