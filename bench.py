@@ -441,7 +441,10 @@ def bench_training(dev, reps=3):
     B, T, H, K, V = 8, 4096, 16, 128, 128
     xs, s0, _, _ = kda_inputs(B, T, H, K, V, dev=dev)
     do = torch.randn(B, T, H, V, generator=g).to(dev, torch.bfloat16)
-    out["kda_C1_backward_ms"] = timed(lambda: kch.kda_recurrent_grad(*xs, do, initial_state=s0))
+    out["kda_C1_backward_ms"] = timed(
+        lambda: kch.kda_recurrent_grad(*xs, do, initial_state=s0, chunked=True))
+    out["kda_C1_recurrent_backward_ms"] = timed(
+        lambda: kch.kda_recurrent_grad(*xs, do, initial_state=s0))
     del xs, s0, do
     B, T, nh, c, m2, win = 4, 32768, 16, 128, 128, 128
     C, Z = (torch.randn(B, T, c, generator=g).to(dev, torch.bfloat16) for _ in range(2))
@@ -486,7 +489,8 @@ def bench_training(dev, reps=3):
     # scores and dp (2 x 2c per pair and head) and form dq and dk (2c + 4c):
     # 2.5x the forward's 4c; the KDA one runs the recurrence forward twice and
     # backward once, taken as 2x the chunk form's forward FLOPs. Against the
-    # fp32 peak: these kernels compute in fp32 on the vector units.
+    # fp32 peak: these kernels compute to fp32 accuracy (split-bf16 MFMA
+    # products, or fp32 on the vector units).
     fl = {"kda_C1_backward_ms": 2.0 * kda_algorithmic(8, 4096, 16, 128, 128)[0],
           "hca_C3_core_backward_ms": 2.5 * hca_core_algorithmic(4, 32768, 128, 128, 16, 128)[0],
           "csa_C2_attention_backward_ms": 2.5 * csa_core_algorithmic(

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define KCH_ABI_VERSION 14
+#define KCH_ABI_VERSION 15
 
 #define KCH_OK 0
 #define KCH_ERR_INVALID 1     /* bad pointer / shape / argument */
@@ -127,6 +127,24 @@ int kch_kda_recurrent_bwd(const void* q, const void* k, const void* v, const voi
                           void* dbeta, void* ds0, int B, int T, int H, int HV, int K, int V,
                           double scale, double g_clamp_min, int dtype, void* ws,
                           size_t ws_bytes, void* stream);
+
+/*
+ * Gradients of naive_chunk_kda (ops_kda.py:340-536, differentiated by the
+ * reference's autograd through the chunk form, including its clamp(max=50) of
+ * the in-chunk decay exponents) computed in the chunk form: four kernels
+ * (per-chunk prepare, forward state pass, reverse state pass, per-chunk
+ * gradients) on split-bf16 MFMA products in fp32. Same arguments and layouts
+ * as kch_kda_recurrent_bwd; chunks of 64 tokens. Coverage: dtype KCH_DT_F32 /
+ * BF16 / F16, K and V in {64, 128}, T >= 1 (other shapes and fp64 take
+ * kch_kda_recurrent_bwd). Tensors 16-byte aligned; ws 256-byte aligned, at
+ * least kch_kda_chunk_bwd_ws_bytes bytes.
+ */
+size_t kch_kda_chunk_bwd_ws_bytes(int B, int T, int H, int HV, int K, int V, int dtype);
+int kch_kda_chunk_bwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                      const void* s0, const void* d_o, const void* ds_final, void* dq, void* dk,
+                      void* dv, void* dg, void* dbeta, void* ds0, int B, int T, int H, int HV, int K,
+                      int V, double scale, double g_clamp_min, int dtype, void* ws, size_t ws_bytes,
+                      void* stream);
 
 
 /*

@@ -265,6 +265,49 @@ int kch_kda_recurrent_bwd(const void* q, const void* k, const void* v, const voi
   return hip_status(fn, kch::kda_bwd_dispatch(p, dtype, ws, (hipStream_t)stream));
 }
 
+size_t kch_kda_chunk_bwd_ws_bytes(int B, int T, int H, int HV, int K, int V, int dtype) {
+  if (B <= 0 || T <= 0 || H < 1 || HV < 1 || HV % H || !dtype_ok(dtype)) return 0;
+  if (!kch::kda_chunk_bwd_supported(K, V, dtype)) return 0;
+  return kch::kda_chunk_bwd_ws_bytes(B, T, H, HV, K, V);
+}
+
+int kch_kda_chunk_bwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                      const void* s0, const void* d_o, const void* ds_final, void* dq, void* dk,
+                      void* dv, void* dg, void* dbeta, void* ds0, int B, int T, int H, int HV, int K,
+                      int V, double scale, double g_clamp_min, int dtype, void* ws, size_t ws_bytes,
+                      void* stream) {
+  const char* fn = "kch_kda_chunk_bwd";
+  if (!dtype_ok(dtype)) return fail(KCH_ERR_UNSUPPORTED, "%s: dtype %d not supported (fp32/bf16/fp16)", fn, dtype);
+  if (B < 0 || T < 1 || H < 1 || HV < 1)
+    return fail(KCH_ERR_INVALID, "%s: bad sizes B=%d T=%d H=%d HV=%d (T >= 1)", fn, B, T, H, HV);
+  if (HV % H) return fail(KCH_ERR_INVALID, "%s: HV=%d must be divisible by H=%d", fn, HV, H);
+  if (!kch::kda_chunk_bwd_supported(K, V, dtype))
+    return fail(KCH_ERR_UNSUPPORTED, "%s: K=%d V=%d not supported (64 or 128 each)", fn, K, V);
+  if (std::isnan(g_clamp_min) || std::isnan(scale))
+    return fail(KCH_ERR_INVALID, "%s: g_clamp_min or scale is NaN", fn);
+  if ((long long)B * T * HV * (3 * K + 1) >= (1LL << 40) || (long long)T * HV * K >= (1LL << 31))
+    return fail(KCH_ERR_UNSUPPORTED, "%s: tensors too large", fn);
+  if (B == 0) return KCH_OK;
+  if (!q || !k || !v || !g || !beta || !d_o || !dq || !dk || !dv || !dg || !dbeta)
+    return fail(KCH_ERR_INVALID, "%s: null tensor pointer", fn);
+  const void* ptrs[] = {q, k, v, g, beta, s0, d_o, ds_final, dq, dk, dv, dg, dbeta, ds0};
+  for (const void* ptr : ptrs)
+    if ((uintptr_t)ptr & 15) return fail(KCH_ERR_INVALID, "%s: tensors must be 16-byte aligned", fn);
+  const size_t need = kch_kda_chunk_bwd_ws_bytes(B, T, H, HV, K, V, dtype);
+  if (!ws || ws_bytes < need)
+    return fail(KCH_ERR_INVALID, "%s: workspace of %zu bytes required, got %zu", fn, need,
+                ws ? ws_bytes : (size_t)0);
+  if ((uintptr_t)ws & 255) return fail(KCH_ERR_INVALID, "%s: workspace must be 256-byte aligned", fn);
+  kch::KdaBwdParams p;
+  p.q = q; p.k = k; p.v = v; p.g = g; p.beta = beta; p.s0 = s0;
+  p.d_o = d_o; p.ds_final = ds_final;
+  p.dq = dq; p.dk = dk; p.dv = dv; p.dg = dg; p.dbeta = dbeta; p.ds0 = ds0;
+  p.B = B; p.T = T; p.H = H; p.HV = HV; p.K = K; p.V = V;
+  p.scale = scale;
+  p.g_clamp_min = g_clamp_min;
+  return hip_status(fn, kch::kda_chunk_bwd_dispatch(p, dtype, ws, (hipStream_t)stream));
+}
+
 size_t kch_hca_attn_bwd_ws_bytes(int B, int T, int nh, int c, int m2, int win) {
   if (B <= 0 || T <= 0 || nh < 1 || (c != 64 && c != 128) || m2 < 1 || T % m2 || win < 0) return 0;
   return kch::hca_bwd_ws_bytes(B, T, nh, c, m2, win, 0);

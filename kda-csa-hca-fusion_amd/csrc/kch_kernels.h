@@ -53,6 +53,15 @@ size_t kda_bwd_ws_bytes(int B, int T, int HV, int K, int V, bool f64);
 // K in {16, 32, 64, 128, 256}; dtype DT_F32 / DT_BF16 / DT_F16 / DT_F64; ws
 // 256-byte aligned, kda_bwd_ws_bytes bytes
 hipError_t kda_bwd_dispatch(KdaBwdParams p, int dtype, void* ws, hipStream_t stream);
+// Sums the per-value-head partial records at p.part ([B,T,HV,(3K+1)] per
+// slice of `cols` columns of V) into dq, dk, dg (clamp mask), dbeta.
+hipError_t kda_bwd_reduce_launch(const KdaBwdParams& p, int cols, int dtype, hipStream_t stream);
+// Chunked backward of naive_chunk_kda (kda_chunk_bwd.hip): bf16/fp16/fp32
+// inputs, K and V in {64, 128}, chunks of 64; ws 256-byte aligned,
+// kda_chunk_bwd_ws_bytes bytes.
+bool kda_chunk_bwd_supported(int K, int V, int dtype);
+size_t kda_chunk_bwd_ws_bytes(int B, int T, int H, int HV, int K, int V);
+hipError_t kda_chunk_bwd_dispatch(KdaBwdParams p, int dtype, void* ws, hipStream_t stream);
 
 // Gradients of the HCA attention (hca_backward.hip), fp32 tensors, c in
 // {64, 128}, nh <= 256 / (c / 8), T a multiple of m2.

@@ -402,7 +402,22 @@ int phases(int B, int HV, int V) {
 
 size_t al256(size_t x) { return (x + 255) & ~size_t(255); }
 
+template <typename InT, typename AccT>
+hipError_t reduce_only(const KdaBwdParams& p, int cols, hipStream_t s) {
+  const int threads = p.K <= 64 ? 64 : (p.K <= 128 ? 128 : 256);
+  hipLaunchKernelGGL((kda_bwd_reduce_kernel<InT, AccT>), dim3((unsigned)((size_t)p.B * p.T * p.H)),
+                     dim3(threads), 0, s, p, cols);
+  return hipGetLastError();
+}
+
 }  // namespace
+
+hipError_t kda_bwd_reduce_launch(const KdaBwdParams& p, int cols, int dtype, hipStream_t stream) {
+  if (dtype == DT_F64) return reduce_only<double, double>(p, cols, stream);
+  if (dtype == DT_F32) return reduce_only<float, float>(p, cols, stream);
+  if (dtype == DT_BF16) return reduce_only<bf16_t, float>(p, cols, stream);
+  return reduce_only<_Float16, float>(p, cols, stream);
+}
 
 size_t kda_bwd_ws_bytes(int B, int T, int HV, int K, int V, bool f64) {
   const int ph = phases(B, HV, V);

@@ -226,14 +226,18 @@ def _bwd_scale(scale, K, f64):
 
 
 def kda_recurrent_grad(q, k, v, g, beta, d_o, scale=None, initial_state=None, ds_final=None,
-                       *, g_clamp_min: float = -10.0):
+                       *, g_clamp_min: float = -10.0, chunked: bool = False):
     """Gradients of ``naive_recurrent_kda`` / ``naive_chunk_kda`` (the same
     function, ``ops_kda.py:175-267`` / ``:464-494``) for the cotangents
     ``d_o = dL/do`` and ``ds_final = dL/dS_T`` (or ``None``), on
-    ``kch_kda_recurrent_bwd``. Returns ``(dq, dk, dv, dg, dbeta, ds0)``: the
-    first five in the input dtype, ``ds0`` in the state dtype (fp32, fp64 for
-    fp64 inputs) or ``None`` without an initial state. K is zero-padded to the
-    kernel's next size; padded channels carry no gradient."""
+    ``kch_kda_recurrent_bwd`` or, with ``chunked`` (the gradient of the chunk
+    form with 64-token chunks, ``ops_kda.py:340-536``), on
+    ``kch_kda_chunk_bwd`` where it covers the shape (fp32 / bf16 / fp16, K
+    padded to 64 or 128, V in {64, 128}). Returns ``(dq, dk, dv, dg, dbeta,
+    ds0)``: the first five in the input dtype, ``ds0`` in the state dtype
+    (fp32, fp64 for fp64 inputs) or ``None`` without an initial state. K is
+    zero-padded to the kernel's next size; padded channels carry no
+    gradient."""
     fn = "kda_recurrent_grad"
     B, T, H, K = q.shape
     HV, V = v.shape[2], v.shape[-1]
@@ -265,9 +269,15 @@ def kda_recurrent_grad(q, k, v, g, beta, d_o, scale=None, initial_state=None, ds
     dv, dbeta = torch.empty_like(v), torch.empty_like(beta)
     ds0 = torch.empty(B, HV, Kp, V, device=q.device, dtype=st) if initial_state is not None \
         else None
-    nbytes = _lib.load().kch_kda_recurrent_bwd_ws_bytes(B, T, HV, Kp, V, code)
+    entry = "kch_kda_recurrent_bwd"
+    if chunked and code != 3 and Kp in (64, 128) and V in (64, 128):
+        entry = "kch_kda_chunk_bwd"
+        q, k, v, g, beta, d_o = (_aligned(t) for t in (q, k, v, g, beta, d_o))
+        nbytes = _lib.load().kch_kda_chunk_bwd_ws_bytes(B, T, H, HV, Kp, V, code)
+    else:
+        nbytes = _lib.load().kch_kda_recurrent_bwd_ws_bytes(B, T, HV, Kp, V, code)
     ws = torch.empty(max(nbytes, 1), device=q.device, dtype=torch.uint8)
-    _lib.call("kch_kda_recurrent_bwd", _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g),
+    _lib.call(entry, _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g),
               _lib.ptr(beta), _lib.ptr(s0), _lib.ptr(d_o), _lib.ptr(dsf), _lib.ptr(dq),
               _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dg), _lib.ptr(dbeta), _lib.ptr(ds0),
               B, T, H, HV, Kp, V, sc, _clamp_value(g_clamp_min), code, _lib.ptr(ws), nbytes,
@@ -280,8 +290,10 @@ def kda_recurrent_grad(q, k, v, g, beta, d_o, scale=None, initial_state=None, ds
 
 class _KdaFunction(torch.autograd.Function):
     """The operators with gradients: forward on the operator's own kernels,
-    backward on ``kch_kda_recurrent_bwd`` (the reference differentiates its
-    torch code with autograd, ``run_correctness.py:765-833, 1032-1092``)."""
+    backward on ``kch_kda_chunk_bwd`` for ``naive_chunk_kda`` with 64-token
+    chunks and on ``kch_kda_recurrent_bwd`` otherwise (the reference
+    differentiates its torch code with autograd, ``run_correctness.py:765-833,
+    1032-1092``)."""
 
     @staticmethod
     def forward(ctx, q, k, v, g, beta, s0, entry, fn_name, scale, g_clamp_min, state_dtype,
@@ -291,6 +303,7 @@ class _KdaFunction(torch.autograd.Function):
                     state_dtype, chunk_size)
         ctx.save_for_backward(q, k, v, g, beta, s0)
         ctx.scale, ctx.g_clamp_min = scale, g_clamp_min
+        ctx.chunked = entry == "kch_kda_chunk_fwd" and (chunk_size is None or chunk_size == 64)
         return o, s
 
     @staticmethod
@@ -299,7 +312,8 @@ class _KdaFunction(torch.autograd.Function):
         if d_o is None:
             d_o = torch.zeros_like(v)
         dq, dk, dv, dg, dbeta, ds0 = kda_recurrent_grad(
-            q, k, v, g, beta, d_o, ctx.scale, s0, d_s, g_clamp_min=ctx.g_clamp_min)
+            q, k, v, g, beta, d_o, ctx.scale, s0, d_s, g_clamp_min=ctx.g_clamp_min,
+            chunked=ctx.chunked)
         if ds0 is not None:
             ds0 = ds0.to(s0.dtype)
         return dq, dk, dv, dg, dbeta, ds0, None, None, None, None, None, None

@@ -254,3 +254,72 @@ def test_fp32_wide_grid_matches_oracle(dev):
     ts, s0t = _leaves(host, s0, dev, torch.float32, torch.float32)
     got = _hip_grads(kch.naive_recurrent_kda, ts, s0t, w_o, w_s)
     _check(got, _ref(host, s0, w_o, w_s), 1e-4, label="fp32 wide")
+
+
+@pytest.mark.parametrize("case", ["strong_decay", "mixed_sign", "gva_fp16"])
+def test_chunk_bwd_exact_path_matches_oracle(dev, case):
+    """``kch_kda_chunk_bwd`` where its decay products are formed exactly (one
+    exponential per pair and channel): gates of -3 to -4 nats a token (in-chunk
+    ranges far beyond 60 nats) and gates of both signs (no clamp reached), fp32
+    against the recurrence oracle at 1e-4 of each tensor's largest gradient;
+    fp16 with grouped value heads (per-head partials summed by the reduce
+    kernel) at the bf16 bar."""
+    import kch
+    B, T, H, HV, K, V = {"strong_decay": (1, 150, 2, 2, 128, 64),
+                         "mixed_sign": (2, 130, 1, 1, 64, 128),
+                         "gva_fp16": (1, 97, 1, 2, 128, 128)}[case]
+    host, s0, w_o, w_s = _make(11 * T + K, B, T, H, HV, K, V)
+    rng = np.random.default_rng(T)
+    if case == "strong_decay":
+        host[3] = host[3] - 3.0
+    elif case == "mixed_sign":
+        host[3] = 0.3 * rng.standard_normal(host[3].shape)
+    if case == "gva_fp16":
+        tb = [torch.tensor(x, dtype=torch.float16) for x in host]
+        host = [t.double().numpy() for t in tb]
+        dtype, tol = torch.float16, (2e-2, 2e-2)
+    else:
+        host = [np.asarray(x, np.float32).astype(np.float64) for x in host]
+        dtype, tol = torch.float32, (1e-4, 0.0)
+    s0 = s0.astype(np.float32).astype(np.float64)
+    ts, s0t = _leaves(host, s0, dev, dtype, torch.float32)
+    got = _hip_grads(kch.naive_chunk_kda, ts, s0t, w_o, w_s)
+    _check(got, _ref(host, s0, w_o, w_s), *tol, label=case)
+
+
+def test_chunk_bwd_clamp_matches_chunk_form_autograd(dev):
+    """Where ``clamp(max=50)`` of the in-chunk decay exponents
+    (``ops_kda.py:414,516``) is reached, the chunk form's gradient is no longer
+    the recurrence's: the clamped exponent has zero gradient. Channel 0 of
+    every head runs a gate valley (-1.7 nats a token for 32 tokens, then +1.7),
+    so ``G_i - G_j`` passes 50 for late rows against mid-chunk columns (in
+    Aqk), with k of that channel scaled by 1e-23 so that ``k e^(G_l - G)``
+    and the clamped ``q k e^50`` stay of order one. The HIP gradients (fp32) are compared with fp64 autograd of
+    ``oracle.kda_torch.chunk_kda`` (the chunk form, clamp included) on the same
+    inputs, at 1e-4 of each tensor's largest gradient."""
+    import kch
+    from oracle.kda_torch import chunk_kda as torch_chunk
+    B, T, H, HV, K, V = 1, 64, 2, 2, 64, 64
+    host, s0, w_o, w_s = _make(404, B, T, H, HV, K, V)
+    q, k, v, g, beta = host
+    k = k.copy()
+    k[..., 0] *= 1e-23
+    g = g.copy()
+    g[:, :32, :, 0] = -1.7
+    g[:, 32:, :, 0] = 1.7
+    host = [np.asarray(x, np.float32).astype(np.float64) for x in (q, k, v, g, beta)]
+    s0 = s0.astype(np.float32).astype(np.float64)
+    ts, s0t = _leaves(host, s0, dev, torch.float32, torch.float32)
+    got = _hip_grads(kch.naive_chunk_kda, ts, s0t, w_o, w_s)
+
+    leaves = [torch.tensor(x, dtype=torch.float64, requires_grad=True) for x in host]
+    s0c = torch.tensor(s0, dtype=torch.float64, requires_grad=True)
+    o, s = torch_chunk(*leaves, initial_state=s0c, dtype=torch.float64)
+    loss = (o * torch.tensor(w_o)).sum() + (s * torch.tensor(w_s)).sum()
+    loss.backward()
+    ref = [t.grad.numpy() for t in leaves] + [s0c.grad.numpy()]
+    # the clamp is reached: the recurrence's gradients of q and g differ visibly
+    rec = _ref(host, s0, w_o, w_s)
+    assert np.abs(rec[0] - ref[0]).max() > 0.5 * np.abs(ref[0]).max()
+    assert np.abs(rec[3] - ref[3]).max() > 1e-2 * np.abs(ref[3]).max()
+    _check(got, ref, 1e-4, label="clamp")
