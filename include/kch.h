@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define KCH_ABI_VERSION 15
+#define KCH_ABI_VERSION 16
 
 #define KCH_OK 0
 #define KCH_ERR_INVALID 1     /* bad pointer / shape / argument */
@@ -146,6 +146,49 @@ int kch_kda_chunk_bwd(const void* q, const void* k, const void* v, const void* g
                       int V, double scale, double g_clamp_min, int dtype, void* ws, size_t ws_bytes,
                       void* stream);
 
+
+/*
+ * Generic CSA / HCA forward: the inputs the MFMA kernels above do not take.
+ * float64 (dtype KCH_DT_F64; the reference computes in fp64 for fp64 inputs,
+ * ops_csa.py:229,263,510,922 and ops_hca.py:138) or float32 (KCH_DT_F32) for
+ * head dims c or c_I above 128, more than 16 indexer heads, or an indexer
+ * mask other than the standard block-causal one. Every sum in the dtype;
+ * contiguous tensors.
+ *
+ * kch_gen_compress: csa_compress_kv (ops_csa.py:198-234; Cb = Zb = Bb = NULL)
+ *   or csa_compress_kv_overlapped (ops_csa.py:237-305): Ca, Za (Cb, Zb)
+ *   [B,T,c], Ba (Bb) [m,c] -> out [B,T/m,c].
+ * kch_gen_l2norm: F.normalize(x, dim=-1) (eps 1e-12) of rows [rows,c] (a copy
+ *   when normalize = 0).
+ * kch_gen_indexer: csa_lightning_indexer (ops_csa.py:330-573): q [B,T,nIh,cI],
+ *   k [B,nb,cI] (already L2-normalised when normalize_qk), w [B,T,nIh] or
+ *   NULL, mask (uint8, element (b,t,n) at b*mask_bstride + t*mask_tstride + n;
+ *   NULL: block n visible when n < (t+1)/causal_m, every block when causal_m
+ *   is 0), logits [B,T,nb] or NULL, idx int64
+ *   [B,T,topk]: descending logit, ties by ascending block index, -1 for
+ *   infinite logits and past min(topk, nb). The sort runs in LDS: nb and
+ *   nIh*cI are bounded by 64 KiB of it (KCH_ERR_UNSUPPORTED beyond).
+ * kch_gen_attn: the joint softmax attention of naive_csa (idx given: the
+ *   selected rows, row maximum clamped at 0 with a sink, ops_csa.py:1100-1155)
+ *   or naive_hca (idx NULL, hca = 1: every block b < (t+1)/m, plain row
+ *   maximum, ops_hca.py:166-186), plus the causal window of win rows of local
+ *   [B,T,c] and the sink [nh] or NULL: q [B,T,nh,c] (L2-normalised inside
+ *   when normalize_q), kv [B,nb,c] -> out [B,T,nh,c]. ws: at least
+ *   kch_gen_attn_ws_bytes bytes (sparse = idx != NULL).
+ */
+int kch_gen_compress(const void* Ca, const void* Cb, const void* Za, const void* Zb, const void* Ba,
+                     const void* Bb, void* out, int B, int T, int m, int c, int dtype, void* stream);
+int kch_gen_l2norm(const void* x, void* y, long long rows, int c, int normalize, int dtype,
+                   void* stream);
+int kch_gen_indexer(const void* q, const void* k, const void* w, const void* mask,
+                    long long mask_bstride, long long mask_tstride, void* logits, long long* idx,
+                    int B, int T, int nb, int nIh, int cI, int topk, int causal_m, double scale,
+                    int normalize_q, int dtype, void* stream);
+size_t kch_gen_attn_ws_bytes(int B, int T, int nh, int nb, int topk, int win, int sparse, int dtype);
+int kch_gen_attn(const void* q, const void* kv, const long long* idx, const void* local,
+                 const void* sink, void* out, int B, int T, int nb, int nh, int c, int topk, int win,
+                 int m, double scale, int normalize_q, int hca, int dtype, void* ws, size_t ws_bytes,
+                 void* stream);
 
 /*
  * Gradients of the HCA attention: the backward of hca_core (ops_hca.py:132-194,

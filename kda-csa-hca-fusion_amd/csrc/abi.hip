@@ -308,6 +308,97 @@ int kch_kda_chunk_bwd(const void* q, const void* k, const void* v, const void* g
   return hip_status(fn, kch::kda_chunk_bwd_dispatch(p, dtype, ws, (hipStream_t)stream));
 }
 
+static bool gen_dtype_ok(int d) { return d == KCH_DT_F32 || d == KCH_DT_F64; }
+static const size_t kGenSmemMax = 65536;
+
+int kch_gen_compress(const void* Ca, const void* Cb, const void* Za, const void* Zb, const void* Ba,
+                     const void* Bb, void* out, int B, int T, int m, int c, int dtype, void* stream) {
+  const char* fn = "kch_gen_compress";
+  if (!gen_dtype_ok(dtype)) return fail(KCH_ERR_UNSUPPORTED, "%s: dtype %d (fp32 or fp64)", fn, dtype);
+  if (B < 0 || T < 0 || m < 1 || c < 1 || T % m)
+    return fail(KCH_ERR_INVALID, "%s: bad sizes B=%d T=%d m=%d c=%d (T a multiple of m)", fn, B, T, m, c);
+  const bool two = Cb || Zb || Bb;
+  if (two && !(Cb && Zb && Bb)) return fail(KCH_ERR_INVALID, "%s: Cb, Zb, Bb go together", fn);
+  if ((long long)B * T * c >= (1LL << 40)) return fail(KCH_ERR_UNSUPPORTED, "%s: tensors too large", fn);
+  if (B == 0 || T == 0) return KCH_OK;
+  if (!Ca || !Za || !Ba || !out) return fail(KCH_ERR_INVALID, "%s: null tensor pointer", fn);
+  kch::GenCompressParams p;
+  p.Ca = Ca; p.Cb = Cb; p.Za = Za; p.Zb = Zb; p.Ba = Ba; p.Bb = Bb; p.out = out;
+  p.B = B; p.T = T; p.m = m; p.c = c; p.overlapped = two ? 1 : 0;
+  return hip_status(fn, kch::gen_compress_launch(p, dtype == KCH_DT_F64, (hipStream_t)stream));
+}
+
+int kch_gen_l2norm(const void* x, void* y, long long rows, int c, int normalize, int dtype,
+                   void* stream) {
+  const char* fn = "kch_gen_l2norm";
+  if (!gen_dtype_ok(dtype)) return fail(KCH_ERR_UNSUPPORTED, "%s: dtype %d (fp32 or fp64)", fn, dtype);
+  if (rows < 0 || c < 1) return fail(KCH_ERR_INVALID, "%s: bad sizes rows=%lld c=%d", fn, rows, c);
+  if (rows == 0) return KCH_OK;
+  if (!x || !y) return fail(KCH_ERR_INVALID, "%s: null tensor pointer", fn);
+  return hip_status(fn, kch::gen_l2norm_launch(x, y, rows, c, normalize, dtype == KCH_DT_F64,
+                                               (hipStream_t)stream));
+}
+
+int kch_gen_indexer(const void* q, const void* k, const void* w, const void* mask,
+                    long long mask_bstride, long long mask_tstride, void* logits, long long* idx,
+                    int B, int T, int nb, int nIh, int cI, int topk, int causal_m, double scale,
+                    int normalize_q, int dtype, void* stream) {
+  const char* fn = "kch_gen_indexer";
+  if (!gen_dtype_ok(dtype)) return fail(KCH_ERR_UNSUPPORTED, "%s: dtype %d (fp32 or fp64)", fn, dtype);
+  if (B < 0 || T < 0 || nb < 0 || nIh < 1 || cI < 1 || topk < 0 || causal_m < 0)
+    return fail(KCH_ERR_INVALID, "%s: bad sizes B=%d T=%d nb=%d nIh=%d cI=%d topk=%d m=%d", fn, B, T,
+                nb, nIh, cI, topk, causal_m);
+  if (std::isnan(scale)) return fail(KCH_ERR_INVALID, "%s: scale is NaN", fn);
+  if (nb > (1 << 20)) return fail(KCH_ERR_UNSUPPORTED, "%s: nb=%d too large", fn, nb);
+  const size_t smem = kch::gen_indexer_smem(nIh, cI, nb, dtype == KCH_DT_F64);
+  if (smem > kGenSmemMax)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: nIh*cI=%d and n_blocks=%d need %zu bytes of LDS (max %zu)",
+                fn, nIh * cI, nb, smem, kGenSmemMax);
+  if (B == 0 || T == 0 || (topk == 0 && !logits)) return KCH_OK;
+  if (!q || (!k && nb) || (!idx && topk)) return fail(KCH_ERR_INVALID, "%s: null tensor pointer", fn);
+  kch::GenIndexerParams p;
+  p.q = q; p.k = k; p.w = w; p.mask = mask; p.mask_bstride = mask_bstride;
+  p.mask_tstride = mask_tstride; p.logits = logits; p.idx = idx;
+  p.B = B; p.T = T; p.nb = nb; p.nIh = nIh; p.cI = cI; p.topk = topk;
+  p.normalize_q = normalize_q; p.sortN = 0; p.causal_m = causal_m; p.scale = scale;
+  return hip_status(fn, kch::gen_indexer_launch(p, dtype == KCH_DT_F64, (hipStream_t)stream));
+}
+
+size_t kch_gen_attn_ws_bytes(int B, int T, int nh, int nb, int topk, int win, int sparse, int dtype) {
+  if (B < 0 || T < 0 || nh < 1 || nb < 0 || topk < 0 || win < 0 || !gen_dtype_ok(dtype)) return 0;
+  const size_t K = (size_t)(sparse ? topk : nb) + win;
+  return (size_t)B * T * nh * K * (dtype == KCH_DT_F64 ? 8 : 4) + 256;
+}
+
+int kch_gen_attn(const void* q, const void* kv, const long long* idx, const void* local,
+                 const void* sink, void* out, int B, int T, int nb, int nh, int c, int topk, int win,
+                 int m, double scale, int normalize_q, int hca, int dtype, void* ws, size_t ws_bytes,
+                 void* stream) {
+  const char* fn = "kch_gen_attn";
+  if (!gen_dtype_ok(dtype)) return fail(KCH_ERR_UNSUPPORTED, "%s: dtype %d (fp32 or fp64)", fn, dtype);
+  if (B < 0 || T < 0 || nb < 0 || nh < 1 || c < 1 || topk < 0 || win < 0 || m < 1)
+    return fail(KCH_ERR_INVALID, "%s: bad sizes B=%d T=%d nb=%d nh=%d c=%d topk=%d win=%d m=%d", fn,
+                B, T, nb, nh, c, topk, win, m);
+  if (std::isnan(scale)) return fail(KCH_ERR_INVALID, "%s: scale is NaN", fn);
+  const int K = (idx ? topk : nb) + win;
+  const size_t smem = kch::gen_attn_smem(nh, c, K, dtype == KCH_DT_F64);
+  if (smem > kGenSmemMax)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: nh*c=%d with %d candidates needs %zu bytes of LDS (max %zu)",
+                fn, nh * c, K, smem, kGenSmemMax);
+  if (B == 0 || T == 0) return KCH_OK;
+  if (!q || !out || (!kv && nb) || (win > 0 && !local))
+    return fail(KCH_ERR_INVALID, "%s: null tensor pointer", fn);
+  const size_t need = kch_gen_attn_ws_bytes(B, T, nh, nb, topk, win, idx != nullptr, dtype);
+  if (!ws || ws_bytes < need)
+    return fail(KCH_ERR_INVALID, "%s: workspace of %zu bytes required, got %zu", fn, need,
+                ws ? ws_bytes : (size_t)0);
+  kch::GenAttnParams p;
+  p.q = q; p.kv = kv; p.idx = idx; p.local = local; p.sink = sink; p.out = out; p.ws = ws;
+  p.B = B; p.T = T; p.nb = nb; p.nh = nh; p.c = c; p.topk = topk; p.win = win; p.m = m;
+  p.normalize_q = normalize_q; p.hca = hca; p.scale = scale;
+  return hip_status(fn, kch::gen_attn_launch(p, dtype == KCH_DT_F64, (hipStream_t)stream));
+}
+
 size_t kch_hca_attn_bwd_ws_bytes(int B, int T, int nh, int c, int m2, int win) {
   if (B <= 0 || T <= 0 || nh < 1 || (c != 64 && c != 128) || m2 < 1 || T % m2 || win < 0) return 0;
   return kch::hca_bwd_ws_bytes(B, T, nh, c, m2, win, 0);

@@ -353,4 +353,49 @@ struct CacheStepParams {
 };
 hipError_t cache_step_dispatch(const CacheStepParams& p, int dtype, hipStream_t s);
 
+
+// Generic CSA / HCA forward (csa_hca_generic.hip): T = float or double
+// (f64), any head dims, indexer heads and indexer mask.
+struct GenCompressParams {
+  const void* Ca;
+  const void* Cb;  // null: single branch
+  const void* Za;
+  const void* Zb;
+  const void* Ba;
+  const void* Bb;
+  void* out;       // [B, T/m, c]
+  int B, T, m, c, overlapped;
+};
+struct GenIndexerParams {
+  const void* q;     // [B,T,nIh,cI]
+  const void* k;     // [B,nb,cI] (normalised by the caller when normalize_qk)
+  const void* w;     // [B,T,nIh] or null (every head weighs 1)
+  const void* mask;  // uint8, element (b, t, n) at b*mask_bstride + t*mask_tstride + n, or null
+  long long mask_bstride, mask_tstride;
+  void* logits;      // [B,T,nb] or null
+  void* idx;         // int64 [B,T,topk]
+  int B, T, nb, nIh, cI, topk, normalize_q, sortN;
+  int causal_m;      // mask null: block n visible when n < (t+1)/causal_m (0: every block)
+  double scale;
+};
+struct GenAttnParams {
+  const void* q;      // [B,T,nh,c]
+  const void* kv;     // [B,nb,c] key/value rows (normalised when the keys are)
+  const void* idx;    // int64 [B,T,topk] (CSA) or null (HCA: every block b < (t+1)/m)
+  const void* local;  // [B,T,c] window rows (win > 0)
+  const void* sink;   // [nh] or null
+  void* out;          // [B,T,nh,c]
+  void* ws;           // [B,T,nh,K] scores and weights, K = (topk or nb) + win
+  int B, T, nb, nh, c, topk, win, m, normalize_q, hca;
+  double scale;
+};
+int gen_sort_n(int nb);
+size_t gen_indexer_smem(int nIh, int cI, int nb, bool f64);
+size_t gen_attn_smem(int nh, int c, int K, bool f64);
+hipError_t gen_compress_launch(const GenCompressParams& p, bool f64, hipStream_t s);
+hipError_t gen_l2norm_launch(const void* x, void* y, long long rows, int c, int normalize, bool f64,
+                             hipStream_t s);
+hipError_t gen_indexer_launch(GenIndexerParams p, bool f64, hipStream_t s);
+hipError_t gen_attn_launch(const GenAttnParams& p, bool f64, hipStream_t s);
+
 }  // namespace kch

@@ -36,6 +36,10 @@ _SIGNATURES = {
     "kch_kda_recurrent_fwd_f64": [_P] * 8 + [_I] * 6 + [_D, _D, _P],
     "kch_kda_recurrent_bwd": [_P] * 14 + [_I] * 6 + [_D, _D, _I, _P, _SZ, _P],
     "kch_kda_chunk_bwd": [_P] * 14 + [_I] * 6 + [_D, _D, _I, _P, _SZ, _P],
+    "kch_gen_compress": [_P] * 7 + [_I] * 5 + [_P],
+    "kch_gen_l2norm": [_P, _P, _L, _I, _I, _I, _P],
+    "kch_gen_indexer": [_P] * 4 + [_L, _L, _P, _P] + [_I] * 7 + [_D, _I, _I, _P],
+    "kch_gen_attn": [_P] * 6 + [_I] * 8 + [_D, _I, _I, _I, _P, _SZ, _P],
     "kch_hca_attn_bwd": [_P] * 16 + [_I] * 6 + [_F, _P, _SZ, _P],
     "kch_csa_attn_bwd": [_P] * 24 + [_I] * 7 + [_F, _I, _P, _SZ, _P],
     "kch_kda_gates_bwd": [_P, _L, _P, _L] + [_P] * 7 + [_I] * 6 + [_F, _I, _P],
@@ -79,6 +83,7 @@ _QUERIES = {
     "kch_kda_chunk_ws_bytes": (_SZ, [_I] * 7),
     "kch_kda_recurrent_bwd_ws_bytes": (_SZ, [_I] * 6),
     "kch_kda_chunk_bwd_ws_bytes": (_SZ, [_I] * 7),
+    "kch_gen_attn_ws_bytes": (_SZ, [_I] * 8),
     "kch_hca_attn_bwd_ws_bytes": (_SZ, [_I] * 6),
     "kch_csa_attn_bwd_ws_bytes": (_SZ, [_I] * 7),
     "kch_csa_ste_bwd_ws_bytes": (_SZ, [_I] * 5),

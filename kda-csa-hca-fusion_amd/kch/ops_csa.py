@@ -29,7 +29,10 @@ Differences, all documented:
   reference's ``torch.topk`` leaves that order unspecified).
 * Attention keys/values are the L2-normalised compressed rows rounded to
   bfloat16 (the reference keeps them in fp32); scores and the softmax are fp32.
-* float64 inputs raise ``NotImplementedError``.
+* float64 inputs, head dims ``c`` or ``c_I`` above 128, more than 16 indexer
+  heads and non-standard ``causal_block_mask`` run on the generic SIMT
+  kernels (``kch.generic``; float64 computed in float64), forward only:
+  gradients through them raise ``NotImplementedError``.
 """
 
 from __future__ import annotations
@@ -39,7 +42,7 @@ import contextlib
 import torch
 import torch.nn.functional as F
 
-from . import _lib
+from . import _lib, generic
 
 # the top-k selections made while ``record_selections()`` is active, else None
 _selection_log = None
@@ -194,6 +197,9 @@ def _compress(fn, C, Z, B_pos, m, *, out_raw=True, key=None, normalize=False, lo
         raise ValueError(f"compression factor m={m} must be >= 1")
     if T % m != 0:
         raise ValueError(f"T={T} must be divisible by m={m}")
+    if key is None and local is None and generic.compute_dtype(C, Z, B_pos) == torch.float64:
+        _lib.require_gpu(fn, C, Z, B_pos)
+        return generic.compress(C, Z, B_pos, m)
     _check_gpu_dtype(fn, C, Z)
     nb = T // m
     C, ldc = _rows(C)
@@ -217,6 +223,10 @@ def _compress_overlapped(fn, Ca, Cb, Za, Zb, Ba, Bb, m, *, out_raw=True, key=Non
         raise ValueError(f"T={T} must be divisible by m={m}")
     if T == 0:
         return Ca.new_zeros(B_, 0, c)
+    if key is None and local is None and \
+            generic.compute_dtype(Ca, Cb, Za, Zb, Ba, Bb) == torch.float64:
+        _lib.require_gpu(fn, Ca, Cb, Za, Zb, Ba, Bb)
+        return generic.compress(Ca, Za, Ba, m, Cb, Zb, Bb)
     _check_gpu_dtype(fn, Ca, Cb, Za, Zb)
     nb = T // m
     (Ca, lca), (Cb, lcb), (Za, lza), (Zb, lzb) = (_rows(x) for x in (Ca, Cb, Za, Zb))
@@ -302,7 +312,9 @@ def csa_lightning_indexer(q_idx, k_idx, w_idx, topk, scale=None, causal_block_ma
     Returns int64 indices ``[B, T, topk]`` (descending logit, ties by ascending
     block index, -1 for masked blocks and padding); with
     ``return_soft_weights`` also the NaN-safe softmax of the logits.
-    ``causal_block_mask`` must be ``None`` or the standard block-causal mask.
+    Any ``causal_block_mask`` broadcastable to ``[B, T, n_blocks]``: the
+    standard block-causal one runs on the MFMA indexer, others (and float64,
+    c_I > 128, nIh > 16) on the generic kernels.
     """
     fn = "csa_lightning_indexer"
     if topk < 0:
@@ -319,10 +331,24 @@ def csa_lightning_indexer(q_idx, k_idx, w_idx, topk, scale=None, causal_block_ma
         raise NotImplementedError(
             "ste_mode='aux_contrastive' is reserved for a future implementation of "
             "DeepSeek-V4's contrastive auxiliary loss on the indexer selection logits.")
-    _check_gpu_dtype(fn, q_idx, k_idx, w_idx)
+    _lib.require_gpu(fn, q_idx, k_idx, w_idx)
     if scale is None:
         scale = 1.0 if normalize_qk else q_idx.shape[-1] ** -0.5
     B_, T, HI, DI = q_idx.shape
+    n_blocks = k_idx.shape[1]
+    std_m = None
+    if causal_block_mask is not None:
+        std_m = _standard_block_mask_m(causal_block_mask.to(q_idx.device), T, n_blocks)
+    if (generic.needs_generic_csa(dtype_tensors=(q_idx, k_idx, w_idx), c_I=DI, nIh=HI)
+            or (causal_block_mask is not None and std_m is None)):
+        # float64, wide heads or a mask other than the block-causal one
+        kn = generic.l2norm(k_idx, normalize_qk, dt=generic.compute_dtype(q_idx, k_idx, w_idx))
+        idx, logits = generic.indexer(q_idx, kn, w_idx, topk, scale, mask=causal_block_mask,
+                                      normalize_q=normalize_qk, want_logits=return_soft_weights)
+        if return_soft_weights:
+            return idx, _nan_safe_softmax(logits, dim=-1)
+        return idx
+    _check_gpu_dtype(fn, q_idx, k_idx, w_idx)
     DIp = _kernel_size(fn, "c_I", DI, _IDX_DIMS)
     HIp = _kernel_size(fn, "nIh", HI, _IDX_HEADS)
     if (DIp, HIp) != (DI, HI):
@@ -336,11 +362,7 @@ def csa_lightning_indexer(q_idx, k_idx, w_idx, topk, scale=None, causal_block_ma
     n_blocks = k_idx.shape[1]
     dense, m = True, 1
     if causal_block_mask is not None:
-        m = _standard_block_mask_m(causal_block_mask.to(q_idx.device), T, n_blocks)
-        if m is None:
-            raise NotImplementedError(
-                f"{fn}: the HIP backend supports causal_block_mask=None or the standard "
-                f"block-causal mask (t + 1) // m > b only")
+        m = std_m
         dense = False
     k_norm = l2_normalize_rows(k_idx, normalize=normalize_qk)
     q_idx = _aligned(q_idx)
@@ -385,6 +407,9 @@ def csa_core(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, *, m,
     if torch.is_grad_enabled() and any(
             t is not None and t.requires_grad
             for t in (Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, sink_logits)):
+        if generic.needs_generic_csa(dtype_tensors=(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx),
+                                     c=Ca.shape[-1], c_I=K_idx.shape[-1], nIh=q_idx.shape[2]):
+            generic.grad_not_supported("csa_core", "float64 inputs or c, c_I > 128, nIh > 16")
         out, idx = _CsaCoreFunction.apply(
             Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, sink_logits,
             dict(m=m, topk=topk, sliding_window=sliding_window, normalize_qk=normalize_qk,
@@ -404,6 +429,16 @@ def _csa_core(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, *, m
         scale = 1.0 if normalize_qk else c ** -0.5
     if idx_scale is None:
         idx_scale = 1.0 if normalize_qk else c_I ** -0.5
+    if generic.needs_generic_csa(dtype_tensors=(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx),
+                                 c=c, c_I=c_I, nIh=nIh):
+        _lib.require_gpu(fn, Ca, q, q_idx)
+        res = generic.csa_core(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, m=m,
+                               topk=topk, sliding_window=sliding_window, sink_logits=sink_logits,
+                               normalize_qk=normalize_qk, scale=scale, idx_scale=idx_scale,
+                               return_indices=True)
+        if topk > 0:
+            _log_selection(res[1])
+        return res if return_indices else res[0]
     cp = _kernel_size(fn, "c", c, _HEAD_DIMS)
     cIp = _kernel_size(fn, "c_I", c_I, _IDX_DIMS)
     nIp = _kernel_size(fn, "nIh", nIh, _IDX_HEADS)
@@ -814,11 +849,7 @@ def naive_csa(H, W_aKV, W_bKV, W_aZ, W_bZ, Ba, Bb, W_DQ, W_UQ, W_IUQ, W_w, W_KV_
             "DeepSeek-V4's contrastive auxiliary loss on the indexer selection logits. "
             "Use 'topk_columns' (the default, simplified STE) or 'full_softmax' (dense STE) "
             "for now.")
-    _check_gpu_dtype(fn, H)
-    if c > _HEAD_DIMS[-1] or c_I > _IDX_DIMS[-1] or nIh > _IDX_HEADS[-1]:
-        raise NotImplementedError(
-            f"{fn}: the HIP kernels cover c <= 128, c_I <= 128 and nIh <= 16; got c={c}, "
-            f"c_I={c_I}, nIh={nIh}")
+    _lib.require_gpu(fn, H)
     original_T = T
     pad = (-T) % m
     if pad:

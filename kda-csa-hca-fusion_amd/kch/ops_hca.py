@@ -5,9 +5,10 @@ Same signature, validation (``ValueError`` / ``TypeError`` messages of
 GEMMs on the GPU (W_KV, W_Z and W_DQ concatenated: one GEMM reads H once); the heavy compression (with L2-normalised bf16 key rows and
 the per-token window keys) and the dense MQA over compressed blocks + window +
 sink run in ``libkch.so``. Keys/values are bf16-rounded L2-normalised rows
-(fp32 in the reference); float64 is not supported. With gradients enabled the
-projections run through autograd and the core's backward is
-``kch_hca_attn_bwd`` (fp32).
+(fp32 in the reference). float64 inputs and head dims c above 128 run on the
+generic SIMT kernels (``kch.generic``; float64 computed in float64), forward
+only. With gradients enabled the projections run through autograd and the
+core's backward is ``kch_hca_attn_bwd`` (fp32).
 """
 
 from __future__ import annotations
@@ -15,7 +16,7 @@ from __future__ import annotations
 import torch
 import torch.nn.functional as F
 
-from . import _lib
+from . import _lib, generic
 from .ops_csa import (_HEAD_DIMS, _aligned, _cat_cached, _check_gpu_dtype, _compress, _f32_cached,
                       _head_groups, _kernel_size, _linear_up, _pad_last, l2_normalize_rows)
 
@@ -32,6 +33,8 @@ def hca_core(C, Z, q, B_pos, *, m2, sliding_window=0, sink_logits=None, scale=1.
     if torch.is_grad_enabled() and any(
             t is not None and t.requires_grad
             for t in (C, Z, q, B_pos, sink_logits, C_local_raw)):
+        if generic.needs_generic_csa(dtype_tensors=(C, Z, q, C_local_raw), c=C.shape[-1]):
+            generic.grad_not_supported("hca_core", "float64 inputs or c > 128")
         return _HcaCoreFunction.apply(C, Z, q, B_pos, sink_logits, C_local_raw, m2,
                                       sliding_window, scale)
     return _hca_core_fwd(C, Z, q, B_pos, m2=m2, sliding_window=sliding_window,
@@ -137,6 +140,10 @@ def _hca_core_fwd(C, Z, q, B_pos, *, m2, sliding_window=0, sink_logits=None, sca
     fn = "hca_core"
     B_, T, c = C.shape
     nh = q.shape[2]
+    if generic.needs_generic_csa(dtype_tensors=(C, Z, q, C_local_raw), c=c):
+        _lib.require_gpu(fn, C, Z, q)
+        return generic.hca_core(C, Z, q, B_pos, m2=m2, sliding_window=sliding_window,
+                                sink_logits=sink_logits, scale=scale, C_local_raw=C_local_raw)
     cp = _kernel_size(fn, "c", c, _HEAD_DIMS)
     if cp != c:
         # zero channels compress to zero and add nothing to norms and scores
@@ -218,9 +225,7 @@ def naive_hca(H, W_KV, W_Z, B_pos, W_DQ, W_UQ, *, m2, nh, c, dc, scale=1.0, slid
             z = torch.zeros(B_, 0, c, dtype=H.dtype, device=device)
             return out_empty, (z, z.clone())
         return out_empty
-    _check_gpu_dtype(fn, H)
-    if c > _HEAD_DIMS[-1]:
-        raise NotImplementedError(f"{fn}: the HIP kernels cover c <= 128; got c={c}")
+    _lib.require_gpu(fn, H)
     original_T = T
     pad = (-T) % m2
     if pad:
