@@ -13,9 +13,12 @@
 //   run (the transposed 3-tap filter), and the run's sums for the filter taps
 //   and the bias, added to fp32 buffers; the first run also writes the
 //   lookback rows' gradient when asked.
-// layer_norm_bwd_kernel wave per row, 16 rows per wave: dx from the recomputed
-//   mean and rstd; the rows' dy x^ and dy sums stay in registers, meet in LDS
-//   across the four waves, then add into fp32 buffers.
+// layer_norm_bwd_kernel wave per row, 8 waves per workgroup (4 above 2048
+//   channels), 1 to 16 rows per wave (as many as keep about 1024 workgroups in flight): dx from the
+//   recomputed mean and rstd; the rows' dy x^ and dy sums stay in registers,
+//   meet in LDS across the eight waves, then add into fp32 buffers. At 4096
+//   rows of 2048 one row per wave takes the kernel from 366 us (64 workgroups
+//   of 16 rows per wave, one wave per CU) to the latency of a few rows.
 
 #include <hip/hip_runtime.h>
 
@@ -138,12 +141,13 @@ __global__ __launch_bounds__(256) void short_conv_bwd_kernel(ShortConvBwdParams 
   }
 }
 
-constexpr int kLnRowsPerWave = 16;
+constexpr int kLnWaves = 8;
+constexpr int kLnMaxRowsPerWave = 16;
 
 // NJ = channels per lane (d <= 64 NJ): the rows' dy x^ and dy sums stay in
 // registers; the four waves meet in LDS at the end.
-template <typename T, typename WT, int NJ>
-__global__ __launch_bounds__(256) void layer_norm_bwd_kernel(LayerNormBwdParams p) {
+template <typename T, typename WT, int NJ, int NW>
+__global__ __launch_bounds__(64 * NW) void layer_norm_bwd_kernel(LayerNormBwdParams p, int rpw) {
   extern __shared__ float lds[];  // [2][d]
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int d = p.d;
@@ -155,8 +159,8 @@ __global__ __launch_bounds__(256) void layer_norm_bwd_kernel(LayerNormBwdParams 
     aw[j] = ab[j] = 0.f;
     wv[j] = i < d ? to_f32(w[i]) : 0.f;
   }
-  const long long r0 = ((long long)blockIdx.x * 4 + wave) * kLnRowsPerWave;
-  for (int rr = 0; rr < kLnRowsPerWave; ++rr) {
+  const long long r0 = ((long long)blockIdx.x * NW + wave) * rpw;
+  for (int rr = 0; rr < rpw; ++rr) {
     const long long row = r0 + rr;
     if (row >= p.rows) break;
     const T* x = static_cast<const T*>(p.x) + row * d;
@@ -200,8 +204,8 @@ __global__ __launch_bounds__(256) void layer_norm_bwd_kernel(LayerNormBwdParams 
       }
     }
   }
-  // the four waves' sums, one wave after another into [2][d] of LDS
-  for (int wv_ = 0; wv_ < 4; ++wv_) {
+  // the waves' sums, one wave after another into [2][d] of LDS
+  for (int wv_ = 0; wv_ < NW; ++wv_) {
     if (wave == wv_) {
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
@@ -214,21 +218,32 @@ __global__ __launch_bounds__(256) void layer_norm_bwd_kernel(LayerNormBwdParams 
     }
     __syncthreads();
   }
-  for (int i = threadIdx.x; i < d; i += 256) {
+  for (int i = threadIdx.x; i < d; i += 64 * NW) {
     atomicAdd(p.dw + i, lds[i]);
     if (p.db) atomicAdd(p.db + i, lds[d + i]);
   }
 }
 
+template <typename T, typename WT, int NJ, int NW>
+void ln_bwd_launch(const LayerNormBwdParams& p, hipStream_t s) {
+  long long rpw = (p.rows + NW * 1024 - 1) / (NW * 1024);
+  rpw = rpw < 1 ? 1 : (rpw > kLnMaxRowsPerWave ? kLnMaxRowsPerWave : rpw);
+  const long long per_block = NW * rpw;
+  const unsigned blocks = (unsigned)((p.rows + per_block - 1) / per_block);
+  const size_t lds = (size_t)2 * p.d * sizeof(float);
+  hipLaunchKernelGGL((layer_norm_bwd_kernel<T, WT, NJ, NW>), dim3(blocks), dim3(64 * NW), lds, s, p,
+                     (int)rpw);
+}
+
+// eight waves per workgroup up to 2048 channels; four beyond (their rows
+// take twice the registers)
 template <typename T, typename WT>
 hipError_t ln_bwd_nj(const LayerNormBwdParams& p, hipStream_t s) {
-  const unsigned blocks = (unsigned)((p.rows + 4 * kLnRowsPerWave - 1) / (4 * kLnRowsPerWave));
-  const size_t lds = (size_t)2 * p.d * sizeof(float);
   const int nj = (p.d + 63) / 64;
-  if (nj <= 8) hipLaunchKernelGGL((layer_norm_bwd_kernel<T, WT, 8>), dim3(blocks), dim3(256), lds, s, p);
-  else if (nj <= 16) hipLaunchKernelGGL((layer_norm_bwd_kernel<T, WT, 16>), dim3(blocks), dim3(256), lds, s, p);
-  else if (nj <= 32) hipLaunchKernelGGL((layer_norm_bwd_kernel<T, WT, 32>), dim3(blocks), dim3(256), lds, s, p);
-  else hipLaunchKernelGGL((layer_norm_bwd_kernel<T, WT, 64>), dim3(blocks), dim3(256), lds, s, p);
+  if (nj <= 8) ln_bwd_launch<T, WT, 8, kLnWaves>(p, s);
+  else if (nj <= 16) ln_bwd_launch<T, WT, 16, kLnWaves>(p, s);
+  else if (nj <= 32) ln_bwd_launch<T, WT, 32, kLnWaves>(p, s);
+  else ln_bwd_launch<T, WT, 64, 4>(p, s);
   return hipGetLastError();
 }
 
