@@ -24,7 +24,7 @@
 //   (i, j, channel), with the reference's clamp(max=50) on the exponent.
 //   Transposes of elementwise data (beta k e(G), k e(G_l - G), beta v) are
 //   MFMA products with a 0/1 selector matrix, exact in fp32 accumulation.
-// kda_state_kernel  one workgroup per (b, hv, 64-column slice of V); sibling
+// kda_state_kernel  one workgroup per (b, hv, 64-, 32- or 16-column slice of V); sibling
 //   slices of one head sit on the same XCD so the shared per-chunk operands
 //   are read from HBM once. The state lives in MFMA accumulators; the operands
 //   of chunk n+2 are prefetched into registers while chunk n is processed.
@@ -870,9 +870,13 @@ hipError_t launch_split(const KdaParams& p, SplitPtrs w, hipStream_t s) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   // 32-column V slices when 64-column ones would leave more than half of the
-  // CUs without a state workgroup (one workgroup per CU either way: the
-  // operand sets need the whole register file)
-  if (V == 128 && 2LL * p.B * p.HV * (V / 64) <= cu_count())
+  // CUs without a state workgroup, 16-column ones when 32-column ones would
+  // (the chain of one chunk is then half as long, and every CU has a head's
+  // slice: the C4 prefill's B = 2)
+  const long long heads = (long long)p.B * p.HV;
+  if (V == 128 && 2LL * heads * (V / 32) <= cu_count())
+    hipLaunchKernelGGL((kda_state_kernel<K, 16, InT>), dim3(p.B * p.HV * (V / 16)), dim3(256), 0, s, p, w);
+  else if (V == 128 && 2LL * heads * (V / 64) <= cu_count())
     hipLaunchKernelGGL((kda_state_kernel<K, 32, InT>), dim3(p.B * p.HV * (V / 32)), dim3(256), 0, s, p, w);
   else
     hipLaunchKernelGGL((kda_state_kernel<K, 64, InT>), dim3(p.B * p.HV * (V / 64)), dim3(256), 0, s, p, w);
