@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define KCH_ABI_VERSION 16
+#define KCH_ABI_VERSION 17
 
 #define KCH_OK 0
 #define KCH_ERR_INVALID 1     /* bad pointer / shape / argument */
@@ -193,8 +193,11 @@ int kch_gen_attn(const void* q, const void* kv, const long long* idx, const void
 /*
  * Gradients of the HCA attention: the backward of hca_core (ops_hca.py:132-194,
  * which the reference differentiates with autograd; the gradient check of the
- * hybrid stack, run_correctness.py:2710-2830, runs through it). fp32 tensors:
- * q, d_out [B,T,nh,c] (queries as given; the kernel normalises them), kc / raw
+ * hybrid stack, run_correctness.py:2710-2830, runs through it). q, d_out and
+ * dq [B,T,nh,c] are stored in qdt (KCH_DT_F32 / BF16 / F16; bf16 and fp16
+ * need nh <= 16, the MFMA kernels' limit: the caller runs more heads as
+ * groups), the queries as given (the kernel normalises them); the other
+ * tensors are fp32: kc / raw
  * [B,T/m2,c] (the L2-normalised and the raw compressed rows of C, Z, B_pos,
  * from kch_compress), kl / lsrc [B,T,c] (the normalised window rows and the
  * rows they normalise; NULL when win = 0), C, Z [B,T,c], B_pos [m2,c], sink
@@ -206,11 +209,11 @@ int kch_gen_attn(const void* q, const void* kv, const long long* idx, const void
  * 256-byte aligned, kch_hca_attn_bwd_ws_bytes bytes.
  */
 size_t kch_hca_attn_bwd_ws_bytes(int B, int T, int nh, int c, int m2, int win);
-int kch_hca_attn_bwd(const float* q, const float* d_out, const float* kc, const float* raw,
+int kch_hca_attn_bwd(const void* q, const void* d_out, const float* kc, const float* raw,
                      const float* kl, const float* lsrc, const float* C, const float* Z,
-                     const float* B_pos, const float* sink, float* dq, float* dC, float* dZ,
+                     const float* B_pos, const float* sink, void* dq, float* dC, float* dZ,
                      float* dBp, float* dlocal, float* sink_part, int B, int T, int nh, int c,
-                     int m2, int win, float scale, void* ws, size_t ws_bytes, void* stream);
+                     int m2, int win, float scale, int qdt, void* ws, size_t ws_bytes, void* stream);
 
 /*
  * Gradients of the CSA attention: the backward of the sparse attention of
@@ -220,7 +223,7 @@ int kch_hca_attn_bwd(const float* q, const float* d_out, const float* kc, const 
  * selection, -1 = unused slot), the overlapped compression's inputs Ca, Cb,
  * Za, Zb [B,T,c], Ba, Bb [m,c] (kc / raw from kch_compress_overlapped; kl,
  * lsrc the window rows of Ca), normalize = 0 for normalize_qk=False (queries
- * and keys used as given). Outputs: dq; dCa, dCb, dZa, dZb [B,T,c] (dCb, dZb
+ * and keys used as given; q, d_out, dq then fp32). Outputs: dq; dCa, dCb, dZa, dZb [B,T,c] (dCb, dZb
  * must be zeroed by the caller: the last block's second-branch rows receive
  * nothing); dBap, dBbp [B,T/m,m,c]; sink_part as for HCA; slot_grad
  * [B,T,topk] (zeroed by the caller): the gradient of each selected row dotted
@@ -231,13 +234,14 @@ int kch_hca_attn_bwd(const float* q, const float* d_out, const float* kc, const 
  * gradient is added into dCa.
  */
 size_t kch_csa_attn_bwd_ws_bytes(int B, int T, int nh, int c, int m, int win, int topk);
-int kch_csa_attn_bwd(const float* q, const float* d_out, const float* kc, const float* raw,
+int kch_csa_attn_bwd(const void* q, const void* d_out, const float* kc, const float* raw,
                      const float* kl, const float* lsrc, const int* idx, const float* Ca,
                      const float* Cb, const float* Za, const float* Zb, const float* Ba,
-                     const float* Bb, const float* sink, float* dq, float* dCa, float* dCb,
+                     const float* Bb, const float* sink, void* dq, float* dCa, float* dCb,
                      float* dZa, float* dZb, float* dBap, float* dBbp, float* sink_part,
                      float* slot_grad, float* gsum, int B, int T, int nh, int c, int m, int topk,
-                     int win, float scale, int normalize, void* ws, size_t ws_bytes, void* stream);
+                     int win, float scale, int normalize, int qdt, void* ws, size_t ws_bytes,
+                     void* stream);
 
 /*
  * The STE surrogate's backward for the CSA indexer (ops_csa.py:1033-1099,

@@ -404,12 +404,16 @@ size_t kch_hca_attn_bwd_ws_bytes(int B, int T, int nh, int c, int m2, int win) {
   return kch::hca_bwd_ws_bytes(B, T, nh, c, m2, win, 0);
 }
 
-int kch_hca_attn_bwd(const float* q, const float* d_out, const float* kc, const float* raw,
+int kch_hca_attn_bwd(const void* q, const void* d_out, const float* kc, const float* raw,
                      const float* kl, const float* lsrc, const float* C, const float* Z,
-                     const float* B_pos, const float* sink, float* dq, float* dC, float* dZ,
+                     const float* B_pos, const float* sink, void* dq, float* dC, float* dZ,
                      float* dBp, float* dlocal, float* sink_part, int B, int T, int nh, int c,
-                     int m2, int win, float scale, void* ws, size_t ws_bytes, void* stream) {
+                     int m2, int win, float scale, int qdt, void* ws, size_t ws_bytes, void* stream) {
   const char* fn = "kch_hca_attn_bwd";
+  if (qdt < 0 || qdt > 2) return fail(KCH_ERR_INVALID, "%s: dtype %d (0 fp32, 1 bf16, 2 fp16)", fn, qdt);
+  if (qdt != 0 && nh > 16)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: bf16 / fp16 q and d_out take at most 16 heads a call (nh=%d)",
+                fn, nh);
   if (B < 0 || T < 1 || nh < 1 || m2 < 1 || win < 0)
     return fail(KCH_ERR_INVALID, "%s: bad sizes B=%d T=%d nh=%d m2=%d win=%d (T >= 1)", fn, B, T, nh,
                 m2, win);
@@ -436,6 +440,7 @@ int kch_hca_attn_bwd(const float* q, const float* d_out, const float* kc, const 
   p.q = q; p.dout = d_out; p.kc = kc; p.raw = raw; p.kl = kl; p.lsrc = lsrc;
   p.C = C; p.Z = Z; p.Bpos = B_pos; p.sink = sink;
   p.dq = dq; p.dC = dC; p.dZ = dZ; p.dBp = dBp; p.dlocal = dlocal; p.sink_part = sink_part;
+  p.qdt = qdt;
   p.B = B; p.T = T; p.nh = nh; p.c = c; p.m2 = m2; p.nb = T / m2; p.win = win;
   p.scale = scale;
   return hip_status(fn, kch::hca_bwd_dispatch(p, ws, (hipStream_t)stream));
@@ -447,14 +452,20 @@ size_t kch_csa_attn_bwd_ws_bytes(int B, int T, int nh, int c, int m, int win, in
   return kch::hca_bwd_ws_bytes(B, T, nh, c, m, win, topk);
 }
 
-int kch_csa_attn_bwd(const float* q, const float* d_out, const float* kc, const float* raw,
+int kch_csa_attn_bwd(const void* q, const void* d_out, const float* kc, const float* raw,
                      const float* kl, const float* lsrc, const int* idx, const float* Ca,
                      const float* Cb, const float* Za, const float* Zb, const float* Ba,
-                     const float* Bb, const float* sink, float* dq, float* dCa, float* dCb,
+                     const float* Bb, const float* sink, void* dq, float* dCa, float* dCb,
                      float* dZa, float* dZb, float* dBap, float* dBbp, float* sink_part,
                      float* slot_grad, float* gsum, int B, int T, int nh, int c, int m, int topk,
-                     int win, float scale, int normalize, void* ws, size_t ws_bytes, void* stream) {
+                     int win, float scale, int normalize, int qdt, void* ws, size_t ws_bytes,
+                     void* stream) {
   const char* fn = "kch_csa_attn_bwd";
+  if (qdt < 0 || qdt > 2) return fail(KCH_ERR_INVALID, "%s: dtype %d (0 fp32, 1 bf16, 2 fp16)", fn, qdt);
+  if (qdt != 0 && (nh > 16 || !normalize))
+    return fail(KCH_ERR_UNSUPPORTED,
+                "%s: bf16 / fp16 q and d_out need normalize=1 and at most 16 heads a call (nh=%d)", fn,
+                nh);
   if (B < 0 || T < 1 || nh < 1 || m < 1 || win < 0 || topk < 0)
     return fail(KCH_ERR_INVALID, "%s: bad sizes B=%d T=%d nh=%d m=%d win=%d topk=%d (T >= 1)", fn, B,
                 T, nh, m, win, topk);
@@ -490,6 +501,7 @@ int kch_csa_attn_bwd(const float* q, const float* d_out, const float* kc, const 
   p.slot_grad = topk > 0 ? slot_grad : nullptr;
   p.gsum = gsum;
   p.normalize = normalize ? 1 : 0;
+  p.qdt = qdt;
   p.B = B; p.T = T; p.nh = nh; p.c = c; p.m2 = m; p.nb = T / m; p.win = win;
   p.scale = scale;
   return hip_status(fn, kch::hca_bwd_dispatch(p, ws, (hipStream_t)stream));

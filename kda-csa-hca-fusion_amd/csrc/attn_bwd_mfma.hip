@@ -41,10 +41,6 @@ namespace {
 constexpr int KQC = 512;  // queries per chunk of the key pass (compressed rows)
 constexpr int KTR = 64;   // key rows per key-pass workgroup
 
-__device__ __forceinline__ void split2(float x, bf16_t& h, bf16_t& l) {
-  h = (bf16_t)x;
-  l = (bf16_t)(x - (float)h);
-}
 __device__ __forceinline__ bf16_t lo_of(float x) { return (bf16_t)(x - (float)(bf16_t)x); }
 
 __device__ __forceinline__ f32x4 mfma3(const bf16x8& ah, const bf16x8& al, const bf16x8& bh,
@@ -54,32 +50,74 @@ __device__ __forceinline__ f32x4 mfma3(const bf16x8& ah, const bf16x8& al, const
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
 }
 
-// Rows of HD fp32, grouped nin to a group, into bf16 hi / lo rows grouped nout
+// Four consecutive elements at element offset off of a row stored in dt
+// (DT_F32 / DT_BF16 / DT_F16), as fp32, and the rounded store of four.
+__device__ __forceinline__ float4 load4(const void* base, long long off, int dt) {
+  if (dt == DT_F32) return *reinterpret_cast<const float4*>(static_cast<const float*>(base) + off);
+  const uint2 r = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(base) + off);
+  if (dt == DT_BF16)
+    return make_float4(__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u),
+                       __uint_as_float(r.y << 16), __uint_as_float(r.y & 0xffff0000u));
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  const h4 h = __builtin_bit_cast(h4, r);
+  return make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
+}
+__device__ __forceinline__ void store4(void* base, long long off, float4 v, int dt) {
+  if (dt == DT_F32) {
+    *reinterpret_cast<float4*>(static_cast<float*>(base) + off) = v;
+  } else if (dt == DT_BF16) {
+    bf16x4 h = {(bf16_t)v.x, (bf16_t)v.y, (bf16_t)v.z, (bf16_t)v.w};
+    *reinterpret_cast<bf16x4*>(static_cast<bf16_t*>(base) + off) = h;
+  } else {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    h4 h = {(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
+    *reinterpret_cast<h4*>(static_cast<_Float16*>(base) + off) = h;
+  }
+}
+
+// Rows of HD values, grouped nin to a group, into bf16 hi / lo rows grouped nout
 // to a group (rows nin .. nout-1 of a group zero): x * f = hi + lo, f = 1 /
 // max(|row|, 1e-12) with normalize (written to rinv per output row), else 1.
-// One wave per output row.
-template <int HD>
-__global__ __launch_bounds__(256) void split_rows_kernel(const float* x, long long ngroups, int nin,
+// Each lane splits 8 consecutive values (16-byte stores of hi and lo), HD / 8
+// lanes per row; input in T (the rows as given: fp32, bf16 or fp16).
+template <int HD, typename T>
+__global__ __launch_bounds__(256) void split_rows_kernel(const T* x, long long ngroups, int nin,
                                                          int nout, bf16_t* hi, bf16_t* lo, float* rinv,
                                                          int normalize) {
-  constexpr int PL = HD / 64;  // values per lane
-  const long long orow = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (orow >= ngroups * nout) return;
-  const int lane = threadIdx.x & 63;
-  const long long g = orow / nout;
-  const int r = (int)(orow - g * nout);
-  float v[PL];
-  float ss = 0.f;
+  constexpr int LPR = HD / 8;  // lanes per row
+  constexpr int RPB = 256 / LPR;
+  const long long orow = (long long)blockIdx.x * RPB + threadIdx.x / LPR;
+  const int lc = threadIdx.x % LPR;
+  const bool act = orow < ngroups * nout;  // no early return: the row sum shuffles
+  const long long g = act ? orow / nout : 0;
+  const int r = act ? (int)(orow - g * nout) : nin;
+  float v[8];
+  if (r < nin) {
+    Load8<T>::run(x + (g * nin + r) * HD + 8 * lc, v);
+  } else {
 #pragma unroll
-  for (int i = 0; i < PL; ++i) {
-    v[i] = r < nin ? x[(g * nin + r) * HD + PL * lane + i] : 0.f;
-    ss += v[i] * v[i];
+    for (int i = 0; i < 8; ++i) v[i] = 0.f;
   }
   float f = 1.f;
-  if (normalize) f = r < nin ? l2_inv(wave_sum(ss)) : 0.f;
+  if (normalize) {
+    float ss = 0.f;
 #pragma unroll
-  for (int i = 0; i < PL; ++i) split2(v[i] * f, hi[orow * HD + PL * lane + i], lo[orow * HD + PL * lane + i]);
-  if (rinv && lane == 0) rinv[orow] = f;
+    for (int i = 0; i < 8; ++i) ss += v[i] * v[i];
+#pragma unroll
+    for (int m = LPR / 2; m >= 1; m >>= 1) ss += __shfl_xor(ss, m);
+    f = r < nin ? l2_inv(ss) : 0.f;
+  }
+  if (!act) return;
+  bf16x8 h, l;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float y = v[i] * f;
+    h[i] = (bf16_t)y;
+    l[i] = (bf16_t)(y - (float)h[i]);
+  }
+  *reinterpret_cast<bf16x8*>(hi + orow * HD + 8 * lc) = h;
+  *reinterpret_cast<bf16x8*>(lo + orow * HD + 8 * lc) = l;
+  if (rinv && lc == 0) rinv[orow] = f;
 }
 
 template <int CTRL>
@@ -319,7 +357,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_q_kernel(HcaBwdParams p) {
 #pragma unroll
     for (int tt = 0; tt < NT; ++tt) {
       float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (n < p.nh) x = *reinterpret_cast<const float4*>(p.q + (bt * p.nh + n) * HD + 16 * tt + 4 * q);
+      if (n < p.nh) x = load4(p.q, (bt * p.nh + n) * HD + 16 * tt + 4 * q, p.qdt);
       qv[tt][0] = x.x * rq; qv[tt][1] = x.y * rq; qv[tt][2] = x.z * rq; qv[tt][3] = x.w * rq;
 #pragma unroll
       for (int e = 0; e < 4; ++e) yd += qv[tt][e] * dq[tt][e];
@@ -333,8 +371,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_q_kernel(HcaBwdParams p) {
         float o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) o[e] = (big ? dq[tt][e] - qv[tt][e] * yd : dq[tt][e]) * rq;
-        *reinterpret_cast<float4*>(p.dq + (bt * p.nh + n) * HD + 16 * tt + 4 * q) =
-            make_float4(o[0], o[1], o[2], o[3]);
+        store4(p.dq, (bt * p.nh + n) * HD + 16 * tt + 4 * q, make_float4(o[0], o[1], o[2], o[3]), p.qdt);
       }
     }
     if (q == 0) {
@@ -580,19 +617,34 @@ hipError_t attn_bwd_mfma_dispatch(HcaBwdParams p, void* ws, hipStream_t s) {
   }
   p.mfma_parts = 1;
   p.part_qc = KQC;
-  auto grid_rows = [](long long rows) { return dim3((unsigned)((rows + 3) / 4)); };
+  // split_rows_kernel: 256 / (HD / 8) rows per workgroup
+  auto grid_rows = [](long long rows, int hd) {
+    const long long rpb = 256 / (hd / 8);
+    return dim3((unsigned)((rows + rpb - 1) / rpb));
+  };
+#define KCH_SPLIT_Q(HDV, QT)                                                                       \
+  do {                                                                                             \
+    hipLaunchKernelGGL((split_rows_kernel<HDV, QT>), grid_rows((long long)BT * 16, HDV), dim3(256), 0, \
+                       s, static_cast<const QT*>(p.q), (long long)BT, p.nh, 16, p.qs_hi, p.qs_lo, p.rq, 1); \
+    hipLaunchKernelGGL((split_rows_kernel<HDV, QT>), grid_rows((long long)BT * 16, HDV), dim3(256), 0, \
+                       s, static_cast<const QT*>(p.dout), (long long)BT, p.nh, 16, p.ds_hi, p.ds_lo,  \
+                       (float*)nullptr, 0);                                                        \
+  } while (0)
 #define KCH_SPLIT(HDV)                                                                              \
   do {                                                                                              \
-    hipLaunchKernelGGL((split_rows_kernel<HDV>), grid_rows((long long)BT * 16), dim3(256), 0, s, p.q, \
-                       (long long)BT, p.nh, 16, p.qs_hi, p.qs_lo, p.rq, 1);                         \
-    hipLaunchKernelGGL((split_rows_kernel<HDV>), grid_rows((long long)BT * 16), dim3(256), 0, s,     \
-                       p.dout, (long long)BT, p.nh, 16, p.ds_hi, p.ds_lo, (float*)nullptr, 0);       \
+    if (p.qdt == DT_BF16)                                                                           \
+      KCH_SPLIT_Q(HDV, bf16_t);                                                                     \
+    else if (p.qdt == DT_F16)                                                                       \
+      KCH_SPLIT_Q(HDV, _Float16);                                                                   \
+    else                                                                                            \
+      KCH_SPLIT_Q(HDV, float);                                                                      \
     if (p.nb > 0)                                                                                   \
-      hipLaunchKernelGGL((split_rows_kernel<HDV>), grid_rows((long long)p.B * p.nb), dim3(256), 0, s, \
-                         p.kc, (long long)p.B * p.nb, 1, 1, p.kc_hi, p.kc_lo, (float*)nullptr, 0);   \
+      hipLaunchKernelGGL((split_rows_kernel<HDV, float>), grid_rows((long long)p.B * p.nb, HDV),    \
+                         dim3(256), 0, s, p.kc, (long long)p.B * p.nb, 1, 1, p.kc_hi, p.kc_lo,      \
+                         (float*)nullptr, 0);                                                       \
     if (p.win > 0)                                                                                  \
-      hipLaunchKernelGGL((split_rows_kernel<HDV>), grid_rows((long long)BT), dim3(256), 0, s, p.kl,   \
-                         (long long)BT, 1, 1, p.kl_hi, p.kl_lo, (float*)nullptr, 0);                 \
+      hipLaunchKernelGGL((split_rows_kernel<HDV, float>), grid_rows((long long)BT, HDV), dim3(256), \
+                         0, s, p.kl, (long long)BT, 1, 1, p.kl_hi, p.kl_lo, (float*)nullptr, 0);    \
   } while (0)
 #define KCH_PASSES(HDV)                                                                            \
   do {                                                                                             \
@@ -618,6 +670,7 @@ hipError_t attn_bwd_mfma_dispatch(HcaBwdParams p, void* ws, hipStream_t s) {
     KCH_PASSES(128);
   }
 #undef KCH_SPLIT
+#undef KCH_SPLIT_Q
 #undef KCH_PASSES
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;

@@ -75,8 +75,8 @@ __global__ __launch_bounds__(256) void hca_bwd_query_kernel(HcaBwdParams p) {
   const int b = (int)(bt / p.T), t = (int)(bt % p.T);
   const size_t qoff = (bt * p.nh + hh) * HD + 8 * lc;
   float qn[8], dv[8];
-  load8(p.q + qoff, qn);
-  load8(p.dout + qoff, dv);
+  load8(static_cast<const float*>(p.q) + qoff, qn);
+  load8(static_cast<const float*>(p.dout) + qoff, dv);
   if (!act) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) qn[e] = dv[e] = 0.f;
@@ -208,7 +208,7 @@ __global__ __launch_bounds__(256) void hca_bwd_query_kernel(HcaBwdParams p) {
 #pragma unroll
     for (int e = 0; e < 8; ++e)
       o[e] = p.normalize ? (nrm > kEps ? dq[e] - qn[e] * yd : dq[e]) * rq : dq[e];
-    float* dst = p.dq + qoff;
+    float* dst = static_cast<float*>(p.dq) + qoff;
     *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
     *reinterpret_cast<float4*>(dst + 4) = make_float4(o[4], o[5], o[6], o[7]);
     if (lc == 0) {
@@ -267,8 +267,8 @@ __global__ __launch_bounds__(256) void hca_bwd_key_kernel(HcaBwdParams p, int mo
   };
   auto fetch = [&](int t, QRow& r) {
     const size_t i0 = ((size_t)b * p.T + t) * p.nh + hh;
-    load8(p.q + i0 * HD + 8 * lc, r.q);
-    load8(p.dout + i0 * HD + 8 * lc, r.d);
+    load8(static_cast<const float*>(p.q) + i0 * HD + 8 * lc, r.q);
+    load8(static_cast<const float*>(p.dout) + i0 * HD + 8 * lc, r.d);
     r.rq = p.rq[i0];
     r.lse = p.lse[i0];
     r.D = p.dval[i0];
@@ -717,6 +717,7 @@ size_t hca_bwd_ws_bytes(int B, int T, int nh, int c, int m2, int win, int topk) 
 
 hipError_t hca_bwd_dispatch(HcaBwdParams p, void* ws, hipStream_t stream) {
   if (attn_bwd_mfma_supported(p)) return attn_bwd_mfma_dispatch(p, ws, stream);
+  if (p.qdt != DT_F32) return hipErrorInvalidValue;  // the SIMT kernels read fp32 rows
   const Plan z = plan(p.B, p.T, p.nb, p.win, p.c);
   char* w = static_cast<char*>(ws);
   const size_t per = al256((size_t)p.B * p.T * p.nh * 4);

@@ -66,8 +66,8 @@ hipError_t kda_chunk_bwd_dispatch(KdaBwdParams p, int dtype, void* ws, hipStream
 // Gradients of the HCA attention (hca_backward.hip), fp32 tensors, c in
 // {64, 128}, nh <= 256 / (c / 8), T a multiple of m2.
 struct HcaBwdParams {
-  const float* q;       // [B,T,nh,c] queries as given (not normalised)
-  const float* dout;    // [B,T,nh,c]
+  const void* q;        // [B,T,nh,c] queries as given (not normalised), in qdt
+  const void* dout;     // [B,T,nh,c], in qdt
   const float* kc;      // [B,nb,c] L2-normalised compressed rows
   const float* raw;     // [B,nb,c] compressed rows
   const float* kl;      // [B,T,c] L2-normalised window rows (win > 0)
@@ -76,13 +76,14 @@ struct HcaBwdParams {
   const float* Z;
   const float* Bpos;    // [m2,c]
   const float* sink;    // [nh] or null
-  float* dq;            // [B,T,nh,c]
+  void* dq;             // [B,T,nh,c], in qdt
   float* dC;            // [B,T,c]
   float* dZ;            // [B,T,c]
   float* dBp;           // [B,nb,m2,c] per-block terms of dB_pos
   float* dlocal;        // [B,T,c] gradient of the window rows' source, or null: added to dC
   float* sink_part;     // [B,T,nh] p_sink * D per query and head, or null
   int normalize = 1;    // 0: queries and keys are used as given (no L2 norms)
+  int qdt = 0;          // storage of q, dout, dq: 0 fp32, 1 bf16, 2 fp16 (the SIMT path: fp32)
   // CSA: the selected blocks (idx [B,T,topk], -1 = unused) instead of every
   // causal block, its bitmap sel [B,T,ceil(nb/32)], the overlapped
   // compression's second branch, and the per-slot gradient of the selected

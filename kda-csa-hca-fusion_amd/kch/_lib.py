@@ -40,8 +40,8 @@ _SIGNATURES = {
     "kch_gen_l2norm": [_P, _P, _L, _I, _I, _I, _P],
     "kch_gen_indexer": [_P] * 4 + [_L, _L, _P, _P] + [_I] * 7 + [_D, _I, _I, _P],
     "kch_gen_attn": [_P] * 6 + [_I] * 8 + [_D, _I, _I, _I, _P, _SZ, _P],
-    "kch_hca_attn_bwd": [_P] * 16 + [_I] * 6 + [_F, _P, _SZ, _P],
-    "kch_csa_attn_bwd": [_P] * 24 + [_I] * 7 + [_F, _I, _P, _SZ, _P],
+    "kch_hca_attn_bwd": [_P] * 16 + [_I] * 6 + [_F, _I, _P, _SZ, _P],
+    "kch_csa_attn_bwd": [_P] * 24 + [_I] * 7 + [_F, _I, _I, _P, _SZ, _P],
     "kch_kda_gates_bwd": [_P, _L, _P, _L] + [_P] * 7 + [_I] * 6 + [_F, _I, _P],
     "kch_csa_ste_bwd": [_P] * 13 + [_I] * 5 + [_F, _I, _P, _SZ, _P],
     "kch_short_conv_bwd": [_P] * 8 + [_I] * 4 + [_P],

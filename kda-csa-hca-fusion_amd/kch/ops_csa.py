@@ -187,6 +187,15 @@ def _head_groups(nh):
     return [(h0, min(nh, h0 + _MAX_HEADS)) for h0 in range(0, nh, _MAX_HEADS)]
 
 
+def _attn_bwd_qdtype(q, d_out, normalize=True):
+    """Storage dtype of q, d_out and dq in the attention backward: theirs when
+    both are bf16 or both fp16 and the queries are normalised (the MFMA
+    kernels read and write them directly), else float32."""
+    if normalize and q.dtype == d_out.dtype and q.dtype in (torch.bfloat16, torch.float16):
+        return q.dtype
+    return torch.float32
+
+
 def _compress(fn, C, Z, B_pos, m, *, out_raw=True, key=None, normalize=False, local=None,
               key_split=0):
     """``key_split``: 0 keys as ``key``'s dtype (bf16 / fp32); 1 bf16 three-part
@@ -499,7 +508,7 @@ def csa_attn_grad(Ca, Cb, Za, Zb, q, Ba, Bb, idx, d_out, *, m, sliding_window=0,
                   sink_logits=None, normalize_qk=True, scale=None, want_gsum=False):
     """Gradients of the CSA attention (``ops_csa.py:869-1155``) with the selection
     ``idx`` ``[B,T,topk]`` (int32, -1 = unused) held fixed, on
-    ``kch_csa_attn_bwd`` (fp32). Returns a dict with ``Ca, Cb, Za, Zb, q, Ba,
+    ``kch_csa_attn_bwd`` (fp32 arithmetic). Returns a dict with ``Ca, Cb, Za, Zb, q, Ba,
     Bb`` (input dtypes), ``sink_logits`` where given, and ``slot`` ``[B,T,topk]``
     (fp32): each selected row's gradient dotted with the row; with
     ``want_gsum`` also ``gsum`` ``[B,T,c]`` (fp32): the sum of the selected
@@ -517,11 +526,14 @@ def csa_attn_grad(Ca, Cb, Za, Zb, q, Ba, Bb, idx, d_out, *, m, sliding_window=0,
     dev = Ca.device
     f32 = torch.float32
 
-    def prep(x):
-        x = x.to(device=dev, dtype=f32)
+    def prep(x, dt=f32):
+        x = x.to(device=dev, dtype=dt)
         return (_pad_last(x, cp) if cp != c else x).contiguous()
 
-    Caf, Cbf, Zaf, Zbf, qf, dof, Baf, Bbf = (prep(x) for x in (Ca, Cb, Za, Zb, q, d_out, Ba, Bb))
+    # q, d_out and dq move in their storage dtype where the MFMA kernels run
+    qdt = _attn_bwd_qdtype(q, d_out, normalize_qk)
+    Caf, Cbf, Zaf, Zbf, Baf, Bbf = (prep(x) for x in (Ca, Cb, Za, Zb, Ba, Bb))
+    qf, dof = _aligned(prep(q, qdt)), _aligned(prep(d_out, qdt))
     nb = T // m
     kc = torch.empty(B_, nb, cp, device=dev, dtype=f32)
     raw = _compress_overlapped(fn, Caf, Cbf, Zaf, Zbf, Baf, Bbf, m, out_raw=True, key=kc,
@@ -543,7 +555,9 @@ def csa_attn_grad(Ca, Cb, Za, Zb, q, Ba, Bb, idx, d_out, *, m, sliding_window=0,
     slot = torch.zeros(B_, T, topk, device=dev, dtype=f32)
     gsum = torch.zeros(B_, T, cp, device=dev, dtype=f32) if want_gsum else None
     dsink = None if sink is None else torch.zeros(nh, device=dev, dtype=f32)
-    hmax = 256 // (cp // 8)
+    # 16 heads a call on the MFMA kernels (normalised rows), else as many as
+    # one SIMT workgroup holds
+    hmax = _MAX_HEADS if normalize_qk else 256 // (cp // 8)
     for h0 in range(0, nh, hmax):
         h1 = min(nh, h0 + hmax)
         g = h1 - h0
@@ -565,7 +579,7 @@ def csa_attn_grad(Ca, Cb, Za, Zb, q, Ba, Bb, idx, d_out, *, m, sliding_window=0,
                   _lib.ptr(oa), _lib.ptr(ob), _lib.ptr(za), _lib.ptr(zb), _lib.ptr(bap),
                   _lib.ptr(bbp), _lib.ptr(sp), _lib.ptr(slot if topk else None), _lib.ptr(gs),
                   B_, T, g, cp, m, topk, win, float(scale), int(bool(normalize_qk)),
-                  _lib.ptr(ws), nbytes, _lib.stream_of(qg))
+                  _lib.dtype_code(fn, qdt), _lib.ptr(ws), nbytes, _lib.stream_of(qg))
         if dqg is not dq:
             dq[:, :, h0:h1] = dqg
         if gs is not None and gs is not gsum:

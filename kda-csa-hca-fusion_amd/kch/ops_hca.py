@@ -17,8 +17,9 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib, generic
-from .ops_csa import (_HEAD_DIMS, _aligned, _cat_cached, _check_gpu_dtype, _compress, _f32_cached,
-                      _head_groups, _kernel_size, _linear_up, _pad_last, l2_normalize_rows)
+from .ops_csa import (_HEAD_DIMS, _MAX_HEADS, _aligned, _attn_bwd_qdtype, _cat_cached,
+                      _check_gpu_dtype, _compress, _f32_cached, _head_groups, _kernel_size,
+                      _linear_up, _pad_last, l2_normalize_rows)
 
 
 def hca_core(C, Z, q, B_pos, *, m2, sliding_window=0, sink_logits=None, scale=1.0,
@@ -57,11 +58,14 @@ def hca_core_grad(C, Z, q, B_pos, d_out, *, m2, sliding_window=0, sink_logits=No
     dev = C.device
     f32 = torch.float32
 
-    def prep(x):
-        x = x.to(f32)
+    def prep(x, dt=f32):
+        x = x.to(dt)
         return (_pad_last(x, cp) if cp != c else x).contiguous()
 
-    Cf, Zf, qf, dof, Bp = (prep(x) for x in (C, Z, q, d_out, B_pos))
+    # q, d_out and dq move in their storage dtype (the MFMA kernels, 16 heads a call)
+    qdt = _attn_bwd_qdtype(q, d_out)
+    Cf, Zf, Bp = (prep(x) for x in (C, Z, B_pos))
+    qf, dof = _aligned(prep(q, qdt)), _aligned(prep(d_out, qdt))
     Clr = None if C_local_raw is None else prep(C_local_raw)
     nb = T // m2
     win = int(sliding_window)
@@ -78,7 +82,7 @@ def hca_core_grad(C, Z, q, B_pos, d_out, *, m2, sliding_window=0, sink_logits=No
     dB = torch.zeros(cp, device=dev, dtype=f32).new_zeros(m2, cp)
     dloc = None if Clr is None else torch.zeros_like(dC)
     dsink = None if sink is None else torch.zeros(nh, device=dev, dtype=f32)
-    hmax = 256 // (cp // 8)
+    hmax = _MAX_HEADS
     for h0 in range(0, nh, hmax):
         h1 = min(nh, h0 + hmax)
         g = h1 - h0
@@ -95,7 +99,8 @@ def hca_core_grad(C, Z, q, B_pos, d_out, *, m2, sliding_window=0, sink_logits=No
                   _lib.ptr(kl), _lib.ptr(lsrc), _lib.ptr(Cf), _lib.ptr(Zf), _lib.ptr(Bp),
                   _lib.ptr(None if sink is None else sink[h0:h1].contiguous()), _lib.ptr(dqg),
                   _lib.ptr(dCg), _lib.ptr(dZg), _lib.ptr(dBp), _lib.ptr(dlg), _lib.ptr(sp),
-                  B_, T, g, cp, m2, win, float(scale), _lib.ptr(ws), nbytes, _lib.stream_of(qg))
+                  B_, T, g, cp, m2, win, float(scale), _lib.dtype_code(fn, qdt), _lib.ptr(ws),
+                  nbytes, _lib.stream_of(qg))
         if dqg is not dq:
             dq[:, :, h0:h1] = dqg
         dC += dCg

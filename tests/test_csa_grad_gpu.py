@@ -94,6 +94,36 @@ def test_attn_grad_matches_oracle(dev, B, T, nh, c, m, topk, win, sink, norm):
         _check(name, g[name].cpu().numpy(), ref[name])
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("B,T,nh,c,m,topk,win,sink,norm", [CASES[0], CASES[2], CASES[3]])
+def test_attn_grad_half_storage_is_exact(dev, dtype, B, T, nh, c, m, topk, win, sink, norm):
+    """bf16 / fp16 q and d_out move in their own dtype where the queries are
+    normalised (read and written by the MFMA kernels; fp32 copies otherwise):
+    the same bits as the fp32-storage path on the same values, dq rounded to
+    nearest even."""
+    import kch
+    rng = np.random.default_rng(T + nh + c + topk + 7)
+    X = {k: rng.standard_normal((B, T, c)) for k in ("Ca", "Cb", "Za", "Zb")}
+    q = rng.standard_normal((B, T, nh, c))
+    Ba, Bb = rng.standard_normal((m, c)) * 0.3, rng.standard_normal((m, c)) * 0.3
+    sk = rng.standard_normal(nh) if sink else None
+    W = rng.standard_normal((B, T, nh, c))
+    idx = torch.tensor(_selection(rng, B, T, m, topk, hole=T // 2), device=dev)
+    t = lambda x: torch.tensor(x, dtype=torch.float32, device=dev)  # noqa: E731
+    qh, Wh = t(q).to(dtype), t(W).to(dtype)
+    args = [t(X[k]) for k in ("Ca", "Cb", "Za", "Zb")]
+    kw = dict(m=m, sliding_window=win, sink_logits=None if sk is None else t(sk),
+              normalize_qk=norm, want_gsum=True)
+    got = kch.ops_csa.csa_attn_grad(*args, qh, t(Ba), t(Bb), idx, Wh, **kw)
+    ref = kch.ops_csa.csa_attn_grad(*args, qh.float(), t(Ba), t(Bb), idx, Wh.float(), **kw)
+    torch.cuda.synchronize()
+    assert got["q"].dtype == dtype
+    assert torch.equal(got["q"], ref["q"].to(dtype)), "dq"
+    for name in ref:
+        if name != "q":
+            assert torch.equal(got[name], ref[name]), name
+
+
 def _torch_reference(X, idx, *, m, topk, win, sink, norm):
     """The reference's CSA forward (compression ``ops_csa.py:237-305``,
     indexer ``:330-573``, the STE gather ``:1033-1099``, attention with window

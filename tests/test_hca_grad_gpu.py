@@ -74,6 +74,28 @@ def test_core_grad_matches_oracle(dev, B, T, nh, c, m2, win, sink, local):
         _check(name, x.grad.cpu().numpy(), ref[name], 1e-4)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("B,T,nh,c,m2,win,sink,local", [CASES[0], CASES[2], CASES[3]])
+def test_core_grad_half_storage_is_exact(dev, dtype, B, T, nh, c, m2, win, sink, local):
+    """bf16 / fp16 q and d_out are read, and dq written, by the kernels in
+    their own dtype: the same bits as the fp32-storage path (checked against
+    the oracle above) run on the same values, dq rounded to nearest even."""
+    from kch.ops_hca import hca_core_grad
+    C, Z, q, Bp, sk, Cl, W = _make(T + nh + c + 7, B, T, nh, c, m2)
+    t = lambda x: torch.tensor(x, dtype=torch.float32, device=dev)  # noqa: E731
+    qh, Wh = t(q).to(dtype), t(W).to(dtype)
+    kw = dict(m2=m2, sliding_window=win, scale=0.9, sink_logits=t(sk) if sink else None,
+              C_local_raw=t(Cl) if local else None)
+    got = hca_core_grad(t(C), t(Z), qh, t(Bp), Wh, **kw)
+    ref = hca_core_grad(t(C), t(Z), qh.float(), t(Bp), Wh.float(), **kw)
+    torch.cuda.synchronize()
+    assert got["q"].dtype == dtype
+    assert torch.equal(got["q"], ref["q"].to(dtype)), "dq"
+    for name in ref:
+        if name != "q":
+            assert torch.equal(got[name], ref[name]), name
+
+
 def test_naive_hca_grad_fp32(dev):
     """Whole operator: projections through autograd, the core through its HIP
     backward; the oracle chain rule through the four linear maps."""
