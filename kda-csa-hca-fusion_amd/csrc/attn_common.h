@@ -406,6 +406,44 @@ struct MqaWave {
     accumulate32(sc, stage, to);
   }
 
+  // Score-layout gathers of 32 key rows. Lane group q = lane / 16 loads the
+  // rows whose scores it holds after the S^T MFMAs: slot k (0..7) is row
+  // row_sl(k, q) = 4q + k (k < 4) or 16 + 4q + k - 4, the key of sc[k]. So
+  // each lane knows the validity of its own scores from the row indices it
+  // loaded (no ballots, no mask bits to assemble). A load instruction still
+  // covers whole rows: with TPR = 16 (HD 128) load i is slot i of every lane
+  // (rows i, 4 + i, 8 + i, 12 + i for i < 4); with TPR = 8 (HD 64) the two
+  // 8-lane halves of a group take slots i and 4 + i.
+  __device__ __forceinline__ static int row_sl(int k, int q) { return 4 * q + k + (k >= 4 ? 12 : 0); }
+  __device__ __forceinline__ static int slot_sl(int i) {
+    return TPR == 16 ? i : i + 4 * ((lane_id() >> 3) & 1);
+  }
+  __device__ __forceinline__ void chunk_sl(const Rows& rr, const bool (&ok)[8], bf16_t* stage,
+                                           const TileOffsets<HD>& to) {
+    const int l = lane_id(), q = l >> 4, c = l % TPR;
+    wave_lds_sync();  // the previous step's reads of the stage are done before the overwrite
+#pragma unroll
+    for (int i = 0; i < NLI; ++i) {
+      const int r = row_sl(slot_sl(i), q);
+      *reinterpret_cast<u32x4*>(stage + r * HD + 8 * (c ^ tile_swz<HD>(r & 15))) = rr.v[i];
+    }
+    wave_lds_sync();  // staged rows visible to the whole wave
+    f32x4 sa, sb;
+    {
+      bf16x8 kf[NS];
+#pragma unroll
+      for (int s = 0; s < NS; ++s) kf[s] = *reinterpret_cast<const bf16x8*>(stage + to.key(s));
+      sa = scores(kf);
+#pragma unroll
+      for (int s = 0; s < NS; ++s) kf[s] = *reinterpret_cast<const bf16x8*>(stage + 16 * HD + to.key(s));
+      sb = scores(kf);
+    }
+    float sc[8] = {sa[0], sa[1], sa[2], sa[3], sb[0], sb[1], sb[2], sb[3]};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) sc[k] = ok[k] ? sc[k] : -INFINITY;
+    accumulate32(sc, stage, to);
+  }
+
   // Totals L over the 4 lanes of each head; call once, after the last step.
   __device__ __forceinline__ void finalize() { L = colq_sum(L); }
 

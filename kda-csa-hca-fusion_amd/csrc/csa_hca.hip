@@ -368,62 +368,103 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(AttnParams p) {
     const __amdgpu_buffer_rsrc_t rs_loc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<bf16_t*>(loc ? loc : kv), 0, nloc * ROWB, 0x00020000);
     const int lane_off = 16 * (lane % W::TPR);
-    // Selected block indices come 64 at a time, one per lane, from a load issued
-    // a group ahead of its use (so that waiting for it never waits for the row
-    // loads issued after it); loads are clamped, read entries are only those of
-    // rows below n_main.
+    const int q4 = lane >> 4;
+    const bool hi_half = W::TPR == 8 && ((lane >> 3) & 1);
+    // Rows are taken in the score layout (MqaWave::chunk_sl): this lane's slot
+    // k of a 32-row step is row row_sl(k, q4), whose score it holds. The row
+    // indices of a step (selected block, causal block or window position) are
+    // fetched two steps ahead of the row loads that use them: the selected
+    // ones through a buffer resource over this query's topk entries (16-byte
+    // loads when nm is a multiple of 4, so that no load straddles its end;
+    // reads past it give 0, and such rows are masked by j < nm).
     const bool has_idx = SPARSE && nm > 0;
-    const int* ip = has_idx ? p.idx + (size_t)qi * p.topk : nullptr;
-    const int ilim = has_idx ? nm : 1;
-    auto idx_group = [&](int g) { return has_idx ? ip[min(64 * g + lane, ilim - 1)] : 0; };
-    // 32-row step st (of the 64-row index group ig), gathered row-major;
-    // returns the step's validity bits (bit r: row 32 st + r)
-    auto load_step = [&](int st, int ig, unsigned& valid) {
-      typename W::Rows rr;
-      valid = 0u;
-      const int j0 = 32 * st;
-      const bool main_step = j0 < nm_pad;  // uniform
-#pragma unroll
-      for (int i = 0; i < W::NLI; ++i) {
-        const int j = j0 + i * W::RPI + lane / W::TPR;
-        bool ok;
-        unsigned off;
-        if (main_step) {
-          const int sel = SPARSE ? __shfl(ig, j & 63) : j;
-          ok = j < nm && sel >= 0 && sel < p.nb;
-          off = ok ? (unsigned)(sel * ROWB + lane_off) : 0xffffffffu;
-        } else {
-          const int jw = j - nm_pad;
-          ok = jw < n_win;
-          off = ok ? (unsigned)((wbase + jw) * ROWB + lane_off) : 0xffffffffu;
-        }
-        rr.v[i] = __builtin_amdgcn_raw_buffer_load_b128(main_step ? rs_kv : rs_loc, (int)off, 0, 0);
-        const unsigned long long m = __ballot(ok);
-#pragma unroll
-        for (int k = 0; k < W::RPI; ++k)
-          valid |= (unsigned)((m >> (W::TPR * k)) & 1ull) << (i * W::RPI + k);
-      }
-      return rr;
+    const __amdgpu_buffer_rsrc_t rs_idx = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int*>(has_idx ? p.idx + (size_t)qi * p.topk : nullptr), 0, has_idx ? nm * 4 : 0,
+        0x00020000);
+    const bool idx16 = (nm & 3) == 0;
+    struct Sel {
+      int v[8];
     };
-    // groups of two 32-row steps, two steps in flight (named registers: an
-    // indexed array of them ends up in scratch memory); refills are
-    // unconditional (past the end they read the default row, masked off) so
-    // that no loaded register is copied
+    auto load_sel = [&](int st, Sel& sl) {
+      const int j0 = 32 * st;
+      if (__builtin_amdgcn_readfirstlane(j0 < nm_pad ? 1 : 0)) {
+        if (SPARSE) {
+          if (idx16) {
+            typedef int i32x4 __attribute__((ext_vector_type(4)));
+            const i32x4 a = __builtin_bit_cast(
+                i32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_idx, (j0 + 4 * q4) * 4, 0, 0));
+            const i32x4 c = __builtin_bit_cast(
+                i32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_idx, (j0 + 16 + 4 * q4) * 4, 0, 0));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              sl.v[e] = a[e];
+              sl.v[4 + e] = c[e];
+            }
+          } else {
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+              sl.v[k] = (int)__builtin_amdgcn_raw_buffer_load_b32(rs_idx, (j0 + W::row_sl(k, q4)) * 4, 0, 0);
+          }
+        } else {
+#pragma unroll
+          for (int k = 0; k < 8; ++k) sl.v[k] = j0 + W::row_sl(k, q4);
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) sl.v[k] = wbase + (j0 - nm_pad) + W::row_sl(k, q4);
+      }
+    };
+    // the row loads of step st from its indices; ok[k]: slot k is a row of
+    // this query. Returns whether any row of the step is (uniform).
+    auto load_rows = [&](int st, const Sel& sl, typename W::Rows& rr, bool (&ok)[8]) {
+      const int j0 = 32 * st;
+      bool any = false;
+      auto issue = [&](const __amdgpu_buffer_rsrc_t rs) {
+#pragma unroll
+        for (int i = 0; i < W::NLI; ++i) {
+          const int v = hi_half ? sl.v[(i + 4) & 7] : sl.v[i];
+          rr.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)((unsigned)v * ROWB + lane_off), 0, 0);
+        }
+      };
+      if (__builtin_amdgcn_readfirstlane(j0 < nm_pad ? 1 : 0)) {
+        issue(rs_kv);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const int j = j0 + W::row_sl(k, q4);
+          ok[k] = (j < nm) & ((unsigned)sl.v[k] < (unsigned)p.nb);
+          any |= ok[k];
+        }
+      } else {
+        issue(rs_loc);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          ok[k] = j0 - nm_pad + W::row_sl(k, q4) < n_win;
+          any |= ok[k];
+        }
+      }
+      return __ballot(any) != 0ull;
+    };
+    // two steps of rows in flight and the indices of the two after them
+    // (named registers: an indexed array of them ends up in scratch memory)
     const TileOffsets<HD> to;
     const int nst = (n_tot + 31) / 32;
     const int ng = (nst + 1) / 2;
-    const int ig0 = idx_group(0);
-    int ig1 = idx_group(1);
-    unsigned vm0, vm1;
-    typename W::Rows fr0 = load_step(0, ig0, vm0);
-    typename W::Rows fr1 = load_step(1, ig0, vm1);
+    Sel s0, s1;
+    typename W::Rows fr0, fr1;
+    bool ok0[8], ok1[8];
+    load_sel(0, s0);
+    load_sel(1, s1);
+    bool any0 = load_rows(0, s0, fr0, ok0);
+    bool any1 = load_rows(1, s1, fr1, ok1);
+    load_sel(2, s0);
+    load_sel(3, s1);
     for (int g = 0; g < ng; ++g) {
-      const int ig2 = idx_group(g + 2);
-      if (vm0) w.chunk_rows(fr0, vm0, stage, to);
-      fr0 = load_step(2 * (g + 1), ig1, vm0);
-      if (vm1) w.chunk_rows(fr1, vm1, stage, to);
-      fr1 = load_step(2 * (g + 1) + 1, ig1, vm1);
-      ig1 = ig2;
+      if (any0) w.chunk_sl(fr0, ok0, stage, to);
+      any0 = load_rows(2 * g + 2, s0, fr0, ok0);
+      load_sel(2 * g + 4, s0);
+      if (any1) w.chunk_sl(fr1, ok1, stage, to);
+      any1 = load_rows(2 * g + 3, s1, fr1, ok1);
+      load_sel(2 * g + 5, s1);
     }
   }
   w.finalize();
