@@ -419,6 +419,8 @@ int kch_hca_attn_bwd(const void* q, const void* d_out, const float* kc, const fl
                 m2, win);
   if (T % m2) return fail(KCH_ERR_INVALID, "%s: T=%d must be a multiple of m2=%d", fn, T, m2);
   if (c != 64 && c != 128) return fail(KCH_ERR_UNSUPPORTED, "%s: c=%d not supported (64 or 128)", fn, c);
+  if ((long long)T * c * 4 >= (1LL << 31))
+    return fail(KCH_ERR_UNSUPPORTED, "%s: T=%d rows of a batch row exceed 2 GiB (32-bit row offsets)", fn, T);
   if (nh * (c / 8) > 256)
     return fail(KCH_ERR_UNSUPPORTED, "%s: nh=%d heads of %d exceed one workgroup", fn, nh, c);
   if (std::isnan(scale)) return fail(KCH_ERR_INVALID, "%s: scale is NaN", fn);
@@ -471,6 +473,8 @@ int kch_csa_attn_bwd(const void* q, const void* d_out, const float* kc, const fl
                 T, nh, m, win, topk);
   if (T % m) return fail(KCH_ERR_INVALID, "%s: T=%d must be a multiple of m=%d", fn, T, m);
   if (c != 64 && c != 128) return fail(KCH_ERR_UNSUPPORTED, "%s: c=%d not supported (64 or 128)", fn, c);
+  if ((long long)T * c * 4 >= (1LL << 31))
+    return fail(KCH_ERR_UNSUPPORTED, "%s: T=%d rows of a batch row exceed 2 GiB (32-bit row offsets)", fn, T);
   if (nh * (c / 8) > 256)
     return fail(KCH_ERR_UNSUPPORTED, "%s: nh=%d heads of %d exceed one workgroup", fn, nh, c);
   if (std::isnan(scale)) return fail(KCH_ERR_INVALID, "%s: scale is NaN", fn);
@@ -681,6 +685,8 @@ static int check_attn(const char* fn, int B, int T, int nb, int nh, int hd, int 
   if (hd != 64 && hd != 128) return fail(KCH_ERR_UNSUPPORTED, "%s: head dim %d not in {64,128}", fn, hd);
   if (odtype != KCH_DT_F32 && odtype != qdtype)
     return fail(KCH_ERR_UNSUPPORTED, "%s: output dtype must be fp32 or the query dtype", fn);
+  if ((long long)(T > nb ? T : nb) * hd * 2 >= (1LL << 31))
+    return fail(KCH_ERR_UNSUPPORTED, "%s: a batch row's key rows exceed 2 GiB (32-bit row offsets)", fn);
   return KCH_OK;
 }
 

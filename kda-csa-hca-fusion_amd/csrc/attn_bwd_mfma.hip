@@ -174,56 +174,96 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_q_kernel(HcaBwdParams p) {
       dl[s] = *reinterpret_cast<const bf16x8*>(p.ds_lo + ro + 32 * s);
     }
   }
-  const int* sel_row = SPARSE ? p.idx + bt * p.topk : nullptr;
   const int nsel = SPARSE ? p.topk : min((t + 1) / p.m2, p.nb);
   const int i0 = p.win > 0 ? max(0, p.win - 1 - t) : 0;
   const int nwin = p.win > 0 ? p.win - i0 : 0;
-  const int nk = nsel + nwin;
   const int wpos0 = t - p.win + 1 + i0;
-  const bf16_t* kch_ = p.kc_hi + (size_t)b * p.nb * HD;
-  const bf16_t* kcl_ = p.kc_lo + (size_t)b * p.nb * HD;
-  const bf16_t* klh_ = p.kl_hi ? p.kl_hi + (size_t)b * p.T * HD : kch_;
-  const bf16_t* kll_ = p.kl_lo ? p.kl_lo + (size_t)b * p.T * HD : kcl_;
-  // a readable row for masked slots: block 0 or the query's own window row
-  const bf16_t* dfh = p.nb > 0 ? kch_ : klh_ + (size_t)t * HD;
-  const bf16_t* dfl = p.nb > 0 ? kcl_ : kll_ + (size_t)t * HD;
-  const int nsteps = (nk + 31) / 32;
+  // The compressed rows are padded to whole 32-row steps (masked), so that a
+  // step reads only compressed or only window rows, each through a buffer
+  // resource over this batch row's rows (hi and lo planes): an offset past its
+  // end reads zeros, so a row address is one multiply-add and masked slots
+  // need no readable default. Rows are taken in the score layout of
+  // MqaWave::chunk_sl: slot k of lane group q is row row_sl(k, q) of the
+  // step, whose scores the lane holds, so each lane masks its own scores
+  // from the indices it loaded.
+  using MW = MqaWave<HD>;
+  constexpr int ROWB = HD * 2;
+  const int nsel_pad = p.nb > 0 ? (nsel + 31) & ~31 : 0;
+  const int nsteps = (nsel_pad + nwin + 31) / 32;
+  const int lane_off = 16 * (lane % TPR);
+  const int hmask = (TPR == 8 && ((lane >> 3) & 1)) ? -1 : 0;  // HD 64: slot i + 4
+  auto rsrc = [](const bf16_t* base, long long bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(base), 0, (int)bytes, 0x00020000);
+  };
+  const long long cbytes = (long long)p.nb * ROWB, wbytes = nwin > 0 ? (long long)p.T * ROWB : 0;
+  const __amdgpu_buffer_rsrc_t rs_ch = rsrc(p.kc_hi + (size_t)b * p.nb * HD, cbytes);
+  const __amdgpu_buffer_rsrc_t rs_cl = rsrc(p.kc_lo + (size_t)b * p.nb * HD, cbytes);
+  const __amdgpu_buffer_rsrc_t rs_wh = rsrc(nwin > 0 ? p.kl_hi + (size_t)b * p.T * HD : p.kc_hi, wbytes);
+  const __amdgpu_buffer_rsrc_t rs_wl = rsrc(nwin > 0 ? p.kl_lo + (size_t)b * p.T * HD : p.kc_lo, wbytes);
+  const bool has_idx = SPARSE && nsel > 0;
+  const __amdgpu_buffer_rsrc_t rs_idx = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int*>(has_idx ? p.idx + bt * p.topk : nullptr), 0, has_idx ? nsel * 4 : 0, 0x00020000);
+  const bool idx16 = (nsel & 3) == 0;  // 16-byte index loads never straddle the end
   const float sc = p.scale * kLog2eF;  // raw score -> log2 units
 
-  // gather 32 rows of step m (row r = key 32 m + r) row-major, hi and lo
-  auto gather = [&](int m, typename W::Rows& rr, unsigned& valid) {
-    valid = 0u;
+  // the row indices of step m: selected or causal block, or window position
+  struct Sel {
+    int v[8];
+  };
+  auto load_sel = [&](int m, Sel& sl) {
+    const int j0 = 32 * m;
+    if (__builtin_amdgcn_readfirstlane(j0 < nsel_pad ? 1 : 0)) {
+      if (SPARSE) {
+        if (idx16) {
+          typedef int i32x4 __attribute__((ext_vector_type(4)));
+          const i32x4 x = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_idx, (j0 + 4 * q) * 4, 0, 0));
+          const i32x4 y = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_idx, (j0 + 16 + 4 * q) * 4, 0, 0));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            sl.v[e] = x[e];
+            sl.v[4 + e] = y[e];
+          }
+        } else {
+#pragma unroll
+          for (int k = 0; k < 8; ++k)
+            sl.v[k] = (int)__builtin_amdgcn_raw_buffer_load_b32(rs_idx, (j0 + MW::row_sl(k, q)) * 4, 0, 0);
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) sl.v[k] = j0 + MW::row_sl(k, q);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) sl.v[k] = wpos0 + (j0 - nsel_pad) + MW::row_sl(k, q);
+    }
+  };
+  // gather the 32 rows of step m (hi and lo planes); ok[k]: slot k is a key
+  auto gather = [&](int m, const Sel& sl, typename W::Rows& rr, bool (&ok)[8]) {
+    const int j0 = 32 * m;
+    const int ms = __builtin_amdgcn_readfirstlane(j0 < nsel_pad ? 1 : 0);
+    const __amdgpu_buffer_rsrc_t rh = ms ? rs_ch : rs_wh;
+    const __amdgpu_buffer_rsrc_t rl = ms ? rs_cl : rs_wl;
 #pragma unroll
     for (int i = 0; i < NLI; ++i) {
-      const int r = i * RPI + lane / TPR, c = lane % TPR;
-      const int j = 32 * m + r;
-      const bf16_t* ph = dfh;
-      const bf16_t* pl = dfl;
-      bool ok = false;
-      if (j < nsel) {
-        const int blk = SPARSE ? sel_row[j] : j;
-        ok = blk >= 0 && blk < p.nb;
-        if (ok) {
-          ph = kch_ + (size_t)blk * HD;
-          pl = kcl_ + (size_t)blk * HD;
-        }
-      } else if (j < nk) {
-        ok = true;
-        ph = klh_ + (size_t)(wpos0 + (j - nsel)) * HD;
-        pl = kll_ + (size_t)(wpos0 + (j - nsel)) * HD;
-      }
-      rr.h[i] = *reinterpret_cast<const typename W::u32x4*>(ph + 8 * c);
-      rr.l[i] = *reinterpret_cast<const typename W::u32x4*>(pl + 8 * c);
-      const unsigned long long mb = __ballot(ok);
+      // (a select of values, not an indexed read: that would put sl in scratch memory)
+      const int v = TPR == 8 ? sl.v[i] ^ ((sl.v[i] ^ sl.v[(i + 4) & 7]) & hmask) : sl.v[i];
+      const int off = (int)((unsigned)v * ROWB + lane_off);
+      rr.h[i] = __builtin_amdgcn_raw_buffer_load_b128(rh, off, 0, 0);
+      rr.l[i] = __builtin_amdgcn_raw_buffer_load_b128(rl, off, 0, 0);
+    }
 #pragma unroll
-      for (int k = 0; k < RPI; ++k) valid |= (unsigned)((mb >> (TPR * k)) & 1ull) << (i * RPI + k);
+    for (int k = 0; k < 8; ++k) {
+      const int j = j0 + MW::row_sl(k, q);
+      const bool okc = (j < nsel) & ((unsigned)sl.v[k] < (unsigned)p.nb);
+      const bool okw = j - nsel_pad < nwin;
+      ok[k] = ms ? okc : okw;
     }
   };
   auto stage = [&](const typename W::Rows& rr) {
     wave_lds_sync();  // the previous step's reads are done
 #pragma unroll
     for (int i = 0; i < NLI; ++i) {
-      const int r = i * RPI + lane / TPR, c = lane % TPR;
+      const int r = MW::row_sl(MW::slot_sl(i), q), c = lane % TPR;
       const int off = r * HD + 8 * (c ^ tile_swz<HD>(r & 15));
       *reinterpret_cast<typename W::u32x4*>(sth + off) = rr.h[i];
       *reinterpret_cast<typename W::u32x4*>(stl + off) = rr.l[i];
@@ -231,7 +271,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_q_kernel(HcaBwdParams p) {
     wave_lds_sync();
   };
   // S^T (log2 units) and dP^T of the staged 32 rows: sc8 / dp8 for keys 4q+e, 16+4q+e of head n
-  auto scores = [&](unsigned valid, float (&s8)[8], float (&d8)[8]) {
+  auto scores = [&](const bool (&ok)[8], float (&s8)[8], float (&d8)[8]) {
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
       f32x4 sa = {0.f, 0.f, 0.f, 0.f}, da = {0.f, 0.f, 0.f, 0.f};
@@ -244,8 +284,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_q_kernel(HcaBwdParams p) {
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const bool ok = (valid >> (16 * half + 4 * q + e)) & 1u;
-        s8[4 * half + e] = ok ? sa[e] * sc : -INFINITY;
+        s8[4 * half + e] = ok[4 * half + e] ? sa[e] * sc : -INFINITY;
         d8[4 * half + e] = da[e];
       }
     }
@@ -255,14 +294,24 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_q_kernel(HcaBwdParams p) {
   float m = -INFINITY, l = 0.f, ad = 0.f;
   {
     typename W::Rows rr;
-    unsigned vm = 0u;
-    if (nsteps > 0) gather(0, rr, vm);
+    Sel sl;
+    bool okn[8];
+    if (nsteps > 0) {
+      load_sel(0, sl);
+      gather(0, sl, rr, okn);
+      load_sel(1, sl);
+    }
     for (int st = 0; st < nsteps; ++st) {
       stage(rr);
-      const unsigned v = vm;
-      if (st + 1 < nsteps) gather(st + 1, rr, vm);
+      bool ok[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) ok[k] = okn[k];
+      if (st + 1 < nsteps) {
+        gather(st + 1, sl, rr, okn);
+        load_sel(st + 2, sl);
+      }
       float s8[8], d8[8];
-      scores(v, s8, d8);
+      scores(ok, s8, d8);
       float mx = s8[0];
 #pragma unroll
       for (int e = 1; e < 8; ++e) mx = fmaxf(mx, s8[e]);
@@ -305,14 +354,24 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_q_kernel(HcaBwdParams p) {
   float psel = 0.f, dssel = 0.f;  // sums over the selected slots (gsum)
   {
     typename W::Rows rr;
-    unsigned vm = 0u;
-    if (nsteps > 0) gather(0, rr, vm);
+    Sel sl;
+    bool okn[8];
+    if (nsteps > 0) {
+      load_sel(0, sl);
+      gather(0, sl, rr, okn);
+      load_sel(1, sl);
+    }
     for (int st = 0; st < nsteps; ++st) {
       stage(rr);
-      const unsigned v = vm;
-      if (st + 1 < nsteps) gather(st + 1, rr, vm);
+      bool ok[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) ok[k] = okn[k];
+      if (st + 1 < nsteps) {
+        gather(st + 1, sl, rr, okn);
+        load_sel(st + 2, sl);
+      }
       float s8[8], d8[8];
-      scores(v, s8, d8);
+      scores(ok, s8, d8);
       float pe[8], dse[8];
       bf16x8 bh, bl;
 #pragma unroll

@@ -369,7 +369,7 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(AttnParams p) {
         const_cast<bf16_t*>(loc ? loc : kv), 0, nloc * ROWB, 0x00020000);
     const int lane_off = 16 * (lane % W::TPR);
     const int q4 = lane >> 4;
-    const bool hi_half = W::TPR == 8 && ((lane >> 3) & 1);
+    const int hmask = (W::TPR == 8 && ((lane >> 3) & 1)) ? -1 : 0;
     // Rows are taken in the score layout (MqaWave::chunk_sl): this lane's slot
     // k of a 32-row step is row row_sl(k, q4), whose score it holds. The row
     // indices of a step (selected block, causal block or window position) are
@@ -418,29 +418,23 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(AttnParams p) {
     // this query. Returns whether any row of the step is (uniform).
     auto load_rows = [&](int st, const Sel& sl, typename W::Rows& rr, bool (&ok)[8]) {
       const int j0 = 32 * st;
+      const int ms = __builtin_amdgcn_readfirstlane(j0 < nm_pad ? 1 : 0);
+      const __amdgpu_buffer_rsrc_t rs = ms ? rs_kv : rs_loc;
+#pragma unroll
+      for (int i = 0; i < W::NLI; ++i) {
+        // HD 64: the upper 8 lanes of a group take slot i + 4 (a select of
+        // values, not an indexed read: that would put sl in scratch memory)
+        const int v = W::TPR == 8 ? sl.v[i] ^ ((sl.v[i] ^ sl.v[(i + 4) & 7]) & hmask) : sl.v[i];
+        rr.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)((unsigned)v * ROWB + lane_off), 0, 0);
+      }
       bool any = false;
-      auto issue = [&](const __amdgpu_buffer_rsrc_t rs) {
 #pragma unroll
-        for (int i = 0; i < W::NLI; ++i) {
-          const int v = hi_half ? sl.v[(i + 4) & 7] : sl.v[i];
-          rr.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)((unsigned)v * ROWB + lane_off), 0, 0);
-        }
-      };
-      if (__builtin_amdgcn_readfirstlane(j0 < nm_pad ? 1 : 0)) {
-        issue(rs_kv);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const int j = j0 + W::row_sl(k, q4);
-          ok[k] = (j < nm) & ((unsigned)sl.v[k] < (unsigned)p.nb);
-          any |= ok[k];
-        }
-      } else {
-        issue(rs_loc);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          ok[k] = j0 - nm_pad + W::row_sl(k, q4) < n_win;
-          any |= ok[k];
-        }
+      for (int k = 0; k < 8; ++k) {
+        const int j = j0 + W::row_sl(k, q4);
+        const bool okm = (j < nm) & ((unsigned)sl.v[k] < (unsigned)p.nb);
+        const bool okw = j - nm_pad < n_win;
+        ok[k] = ms ? okm : okw;
+        any |= ok[k];
       }
       return __ballot(any) != 0ull;
     };
