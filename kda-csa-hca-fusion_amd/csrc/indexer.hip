@@ -101,11 +101,13 @@ __host__ __device__ inline bool indexer_lean(const IndexerParams& p) {
   return !p.sorted && p.nb <= 256 * RG;
 }
 
-__host__ __device__ inline size_t indexer_lds(int nb, int nIh, int topk, bool lean) {
+// LDS of a launch with CT column tiles (CT * 16 / nIh queries, 4 * CT waves)
+__host__ __device__ inline size_t indexer_lds(int nb, int nIh, int topk, bool lean, int ct = 1) {
   int ptop = 1;
   while (ptop < topk) ptop <<= 1;
-  const size_t base = (size_t)(16 / nIh) * ((nb + 3) & ~3) * 4 + 4 * 64 * 4;
-  return lean ? base : base + 4 * 256 * 4 + 4 * (size_t)ptop * 8;
+  const int nwv = 4 * ct;
+  const size_t base = (size_t)(ct * 16 / nIh) * ((nb + 3) & ~3) * 4 + (size_t)nwv * 64 * 4;
+  return lean ? base : base + (size_t)nwv * 256 * 4 + (size_t)nwv * ptop * 8;
 }
 
 // Top-k of one query's logits row lg[0 .. nv) (LDS, 16-byte aligned) by one
@@ -209,12 +211,14 @@ __device__ __forceinline__ void select_in_registers(const float* lg, int nv, int
 
 }  // namespace
 
-template <typename QT, int CI, int NIH, int KM>
-__global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
+template <typename QT, int CI, int NIH, int KM, int CT>
+__global__ __launch_bounds__(256 * CT, CT == 2 ? 4 : 1) void indexer_kernel(IndexerParams p) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   constexpr int NS = CI / 32;
   constexpr int nIh = NIH;
-  constexpr int QPW = 16 / NIH;  // queries per workgroup
+  constexpr int NWV = 4 * CT;         // waves per workgroup
+  constexpr int QPT = 16 / NIH;       // queries per column tile
+  constexpr int QPW = CT * QPT;       // queries per workgroup
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int q4 = lane >> 4, n = lane & 15;
@@ -228,14 +232,14 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
   const size_t lg_bytes = (size_t)QPW * ldl * 4;
   int ptop = 1;
   while (ptop < topk) ptop <<= 1;
-  // LDS: logits [QPW][ldl] | sink words [4][64] | (unless lean) histograms
-  // [4][256] and selections [4][ptop]. Lean: unsorted output of rows that the
-  // register selection handles, whose indices go straight to global memory.
+  // LDS: logits [QPW][ldl] | sink words [NWV][64] | (unless lean) histograms
+  // [NWV][256] and selections [NWV][ptop]. Lean: unsorted output of rows that
+  // the register selection handles, whose indices go straight to global memory.
   const bool lean = indexer_lean(p);
   float* logits = reinterpret_cast<float*>(smem);
   float* sink = reinterpret_cast<float*>(smem + lg_bytes) + 64 * wave;
-  uint32_t* hist = reinterpret_cast<uint32_t*>(smem + lg_bytes + 4 * 64 * 4) + 256 * wave;
-  u64* sel = reinterpret_cast<u64*>(smem + lg_bytes + 4 * 64 * 4 + 4 * 256 * 4) +
+  uint32_t* hist = reinterpret_cast<uint32_t*>(smem + lg_bytes + NWV * 64 * 4) + 256 * wave;
+  u64* sel = reinterpret_cast<u64*>(smem + lg_bytes + NWV * 64 * 4 + NWV * 256 * 4) +
              (size_t)ptop * wave;
 
   auto nvis_of = [&](int t) {
@@ -244,19 +248,26 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
     return v < nb ? v : nb;
   };
 
-  // ---- this lane's query column: query tq = t0 + n / nIh, head h = n % nIh ----
-  const int jq = n / nIh, hh = n - jq * nIh;
-  const int tq = t0 + jq;
-  const bool qok = tq < p.T;
+  // ---- this lane's query columns: tile ct, query jq = ct QPT + n / nIh, head n % nIh ----
+  const int hh = n % nIh;
+  int jq[CT], tq[CT];
+  bool qok[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) {
+    jq[ct] = ct * QPT + n / nIh;
+    tq[ct] = t0 + jq[ct];
+    qok[ct] = tq[ct] < p.T;
+  }
   // q parts: bf16 hi / mid / lo (KM 0, 1) or fp16 hi / lo of 256 q (KM 2)
-  bf16x8 qhi[NS], qmid[NS], qlo[NS];
-  f16x8 qh16[NS], ql16[NS];
-  float wq = 0.f;
-  {
+  bf16x8 qhi[CT][NS], qmid[CT][NS], qlo[CT][NS];
+  f16x8 qh16[CT][NS], ql16[CT][NS];
+  float wq[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) {
     float f[NS][8];
     float ss = 0.f;
     const QT* qrow = static_cast<const QT*>(p.q_idx) +
-                     (((size_t)b * p.T + (qok ? tq : 0)) * nIh + hh) * CI;
+                     (((size_t)b * p.T + (qok[ct] ? tq[ct] : 0)) * nIh + hh) * CI;
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       Load8<QT>::run(qrow + 32 * s + 8 * q4, f[s]);
@@ -267,13 +278,14 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) f[s][i] = qok ? f[s][i] * inv : 0.f;
-      if constexpr (KM == 2) split2_f16(f[s], qh16[s], ql16[s]);
-      else split3_bf16(f[s], qhi[s], qmid[s], qlo[s]);
+      for (int i = 0; i < 8; ++i) f[s][i] = qok[ct] ? f[s][i] * inv : 0.f;
+      if constexpr (KM == 2) split2_f16(f[s], qh16[ct][s], ql16[ct][s]);
+      else split3_bf16(f[s], qhi[ct][s], qmid[ct][s], qlo[ct][s]);
     }
-    if (qok) {
-      const size_t wi = ((size_t)b * p.T + tq) * nIh + hh;
-      wq = p.w_idx ? ld_f32(static_cast<const QT*>(p.w_idx) + wi) : 1.f;
+    wq[ct] = 0.f;
+    if (qok[ct]) {
+      const size_t wi = ((size_t)b * p.T + tq[ct]) * nIh + hh;
+      wq[ct] = p.w_idx ? ld_f32(static_cast<const QT*>(p.w_idx) + wi) : 1.f;
     }
   }
 
@@ -281,17 +293,19 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
   int nv_max = 0;
   for (int j = 0; j < QPW; ++j)
     if (t0 + j < p.T) nv_max = max(nv_max, nvis_of(t0 + j));
-  const int nv_me = qok ? nvis_of(tq) : 0;
+  int nv_me[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) nv_me[ct] = qok[ct] ? nvis_of(tq[ct]) : 0;
   // key rows of chunk c (row 16c + n, clamped: past the end the last row is
-  // re-read and masked); wave w takes chunks w, w + 4, ..., D in flight;
+  // re-read and masked); wave w takes chunks w, w + NWV, ..., D in flight;
   // refills are unconditional so that no loaded register is copied. A row is
   // CI fp32 (KM 0: 4 bytes per channel, split here), CI bf16 high, middle and
   // low parts (KM 1: 6 bytes per channel), or CI fp16 high and low parts
   // (KM 2: 4 bytes per channel).
-  constexpr int D = 4;
+  constexpr int D = CT == 1 ? 4 : 2;
   constexpr int ROW_BYTES = KM == 1 ? 6 * CI : 4 * CI;
   const int nch = (nv_max + 15) / 16;
-  const int mine = nch > wave ? (nch - wave + 3) / 4 : 0;
+  const int mine = nch > wave ? (nch - wave + NWV - 1) / NWV : 0;
   // batch stride: k_bstride (4-byte units, fp32 rows only) or nb whole rows
   const long long kbs = (KM == 0 && p.k_bstride) ? p.k_bstride * 4 : (long long)nb * ROW_BYTES;
   const char* kbase = reinterpret_cast<const char*>(p.k_idx) + (size_t)b * kbs;
@@ -333,47 +347,52 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
   // folded into the head weight: relu(a s) w = relu(a) (s w) for s > 0
   const float lscale = KM == 2 ? p.scale * kSplit16Unscale : p.scale;
   const bool fold = lscale > 0.f;
-  const float wqs = fold ? wq * lscale : wq;
+  float wqs[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) wqs[ct] = fold ? wq[ct] * lscale : wq[ct];
   const float ascale = fold ? 1.f : lscale;
   auto consume = [&](int c, const KFrag& kf) {
-    // the smallest cross products first, so that each later (larger) term is
-    // added to an accumulator of the smaller ones
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    if constexpr (KM == 2) {
 #pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf.hi[s], ql16[s], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf.lo[s], qh16[s], acc, 0, 0, 0);
+    for (int ct = 0; ct < CT; ++ct) {
+      // the smallest cross products first, so that each later (larger) term
+      // is added to an accumulator of the smaller ones
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (KM == 2) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf.hi[s], ql16[ct][s], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf.lo[s], qh16[ct][s], acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf.hi[s], qh16[ct][s], acc, 0, 0, 0);
+      } else {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.mid[s], qmid[ct][s], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.hi[s], qlo[ct][s], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.lo[s], qhi[ct][s], acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.hi[s], qmid[ct][s], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.mid[s], qhi[ct][s], acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.hi[s], qhi[ct][s], acc, 0, 0, 0);
       }
+      // acc[e]: block 16c + 4*q4 + e, column n. No branch in here: the lanes
+      // whose value is not kept write their own word of this wave's sink
+      // words, since a branch costs the overlap of the chunks loaded ahead.
 #pragma unroll
-      for (int s = 0; s < NS; ++s)
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf.hi[s], qh16[s], acc, 0, 0, 0);
-    } else {
-#pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.mid[s], qmid[s], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.hi[s], qlo[s], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.lo[s], qhi[s], acc, 0, 0, 0);
+      for (int e = 0; e < 4; ++e) {
+        const float v = head_sum<NIH>(fmaxf(acc[e] * ascale, 0.f) * wqs[ct]);
+        const int blk = 16 * c + 4 * q4 + e;
+        float* dst = (hh == 0 && qok[ct] && blk < nv_me[ct]) ? logits + jq[ct] * ldl + blk
+                                                             : sink + lane;
+        *dst = v;
       }
-#pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.hi[s], qmid[s], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.mid[s], qhi[s], acc, 0, 0, 0);
-      }
-#pragma unroll
-      for (int s = 0; s < NS; ++s)
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.hi[s], qhi[s], acc, 0, 0, 0);
-    }
-    // acc[e]: block 16c + 4*q4 + e, column n. No branch in here: the lanes
-    // whose value is not kept write their own word of this wave's sink
-    // words, since a branch costs the overlap of the chunks loaded ahead.
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float v = head_sum<NIH>(fmaxf(acc[e] * ascale, 0.f) * wqs);
-      const int blk = 16 * c + 4 * q4 + e;
-      float* dst = (hh == 0 && qok && blk < nv_me) ? logits + jq * ldl + blk
-                                                   : sink + lane;
-      *dst = v;
     }
   };
   KFrag kf[D];
@@ -382,7 +401,7 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
   // also cover the chunks loaded after it)
 #pragma unroll
   for (int d = 0; d < D; ++d) {
-    load(wave + 4 * d, kf[d]);
+    load(wave + NWV * d, kf[d]);
     __builtin_amdgcn_sched_barrier(0);
   }
   // chunks past this wave's last are consumed too: their blocks lie beyond
@@ -391,21 +410,21 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
   for (int m0 = 0; m0 < mine; m0 += D) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
-      consume(wave + 4 * (m0 + d), kf[d]);
-      load(wave + 4 * (m0 + d + D), kf[d]);
+      consume(wave + NWV * (m0 + d), kf[d]);
+      load(wave + NWV * (m0 + d + D), kf[d]);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
   __syncthreads();
 
-  // ---- per query: top-k (wave w takes queries w, w + 4, ...) ----
+  // ---- per query: top-k (wave w takes queries w, w + NWV, ...) ----
   // Rows of up to 256 * RG visible blocks: select_in_registers. Longer rows:
   // an 8-bit radix select on the order keys below the leading bits common to
   // all of them, stopped as soon as the boundary digit holds exactly the keys
   // still needed, then one gather in index order. The selected (key, ~index)
   // values are sorted (descending) only when asked.
   constexpr int U = 8;  // LDS reads in flight per pass
-  for (int j = wave; j < QPW; j += 4) {
+  for (int j = wave; j < QPW; j += NWV) {
     const int t = t0 + j;
     if (t >= p.T) break;
     const int nv = nvis_of(t);
@@ -558,12 +577,31 @@ __global__ __launch_bounds__(256) void indexer_kernel(IndexerParams p) {
 
 size_t indexer_lds_bytes(int nb, int nIh, int topk) { return indexer_lds(nb, nIh, topk, false); }
 
+// Two column tiles (8 waves, twice the queries per key row read) when the
+// logits of twice the queries leave room for two workgroups per CU; one
+// otherwise, and for a single query per row (decode).
+static int indexer_ct(const IndexerParams& p) {
+  // (fp16-split keys of up to 64 channels: other row formats and widths need
+  // more registers for a second tile than four waves per SIMD leave)
+  return p.k_split == 2 && p.cI <= 64 && p.T >= 16 &&
+                 indexer_lds(p.nb, p.nIh, p.topk, indexer_lean(p), 2) <= 80 * 1024
+             ? 2
+             : 1;
+}
+
 hipError_t indexer_dispatch(const IndexerParams& p, int dtype, hipStream_t s) {
-  const int QPW = 16 / p.nIh;
-  const size_t lds = indexer_lds(p.nb, p.nIh, p.topk, indexer_lean(p));
+  const int CT = indexer_ct(p);
+  const int QPW = CT * 16 / p.nIh;
+  const size_t lds = indexer_lds(p.nb, p.nIh, p.topk, indexer_lean(p), CT);
   const unsigned groups = (unsigned)(p.B * ((p.T + QPW - 1) / QPW));
-#define KCH_IDX_T(QT, CI, NIH, KS) \
-  hipLaunchKernelGGL((indexer_kernel<QT, CI, NIH, KS>), dim3(groups), dim3(256), lds, s, p)
+#define KCH_IDX_T(QT, CI, NIH, KS)                                                                   \
+  do {                                                                                              \
+    if (KS == 2 && CI <= 64 && CT == 2)                                                             \
+      hipLaunchKernelGGL((indexer_kernel<QT, CI, NIH, KS, (KS == 2 && CI <= 64 ? 2 : 1)>), dim3(groups), \
+                         dim3(512), lds, s, p);                                                     \
+    else                                                                                            \
+      hipLaunchKernelGGL((indexer_kernel<QT, CI, NIH, KS, 1>), dim3(groups), dim3(256), lds, s, p);  \
+  } while (0)
 #define KCH_IDX_NIH(QT, CI, NIH)                   \
   do {                                             \
     if (p.k_split == 2) KCH_IDX_T(QT, CI, NIH, 2); \
