@@ -95,19 +95,21 @@ __device__ __forceinline__ float head_sum(float v) {
 // lane and group): rows of up to 256 * RG visible blocks are selected there.
 constexpr int RG = 8;
 
-// Unsorted output with every row short enough for the register selection:
-// the launch needs no histogram or selection buffers in LDS.
-__host__ __device__ inline bool indexer_lean(const IndexerParams& p) {
-  return !p.sorted && p.nb <= 256 * RG;
-}
+// Unsorted output: the selected indices go straight to global memory, so the
+// launch needs no selection buffers in LDS.
+__host__ __device__ inline bool indexer_lean(const IndexerParams& p) { return !p.sorted; }
 
-// LDS of a launch with CT column tiles (CT * 16 / nIh queries, 4 * CT waves)
+// LDS of a launch with CT column tiles (CT * 16 / nIh queries, 4 * CT waves):
+// logits and sink words, per-wave histograms when a row can exceed the
+// register selection (nb > 256 RG), per-wave selection buffers unless lean.
 __host__ __device__ inline size_t indexer_lds(int nb, int nIh, int topk, bool lean, int ct = 1) {
   int ptop = 1;
   while (ptop < topk) ptop <<= 1;
   const int nwv = 4 * ct;
-  const size_t base = (size_t)(ct * 16 / nIh) * ((nb + 3) & ~3) * 4 + (size_t)nwv * 64 * 4;
-  return lean ? base : base + (size_t)nwv * 256 * 4 + (size_t)nwv * ptop * 8;
+  size_t z = (size_t)(ct * 16 / nIh) * ((nb + 3) & ~3) * 4 + (size_t)nwv * 64 * 4;
+  if (nb > 256 * RG) z += (size_t)nwv * 256 * 4;
+  if (!lean) z += (size_t)nwv * ptop * 8;
+  return z;
 }
 
 // Top-k of one query's logits row lg[0 .. nv) (LDS, 16-byte aligned) by one
@@ -232,15 +234,15 @@ __global__ __launch_bounds__(256 * CT, CT == 2 ? 4 : 1) void indexer_kernel(Inde
   const size_t lg_bytes = (size_t)QPW * ldl * 4;
   int ptop = 1;
   while (ptop < topk) ptop <<= 1;
-  // LDS: logits [QPW][ldl] | sink words [NWV][64] | (unless lean) histograms
-  // [NWV][256] and selections [NWV][ptop]. Lean: unsorted output of rows that
-  // the register selection handles, whose indices go straight to global memory.
+  // LDS: logits [QPW][ldl] | sink words [NWV][64] | (nb > 256 RG) histograms
+  // [NWV][256] | (unless lean) selections [NWV][ptop]. Lean: unsorted output,
+  // whose indices go straight to global memory.
   const bool lean = indexer_lean(p);
+  const size_t hist_bytes = nb > 256 * RG ? (size_t)NWV * 256 * 4 : 0;
   float* logits = reinterpret_cast<float*>(smem);
   float* sink = reinterpret_cast<float*>(smem + lg_bytes) + 64 * wave;
   uint32_t* hist = reinterpret_cast<uint32_t*>(smem + lg_bytes + NWV * 64 * 4) + 256 * wave;
-  u64* sel = reinterpret_cast<u64*>(smem + lg_bytes + NWV * 64 * 4 + NWV * 256 * 4) +
-             (size_t)ptop * wave;
+  u64* sel = reinterpret_cast<u64*>(smem + lg_bytes + NWV * 64 * 4 + hist_bytes) + (size_t)ptop * wave;
 
   auto nvis_of = [&](int t) {
     if (p.dense_visible) return nb;
@@ -528,7 +530,8 @@ __global__ __launch_bounds__(256 * CT, CT == 2 ? 4 : 1) void indexer_kernel(Inde
       for (int i = lane; i < nv; i += 64) lk[i] = order_key(lg[i]);
       wave_lds_sync();
     }
-    // gather the cnt selected values (key, ~index) in index order
+    // gather the cnt selected values (key, ~index) in index order; lean: the
+    // indices straight to global memory, -1 past the selected count
     int at = 0, eqs = 0;
     for (int i0 = 0; i0 < nv; i0 += 64) {
       const int i = i0 + lane;
@@ -538,9 +541,22 @@ __global__ __launch_bounds__(256 * CT, CT == 2 ? 4 : 1) void indexer_kernel(Inde
       const unsigned long long em = __ballot(eq);
       const bool tk = gt || (eq && eqs + mbcnt64(em) < tie_take);
       const unsigned long long tm = __ballot(tk);
-      if (tk) sel[at + mbcnt64(tm)] = kv64(k, i);
+      if (tk) {
+        const int o = at + mbcnt64(tm);
+        if (!lean) sel[o] = kv64(k, i);
+        else if (p.idx64) static_cast<long long*>(p.idx_out)[orow + o] = i;
+        else static_cast<int*>(p.idx_out)[orow + o] = i;
+      }
       at += __popcll(tm);
       eqs += __popcll(em);
+    }
+    if (lean) {
+      for (int i = at + lane; i < topk; i += 64) {
+        if (p.idx64) static_cast<long long*>(p.idx_out)[orow + i] = -1;
+        else static_cast<int*>(p.idx_out)[orow + i] = -1;
+      }
+      wave_lds_sync();  // this wave's reads of its row and histogram are done
+      continue;
     }
     }
     wave_lds_sync();  // the selected values are in LDS

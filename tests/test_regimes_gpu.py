@@ -15,6 +15,10 @@
   blocks within 2 eps of the boundary. The mismatch fraction is printed.
   Outputs at those queries are checked against the oracle on the selection
   the kernel made.
+* rows beyond the register selection: the indexer at configs[4]'s prefill
+  length (T=16384, 4096 blocks) takes the radix select; its unsorted and
+  sorted selections hold the same sets, the unsorted rows in ascending
+  index, and both match the oracle at 192 late queries under the same bound.
 * ``configs[3]`` at full length: ``hca_core`` at T=32768 (B=1; m'=128, 256
   compressed blocks in two key tiles, window 128 + sink, 16 heads of 128) on
   projections of random layer weights, at 448 queries (the first 64, 128
@@ -150,6 +154,53 @@ def test_csa_config2_late_queries(dev):
     print(f"C2 selection: {differ} of {rows} rows differ from the oracle "
           f"({differ / rows:.4f}); {near} rows have a k-th/(k+1)-th gap within 2 eps; "
           f"largest logit error {worst:.3f} eps", file=sys.stderr)
+
+
+def test_csa_rows_beyond_register_select(dev):
+    """Rows longer than the register selection's 2048 blocks (configs[4]'s
+    prefill length, T=16384: 4096 blocks) take the radix select: the unsorted
+    selection (indices written straight to global memory in ascending order,
+    as csa_core's attention takes them) and the sorted one (the indexer
+    boundary's order) hold the same sets, and both agree with the oracle at
+    late queries within the logit bound."""
+    import kch
+    from kch import ops_csa
+    B, T, m, topk, win, cI = 1, 16384, 4, 512, 128, 64
+    proj, par, sink = _c2_projections(dev, B, T, seed=23)
+    out, idx = kch.csa_core(*proj, *par, m=m, topk=topk, sliding_window=win, sink_logits=sink,
+                            normalize_qk=True, return_indices=True)
+    nb = T // m
+    k_split = torch.empty(B, nb, 2 * cI, device=dev, dtype=torch.float16)
+    ops_csa._compress("t", proj[4], proj[5], par[2], m, out_raw=False, key=k_split,
+                      normalize=True, key_split=2)
+    sel = {}
+    for srt in (False, True):
+        sel[srt], _ = ops_csa._indexer("t", proj[7], k_split, proj[8], topk, 1.0, m, dense=False,
+                                       normalize_q=True, idx64=False, want_logits=False,
+                                       sorted_=srt, key_split=2)
+    torch.cuda.synchronize()
+    # every row: the same set; unsorted rows in ascending index, padding -1 last
+    a = sel[False].cpu().numpy().astype(np.int64)
+    s = sel[True].cpu().numpy().astype(np.int64)
+    assert np.array_equal(np.sort(a, -1), np.sort(s, -1))
+    assert np.array_equal(np.sort(a, -1), np.sort(idx.cpu().numpy().astype(np.int64), -1))
+    big = np.iinfo(np.int64).max
+    d = np.diff(np.where(a >= 0, a, big), axis=-1)
+    assert np.all((d > 0) | ((d == 0) & (a[..., 1:] < 0))), "unsorted rows not ascending"
+    Q = np.concatenate([np.arange(8256, 8256 + 64), np.arange(T - 128, T)])
+    hp = [x.float().cpu().numpy() for x in proj]
+    hpar = [x.float().cpu().numpy() for x in par]
+    _, ref_idx, lg = OC.csa_core_at(*hp, *hpar, m=m, topk=topk, queries=Q, sliding_window=win,
+                                    sink_logits=sink.cpu().numpy(), compute=np.float64)
+    assert np.all(np.isfinite(lg).sum(-1) > 2048)   # the rows the radix select takes
+    eps = logit_eps(hp[8][:, Q], 4)
+    r, d, n = check_selection("long rows (unsorted)", a[:, Q], ref_idx, lg, eps, sorted_=False)
+    r2, d2, _ = check_selection("long rows (sorted)", s[:, Q], ref_idx, lg, eps, sorted_=True)
+    print(f"long rows: {d} and {d2} of {r} rows differ from the oracle ({n} near-ties)",
+          file=sys.stderr)
+    ref_out, _, _ = OC.csa_core_at(*hp, *hpar, m=m, topk=topk, queries=Q, sliding_window=win,
+                                   sink_logits=sink.cpu().numpy(), indices=a[:, Q])
+    close("long rows csa_core out", out.float().cpu().numpy()[:, Q], ref_out)
 
 
 def test_hca_config3_full_length(dev):
