@@ -1033,7 +1033,8 @@ DecodePlan decode_plan(int B, int nb, int nh, int hd, int topk, int ring_len, bo
     pl.ko = (nb + 3) & ~3;
   }
   pl.na = sparse ? (sel ? topk : 0) : nb;
-  const long long rows = (long long)pl.na + ring_len;
+  // the attention takes the attended blocks in whole 32-row steps (padded)
+  const long long rows = (long long)((pl.na + 31) & ~31) + ring_len;
   // row groups (one workgroup each): about 768 over the batch (three resident
   // per CU: one round), at least 128 rows, at most 64 per sequence, a
   // multiple of 64 rows
@@ -1070,6 +1071,8 @@ int run_decode_attn(const char* fn, const DecodePlan& pl, const void* q, const v
                     int ring_len, const float* sink, void* out, int B, int nb, int nh, int hd,
                     float scale, int normalize_q, int qdtype, int odtype, char* ws,
                     hipStream_t s, const DynStep& dyn = DynStep()) {
+  if ((long long)nb * hd * 2 >= (1LL << 31) || (long long)ring_len * hd * 2 >= (1LL << 31))
+    return fail(KCH_ERR_UNSUPPORTED, "%s: a sequence's cached rows exceed 2 GiB (32-bit row offsets)", fn);
   kch::DecodeAttnParams a;
   a.n_seen = dyn.n_seen;
   a.m = dyn.m;

@@ -420,12 +420,15 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(AttnParams p) {
       const int j0 = 32 * st;
       const int ms = __builtin_amdgcn_readfirstlane(j0 < nm_pad ? 1 : 0);
       const __amdgpu_buffer_rsrc_t rs = ms ? rs_kv : rs_loc;
+      // a step past the query's rows (the loop loads two ahead) reads nothing
+      // from memory: its offsets get bit 31 set, beyond every resource (< 2 GiB)
+      const unsigned past = __builtin_amdgcn_readfirstlane(j0 >= n_tot ? 0x80000000u : 0u);
 #pragma unroll
       for (int i = 0; i < W::NLI; ++i) {
         // HD 64: the upper 8 lanes of a group take slot i + 4 (a select of
         // values, not an indexed read: that would put sl in scratch memory)
         const int v = W::TPR == 8 ? sl.v[i] ^ ((sl.v[i] ^ sl.v[(i + 4) & 7]) & hmask) : sl.v[i];
-        rr.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)((unsigned)v * ROWB + lane_off), 0, 0);
+        rr.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(((unsigned)v * ROWB + lane_off) | past), 0, 0);
       }
       bool any = false;
 #pragma unroll

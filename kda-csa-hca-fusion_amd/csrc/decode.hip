@@ -1039,76 +1039,116 @@ __global__ __launch_bounds__(256, 3) void attn_kernel(DecodeAttnParams p) {
     ring_len = min(t1, p.win);
     if (!p.idx) na = nb;
   }
-  const int nrows = na + ring_len;
+  // the attended rows in 32-row steps: blocks j < na (padded to na_pad, a
+  // multiple of 32, with masked rows), then the ring rows; a step holds only
+  // one kind (row groups start at multiples of 64)
+  const int na_pad = (na + 31) & ~31;
+  const int nrows = na_pad + ring_len;
   const int jg0 = g * p.rows_per_group, jg1 = min(nrows, jg0 + p.rows_per_group);
 
   const QT* qrow = static_cast<const QT*>(p.q) + (size_t)b * (p.ld_qb ? p.ld_qb : (long long)p.nh * HD) +
                    (size_t)n * HD;
   W w;
   w.template init<QT>(n < p.nh ? qrow : nullptr, p.normalize_q != 0, p.scale);
-  const bf16_t* kv = p.kv + (size_t)b * p.kv_bstride;
-  const bf16_t* ring = p.ring ? p.ring + (size_t)b * p.ring_bstride : nullptr;
-  const int* idx = p.idx ? p.idx + (size_t)b * p.na : nullptr;
-  // rows of padding lanes must still be readable: a cached block when there is
-  // one, else the ring (a group only exists when one of the two holds rows; a
-  // device-driven step always has the key storage)
-  const bf16_t* dflt = (na > 0 || !ring) ? kv : ring;
-  // The group's rows come in 32-row steps, wave w taking steps w, w + 4, ...,
-  // gathered row-major (whole rows per TPR lanes: a load instruction covers
-  // RPI full rows, contiguous for consecutive cached blocks) with nontemporal
-  // loads (every row is read once). Block indices of a step (one per lane of
-  // the first 32) are loaded two steps ahead; the loads are clamped, entries
-  // are read only for rows below min(jg1, na). Without indices a readable word
-  // is loaded.
-  const int* ip = idx ? idx : reinterpret_cast<const int*>(dflt);
-  const int ilim = idx ? max(min(jg1, na), 1) : 1;
-  auto row_j = [&](int m, int r) { return jg0 + 32 * (wv + 4 * m) + r; };
-  auto idx_of = [&](int m) { return ip[min(row_j(m, lane & 31), ilim - 1)]; };
-  typedef typename W::u32x4 u32x4;
-  auto load_step = [&](int m, int ix, unsigned& valid) {
-    typename W::Rows rr;
-    valid = 0u;
+  // Rows are read through buffer resources over this sequence's cached
+  // blocks and ring rows with 32-bit byte offsets (an offset past a
+  // resource's end reads zeros: a -1 slot, a block beyond nb, a padding row),
+  // nontemporal (every row is read once). They are taken in the score layout
+  // (MqaWave::chunk_sl): slot k of lane group q4 is row row_sl(k, q4) of the
+  // step, the row whose scores the lane holds; its 8 block indices are
+  // fetched a step ahead (16-byte loads when na is a multiple of 4).
+  constexpr int ROWB = HD * 2;
+  const int lane_off = 16 * (lane % W::TPR), q4 = lane >> 4;
+  const int hmask = (W::TPR == 8 && ((lane >> 3) & 1)) ? -1 : 0;  // HD 64: slot i + 4
+  const __amdgpu_buffer_rsrc_t rs_kv = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<bf16_t*>(p.kv + (size_t)b * p.kv_bstride), 0, nb * ROWB, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs_ring = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<bf16_t*>(p.ring ? p.ring + (size_t)b * p.ring_bstride : p.kv), 0,
+      p.ring ? ring_len * ROWB : 0, 0x00020000);
+  const bool has_idx = p.idx != nullptr && na > 0;
+  const __amdgpu_buffer_rsrc_t rs_idx = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int*>(has_idx ? p.idx + (size_t)b * p.na : nullptr), 0, has_idx ? na * 4 : 0,
+      0x00020000);
+  const bool idx16 = (na & 3) == 0;
+  auto row_j = [&](int m) { return jg0 + 32 * (wv + 4 * m); };  // first row of step m
+  struct Sel {
+    int v[8];
+  };
+  auto load_sel = [&](int m, Sel& sl) {
+    const int j0 = row_j(m);
+    if (__builtin_amdgcn_readfirstlane(j0 < na_pad ? 1 : 0)) {
+      if (p.idx) {
+        if (idx16) {
+          typedef int i32x4 __attribute__((ext_vector_type(4)));
+          const i32x4 x = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_idx, (j0 + 4 * q4) * 4, 0, 0));
+          const i32x4 y = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_idx, (j0 + 16 + 4 * q4) * 4, 0, 0));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            sl.v[e] = x[e];
+            sl.v[4 + e] = y[e];
+          }
+        } else {
+#pragma unroll
+          for (int k = 0; k < 8; ++k)
+            sl.v[k] = (int)__builtin_amdgcn_raw_buffer_load_b32(rs_idx, (j0 + W::row_sl(k, q4)) * 4, 0, 0);
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) sl.v[k] = j0 + W::row_sl(k, q4);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) sl.v[k] = j0 - na_pad + W::row_sl(k, q4);
+    }
+  };
+  // the loads of step m; ok[k]: slot k is a row of this group. Returns
+  // whether any row of the step is (uniform).
+  auto load_rows = [&](int m, const Sel& sl, typename W::Rows& rr, bool (&ok)[8]) {
+    const int j0 = row_j(m);
+    const int ms = __builtin_amdgcn_readfirstlane(j0 < na_pad ? 1 : 0);
+    const __amdgpu_buffer_rsrc_t rs = ms ? rs_kv : rs_ring;
+    // a step past the group (the loop loads two ahead) reads nothing from
+    // memory: its offsets get bit 31 set, beyond every resource (< 2 GiB)
+    const unsigned past = __builtin_amdgcn_readfirstlane(j0 >= jg1 ? 0x80000000u : 0u);
 #pragma unroll
     for (int i = 0; i < W::NLI; ++i) {
-      const int r = i * W::RPI + lane / W::TPR;
-      const int j = row_j(m, r);
-      const int blk = idx ? __shfl(ix, r) : j;
-      bool ok = j < jg1;
-      const bf16_t* row = dflt;
-      if (j < na) {
-        ok = ok && blk >= 0 && blk < nb;
-        if (ok) row = kv + (size_t)blk * HD;
-      } else if (ok) {
-        row = ring + (size_t)(j - na) * HD;
-      }
-      rr.v[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(row + 8 * (lane % W::TPR)));
-      const unsigned long long mb = __ballot(ok);
-#pragma unroll
-      for (int k = 0; k < W::RPI; ++k)
-        valid |= (unsigned)((mb >> (W::TPR * k)) & 1ull) << (i * W::RPI + k);
+      // (a select of values, not an indexed read: that would put sl in scratch memory)
+      const int v = W::TPR == 8 ? sl.v[i] ^ ((sl.v[i] ^ sl.v[(i + 4) & 7]) & hmask) : sl.v[i];
+      rr.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(((unsigned)v * ROWB + lane_off) | past),
+                                                      0, 2 /* nontemporal */);
     }
-    return rr;
+    bool any = false;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int j = j0 + W::row_sl(k, q4);
+      const bool okb = (j < na) & ((unsigned)sl.v[k] < (unsigned)nb);
+      const bool okr = j - na_pad < ring_len;
+      ok[k] = (j < jg1) & (ms ? okb : okr);
+      any |= ok[k];
+    }
+    return __ballot(any) != 0ull;
   };
   const TileOffsets<HD> to;
   const int nsg = (jg1 - jg0 + 31) / 32;                   // steps in the group
   const int mine = nsg > wv ? (nsg - wv + 3) / 4 : 0;      // this wave's
-  // two steps in flight (named registers: an indexed array of them ends up in
-  // scratch memory); refills are unconditional (past the end they read the
-  // default row, masked off), and a wave's odd last step is masked (vm = 0)
-  // rather than peeled off
-  int ix0 = idx_of(0), ix1 = idx_of(1);
-  unsigned vm0, vm1;
-  typename W::Rows fr0 = load_step(0, ix0, vm0);
-  ix0 = idx_of(2);
-  typename W::Rows fr1 = load_step(1, ix1, vm1);
-  ix1 = idx_of(3);
+  // two steps in flight and the indices of the next (named registers: an
+  // indexed array of them ends up in scratch memory); steps past this wave's
+  // last are loaded (masked, any = false) rather than peeled
+  Sel sl;
+  typename W::Rows fr0, fr1;
+  bool ok0[8], ok1[8];
+  load_sel(0, sl);
+  bool any0 = load_rows(0, sl, fr0, ok0);
+  load_sel(1, sl);
+  bool any1 = load_rows(1, sl, fr1, ok1);
+  load_sel(2, sl);
   for (int m0 = 0; m0 < mine; m0 += 2) {
-    if (vm0) w.chunk_rows(fr0, vm0, stage, to);
-    fr0 = load_step(m0 + 2, ix0, vm0);
-    ix0 = idx_of(m0 + 4);
-    if (vm1) w.chunk_rows(fr1, vm1, stage, to);
-    fr1 = load_step(m0 + 3, ix1, vm1);
-    ix1 = idx_of(m0 + 5);
+    if (any0) w.chunk_sl(fr0, ok0, stage, to);
+    any0 = load_rows(m0 + 2, sl, fr0, ok0);
+    load_sel(m0 + 3, sl);
+    if (any1) w.chunk_sl(fr1, ok1, stage, to);
+    any1 = load_rows(m0 + 3, sl, fr1, ok1);
+    load_sel(m0 + 4, sl);
   }
   w.finalize();
 
