@@ -43,6 +43,17 @@ constexpr int KTR = 64;   // key rows per key-pass workgroup
 
 __device__ __forceinline__ bf16_t lo_of(float x) { return (bf16_t)(x - (float)(bf16_t)x); }
 
+// acc + a * b with b exactly bf16 (its low part zero): al*bh + ah*bh
+__device__ __forceinline__ f32x4 mfma2a(const bf16x8& ah, const bf16x8& al, const bf16x8& bh, f32x4 acc) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
+}
+// acc + a * b with a exactly bf16: ah*bl + ah*bh
+__device__ __forceinline__ f32x4 mfma2b(const bf16x8& ah, const bf16x8& bh, const bf16x8& bl, f32x4 acc) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
+}
+
 __device__ __forceinline__ f32x4 mfma3(const bf16x8& ah, const bf16x8& al, const bf16x8& bh,
                                        const bf16x8& bl, f32x4 acc) {
   acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
@@ -145,7 +156,9 @@ struct QWave {
 };
 
 // ---------------------------------------------------------------- query pass
-template <int HD, bool SPARSE>
+// DL0: dout is exactly bf16 (bf16 input; its split's low part is zero), so
+// the products with it take two MFMAs instead of three.
+template <int HD, bool SPARSE, bool DL0>
 __global__ __launch_bounds__(256, 2) void attn_bwd_q_kernel(HcaBwdParams p) {
   using W = QWave<HD>;
   constexpr int NS = W::NS, NT = W::NT, TPR = W::TPR, RPI = W::RPI, NLI = W::NLI;
@@ -171,7 +184,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_q_kernel(HcaBwdParams p) {
       qh[s] = *reinterpret_cast<const bf16x8*>(p.qs_hi + ro + 32 * s);
       ql[s] = *reinterpret_cast<const bf16x8*>(p.qs_lo + ro + 32 * s);
       dh[s] = *reinterpret_cast<const bf16x8*>(p.ds_hi + ro + 32 * s);
-      dl[s] = *reinterpret_cast<const bf16x8*>(p.ds_lo + ro + 32 * s);
+      dl[s] = DL0 ? bf16x8{} : *reinterpret_cast<const bf16x8*>(p.ds_lo + ro + 32 * s);
     }
   }
   const int nsel = SPARSE ? p.topk : min((t + 1) / p.m2, p.nb);
@@ -280,7 +293,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_q_kernel(HcaBwdParams p) {
         const bf16x8 kh = *reinterpret_cast<const bf16x8*>(sth + 16 * HD * half + to.key(s));
         const bf16x8 kl = *reinterpret_cast<const bf16x8*>(stl + 16 * HD * half + to.key(s));
         sa = mfma3(kh, kl, qh[s], ql[s], sa);
-        da = mfma3(kh, kl, dh[s], dl[s], da);
+        da = DL0 ? mfma2a(kh, kl, dh[s], da) : mfma3(kh, kl, dh[s], dl[s], da);
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -466,7 +479,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_q_kernel(HcaBwdParams p) {
 // ------------------------------------------------------------------ key pass
 // MODE 0: compressed rows (HCA: visible when n < (t+1) / m2; CSA: selected),
 // chunk ci of KQC queries; MODE 1: window rows (row u seen by t in [u, u + win)).
-template <int HD, int MODE>
+template <int HD, int MODE, bool DL0>
 __global__ __launch_bounds__(256, 2) void attn_bwd_k_kernel(HcaBwdParams p, int nchunk) {
   constexpr int NS = HD / 32, NT = HD / 16;
   constexpr int TILE = 32 * HD;
@@ -567,9 +580,13 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_k_kernel(HcaBwdParams p, int 
         const bf16x8 xh = *reinterpret_cast<const bf16x8*>(qs_h + ko);
         const bf16x8 xl = *reinterpret_cast<const bf16x8*>(qs_l + ko);
         const bf16x8 yh = *reinterpret_cast<const bf16x8*>(ds_h + ko);
-        const bf16x8 yl = *reinterpret_cast<const bf16x8*>(ds_l + ko);
         sa = mfma3(xh, xl, kh[s], kl[s], sa);
-        da = mfma3(yh, yl, kh[s], kl[s], da);
+        if constexpr (DL0) {
+          da = mfma2b(yh, kh[s], kl[s], da);
+        } else {
+          const bf16x8 yl = *reinterpret_cast<const bf16x8*>(ds_l + ko);
+          da = mfma3(yh, yl, kh[s], kl[s], da);
+        }
       }
       // lane: heads 4q .. 4q+3 of query tq, key rk
       const bool vis = visible(tq);
@@ -592,9 +609,13 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_k_kernel(HcaBwdParams p, int 
       const bf16x8 bqh = MqaWave<HD>::vt_frag(qs_h, to, tt);
       const bf16x8 bql = MqaWave<HD>::vt_frag(qs_l, to, tt);
       const bf16x8 bdh = MqaWave<HD>::vt_frag(ds_h, to, tt);
-      const bf16x8 bdl = MqaWave<HD>::vt_frag(ds_l, to, tt);
       dk[tt] = mfma3(ash, asl, bqh, bql, dk[tt]);
-      dk[tt] = mfma3(aph, apl, bdh, bdl, dk[tt]);
+      if constexpr (DL0) {
+        dk[tt] = mfma2a(aph, apl, bdh, dk[tt]);
+      } else {
+        const bf16x8 bdl = MqaWave<HD>::vt_frag(ds_l, to, tt);
+        dk[tt] = mfma3(aph, apl, bdh, bdl, dk[tt]);
+      }
     }
     if (more) put(lds[buf ^ 1], pv);
     __syncthreads();
@@ -705,21 +726,28 @@ hipError_t attn_bwd_mfma_dispatch(HcaBwdParams p, void* ws, hipStream_t s) {
       hipLaunchKernelGGL((split_rows_kernel<HDV, float>), grid_rows((long long)BT, HDV), dim3(256), \
                          0, s, p.kl, (long long)BT, 1, 1, p.kl_hi, p.kl_lo, (float*)nullptr, 0);    \
   } while (0)
-#define KCH_PASSES(HDV)                                                                            \
+#define KCH_PASSES_D(HDV, DL)                                                                      \
   do {                                                                                             \
     const unsigned qg = (unsigned)(p.B * ((p.T + 3) / 4));                                         \
     if (p.sparse)                                                                                  \
-      hipLaunchKernelGGL((attn_bwd_q_kernel<HDV, true>), dim3(qg), dim3(256), 0, s, p);            \
+      hipLaunchKernelGGL((attn_bwd_q_kernel<HDV, true, DL>), dim3(qg), dim3(256), 0, s, p);        \
     else                                                                                           \
-      hipLaunchKernelGGL((attn_bwd_q_kernel<HDV, false>), dim3(qg), dim3(256), 0, s, p);           \
+      hipLaunchKernelGGL((attn_bwd_q_kernel<HDV, false, DL>), dim3(qg), dim3(256), 0, s, p);       \
     if (p.nb > 0 && !(p.sparse && p.topk == 0)) {                                                  \
       const int ntile = (p.nb + KTR - 1) / KTR;                                                    \
-      hipLaunchKernelGGL((attn_bwd_k_kernel<HDV, 0>), dim3(ntile * nchunk, p.B), dim3(256), 0, s, p, \
-                         nchunk);                                                                  \
+      hipLaunchKernelGGL((attn_bwd_k_kernel<HDV, 0, DL>), dim3(ntile * nchunk, p.B), dim3(256), 0, s, \
+                         p, nchunk);                                                               \
     }                                                                                              \
     if (p.win > 0)                                                                                 \
-      hipLaunchKernelGGL((attn_bwd_k_kernel<HDV, 1>), dim3((p.T + KTR - 1) / KTR, p.B), dim3(256), 0, \
-                         s, p, nchunk);                                                            \
+      hipLaunchKernelGGL((attn_bwd_k_kernel<HDV, 1, DL>), dim3((p.T + KTR - 1) / KTR, p.B), dim3(256), \
+                         0, s, p, nchunk);                                                         \
+  } while (0)
+#define KCH_PASSES(HDV)                                                                            \
+  do {                                                                                             \
+    if (p.qdt == DT_BF16)                                                                          \
+      KCH_PASSES_D(HDV, true);                                                                     \
+    else                                                                                           \
+      KCH_PASSES_D(HDV, false);                                                                    \
   } while (0)
   if (HD == 64) {
     KCH_SPLIT(64);
@@ -731,6 +759,7 @@ hipError_t attn_bwd_mfma_dispatch(HcaBwdParams p, void* ws, hipStream_t s) {
 #undef KCH_SPLIT
 #undef KCH_SPLIT_Q
 #undef KCH_PASSES
+#undef KCH_PASSES_D
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (p.nb > 0 && p.sparse && p.topk == 0) {
