@@ -1042,6 +1042,10 @@ DecodePlan decode_plan(int B, int nb, int nh, int hd, int topk, int ring_len, bo
   grows = grows < 128 ? 128 : grows;
   grows = grows < (rows + 63) / 64 ? (rows + 63) / 64 : grows;
   grows = (grows + 63) & ~63LL;
+  // a short step (at most 24 steps of 32 rows per sequence, a batch the
+  // minimum group size would spread over one round) takes one group per
+  // sequence: a merge launch costs more than the group's extra steps
+  if (rows <= 768 && (long long)B * rows <= 768LL * 128) grows = (rows + 63) & ~63LL;
   pl.grows = (int)grows;
   pl.ngrp = rows > 0 ? (int)((rows + grows - 1) / grows) : 0;
   size_t off = 0;

@@ -1017,12 +1017,70 @@ __global__ __launch_bounds__(256) void idx_merge_kernel(DecodeIdxParams p) {
   write_sorted<true>(sel, cnt, topk, p.idx_out + (size_t)b * topk);
 }
 
+// Merges the ngrp partials of (sequence b, head h), dims 8 d8 .. 8 d8 + 7,
+// and adds the sink: one pass with a running reference point, the partial
+// loads of four groups in flight.
+template <int HD, typename OT>
+__device__ __forceinline__ void combine_partials(const DecodeAttnParams& p, int b, int h, int d8) {
+  float M = -INFINITY, L = 0.f, acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+  auto fold = [&](float2 ml, float4 x0, float4 x1) {
+    if (!(ml.y > 0.f)) return;
+    const float Mn = fmaxf(M, ml.x);
+    const float a = fast_exp2(M - Mn), c = fast_exp2(ml.x - Mn);
+    L = L * a + ml.y * c;
+    const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = acc[i] * a + xs[i] * c;
+    M = Mn;
+  };
+  const size_t s0 = (size_t)b * p.ngrp;
+  auto ld = [&](int s, float2& ml, float4& x0, float4& x1) {
+    const size_t sl = (s0 + s) * p.nh + h;
+    ml = *reinterpret_cast<const float2*>(p.part_ml + sl * 2);
+    const float* po = p.part_o + sl * HD + 8 * d8;
+    x0 = *reinterpret_cast<const float4*>(po);
+    x1 = *reinterpret_cast<const float4*>(po + 4);
+  };
+  int s = 0;
+  for (; s + 4 <= p.ngrp; s += 4) {
+    float2 ml[4];
+    float4 x0[4], x1[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) ld(s + u, ml[u], x0[u], x1[u]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) fold(ml[u], x0[u], x1[u]);
+  }
+  for (; s < p.ngrp; ++s) {
+    float2 ml;
+    float4 x0, x1;
+    ld(s, ml, x0, x1);
+    fold(ml, x0, x1);
+  }
+  float f = 0.f;
+  if (L > 0.f) {
+    float denom = L;
+    if (p.sink) denom += fast_exp2(p.sink[h] * kLog2eF - M);
+    f = 1.f / denom;
+  }
+  OT* out = static_cast<OT*>(p.out) + ((size_t)b * p.nh + h) * HD + 8 * d8;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) out[i] = from_f32<OT>(acc[i] * f);
+}
+
 // Decode attention over one group of rows of one sequence (a workgroup): the
-// 4 waves take the group's 16-row chunks in turn (wave w: chunks w, w + 4,
-// ...), four chunks in flight per wave, merge their (M, L, o) in LDS, and
+// 4 waves take the group's 32-row steps in turn (wave w: steps w, w + 4,
+// ...), two steps in flight per wave, merge their (M, L, o) in LDS, and
 // either finish the sequence (one group) or leave a partial for
 // attn_combine_kernel.
-template <int HD, typename QT, typename OT>
+// DENSE (no index list: every cached block, then the ring) computes the row
+// numbers of a step instead of loading them. That is not only fewer loads: the
+// indexed form's index loads are issued behind the previous step's row loads,
+// so waiting for them waits for those rows too; a kernel holding both forms
+// gets that wait on the dense path as well (it sits where the paths join),
+// which leaves one step in flight per wave instead of two.
+template <int HD, typename QT, typename OT, bool DENSE>
 __global__ __launch_bounds__(256, 3) void attn_kernel(DecodeAttnParams p) {
   using W = MqaWave<HD>;
   constexpr int STAGE = W::STAGE_ELEMS;                 // bf16 per wave
@@ -1046,10 +1104,19 @@ __global__ __launch_bounds__(256, 3) void attn_kernel(DecodeAttnParams p) {
   const int nrows = na_pad + ring_len;
   const int jg0 = g * p.rows_per_group, jg1 = min(nrows, jg0 + p.rows_per_group);
 
+  // The query's words are loaded first and converted only after the first
+  // rows are requested: a wait for a load also waits for every load issued
+  // before it, so the rows must not be issued ahead of the query.
   const QT* qrow = static_cast<const QT*>(p.q) + (size_t)b * (p.ld_qb ? p.ld_qb : (long long)p.nh * HD) +
-                   (size_t)n * HD;
-  W w;
-  w.template init<QT>(n < p.nh ? qrow : nullptr, p.normalize_q != 0, p.scale);
+                   (size_t)(n < p.nh ? n : 0) * HD;
+  typedef uint32_t u32x4q __attribute__((ext_vector_type(4)));
+  constexpr int QW = sizeof(QT) == 4 ? 2 : 1;  // 16-byte words per 8 query elements
+  u32x4q qraw[W::NS][QW];
+#pragma unroll
+  for (int s = 0; s < W::NS; ++s)
+#pragma unroll
+    for (int h = 0; h < QW; ++h)
+      qraw[s][h] = *reinterpret_cast<const u32x4q*>(qrow + 32 * s + 8 * (lane >> 4) + 4 * h);
   // Rows are read through buffer resources over this sequence's cached
   // blocks and ring rows with 32-bit byte offsets (an offset past a
   // resource's end reads zeros: a -1 slot, a block beyond nb, a padding row),
@@ -1065,7 +1132,7 @@ __global__ __launch_bounds__(256, 3) void attn_kernel(DecodeAttnParams p) {
   const __amdgpu_buffer_rsrc_t rs_ring = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<bf16_t*>(p.ring ? p.ring + (size_t)b * p.ring_bstride : p.kv), 0,
       p.ring ? ring_len * ROWB : 0, 0x00020000);
-  const bool has_idx = p.idx != nullptr && na > 0;
+  const bool has_idx = !DENSE && p.idx != nullptr && na > 0;
   const __amdgpu_buffer_rsrc_t rs_idx = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<int*>(has_idx ? p.idx + (size_t)b * p.na : nullptr), 0, has_idx ? na * 4 : 0,
       0x00020000);
@@ -1076,7 +1143,11 @@ __global__ __launch_bounds__(256, 3) void attn_kernel(DecodeAttnParams p) {
   };
   auto load_sel = [&](int m, Sel& sl) {
     const int j0 = row_j(m);
-    if (__builtin_amdgcn_readfirstlane(j0 < na_pad ? 1 : 0)) {
+    if constexpr (DENSE) {
+      const int r0 = j0 < na_pad ? j0 : j0 - na_pad;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) sl.v[k] = r0 + W::row_sl(k, q4);
+    } else if (__builtin_amdgcn_readfirstlane(j0 < na_pad ? 1 : 0)) {
       if (p.idx) {
         if (idx16) {
           typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -1142,6 +1213,28 @@ __global__ __launch_bounds__(256, 3) void attn_kernel(DecodeAttnParams p) {
   load_sel(1, sl);
   bool any1 = load_rows(1, sl, fr1, ok1);
   load_sel(2, sl);
+  W w;
+  {
+    float f[W::NS][8];
+    const bool keep = n < p.nh;
+#pragma unroll
+    for (int s = 0; s < W::NS; ++s) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float x;
+        if constexpr (sizeof(QT) == 4) {
+          x = __uint_as_float(qraw[s][i >> 2][i & 3]);
+        } else {
+          const uint32_t wd = qraw[s][0][i >> 1];
+          const uint16_t hb = (uint16_t)((i & 1) ? (wd >> 16) : (wd & 0xffffu));
+          if constexpr (std::is_same<QT, bf16_t>::value) x = __uint_as_float((uint32_t)hb << 16);
+          else x = (float)__builtin_bit_cast(_Float16, hb);
+        }
+        f[s][i] = keep ? x : 0.f;
+      }
+    }
+    w.setup(f, p.normalize_q != 0, p.scale);
+  }
   for (int m0 = 0; m0 < mine; m0 += 2) {
     if (any0) w.chunk_sl(fr0, ok0, stage, to);
     any0 = load_rows(m0 + 2, sl, fr0, ok0);
@@ -1214,9 +1307,8 @@ __global__ __launch_bounds__(256, 3) void attn_kernel(DecodeAttnParams p) {
   }
 }
 
-// Merges the ngrp partials of each (sequence, head) and adds the sink; thread
-// -> (sequence, head, 8 dims), one pass with a running reference point, the
-// partial loads of four groups in flight.
+// Merges the ngrp partials of each (sequence, head): thread -> (sequence,
+// head, 8 dims).
 template <int HD, typename OT>
 __global__ __launch_bounds__(256) void attn_combine_kernel(DecodeAttnParams p) {
   constexpr int PH = HD / 8;
@@ -1224,52 +1316,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(DecodeAttnParams p) {
   if (gid >= (long long)p.B * p.nh * PH) return;
   const int d8 = (int)(gid % PH);
   const long long bh = gid / PH;
-  const int h = (int)(bh % p.nh), b = (int)(bh / p.nh);
-  float M = -INFINITY, L = 0.f, acc[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
-  auto fold = [&](float2 ml, float4 x0, float4 x1) {
-    if (!(ml.y > 0.f)) return;
-    const float Mn = fmaxf(M, ml.x);
-    const float a = fast_exp2(M - Mn), c = fast_exp2(ml.x - Mn);
-    L = L * a + ml.y * c;
-    const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = acc[i] * a + xs[i] * c;
-    M = Mn;
-  };
-  const size_t s0 = (size_t)b * p.ngrp;
-  auto ld = [&](int s, float2& ml, float4& x0, float4& x1) {
-    const size_t sl = (s0 + s) * p.nh + h;
-    ml = *reinterpret_cast<const float2*>(p.part_ml + sl * 2);
-    const float* po = p.part_o + sl * HD + 8 * d8;
-    x0 = *reinterpret_cast<const float4*>(po);
-    x1 = *reinterpret_cast<const float4*>(po + 4);
-  };
-  int s = 0;
-  for (; s + 4 <= p.ngrp; s += 4) {
-    float2 ml[4];
-    float4 x0[4], x1[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) ld(s + u, ml[u], x0[u], x1[u]);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) fold(ml[u], x0[u], x1[u]);
-  }
-  for (; s < p.ngrp; ++s) {
-    float2 ml;
-    float4 x0, x1;
-    ld(s, ml, x0, x1);
-    fold(ml, x0, x1);
-  }
-  float f = 0.f;
-  if (L > 0.f) {
-    float denom = L;
-    if (p.sink) denom += fast_exp2(p.sink[h] * kLog2eF - M);
-    f = 1.f / denom;
-  }
-  OT* out = static_cast<OT*>(p.out) + ((size_t)b * p.nh + h) * HD + 8 * d8;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) out[i] = from_f32<OT>(acc[i] * f);
+  combine_partials<HD, OT>(p, (int)(bh / p.nh), (int)(bh % p.nh), d8);
 }
 
 __global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* p, long long n, uint32_t v) {
@@ -1360,10 +1407,12 @@ hipError_t decode_idx_dispatch(const DecodeIdxParams& p, int qdtype, int kdtype,
 
 hipError_t decode_attn_dispatch(const DecodeAttnParams& p, int qdtype, int odtype, hipStream_t s) {
   const dim3 grid((unsigned)((long long)p.B * p.ngrp)), block(256);
-#define KCH_DATT(HD, QT)                                                                          \
-  if (odtype == DT_F32) hipLaunchKernelGGL((attn_kernel<HD, QT, float>), grid, block, 0, s, p);    \
-  else if (odtype == DT_BF16) hipLaunchKernelGGL((attn_kernel<HD, QT, bf16_t>), grid, block, 0, s, p); \
-  else hipLaunchKernelGGL((attn_kernel<HD, QT, _Float16>), grid, block, 0, s, p);
+#define KCH_DATT_D(HD, QT, D)                                                                        \
+  if (odtype == DT_F32) hipLaunchKernelGGL((attn_kernel<HD, QT, float, D>), grid, block, 0, s, p);    \
+  else if (odtype == DT_BF16) hipLaunchKernelGGL((attn_kernel<HD, QT, bf16_t, D>), grid, block, 0, s, p); \
+  else hipLaunchKernelGGL((attn_kernel<HD, QT, _Float16, D>), grid, block, 0, s, p);
+#define KCH_DATT(HD, QT) \
+  if (p.idx) { KCH_DATT_D(HD, QT, false) } else { KCH_DATT_D(HD, QT, true) }
   if (p.hd == 128) {
     if (qdtype == DT_F32) { KCH_DATT(128, float) }
     else if (qdtype == DT_BF16) { KCH_DATT(128, bf16_t) }
@@ -1374,6 +1423,7 @@ hipError_t decode_attn_dispatch(const DecodeAttnParams& p, int qdtype, int odtyp
     else { KCH_DATT(64, _Float16) }
   }
 #undef KCH_DATT
+#undef KCH_DATT_D
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.ngrp == 1) return e;
   const long long outs = (long long)p.B * p.nh * (p.hd / 8);

@@ -57,9 +57,11 @@ def _run(name, dev, B, nb, c, cI, nh, nIh, win, topk, seed):
 
 def test_noalloc_matches_workspace_entry_point(dev):
     name = "kch_csa_decode_noalloc"
-    # two calls in a row: a large multi-range step, then a smaller one
+    # calls in a row: a large multi-range step, a smaller one, then a larger
+    # batch again
     for (B, nb, c, cI, nh, nIh, win, topk, seed) in [(4, 20000, 128, 64, 16, 4, 128, 512, 1),
-                                                      (2, 3000, 64, 32, 8, 2, 16, 64, 2)]:
+                                                      (2, 3000, 64, 32, 8, 2, 16, 64, 2),
+                                                      (96, 2000, 128, 64, 16, 4, 128, 256, 3)]:
         print(f"{name}: B={B} nb={nb} topk={topk} win={win}", flush=True)
         (o_ws, o_na), (i_ws, i_na) = _run(name, dev, B, nb, c, cI, nh, nIh, win, topk, seed)
         assert np.isfinite(o_na).all()
