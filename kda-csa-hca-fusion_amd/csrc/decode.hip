@@ -1081,7 +1081,7 @@ __device__ __forceinline__ void combine_partials(const DecodeAttnParams& p, int 
 // gets that wait on the dense path as well (it sits where the paths join),
 // which leaves one step in flight per wave instead of two.
 template <int HD, typename QT, typename OT, bool DENSE>
-__global__ __launch_bounds__(256, 3) void attn_kernel(DecodeAttnParams p) {
+__global__ __launch_bounds__(256, DENSE ? 3 : 2) void attn_kernel(DecodeAttnParams p) {
   using W = MqaWave<HD>;
   constexpr int STAGE = W::STAGE_ELEMS;                 // bf16 per wave
   constexpr int MERGE = 4 * 16 * HD + 4 * 16 * 2;       // floats: o and (M, L) per wave and head
@@ -1202,17 +1202,28 @@ __global__ __launch_bounds__(256, 3) void attn_kernel(DecodeAttnParams p) {
   const TileOffsets<HD> to;
   const int nsg = (jg1 - jg0 + 31) / 32;                   // steps in the group
   const int mine = nsg > wv ? (nsg - wv + 3) / 4 : 0;      // this wave's
-  // two steps in flight and the indices of the next (named registers: an
-  // indexed array of them ends up in scratch memory); steps past this wave's
-  // last are loaded (masked, any = false) rather than peeled
-  Sel sl;
+  // Two steps in flight (named registers: an indexed array of them ends up in
+  // scratch memory). Indexed steps keep the indices of the two after them: a
+  // step's indices are requested before the rows of the step ahead of it, so
+  // waiting for them never waits for rows not yet consumed. Steps past this
+  // wave's last are loaded (masked, any = false) rather than peeled.
+  Sel s0, s1;
   typename W::Rows fr0, fr1;
   bool ok0[8], ok1[8];
-  load_sel(0, sl);
-  bool any0 = load_rows(0, sl, fr0, ok0);
-  load_sel(1, sl);
-  bool any1 = load_rows(1, sl, fr1, ok1);
-  load_sel(2, sl);
+  bool any0, any1;
+  if constexpr (DENSE) {
+    load_sel(0, s0);
+    any0 = load_rows(0, s0, fr0, ok0);
+    load_sel(1, s0);
+    any1 = load_rows(1, s0, fr1, ok1);
+  } else {
+    load_sel(0, s0);
+    load_sel(1, s1);
+    any0 = load_rows(0, s0, fr0, ok0);
+    any1 = load_rows(1, s1, fr1, ok1);
+    load_sel(2, s0);
+    load_sel(3, s1);
+  }
   W w;
   {
     float f[W::NS][8];
@@ -1236,12 +1247,21 @@ __global__ __launch_bounds__(256, 3) void attn_kernel(DecodeAttnParams p) {
     w.setup(f, p.normalize_q != 0, p.scale);
   }
   for (int m0 = 0; m0 < mine; m0 += 2) {
-    if (any0) w.chunk_sl(fr0, ok0, stage, to);
-    any0 = load_rows(m0 + 2, sl, fr0, ok0);
-    load_sel(m0 + 3, sl);
-    if (any1) w.chunk_sl(fr1, ok1, stage, to);
-    any1 = load_rows(m0 + 3, sl, fr1, ok1);
-    load_sel(m0 + 4, sl);
+    if constexpr (DENSE) {
+      if (any0) w.chunk_sl(fr0, ok0, stage, to);
+      load_sel(m0 + 2, s0);
+      any0 = load_rows(m0 + 2, s0, fr0, ok0);
+      if (any1) w.chunk_sl(fr1, ok1, stage, to);
+      load_sel(m0 + 3, s0);
+      any1 = load_rows(m0 + 3, s0, fr1, ok1);
+    } else {
+      if (any0) w.chunk_sl(fr0, ok0, stage, to);
+      any0 = load_rows(m0 + 2, s0, fr0, ok0);
+      load_sel(m0 + 4, s0);
+      if (any1) w.chunk_sl(fr1, ok1, stage, to);
+      any1 = load_rows(m0 + 3, s1, fr1, ok1);
+      load_sel(m0 + 5, s1);
+    }
   }
   w.finalize();
 
