@@ -580,7 +580,8 @@ def bench_decode_bw(dev, reps=5):
       CSA: B=64, 1M-token context (262144 blocks of m=4), indexer 4 x 64 top-512
            over bf16 key rows, 16 heads of 128, window 128 + sink;
       HCA: B=128, 1M-token context (8192 blocks of m'=128), 16 heads of 128,
-           window 128 + sink.
+           window 128 + sink; and the same at a 4M-token context (32768 blocks,
+           1.08 GB per step).
     Algorithmic bytes: every key row, its inverse norm, the selected rows and the
     window for CSA; every compressed row and the window for HCA."""
     from kch import _lib
@@ -629,21 +630,26 @@ def bench_decode_bw(dev, reps=5):
                   "hbm_frac": byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
     del kr, kinv, kv, ring, ws
     torch.cuda.empty_cache()
-    B, nb = 128, 8192
-    kv = torch.nn.functional.normalize(torch.randn(B, nb, c, device=dev, generator=g), dim=-1).to(torch.bfloat16)
-    ring = torch.nn.functional.normalize(torch.randn(B, win, c, device=dev, generator=g), dim=-1).to(torch.bfloat16)
-    q = torch.randn(B, nh, c, device=dev, generator=g)
-    out = torch.empty(B, nh, c, device=dev)
-    nbytes = lib.kch_decode_ws_bytes(B, nb, nh, c, 0, win, 0)
-    ws = torch.empty(nbytes, device=dev, dtype=torch.uint8)
+    # HCA at two cache sizes: the step's fixed costs (launch, the first rows'
+    # latency, the partials' merge launch: about 9 us) weigh on 275 MB and
+    # much less on 1.08 GB
+    for name, B, nb in (("hca", 128, 8192), ("hca_4M", 128, 32768)):
+        kv = torch.nn.functional.normalize(torch.randn(B, nb, c, device=dev, generator=g), dim=-1).to(torch.bfloat16)
+        ring = torch.nn.functional.normalize(torch.randn(B, win, c, device=dev, generator=g), dim=-1).to(torch.bfloat16)
+        q = torch.randn(B, nh, c, device=dev, generator=g)
+        out = torch.empty(B, nh, c, device=dev)
+        nbytes = lib.kch_decode_ws_bytes(B, nb, nh, c, 0, win, 0)
+        ws = torch.empty(nbytes, device=dev, dtype=torch.uint8)
 
-    def hca():
-        _lib.call("kch_hca_decode", _lib.ptr(q), _lib.ptr(kv), nb * c, _lib.ptr(ring), win * c, win,
-                  _lib.ptr(sink), _lib.ptr(out), B, nb, nh, c, 1.0, 1, 0, 0, _lib.ptr(ws), nbytes, st)
-    ms = timed(hca)
-    byts = B * ((nb + win) * c * 2 + nh * c * 4 * 2)
-    res["hca"] = {"B": B, "context": nb * 128, "blocks": nb, "ms": ms, "algorithmic_bytes": byts,
-                  "gbs": byts / (ms * 1e-3) / 1e9, "hbm_frac": byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+        def hca():
+            _lib.call("kch_hca_decode", _lib.ptr(q), _lib.ptr(kv), nb * c, _lib.ptr(ring), win * c, win,
+                      _lib.ptr(sink), _lib.ptr(out), B, nb, nh, c, 1.0, 1, 0, 0, _lib.ptr(ws), nbytes, st)
+        ms = timed(hca)
+        byts = B * ((nb + win) * c * 2 + nh * c * 4 * 2)
+        res[name] = {"B": B, "context": nb * 128, "blocks": nb, "ms": ms, "algorithmic_bytes": byts,
+                     "gbs": byts / (ms * 1e-3) / 1e9, "hbm_frac": byts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+        del kv, ring, ws
+        torch.cuda.empty_cache()
     return res
 
 

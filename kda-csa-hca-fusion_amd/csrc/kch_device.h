@@ -15,6 +15,8 @@
 //   stored row-major [row][k] and B stored transposed [col][k].
 #pragma once
 
+#include <type_traits>
+
 #include <hip/hip_runtime.h>
 #include <hip/hip_bf16.h>
 #include <hip/hip_fp16.h>
@@ -128,6 +130,37 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 __device__ __forceinline__ float silu_f(float x) { return x / (1.f + expf(-x)); }
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.f / (1.f + expf(-x)); }
 __device__ __forceinline__ float softplus_f(float x) { return x > 20.f ? x : log1pf(expf(x)); }
+
+// The same activations for results rounded to bf16 next, with the hardware
+// base-2 exponential (v_exp_f32, about 1 ulp; e^x = 2^(x log2 e)) and
+// logarithm in place of the library's range-reduced expf / log1pf; the IEEE
+// divisions stay. Over every finite bf16 input the bf16-rounded results equal
+// those of silu_f / sigmoid_f / softplus_f (checked exhaustively on gfx950,
+// tests/test_hybrid_gpu.py::test_kda_gates_fast_activations_exhaustive); for
+// fp16 results they do not always, so fp16 keeps the library forms. log1p(t)
+// is Goldberg's t log(u) / (u - 1), u = 1 + t (exact where u rounds to 1;
+// D. Goldberg, "What every computer scientist should know about
+// floating-point arithmetic", 1991, Theorem 4); below x = -80, where e^x
+// leaves the normal range, the library exponential keeps the denormal tail.
+__device__ __forceinline__ float exp_hw(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+__device__ __forceinline__ float silu_bf(float x) { return x / (1.f + exp_hw(-x)); }
+__device__ __forceinline__ float sigmoid_bf(float x) { return 1.f / (1.f + exp_hw(-x)); }
+__device__ __forceinline__ float softplus_bf(float x) {
+  if (x > 20.f) return x;
+  const float t = x < -80.f ? expf(x) : exp_hw(x);
+  const float u = 1.f + t, d = u - 1.f;
+  return d == 0.f ? t : (__builtin_amdgcn_logf(u) * 0.6931471805599453f) * t / d;
+}
+// The activations a kernel with 16-bit results of type T uses.
+template <typename T> __device__ __forceinline__ float silu_t(float x) {
+  if constexpr (std::is_same<T, bf16_t>::value) return silu_bf(x); else return silu_f(x);
+}
+template <typename T> __device__ __forceinline__ float sigmoid_t(float x) {
+  if constexpr (std::is_same<T, bf16_t>::value) return sigmoid_bf(x); else return sigmoid_f(x);
+}
+template <typename T> __device__ __forceinline__ float softplus_t(float x) {
+  if constexpr (std::is_same<T, bf16_t>::value) return softplus_bf(x); else return softplus_f(x);
+}
 
 // The value a tensor of type T stores for x (identity for fp32): each torch
 // operation of the reference writes its result in the layer's dtype, and the

@@ -153,7 +153,9 @@ __global__ __launch_bounds__(256) void kda_gates_kernel(KdaGatesParams p) {
 // (LPH lanes per head vector, LPH = K / 8) takes 8 consecutive channels. The
 // q/k head vectors go 64 / LPH per pass (the L2 norm is a reduction over the
 // head's LPH lanes), then v, g and beta, the loads of four passes in flight
-// together. Rounding as in kda_gates_kernel.
+// together. Rounding as in kda_gates_kernel; bf16 results take the
+// activations on the hardware exponential (silu_t and the like), which round
+// to the same bf16 values.
 template <typename T, int LPH>
 __global__ __launch_bounds__(256) void kda_gates_vec_kernel(KdaGatesParams p, long long rows) {
   constexpr int U = 4;  // passes whose loads are in flight together
@@ -176,11 +178,13 @@ __global__ __launch_bounds__(256) void kda_gates_vec_kernel(KdaGatesParams p, lo
       float ss = 0.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        f[u][i] = stored<T>(silu_f(f[u][i]));
+        f[u][i] = stored<T>(silu_t<T>(f[u][i]));
         ss += f[u][i] * f[u][i];
       }
 #pragma unroll
       for (int o = 1; o < LPH; o <<= 1) ss += __shfl_xor(ss, o);
+      // (an IEEE division: quotients of two 16-bit values often sit exactly
+      // on a rounding tie, where a reciprocal's ulp decides the result)
       const float nrm = fmaxf(stored<T>(sqrtf(ss)), 1e-12f);
 #pragma unroll
       for (int i = 0; i < 8; ++i) f[u][i] = f[u][i] / nrm;
@@ -201,7 +205,7 @@ __global__ __launch_bounds__(256) void kda_gates_vec_kernel(KdaGatesParams p, lo
 #pragma unroll
     for (int u = 0; u < U; ++u) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) f[u][e] = silu_f(f[u][e]);
+      for (int e = 0; e < 8; ++e) f[u][e] = silu_t<T>(f[u][e]);
       if (i0 + 64 * u < nv8) store_vec<T, 8>(v + 8 * (i0 + 64 * u), f[u]);
     }
   }
@@ -213,12 +217,12 @@ __global__ __launch_bounds__(256) void kda_gates_vec_kernel(KdaGatesParams p, lo
 #pragma unroll
     for (int u = 0; u < U; ++u) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) f[u][e] = -stored<T>(softplus_f(f[u][e])) * p.decay_scale;
+      for (int e = 0; e < 8; ++e) f[u][e] = -stored<T>(softplus_t<T>(f[u][e])) * p.decay_scale;
       if (i0 + 64 * u < ng8) store_vec<T, 8>(g + 8 * (i0 + 64 * u), f[u]);
     }
   }
   T* beta = static_cast<T*>(p.beta) + row * p.HV;
-  for (int i = lane; i < p.HV; i += 64) beta[i] = from_f32<T>(sigmoid_f(to_f32(pr[2 * HK + 8 * nv8 + i])));
+  for (int i = lane; i < p.HV; i += 64) beta[i] = from_f32<T>(sigmoid_t<T>(to_f32(pr[2 * HK + 8 * nv8 + i])));
 }
 
 // One workgroup per row: the row's values stay in registers (d <= 4096), the

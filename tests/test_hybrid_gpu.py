@@ -132,6 +132,50 @@ def test_kda_gates(dev, dtype, H, HV, K, V, aligned):
             assert exact >= 0.99, f"{name}: only {exact:.4f} of the elements bit-identical"
 
 
+def test_kda_gates_fast_activations_exhaustive(dev):
+    """The wave-per-row kernel (rows of whole 16-byte pieces) takes bf16
+    activations on the hardware exponential; the element-wise kernel (odd row
+    strides) the library's expf / log1pf. On inputs that hold every finite
+    bf16 value in every activation's position, the two give bit-identical
+    q, k, v, g and beta."""
+    from kch import _lib
+    B, T, H, HV, K, V = 1, 16384, 1, 4, 128, 128
+    width = 2 * H * K + HV * V + HV
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    finite = bits[torch.isfinite(bits.float())]
+    gen = torch.Generator().manual_seed(0)
+
+    def fill(n):  # n values cycling through every finite bf16 value, shuffled
+        reps = -(-n // finite.numel())
+        v = finite.repeat(reps)[:n]
+        return v[torch.randperm(n, generator=gen)]
+
+    cols = torch.cat([fill(T * 2 * H * K).view(T, -1), fill(T * HV * V).view(T, -1),
+                      finite.repeat(-(-T * HV // finite.numel()))[:T * HV].view(T, HV)], dim=1)
+    assert cols.shape[1] == width
+    gl_vals = fill(T * HV * K).view(B, T, HV * K)
+    outs = []
+    for ld in (width + (-width) % 8, width + 1 - width % 2):  # aligned, then odd
+        proj = torch.zeros(B, T, ld, dtype=torch.bfloat16)
+        proj[0, :, :width] = cols
+        proj = proj.to(dev)
+        gl = gl_vals.to(dev)
+        q = torch.empty(B, T, H, K, device=dev, dtype=torch.bfloat16)
+        k = torch.empty_like(q)
+        v = torch.empty(B, T, HV, V, device=dev, dtype=torch.bfloat16)
+        g = torch.empty(B, T, HV, K, device=dev, dtype=torch.bfloat16)
+        beta = torch.empty(B, T, HV, device=dev, dtype=torch.bfloat16)
+        _lib.call("kch_kda_gates", _lib.ptr(proj), proj.stride(1), _lib.ptr(gl), gl.stride(1),
+                  _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(beta),
+                  B, T, H, HV, K, V, 0.1, _lib.dtype_code("t", torch.bfloat16),
+                  _lib.stream_of(proj))
+        torch.cuda.synchronize()
+        outs.append([t.view(torch.int16).cpu() for t in (q, k, v, g, beta)])
+    for name, a, b in zip(("q", "k", "v", "g", "beta"), *outs):
+        diff = int((a != b).sum())
+        assert diff == 0, f"{name}: {diff} of {a.numel()} elements differ"
+
+
 @pytest.mark.parametrize("dtype,wdtype", [(torch.bfloat16, torch.float32),
                                           (torch.bfloat16, torch.bfloat16),
                                           (torch.float16, torch.float32)])
