@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define KCH_ABI_VERSION 17
+#define KCH_ABI_VERSION 18
 
 #define KCH_OK 0
 #define KCH_ERR_INVALID 1     /* bad pointer / shape / argument */
@@ -605,6 +605,32 @@ int kch_csa_cache_append(const void* proj, long long ld_proj, void* acc, void* p
 int kch_hca_cache_append(const void* proj, long long ld_proj, void* acc, const float* B_pos,
                          void* ring, void* c_rows, void* c_keys, const int* n_seen, int B, int c,
                          int m2, int win, int cap, int normalize, int dtype, void* stream);
+
+/*
+ * kch_csa_cache_append / kch_hca_cache_append and a row projection of the same
+ * decode step, y[b, :] = x[b, :] W^T for the B rows (W [N, K], row strides
+ * ldx, ldw, ldy in elements; kch_linear_rows_fused without norm, residual or
+ * counter), in one launch: both read only the step's projection row, so their
+ * workgroups run side by side. It serves the decode step's query
+ * up-projection (the q of CSADecodingCache.forward_step /
+ * HCADecodingCache.forward_step, ops_decoding_cache.py:783-1070, 1268-1395,
+ * from W_UQ, ops_csa.py:876-878,923 and ops_hca.py:136-141) beside the append
+ * (ops_decoding_cache.py:631-782, 1200-1267). Results are those of the two
+ * separate calls. bf16 / fp16 only, B <= 16, K a multiple of 32, x and W rows
+ * 16-byte aligned.
+ */
+int kch_csa_cache_append_rows(const void* proj, long long ld_proj, void* acc, void* prev,
+                              const float* Ba, const float* Bb, const float* B_idx, void* ring,
+                              void* c_rows, void* c_keys, void* k_rows, float* k_inv,
+                              const int* n_seen, int B, int c, int cI, int m, int win, int cap,
+                              int normalize, const void* x, long long ldx, const void* w,
+                              long long ldw, void* y, long long ldy, int N, int K, int dtype,
+                              void* stream);
+int kch_hca_cache_append_rows(const void* proj, long long ld_proj, void* acc, const float* B_pos,
+                              void* ring, void* c_rows, void* c_keys, const int* n_seen, int B,
+                              int c, int m2, int win, int cap, int normalize, const void* x,
+                              long long ldx, const void* w, long long ldw, void* y, long long ldy,
+                              int N, int K, int dtype, void* stream);
 
 /*
  * Workspace bytes of kch_csa_decode_dyn (sparse = 1) / kch_hca_decode_dyn for

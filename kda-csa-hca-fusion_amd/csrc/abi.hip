@@ -1002,6 +1002,69 @@ int kch_hca_cache_append(const void* proj, long long ld_proj, void* acc, const f
   return hip_status(fn, kch::cache_step_dispatch(p, dtype, (hipStream_t)stream));
 }
 
+// A row projection y = x W^T launched beside a cache append: bf16 / fp16, M
+// rows (M <= 16), K a multiple of 32, 16-byte aligned x and w rows.
+static int rows_beside(const char* fn, const void* x, long long ldx, const void* w, long long ldw,
+                       void* y, long long ldy, int M, int N, int K, int dtype,
+                       kch::LinearRowsParams* out) {
+  if (dtype != KCH_DT_BF16 && dtype != KCH_DT_F16)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: dtype %d (bf16 or fp16 only)", fn, dtype);
+  if (M > 16) return fail(KCH_ERR_UNSUPPORTED, "%s: B=%d > 16 rows", fn, M);
+  if (N < 1 || K < 32 || K % 32)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: N=%d, K=%d (K a multiple of 32)", fn, N, K);
+  if (!x || !w || !y) return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
+  if (ldx < K || ldw < K || ldy < N)
+    return fail(KCH_ERR_INVALID, "%s: row strides below the row lengths", fn);
+  if ((ldx | ldw) % 8 || (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) % 16)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: x and w rows must be 16-byte aligned", fn);
+  *out = kch::LinearRowsParams{x, w, y, ldx, ldw, ldy, M, N, K};
+  return KCH_OK;
+}
+
+int kch_csa_cache_append_rows(const void* proj, long long ld_proj, void* acc, void* prev,
+                              const float* Ba, const float* Bb, const float* B_idx, void* ring,
+                              void* c_rows, void* c_keys, void* k_rows, float* k_inv,
+                              const int* n_seen, int B, int c, int cI, int m, int win, int cap,
+                              int normalize, const void* x, long long ldx, const void* w,
+                              long long ldw, void* y, long long ldy, int N, int K, int dtype,
+                              void* stream) {
+  const char* fn = "kch_csa_cache_append_rows";
+  if (c < 1 || cI < 1 || c > 256 || c + cI > 256)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: c=%d, cI=%d (c + cI at most 256)", fn, c, cI);
+  int rc = check_cache_append(fn, proj, ld_proj, 4LL * c + 2LL * cI, acc, c_rows, c_keys, n_seen,
+                              B, c, m, win, ring, cap, dtype);
+  if (rc) return rc;
+  if (B == 0) return KCH_OK;
+  if (!prev || !Ba || !Bb || !B_idx || !k_rows || !k_inv)
+    return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
+  kch::LinearRowsParams lp;
+  if ((rc = rows_beside(fn, x, ldx, w, ldw, y, ldy, B, N, K, dtype, &lp))) return rc;
+  kch::CacheStepParams p{proj, ld_proj, acc, prev, Ba, Bb, B_idx, win > 0 ? ring : nullptr,
+                         c_rows, c_keys, k_rows, k_inv, n_seen, B, c, cI, m, win, cap,
+                         normalize != 0, 1};
+  return hip_status(fn, kch::cache_step_rows_dispatch(p, lp, dtype, (hipStream_t)stream));
+}
+
+int kch_hca_cache_append_rows(const void* proj, long long ld_proj, void* acc, const float* B_pos,
+                              void* ring, void* c_rows, void* c_keys, const int* n_seen, int B,
+                              int c, int m2, int win, int cap, int normalize, const void* x,
+                              long long ldx, const void* w, long long ldw, void* y, long long ldy,
+                              int N, int K, int dtype, void* stream) {
+  const char* fn = "kch_hca_cache_append_rows";
+  if (c < 1 || c > 256) return fail(KCH_ERR_UNSUPPORTED, "%s: c=%d > 256", fn, c);
+  int rc = check_cache_append(fn, proj, ld_proj, 2LL * c, acc, c_rows, c_keys, n_seen, B, c, m2,
+                              win, ring, cap, dtype);
+  if (rc) return rc;
+  if (B == 0) return KCH_OK;
+  if (!B_pos) return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
+  kch::LinearRowsParams lp;
+  if ((rc = rows_beside(fn, x, ldx, w, ldw, y, ldy, B, N, K, dtype, &lp))) return rc;
+  kch::CacheStepParams p{proj, ld_proj, acc, nullptr, B_pos, nullptr, nullptr,
+                         win > 0 ? ring : nullptr, c_rows, c_keys, nullptr, nullptr, n_seen, B, c,
+                         0, m2, win, cap, normalize != 0, 0};
+  return hip_status(fn, kch::cache_step_rows_dispatch(p, lp, dtype, (hipStream_t)stream));
+}
+
 }  // extern "C"
 
 namespace {

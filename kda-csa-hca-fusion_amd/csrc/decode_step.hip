@@ -25,9 +25,12 @@
 //   attention key row and, for CSA, its indexer key row with the inverse norm;
 //   then the b-branch rows the next CSA block overlaps with. One workgroup per
 //   sequence.
+// cache_step_rows_kernel  the append beside a row projection of the same step
+//   (the query up-projection: linear_rows_body.h) in one launch.
 
 #include "attn_common.h"
 #include "kch_kernels.h"
+#include "linear_rows_body.h"
 
 namespace kch {
 
@@ -261,10 +264,11 @@ __device__ __forceinline__ float block_mean(int m, bool prev, VA va, ZA za, VB v
   return num / den;
 }
 
+// The append of sequence b (one workgroup of 256 threads).
 template <typename T>
-__global__ __launch_bounds__(256) void cache_step_kernel(CacheStepParams p) {
+__device__ __forceinline__ void cache_step_block(const CacheStepParams& p, int b) {
   __shared__ float red[8];
-  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int t = p.n_seen[0];
   const int m = p.m, c = p.c, cI = p.cI;
   const int W = p.csa ? 4 * c + 2 * cI : 2 * c;
@@ -352,6 +356,22 @@ __global__ __launch_bounds__(256) void cache_step_kernel(CacheStepParams p) {
 }
 
 template <typename T>
+__global__ __launch_bounds__(256) void cache_step_kernel(CacheStepParams p) {
+  cache_step_block<T>(p, (int)blockIdx.x);
+}
+
+// A cache append and a row projection of the same decode step in one launch:
+// the first ngemv workgroups take the projection's 16-column tiles, the rest
+// one sequence's append each. Both read only the step's projection row.
+template <typename T>
+__global__ __launch_bounds__(256) void cache_step_rows_kernel(CacheStepParams cp, LinearRowsParams lp,
+                                                              int ngemv) {
+  const int blk = (int)blockIdx.x;
+  if (blk < ngemv) rows_detail::linear_rows_block<T, void>(lp, blk);
+  else cache_step_block<T>(cp, blk - ngemv);
+}
+
+template <typename T>
 hipError_t kda_front_launch(const KdaFrontParams& p, int wdtype, hipStream_t s) {
   const dim3 grid((unsigned)p.B), block(256);
   if (wdtype == DT_F32) hipLaunchKernelGGL((kda_front_kernel<T, float>), grid, block, 0, s, p);
@@ -385,6 +405,15 @@ hipError_t kda_step_dispatch(const KdaStepParams& p, int dtype, hipStream_t s) {
   if (dtype == DT_F32) return kda_step_launch<float>(p, s);
   if (dtype == DT_BF16) return kda_step_launch<bf16_t>(p, s);
   return kda_step_launch<_Float16>(p, s);
+}
+
+hipError_t cache_step_rows_dispatch(const CacheStepParams& cp, const LinearRowsParams& lp, int dtype,
+                                   hipStream_t s) {
+  const int ngemv = (lp.N + 15) / 16;
+  const dim3 grid((unsigned)(ngemv + cp.B)), block(256);
+  if (dtype == DT_BF16) hipLaunchKernelGGL(cache_step_rows_kernel<bf16_t>, grid, block, 0, s, cp, lp, ngemv);
+  else hipLaunchKernelGGL(cache_step_rows_kernel<_Float16>, grid, block, 0, s, cp, lp, ngemv);
+  return hipGetLastError();
 }
 
 hipError_t cache_step_dispatch(const CacheStepParams& p, int dtype, hipStream_t s) {

@@ -353,6 +353,10 @@ struct CacheStepParams {
   int B, c, cI, m, win, cap, normalize, csa;
 };
 hipError_t cache_step_dispatch(const CacheStepParams& p, int dtype, hipStream_t s);
+// The append and a row projection (no norm, residual or counter; bf16 / fp16)
+// in one launch (decode_step.hip).
+hipError_t cache_step_rows_dispatch(const CacheStepParams& cp, const LinearRowsParams& lp, int dtype,
+                                   hipStream_t s);
 
 
 // Generic CSA / HCA forward (csa_hca_generic.hip): T = float or double

@@ -72,6 +72,10 @@ _SIGNATURES = {
     "kch_kda_decode_step": [_P, _L, _P, _P, _P] + [_I] * 5 + [_F] * 3 + [_I, _P],
     "kch_csa_cache_append": [_P, _L] + [_P] * 11 + [_I] * 8 + [_P],
     "kch_hca_cache_append": [_P, _L] + [_P] * 6 + [_I] * 7 + [_P],
+    "kch_csa_cache_append_rows": [_P, _L] + [_P] * 11 + [_I] * 7 + [_P, _L, _P, _L, _P, _L, _I, _I,
+                                                                    _I, _P],
+    "kch_hca_cache_append_rows": [_P, _L] + [_P] * 6 + [_I] * 6 + [_P, _L, _P, _L, _P, _L, _I, _I,
+                                                                   _I, _P],
     "kch_csa_decode_dyn": [_P, _L] * 7 + [_P, _I, _I, _I, _P, _P, _P] + [_I] * 6 + [_F, _F]
                           + [_I] * 5 + [_P, _SZ, _P],
     "kch_hca_decode_dyn": [_P, _L] * 3 + [_P, _I, _I, _I, _P, _P, _I, _I, _I, _F, _I, _I, _I,

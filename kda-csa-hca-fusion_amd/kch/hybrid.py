@@ -1140,8 +1140,11 @@ class HybridDecoding(nn.Module):
                 P = linear(x_cur, x_cur.stride(0), Wp, torch.empty(B, NP, device=dev, dtype=dt),
                            NP, norm=norm)
                 off_cq = 4 * c + 2 * cfg.csa_cI if csa else 2 * c
-                Q = linear(P[:, off_cq:off_cq + dc], NP, Wq,
-                           torch.empty(B, NQ, device=dev, dtype=dt), NQ)
+                # the query up-projection Q = P[:, cq] Wq^T runs in the cache
+                # append's launch (both read only P)
+                Q = torch.empty(B, NQ, device=dev, dtype=dt)
+                NW, KW = Wq.shape
+                q_rows = (_lib.ptr(P[:, off_cq:]), NP, _lib.ptr(Wq), KW, _lib.ptr(Q), NQ, NW, KW)
                 sw = cache._sw
                 ring = None if sw is None else sw._buf
                 win = 0 if sw is None else sw.win
@@ -1149,11 +1152,12 @@ class HybridDecoding(nn.Module):
                 out = torch.empty(B, nh * c, device=dev, dtype=dt)
                 if csa:
                     cI, nIh, topk, m = cfg.csa_cI, cfg.csa_nIh, cfg.csa_topk, cfg.csa_m
-                    _lib.call("kch_csa_cache_append", _lib.ptr(P), NP, _lib.ptr(cache._acc_buf),
-                              _lib.ptr(cache._prev_buf), _lib.ptr(Ba), _lib.ptr(Bb), _lib.ptr(Bk),
-                              _lib.ptr(ring), _lib.ptr(cache._C.rows), _lib.ptr(cache._C.keys),
-                              _lib.ptr(cache._K.rows), _lib.ptr(cache._K.inv), _lib.ptr(n_dev),
-                              B, c, cI, m, win, cap, normalize, code, stream)
+                    _lib.call("kch_csa_cache_append_rows", _lib.ptr(P), NP,
+                              _lib.ptr(cache._acc_buf), _lib.ptr(cache._prev_buf), _lib.ptr(Ba),
+                              _lib.ptr(Bb), _lib.ptr(Bk), _lib.ptr(ring), _lib.ptr(cache._C.rows),
+                              _lib.ptr(cache._C.keys), _lib.ptr(cache._K.rows),
+                              _lib.ptr(cache._K.inv), _lib.ptr(n_dev), B, c, cI, m, win, cap,
+                              normalize, *q_rows, code, stream)
                     nbytes = lib.kch_decode_dyn_ws_bytes(B, cap, nh, c, topk, win, 1)
                     ws = torch.empty(max(nbytes, 256), device=dev, dtype=torch.uint8)
                     idx = torch.empty(B, topk, device=dev, dtype=torch.int32)
@@ -1168,10 +1172,10 @@ class HybridDecoding(nn.Module):
                     csa_i += 1
                 else:
                     m2 = cfg.hca_m2
-                    _lib.call("kch_hca_cache_append", _lib.ptr(P), NP, _lib.ptr(cache._acc_buf),
-                              _lib.ptr(Bpos), _lib.ptr(ring), _lib.ptr(cache._C.rows),
-                              _lib.ptr(cache._C.keys), _lib.ptr(n_dev), B, c, m2, win, cap,
-                              normalize, code, stream)
+                    _lib.call("kch_hca_cache_append_rows", _lib.ptr(P), NP,
+                              _lib.ptr(cache._acc_buf), _lib.ptr(Bpos), _lib.ptr(ring),
+                              _lib.ptr(cache._C.rows), _lib.ptr(cache._C.keys), _lib.ptr(n_dev),
+                              B, c, m2, win, cap, normalize, *q_rows, code, stream)
                     nbytes = lib.kch_decode_dyn_ws_bytes(B, cap, nh, c, 0, win, 0)
                     ws = torch.empty(max(nbytes, 256), device=dev, dtype=torch.uint8)
                     _lib.call("kch_hca_decode_dyn", _lib.ptr(Q), NQ, _lib.ptr(cache._C.keys),

@@ -226,3 +226,79 @@ def test_cache_append_matches_append_step(dev, kind):
         torch.testing.assert_close(cd._K.inv[:, new], ce._K.inv[:, new], rtol=1e-6, atol=0)
         # the block rows of the overlapped compression as the bulk kernel computes them
         assert torch.equal(cd._C.rows[:, new], ce._C.rows[:, new])
+
+
+@pytest.mark.parametrize("kind", ["csa", "hca"])
+def test_cache_append_rows_matches_separate_calls(dev, kind):
+    """kch_{csa,hca}_cache_append_rows (the append and the query
+    up-projection in one launch) against kch_{csa,hca}_cache_append followed
+    by kch_linear_rows_fused: the caches and the projected rows bit-identical
+    over steps that complete blocks."""
+    import kch
+    from kch import _lib
+    torch.manual_seed(6)
+    B, c, cI, win, dc, NQ = 3, 128, 64, 8, 128, 2304
+    m = 4 if kind == "csa" else 16
+    dt = torch.bfloat16
+    code = _lib.dtype_code("t", dt)
+    W = 4 * c + 2 * cI if kind == "csa" else 2 * c
+    LD = W + dc + 8
+    T0, steps = 21, 40
+    P = torch.randn(B, T0 + steps, LD, device=dev).to(dt)
+    Wq = (torch.randn(NQ, dc, device=dev) / dc ** 0.5).to(dt)
+    if kind == "csa":
+        Ba, Bb, Bk = (0.1 * torch.randn(m, w, device=dev) for w in (c, c, cI))
+        caches = [kch.CSADecodingCache(B, c, cI, m, win, dev, dt) for _ in range(2)]
+        for cc in caches:
+            cc.append_step(*P[:, :T0, :W].split([c, c, c, c, cI, cI], -1), Ba, Bb, Bk)
+    else:
+        Bp = 0.1 * torch.randn(m, c, device=dev)
+        caches = [kch.HCADecodingCache(B, c, m, win, dev, dt) for _ in range(2)]
+        for cc in caches:
+            cc.append_step(*P[:, :T0, :W].split([c, c], -1), Bp)
+    n_seen = torch.zeros(1, device=dev, dtype=torch.int32)
+    for t in range(T0, T0 + steps):
+        row = P[:, t].contiguous()
+        qs = []
+        for i, cd in enumerate(caches):
+            cap = cd._device_buffers()
+            if kind == "csa":
+                cap = max(cd._C.rows.shape[1], cd._K.rows.shape[1])
+                cd._C.ensure(cd.n_blocks, cap)
+                cd._K.ensure(cd.n_blocks, cap)
+            n_seen.fill_(cd.n_tokens_seen)
+            q = torch.empty(B, NQ, device=dev, dtype=dt)
+            rows = (_lib.ptr(row[:, W:]), LD, _lib.ptr(Wq), dc, _lib.ptr(q), NQ, NQ, dc)
+            if kind == "csa":
+                cargs = (_lib.ptr(row), LD, _lib.ptr(cd._acc_buf), _lib.ptr(cd._prev_buf),
+                         _lib.ptr(Ba), _lib.ptr(Bb), _lib.ptr(Bk), _lib.ptr(cd._sw._buf),
+                         _lib.ptr(cd._C.rows), _lib.ptr(cd._C.keys), _lib.ptr(cd._K.rows),
+                         _lib.ptr(cd._K.inv), _lib.ptr(n_seen), B, c, cI, m, win, cap, 1)
+            else:
+                cargs = (_lib.ptr(row), LD, _lib.ptr(cd._acc_buf), _lib.ptr(Bp),
+                         _lib.ptr(cd._sw._buf), _lib.ptr(cd._C.rows), _lib.ptr(cd._C.keys),
+                         _lib.ptr(n_seen), B, c, m, win, cap, 1)
+            if i == 0:
+                _lib.call(f"kch_{kind}_cache_append", *cargs, code, _lib.stream_of(row))
+                _lib.call("kch_linear_rows_fused", rows[0], LD, rows[2], dc, rows[4], NQ, B, NQ,
+                          dc, None, None, 0.0, 0, None, 0, None, code, _lib.stream_of(row))
+            else:
+                _lib.call(f"kch_{kind}_cache_append_rows", *cargs, *rows, code,
+                          _lib.stream_of(row))
+            torch.cuda.synchronize()
+            cd._device_advance()
+            qs.append(q)
+        assert torch.equal(qs[0], qs[1]), f"step {t}: projected rows differ"
+    a, b = caches
+    assert a.n_blocks == b.n_blocks == (T0 + steps) // m
+    for x, y in zip(_cache_state(a), _cache_state(b)):
+        assert torch.equal(x, y)
+
+
+def _cache_state(cache):
+    """The written part of a decode cache's buffers."""
+    nb, acc = cache.n_blocks, cache.accumulator_len
+    bufs = [cache._sw._buf, cache._acc_buf[:, :acc], cache._C.rows[:, :nb], cache._C.keys[:, :nb]]
+    if hasattr(cache, "_K"):
+        bufs += [cache._prev_buf, cache._K.rows[:, :nb], cache._K.inv[:, :nb]]
+    return bufs
