@@ -607,6 +607,33 @@ int kch_hca_cache_append(const void* proj, long long ld_proj, void* acc, const f
                          int m2, int win, int cap, int normalize, int dtype, void* stream);
 
 /*
+ * The front of a KDA sub-layer and its input projection for one token, in one
+ * launch: h = LayerNorm(x) (as kch_kda_decode_front: _Fp32LayerNorm rounded to
+ * the dtype), then the causal depthwise convolution over [lookback ; h]
+ * (KDAHybridLayer.forward_functional, ops_fused.py:480-551), then
+ * y = conv W^T (the fused input projection, ops_fused.py:571-581), d = K.
+ * The lookback [B, 2, d] is only read; h [B, d] is written to h_out, and
+ * kch_kda_decode_step_shift of the same step advances the lookback from it.
+ * bf16 / fp16, B <= 16, d a multiple of 32 (at most 4096, B d <= 32768),
+ * operands 16-byte aligned; ln_w / ln_b of wdtype.
+ */
+int kch_kda_front_rows(const void* x, long long ldx, const void* ln_w, const void* ln_b,
+                       float eps, int wdtype, const void* lookback, const void* conv_w,
+                       const void* conv_b, void* h_out, const void* w, long long ldw, void* y,
+                       long long ldy, int B, int N, int d, int dtype, void* stream);
+
+/*
+ * kch_kda_decode_step that also advances the conv lookback:
+ * lookback [B, 2, d] <- [lookback[1] ; h] with h [B, d] from
+ * kch_kda_front_rows (ops_fused.py:480-527, the lookback carried to the next
+ * token), the channels split over the step's workgroups.
+ */
+int kch_kda_decode_step_shift(const void* proj, long long ld_proj, const void* g_up, float* state,
+                              void* o, int B, int H, int HV, int K, int V, float scale,
+                              float decay_scale, float g_clamp_min, void* lookback,
+                              const void* h, int d, int dtype, void* stream);
+
+/*
  * kch_csa_cache_append / kch_hca_cache_append and a row projection of the same
  * decode step, y[b, :] = x[b, :] W^T for the B rows (W [N, K], row strides
  * ldx, ldw, ldy in elements; kch_linear_rows_fused without norm, residual or

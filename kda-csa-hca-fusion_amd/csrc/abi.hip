@@ -930,10 +930,13 @@ int kch_kda_decode_front(const void* x, long long ldx, const void* ln_w, const v
   return hip_status(fn, kch::kda_front_dispatch(p, dtype, wdtype, (hipStream_t)stream));
 }
 
-int kch_kda_decode_step(const void* proj, long long ld_proj, const void* g_up, float* state,
-                        void* o, int B, int H, int HV, int K, int V, float scale,
-                        float decay_scale, float g_clamp_min, int dtype, void* stream) {
-  const char* fn = "kch_kda_decode_step";
+}  // extern "C"
+
+// kch_kda_decode_step, and with lookback non-null the conv lookback's advance.
+static int kda_decode_step(const char* fn, const void* proj, long long ld_proj, const void* g_up,
+                           float* state, void* o, int B, int H, int HV, int K, int V, float scale,
+                           float decay_scale, float g_clamp_min, void* lookback, const void* h,
+                           int d, int dtype, void* stream) {
   if (!dtype_ok(dtype)) return fail(KCH_ERR_INVALID, "%s: unknown dtype %d", fn, dtype);
   if (B < 0 || H < 1 || HV < 1 || V < 1) return fail(KCH_ERR_INVALID, "%s: bad sizes", fn);
   if (HV % H) return fail(KCH_ERR_INVALID, "%s: HV=%d must be divisible by H=%d", fn, HV, H);
@@ -949,7 +952,65 @@ int kch_kda_decode_step(const void* proj, long long ld_proj, const void* g_up, f
   if ((uintptr_t)g_up % 16) return fail(KCH_ERR_INVALID, "%s: g_up must be 16-byte aligned", fn);
   kch::KdaStepParams p{proj, ld_proj, g_up, state, o, B, H, HV, K, V, scale, decay_scale,
                        g_clamp_min};
+  p.look = lookback;
+  p.h_in = h;
+  p.d = d;
   return hip_status(fn, kch::kda_step_dispatch(p, dtype, (hipStream_t)stream));
+}
+
+extern "C" {
+
+int kch_kda_decode_step(const void* proj, long long ld_proj, const void* g_up, float* state,
+                        void* o, int B, int H, int HV, int K, int V, float scale,
+                        float decay_scale, float g_clamp_min, int dtype, void* stream) {
+  return kda_decode_step("kch_kda_decode_step", proj, ld_proj, g_up, state, o, B, H, HV, K, V,
+                         scale, decay_scale, g_clamp_min, nullptr, nullptr, 0, dtype, stream);
+}
+
+int kch_kda_front_rows(const void* x, long long ldx, const void* ln_w, const void* ln_b,
+                       float eps, int wdtype, const void* lookback, const void* conv_w,
+                       const void* conv_b, void* h_out, const void* w, long long ldw, void* y,
+                       long long ldy, int B, int N, int d, int dtype, void* stream) {
+  const char* fn = "kch_kda_front_rows";
+  if (dtype != KCH_DT_BF16 && dtype != KCH_DT_F16)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: dtype %d (bf16 or fp16 only)", fn, dtype);
+  if (!dtype_ok(wdtype)) return fail(KCH_ERR_INVALID, "%s: unknown norm dtype %d", fn, wdtype);
+  if (B < 0 || N < 0 || d < 1) return fail(KCH_ERR_INVALID, "%s: bad sizes", fn);
+  if (B == 0 || N == 0) return KCH_OK;
+  if (B > 16) return fail(KCH_ERR_UNSUPPORTED, "%s: B=%d > 16 rows", fn, B);
+  if (d < 32 || d % 32 || d > 4096 || (long long)B * d > kch::kLinearLnMax)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: d=%d (a multiple of 32, at most 4096; B d at most %d)",
+                fn, d, kch::kLinearLnMax);
+  if (!x || !ln_w || !lookback || !conv_w || !h_out || !w || !y)
+    return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
+  if (ldx < d || ldw < d || ldy < N)
+    return fail(KCH_ERR_INVALID, "%s: row strides below the row lengths", fn);
+  const uintptr_t a = (uintptr_t)x | (uintptr_t)ln_w | (uintptr_t)ln_b | (uintptr_t)lookback |
+                      (uintptr_t)conv_w | (uintptr_t)conv_b | (uintptr_t)h_out | (uintptr_t)w;
+  if (a % 16 || (ldx | ldw) % 8) return fail(KCH_ERR_UNSUPPORTED, "%s: operands must be 16-byte aligned", fn);
+  if (std::isnan(eps) || eps < 0.f) return fail(KCH_ERR_INVALID, "%s: bad eps", fn);
+  kch::LinearRowsParams p{x, w, y, ldx, ldw, ldy, B, N, d};
+  p.ln_w = ln_w;
+  p.ln_b = ln_b;
+  p.ln_eps = eps;
+  p.ln_wdtype = wdtype;
+  p.conv_w = conv_w;
+  p.conv_b = conv_b;
+  p.look = lookback;
+  p.h_out = h_out;
+  return hip_status(fn, kch::linear_rows_dispatch(p, dtype, (hipStream_t)stream));
+}
+
+int kch_kda_decode_step_shift(const void* proj, long long ld_proj, const void* g_up, float* state,
+                              void* o, int B, int H, int HV, int K, int V, float scale,
+                              float decay_scale, float g_clamp_min, void* lookback,
+                              const void* h, int d, int dtype, void* stream) {
+  const char* fn = "kch_kda_decode_step_shift";
+  if (d < 1) return fail(KCH_ERR_INVALID, "%s: d=%d", fn, d);
+  if (B > 0 && (!lookback || !h)) return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
+  int rc = kda_decode_step(fn, proj, ld_proj, g_up, state, o, B, H, HV, K, V, scale, decay_scale,
+                           g_clamp_min, lookback, h, d, dtype, stream);
+  return rc;
 }
 
 // Shared checks of the cache append entry points.

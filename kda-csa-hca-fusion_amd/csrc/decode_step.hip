@@ -16,7 +16,9 @@
 //   reference stores it, and the recurrent update of the state
 //   (ops_kda.py:175-267: S <- S e^g; S <- S + beta k (v - k^T S); o = q^T S
 //   scale). Workgroup (sequence, value head, 32 value columns); thread
-//   (column tid / 8, phase tid % 8) owns state rows phase + 8 i.
+//   (column tid / 8, phase tid % 8) owns state rows phase + 8 i. Optionally it
+//   also advances the conv lookback (the front then ran in the projection's
+//   prologue: linear_rows_body.h).
 // cache_step_kernel  CSADecodingCache.append_step / HCADecodingCache.append_step
 //   for one token (ops_decoding_cache.py:631-782, 1200-1267): the ring-window
 //   row, the accumulator row and, on the block's last token, the block's
@@ -151,6 +153,20 @@ __global__ __launch_bounds__(256) void kda_step_kernel(KdaStepParams p) {
   const int HK = p.H * K, HVV = p.HV * p.V;
   const T* pr = static_cast<const T*>(p.proj) + (size_t)b * p.ld_proj;
   float* st = p.state + (size_t)(b * p.HV + hv) * K * p.V + col;
+  if (p.look) {
+    // the conv lookback advances: [look[0] ; look[1]] <- [look[1] ; h], this
+    // workgroup's slice of the d channels (the projection that read the old
+    // lookback has finished)
+    const int nwg = p.HV * nvs, wi = hv * nvs + vs;
+    const int per = ((p.d + nwg - 1) / nwg + 7) & ~7;
+    const int c1 = min(p.d, (wi + 1) * per);
+    T* lk = static_cast<T*>(p.look) + (size_t)b * 2 * p.d;
+    const T* hh = static_cast<const T*>(p.h_in) + (size_t)b * p.d;
+    for (int c = wi * per + tid; c < c1; c += 256) {
+      lk[c] = lk[p.d + c];
+      lk[p.d + c] = hh[c];
+    }
+  }
 
   // the state column and this thread's gate weights first: their loads
   // overlap the activations below

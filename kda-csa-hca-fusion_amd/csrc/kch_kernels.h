@@ -261,6 +261,11 @@ hipError_t layer_norm_dispatch(const LayerNormParams& p, int dtype, int wdtype, 
 //   y <- res + y (res non-null; y rounded to the dtype before the add, as a
 //        separate residual add would see it),
 //   and (*counter)++ by one thread (counter non-null).
+// With the norm, conv_w non-null makes x the KDA layer's front for one token
+// (KDAHybridLayer.forward_functional, ops_fused.py:480-551): h = LN(x) rounded
+// to the dtype, then x <- bias + w0 look[0] + w1 look[1] + w2 h, the causal
+// depthwise convolution over [lookback ; h]; tile 0 writes h to h_out (the
+// lookback's next row), the lookback itself is only read.
 constexpr int kLinearLnMax = 32768;
 struct LinearRowsParams {
   const void* x = nullptr;
@@ -275,6 +280,10 @@ struct LinearRowsParams {
   const void* res = nullptr;   // [M, N], row stride ldr, of the dtype (may be y itself)
   long long ldr = 0;
   int* counter = nullptr;
+  const void* conv_w = nullptr;  // [K, 3] of the dtype (with ln_w)
+  const void* conv_b = nullptr;  // [K] of the dtype or null
+  const void* look = nullptr;    // [M, 2, K] of the dtype
+  void* h_out = nullptr;         // [M, K] of the dtype
 };
 hipError_t linear_rows_dispatch(const LinearRowsParams& p, int dtype, hipStream_t stream);
 
@@ -325,6 +334,11 @@ struct KdaStepParams {
   void* o;
   int B, H, HV, K, V;
   float scale, decay_scale, g_clamp_min;
+  // non-null: the conv lookback [B, 2, d] advances, look <- [look[1] ; h_in]
+  // (h_in [B, d]: the token's LayerNorm rows), each workgroup a slice of d
+  void* look = nullptr;
+  const void* h_in = nullptr;
+  int d = 0;
 };
 hipError_t kda_step_dispatch(const KdaStepParams& p, int dtype, hipStream_t s);
 

@@ -64,13 +64,121 @@ __device__ __forceinline__ void linear_rows_block(const LinearRowsParams& p, int
   const int r = lane & 15, q = lane >> 4;
   const int n0 = blk * 16;
   const int ldl = p.K + 8;  // LDS row stride (elements)
+  // rows past N re-read row N - 1 (their results are not stored); rows of x
+  // past M read row 0 and are zeroed
+  const T* wrow = static_cast<const T*>(p.w) + (size_t)min(n0 + r, p.N - 1) * p.ldw + 8 * q;
+  const int ks = p.K / 32;
+  const int per = (ks + 3) / 4;
+  const int s0 = wv * per, s1 = min(ks, s0 + per);
+  // the first batch of W is requested before the normalisation (it does not
+  // depend on x), so the stream of W starts at once
+  v8 a[kBatch];
+  auto load_w = [&](int sb) {
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) a[u] = *reinterpret_cast<const v8*>(wrow + 32 * min(sb + u, s1 - 1));
+  };
+  if (s0 < s1) load_w(s0);
   if constexpr (LN) {
     // rows of LayerNorm(x) in the dtype, as a separate norm would store them
+    // (with the KDA front: the convolution over [lookback ; LN(x)])
     T* xs = reinterpret_cast<T*>(xs_raw);
     const WT* lw = static_cast<const WT*>(p.ln_w);
     const WT* lb = static_cast<const WT*>(p.ln_b);
+    if (p.K <= 2048) {
+      // a thread per 8 channels, all four waves on every row, the rows two at
+      // a time: the parameters, then both rows' x (and lookback) loads are in
+      // flight together, and each statistic is one block reduction
+      __shared__ float red2[2][4][2];
+      const int tid = threadIdx.x, k0 = 8 * tid;
+      const bool act = k0 < p.K;
+      const int kk = act ? k0 : 0;
+      float w8[8], b8[8], w3[24], cb[8];
+      Load8<WT>::run(lw + kk, w8);
+      if (lb) {
+        Load8<WT>::run(lb + kk, b8);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) b8[i] = 0.f;
+      }
+      if (p.conv_w) {
+#pragma unroll
+        for (int u3 = 0; u3 < 3; ++u3)
+          Load8<T>::run(static_cast<const T*>(p.conv_w) + 3 * kk + 8 * u3, w3 + 8 * u3);
+        if (p.conv_b) {
+          Load8<T>::run(static_cast<const T*>(p.conv_b) + kk, cb);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) cb[i] = 0.f;
+        }
+      }
+      for (int m0 = 0; m0 < p.M; m0 += 2) {
+        float v[2][8], l0[2][8], l1[2][8];
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+          const int m = min(m0 + rr, p.M - 1);
+          Load8<T>::run(static_cast<const T*>(p.x) + (size_t)m * p.ldx + kk, v[rr]);
+          if (p.conv_w) {
+            const T* lk = static_cast<const T*>(p.look) + (size_t)m * 2 * p.K;
+            Load8<T>::run(lk + kk, l0[rr]);
+            Load8<T>::run(lk + p.K + kk, l1[rr]);
+          }
+        }
+        float mean[2], rstd[2];
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+          float sm = 0.f;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) sm += v[rr][i];
+          sm = wave_sum(act ? sm : 0.f);
+          if (lane == 0) red2[0][wv][rr] = sm;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+          mean[rr] = (red2[0][0][rr] + red2[0][1][rr] + red2[0][2][rr] + red2[0][3][rr]) / (float)p.K;
+          float sq = 0.f;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const float dv = v[rr][i] - mean[rr];
+            sq += dv * dv;
+          }
+          sq = wave_sum(act ? sq : 0.f);
+          if (lane == 0) red2[1][wv][rr] = sq;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+          const int m = m0 + rr;
+          rstd[rr] = 1.f / sqrtf((red2[1][0][rr] + red2[1][1][rr] + red2[1][2][rr] + red2[1][3][rr]) /
+                                     (float)p.K + p.ln_eps);
+          if (m >= p.M || !act) continue;
+          float y8[8];
+#pragma unroll
+          for (int i = 0; i < 8; ++i) y8[i] = (v[rr][i] - mean[rr]) * rstd[rr] * w8[i] + b8[i];
+          if (p.conv_w) {
+            float h8[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              h8[i] = stored<T>(y8[i]);
+              y8[i] = fmaf(w3[3 * i + 2], h8[i], fmaf(w3[3 * i + 1], l1[rr][i], fmaf(w3[3 * i], l0[rr][i], cb[i])));
+            }
+            if (blk == 0 && p.h_out) {
+              union { T h[8]; v8 vv; } uh;
+#pragma unroll
+              for (int i = 0; i < 8; ++i) uh.h[i] = from_f32<T>(h8[i]);
+              *reinterpret_cast<v8*>(static_cast<T*>(p.h_out) + (size_t)m * p.K + k0) = uh.vv;
+            }
+          }
+          union { T h[8]; v8 vv; } u;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) u.h[i] = from_f32<T>(y8[i]);
+          *reinterpret_cast<v8*>(xs + (size_t)m * ldl + k0) = u.vv;
+        }
+      }
+      __syncthreads();
+    }
     constexpr int G = 8;  // 8-element groups per lane: K <= 4096
-    for (int m = wv; m < p.M; m += 4) {
+    for (int m = p.K <= 2048 ? p.M : wv; m < p.M; m += 4) {
       const T* xr = static_cast<const T*>(p.x) + (size_t)m * p.ldx;
       float v[G][8];
       float s = 0.f;
@@ -112,6 +220,34 @@ __device__ __forceinline__ void linear_rows_block(const LinearRowsParams& p, int
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) y8[i] = (v[g][i] - mean) * rstd * w8[i] + b8[i];
+        if (p.conv_w) {
+          // the LayerNorm output as the layer receives it (rounded to the
+          // dtype), then out = bias + w0 look[0] + w1 look[1] + w2 h
+          const T* lk = static_cast<const T*>(p.look) + (size_t)m * 2 * p.K;
+          float l0[8], l1[8], w3[24], bias[8], h8[8];
+          Load8<T>::run(lk + k0, l0);
+          Load8<T>::run(lk + p.K + k0, l1);
+#pragma unroll
+          for (int u3 = 0; u3 < 3; ++u3)
+            Load8<T>::run(static_cast<const T*>(p.conv_w) + 3 * k0 + 8 * u3, w3 + 8 * u3);
+          if (p.conv_b) {
+            Load8<T>::run(static_cast<const T*>(p.conv_b) + k0, bias);
+          } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) bias[i] = 0.f;
+          }
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            h8[i] = stored<T>(y8[i]);
+            y8[i] = fmaf(w3[3 * i + 2], h8[i], fmaf(w3[3 * i + 1], l1[i], fmaf(w3[3 * i], l0[i], bias[i])));
+          }
+          if (blk == 0 && p.h_out) {
+            union { T h[8]; v8 vv; } uh;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) uh.h[i] = from_f32<T>(h8[i]);
+            *reinterpret_cast<v8*>(static_cast<T*>(p.h_out) + (size_t)m * p.K + k0) = uh.vv;
+          }
+        }
         union { T h[8]; v8 vv; } u;
 #pragma unroll
         for (int i = 0; i < 8; ++i) u.h[i] = from_f32<T>(y8[i]);
@@ -120,28 +256,19 @@ __device__ __forceinline__ void linear_rows_block(const LinearRowsParams& p, int
     }
     __syncthreads();
   }
-  // rows past N re-read row N - 1 (their results are not stored); rows of x
-  // past M read row 0 and are zeroed
-  const T* wrow = static_cast<const T*>(p.w) + (size_t)min(n0 + r, p.N - 1) * p.ldw + 8 * q;
   const bool mok = r < p.M;
   const T* xrow = LN ? reinterpret_cast<const T*>(xs_raw) + (size_t)(mok ? r : 0) * ldl + 8 * q
                      : static_cast<const T*>(p.x) + (size_t)(mok ? r : 0) * p.ldx + 8 * q;
-  const int ks = p.K / 32;
-  const int per = (ks + 3) / 4;
-  const int s0 = wv * per, s1 = min(ks, s0 + per);
   const v8 zero = {};
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   for (int sb = s0; sb < s1; sb += kBatch) {
-    v8 a[kBatch], b[kBatch];
+    if (sb != s0) load_w(sb);
+    v8 b[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) b[u] = *reinterpret_cast<const v8*>(xrow + 32 * min(sb + u, s1 - 1));
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      const int s = min(sb + u, s1 - 1);  // past the range: a repeated step, zeroed below
-      a[u] = *reinterpret_cast<const v8*>(wrow + 32 * s);
-      b[u] = *reinterpret_cast<const v8*>(xrow + 32 * s);
-    }
-#pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      const bool live = mok && sb + u < s1;
+      const bool live = mok && sb + u < s1;  // past the range: a repeated step, zeroed
       acc = V::mfma(a[u], live ? b[u] : zero, acc);
     }
   }

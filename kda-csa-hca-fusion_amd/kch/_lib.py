@@ -70,6 +70,10 @@ _SIGNATURES = {
                               _I, _P],
     "kch_kda_decode_front": [_P, _L, _P, _P, _F, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "kch_kda_decode_step": [_P, _L, _P, _P, _P] + [_I] * 5 + [_F] * 3 + [_I, _P],
+    "kch_kda_front_rows": [_P, _L, _P, _P, _F, _I, _P, _P, _P, _P, _P, _L, _P, _L, _I, _I, _I,
+                           _I, _P],
+    "kch_kda_decode_step_shift": [_P, _L, _P, _P, _P] + [_I] * 5 + [_F] * 3 + [_P, _P, _I, _I,
+                                                                               _P],
     "kch_csa_cache_append": [_P, _L] + [_P] * 11 + [_I] * 8 + [_P],
     "kch_hca_cache_append": [_P, _L] + [_P] * 6 + [_I] * 7 + [_P],
     "kch_csa_cache_append_rows": [_P, _L] + [_P] * 11 + [_I] * 7 + [_P, _L, _P, _L, _P, _L, _I, _I,

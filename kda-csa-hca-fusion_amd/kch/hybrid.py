@@ -1111,18 +1111,24 @@ class HybridDecoding(nn.Module):
             if kind == 'kda':
                 H, HV, K, V = cfg.n_heads_qk, cfg.n_heads_v, cfg.head_dim_k, cfg.head_dim_v
                 W, w_conv, b_conv, g_up = op
-                xc = torch.empty(B, d, device=dev, dtype=dt)
                 ln_w, ln_b = norm.weight, norm.bias
-                _lib.call("kch_kda_decode_front", _lib.ptr(x_cur), x_cur.stride(0), _lib.ptr(ln_w),
-                          _lib.ptr(ln_b), float(norm.eps), _lib.ptr(layer._conv_lookback),
-                          _lib.ptr(w_conv), _lib.ptr(b_conv), _lib.ptr(xc), B, d, code,
-                          _lib.dtype_code("HybridDecoding", ln_w.dtype), stream)
                 NP = _pad8(W.shape[0])
-                proj = linear(xc, d, W, torch.empty(B, NP, device=dev, dtype=dt), NP)
+                # the front (LayerNorm + conv over [lookback ; h]) in the
+                # projection's prologue; the step kernel then advances the
+                # lookback from h
+                h = torch.empty(B, d, device=dev, dtype=dt)
+                proj = torch.empty(B, NP, device=dev, dtype=dt)
+                _lib.call("kch_kda_front_rows", _lib.ptr(x_cur), x_cur.stride(0), _lib.ptr(ln_w),
+                          _lib.ptr(ln_b), float(norm.eps),
+                          _lib.dtype_code("HybridDecoding", ln_w.dtype),
+                          _lib.ptr(layer._conv_lookback), _lib.ptr(w_conv), _lib.ptr(b_conv),
+                          _lib.ptr(h), _lib.ptr(W), W.shape[1], _lib.ptr(proj), NP, B,
+                          W.shape[0], d, code, stream)
                 o = torch.empty(B, HV * V, device=dev, dtype=dt)
-                _lib.call("kch_kda_decode_step", _lib.ptr(proj), NP, _lib.ptr(g_up),
+                _lib.call("kch_kda_decode_step_shift", _lib.ptr(proj), NP, _lib.ptr(g_up),
                           _lib.ptr(stacked[kda_i]), _lib.ptr(o), B, H, HV, K, V,
-                          layer._scale_value(), float(cfg.kda_decay_scale), -10.0, code, stream)
+                          layer._scale_value(), float(cfg.kda_decay_scale), -10.0,
+                          _lib.ptr(layer._conv_lookback), _lib.ptr(h), d, code, stream)
                 kda_i += 1
             else:
                 csa = kind == 'csa'

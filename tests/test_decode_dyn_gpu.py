@@ -302,3 +302,61 @@ def _cache_state(cache):
     if hasattr(cache, "_K"):
         bufs += [cache._prev_buf, cache._K.rows[:, :nb], cache._K.inv[:, :nb]]
     return bufs
+
+
+def test_kda_front_rows_matches_separate_calls(dev):
+    """kch_kda_front_rows (LayerNorm + conv over [lookback ; h] in the input
+    projection's prologue) followed by kch_kda_decode_step_shift, against
+    kch_kda_decode_front + kch_linear_rows_fused + kch_kda_decode_step, over
+    several tokens: the lookback rows, the projection and the outputs agree to
+    the dtype's rounding (the LayerNorm statistics are summed in another order)."""
+    from kch import _lib
+    torch.manual_seed(7)
+    B, d, H, HV, K, V = 3, 2048, 4, 4, 128, 128
+    dt = torch.bfloat16
+    code = _lib.dtype_code("t", dt)
+    NW = 2 * H * K + HV * V + HV + K
+    NP = (NW + 7) // 8 * 8
+    W = (torch.randn(NW, d, device=dev) / d ** 0.5).to(dt)
+    ln_w = 1 + 0.1 * torch.randn(d, device=dev)
+    ln_b = 0.1 * torch.randn(d, device=dev)
+    conv_w = (0.5 * torch.randn(d, 3, device=dev)).to(dt)
+    conv_b = (0.1 * torch.randn(d, device=dev)).to(dt)
+    g_up = (torch.randn(HV * K, K, device=dev) / K ** 0.5).to(dt)
+    look = [(0.5 * torch.randn(B, 2, d, device=dev)).to(dt) for _ in range(2)]
+    look[1].copy_(look[0])
+    state = [0.02 * torch.randn(B, HV, K, V, device=dev) for _ in range(2)]
+    state[1].copy_(state[0])
+    st = _lib.stream_of(W)
+    for step in range(4):
+        x = torch.randn(B, d, device=dev).to(dt)
+        # separate launches
+        xc = torch.empty(B, d, device=dev, dtype=dt)
+        _lib.call("kch_kda_decode_front", _lib.ptr(x), d, _lib.ptr(ln_w), _lib.ptr(ln_b), 1e-5,
+                  _lib.ptr(look[0]), _lib.ptr(conv_w), _lib.ptr(conv_b), _lib.ptr(xc), B, d, code,
+                  0, st)
+        p0 = torch.empty(B, NP, device=dev, dtype=dt)
+        _lib.call("kch_linear_rows_fused", _lib.ptr(xc), d, _lib.ptr(W), d, _lib.ptr(p0), NP, B,
+                  NW, d, None, None, 0.0, 0, None, 0, None, code, st)
+        o0 = torch.empty(B, HV * V, device=dev, dtype=dt)
+        _lib.call("kch_kda_decode_step", _lib.ptr(p0), NP, _lib.ptr(g_up), _lib.ptr(state[0]),
+                  _lib.ptr(o0), B, H, HV, K, V, K ** -0.5, 0.5, -10.0, code, st)
+        # the front in the projection's prologue, the shift in the step
+        h = torch.empty(B, d, device=dev, dtype=dt)
+        p1 = torch.empty(B, NP, device=dev, dtype=dt)
+        _lib.call("kch_kda_front_rows", _lib.ptr(x), d, _lib.ptr(ln_w), _lib.ptr(ln_b), 1e-5, 0,
+                  _lib.ptr(look[1]), _lib.ptr(conv_w), _lib.ptr(conv_b), _lib.ptr(h), _lib.ptr(W),
+                  d, _lib.ptr(p1), NP, B, NW, d, code, st)
+        o1 = torch.empty(B, HV * V, device=dev, dtype=dt)
+        _lib.call("kch_kda_decode_step_shift", _lib.ptr(p1), NP, _lib.ptr(g_up),
+                  _lib.ptr(state[1]), _lib.ptr(o1), B, H, HV, K, V, K ** -0.5, 0.5, -10.0,
+                  _lib.ptr(look[1]), _lib.ptr(h), d, code, st)
+        torch.cuda.synchronize()
+        for name, a, b in (("lookback", look[0], look[1]), ("proj", p0[:, :NW], p1[:, :NW]),
+                           ("o", o0, o1), ("state", state[0], state[1])):
+            torch.testing.assert_close(b.float(), a.float(), rtol=2 ** -6, atol=1e-4,
+                                       msg=f"step {step}: {name}")
+        exact = (look[0] == look[1]).float().mean().item()
+        assert exact > 0.99, f"step {step}: only {exact:.4f} of the lookback bit-identical"
+        look[1].copy_(look[0])  # keep the two paths on the same history
+        state[1].copy_(state[0])
