@@ -304,7 +304,8 @@ def _cache_state(cache):
     return bufs
 
 
-def test_kda_front_rows_matches_separate_calls(dev):
+@pytest.mark.parametrize("d", [2048, 4096, 96])
+def test_kda_front_rows_matches_separate_calls(dev, d):
     """kch_kda_front_rows (LayerNorm + conv over [lookback ; h] in the input
     projection's prologue) followed by kch_kda_decode_step_shift, against
     kch_kda_decode_front + kch_linear_rows_fused + kch_kda_decode_step, over
@@ -312,7 +313,7 @@ def test_kda_front_rows_matches_separate_calls(dev):
     the dtype's rounding (the LayerNorm statistics are summed in another order)."""
     from kch import _lib
     torch.manual_seed(7)
-    B, d, H, HV, K, V = 3, 2048, 4, 4, 128, 128
+    B, H, HV, K, V = 3, 4, 4, 128, 128
     dt = torch.bfloat16
     code = _lib.dtype_code("t", dt)
     NW = 2 * H * K + HV * V + HV + K
