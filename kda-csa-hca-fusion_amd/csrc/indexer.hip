@@ -72,7 +72,9 @@ __device__ __forceinline__ int mbcnt64(unsigned long long m) {
 
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+  // (every lane's source lies in its own row for the patterns used here, so
+  // no old value is needed: bound_ctrl)
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, true));
 }
 
 // Sum over the NIH adjacent lanes (a query's heads) of a 16-lane row, with DPP
@@ -100,13 +102,14 @@ constexpr int RG = 8;
 __host__ __device__ inline bool indexer_lean(const IndexerParams& p) { return !p.sorted; }
 
 // LDS of a launch with CT column tiles (CT * 16 / nIh queries, 4 * CT waves):
-// logits and sink words, per-wave histograms when a row can exceed the
+// logits (rows of whole 16-block chunks) and 16-byte sink words per lane,
+// per-wave histograms when a row can exceed the
 // register selection (nb > 256 RG), per-wave selection buffers unless lean.
 __host__ __device__ inline size_t indexer_lds(int nb, int nIh, int topk, bool lean, int ct = 1) {
   int ptop = 1;
   while (ptop < topk) ptop <<= 1;
   const int nwv = 4 * ct;
-  size_t z = (size_t)(ct * 16 / nIh) * ((nb + 3) & ~3) * 4 + (size_t)nwv * 64 * 4;
+  size_t z = (size_t)(ct * 16 / nIh) * ((nb + 15) & ~15) * 4 + (size_t)nwv * 256 * 4;
   if (nb > 256 * RG) z += (size_t)nwv * 256 * 4;
   if (!lean) z += (size_t)nwv * ptop * 8;
   return z;
@@ -230,19 +233,21 @@ __global__ __launch_bounds__(256 * CT, CT == 2 ? 4 : 1) void indexer_kernel(Inde
   const int nb = p.nb;
   const int topk = p.topk;
 
-  const int ldl = (nb + 3) & ~3;  // logits row stride: rows start 16-byte aligned
+  // logits row stride: whole 16-block chunks, so that a chunk's four logits
+  // per lane are one aligned 16-byte store within the row
+  const int ldl = (nb + 15) & ~15;
   const size_t lg_bytes = (size_t)QPW * ldl * 4;
   int ptop = 1;
   while (ptop < topk) ptop <<= 1;
-  // LDS: logits [QPW][ldl] | sink words [NWV][64] | (nb > 256 RG) histograms
+  // LDS: logits [QPW][ldl] | sink words [NWV][64][4] | (nb > 256 RG) histograms
   // [NWV][256] | (unless lean) selections [NWV][ptop]. Lean: unsorted output,
   // whose indices go straight to global memory.
   const bool lean = indexer_lean(p);
   const size_t hist_bytes = nb > 256 * RG ? (size_t)NWV * 256 * 4 : 0;
   float* logits = reinterpret_cast<float*>(smem);
-  float* sink = reinterpret_cast<float*>(smem + lg_bytes) + 64 * wave;
-  uint32_t* hist = reinterpret_cast<uint32_t*>(smem + lg_bytes + NWV * 64 * 4) + 256 * wave;
-  u64* sel = reinterpret_cast<u64*>(smem + lg_bytes + NWV * 64 * 4 + hist_bytes) + (size_t)ptop * wave;
+  float* sink = reinterpret_cast<float*>(smem + lg_bytes) + 256 * wave + 4 * (threadIdx.x & 63);
+  uint32_t* hist = reinterpret_cast<uint32_t*>(smem + lg_bytes + NWV * 256 * 4) + 256 * wave;
+  u64* sel = reinterpret_cast<u64*>(smem + lg_bytes + NWV * 256 * 4 + hist_bytes) + (size_t)ptop * wave;
 
   auto nvis_of = [&](int t) {
     if (p.dense_visible) return nb;
@@ -384,17 +389,23 @@ __global__ __launch_bounds__(256 * CT, CT == 2 ? 4 : 1) void indexer_kernel(Inde
         for (int s = 0; s < NS; ++s)
           acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf.hi[s], qhi[ct][s], acc, 0, 0, 0);
       }
-      // acc[e]: block 16c + 4*q4 + e, column n. No branch in here: the lanes
-      // whose value is not kept write their own word of this wave's sink
-      // words, since a branch costs the overlap of the chunks loaded ahead.
+      // acc[e]: block 16c + 4*q4 + e, column n. The head-0 lane of a query
+      // writes its four logits as one 16-byte store into the query's row
+      // (whole chunks fit the padded row; blocks past the query's visible
+      // count hold finite values that its selection never reads); the other
+      // lanes, and every lane of a chunk past the last (uniform), write this
+      // lane's sink words. No branch: one would cost the overlap of the
+      // chunks loaded ahead.
+      f32x4 v;
+      if (fold) {  // (uniform) the scale is in the head weight
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float v = head_sum<NIH>(fmaxf(acc[e] * ascale, 0.f) * wqs[ct]);
-        const int blk = 16 * c + 4 * q4 + e;
-        float* dst = (hh == 0 && qok[ct] && blk < nv_me[ct]) ? logits + jq[ct] * ldl + blk
-                                                             : sink + lane;
-        *dst = v;
+        for (int e = 0; e < 4; ++e) v[e] = head_sum<NIH>(fmaxf(acc[e], 0.f) * wqs[ct]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = head_sum<NIH>(fmaxf(acc[e] * ascale, 0.f) * wqs[ct]);
       }
+      float* dst = (hh == 0 && c < nch) ? logits + jq[ct] * ldl + 16 * c + 4 * q4 : sink;
+      *reinterpret_cast<f32x4*>(dst) = v;
     }
   };
   KFrag kf[D];
