@@ -418,8 +418,9 @@ struct MqaWave {
   __device__ __forceinline__ static int slot_sl(int i) {
     return TPR == 16 ? i : i + 4 * ((lane_id() >> 3) & 1);
   }
+  // full: every row of the step is valid (ok is not read).
   __device__ __forceinline__ void chunk_sl(const Rows& rr, const bool (&ok)[8], bf16_t* stage,
-                                           const TileOffsets<HD>& to) {
+                                           const TileOffsets<HD>& to, bool full = false) {
     const int l = lane_id(), q = l >> 4, c = l % TPR;
     wave_lds_sync();  // the previous step's reads of the stage are done before the overwrite
 #pragma unroll
@@ -439,8 +440,10 @@ struct MqaWave {
       sb = scores(kf);
     }
     float sc[8] = {sa[0], sa[1], sa[2], sa[3], sb[0], sb[1], sb[2], sb[3]};
+    if (!full) {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) sc[k] = ok[k] ? sc[k] : -INFINITY;
+      for (int k = 0; k < 8; ++k) sc[k] = ok[k] ? sc[k] : -INFINITY;
+    }
     accumulate32(sc, stage, to);
   }
 

@@ -415,8 +415,9 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(AttnParams p) {
       }
     };
     // the row loads of step st from its indices; ok[k]: slot k is a row of
-    // this query. Returns whether any row of the step is (uniform).
-    auto load_rows = [&](int st, const Sel& sl, typename W::Rows& rr, bool (&ok)[8]) {
+    // this query. Returns (uniform) 0 when no row of the step is, 2 when every
+    // row is (ok then unset), else 1.
+    auto load_rows = [&](int st, const Sel& sl, typename W::Rows& rr, bool (&ok)[8]) -> int {
       const int j0 = 32 * st;
       const int ms = __builtin_amdgcn_readfirstlane(j0 < nm_pad ? 1 : 0);
       const __amdgpu_buffer_rsrc_t rs = ms ? rs_kv : rs_loc;
@@ -430,16 +431,27 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(AttnParams p) {
         const int v = W::TPR == 8 ? sl.v[i] ^ ((sl.v[i] ^ sl.v[(i + 4) & 7]) & hmask) : sl.v[i];
         rr.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(((unsigned)v * ROWB + lane_off) | past), 0, 0);
       }
+      // a step wholly inside the window rows is all valid; one wholly inside
+      // the selected slots needs only each slot's -1 / range test
+      if (!ms && j0 - nm_pad + 32 <= n_win) return 2;
       bool any = false;
+      if (ms && j0 + 32 <= nm) {
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const int j = j0 + W::row_sl(k, q4);
-        const bool okm = (j < nm) & ((unsigned)sl.v[k] < (unsigned)p.nb);
-        const bool okw = j - nm_pad < n_win;
-        ok[k] = ms ? okm : okw;
-        any |= ok[k];
+        for (int k = 0; k < 8; ++k) {
+          ok[k] = (unsigned)sl.v[k] < (unsigned)p.nb;
+          any |= ok[k];
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const int j = j0 + W::row_sl(k, q4);
+          const bool okm = (j < nm) & ((unsigned)sl.v[k] < (unsigned)p.nb);
+          const bool okw = j - nm_pad < n_win;
+          ok[k] = ms ? okm : okw;
+          any |= ok[k];
+        }
       }
-      return __ballot(any) != 0ull;
+      return __ballot(any) != 0ull ? 1 : 0;
     };
     // two steps of rows in flight and the indices of the two after them
     // (named registers: an indexed array of them ends up in scratch memory)
@@ -451,15 +463,15 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(AttnParams p) {
     bool ok0[8], ok1[8];
     load_sel(0, s0);
     load_sel(1, s1);
-    bool any0 = load_rows(0, s0, fr0, ok0);
-    bool any1 = load_rows(1, s1, fr1, ok1);
+    int any0 = load_rows(0, s0, fr0, ok0);
+    int any1 = load_rows(1, s1, fr1, ok1);
     load_sel(2, s0);
     load_sel(3, s1);
     for (int g = 0; g < ng; ++g) {
-      if (any0) w.chunk_sl(fr0, ok0, stage, to);
+      if (any0) w.chunk_sl(fr0, ok0, stage, to, any0 == 2);
       any0 = load_rows(2 * g + 2, s0, fr0, ok0);
       load_sel(2 * g + 4, s0);
-      if (any1) w.chunk_sl(fr1, ok1, stage, to);
+      if (any1) w.chunk_sl(fr1, ok1, stage, to, any1 == 2);
       any1 = load_rows(2 * g + 3, s1, fr1, ok1);
       load_sel(2 * g + 5, s1);
     }
