@@ -1173,8 +1173,9 @@ __global__ __launch_bounds__(256, DENSE ? 3 : 2) void attn_kernel(DecodeAttnPara
     }
   };
   // the loads of step m; ok[k]: slot k is a row of this group. Returns
-  // whether any row of the step is (uniform).
-  auto load_rows = [&](int m, const Sel& sl, typename W::Rows& rr, bool (&ok)[8]) {
+  // (uniform) 0 when no row of the step is, 2 when every row is (ok then
+  // unset), else 1.
+  auto load_rows = [&](int m, const Sel& sl, typename W::Rows& rr, bool (&ok)[8]) -> int {
     const int j0 = row_j(m);
     const int ms = __builtin_amdgcn_readfirstlane(j0 < na_pad ? 1 : 0);
     const __amdgpu_buffer_rsrc_t rs = ms ? rs_kv : rs_ring;
@@ -1188,6 +1189,10 @@ __global__ __launch_bounds__(256, DENSE ? 3 : 2) void attn_kernel(DecodeAttnPara
       rr.v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(((unsigned)v * ROWB + lane_off) | past),
                                                       0, 2 /* nontemporal */);
     }
+    // a step wholly inside the group and its ring rows, or (dense) wholly
+    // inside the cached blocks, is all valid
+    if (j0 + 32 <= jg1 && (ms ? (DENSE && j0 + 32 <= min(na, nb)) : j0 - na_pad + 32 <= ring_len))
+      return 2;
     bool any = false;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
@@ -1197,7 +1202,7 @@ __global__ __launch_bounds__(256, DENSE ? 3 : 2) void attn_kernel(DecodeAttnPara
       ok[k] = (j < jg1) & (ms ? okb : okr);
       any |= ok[k];
     }
-    return __ballot(any) != 0ull;
+    return __ballot(any) != 0ull ? 1 : 0;
   };
   const TileOffsets<HD> to;
   const int nsg = (jg1 - jg0 + 31) / 32;                   // steps in the group
@@ -1210,7 +1215,7 @@ __global__ __launch_bounds__(256, DENSE ? 3 : 2) void attn_kernel(DecodeAttnPara
   Sel s0, s1;
   typename W::Rows fr0, fr1;
   bool ok0[8], ok1[8];
-  bool any0, any1;
+  int any0, any1;
   if constexpr (DENSE) {
     load_sel(0, s0);
     any0 = load_rows(0, s0, fr0, ok0);
@@ -1248,17 +1253,17 @@ __global__ __launch_bounds__(256, DENSE ? 3 : 2) void attn_kernel(DecodeAttnPara
   }
   for (int m0 = 0; m0 < mine; m0 += 2) {
     if constexpr (DENSE) {
-      if (any0) w.chunk_sl(fr0, ok0, stage, to);
+      if (any0) w.chunk_sl(fr0, ok0, stage, to, any0 == 2);
       load_sel(m0 + 2, s0);
       any0 = load_rows(m0 + 2, s0, fr0, ok0);
-      if (any1) w.chunk_sl(fr1, ok1, stage, to);
+      if (any1) w.chunk_sl(fr1, ok1, stage, to, any1 == 2);
       load_sel(m0 + 3, s0);
       any1 = load_rows(m0 + 3, s0, fr1, ok1);
     } else {
-      if (any0) w.chunk_sl(fr0, ok0, stage, to);
+      if (any0) w.chunk_sl(fr0, ok0, stage, to, any0 == 2);
       any0 = load_rows(m0 + 2, s0, fr0, ok0);
       load_sel(m0 + 4, s0);
-      if (any1) w.chunk_sl(fr1, ok1, stage, to);
+      if (any1) w.chunk_sl(fr1, ok1, stage, to, any1 == 2);
       any1 = load_rows(m0 + 3, s1, fr1, ok1);
       load_sel(m0 + 5, s1);
     }
