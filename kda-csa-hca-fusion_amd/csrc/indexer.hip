@@ -142,6 +142,9 @@ __device__ __forceinline__ void select_in_registers(const float* lg, int nv, int
     key[4 * g + 2] = b0 + 2 < nv ? order_key(v.z) : 0u;
     key[4 * g + 3] = b0 + 3 < nv ? order_key(v.w) : 0u;
   }
+  // groups of 256 blocks that hold a visible block (wave-uniform): the counts
+  // and the output pass skip the groups past them, whose keys are all 0
+  const int ng = (nv + 255) >> 8;
   uint32_t K = 0u;  // with nv <= topk every block is taken: keys > 0
   int need = 0;
   if (nv > topk) {
@@ -165,7 +168,13 @@ __device__ __forceinline__ void select_in_registers(const float* lg, int nv, int
       const uint32_t cand = K | (1u << bit);
       int c = 0;
 #pragma unroll
-      for (int r = 0; r < 4 * RG; ++r) c += __popcll(__builtin_amdgcn_ballot_w64(key[r] >= cand));
+      for (int g = 0; g < RG; ++g) {
+        if (g < ng) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            c += __popcll(__builtin_amdgcn_ballot_w64(key[4 * g + e] >= cand));
+        }
+      }
       if (c == topk) {
         // exactly topk keys are >= cand: taking every key above cand - 1
         // (none equal to it is needed) selects them
@@ -176,12 +185,18 @@ __device__ __forceinline__ void select_in_registers(const float* lg, int nv, int
     }
     int gt = 0;
 #pragma unroll
-    for (int r = 0; r < 4 * RG; ++r) gt += __popcll(__builtin_amdgcn_ballot_w64(key[r] > K));
+    for (int g = 0; g < RG; ++g) {
+      if (g < ng) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) gt += __popcll(__builtin_amdgcn_ballot_w64(key[4 * g + e] > K));
+      }
+    }
     need = topk - gt;  // keys equal to K still to take, lowest block index first
   }
   int base_out = 0, base_eq = 0;
 #pragma unroll
   for (int g = 0; g < RG; ++g) {
+    if (g >= ng) break;
     int neq = 0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) neq += (key[4 * g + e] == K && key[4 * g + e]) ? 1 : 0;
