@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define KCH_ABI_VERSION 18
+#define KCH_ABI_VERSION 19
 
 #define KCH_OK 0
 #define KCH_ERR_INVALID 1     /* bad pointer / shape / argument */
@@ -298,7 +298,13 @@ int kch_layer_norm_bwd(const void* x, const void* w, const void* dy, void* dx, f
  *            row's high, middle then low parts of its fp32 value
  *            (x = hi + mid + lo, the operands of kch_csa_indexer_topk with
  *            key_split = 1), or (3, normalize only) [B,T/m,2,c] fp16, the
- *            high then low parts of 256 x (key_split = 2); or NULL
+ *            high then low parts of 256 x (key_split = 2), or (4, normalize
+ *            only, c a multiple of 32) those parts chunk-major
+ *            (key_split = 3): per batch row ceil(T/m/16) chunks of 16 rows,
+ *            each 2c/32 pieces of 64 lanes x 8 fp16, where channel ch of row r,
+ *            part p (0 high, 1 low) is piece p c/32 + ch/32, lane r % 16 +
+ *            16 ((ch % 32) / 8), element ch % 8 (the last chunk's rows past
+ *            T/m are not written); or NULL
  *   local    [B,T,c] bf16 per-token window keys L2norm(C) (raw C when not
  *            `normalize`), or NULL
  * T must be a multiple of m (callers right-pad as ops_csa.py:772-777 does).
@@ -326,8 +332,10 @@ int kch_compress_overlapped(const void* Ca, long long ldCa, const void* Cb, long
  *   q_idx [B,T,nIh,cI] (dtype), k_idx [B,nb,cI] fp32, or with key_split = 1
  *   [B,nb,3,cI] bf16 high / middle / low parts of each row (kch_compress
  *   key_f32 = 2), or with key_split = 2 (normalize_q only) [B,nb,2,cI] fp16
- *   high / low parts of 256 x (key_f32 = 3); the logits carry fp32-level
- *   error (three-part bf16 or two-part fp16 products);
+ *   high / low parts of 256 x (key_f32 = 3), or with key_split = 3
+ *   (normalize_q only) those parts chunk-major (key_f32 = 4: each of the
+ *   indexer's loads reads 1 KB of contiguous memory); the logits carry
+ *   fp32-level error (three-part bf16 or two-part fp16 products);
  *   already L2-normalised when normalize_q. w_idx [B,T,nIh] (dtype) or NULL
  *   (= all ones)
  *   idx_out [B,T,topk] int64 (idx64) or int32: the top-k blocks by descending

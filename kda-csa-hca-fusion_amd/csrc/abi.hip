@@ -605,6 +605,17 @@ int kch_layer_norm_bwd(const void* x, const void* w, const void* dy, void* dx, f
   return hip_status(fn, kch::layer_norm_bwd_dispatch(p, dtype, wdtype, (hipStream_t)stream));
 }
 
+// key row formats of kch_compress: 0 bf16, 1 fp32, 2 bf16 three-part, 3 fp16
+// two-part (normalised rows), 4 the parts of 3 chunk-major (c a multiple of 32)
+static int check_key_format(const char* fn, int key_f32, int normalize, int c) {
+  if (key_f32 < 0 || key_f32 > 4) return fail(KCH_ERR_INVALID, "%s: key format %d", fn, key_f32);
+  if (key_f32 >= 3 && !normalize)
+    return fail(KCH_ERR_INVALID, "%s: fp16 split keys (key_f32=%d) need normalize", fn, key_f32);
+  if (key_f32 == 4 && c % 32)
+    return fail(KCH_ERR_UNSUPPORTED, "%s: chunk-major keys need c %% 32 == 0 (c=%d)", fn, c);
+  return KCH_OK;
+}
+
 int kch_compress(const void* C, long long ldC, const void* Z, long long ldZ, const float* B_pos,
                  float* out_raw, void* out_key, int key_f32, int normalize, void* local, int B,
                  int T, int m, int c, int dtype, void* stream) {
@@ -614,9 +625,7 @@ int kch_compress(const void* C, long long ldC, const void* Z, long long ldZ, con
   if (B < 0 || T < 0 || c < 1) return fail(KCH_ERR_INVALID, "%s: bad sizes B=%d T=%d c=%d", fn, B, T, c);
   if (T % m) return fail(KCH_ERR_INVALID, "%s: T=%d must be divisible by m=%d", fn, T, m);
   if (c > 128) return fail(KCH_ERR_UNSUPPORTED, "%s: c=%d > 128 not supported", fn, c);
-  if (key_f32 < 0 || key_f32 > 3) return fail(KCH_ERR_INVALID, "%s: key format %d", fn, key_f32);
-  if (key_f32 == 3 && !normalize)
-    return fail(KCH_ERR_INVALID, "%s: fp16 split keys (key_f32=3) need normalize", fn);
+  if (int rc = check_key_format(fn, key_f32, normalize, c)) return rc;
   if (B * T == 0) return KCH_OK;
   if (!C || !Z || !B_pos) return fail(KCH_ERR_INVALID, "%s: null input pointer", fn);
   if (ldC < c || ldZ < c) return fail(KCH_ERR_INVALID, "%s: row strides must be >= c", fn);
@@ -636,6 +645,7 @@ int kch_compress_overlapped(const void* Ca, long long ldCa, const void* Cb, long
   if (B < 0 || T < 0 || c < 1) return fail(KCH_ERR_INVALID, "%s: bad sizes B=%d T=%d c=%d", fn, B, T, c);
   if (T % m) return fail(KCH_ERR_INVALID, "%s: T=%d must be divisible by m=%d", fn, T, m);
   if (c > 128) return fail(KCH_ERR_UNSUPPORTED, "%s: c=%d > 128 not supported", fn, c);
+  if (int rc = check_key_format(fn, key_f32, normalize, c)) return rc;
   if (B * T == 0) return KCH_OK;
   if (!Ca || !Cb || !Za || !Zb || !Ba || !Bb) return fail(KCH_ERR_INVALID, "%s: null input pointer", fn);
   if (ldCa < c || ldCb < c || ldZa < c || ldZb < c)
@@ -658,9 +668,9 @@ int kch_csa_indexer_topk(const void* q_idx, const void* k_idx, const void* w_idx
     return fail(KCH_ERR_UNSUPPORTED, "%s: nIh=%d not in {1,2,4,8,16}", fn, nIh);
   if (cI != 32 && cI != 64 && cI != 128)
     return fail(KCH_ERR_UNSUPPORTED, "%s: cI=%d not in {32,64,128}", fn, cI);
-  if (key_split < 0 || key_split > 2) return fail(KCH_ERR_INVALID, "%s: key_split=%d", fn, key_split);
-  if (key_split == 2 && !normalize_q)
-    return fail(KCH_ERR_INVALID, "%s: fp16 split keys (key_split=2) need normalize_q", fn);
+  if (key_split < 0 || key_split > 3) return fail(KCH_ERR_INVALID, "%s: key_split=%d", fn, key_split);
+  if (key_split >= 2 && !normalize_q)
+    return fail(KCH_ERR_INVALID, "%s: fp16 split keys (key_split=%d) need normalize_q", fn, key_split);
   if (B * T == 0 || topk == 0) return KCH_OK;
   if (!q_idx || !idx_out || (nb > 0 && !k_idx)) return fail(KCH_ERR_INVALID, "%s: null pointer", fn);
   const long long lds = (long long)kch::indexer_lds_bytes(nb, nIh, topk);

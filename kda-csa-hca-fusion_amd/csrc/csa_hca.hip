@@ -27,7 +27,20 @@ namespace kch {
 // three bf16 parts x = hi + mid + lo of the fp32 value (2), stored as three
 // part rows [hi(c) | mid(c) | lo(c)], or (3, L2-normalised rows only) the two
 // fp16 parts of 256 x, [hi(c) | lo(c)] -- the splits the indexer's MFMA
-// products use.
+// products use. Format 4 holds the parts of format 3 chunk-major: the rows of
+// each 16-row chunk (the last one padded) in the order the indexer's lanes
+// load them, so that each of its loads reads 1 KB of contiguous memory:
+// piece j = part * c / 32 + ch / 32 of the chunk is 64 lanes of 8 channels,
+// lane (row % 16) + 16 * ((ch % 32) / 8), element ch % 8.
+__device__ __forceinline__ size_t chunked_key_offset(size_t orow, int nb, int c, int part, int ch) {
+  // batch row and block (B * nb < 2^31: the caller's row count)
+  const unsigned bi = (unsigned)orow / (unsigned)nb, r = (unsigned)orow - bi * (unsigned)nb;
+  const size_t chunk = (size_t)bi * (unsigned)((nb + 15) >> 4) + (r >> 4);
+  const int piece = part * (c >> 5) + (ch >> 5);
+  const int lane = (int)(r & 15) + 16 * ((ch & 31) >> 3);
+  return chunk * 32 * (size_t)c + (size_t)piece * 512 + (size_t)lane * 8 + (ch & 7);
+}
+
 __device__ __forceinline__ void store_key(const CompressParams& p, size_t orow, int c, int ch,
                                           float x) {
   if (p.key_f32 == 1) {
@@ -46,6 +59,13 @@ __device__ __forceinline__ void store_key(const CompressParams& p, size_t orow, 
     _Float16* row = static_cast<_Float16*>(p.out_key) + orow * 2 * c;
     row[ch] = hi;
     row[c + ch] = (_Float16)(xs - (float)hi);
+  } else if (p.key_f32 == 4) {
+    const float xs = x * kSplit16Scale;
+    const _Float16 hi = (_Float16)xs;
+    const int nb = p.T / p.m;
+    _Float16* base = static_cast<_Float16*>(p.out_key);
+    base[chunked_key_offset(orow, nb, c, 0, ch)] = hi;
+    base[chunked_key_offset(orow, nb, c, 1, ch)] = (_Float16)(xs - (float)hi);
   } else {
     static_cast<bf16_t*>(p.out_key)[orow * c + ch] = (bf16_t)x;
   }

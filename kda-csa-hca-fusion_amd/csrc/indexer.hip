@@ -21,7 +21,12 @@
 //   KM 1: rows of the three bf16 parts [hi | mid | lo], the same products;
 //   KM 2: L2-normalised rows as the two fp16 parts of 256 x [hi | lo] (q split
 //         the same way; hi*hi + hi*lo + lo*hi is 2^16 times the dot product to
-//         about 2^-22 relative): three MFMAs per step instead of six.
+//         about 2^-22 relative): three MFMAs per step instead of six; with
+//         k_split 3 the same parts chunk-major (16-row chunks in the lanes'
+//         load order), so that each load instruction reads 1 KB of contiguous
+//         memory in whole cache lines instead of 64 bytes of each of 16 rows
+//         (half of every line it touches, each line fetched twice): the logits
+//         of configs[2] take half the time.
 // Per query, the logits sit
 // in LDS as 32-bit order keys. A row of up to 256 * RG visible blocks is
 // selected by one wave in registers (the k-th largest key found bit by bit
@@ -329,7 +334,10 @@ __global__ __launch_bounds__(256 * CT, CT == 2 ? 4 : 1) void indexer_kernel(Inde
   const int nch = (nv_max + 15) / 16;
   const int mine = nch > wave ? (nch - wave + NWV - 1) / NWV : 0;
   // batch stride: k_bstride (4-byte units, fp32 rows only) or nb whole rows
-  const long long kbs = (KM == 0 && p.k_bstride) ? p.k_bstride * 4 : (long long)nb * ROW_BYTES;
+  const bool chunked = KM == 2 && p.k_split == 3;
+  const long long kbs = (KM == 0 && p.k_bstride) ? p.k_bstride * 4
+                        : chunked                ? (long long)((nb + 15) & ~15) * ROW_BYTES
+                                                 : (long long)nb * ROW_BYTES;
   const char* kbase = reinterpret_cast<const char*>(p.k_idx) + (size_t)b * kbs;
   struct KFrag3 {
     bf16x8 hi[NS], mid[NS], lo[NS];
@@ -342,6 +350,18 @@ __global__ __launch_bounds__(256 * CT, CT == 2 ? 4 : 1) void indexer_kernel(Inde
     const int r = min(16 * c + n, nb - 1);
     const char* krow = kbase + (size_t)r * ROW_BYTES;
     if constexpr (KM == 2) {
+      if (chunked) {
+        // chunk c (past the last: the last, masked) as 2 NS pieces of 1 KB
+        const int cc = min(c, (nb - 1) >> 4);
+        const _Float16* kc =
+            reinterpret_cast<const _Float16*>(kbase + (size_t)cc * 16 * ROW_BYTES) + 8 * lane;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          kf.hi[s] = *reinterpret_cast<const f16x8*>(kc + 512 * s);
+          kf.lo[s] = *reinterpret_cast<const f16x8*>(kc + 512 * (NS + s));
+        }
+        return;
+      }
       const _Float16* kh = reinterpret_cast<const _Float16*>(krow);
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
@@ -625,7 +645,7 @@ size_t indexer_lds_bytes(int nb, int nIh, int topk) { return indexer_lds(nb, nIh
 static int indexer_ct(const IndexerParams& p) {
   // (fp16-split keys of up to 64 channels: other row formats and widths need
   // more registers for a second tile than four waves per SIMD leave)
-  return p.k_split == 2 && p.cI <= 64 && p.T >= 16 &&
+  return p.k_split >= 2 && p.cI <= 64 && p.T >= 16 &&
                  indexer_lds(p.nb, p.nIh, p.topk, indexer_lean(p), 2) <= 80 * 1024
              ? 2
              : 1;
@@ -646,7 +666,7 @@ hipError_t indexer_dispatch(const IndexerParams& p, int dtype, hipStream_t s) {
   } while (0)
 #define KCH_IDX_NIH(QT, CI, NIH)                   \
   do {                                             \
-    if (p.k_split == 2) KCH_IDX_T(QT, CI, NIH, 2); \
+    if (p.k_split >= 2) KCH_IDX_T(QT, CI, NIH, 2); \
     else if (p.k_split) KCH_IDX_T(QT, CI, NIH, 1); \
     else KCH_IDX_T(QT, CI, NIH, 0);                \
   } while (0)

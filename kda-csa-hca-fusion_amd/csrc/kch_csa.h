@@ -14,7 +14,9 @@ struct CompressParams {
   long long ldCa, ldZa, ldCb, ldZb;
   const float* Ba; const float* Bb;
   float* out_raw;   // [B, nb, c] fp32 or null
-  void* out_key;    // [B, nb, c] bf16 (key_f32 0) / fp32 (1), [B, nb, 2, c] split bf16 (2), or null
+  void* out_key;    // [B, nb, c] bf16 (key_f32 0) / fp32 (1), [B, nb, 3, c] split bf16 (2),
+                    // [B, nb, 2, c] split fp16 (3), the same chunk-major in whole 16-row
+                    // chunks (4), or null
   bf16_t* local;    // [B, T, c] bf16 window keys (from Ca) or null
   int B, T, m, c;
   int overlap, normalize, key_f32;
@@ -44,7 +46,9 @@ struct IndexerParams {
   const void* q_idx;     // [B, T, nIh, cI]
   const void* k_idx;     // [B, nb, cI] fp32, or (k_split 1) [B, nb, 3, cI] bf16 high / middle /
                          // low parts of each row, or (k_split 2, L2-normalised rows and
-                         // normalize_q) [B, nb, 2, cI] fp16 high / low parts of 256 x;
+                         // normalize_q) [B, nb, 2, cI] fp16 high / low parts of 256 x, or
+                         // (k_split 3) the same parts chunk-major, [B, ceil(nb / 16)] chunks
+                         // of 16 rows in the lanes' load order (compression key format 4);
                          // already L2-normalised when normalize
   const void* w_idx;     // [B, T, nIh] or null (= ones)
   void* idx_out;         // [B, T, topk] int32 or int64
@@ -55,7 +59,8 @@ struct IndexerParams {
   int sorted;            // 1: indices by descending logit; 0: the same set in ascending index
   float scale;
   long long k_bstride;   // 4-byte units between batches of fp32 k_idx (0: nb * cI; split rows: nb rows)
-  int k_split;           // 0: fp32 rows; 1: bf16 three-part rows; 2: fp16 two-part rows
+  int k_split;           // 0: fp32 rows; 1: bf16 three-part rows; 2: fp16 two-part rows;
+                         // 3: fp16 two-part chunks
 };
 hipError_t indexer_dispatch(const IndexerParams& p, int dtype, hipStream_t s);
 size_t indexer_lds_bytes(int nb, int nIh, int topk);  // dynamic LDS of the indexer kernel

@@ -200,7 +200,8 @@ def _compress(fn, C, Z, B_pos, m, *, out_raw=True, key=None, normalize=False, lo
               key_split=0):
     """``key_split``: 0 keys as ``key``'s dtype (bf16 / fp32); 1 bf16 three-part
     rows ``[B,nb,3c]``; 2 fp16 two-part rows of 256 x ``[B,nb,2c]`` (normalize
-    only): the indexer's operands."""
+    only); 3 the parts of 2 chunk-major, ``[B, ceil(nb/16)*16, 2c]`` (normalize
+    only, c a multiple of 32): the indexer's operands."""
     B_, T, c = C.shape
     if m < 1:
         raise ValueError(f"compression factor m={m} must be >= 1")
@@ -215,7 +216,7 @@ def _compress(fn, C, Z, B_pos, m, *, out_raw=True, key=None, normalize=False, lo
     Z, ldz = _rows(Z)
     bpos = _f32_cached(B_pos, C.device)
     raw = torch.empty(B_, nb, c, device=C.device, dtype=torch.float32) if out_raw else None
-    key_f32 = {1: 2, 2: 3}.get(int(key_split),
+    key_f32 = {1: 2, 2: 3, 3: 4}.get(int(key_split),
                                1 if (key is not None and key.dtype == torch.float32) else 0)
     _lib.call("kch_compress", _lib.ptr(C), ldc, _lib.ptr(Z), ldz, _lib.ptr(bpos), _lib.ptr(raw),
               _lib.ptr(key), key_f32, int(normalize), _lib.ptr(local), B_, T, m, c,
@@ -289,9 +290,10 @@ def _standard_block_mask_m(mask, T, n_blocks):
 
 
 def _indexer(fn, q_idx, k_norm, w_idx, topk, scale, m, *, dense, pos0=0, normalize_q,
-             idx64=True, want_logits=False, sorted_=True, key_split=0):
+             idx64=True, want_logits=False, sorted_=True, key_split=0, nb=None):
     B_, T, HI, DI = q_idx.shape
-    nb = k_norm.shape[1]
+    if nb is None:
+        nb = k_norm.shape[1]
     q_idx = _aligned(q_idx)
     if w_idx is not None:
         w_idx = w_idx.to(q_idx.dtype).contiguous()
@@ -473,10 +475,15 @@ def _csa_core(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, *, m
     _compress_overlapped(fn, Ca, Cb, Za, Zb, Ba, Bb, m, out_raw=False, key=kv,
                          normalize=normalize_qk, local=local)
     # indexer keys as the indexer's split MFMA operands: unit rows as the fp16
-    # high and low parts of 256 x, raw rows as bf16 high, middle and low parts
-    ksplit = 2 if normalize_qk else 1
-    k_norm = torch.empty(B_, n_blocks, (4 - ksplit) * c_I, device=device,
-                         dtype=torch.float16 if ksplit == 2 else torch.bfloat16)
+    # high and low parts of 256 x, chunk-major (whole 16-row chunks in the
+    # indexer's load order), raw rows as bf16 high, middle and low parts
+    if normalize_qk:
+        ksplit = 3
+        k_norm = torch.empty(B_, (n_blocks + 15) // 16 * 16, 2 * c_I, device=device,
+                             dtype=torch.float16)
+    else:
+        ksplit = 1
+        k_norm = torch.empty(B_, n_blocks, 3 * c_I, device=device, dtype=torch.bfloat16)
     _compress(fn, K_idx, Z_idx, B_idx, m, out_raw=False, key=k_norm, normalize=normalize_qk,
               key_split=ksplit)
     idx = None
@@ -484,7 +491,7 @@ def _csa_core(Ca, Cb, Za, Zb, K_idx, Z_idx, q, q_idx, w_idx, Ba, Bb, B_idx, *, m
         # the attention takes the selected set in any order: sort only for a caller
         idx, _ = _indexer(fn, q_idx, k_norm, w_idx, topk, idx_scale, m, dense=False,
                           normalize_q=normalize_qk, idx64=False, sorted_=bool(return_indices),
-                          key_split=ksplit)
+                          key_split=ksplit, nb=n_blocks)
         _log_selection(idx)
     sink = None if sink_logits is None else _f32_cached(sink_logits, device)
     out = torch.empty(B_, T, nh, c, device=device, dtype=q.dtype)

@@ -154,6 +154,51 @@ def test_compress_key_and_window_outputs(dev, m, c, overlap, dt, key_dt):
     assert np.abs(host(local) - lref).max() <= 8e-3
 
 
+@pytest.mark.parametrize("B,nb,cI,nIh,T_q,topk", [
+    (2, 37, 64, 4, 148, 16),     # nb not a multiple of 16 (padded last chunk), two-tile kernel
+    (1, 2048, 64, 4, 192, 512),  # configs[2]'s key count and top-k
+    (2, 40, 32, 2, 12, 8),       # one-tile kernel (T < 16), two pieces per chunk
+    (1, 50, 128, 8, 64, 24),     # 128 channels: eight pieces per chunk
+])
+def test_indexer_chunk_major_keys(dev, B, nb, cI, nIh, T_q, topk):
+    """Compression key format 4 holds format 3's fp16 parts chunk-major (checked
+    element by element against a host relayout of format 3), and the indexer
+    reading them (key_split 3) returns the same logits and indices, bit for
+    bit, as from the row-major parts (key_split 2)."""
+    from kch.ops_csa import _compress, _indexer
+    m = 4
+    T = nb * m
+    rng = np.random.default_rng(nb * 7 + cI)
+    C = bf16_dev(rng.standard_normal((B, T, cI)), dev)
+    Z = bf16_dev(rng.standard_normal((B, T, cI)), dev)
+    Bp = torch.from_numpy((0.5 * rng.standard_normal((m, cI))).astype(np.float32)).to(dev)
+    rows = torch.empty(B, nb, 2 * cI, device=dev, dtype=torch.float16)
+    npad = (nb + 15) // 16 * 16
+    chunked = torch.zeros(B, npad, 2 * cI, device=dev, dtype=torch.float16)
+    _compress("t", C, Z, Bp, m, out_raw=False, key=rows, normalize=True, key_split=2)
+    _compress("t", C, Z, Bp, m, out_raw=False, key=chunked, normalize=True, key_split=3)
+    torch.cuda.synchronize()
+    # host relayout: [B, chunk, n, part, s, q4, i] -> [B, chunk, part, s, q4, n, i]
+    r = torch.zeros(B, npad, 2 * cI, dtype=torch.float16)
+    r[:, :nb] = rows.cpu()
+    expect = (r.view(B, npad // 16, 16, 2, cI // 32, 4, 8).permute(0, 1, 3, 4, 5, 2, 6)
+              .reshape(B, npad, 2 * cI))
+    assert torch.equal(chunked.cpu().view(torch.int16), expect.view(torch.int16))
+
+    q = bf16_dev(rng.standard_normal((B, T_q, nIh, cI)), dev)
+    w = bf16_dev(rng.standard_normal((B, T_q, nIh)), dev)
+    pos0 = T - T_q  # the queries are the last T_q positions
+    for sorted_ in (True, False):  # unsorted: the lean two-tile launch where LDS allows
+        kw = dict(dense=False, pos0=pos0, normalize_q=True, idx64=False, want_logits=True,
+                  sorted_=sorted_, nb=nb)
+        i_row, l_row = _indexer("t", q, rows, w, topk, 1.0, m, key_split=2, **kw)
+        i_chk, l_chk = _indexer("t", q, chunked, w, topk, 1.0, m, key_split=3, **kw)
+        torch.cuda.synchronize()
+        assert torch.equal(i_row, i_chk), sorted_
+        assert torch.equal(l_row.view(torch.int32), l_chk.view(torch.int32)), sorted_
+        assert (i_row >= 0).any()
+
+
 @pytest.mark.parametrize("normalize", [True, False])
 @pytest.mark.parametrize("T,m,topk", [(128, 4, 8), (64, 4, 32), (200, 4, 16), (96, 8, 0)])
 def test_indexer_matches_oracle(dev, normalize, T, m, topk):
