@@ -166,27 +166,47 @@ __device__ __forceinline__ void select_in_registers(const float* lg, int nv, int
       a &= (uint32_t)__shfl_xor((int)a, d);
       o |= (uint32_t)__shfl_xor((int)o, d);
     }
+    // (uniform values, held in scalar registers: the search loop is scalar)
+    a = __builtin_amdgcn_readfirstlane(a);
+    o = __builtin_amdgcn_readfirstlane(o);
     const uint32_t diff = a ^ o;
     const int hb = diff ? 31 - __clz((int)diff) : -1;  // highest bit that differs
     K = hb >= 31 ? 0u : (a & (~0u << (hb + 1)));      // the common leading bits
-    for (int bit = hb; bit >= 0; --bit) {
-      const uint32_t cand = K | (1u << bit);
-      int c = 0;
+    // The bit search, compiled per count of groups holding visible blocks (no
+    // per-group branch in the loop); each group's four ballots are formed
+    // before they are counted, so that they take four scalar register pairs
+    // instead of queueing on one.
+    auto search = [&](auto ngc) {
+      constexpr int NG = decltype(ngc)::value;
+      for (int bit = hb; bit >= 0; --bit) {
+        const uint32_t cand = K | (1u << bit);
+        int c = 0;
 #pragma unroll
-      for (int g = 0; g < RG; ++g) {
-        if (g < ng) {
+        for (int g = 0; g < NG; ++g) {
+          u64 bl[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            c += __popcll(__builtin_amdgcn_ballot_w64(key[4 * g + e] >= cand));
+          for (int e = 0; e < 4; ++e) bl[e] = __builtin_amdgcn_ballot_w64(key[4 * g + e] >= cand);
+          c += (__popcll(bl[0]) + __popcll(bl[1])) + (__popcll(bl[2]) + __popcll(bl[3]));
         }
+        if (c == topk) {
+          // exactly topk keys are >= cand: taking every key above cand - 1
+          // (none equal to it is needed) selects them
+          K = cand - 1u;
+          break;
+        }
+        if (c > topk) K = cand;
       }
-      if (c == topk) {
-        // exactly topk keys are >= cand: taking every key above cand - 1
-        // (none equal to it is needed) selects them
-        K = cand - 1u;
-        break;
-      }
-      if (c > topk) K = cand;
+    };
+    static_assert(RG == 8, "one search per group count");
+    switch (ng) {
+      case 1: search(std::integral_constant<int, 1>{}); break;
+      case 2: search(std::integral_constant<int, 2>{}); break;
+      case 3: search(std::integral_constant<int, 3>{}); break;
+      case 4: search(std::integral_constant<int, 4>{}); break;
+      case 5: search(std::integral_constant<int, 5>{}); break;
+      case 6: search(std::integral_constant<int, 6>{}); break;
+      case 7: search(std::integral_constant<int, 7>{}); break;
+      default: search(std::integral_constant<int, 8>{}); break;
     }
     int gt = 0;
 #pragma unroll
