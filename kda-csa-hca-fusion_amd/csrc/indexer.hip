@@ -218,38 +218,53 @@ __device__ __forceinline__ void select_in_registers(const float* lg, int nv, int
     }
     need = topk - gt;  // keys equal to K still to take, lowest block index first
   }
-  int base_out = 0, base_eq = 0;
+  // The output pass in ascending block order; without keys equal to K still
+  // needed (the usual case: the search stopped at an exact split, or every
+  // visible block is taken) the equal-key ranks are not formed.
+  int base_out = 0;
+  auto emit = [&](auto tiesc) {
+    constexpr bool TIES = decltype(tiesc)::value;
+    int base_eq = 0;
 #pragma unroll
-  for (int g = 0; g < RG; ++g) {
-    if (g >= ng) break;
-    int neq = 0;
+    for (int g = 0; g < RG; ++g) {
+      if (g >= ng) break;
+      int eq_incl = 0, eq_rank = 0;
+      if constexpr (TIES) {
+        int neq = 0;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) neq += (key[4 * g + e] == K && key[4 * g + e]) ? 1 : 0;
-    const int eq_incl = wave_incl_scan(neq);
-    int eq_rank = base_eq + eq_incl - neq;
-    bool take[4];
-    int ntake = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t k = key[4 * g + e];
-      const bool eq = k == K && k;
-      take[e] = k > K || (eq && eq_rank < need);
-      eq_rank += eq ? 1 : 0;
-      ntake += take[e] ? 1 : 0;
-    }
-    const int out_incl = wave_incl_scan(ntake);
-    int at = base_out + out_incl - ntake;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      if (take[e]) {
-        if (sel) sel[at] = kv64(key[4 * g + e], 256 * g + 4 * lane + e);
-        else out[at] = (IdxT)(256 * g + 4 * lane + e);
-        ++at;
+        for (int e = 0; e < 4; ++e) neq += (key[4 * g + e] == K && key[4 * g + e]) ? 1 : 0;
+        eq_incl = wave_incl_scan(neq);
+        eq_rank = base_eq + eq_incl - neq;
       }
+      bool take[4];
+      int ntake = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t k = key[4 * g + e];
+        take[e] = k > K;
+        if constexpr (TIES) {
+          const bool eq = k == K && k;
+          take[e] = take[e] || (eq && eq_rank < need);
+          eq_rank += eq ? 1 : 0;
+        }
+        ntake += take[e] ? 1 : 0;
+      }
+      const int out_incl = wave_incl_scan(ntake);
+      int at = base_out + out_incl - ntake;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        if (take[e]) {
+          if (sel) sel[at] = kv64(key[4 * g + e], 256 * g + 4 * lane + e);
+          else out[at] = (IdxT)(256 * g + 4 * lane + e);
+          ++at;
+        }
+      }
+      base_out += __builtin_amdgcn_readlane(out_incl, 63);
+      if constexpr (TIES) base_eq += __builtin_amdgcn_readlane(eq_incl, 63);
     }
-    base_out += __builtin_amdgcn_readlane(out_incl, 63);
-    base_eq += __builtin_amdgcn_readlane(eq_incl, 63);
-  }
+  };
+  if (need > 0) emit(std::true_type{});
+  else emit(std::false_type{});
   if (!sel)
     for (int i = base_out + lane; i < topk; i += 64) out[i] = (IdxT)-1;
 }
