@@ -336,10 +336,15 @@ hipError_t compress_dispatch(const CompressParams& p, int dtype, hipStream_t str
 // Joint-softmax MQA prefill. Key tables are bf16 rows of head dim HD.
 // ---------------------------------------------------------------------------
 
-template <int HD, typename QT, typename OT, bool SPARSE>
+// Selected indices a wave keeps in LDS (IDXL): the whole top-k of its query.
+constexpr int kIdxLds = 512;
+
+template <int HD, typename QT, typename OT, bool SPARSE, bool IDXL = false>
 __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(AttnParams p) {
   using W = MqaWave<HD>;
+  static_assert(!IDXL || SPARSE, "LDS indices are the selected blocks'");
   __shared__ __attribute__((aligned(16))) bf16_t stage_all[4][W::STAGE_ELEMS];
+  __shared__ __attribute__((aligned(16))) int idx_all[IDXL ? 4 * kIdxLds : 4];
   static_assert(16 * HD * sizeof(OT) <= sizeof(stage_all[0]), "output rows fit in the stage");
   const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int lane = threadIdx.x & 63;
@@ -402,15 +407,48 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(AttnParams p) {
         const_cast<int*>(has_idx ? p.idx + (size_t)qi * p.topk : nullptr), 0, has_idx ? nm * 4 : 0,
         0x00020000);
     const bool idx16 = (nm & 3) == 0;
+    typedef int i32x4 __attribute__((ext_vector_type(4)));
+    // IDXL (nm <= kIdxLds): the query's indices go to the wave's LDS once, 8
+    // per lane, and each step reads its own from there. The row gathers are
+    // then the loop's only memory loads, so every wait before a row's use
+    // counts exactly the loads issued after it (an index load in a branch of
+    // the loop made the waits there drain every load in flight).
+    int* const idx_lds = idx_all + (IDXL ? wv * kIdxLds : 0);
+    if constexpr (IDXL) {
+      if (has_idx) {
+        i32x4 a, c;
+        if (idx16) {
+          a = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_idx, 32 * lane, 0, 0));
+          c = __builtin_bit_cast(i32x4,
+                                 __builtin_amdgcn_raw_buffer_load_b128(rs_idx, 32 * lane + 16, 0, 0));
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            a[e] = (int)__builtin_amdgcn_raw_buffer_load_b32(rs_idx, 32 * lane + 4 * e, 0, 0);
+            c[e] = (int)__builtin_amdgcn_raw_buffer_load_b32(rs_idx, 32 * lane + 16 + 4 * e, 0, 0);
+          }
+        }
+        *reinterpret_cast<i32x4*>(idx_lds + 8 * lane) = a;
+        *reinterpret_cast<i32x4*>(idx_lds + 8 * lane + 4) = c;
+        wave_lds_sync();
+      }
+    }
     struct Sel {
       int v[8];
     };
     auto load_sel = [&](int st, Sel& sl) {
       const int j0 = 32 * st;
       if (__builtin_amdgcn_readfirstlane(j0 < nm_pad ? 1 : 0)) {
-        if (SPARSE) {
+        if constexpr (IDXL) {
+          const i32x4 a = *reinterpret_cast<const i32x4*>(idx_lds + j0 + 4 * q4);
+          const i32x4 c = *reinterpret_cast<const i32x4*>(idx_lds + j0 + 16 + 4 * q4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            sl.v[e] = a[e];
+            sl.v[4 + e] = c[e];
+          }
+        } else if (SPARSE) {
           if (idx16) {
-            typedef int i32x4 __attribute__((ext_vector_type(4)));
             const i32x4 a = __builtin_bit_cast(
                 i32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_idx, (j0 + 4 * q4) * 4, 0, 0));
             const i32x4 c = __builtin_bit_cast(
@@ -721,8 +759,12 @@ template <int HD, bool SPARSE>
 static hipError_t launch_attn(const AttnParams& p, int qdtype, int odtype, hipStream_t s) {
   const long long nq = (long long)p.B * p.T;
   const dim3 grid((unsigned)((nq + 3) / 4)), block(256);
-#define KCH_ATTN_LAUNCH(QT, OT) \
-  hipLaunchKernelGGL((attn_prefill_kernel<HD, QT, OT, SPARSE>), grid, block, 0, s, p)
+  const bool idxl = SPARSE && p.topk <= kIdxLds;
+#define KCH_ATTN_LAUNCH(QT, OT)                                                                 \
+  do {                                                                                          \
+    if (idxl) hipLaunchKernelGGL((attn_prefill_kernel<HD, QT, OT, SPARSE, SPARSE>), grid, block, 0, s, p); \
+    else hipLaunchKernelGGL((attn_prefill_kernel<HD, QT, OT, SPARSE, false>), grid, block, 0, s, p); \
+  } while (0)
   if (qdtype == DT_BF16) {
     if (odtype == DT_F32) KCH_ATTN_LAUNCH(bf16_t, float);
     else KCH_ATTN_LAUNCH(bf16_t, bf16_t);
