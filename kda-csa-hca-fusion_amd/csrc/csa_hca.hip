@@ -8,6 +8,8 @@
 //   logits are -inf and its values zero). Optional outputs: the raw fp32 block,
 //   the attention key row (L2-normalised or raw, bf16 or fp32), and the per-token
 //   window keys L2norm(C) (or raw C) of the block's source tokens.
+//   compress_lanes_kernel (short blocks, aligned rows) and compress_rows_kernel
+//   (long blocks) compute the same outputs with 16-byte row accesses.
 //
 // hca_attn_kernel  naive_hca core (/root/reference/ops_hca.py:132-194): query t
 //   attends to the compressed blocks b < (t+1)//m (ops_csa.py:179-195) and to
@@ -140,6 +142,169 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressParams p) {
       if (p.normalize) inv = l2_inv(wave_sum(v[0] * v[0] + v[1] * v[1]));
       for (int u = 0; u < 2; ++u)
         if (lane + 64 * u < c) p.local[t * c + lane + 64 * u] = (bf16_t)(v[u] * inv);
+    }
+  }
+}
+
+// Eight consecutive channels ch0 .. ch0 + 7 of a compressed key row in
+// every format of store_key (ch0 a multiple of 8): one or two whole stores
+// per part instead of eight scalar ones.
+__device__ __forceinline__ void store_key8(const CompressParams& p, size_t orow, int c, int ch0,
+                                           const float (&x)[8]) {
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  if (p.key_f32 == 1) {
+    float* d = static_cast<float*>(p.out_key) + orow * c + ch0;
+    *reinterpret_cast<float4*>(d) = make_float4(x[0], x[1], x[2], x[3]);
+    *reinterpret_cast<float4*>(d + 4) = make_float4(x[4], x[5], x[6], x[7]);
+  } else if (p.key_f32 == 2) {
+    float hi[8], mid[8], lo[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const bf16_t h = (bf16_t)x[i];
+      const float r = x[i] - (float)h;
+      const bf16_t md = (bf16_t)r;
+      hi[i] = (float)h;
+      mid[i] = (float)md;
+      lo[i] = r - (float)md;
+    }
+    bf16_t* row = static_cast<bf16_t*>(p.out_key) + orow * 3 * c;
+    *reinterpret_cast<bf16x8*>(row + ch0) = to_bf16x8(hi);
+    *reinterpret_cast<bf16x8*>(row + c + ch0) = to_bf16x8(mid);
+    *reinterpret_cast<bf16x8*>(row + 2 * c + ch0) = to_bf16x8(lo);
+  } else if (p.key_f32 == 3 || p.key_f32 == 4) {
+    h8 hi, lo;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float xs = x[i] * kSplit16Scale;
+      hi[i] = (_Float16)xs;
+      lo[i] = (_Float16)(xs - (float)hi[i]);
+    }
+    _Float16* base = static_cast<_Float16*>(p.out_key);
+    if (p.key_f32 == 3) {
+      *reinterpret_cast<h8*>(base + orow * 2 * c + ch0) = hi;
+      *reinterpret_cast<h8*>(base + orow * 2 * c + c + ch0) = lo;
+    } else {
+      const int nb = p.T / p.m;
+      *reinterpret_cast<h8*>(base + chunked_key_offset(orow, nb, c, 0, ch0)) = hi;
+      *reinterpret_cast<h8*>(base + chunked_key_offset(orow, nb, c, 1, ch0)) = lo;
+    }
+  } else {
+    *reinterpret_cast<bf16x8*>(static_cast<bf16_t*>(p.out_key) + orow * c + ch0) = to_bf16x8(x);
+  }
+}
+
+// Lane-parallel compression for short blocks (m, or 2m when overlapped,
+// below 16 rows; c in {32,64,128}, 16-byte aligned rows): LPR = C / 8 lanes
+// per compressed block, each owning 8 channels with 16-byte loads and stores,
+// 64 / LPR blocks per wave. Per channel the same two passes as
+// compress_kernel, in the same order (max over the a-branch logits then the
+// b-branch ones; sums likewise), so the block values are those of
+// compress_kernel bit for bit; the row norms reduce over the block's LPR lanes.
+template <typename InT, bool OVERLAP, int C>
+__global__ __launch_bounds__(256) void compress_lanes_kernel(CompressParams p) {
+  constexpr int LPR = C / 8;
+  constexpr int BPW = 64 / LPR;
+  const int lane = threadIdx.x & 63;
+  const int nb = p.T / p.m;
+  const long long blocks = (long long)p.B * nb;
+  const long long gblk = ((long long)blockIdx.x * 4 + (threadIdx.x >> 6)) * BPW + lane / LPR;
+  const bool active = gblk < blocks;
+  const long long gb = active ? gblk : blocks - 1;  // (inactive lanes compute a copy, store nothing)
+  const int b = (int)(gb / nb), blk = (int)(gb - (long long)b * nb);
+  const int m = p.m;
+  const int ch0 = 8 * (lane % LPR);
+  const InT* Ca = static_cast<const InT*>(p.Ca);
+  const InT* Za = static_cast<const InT*>(p.Za);
+  const InT* Cb = static_cast<const InT*>(p.Cb);
+  const InT* Zb = static_cast<const InT*>(p.Zb);
+  const size_t ta = (size_t)b * p.T + (size_t)blk * m;
+  const bool prev = OVERLAP && blk > 0;
+  const size_t tb = ta - m;
+  float mx[8], z[8], bp[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) mx[i] = -INFINITY;
+  for (int j = 0; j < m; ++j) {
+    Load8<InT>::run(Za + (ta + j) * p.ldZa + ch0, z);
+    Load8<float>::run(p.Ba + j * C + ch0, bp);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) mx[i] = fmaxf(mx[i], z[i] + bp[i]);
+  }
+  if (prev)
+    for (int j = 0; j < m; ++j) {
+      Load8<InT>::run(Zb + (tb + j) * p.ldZb + ch0, z);
+      Load8<float>::run(p.Bb + j * C + ch0, bp);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) mx[i] = fmaxf(mx[i], z[i] + bp[i]);
+    }
+  float den[8], num[8], cv[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) den[i] = num[i] = 0.f;
+  for (int j = 0; j < m; ++j) {
+    Load8<InT>::run(Za + (ta + j) * p.ldZa + ch0, z);
+    Load8<float>::run(p.Ba + j * C + ch0, bp);
+    Load8<InT>::run(Ca + (ta + j) * p.ldCa + ch0, cv);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float e = expf(z[i] + bp[i] - mx[i]);
+      den[i] += e;
+      num[i] += e * cv[i];
+    }
+  }
+  if (prev)
+    for (int j = 0; j < m; ++j) {
+      Load8<InT>::run(Zb + (tb + j) * p.ldZb + ch0, z);
+      Load8<float>::run(p.Bb + j * C + ch0, bp);
+      Load8<InT>::run(Cb + (tb + j) * p.ldCb + ch0, cv);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float e = expf(z[i] + bp[i] - mx[i]);
+        den[i] += e;
+        num[i] += e * cv[i];
+      }
+    }
+  float acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = num[i] / den[i];
+  // sum of squares over the block's LPR lanes (aligned lane groups)
+  auto group_sum = [&](float v) {
+#pragma unroll
+    for (int d = 1; d < LPR; d <<= 1) v += __shfl_xor(v, d);
+    return v;
+  };
+  const size_t orow = (size_t)b * nb + blk;
+  if (p.out_raw && active) {
+    float* d = p.out_raw + orow * C + ch0;
+    *reinterpret_cast<float4*>(d) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    *reinterpret_cast<float4*>(d + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+  }
+  if (p.out_key) {
+    float inv = 1.f;
+    if (p.normalize) {
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss += acc[i] * acc[i];
+      inv = l2_inv(group_sum(ss));
+    }
+    float kx[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) kx[i] = acc[i] * inv;
+    if (active) store_key8(p, orow, C, ch0, kx);
+  }
+  if (p.local) {
+    // window keys of the block's m source tokens (from the a-branch values)
+    for (int j = 0; j < m; ++j) {
+      const size_t t = ta + j;
+      Load8<InT>::run(Ca + t * p.ldCa + ch0, cv);
+      float inv = 1.f;
+      if (p.normalize) {
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss += cv[i] * cv[i];
+        inv = l2_inv(group_sum(ss));
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) cv[i] *= inv;
+      if (active) *reinterpret_cast<bf16x8*>(p.local + t * C + ch0) = to_bf16x8(cv);
     }
   }
 }
@@ -307,7 +472,44 @@ static void launch_compress_rows(const CompressParams& p, int dtype, hipStream_t
   else hipLaunchKernelGGL((compress_rows_kernel<_Float16, OVERLAP, C>), grid, block, 0, stream, p);
 }
 
+// The lane-parallel form: short blocks, c in {32,64,128}, 16-byte aligned rows
+// (Ba / Bb rows of c fp32 are then 16-byte aligned too).
+static bool compress_lanes_ok(const CompressParams& p, int dtype) {
+  const int rows = p.m * (p.overlap ? 2 : 1);
+  if (rows >= 16 || (p.c != 32 && p.c != 64 && p.c != 128)) return false;
+  const long long es = dtype == DT_F32 ? 4 : 2;
+  auto al = [](const void* q) { return q == nullptr || ((uintptr_t)q & 15) == 0; };
+  auto ld_ok = [&](long long ld) { return (ld * es) % 16 == 0; };
+  bool ok = al(p.Ca) && al(p.Za) && al(p.Ba) && al(p.local) && al(p.out_raw) && al(p.out_key) &&
+            ld_ok(p.ldCa) && ld_ok(p.ldZa);
+  if (p.overlap) ok = ok && al(p.Cb) && al(p.Zb) && al(p.Bb) && ld_ok(p.ldCb) && ld_ok(p.ldZb);
+  return ok;
+}
+
+template <bool OVERLAP, int C>
+static void launch_compress_lanes(const CompressParams& p, int dtype, hipStream_t stream) {
+  constexpr int BPW = 64 / (C / 8);
+  const long long blocks = (long long)p.B * (p.T / p.m);
+  const long long waves = (blocks + BPW - 1) / BPW;
+  const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
+  if (dtype == DT_F32) hipLaunchKernelGGL((compress_lanes_kernel<float, OVERLAP, C>), grid, block, 0, stream, p);
+  else if (dtype == DT_BF16) hipLaunchKernelGGL((compress_lanes_kernel<bf16_t, OVERLAP, C>), grid, block, 0, stream, p);
+  else hipLaunchKernelGGL((compress_lanes_kernel<_Float16, OVERLAP, C>), grid, block, 0, stream, p);
+}
+
 hipError_t compress_dispatch(const CompressParams& p, int dtype, hipStream_t stream) {
+  if (p.B * (p.T / p.m) > 0 && compress_lanes_ok(p, dtype)) {
+    if (p.overlap) {
+      if (p.c == 128) launch_compress_lanes<true, 128>(p, dtype, stream);
+      else if (p.c == 64) launch_compress_lanes<true, 64>(p, dtype, stream);
+      else launch_compress_lanes<true, 32>(p, dtype, stream);
+    } else {
+      if (p.c == 128) launch_compress_lanes<false, 128>(p, dtype, stream);
+      else if (p.c == 64) launch_compress_lanes<false, 64>(p, dtype, stream);
+      else launch_compress_lanes<false, 32>(p, dtype, stream);
+    }
+    return hipGetLastError();
+  }
   if (p.B * (p.T / p.m) > 0 && compress_rows_ok(p, dtype)) {
     if (p.overlap) {
       if (p.c == 128) launch_compress_rows<true, 128>(p, dtype, stream);

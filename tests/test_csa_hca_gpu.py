@@ -118,8 +118,8 @@ def test_compress_overlapped(dev, m, c):
     (32, 128, False, "bf16", "bf16"),   # row-parallel kernel, strided rows
     (16, 64, True, "fp32", "fp32"),     # row-parallel, overlapped, fp32 inputs
     (128, 64, False, "fp16", "bf16"),   # row-parallel, long blocks
-    (4, 128, True, "bf16", "bf16"),     # per-block kernel (8 rows)
-    (5, 64, False, "fp32", "fp32"),     # per-block kernel, odd m
+    (4, 128, True, "bf16", "bf16"),     # lane-parallel kernel (8 rows)
+    (5, 64, False, "fp32", "fp32"),     # lane-parallel kernel, odd m
 ])
 def test_compress_key_and_window_outputs(dev, m, c, overlap, dt, key_dt):
     """All compression outputs: raw fp32 blocks, L2-normalised key rows (bf16 or
@@ -152,6 +152,70 @@ def test_compress_key_and_window_outputs(dev, m, c, overlap, dt, key_dt):
     assert np.abs(host(key) - kref).max() <= ktol
     lref = l2_normalize(host(Ca).astype(np.float32))
     assert np.abs(host(local) - lref).max() <= 8e-3
+
+
+@pytest.mark.parametrize("m,c,overlap,dt", [
+    (4, 128, True, "bf16"),    # configs[2]'s CSA compression
+    (4, 64, False, "bf16"),    # its indexer keys
+    (7, 32, True, "fp32"),
+    (5, 128, False, "fp16"),
+    (1, 64, True, "bf16"),
+])
+@pytest.mark.parametrize("key_fmt", [0, 1, 2, 3, 4])
+def test_compress_lane_kernel_matches_block_kernel(dev, m, c, overlap, dt, key_fmt):
+    """Short blocks with 16-byte aligned rows take the lane-parallel kernel,
+    other row strides the one-wave-per-block kernel: the same raw blocks bit for
+    bit (the same per-channel arithmetic in the same order), and the same keys
+    and window rows up to the norm's summation order (the keys' formats
+    decoded: fp32, split bf16, split fp16, chunk-major split fp16, bf16)."""
+    from kch._lib import call, ptr, stream_of, dtype_code
+    dts = {"bf16": torch.bfloat16, "fp32": torch.float32, "fp16": torch.float16}
+    B, T = 3, 37 * m
+    nb = T // m
+    rng = np.random.default_rng(m * 131 + c + key_fmt)
+    wide = torch.from_numpy(rng.standard_normal((B, T, 4 * c + 8)).astype(np.float32)).to(dev, dts[dt])
+    odd = torch.empty(B, T, 4 * c + 1, device=dev, dtype=dts[dt])  # unaligned row stride
+    odd[..., :4 * c] = wide[..., :4 * c]
+    Bab = torch.from_numpy((0.5 * rng.standard_normal((2, m, c))).astype(np.float32)).to(dev)
+    kdt = {0: torch.bfloat16, 1: torch.float32, 2: torch.bfloat16, 3: torch.float16,
+           4: torch.float16}[key_fmt]
+    kw = {0: c, 1: c, 2: 3 * c, 3: 2 * c, 4: 2 * c}[key_fmt]
+    krows = nb if key_fmt != 4 else (nb + 15) // 16 * 16
+    outs = []
+    for src in (wide, odd):
+        raw = torch.empty(B, nb, c, device=dev, dtype=torch.float32)
+        key = torch.zeros(B, krows, kw, device=dev, dtype=kdt)
+        local = torch.empty(B, T, c, device=dev, dtype=torch.bfloat16)
+        ld = src.shape[-1]
+        Ca, Cb, Za, Zb = (src[..., i * c:(i + 1) * c] for i in range(4))
+        if overlap:
+            call("kch_compress_overlapped", ptr(Ca), ld, ptr(Cb), ld, ptr(Za), ld, ptr(Zb), ld,
+                 ptr(Bab[0]), ptr(Bab[1]), ptr(raw), ptr(key), key_fmt, 1, ptr(local), B, T, m, c,
+                 dtype_code("t", src.dtype), stream_of(src))
+        else:
+            call("kch_compress", ptr(Ca), ld, ptr(Za), ld, ptr(Bab[0]), ptr(raw), ptr(key), key_fmt,
+                 1, ptr(local), B, T, m, c, dtype_code("t", src.dtype), stream_of(src))
+        outs.append((raw, key, local))
+    torch.cuda.synchronize()
+    (r0, k0, l0), (r1, k1, l1) = outs
+    assert torch.equal(r0.view(torch.int32), r1.view(torch.int32))
+
+    def decode(k):
+        k = k.float()
+        if key_fmt == 4:  # chunk-major [chunk, part, s, q4, n, i] -> rows [chunk, n, part, s, q4, i]
+            k = (k.view(B, krows // 16, 2, c // 32, 4, 16, 8).permute(0, 1, 5, 2, 3, 4, 6)
+                 .reshape(B, krows, 2 * c)[:, :nb])
+        if key_fmt == 2:
+            return k[..., :c] + k[..., c:2 * c] + k[..., 2 * c:]
+        if key_fmt in (3, 4):
+            return (k[..., :c] + k[..., c:]) / 256.0
+        return k
+    d = (decode(k0) - decode(k1)).abs().max().item()
+    tol = {0: 2.0 ** -8, 1: 1e-6, 2: 1e-6, 3: 1e-6, 4: 1e-6}[key_fmt]
+    assert d <= tol, d
+    ref = torch.nn.functional.normalize(r0, dim=-1)  # the keys are the unit raw blocks
+    assert (decode(k0) - ref).abs().max().item() <= (2.0 ** -8 if key_fmt == 0 else 1e-6)
+    assert (l0.float() - l1.float()).abs().max().item() <= 2.0 ** -8
 
 
 @pytest.mark.parametrize("B,nb,cI,nIh,T_q,topk", [
