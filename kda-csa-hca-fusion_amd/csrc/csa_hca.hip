@@ -95,7 +95,8 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressParams p) {
   for (int u = 0; u < 2; ++u) {
     const int ch = lane + 64 * u;
     if (ch >= c) continue;
-    // pass 1: max of the logits; pass 2: exp-weighted sums (torch.softmax order)
+    // pass 1: max of the logits; pass 2: exp-weighted sums (torch.softmax
+    // order; the exponentials of the hardware's exp2, within 2 ulp)
     float mx = -INFINITY;
     const size_t ta = (size_t)b * p.T + (size_t)blk * m;
     for (int j = 0; j < m; ++j)
@@ -107,13 +108,13 @@ __global__ __launch_bounds__(256) void compress_kernel(CompressParams p) {
         mx = fmaxf(mx, to_f32(Zb[(tb + j) * p.ldZb + ch]) + p.Bb[j * c + ch]);
     float den = 0.f, num = 0.f;
     for (int j = 0; j < m; ++j) {
-      const float e = expf(to_f32(Za[(ta + j) * p.ldZa + ch]) + p.Ba[j * c + ch] - mx);
+      const float e = exp_hw(to_f32(Za[(ta + j) * p.ldZa + ch]) + p.Ba[j * c + ch] - mx);
       den += e;
       num += e * to_f32(Ca[(ta + j) * p.ldCa + ch]);
     }
     if (prev)
       for (int j = 0; j < m; ++j) {
-        const float e = expf(to_f32(Zb[(tb + j) * p.ldZb + ch]) + p.Bb[j * c + ch] - mx);
+        const float e = exp_hw(to_f32(Zb[(tb + j) * p.ldZb + ch]) + p.Bb[j * c + ch] - mx);
         den += e;
         num += e * to_f32(Cb[(tb + j) * p.ldCb + ch]);
       }
@@ -200,7 +201,9 @@ __device__ __forceinline__ void store_key8(const CompressParams& p, size_t orow,
 // compress_kernel, in the same order (max over the a-branch logits then the
 // b-branch ones; sums likewise), so the block values are those of
 // compress_kernel bit for bit; the row norms reduce over the block's LPR lanes.
-template <typename InT, bool OVERLAP, int C>
+// MR > 0 (two-byte inputs, m <= MR): the block's rows are all loaded before
+// the passes, which then run from registers.
+template <typename InT, bool OVERLAP, int C, int MR>
 __global__ __launch_bounds__(256) void compress_lanes_kernel(CompressParams p) {
   constexpr int LPR = C / 8;
   constexpr int BPW = 64 / LPR;
@@ -220,48 +223,102 @@ __global__ __launch_bounds__(256) void compress_lanes_kernel(CompressParams p) {
   const size_t ta = (size_t)b * p.T + (size_t)blk * m;
   const bool prev = OVERLAP && blk > 0;
   const size_t tb = ta - m;
-  float mx[8], z[8], bp[8];
+  float mx[8], z[8], bp[8], cv[8], den[8], num[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) mx[i] = -INFINITY;
-  for (int j = 0; j < m; ++j) {
-    Load8<InT>::run(Za + (ta + j) * p.ldZa + ch0, z);
-    Load8<float>::run(p.Ba + j * C + ch0, bp);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) mx[i] = fmaxf(mx[i], z[i] + bp[i]);
+  for (int i = 0; i < 8; ++i) {
+    mx[i] = -INFINITY;
+    den[i] = num[i] = 0.f;
   }
-  if (prev)
+  if constexpr (MR > 0) {
+    // every Z and C row of the block loaded at once (16 bytes each, one
+    // round trip), then both passes from registers
+    static_assert(sizeof(InT) == 2, "register rows hold 8 two-byte values");
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 zr[2][MR], cr[2][MR];
+    const size_t tbs = prev ? tb : ta;  // (a readable row when there is no b-branch)
+#pragma unroll
+    for (int j = 0; j < MR; ++j) {
+      if (j < m) {
+        zr[0][j] = *reinterpret_cast<const u32x4*>(Za + (ta + j) * p.ldZa + ch0);
+        cr[0][j] = *reinterpret_cast<const u32x4*>(Ca + (ta + j) * p.ldCa + ch0);
+        if (OVERLAP) {
+          zr[1][j] = *reinterpret_cast<const u32x4*>(Zb + (tbs + j) * p.ldZb + ch0);
+          cr[1][j] = *reinterpret_cast<const u32x4*>(Cb + (tbs + j) * p.ldCb + ch0);
+        }
+      }
+    }
+    auto unpack = [](const u32x4& r, float* f) { Load8<InT>::run(reinterpret_cast<const InT*>(&r), f); };
+#pragma unroll
+    for (int br = 0; br < (OVERLAP ? 2 : 1); ++br) {
+      if (br == 1 && !prev) break;
+      const float* Bp = br ? p.Bb : p.Ba;
+#pragma unroll
+      for (int j = 0; j < MR; ++j) {
+        if (j < m) {
+          unpack(zr[br][j], z);
+          Load8<float>::run(Bp + j * C + ch0, bp);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) mx[i] = fmaxf(mx[i], z[i] + bp[i]);
+        }
+      }
+    }
+#pragma unroll
+    for (int br = 0; br < (OVERLAP ? 2 : 1); ++br) {
+      if (br == 1 && !prev) break;
+      const float* Bp = br ? p.Bb : p.Ba;
+#pragma unroll
+      for (int j = 0; j < MR; ++j) {
+        if (j < m) {
+          unpack(zr[br][j], z);
+          unpack(cr[br][j], cv);
+          Load8<float>::run(Bp + j * C + ch0, bp);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const float e = exp_hw(z[i] + bp[i] - mx[i]);
+            den[i] += e;
+            num[i] += e * cv[i];
+          }
+        }
+      }
+    }
+  } else {
     for (int j = 0; j < m; ++j) {
-      Load8<InT>::run(Zb + (tb + j) * p.ldZb + ch0, z);
-      Load8<float>::run(p.Bb + j * C + ch0, bp);
+      Load8<InT>::run(Za + (ta + j) * p.ldZa + ch0, z);
+      Load8<float>::run(p.Ba + j * C + ch0, bp);
 #pragma unroll
       for (int i = 0; i < 8; ++i) mx[i] = fmaxf(mx[i], z[i] + bp[i]);
     }
-  float den[8], num[8], cv[8];
+    if (prev)
+      for (int j = 0; j < m; ++j) {
+        Load8<InT>::run(Zb + (tb + j) * p.ldZb + ch0, z);
+        Load8<float>::run(p.Bb + j * C + ch0, bp);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) den[i] = num[i] = 0.f;
-  for (int j = 0; j < m; ++j) {
-    Load8<InT>::run(Za + (ta + j) * p.ldZa + ch0, z);
-    Load8<float>::run(p.Ba + j * C + ch0, bp);
-    Load8<InT>::run(Ca + (ta + j) * p.ldCa + ch0, cv);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float e = expf(z[i] + bp[i] - mx[i]);
-      den[i] += e;
-      num[i] += e * cv[i];
-    }
-  }
-  if (prev)
+        for (int i = 0; i < 8; ++i) mx[i] = fmaxf(mx[i], z[i] + bp[i]);
+      }
     for (int j = 0; j < m; ++j) {
-      Load8<InT>::run(Zb + (tb + j) * p.ldZb + ch0, z);
-      Load8<float>::run(p.Bb + j * C + ch0, bp);
-      Load8<InT>::run(Cb + (tb + j) * p.ldCb + ch0, cv);
+      Load8<InT>::run(Za + (ta + j) * p.ldZa + ch0, z);
+      Load8<float>::run(p.Ba + j * C + ch0, bp);
+      Load8<InT>::run(Ca + (ta + j) * p.ldCa + ch0, cv);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float e = expf(z[i] + bp[i] - mx[i]);
+        const float e = exp_hw(z[i] + bp[i] - mx[i]);
         den[i] += e;
         num[i] += e * cv[i];
       }
     }
+    if (prev)
+      for (int j = 0; j < m; ++j) {
+        Load8<InT>::run(Zb + (tb + j) * p.ldZb + ch0, z);
+        Load8<float>::run(p.Bb + j * C + ch0, bp);
+        Load8<InT>::run(Cb + (tb + j) * p.ldCb + ch0, cv);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float e = exp_hw(z[i] + bp[i] - mx[i]);
+          den[i] += e;
+          num[i] += e * cv[i];
+        }
+      }
+  }
   float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = num[i] / den[i];
@@ -492,9 +549,16 @@ static void launch_compress_lanes(const CompressParams& p, int dtype, hipStream_
   const long long blocks = (long long)p.B * (p.T / p.m);
   const long long waves = (blocks + BPW - 1) / BPW;
   const dim3 grid((unsigned)((waves + 3) / 4)), block(256);
-  if (dtype == DT_F32) hipLaunchKernelGGL((compress_lanes_kernel<float, OVERLAP, C>), grid, block, 0, stream, p);
-  else if (dtype == DT_BF16) hipLaunchKernelGGL((compress_lanes_kernel<bf16_t, OVERLAP, C>), grid, block, 0, stream, p);
-  else hipLaunchKernelGGL((compress_lanes_kernel<_Float16, OVERLAP, C>), grid, block, 0, stream, p);
+  const bool regs = p.m <= 4;
+  if (dtype == DT_F32)
+    hipLaunchKernelGGL((compress_lanes_kernel<float, OVERLAP, C, 0>), grid, block, 0, stream, p);
+  else if (dtype == DT_BF16) {
+    if (regs) hipLaunchKernelGGL((compress_lanes_kernel<bf16_t, OVERLAP, C, 4>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((compress_lanes_kernel<bf16_t, OVERLAP, C, 0>), grid, block, 0, stream, p);
+  } else {
+    if (regs) hipLaunchKernelGGL((compress_lanes_kernel<_Float16, OVERLAP, C, 4>), grid, block, 0, stream, p);
+    else hipLaunchKernelGGL((compress_lanes_kernel<_Float16, OVERLAP, C, 0>), grid, block, 0, stream, p);
+  }
 }
 
 hipError_t compress_dispatch(const CompressParams& p, int dtype, hipStream_t stream) {
