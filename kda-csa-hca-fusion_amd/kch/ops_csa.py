@@ -24,7 +24,9 @@ Differences, all documented:
   cotangent and ``soft^T gsum`` to the compressed rows'). ``'aux_contrastive'``
   raises ``NotImplementedError``, as the reference's indexer does. The
   forward value is the hard top-k path either way (the surrogate adds zero).
-* Indexer logits are fp32-level: three-part split-bf16 MFMA products.
+* Indexer logits are fp32-level: split-operand MFMA products (two fp16
+  parts of unit rows, stored chunk-major for the indexer's loads, or three
+  bf16 parts of raw rows).
 * Exactly-equal indexer logits are ordered by ascending block index (the
   reference's ``torch.topk`` leaves that order unspecified).
 * Attention keys/values are the L2-normalised compressed rows rounded to
