@@ -223,6 +223,7 @@ def test_compress_lane_kernel_matches_block_kernel(dev, m, c, overlap, dt, key_f
     (1, 2048, 64, 4, 192, 512),  # configs[2]'s key count and top-k
     (2, 40, 32, 2, 12, 8),       # one-tile kernel (T < 16), two pieces per chunk
     (1, 50, 128, 8, 64, 24),     # 128 channels: eight pieces per chunk
+    (1, 4096, 64, 4, 48, 512),   # rows beyond the register selection (configs[4]'s prefill)
 ])
 def test_indexer_chunk_major_keys(dev, B, nb, cI, nIh, T_q, topk):
     """Compression key format 4 holds format 3's fp16 parts chunk-major (checked
