@@ -430,10 +430,10 @@ __global__ __launch_bounds__(256) void compress_rows_kernel(CompressParams p) {
       if (r0 + k * NSLOT >= nrows) continue;  // same for the whole slot
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        // online softmax step: one exp per element
+        // online softmax step: one exp per element (the hardware exp2)
         const float d = z[k][i] - mx[i];
         const bool up = d > 0.f;
-        const float e = expf(up ? -d : d);  // mx = -inf: d = +inf, e = 0
+        const float e = exp_hw(up ? -d : d);  // mx = -inf: d = +inf, e = 0
         den[i] = up ? fmaf(den[i], e, 1.f) : den[i] + e;
         num[i] = up ? fmaf(num[i], e, v[k][i]) : fmaf(e, v[k][i], num[i]);
         mx[i] = up ? z[k][i] : mx[i];
@@ -461,7 +461,7 @@ __global__ __launch_bounds__(256) void compress_rows_kernel(CompressParams p) {
       const float m2 = __shfl_xor(mx[i], o), d2 = __shfl_xor(den[i], o), n2 = __shfl_xor(num[i], o);
       const float mm = fmaxf(mx[i], m2);
       if (mm != -INFINITY) {
-        const float e1 = expf(mx[i] - mm), e2 = expf(m2 - mm);
+        const float e1 = exp_hw(mx[i] - mm), e2 = exp_hw(m2 - mm);
         den[i] = den[i] * e1 + d2 * e2;
         num[i] = num[i] * e1 + n2 * e2;
         mx[i] = mm;
@@ -488,7 +488,7 @@ __global__ __launch_bounds__(256) void compress_rows_kernel(CompressParams p) {
     for (int w = 0; w < 4; ++w) {
       const float mw = part[w][0][ch];
       if (mw != -INFINITY) {
-        const float e = expf(mw - M);
+        const float e = exp_hw(mw - M);
         dd += part[w][1][ch] * e;
         nn += part[w][2][ch] * e;
       }
