@@ -622,9 +622,41 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(AttnParams p) {
   if (qi >= (long long)p.B * T) return;
   const int b = (int)(qi / T), t = (int)(qi - (long long)b * T);
 
-  const QT* qrow = static_cast<const QT*>(p.q) + ((size_t)qi * p.nh + n) * HD;
+  // The query's words are requested first and converted once the first rows
+  // are in flight: their latency overlaps the index and row requests (a wait
+  // for a load also waits for the loads issued before it, so the query goes
+  // first). A padding head (n >= nh) reads head 0 and is zeroed.
+  const QT* qrow = static_cast<const QT*>(p.q) + ((size_t)qi * p.nh + (n < p.nh ? n : 0)) * HD;
+  typedef uint32_t u32x4q __attribute__((ext_vector_type(4)));
+  constexpr int QWD = sizeof(QT) == 4 ? 2 : 1;  // 16-byte words per 8 query elements
+  u32x4q qraw[W::NS][QWD];
+#pragma unroll
+  for (int s = 0; s < W::NS; ++s)
+#pragma unroll
+    for (int h = 0; h < QWD; ++h)
+      qraw[s][h] = *reinterpret_cast<const u32x4q*>(qrow + 32 * s + 8 * (lane >> 4) + 4 * h);
   W w;
-  w.template init<QT>(n < p.nh ? qrow : nullptr, p.normalize_q != 0, p.scale);
+  auto setup_q = [&]() {
+    float f[W::NS][8];
+    const bool keep = n < p.nh;
+#pragma unroll
+    for (int s = 0; s < W::NS; ++s) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float x;
+        if constexpr (sizeof(QT) == 4) {
+          x = __uint_as_float(qraw[s][i >> 2][i & 3]);
+        } else {
+          const uint32_t wd = qraw[s][0][i >> 1];
+          const uint16_t hb = (uint16_t)((i & 1) ? (wd >> 16) : (wd & 0xffffu));
+          if constexpr (std::is_same<QT, bf16_t>::value) x = __uint_as_float((uint32_t)hb << 16);
+          else x = (float)__builtin_bit_cast(_Float16, hb);
+        }
+        f[s][i] = keep ? x : 0.f;
+      }
+    }
+    w.setup(f, p.normalize_q != 0, p.scale);
+  };
 
   // The rows of this query: n_main compressed rows (the selected blocks, -1 =
   // unused slot; or the causally visible blocks), then n_win window rows (the
@@ -791,6 +823,7 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(AttnParams p) {
     int any1 = load_rows(1, s1, fr1, ok1);
     load_sel(2, s0);
     load_sel(3, s1);
+    setup_q();
     for (int g = 0; g < ng; ++g) {
       if (any0) w.chunk_sl(fr0, ok0, stage, to, any0 == 2);
       any0 = load_rows(2 * g + 2, s0, fr0, ok0);
@@ -799,6 +832,8 @@ __global__ __launch_bounds__(256, 3) void attn_prefill_kernel(AttnParams p) {
       any1 = load_rows(2 * g + 3, s1, fr1, ok1);
       load_sel(2 * g + 5, s1);
     }
+  } else {
+    setup_q();
   }
   w.finalize();
   const float f = w.finish(p.sink != nullptr, (p.sink && n < p.nh) ? p.sink[n] : 0.f);
